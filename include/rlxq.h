@@ -1,0 +1,201 @@
+/*
+ * rlxq.h -- C ABI of the MI355X (gfx950) quantized-matmul library.
+ *
+ * One shared library (librlxq.so) with its gfx950 code object built in.  It
+ * replaces the backend kernel behind rlx-models' group-wise packed-weight
+ * linear op and its grouped-expert siblings.  Every entry point is plain C:
+ * pointers, sizes and an opaque stream, no C++ or torch types.
+ *
+ * Conventions shared by every entry point
+ *   - Device pointers (x, w, scales, biases, y, expert_idx, ids, probs) are
+ *     owned by the caller and must stay valid until the stream has run the
+ *     call.  `stream` is a hipStream_t passed as void* (NULL = null stream).
+ *   - W is logically [N, K] row-major, K contiguous, and y = x . W^T, as in
+ *     `Op::DequantMatMul` (crates/rlx-models-core/src/standard_decoder.rs:727-738,
+ *     crates/rlx-qwen3/src/precision.rs:98-112).  Int8Block weights are
+ *     [K, N] like the reference's (crates/rlx-kimi-k3/examples/int8_kernel.rs:59-89).
+ *   - Results are written with fp32 accumulation.  The reference's output is
+ *     always F32; RLXQ_BF16 output (round to nearest even) is offered for
+ *     prefill callers.
+ *   - Return value: RLXQ_OK (0) or a negative rlxq_status.  Shape, scheme,
+ *     dtype, alignment and null-pointer problems are rejected on the host
+ *     before any kernel is launched; rlxq_last_error() names the argument.
+ *   - A context is used by one host thread at a time (the reference's
+ *     CompiledGraph is &mut self); calls on different streams may overlap.
+ */
+#ifndef RLXQ_H
+#define RLXQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Weight schemes.  Names mirror rlx_ir::quant::QuantScheme variants. */
+typedef enum rlxq_scheme {
+    RLXQ_GGUF_Q8_0 = 1,   /* GgufQ8_0: 34 B / 32 w: f16 d, 32 x i8; w = d*q      */
+    RLXQ_GGUF_Q4_0 = 2,   /* GgufQ4_0: 18 B / 32 w: f16 d, 16 B nibbles; d*(q-8) */
+    RLXQ_GGUF_Q4_1 = 3,   /* GgufQ4_1: 20 B / 32 w: f16 d, f16 m, nibbles; d*q+m */
+    RLXQ_MLX_AFFINE4 = 4, /* MlxAffine{bits:4, group_size}: u32 LSB-first codes,
+                             scale*code + bias, scales/biases [N, K/group]       */
+    RLXQ_MLX_AFFINE8 = 5, /* MlxAffine{bits:8, group_size}                       */
+    RLXQ_INT8_BLOCK = 6   /* Int8Block{block_size: K}: i8 [K, N], scale [N],
+                             zp [N] (NULL = 0); y = x . ((Wq - zp) * scale)      */
+} rlxq_scheme;
+
+/* Element types of activations, outputs and MLX scale/bias slabs. */
+typedef enum rlxq_dtype {
+    RLXQ_F32 = 0,
+    RLXQ_BF16 = 1
+} rlxq_dtype;
+
+typedef enum rlxq_status {
+    RLXQ_OK = 0,
+    RLXQ_E_NULL = -1,     /* a required pointer is NULL                      */
+    RLXQ_E_SHAPE = -2,    /* m/k/n/rows/experts out of range or inconsistent */
+    RLXQ_E_SCHEME = -3,   /* unknown scheme, or not valid for this call     */
+    RLXQ_E_ALIGN = -4,    /* pointer or K not aligned as the scheme needs   */
+    RLXQ_E_DTYPE = -5,    /* unsupported activation / output dtype          */
+    RLXQ_E_HIP = -6,      /* a HIP runtime call failed                      */
+    RLXQ_E_NOMEM = -7,    /* device or host allocation failed               */
+    RLXQ_E_INDEX = -8,    /* expert index outside [0, num_experts)          */
+    RLXQ_E_NOKERNEL = -9, /* code object lacks the kernel for this variant  */
+    RLXQ_E_DEVICE = -10   /* device is not gfx950 or does not exist         */
+} rlxq_status;
+
+typedef struct rlxq_ctx rlxq_ctx;
+
+/* Context: loads the embedded gfx950 code object on `device` with
+ * hipModuleLoadData and resolves every kernel.  Replaces the per-backend
+ * setup behind Session::new(Device::Rocm) (external rlx-runtime; caller
+ * crates/rlx-laguna/src/device_matmul.rs:94-111 `DeviceMatmul::try_new`). */
+int rlxq_init(int device, rlxq_ctx** out);
+int rlxq_destroy(rlxq_ctx* ctx);
+const char* rlxq_strerror(int status);
+/* Detail of the last failure on this context (empty if none). */
+const char* rlxq_last_error(const rlxq_ctx* ctx);
+/* Library version string, e.g. "rlxq 0.1.0 gfx950". */
+const char* rlxq_version(void);
+
+/* Dense DequantMatMul: y[m, n] = sum_k x[m, k] * dequant(W)[n, k].
+ * Replaces the backend kernel of Op::DequantMatMul{scheme} (the IR op is
+ * emitted at crates/rlx-models-core/src/standard_decoder.rs:727-738 and
+ * crates/rlx-qwen3/src/precision.rs:98-112; host twin
+ * rlx_cpu::gguf_matmul::gguf_matmul_bt, call sites
+ * crates/rlx-laguna/src/packed_forward.rs:30,233-241).
+ *   GGUF schemes ("Packed2"): w = packed blocks, N rows of K/32 blocks;
+ *     scales = biases = NULL, group_size ignored.  K % 64 == 0 for Q8_0 and
+ *     Q4_0 (block pairs are read dword aligned), K % 32 == 0 for Q4_1.
+ *   MLX affine ("Affine4"): w = u32 codes [N, K*bits/32]; scales/biases
+ *     [N, K/group_size] of `sb_dtype`; group_size in {32, 64, 128}.
+ *   Int8Block: w = i8 [K, N]; scales = f32 [N]; biases = zp f32 [N] or NULL.
+ * x: [M, K] of x_dtype; y: [M, N] of y_dtype. */
+int rlxq_dequant_matmul(rlxq_ctx* ctx, int scheme, int group_size,
+                        const void* x, int x_dtype, const void* w,
+                        const void* scales, const void* biases, int sb_dtype,
+                        int64_t m, int64_t k, int64_t n, void* y, int y_dtype,
+                        void* stream);
+
+/* Grouped expert DequantMatMul: out[r, :] = x[r, :] . dequant(bank[e[r]])^T.
+ * Replaces Op::DequantGroupedMatMul{scheme} (crates/rlx-qwen35/src/builder.rs:2955-2973;
+ * host twin rlx_cpu::gguf_matmul::gguf_grouped_matmul_bt_fused, call site
+ * crates/rlx-laguna/src/packed_forward.rs:583-623) and, for MLX schemes,
+ * Op::DequantGroupedMatMulMlx (standard_decoder.rs:12731-12760, bf16 scale
+ * slabs [E, N, K/group]).  bank = E contiguous [N, K] slabs; expert_idx is
+ * F32 [rows] like the IR's TopK output.  The rows are routed on the device:
+ * each fired expert's weights are streamed once for all of its rows.  The
+ * indices live on the device, so they are not read back: a row whose index
+ * is not an integer in [0, num_experts) gets a zero output row (the host
+ * session API below validates host indices and returns RLXQ_E_INDEX). */
+int rlxq_dequant_grouped_matmul(rlxq_ctx* ctx, int scheme, int group_size,
+                                const void* x, int x_dtype, const void* bank,
+                                const void* scales, const void* biases,
+                                int sb_dtype, const float* expert_idx,
+                                int64_t rows, int64_t k, int64_t n,
+                                int64_t num_experts, void* y, int y_dtype,
+                                void* stream);
+
+/* MoE routed-expert grouped GEMV driven by a device routing table built from
+ * ids [rows, top_k] (int32).  Two modes, which together make one expert FFN
+ * (crates/rlx-unlimited-ocr/tests/quant_parity_backends.rs:338-373 and
+ * standard_decoder.rs:12612-12760):
+ *   RLXQ_MOE_EXPAND : x [rows, K] -> y [rows*top_k, N],
+ *                     y[r*top_k + j] = x[r] . W[ids[r, j]]^T   (probs unused)
+ *   RLXQ_MOE_COMBINE: x [rows*top_k, K] -> y [rows, N],
+ *                     y[r] = sum_j probs[r, j] * (x[r*top_k + j] . W[ids[r, j]]^T)
+ * GGUF schemes only (scales/biases NULL). */
+typedef enum rlxq_moe_mode { RLXQ_MOE_EXPAND = 0, RLXQ_MOE_COMBINE = 1 } rlxq_moe_mode;
+int rlxq_moe_grouped(rlxq_ctx* ctx, int scheme, int mode, const void* x,
+                     int x_dtype, const void* bank, const int32_t* ids,
+                     const float* probs, int64_t rows, int64_t top_k,
+                     int64_t k, int64_t n, int64_t num_experts, void* y,
+                     int y_dtype, void* stream);
+
+/* Router: row softmax of logits [rows, E] (f32), top-k by probability
+ * (ties to the lower expert id), optional renormalisation of the kept
+ * probabilities (norm_topk_prob, standard_decoder.rs:12634-12661).
+ * Writes ids [rows, top_k] int32 and probs [rows, top_k] f32. */
+int rlxq_moe_route(rlxq_ctx* ctx, const float* logits, int64_t rows,
+                   int64_t num_experts, int64_t top_k, int renorm,
+                   int32_t* ids, float* probs, void* stream);
+
+/* SwiGLU between the fused gate|up projection and down: for each row,
+ * out[i] = silu(gu[i]) * gu[inter + i], gu [rows, 2*inter] -> out [rows, inter]
+ * (crates/rlx-laguna/src/device_matmul.rs:383-426 GroupedSwiglu graph). */
+int rlxq_swiglu(rlxq_ctx* ctx, const void* gu, int gu_dtype, int64_t rows,
+                int64_t inter, void* out, int out_dtype, void* stream);
+
+/* W8A8 GEMM: per-row int8 activation quantisation computed on the fly
+ * (crates/rlx-quant-calib/src/bitnet.rs:76-93) times per-channel int8
+ * weights (crates/rlx-kimi-k3/src/common.rs:466-482, wq [K, N], w_scale [N])
+ * on int8 MFMA with int32 accumulation: y = (sum qx*qw) * sx[m] * sw[n].
+ * The reference has no such kernel; it has the two quantisers. */
+int rlxq_w8a8_gemm(rlxq_ctx* ctx, const void* x, int x_dtype,
+                   const int8_t* wq, const float* w_scale, int64_t m,
+                   int64_t k, int64_t n, void* y, int y_dtype, void* stream);
+
+/* The activation quantiser used by rlxq_w8a8_gemm, exposed for checking:
+ * q [m, k] int8 and scales [m] f32. */
+int rlxq_quantize_act_int8(rlxq_ctx* ctx, const void* x, int x_dtype,
+                           int64_t m, int64_t k, int8_t* q, float* scales,
+                           void* stream);
+
+/* Dequantize `rows` packed rows of K weights to f32 [rows, K] with the same
+ * arithmetic the kernels use (bit-exact against the CPU codec).  GGUF and
+ * MLX schemes; MLX takes scales/biases as in rlxq_dequant_matmul. */
+int rlxq_dequantize(rlxq_ctx* ctx, int scheme, int group_size, const void* w,
+                    const void* scales, const void* biases, int sb_dtype,
+                    int64_t rows, int64_t k, float* out, void* stream);
+
+/* Bytes of one packed row of K weights for a GGUF scheme (-1 if invalid). */
+int64_t rlxq_row_bytes(int scheme, int64_t k);
+
+/* ---- Host-side session API ----------------------------------------------
+ * Mirrors rlx-laguna's DeviceMatmul (crates/rlx-laguna/src/device_matmul.rs:
+ * 82-200): host slices in, host f32 out, weights uploaded once per distinct
+ * host pointer and length and kept resident (`uploaded_ptr`, :41-62,301-352),
+ * shape mismatch and unknown scheme rejected (:129-146, :64-76). */
+typedef struct rlxq_device_matmul rlxq_device_matmul;
+int rlxq_dm_try_new(int device, rlxq_device_matmul** out);
+void rlxq_dm_free(rlxq_device_matmul* dm);
+const char* rlxq_dm_last_error(const rlxq_device_matmul* dm);
+/* y[m*n] = x[m*k] . W^T, W = packed GGUF bytes [n, k] (w_len bytes). */
+int rlxq_dm_matmul(rlxq_device_matmul* dm, const float* x, size_t x_len,
+                   const uint8_t* w_bytes, size_t w_len, size_t m, size_t k,
+                   size_t n, int scheme, float* y);
+/* out[i] = x[i] . expert[expert_idx[i]]^T over a resident expert stack. */
+int rlxq_dm_grouped_matmul(rlxq_device_matmul* dm, const float* x,
+                           size_t x_len, const uint8_t* w_bytes, size_t w_len,
+                           const float* expert_idx, size_t idx_len, size_t m,
+                           size_t k, size_t n, size_t num_experts, int scheme,
+                           float* y);
+/* Number of weight uploads performed so far (re-upload is skipped when the
+ * same host pointer and length come back). */
+int64_t rlxq_dm_upload_count(const rlxq_device_matmul* dm);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RLXQ_H */

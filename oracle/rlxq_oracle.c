@@ -1,0 +1,571 @@
+/*
+ * rlxq_oracle.c -- CPU restatement of rlx-models' quantized-matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see rlxq_oracle.h).  Built with
+ * -ffp-contract=off so that every multiply-add below rounds exactly where the
+ * restated reference code rounds; explicit fmaf() marks the places where the
+ * reference itself calls f32::mul_add.
+ */
+#include "rlxq_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define QK 32
+
+/* ------------------------------------------------------------------------ */
+/* Scalar conversions                                                        */
+/* ------------------------------------------------------------------------ */
+
+static uint32_t f2u(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    return u;
+}
+static float u2f(uint32_t u) {
+    float v;
+    memcpy(&v, &u, 4);
+    return v;
+}
+
+/* IEEE binary32 -> binary16, round to nearest even, with subnormals, the
+ * conversion `half::f16::from_f32` performs (the reference writes every GGUF
+ * scale through it, e.g. crates/rlx-flint/src/quant.rs:91). */
+uint16_t orc_f32_to_f16(float v) {
+    uint32_t x = f2u(v);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) {
+        if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+        return (uint16_t)(sign | 0x7c00u);
+    }
+    uint32_t e = ax >> 23;
+    int he = (int)e - 127 + 15;
+    if (he >= 1) {
+        uint32_t m = ax & 0x7fffffu;
+        uint32_t h = ((uint32_t)he << 10) | (m >> 13);
+        uint32_t rem = m & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+        if (h >= 0x7c00u) h = 0x7c00u;
+        return (uint16_t)(sign | h);
+    }
+    int shift = 126 - (int)e;
+    if (shift > 24) return (uint16_t)sign;
+    uint32_t m = (ax & 0x7fffffu) | 0x800000u;
+    uint32_t h = m >> shift;
+    uint32_t rem = m & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    if (e == 0x1f) return u2f(sign | 0x7f800000u | (m << 13));
+    if (e == 0) {
+        if (m == 0) return u2f(sign);
+        /* subnormal: m * 2^-24, exact in f32 */
+        float v = (float)m * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* f32 -> bf16, round to nearest even, NaN kept quiet (`half::bf16::from_f32`,
+ * crates/rlx-diffusiongemma/tests/real_layer_precision.rs:89-92). */
+uint16_t orc_f32_to_bf16(float v) {
+    uint32_t x = f2u(v);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+    uint32_t lsb = (x >> 16) & 1u;
+    x += 0x7fffu + lsb;
+    return (uint16_t)(x >> 16);
+}
+
+/* bf16 -> f32 is a 16-bit shift (crates/rlx-moshi/src/mlx_dequant.rs:79-81). */
+float orc_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+void orc_f32_to_f16_n(const float* s, int64_t n, uint16_t* d) {
+    for (int64_t i = 0; i < n; i++) d[i] = orc_f32_to_f16(s[i]);
+}
+void orc_f16_to_f32_n(const uint16_t* s, int64_t n, float* d) {
+    for (int64_t i = 0; i < n; i++) d[i] = orc_f16_to_f32(s[i]);
+}
+void orc_f32_to_bf16_n(const float* s, int64_t n, uint16_t* d) {
+    for (int64_t i = 0; i < n; i++) d[i] = orc_f32_to_bf16(s[i]);
+}
+void orc_bf16_to_f32_n(const uint16_t* s, int64_t n, float* d) {
+    for (int64_t i = 0; i < n; i++) d[i] = orc_bf16_to_f32(s[i]);
+}
+
+static float rd_f16(const uint8_t* p) { return orc_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+static void wr_f16(uint8_t* p, float v) {
+    uint16_t h = orc_f32_to_f16(v);
+    p[0] = (uint8_t)(h & 0xff);
+    p[1] = (uint8_t)(h >> 8);
+}
+
+/* ------------------------------------------------------------------------ */
+/* GGUF legacy block codecs                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Block sizes: Q8_0 = f16 d + 32 x i8 (crates/rlx-flint/src/quant.rs:72-77),
+ * Q4_0 = f16 d + 16 nibble bytes (same lines), Q4_1 = f16 d + f16 m + 16
+ * nibble bytes (GGML block_q4_1; QuantScheme::GgufQ4_1,
+ * crates/rlx-models-core/src/weight_loader.rs:508). */
+int64_t orc_block_bytes(int scheme) {
+    switch (scheme) {
+        case ORC_GGUF_Q8_0: return 2 + QK;
+        case ORC_GGUF_Q4_0: return 2 + QK / 2;
+        case ORC_GGUF_Q4_1: return 4 + QK / 2;
+        default: return -1;
+    }
+}
+
+int64_t orc_row_bytes(int scheme, int64_t k) {
+    int64_t bb = orc_block_bytes(scheme);
+    if (bb < 0 || k % QK) return -1;
+    return k / QK * bb;
+}
+
+/* Rust `f32::round`: half away from zero (C roundf). */
+static float rnd_away(float v) { return roundf(v); }
+
+/* Q8_0 encoder: crates/rlx-flint/src/quant.rs:86-95. */
+static void quant_q8_0_block(const float* x, uint8_t* out) {
+    float amax = 0.f;
+    for (int i = 0; i < QK; i++) {
+        float a = fabsf(x[i]);
+        if (a > amax) amax = a;
+    }
+    float d = amax / 127.0f;
+    float inv = d == 0.0f ? 0.0f : 1.0f / d;
+    wr_f16(out, d);
+    for (int i = 0; i < QK; i++) {
+        float q = rnd_away(x[i] * inv);
+        if (q < -127.f) q = -127.f;
+        if (q > 127.f) q = 127.f;
+        out[2 + i] = (uint8_t)(int8_t)q;
+    }
+}
+
+/* Q4_0 encoder: crates/rlx-flint/src/quant.rs:97-110 (signed extreme, d =
+ * max / -8, q = (v*inv + 8.5) truncated, clamped to 0..15). */
+static void quant_q4_0_block(const float* x, uint8_t* out) {
+    float mx = 0.f;
+    for (int i = 0; i < QK; i++)
+        if (fabsf(x[i]) > fabsf(mx)) mx = x[i];
+    float d = mx / -8.0f;
+    float inv = d == 0.0f ? 0.0f : 1.0f / d;
+    wr_f16(out, d);
+    for (int j = 0; j < QK / 2; j++) {
+        float a = x[j] * inv + 8.5f, b = x[j + QK / 2] * inv + 8.5f;
+        int qa = (int)a, qb = (int)b; /* truncation toward zero, as `as i32` */
+        qa = qa < 0 ? 0 : (qa > 15 ? 15 : qa);
+        qb = qb < 0 ? 0 : (qb > 15 ? 15 : qb);
+        out[2 + j] = (uint8_t)(qa | (qb << 4));
+    }
+}
+
+/* Q4_1 encoder: min/max rule of
+ * crates/rlx-diffusiongemma/tests/real_layer_precision.rs:129-146 (d = (max -
+ * min) / 15, q = floor((x - min)*id + 0.5) clamped to 15), stored as GGML
+ * block_q4_1: f16 d, f16 min, byte j = q[j] | q[j+16] << 4. */
+static void quant_q4_1_block(const float* x, uint8_t* out) {
+    float mn = INFINITY, mx = -INFINITY;
+    for (int i = 0; i < QK; i++) {
+        if (x[i] < mn) mn = x[i];
+        if (x[i] > mx) mx = x[i];
+    }
+    float d = (mx - mn) / 15.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    wr_f16(out, d);
+    wr_f16(out + 2, mn);
+    for (int j = 0; j < QK / 2; j++) {
+        int qa = (int)floorf((x[j] - mn) * id + 0.5f);
+        int qb = (int)floorf((x[j + QK / 2] - mn) * id + 0.5f);
+        qa = qa < 0 ? 0 : (qa > 15 ? 15 : qa);
+        qb = qb < 0 ? 0 : (qb > 15 ? 15 : qb);
+        out[4 + j] = (uint8_t)(qa | (qb << 4));
+    }
+}
+
+int orc_quantize(int scheme, const float* src, int64_t n, uint8_t* dst) {
+    int64_t bb = orc_block_bytes(scheme);
+    if (bb < 0 || n % QK) return -1;
+    for (int64_t b = 0; b < n / QK; b++) {
+        const float* x = src + b * QK;
+        uint8_t* o = dst + b * bb;
+        if (scheme == ORC_GGUF_Q8_0) quant_q8_0_block(x, o);
+        else if (scheme == ORC_GGUF_Q4_0) quant_q4_0_block(x, o);
+        else quant_q4_1_block(x, o);
+    }
+    return 0;
+}
+
+/* Dequantize one block into 32 floats.
+ *  Q8_0: w = d * q (crates/rlx-flint/src/quant.rs:124-127);
+ *  Q4_0: w[j] = d*((b&15)-8), w[j+16] = d*((b>>4)-8) (quant.rs:128-135);
+ *  Q4_1: w = d*q + m (GGML dequantize_row_q4_1; every product d*q is exact
+ *        in f32, so the one rounding is on the add). */
+static void dequant_block(int scheme, const uint8_t* b, float* o) {
+    float d = rd_f16(b);
+    if (scheme == ORC_GGUF_Q8_0) {
+        for (int i = 0; i < QK; i++) o[i] = d * (float)(int8_t)b[2 + i];
+    } else if (scheme == ORC_GGUF_Q4_0) {
+        for (int j = 0; j < QK / 2; j++) {
+            o[j] = d * (float)((int)(b[2 + j] & 0x0f) - 8);
+            o[j + QK / 2] = d * (float)((int)(b[2 + j] >> 4) - 8);
+        }
+    } else {
+        float m = rd_f16(b + 2);
+        for (int j = 0; j < QK / 2; j++) {
+            o[j] = d * (float)(b[4 + j] & 0x0f) + m;
+            o[j + QK / 2] = d * (float)(b[4 + j] >> 4) + m;
+        }
+    }
+}
+
+int orc_dequantize(int scheme, const uint8_t* src, int64_t n, float* dst) {
+    int64_t bb = orc_block_bytes(scheme);
+    if (bb < 0 || n % QK) return -1;
+    for (int64_t b = 0; b < n / QK; b++) dequant_block(scheme, src + b * bb, dst + b * QK);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MLX affine                                                                */
+/* ------------------------------------------------------------------------ */
+
+/* pack_codes, crates/rlx-laguna/src/mlx_affine.rs:272-288: `bits`-wide codes
+ * LSB-first, 32/bits per u32, contiguous per row. */
+int orc_mlx_pack(const uint32_t* codes, int64_t rows, int64_t cols, int bits,
+                 uint32_t* dst) {
+    if (bits != 4 && bits != 8) return -1;
+    int per = 32 / bits;
+    if (cols % per) return -1;
+    uint32_t mask = (1u << bits) - 1u;
+    int64_t wpr = cols / per;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t w = 0; w < wpr; w++) {
+            uint32_t word = 0;
+            for (int j = 0; j < per; j++)
+                word |= (codes[r * cols + w * per + j] & mask) << (j * bits);
+            dst[r * wpr + w] = word;
+        }
+    return 0;
+}
+
+/* dequantize_affine, crates/rlx-moshi/src/mlx_dequant.rs:12-76: code s of a
+ * word sits at bits [s*bits, (s+1)*bits); w = scale*code + bias (a multiply
+ * rounded, then an add rounded -- no fused multiply-add). */
+int orc_mlx_dequantize(const uint32_t* wq, const float* scales,
+                       const float* biases, int64_t rows, int64_t cols,
+                       int bits, int group, float* dst) {
+    if (bits != 4 && bits != 8) return -1;
+    if (group <= 0 || cols % group) return -1;
+    int per = 32 / bits;
+    if (cols % per) return -1;
+    uint32_t mask = (1u << bits) - 1u;
+    int64_t wpr = cols / per, ng = cols / group;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t c = 0; c < cols; c++) {
+            uint32_t word = wq[r * wpr + c / per];
+            float code = (float)((word >> ((c % per) * bits)) & mask);
+            int64_t g = c / group;
+            float prod = scales[r * ng + g] * code;
+            dst[r * cols + c] = prod + biases[r * ng + g];
+        }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Dense matmul                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* y = x . W^T with W [n, k] row-major (host_matmul_t,
+ * crates/rlx-unlimited-ocr/tests/quant_parity_backends.rs:74-86), evaluated
+ * on the dequantized weights in double. */
+int orc_matmul_f64(int scheme, const float* x, const uint8_t* w, int64_t m,
+                   int64_t k, int64_t n, double* y) {
+    int64_t rb = orc_row_bytes(scheme, k);
+    if (rb < 0) return -1;
+    float* row = (float*)malloc(sizeof(float) * (size_t)k);
+    if (!row) return -2;
+    for (int64_t j = 0; j < n; j++) {
+        orc_dequantize(scheme, w + j * rb, k, row);
+        for (int64_t r = 0; r < m; r++) {
+            double acc = 0.0;
+            const float* xr = x + r * k;
+            for (int64_t i = 0; i < k; i++) acc += (double)xr[i] * (double)row[i];
+            y[r * n + j] = acc;
+        }
+    }
+    free(row);
+    return 0;
+}
+
+/* One output element in the reference's block-dot order.
+ * Q8_0: crates/rlx-flint/src/quant.rs:250-268; Q4_0: quant.rs:272-292.
+ * Q4_1 has no in-tree restatement; it uses the Q4_0 loop shape with the
+ * unsigned code and adds m * sum(x) for the block. */
+static float dot_refl(int scheme, const float* x, const uint8_t* row, int64_t k) {
+    int64_t bb = orc_block_bytes(scheme);
+    float sum = 0.f;
+    for (int64_t b = 0; b < k / QK; b++) {
+        const float* xs = x + b * QK;
+        const uint8_t* blk = row + b * bb;
+        float d = rd_f16(blk);
+        if (scheme == ORC_GGUF_Q8_0) {
+            float acc[8] = {0};
+            for (int l = 0; l < QK / 8; l++)
+                for (int i = 0; i < 8; i++)
+                    acc[i] = fmaf(xs[l * 8 + i], (float)(int8_t)blk[2 + l * 8 + i], acc[i]);
+            float s = 0.f;
+            for (int i = 0; i < 8; i++) s += acc[i];
+            sum = fmaf(d, s, sum);
+        } else if (scheme == ORC_GGUF_Q4_0) {
+            float acc[16] = {0};
+            for (int j = 0; j < QK / 2; j++) {
+                int lo = (blk[2 + j] & 0x0f) - 8, hi = (blk[2 + j] >> 4) - 8;
+                acc[j] = fmaf(xs[j], (float)lo, acc[j]);
+                acc[j] = fmaf(xs[j + QK / 2], (float)hi, acc[j]);
+            }
+            float s = 0.f;
+            for (int i = 0; i < 16; i++) s += acc[i];
+            sum = fmaf(d, s, sum);
+        } else {
+            float mm = rd_f16(blk + 2);
+            float acc[16] = {0};
+            float xsum = 0.f;
+            for (int j = 0; j < QK / 2; j++) {
+                int lo = blk[4 + j] & 0x0f, hi = blk[4 + j] >> 4;
+                acc[j] = fmaf(xs[j], (float)lo, acc[j]);
+                acc[j] = fmaf(xs[j + QK / 2], (float)hi, acc[j]);
+            }
+            for (int i = 0; i < QK; i++) xsum += xs[i];
+            float s = 0.f;
+            for (int i = 0; i < 16; i++) s += acc[i];
+            sum = fmaf(d, s, sum);
+            sum = fmaf(mm, xsum, sum);
+        }
+    }
+    return sum;
+}
+
+int orc_matmul_refl(int scheme, const float* x, const uint8_t* w, int64_t m,
+                    int64_t k, int64_t n, float* y) {
+    int64_t rb = orc_row_bytes(scheme, k);
+    if (rb < 0) return -1;
+    for (int64_t r = 0; r < m; r++)
+        for (int64_t j = 0; j < n; j++) y[r * n + j] = dot_refl(scheme, x + r * k, w + j * rb, k);
+    return 0;
+}
+
+/* Output rows split over threads like gguf_matmul_bt_parallel's rayon
+ * partition (call site crates/rlx-laguna/src/packed_forward.rs:226-241). */
+int orc_matmul_refl_par(int scheme, const float* x, const uint8_t* w,
+                        int64_t m, int64_t k, int64_t n, float* y,
+                        int nthreads) {
+    int64_t rb = orc_row_bytes(scheme, k);
+    if (rb < 0) return -1;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int64_t j = 0; j < n; j++)
+        for (int64_t r = 0; r < m; r++) y[r * n + j] = dot_refl(scheme, x + r * k, w + j * rb, k);
+    (void)nthreads;
+    return 0;
+}
+
+int orc_mlx_matmul_f64(const float* x, const uint32_t* wq, const float* scales,
+                       const float* biases, int64_t m, int64_t k, int64_t n,
+                       int bits, int group, double* y) {
+    float* wd = (float*)malloc(sizeof(float) * (size_t)(n * k));
+    if (!wd) return -2;
+    int rc = orc_mlx_dequantize(wq, scales, biases, n, k, bits, group, wd);
+    if (rc) {
+        free(wd);
+        return rc;
+    }
+    for (int64_t r = 0; r < m; r++)
+        for (int64_t j = 0; j < n; j++) {
+            double acc = 0.0;
+            for (int64_t i = 0; i < k; i++) acc += (double)x[r * k + i] * (double)wd[j * k + i];
+            y[r * n + j] = acc;
+        }
+    free(wd);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Grouped experts and MoE                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* crates/rlx-unlimited-ocr/tests/quant_parity_backends.rs:268-281: expert e
+ * is bank rows e*N..(e+1)*N; row r uses expert e[r]. */
+int orc_grouped_matmul_f64(int scheme, const float* x, const uint8_t* bank,
+                           const float* expert_idx, int64_t rows, int64_t k,
+                           int64_t n, int64_t num_experts, double* y) {
+    int64_t rb = orc_row_bytes(scheme, k);
+    if (rb < 0) return -1;
+    for (int64_t r = 0; r < rows; r++) {
+        float ef = expert_idx[r];
+        int64_t e = (int64_t)ef;
+        if (!(ef >= 0.f) || e >= num_experts || (float)e != ef) return -3;
+        int rc = orc_matmul_f64(scheme, x + r * k, bank + e * n * rb, 1, k, n, y + r * n);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+/* topk_softmax, crates/rlx-unlimited-ocr/src/nn.rs:371-379 (softmax, sort by
+ * probability descending, keep k); optional renormalisation of the kept
+ * probabilities, crates/rlx-models-core/src/standard_decoder.rs:12657-12661. */
+int orc_topk_softmax(const float* logits, int64_t rows, int64_t e, int64_t k,
+                     int renorm, int32_t* ids, float* probs) {
+    if (k <= 0 || k > e) return -1;
+    float* p = (float*)malloc(sizeof(float) * (size_t)e);
+    unsigned char* used = (unsigned char*)malloc((size_t)e);
+    if (!p || !used) {
+        free(p);
+        free(used);
+        return -2;
+    }
+    for (int64_t r = 0; r < rows; r++) {
+        const float* l = logits + r * e;
+        float mx = -INFINITY;
+        for (int64_t i = 0; i < e; i++)
+            if (l[i] > mx) mx = l[i];
+        float s = 0.f;
+        for (int64_t i = 0; i < e; i++) {
+            p[i] = expf(l[i] - mx);
+            s += p[i];
+        }
+        for (int64_t i = 0; i < e; i++) p[i] /= s;
+        memset(used, 0, (size_t)e);
+        float kept = 0.f;
+        for (int64_t j = 0; j < k; j++) {
+            int64_t best = -1;
+            for (int64_t i = 0; i < e; i++)
+                if (!used[i] && (best < 0 || p[i] > p[best])) best = i;
+            used[best] = 1;
+            ids[r * k + j] = (int32_t)best;
+            probs[r * k + j] = p[best];
+            kept += p[best];
+        }
+        if (renorm)
+            for (int64_t j = 0; j < k; j++) probs[r * k + j] /= kept;
+    }
+    free(p);
+    free(used);
+    return 0;
+}
+
+/* quant_parity_backends.rs:360-373: for each (row, slot) the expert's
+ * product, weighted by its probability, accumulated over the slots. */
+int orc_moe_f64(int scheme, const float* x, const uint8_t* bank,
+                const int32_t* ids, const float* probs, int64_t rows,
+                int64_t topk, int64_t k, int64_t n, int64_t num_experts,
+                double* y) {
+    int64_t rb = orc_row_bytes(scheme, k);
+    if (rb < 0) return -1;
+    double* tmp = (double*)malloc(sizeof(double) * (size_t)n);
+    if (!tmp) return -2;
+    for (int64_t i = 0; i < rows * n; i++) y[i] = 0.0;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t j = 0; j < topk; j++) {
+            int32_t e = ids[r * topk + j];
+            if (e < 0 || e >= num_experts) {
+                free(tmp);
+                return -3;
+            }
+            orc_matmul_f64(scheme, x + r * k, bank + (int64_t)e * n * rb, 1, k, n, tmp);
+            double pr = probs[r * topk + j];
+            for (int64_t c = 0; c < n; c++) y[r * n + c] += pr * tmp[c];
+        }
+    free(tmp);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* int8                                                                      */
+/* ------------------------------------------------------------------------ */
+
+int orc_quantize_act_int8(const float* x, int64_t rows, int64_t cols,
+                          int8_t* q, float* scales) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float* row = x + r * cols;
+        float amax = 0.f;
+        for (int64_t c = 0; c < cols; c++) {
+            float a = fabsf(row[c]);
+            if (a > amax) amax = a;
+        }
+        float s = amax > 0.f ? amax / 127.0f : 1.0f;
+        float inv = 1.0f / s;
+        for (int64_t c = 0; c < cols; c++) {
+            float v = rnd_away(row[c] * inv);
+            if (v < -127.f) v = -127.f;
+            if (v > 127.f) v = 127.f;
+            q[r * cols + c] = (int8_t)v;
+        }
+        scales[r] = s;
+    }
+    return 0;
+}
+
+int orc_quantize_int8_col(const float* w, int64_t k, int64_t n, int8_t* q,
+                          float* scales) {
+    for (int64_t c = 0; c < n; c++) {
+        float amax = 0.f;
+        for (int64_t r = 0; r < k; r++) {
+            float a = fabsf(w[r * n + c]);
+            if (a > amax) amax = a;
+        }
+        float s = amax > 0.f ? amax / 127.0f : 1.0f;
+        scales[c] = s;
+        for (int64_t r = 0; r < k; r++) {
+            float v = rnd_away(w[r * n + c] / s);
+            if (v < -127.f) v = -127.f;
+            if (v > 127.f) v = 127.f;
+            q[r * n + c] = (int8_t)v;
+        }
+    }
+    return 0;
+}
+
+/* y = acc * sx[m] * sw[n], acc the exact int32 dot; the two scale products
+ * are applied as (acc * sx) * sw in f32. */
+int orc_w8a8_matmul(const int8_t* qx, const float* sx, const int8_t* qw,
+                    const float* sw, int64_t m, int64_t k, int64_t n,
+                    float* y) {
+    for (int64_t r = 0; r < m; r++)
+        for (int64_t c = 0; c < n; c++) {
+            int64_t acc = 0;
+            for (int64_t i = 0; i < k; i++) acc += (int64_t)qx[r * k + i] * (int64_t)qw[i * n + c];
+            y[r * n + c] = ((float)acc * sx[r]) * sw[c];
+        }
+    return 0;
+}
+
+int orc_int8_block_matmul_f64(const float* x, const int8_t* wq,
+                              const float* scale, const float* zp, int64_t m,
+                              int64_t k, int64_t n, double* y) {
+    for (int64_t r = 0; r < m; r++)
+        for (int64_t c = 0; c < n; c++) {
+            double acc = 0.0;
+            for (int64_t i = 0; i < k; i++) {
+                float wv = ((float)wq[i * n + c] - zp[c]) * scale[c];
+                acc += (double)x[r * k + i] * (double)wv;
+            }
+            y[r * n + c] = acc;
+        }
+    return 0;
+}

@@ -1,0 +1,113 @@
+"""Builds librlxq.so (gfx950 code objects embedded) and the CPU oracle.
+
+    python rlx-models_amd/build.py            # everything
+    python rlx-models_amd/build.py --no-oracle
+
+Outputs (git-ignored, they travel with the tree to the GPU box):
+    rlx-models_amd/lib/librlxq.so        the product: C ABI of include/rlxq.h
+    rlx-models_amd/lib/co/*.co           intermediate gfx950 code objects
+    oracle/liboracle.so                  CPU restatement (tests/bench only)
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+KDIR = PKG / "csrc" / "kernels"
+HDIR = PKG / "csrc" / "host"
+LIB = PKG / "lib"
+CO = LIB / "co"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+HIPCC = str(ROCM / "bin" / "hipcc")
+
+# Code objects the host library embeds (rlxq.cpp RLXQ_EMBED lines).  A name
+# without a source file is embedded empty and skipped at load time.
+CODE_OBJECTS = ("gemv", "misc", "gemm", "moe")
+
+HIP_FLAGS = [
+    "--genco", "--offload-arch=gfx950", "-O3", "-std=c++17",
+    # No packed fp32 arithmetic (v_pk_*_f32) in any kernel: its forms have
+    # given silent wrong results on this hardware pool.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd: list[str], what: str) -> None:
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"{what} failed ({r.returncode}):\n{' '.join(cmd)}\n{out}")
+
+
+def build_code_objects() -> None:
+    CO.mkdir(parents=True, exist_ok=True)
+    jobs = []
+    for name in CODE_OBJECTS:
+        src = KDIR / f"{name}.hip"
+        dst = CO / f"{name}.co"
+        if not src.exists():
+            dst.write_bytes(b"")
+            continue
+        jobs.append((name, [HIPCC, *HIP_FLAGS, "-I", str(KDIR), str(src), "-o", str(dst)]))
+    with cf.ThreadPoolExecutor(max_workers=min(8, max(1, len(jobs)))) as ex:
+        futs = [ex.submit(_run, cmd, f"hipcc {name}") for name, cmd in jobs]
+        for f in futs:
+            f.result()
+
+
+def build_host() -> Path:
+    LIB.mkdir(parents=True, exist_ok=True)
+    out = LIB / "librlxq.so"
+    tmp = LIB / "librlxq.so.tmp"
+    srcs = sorted(str(p) for p in HDIR.glob("*.cpp"))
+    cmd = [
+        "g++", "-std=c++17", "-O2", "-fPIC", "-shared",
+        "-D__HIP_PLATFORM_AMD__", f"-DRLXQ_CO_DIR=\"{CO}\"",
+        "-I", str(ROOT / "include"), "-I", str(HDIR), "-I", str(ROCM / "include"),
+        *srcs, "-o", str(tmp),
+        "-L", str(ROCM / "lib"), "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}",
+        "-Wl,--version-script=" + str(HDIR / "exports.map"),
+    ]
+    _run(cmd, "g++ librlxq")
+    os.replace(tmp, out)
+    return out
+
+
+def build_oracle() -> Path:
+    odir = ROOT / "oracle"
+    out = odir / "liboracle.so"
+    tmp = odir / "liboracle.so.tmp"
+    # -ffp-contract=off keeps every multiply-add rounded where the restated
+    # reference rounds; x86-64-v3 (AVX2 + FMA) so fmaf() is one instruction on
+    # any host the GPU box may have.
+    cmd = ["gcc", "-std=c11", "-O3", "-march=x86-64-v3", "-ffp-contract=off", "-fopenmp",
+           "-fPIC", "-shared", str(odir / "rlxq_oracle.c"), "-o", str(tmp), "-lm"]
+    _run(cmd, "gcc liboracle")
+    os.replace(tmp, out)
+    return out
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--no-oracle", action="store_true")
+    ap.add_argument("--host-only", action="store_true", help="relink librlxq.so from existing code objects")
+    a = ap.parse_args(argv)
+    if shutil.which("g++") is None or not Path(HIPCC).exists():
+        raise RuntimeError("need g++ and hipcc")
+    if not a.host_only:
+        build_code_objects()
+    build_host()
+    if not a.no_oracle:
+        build_oracle()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

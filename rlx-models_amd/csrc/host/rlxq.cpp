@@ -1,0 +1,246 @@
+// librlxq: context, code-object loading, argument validation and the C ABI
+// entry points of include/rlxq.h.
+//
+// The gfx950 code objects are assembled into this shared library at build
+// time (.incbin) and loaded with hipModuleLoadData; kernels are launched with
+// hipModuleLaunchKernel.  Nothing here allocates on the hot path except the
+// context scratch, which grows once to the largest size a call has needed.
+#include <hip/hip_runtime_api.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "rlxq.h"
+#include "rlxq_internal.hpp"
+
+#ifndef RLXQ_CO_DIR
+#error "RLXQ_CO_DIR must name the directory holding the built code objects"
+#endif
+
+#define RLXQ_EMBED(sym, file)                                                                  \
+  asm(".pushsection .rodata." #sym ",\"a\",@progbits\n"                                        \
+      ".balign 64\n"                                                                           \
+      ".globl " #sym "_begin\n"                                                                \
+      ".hidden " #sym "_begin\n" #sym "_begin:\n"                                              \
+      ".incbin \"" RLXQ_CO_DIR "/" file "\"\n"                                                 \
+      ".globl " #sym "_end\n"                                                                  \
+      ".hidden " #sym "_end\n" #sym "_end:\n"                                                  \
+      ".byte 0\n"                                                                              \
+      ".popsection\n");                                                                        \
+  extern "C" __attribute__((visibility("hidden"))) const unsigned char sym##_begin[];         \
+  extern "C" __attribute__((visibility("hidden"))) const unsigned char sym##_end[];
+
+RLXQ_EMBED(rlxq_co_gemv, "gemv.co")
+RLXQ_EMBED(rlxq_co_misc, "misc.co")
+RLXQ_EMBED(rlxq_co_gemm, "gemm.co")
+RLXQ_EMBED(rlxq_co_moe, "moe.co")
+
+namespace {
+
+struct Image {
+  const unsigned char* begin;
+  const unsigned char* end;
+  const char* name;
+};
+
+const Image kImages[] = {
+    {rlxq_co_gemv_begin, rlxq_co_gemv_end, "gemv"},
+    {rlxq_co_misc_begin, rlxq_co_misc_end, "misc"},
+    {rlxq_co_gemm_begin, rlxq_co_gemm_end, "gemm"},
+    {rlxq_co_moe_begin, rlxq_co_moe_end, "moe"},
+};
+
+std::string hip_msg(hipError_t e) { return std::string(hipGetErrorName(e)) + ": " + hipGetErrorString(e); }
+
+}  // namespace
+
+namespace rlxq {
+
+int fail(rlxq_ctx* ctx, int code, const std::string& msg) {
+  if (ctx) ctx->last_error = msg;
+  return code;
+}
+
+DeviceGuard::DeviceGuard(int dev) {
+  if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+  if (prev_ == dev) {
+    ok_ = true;
+    return;
+  }
+  ok_ = hipSetDevice(dev) == hipSuccess;
+}
+
+DeviceGuard::~DeviceGuard() {
+  int cur = -1;
+  if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_) (void)hipSetDevice(prev_);
+}
+
+int get_fn(rlxq_ctx* ctx, const std::string& name, hipFunction_t* out) {
+  auto it = ctx->fn_cache.find(name);
+  if (it != ctx->fn_cache.end()) {
+    *out = it->second;
+    return RLXQ_OK;
+  }
+  for (hipModule_t m : ctx->modules) {
+    hipFunction_t f = nullptr;
+    if (hipModuleGetFunction(&f, m, name.c_str()) == hipSuccess && f) {
+      ctx->fn_cache.emplace(name, f);
+      *out = f;
+      return RLXQ_OK;
+    }
+    // A miss in one module is expected; do not leave it as the thread's
+    // last HIP error for the caller's runtime to report later.
+    (void)hipGetLastError();
+  }
+  return fail(ctx, RLXQ_E_NOKERNEL, "kernel not found in the gfx950 code objects: " + name);
+}
+
+int launch(rlxq_ctx* ctx, hipFunction_t fn, dim3 grid, dim3 block, size_t lds, void* stream,
+           void** args, const char* what) {
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return RLXQ_OK;
+  if (lds > ctx->max_lds)
+    return fail(ctx, RLXQ_E_SHAPE,
+                std::string(what) + ": needs " + std::to_string(lds) + " B of LDS, device has " +
+                    std::to_string(ctx->max_lds));
+  hipError_t e = hipModuleLaunchKernel(fn, grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                                       (unsigned)lds, (hipStream_t)stream, args, nullptr);
+  if (e != hipSuccess) return fail(ctx, RLXQ_E_HIP, std::string(what) + ": launch failed: " + hip_msg(e));
+  return RLXQ_OK;
+}
+
+int workspace(rlxq_ctx* ctx, size_t bytes, void** out) {
+  if (bytes <= ctx->ws_bytes) {
+    *out = ctx->ws;
+    return RLXQ_OK;
+  }
+  // Growing frees the old buffer, which other streams may still use: wait.
+  if (ctx->ws) {
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return fail(ctx, RLXQ_E_HIP, "workspace: sync: " + hip_msg(e));
+    (void)hipFree(ctx->ws);
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+  }
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  want = (want + 4095) & ~size_t(4095);
+  hipError_t e = hipMalloc(&ctx->ws, want);
+  if (e != hipSuccess) {
+    ctx->ws = nullptr;
+    return fail(ctx, RLXQ_E_NOMEM, "workspace: hipMalloc(" + std::to_string(want) + "): " + hip_msg(e));
+  }
+  ctx->ws_bytes = want;
+  *out = ctx->ws;
+  return RLXQ_OK;
+}
+
+bool is_gguf(int s) { return s == RLXQ_GGUF_Q8_0 || s == RLXQ_GGUF_Q4_0 || s == RLXQ_GGUF_Q4_1; }
+bool is_mlx(int s) { return s == RLXQ_MLX_AFFINE4 || s == RLXQ_MLX_AFFINE8; }
+
+int64_t gguf_block_bytes(int s) {
+  switch (s) {
+    case RLXQ_GGUF_Q8_0: return 34;
+    case RLXQ_GGUF_Q4_0: return 18;
+    case RLXQ_GGUF_Q4_1: return 20;
+    default: return -1;
+  }
+}
+
+}  // namespace rlxq
+
+using namespace rlxq;
+
+extern "C" {
+
+const char* rlxq_version(void) { return "rlxq 0.1.0 gfx950"; }
+
+const char* rlxq_strerror(int s) {
+  switch (s) {
+    case RLXQ_OK: return "ok";
+    case RLXQ_E_NULL: return "null pointer";
+    case RLXQ_E_SHAPE: return "bad shape";
+    case RLXQ_E_SCHEME: return "unsupported scheme";
+    case RLXQ_E_ALIGN: return "misaligned pointer or K";
+    case RLXQ_E_DTYPE: return "unsupported dtype";
+    case RLXQ_E_HIP: return "HIP runtime error";
+    case RLXQ_E_NOMEM: return "out of memory";
+    case RLXQ_E_INDEX: return "expert index out of range";
+    case RLXQ_E_NOKERNEL: return "kernel variant not available";
+    case RLXQ_E_DEVICE: return "device is not gfx950";
+    default: return "unknown status";
+  }
+}
+
+const char* rlxq_last_error(const rlxq_ctx* ctx) { return ctx ? ctx->last_error.c_str() : ""; }
+
+int64_t rlxq_row_bytes(int scheme, int64_t k) {
+  int64_t bb = gguf_block_bytes(scheme);
+  if (bb < 0 || k <= 0 || k % 32) return -1;
+  return k / 32 * bb;
+}
+
+int rlxq_init(int device, rlxq_ctx** out) {
+  if (!out) return RLXQ_E_NULL;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) {
+    (void)hipGetLastError();
+    return RLXQ_E_DEVICE;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return RLXQ_E_HIP;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return RLXQ_E_DEVICE;
+  DeviceGuard g(device);
+  if (!g.ok()) return RLXQ_E_HIP;
+  rlxq_ctx* ctx = new (std::nothrow) rlxq_ctx();
+  if (!ctx) return RLXQ_E_NOMEM;
+  ctx->device = device;
+  ctx->cu_count = prop.multiProcessorCount;
+  ctx->max_lds = prop.sharedMemPerBlock;
+  for (const Image& im : kImages) {
+    if (im.end - im.begin <= 1) continue;  // component not built into this library
+    hipModule_t m = nullptr;
+    hipError_t e = hipModuleLoadData(&m, im.begin);
+    if (e != hipSuccess) {
+      std::fprintf(stderr, "rlxq: hipModuleLoadData(%s): %s\n", im.name, hip_msg(e).c_str());
+      for (hipModule_t mm : ctx->modules) (void)hipModuleUnload(mm);
+      delete ctx;
+      return RLXQ_E_HIP;
+    }
+    ctx->modules.push_back(m);
+  }
+  *out = ctx;
+  return RLXQ_OK;
+}
+
+int rlxq_destroy(rlxq_ctx* ctx) {
+  if (!ctx) return RLXQ_E_NULL;
+  {
+    DeviceGuard g(ctx->device);
+    if (ctx->ws) {
+      (void)hipDeviceSynchronize();
+      (void)hipFree(ctx->ws);
+    }
+    for (hipModule_t m : ctx->modules) (void)hipModuleUnload(m);
+  }
+  delete ctx;
+  return RLXQ_OK;
+}
+
+int rlxq_dequant_matmul(rlxq_ctx* ctx, int scheme, int group_size, const void* x, int x_dtype,
+                        const void* w, const void* scales, const void* biases, int sb_dtype,
+                        int64_t m, int64_t k, int64_t n, void* y, int y_dtype, void* stream) {
+  if (!ctx) return RLXQ_E_NULL;
+  ctx->last_error.clear();
+  if (!x || !w || !y) return fail(ctx, RLXQ_E_NULL, "dequant_matmul: x, w and y must be non-null");
+  if (m < 0 || k <= 0 || n < 0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: need m >= 0, k > 0, n >= 0");
+  if (x_dtype != RLXQ_F32 && x_dtype != RLXQ_BF16) return fail(ctx, RLXQ_E_DTYPE, "dequant_matmul: x_dtype");
+  if (y_dtype != RLXQ_F32 && y_dtype != RLXQ_BF16) return fail(ctx, RLXQ_E_DTYPE, "dequant_matmul: y_dtype");
+  if (m == 0 || n == 0) return RLXQ_OK;
+  DeviceGuard g(ctx->device);
+  if (!g.ok()) return fail(ctx, RLXQ_E_HIP, "dequant_matmul: hipSetDevice");
+  return gemv_dispatch(ctx, scheme, group_size, x, x_dtype, w, scales, biases, sb_dtype, m, k, n, y,
+                       y_dtype, stream);
+}
+
+}  // extern "C"

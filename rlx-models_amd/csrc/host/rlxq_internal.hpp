@@ -1,0 +1,62 @@
+// Internal declarations shared by the host-side translation units of librlxq.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "rlxq.h"
+
+struct rlxq_ctx {
+  int device = 0;
+  std::vector<hipModule_t> modules;
+  std::unordered_map<std::string, hipFunction_t> fn_cache;
+  std::string last_error;
+  int cu_count = 0;
+  size_t max_lds = 65536;
+  // Library-owned scratch (routing tables, quantised activations, split-K
+  // partials).  Grown on demand; freed by rlxq_destroy.
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+};
+
+namespace rlxq {
+
+// Records `msg` as the context's last error and returns `code`.
+int fail(rlxq_ctx* ctx, int code, const std::string& msg);
+
+// Sets the context's device current for the lifetime of the guard.
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int dev);
+  ~DeviceGuard();
+  bool ok() const { return ok_; }
+
+ private:
+  int prev_ = -1;
+  bool ok_ = false;
+};
+
+// Looks a kernel up by name across the loaded code objects.
+int get_fn(rlxq_ctx* ctx, const std::string& name, hipFunction_t* out);
+
+// Launches `fn` with the kernelParams array `args`.
+int launch(rlxq_ctx* ctx, hipFunction_t fn, dim3 grid, dim3 block, size_t lds, void* stream,
+           void** args, const char* what);
+
+// Ensures at least `bytes` of context scratch; returns its device pointer.
+int workspace(rlxq_ctx* ctx, size_t bytes, void** out);
+
+bool is_gguf(int scheme);
+bool is_mlx(int scheme);
+int64_t gguf_block_bytes(int scheme);
+
+// Entry points implemented in other translation units.
+int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dtype, const void* w,
+                  const void* scales, const void* biases, int sb_dtype, int64_t m, int64_t k,
+                  int64_t n, void* y, int y_dtype, void* stream);
+
+}  // namespace rlxq

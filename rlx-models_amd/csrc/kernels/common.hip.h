@@ -1,0 +1,78 @@
+// Device-side helpers shared by the gfx950 kernels of librlxq.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define RLXQ_DEV __device__ __forceinline__
+
+typedef __bf16 rlxq_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 rlxq_f16x2_t __attribute__((ext_vector_type(2)));
+
+// Scheme ids (same numbering as include/rlxq.h).
+enum : int {
+  SCH_Q8_0 = 1,
+  SCH_Q4_0 = 2,
+  SCH_Q4_1 = 3,
+  SCH_MLX4 = 4,
+  SCH_MLX8 = 5,
+};
+
+// D = a.lo*b.lo + a.hi*b.hi + c with bf16 pairs and an f32 accumulator
+// (v_dot2c_f32_bf16).  Products of two bf16 values are exact in f32.
+RLXQ_DEV float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(rlxq_bf16x2_t, a),
+                                         __builtin_bit_cast(rlxq_bf16x2_t, b), c, false);
+}
+
+// Same with f16 pairs (v_dot2c_f32_f16).  Products of two f16 values are
+// exact in f32.
+RLXQ_DEV float dot2_f16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(rlxq_f16x2_t, a),
+                                __builtin_bit_cast(rlxq_f16x2_t, b), c, false);
+}
+
+RLXQ_DEV float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+
+// f32 -> bf16 bits, round to nearest even (NaN kept quiet).
+RLXQ_DEV uint32_t f32_to_bf16_bits(float v) {
+  uint32_t x = __float_as_uint(v);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (x >> 16) | 0x40u;
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return x >> 16;
+}
+
+RLXQ_DEV float f16_bits_to_f32(uint32_t h16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+// f32 -> f16 bits with the hardware conversion (round to nearest even).
+RLXQ_DEV uint32_t f32_to_f16_bits(float v) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// 32-bit byte funnel: bytes [s, s+4) of the 8-byte value hi:lo.
+RLXQ_DEV uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
+  return __builtin_amdgcn_alignbyte(hi, lo, s);
+}
+
+RLXQ_DEV uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+template <int WIDTH>
+RLXQ_DEV float group_sum(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Global loads.  GGUF blocks are 18/20/34 bytes, so a 16-byte load is only
+// dword aligned; the vector type says so (global_load_dwordx4 needs 4).
+typedef uint32_t rlxq_u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+RLXQ_DEV uint32_t ld_u32(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+RLXQ_DEV uint4 ld_u128(const uint8_t* p) {
+  rlxq_u32x4_a4 v = *reinterpret_cast<const rlxq_u32x4_a4*>(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}

@@ -1,0 +1,183 @@
+// Small kernels around the quantized matmuls: weight dequantization (the
+// bit-exact check entry), SwiGLU between fused gate|up and down, per-row int8
+// activation quantisation, and the MoE router (softmax + top-k).
+#include "common.hip.h"
+
+// One thread per 32-weight block.  Q8_0: d*q; Q4_0: d*(q-8); Q4_1: d*q + m
+// (d*q is exact in f32, so the single rounding is the add); MLX: scale*code
+// rounded, then + bias rounded (no contraction), as
+// crates/rlx-moshi/src/mlx_dequant.rs:66-71 evaluates it.
+extern "C" __global__ __launch_bounds__(256) void rlxq_dequant_rows(
+    int scheme, const uint8_t* __restrict__ w, const void* __restrict__ scales,
+    const void* __restrict__ biases, int sb_bf16, int group, int64_t rows, int K, int64_t rb,
+    float* __restrict__ out) {
+  // Two roundings (multiply, then add), never a fused multiply-add: the
+  // pragma governs the expressions written below.
+#pragma clang fp contract(off)
+  const int bpr = K >> 5;
+  const int64_t blk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (blk >= rows * bpr) return;
+  const int64_t r = blk / bpr;
+  const int b = (int)(blk - r * bpr);
+  float* o = out + r * (int64_t)K + (int64_t)b * 32;
+  if (scheme == SCH_Q8_0 || scheme == SCH_Q4_0 || scheme == SCH_Q4_1) {
+    const int bb = scheme == SCH_Q8_0 ? 34 : (scheme == SCH_Q4_0 ? 18 : 20);
+    const uint8_t* p = w + r * rb + (int64_t)b * bb;
+    const float d = f16_bits_to_f32((uint32_t)p[0] | ((uint32_t)p[1] << 8));
+    if (scheme == SCH_Q8_0) {
+      for (int i = 0; i < 32; i++) o[i] = d * (float)(int8_t)p[2 + i];
+    } else if (scheme == SCH_Q4_0) {
+      for (int j = 0; j < 16; j++) {
+        o[j] = d * (float)((int)(p[2 + j] & 15) - 8);
+        o[j + 16] = d * (float)((int)(p[2 + j] >> 4) - 8);
+      }
+    } else {
+      const float m = f16_bits_to_f32((uint32_t)p[2] | ((uint32_t)p[3] << 8));
+      for (int j = 0; j < 16; j++) {
+        o[j] = d * (float)(p[4 + j] & 15) + m;
+        o[j + 16] = d * (float)(p[4 + j] >> 4) + m;
+      }
+    }
+    return;
+  }
+  // MLX affine: 32 codes of this block; one scale/bias per group.
+  const int bits = scheme == SCH_MLX4 ? 4 : 8;
+  const int64_t gi = r * (int64_t)(K / group) + ((int64_t)b * 32) / group;
+  float s, bi;
+  if (sb_bf16) {
+    s = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(scales)[gi]);
+    bi = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(biases)[gi]);
+  } else {
+    s = reinterpret_cast<const float*>(scales)[gi];
+    bi = reinterpret_cast<const float*>(biases)[gi];
+  }
+  const uint32_t* wq = reinterpret_cast<const uint32_t*>(w + r * rb) + (b * 32 * bits) / 32;
+  const int per = 32 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  for (int i = 0; i < 32; i++) {
+    const uint32_t code = (wq[i / per] >> ((i % per) * bits)) & mask;
+    o[i] = s * (float)code + bi;
+  }
+}
+
+// out[r, i] = silu(gu[r, i]) * gu[r, inter + i] with silu(v) = v / (1 + e^-v)
+// (crates/rlx-laguna/src/mlx_affine.rs:126-128), f32 arithmetic.
+extern "C" __global__ __launch_bounds__(256) void rlxq_swiglu_k(
+    const void* __restrict__ gu, int gu_bf16, int64_t rows, int64_t inter, void* __restrict__ out,
+    int out_bf16) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * inter) return;
+  const int64_t r = i / inter, c = i - r * inter;
+  const int64_t gi = r * 2 * inter + c, ui = gi + inter;
+  float g, u;
+  if (gu_bf16) {
+    g = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(gu)[gi]);
+    u = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(gu)[ui]);
+  } else {
+    g = reinterpret_cast<const float*>(gu)[gi];
+    u = reinterpret_cast<const float*>(gu)[ui];
+  }
+  const float v = g / (1.0f + expf(-g)) * u;
+  if (out_bf16) reinterpret_cast<uint16_t*>(out)[i] = (uint16_t)f32_to_bf16_bits(v);
+  else reinterpret_cast<float*>(out)[i] = v;
+}
+
+// Per-row int8 activation quantisation (crates/rlx-quant-calib/src/bitnet.rs:76-93):
+// s = amax/127 (1 when the row is all zero), q = round_half_away(x * (1/s))
+// clamped to +-127.  One workgroup of 256 threads per row.
+extern "C" __global__ __launch_bounds__(256) void rlxq_quant_act_i8(
+    const void* __restrict__ x, int x_bf16, int64_t M, int K, int8_t* __restrict__ q,
+    float* __restrict__ scales) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  if (r >= M) return;
+  auto ld = [&](int c) -> float {
+    if (x_bf16) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(x)[r * K + c]);
+    return reinterpret_cast<const float*>(x)[r * K + c];
+  };
+  float amax = 0.f;
+  for (int c = threadIdx.x; c < K; c += blockDim.x) amax = fmaxf(amax, fabsf(ld(c)));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = amax > 0.f ? __fdiv_rn(amax, 127.0f) : 1.0f;
+  const float inv = __fdiv_rn(1.0f, s);
+  for (int c = threadIdx.x; c < K; c += blockDim.x) {
+    float v = roundf(__fmul_rn(ld(c), inv));
+    v = fminf(fmaxf(v, -127.f), 127.f);
+    q[r * K + c] = (int8_t)v;
+  }
+  if (threadIdx.x == 0) scales[r] = s;
+}
+
+// Router: softmax over E logits then top-k by probability, ties to the lower
+// expert id; optional renormalisation of the kept probabilities.  One wave per
+// row; E <= 1024.
+extern "C" __global__ __launch_bounds__(64) void rlxq_moe_route_k(
+    const float* __restrict__ logits, int64_t rows, int E, int topk, int renorm,
+    int32_t* __restrict__ ids, float* __restrict__ probs) {
+  const int64_t r = blockIdx.x;
+  if (r >= rows) return;
+  const int lane = threadIdx.x;
+  const float* l = logits + r * E;
+  constexpr int MAXE = 1024 / 64;
+  float p[MAXE];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < MAXE; i++) {
+    const int e = lane + 64 * i;
+    p[i] = e < E ? l[e] : -INFINITY;
+    mx = fmaxf(mx, p[i]);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXE; i++) {
+    const int e = lane + 64 * i;
+    p[i] = e < E ? expf(p[i] - mx) : 0.f;
+    s += p[i];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+#pragma unroll
+  for (int i = 0; i < MAXE; i++) {
+    const int e = lane + 64 * i;
+    p[i] = e < E ? p[i] / s : -1.f;
+  }
+  float kept = 0.f;
+  for (int j = 0; j < topk; j++) {
+    // lane-local best (highest probability, lowest id on ties)
+    float bv = -2.f;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < MAXE; i++) {
+      const int e = lane + 64 * i;
+      if (p[i] > bv || (p[i] == bv && e < be)) {
+        bv = p[i];
+        be = e;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oe = __shfl_xor(be, off, 64);
+      if (ov > bv || (ov == bv && oe < be)) {
+        bv = ov;
+        be = oe;
+      }
+    }
+    if (lane == 0) {
+      ids[r * topk + j] = be;
+      probs[r * topk + j] = bv;
+    }
+    kept += bv;
+#pragma unroll
+    for (int i = 0; i < MAXE; i++)
+      if (lane + 64 * i == be) p[i] = -1.f;
+  }
+  if (renorm && lane == 0)
+    for (int j = 0; j < topk; j++) probs[r * topk + j] = probs[r * topk + j] / kept;
+}

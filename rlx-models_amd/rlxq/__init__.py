@@ -1,0 +1,281 @@
+"""Python binding of librlxq (include/rlxq.h) for tests, smoke and bench.
+
+The product is the C ABI; this module only forwards device pointers of torch
+tensors (torch is plumbing for HBM allocations and streams here).  Loading
+fails loudly when librlxq.so has not been built: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent.parent
+LIBPATH = Path(os.environ.get("RLXQ_LIB", PKG / "lib" / "librlxq.so"))
+HEADER = PKG.parent / "include" / "rlxq.h"
+
+GGUF_Q8_0, GGUF_Q4_0, GGUF_Q4_1, MLX_AFFINE4, MLX_AFFINE8, INT8_BLOCK = 1, 2, 3, 4, 5, 6
+F32, BF16 = 0, 1
+MOE_EXPAND, MOE_COMBINE = 0, 1
+OK = 0
+E_NULL, E_SHAPE, E_SCHEME, E_ALIGN, E_DTYPE, E_HIP, E_NOMEM, E_INDEX, E_NOKERNEL, E_DEVICE = range(-1, -11, -1)
+
+_lib = None
+
+
+class RlxqError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"rlxq status {status}: {msg}")
+        self.status = status
+
+
+def lib() -> C.CDLL:
+    """Loads librlxq.so (raises if it is missing)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIBPATH.exists():
+        raise RuntimeError(f"{LIBPATH} is missing: build it with `python rlx-models_amd/build.py`")
+    L = C.CDLL(str(LIBPATH))
+    P, I, I64, S = C.c_void_p, C.c_int, C.c_int64, C.c_size_t
+    sig = {
+        "rlxq_init": (I, [I, C.POINTER(P)]),
+        "rlxq_destroy": (I, [P]),
+        "rlxq_strerror": (C.c_char_p, [I]),
+        "rlxq_last_error": (C.c_char_p, [P]),
+        "rlxq_version": (C.c_char_p, []),
+        "rlxq_row_bytes": (I64, [I, I64]),
+        "rlxq_dequant_matmul": (I, [P, I, I, P, I, P, P, P, I, I64, I64, I64, P, I, P]),
+        "rlxq_dequant_grouped_matmul": (I, [P, I, I, P, I, P, P, P, I, P, I64, I64, I64, I64, P, I, P]),
+        "rlxq_moe_grouped": (I, [P, I, I, P, I, P, P, P, I64, I64, I64, I64, I64, P, I, P]),
+        "rlxq_moe_route": (I, [P, P, I64, I64, I64, I, P, P, P]),
+        "rlxq_swiglu": (I, [P, P, I, I64, I64, P, I, P]),
+        "rlxq_w8a8_gemm": (I, [P, P, I, P, P, I64, I64, I64, P, I, P]),
+        "rlxq_quantize_act_int8": (I, [P, P, I, I64, I64, P, P, P]),
+        "rlxq_dequantize": (I, [P, I, I, P, P, P, I, I64, I64, P, P]),
+        "rlxq_dm_try_new": (I, [I, C.POINTER(P)]),
+        "rlxq_dm_free": (None, [P]),
+        "rlxq_dm_last_error": (C.c_char_p, [P]),
+        "rlxq_dm_matmul": (I, [P, P, S, P, S, S, S, S, I, P]),
+        "rlxq_dm_grouped_matmul": (I, [P, P, S, P, S, P, S, S, S, S, S, I, P]),
+        "rlxq_dm_upload_count": (I64, [P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def declared_symbols() -> list[str]:
+    """Function names declared in include/rlxq.h."""
+    import re
+
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rlxq_\w+)\s*\(", text)))
+
+
+def strerror(status: int) -> str:
+    return lib().rlxq_strerror(status).decode()
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+
+        return torch.cuda.current_stream().cuda_stream or None
+    return int(stream)
+
+
+def _dt(t) -> int:
+    import torch
+
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.bfloat16:
+        return BF16
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+class Context:
+    """Owns an rlxq_ctx on one device (rlxq_init / rlxq_destroy)."""
+
+    def __init__(self, device: int = 0):
+        self.device = device
+        h = C.c_void_p()
+        rc = lib().rlxq_init(device, C.byref(h))
+        if rc != OK:
+            raise RlxqError(rc, f"rlxq_init({device}): {strerror(rc)}")
+        self.h = h
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().rlxq_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc: int, what: str) -> None:
+        if rc != OK:
+            raise RlxqError(rc, f"{what}: {strerror(rc)}: {lib().rlxq_last_error(self.h).decode()}")
+
+    def dequant_matmul(self, x, w, scheme: int, n: int, *, group: int = 32, scales=None, biases=None,
+                       y=None, y_dtype=None, stream=None):
+        """y[m, n] = x[m, k] . dequant(w)^T; returns y (allocated if not given)."""
+        import torch
+
+        m, k = x.shape
+        if y is None:
+            y = torch.empty((m, n), dtype=y_dtype or torch.float32, device=x.device)
+        sb = _dt(scales) if scales is not None else F32
+        rc = lib().rlxq_dequant_matmul(self.h, scheme, group, _ptr(x), _dt(x), _ptr(w), _ptr(scales), _ptr(biases),
+                                       sb, m, k, n, _ptr(y), _dt(y), _stream(stream))
+        self._check(rc, "dequant_matmul")
+        return y
+
+    def dequantize(self, w, scheme: int, rows: int, k: int, *, group: int = 32, scales=None, biases=None,
+                   out=None, stream=None):
+        import torch
+
+        if out is None:
+            out = torch.empty((rows, k), dtype=torch.float32, device=w.device)
+        sb = _dt(scales) if scales is not None else F32
+        rc = lib().rlxq_dequantize(self.h, scheme, group, _ptr(w), _ptr(scales), _ptr(biases), sb, rows, k,
+                                   _ptr(out), _stream(stream))
+        self._check(rc, "dequantize")
+        return out
+
+    def grouped_matmul(self, x, bank, expert_idx, scheme: int, n: int, num_experts: int, *, group: int = 32,
+                       scales=None, biases=None, y=None, y_dtype=None, stream=None):
+        import torch
+
+        rows, k = x.shape
+        if y is None:
+            y = torch.empty((rows, n), dtype=y_dtype or torch.float32, device=x.device)
+        sb = _dt(scales) if scales is not None else F32
+        rc = lib().rlxq_dequant_grouped_matmul(self.h, scheme, group, _ptr(x), _dt(x), _ptr(bank), _ptr(scales),
+                                               _ptr(biases), sb, _ptr(expert_idx), rows, k, n, num_experts,
+                                               _ptr(y), _dt(y), _stream(stream))
+        self._check(rc, "dequant_grouped_matmul")
+        return y
+
+    def moe_grouped(self, x, bank, ids, probs, scheme: int, mode: int, n: int, num_experts: int, *,
+                    y=None, y_dtype=None, stream=None):
+        import torch
+
+        rows, top_k = ids.shape
+        k = x.shape[1]
+        out_rows = rows * top_k if mode == MOE_EXPAND else rows
+        if y is None:
+            y = torch.empty((out_rows, n), dtype=y_dtype or torch.float32, device=x.device)
+        rc = lib().rlxq_moe_grouped(self.h, scheme, mode, _ptr(x), _dt(x), _ptr(bank), _ptr(ids), _ptr(probs),
+                                    rows, top_k, k, n, num_experts, _ptr(y), _dt(y), _stream(stream))
+        self._check(rc, "moe_grouped")
+        return y
+
+    def moe_route(self, logits, top_k: int, renorm: bool, *, stream=None):
+        import torch
+
+        rows, e = logits.shape
+        ids = torch.empty((rows, top_k), dtype=torch.int32, device=logits.device)
+        probs = torch.empty((rows, top_k), dtype=torch.float32, device=logits.device)
+        rc = lib().rlxq_moe_route(self.h, _ptr(logits), rows, e, top_k, int(renorm), _ptr(ids), _ptr(probs),
+                                  _stream(stream))
+        self._check(rc, "moe_route")
+        return ids, probs
+
+    def swiglu(self, gu, inter: int, *, out=None, out_dtype=None, stream=None):
+        import torch
+
+        rows = gu.shape[0]
+        if out is None:
+            out = torch.empty((rows, inter), dtype=out_dtype or gu.dtype, device=gu.device)
+        rc = lib().rlxq_swiglu(self.h, _ptr(gu), _dt(gu), rows, inter, _ptr(out), _dt(out), _stream(stream))
+        self._check(rc, "swiglu")
+        return out
+
+    def quantize_act_int8(self, x, *, stream=None):
+        import torch
+
+        m, k = x.shape
+        q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+        s = torch.empty((m,), dtype=torch.float32, device=x.device)
+        rc = lib().rlxq_quantize_act_int8(self.h, _ptr(x), _dt(x), m, k, _ptr(q), _ptr(s), _stream(stream))
+        self._check(rc, "quantize_act_int8")
+        return q, s
+
+    def w8a8_gemm(self, x, wq, w_scale, n: int, *, y=None, y_dtype=None, stream=None):
+        import torch
+
+        m, k = x.shape
+        if y is None:
+            y = torch.empty((m, n), dtype=y_dtype or torch.float32, device=x.device)
+        rc = lib().rlxq_w8a8_gemm(self.h, _ptr(x), _dt(x), _ptr(wq), _ptr(w_scale), m, k, n, _ptr(y), _dt(y),
+                                  _stream(stream))
+        self._check(rc, "w8a8_gemm")
+        return y
+
+
+class DeviceMatmul:
+    """The host-slice session API (rlxq_dm_*), mirroring rlx-laguna's DeviceMatmul."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        rc = lib().rlxq_dm_try_new(device, C.byref(h))
+        if rc != OK:
+            raise RlxqError(rc, f"rlxq_dm_try_new({device}): {strerror(rc)}")
+        self.h = h
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().rlxq_dm_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc: int) -> None:
+        if rc != OK:
+            raise RlxqError(rc, lib().rlxq_dm_last_error(self.h).decode())
+
+    @property
+    def uploads(self) -> int:
+        return int(lib().rlxq_dm_upload_count(self.h))
+
+    def matmul(self, x, w_bytes, m: int, k: int, n: int, scheme: int):
+        import numpy as np
+
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        w_bytes = np.ascontiguousarray(w_bytes, dtype=np.uint8).ravel()
+        y = np.empty(m * n, np.float32)
+        rc = lib().rlxq_dm_matmul(self.h, x.ctypes.data, x.size, w_bytes.ctypes.data, w_bytes.size, m, k, n,
+                                  scheme, y.ctypes.data)
+        self._check(rc)
+        return y
+
+    def grouped_matmul(self, x, w_bytes, expert_idx, m: int, k: int, n: int, num_experts: int, scheme: int):
+        import numpy as np
+
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        w_bytes = np.ascontiguousarray(w_bytes, dtype=np.uint8).ravel()
+        idx = np.ascontiguousarray(expert_idx, dtype=np.float32).ravel()
+        y = np.empty(m * n, np.float32)
+        rc = lib().rlxq_dm_grouped_matmul(self.h, x.ctypes.data, x.size, w_bytes.ctypes.data, w_bytes.size,
+                                          idx.ctypes.data, idx.size, m, k, n, num_experts, scheme, y.ctypes.data)
+        self._check(rc)
+        return y

@@ -1,0 +1,336 @@
+"""Pins the CPU oracle (oracle/rlxq_oracle.c) before anything is compared with it.
+
+Each check is chosen so that a plausible mistake in the restatement -- a wrong
+nibble order, a dropped min term, a sign or rounding-mode slip, a transposed
+operand -- fails at least one of them:
+  * known-answer tests taken from the reference's own tests (file:line cited),
+  * closed forms evaluated independently (exact rationals / numpy / torch),
+  * exhaustive or randomised cross-checks of the scalar conversions,
+  * round trips of representable blocks through quantize -> dequantize.
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+
+# ---------------------------------------------------------------- conversions
+def test_f16_to_f32_exhaustive(orc):
+    bits = np.arange(65536, dtype=np.uint16)
+    got = orc.f16_bits_to_f32(bits)
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_numpy_rne(orc, rng):
+    u = rng.integers(0, 2**32, 400000, dtype=np.uint64).astype(np.uint32)
+    special = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x477FE000, 0x477FF000, 0x477FEFFF,
+                        0x33000000, 0x33000001, 0x387FC000, 0x38800000, 0x3F800000, 0x3F801000,
+                        0x3F803000, 0x3F802000, 0x33800000], dtype=np.uint32)
+    f = np.concatenate([u, special]).view(np.float32)
+    # scale most samples into the f16 range so every rounding path is exercised
+    with np.errstate(invalid="ignore", over="ignore"):
+        f = np.where(np.arange(f.size) % 2 == 0, f, (f / np.float32(2.0**100)).astype(np.float32))
+    f = f[~np.isnan(f)]
+    got = orc.f32_to_f16_bits(f)
+    with np.errstate(over="ignore"):
+        want = f.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_f32_to_bf16_matches_torch_rne(orc, rng):
+    u = rng.integers(0, 2**32, 300000, dtype=np.uint64).astype(np.uint32)
+    f = u.view(np.float32)
+    f = f[~np.isnan(f)]
+    got = orc.f32_to_bf16_bits(f)
+    want = torch.from_numpy(f.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+    back = orc.bf16_bits_to_f32(got)
+    assert np.array_equal(back, torch.from_numpy(want.view(np.int16)).view(torch.bfloat16).float().numpy())
+
+
+# -------------------------------------------------------------- GGUF Q4_0 KAT
+def _synthetic_q4_0(k, n):
+    """crates/rlx-models/tests/gguf_legacy_quant_matmul.rs:53-65."""
+    d = np.float16(0.5).view(np.uint16)
+    blocks = k * n // 32
+    out = bytearray()
+    for b in range(blocks):
+        out += int(d).to_bytes(2, "little")
+        for j in range(16):
+            out.append(((b + j) & 0x0F) | (((b + j + 1) & 0x0F) << 4))
+    return np.frombuffer(bytes(out), np.uint8)
+
+
+def test_q4_0_known_answer_fused_matches_reference(orc):
+    """fused_q4_0_matches_reference (gguf_legacy_quant_matmul.rs:124-142), m=2 k=32 n=4,
+    x = 0.01*(i+1); want computed here in exact rationals from the blob's definition."""
+    k, n, m = 32, 4, 2
+    packed = _synthetic_q4_0(k, n)
+    x = np.array([0.01 * (i + 1) for i in range(m * k)], np.float32).reshape(m, k)
+    w = orc.dequantize(orc.Q4_0, packed, k)
+    for b in range(n):
+        for j in range(16):
+            lo = ((b + j) & 15) - 8
+            hi = ((b + j + 1) & 15) - 8
+            assert w[b, j] == 0.5 * lo and w[b, j + 16] == 0.5 * hi
+    exact = [[sum(Fraction(float(x[r, i])) * Fraction(float(w[c, i])) for i in range(k)) for c in range(n)]
+             for r in range(m)]
+    y64 = orc.matmul_f64(orc.Q4_0, x, packed, n)
+    yref = orc.matmul_refl(orc.Q4_0, x, packed, n)
+    for r in range(m):
+        for c in range(n):
+            assert abs(y64[r, c] - float(exact[r][c])) < 1e-12
+            assert abs(yref[r, c] - float(exact[r][c])) < 1e-4  # the reference's tolerance
+
+
+def test_q4_0_representable_block_round_trips(orc):
+    """crates/rlx-flint/src/quant.rs:525-536: d=0.25, x_i = d*((i%16)-8); one-hot dots give x_i exactly."""
+    d = 0.25
+    x = np.array([d * ((i % 16) - 8) for i in range(32)], np.float32)
+    q = orc.quantize(orc.Q4_0, x.reshape(1, 32))
+    for i in range(32):
+        onehot = np.zeros((1, 32), np.float32)
+        onehot[0, i] = 1.0
+        assert orc.matmul_refl(orc.Q4_0, onehot, q, 1)[0, 0] == x[i]
+
+
+@pytest.mark.parametrize("scheme,tol", [("Q8_0", 0.15), ("Q4_0", 0.6)])
+def test_lm_precision_round_trips(orc, scheme, tol):
+    """crates/rlx-unlimited-ocr/src/lm_precision.rs:639-658: v = 0.1*i - 3, i < 64."""
+    v = np.array([i * 0.1 - 3.0 for i in range(64)], np.float32).reshape(2, 32)
+    s = getattr(orc, scheme)
+    back = orc.dequantize(s, orc.quantize(s, v), 32)
+    assert np.max(np.abs(back - v)) < tol
+
+
+def test_q8_0_encoder_rule(orc):
+    """quant.rs:86-95: d = amax/127 stored f16, q = round_half_away(v/d) clamped."""
+    x = np.zeros((1, 32), np.float32)
+    x[0, :4] = [127.0, -63.5, 0.5, -0.5]  # amax 127 -> d = 1; ties round away from zero
+    q = orc.quantize(orc.Q8_0, x)
+    assert q[0, 0] == 0x00 and q[0, 1] == 0x3C  # f16(1.0) little-endian
+    codes = q[0, 2:].view(np.int8)
+    assert list(codes[:4]) == [127, -64, 1, -1]
+    assert np.all(codes[4:] == 0)
+    z = orc.quantize(orc.Q8_0, np.zeros((1, 32), np.float32))
+    assert np.all(z == 0)
+
+
+def test_q8_0_representable_round_trip(orc, rng):
+    n = 64
+    codes = rng.integers(-127, 128, (n, 32)).astype(np.int8)
+    codes[:, 5] = np.where(rng.random(n) < 0.5, 127, -127)
+    d = rng.uniform(0.002, 0.02, n).astype(np.float16).astype(np.float32)
+    w = (codes.astype(np.float32) * d[:, None]).astype(np.float32)
+    q = orc.quantize(orc.Q8_0, w)
+    assert np.array_equal(q[:, 2:].view(np.int8), codes)
+    assert np.array_equal(orc.dequantize(orc.Q8_0, q, 32), w)
+
+
+# ----------------------------------------------------------------------- Q4_1
+def _q4_1_block(d, m, lo, hi):
+    b = bytearray()
+    b += np.float16(d).tobytes() + np.float16(m).tobytes()
+    for j in range(16):
+        b.append((lo[j] & 15) | ((hi[j] & 15) << 4))
+    return np.frombuffer(bytes(b), np.uint8)
+
+
+def test_q4_1_layout_and_closed_form(orc):
+    """GGML block_q4_1: f16 d at +0, f16 m at +2, byte j = element j (low nibble) and
+    element j+16 (high nibble); w = d*q + m."""
+    lo = list(range(16))
+    hi = [15 - j for j in range(16)]
+    blk = _q4_1_block(0.25, -1.5, lo, hi)
+    w = orc.dequantize(orc.Q4_1, blk, 32)[0]
+    want = [0.25 * q - 1.5 for q in lo + hi]
+    assert list(w) == want
+
+
+def test_q4_1_representable_round_trip(orc, rng):
+    """quantize(min/max rule of real_layer_precision.rs:129-146) recovers codes, d and m."""
+    n = 256
+    codes = rng.integers(0, 16, (n, 32))
+    codes[:, 3] = 0
+    codes[:, 7] = 15
+    d = rng.uniform(0.005, 0.05, n).astype(np.float16)
+    mn = rng.uniform(-0.4, 0.0, n).astype(np.float16)
+    w = (codes * d.astype(np.float32)[:, None] + mn.astype(np.float32)[:, None]).astype(np.float32)
+    q = orc.quantize(orc.Q4_1, w)
+    assert np.array_equal(q[:, 0:2].copy().view(np.float16).ravel(), d)
+    assert np.array_equal(q[:, 2:4].copy().view(np.float16).ravel(), mn)
+    got_codes = np.concatenate([q[:, 4:] & 15, q[:, 4:] >> 4], axis=1)
+    assert np.array_equal(got_codes, codes)
+    assert np.array_equal(orc.dequantize(orc.Q4_1, q, 32), w)
+
+
+def test_q4_1_matmul_min_term(orc):
+    """With all codes 0, y = m * sum(x) per block: a dropped or mis-scaled min term fails."""
+    blk = np.concatenate([_q4_1_block(0.5, -0.25, [0] * 16, [0] * 16), _q4_1_block(0.5, 2.0, [0] * 16, [0] * 16)])
+    x = np.arange(64, dtype=np.float32).reshape(1, 64) * 0.125
+    want = -0.25 * x[0, :32].sum() + 2.0 * x[0, 32:].sum()
+    assert orc.matmul_f64(orc.Q4_1, x, blk, 1)[0, 0] == pytest.approx(want, abs=1e-9)
+    assert orc.matmul_refl(orc.Q4_1, x, blk, 1)[0, 0] == pytest.approx(want, rel=1e-6)
+
+
+def _np_dequant(scheme, packed, k):
+    """An independent vectorised numpy restatement of the three GGUF decoders."""
+    bb = {1: 34, 2: 18, 3: 20}[scheme]
+    blk = packed.reshape(-1, bb)
+    d = blk[:, 0:2].copy().view(np.float16).astype(np.float32)
+    if scheme == 1:
+        return (d * blk[:, 2:].view(np.int8).astype(np.float32)).reshape(-1, k)
+    off = 2 if scheme == 2 else 4
+    q = np.concatenate([blk[:, off:] & 15, blk[:, off:] >> 4], axis=1).astype(np.float32)
+    if scheme == 2:
+        return (d * (q - 8)).reshape(-1, k)
+    m = blk[:, 2:4].copy().view(np.float16).astype(np.float32)
+    return (d * q + m).astype(np.float32).reshape(-1, k)
+
+
+@pytest.mark.parametrize("scheme", [1, 2, 3])
+def test_dequant_matches_independent_numpy(orc, rng, scheme):
+    k, n = 256, 48
+    packed = orc.synth(scheme, rng, n, k)
+    assert np.array_equal(orc.dequantize(scheme, packed, k), _np_dequant(scheme, packed.ravel(), k))
+
+
+@pytest.mark.parametrize("scheme", [1, 2, 3])
+def test_matmul_f64_and_reference_order(orc, rng, scheme):
+    m, k, n = 3, 512, 40
+    packed = orc.synth(scheme, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = _np_dequant(scheme, packed.ravel(), k)
+    want = x.astype(np.float64) @ w.astype(np.float64).T  # y = x . W^T, W [n, k]
+    y64 = orc.matmul_f64(scheme, x, packed, n)
+    assert np.allclose(y64, want, rtol=1e-12, atol=1e-12)
+    yr = orc.matmul_refl(scheme, x, packed, n)
+    assert np.max(np.abs(yr - want)) / np.max(np.abs(want)) < 1e-5
+    yp = orc.matmul_refl(scheme, x, packed, n, threads=4)
+    assert np.array_equal(yp, yr)
+
+
+def test_matmul_is_not_transposed(orc, rng):
+    """A non-square case where using W [k, n] instead of [n, k] cannot match."""
+    k, n = 64, 3
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    packed = orc.quantize(orc.Q8_0, w)
+    x = np.zeros((1, k), np.float32)
+    x[0, 33] = 1.0
+    y = orc.matmul_f64(orc.Q8_0, x, packed, n)
+    assert np.allclose(y[0], orc.dequantize(orc.Q8_0, packed, k)[:, 33])
+
+
+# ------------------------------------------------------------------ MLX affine
+def test_mlx_lsb_first_known_answer(orc):
+    """crates/rlx-moshi/src/mlx_dequant.rs:100-110: 0x76543210 -> codes 0..7; scale 2, bias -1."""
+    wq = np.array([[0x76543210]], np.uint32)
+    out = orc.mlx_dequantize(wq, np.array([[2.0]]), np.array([[-1.0]]), 8, 4, 8)
+    assert list(out[0]) == [2.0 * c - 1.0 for c in range(8)]
+
+
+def test_mlx_pack_matches_reference_pack_codes(orc):
+    """pack_codes, crates/rlx-laguna/src/mlx_affine.rs:272-288, for 4 and 8 bits."""
+    codes4 = np.arange(16, dtype=np.uint32).reshape(1, 16) % 16
+    assert list(orc.mlx_pack(codes4, 4)[0]) == [0x76543210, 0xFEDCBA98]
+    codes8 = np.array([[1, 2, 3, 250]], np.uint32)
+    assert list(orc.mlx_pack(codes8, 8)[0]) == [0xFA030201]
+
+
+def test_mlx_affine_matmul_matches_reference_test(orc):
+    """affine_matmul_matches_reference, crates/rlx-laguna/src/mlx_affine.rs:290-330."""
+    out, inn, bits, gs = 3, 64, 4, 64
+    ng = inn // gs
+    codes = (np.arange(out * inn) % 13).astype(np.uint32).reshape(out, inn)
+    wq = orc.mlx_pack(codes, bits)
+    scales = np.array([0.1 + 0.05 * i for i in range(out * ng)], np.float32).reshape(out, ng)
+    biases = np.array([-0.3 + 0.02 * i for i in range(out * ng)], np.float32).reshape(out, ng)
+    seq = 2
+    x = np.sin(np.arange(seq * inn, dtype=np.float32) * np.float32(0.01)).astype(np.float32).reshape(seq, inn)
+    w_ref = (scales.repeat(gs, axis=1) * codes.astype(np.float32) + biases.repeat(gs, axis=1)).astype(np.float32)
+    assert np.array_equal(orc.mlx_dequantize(wq, scales, biases, inn, bits, gs), w_ref)
+    y_ref = x.astype(np.float64) @ w_ref.astype(np.float64).T
+    y = orc.mlx_matmul_f64(x, wq, scales, biases, out, bits, gs)
+    assert np.max(np.abs(y - y_ref)) < 1e-5
+
+
+# --------------------------------------------------------------- grouped / MoE
+def test_grouped_matches_per_row_dense(orc, rng):
+    """quant_parity_backends.rs:268-281: bank [E, N, K], row r uses expert (7r+1) % E."""
+    rows, k, n, E = 6, 128, 16, 3
+    bank = orc.synth(orc.Q4_1, rng, E * n, k)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    idx = np.array([(7 * r + 1) % E for r in range(rows)], np.float32)
+    y = orc.grouped_matmul_f64(orc.Q4_1, x, bank, idx, n, E)
+    for r in range(rows):
+        e = int(idx[r])
+        want = orc.matmul_f64(orc.Q4_1, x[r:r + 1], bank[e * n:(e + 1) * n], n)
+        assert np.array_equal(y[r], want[0])
+    with pytest.raises(ValueError):
+        orc.grouped_matmul_f64(orc.Q4_1, x, bank, np.full(rows, 3.0, np.float32), n, E)
+
+
+def test_topk_softmax_known_answer(orc):
+    """topk_softmax_picks_largest, crates/rlx-unlimited-ocr/src/nn.rs:445-452."""
+    ids, probs = orc.topk_softmax(np.array([[0.0, 5.0, 1.0, -2.0]]), 2)
+    assert list(ids[0]) == [1, 2] and probs[0, 0] > probs[0, 1]
+    e = np.exp(np.array([0.0, 5.0, 1.0, -2.0]) - 5.0)
+    assert probs[0, 0] == pytest.approx(e[1] / e.sum(), rel=1e-6)
+    ids2, p2 = orc.topk_softmax(np.array([[0.0, 5.0, 1.0, -2.0]]), 2, renorm=True)
+    assert p2[0].sum() == pytest.approx(1.0, rel=1e-6) and list(ids2[0]) == [1, 2]
+
+
+def test_moe_is_prob_weighted_sum_of_grouped(orc, rng):
+    rows, k, n, E, topk = 4, 64, 8, 5, 2
+    bank = orc.synth(orc.Q8_0, rng, E * n, k)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    ids, probs = orc.topk_softmax(rng.standard_normal((rows, E)).astype(np.float32), topk)
+    y = orc.moe_f64(orc.Q8_0, x, bank, ids, probs, n, E)
+    want = np.zeros((rows, n))
+    for j in range(topk):
+        want += probs[:, j:j + 1].astype(np.float64) * orc.grouped_matmul_f64(orc.Q8_0, x, bank,
+                                                                               ids[:, j].astype(np.float32), n, E)
+    assert np.allclose(y, want, rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------------ int8
+def test_act_int8_known_answers(orc):
+    """bitnet.rs:76-93: s = amax/127 (1 for an all-zero row), q = f32::round (half away from zero)."""
+    x = np.array([[2.5, -2.5, 127.0, 0.49], [0.0, 0.0, 0.0, 0.0]], np.float32)
+    q, s = orc.quantize_act_int8(x)
+    assert list(q[0]) == [3, -3, 127, 0] and s[0] == 1.0
+    assert list(q[1]) == [0, 0, 0, 0] and s[1] == 1.0
+
+
+def test_int8_col_is_per_output_channel(orc):
+    """common.rs:466-482: w [k, n], one scale per column n."""
+    w = np.array([[1.0, 10.0, 0.0], [-2.0, 5.0, 0.0]], np.float32)  # k=2, n=3
+    q, s = orc.quantize_int8_col(w)
+    assert np.allclose(s, [2.0 / 127, 10.0 / 127, 1.0])
+    assert q[1, 0] == -127 and q[0, 1] == 127 and q[1, 1] == 64 and q[0, 2] == 0
+
+
+def test_w8a8_exact_integer_sum(orc, rng):
+    m, k, n = 3, 96, 5
+    qx = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    qw = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    sx = rng.uniform(0.01, 0.1, m).astype(np.float32)
+    sw = rng.uniform(0.01, 0.1, n).astype(np.float32)
+    acc = qx.astype(np.int64) @ qw.astype(np.int64)
+    want = ((acc.astype(np.float32) * sx[:, None]).astype(np.float32) * sw[None, :]).astype(np.float32)
+    assert np.array_equal(orc.w8a8_matmul(qx, sx, qw, sw), want)
+
+
+def test_int8_block_matmul(orc, rng):
+    """int8_kernel.rs:59-89: y = x . ((Wq - zp) * s), Wq [k, n]."""
+    m, k, n = 2, 64, 7
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    wq = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    s = rng.uniform(0.01, 0.1, n).astype(np.float32)
+    zp = np.zeros(n, np.float32)
+    want = x.astype(np.float64) @ ((wq.astype(np.float32) - zp) * s).astype(np.float64)
+    assert np.allclose(orc.int8_block_matmul_f64(x, wq, s, zp), want, rtol=1e-12, atol=1e-12)
