@@ -128,11 +128,13 @@ def main() -> int:
 
     # ---- per-shape launch durations with HIP events on the launch stream ---
     per = {}
+    kern_of = {}
     for name, k, n in SHAPES:
         reps = 3
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         for lw in layers:
             one(name, k, n, lw[name])
+        kern_of[name] = ctx.last_kernel
         ev0.record(stream)
         for _ in range(reps):
             for lw in layers:
@@ -141,13 +143,11 @@ def main() -> int:
         ev1.synchronize()
         us = ev0.elapsed_time(ev1) * 1e3 / (reps * LAYERS)
         b = gemv_bytes(k, n)
-        per[name] = {"k": k, "n": n, "us": round(us, 3), "GBps": round(b / us / 1e3, 1),
+        per[name] = {"k": k, "n": n, "kernel": kern_of[name], "us": round(us, 3), "GBps": round(b / us / 1e3, 1),
                      "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
     layer_us = sum(v["us"] for v in per.values())
 
-    # dominant kernel = largest total time; the K=4096 shapes share one kernel
-    kern_of = {"o_proj": "q4_1_bf16_L64_P4_C2_M1", "qkv": "q4_1_bf16_L64_P4_C2_M1",
-               "gate_up": "q4_1_bf16_L64_P4_C2_M1", "down": "q4_1_bf16_L64_P2_C3_M1"}
+    # dominant kernel = the one with the largest total time
     tot = {}
     for name, v in per.items():
         t = tot.setdefault(kern_of[name], [0.0, 0.0, 0])
@@ -157,7 +157,7 @@ def main() -> int:
     dom = max(tot, key=lambda kk: tot[kk][0])
     d_us, d_bytes, d_n = tot[dom]
     achieved = (d_bytes / d_n) / (d_us / d_n) / 1e3  # GB/s
-    roofline = {"bound": "hbm", "kernel": "rlxq_gemv_" + dom, "achieved": round(achieved, 1),
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "bytes_per_launch": round(d_bytes / d_n), "us_per_launch": round(d_us / d_n, 3),
                 "traffic": None}

@@ -76,6 +76,9 @@ int rlxq_destroy(rlxq_ctx* ctx);
 const char* rlxq_strerror(int status);
 /* Detail of the last failure on this context (empty if none). */
 const char* rlxq_last_error(const rlxq_ctx* ctx);
+/* Name of the last kernel this context launched (diagnostics and profiling;
+ * no counterpart in the reference). */
+const char* rlxq_last_kernel(const rlxq_ctx* ctx);
 /* Library version string, e.g. "rlxq 0.1.0 gfx950". */
 const char* rlxq_version(void);
 

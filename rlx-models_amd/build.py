@@ -70,7 +70,7 @@ def build_host() -> Path:
     cmd = [
         "g++", "-std=c++17", "-O2", "-fPIC", "-shared",
         "-D__HIP_PLATFORM_AMD__", f"-DRLXQ_CO_DIR=\"{CO}\"",
-        "-I", str(ROOT / "include"), "-I", str(HDIR), "-I", str(ROCM / "include"),
+        "-I", str(ROOT / "include"), "-I", str(HDIR), "-I", str(KDIR), "-I", str(ROCM / "include"),
         *srcs, "-o", str(tmp),
         "-L", str(ROCM / "lib"), "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}",
         "-Wl,--version-script=" + str(HDIR / "exports.map"),

@@ -4,10 +4,12 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
 #include "rlxq.h"
 #include "rlxq_internal.hpp"
+#include "gemv_args.h"
 
 namespace rlxq {
 
@@ -27,7 +29,7 @@ const char* scheme_name(int s) {
 }
 
 struct GemvCfg {
-  int L, P, C, MT;
+  int L, P, C, MT, D, W;
 };
 
 // Lanes per row: the candidate that leaves the fewest idle unit slots
@@ -44,6 +46,28 @@ int pick_lanes(int64_t units, const int* cands, int ncand) {
     }
   }
   return best;
+}
+
+// Variant selection for the decode GEMV, from MI355X measurements.  For the
+// single-row family, RLXQ_GEMV_CFG="L,P,C,D,W" overrides it (tuning sweeps and
+// the per-variant parity test); a variant that was not compiled fails with
+// RLXQ_E_NOKERNEL.
+GemvCfg pick_gemv(int64_t m, int64_t units, int64_t lds_rec_bytes_m4, size_t max_lds) {
+  GemvCfg c;
+  if (m >= 2 && lds_rec_bytes_m4 <= (int64_t)max_lds) {
+    static const int c4[] = {64, 8};
+    c = {pick_lanes(units, c4, 2), 2, 1, 4, 1, 8};
+  } else {
+    static const int c1[] = {64, 32, 16, 8};
+    const int L = pick_lanes(units, c1, 4);
+    c = L == 64 ? GemvCfg{64, 1, 2, 1, 2, 16} : GemvCfg{L, 2, 1, 1, 2, 8};
+  }
+  const char* e = c.MT == 1 ? std::getenv("RLXQ_GEMV_CFG") : nullptr;
+  if (e) {
+    int L, P, C, D, W;
+    if (std::sscanf(e, "%d,%d,%d,%d,%d", &L, &P, &C, &D, &W) == 5) c = {L, P, C, 1, D, W};
+  }
+  return c;
 }
 
 }  // namespace
@@ -90,47 +114,79 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   const bool xbf = x_dtype == RLXQ_BF16;
   const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0) ? 2 : 1;
   const int64_t units = (k / 32) / blocks;
+
+  rlxq_gemv_args a;
+  a.x = x;
+  a.w = static_cast<const uint8_t*>(w);
+  a.scales = scales;
+  a.biases = biases;
+  a.y = y;
+  a.row_map = nullptr;
+  a.row_scale = nullptr;
+  a.M = m;
+  a.N = n;
+  a.rb = rb;
+  a.y_ld = n;
+  a.K = (int32_t)k;
+  a.group = is_mlx(scheme) ? group : 32;
+  a.sb_bf16 = sb_dtype == RLXQ_BF16 ? 1 : 0;
+  a.y_bf16 = y_dtype == RLXQ_BF16 ? 1 : 0;
+  void* args[] = {&a};
+  char name[96];
+  hipFunction_t fn;
+
+  // Single activation row, bf16, 4-bit codes, at most 4 unit chunks per row:
+  // activations held in registers (no LDS stage).  RLXQ_GEMV_XR="NU,D,W"
+  // picks the variant, "0" turns the path off (tuning).
+  const bool xr_scheme = scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_MLX_AFFINE4;
+  const int64_t nchunk64 = (units + 63) / 64;
+  int xr_nu = (int)nchunk64, xr_d = nchunk64 <= 2 ? 2 : (nchunk64 == 3 ? 2 : 1), xr_w = 4;
+  bool use_xr = m == 1 && xbf && xr_scheme && nchunk64 <= 4;
+  if (const char* e = std::getenv("RLXQ_GEMV_XR")) {
+    int nu, d, wv;
+    if (std::sscanf(e, "%d,%d,%d", &nu, &d, &wv) == 3) {
+      xr_d = d;
+      xr_w = wv;
+      if (nu < xr_nu) use_xr = false;
+      else xr_nu = nu;
+    } else if (e[0] == '0') {
+      use_xr = false;
+    }
+  }
+  if (use_xr) {
+    std::snprintf(name, sizeof name, "rlxq_gemvxr_%s_U%d_D%d_W%d", scheme_name(scheme), xr_nu, xr_d, xr_w);
+    if ((rc = get_fn(ctx, name, &fn))) return rc;
+    const int per_cu = blocks_per_cu(ctx, name, fn, 64 * xr_w, 0);
+    const int64_t wgs_needed = (n + xr_w - 1) / xr_w;
+    int64_t gx = (int64_t)ctx->cu_count * per_cu;
+    if (gx > wgs_needed) gx = wgs_needed;
+    return launch(ctx, fn, dim3((unsigned)gx, 1, 1), dim3(64 * xr_w, 1, 1), 0, stream, args, name);
+  }
+
   const int64_t rec_bytes = (xbf ? 20 : 36) * 4;
   const int64_t bpr = k / 32;
-
-  GemvCfg cfg;
-  if (m >= 2 && 4 * bpr * rec_bytes <= (int64_t)ctx->max_lds) {
-    static const int c4[] = {64, 8};
-    cfg = {pick_lanes(units, c4, 2), 2, 2, 4};
-  } else {
-    static const int c1[] = {64, 16, 8};
-    const int L = pick_lanes(units, c1, 3);
-    if (L == 64 && (units + 63) / 64 > 2) cfg = {64, 2, 3, 1};
-    else cfg = {L, 4, 2, 1};
-  }
+  const GemvCfg cfg = pick_gemv(m, units, 4 * bpr * rec_bytes, ctx->max_lds);
+  const int waves = cfg.W;
+  const int64_t tile = (int64_t)waves * cfg.P * (64 / cfg.L);
   const int64_t lds = cfg.MT * bpr * rec_bytes;
   if (lds > (int64_t)ctx->max_lds)
     return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: K too large for the LDS activation stage");
 
-  char name[96];
-  std::snprintf(name, sizeof name, "rlxq_gemv_%s_%s_L%d_P%d_C%d_M%d", scheme_name(scheme),
-                xbf ? "bf16" : "f32", cfg.L, cfg.P, cfg.C, cfg.MT);
-  hipFunction_t fn;
+  std::snprintf(name, sizeof name, "rlxq_gemv_%s_%s_L%d_P%d_C%d_M%d_D%d_W%d", scheme_name(scheme),
+                xbf ? "bf16" : "f32", cfg.L, cfg.P, cfg.C, cfg.MT, cfg.D, cfg.W);
   if ((rc = get_fn(ctx, name, &fn))) return rc;
 
-  const int waves = 4;
-  const int64_t rows_per_wg = (int64_t)waves * cfg.P * (64 / cfg.L);
-  const int64_t gx = (n + rows_per_wg - 1) / rows_per_wg;
+  // Persistent grid: as many workgroups as the device holds at once, with the
+  // row tiles spread evenly over them.
+  const int per_cu = blocks_per_cu(ctx, name, fn, 64 * waves, (size_t)lds);
+  const int64_t ntiles = (n + tile - 1) / tile;
+  const int64_t maxgrid = (int64_t)ctx->cu_count * per_cu;
+  const int64_t tpw = (ntiles + maxgrid - 1) / maxgrid;
+  const int64_t gx = (ntiles + tpw - 1) / tpw;
   const int64_t gy = (m + cfg.MT - 1) / cfg.MT;
   if (gx > 0x7fffffff || gy > 65535) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: grid too large");
-
-  int sb_bf16 = sb_dtype == RLXQ_BF16 ? 1 : 0;
-  int grp = is_mlx(scheme) ? group : 32;
-  int y_bf16 = y_dtype == RLXQ_BF16 ? 1 : 0;
-  int64_t M = m, N = n, RB = rb, YLD = n;
-  int K = (int)k;
-  const int32_t* row_map = nullptr;
-  const float* row_scale = nullptr;
-  void* args[] = {(void*)&x,   (void*)&w,      (void*)&scales, (void*)&biases,   (void*)&sb_bf16,
-                  (void*)&grp, (void*)&y,      (void*)&y_bf16, (void*)&M,        (void*)&K,
-                  (void*)&N,   (void*)&RB,     (void*)&row_map, (void*)&row_scale, (void*)&YLD};
-  return launch(ctx, fn, dim3((unsigned)gx, (unsigned)gy, 1), dim3(64 * waves, 1, 1), (size_t)lds, stream,
-                args, name);
+  return launch(ctx, fn, dim3((unsigned)gx, (unsigned)gy, 1), dim3(64 * waves, 1, 1), (size_t)lds, stream, args,
+                name);
 }
 
 }  // namespace rlxq

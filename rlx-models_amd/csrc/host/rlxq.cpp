@@ -96,8 +96,22 @@ int get_fn(rlxq_ctx* ctx, const std::string& name, hipFunction_t* out) {
   return fail(ctx, RLXQ_E_NOKERNEL, "kernel not found in the gfx950 code objects: " + name);
 }
 
+int blocks_per_cu(rlxq_ctx* ctx, const std::string& name, hipFunction_t fn, int threads, size_t lds) {
+  const std::string key = name + "@" + std::to_string(lds);
+  auto it = ctx->occ_cache.find(key);
+  if (it != ctx->occ_cache.end()) return it->second;
+  int per_cu = 0;
+  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds) != hipSuccess || per_cu < 1) {
+    (void)hipGetLastError();
+    per_cu = 1;
+  }
+  ctx->occ_cache.emplace(key, per_cu);
+  return per_cu;
+}
+
 int launch(rlxq_ctx* ctx, hipFunction_t fn, dim3 grid, dim3 block, size_t lds, void* stream,
            void** args, const char* what) {
+  ctx->last_kernel = what;
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return RLXQ_OK;
   if (lds > ctx->max_lds)
     return fail(ctx, RLXQ_E_SHAPE,
@@ -172,6 +186,8 @@ const char* rlxq_strerror(int s) {
 }
 
 const char* rlxq_last_error(const rlxq_ctx* ctx) { return ctx ? ctx->last_error.c_str() : ""; }
+
+const char* rlxq_last_kernel(const rlxq_ctx* ctx) { return ctx ? ctx->last_kernel.c_str() : ""; }
 
 int64_t rlxq_row_bytes(int scheme, int64_t k) {
   int64_t bb = gguf_block_bytes(scheme);

@@ -14,7 +14,9 @@ struct rlxq_ctx {
   int device = 0;
   std::vector<hipModule_t> modules;
   std::unordered_map<std::string, hipFunction_t> fn_cache;
+  std::unordered_map<std::string, int> occ_cache;  // "kernel@lds" -> workgroups per CU
   std::string last_error;
+  std::string last_kernel;
   int cu_count = 0;
   size_t max_lds = 65536;
   // Library-owned scratch (routing tables, quantised activations, split-K
@@ -42,6 +44,10 @@ class DeviceGuard {
 
 // Looks a kernel up by name across the loaded code objects.
 int get_fn(rlxq_ctx* ctx, const std::string& name, hipFunction_t* out);
+
+// Workgroups of `threads` threads and `lds` bytes of LDS that one CU holds
+// at once (cached per kernel and LDS size; at least 1).
+int blocks_per_cu(rlxq_ctx* ctx, const std::string& name, hipFunction_t fn, int threads, size_t lds);
 
 // Launches `fn` with the kernelParams array `args`.
 int launch(rlxq_ctx* ctx, hipFunction_t fn, dim3 grid, dim3 block, size_t lds, void* stream,

@@ -24,6 +24,7 @@
 //     single plane.  8-bit schemes scale each block of x by a power of two so
 //     that f16 cannot overflow (the factor is folded into the block scale).
 #include "common.hip.h"
+#include "gemv_args.h"
 
 namespace rlxq {
 
@@ -97,135 +98,200 @@ struct Rec {
   static constexpr int STRIDE = NPL * 16 + 4;
 };
 
-// Build the x records of MT activation rows into LDS.
-template <int SCH, bool XBF16, int NPL>
-RLXQ_DEV void stage_x(uint32_t* lds, const void* xv, int64_t m0, int64_t M, int K, int MT) {
-  constexpr bool BIT8 = Unit<SCH>::BIT8;
-  constexpr int RS = Rec<NPL>::STRIDE;
-  const int bpr = K >> 5;
-  const int nrec = MT * bpr;
-  for (int r = threadIdx.x; r < nrec; r += blockDim.x) {
-    const int m = r / bpr, b = r - m * bpr;
-    float v[32];
-    const int64_t row = m0 + m;
-    if (row < M) {
-      if constexpr (XBF16) {
-        const uint4* p = reinterpret_cast<const uint4*>(
-            reinterpret_cast<const uint16_t*>(xv) + row * (int64_t)K + (int64_t)b * 32);
+// Sum / max over aligned groups of 8 lanes (DPP quad butterflies, then the
+// half-row mirror); every lane of the group gets the result.
+RLXQ_DEV float group8_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+RLXQ_DEV float group8_max(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+  return v;
+}
+RLXQ_DEV uint32_t swap_lane_pair(uint32_t v) {  // value of lane ^ 1
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+}
+
+// Building the x records of MT activation rows into LDS.  Eight lanes share
+// a record; lane q converts elements 4q..4q+3 of it and writes the two plane
+// dwords they form (and their lo twins), lane 0 of the group the sums and the
+// block scale.  Tasks (record, q) of one activation row are numbered
+// 8*block + q; a thread handles tasks threadIdx.x + i*blockDim.x in batches of
+// XB: stage_fetch issues a batch's activation loads, stage_store converts and
+// writes it.  The loop structure is uniform over the workgroup (the group
+// reductions use DPP).
+template <bool XBF16>
+struct XRaw {
+  static constexpr int XB = XBF16 ? 8 : 4;
+  uint32_t w[XB][XBF16 ? 2 : 4];
+};
+
+template <bool XBF16>
+RLXQ_DEV void stage_fetch(XRaw<XBF16>& raw, const void* xv, int64_t row, int64_t M, int K, int base) {
+  constexpr int XB = XRaw<XBF16>::XB;
+  const int ntask = (K >> 5) * 8;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          uint4 u = p[q];
-          uint32_t w4[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-          for (int h = 0; h < 4; h++) {
-            v[q * 8 + 2 * h] = bf16_bits_to_f32(w4[h] & 0xffffu);
-            v[q * 8 + 2 * h + 1] = bf16_bits_to_f32(w4[h] >> 16);
-          }
-        }
-      } else {
-        const float4* p = reinterpret_cast<const float4*>(
-            reinterpret_cast<const float*>(xv) + row * (int64_t)K + (int64_t)b * 32);
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-          float4 f = p[q];
-          v[4 * q] = f.x;
-          v[4 * q + 1] = f.y;
-          v[4 * q + 2] = f.z;
-          v[4 * q + 3] = f.w;
-        }
-      }
+  for (int i = 0; i < XB; i++) {
+    const int task = base + i * blockDim.x + threadIdx.x;
+    const int64_t off = row * (int64_t)K + 4 * task;
+    if constexpr (XBF16) {
+      uint2 u = make_uint2(0u, 0u);
+      if (task < ntask && row < M) u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(xv) + off);
+      raw.w[i][0] = u.x;
+      raw.w[i][1] = u.y;
     } else {
-#pragma unroll
-      for (int i = 0; i < 32; i++) v[i] = 0.f;
+      uint4 u = make_uint4(0u, 0u, 0u, 0u);
+      if (task < ntask && row < M) u = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(xv) + off);
+      raw.w[i][0] = u.x; raw.w[i][1] = u.y; raw.w[i][2] = u.z; raw.w[i][3] = u.w;
     }
-    float sx = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) sx += v[i];
-    float scl = 1.f;
-    if constexpr (BIT8) {
-      float amax = 0.f;
-#pragma unroll
-      for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
-      if (amax > 0.f && amax < INFINITY) {
-        int e = ilogbf(amax) - 14;  // scaled max lands in [2^14, 2^15)
-        scl = ldexpf(1.f, e);
-        const float inv = ldexpf(1.f, -e);
-#pragma unroll
-        for (int i = 0; i < 32; i++) v[i] *= inv;
-      }
-    }
-    uint32_t hi[32], lo[32];
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-      if constexpr (BIT8) {
-        hi[i] = f32_to_f16_bits(v[i]);
-        const float hv = f16_bits_to_f32(hi[i]);
-        if constexpr (NPL == 2) {
-          lo[i] = f32_to_f16_bits(v[i] - hv);
-          s += hv + f16_bits_to_f32(lo[i]);
-        } else {
-          lo[i] = 0;
-          s += hv;
-        }
-      } else {
-        hi[i] = f32_to_bf16_bits(v[i]);
-        const float hv = bf16_bits_to_f32(hi[i]);
-        if constexpr (NPL == 2) {
-          lo[i] = f32_to_bf16_bits(v[i] - hv);
-          s += hv + bf16_bits_to_f32(lo[i]);
-        } else {
-          lo[i] = 0;
-          s += hv;
-        }
-      }
-    }
-    uint32_t* rec = lds + (size_t)r * RS;
-#pragma unroll
-    for (int t = 0; t < 16; t++) {
-      int a, bb;
-      plane_pair<SCH>(t, a, bb);
-      rec[t] = hi[a] | (hi[bb] << 16);
-      if constexpr (NPL == 2) rec[16 + t] = lo[a] | (lo[bb] << 16);
-    }
-    rec[NPL * 16 + 0] = __float_as_uint(s);
-    rec[NPL * 16 + 1] = __float_as_uint(sx);
-    rec[NPL * 16 + 2] = __float_as_uint(scl);
-    rec[NPL * 16 + 3] = 0u;
   }
 }
 
-// Decoded block: 16 pair-dwords of (bias + code) values plus its scale terms.
-struct DecBlock {
-  uint32_t pw[16];
-  float d;  // multiplies the dot chain
-  float m;  // multiplies the block sum of x (Q4_1 min, MLX bias), else 0
-};
-
-// 4-bit: four pairs per qs dword.
-RLXQ_DEV void nib_pairs(uint32_t w, uint32_t* out) {
-  out[0] = (w & 0x000F000Fu) | 0x43004300u;
-  out[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  out[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  out[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+template <int SCH, bool XBF16, int NPL>
+RLXQ_DEV void stage_store(uint32_t* lds, const XRaw<XBF16>& raw, int m, int K, int base) {
+  constexpr bool BIT8 = Unit<SCH>::BIT8;
+  constexpr int RS = Rec<NPL>::STRIDE;
+  constexpr int XB = XRaw<XBF16>::XB;
+  const int bpr = K >> 5;
+  const int ntask = bpr * 8;
+#pragma unroll
+  for (int i = 0; i < XB; i++) {
+    if (base + i * (int)blockDim.x >= ntask) break;  // uniform
+    const int task = base + i * blockDim.x + threadIdx.x;
+    const bool active = task < ntask;
+    const int r = m * bpr + (task >> 3), q = task & 7;
+    float v[4];
+    if constexpr (XBF16) {
+      v[0] = bf16_bits_to_f32(raw.w[i][0] & 0xffffu);
+      v[1] = bf16_bits_to_f32(raw.w[i][0] >> 16);
+      v[2] = bf16_bits_to_f32(raw.w[i][1] & 0xffffu);
+      v[3] = bf16_bits_to_f32(raw.w[i][1] >> 16);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; k++) v[k] = __uint_as_float(raw.w[i][k]);
+    }
+    const float sx = group8_sum((v[0] + v[1]) + (v[2] + v[3]));
+    float scl = 1.f;
+    if constexpr (BIT8) {
+      const float amax = group8_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+      if (amax > 0.f && amax < INFINITY) {
+        const int e = ilogbf(amax) - 14;  // scaled max lands in [2^14, 2^15)
+        scl = ldexpf(1.f, e);
+        const float inv = ldexpf(1.f, -e);
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] *= inv;
+      }
+    }
+    uint32_t hi[4], lo[4];
+    float ps = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      if constexpr (BIT8) {
+        hi[k] = f32_to_f16_bits(v[k]);
+        const float hv = f16_bits_to_f32(hi[k]);
+        lo[k] = NPL == 2 ? f32_to_f16_bits(v[k] - hv) : 0u;
+        ps += NPL == 2 ? hv + f16_bits_to_f32(lo[k]) : hv;
+      } else if constexpr (XBF16) {
+        hi[k] = __float_as_uint(v[k]) >> 16;  // exact: the input is bf16
+        lo[k] = 0u;
+      } else {
+        hi[k] = f32_to_bf16_bits(v[k]);
+        const float hv = bf16_bits_to_f32(hi[k]);
+        lo[k] = f32_to_bf16_bits(v[k] - hv);
+        ps += hv + bf16_bits_to_f32(lo[k]);
+      }
+    }
+    const float S = (!BIT8 && XBF16) ? sx : group8_sum(ps);
+    // the two plane dwords of this lane and their positions t0, t1
+    uint32_t h0, h1, l0 = 0u, l1 = 0u;
+    int t0, t1;
+    if constexpr (SCH == SCH_MLX4) {
+      // pairs (8j+e, 8j+e+4): even lanes hold 8j..8j+3, odd lanes 8j+4..8j+7
+      const uint32_t hp01 = swap_lane_pair(hi[0] | (hi[1] << 16)), hp23 = swap_lane_pair(hi[2] | (hi[3] << 16));
+      const uint32_t lp01 = swap_lane_pair(lo[0] | (lo[1] << 16)), lp23 = swap_lane_pair(lo[2] | (lo[3] << 16));
+      const int j = q >> 1;
+      if ((q & 1) == 0) {
+        h0 = hi[0] | (hp01 << 16);
+        h1 = hi[1] | (hp01 & 0xffff0000u);
+        l0 = lo[0] | (lp01 << 16);
+        l1 = lo[1] | (lp01 & 0xffff0000u);
+        t0 = 4 * j;
+        t1 = 4 * j + 1;
+      } else {
+        h0 = (hp23 & 0xffffu) | (hi[2] << 16);
+        h1 = (hp23 >> 16) | (hi[3] << 16);
+        l0 = (lp23 & 0xffffu) | (lo[2] << 16);
+        l1 = (lp23 >> 16) | (lo[3] << 16);
+        t0 = 4 * j + 2;
+        t1 = 4 * j + 3;
+      }
+    } else {
+      // pairs (4q, 4q+2) and (4q+1, 4q+3)
+      h0 = hi[0] | (hi[2] << 16);
+      h1 = hi[1] | (hi[3] << 16);
+      l0 = lo[0] | (lo[2] << 16);
+      l1 = lo[1] | (lo[3] << 16);
+      if constexpr (BIT8) {
+        t0 = 2 * q;
+        t1 = 2 * q + 1;
+      } else {
+        // GGUF nibble order: elements 4i.. -> e = 0/2, elements 16+4i.. -> e = 1/3
+        t0 = q < 4 ? 4 * q : 4 * (q - 4) + 1;
+        t1 = t0 + 2;
+      }
+    }
+    if (active) {
+      uint32_t* rec = lds + (size_t)r * RS;
+      rec[t0] = h0;
+      rec[t1] = h1;
+      if constexpr (NPL == 2) {
+        rec[16 + t0] = l0;
+        rec[16 + t1] = l1;
+      }
+      if (q == 0) {
+        rec[NPL * 16 + 0] = __float_as_uint(S);
+        rec[NPL * 16 + 1] = __float_as_uint(sx);
+        rec[NPL * 16 + 2] = __float_as_uint(scl);
+        rec[NPL * 16 + 3] = 0u;
+      }
+    }
+  }
 }
 
-// 8-bit: two f16 pairs per dword of unsigned codes.
+// Constants of the code -> float tricks, held in VGPRs so that the unpack
+// compiles to one v_and_or_b32 per pair (a VOP3 instruction on gfx950 cannot
+// take two literal operands).
+struct UnpackK {
+  uint32_t mask, magic;
+};
+RLXQ_DEV UnpackK unpack_consts() {
+  UnpackK k{0x000F000Fu, 0x43004300u};
+  asm volatile("" : "+v"(k.mask), "+v"(k.magic));
+  return k;
+}
+
+// 4-bit: four bf16 (128 + q) pairs per dword of nibbles.
+RLXQ_DEV void nib_pairs(uint32_t w, uint32_t* out, const UnpackK& k) {
+  out[0] = (w & k.mask) | k.magic;
+  out[1] = ((w >> 4) & k.mask) | k.magic;
+  out[2] = ((w >> 8) & k.mask) | k.magic;
+  out[3] = ((w >> 12) & k.mask) | k.magic;
+}
+
+// 8-bit: two f16 (1024 + u) pairs per dword of unsigned byte codes.
 RLXQ_DEV void byte_pairs(uint32_t u, uint32_t* out) {
   out[0] = perm_b32(0x64646464u, u, 0x04020400u);
   out[1] = perm_b32(0x64646464u, u, 0x04030401u);
 }
 
-// Fetch one unit of row `n` (zeros when out of range).
+// Fetch one unit at p (always a valid address; out-of-range units are
+// clamped by the caller and their scales zeroed).
 template <int SCH>
-RLXQ_DEV void load_unit(uint32_t* dw, const uint8_t* w, int64_t rb, int64_t n, int u, bool ok) {
-  constexpr int DW = Unit<SCH>::DW;
-  if (!ok) {
-#pragma unroll
-    for (int i = 0; i < DW; i++) dw[i] = 0u;
-    return;
-  }
-  const uint8_t* p = w + n * rb + (int64_t)u * Unit<SCH>::BYTES;
+RLXQ_DEV void load_unit(uint32_t* dw, const uint8_t* p) {
   if constexpr (SCH == SCH_Q4_1) {
     dw[0] = ld_u32(p);
     uint4 q = ld_u128(p + 4);
@@ -252,64 +318,70 @@ RLXQ_DEV void load_unit(uint32_t* dw, const uint8_t* w, int64_t rb, int64_t n, i
   }
 }
 
-// Decode block `blk` (0 or 1) of a fetched unit.
+// Block scale terms of block `blk` of a fetched unit: d multiplies the dot
+// chain, m (Q4_1 min) multiplies the block sum of x.
 template <int SCH>
-RLXQ_DEV void decode_block(const uint32_t* dw, int blk, float ms, float mb, DecBlock& o) {
+RLXQ_DEV void block_scales(const uint32_t* dw, int blk, float& d, float& m) {
   if constexpr (SCH == SCH_Q4_1) {
-    o.d = f16_bits_to_f32(dw[0] & 0xffffu);
-    o.m = f16_bits_to_f32(dw[0] >> 16);
-#pragma unroll
-    for (int i = 0; i < 4; i++) nib_pairs(dw[1 + i], &o.pw[4 * i]);
-  } else if constexpr (SCH == SCH_Q4_0) {
-    o.m = 0.f;
-    if (blk == 0) {
-      // block A: d = bytes 0-1, qs = bytes 2..17 (re-aligned by 2 bytes)
-      o.d = f16_bits_to_f32(dw[0] & 0xffffu);
-#pragma unroll
-      for (int i = 0; i < 4; i++) nib_pairs(align_bytes(dw[i + 1], dw[i], 2), &o.pw[4 * i]);
-    } else {
-      // block B: d = bytes 18-19, qs = bytes 20..35
-      o.d = f16_bits_to_f32(dw[4] >> 16);
-#pragma unroll
-      for (int i = 0; i < 4; i++) nib_pairs(dw[5 + i], &o.pw[4 * i]);
-    }
-  } else if constexpr (SCH == SCH_Q8_0) {
-    o.m = 0.f;
-    if (blk == 0) {
-      o.d = f16_bits_to_f32(dw[0] & 0xffffu);
-#pragma unroll
-      for (int i = 0; i < 8; i++) byte_pairs(align_bytes(dw[i + 1], dw[i], 2) ^ 0x80808080u, &o.pw[2 * i]);
-    } else {
-      o.d = f16_bits_to_f32(dw[8] >> 16);
-#pragma unroll
-      for (int i = 0; i < 8; i++) byte_pairs(dw[9 + i] ^ 0x80808080u, &o.pw[2 * i]);
-    }
-  } else if constexpr (SCH == SCH_MLX4) {
-    o.d = ms;
-    o.m = mb;
-#pragma unroll
-    for (int i = 0; i < 4; i++) nib_pairs(dw[i], &o.pw[4 * i]);
+    d = f16_bits_to_f32(dw[0] & 0xffffu);
+    m = f16_bits_to_f32(dw[0] >> 16);
+  } else if constexpr (SCH == SCH_Q4_0 || SCH == SCH_Q8_0) {
+    constexpr int HI = SCH == SCH_Q4_0 ? 4 : 8;  // dword holding block B's d in its high half
+    d = blk == 0 ? f16_bits_to_f32(dw[0] & 0xffffu) : f16_bits_to_f32(dw[HI] >> 16);
+    m = 0.f;
   } else {
-    o.d = ms;
-    o.m = mb;
-#pragma unroll
-    for (int i = 0; i < 8; i++) byte_pairs(dw[i], &o.pw[2 * i]);
+    d = 0.f;
+    m = 0.f;
   }
 }
 
+// The 16 pair-dwords of block `blk` of a fetched unit.
+template <int SCH>
+RLXQ_DEV void block_pairs(const uint32_t* dw, int blk, uint32_t* pw, const UnpackK& k) {
+  if constexpr (SCH == SCH_Q4_1) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) nib_pairs(dw[1 + i], &pw[4 * i], k);
+  } else if constexpr (SCH == SCH_Q4_0) {
+    if (blk == 0) {
+      // block A: d = bytes 0-1, qs = bytes 2..17 (re-aligned by 2 bytes)
+#pragma unroll
+      for (int i = 0; i < 4; i++) nib_pairs(align_bytes(dw[i + 1], dw[i], 2), &pw[4 * i], k);
+    } else {
+      // block B: d = bytes 18-19, qs = bytes 20..35
+#pragma unroll
+      for (int i = 0; i < 4; i++) nib_pairs(dw[5 + i], &pw[4 * i], k);
+    }
+  } else if constexpr (SCH == SCH_Q8_0) {
+    if (blk == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) byte_pairs(align_bytes(dw[i + 1], dw[i], 2) ^ 0x80808080u, &pw[2 * i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) byte_pairs(dw[9 + i] ^ 0x80808080u, &pw[2 * i]);
+    }
+  } else if constexpr (SCH == SCH_MLX4) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) nib_pairs(dw[i], &pw[4 * i], k);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) byte_pairs(dw[i], &pw[2 * i]);
+  }
+}
+
+// sum over the block of (bias + code) * x, started at -bias * S so that it
+// ends at sum(w_int * x).
 template <int SCH, int NPL>
-RLXQ_DEV float block_dot(const DecBlock& db, const uint32_t* xr) {
+RLXQ_DEV float block_dot(const uint32_t* pw, const uint32_t* xr) {
   constexpr bool BIT8 = Unit<SCH>::BIT8;
-  const float S = __uint_as_float(xr[NPL * 16 + 0]);
-  float c = -chain_bias<SCH>() * S;
+  float c = -chain_bias<SCH>() * __uint_as_float(xr[NPL * 16 + 0]);
 #pragma unroll
   for (int t = 0; t < 16; t++) {
     if constexpr (BIT8) {
-      c = dot2_f16(db.pw[t], xr[t], c);
-      if constexpr (NPL == 2) c = dot2_f16(db.pw[t], xr[16 + t], c);
+      c = dot2_f16(pw[t], xr[t], c);
+      if constexpr (NPL == 2) c = dot2_f16(pw[t], xr[16 + t], c);
     } else {
-      c = dot2_bf16(db.pw[t], xr[t], c);
-      if constexpr (NPL == 2) c = dot2_bf16(db.pw[t], xr[16 + t], c);
+      c = dot2_bf16(pw[t], xr[t], c);
+      if constexpr (NPL == 2) c = dot2_bf16(pw[t], xr[16 + t], c);
     }
   }
   return c;
@@ -321,31 +393,89 @@ RLXQ_DEV float load_sb(const void* p, int64_t idx, bool bf16) {
   return reinterpret_cast<const float*>(p)[idx];
 }
 
-template <int SCH, bool XBF16, int L, int P, int NBC, int MT>
-RLXQ_DEV void gemv_body(const void* __restrict__ x, const uint8_t* __restrict__ w,
-                        const void* __restrict__ scales, const void* __restrict__ biases,
-                        int sb_bf16, int group, void* __restrict__ y, int y_bf16,
-                        int64_t M, int K, int64_t N, int64_t rb, const int32_t* __restrict__ row_map,
-                        const float* __restrict__ row_scale, int64_t y_ld) {
+// Sum over aligned groups of L lanes with DPP row operations; for L = 64 the
+// four 16-lane row sums are combined through readlane, so every lane ends
+// with its group's sum.
+template <int L>
+RLXQ_DEV float lane_group_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  if constexpr (L == 2) return v;
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  if constexpr (L == 4) return v;
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  if constexpr (L == 8) return v;
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  if constexpr (L == 16) return v;
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  if constexpr (L == 32) return (threadIdx.x & 32) ? r2 + r3 : r0 + r1;
+  return (r0 + r1) + (r2 + r3);
+}
+
+// One decode GEMV pass.
+//
+// A workgroup (WAVES waves) stages its MT activation rows once and then walks row
+// tiles t = blockIdx.x, blockIdx.x + gridDim.x, ...; the host sizes the grid
+// to what the device holds at once.  Each wave owns P*RP rows of a tile and
+// covers them in steps of C unit chunks (C*L units of each row per step, so a
+// step requests whole rows when C*L covers K).  A ring of D register buffers
+// keeps the loads of the next D steps in flight while a step is computed; the
+// first D steps are requested right after the activations, before the
+// activation records are built.
+template <int SCH, bool XBF16, int L, int P, int C, int MT, int D, int WAVES>
+RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
   constexpr bool BIT8 = Unit<SCH>::BIT8;
   constexpr int NPL = (XBF16 ? 1 : 2);
   constexpr int RS = Rec<NPL>::STRIDE;
   constexpr int BLOCKS = Unit<SCH>::BLOCKS;
   constexpr int DW = Unit<SCH>::DW;
+  constexpr int BYTES = Unit<SCH>::BYTES;
   constexpr int RP = 64 / L;
+  constexpr int TILE = WAVES * P * RP;
   constexpr bool MLX = (SCH == SCH_MLX4 || SCH == SCH_MLX8);
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || MLX);
   extern __shared__ uint32_t lds[];
 
+  const int K = a.K;
   const int bpr = K >> 5;
   const int U = bpr / BLOCKS;
+  const int nchunk = (U + L - 1) / L;
+  const int ng = (nchunk + C - 1) / C;  // steps per tile
+  const int64_t ntiles = (a.N + TILE - 1) / TILE;
   const int64_t m0 = (int64_t)blockIdx.y * MT;
-  stage_x<SCH, XBF16, NPL>(lds, x, m0, M, K, MT);
-  __syncthreads();
-
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane / L, li = lane % L;
-  const int waves = blockDim.x >> 6;
-  const int64_t row0 = ((int64_t)blockIdx.x * waves + wv) * (P * RP) + g;
+  const int gpr = MLX ? K / a.group : 0;  // MLX groups per row
+  const int64_t row_off = wv * (P * RP) + g;
+
+  struct Buf {
+    uint32_t dw[P][C][DW];
+    float sm[P][C][BLOCKS], bm[P][C][BLOCKS];
+  };
+  auto load = [&](int64_t t, int jg, Buf& bf) {
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+      int64_t n = t * TILE + row_off + p * RP;
+      n = (n < a.N && t < ntiles) ? n : 0;
+      const uint8_t* rp = a.w + n * a.rb;
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        const int u = li + L * (jg * C + c);
+        const int uc = u < U ? u : U - 1;
+        load_unit<SCH>(bf.dw[p][c], rp + (int64_t)uc * BYTES);
+        if constexpr (MLX) {
+#pragma unroll
+          for (int bl = 0; bl < BLOCKS; bl++) {
+            const int64_t gi = n * gpr + ((uc * BLOCKS + bl) * 32) / a.group;
+            bf.sm[p][c][bl] = load_sb(a.scales, gi, a.sb_bf16 != 0);
+            bf.bm[p][c][bl] = load_sb(a.biases, gi, a.sb_bf16 != 0);
+          }
+        }
+      }
+    }
+  };
 
   float acc[P][MT];
 #pragma unroll
@@ -353,82 +483,279 @@ RLXQ_DEV void gemv_body(const void* __restrict__ x, const uint8_t* __restrict__ 
 #pragma unroll
     for (int m = 0; m < MT; m++) acc[p][m] = 0.f;
 
-  const int nb = (U + L - 1) / L;  // units per lane per row
-  for (int j0 = 0; j0 < nb; j0 += NBC) {
-    uint32_t dw[P][NBC][DW];
-    float msc[P][NBC][BLOCKS], mbi[P][NBC][BLOCKS];
+  const UnpackK kc = unpack_consts();
+  auto compute = [&](int64_t t, int jg, const Buf& bf) {
 #pragma unroll
-    for (int p = 0; p < P; p++) {
-      const int64_t n = row0 + p * RP;
-#pragma unroll
-      for (int jj = 0; jj < NBC; jj++) {
-        const int u = li + L * (j0 + jj);
-        const bool ok = (n < N) && (u < U) && (j0 + jj < nb);
-        load_unit<SCH>(dw[p][jj], w, rb, n, u, ok);
-#pragma unroll
-        for (int bl = 0; bl < BLOCKS; bl++) {
-          msc[p][jj][bl] = 0.f;
-          mbi[p][jj][bl] = 0.f;
-          if constexpr (MLX) {
-            if (ok) {
-              const int64_t gi = n * (int64_t)(K / group) + ((int64_t)(u * BLOCKS + bl) * 32) / group;
-              msc[p][jj][bl] = load_sb(scales, gi, sb_bf16 != 0);
-              mbi[p][jj][bl] = load_sb(biases, gi, sb_bf16 != 0);
-            }
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int jj = 0; jj < NBC; jj++) {
-      const int u = li + L * (j0 + jj);
-      const int uc = u < U ? u : U - 1;
+    for (int c = 0; c < C; c++) {
+      const int u = li + L * (jg * C + c);
+      const bool uok = u < U;
+      const int uc = uok ? u : U - 1;
 #pragma unroll
       for (int bl = 0; bl < BLOCKS; bl++) {
-        DecBlock db[P];
-#pragma unroll
-        for (int p = 0; p < P; p++) decode_block<SCH>(dw[p][jj], bl, msc[p][jj][bl], mbi[p][jj][bl], db[p]);
         const int b = uc * BLOCKS + bl;
+        float d[P], mn[P];
+        uint32_t pw[P][16];
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+          if constexpr (MLX) {
+            d[p] = bf.sm[p][c][bl];
+            mn[p] = bf.bm[p][c][bl];
+          } else {
+            block_scales<SCH>(bf.dw[p][c], bl, d[p], mn[p]);
+          }
+          const bool rok = t * TILE + row_off + p * RP < a.N;
+          if (!(rok && uok)) {
+            d[p] = 0.f;
+            mn[p] = 0.f;
+          }
+          block_pairs<SCH>(bf.dw[p][c], bl, pw[p], kc);
+        }
 #pragma unroll
         for (int m = 0; m < MT; m++) {
           const uint32_t* xr = lds + (size_t)(m * bpr + b) * RS;
           uint32_t xrec[RS];
 #pragma unroll
-          for (int t = 0; t < RS; t += 4) {
-            uint4 q = *reinterpret_cast<const uint4*>(xr + t);
-            xrec[t] = q.x; xrec[t + 1] = q.y; xrec[t + 2] = q.z; xrec[t + 3] = q.w;
+          for (int q = 0; q < RS; q += 4) {
+            const uint4 v = *reinterpret_cast<const uint4*>(xr + q);
+            xrec[q] = v.x; xrec[q + 1] = v.y; xrec[q + 2] = v.z; xrec[q + 3] = v.w;
           }
           const float sx = __uint_as_float(xrec[NPL * 16 + 1]);
           const float scl = __uint_as_float(xrec[NPL * 16 + 2]);
 #pragma unroll
           for (int p = 0; p < P; p++) {
-            const float c = block_dot<SCH, NPL>(db[p], xrec);
-            const float dd = BIT8 ? db[p].d * scl : db[p].d;
-            acc[p][m] = fmaf(dd, c, acc[p][m]);
-            if constexpr (SCH == SCH_Q4_1 || MLX) acc[p][m] = fmaf(db[p].m, sx, acc[p][m]);
+            const float cc = block_dot<SCH, NPL>(pw[p], xrec);
+            acc[p][m] = fmaf(BIT8 ? d[p] * scl : d[p], cc, acc[p][m]);
+            if constexpr (HAS_MIN) acc[p][m] = fmaf(mn[p], sx, acc[p][m]);
           }
         }
       }
     }
+    if (jg == ng - 1) {
+#pragma unroll
+      for (int p = 0; p < P; p++) {
+        const int64_t n = t * TILE + row_off + p * RP;
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+          const float v = lane_group_sum<L>(acc[p][m]);
+          acc[p][m] = 0.f;
+          const int64_t row = m0 + m;
+          if (li == 0 && n < a.N && row < a.M) {
+            int64_t yrow = row;
+            float sc = 1.f;
+            if (a.row_map) yrow = a.row_map[row];
+            if (a.row_scale) sc = a.row_scale[row];
+            if (yrow >= 0) {
+              const int64_t off = yrow * a.y_ld + n;
+              if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v * sc);
+              else reinterpret_cast<float*>(a.y)[off] = v * sc;
+            }
+          }
+        }
+      }
+    }
+  };
+
+  auto next = [&](int64_t& t, int& jg) {
+    if (++jg == ng) {
+      jg = 0;
+      t += gridDim.x;
+    }
+  };
+
+  // The activation loads go out first, then the first D steps of weights, so
+  // the x records can be built while the weights are in flight.
+  XRaw<XBF16> raw;
+  stage_fetch<XBF16>(raw, a.x, m0, a.M, K, 0);
+  Buf ring[D];
+  int64_t lt = blockIdx.x;  // load cursor
+  int lj = 0;
+#pragma unroll
+  for (int i = 0; i < D; i++) {
+    if (lt < ntiles) load(lt, lj, ring[i]);
+    next(lt, lj);
+  }
+  stage_store<SCH, XBF16, NPL>(lds, raw, 0, K, 0);
+  for (int m = 0; m < MT; m++)
+    for (int base = m == 0 ? (int)blockDim.x * XRaw<XBF16>::XB : 0; base < bpr * 8;
+         base += blockDim.x * XRaw<XBF16>::XB) {
+      stage_fetch<XBF16>(raw, a.x, m0 + m, a.M, K, base);
+      stage_store<SCH, XBF16, NPL>(lds, raw, m, K, base);
+    }
+  __syncthreads();
+
+  int64_t ct = blockIdx.x;  // compute cursor
+  int cj = 0;
+  while (ct < ntiles) {
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+      if (ct < ntiles) {
+        compute(ct, cj, ring[i]);
+        next(ct, cj);
+        if (lt < ntiles) load(lt, lj, ring[i]);
+        next(lt, lj);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Register-resident activations for the single-row decode GEMV (M = 1, bf16
+// activations, 4-bit codes).  Lane li owns units li + 64c (c < NU) of every
+// row, so it only ever needs the activations of those units: it loads them
+// once from global memory and builds their bf16 pairs (in the code-extraction
+// order) and block sums in registers.  There is no LDS stage and no barrier;
+// a wave starts on its first row as soon as its own activations and weights
+// arrive.  Waves take rows n = global wave id + i * (total waves), with a ring
+// of D rows of weight loads in flight.
+// ---------------------------------------------------------------------------
+
+// Plane dwords of one 32-element block from its 16 raw bf16-pair dwords
+// R[i] = (x[2i], x[2i+1]), in the extraction order of plane_pair<SCH>.
+template <int SCH>
+RLXQ_DEV void pairs_from_raw(const uint32_t* R, uint32_t* X) {
+  constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;  // low / high halves of (R[a], R[b])
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if constexpr (SCH == SCH_MLX4) {
+      // t = 4i+e holds (8i+e, 8i+e+4): R[4i + e/2] and R[4i + 2 + e/2]
+      X[4 * i + 0] = perm_b32(R[4 * i + 2], R[4 * i + 0], LO);
+      X[4 * i + 1] = perm_b32(R[4 * i + 2], R[4 * i + 0], HI);
+      X[4 * i + 2] = perm_b32(R[4 * i + 3], R[4 * i + 1], LO);
+      X[4 * i + 3] = perm_b32(R[4 * i + 3], R[4 * i + 1], HI);
+    } else {
+      // GGUF nibble order: t = 4i + e, e=0 (4i, 4i+2), e=1 (4i+16, 4i+18),
+      // e=2 (4i+1, 4i+3), e=3 (4i+17, 4i+19)
+      X[4 * i + 0] = perm_b32(R[2 * i + 1], R[2 * i], LO);
+      X[4 * i + 2] = perm_b32(R[2 * i + 1], R[2 * i], HI);
+      X[4 * i + 1] = perm_b32(R[2 * i + 9], R[2 * i + 8], LO);
+      X[4 * i + 3] = perm_b32(R[2 * i + 9], R[2 * i + 8], HI);
+    }
+  }
+}
+
+template <int SCH, int NU, int D, int WAVES>
+RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
+  constexpr int BLOCKS = Unit<SCH>::BLOCKS;
+  constexpr int DW = Unit<SCH>::DW;
+  constexpr int BYTES = Unit<SCH>::BYTES;
+  constexpr bool MLX = SCH == SCH_MLX4;
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || MLX);
+  static_assert(!Unit<SCH>::BIT8, "register activations serve 4-bit codes");
+
+  const int K = a.K;
+  const int bpr = K >> 5;
+  const int U = bpr / BLOCKS;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t G = (int64_t)gridDim.x * WAVES;
+  const int64_t n0 = (int64_t)blockIdx.x * WAVES + wv;
+  const int gpr = MLX ? K / a.group : 0;
+
+  int uc[NU];
+  bool uok[NU];
+#pragma unroll
+  for (int c = 0; c < NU; c++) {
+    const int u = lane + 64 * c;
+    uok[c] = u < U;
+    uc[c] = uok[c] ? u : U - 1;
   }
 
+  // activations of my units (raw bf16 pairs)
+  uint32_t X[NU][BLOCKS][16];
+  const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x);
 #pragma unroll
-  for (int p = 0; p < P; p++) {
-    const int64_t n = row0 + p * RP;
+  for (int c = 0; c < NU; c++)
 #pragma unroll
-    for (int m = 0; m < MT; m++) {
-      float v = group_sum<L>(acc[p][m]);
-      const int64_t row = m0 + m;
-      if (li == 0 && n < N && row < M) {
-        int64_t yrow = row;
-        float sc = 1.f;
-        if (row_map) yrow = row_map[row];
-        if (row_scale) sc = row_scale[row];
-        if (yrow >= 0) {
-          const int64_t off = yrow * y_ld + n;
-          if (y_bf16) reinterpret_cast<uint16_t*>(y)[off] = (uint16_t)f32_to_bf16_bits(v * sc);
-          else reinterpret_cast<float*>(y)[off] = v * sc;
+    for (int bl = 0; bl < BLOCKS; bl++) {
+      const uint4* p = reinterpret_cast<const uint4*>(xb + (int64_t)(uc[c] * BLOCKS + bl) * 32);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint4 v = p[q];
+        X[c][bl][4 * q] = v.x; X[c][bl][4 * q + 1] = v.y; X[c][bl][4 * q + 2] = v.z; X[c][bl][4 * q + 3] = v.w;
+      }
+    }
+
+  struct Buf {
+    uint32_t dw[NU][DW];
+    float sm[NU][BLOCKS], bm[NU][BLOCKS];
+  };
+  auto load = [&](int64_t n, Buf& bf) {
+    const int64_t nn = n < a.N ? n : 0;
+    const uint8_t* rp = a.w + nn * a.rb;
+#pragma unroll
+    for (int c = 0; c < NU; c++) {
+      load_unit<SCH>(bf.dw[c], rp + (int64_t)uc[c] * BYTES);
+      if constexpr (MLX) {
+        const int64_t gi = nn * gpr + (uc[c] * 32) / a.group;
+        bf.sm[c][0] = load_sb(a.scales, gi, a.sb_bf16 != 0);
+        bf.bm[c][0] = load_sb(a.biases, gi, a.sb_bf16 != 0);
+      }
+    }
+  };
+  Buf ring[D];
+#pragma unroll
+  for (int i = 0; i < D; i++) load(n0 + i * G, ring[i]);
+
+  // pairs and block sums
+  float S[NU][BLOCKS];
+#pragma unroll
+  for (int c = 0; c < NU; c++)
+#pragma unroll
+    for (int bl = 0; bl < BLOCKS; bl++) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; i++) s = dot2_bf16(X[c][bl][i], 0x3F803F80u, s);
+      S[c][bl] = s;
+      uint32_t R[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) R[i] = X[c][bl][i];
+      pairs_from_raw<SCH>(R, X[c][bl]);
+    }
+
+  const UnpackK kc = unpack_consts();
+  int64_t n = n0;
+  while (n < a.N) {
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+      if (n < a.N) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < NU; c++)
+#pragma unroll
+          for (int bl = 0; bl < BLOCKS; bl++) {
+            float d, mn;
+            if constexpr (MLX) {
+              d = ring[i].sm[c][bl];
+              mn = ring[i].bm[c][bl];
+            } else {
+              block_scales<SCH>(ring[i].dw[c], bl, d, mn);
+            }
+            if (!uok[c]) {
+              d = 0.f;
+              mn = 0.f;
+            }
+            uint32_t pw[16];
+            block_pairs<SCH>(ring[i].dw[c], bl, pw, kc);
+            float ch = -chain_bias<SCH>() * S[c][bl];
+#pragma unroll
+            for (int t = 0; t < 16; t++) ch = dot2_bf16(pw[t], X[c][bl][t], ch);
+            acc = fmaf(d, ch, acc);
+            if constexpr (HAS_MIN) acc = fmaf(mn, S[c][bl], acc);
+          }
+        const float v = lane_group_sum<64>(acc);
+        if (lane == 0) {
+          int64_t yrow = 0;
+          float sc = 1.f;
+          if (a.row_map) yrow = a.row_map[0];
+          if (a.row_scale) sc = a.row_scale[0];
+          if (yrow >= 0) {
+            const int64_t off = yrow * a.y_ld + n;
+            if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v * sc);
+            else reinterpret_cast<float*>(a.y)[off] = v * sc;
+          }
         }
+        const int64_t nl = n + (int64_t)D * G;
+        if (nl < a.N) load(nl, ring[i]);
+        n += G;
       }
     }
   }
@@ -437,32 +764,49 @@ RLXQ_DEV void gemv_body(const void* __restrict__ x, const uint8_t* __restrict__ 
 }  // namespace rlxq
 
 // ---------------------------------------------------------------------------
-// Instantiations: rlxq_gemv_<scheme>_<x>_L<L>_P<P>_C<NBC>_M<MT>
-// Arguments (all kernels): x, w, scales, biases, sb_bf16, group, y, y_bf16,
-// M, K, N, rb (row bytes), row_map (NULL), row_scale (NULL), y_ld.
+// Instantiations: rlxq_gemv_<scheme>_<x>_L<L>_P<P>_C<C>_M<MT>_D<D>_W<WAVES>,
+// one rlxq_gemv_args argument.
 // ---------------------------------------------------------------------------
-#define RLXQ_GEMV_INST(NAME, SCH, XBF, L, P, NBC, MT)                                          \
-  extern "C" __global__ __launch_bounds__(256) void NAME(                                      \
-      const void* x, const uint8_t* w, const void* scales, const void* biases, int sb_bf16,    \
-      int group, void* y, int y_bf16, int64_t M, int K, int64_t N, int64_t rb,                 \
-      const int32_t* row_map, const float* row_scale, int64_t y_ld) {                          \
-    rlxq::gemv_body<SCH, XBF, L, P, NBC, MT>(x, w, scales, biases, sb_bf16, group, y, y_bf16, \
-                                             M, K, N, rb, row_map, row_scale, y_ld);           \
+#define RLXQ_GEMV_INST(NAME, SCH, XBF, L, P, C, MT, D, W)                                \
+  extern "C" __global__ __launch_bounds__(64 * W) void NAME(rlxq_gemv_args a) {         \
+    rlxq::gemv_body<SCH, XBF, L, P, C, MT, D, W>(a);                                     \
   }
 
-#define RLXQ_GEMV_SCHEME(SNAME, SCH)                                              \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_bf16_L64_P4_C2_M1, SCH, true, 64, 4, 2, 1)  \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_bf16_L64_P2_C3_M1, SCH, true, 64, 2, 3, 1)  \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_bf16_L16_P4_C2_M1, SCH, true, 16, 4, 2, 1)  \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_bf16_L8_P4_C2_M1, SCH, true, 8, 4, 2, 1)    \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_bf16_L64_P2_C2_M4, SCH, true, 64, 2, 2, 4)  \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_bf16_L8_P2_C2_M4, SCH, true, 8, 2, 2, 4)    \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_f32_L64_P4_C2_M1, SCH, false, 64, 4, 2, 1)  \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_f32_L64_P2_C3_M1, SCH, false, 64, 2, 3, 1)  \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_f32_L16_P4_C2_M1, SCH, false, 16, 4, 2, 1)  \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_f32_L8_P4_C2_M1, SCH, false, 8, 4, 2, 1)    \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_f32_L64_P2_C2_M4, SCH, false, 64, 2, 2, 4)  \
-  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_f32_L8_P2_C2_M4, SCH, false, 8, 2, 2, 4)
+#ifndef RLXQ_GEMV_SWEEP
+#define RLXQ_GEMV_X(SNAME, SCH, XN, XBF)                                                     \
+  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_##XN##_L64_P1_C2_M1_D1_W16, SCH, XBF, 64, 1, 2, 1, 1, 16) \
+  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_##XN##_L64_P1_C2_M1_D2_W16, SCH, XBF, 64, 1, 2, 1, 2, 16) \
+  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_##XN##_L64_P1_C2_M1_D3_W16, SCH, XBF, 64, 1, 2, 1, 3, 16) \
+  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_##XN##_L64_P1_C2_M1_D2_W8, SCH, XBF, 64, 1, 2, 1, 2, 8)   \
+  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_##XN##_L64_P1_C1_M1_D4_W16, SCH, XBF, 64, 1, 1, 1, 4, 16) \
+  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_##XN##_L64_P2_C1_M1_D2_W8, SCH, XBF, 64, 2, 1, 1, 2, 8)   \
+  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_##XN##_L32_P2_C1_M1_D2_W8, SCH, XBF, 32, 2, 1, 1, 2, 8)   \
+  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_##XN##_L16_P2_C1_M1_D2_W8, SCH, XBF, 16, 2, 1, 1, 2, 8)   \
+  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_##XN##_L8_P2_C1_M1_D2_W8, SCH, XBF, 8, 2, 1, 1, 2, 8)     \
+  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_##XN##_L64_P2_C1_M4_D1_W8, SCH, XBF, 64, 2, 1, 4, 1, 8)   \
+  RLXQ_GEMV_INST(rlxq_gemv_##SNAME##_##XN##_L8_P2_C1_M4_D1_W8, SCH, XBF, 8, 2, 1, 4, 1, 8)
+#endif
+
+#define RLXQ_GEMV_SCHEME(SNAME, SCH) \
+  RLXQ_GEMV_X(SNAME, SCH, bf16, true) \
+  RLXQ_GEMV_X(SNAME, SCH, f32, false)
+
+// Register-activation variants: rlxq_gemvxr_<scheme>_U<NU>_D<D>_W<WAVES>.
+#define RLXQ_GEMVXR_INST(NAME, SCH, NU, D, W)                                         \
+  extern "C" __global__ __launch_bounds__(64 * W) void NAME(rlxq_gemv_args a) {      \
+    rlxq::gemv_xr_body<SCH, NU, D, W>(a);                                             \
+  }
+#define RLXQ_GEMVXR_SCHEME(SNAME, SCH)                                  \
+  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U1_D2_W4, SCH, 1, 2, 4)       \
+  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U2_D2_W4, SCH, 2, 2, 4)       \
+  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U2_D1_W4, SCH, 2, 1, 4)       \
+  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U2_D3_W4, SCH, 2, 3, 4)       \
+  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U2_D2_W2, SCH, 2, 2, 2)       \
+  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U3_D2_W4, SCH, 3, 2, 4)       \
+  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U4_D1_W4, SCH, 4, 1, 4)
+RLXQ_GEMVXR_SCHEME(q4_1, SCH_Q4_1)
+RLXQ_GEMVXR_SCHEME(q4_0, SCH_Q4_0)
+RLXQ_GEMVXR_SCHEME(mlx4, SCH_MLX4)
 
 RLXQ_GEMV_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMV_SCHEME(q4_0, SCH_Q4_0)

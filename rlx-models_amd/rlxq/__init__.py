@@ -43,6 +43,7 @@ def lib() -> C.CDLL:
         "rlxq_destroy": (I, [P]),
         "rlxq_strerror": (C.c_char_p, [I]),
         "rlxq_last_error": (C.c_char_p, [P]),
+        "rlxq_last_kernel": (C.c_char_p, [P]),
         "rlxq_version": (C.c_char_p, []),
         "rlxq_row_bytes": (I64, [I, I64]),
         "rlxq_dequant_matmul": (I, [P, I, I, P, I, P, P, P, I, I64, I64, I64, P, I, P]),
@@ -130,6 +131,10 @@ class Context:
     def _check(self, rc: int, what: str) -> None:
         if rc != OK:
             raise RlxqError(rc, f"{what}: {strerror(rc)}: {lib().rlxq_last_error(self.h).decode()}")
+
+    @property
+    def last_kernel(self) -> str:
+        return lib().rlxq_last_kernel(self.h).decode()
 
     def dequant_matmul(self, x, w, scheme: int, n: int, *, group: int = 32, scales=None, biases=None,
                        y=None, y_dtype=None, stream=None):

@@ -271,3 +271,74 @@ def test_device_matmul_session(orc):
         dm.matmul(x, packed, m, k, n, rlxq.MLX_AFFINE4)
     assert e.value.status == rlxq.E_SCHEME
     dm.close()
+
+
+# Every compiled single-row GEMV variant (lanes per row, rows and unit chunks
+# per step, prefetch depth, waves per workgroup), forced through the dispatcher's override, on shapes that
+# leave ragged tiles, partial chunks and odd unit counts.
+GEMV_VARIANTS = ["64,1,2,1,16", "64,1,2,2,16", "64,1,2,3,16", "64,1,2,2,8", "64,1,1,4,16", "64,2,1,2,8", "32,2,1,2,8",
+                 "16,2,1,2,8", "8,2,1,2,8"]
+
+
+@pytest.mark.parametrize("cfg", GEMV_VARIANTS)
+@pytest.mark.parametrize("scheme", [1, 2, 3, 4])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_every_gemv_variant(ctx, orc, monkeypatch, cfg, scheme, xdt):
+    import torch
+    import rlxq
+
+    monkeypatch.setenv("RLXQ_GEMV_CFG", cfg)
+    for (m, k, n) in [(1, 4096, 300), (1, 768, 37), (3, 1280, 129), (1, 12288, 65)]:
+        announce(f"variant {cfg} scheme={scheme} x={xdt} {m}x{k}x{n}")
+        rng = np.random.default_rng(k + n + scheme)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        if scheme == 4:
+            codes = rng.integers(0, 16, (n, k)).astype(np.uint32)
+            wq = orc.mlx_pack(codes, 4)
+            sc = rng.uniform(0.01, 0.1, (n, k // 64)).astype(np.float32)
+            bi = rng.uniform(-0.5, 0.1, (n, k // 64)).astype(np.float32)
+            xt, xv = _x_as(x, xdt)
+            y = ctx.dequant_matmul(xt, _t(wq.view(np.uint8)), rlxq.MLX_AFFINE4, n, group=64, scales=_t(sc),
+                                   biases=_t(bi))
+            torch.cuda.synchronize()
+            got, want = y.cpu().numpy(), orc.mlx_matmul_f64(xv, wq, sc, bi, n, 4, 64)
+        else:
+            packed = orc.synth(scheme, rng, n, k)
+            got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt=xdt)
+        assert rel_err(got, want) <= TOL_F32, (cfg, m, k, n)
+
+
+# The register-activation path (M = 1, bf16 activations, 4-bit codes): every
+# compiled variant, including units per lane above what the shape needs
+# (masked chunks) and row counts that leave waves idle.
+XR_VARIANTS = ["1,2,4", "2,2,4", "2,1,4", "2,3,4", "2,2,2", "3,2,4", "4,1,4"]
+
+
+@pytest.mark.parametrize("cfg", XR_VARIANTS)
+@pytest.mark.parametrize("scheme", [2, 3, 4])
+def test_every_xr_variant(ctx, orc, monkeypatch, cfg, scheme):
+    import torch
+    import rlxq
+
+    monkeypatch.setenv("RLXQ_GEMV_XR", cfg)
+    nu = int(cfg.split(",")[0])
+    for (k, n) in [(2048, 300), (4096, 1031), (768, 37), (64 * 32 * nu, 5000)]:
+        if scheme == 2 and (k // 64 + 63) // 64 > nu or scheme != 2 and (k // 32 + 63) // 64 > nu:
+            continue
+        announce(f"xr {cfg} scheme={scheme} k={k} n={n}")
+        rng = np.random.default_rng(k + n + scheme)
+        x = rng.standard_normal((1, k)).astype(np.float32)
+        if scheme == 4:
+            codes = rng.integers(0, 16, (n, k)).astype(np.uint32)
+            wq = orc.mlx_pack(codes, 4)
+            sc = rng.uniform(0.01, 0.1, (n, k // 32)).astype(np.float32)
+            bi = rng.uniform(-0.5, 0.1, (n, k // 32)).astype(np.float32)
+            xt, xv = _x_as(x, "bf16")
+            y = ctx.dequant_matmul(xt, _t(wq.view(np.uint8)), rlxq.MLX_AFFINE4, n, group=32, scales=_t(sc),
+                                   biases=_t(bi))
+            torch.cuda.synchronize()
+            got, want = y.cpu().numpy(), orc.mlx_matmul_f64(xv, wq, sc, bi, n, 4, 32)
+        else:
+            packed = orc.synth(scheme, rng, n, k)
+            got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt="bf16")
+        assert rel_err(got, want) <= TOL_F32, (cfg, k, n)
