@@ -5,11 +5,13 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <string>
 
 #include "rlxq.h"
 #include "rlxq_internal.hpp"
 #include "gemv_args.h"
+#include "gemm_args.h"
 
 namespace rlxq {
 
@@ -99,6 +101,38 @@ int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const 
   return fail(ctx, RLXQ_E_SCHEME, std::string(what) + ": unsupported scheme " + std::to_string(scheme));
 }
 
+// Prefill dequant-GEMM launch: 128 x 128 output tiles, M tiles fastest so
+// neighbouring workgroups share a weight tile.
+int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const void* w, const void* scales,
+                  const void* biases, int sb_dtype, int64_t rb, int64_t m, int64_t k, int64_t n, void* y,
+                  int y_dtype, void* stream) {
+  char name[64];
+  std::snprintf(name, sizeof name, "rlxq_gemm_%s_t128", scheme_name(scheme));
+  hipFunction_t fn;
+  int rc;
+  if ((rc = get_fn(ctx, name, &fn))) return rc;
+  rlxq_gemm_args a;
+  a.x = x;
+  a.w = static_cast<const uint8_t*>(w);
+  a.scales = scales;
+  a.biases = biases;
+  a.y = y;
+  a.M = m;
+  a.N = n;
+  a.K = k;
+  a.rb = rb;
+  a.y_ld = n;
+  a.group = is_mlx(scheme) ? group : 32;
+  a.sb_bf16 = sb_dtype == RLXQ_BF16 ? 1 : 0;
+  a.y_bf16 = y_dtype == RLXQ_BF16 ? 1 : 0;
+  a.pad = 0;
+  void* args[] = {&a};
+  const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
+  if (tiles > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
+  const size_t lds = 2 * (128 + 128) * 72 * sizeof(uint16_t);
+  return launch(ctx, fn, dim3((unsigned)tiles, 1, 1), dim3(256, 1, 1), lds, stream, args, name);
+}
+
 int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dtype, const void* w,
                   const void* scales, const void* biases, int sb_dtype, int64_t m, int64_t k,
                   int64_t n, void* y, int y_dtype, void* stream) {
@@ -114,6 +148,20 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   const bool xbf = x_dtype == RLXQ_BF16;
   const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0) ? 2 : 1;
   const int64_t units = (k / 32) / blocks;
+
+  // Prefill: bf16 activations and bf16 output with at least 64 rows go to the
+  // MFMA dequant-GEMM (weights rounded to bf16 in LDS, fp32 accumulation).
+  // Everything else stays on the GEMV family, which keeps the products exact.
+  // RLXQ_PREFILL=gemv|gemm forces one of them where both apply (tests).
+  {
+    bool gemm_ok = xbf && k % 64 == 0 && m >= 1;
+    bool use_gemm = gemm_ok && y_dtype == RLXQ_BF16 && m >= 64;
+    if (const char* e = std::getenv("RLXQ_PREFILL")) {
+      if (!std::strcmp(e, "gemv")) use_gemm = false;
+      if (!std::strcmp(e, "gemm")) use_gemm = gemm_ok;
+    }
+    if (use_gemm) return gemm_dispatch(ctx, scheme, group, x, w, scales, biases, sb_dtype, rb, m, k, n, y, y_dtype, stream);
+  }
 
   rlxq_gemv_args a;
   a.x = x;

@@ -1,0 +1,17 @@
+/* Kernel argument block of the prefill dequant-GEMM kernels, shared by the
+ * host (g++) and device (hipcc) compilers: plain C types only. */
+#ifndef RLXQ_GEMM_ARGS_H
+#define RLXQ_GEMM_ARGS_H
+#include <stdint.h>
+
+typedef struct rlxq_gemm_args {
+  const void* x;          /* [M, K] bf16 activations                      */
+  const uint8_t* w;       /* packed weight rows, row stride rb bytes      */
+  const void* scales;     /* MLX: [N, K/group] (f32 or bf16), else NULL   */
+  const void* biases;     /* MLX: [N, K/group], else NULL                 */
+  void* y;                /* [M, N] output, leading dimension y_ld        */
+  int64_t M, N, K, rb, y_ld;
+  int32_t group, sb_bf16, y_bf16, pad;
+} rlxq_gemm_args;
+
+#endif

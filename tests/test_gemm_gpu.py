@@ -1,0 +1,109 @@
+"""Parity of the prefill dequant-GEMM (bf16 MFMA, weights rounded to bf16 in
+LDS, fp32 accumulation) against the CPU oracle, through the C ABI.  Bar:
+max|got - want| / max|want| <= 2e-2 with bf16 output (the prefill contract);
+`want` is the oracle's dequantized weights contracted in float64 with the
+bf16 activations the kernel saw."""
+import numpy as np
+import pytest
+
+from conftest import announce
+from test_gemv_gpu import _t, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL_PREFILL = 2e-2
+
+
+def run_gemm(ctx, orc, scheme, x32, packed, n, ydt="bf16", **kw):
+    import torch
+
+    k = x32.shape[1]
+    xt = _t(x32).to(torch.bfloat16)
+    y = ctx.dequant_matmul(xt, _t(packed), scheme, n, y_dtype=torch.bfloat16 if ydt == "bf16" else torch.float32, **kw)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy(), xt.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("scheme", [1, 2, 3])
+@pytest.mark.parametrize("mkn", [(128, 256, 128), (512, 4096, 1024), (300, 1280, 200), (64, 768, 96),
+                                 (129, 192, 130)], ids=str)
+def test_gemm_matches_oracle(ctx, orc, scheme, mkn):
+    m, k, n = mkn
+    announce(f"gemm scheme={scheme} {mkn}")
+    rng = np.random.default_rng(m + k + n)
+    packed = orc.synth(scheme, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got, xv = run_gemm(ctx, orc, scheme, x, packed, n)
+    assert ctx.last_kernel.startswith("rlxq_gemm_")
+    w = orc.dequantize(scheme, packed, k).astype(np.float64)
+    assert rel_err(got, xv.astype(np.float64) @ w.T) <= TOL_PREFILL
+
+
+@pytest.mark.parametrize("kn", [(4096, 24576), (12288, 4096)], ids=lambda s: f"{s[0]}to{s[1]}")
+def test_gemm_config4_shapes_m512(ctx, orc, kn):
+    """Config 4 shapes at M=512 (the larger M use the same tiles); f64 truth."""
+    k, n = kn
+    m = 512
+    announce(f"gemm config4 {k}->{n} m={m}")
+    rng = np.random.default_rng(4)
+    packed = orc.synth_q4_1(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got, xv = run_gemm(ctx, orc, 3, x, packed, n)
+    w = orc.dequantize(3, packed, k).astype(np.float64)
+    assert rel_err(got, xv.astype(np.float64) @ w.T) <= TOL_PREFILL
+
+
+def test_gemm_linearity_full_size(ctx, orc):
+    """Size-independent check at M=4096, 4096->24576: y(x1 + x2) = y(x1) + y(x2)
+    within bf16 rounding, on a sampled set of outputs checked against f64."""
+    import torch
+    import rlxq
+
+    m, k, n = 4096, 4096, 24576
+    announce("gemm linearity full size")
+    g = torch.Generator(device="cuda").manual_seed(7)
+    from bench import synth_q4_1_gpu
+
+    w = synth_q4_1_gpu(n, k, g)
+    x1 = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+    y1 = ctx.dequant_matmul(x1, w, rlxq.GGUF_Q4_1, n, y_dtype=torch.float32)
+    rows = torch.tensor([0, 1, 777, 2048, 4095], device="cuda")
+    torch.cuda.synchronize()
+    packed = w.cpu().numpy()
+    wd = orc.dequantize(3, packed.reshape(n, -1), k).astype(np.float64)
+    want = x1[rows].float().cpu().numpy().astype(np.float64) @ wd.T
+    got = y1[rows].cpu().numpy()
+    assert rel_err(got, want) <= TOL_PREFILL
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gemm_mlx(ctx, orc, bits):
+    import torch
+    import rlxq
+
+    m, k, n, group = 192, 512, 160, 64
+    announce(f"gemm mlx bits={bits}")
+    rng = np.random.default_rng(bits)
+    codes = rng.integers(0, 1 << bits, (n, k)).astype(np.uint32)
+    wq = orc.mlx_pack(codes, bits)
+    sc = rng.uniform(0.01, 0.1, (n, k // group)).astype(np.float32)
+    bi = rng.uniform(-0.5, 0.1, (n, k // group)).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    scheme = rlxq.MLX_AFFINE4 if bits == 4 else rlxq.MLX_AFFINE8
+    got, xv = run_gemm(ctx, orc, scheme, x, wq.view(np.uint8), n, group=group, scales=_t(sc), biases=_t(bi))
+    assert ctx.last_kernel.startswith("rlxq_gemm_")
+    want = xv.astype(np.float64) @ orc.mlx_dequantize(wq, sc, bi, k, bits, group).astype(np.float64).T
+    assert rel_err(got, want) <= TOL_PREFILL
+
+
+def test_gemm_forced_for_small_m_and_f32_output(ctx, orc, monkeypatch):
+    """The dispatcher override runs the GEMM for M=1..63 and f32 output too."""
+    monkeypatch.setenv("RLXQ_PREFILL", "gemm")
+    rng = np.random.default_rng(9)
+    for m in (1, 7, 63):
+        packed = orc.synth_q4_1(rng, 200, 256)
+        x = rng.standard_normal((m, 256)).astype(np.float32)
+        got, xv = run_gemm(ctx, orc, 3, x, packed, 200, ydt="f32")
+        assert ctx.last_kernel.startswith("rlxq_gemm_")
+        w = orc.dequantize(3, packed, 256).astype(np.float64)
+        assert rel_err(got, xv.astype(np.float64) @ w.T) <= TOL_PREFILL
