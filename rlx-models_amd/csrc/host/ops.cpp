@@ -19,6 +19,8 @@ namespace {
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+}  // namespace
+
 const char* scheme_name(int s) {
   switch (s) {
     case RLXQ_GGUF_Q8_0: return "q8_0";
@@ -29,6 +31,8 @@ const char* scheme_name(int s) {
     default: return nullptr;
   }
 }
+
+namespace {
 
 struct GemvCfg {
   int L, P, C, MT, D, W;
@@ -318,19 +322,6 @@ int rlxq_moe_route(rlxq_ctx* ctx, const float* logits, int64_t rows, int64_t num
   int E = (int)num_experts, K = (int)top_k, rn = renorm ? 1 : 0;
   void* args[] = {(void*)&logits, &R, &E, &K, &rn, (void*)&ids, (void*)&probs};
   return launch(ctx, fn, dim3((unsigned)rows), dim3(64), 0, stream, args, "moe_route");
-}
-
-int rlxq_dequant_grouped_matmul(rlxq_ctx* ctx, int, int, const void*, int, const void*, const void*,
-                                const void*, int, const float*, int64_t, int64_t, int64_t, int64_t, void*,
-                                int, void*) {
-  if (!ctx) return RLXQ_E_NULL;
-  return fail(ctx, RLXQ_E_NOKERNEL, "dequant_grouped_matmul: not built yet");
-}
-
-int rlxq_moe_grouped(rlxq_ctx* ctx, int, int, const void*, int, const void*, const int32_t*, const float*,
-                     int64_t, int64_t, int64_t, int64_t, int64_t, void*, int, void*) {
-  if (!ctx) return RLXQ_E_NULL;
-  return fail(ctx, RLXQ_E_NOKERNEL, "moe_grouped: not built yet");
 }
 
 int rlxq_w8a8_gemm(rlxq_ctx* ctx, const void*, int, const int8_t*, const float*, int64_t, int64_t, int64_t,

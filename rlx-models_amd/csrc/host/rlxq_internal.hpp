@@ -60,6 +60,12 @@ bool is_gguf(int scheme);
 bool is_mlx(int scheme);
 int64_t gguf_block_bytes(int scheme);
 
+// Validates a weight operand (scheme, alignment, MLX scale slabs) and returns
+// the packed row stride in bytes.
+int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const void* w, const void* scales,
+                  const void* biases, int sb_dtype, int64_t k, int64_t* rb);
+const char* scheme_name(int scheme);
+
 // Entry points implemented in other translation units.
 int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dtype, const void* w,
                   const void* scales, const void* biases, int sb_dtype, int64_t m, int64_t k,

@@ -1,0 +1,396 @@
+// Building blocks of the dequant-GEMV family (dense decode and grouped
+// experts): per-scheme unit geometry, activation records, code unpacking and
+// block dot products.  See gemv.hip for how they are put together.
+#pragma once
+#include "common.hip.h"
+#include "gemv_args.h"
+
+namespace rlxq {
+
+template <int SCH>
+struct Unit;
+template <>
+struct Unit<SCH_Q4_1> {
+  static constexpr int BLOCKS = 1, BYTES = 20, DW = 5;
+  static constexpr bool BIT8 = false;
+};
+template <>
+struct Unit<SCH_Q4_0> {
+  static constexpr int BLOCKS = 2, BYTES = 36, DW = 9;
+  static constexpr bool BIT8 = false;
+};
+template <>
+struct Unit<SCH_Q8_0> {
+  static constexpr int BLOCKS = 2, BYTES = 68, DW = 17;
+  static constexpr bool BIT8 = true;
+};
+template <>
+struct Unit<SCH_MLX4> {
+  static constexpr int BLOCKS = 1, BYTES = 16, DW = 4;
+  static constexpr bool BIT8 = false;
+};
+template <>
+struct Unit<SCH_MLX8> {
+  static constexpr int BLOCKS = 1, BYTES = 32, DW = 8;
+  static constexpr bool BIT8 = true;
+};
+
+// Offset that the code -> float trick adds to each code, and the value the
+// dot chain starts from (in units of the block's plane sum) so that the chain
+// ends at sum(w_int * x) where w_int is the scheme's integer weight:
+//   Q4_1/MLX4: q (bias 128)    Q4_0: q - 8 (bias 136)
+//   Q8_0: q (bias 1024 + 128, codes stored as q ^ 0x80)   MLX8: code (1024)
+template <int SCH>
+RLXQ_DEV constexpr float chain_bias() {
+  return SCH == SCH_Q4_0 ? 136.f : (SCH == SCH_Q8_0 ? 1152.f : (SCH == SCH_MLX8 ? 1024.f : 128.f));
+}
+
+// Element pair (a, b) of a 32-element block that plane dword t carries.
+template <int SCH>
+RLXQ_DEV void plane_pair(int t, int& a, int& b) {
+  if constexpr (SCH == SCH_Q4_0 || SCH == SCH_Q4_1) {
+    // qs dword i holds bytes 4i..4i+3; byte j = element j (low nibble) and
+    // element j+16 (high nibble).  Extraction e shifts by 4e and masks
+    // 0x000F000F: e=0 -> (4i, 4i+2), e=1 -> (4i+16, 4i+18),
+    // e=2 -> (4i+1, 4i+3), e=3 -> (4i+17, 4i+19).
+    int i = t >> 2, e = t & 3;
+    int base = 4 * i + ((e & 1) ? 16 : 0) + ((e & 2) ? 1 : 0);
+    a = base;
+    b = base + 2;
+  } else if constexpr (SCH == SCH_MLX4) {
+    // u32 word i holds codes 8i..8i+7 LSB-first; extraction e -> (8i+e, 8i+e+4).
+    int i = t >> 2, e = t & 3;
+    a = 8 * i + e;
+    b = 8 * i + e + 4;
+  } else {
+    // byte codes, dword i = codes 4i..4i+3; e=0 -> (4i, 4i+2), e=1 -> (4i+1, 4i+3).
+    int i = t >> 1, e = t & 1;
+    a = 4 * i + e;
+    b = 4 * i + e + 2;
+  }
+}
+
+// Record layout (dwords): NPL planes of 16 pair-dwords, then
+// [S = sum of the plane values, SX = sum of x, SCL = block x scale, 0].
+template <int NPL>
+struct Rec {
+  static constexpr int STRIDE = NPL * 16 + 4;
+};
+
+// Sum / max over aligned groups of 8 lanes (DPP quad butterflies, then the
+// half-row mirror); every lane of the group gets the result.
+RLXQ_DEV float group8_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+RLXQ_DEV float group8_max(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+  return v;
+}
+RLXQ_DEV uint32_t swap_lane_pair(uint32_t v) {  // value of lane ^ 1
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+}
+
+// Building the x records of MT activation rows into LDS.  Eight lanes share
+// a record; lane q converts elements 4q..4q+3 of it and writes the two plane
+// dwords they form (and their lo twins), lane 0 of the group the sums and the
+// block scale.  Tasks (record, q) of one activation row are numbered
+// 8*block + q; a thread handles tasks threadIdx.x + i*blockDim.x in batches of
+// XB: stage_fetch issues a batch's activation loads, stage_store converts and
+// writes it.  The loop structure is uniform over the workgroup (the group
+// reductions use DPP).
+template <bool XBF16>
+struct XRaw {
+  static constexpr int XB = XBF16 ? 8 : 4;
+  uint32_t w[XB][XBF16 ? 2 : 4];
+};
+
+template <bool XBF16>
+RLXQ_DEV void stage_fetch(XRaw<XBF16>& raw, const void* xv, int64_t row, int64_t M, int K, int base) {
+  constexpr int XB = XRaw<XBF16>::XB;
+  const int ntask = (K >> 5) * 8;
+#pragma unroll
+  for (int i = 0; i < XB; i++) {
+    const int task = base + i * blockDim.x + threadIdx.x;
+    const int64_t off = row * (int64_t)K + 4 * task;
+    if constexpr (XBF16) {
+      uint2 u = make_uint2(0u, 0u);
+      if (task < ntask && row < M) u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(xv) + off);
+      raw.w[i][0] = u.x;
+      raw.w[i][1] = u.y;
+    } else {
+      uint4 u = make_uint4(0u, 0u, 0u, 0u);
+      if (task < ntask && row < M) u = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(xv) + off);
+      raw.w[i][0] = u.x; raw.w[i][1] = u.y; raw.w[i][2] = u.z; raw.w[i][3] = u.w;
+    }
+  }
+}
+
+template <int SCH, bool XBF16, int NPL>
+RLXQ_DEV void stage_store(uint32_t* lds, const XRaw<XBF16>& raw, int m, int K, int base) {
+  constexpr bool BIT8 = Unit<SCH>::BIT8;
+  constexpr int RS = Rec<NPL>::STRIDE;
+  constexpr int XB = XRaw<XBF16>::XB;
+  const int bpr = K >> 5;
+  const int ntask = bpr * 8;
+#pragma unroll
+  for (int i = 0; i < XB; i++) {
+    if (base + i * (int)blockDim.x >= ntask) break;  // uniform
+    const int task = base + i * blockDim.x + threadIdx.x;
+    const bool active = task < ntask;
+    const int r = m * bpr + (task >> 3), q = task & 7;
+    float v[4];
+    if constexpr (XBF16) {
+      v[0] = bf16_bits_to_f32(raw.w[i][0] & 0xffffu);
+      v[1] = bf16_bits_to_f32(raw.w[i][0] >> 16);
+      v[2] = bf16_bits_to_f32(raw.w[i][1] & 0xffffu);
+      v[3] = bf16_bits_to_f32(raw.w[i][1] >> 16);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; k++) v[k] = __uint_as_float(raw.w[i][k]);
+    }
+    const float sx = group8_sum((v[0] + v[1]) + (v[2] + v[3]));
+    float scl = 1.f;
+    if constexpr (BIT8) {
+      const float amax = group8_max(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+      if (amax > 0.f && amax < INFINITY) {
+        const int e = ilogbf(amax) - 14;  // scaled max lands in [2^14, 2^15)
+        scl = ldexpf(1.f, e);
+        const float inv = ldexpf(1.f, -e);
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] *= inv;
+      }
+    }
+    uint32_t hi[4], lo[4];
+    float ps = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      if constexpr (BIT8) {
+        hi[k] = f32_to_f16_bits(v[k]);
+        const float hv = f16_bits_to_f32(hi[k]);
+        lo[k] = NPL == 2 ? f32_to_f16_bits(v[k] - hv) : 0u;
+        ps += NPL == 2 ? hv + f16_bits_to_f32(lo[k]) : hv;
+      } else if constexpr (XBF16) {
+        hi[k] = __float_as_uint(v[k]) >> 16;  // exact: the input is bf16
+        lo[k] = 0u;
+      } else {
+        hi[k] = f32_to_bf16_bits(v[k]);
+        const float hv = bf16_bits_to_f32(hi[k]);
+        lo[k] = f32_to_bf16_bits(v[k] - hv);
+        ps += hv + bf16_bits_to_f32(lo[k]);
+      }
+    }
+    const float S = (!BIT8 && XBF16) ? sx : group8_sum(ps);
+    // the two plane dwords of this lane and their positions t0, t1
+    uint32_t h0, h1, l0 = 0u, l1 = 0u;
+    int t0, t1;
+    if constexpr (SCH == SCH_MLX4) {
+      // pairs (8j+e, 8j+e+4): even lanes hold 8j..8j+3, odd lanes 8j+4..8j+7
+      const uint32_t hp01 = swap_lane_pair(hi[0] | (hi[1] << 16)), hp23 = swap_lane_pair(hi[2] | (hi[3] << 16));
+      const uint32_t lp01 = swap_lane_pair(lo[0] | (lo[1] << 16)), lp23 = swap_lane_pair(lo[2] | (lo[3] << 16));
+      const int j = q >> 1;
+      if ((q & 1) == 0) {
+        h0 = hi[0] | (hp01 << 16);
+        h1 = hi[1] | (hp01 & 0xffff0000u);
+        l0 = lo[0] | (lp01 << 16);
+        l1 = lo[1] | (lp01 & 0xffff0000u);
+        t0 = 4 * j;
+        t1 = 4 * j + 1;
+      } else {
+        h0 = (hp23 & 0xffffu) | (hi[2] << 16);
+        h1 = (hp23 >> 16) | (hi[3] << 16);
+        l0 = (lp23 & 0xffffu) | (lo[2] << 16);
+        l1 = (lp23 >> 16) | (lo[3] << 16);
+        t0 = 4 * j + 2;
+        t1 = 4 * j + 3;
+      }
+    } else {
+      // pairs (4q, 4q+2) and (4q+1, 4q+3)
+      h0 = hi[0] | (hi[2] << 16);
+      h1 = hi[1] | (hi[3] << 16);
+      l0 = lo[0] | (lo[2] << 16);
+      l1 = lo[1] | (lo[3] << 16);
+      if constexpr (BIT8) {
+        t0 = 2 * q;
+        t1 = 2 * q + 1;
+      } else {
+        // GGUF nibble order: elements 4i.. -> e = 0/2, elements 16+4i.. -> e = 1/3
+        t0 = q < 4 ? 4 * q : 4 * (q - 4) + 1;
+        t1 = t0 + 2;
+      }
+    }
+    if (active) {
+      uint32_t* rec = lds + (size_t)r * RS;
+      rec[t0] = h0;
+      rec[t1] = h1;
+      if constexpr (NPL == 2) {
+        rec[16 + t0] = l0;
+        rec[16 + t1] = l1;
+      }
+      if (q == 0) {
+        rec[NPL * 16 + 0] = __float_as_uint(S);
+        rec[NPL * 16 + 1] = __float_as_uint(sx);
+        rec[NPL * 16 + 2] = __float_as_uint(scl);
+        rec[NPL * 16 + 3] = 0u;
+      }
+    }
+  }
+}
+
+// Constants of the code -> float tricks, held in VGPRs so that the unpack
+// compiles to one v_and_or_b32 per pair (a VOP3 instruction on gfx950 cannot
+// take two literal operands).
+struct UnpackK {
+  uint32_t mask, magic;
+};
+RLXQ_DEV UnpackK unpack_consts() {
+  UnpackK k{0x000F000Fu, 0x43004300u};
+  asm volatile("" : "+v"(k.mask), "+v"(k.magic));
+  return k;
+}
+
+// 4-bit: four bf16 (128 + q) pairs per dword of nibbles.
+RLXQ_DEV void nib_pairs(uint32_t w, uint32_t* out, const UnpackK& k) {
+  out[0] = (w & k.mask) | k.magic;
+  out[1] = ((w >> 4) & k.mask) | k.magic;
+  out[2] = ((w >> 8) & k.mask) | k.magic;
+  out[3] = ((w >> 12) & k.mask) | k.magic;
+}
+
+// 8-bit: two f16 (1024 + u) pairs per dword of unsigned byte codes.
+RLXQ_DEV void byte_pairs(uint32_t u, uint32_t* out) {
+  out[0] = perm_b32(0x64646464u, u, 0x04020400u);
+  out[1] = perm_b32(0x64646464u, u, 0x04030401u);
+}
+
+// Fetch one unit at p (always a valid address; out-of-range units are
+// clamped by the caller and their scales zeroed).
+template <int SCH>
+RLXQ_DEV void load_unit(uint32_t* dw, const uint8_t* p) {
+  if constexpr (SCH == SCH_Q4_1) {
+    dw[0] = ld_u32(p);
+    uint4 q = ld_u128(p + 4);
+    dw[1] = q.x; dw[2] = q.y; dw[3] = q.z; dw[4] = q.w;
+  } else if constexpr (SCH == SCH_Q4_0) {
+    uint4 a = ld_u128(p), b = ld_u128(p + 16);
+    dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
+    dw[4] = b.x; dw[5] = b.y; dw[6] = b.z; dw[7] = b.w;
+    dw[8] = ld_u32(p + 32);
+  } else if constexpr (SCH == SCH_Q8_0) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint4 a = ld_u128(p + 16 * q);
+      dw[4 * q] = a.x; dw[4 * q + 1] = a.y; dw[4 * q + 2] = a.z; dw[4 * q + 3] = a.w;
+    }
+    dw[16] = ld_u32(p + 64);
+  } else if constexpr (SCH == SCH_MLX4) {
+    uint4 a = ld_u128(p);
+    dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
+  } else {
+    uint4 a = ld_u128(p), b = ld_u128(p + 16);
+    dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
+    dw[4] = b.x; dw[5] = b.y; dw[6] = b.z; dw[7] = b.w;
+  }
+}
+
+// Block scale terms of block `blk` of a fetched unit: d multiplies the dot
+// chain, m (Q4_1 min) multiplies the block sum of x.
+template <int SCH>
+RLXQ_DEV void block_scales(const uint32_t* dw, int blk, float& d, float& m) {
+  if constexpr (SCH == SCH_Q4_1) {
+    d = f16_bits_to_f32(dw[0] & 0xffffu);
+    m = f16_bits_to_f32(dw[0] >> 16);
+  } else if constexpr (SCH == SCH_Q4_0 || SCH == SCH_Q8_0) {
+    constexpr int HI = SCH == SCH_Q4_0 ? 4 : 8;  // dword holding block B's d in its high half
+    d = blk == 0 ? f16_bits_to_f32(dw[0] & 0xffffu) : f16_bits_to_f32(dw[HI] >> 16);
+    m = 0.f;
+  } else {
+    d = 0.f;
+    m = 0.f;
+  }
+}
+
+// The 16 pair-dwords of block `blk` of a fetched unit.
+template <int SCH>
+RLXQ_DEV void block_pairs(const uint32_t* dw, int blk, uint32_t* pw, const UnpackK& k) {
+  if constexpr (SCH == SCH_Q4_1) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) nib_pairs(dw[1 + i], &pw[4 * i], k);
+  } else if constexpr (SCH == SCH_Q4_0) {
+    if (blk == 0) {
+      // block A: d = bytes 0-1, qs = bytes 2..17 (re-aligned by 2 bytes)
+#pragma unroll
+      for (int i = 0; i < 4; i++) nib_pairs(align_bytes(dw[i + 1], dw[i], 2), &pw[4 * i], k);
+    } else {
+      // block B: d = bytes 18-19, qs = bytes 20..35
+#pragma unroll
+      for (int i = 0; i < 4; i++) nib_pairs(dw[5 + i], &pw[4 * i], k);
+    }
+  } else if constexpr (SCH == SCH_Q8_0) {
+    if (blk == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) byte_pairs(align_bytes(dw[i + 1], dw[i], 2) ^ 0x80808080u, &pw[2 * i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) byte_pairs(dw[9 + i] ^ 0x80808080u, &pw[2 * i]);
+    }
+  } else if constexpr (SCH == SCH_MLX4) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) nib_pairs(dw[i], &pw[4 * i], k);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) byte_pairs(dw[i], &pw[2 * i]);
+  }
+}
+
+// sum over the block of (bias + code) * x, started at -bias * S so that it
+// ends at sum(w_int * x).
+template <int SCH, int NPL>
+RLXQ_DEV float block_dot(const uint32_t* pw, const uint32_t* xr) {
+  constexpr bool BIT8 = Unit<SCH>::BIT8;
+  float c = -chain_bias<SCH>() * __uint_as_float(xr[NPL * 16 + 0]);
+#pragma unroll
+  for (int t = 0; t < 16; t++) {
+    if constexpr (BIT8) {
+      c = dot2_f16(pw[t], xr[t], c);
+      if constexpr (NPL == 2) c = dot2_f16(pw[t], xr[16 + t], c);
+    } else {
+      c = dot2_bf16(pw[t], xr[t], c);
+      if constexpr (NPL == 2) c = dot2_bf16(pw[t], xr[16 + t], c);
+    }
+  }
+  return c;
+}
+
+// MLX scale/bias for (row n, block b); sb_bf16 selects the slab dtype.
+RLXQ_DEV float load_sb(const void* p, int64_t idx, bool bf16) {
+  if (bf16) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[idx]);
+  return reinterpret_cast<const float*>(p)[idx];
+}
+
+// Sum over aligned groups of L lanes with DPP row operations; for L = 64 the
+// four 16-lane row sums are combined through readlane, so every lane ends
+// with its group's sum.
+template <int L>
+RLXQ_DEV float lane_group_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  if constexpr (L == 2) return v;
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  if constexpr (L == 4) return v;
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  if constexpr (L == 8) return v;
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  if constexpr (L == 16) return v;
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  if constexpr (L == 32) return (threadIdx.x & 32) ? r2 + r3 : r0 + r1;
+  return (r0 + r1) + (r2 + r3);
+}
+
+}  // namespace rlxq

@@ -1,0 +1,36 @@
+/* Argument blocks of the grouped-expert kernels, shared by the host (g++)
+ * and device (hipcc) compilers: plain C types only. */
+#ifndef RLXQ_MOE_ARGS_H
+#define RLXQ_MOE_ARGS_H
+#include <stdint.h>
+
+/* Routing table in scratch memory (int32):
+ *   [0]                      number of fired experts F
+ *   [1, 1 + E)               fired expert ids, slots 0..F-1
+ *   [1 + E, 2 + 2E)          entry offsets per slot, F + 1 valid
+ *   [2 + 2E, 2 + 2E + n)     entry ids grouped by slot
+ * An entry is one (token row, top-k slot) pair: entry = row * top_k + slot. */
+typedef struct rlxq_moe_table_args {
+  const int32_t* ids;     /* [n] int32 expert ids, or NULL               */
+  const float* idx_f32;   /* [n] f32 expert ids (IR form), or NULL       */
+  int32_t* table;         /* routing table, 2 + 2E + n int32             */
+  void* zero_rows;        /* rows of invalid entries are zeroed here     */
+  int64_t n, N, zero_ld;  /* entries, row length, row stride of zero_rows */
+  int32_t E, zero_bf16;
+} rlxq_moe_table_args;
+
+typedef struct rlxq_moe_gemv_args {
+  const void* x;          /* activations                                  */
+  const uint8_t* bank;    /* E contiguous [N, K] packed slabs             */
+  const void* scales;     /* MLX: [E, N, K/group], else NULL              */
+  const void* biases;
+  const int32_t* table;   /* routing table (see above)                   */
+  void* y;                /* output rows, leading dimension y_ld          */
+  int64_t N, rb, y_ld, x_ld;
+  int32_t K, E, group, sb_bf16, y_bf16;
+  int32_t x_div;          /* activation row of entry = entry / x_div      */
+  int32_t tiles_n;        /* row tiles per expert                         */
+  int32_t pad;
+} rlxq_moe_gemv_args;
+
+#endif

@@ -1,0 +1,230 @@
+"""Parity of the grouped-expert path (device routing table + grouped GEMV),
+the router and SwiGLU, against the CPU oracle, through the C ABI.  Bar:
+max|got - want| / max|want| <= 1e-3 with f32 output (the reference's own
+bars are 1e-2 grouped and 2e-2 MoE accumulate,
+crates/rlx-unlimited-ocr/tests/quant_parity_backends.rs:301,424)."""
+import numpy as np
+import pytest
+
+from conftest import announce
+from test_gemv_gpu import _ref_input, _ref_weight, _t, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+# (rows, k, n, experts), quant_parity_backends.rs:260-266
+GROUPED_SHAPES = [(4, 256, 128, 3), (1, 1280, 896, 8), (128, 1280, 896, 64), (128, 896, 1280, 64)]
+
+
+def _bank(orc, scheme, n, k, e_count, seed0=0.3, step=1.0):
+    bank = np.concatenate([_ref_weight(n, k, seed0 + e * step) for e in range(e_count)])
+    return orc.quantize(scheme, bank)
+
+
+@pytest.mark.parametrize("scheme", [1, 2, 3])
+@pytest.mark.parametrize("shape", GROUPED_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_grouped_reference_shapes(ctx, orc, scheme, shape):
+    """check_grouped: bank [E, N, K], row r uses expert (7r + 1) % E."""
+    import torch
+
+    rows, k, n, E = shape
+    announce(f"grouped scheme={scheme} {shape}")
+    x = _ref_input(rows, k)
+    packed = _bank(orc, scheme, n, k, E)
+    idx = np.array([(r * 7 + 1) % E for r in range(rows)], np.float32)
+    y = ctx.grouped_matmul(_t(x), _t(packed), _t(idx), scheme, n, E)
+    torch.cuda.synchronize()
+    want = orc.grouped_matmul_f64(scheme, x, packed, idx, n, E)
+    assert rel_err(y.cpu().numpy(), want) <= TOL
+
+
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_grouped_many_rows_per_expert(ctx, orc, xdt):
+    """Skewed routing: one expert takes most rows (several MT chunks)."""
+    import torch
+
+    rows, k, n, E = 37, 512, 300, 5
+    announce(f"grouped skewed x={xdt}")
+    rng = np.random.default_rng(1)
+    packed = orc.synth_q4_1(rng, E * n, k)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    idx = np.where(np.arange(rows) % 5 == 0, 4, 2).astype(np.float32)
+    xt = _t(x) if xdt == "f32" else _t(x).to(torch.bfloat16)
+    y = ctx.grouped_matmul(xt, _t(packed), _t(idx), 3, n, E)
+    torch.cuda.synchronize()
+    xv = xt.float().cpu().numpy()
+    assert rel_err(y.cpu().numpy(), orc.grouped_matmul_f64(3, xv, packed, idx, n, E)) <= TOL
+
+
+def test_grouped_invalid_index_gives_zero_row(ctx, orc):
+    import torch
+
+    rows, k, n, E = 6, 256, 64, 4
+    announce("grouped invalid index")
+    rng = np.random.default_rng(2)
+    packed = orc.synth_q8_0(rng, E * n, k)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    idx = np.array([0, 1.5, 3, 4, -1, 2], np.float32)
+    y = ctx.grouped_matmul(_t(x), _t(packed), _t(idx), 1, n, E)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    for r in (1, 3, 4):
+        assert np.all(got[r] == 0.0)
+    for r in (0, 2, 5):
+        want = orc.matmul_f64(1, x[r:r + 1], packed[int(idx[r]) * n:(int(idx[r]) + 1) * n], n)
+        assert rel_err(got[r:r + 1], want) <= TOL
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_grouped_mlx_bf16_slabs(ctx, orc, bits):
+    """Op::DequantGroupedMatMulMlx: bf16 scale/bias slabs [E, N, K/group]."""
+    import torch
+    import rlxq
+
+    rows, k, n, E, group = 9, 256, 96, 3, 64
+    announce(f"grouped mlx bits={bits}")
+    rng = np.random.default_rng(bits)
+    codes = rng.integers(0, 1 << bits, (E * n, k)).astype(np.uint32)
+    wq = orc.mlx_pack(codes, bits)
+    sc = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(rng.uniform(0.01, 0.1, (E * n, k // group))))
+    bi = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(rng.uniform(-0.5, 0.1, (E * n, k // group))))
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    idx = (np.arange(rows) % E).astype(np.float32)
+    scheme = rlxq.MLX_AFFINE4 if bits == 4 else rlxq.MLX_AFFINE8
+    y = ctx.grouped_matmul(_t(x), _t(wq.view(np.uint8)), _t(idx), scheme, n, E, group=group,
+                           scales=_t(sc).to(torch.bfloat16), biases=_t(bi).to(torch.bfloat16))
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    want = np.zeros((rows, n))
+    for r in range(rows):
+        e = int(idx[r])
+        sl = slice(e * n, (e + 1) * n)
+        want[r] = orc.mlx_matmul_f64(x[r:r + 1], wq[sl], sc[sl], bi[sl], n, bits, group)[0]
+    assert rel_err(got, want) <= TOL
+
+
+def _moe_logits(rows, ne):
+    """quant_parity_backends.rs:350-352."""
+    i = np.arange(rows * ne, dtype=np.float32)
+    return ((np.sin(i * np.float32(0.29)) * np.float32(2.0)) + (i // ne).astype(np.float32) * np.float32(0.05)).reshape(rows, ne)
+
+
+@pytest.mark.parametrize("scheme", [1, 2])
+@pytest.mark.parametrize("top_k", [1, 6])
+def test_moe_accumulate_reference(ctx, orc, scheme, top_k):
+    """check_moe_accumulate: softmax -> top-k -> per-slot grouped matmul ->
+    probability-weighted sum (64 rows, K=1280, N=896, E=64), through the
+    device router and the COMBINE mode."""
+    import torch
+    import rlxq
+
+    ROWS, K, N, NE = 64, 1280, 896, 64
+    announce(f"moe accumulate scheme={scheme} k={top_k}")
+    x = _ref_input(ROWS, K)
+    packed = _bank(orc, scheme, N, K, NE, 0.3, 0.11)
+    logits = _moe_logits(ROWS, NE)
+    ids, probs = ctx.moe_route(_t(logits), top_k, False)
+    torch.cuda.synchronize()
+    oids, oprobs = orc.topk_softmax(logits, top_k)
+    assert np.array_equal(ids.cpu().numpy(), oids)
+    assert np.allclose(probs.cpu().numpy(), oprobs, rtol=1e-5, atol=1e-7)
+    x_exp = np.repeat(x, top_k, axis=0)
+    y = ctx.moe_grouped(_t(x_exp), _t(packed), ids, probs, scheme, rlxq.MOE_COMBINE, N, NE)
+    torch.cuda.synchronize()
+    want = orc.moe_f64(scheme, x, packed, oids, probs.cpu().numpy(), N, NE)
+    assert rel_err(y.cpu().numpy(), want) <= TOL
+    y_exp = ctx.moe_grouped(_t(x), _t(packed), ids, probs, scheme, rlxq.MOE_EXPAND, N, NE)
+    torch.cuda.synchronize()
+    want_exp = orc.grouped_matmul_f64(scheme, x_exp, packed, oids.ravel().astype(np.float32), N, NE)
+    assert rel_err(y_exp.cpu().numpy(), want_exp) <= TOL
+
+
+def test_moe_ffn_config5(ctx, orc):
+    """Config 5: 128 experts, hidden 2048, expert intermediate 768 (gate|up
+    2048->1536 fused, down 768->2048), top-8 of softmax(N(0,1)) logits, 16
+    tokens, Q4_1; renormalised top-k (norm_topk_prob)."""
+    import torch
+    import rlxq
+
+    T, H, I, E, TOPK = 16, 2048, 768, 128, 8
+    announce("moe ffn config 5")
+    rng = np.random.default_rng(0)
+    gate_up = orc.synth_q4_1(rng, E * 2 * I, H)
+    down = orc.synth_q4_1(rng, E * H, I)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    xt = _t(x).to(torch.bfloat16)
+    xv = xt.float().cpu().numpy()
+    ids, probs = ctx.moe_route(_t(logits), TOPK, True)
+    gu = ctx.moe_grouped(xt, _t(gate_up), ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_EXPAND, 2 * I, E)
+    act = ctx.swiglu(gu, I, out_dtype=torch.bfloat16)
+    y = ctx.moe_grouped(act, _t(down), ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_COMBINE, H, E)
+    torch.cuda.synchronize()
+    oids, oprobs = orc.topk_softmax(logits, TOPK, renorm=True)
+    assert np.array_equal(ids.cpu().numpy(), oids)
+    # oracle chain in float64 on the same intermediate rounding points
+    gu_w = orc.grouped_matmul_f64(3, np.repeat(xv, TOPK, axis=0), gate_up, oids.ravel().astype(np.float32), 2 * I, E)
+    assert rel_err(gu.cpu().numpy(), gu_w) <= TOL
+    g, u = gu.cpu().numpy()[:, :I].astype(np.float64), gu.cpu().numpy()[:, I:].astype(np.float64)
+    act_w = g / (1.0 + np.exp(-g)) * u
+    assert rel_err(act.float().cpu().numpy(), act_w) <= 1e-2  # bf16 output
+    act_v = act.float().cpu().numpy()
+    want = np.zeros((T, H))
+    dn = orc.grouped_matmul_f64(3, act_v, down, oids.ravel().astype(np.float32), H, E)
+    pv = probs.cpu().numpy()
+    for r in range(T):
+        for j in range(TOPK):
+            want[r] += pv[r, j] * dn[r * TOPK + j]
+    assert rel_err(y.cpu().numpy(), want) <= TOL
+
+
+def test_route_matches_oracle(ctx, orc):
+    import torch
+
+    rng = np.random.default_rng(5)
+    for (rows, E, k, renorm) in [(16, 128, 8, True), (3, 7, 7, False), (33, 1024, 2, False), (1, 64, 1, True)]:
+        announce(f"route rows={rows} E={E} k={k}")
+        logits = rng.standard_normal((rows, E)).astype(np.float32) * 3
+        ids, probs = ctx.moe_route(_t(logits), k, renorm)
+        torch.cuda.synchronize()
+        oids, oprobs = orc.topk_softmax(logits, k, renorm)
+        assert np.array_equal(ids.cpu().numpy(), oids)
+        assert np.allclose(probs.cpu().numpy(), oprobs, rtol=1e-5, atol=1e-7)
+
+
+def test_swiglu(ctx):
+    import torch
+
+    rng = np.random.default_rng(6)
+    gu = rng.standard_normal((5, 2 * 300)).astype(np.float32) * 4
+    out = ctx.swiglu(_t(gu), 300)
+    torch.cuda.synchronize()
+    g, u = gu[:, :300].astype(np.float64), gu[:, 300:].astype(np.float64)
+    assert np.allclose(out.cpu().numpy(), g / (1 + np.exp(-g)) * u, rtol=1e-5, atol=1e-6)
+
+
+def test_device_matmul_grouped_session(orc):
+    import torch
+    import rlxq
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    announce("DeviceMatmul grouped session")
+    dm = rlxq.DeviceMatmul(0)
+    rng = np.random.default_rng(8)
+    m, k, n, E = 12, 1280, 896, 8
+    packed = orc.synth_q8_0(rng, E * n, k).ravel()
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    idx = (np.arange(m) * 3 % E).astype(np.float32)
+    y = dm.grouped_matmul(x, packed, idx, m, k, n, E, rlxq.GGUF_Q8_0).reshape(m, n)
+    assert rel_err(y, orc.grouped_matmul_f64(1, x, packed, idx, n, E)) <= TOL
+    bad = idx.copy()
+    bad[3] = E
+    with pytest.raises(rlxq.RlxqError) as e:
+        dm.grouped_matmul(x, packed, bad, m, k, n, E, rlxq.GGUF_Q8_0)
+    assert e.value.status == rlxq.E_INDEX
+    with pytest.raises(rlxq.RlxqError) as e:
+        dm.grouped_matmul(x, packed, idx[:5], m, k, n, E, rlxq.GGUF_Q8_0)
+    assert e.value.status == rlxq.E_SHAPE and "expert_idx len" in str(e.value)
+    dm.close()
