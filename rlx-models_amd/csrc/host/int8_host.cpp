@@ -1,0 +1,194 @@
+// Host side of the int8 paths: the W8A8 GEMM entry point and the Int8Block
+// branch of rlxq_dequant_matmul.
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "rlxq.h"
+#include "rlxq_internal.hpp"
+#include "int8_args.h"
+
+namespace rlxq {
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+struct W8a8Cfg {
+  const char* name;  // kernel name suffix
+  int BM, BN, BK, WGM, WGN;
+};
+
+// Compiled W8A8 tilings (kernel rlxq_w8a8_<name>).
+const W8a8Cfg kW8a8[] = {
+    {"m128n128k64w22", 128, 128, 64, 2, 2},  {"m128n128k128w22", 128, 128, 128, 2, 2},
+    {"m256n128k64w22", 256, 128, 64, 2, 2},  {"m128n256k64w22", 128, 256, 64, 2, 2},
+    {"m256n256k64w24", 256, 256, 64, 2, 4},
+};
+
+// Tiling choice; RLXQ_W8A8_CFG=<name> selects one (tuning sweeps and the
+// per-variant parity test).
+const W8a8Cfg* pick_w8a8(int64_t m, int64_t n) {
+  if (const char* e = std::getenv("RLXQ_W8A8_CFG")) {
+    for (const auto& c : kW8a8)
+      if (std::strcmp(c.name, e) == 0) return &c;
+    return nullptr;
+  }
+  (void)m;
+  (void)n;
+  return &kW8a8[0];
+}
+
+}  // namespace
+
+// Int8Block{block_size: K}: w = i8 [K, N], scales = f32 [N], biases = zero
+// points f32 [N] or NULL.  Workgroups take (256 columns, K split, 16*MT rows);
+// the K splits are sized so the grid covers the chip, and their partial sums
+// are added in split order by rlxq_i8b_reduce.
+int i8b_dispatch(rlxq_ctx* ctx, int group, const void* x, int x_dtype, const void* w, const void* scales,
+                 const void* zp, int sb_dtype, int64_t m, int64_t k, int64_t n, void* y, int y_dtype,
+                 void* stream) {
+  if (!scales) return fail(ctx, RLXQ_E_NULL, "dequant_matmul: Int8Block needs scales [N]");
+  if (sb_dtype != RLXQ_F32) return fail(ctx, RLXQ_E_DTYPE, "dequant_matmul: Int8Block scales/zp are F32");
+  if (group != 0 && group != k)
+    return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: Int8Block block_size must equal K (one scale per column)");
+  if (n % 16) return fail(ctx, RLXQ_E_ALIGN, "dequant_matmul: Int8Block needs N % 16 == 0");
+  if (!aligned16(w)) return fail(ctx, RLXQ_E_ALIGN, "dequant_matmul: Int8Block weights must be 16-byte aligned");
+  if (k > ((int64_t)1 << 31) || n > ((int64_t)1 << 31) || m > ((int64_t)1 << 31))
+    return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: Int8Block shape too large");
+
+  const int MT = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+  const int64_t MC = 16 * MT;
+  const int64_t tiles_n = (n + 255) / 256, mch = (m + MC - 1) / MC;
+  const int64_t ksteps = (k + 127) / 128;
+  const int64_t base = tiles_n * mch;
+  const int64_t target = 4 * (int64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256);
+  int64_t splits = (target + base - 1) / base;
+  if (splits > ksteps) splits = ksteps;
+  const int64_t cap = (int64_t)256 << 20;  // partial sums kept under 256 MiB
+  if (splits > 1 && splits * m * n * 4 > cap) splits = cap / (m * n * 4);
+  if (splits < 1) splits = 1;
+  const int64_t kslice = ((ksteps + splits - 1) / splits) * 128;
+  splits = (k + kslice - 1) / kslice;
+  if (tiles_n * mch * splits > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: Int8Block grid");
+
+  const size_t part_bytes = splits > 1 ? round256((size_t)(splits * m * n) * 4) : 0;
+  const size_t xsum_bytes = zp ? round256((size_t)m * 4) : 0;
+  void* ws = nullptr;
+  int rc;
+  if (part_bytes + xsum_bytes && (rc = workspace(ctx, part_bytes + xsum_bytes, &ws))) return rc;
+
+  rlxq_i8b_args a;
+  std::memset(&a, 0, sizeof a);
+  a.x = x;
+  a.wq = static_cast<const int8_t*>(w);
+  a.scale = static_cast<const float*>(scales);
+  a.zp = static_cast<const float*>(zp);
+  a.part = part_bytes ? static_cast<float*>(ws) : nullptr;
+  a.xsum = zp ? reinterpret_cast<const float*>(static_cast<char*>(ws) + part_bytes) : nullptr;
+  a.y = y;
+  a.M = m;
+  a.N = n;
+  a.K = k;
+  a.y_ld = n;
+  a.kslice = (int32_t)kslice;
+  a.splits = (int32_t)splits;
+  a.tiles_n = (int32_t)tiles_n;
+  a.x_bf16 = x_dtype == RLXQ_BF16;
+  a.y_bf16 = y_dtype == RLXQ_BF16;
+
+  hipFunction_t fn;
+  if (zp) {
+    if ((rc = get_fn(ctx, "rlxq_row_sum", &fn))) return rc;
+    int xb = a.x_bf16;
+    int64_t M = m, K = k;
+    float* out = const_cast<float*>(a.xsum);
+    void* args[] = {(void*)&x, &xb, &M, &K, &out};
+    if ((rc = launch(ctx, fn, dim3((unsigned)m), dim3(256), 0, stream, args, "rlxq_row_sum"))) return rc;
+  }
+  char name[48];
+  std::snprintf(name, sizeof name, "rlxq_i8b_%s_mt%d", a.x_bf16 ? "bf16" : "f32", MT);
+  if ((rc = get_fn(ctx, name, &fn))) return rc;
+  const size_t lds = 128 * (256 + 16) + 2 * (size_t)MC * (128 + 8) * 2;
+  void* args[] = {&a};
+  if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name)))
+    return rc;
+  if (splits > 1) {
+    if ((rc = get_fn(ctx, "rlxq_i8b_reduce", &fn))) return rc;
+    const int64_t total = m * n;
+    if ((total + 255) / 256 > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: Int8Block output");
+    void* rargs[] = {&a};
+    // the last kernel launched names the path in rlxq_last_kernel: keep the
+    // matmul's name there, the reduction is its tail
+    rc = launch(ctx, fn, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, rargs, "rlxq_i8b_reduce");
+    if (!rc) ctx->last_kernel = name;
+  }
+  return rc;
+}
+
+}  // namespace rlxq
+
+using namespace rlxq;
+
+extern "C" {
+
+int rlxq_w8a8_gemm(rlxq_ctx* ctx, const void* x, int x_dtype, const int8_t* wq, const float* w_scale, int64_t m,
+                   int64_t k, int64_t n, void* y, int y_dtype, void* stream) {
+  if (!ctx) return RLXQ_E_NULL;
+  ctx->last_error.clear();
+  // with no rows nothing is read or written: x and y may be NULL then
+  if (!wq || !w_scale || (m > 0 && (!x || !y))) return fail(ctx, RLXQ_E_NULL, "w8a8_gemm: null pointer");
+  if (m < 0 || k <= 0 || n <= 0) return fail(ctx, RLXQ_E_SHAPE, "w8a8_gemm: need m >= 0, k > 0, n > 0");
+  // |acc| <= 127 * 127 * K must stay inside int32
+  if (k > 131072 || m > 0x7fffffff || n > 0x7fffffff)
+    return fail(ctx, RLXQ_E_SHAPE, "w8a8_gemm: K above 131072 or M, N above 2^31");
+  if (k % 16 || n % 16) return fail(ctx, RLXQ_E_ALIGN, "w8a8_gemm: K and N must be multiples of 16");
+  if (x_dtype != RLXQ_F32 && x_dtype != RLXQ_BF16) return fail(ctx, RLXQ_E_DTYPE, "w8a8_gemm: x_dtype");
+  if (y_dtype != RLXQ_F32 && y_dtype != RLXQ_BF16) return fail(ctx, RLXQ_E_DTYPE, "w8a8_gemm: y_dtype");
+  if (!aligned16(wq)) return fail(ctx, RLXQ_E_ALIGN, "w8a8_gemm: wq must be 16-byte aligned");
+  if (m == 0) return RLXQ_OK;
+
+  const W8a8Cfg* c = pick_w8a8(m, n);
+  if (!c) return fail(ctx, RLXQ_E_NOKERNEL, "w8a8_gemm: RLXQ_W8A8_CFG names no compiled tiling");
+  const int64_t tiles_m = (m + c->BM - 1) / c->BM, tiles_n = (n + c->BN - 1) / c->BN;
+  if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "w8a8_gemm: too many tiles");
+
+  DeviceGuard g(ctx->device);
+  const size_t q_bytes = round256((size_t)(m * k));
+  void* ws = nullptr;
+  int rc;
+  if ((rc = workspace(ctx, q_bytes + round256((size_t)m * 4), &ws))) return rc;
+  int8_t* qx = static_cast<int8_t*>(ws);
+  float* sx = reinterpret_cast<float*>(static_cast<char*>(ws) + q_bytes);
+  if ((rc = rlxq_quantize_act_int8(ctx, x, x_dtype, m, k, qx, sx, stream))) return rc;
+
+  char name[48];
+  std::snprintf(name, sizeof name, "rlxq_w8a8_%s", c->name);
+  hipFunction_t fn;
+  if ((rc = get_fn(ctx, name, &fn))) return rc;
+  rlxq_w8a8_args a;
+  std::memset(&a, 0, sizeof a);
+  a.qx = qx;
+  a.sx = sx;
+  a.wq = wq;
+  a.sw = w_scale;
+  a.y = y;
+  a.M = m;
+  a.N = n;
+  a.K = k;
+  a.y_ld = n;
+  a.tiles_m = (int32_t)tiles_m;
+  a.tiles_n = (int32_t)tiles_n;
+  a.y_bf16 = y_dtype == RLXQ_BF16;
+  const int64_t grid = 8 * ((tiles_m * tiles_n + 7) / 8);
+  const size_t lds = 2 * (size_t)c->BM * (c->BK + 16) + 2 * (size_t)c->BK * (c->BN + 16);
+  void* args[] = {&a};
+  return launch(ctx, fn, dim3((unsigned)grid), dim3(64 * c->WGM * c->WGN), lds, stream, args, name);
+}
+
+}  // extern "C"

@@ -141,7 +141,7 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
                   const void* scales, const void* biases, int sb_dtype, int64_t m, int64_t k,
                   int64_t n, void* y, int y_dtype, void* stream) {
   if (scheme == RLXQ_INT8_BLOCK)
-    return fail(ctx, RLXQ_E_NOKERNEL, "dequant_matmul: Int8Block is served by a later kernel");
+    return i8b_dispatch(ctx, group, x, x_dtype, w, scales, biases, sb_dtype, m, k, n, y, y_dtype, stream);
   int64_t rb = 0;
   int rc = check_weights(ctx, "dequant_matmul", scheme, group, w, scales, biases, sb_dtype, k, &rb);
   if (rc) return rc;
@@ -322,12 +322,6 @@ int rlxq_moe_route(rlxq_ctx* ctx, const float* logits, int64_t rows, int64_t num
   int E = (int)num_experts, K = (int)top_k, rn = renorm ? 1 : 0;
   void* args[] = {(void*)&logits, &R, &E, &K, &rn, (void*)&ids, (void*)&probs};
   return launch(ctx, fn, dim3((unsigned)rows), dim3(64), 0, stream, args, "moe_route");
-}
-
-int rlxq_w8a8_gemm(rlxq_ctx* ctx, const void*, int, const int8_t*, const float*, int64_t, int64_t, int64_t,
-                   void*, int, void*) {
-  if (!ctx) return RLXQ_E_NULL;
-  return fail(ctx, RLXQ_E_NOKERNEL, "w8a8_gemm: not built yet");
 }
 
 }  // extern "C"

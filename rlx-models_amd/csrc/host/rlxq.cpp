@@ -35,6 +35,7 @@ RLXQ_EMBED(rlxq_co_gemv, "gemv.co")
 RLXQ_EMBED(rlxq_co_misc, "misc.co")
 RLXQ_EMBED(rlxq_co_gemm, "gemm.co")
 RLXQ_EMBED(rlxq_co_moe, "moe.co")
+RLXQ_EMBED(rlxq_co_int8, "int8.co")
 
 namespace {
 
@@ -49,6 +50,7 @@ const Image kImages[] = {
     {rlxq_co_misc_begin, rlxq_co_misc_end, "misc"},
     {rlxq_co_gemm_begin, rlxq_co_gemm_end, "gemm"},
     {rlxq_co_moe_begin, rlxq_co_moe_end, "moe"},
+    {rlxq_co_int8_begin, rlxq_co_int8_end, "int8"},
 };
 
 std::string hip_msg(hipError_t e) { return std::string(hipGetErrorName(e)) + ": " + hipGetErrorString(e); }

@@ -60,6 +60,27 @@ RLXQ_DEV uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// Workgroup -> output tile (tm, tn) of a tiles_m x tiles_n grid.  The
+// dispatcher deals workgroups to the 8 XCDs round-robin (workgroup b runs on
+// XCD b % 8) and every XCD has its own L2, so each XCD is given a contiguous
+// range of logical tiles; logical tiles run in bands of GM tile-rows, so the
+// workgroups resident on one XCD at a time share activation rows and weight
+// columns in that L2.  The grid is launched rounded up to a multiple of 8;
+// returns false for the padding workgroups.
+RLXQ_DEV bool tile_of(int bid, int tiles_m, int tiles_n, int GM, int& tm, int& tn) {
+  const int G = tiles_m * tiles_n;
+  const int per = (G + 7) >> 3;
+  const int logical = (bid & 7) * per + (bid >> 3);
+  if (logical >= G) return false;
+  const int band = GM * tiles_n;
+  const int first = (logical / band) * GM;
+  const int gm = tiles_m - first < GM ? tiles_m - first : GM;
+  const int r = logical % band;
+  tm = first + r % gm;
+  tn = r / gm;
+  return true;
+}
+
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
 template <int WIDTH>
 RLXQ_DEV float group_sum(float v) {

@@ -1,0 +1,348 @@
+// Int8 kernels on gfx950 MFMA.  Both read weights stored the reference's way,
+// int8 [K, N] row-major with one f32 scale per column
+// (crates/rlx-kimi-k3/src/common.rs:466-482):
+//
+//  * rlxq_w8a8_*: the W8A8 GEMM.  Activations are quantised per row to int8
+//    (rlxq_quant_act_i8, crates/rlx-quant-calib/src/bitnet.rs:76-93); the
+//    product runs on v_mfma_i32_32x32x32_i8 with int32 accumulation (exact),
+//    and the epilogue is y = (float(acc) * sx[m]) * sw[n].
+//  * rlxq_i8b_*: QuantScheme::Int8Block (crates/rlx-kimi-k3/examples/int8_kernel.rs:59-89),
+//    y = x . ((Wq - zp) * s) with f32 or bf16 activations.  x is split into
+//    two bf16 terms hi + lo (16 significant bits); int8 codes are exact in
+//    bf16, so v_mfma_f32_16x16x32_bf16 forms the products to ~2^-17 relative
+//    with fp32 accumulation.  Evaluated as s * (sum x*q - zp * sum x).
+//
+// The weight tile is copied into LDS unchanged ([k][n], N contiguous).  The
+// MFMA B operand needs consecutive k in each lane; it is read with the LDS
+// transpose read ds_read_b64_tr_b8: in each group of 16 lanes, lanes 2r and
+// 2r+1 name the two 8-byte halves of a 16-byte row r, and lane i receives
+// byte i of rows 0..7 (8 consecutive k of column i).
+#include "common.hip.h"
+#include "int8_args.h"
+
+namespace rlxq {
+
+typedef int32_t i32x2_t __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef i32x2_t __attribute__((address_space(3))) lds_i32x2_t;
+
+RLXQ_DEV i32x2_t lds_tr8(const uint8_t* p) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2_t*)(p));
+}
+
+// ---------------------------------------------------------------- W8A8 GEMM
+
+// y[m, n] = (float(acc) * sx[m]) * sw[n], two roundings in this order.
+template <int TM, int TN>
+RLXQ_DEV void w8a8_epilogue(const rlxq_w8a8_args& a, const i32x16_t (&acc)[TM][TN], int64_t mb, int64_t nb,
+                            int lane) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int64_t n = nb + j * 32 + (lane & 31);
+    if (n >= a.N) continue;
+    const float sw = a.sw[n];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int64_t m = mb + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+        if (m < a.M) {
+          const float v = ((float)acc[i][j][r] * a.sx[m]) * sw;
+          if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
+          else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+        }
+      }
+  }
+}
+
+// Workgroup of WGM x WGN waves owns a BM x BN output tile and walks K in steps
+// of BK bytes; each wave computes a (BM/WGM) x (BN/WGN) sub-tile from 32x32
+// MFMA tiles.  Global loads of step k+1 are in flight during the MFMAs of step
+// k; LDS tiles are double-buffered with one barrier per step.
+template <int BM, int BN, int BK, int WGM, int WGN, int GM>
+RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
+  constexpr int NT = WGM * WGN * 64;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int AST = BK + 16;  // A row stride (bytes): 16-byte reads of 8 rows hit distinct banks
+  constexpr int BST = BN + 16;  // B row stride: transpose reads of 8 rows hit distinct banks
+  constexpr int ACH = BK / 16, BCH = BN / 16;
+  constexpr int AP = BM * ACH / NT, BP = BK * BCH / NT;
+  static_assert((BM * ACH) % NT == 0 && (BK * BCH) % NT == 0, "tile / threads");
+  static_assert(WM % 32 == 0 && WN % 32 == 0 && BK % 32 == 0, "tile shape");
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint8_t* As = smem;                 // [2][BM][AST]
+  uint8_t* Bs = smem + 2 * BM * AST;  // [2][BK][BST]
+
+  int tm, tn;
+  if (!tile_of(blockIdx.x, a.tiles_m, a.tiles_n, GM, tm, tn)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wm = wv % WGM, wn = wv / WGM;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int KT = (int)((a.K + BK - 1) / BK);
+
+  uint4 ar[AP], br[BP];
+  auto load = [&](int kt) {
+    const int64_t k0 = (int64_t)kt * BK;
+#pragma unroll
+    for (int i = 0; i < AP; i++) {
+      const int c = tid + NT * i, r = c / ACH, cc = c % ACH;
+      const int64_t m = m0 + r, k = k0 + 16 * cc;
+      ar[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (m < a.M && k < a.K) ar[i] = *reinterpret_cast<const uint4*>(a.qx + m * a.K + k);
+    }
+#pragma unroll
+    for (int i = 0; i < BP; i++) {
+      const int c = tid + NT * i, r = c / BCH, cc = c % BCH;
+      const int64_t k = k0 + r, n = n0 + 16 * cc;
+      br[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (k < a.K && n < a.N) br[i] = *reinterpret_cast<const uint4*>(a.wq + k * a.N + n);
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < AP; i++) {
+      const int c = tid + NT * i, r = c / ACH, cc = c % ACH;
+      *reinterpret_cast<uint4*>(As + (buf * BM + r) * AST + 16 * cc) = ar[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BP; i++) {
+      const int c = tid + NT * i, r = c / BCH, cc = c % BCH;
+      *reinterpret_cast<uint4*>(Bs + (buf * BK + r) * BST + 16 * cc) = br[i];
+    }
+  };
+
+  i32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+
+  load(0);
+  store(0);
+  __syncthreads();
+  const int g = lane >> 4, s = lane & 15;
+  for (int kt = 0; kt < KT; kt++) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < KT;
+    if (more) load(kt + 1);
+    const uint8_t* Ab = As + (cur * BM + wm * WM) * AST;
+    const uint8_t* Bb = Bs + cur * BK * BST + wn * WN;
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ks++) {
+      i32x4_t af[TM], bq[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        af[i] = *reinterpret_cast<const i32x4_t*>(Ab + (i * 32 + (lane & 31)) * AST + ks * 32 + 16 * (lane >> 5));
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        // B[k][j] of the 32x32x32 tile sits in lane j + 32*(k/16), byte k%16:
+        // group g covers columns 16*(g&1).., k = 16*(g>>1) + 0..7 and + 8..15.
+        const uint8_t* p = Bb + (ks * 32 + 16 * (g >> 1) + (s >> 1)) * BST + j * 32 + 16 * (g & 1) + 8 * (s & 1);
+        const i32x2_t lo = lds_tr8(p), hi = lds_tr8(p + 8 * BST);
+        bq[j] = i32x4_t{lo.x, lo.y, hi.x, hi.y};
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bq[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) store(cur ^ 1);
+    __syncthreads();
+  }
+  w8a8_epilogue<TM, TN>(a, acc, m0 + wm * WM, n0 + wn * WN, lane);
+}
+
+// ------------------------------------------------------------- Int8Block
+
+constexpr int I8B_BN = 256;   // columns per workgroup (64 per wave)
+constexpr int I8B_KST = 128;  // K rows per LDS step
+constexpr int I8B_WST = I8B_BN + 16;
+constexpr int I8B_XST = I8B_KST + 8;
+
+RLXQ_DEV uint32_t i8_pair_bf16(uint32_t w, int sh) {
+  const float f0 = (float)(int8_t)((w >> sh) & 0xffu);
+  const float f1 = (float)(int8_t)((w >> (sh + 8)) & 0xffu);
+  // small integers: the bf16 is the high half of the f32, exactly
+  return perm_b32(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+}
+
+RLXQ_DEV float i8b_finish(const rlxq_i8b_args& a, float v, int64_t m, int64_t n) {
+  if (a.zp) v = fmaf(-a.zp[n], a.xsum[m], v);
+  return v * a.scale[n];
+}
+
+// Workgroup = (256-column block, K split, chunk of 16*MT rows); each wave owns
+// 64 columns as four 16-column MFMA tiles.
+template <int MT, bool XBF16>
+RLXQ_DEV void i8b_body(const rlxq_i8b_args& a) {
+  constexpr int MC = 16 * MT;
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint8_t* Ws = smem;                                                     // [KST][WST]
+  uint16_t* Xh = reinterpret_cast<uint16_t*>(smem + I8B_KST * I8B_WST);  // [MC][XST]
+  uint16_t* Xl = Xh + MC * I8B_XST;
+
+  const int tn = blockIdx.x % a.tiles_n;
+  const int sp = (blockIdx.x / a.tiles_n) % a.splits;
+  const int mc = blockIdx.x / (a.tiles_n * a.splits);
+  const int64_t n0 = (int64_t)tn * I8B_BN, m0 = (int64_t)mc * MC;
+  const int64_t kb = (int64_t)sp * a.kslice;
+  const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int g = lane >> 4, s = lane & 15;
+
+  f32x4_t acc[MT][4];
+#pragma unroll
+  for (int t = 0; t < MT; t++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[t][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int64_t k0 = kb; k0 < ke; k0 += I8B_KST) {
+    uint4 wr[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int c = tid + 256 * i, r = c >> 4, cc = c & 15;
+      const int64_t k = k0 + r, n = n0 + 16 * cc;
+      wr[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (k < ke && n < a.N) wr[i] = *reinterpret_cast<const uint4*>(a.wq + k * a.N + n);
+    }
+    for (int u = tid; u < MC * (I8B_KST / 8); u += 256) {
+      const int row = u / (I8B_KST / 8), c8 = u % (I8B_KST / 8);
+      const int64_t m = m0 + row, k = k0 + 8 * c8;
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float v[2];
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+          const int64_t kk = k + e + q;
+          v[q] = 0.f;
+          if (m < a.M && kk < ke) {
+            if constexpr (XBF16) v[q] = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(a.x)[m * a.K + kk]);
+            else v[q] = reinterpret_cast<const float*>(a.x)[m * a.K + kk];
+          }
+        }
+        const uint32_t h0 = f32_to_bf16_bits(v[0]), h1 = f32_to_bf16_bits(v[1]);
+        h[e / 2] = h0 | (h1 << 16);
+        if constexpr (!XBF16) {
+          const uint32_t l0 = f32_to_bf16_bits(v[0] - bf16_bits_to_f32(h0));
+          const uint32_t l1 = f32_to_bf16_bits(v[1] - bf16_bits_to_f32(h1));
+          l[e / 2] = l0 | (l1 << 16);
+        }
+      }
+      *reinterpret_cast<uint4*>(Xh + row * I8B_XST + 8 * c8) = make_uint4(h[0], h[1], h[2], h[3]);
+      if constexpr (!XBF16)
+        *reinterpret_cast<uint4*>(Xl + row * I8B_XST + 8 * c8) = make_uint4(l[0], l[1], l[2], l[3]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int c = tid + 256 * i, r = c >> 4, cc = c & 15;
+      *reinterpret_cast<uint4*>(Ws + r * I8B_WST + 16 * cc) = wr[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < I8B_KST / 32; ks++) {
+      // A[i][k] of the 16x16x32 tile: lane i%16 + 16*(k/8); B[k][j]: lane j + 16*(k/8)
+      bf16x8_t ah[MT], al[MT];
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        const int off = (t * 16 + s) * I8B_XST + ks * 32 + 8 * g;
+        ah[t] = *reinterpret_cast<const bf16x8_t*>(Xh + off);
+        if constexpr (!XBF16) al[t] = *reinterpret_cast<const bf16x8_t*>(Xl + off);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint8_t* p = Ws + (ks * 32 + 8 * g + (s >> 1)) * I8B_WST + 64 * wv + 16 * j + 8 * (s & 1);
+        const i32x2_t q = lds_tr8(p);
+        const uint32_t q0 = (uint32_t)q.x, q1 = (uint32_t)q.y;
+        uint32_t bw[4] = {i8_pair_bf16(q0, 0), i8_pair_bf16(q0, 16), i8_pair_bf16(q1, 0), i8_pair_bf16(q1, 16)};
+        const bf16x8_t b = __builtin_bit_cast(bf16x8_t, bw);
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[t], b, acc[t][j], 0, 0, 0);
+          if constexpr (!XBF16) acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[t], b, acc[t][j], 0, 0, 0);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
+#pragma unroll
+  for (int t = 0; t < MT; t++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int64_t m = m0 + t * 16 + 4 * g + r;
+        const int64_t n = n0 + 64 * wv + 16 * j + s;
+        if (m >= a.M || n >= a.N) continue;
+        const float v = acc[t][j][r];
+        if (a.splits > 1) {
+          a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
+        } else {
+          const float o = i8b_finish(a, v, m, n);
+          if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(o);
+          else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = o;
+        }
+      }
+}
+
+}  // namespace rlxq
+
+#define RLXQ_W8A8_INST(BM, BN, BK, WGM, WGN)                                                        \
+  extern "C" __global__ __launch_bounds__(WGM * WGN * 64) void rlxq_w8a8_m##BM##n##BN##k##BK##w##WGM##WGN( \
+      rlxq_w8a8_args a) {                                                                          \
+    rlxq::w8a8_body<BM, BN, BK, WGM, WGN, 8>(a);                                                   \
+  }
+RLXQ_W8A8_INST(128, 128, 64, 2, 2)
+RLXQ_W8A8_INST(128, 128, 128, 2, 2)
+RLXQ_W8A8_INST(256, 128, 64, 2, 2)
+RLXQ_W8A8_INST(128, 256, 64, 2, 2)
+RLXQ_W8A8_INST(256, 256, 64, 2, 4)
+
+#define RLXQ_I8B_INST(MT, XN, XBF)                                                        \
+  extern "C" __global__ __launch_bounds__(256) void rlxq_i8b_##XN##_mt##MT(rlxq_i8b_args a) { \
+    rlxq::i8b_body<MT, XBF>(a);                                                           \
+  }
+RLXQ_I8B_INST(1, f32, false)
+RLXQ_I8B_INST(2, f32, false)
+RLXQ_I8B_INST(4, f32, false)
+RLXQ_I8B_INST(1, bf16, true)
+RLXQ_I8B_INST(2, bf16, true)
+RLXQ_I8B_INST(4, bf16, true)
+
+// Split-K reduction of the Int8Block partials, summed in split order.
+extern "C" __global__ __launch_bounds__(256) void rlxq_i8b_reduce(rlxq_i8b_args a) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.M * a.N) return;
+  const int64_t m = i / a.N, n = i - m * a.N;
+  float v = 0.f;
+  for (int sp = 0; sp < a.splits; sp++) v += a.part[(int64_t)sp * a.M * a.N + i];
+  const float o = rlxq::i8b_finish(a, v, m, n);
+  if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(o);
+  else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = o;
+}
+
+// Row sums of x (f32 accumulation), for the zero-point term.  One workgroup
+// of 256 per row.
+extern "C" __global__ __launch_bounds__(256) void rlxq_row_sum(const void* __restrict__ x, int x_bf16, int64_t M,
+                                                               int64_t K, float* __restrict__ out) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  if (r >= M) return;
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < K; c += 256)
+    s += x_bf16 ? bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(x)[r * K + c])
+                : reinterpret_cast<const float*>(x)[r * K + c];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) out[r] = (red[0] + red[1]) + (red[2] + red[3]);
+}
