@@ -105,17 +105,35 @@ int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const 
   return fail(ctx, RLXQ_E_SCHEME, std::string(what) + ": unsupported scheme " + std::to_string(scheme));
 }
 
-// Prefill dequant-GEMM launch: 128 x 128 output tiles, M tiles fastest so
-// neighbouring workgroups share a weight tile.
+// Prefill dequant-GEMM launch.  256 x 256 tiles (one workgroup per CU, 4
+// waves of 128 x 128) for M >= 256, else 128 x 128 tiles (4 waves of 64 x 64).
+// RLXQ_GEMM_TILE=128|256 forces one of them (tests, sweeps).
 int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const void* w, const void* scales,
                   const void* biases, int sb_dtype, int64_t rb, int64_t m, int64_t k, int64_t n, void* y,
                   int y_dtype, void* stream) {
+  // Tiling from a measured cost model: a round of resident 128 x 128 tiles
+  // (two workgroups per CU) takes ~0.65 of a round of 256 x 256 tiles (one
+  // per CU, 8 waves), per unit of K.
+  const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  const int64_t t128 = ((m + 127) / 128) * ((n + 127) / 128), t256 = ((m + 255) / 256) * ((n + 255) / 256);
+  const double c128 = 0.7 * (double)((t128 + 2 * cus - 1) / (2 * cus)), c256 = (double)((t256 + cus - 1) / cus);
+  int tile = c256 < c128 ? 256 : 128;
+  // 256 tiles: 8 waves, global loads two K steps ahead, except for the 8-bit
+  // schemes whose larger raw blocks do not fit two stages in 256 VGPRs
+  const bool bit8 = scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_MLX_AFFINE8;
+  const char* var = tile == 256 ? (bit8 ? "w8" : "w8p2") : "";
+  if (const char* e = std::getenv("RLXQ_GEMM_TILE")) {
+    tile = std::atoi(e) == 128 ? 128 : 256;
+    var = tile == 128 ? "" : (std::strncmp(e, "256w8", 5) == 0 ? e + 3 : "");
+  }
+  const bool w8 = tile == 256 && var[0] == 'w';
   char name[64];
-  std::snprintf(name, sizeof name, "rlxq_gemm_%s_t128", scheme_name(scheme));
+  std::snprintf(name, sizeof name, "rlxq_gemm_%s_t%d%s", scheme_name(scheme), tile, var);
   hipFunction_t fn;
   int rc;
   if ((rc = get_fn(ctx, name, &fn))) return rc;
   rlxq_gemm_args a;
+  std::memset(&a, 0, sizeof a);
   a.x = x;
   a.w = static_cast<const uint8_t*>(w);
   a.scales = scales;
@@ -129,12 +147,18 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
   a.group = is_mlx(scheme) ? group : 32;
   a.sb_bf16 = sb_dtype == RLXQ_BF16 ? 1 : 0;
   a.y_bf16 = y_dtype == RLXQ_BF16 ? 1 : 0;
-  a.pad = 0;
+  const int64_t tiles_m = (m + tile - 1) / tile, tiles_n = (n + tile - 1) / tile;
+  if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
+  a.tiles_m = (int32_t)tiles_m;
+  a.tiles_n = (int32_t)tiles_n;
   void* args[] = {&a};
-  const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
-  if (tiles > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
-  const size_t lds = 2 * (128 + 128) * 72 * sizeof(uint16_t);
-  return launch(ctx, fn, dim3((unsigned)tiles, 1, 1), dim3(256, 1, 1), lds, stream, args, name);
+  if (tile == 128) {
+    const size_t lds = 2 * (128 + 128) * 72 * sizeof(uint16_t);
+    return launch(ctx, fn, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), lds, stream, args, name);
+  }
+  const size_t lds = 2 * (256 + 256) * 72 * sizeof(uint16_t);
+  const int64_t grid = 8 * ((tiles_m * tiles_n + 7) / 8);
+  return launch(ctx, fn, dim3((unsigned)grid), dim3(w8 ? 512 : 256), lds, stream, args, name);
 }
 
 int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dtype, const void* w,

@@ -34,12 +34,16 @@ RLXQ_DEV float dot2_f16(uint32_t a, uint32_t b, float c) {
 
 RLXQ_DEV float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
 
-// f32 -> bf16 bits, round to nearest even (NaN kept quiet).
-RLXQ_DEV uint32_t f32_to_bf16_bits(float v) {
-  uint32_t x = __float_as_uint(v);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return (x >> 16) | 0x40u;
-  x += 0x7fffu + ((x >> 16) & 1u);
-  return x >> 16;
+// f32 -> bf16 bits with the hardware conversion (v_cvt_pk_bf16_f32: round to
+// nearest even, NaN stays NaN).
+RLXQ_DEV uint32_t f32_to_bf16_bits(float v) { return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v); }
+
+typedef __bf16 rlxq_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float rlxq_f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two f32 -> one dword of two bf16 (lo in bits 0..15), one v_cvt_pk_bf16_f32.
+RLXQ_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((rlxq_f32x2_t){lo, hi}, rlxq_bf16x2_t));
 }
 
 RLXQ_DEV float f16_bits_to_f32(uint32_t h16) {

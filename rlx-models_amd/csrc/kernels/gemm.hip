@@ -25,52 +25,89 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr int GBK = 64;        // K per step
 constexpr int GLD = GBK + 8;   // LDS row stride (bf16 elements)
 
-// Two f32 -> one dword of two bf16 (round to nearest even).
-RLXQ_DEV uint32_t pack_bf16x2(float a, float b) { return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16); }
 
-// Dequantize one 32-weight block of row `row` (K-block `kb`) into 16 dwords of
-// bf16 pairs in natural element order.  `ok` = false yields zeros.
+// Raw bytes of one 32-weight block, loaded ahead of their conversion so the
+// global loads of a K step can be in flight while the previous step computes.
+// All-zero raw bytes convert to zero weights (d = 0, or scale = bias = 0).
+template <int SCH> struct RawBlk;
+template <> struct RawBlk<SCH_Q4_1> { uint32_t h; uint4 q; };
+template <> struct RawBlk<SCH_Q4_0> { uint32_t w[5]; uint32_t off; };
+template <> struct RawBlk<SCH_Q8_0> { uint32_t w[9]; uint32_t off; };
+template <> struct RawBlk<SCH_MLX4> { uint4 q; float s, b; };
+template <> struct RawBlk<SCH_MLX8> { uint4 q0, q1; float s, b; };
+
+// Loads block `kb` of weight row `row` (a valid row); `ok` = false zeroes it
+// with selects, so the caller's loop body stays free of branches.
 template <int SCH>
-RLXQ_DEV void dequant_block_bf16(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok, uint32_t* out) {
-  if (!ok) {
-#pragma unroll
-    for (int i = 0; i < 16; i++) out[i] = 0u;
-    return;
-  }
+RLXQ_DEV void load_blk(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok, RawBlk<SCH>& r) {
   const uint8_t* rp = a.w + row * a.rb;
+  if constexpr (SCH == SCH_Q4_1) {
+    const uint8_t* p = rp + kb * 20;
+    r.h = ok ? ld_u32(p) : 0u;
+    const uint4 q = ld_u128(p + 4);
+    r.q = q;
+  } else if constexpr (SCH == SCH_Q4_0 || SCH == SCH_Q8_0) {
+    // 18- and 34-byte blocks are 2-byte aligned: read the dwords covering the
+    // block without touching a byte beyond it (the tail is a 16-bit load when
+    // the block starts dword aligned)
+    constexpr int BB = SCH == SCH_Q4_0 ? 18 : 34, NW = SCH == SCH_Q4_0 ? 5 : 9;
+    const uint32_t off = (uint32_t)(kb * BB) & 3u;
+    const uint8_t* base = rp + kb * BB - off;
+#pragma unroll
+    for (int i = 0; i < NW - 1; i++) r.w[i] = ld_u32(base + 4 * i);
+    r.w[NW - 1] = off ? ld_u32(base + 4 * (NW - 1))
+                      : (uint32_t)*reinterpret_cast<const uint16_t*>(base + 4 * (NW - 1));
+    r.off = off;
+    if (!ok) r.w[0] = 0u, r.w[1] = 0u;  // zero scale (it sits in w[0] or the low half of w[1])
+  } else {
+    constexpr int BITS = SCH == SCH_MLX4 ? 4 : 8;
+    const uint8_t* q = rp + kb * BITS * 4;
+    const int64_t gi = row * (int64_t)(a.K / a.group) + (kb * 32) / a.group;
+    float s, bi;
+    if (a.sb_bf16) {
+      s = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(a.scales)[gi]);
+      bi = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(a.biases)[gi]);
+    } else {
+      s = reinterpret_cast<const float*>(a.scales)[gi];
+      bi = reinterpret_cast<const float*>(a.biases)[gi];
+    }
+    r.s = ok ? s : 0.f;
+    r.b = ok ? bi : 0.f;
+    if constexpr (SCH == SCH_MLX4) {
+      r.q = ld_u128(q);
+    } else {
+      r.q0 = ld_u128(q);
+      r.q1 = ld_u128(q + 16);
+    }
+  }
+}
+
+// Converts a raw block into 16 dwords of bf16 pairs in natural element order:
+// f32 d*q + m (the CPU decoder's arithmetic), rounded to bf16 (nearest even).
+template <int SCH>
+RLXQ_DEV void conv_blk(const RawBlk<SCH>& r, uint32_t* out) {
   float v[32];
   if constexpr (SCH == SCH_Q4_1 || SCH == SCH_Q4_0) {
-    constexpr int BB = SCH == SCH_Q4_1 ? 20 : 18;
-    const uint8_t* p = rp + kb * BB;
     uint32_t qs[4];
     float d, m;
     if constexpr (SCH == SCH_Q4_1) {
-      const uint32_t h = ld_u32(p);
-      const uint4 q = ld_u128(p + 4);
-      qs[0] = q.x; qs[1] = q.y; qs[2] = q.z; qs[3] = q.w;
-      d = f16_bits_to_f32(h & 0xffffu);
-      m = f16_bits_to_f32(h >> 16);
+      qs[0] = r.q.x; qs[1] = r.q.y; qs[2] = r.q.z; qs[3] = r.q.w;
+      d = f16_bits_to_f32(r.h & 0xffffu);
+      m = f16_bits_to_f32(r.h >> 16);
     } else {
-      // 18-byte blocks are 2-byte aligned: read the dwords covering the
-      // block without touching a byte beyond it (the tail is a 16-bit load
-      // when the block starts dword aligned).
-      const uint32_t off = (uint32_t)(kb * BB) & 3u;
-      const uint8_t* base = p - off;
-      uint32_t w5[5];
-#pragma unroll
-      for (int i = 0; i < 4; i++) w5[i] = ld_u32(base + 4 * i);
-      w5[4] = off ? ld_u32(base + 16) : (uint32_t)*reinterpret_cast<const uint16_t*>(base + 16);
-      const uint32_t hd = off ? (w5[0] >> 16) : (w5[0] & 0xffffu);
-#pragma unroll
+      const uint32_t hd = r.off ? (r.w[0] >> 16) : (r.w[0] & 0xffffu);
       // qs starts 2 bytes after the block start: byte off + 2 of the span
       // (v_alignbyte takes shifts 0..3, so a 4-byte shift is the next dword)
-      for (int i = 0; i < 4; i++) qs[i] = off ? w5[i + 1] : align_bytes(w5[i + 1], w5[i], 2);
+#pragma unroll
+      for (int i = 0; i < 4; i++) qs[i] = r.off ? r.w[i + 1] : align_bytes(r.w[i + 1], r.w[i], 2);
       d = f16_bits_to_f32(hd);
       m = -8.f * d;
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const uint32_t lo = qs[i] & 0x0F0F0F0Fu, hi = (qs[i] >> 4) & 0x0F0F0F0Fu;
+      uint32_t lo = qs[i] & 0x0F0F0F0Fu, hi = (qs[i] >> 4) & 0x0F0F0F0Fu;
+      // opaque to the optimiser, so each byte converts with one v_cvt_f32_ubyteN
+      asm volatile("" : "+v"(lo), "+v"(hi));
       v[4 * i + 0] = fmaf(d, (float)(lo & 0xffu), m);
       v[4 * i + 1] = fmaf(d, (float)((lo >> 8) & 0xffu), m);
       v[4 * i + 2] = fmaf(d, (float)((lo >> 16) & 0xffu), m);
@@ -81,43 +118,40 @@ RLXQ_DEV void dequant_block_bf16(const rlxq_gemm_args& a, int64_t row, int64_t k
       v[16 + 4 * i + 3] = fmaf(d, (float)(hi >> 24), m);
     }
   } else if constexpr (SCH == SCH_Q8_0) {
-    // 34-byte blocks: as for Q4_0, no byte beyond the block is read.
-    const uint32_t off = (uint32_t)(kb * 34) & 3u;
-    const uint8_t* base = rp + kb * 34 - off;
-    uint32_t w9[9];
-#pragma unroll
-    for (int i = 0; i < 8; i++) w9[i] = ld_u32(base + 4 * i);
-    w9[8] = off ? ld_u32(base + 32) : (uint32_t)*reinterpret_cast<const uint16_t*>(base + 32);
-    const float d = f16_bits_to_f32(off ? (w9[0] >> 16) : (w9[0] & 0xffffu));
+    const float d = f16_bits_to_f32(r.off ? (r.w[0] >> 16) : (r.w[0] & 0xffffu));
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const uint32_t q = off ? w9[i + 1] : align_bytes(w9[i + 1], w9[i], 2);
+      const uint32_t q = r.off ? r.w[i + 1] : align_bytes(r.w[i + 1], r.w[i], 2);
 #pragma unroll
       for (int e = 0; e < 4; e++) v[4 * i + e] = d * (float)(int8_t)((q >> (8 * e)) & 0xffu);
     }
   } else {
-    // MLX affine: codes LSB-first in u32 words, one scale/bias per group.
+    // MLX affine: codes LSB-first in u32 words, scale * code + bias
     constexpr int BITS = SCH == SCH_MLX4 ? 4 : 8;
-    const uint32_t* wq = reinterpret_cast<const uint32_t*>(rp) + kb * BITS;
-    const int64_t gi = row * (int64_t)(a.K / a.group) + (kb * 32) / a.group;
-    float s, bi;
-    if (a.sb_bf16) {
-      s = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(a.scales)[gi]);
-      bi = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(a.biases)[gi]);
+    uint32_t wq[BITS];
+    if constexpr (SCH == SCH_MLX4) {
+      wq[0] = r.q.x; wq[1] = r.q.y; wq[2] = r.q.z; wq[3] = r.q.w;
     } else {
-      s = reinterpret_cast<const float*>(a.scales)[gi];
-      bi = reinterpret_cast<const float*>(a.biases)[gi];
+      wq[0] = r.q0.x; wq[1] = r.q0.y; wq[2] = r.q0.z; wq[3] = r.q0.w;
+      wq[4] = r.q1.x; wq[5] = r.q1.y; wq[6] = r.q1.z; wq[7] = r.q1.w;
     }
+    constexpr int PER = 32 / BITS;
 #pragma unroll
-    for (int i = 0; i < BITS; i++) {
-      const uint32_t w = wq[i];
-      constexpr int PER = 32 / BITS;
+    for (int i = 0; i < BITS; i++)
 #pragma unroll
-      for (int e = 0; e < PER; e++) v[PER * i + e] = fmaf(s, (float)((w >> (BITS * e)) & ((1u << BITS) - 1u)), bi);
-    }
+      for (int e = 0; e < PER; e++) v[PER * i + e] = fmaf(r.s, (float)((wq[i] >> (BITS * e)) & ((1u << BITS) - 1u)), r.b);
   }
 #pragma unroll
   for (int i = 0; i < 16; i++) out[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+}
+
+// Dequantize one 32-weight block of row `row` (K-block `kb`) into 16 dwords of
+// bf16 pairs in natural element order.  `ok` = false yields zeros.
+template <int SCH>
+RLXQ_DEV void dequant_block_bf16(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok, uint32_t* out) {
+  RawBlk<SCH> r;
+  load_blk<SCH>(a, row, kb, ok, r);
+  conv_blk<SCH>(r, out);
 }
 
 template <int SCH, int BM, int BN>
@@ -229,6 +263,176 @@ RLXQ_DEV void gemm_body(const rlxq_gemm_args& a) {
       }
 }
 
+// 256 x 256 output tile, one workgroup per CU (144 KB of LDS), WGM x WGN
+// waves each owning a (256/WGM) x (256/WGN) sub-tile of 32x32 MFMA tiles with
+// f32 accumulators in AGPRs.  With 4 waves (2 x 2, 128 x 128 each) a wave
+// issues 64 MFMAs per K step against 32 KB of LDS operand reads, half the LDS
+// bytes per MFMA of a 64 x 64 wave tile; with 8 waves (2 x 4) two waves share
+// each SIMD, so one wave's dequantisation and waits overlap the other's
+// MFMAs.  The loop body has no branches (row bounds are clamped addresses plus
+// selects), and the next step's LDS stores and conversions sit between the
+// MFMA groups of the current step.
+template <int SCH, int WGM, int WGN, int PF>
+RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
+  constexpr int BM = 256, BN = 256;
+  constexpr int NT = 64 * WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int AP = 2048 / NT;   // 16-byte activation chunks per thread per step
+  constexpr int BPT = 512 / NT;   // weight blocks per thread per step
+  static_assert(AP % 2 == 0 && BPT >= 1, "threads");
+  extern __shared__ uint16_t smem[];
+  uint16_t* As = smem;                // [2][BM][GLD]
+  uint16_t* Bs = smem + 2 * BM * GLD;  // [2][BN][GLD]
+
+  int tm, tn;
+  if (!tile_of(blockIdx.x, a.tiles_m, a.tiles_n, 4, tm, tn)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wm = wv % WGM, wn = wv / WGM;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int KT = (int)(a.K / GBK);
+  const uint16_t* xg = reinterpret_cast<const uint16_t*>(a.x);
+
+  // activation tile: 256 rows x 128 B = 2048 chunks of 16 B
+  int64_t arow[AP];
+  bool aok[AP];
+#pragma unroll
+  for (int i = 0; i < AP; i++) {
+    const int c = tid + NT * i, r = c >> 3;
+    aok[i] = m0 + r < a.M;
+    arow[i] = (aok[i] ? m0 + r : a.M - 1) * a.K + (c & 7) * 8;
+  }
+  // weight tile: 256 rows x 2 blocks; thread -> row n0 + (tid & 255), blocks
+  // (tid >> 8) + q * (NT / 256)
+  const int brl = tid & 255;
+  const bool bok = n0 + brl < a.N;
+  const int64_t brow = bok ? n0 + brl : a.N - 1;
+
+  // Global loads run PF steps ahead of the MFMAs (PF register stages); the
+  // LDS stores and conversions of the next step sit between the MFMA groups
+  // of the current one.
+  struct Stage {
+    uint4 a[AP];
+    RawBlk<SCH> b[BPT];
+  };
+  auto gload = [&](int kt, Stage& P) {
+#pragma unroll
+    for (int i = 0; i < AP; i++) {
+      const uint4 v = *reinterpret_cast<const uint4*>(xg + arow[i] + (int64_t)kt * GBK);
+      P.a[i] = aok[i] ? v : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int q = 0; q < BPT; q++) load_blk<SCH>(a, brow, 2 * (int64_t)kt + (tid >> 8) + q, bok, P.b[q]);
+  };
+  auto store_a = [&](const Stage& P, int buf, int half) {
+#pragma unroll
+    for (int i = half * AP / 2; i < (half + 1) * AP / 2; i++) {
+      const int c = tid + NT * i;
+      *reinterpret_cast<uint4*>(As + (buf * BM + (c >> 3)) * GLD + (c & 7) * 8) = P.a[i];
+    }
+  };
+  auto store_b = [&](const Stage& P, int buf, int q) {
+    uint32_t o[16];
+    conv_blk<SCH>(P.b[q], o);
+    uint16_t* dst = Bs + (buf * BN + brl) * GLD + ((tid >> 8) + q) * 32;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      *reinterpret_cast<uint4*>(dst + 8 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+  };
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  auto compute_ks = [&](int cur, int ks) {
+    const uint16_t* Ab = As + (cur * BM + wm * WM) * GLD;
+    const uint16_t* Bb = Bs + (cur * BN + wn * WN) * GLD;
+    bf16x8_t af[TM], bfr[TN];
+    const int kof = ks * 16 + 8 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; i++) af[i] = *reinterpret_cast<const bf16x8_t*>(Ab + (i * 32 + (lane & 31)) * GLD + kof);
+#pragma unroll
+    for (int j = 0; j < TN; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(Bb + (j * 32 + (lane & 31)) * GLD + kof);
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+  };
+  auto store_all = [&](const Stage& P, int buf) {
+    store_a(P, buf, 0);
+    store_a(P, buf, 1);
+#pragma unroll
+    for (int q = 0; q < BPT; q++) store_b(P, buf, q);
+  };
+  // one K step: MFMAs from buffer `cur` while stage `Pn` goes into cur ^ 1
+  auto step = [&](int cur, const Stage& Pn) {
+    compute_ks(cur, 0);
+    compute_ks(cur, 1);
+    store_a(Pn, cur ^ 1, 0);
+    compute_ks(cur, 2);
+    store_a(Pn, cur ^ 1, 1);
+    store_b(Pn, cur ^ 1, 0);
+    compute_ks(cur, 3);
+#pragma unroll
+    for (int q = 1; q < BPT; q++) store_b(Pn, cur ^ 1, q);
+  };
+
+  if constexpr (PF == 1) {
+    Stage P;
+    gload(0, P);
+    store_all(P, 0);
+    __syncthreads();
+    for (int kt = 0; kt + 1 < KT; kt++) {
+      gload(kt + 1, P);
+      step(kt & 1, P);
+      __syncthreads();
+    }
+  } else {
+    // two stages, the loop unrolled by two so each stage is a fixed register set
+    Stage P0, P1;
+    gload(0, P0);
+    gload(KT > 1 ? 1 : 0, P1);
+    store_all(P0, 0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 2 < KT; kt += 2) {
+      gload(kt + 2, P0);
+      step(0, P1);
+      __syncthreads();
+      gload(kt + 3 < KT ? kt + 3 : KT - 1, P1);
+      step(1, P0);
+      __syncthreads();
+    }
+    if (kt + 1 < KT) {
+      step(0, P1);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int ks = 0; ks < GBK / 16; ks++) compute_ks((KT - 1) & 1, ks);
+
+  // epilogue: C[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2), reg 4*(i/8) + i%4
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int64_t n = n0 + wn * WN + j * 32 + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int64_t m = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+        if (m < a.M && n < a.N) {
+          const float v = acc[i][j][r];
+          if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
+          else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+        }
+      }
+    }
+}
+
 }  // namespace rlxq
 
 #define RLXQ_GEMM_INST(NAME, SCH)                                                         \
@@ -240,3 +444,19 @@ RLXQ_GEMM_INST(rlxq_gemm_q4_0_t128, SCH_Q4_0)
 RLXQ_GEMM_INST(rlxq_gemm_q8_0_t128, SCH_Q8_0)
 RLXQ_GEMM_INST(rlxq_gemm_mlx4_t128, SCH_MLX4)
 RLXQ_GEMM_INST(rlxq_gemm_mlx8_t128, SCH_MLX8)
+
+#define RLXQ_GEMM256_INST(SNAME, SCH)                                                        \
+  extern "C" __global__ __launch_bounds__(256, 1) void rlxq_gemm_##SNAME##_t256(rlxq_gemm_args a) { \
+    rlxq::gemm256_body<SCH, 2, 2, 1>(a);                                                           \
+  }                                                                                                \
+  extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8(rlxq_gemm_args a) { \
+    rlxq::gemm256_body<SCH, 2, 4, 1>(a);                                                           \
+  }                                                                                                \
+  extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8p2(rlxq_gemm_args a) { \
+    rlxq::gemm256_body<SCH, 2, 4, 2>(a);                                                           \
+  }
+RLXQ_GEMM256_INST(q4_1, SCH_Q4_1)
+RLXQ_GEMM256_INST(q4_0, SCH_Q4_0)
+RLXQ_GEMM256_INST(q8_0, SCH_Q8_0)
+RLXQ_GEMM256_INST(mlx4, SCH_MLX4)
+RLXQ_GEMM256_INST(mlx8, SCH_MLX8)

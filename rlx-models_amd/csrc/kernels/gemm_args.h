@@ -12,6 +12,7 @@ typedef struct rlxq_gemm_args {
   void* y;                /* [M, N] output, leading dimension y_ld        */
   int64_t M, N, K, rb, y_ld;
   int32_t group, sb_bf16, y_bf16, pad;
+  int32_t tiles_m, tiles_n;   /* output tile grid (256 x 256 kernels)     */
 } rlxq_gemm_args;
 
 #endif

@@ -107,3 +107,40 @@ def test_gemm_forced_for_small_m_and_f32_output(ctx, orc, monkeypatch):
         assert ctx.last_kernel.startswith("rlxq_gemm_")
         w = orc.dequantize(3, packed, 256).astype(np.float64)
         assert rel_err(got, xv.astype(np.float64) @ w.T) <= TOL_PREFILL
+
+
+@pytest.mark.parametrize("scheme", [1, 2, 3, 4, 5])
+def test_every_gemm_tiling(ctx, orc, scheme, monkeypatch):
+    """Every tiling (128 x 128; 256 x 256 with 4 or 8 waves) on a ragged shape, every scheme:
+    each within the prefill bar, and the two agree to ~1e-6 (f32 output; both
+    accumulate K in the same order)."""
+    import torch
+    import rlxq
+
+    m, k, n = 300, 640, 272
+    rng = np.random.default_rng(scheme)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    kw = {}
+    if scheme in (rlxq.MLX_AFFINE4, rlxq.MLX_AFFINE8):
+        bits, group = (4, 32) if scheme == rlxq.MLX_AFFINE4 else (8, 128)
+        codes = rng.integers(0, 1 << bits, (n, k)).astype(np.uint32)
+        wq = orc.mlx_pack(codes, bits)
+        sc = rng.uniform(0.01, 0.1, (n, k // group)).astype(np.float32)
+        bi = rng.uniform(-0.5, 0.1, (n, k // group)).astype(np.float32)
+        packed = wq.view(np.uint8)
+        kw = dict(group=group, scales=_t(sc), biases=_t(bi))
+        wd = orc.mlx_dequantize(wq, sc, bi, k, bits, group).astype(np.float64)
+    else:
+        packed = orc.synth(scheme, rng, n, k)
+        wd = orc.dequantize(scheme, packed, k).astype(np.float64)
+    outs = {}
+    monkeypatch.setenv("RLXQ_PREFILL", "gemm")
+    for tile in ("128", "256", "256w8", "256w8p2"):
+        monkeypatch.setenv("RLXQ_GEMM_TILE", tile)
+        announce(f"gemm tiling t{tile} scheme={scheme} m={m} k={k} n={n}")
+        got, xv = run_gemm(ctx, orc, scheme, x, packed, n, ydt="f32", **kw)
+        assert ctx.last_kernel.endswith(f"_t{tile}")
+        assert rel_err(got, xv.astype(np.float64) @ wd.T) <= TOL_PREFILL
+        outs[tile] = got
+    for t in ("256", "256w8", "256w8p2"):
+        assert np.allclose(outs["128"], outs[t], rtol=1e-6, atol=1e-6 * np.abs(outs["128"]).max())
