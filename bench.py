@@ -1,6 +1,6 @@
 """Benchmark of the quantized-matmul hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
 
 One "step" is the decode-token GEMV work of Qwen3-8B with Q4_1 group-32
 weights at M=1: 36 layers x (o 4096->4096, fused qkv
@@ -8,12 +8,23 @@ weights at M=1: 36 layers x (o 4096->4096, fused qkv
 own weights (4.35 GB in HBM, so the 256 MB MALL cannot serve repeats),
 activations bf16 N(0,1), outputs f32.  Inputs are resident in HBM before the
 timed region.  `value` is algorithmic bytes (N*K*0.625 + K*2 + N*4 per GEMV)
-moved per second.
+moved per second over K timed steps.
 
-The same run also reports, as extra keys: per-shape microseconds and GB/s,
-the roofline object for the dominant kernel (HIP events on the launch stream),
-the prefill dequant-GEMM TFLOP/s (config 4) and the CPU baseline: the C
-restatement of the reference CPU algorithm timed on this host's cores.
+Extra keys of the same JSON line:
+  roofline        the dominant kernel of the step (largest total time):
+                  algorithmic bytes per launch / average launch duration, the
+                  durations from HIP events on the launch stream around runs
+                  of the step's launches of one shape, back to back
+  per_shape       per-projection microseconds and GB/s (same runs)
+  prefill         config 4: Q4_1 dequant-GEMM, M in {512, 2048, 4096}, bf16
+                  in/out, TFLOP/s; and the W8A8 variant (per-row int8
+                  activations computed on the fly x per-channel int8 weights)
+  batched_decode  config 3: Q4_1 and Q8_0, M in {1, 4, 16, 64}
+  moe             config 5: routed-expert grouped GEMV, 16 tokens, top-8 of 128
+  q8_gemv         config 1: Q8_0 2048->2048, f32 activations
+  cpu_baseline    the C restatement of the reference CPU algorithm timed on
+                  this host's cores over a bounded sample
+Weights in the extra sections rotate over enough copies to exceed the MALL.
 """
 from __future__ import annotations
 
@@ -30,9 +41,12 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+INT8_PEAK_TOPS = 5000.0
 LAYERS = 36
 SHAPES = [("o_proj", 4096, 4096), ("qkv", 4096, 6144), ("gate_up", 4096, 24576), ("down", 12288, 4096)]
 Q4_1_BPW = 20 / 32
+Q8_0_BPW = 34 / 32
+MALL_BYTES = 256 << 20
 
 
 def gemv_bytes(k: int, n: int, m: int = 1, bpw: float = Q4_1_BPW, xsize: int = 2, ysize: int = 4) -> float:
@@ -49,6 +63,34 @@ def synth_q4_1_gpu(n: int, k: int, gen):
     m = torch.empty(nb, device="cuda").uniform_(-0.4, 0.0, generator=gen).half().view(torch.uint8).view(nb, 2)
     q = torch.randint(0, 256, (nb, 16), device="cuda", dtype=torch.uint8, generator=gen)
     return torch.cat([d, m, q], dim=1).contiguous().view(-1)
+
+
+def synth_q8_0_gpu(n: int, k: int, gen):
+    """Q8_0 rows on the device: codes ~U{-127..127}, d ~U(0.002, 0.02) fp16 (config 1)."""
+    import torch
+
+    nb = n * (k // 32)
+    d = torch.empty(nb, device="cuda").uniform_(0.002, 0.02, generator=gen).half().view(torch.uint8).view(nb, 2)
+    q = torch.randint(-127, 128, (nb, 32), device="cuda", dtype=torch.int8, generator=gen).view(torch.uint8)
+    return torch.cat([d, q], dim=1).contiguous().view(-1)
+
+
+def _copies(nbytes: float) -> int:
+    """Weight copies whose total exceeds the 256 MB MALL (at least 2)."""
+    return max(2, int(MALL_BYTES // nbytes) + 2)
+
+
+def _time_us(fn, reps: int, stream) -> float:
+    """Mean microseconds of fn() over reps calls, HIP events on `stream`."""
+    import torch
+
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for i in range(reps):
+        fn(i)
+    ev1.record(stream)
+    ev1.synchronize()
+    return ev0.elapsed_time(ev1) * 1e3 / reps
 
 
 def cpu_baseline(seconds: float = 10.0) -> dict:
@@ -77,13 +119,177 @@ def cpu_baseline(seconds: float = 10.0) -> dict:
                       f"{el:.1f} s, reference-order C restatement (OpenMP)"}
 
 
+# ---------------------------------------------------------------- sections
+def decode_roofline(ctx, layers, xs, ys, sptr, stream, reps: int) -> tuple[dict, dict]:
+    """Per-shape launch durations: HIP events on the launch stream around runs
+    of the step's own launches of one shape (the 36 layers' weights, back to
+    back, `reps` times), so the launches keep the back-to-back dispatch of the
+    step; the dominant kernel is the one with the largest total time."""
+    import torch
+    import rlxq
+
+    per, tot = {}, {}
+    for name, k, n in SHAPES:
+        def run(i, name=name, k=k, n=n):
+            ctx.dequant_matmul(xs[k], layers[i % LAYERS][name], rlxq.GGUF_Q4_1, n, y=ys[name], stream=sptr)
+        for i in range(LAYERS):
+            run(i)
+        kern = ctx.last_kernel
+        us = _time_us(run, reps * LAYERS, stream)
+        b = gemv_bytes(k, n)
+        per[name] = {"k": k, "n": n, "kernel": kern, "us": round(us, 3), "GBps": round(b / us / 1e3, 1),
+                     "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        t = tot.setdefault(kern, [0.0, 0.0, 0])
+        t[0] += us
+        t[1] += b
+        t[2] += 1
+    dom = max(tot, key=lambda kk: tot[kk][0])
+    d_us, d_bytes, d_n = tot[dom]
+    achieved = d_bytes / d_us / 1e3
+    roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "bytes_per_launch": round(d_bytes / d_n), "us_per_launch": round(d_us / d_n, 3),
+            "shapes": [nm for nm, p in per.items() if p["kernel"] == dom],
+            "share_of_layer_time": round(d_us / sum(t[0] for t in tot.values()), 3)}
+    return roof, per
+
+
+def prefill_section(ctx, gen, sptr, stream, quick: bool) -> dict:
+    """Config 4: Q4_1 dequant-GEMM and the W8A8 variant, bf16 in/out."""
+    import torch
+    import rlxq
+
+    res = {"q4_1": {}, "w8a8": {}}
+    ms_list = (4096,) if quick else (512, 2048, 4096)
+    for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):
+        w = synth_q4_1_gpu(n, k, gen)
+        for m in ms_list:
+            x = torch.randn((m, k), generator=gen, device="cuda").to(torch.bfloat16)
+            y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+            run = lambda i: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_1, n, y=y, stream=sptr)
+            run(0)
+            torch.cuda.synchronize()
+            us = _time_us(run, 5, stream)
+            tf = 2.0 * m * n * k / us / 1e6
+            res["q4_1"][f"{name}_m{m}"] = {"m": m, "k": k, "n": n, "kernel": ctx.last_kernel, "us": round(us, 1),
+                                           "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+            del x, y
+        del w
+        m = 4096
+        wq = torch.randint(-127, 128, (k, n), device="cuda", dtype=torch.int8, generator=gen)
+        sw = torch.rand((n,), device="cuda", generator=gen) * 0.01 + 1e-4
+        x = torch.randn((m, k), generator=gen, device="cuda").to(torch.bfloat16)
+        y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        run = lambda i: ctx.w8a8_gemm(x, wq, sw, n, y=y, stream=sptr)
+        run(0)
+        torch.cuda.synchronize()
+        us = _time_us(run, 5, stream)
+        tops = 2.0 * m * n * k / us / 1e6
+        res["w8a8"][f"{name}_m{m}"] = {"m": m, "k": k, "n": n, "kernel": ctx.last_kernel, "us": round(us, 1),
+                                       "TOPs": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                                       "includes": "per-row int8 activation quantisation pre-pass"}
+        del wq, sw, x, y
+        torch.cuda.empty_cache()
+    return res
+
+
+def batched_section(ctx, gen, sptr, stream) -> dict:
+    """Config 3: batched decode, Q4_1 and Q8_0, M in {1, 4, 16, 64}, bf16 x, f32 y."""
+    import torch
+    import rlxq
+
+    res = {}
+    for sname, scheme, bpw, synth in (("q4_1", rlxq.GGUF_Q4_1, Q4_1_BPW, synth_q4_1_gpu),
+                                      ("q8_0", rlxq.GGUF_Q8_0, Q8_0_BPW, synth_q8_0_gpu)):
+        for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):
+            wb = n * k * bpw
+            ws = [synth(n, k, gen) for _ in range(_copies(wb))]
+            for m in (1, 4, 16, 64):
+                x = torch.randn((m, k), generator=gen, device="cuda").to(torch.bfloat16)
+                y = torch.empty((m, n), device="cuda")
+                run = lambda i: ctx.dequant_matmul(x, ws[i % len(ws)], scheme, n, y=y, stream=sptr)
+                for i in range(len(ws)):
+                    run(i)
+                torch.cuda.synchronize()
+                us = _time_us(run, 4 * len(ws), stream)
+                b = gemv_bytes(k, n, m=m, bpw=bpw)
+                res[f"{sname}_{name}_m{m}"] = {"kernel": ctx.last_kernel, "us": round(us, 2),
+                                               "GBps": round(b / us / 1e3, 1),
+                                               "TFLOPs": round(2.0 * m * n * k / us / 1e6, 2)}
+            del ws
+            torch.cuda.empty_cache()
+    return res
+
+
+def moe_section(ctx, gen, sptr, stream) -> dict:
+    """Config 5: one MoE FFN of a Qwen3-30B-A3B-like layer for 16 tokens: route
+    (softmax of N(0,1) logits over 128 experts, top-8), gate|up 2048->1536 per
+    (token, slot), SwiGLU, down 768->2048 with the probability-weighted
+    combine.  Two layers with their own expert banks alternate (755 MB)."""
+    import torch
+    import rlxq
+
+    E, H, I, TOPK, T = 128, 2048, 768, 8, 16
+    res = {}
+    banks = [(synth_q4_1_gpu(E * 2 * I, H, gen), synth_q4_1_gpu(E * H, I, gen)) for _ in range(2)]
+    logits = [torch.randn((T, E), generator=gen, device="cuda") for _ in range(2)]
+    routes = [ctx.moe_route(lg, TOPK, True, stream=sptr) for lg in logits]
+    x = torch.randn((T, H), generator=gen, device="cuda").to(torch.bfloat16)
+    gu = torch.empty((T * TOPK, 2 * I), device="cuda", dtype=torch.bfloat16)
+    act = torch.empty((T * TOPK, I), device="cuda", dtype=torch.bfloat16)
+    y = torch.empty((T, H), device="cuda")
+
+    def layer(i):
+        (bgu, bdn), (ids, probs) = banks[i % 2], routes[i % 2]
+        ctx.moe_grouped(x, bgu, ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_EXPAND, 2 * I, E, y=gu, stream=sptr)
+        ctx.swiglu(gu, I, out=act, stream=sptr)
+        ctx.moe_grouped(act, bdn, ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_COMBINE, H, E, y=y, stream=sptr)
+
+    for i in range(4):
+        layer(i)
+    torch.cuda.synchronize()
+    us = _time_us(layer, 40, stream)
+    uniq = [int(torch.unique(r[0]).numel()) for r in routes]
+    u = sum(uniq) / len(uniq)
+    per_expert = 2 * I * H * Q4_1_BPW + H * I * Q4_1_BPW
+    b = u * per_expert + T * H * 2 + T * TOPK * (2 * I * 2 + I * 2) + T * H * 4
+    res = {"us_per_layer": round(us, 2), "unique_experts": u, "GBps": round(b / us / 1e3, 1),
+           "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+           "bytes_model": "unique experts x (1,966,080 + 983,040) B + activations",
+           "launches_per_layer": "expand (table + grouped GEMV), swiglu, combine (table + grouped GEMV + reduce)"}
+    return res
+
+
+def q8_section(ctx, gen, sptr, stream) -> dict:
+    """Config 1: Q8_0 GEMV 2048->2048 with f32 activations, warm and rotated."""
+    import torch
+    import rlxq
+
+    k = n = 2048
+    wb = n * k * Q8_0_BPW
+    ws = [synth_q8_0_gpu(n, k, gen) for _ in range(_copies(wb))]
+    x = torch.randn((1, k), generator=gen, device="cuda")
+    y = torch.empty((1, n), device="cuda")
+    b = gemv_bytes(k, n, bpw=Q8_0_BPW, xsize=4)
+    out = {}
+    for label, pick in (("warm", lambda i: ws[0]), ("rotated", lambda i: ws[i % len(ws)])):
+        run = lambda i: ctx.dequant_matmul(x, pick(i), rlxq.GGUF_Q8_0, n, y=y, stream=sptr)
+        for i in range(len(ws)):
+            run(i)
+        torch.cuda.synchronize()
+        us = _time_us(run, 4 * len(ws), stream)
+        out[label] = {"kernel": ctx.last_kernel, "us": round(us, 3), "GBps": round(b / us / 1e3, 1)}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="only the decode step and its roofline")
+    ap.add_argument("--quick", action="store_true", help="prefill at M=4096 only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     a = ap.parse_args()
     if a.gpus != 1:
@@ -106,13 +312,10 @@ def main() -> int:
     ys = {name: torch.empty((1, n), device="cuda") for name, _, n in SHAPES}
     torch.cuda.synchronize()
 
-    def one(name, k, n, w):
-        ctx.dequant_matmul(xs[k], w, rlxq.GGUF_Q4_1, n, y=ys[name], stream=sptr)
-
     def step():
         for lw in layers:
             for name, k, n in SHAPES:
-                one(name, k, n, lw[name])
+                ctx.dequant_matmul(xs[k], lw[name], rlxq.GGUF_Q4_1, n, y=ys[name], stream=sptr)
 
     for _ in range(a.warmup):
         step()
@@ -126,41 +329,9 @@ def main() -> int:
     ms_per_step = wall / a.steps * 1e3
     value = step_bytes * a.steps / wall / 1e9
 
-    # ---- per-shape launch durations with HIP events on the launch stream ---
-    per = {}
-    kern_of = {}
-    for name, k, n in SHAPES:
-        reps = 3
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        for lw in layers:
-            one(name, k, n, lw[name])
-        kern_of[name] = ctx.last_kernel
-        ev0.record(stream)
-        for _ in range(reps):
-            for lw in layers:
-                one(name, k, n, lw[name])
-        ev1.record(stream)
-        ev1.synchronize()
-        us = ev0.elapsed_time(ev1) * 1e3 / (reps * LAYERS)
-        b = gemv_bytes(k, n)
-        per[name] = {"k": k, "n": n, "kernel": kern_of[name], "us": round(us, 3), "GBps": round(b / us / 1e3, 1),
-                     "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
-    layer_us = sum(v["us"] for v in per.values())
-
-    # dominant kernel = the one with the largest total time
-    tot = {}
-    for name, v in per.items():
-        t = tot.setdefault(kern_of[name], [0.0, 0.0, 0])
-        t[0] += v["us"]
-        t[1] += gemv_bytes(v["k"], v["n"])
-        t[2] += 1
-    dom = max(tot, key=lambda kk: tot[kk][0])
-    d_us, d_bytes, d_n = tot[dom]
-    achieved = (d_bytes / d_n) / (d_us / d_n) / 1e3  # GB/s
-    roofline = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "bytes_per_launch": round(d_bytes / d_n), "us_per_launch": round(d_us / d_n, 3),
-                "traffic": None}
+    roofline, per = decode_roofline(ctx, layers, xs, ys, sptr, stream, reps=3)
+    del layers
+    torch.cuda.empty_cache()
 
     out = {
         "metric": "Q4 GEMV HBM GB/s (% peak) at M=1; prefill dequant-GEMM TFLOP/s",
@@ -180,50 +351,20 @@ def main() -> int:
                                "per layer (4.35 GB)",
                    "accumulate": "f32", "x": "bf16", "y": "f32"},
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
-        "us_per_layer": round(layer_us, 3),
+        "us_per_layer": round(sum(p["us"] for p in per.values()), 3),
         "per_shape": per,
         "roofline": roofline,
     }
-
-    if not a.no_prefill:
-        out["prefill"] = prefill_bench(ctx, gen, sptr)
+    if not a.no_extra:
+        out["prefill"] = prefill_section(ctx, gen, sptr, stream, a.quick)
+        out["batched_decode"] = batched_section(ctx, gen, sptr, stream)
+        out["moe"] = moe_section(ctx, gen, sptr, stream)
+        out["q8_gemv"] = q8_section(ctx, gen, sptr, stream)
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(a.cpu_seconds)
     print(json.dumps(out), flush=True)
     ctx.close()
     return 0
-
-
-def prefill_bench(ctx, gen, sptr) -> dict:
-    """Config 4: Q4_1 dequant-GEMM, M=4096 at 4096->24576 and 12288->4096, bf16 out."""
-    import torch
-    import rlxq
-
-    res = {}
-    for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):
-        m = 4096
-        w = synth_q4_1_gpu(n, k, gen)
-        x = torch.randn((m, k), generator=gen, device="cuda").to(torch.bfloat16)
-        y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
-        try:
-            ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_1, n, y=y, stream=sptr)
-        except rlxq.RlxqError as e:
-            res[name] = {"error": str(e)}
-            continue
-        torch.cuda.synchronize()
-        reps = 5
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        ev0.record()
-        for _ in range(reps):
-            ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_1, n, y=y, stream=sptr)
-        ev1.record()
-        ev1.synchronize()
-        ms = ev0.elapsed_time(ev1) / reps
-        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        res[name] = {"m": m, "k": k, "n": n, "ms": round(ms, 4), "TFLOPs": round(tf, 1),
-                     "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
-        del w, x, y
-    return res
 
 
 if __name__ == "__main__":

@@ -33,15 +33,15 @@ const W8a8Cfg kW8a8[] = {
 
 // Tiling choice; RLXQ_W8A8_CFG=<name> selects one (tuning sweeps and the
 // per-variant parity test).
-const W8a8Cfg* pick_w8a8(int64_t m, int64_t n) {
+// Default: 256 x 256 tiles (8 waves) once they cover the CUs, else 128 x 128.
+const W8a8Cfg* pick_w8a8(int64_t m, int64_t n, int cus) {
   if (const char* e = std::getenv("RLXQ_W8A8_CFG")) {
     for (const auto& c : kW8a8)
       if (std::strcmp(c.name, e) == 0) return &c;
     return nullptr;
   }
-  (void)m;
-  (void)n;
-  return &kW8a8[0];
+  const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256);
+  return t256 >= (cus > 0 ? cus : 256) ? &kW8a8[4] : &kW8a8[0];
 }
 
 }  // namespace
@@ -153,7 +153,7 @@ int rlxq_w8a8_gemm(rlxq_ctx* ctx, const void* x, int x_dtype, const int8_t* wq, 
   if (!aligned16(wq)) return fail(ctx, RLXQ_E_ALIGN, "w8a8_gemm: wq must be 16-byte aligned");
   if (m == 0) return RLXQ_OK;
 
-  const W8a8Cfg* c = pick_w8a8(m, n);
+  const W8a8Cfg* c = pick_w8a8(m, n, ctx->cu_count);
   if (!c) return fail(ctx, RLXQ_E_NOKERNEL, "w8a8_gemm: RLXQ_W8A8_CFG names no compiled tiling");
   const int64_t tiles_m = (m + c->BM - 1) / c->BM, tiles_n = (n + c->BN - 1) / c->BN;
   if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "w8a8_gemm: too many tiles");
