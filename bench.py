@@ -75,6 +75,19 @@ def synth_q8_0_gpu(n: int, k: int, gen):
     return torch.cat([d, q], dim=1).contiguous().view(-1)
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (scaled by the plain-copy calibration), or None."""
+    path = ROOT / "profiles" / "gemv_q4_1_m1_qwen3_8b_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic-bytes-per-launch" and f[1] == kernel:
+            return int(f[2])
+    return None
+
+
 def _copies(nbytes: float) -> int:
     """Weight copies whose total exceeds the 256 MB MALL (at least 2)."""
     return max(2, int(MALL_BYTES // nbytes) + 2)
@@ -147,7 +160,7 @@ def decode_roofline(ctx, layers, xs, ys, sptr, stream, reps: int) -> tuple[dict,
     d_us, d_bytes, d_n = tot[dom]
     achieved = d_bytes / d_us / 1e3
     roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
             "bytes_per_launch": round(d_bytes / d_n), "us_per_launch": round(d_us / d_n, 3),
             "shapes": [nm for nm, p in per.items() if p["kernel"] == dom],
             "share_of_layer_time": round(d_us / sum(t[0] for t in tot.values()), 3)}
@@ -291,6 +304,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="only the decode step and its roofline")
     ap.add_argument("--quick", action="store_true", help="prefill at M=4096 only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 512 MiB device copy 3 times (the reference for FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py: this build measures one GPU only; every GPU box here has one GPU, "
@@ -299,6 +314,15 @@ def main() -> int:
 
     import torch
     import rlxq
+
+    if a.copy_calibration:
+        src = torch.ones((512 << 20) // 4, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "copies": 3}), flush=True)
+        return 0
 
     ctx = rlxq.Context(0)
     stream = torch.cuda.current_stream()
