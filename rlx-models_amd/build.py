@@ -29,7 +29,7 @@ HIPCC = str(ROCM / "bin" / "hipcc")
 
 # Code objects the host library embeds (rlxq.cpp RLXQ_EMBED lines).  A name
 # without a source file is embedded empty and skipped at load time.
-CODE_OBJECTS = ("gemv", "misc", "gemm", "moe", "int8")
+CODE_OBJECTS = ("gemv", "misc", "gemm", "moe", "int8", "skinny")
 
 HIP_FLAGS = [
     "--genco", "--offload-arch=gfx950", "-O3", "-std=c++17",

@@ -190,6 +190,17 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     }
     if (use_gemm) return gemm_dispatch(ctx, scheme, group, x, w, scales, biases, sb_dtype, rb, m, k, n, y, y_dtype, stream);
   }
+  // Batched decode: from 5 rows, GGUF weights stream once for all rows through
+  // the f16-MFMA kernel.  RLXQ_DECODE=gemv|skinny forces one where both apply.
+  {
+    const bool sk_ok = skinny_applies(scheme, m, k);
+    bool use_sk = sk_ok && m >= 5;
+    if (const char* e = std::getenv("RLXQ_DECODE")) {
+      if (!std::strcmp(e, "gemv")) use_sk = false;
+      if (!std::strcmp(e, "skinny")) use_sk = sk_ok;
+    }
+    if (use_sk) return skinny_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream);
+  }
 
   rlxq_gemv_args a;
   a.x = x;

@@ -36,6 +36,7 @@ RLXQ_EMBED(rlxq_co_misc, "misc.co")
 RLXQ_EMBED(rlxq_co_gemm, "gemm.co")
 RLXQ_EMBED(rlxq_co_moe, "moe.co")
 RLXQ_EMBED(rlxq_co_int8, "int8.co")
+RLXQ_EMBED(rlxq_co_skinny, "skinny.co")
 
 namespace {
 
@@ -51,6 +52,7 @@ const Image kImages[] = {
     {rlxq_co_gemm_begin, rlxq_co_gemm_end, "gemm"},
     {rlxq_co_moe_begin, rlxq_co_moe_end, "moe"},
     {rlxq_co_int8_begin, rlxq_co_int8_end, "int8"},
+    {rlxq_co_skinny_begin, rlxq_co_skinny_end, "skinny"},
 };
 
 std::string hip_msg(hipError_t e) { return std::string(hipGetErrorName(e)) + ": " + hipGetErrorString(e); }

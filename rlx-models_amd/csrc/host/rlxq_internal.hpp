@@ -70,6 +70,9 @@ const char* scheme_name(int scheme);
 int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dtype, const void* w,
                   const void* scales, const void* biases, int sb_dtype, int64_t m, int64_t k,
                   int64_t n, void* y, int y_dtype, void* stream);
+bool skinny_applies(int scheme, int64_t m, int64_t k);
+int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
+                    int64_t k, int64_t n, void* y, int y_dtype, void* stream);
 int i8b_dispatch(rlxq_ctx* ctx, int group, const void* x, int x_dtype, const void* w, const void* scales,
                  const void* zp, int sb_dtype, int64_t m, int64_t k, int64_t n, void* y, int y_dtype,
                  void* stream);

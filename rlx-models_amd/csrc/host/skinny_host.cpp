@@ -1,0 +1,108 @@
+// Host side of the batched-decode (small M) dequant-GEMM: activation
+// preparation, then the skinny kernel, then (small N only) the split-K sum.
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "rlxq.h"
+#include "rlxq_internal.hpp"
+#include "skinny_args.h"
+
+namespace rlxq {
+
+namespace {
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+}  // namespace
+
+bool skinny_applies(int scheme, int64_t m, int64_t k) {
+  return (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q4_1) && m >= 1 &&
+         m <= 256 && k % 128 == 0;
+}
+
+// Workgroups: (128 weight rows, K split, 64-row chunk).  K splits only where
+// the row tiles do not cover the CUs: the smallest power of two that does,
+// at most 32 and at most one split per K step; their partial sums (f32,
+// [splits, M, N]) are added in split order.
+int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
+                    int64_t k, int64_t n, void* y, int y_dtype, void* stream) {
+  const int MT = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+  // blocks per thread per step (K per step = 64 * BPT); 2 measured fastest,
+  // RLXQ_SKINNY_BPT selects another compiled one (2 or 8 for MT <= 2, 2 or 4
+  // for MT = 4)
+  int BPT = 2;
+  if (const char* e = std::getenv("RLXQ_SKINNY_BPT")) BPT = std::atoi(e);
+  if (k % (64 * BPT)) BPT = 2;
+  const int64_t KS = 64 * BPT;
+  const int64_t MC = 16 * MT;
+  const int64_t tiles_n = (n + 127) / 128, mch = (m + MC - 1) / MC;
+  const int64_t ksteps = k / KS;
+  const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  int64_t target = cus;
+  if (const char* e = std::getenv("RLXQ_SKINNY_WGS")) target = cus * std::atoi(e);
+  int64_t splits = 1;
+  while (tiles_n * mch * splits < target && splits * 2 <= ksteps && splits < 32) splits *= 2;
+  const int64_t kslice = ((ksteps + splits - 1) / splits) * KS;
+  splits = (k + kslice - 1) / kslice;
+  if (tiles_n * mch * splits > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: batched-decode grid");
+
+  const size_t x16_bytes = round256((size_t)(m * k) * 2), s_bytes = round256((size_t)m * 4);
+  const size_t part_bytes = splits > 1 ? round256((size_t)(splits * m * n) * 4) : 0;
+  void* ws = nullptr;
+  int rc;
+  if ((rc = workspace(ctx, x16_bytes + s_bytes + part_bytes, &ws))) return rc;
+  char* wsb = static_cast<char*>(ws);
+
+  rlxq_x16_args xa;
+  std::memset(&xa, 0, sizeof xa);
+  xa.x = x;
+  xa.x16 = reinterpret_cast<uint16_t*>(wsb);
+  xa.inv_s = reinterpret_cast<float*>(wsb + x16_bytes);
+  xa.M = m;
+  xa.K = k;
+  xa.x_bf16 = x_dtype == RLXQ_BF16;
+  xa.nibble_order = scheme != RLXQ_GGUF_Q8_0;
+  hipFunction_t fn;
+  if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
+  void* xargs[] = {&xa};
+  if ((rc = launch(ctx, fn, dim3((unsigned)m), dim3(256), 0, stream, xargs, "rlxq_x16_prep"))) return rc;
+
+  rlxq_skinny_args a;
+  std::memset(&a, 0, sizeof a);
+  a.x16 = xa.x16;
+  a.inv_s = xa.inv_s;
+  a.w = static_cast<const uint8_t*>(w);
+  a.part = part_bytes ? reinterpret_cast<float*>(wsb + x16_bytes + s_bytes) : nullptr;
+  a.y = y;
+  a.M = m;
+  a.N = n;
+  a.K = k;
+  a.rb = rb;
+  a.y_ld = n;
+  a.kslice = (int32_t)kslice;
+  a.splits = (int32_t)splits;
+  a.tiles_n = (int32_t)tiles_n;
+  a.y_bf16 = y_dtype == RLXQ_BF16;
+  char name[48];
+  std::snprintf(name, sizeof name, "rlxq_skinny_%s_mt%d_b%d", scheme_name(scheme), MT, BPT);
+  if ((rc = get_fn(ctx, name, &fn))) return rc;
+  const int rdw = 2 * BPT * (scheme == RLXQ_GGUF_Q8_0 ? 9 : 5) + 2;
+  const size_t stage = 128 * (size_t)rdw * 4 + (size_t)MC * (KS + 8) * 2;
+  const size_t red = 2 * (size_t)(MT * 8 * 4) * 64 * 4;
+  const size_t lds = stage > red ? stage : red;
+  void* args[] = {&a};
+  if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name))) return rc;
+  if (splits > 1) {
+    if ((rc = get_fn(ctx, "rlxq_skinny_reduce", &fn))) return rc;
+    const int64_t total = m * n;
+    void* rargs[] = {&a};
+    rc = launch(ctx, fn, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, rargs, "rlxq_skinny_reduce");
+    if (!rc) ctx->last_kernel = name;
+  }
+  return rc;
+}
+
+}  // namespace rlxq

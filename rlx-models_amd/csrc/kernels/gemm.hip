@@ -16,6 +16,7 @@
 // the LDS tiles are double-buffered, one barrier per step.
 #include "common.hip.h"
 #include "gemm_args.h"
+#include "gemm_dq.hip.h"
 
 namespace rlxq {
 
@@ -25,134 +26,6 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr int GBK = 64;        // K per step
 constexpr int GLD = GBK + 8;   // LDS row stride (bf16 elements)
 
-
-// Raw bytes of one 32-weight block, loaded ahead of their conversion so the
-// global loads of a K step can be in flight while the previous step computes.
-// All-zero raw bytes convert to zero weights (d = 0, or scale = bias = 0).
-template <int SCH> struct RawBlk;
-template <> struct RawBlk<SCH_Q4_1> { uint32_t h; uint4 q; };
-template <> struct RawBlk<SCH_Q4_0> { uint32_t w[5]; uint32_t off; };
-template <> struct RawBlk<SCH_Q8_0> { uint32_t w[9]; uint32_t off; };
-template <> struct RawBlk<SCH_MLX4> { uint4 q; float s, b; };
-template <> struct RawBlk<SCH_MLX8> { uint4 q0, q1; float s, b; };
-
-// Loads block `kb` of weight row `row` (a valid row); `ok` = false zeroes it
-// with selects, so the caller's loop body stays free of branches.
-template <int SCH>
-RLXQ_DEV void load_blk(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok, RawBlk<SCH>& r) {
-  const uint8_t* rp = a.w + row * a.rb;
-  if constexpr (SCH == SCH_Q4_1) {
-    const uint8_t* p = rp + kb * 20;
-    r.h = ok ? ld_u32(p) : 0u;
-    const uint4 q = ld_u128(p + 4);
-    r.q = q;
-  } else if constexpr (SCH == SCH_Q4_0 || SCH == SCH_Q8_0) {
-    // 18- and 34-byte blocks are 2-byte aligned: read the dwords covering the
-    // block without touching a byte beyond it (the tail is a 16-bit load when
-    // the block starts dword aligned)
-    constexpr int BB = SCH == SCH_Q4_0 ? 18 : 34, NW = SCH == SCH_Q4_0 ? 5 : 9;
-    const uint32_t off = (uint32_t)(kb * BB) & 3u;
-    const uint8_t* base = rp + kb * BB - off;
-#pragma unroll
-    for (int i = 0; i < NW - 1; i++) r.w[i] = ld_u32(base + 4 * i);
-    r.w[NW - 1] = off ? ld_u32(base + 4 * (NW - 1))
-                      : (uint32_t)*reinterpret_cast<const uint16_t*>(base + 4 * (NW - 1));
-    r.off = off;
-    if (!ok) r.w[0] = 0u, r.w[1] = 0u;  // zero scale (it sits in w[0] or the low half of w[1])
-  } else {
-    constexpr int BITS = SCH == SCH_MLX4 ? 4 : 8;
-    const uint8_t* q = rp + kb * BITS * 4;
-    const int64_t gi = row * (int64_t)(a.K / a.group) + (kb * 32) / a.group;
-    float s, bi;
-    if (a.sb_bf16) {
-      s = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(a.scales)[gi]);
-      bi = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(a.biases)[gi]);
-    } else {
-      s = reinterpret_cast<const float*>(a.scales)[gi];
-      bi = reinterpret_cast<const float*>(a.biases)[gi];
-    }
-    r.s = ok ? s : 0.f;
-    r.b = ok ? bi : 0.f;
-    if constexpr (SCH == SCH_MLX4) {
-      r.q = ld_u128(q);
-    } else {
-      r.q0 = ld_u128(q);
-      r.q1 = ld_u128(q + 16);
-    }
-  }
-}
-
-// Converts a raw block into 16 dwords of bf16 pairs in natural element order:
-// f32 d*q + m (the CPU decoder's arithmetic), rounded to bf16 (nearest even).
-template <int SCH>
-RLXQ_DEV void conv_blk(const RawBlk<SCH>& r, uint32_t* out) {
-  float v[32];
-  if constexpr (SCH == SCH_Q4_1 || SCH == SCH_Q4_0) {
-    uint32_t qs[4];
-    float d, m;
-    if constexpr (SCH == SCH_Q4_1) {
-      qs[0] = r.q.x; qs[1] = r.q.y; qs[2] = r.q.z; qs[3] = r.q.w;
-      d = f16_bits_to_f32(r.h & 0xffffu);
-      m = f16_bits_to_f32(r.h >> 16);
-    } else {
-      const uint32_t hd = r.off ? (r.w[0] >> 16) : (r.w[0] & 0xffffu);
-      // qs starts 2 bytes after the block start: byte off + 2 of the span
-      // (v_alignbyte takes shifts 0..3, so a 4-byte shift is the next dword)
-#pragma unroll
-      for (int i = 0; i < 4; i++) qs[i] = r.off ? r.w[i + 1] : align_bytes(r.w[i + 1], r.w[i], 2);
-      d = f16_bits_to_f32(hd);
-      m = -8.f * d;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      uint32_t lo = qs[i] & 0x0F0F0F0Fu, hi = (qs[i] >> 4) & 0x0F0F0F0Fu;
-      // opaque to the optimiser, so each byte converts with one v_cvt_f32_ubyteN
-      asm volatile("" : "+v"(lo), "+v"(hi));
-      v[4 * i + 0] = fmaf(d, (float)(lo & 0xffu), m);
-      v[4 * i + 1] = fmaf(d, (float)((lo >> 8) & 0xffu), m);
-      v[4 * i + 2] = fmaf(d, (float)((lo >> 16) & 0xffu), m);
-      v[4 * i + 3] = fmaf(d, (float)(lo >> 24), m);
-      v[16 + 4 * i + 0] = fmaf(d, (float)(hi & 0xffu), m);
-      v[16 + 4 * i + 1] = fmaf(d, (float)((hi >> 8) & 0xffu), m);
-      v[16 + 4 * i + 2] = fmaf(d, (float)((hi >> 16) & 0xffu), m);
-      v[16 + 4 * i + 3] = fmaf(d, (float)(hi >> 24), m);
-    }
-  } else if constexpr (SCH == SCH_Q8_0) {
-    const float d = f16_bits_to_f32(r.off ? (r.w[0] >> 16) : (r.w[0] & 0xffffu));
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t q = r.off ? r.w[i + 1] : align_bytes(r.w[i + 1], r.w[i], 2);
-#pragma unroll
-      for (int e = 0; e < 4; e++) v[4 * i + e] = d * (float)(int8_t)((q >> (8 * e)) & 0xffu);
-    }
-  } else {
-    // MLX affine: codes LSB-first in u32 words, scale * code + bias
-    constexpr int BITS = SCH == SCH_MLX4 ? 4 : 8;
-    uint32_t wq[BITS];
-    if constexpr (SCH == SCH_MLX4) {
-      wq[0] = r.q.x; wq[1] = r.q.y; wq[2] = r.q.z; wq[3] = r.q.w;
-    } else {
-      wq[0] = r.q0.x; wq[1] = r.q0.y; wq[2] = r.q0.z; wq[3] = r.q0.w;
-      wq[4] = r.q1.x; wq[5] = r.q1.y; wq[6] = r.q1.z; wq[7] = r.q1.w;
-    }
-    constexpr int PER = 32 / BITS;
-#pragma unroll
-    for (int i = 0; i < BITS; i++)
-#pragma unroll
-      for (int e = 0; e < PER; e++) v[PER * i + e] = fmaf(r.s, (float)((wq[i] >> (BITS * e)) & ((1u << BITS) - 1u)), r.b);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; i++) out[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
-}
-
-// Dequantize one 32-weight block of row `row` (K-block `kb`) into 16 dwords of
-// bf16 pairs in natural element order.  `ok` = false yields zeros.
-template <int SCH>
-RLXQ_DEV void dequant_block_bf16(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok, uint32_t* out) {
-  RawBlk<SCH> r;
-  load_blk<SCH>(a, row, kb, ok, r);
-  conv_blk<SCH>(r, out);
-}
 
 template <int SCH, int BM, int BN>
 RLXQ_DEV void gemm_body(const rlxq_gemm_args& a) {

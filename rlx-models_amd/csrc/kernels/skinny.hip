@@ -1,0 +1,386 @@
+// Batched-decode dequant-GEMM for small M (the multi-row decode path):
+// y[m, n] = sum_k x[m, k] * dequant(W)[n, k] for up to 64 activation rows and
+// GGUF Q8_0 / Q4_0 / Q4_1 weights, streaming every weight once for all rows.
+// Replaces the backend kernel of Op::DequantMatMul at decode batch sizes
+// (crates/rlx-models-core/src/standard_decoder.rs:727-738, M rows per call).
+//
+//  * rlxq_x16_prep: each activation row to f16, scaled by a power of two so
+//    its largest element lies in [2^13, 2^14) (exact; undone in the
+//    epilogue), and permuted within each 32-element block to the order in
+//    which a lane unpacks the codes: for the nibble formats position
+//    8g + e holds element 4g + e (e < 4) or 16 + 4g + e - 4.
+//  * rlxq_skinny_*: a workgroup takes 128 weight rows, a K split and all M
+//    rows.  Per step the raw blocks are staged in LDS (a run of blocks per
+//    thread, normalised to a dword scale word plus the code dwords) and the
+//    prepared activations next to them; wave w then contracts blocks w,
+//    w + 4, ... of the step: each lane turns its 8 codes into f16 weights with packed f16
+//    arithmetic (exact codes, then d*q + m with one rounding) as the B operand
+//    of v_mfma_f32_16x16x32_f16.  f16 weights keep the products within ~2^-12
+//    of the exact dequantised weights (bf16 weights would not meet a 1e-3
+//    output bound).  The four waves' partial sums are added in a fixed order.
+//  * rlxq_skinny_reduce: K splits added in split order (small N only).
+#include "common.hip.h"
+#include "gemm_dq.hip.h"
+#include "skinny_args.h"
+
+namespace rlxq {
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Element of a 32-block held at position p (see above).
+RLXQ_DEV int perm_k(int p, bool nibble) {
+  if (!nibble) return p;
+  const int g = p >> 3, e = p & 7;
+  return e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4);
+}
+
+constexpr int SK_BN = 128;          // weight rows per workgroup
+
+// Normalised LDS block: scale dword (Q4_1: d | m << 16, else d) + code dwords.
+template <int SCH> constexpr int sk_bdw() { return SCH == SCH_Q8_0 ? 9 : 5; }
+
+RLXQ_DEV f16x2_t as_h2(uint32_t v) { return __builtin_bit_cast(f16x2_t, v); }
+RLXQ_DEV uint32_t as_u(f16x2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Two codes of bytes (b0, b1) or (b2, b3) of `u` as f16 1024 + code.
+RLXQ_DEV f16x2_t magic_lo(uint32_t u) { return as_h2(perm_b32(0x64646464u, u, 0x04010400u)); }
+RLXQ_DEV f16x2_t magic_hi(uint32_t u) { return as_h2(perm_b32(0x64646464u, u, 0x04030402u)); }
+
+// The lane's B operand: 8 f16 weights of one block of one row, positions
+// 8g .. 8g + 7.  `bp` points at the normalised block.
+template <int SCH>
+RLXQ_DEV f16x8_t dequant_lane(const uint32_t* bp, int g) {
+  const uint32_t dm = bp[0];
+  const f16x2_t d2 = as_h2(perm_b32(dm, dm, 0x01000100u));
+  f16x2_t w[4];
+  if constexpr (SCH == SCH_Q8_0) {
+    const uint32_t u0 = bp[1 + 2 * g] ^ 0x80808080u, u1 = bp[2 + 2 * g] ^ 0x80808080u;
+    const f16x2_t off = {(_Float16)-1152.f, (_Float16)-1152.f};
+    w[0] = (magic_lo(u0) + off) * d2;
+    w[1] = (magic_hi(u0) + off) * d2;
+    w[2] = (magic_lo(u1) + off) * d2;
+    w[3] = (magic_hi(u1) + off) * d2;
+  } else {
+    const uint32_t qs = bp[1 + g];
+    const uint32_t lo = qs & 0x0F0F0F0Fu, hi = (qs >> 4) & 0x0F0F0F0Fu;
+    if constexpr (SCH == SCH_Q4_1) {
+      const f16x2_t m2 = as_h2(perm_b32(dm, dm, 0x03020302u));
+      const f16x2_t off = {(_Float16)-1024.f, (_Float16)-1024.f};
+      w[0] = __builtin_elementwise_fma(magic_lo(lo) + off, d2, m2);
+      w[1] = __builtin_elementwise_fma(magic_hi(lo) + off, d2, m2);
+      w[2] = __builtin_elementwise_fma(magic_lo(hi) + off, d2, m2);
+      w[3] = __builtin_elementwise_fma(magic_hi(hi) + off, d2, m2);
+    } else {
+      const f16x2_t off = {(_Float16)-1032.f, (_Float16)-1032.f};
+      w[0] = (magic_lo(lo) + off) * d2;
+      w[1] = (magic_hi(lo) + off) * d2;
+      w[2] = (magic_lo(hi) + off) * d2;
+      w[3] = (magic_hi(hi) + off) * d2;
+    }
+  }
+  return f16x8_t{w[0].x, w[0].y, w[1].x, w[1].y, w[2].x, w[2].y, w[3].x, w[3].y};
+}
+
+// Raw block -> normalised dwords.
+template <int SCH>
+RLXQ_DEV void normalise(const RawBlk<SCH>& r, uint32_t* o) {
+  if constexpr (SCH == SCH_Q4_1) {
+    o[0] = r.h;
+    o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;
+  } else {
+    constexpr int NQ = SCH == SCH_Q8_0 ? 8 : 4;
+    o[0] = r.off ? (r.w[0] >> 16) : (r.w[0] & 0xffffu);
+#pragma unroll
+    for (int i = 0; i < NQ; i++) o[1 + i] = r.off ? r.w[i + 1] : align_bytes(r.w[i + 1], r.w[i], 2);
+  }
+}
+
+// BPT blocks per thread per step: 2 threads per weight row, so a step spans
+// NB = 2 * BPT blocks (KS = 32 * NB of K) and wave w contracts blocks
+// w, w + 4, ...  One LDS buffer: the raw blocks of step s + 1 are in flight
+// in registers while step s is contracted from LDS.
+template <int SCH, int MT, int BPT>
+RLXQ_DEV void skinny_body(const rlxq_skinny_args& a) {
+  constexpr int NT = SK_BN / 16;   // 16-row N tiles per wave
+  constexpr int NB = 2 * BPT, KS = 32 * NB;
+  constexpr int BDW = sk_bdw<SCH>();
+  // row stride: NB blocks + 2 dwords, so that the scale and code reads of 16
+  // rows by 4 lane groups spread over the banks
+  constexpr int RDW = NB * BDW + 2;
+  constexpr int MC = 16 * MT;
+  constexpr int XST = KS + 8;                  // activation LDS row stride (f16)
+  constexpr int XC = MC * (KS / 8) / 256;      // 16-byte activation chunks per thread per step
+  static_assert(XC >= 1 && (MC * (KS / 8)) % 256 == 0, "rows");
+  extern __shared__ __align__(16) uint32_t sm[];
+  uint32_t* Wl = sm;                                              // [SK_BN][RDW]
+  uint16_t* Xl = reinterpret_cast<uint16_t*>(sm + SK_BN * RDW);    // [MC][XST]
+
+  const int tn = blockIdx.x % a.tiles_n;
+  const int sp = (blockIdx.x / a.tiles_n) % a.splits;
+  const int mc = blockIdx.x / (a.tiles_n * a.splits);
+  const int64_t n0 = (int64_t)tn * SK_BN, m0 = (int64_t)mc * MC;
+  const int64_t kb = (int64_t)sp * a.kslice;
+  const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
+  const int steps = (int)((ke - kb) / KS);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int g = lane >> 4, j = lane & 15;
+
+  rlxq_gemm_args ga;
+  ga.w = a.w;
+  ga.rb = a.rb;
+  ga.K = a.K;
+  ga.group = 32;
+  ga.sb_bf16 = 0;
+  ga.scales = nullptr;
+  ga.biases = nullptr;
+
+  // staging: thread -> weight row tid >> 1, blocks (tid & 1) * BPT + q
+  const int srow = tid >> 1, sblk = (tid & 1) * BPT;
+  const bool sok = n0 + srow < a.N;
+  const int64_t grow = sok ? n0 + srow : a.N - 1;
+  RawBlk<SCH> rb[BPT];
+  uint4 xr[XC];
+  int64_t xoff[XC];
+  bool xok[XC];
+#pragma unroll
+  for (int i = 0; i < XC; i++) {
+    const int c = tid + 256 * i, row = c / (KS / 8);
+    xok[i] = m0 + row < a.M;
+    xoff[i] = (xok[i] ? m0 + row : a.M - 1) * a.K + (c % (KS / 8)) * 8;
+  }
+
+  auto gload = [&](int s) {
+    const int64_t k0 = kb + (int64_t)s * KS;
+#pragma unroll
+    for (int q = 0; q < BPT; q++) load_blk<SCH>(ga, grow, k0 / 32 + sblk + q, sok, rb[q]);
+#pragma unroll
+    for (int i = 0; i < XC; i++) {
+      const uint4 v = *reinterpret_cast<const uint4*>(a.x16 + xoff[i] + k0);
+      xr[i] = xok[i] ? v : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int q = 0; q < BPT; q++) {
+      uint32_t o[BDW];
+      normalise<SCH>(rb[q], o);
+      uint32_t* dst = Wl + srow * RDW + (sblk + q) * BDW;
+#pragma unroll
+      for (int i = 0; i < BDW; i++) dst[i] = o[i];
+    }
+#pragma unroll
+    for (int i = 0; i < XC; i++) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<uint4*>(Xl + (c / (KS / 8)) * XST + (c % (KS / 8)) * 8) = xr[i];
+    }
+  };
+
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // wave wv contracts blocks wv + 4i of the step: A = activations, 16 rows x
+  // 8 positions per lane (lane j + 16g: row j, positions 8g..8g+7 of the
+  // block), B = the weights of 16 rows likewise
+  auto compute = [&]() {
+#pragma unroll
+    for (int i = 0; i < NB / 4; i++) {
+      const int blk = wv + 4 * i;
+      f16x8_t af[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++)
+        af[mt] = *reinterpret_cast<const f16x8_t*>(Xl + (16 * mt + j) * XST + 32 * blk + 8 * g);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const f16x8_t b = dequant_lane<SCH>(Wl + (16 * t + j) * RDW + blk * BDW, g);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mt], b, acc[mt][t], 0, 0, 0);
+      }
+    }
+  };
+
+  gload(0);
+  lstore();
+  __syncthreads();
+  for (int s = 0; s + 1 < steps; s++) {
+    gload(s + 1);
+    compute();
+    __syncthreads();
+    lstore();
+    __syncthreads();
+  }
+  compute();
+
+  // Add the four waves' sums in the fixed order (w0 + w2) + (w1 + w3).
+  constexpr int E = MT * NT * 4;
+  float* R = reinterpret_cast<float*>(sm);   // [2][E][64], reuses the staging LDS
+  __syncthreads();
+  if (wv >= 2) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) R[((wv - 2) * E + (mt * NT + t) * 4 + r) * 64 + lane] = acc[mt][t][r];
+  }
+  __syncthreads();
+  if (wv < 2) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[mt][t][r] += R[(wv * E + (mt * NT + t) * 4 + r) * 64 + lane];
+  }
+  __syncthreads();
+  if (wv == 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) R[((mt * NT + t) * 4 + r) * 64 + lane] = acc[mt][t][r];
+  }
+  __syncthreads();
+  if (wv != 0) return;
+  // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int64_t m = m0 + 16 * mt + 4 * g + r;
+      if (m >= a.M) continue;
+      const float is = a.inv_s[m];
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const int64_t n = n0 + 16 * t + j;
+        if (n >= a.N) continue;
+        const float v = (acc[mt][t][r] + R[((mt * NT + t) * 4 + r) * 64 + lane]) * is;
+        if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
+        else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
+        else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+      }
+    }
+}
+
+}  // namespace rlxq
+
+// One workgroup of 256 per activation row; each thread owns whole 32-element
+// blocks (held in registers, so the permutation is local): blocks t, t + 256,
+// t + 512 (K <= 24576 keeps a row in registers; longer rows are read twice).
+extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a) {
+  constexpr int RB = 3;   // register-resident blocks per thread
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  if (r >= a.M) return;
+  const int64_t nblk = a.K >> 5;
+  const int t = threadIdx.x;
+  auto load_blk32 = [&](int64_t b, float* v) {
+    if (a.x_bf16) {
+      const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + r * a.K + b * 32);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint4 u = p[q];
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          v[8 * q + 2 * e] = bf16_bits_to_f32(w[e] & 0xffffu);
+          v[8 * q + 2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+        }
+      }
+    } else {
+      const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.x) + r * a.K + b * 32);
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const float4 u = p[q];
+        v[4 * q] = u.x; v[4 * q + 1] = u.y; v[4 * q + 2] = u.z; v[4 * q + 3] = u.w;
+      }
+    }
+  };
+  float v[RB][32];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < RB; i++) {
+    const int64_t b = t + 256 * i;
+    if (b < nblk) {
+      load_blk32(b, v[i]);
+#pragma unroll
+      for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(v[i][e]));
+    }
+  }
+  for (int64_t b = t + 256 * RB; b < nblk; b += 256) {
+    float w[32];
+    load_blk32(b, w);
+#pragma unroll
+    for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(w[e]));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  if ((t & 63) == 0) red[t >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // a power-of-two scale putting the row maximum in [2^13, 2^14)
+  float s = 1.f, inv = 1.f;
+  if (amax > 0.f && amax <= 3.4e38f) {
+    int sh = 13 - ilogbf(amax);
+    sh = sh < -126 ? -126 : (sh > 126 ? 126 : sh);
+    s = ldexpf(1.f, sh);
+    inv = ldexpf(1.f, -sh);
+  }
+  const bool nib = a.nibble_order != 0;
+  auto store_blk32 = [&](int64_t b, const float* w) {
+    uint32_t o[16];
+#pragma unroll
+    for (int p = 0; p < 32; p += 2) {
+      const uint32_t h0 = f32_to_f16_bits(w[rlxq::perm_k(p, nib)] * s);
+      const uint32_t h1 = f32_to_f16_bits(w[rlxq::perm_k(p + 1, nib)] * s);
+      o[p / 2] = h0 | (h1 << 16);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(a.x16 + r * a.K + b * 32);
+#pragma unroll
+    for (int q = 0; q < 4; q++) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+  };
+#pragma unroll
+  for (int i = 0; i < RB; i++) {
+    const int64_t b = t + 256 * i;
+    if (b < nblk) store_blk32(b, v[i]);
+  }
+  for (int64_t b = t + 256 * RB; b < nblk; b += 256) {
+    float w[32];
+    load_blk32(b, w);
+    store_blk32(b, w);
+  }
+  if (t == 0) a.inv_s[r] = inv;
+}
+
+// Split-K partial sums added in split order.
+extern "C" __global__ __launch_bounds__(256) void rlxq_skinny_reduce(rlxq_skinny_args a) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= a.M * a.N) return;
+  const int64_t m = i / a.N, n = i - m * a.N;
+  float v = 0.f;
+  for (int sp = 0; sp < a.splits; sp++) v += a.part[(int64_t)sp * a.M * a.N + i];
+  if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
+  else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+}
+
+#define RLXQ_SKINNY_INST(SNAME, SCH, MT, BPT)                                                      \
+  extern "C" __global__ __launch_bounds__(256, 2) void rlxq_skinny_##SNAME##_mt##MT##_b##BPT(       \
+      rlxq_skinny_args a) {                                                                        \
+    rlxq::skinny_body<SCH, MT, BPT>(a);                                                            \
+  }
+#define RLXQ_SKINNY_SCHEME(SNAME, SCH) \
+  RLXQ_SKINNY_INST(SNAME, SCH, 1, 2)   \
+  RLXQ_SKINNY_INST(SNAME, SCH, 1, 8)   \
+  RLXQ_SKINNY_INST(SNAME, SCH, 2, 2)   \
+  RLXQ_SKINNY_INST(SNAME, SCH, 2, 8)   \
+  RLXQ_SKINNY_INST(SNAME, SCH, 4, 2)   \
+  RLXQ_SKINNY_INST(SNAME, SCH, 4, 4)
+RLXQ_SKINNY_SCHEME(q4_1, SCH_Q4_1)
+RLXQ_SKINNY_SCHEME(q4_0, SCH_Q4_0)
+RLXQ_SKINNY_SCHEME(q8_0, SCH_Q8_0)

@@ -1,0 +1,29 @@
+/* Argument blocks of the batched-decode ("skinny", small M) kernels, shared
+ * by the host (g++) and device (hipcc) compilers: plain C types only. */
+#ifndef RLXQ_SKINNY_ARGS_H
+#define RLXQ_SKINNY_ARGS_H
+#include <stdint.h>
+
+/* Activation preparation: x [M, K] (f32 or bf16) -> x16 [M, K] f16 scaled by
+ * a power of two per row (inv_s[m] = 1 / scale) and permuted within each
+ * 32-element block to the order the packed codes unpack to. */
+typedef struct rlxq_x16_args {
+  const void* x;
+  uint16_t* x16;
+  float* inv_s;
+  int64_t M, K;
+  int32_t x_bf16, nibble_order;
+} rlxq_x16_args;
+
+typedef struct rlxq_skinny_args {
+  const uint16_t* x16;    /* prepared activations [M, K] f16              */
+  const float* inv_s;     /* [M]                                          */
+  const uint8_t* w;       /* packed GGUF rows, row stride rb bytes        */
+  float* part;            /* [splits, M, N] partial sums (splits > 1)     */
+  void* y;                /* [M, N] output (splits == 1)                  */
+  int64_t M, N, K, rb, y_ld;
+  int32_t kslice;         /* K per split, a multiple of 128               */
+  int32_t splits, tiles_n, y_bf16;
+} rlxq_skinny_args;
+
+#endif

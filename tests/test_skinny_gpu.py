@@ -1,0 +1,67 @@
+"""Parity of the batched-decode (small M) dequant-GEMM against the CPU oracle,
+through the C ABI: f16 weights (one rounding of d*q + m) and f16 activations
+(exact for bf16 inputs, power-of-two row scaling) on f16 MFMA with fp32
+accumulation.  Bar: max|got - want| / max|want| <= 1e-3 (f32 output), 1e-2
+(bf16 output), `want` the oracle's dequantized weights contracted in float64."""
+import numpy as np
+import pytest
+
+from conftest import announce
+from test_gemv_gpu import TOL_BF16, TOL_F32, rel_err, run_dense
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _force_skinny(monkeypatch):
+    monkeypatch.setenv("RLXQ_DECODE", "skinny")
+
+
+@pytest.mark.parametrize("scheme", [1, 2, 3])
+@pytest.mark.parametrize("mkn", [(5, 128, 7), (16, 640, 128), (17, 1024, 300), (33, 512, 129),
+                                 (64, 4096, 256), (65, 256, 64), (100, 384, 200), (256, 128, 40)], ids=str)
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_skinny_matches_oracle(ctx, orc, scheme, mkn, xdt):
+    m, k, n = mkn
+    announce(f"skinny scheme={scheme} x={xdt} {mkn}")
+    rng = np.random.default_rng(m * 7 + k + n)
+    packed = orc.synth(scheme, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt=xdt)
+    assert ctx.last_kernel.startswith("rlxq_skinny_"), ctx.last_kernel
+    assert rel_err(got, want) <= TOL_F32
+
+
+@pytest.mark.parametrize("scheme", [1, 3])
+def test_skinny_split_k_and_bf16_out(ctx, orc, scheme):
+    """Small N with long K takes the split-K path; bf16 output."""
+    m, k, n = 16, 12288, 136
+    announce(f"skinny split-k scheme={scheme}")
+    rng = np.random.default_rng(scheme)
+    packed = orc.synth(scheme, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt="bf16")
+    assert rel_err(got, want) <= TOL_F32
+    got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt="bf16", ydt="bf16")
+    assert rel_err(got, want) <= TOL_BF16
+
+
+@pytest.mark.parametrize("scheme", [1, 3])
+def test_skinny_activation_range(ctx, orc, scheme):
+    """Rows far outside the f16 range and rows of tiny values: the per-row
+    power-of-two scale keeps each row's products accurate."""
+    m, k, n = 8, 512, 96
+    announce(f"skinny activation range scheme={scheme}")
+    rng = np.random.default_rng(20 + scheme)
+    packed = orc.synth(scheme, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[0] *= 1e6
+    x[1] *= 1e-6
+    x[2, 7] = 3e5
+    x[3] = 0.0
+    got, want = run_dense(ctx, orc, scheme, x, packed, n)
+    for r in range(m):
+        if r == 3:
+            assert np.all(got[r] == 0.0)
+            continue
+        assert rel_err(got[r:r + 1], want[r:r + 1]) <= TOL_F32, r
