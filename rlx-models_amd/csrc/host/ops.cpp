@@ -190,10 +190,12 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     }
     if (use_gemm) return gemm_dispatch(ctx, scheme, group, x, w, scales, biases, sb_dtype, rb, m, k, n, y, y_dtype, stream);
   }
-  // Batched decode: from 5 rows, GGUF weights stream once for all rows through
-  // the f16-MFMA kernel.  RLXQ_DECODE=gemv|skinny forces one where both apply.
+  // Batched decode: from 5 rows of bf16 activations (exact in f16 once scaled),
+  // GGUF weights stream once for all rows through the f16-MFMA kernel; f32
+  // activations would lose bits in f16 and stay on the GEMV.
+  // RLXQ_DECODE=gemv|skinny forces one where both apply.
   {
-    const bool sk_ok = skinny_applies(scheme, m, k);
+    const bool sk_ok = skinny_applies(scheme, m, k) && xbf;
     bool use_sk = sk_ok && m >= 5;
     if (const char* e = std::getenv("RLXQ_DECODE")) {
       if (!std::strcmp(e, "gemv")) use_sk = false;

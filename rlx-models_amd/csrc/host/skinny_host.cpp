@@ -36,7 +36,12 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   int BPT = 2;
   if (const char* e = std::getenv("RLXQ_SKINNY_BPT")) BPT = std::atoi(e);
   if (k % (64 * BPT)) BPT = 2;
-  const int64_t KS = 64 * BPT;
+  // Q4_1, up to 16 rows, K % 256 == 0: the LDS-DMA ring variant (measured
+  // faster there; RLXQ_SKINNY_DMA=0|1 forces it off or on where it applies)
+  bool dma = scheme == RLXQ_GGUF_Q4_1 && k % 256 == 0 && MT == 1;
+  if (const char* e = std::getenv("RLXQ_SKINNY_DMA"))
+    dma = scheme == RLXQ_GGUF_Q4_1 && k % 256 == 0 && std::atoi(e) != 0;
+  const int64_t KS = dma ? 256 : 64 * BPT;
   const int64_t MC = 16 * MT;
   const int64_t tiles_n = (n + 127) / 128, mch = (m + MC - 1) / MC;
   const int64_t ksteps = k / KS;
@@ -87,10 +92,12 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   a.tiles_n = (int32_t)tiles_n;
   a.y_bf16 = y_dtype == RLXQ_BF16;
   char name[48];
-  std::snprintf(name, sizeof name, "rlxq_skinny_%s_mt%d_b%d", scheme_name(scheme), MT, BPT);
+  if (dma) std::snprintf(name, sizeof name, "rlxq_skinny_q4_1_mt%d_dma", MT);
+  else std::snprintf(name, sizeof name, "rlxq_skinny_%s_mt%d_b%d", scheme_name(scheme), MT, BPT);
   if ((rc = get_fn(ctx, name, &fn))) return rc;
   const int rdw = 2 * BPT * (scheme == RLXQ_GGUF_Q8_0 ? 9 : 5) + 2;
-  const size_t stage = 128 * (size_t)rdw * 4 + (size_t)MC * (KS + 8) * 2;
+  const size_t stage = dma ? 3 * (128 * 160 + (size_t)MC * 512)
+                           : 128 * (size_t)rdw * 4 + (size_t)MC * (KS + 8) * 2;
   const size_t red = 2 * (size_t)(MT * 8 * 4) * 64 * 4;
   const size_t lds = stage > red ? stage : red;
   void* args[] = {&a};

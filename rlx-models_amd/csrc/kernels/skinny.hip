@@ -41,6 +41,11 @@ constexpr int SK_BN = 128;          // weight rows per workgroup
 // Normalised LDS block: scale dword (Q4_1: d | m << 16, else d) + code dwords.
 template <int SCH> constexpr int sk_bdw() { return SCH == SCH_Q8_0 ? 9 : 5; }
 
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8): wait on one counter, leave the others unconstrained.
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8); }
+constexpr int lgkmcnt0_imm() { return 0xF | (0x3 << 14) | (0x7 << 4); }
+
 RLXQ_DEV f16x2_t as_h2(uint32_t v) { return __builtin_bit_cast(f16x2_t, v); }
 RLXQ_DEV uint32_t as_u(f16x2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
@@ -268,6 +273,166 @@ RLXQ_DEV void skinny_body(const rlxq_skinny_args& a) {
     }
 }
 
+// Q4_1 with the weight and activation tiles copied global -> LDS by the
+// gfx950 LDS-DMA load (global_load_lds_dwordx4: the 16 bytes of lane l land
+// at the wave's LDS pointer + 16 l), into a ring of D stages of 256 K each, so
+// D - 1 steps of loads are in flight without registers.  A stage holds
+// 128 rows x 8 blocks (160 B per row, the blocks' raw bytes) and MC
+// activation rows x 256 f16 (512 B per row, 16-byte chunks XOR-swizzled by
+// row so the MFMA operand reads of 16 rows spread over the banks).
+template <int MT, int D>
+RLXQ_DEV void skinny_dma_body(const rlxq_skinny_args& a) {
+  constexpr int NT = SK_BN / 16;
+  constexpr int KS = 256, NB = 8;              // K and blocks per step
+  constexpr int WROW = NB * 20;                // raw weight bytes per row per step
+  constexpr int WCH = SK_BN * WROW / 16;       // 16-byte weight chunks per stage
+  constexpr int MC = 16 * MT;
+  constexpr int XCH = MC * KS * 2 / 16;        // 16-byte activation chunks per stage
+  constexpr int NIW = WCH / 256, NIX = XCH / 256;   // DMA instructions per wave per stage
+  static_assert(WCH % 256 == 0 && XCH % 256 == 0, "stage / waves");
+  constexpr int WST = SK_BN * WROW, XSTB = MC * KS * 2, STAGE = WST + XSTB;   // bytes
+  extern __shared__ __align__(16) uint8_t smb[];
+
+  const int tn = blockIdx.x % a.tiles_n;
+  const int sp = (blockIdx.x / a.tiles_n) % a.splits;
+  const int mc = blockIdx.x / (a.tiles_n * a.splits);
+  const int64_t n0 = (int64_t)tn * SK_BN, m0 = (int64_t)mc * MC;
+  const int64_t kb = (int64_t)sp * a.kslice;
+  const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
+  const int steps = (int)((ke - kb) / KS);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int g = lane >> 4, j = lane & 15;
+
+  // per-lane global sources of this wave's DMA instructions (step offset added later)
+  const uint8_t* wsrc[NIW];
+#pragma unroll
+  for (int i = 0; i < NIW; i++) {
+    const int c = (wv * NIW + i) * 64 + lane;          // chunk of the stage
+    const int r = c / (WROW / 16), piece = c % (WROW / 16);
+    const int64_t row = n0 + r < a.N ? n0 + r : a.N - 1;
+    wsrc[i] = a.w + row * a.rb + 16 * piece;
+  }
+  const uint16_t* xsrc[NIX];
+#pragma unroll
+  for (int i = 0; i < NIX; i++) {
+    const int c = (wv * NIX + i) * 64 + lane;          // LDS chunk position
+    const int r = c / 32, cp = c % 32;                 // 32 chunks per activation row
+    const int lc = cp ^ (r & 15);                      // the logical chunk stored there
+    const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;
+    xsrc[i] = a.x16 + m * a.K + 8 * lc;
+  }
+  auto issue = [&](int s) {
+    uint8_t* st = smb + (s % D) * STAGE;
+    const int64_t k0 = kb + (int64_t)s * KS;
+#pragma unroll
+    for (int i = 0; i < NIW; i++)
+      __builtin_amdgcn_global_load_lds(wsrc[i] + (k0 / 32) * 20, st + (wv * NIW + i) * 1024, 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < NIX; i++)
+      __builtin_amdgcn_global_load_lds(xsrc[i] + k0, st + WST + (wv * NIX + i) * 1024, 16, 0, 0);
+  };
+  // wait until this wave's loads of step s have landed: at most `later`
+  // steps' loads issued after them may still be outstanding
+  auto wait_for = [&](int later) {
+    constexpr int PER = NIW + NIX;
+    if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER));
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  };
+
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int s) {
+    const uint8_t* st = smb + (s % D) * STAGE;
+    const uint32_t* Wl = reinterpret_cast<const uint32_t*>(st);
+    const uint16_t* Xl = reinterpret_cast<const uint16_t*>(st + WST);
+#pragma unroll
+    for (int i = 0; i < NB / 4; i++) {
+      const int blk = wv + 4 * i;
+      f16x8_t af[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) {
+        const int r = 16 * mt + j, lc = 4 * blk + g;
+        af[mt] = *reinterpret_cast<const f16x8_t*>(Xl + r * KS + 8 * (lc ^ (r & 15)));
+      }
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const f16x8_t b = dequant_lane<SCH_Q4_1>(Wl + (16 * t + j) * (WROW / 4) + blk * 5, g);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mt], b, acc[mt][t], 0, 0, 0);
+      }
+    }
+  };
+
+  static_assert(D == 3, "the wait counts below assume a ring of 3");
+  for (int s = 0; s < D - 1 && s < steps; s++) issue(s);
+  for (int s = 0; s < steps; s++) {
+    const int later = steps - 1 - s < D - 2 ? steps - 1 - s : D - 2;
+    wait_for(later);
+    // this wave's operand reads of step s - 1 are complete, then the barrier:
+    // step s landed for every wave, and no wave still reads step s - 1's slot
+    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
+    __builtin_amdgcn_s_barrier();
+    if (s + D - 1 < steps) issue(s + D - 1);
+    compute(s);
+  }
+
+  // Add the four waves' sums in the fixed order (w0 + w2) + (w1 + w3).
+  constexpr int E = MT * NT * 4;
+  float* R = reinterpret_cast<float*>(smb);
+  __syncthreads();
+  if (wv >= 2) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) R[((wv - 2) * E + (mt * NT + t) * 4 + r) * 64 + lane] = acc[mt][t][r];
+  }
+  __syncthreads();
+  if (wv < 2) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[mt][t][r] += R[(wv * E + (mt * NT + t) * 4 + r) * 64 + lane];
+  }
+  __syncthreads();
+  if (wv == 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) R[((mt * NT + t) * 4 + r) * 64 + lane] = acc[mt][t][r];
+  }
+  __syncthreads();
+  if (wv != 0) return;
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int64_t m = m0 + 16 * mt + 4 * g + r;
+      if (m >= a.M) continue;
+      const float is = a.inv_s[m];
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const int64_t n = n0 + 16 * t + j;
+        if (n >= a.N) continue;
+        const float v = (acc[mt][t][r] + R[((mt * NT + t) * 4 + r) * 64 + lane]) * is;
+        if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
+        else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
+        else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+      }
+    }
+}
+
 }  // namespace rlxq
 
 // One workgroup of 256 per activation row; each thread owns whole 32-element
@@ -384,3 +549,11 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_skinny_reduce(rlxq_skinny
 RLXQ_SKINNY_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_SKINNY_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_SKINNY_SCHEME(q8_0, SCH_Q8_0)
+
+#define RLXQ_SKINNY_DMA_INST(MT)                                                                  \
+  extern "C" __global__ __launch_bounds__(256, 2) void rlxq_skinny_q4_1_mt##MT##_dma(rlxq_skinny_args a) { \
+    rlxq::skinny_dma_body<MT, 3>(a);                                                              \
+  }
+RLXQ_SKINNY_DMA_INST(1)
+RLXQ_SKINNY_DMA_INST(2)
+RLXQ_SKINNY_DMA_INST(4)
