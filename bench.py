@@ -235,42 +235,41 @@ def batched_section(ctx, gen, sptr, stream) -> dict:
 
 
 def moe_section(ctx, gen, sptr, stream) -> dict:
-    """Config 5: one MoE FFN of a Qwen3-30B-A3B-like layer for 16 tokens: route
-    (softmax of N(0,1) logits over 128 experts, top-8), gate|up 2048->1536 per
-    (token, slot), SwiGLU, down 768->2048 with the probability-weighted
-    combine.  Two layers with their own expert banks alternate (755 MB)."""
+    """Config 5: one MoE FFN of a Qwen3-30B-A3B-like layer for 16 tokens, as
+    three launches: route (softmax of N(0,1) logits over 128 experts, top-8,
+    renormalised), the fused gate|up 2048->1536 + SwiGLU per (token, slot),
+    and down 768->2048 with the probability-weighted combine.  Two layers with
+    their own expert banks and logits alternate (755 MB of banks)."""
     import torch
     import rlxq
 
     E, H, I, TOPK, T = 128, 2048, 768, 8, 16
-    res = {}
     banks = [(synth_q4_1_gpu(E * 2 * I, H, gen), synth_q4_1_gpu(E * H, I, gen)) for _ in range(2)]
     logits = [torch.randn((T, E), generator=gen, device="cuda") for _ in range(2)]
-    routes = [ctx.moe_route(lg, TOPK, True, stream=sptr) for lg in logits]
     x = torch.randn((T, H), generator=gen, device="cuda").to(torch.bfloat16)
-    gu = torch.empty((T * TOPK, 2 * I), device="cuda", dtype=torch.bfloat16)
     act = torch.empty((T * TOPK, I), device="cuda", dtype=torch.bfloat16)
     y = torch.empty((T, H), device="cuda")
+    routes = [None, None]
 
     def layer(i):
-        (bgu, bdn), (ids, probs) = banks[i % 2], routes[i % 2]
-        ctx.moe_grouped(x, bgu, ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_EXPAND, 2 * I, E, y=gu, stream=sptr)
-        ctx.swiglu(gu, I, out=act, stream=sptr)
+        bgu, bdn = banks[i % 2]
+        ids, probs = ctx.moe_route(logits[i % 2], TOPK, True, stream=sptr)
+        routes[i % 2] = ids
+        ctx.moe_grouped(x, bgu, ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_EXPAND_SWIGLU, 2 * I, E, y=act, stream=sptr)
         ctx.moe_grouped(act, bdn, ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_COMBINE, H, E, y=y, stream=sptr)
 
     for i in range(4):
         layer(i)
     torch.cuda.synchronize()
     us = _time_us(layer, 40, stream)
-    uniq = [int(torch.unique(r[0]).numel()) for r in routes]
+    uniq = [int(torch.unique(r).numel()) for r in routes]
     u = sum(uniq) / len(uniq)
     per_expert = 2 * I * H * Q4_1_BPW + H * I * Q4_1_BPW
-    b = u * per_expert + T * H * 2 + T * TOPK * (2 * I * 2 + I * 2) + T * H * 4
-    res = {"us_per_layer": round(us, 2), "unique_experts": u, "GBps": round(b / us / 1e3, 1),
-           "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-           "bytes_model": "unique experts x (1,966,080 + 983,040) B + activations",
-           "launches_per_layer": "expand (table + grouped GEMV), swiglu, combine (table + grouped GEMV + reduce)"}
-    return res
+    b = u * per_expert + T * H * 2 + T * TOPK * I * 2 * 2 + T * H * 4
+    return {"us_per_layer": round(us, 2), "unique_experts": u, "GBps": round(b / us / 1e3, 1),
+            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+            "bytes_model": "unique experts x (1,966,080 + 983,040) B + activations",
+            "launches_per_layer": "route, gate|up + SwiGLU (routing in the workgroups), down + combine"}
 
 
 def q8_section(ctx, gen, sptr, stream) -> dict:

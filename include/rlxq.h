@@ -120,16 +120,26 @@ int rlxq_dequant_grouped_matmul(rlxq_ctx* ctx, int scheme, int group_size,
                                 int64_t num_experts, void* y, int y_dtype,
                                 void* stream);
 
-/* MoE routed-expert grouped GEMV driven by a device routing table built from
- * ids [rows, top_k] (int32).  Two modes, which together make one expert FFN
+/* MoE routed-expert grouped GEMV, routed on the device from ids [rows, top_k]
+ * (int32).  Modes, which together make one expert FFN
  * (crates/rlx-unlimited-ocr/tests/quant_parity_backends.rs:338-373 and
  * standard_decoder.rs:12612-12760):
  *   RLXQ_MOE_EXPAND : x [rows, K] -> y [rows*top_k, N],
  *                     y[r*top_k + j] = x[r] . W[ids[r, j]]^T   (probs unused)
  *   RLXQ_MOE_COMBINE: x [rows*top_k, K] -> y [rows, N],
  *                     y[r] = sum_j probs[r, j] * (x[r*top_k + j] . W[ids[r, j]]^T)
- * GGUF schemes only (scales/biases NULL). */
-typedef enum rlxq_moe_mode { RLXQ_MOE_EXPAND = 0, RLXQ_MOE_COMBINE = 1 } rlxq_moe_mode;
+ *   RLXQ_MOE_EXPAND_SWIGLU: the fused gate|up projection with its SwiGLU
+ *                     (the GroupedSwiglu graph, crates/rlx-laguna/src/device_matmul.rs:383-426):
+ *                     expert slabs hold gate rows [0, N/2) then up rows
+ *                     [N/2, N); y [rows*top_k, N/2] = silu(g) * u with
+ *                     g, u = x[r] . W^T rows, silu(g) = g / (1 + exp(-g))
+ * GGUF schemes only (scales/biases NULL).  An id outside [0, num_experts)
+ * gives a zero output row (EXPAND) or a zero contribution (COMBINE). */
+typedef enum rlxq_moe_mode {
+    RLXQ_MOE_EXPAND = 0,
+    RLXQ_MOE_COMBINE = 1,
+    RLXQ_MOE_EXPAND_SWIGLU = 2
+} rlxq_moe_mode;
 int rlxq_moe_grouped(rlxq_ctx* ctx, int scheme, int mode, const void* x,
                      int x_dtype, const void* bank, const int32_t* ids,
                      const float* probs, int64_t rows, int64_t top_k,
@@ -139,6 +149,7 @@ int rlxq_moe_grouped(rlxq_ctx* ctx, int scheme, int mode, const void* x,
 /* Router: row softmax of logits [rows, E] (f32), top-k by probability
  * (ties to the lower expert id), optional renormalisation of the kept
  * probabilities (norm_topk_prob, standard_decoder.rs:12634-12661).
+ * E <= 1024, top_k <= 64.
  * Writes ids [rows, top_k] int32 and probs [rows, top_k] f32. */
 int rlxq_moe_route(rlxq_ctx* ctx, const float* logits, int64_t rows,
                    int64_t num_experts, int64_t top_k, int renorm,

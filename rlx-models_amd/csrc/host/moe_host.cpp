@@ -1,10 +1,14 @@
 // Host side of the grouped-expert entry points: rlxq_dequant_grouped_matmul
-// and rlxq_moe_grouped.  Both build the device routing table from the expert
-// indices, then run the grouped GEMV over the fired experts.
+// and rlxq_moe_grouped.  Both route the entries by expert (a device routing
+// table, or inside the GEMV's workgroups for decode-sized calls), then run
+// the grouped GEMV over the fired experts.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <string>
 
 #include "moe_args.h"
@@ -23,7 +27,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
                 const void* bank, const void* scales, const void* biases, int sb_dtype, const int32_t* ids,
                 const float* idx, int64_t n_entries, int64_t x_rows, int32_t x_div, int64_t k, int64_t n,
                 int64_t num_experts, void* y, int y_dtype, const float* probs, int64_t rows, int32_t top_k,
-                void* stream) {
+                bool swiglu, void* stream) {
   if (!x || !bank || !y || (!ids && !idx)) return fail(ctx, RLXQ_E_NULL, std::string(what) + ": null pointer");
   if (k <= 0 || n < 0 || n_entries < 0 || x_rows < 0) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": bad sizes");
   if (num_experts <= 0 || num_experts > 1024)
@@ -40,40 +44,105 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   if (!g.ok()) return fail(ctx, RLXQ_E_HIP, std::string(what) + ": hipSetDevice");
 
   const bool combine = probs != nullptr;
-  const size_t table_bytes = ((size_t)(2 + 2 * num_experts + n_entries) * 4 + 255) & ~size_t(255);
-  const size_t tmp_bytes = combine ? (size_t)n_entries * n * 4 : 0;
+  const int64_t width = swiglu ? n / 2 : n;   // output columns
+  // Routing inside the grouped GEMV's workgroups for decode-sized calls (no
+  // table launch; the entries of each expert cut into chunks of MT, one
+  // workgroup per chunk and tile); the device table for larger ones.
+  // RLXQ_MOE_ROUTE=table|fused forces one (fused only where it applies).
+  const bool fusable = n_entries <= 1024 && num_experts <= 1024;
+  bool fused = fusable, route_forced = false;
+  if (const char* e = std::getenv("RLXQ_MOE_ROUTE")) {
+    if (!std::strcmp(e, "table")) fused = false, route_forced = true;
+    if (!std::strcmp(e, "fused")) fused = fusable, route_forced = true;
+  }
+  // kernel choice
+  const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0) ? 2 : 1;
+  const int64_t units = (k / 32) / blocks;
+  const bool xbf = x_dtype == RLXQ_BF16;
+  const int64_t fired_est = num_experts < n_entries ? num_experts : n_entries;
+  const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  rlxq_moe_gemv_args ga;
+  std::memset(&ga, 0, sizeof ga);
+  char name[80];
+  int MT = 2;   // entries served per weight pass
+  // Register-activation kernels (4-bit codes: Q4_1, Q4_0, MLX affine 4-bit;
+  // bf16 activations; up to 256 units per row): lane groups of L lanes x NU
+  // units cover a row with the least padding, MT entries are served per
+  // weight pass.  The LDS-record kernels serve everything else.
+  const bool q40 = scheme == RLXQ_GGUF_Q4_0;   // two blocks per unit
+  bool xr = xbf && (scheme == RLXQ_GGUF_Q4_1 || q40 || scheme == RLXQ_MLX_AFFINE4) &&
+            units <= (q40 ? 128 : 256) && !(is_mlx(scheme) && group % 32);
+  if (const char* ev = std::getenv("RLXQ_MOE_KERNEL")) {
+    if (!std::strcmp(ev, "lds")) xr = false;
+  }
+  // The balanced in-workgroup routing pays for the register kernels (every
+  // workgroup one chunk of MT entries); the LDS-record kernels measure faster
+  // with the device table.
+  if (!xr && fused && !route_forced) fused = false;
+  if (xr) {
+    static const int cand[][2] = {{64, 1}, {64, 2}, {64, 4}, {8, 1}, {8, 2}, {8, 3}, {8, 4}};
+    int L = 0, NU = 0;
+    for (const auto& c : cand)
+      if (!(q40 && c[1] > 2) && c[0] * c[1] >= units && (L == 0 || c[0] * c[1] < L * NU)) L = c[0], NU = c[1];
+    // one entry per pass while experts hold few entries: the chunks of one
+    // expert then run side by side and share its rows through the caches
+    const double avg = (double)n_entries / (double)fired_est;
+    MT = avg < 3.0 ? 1 : (avg < 6.0 ? 2 : 4);
+    if (const char* ev = std::getenv("RLXQ_MOE_MT")) MT = std::atoi(ev);
+    if (MT != 1 && MT != 2 && MT != 4) MT = 2;
+    if (NU >= 3 && MT > 2) MT = 2;          // register budget of the instantiated kernels
+    if (q40) MT = std::min(MT, 2 / NU);
+    // workgroups (4 waves) per expert: about 16 waves per CU over the fired
+    // experts, and no more waves than column steps
+    const int64_t rp = 64 / L;
+    int64_t tiles = (4 * cus + fired_est - 1) / fired_est;
+    if (const char* ev = std::getenv("RLXQ_MOE_WGS")) tiles = std::max<int64_t>(1, tiles * std::atof(ev));
+    tiles = std::min<int64_t>(tiles, (width + 4 * rp - 1) / (4 * rp));
+    ga.tiles_n = (int32_t)std::max<int64_t>(tiles, 1);
+    ga.tile_rows = 0;
+    std::snprintf(name, sizeof name, "rlxq_moexr%s_%s_L%d_U%d_M%d%s", fused ? "f" : "", scheme_name(scheme), L, NU,
+                  MT, swiglu ? "_sw" : "");
+  } else {
+    const int L = units >= 48 ? 64 : 8;
+    std::snprintf(name, sizeof name, "rlxq_moe_gemv%s_%s_%s_L%d_M%d%s", fused ? "f" : "", scheme_name(scheme),
+                  xbf ? "bf16" : "f32", L, MT, swiglu ? "_sw" : "");
+    // Rows per workgroup tile; RLXQ_MOE_TILE=64|128|192|256 forces it.
+    int tile = 64;
+    if (const char* ev = std::getenv("RLXQ_MOE_TILE")) {
+      const int t = std::atoi(ev);
+      if (t == 64 || t == 128 || t == 192 || t == 256) tile = t;
+    }
+    ga.tile_rows = tile;
+    ga.tiles_n = (int32_t)(swiglu ? (width + tile / 2 - 1) / (tile / 2) : (n + tile - 1) / tile);
+  }
+  const size_t table_bytes = fused ? 0 : ((size_t)(2 + 2 * num_experts + n_entries) * 4 + 255) & ~size_t(255);
+  const size_t tmp_bytes = combine ? (size_t)n_entries * width * 4 : 0;
   void* ws = nullptr;
-  if ((rc = workspace(ctx, table_bytes + tmp_bytes, &ws))) return rc;
-  int32_t* table = static_cast<int32_t*>(ws);
+  if (table_bytes + tmp_bytes && (rc = workspace(ctx, table_bytes + tmp_bytes, &ws))) return rc;
+  int32_t* table = fused ? nullptr : static_cast<int32_t*>(ws);
   float* tmp = combine ? reinterpret_cast<float*>(static_cast<char*>(ws) + table_bytes) : nullptr;
 
   // 1. routing table
-  hipFunction_t ft;
-  if ((rc = get_fn(ctx, "rlxq_moe_table_k", &ft))) return rc;
-  rlxq_moe_table_args ta;
-  ta.ids = ids;
-  ta.idx_f32 = idx;
-  ta.table = table;
-  ta.zero_rows = combine ? static_cast<void*>(tmp) : y;
-  ta.n = n_entries;
-  ta.N = n;
-  ta.zero_ld = n;
-  ta.E = (int32_t)num_experts;
-  ta.zero_bf16 = (!combine && y_dtype == RLXQ_BF16) ? 1 : 0;
-  void* targs[] = {&ta};
-  if ((rc = launch(ctx, ft, dim3(1), dim3(1024), 0, stream, targs, "rlxq_moe_table_k"))) return rc;
+  if (!fused) {
+    hipFunction_t ft;
+    if ((rc = get_fn(ctx, "rlxq_moe_table_k", &ft))) return rc;
+    rlxq_moe_table_args ta;
+    ta.ids = ids;
+    ta.idx_f32 = idx;
+    ta.table = table;
+    ta.zero_rows = combine ? static_cast<void*>(tmp) : y;
+    ta.n = n_entries;
+    ta.N = width;
+    ta.zero_ld = width;
+    ta.E = (int32_t)num_experts;
+    ta.zero_bf16 = (!combine && y_dtype == RLXQ_BF16) ? 1 : 0;
+    void* targs[] = {&ta};
+    if ((rc = launch(ctx, ft, dim3(1), dim3(1024), 0, stream, targs, "rlxq_moe_table_k"))) return rc;
+  }
 
-  // 2. grouped GEMV over (fired expert, 32-row tile)
-  const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0) ? 2 : 1;
-  const int64_t units = (k / 32) / blocks;
-  const int L = units >= 48 ? 64 : 8;
-  const int MT = 2;
-  const bool xbf = x_dtype == RLXQ_BF16;
-  char name[80];
-  std::snprintf(name, sizeof name, "rlxq_moe_gemv_%s_%s_L%d_M%d", scheme_name(scheme), xbf ? "bf16" : "f32", L, MT);
+  // 2. grouped GEMV over (expert or chunk, tile)
   hipFunction_t fg;
   if ((rc = get_fn(ctx, name, &fg))) return rc;
-  rlxq_moe_gemv_args ga;
   ga.x = x;
   ga.bank = static_cast<const uint8_t*>(bank);
   ga.scales = scales;
@@ -82,7 +151,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   ga.y = combine ? static_cast<void*>(tmp) : y;
   ga.N = n;
   ga.rb = rb;
-  ga.y_ld = n;
+  ga.y_ld = width;
   ga.x_ld = k;
   ga.K = (int32_t)k;
   ga.E = (int32_t)num_experts;
@@ -90,12 +159,16 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   ga.sb_bf16 = sb_dtype == RLXQ_BF16 ? 1 : 0;
   ga.y_bf16 = (!combine && y_dtype == RLXQ_BF16) ? 1 : 0;
   ga.x_div = x_div;
-  ga.tiles_n = (int32_t)((n + 31) / 32);
-  ga.pad = 0;
-  const int64_t slots = num_experts < n_entries ? num_experts : n_entries;
+  ga.swiglu = swiglu ? 1 : 0;
+  ga.ids = ids;
+  ga.idx_f32 = idx;
+  ga.n_entries = (int32_t)n_entries;
+  // fused: chunks number at most min(E, n) + n / MT, plus the one that zeroes
+  // the rows of invalid entries
+  const int64_t slots = fused ? fired_est + (n_entries + MT - 1) / MT + 1 : fired_est;
   const int64_t grid = slots * ga.tiles_n;
   if (grid > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": grid too large");
-  const size_t lds = (size_t)MT * (k / 32) * (xbf ? 20 : 36) * 4;
+  const size_t lds = xr ? 0 : (size_t)2 * (k / 32) * (xbf ? 20 : 36) * 4;
   void* gargs[] = {&ga};
   if ((rc = launch(ctx, fg, dim3((unsigned)grid), dim3(256), lds, stream, gargs, name))) return rc;
 
@@ -103,10 +176,10 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   if (combine) {
     hipFunction_t fc;
     if ((rc = get_fn(ctx, "rlxq_moe_combine_k", &fc))) return rc;
-    int64_t R = rows, N = n;
+    int64_t R = rows, N = width;
     int32_t tk = top_k, yb = y_dtype == RLXQ_BF16 ? 1 : 0;
     void* cargs[] = {&tmp, (void*)&probs, &R, &tk, &N, &y, &yb};
-    const int64_t total = rows * n;
+    const int64_t total = rows * width;
     if ((rc = launch(ctx, fc, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, cargs,
                      "rlxq_moe_combine_k")))
       return rc;
@@ -130,7 +203,8 @@ int rlxq_dequant_grouped_matmul(rlxq_ctx* ctx, int scheme, int group_size, const
   ctx->last_error.clear();
   if (!expert_idx) return fail(ctx, RLXQ_E_NULL, "dequant_grouped_matmul: expert_idx is null");
   return grouped_run(ctx, "dequant_grouped_matmul", scheme, group_size, x, x_dtype, bank, scales, biases, sb_dtype,
-                     nullptr, expert_idx, rows, rows, 1, k, n, num_experts, y, y_dtype, nullptr, rows, 1, stream);
+                     nullptr, expert_idx, rows, rows, 1, k, n, num_experts, y, y_dtype, nullptr, rows, 1, false,
+                     stream);
 }
 
 int rlxq_moe_grouped(rlxq_ctx* ctx, int scheme, int mode, const void* x, int x_dtype, const void* bank,
@@ -141,17 +215,20 @@ int rlxq_moe_grouped(rlxq_ctx* ctx, int scheme, int mode, const void* x, int x_d
   if (!ids) return fail(ctx, RLXQ_E_NULL, "moe_grouped: ids is null");
   if (!is_gguf(scheme)) return fail(ctx, RLXQ_E_SCHEME, "moe_grouped: GGUF schemes only");
   if (rows < 0 || top_k <= 0 || top_k > 64) return fail(ctx, RLXQ_E_SHAPE, "moe_grouped: need 0 < top_k <= 64");
-  if (mode == RLXQ_MOE_EXPAND)
+  if (mode == RLXQ_MOE_EXPAND || mode == RLXQ_MOE_EXPAND_SWIGLU) {
+    const bool sw = mode == RLXQ_MOE_EXPAND_SWIGLU;
+    if (sw && n % 2) return fail(ctx, RLXQ_E_SHAPE, "moe_grouped: EXPAND_SWIGLU needs an even N (gate | up)");
     return grouped_run(ctx, "moe_grouped", scheme, 32, x, x_dtype, bank, nullptr, nullptr, RLXQ_F32, ids, nullptr,
                        rows * top_k, rows, (int32_t)top_k, k, n, num_experts, y, y_dtype, nullptr, rows,
-                       (int32_t)top_k, stream);
+                       (int32_t)top_k, sw, stream);
+  }
   if (mode == RLXQ_MOE_COMBINE) {
     if (!probs) return fail(ctx, RLXQ_E_NULL, "moe_grouped: COMBINE needs probs");
     return grouped_run(ctx, "moe_grouped", scheme, 32, x, x_dtype, bank, nullptr, nullptr, RLXQ_F32, ids, nullptr,
                        rows * top_k, rows * top_k, 1, k, n, num_experts, y, y_dtype, probs, rows, (int32_t)top_k,
-                       stream);
+                       false, stream);
   }
-  return fail(ctx, RLXQ_E_SHAPE, "moe_grouped: mode must be EXPAND or COMBINE");
+  return fail(ctx, RLXQ_E_SHAPE, "moe_grouped: mode must be EXPAND, COMBINE or EXPAND_SWIGLU");
 }
 
 }  // extern "C"

@@ -347,9 +347,9 @@ int rlxq_moe_route(rlxq_ctx* ctx, const float* logits, int64_t rows, int64_t num
   if (!ctx) return RLXQ_E_NULL;
   ctx->last_error.clear();
   if (!logits || !ids || !probs) return fail(ctx, RLXQ_E_NULL, "moe_route: null pointer");
-  if (rows < 0 || num_experts <= 0 || num_experts > 1024 || top_k <= 0 || top_k > num_experts ||
+  if (rows < 0 || num_experts <= 0 || num_experts > 1024 || top_k <= 0 || top_k > num_experts || top_k > 64 ||
       rows > 0x7fffffff)
-    return fail(ctx, RLXQ_E_SHAPE, "moe_route: need 0 < top_k <= num_experts <= 1024");
+    return fail(ctx, RLXQ_E_SHAPE, "moe_route: need 0 < top_k <= min(num_experts, 64), num_experts <= 1024");
   if (rows == 0) return RLXQ_OK;
   DeviceGuard g(ctx->device);
   hipFunction_t fn;

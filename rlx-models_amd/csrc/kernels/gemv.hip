@@ -222,30 +222,6 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
 // of D rows of weight loads in flight.
 // ---------------------------------------------------------------------------
 
-// Plane dwords of one 32-element block from its 16 raw bf16-pair dwords
-// R[i] = (x[2i], x[2i+1]), in the extraction order of plane_pair<SCH>.
-template <int SCH>
-RLXQ_DEV void pairs_from_raw(const uint32_t* R, uint32_t* X) {
-  constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;  // low / high halves of (R[a], R[b])
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    if constexpr (SCH == SCH_MLX4) {
-      // t = 4i+e holds (8i+e, 8i+e+4): R[4i + e/2] and R[4i + 2 + e/2]
-      X[4 * i + 0] = perm_b32(R[4 * i + 2], R[4 * i + 0], LO);
-      X[4 * i + 1] = perm_b32(R[4 * i + 2], R[4 * i + 0], HI);
-      X[4 * i + 2] = perm_b32(R[4 * i + 3], R[4 * i + 1], LO);
-      X[4 * i + 3] = perm_b32(R[4 * i + 3], R[4 * i + 1], HI);
-    } else {
-      // GGUF nibble order: t = 4i + e, e=0 (4i, 4i+2), e=1 (4i+16, 4i+18),
-      // e=2 (4i+1, 4i+3), e=3 (4i+17, 4i+19)
-      X[4 * i + 0] = perm_b32(R[2 * i + 1], R[2 * i], LO);
-      X[4 * i + 2] = perm_b32(R[2 * i + 1], R[2 * i], HI);
-      X[4 * i + 1] = perm_b32(R[2 * i + 9], R[2 * i + 8], LO);
-      X[4 * i + 3] = perm_b32(R[2 * i + 9], R[2 * i + 8], HI);
-    }
-  }
-}
-
 template <int SCH, int NU, int D, int WAVES>
 RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   constexpr int BLOCKS = Unit<SCH>::BLOCKS;

@@ -112,9 +112,59 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_quant_act_i8(
   if (threadIdx.x == 0) scales[r] = s;
 }
 
+namespace rlxq {
+
+// DPP moves within 16-lane rows: xor 1 and xor 2 (quad_perm), the 8-lane half
+// mirror and the 16-lane mirror; after the four, every lane of a row holds
+// the row's reduction.
+#define RLXQ_DPP(v, ctrl) __builtin_amdgcn_mov_dpp((v), (ctrl), 0xF, 0xF, false)
+
+template <typename Op>
+RLXQ_DEV float wave_reduce(float v, Op op) {
+  v = op(v, __int_as_float(RLXQ_DPP(__float_as_int(v), 0xB1)));
+  v = op(v, __int_as_float(RLXQ_DPP(__float_as_int(v), 0x4E)));
+  v = op(v, __int_as_float(RLXQ_DPP(__float_as_int(v), 0x141)));
+  v = op(v, __int_as_float(RLXQ_DPP(__float_as_int(v), 0x140)));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return op(op(r0, r1), op(r2, r3));
+}
+
+// (probability, expert) maximum over the wave: larger probability, then the
+// lower expert id.  The result is the same in every lane.
+RLXQ_DEV void wave_argmax(float& v, int& e) {
+  auto take = [&](float ov, int oe) {
+    if (ov > v || (ov == v && oe < e)) {
+      v = ov;
+      e = oe;
+    }
+  };
+  take(__int_as_float(RLXQ_DPP(__float_as_int(v), 0xB1)), RLXQ_DPP(e, 0xB1));
+  take(__int_as_float(RLXQ_DPP(__float_as_int(v), 0x4E)), RLXQ_DPP(e, 0x4E));
+  take(__int_as_float(RLXQ_DPP(__float_as_int(v), 0x141)), RLXQ_DPP(e, 0x141));
+  take(__int_as_float(RLXQ_DPP(__float_as_int(v), 0x140)), RLXQ_DPP(e, 0x140));
+  float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  int be = __builtin_amdgcn_readlane(e, 0);
+#pragma unroll
+  for (int row = 1; row < 4; row++) {
+    const float ov = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * row));
+    const int oe = __builtin_amdgcn_readlane(e, 16 * row);
+    if (ov > bv || (ov == bv && oe < be)) {
+      bv = ov;
+      be = oe;
+    }
+  }
+  v = bv;
+  e = be;
+}
+
+}  // namespace rlxq
+
 // Router: softmax over E logits then top-k by probability, ties to the lower
 // expert id; optional renormalisation of the kept probabilities.  One wave per
-// row; E <= 1024.
+// row, E <= 1024; the reductions use DPP row moves and readlane.
 extern "C" __global__ __launch_bounds__(64) void rlxq_moe_route_k(
     const float* __restrict__ logits, int64_t rows, int E, int topk, int renorm,
     int32_t* __restrict__ ids, float* __restrict__ probs) {
@@ -123,61 +173,55 @@ extern "C" __global__ __launch_bounds__(64) void rlxq_moe_route_k(
   const int lane = threadIdx.x;
   const float* l = logits + r * E;
   constexpr int MAXE = 1024 / 64;
+  const int nper = (E + 63) / 64;   // experts per lane actually present
   float p[MAXE];
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < MAXE; i++) {
     const int e = lane + 64 * i;
-    p[i] = e < E ? l[e] : -INFINITY;
+    p[i] = (i < nper && e < E) ? l[e] : -INFINITY;
     mx = fmaxf(mx, p[i]);
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  mx = rlxq::wave_reduce(mx, [](float x, float y) { return fmaxf(x, y); });
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXE; i++) {
     const int e = lane + 64 * i;
-    p[i] = e < E ? expf(p[i] - mx) : 0.f;
+    p[i] = (i < nper && e < E) ? expf(p[i] - mx) : 0.f;
     s += p[i];
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  s = rlxq::wave_reduce(s, [](float x, float y) { return x + y; });
 #pragma unroll
   for (int i = 0; i < MAXE; i++) {
     const int e = lane + 64 * i;
-    p[i] = e < E ? p[i] / s : -1.f;
+    p[i] = (i < nper && e < E) ? p[i] / s : -1.f;
   }
-  float kept = 0.f;
+  float kept = 0.f, sel_p = 0.f;
+  int sel_e = 0;
   for (int j = 0; j < topk; j++) {
-    // lane-local best (highest probability, lowest id on ties)
+    // lane-local best (highest probability, lowest id on ties), then the wave's
     float bv = -2.f;
     int be = 0x7fffffff;
 #pragma unroll
     for (int i = 0; i < MAXE; i++) {
       const int e = lane + 64 * i;
-      if (p[i] > bv || (p[i] == bv && e < be)) {
+      if (i < nper && (p[i] > bv || (p[i] == bv && e < be))) {
         bv = p[i];
         be = e;
       }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oe = __shfl_xor(be, off, 64);
-      if (ov > bv || (ov == bv && oe < be)) {
-        bv = ov;
-        be = oe;
-      }
-    }
-    if (lane == 0) {
-      ids[r * topk + j] = be;
-      probs[r * topk + j] = bv;
+    rlxq::wave_argmax(bv, be);
+    if (lane == j) {
+      sel_p = bv;
+      sel_e = be;
     }
     kept += bv;
 #pragma unroll
     for (int i = 0; i < MAXE; i++)
       if (lane + 64 * i == be) p[i] = -1.f;
   }
-  if (renorm && lane == 0)
-    for (int j = 0; j < topk; j++) probs[r * topk + j] = probs[r * topk + j] / kept;
+  if (lane < topk) {
+    ids[r * topk + lane] = sel_e;
+    probs[r * topk + lane] = renorm ? sel_p / kept : sel_p;
+  }
 }

@@ -102,12 +102,34 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_moe_combine_k(const float
 
 namespace rlxq {
 
-// Workgroup (4 waves) = (fired expert slot, tile of TILE weight rows).  The
-// activations of the expert's entries are staged MT at a time; each wave
-// walks RPW rows of the tile, L lanes per row, every lane decoding units
-// li, li+L, ... of the row against the MT staged records.
-template <int SCH, bool XBF16, int L, int MT>
-RLXQ_DEV void moe_gemv_body(const rlxq_moe_gemv_args& a) {
+constexpr int MOE_TILE_MAX = 256;  // most weight rows per workgroup tile
+constexpr int MOE_RING = 4;        // weight units in flight per lane
+
+// Weight row of local tile row lr of tile tn, and whether it exists.  Plain:
+// tile_rows consecutive rows.  SwiGLU: tile_rows/2 gate rows and the
+// matching up rows N/2 further on.
+template <bool SWIGLU>
+RLXQ_DEV int64_t tile_row(const rlxq_moe_gemv_args& a, int tn, int lr, bool& ok) {
+  if constexpr (SWIGLU) {
+    const int H = a.tile_rows / 2;
+    const int64_t half = a.N / 2, c = (int64_t)tn * H + (lr % H);
+    ok = c < half;
+    return lr < H ? c : half + c;
+  } else {
+    const int64_t n = (int64_t)tn * a.tile_rows + lr;
+    ok = n < a.N;
+    return n;
+  }
+}
+
+// One tile of expert e's weight rows against the entries perm[beg .. end)
+// (perm in global or LDS memory).  The activations of MT entries at a time
+// are staged in LDS as records once; the waves then walk the tile's rows,
+// RP rows per pass with L lanes per row, every lane decoding units li,
+// li + L, ... of its row.  The (pass, unit) steps are flattened and the
+// weight units run MOE_RING steps ahead of the arithmetic in a register ring.
+template <int SCH, bool XBF16, int L, int MT, bool SWIGLU>
+RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, int beg, int end, int tn) {
   constexpr bool BIT8 = Unit<SCH>::BIT8;
   constexpr int NPL = XBF16 ? 1 : 2;
   constexpr int RS = Rec<NPL>::STRIDE;
@@ -115,30 +137,43 @@ RLXQ_DEV void moe_gemv_body(const rlxq_moe_gemv_args& a) {
   constexpr int DW = Unit<SCH>::DW;
   constexpr int BYTES = Unit<SCH>::BYTES;
   constexpr int RP = 64 / L;
-  constexpr int TILE = 32;
-  constexpr int RPW = TILE / 4 / RP;  // row passes per wave
+  const int NPASS = a.tile_rows / 4 / RP;  // row passes per wave
+  constexpr int D = MOE_RING;
   constexpr bool MLX = (SCH == SCH_MLX4 || SCH == SCH_MLX8);
   constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || MLX);
   extern __shared__ uint32_t lds[];
-
-  const int slot = blockIdx.x / a.tiles_n, tn = blockIdx.x % a.tiles_n;
-  const int nf = a.table[0];
-  if (slot >= nf) return;
-  const int e = a.table[1 + slot];
-  const int beg = a.table[1 + a.E + slot], end = a.table[1 + a.E + slot + 1];
-  const int32_t* perm = a.table + 2 + 2 * a.E;
+  __shared__ float res[SWIGLU ? MT * MOE_TILE_MAX : 1];
 
   const int K = a.K;
   const int bpr = K >> 5;
   const int U = bpr / BLOCKS;
   const int nchunk = (U + L - 1) / L;
+  const int S = NPASS * nchunk;   // steps per c0 chunk
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane / L, li = lane % L;
   const uint8_t* wbase = a.bank + (int64_t)e * a.N * a.rb;
   const int gpr = MLX ? K / a.group : 0;
   const UnpackK kc = unpack_consts();
 
+  auto step_row = [&](int s, int& lr, int& j) {
+    const int p = s / nchunk;
+    j = s - p * nchunk;
+    lr = (p * 4 + wv) * RP + g;
+  };
+  auto load_step = [&](int s, uint32_t* dw) {
+    int lr, j;
+    step_row(s, lr, j);
+    bool rok;
+    const int64_t n = tile_row<SWIGLU>(a, tn, lr, rok);
+    const int u = li + L * j;
+    load_unit<SCH>(dw, wbase + (rok ? n : 0) * a.rb + (int64_t)(u < U ? u : U - 1) * BYTES);
+  };
+
   for (int c0 = beg; c0 < end; c0 += MT) {
+    uint32_t ring[D][DW];
+#pragma unroll
+    for (int d = 0; d < D - 1; d++)
+      if (d < S) load_step(d, ring[d]);
     // stage the activation rows of entries c0 .. c0+MT-1
     for (int m = 0; m < MT; m++) {
       const int ent = c0 + m < end ? perm[c0 + m] : -1;
@@ -151,60 +186,86 @@ RLXQ_DEV void moe_gemv_body(const rlxq_moe_gemv_args& a) {
       }
     }
     __syncthreads();
-    for (int rp = 0; rp < RPW; rp++) {
-      const int64_t n = (int64_t)tn * TILE + (wv * RPW + rp) * RP + g;
-      const bool rok = n < a.N;
-      const int64_t nn = rok ? n : 0;
-      const uint8_t* rowp = wbase + nn * a.rb;
-      float acc[MT];
+    float acc[MT];
+    for (int s0 = 0; s0 < S; s0 += D) {
 #pragma unroll
-      for (int m = 0; m < MT; m++) acc[m] = 0.f;
-      for (int j = 0; j < nchunk; j++) {
-        const int u = li + L * j;
-        const bool uok = u < U;
-        const int uc = uok ? u : U - 1;
-        uint32_t dw[DW];
-        load_unit<SCH>(dw, rowp + (int64_t)uc * BYTES);
+      for (int d = 0; d < D; d++) {
+        const int s = s0 + d;
+        if (s + D - 1 < S) load_step(s + D - 1, ring[(d + D - 1) % D]);
+        if (s < S) {
+          int lr, j;
+          step_row(s, lr, j);
+          bool rok;
+          const int64_t n = tile_row<SWIGLU>(a, tn, lr, rok);
+          const int64_t nn = rok ? n : 0;
+          const int u = li + L * j;
+          const bool uok = u < U;
+          const int uc = uok ? u : U - 1;
+          if (j == 0) {
 #pragma unroll
-        for (int bl = 0; bl < BLOCKS; bl++) {
-          float d, mn;
-          if constexpr (MLX) {
-            const int64_t gi = ((int64_t)e * a.N + nn) * gpr + ((uc * BLOCKS + bl) * 32) / a.group;
-            d = load_sb(a.scales, gi, a.sb_bf16 != 0);
-            mn = load_sb(a.biases, gi, a.sb_bf16 != 0);
-          } else {
-            block_scales<SCH>(dw, bl, d, mn);
+            for (int m = 0; m < MT; m++) acc[m] = 0.f;
           }
-          if (!(rok && uok)) {
-            d = 0.f;
-            mn = 0.f;
-          }
-          uint32_t pw[16];
-          block_pairs<SCH>(dw, bl, pw, kc);
-          const int b = uc * BLOCKS + bl;
 #pragma unroll
-          for (int m = 0; m < MT; m++) {
-            const uint32_t* xr = lds + (size_t)(m * bpr + b) * RS;
-            uint32_t xrec[RS];
-#pragma unroll
-            for (int q = 0; q < RS; q += 4) {
-              const uint4 v = *reinterpret_cast<const uint4*>(xr + q);
-              xrec[q] = v.x; xrec[q + 1] = v.y; xrec[q + 2] = v.z; xrec[q + 3] = v.w;
+          for (int bl = 0; bl < BLOCKS; bl++) {
+            float dd, mn;
+            if constexpr (MLX) {
+              const int64_t gi = ((int64_t)e * a.N + nn) * gpr + ((uc * BLOCKS + bl) * 32) / a.group;
+              dd = load_sb(a.scales, gi, a.sb_bf16 != 0);
+              mn = load_sb(a.biases, gi, a.sb_bf16 != 0);
+            } else {
+              block_scales<SCH>(ring[d], bl, dd, mn);
             }
-            const float cc = block_dot<SCH, NPL>(pw, xrec);
-            const float scl = __uint_as_float(xrec[NPL * 16 + 2]);
-            acc[m] = fmaf(BIT8 ? d * scl : d, cc, acc[m]);
-            if constexpr (HAS_MIN) acc[m] = fmaf(mn, __uint_as_float(xrec[NPL * 16 + 1]), acc[m]);
+            if (!(rok && uok)) {
+              dd = 0.f;
+              mn = 0.f;
+            }
+            uint32_t pw[16];
+            block_pairs<SCH>(ring[d], bl, pw, kc);
+            const int b = uc * BLOCKS + bl;
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+              const uint32_t* xr = lds + (size_t)(m * bpr + b) * RS;
+              uint32_t xrec[RS];
+#pragma unroll
+              for (int q = 0; q < RS; q += 4) {
+                const uint4 v = *reinterpret_cast<const uint4*>(xr + q);
+                xrec[q] = v.x; xrec[q + 1] = v.y; xrec[q + 2] = v.z; xrec[q + 3] = v.w;
+              }
+              const float cc = block_dot<SCH, NPL>(pw, xrec);
+              const float scl = __uint_as_float(xrec[NPL * 16 + 2]);
+              acc[m] = fmaf(BIT8 ? dd * scl : dd, cc, acc[m]);
+              if constexpr (HAS_MIN) acc[m] = fmaf(mn, __uint_as_float(xrec[NPL * 16 + 1]), acc[m]);
+            }
+          }
+          if (j == nchunk - 1) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+              const float v = lane_group_sum<L>(acc[m]);
+              if constexpr (SWIGLU) {
+                if (li == 0) res[m * MOE_TILE_MAX + lr] = v;
+              } else if (li == 0 && rok && c0 + m < end) {
+                const int64_t off = (int64_t)perm[c0 + m] * a.y_ld + n;
+                if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v);
+                else reinterpret_cast<float*>(a.y)[off] = v;
+              }
+            }
           }
         }
       }
-#pragma unroll
-      for (int m = 0; m < MT; m++) {
-        const float v = lane_group_sum<L>(acc[m]);
-        if (li == 0 && rok && c0 + m < end) {
-          const int64_t off = (int64_t)perm[c0 + m] * a.y_ld + n;
-          if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v);
-          else reinterpret_cast<float*>(a.y)[off] = v;
+    }
+    if constexpr (SWIGLU) {
+      // out = silu(g) * u = g / (1 + exp(-g)) * u, the GroupedSwiglu rule
+      const int H = a.tile_rows / 2;
+      __syncthreads();
+      for (int t = threadIdx.x; t < MT * H; t += blockDim.x) {
+        const int m = t / H, c = t % H;
+        const int64_t col = (int64_t)tn * H + c;
+        if (c0 + m < end && col < a.N / 2) {
+          const float gv = res[m * MOE_TILE_MAX + c], uv = res[m * MOE_TILE_MAX + H + c];
+          const float o = gv / (1.f + expf(-gv)) * uv;
+          const int64_t off = (int64_t)perm[c0 + m] * a.y_ld + col;
+          if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(o);
+          else reinterpret_cast<float*>(a.y)[off] = o;
         }
       }
     }
@@ -212,19 +273,332 @@ RLXQ_DEV void moe_gemv_body(const rlxq_moe_gemv_args& a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Register-activation tile (4-bit codes, bf16 activations).  Lane li of an
+// L-lane group owns units li + L c (c < NU) of every row of the expert, so it
+// needs only the activations of those units: it loads the bf16 values of the
+// MT entries being served straight from global memory and builds their
+// pairs (in the code-extraction order) and block sums in registers.  There
+// is no LDS stage and no barrier.  The nw waves given to an expert take its
+// output columns (a row, or a gate/up row pair for SwiGLU) in a stride of
+// RP * nw, with D column steps of weight loads in flight.
+// ---------------------------------------------------------------------------
+template <int SCH, int L, int NU, int MT, int D, bool SWIGLU>
+RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, int beg, int end, int wq,
+                          int nw) {
+  constexpr int BLOCKS = Unit<SCH>::BLOCKS;
+  constexpr int DW = Unit<SCH>::DW;
+  constexpr int BYTES = Unit<SCH>::BYTES;
+  constexpr int RP = 64 / L;
+  constexpr int R2 = SWIGLU ? 2 : 1;
+  constexpr bool MLX = SCH == SCH_MLX4;
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || MLX);
+  static_assert(!Unit<SCH>::BIT8, "register activations serve 4-bit codes");
+
+  const int K = a.K;
+  const int U = (K >> 5) / BLOCKS;
+  const int lane = threadIdx.x & 63, g = lane / L, li = lane % L;
+  const int64_t width = SWIGLU ? a.N / 2 : a.N;
+  const uint8_t* wbase = a.bank + (int64_t)e * a.N * a.rb;
+  const int gpr = MLX ? K / a.group : 0;
+  const int64_t cstride = (int64_t)nw * RP;
+
+  int uc[NU];
+  bool uok[NU];
+#pragma unroll
+  for (int c = 0; c < NU; c++) {
+    const int u = li + L * c;
+    uok[c] = u < U;
+    uc[c] = uok[c] ? u : U - 1;
+  }
+
+  struct Buf {
+    uint32_t dw[R2][NU][DW];
+    float sm[R2][NU], bm[R2][NU];
+  };
+  // rows of output column col: col (and width + col, the up row, for SwiGLU)
+  auto load = [&](int64_t col, Buf& bf) {
+    const int64_t cc = col < width ? col : 0;
+#pragma unroll
+    for (int r = 0; r < R2; r++) {
+      const int64_t n = r == 0 ? cc : width + cc;
+      const uint8_t* rp = wbase + n * a.rb;
+#pragma unroll
+      for (int c = 0; c < NU; c++) {
+        load_unit<SCH>(bf.dw[r][c], rp + (int64_t)uc[c] * BYTES);
+        if constexpr (MLX) {
+          const int64_t gi = ((int64_t)e * a.N + n) * gpr + (uc[c] * 32) / a.group;
+          bf.sm[r][c] = load_sb(a.scales, gi, a.sb_bf16 != 0);
+          bf.bm[r][c] = load_sb(a.biases, gi, a.sb_bf16 != 0);
+        }
+      }
+    }
+  };
+
+  const UnpackK kc = unpack_consts();
+  const int64_t base = (int64_t)wq * RP;  // the wave's first column (wave-uniform)
+  for (int c0 = beg; c0 < end; c0 += MT) {
+    Buf ring[D];
+#pragma unroll
+    for (int i = 0; i < D; i++) load(base + i * cstride + g, ring[i]);
+
+    // activations of the MT entries: pairs and block sums of my units
+    int ent[MT];
+    uint32_t X[MT][NU][BLOCKS][16];
+    float S[MT][NU][BLOCKS];
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+      ent[m] = c0 + m < end ? perm[c0 + m] : -1;
+      const int64_t xrow = ent[m] >= 0 ? ent[m] / a.x_div : 0;
+      const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x) + xrow * a.x_ld;
+#pragma unroll
+      for (int c = 0; c < NU; c++)
+#pragma unroll
+        for (int bl = 0; bl < BLOCKS; bl++) {
+          const uint4* p = reinterpret_cast<const uint4*>(xb + (int64_t)(uc[c] * BLOCKS + bl) * 32);
+          uint32_t R[16];
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const uint4 v = p[q];
+            const bool live = ent[m] >= 0;
+            R[4 * q] = live ? v.x : 0u;
+            R[4 * q + 1] = live ? v.y : 0u;
+            R[4 * q + 2] = live ? v.z : 0u;
+            R[4 * q + 3] = live ? v.w : 0u;
+          }
+          float sum = 0.f;
+#pragma unroll
+          for (int t = 0; t < 16; t++) sum = dot2_bf16(R[t], 0x3F803F80u, sum);
+          S[m][c][bl] = sum;
+          pairs_from_raw<SCH>(R, X[m][c][bl]);
+        }
+    }
+
+    int64_t col = base;
+    while (col < width) {
+#pragma unroll
+      for (int i = 0; i < D; i++) {
+        if (col < width) {
+          float acc[R2][MT];
+#pragma unroll
+          for (int r = 0; r < R2; r++)
+#pragma unroll
+            for (int m = 0; m < MT; m++) acc[r][m] = 0.f;
+#pragma unroll
+          for (int r = 0; r < R2; r++)
+#pragma unroll
+            for (int c = 0; c < NU; c++)
+#pragma unroll
+              for (int bl = 0; bl < BLOCKS; bl++) {
+                float d, mn;
+                if constexpr (MLX) {
+                  d = ring[i].sm[r][c];
+                  mn = ring[i].bm[r][c];
+                } else {
+                  block_scales<SCH>(ring[i].dw[r][c], bl, d, mn);
+                }
+                if (!uok[c]) {
+                  d = 0.f;
+                  mn = 0.f;
+                }
+                uint32_t pw[16];
+                block_pairs<SCH>(ring[i].dw[r][c], bl, pw, kc);
+#pragma unroll
+                for (int m = 0; m < MT; m++) {
+                  float ch = -chain_bias<SCH>() * S[m][c][bl];
+#pragma unroll
+                  for (int t = 0; t < 16; t++) ch = dot2_bf16(pw[t], X[m][c][bl][t], ch);
+                  acc[r][m] = fmaf(d, ch, acc[r][m]);
+                  if constexpr (HAS_MIN) acc[r][m] = fmaf(mn, S[m][c][bl], acc[r][m]);
+                }
+              }
+          float v[R2][MT];
+#pragma unroll
+          for (int r = 0; r < R2; r++)
+#pragma unroll
+            for (int m = 0; m < MT; m++) v[r][m] = lane_group_sum<L>(acc[r][m]);
+          const int64_t nl = col + (int64_t)D * cstride;
+          if (nl < width) load(nl + g, ring[i]);
+          const int64_t mycol = col + g;
+          if (li == 0 && mycol < width) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+              if (ent[m] >= 0) {
+                float o = v[0][m];
+                if constexpr (SWIGLU) o = o / (1.f + expf(-o)) * v[1][m];  // silu(g) * u
+                const int64_t off = (int64_t)ent[m] * a.y_ld + mycol;
+                if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(o);
+                else reinterpret_cast<float*>(a.y)[off] = o;
+              }
+            }
+          }
+          col += cstride;
+        }
+      }
+    }
+  }
+}
+
+// Table-driven: workgroup = (fired expert slot, tile); work(e, perm, beg,
+// end, tn) serves entries perm[beg .. end) of expert e.
+template <class Work>
+RLXQ_DEV void table_dispatch(const rlxq_moe_gemv_args& a, Work work) {
+  const int slot = blockIdx.x / a.tiles_n, tn = blockIdx.x % a.tiles_n;
+  const int nf = a.table[0];
+  if (slot >= nf) return;
+  const int e = a.table[1 + slot];
+  const int beg = a.table[1 + a.E + slot], end = a.table[1 + a.E + slot + 1];
+  work(e, a.table + 2 + 2 * a.E, beg, end, tn);
+}
+
+// Expert of entry i of the id list (int32 ids or f32 indices), -1 if invalid.
+RLXQ_DEV int entry_expert(const rlxq_moe_gemv_args& a, int i) {
+  if (a.ids) {
+    const int32_t v = a.ids[i];
+    return (v >= 0 && v < a.E) ? v : -1;
+  }
+  const float f = a.idx_f32[i];
+  return (!(f >= 0.f) || f >= (float)a.E || (float)(int)f != f) ? -1 : (int)f;
+}
+
+// Exclusive sum over the 256 threads of v (every thread gets its prefix and
+// the total).  ws: 4 ints of LDS not in use by other threads.
+RLXQ_DEV int block_exclusive_sum(int v, int32_t* ws, int& total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += o;
+  }
+  if (lane == 63) ws[wv] = inc;
+  __syncthreads();
+  int base = 0;
+#pragma unroll
+  for (int w = 0; w < 4; w++) base += w < wv ? ws[w] : 0;
+  total = ws[0] + ws[1] + ws[2] + ws[3];
+  return base + inc - v;
+}
+
+// Routing in the workgroup, balanced over experts: the entries of each expert
+// (in increasing order) are cut into chunks of MT, and workgroup = (chunk,
+// tile) over the chunks of all experts in expert order, so that every
+// workgroup serves at most MT entries of one expert whatever the skew.
+// Chunk number C (the count of chunks; the grid always holds it) zeroes the
+// output rows of invalid entries, its tiles splitting the rows.  Chunks past
+// C exit.  E <= 1024, n_entries <= 1024, 256 threads.
+template <int MT, class Work>
+RLXQ_DEV void balanced_dispatch(const rlxq_moe_gemv_args& a, Work work) {
+  __shared__ int32_t cnt[1024];
+  __shared__ int32_t ent[1024];
+  __shared__ int32_t ws0[4], ws1[4], pick[2];
+  const int chunk = blockIdx.x / a.tiles_n, tn = blockIdx.x % a.tiles_n;
+  const int t = threadIdx.x;
+  const int E = a.E;
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+    if (4 * t + q < E) cnt[4 * t + q] = 0;
+  if (t == 0) {
+    pick[0] = -1;
+    pick[1] = 0;
+  }
+  __syncthreads();
+  int ex[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int i = 4 * t + q;
+    ex[q] = i < a.n_entries ? entry_expert(a, i) : -2;
+    if (ex[q] >= 0) atomicAdd(&cnt[ex[q]], 1);
+  }
+  __syncthreads();
+  // chunk offsets: exclusive sum of ceil(count / MT) over the experts
+  int c4[4], s = 0;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int e = 4 * t + q;
+    c4[q] = e < E ? (cnt[e] + MT - 1) / MT : 0;
+    s += c4[q];
+  }
+  int nchunks;
+  int off = block_exclusive_sum(s, ws0, nchunks);
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    if (chunk >= off && chunk < off + c4[q]) {
+      pick[0] = 4 * t + q;
+      pick[1] = chunk - off;
+    }
+    off += c4[q];
+  }
+  if (t == 0 && chunk == nchunks) pick[0] = E;
+  __syncthreads();
+  const int e = pick[0], j = pick[1];
+  if (e < 0) return;
+  // entries of e (e == E: the invalid ones) in increasing order
+  int mine[4], c = 0;
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+    if (ex[q] == e || (e == E && ex[q] == -1)) mine[c++] = 4 * t + q;
+  int total;
+  const int first = block_exclusive_sum(c, ws1, total);
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+    if (q < c) ent[first + q] = mine[q];
+  __syncthreads();
+  if (e == E) {
+    const int64_t width = a.swiglu ? a.N / 2 : a.N;
+    for (int64_t idx = (int64_t)tn * blockDim.x + t; idx < (int64_t)total * width;
+         idx += (int64_t)blockDim.x * a.tiles_n) {
+      const int64_t o = (int64_t)ent[idx / width] * a.y_ld + idx % width;
+      if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[o] = 0;
+      else reinterpret_cast<float*>(a.y)[o] = 0.f;
+    }
+    return;
+  }
+  const int beg = j * MT;
+  work(e, ent, beg, beg + MT < total ? beg + MT : total, tn);
+}
+
+template <int SCH, bool XBF16, int L, int MT, bool SWIGLU, bool FUSED>
+RLXQ_DEV void moe_gemv_body(const rlxq_moe_gemv_args& a) {
+  auto work = [&](int e, const int32_t* perm, int beg, int end, int tn) {
+    moe_tile<SCH, XBF16, L, MT, SWIGLU>(a, e, perm, beg, end, tn);
+  };
+  if constexpr (FUSED) balanced_dispatch<MT>(a, work);
+  else table_dispatch(a, work);
+}
+
+template <int SCH, int L, int NU, int MT, int D, bool SWIGLU, bool FUSED>
+RLXQ_DEV void moe_xr_body(const rlxq_moe_gemv_args& a) {
+  auto work = [&](int e, const int32_t* perm, int beg, int end, int tn) {
+    moe_xr_wave<SCH, L, NU, MT, D, SWIGLU>(a, e, perm, beg, end, tn * 4 + (int)(threadIdx.x >> 6), a.tiles_n * 4);
+  };
+  if constexpr (FUSED) balanced_dispatch<MT>(a, work);
+  else table_dispatch(a, work);
+}
+
 }  // namespace rlxq
 
-#define RLXQ_MOE_INST(NAME, SCH, XBF, L, MT)                                           \
+#define RLXQ_MOE_INST(NAME, SCH, XBF, L, MT, SW)                                        \
   extern "C" __global__ __launch_bounds__(256) void NAME(rlxq_moe_gemv_args a) {      \
-    rlxq::moe_gemv_body<SCH, XBF, L, MT>(a);                                            \
+    rlxq::moe_gemv_body<SCH, XBF, L, MT, SW, false>(a);                                 \
   }
-#define RLXQ_MOE_X(SNAME, SCH, XN, XBF)                                          \
-  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L64_M1, SCH, XBF, 64, 1)         \
-  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L64_M2, SCH, XBF, 64, 2)         \
-  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L64_M4, SCH, XBF, 64, 4)         \
-  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L8_M1, SCH, XBF, 8, 1)           \
-  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L8_M2, SCH, XBF, 8, 2)           \
-  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L8_M4, SCH, XBF, 8, 4)
+#define RLXQ_MOEF_INST(NAME, SCH, XBF, L, MT, SW)                                       \
+  extern "C" __global__ __launch_bounds__(256) void NAME(rlxq_moe_gemv_args a) {      \
+    rlxq::moe_gemv_body<SCH, XBF, L, MT, SW, true>(a);                                  \
+  }
+#define RLXQ_MOE_X(SNAME, SCH, XN, XBF)                                                   \
+  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L64_M1, SCH, XBF, 64, 1, false)           \
+  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L64_M2, SCH, XBF, 64, 2, false)           \
+  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L64_M4, SCH, XBF, 64, 4, false)           \
+  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L8_M1, SCH, XBF, 8, 1, false)             \
+  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L8_M2, SCH, XBF, 8, 2, false)             \
+  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L8_M4, SCH, XBF, 8, 4, false)             \
+  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L64_M2_sw, SCH, XBF, 64, 2, true)         \
+  RLXQ_MOE_INST(rlxq_moe_gemv_##SNAME##_##XN##_L8_M2_sw, SCH, XBF, 8, 2, true)           \
+  RLXQ_MOEF_INST(rlxq_moe_gemvf_##SNAME##_##XN##_L64_M2, SCH, XBF, 64, 2, false)         \
+  RLXQ_MOEF_INST(rlxq_moe_gemvf_##SNAME##_##XN##_L8_M2, SCH, XBF, 8, 2, false)           \
+  RLXQ_MOEF_INST(rlxq_moe_gemvf_##SNAME##_##XN##_L64_M2_sw, SCH, XBF, 64, 2, true)       \
+  RLXQ_MOEF_INST(rlxq_moe_gemvf_##SNAME##_##XN##_L8_M2_sw, SCH, XBF, 8, 2, true)
 #define RLXQ_MOE_SCHEME(SNAME, SCH) \
   RLXQ_MOE_X(SNAME, SCH, bf16, true) \
   RLXQ_MOE_X(SNAME, SCH, f32, false)
@@ -234,3 +608,45 @@ RLXQ_MOE_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_MOE_SCHEME(q8_0, SCH_Q8_0)
 RLXQ_MOE_SCHEME(mlx4, SCH_MLX4)
 RLXQ_MOE_SCHEME(mlx8, SCH_MLX8)
+
+// Register-activation variants (4-bit codes, bf16 activations):
+// rlxq_moexr[f]_<scheme>_L<L>_U<NU>_M<MT>[_sw]; f = routing in the workgroup.
+// The ring depth D shrinks as the units per lane grow.
+#define RLXQ_MOEXR_INST(NAME, SCH, L, NU, MT, D, SW, F)                                \
+  extern "C" __global__ __launch_bounds__(256) void NAME(rlxq_moe_gemv_args a) {      \
+    rlxq::moe_xr_body<SCH, L, NU, MT, D, SW, F>(a);                                     \
+  }
+#define RLXQ_MOEXR_LU(SNAME, SCH, L, NU, MT, D)                                                       \
+  RLXQ_MOEXR_INST(rlxq_moexr_##SNAME##_L##L##_U##NU##_M##MT, SCH, L, NU, MT, D, false, false)        \
+  RLXQ_MOEXR_INST(rlxq_moexr_##SNAME##_L##L##_U##NU##_M##MT##_sw, SCH, L, NU, MT, D, true, false)    \
+  RLXQ_MOEXR_INST(rlxq_moexrf_##SNAME##_L##L##_U##NU##_M##MT, SCH, L, NU, MT, D, false, true)        \
+  RLXQ_MOEXR_INST(rlxq_moexrf_##SNAME##_L##L##_U##NU##_M##MT##_sw, SCH, L, NU, MT, D, true, true)
+#define RLXQ_MOEXR_SCHEME(SNAME, SCH)        \
+  RLXQ_MOEXR_LU(SNAME, SCH, 64, 1, 1, 4)     \
+  RLXQ_MOEXR_LU(SNAME, SCH, 64, 1, 2, 4)     \
+  RLXQ_MOEXR_LU(SNAME, SCH, 64, 1, 4, 4)     \
+  RLXQ_MOEXR_LU(SNAME, SCH, 64, 2, 1, 2)     \
+  RLXQ_MOEXR_LU(SNAME, SCH, 64, 2, 2, 2)     \
+  RLXQ_MOEXR_LU(SNAME, SCH, 64, 2, 4, 2)     \
+  RLXQ_MOEXR_LU(SNAME, SCH, 64, 4, 1, 1)     \
+  RLXQ_MOEXR_LU(SNAME, SCH, 64, 4, 2, 1)     \
+  RLXQ_MOEXR_LU(SNAME, SCH, 8, 1, 1, 4)      \
+  RLXQ_MOEXR_LU(SNAME, SCH, 8, 1, 2, 4)      \
+  RLXQ_MOEXR_LU(SNAME, SCH, 8, 1, 4, 4)      \
+  RLXQ_MOEXR_LU(SNAME, SCH, 8, 2, 1, 2)      \
+  RLXQ_MOEXR_LU(SNAME, SCH, 8, 2, 2, 2)      \
+  RLXQ_MOEXR_LU(SNAME, SCH, 8, 2, 4, 2)      \
+  RLXQ_MOEXR_LU(SNAME, SCH, 8, 3, 1, 2)      \
+  RLXQ_MOEXR_LU(SNAME, SCH, 8, 3, 2, 2)      \
+  RLXQ_MOEXR_LU(SNAME, SCH, 8, 4, 1, 1)      \
+  RLXQ_MOEXR_LU(SNAME, SCH, 8, 4, 2, 1)
+RLXQ_MOEXR_SCHEME(q4_1, SCH_Q4_1)
+RLXQ_MOEXR_SCHEME(mlx4, SCH_MLX4)
+// Q4_0 units hold two blocks: at most four blocks of activations per lane
+// and entry (NU * MT <= 2).
+RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 64, 1, 1, 4)
+RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 64, 1, 2, 4)
+RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 64, 2, 1, 2)
+RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 8, 1, 1, 4)
+RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 8, 1, 2, 4)
+RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 8, 2, 1, 2)

@@ -30,7 +30,15 @@ typedef struct rlxq_moe_gemv_args {
   int32_t K, E, group, sb_bf16, y_bf16;
   int32_t x_div;          /* activation row of entry = entry / x_div      */
   int32_t tiles_n;        /* row tiles per expert                         */
-  int32_t pad;
+  int32_t tile_rows;      /* weight rows per tile: 64, 128, 192 or 256    */
+  int32_t swiglu;         /* 1: rows [0, N/2) gate, [N/2, N) up; y [entries, N/2]
+                             = silu(x.Wg^T) * (x.Wu^T)                     */
+  /* routing built in each workgroup (small entry counts): expert of each of
+   * the n_entries entries as int32 ids or f32 indices (one of them); the
+   * table above is then unused                                             */
+  const int32_t* ids;
+  const float* idx_f32;
+  int32_t n_entries;
 } rlxq_moe_gemv_args;
 
 #endif

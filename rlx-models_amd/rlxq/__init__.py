@@ -16,7 +16,7 @@ HEADER = PKG.parent / "include" / "rlxq.h"
 
 GGUF_Q8_0, GGUF_Q4_0, GGUF_Q4_1, MLX_AFFINE4, MLX_AFFINE8, INT8_BLOCK = 1, 2, 3, 4, 5, 6
 F32, BF16 = 0, 1
-MOE_EXPAND, MOE_COMBINE = 0, 1
+MOE_EXPAND, MOE_COMBINE, MOE_EXPAND_SWIGLU = 0, 1, 2
 OK = 0
 E_NULL, E_SHAPE, E_SCHEME, E_ALIGN, E_DTYPE, E_HIP, E_NOMEM, E_INDEX, E_NOKERNEL, E_DEVICE = range(-1, -11, -1)
 
@@ -182,9 +182,10 @@ class Context:
 
         rows, top_k = ids.shape
         k = x.shape[1]
-        out_rows = rows * top_k if mode == MOE_EXPAND else rows
+        out_rows = rows if mode == MOE_COMBINE else rows * top_k
+        width = n // 2 if mode == MOE_EXPAND_SWIGLU else n
         if y is None:
-            y = torch.empty((out_rows, n), dtype=y_dtype or torch.float32, device=x.device)
+            y = torch.empty((out_rows, width), dtype=y_dtype or torch.float32, device=x.device)
         rc = lib().rlxq_moe_grouped(self.h, scheme, mode, _ptr(x), _dt(x), _ptr(bank), _ptr(ids), _ptr(probs),
                                     rows, top_k, k, n, num_experts, _ptr(y), _dt(y), _stream(stream))
         self._check(rc, "moe_grouped")

@@ -228,3 +228,201 @@ def test_device_matmul_grouped_session(orc):
         dm.grouped_matmul(x, packed, idx[:5], m, k, n, E, rlxq.GGUF_Q8_0)
     assert e.value.status == rlxq.E_SHAPE and "expert_idx len" in str(e.value)
     dm.close()
+
+
+# ------------------------------------------------- routing variants and SwiGLU
+@pytest.mark.parametrize("route", ["table", "fused"])
+@pytest.mark.parametrize("scheme", [1, 3])
+def test_grouped_both_routings(ctx, orc, monkeypatch, route, scheme):
+    """The device routing table and the in-workgroup routing give the same
+    rows, including skewed experts and invalid indices (zero rows)."""
+    import torch
+
+    monkeypatch.setenv("RLXQ_MOE_ROUTE", route)
+    rows, k, n, E = 45, 640, 200, 9
+    announce(f"grouped routing={route} scheme={scheme}")
+    rng = np.random.default_rng(30 + scheme)
+    packed = orc.synth(scheme, rng, E * n, k)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    idx = rng.integers(0, E, rows).astype(np.float32)
+    idx[::7] = 3            # a crowded expert
+    idx[5], idx[11], idx[20] = -1, 2.5, E   # invalid indices
+    y = ctx.grouped_matmul(_t(x), _t(packed), _t(idx), scheme, n, E)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    for r in (5, 11, 20):
+        assert np.all(got[r] == 0.0)
+    ok = np.array([r not in (5, 11, 20) for r in range(rows)])
+    want = orc.grouped_matmul_f64(scheme, x[ok], packed, idx[ok], n, E)
+    assert rel_err(got[ok], want) <= TOL
+
+
+@pytest.mark.parametrize("route", ["table", "fused"])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_moe_expand_swiglu(ctx, orc, monkeypatch, route, xdt):
+    """EXPAND_SWIGLU: y = silu(x.Wg) * (x.Wu) per (token, slot), against the
+    float64 chain (grouped products, then g / (1 + e^-g) * u)."""
+    import torch
+    import rlxq
+
+    monkeypatch.setenv("RLXQ_MOE_ROUTE", route)
+    T, H, I, E, TOPK = 7, 512, 96, 12, 3
+    announce(f"moe expand swiglu route={route} x={xdt}")
+    rng = np.random.default_rng(41)
+    gate_up = orc.synth_q4_1(rng, E * 2 * I, H)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    xt = _t(x) if xdt == "f32" else _t(x).to(torch.bfloat16)
+    xv = xt.float().cpu().numpy()
+    ids, probs = ctx.moe_route(_t(logits), TOPK, True)
+    act = ctx.moe_grouped(xt, _t(gate_up), ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_EXPAND_SWIGLU, 2 * I, E)
+    torch.cuda.synchronize()
+    assert act.shape == (T * TOPK, I)
+    flat = ids.cpu().numpy().ravel().astype(np.float32)
+    gu = orc.grouped_matmul_f64(3, np.repeat(xv, TOPK, axis=0), gate_up, flat, 2 * I, E)
+    g, u = gu[:, :I], gu[:, I:]
+    assert rel_err(act.cpu().numpy(), g / (1.0 + np.exp(-g)) * u) <= TOL
+
+
+def test_moe_ffn_config5_fused_swiglu(ctx, orc):
+    """Config 5 with the fused gate|up + SwiGLU launch: route, EXPAND_SWIGLU,
+    COMBINE (three launches) against the float64 chain."""
+    import torch
+    import rlxq
+
+    T, H, I, E, TOPK = 16, 2048, 768, 128, 8
+    announce("moe ffn config 5 fused swiglu")
+    rng = np.random.default_rng(0)
+    gate_up = orc.synth_q4_1(rng, E * 2 * I, H)
+    down = orc.synth_q4_1(rng, E * H, I)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    xt = _t(x).to(torch.bfloat16)
+    xv = xt.float().cpu().numpy()
+    ids, probs = ctx.moe_route(_t(logits), TOPK, True)
+    act = ctx.moe_grouped(xt, _t(gate_up), ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_EXPAND_SWIGLU, 2 * I, E,
+                          y_dtype=torch.bfloat16)
+    y = ctx.moe_grouped(act, _t(down), ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_COMBINE, H, E)
+    torch.cuda.synchronize()
+    oids = ids.cpu().numpy().ravel().astype(np.float32)
+    gu = orc.grouped_matmul_f64(3, np.repeat(xv, TOPK, axis=0), gate_up, oids, 2 * I, E)
+    g, u = gu[:, :I], gu[:, I:]
+    assert rel_err(act.float().cpu().numpy(), g / (1.0 + np.exp(-g)) * u) <= 1e-2   # bf16 output
+    act_v = act.float().cpu().numpy()
+    dn = orc.grouped_matmul_f64(3, act_v, down, oids, H, E)
+    pv = probs.cpu().numpy()
+    want = np.zeros((T, H))
+    for r in range(T):
+        for j in range(TOPK):
+            want[r] += pv[r, j] * dn[r * TOPK + j]
+    assert rel_err(y.cpu().numpy(), want) <= TOL
+
+
+# (k, lane-group shape the register path picks for Q4_1: L lanes x NU units)
+XR_SHAPES = [(96, "L8_U1"), (512, "L8_U2"), (768, "L8_U3"), (1024, "L8_U4"), (2048, "L64_U1"),
+             (2560, "L64_U2"), (8192, "L64_U4")]
+
+
+@pytest.mark.parametrize("mt", ["1", "2", "4"])
+@pytest.mark.parametrize("route", ["table", "fused"])
+@pytest.mark.parametrize("k,shape", XR_SHAPES, ids=[str(k) for k, _ in XR_SHAPES])
+def test_grouped_register_path(ctx, orc, monkeypatch, k, shape, route, mt):
+    """Register-activation kernels (Q4_1, bf16 activations): every lane-group
+    shape, both routings, 1/2/4 entries per weight pass, a crowded expert
+    (several passes) and invalid indices (zero rows)."""
+    import torch
+
+    monkeypatch.setenv("RLXQ_MOE_ROUTE", route)
+    monkeypatch.setenv("RLXQ_MOE_MT", mt)
+    rows, n, E = 23, 136, 6
+    announce(f"grouped register path k={k} route={route} mt={mt}")
+    rng = np.random.default_rng(k + int(mt))
+    packed = orc.synth_q4_1(rng, E * n, k)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    idx = rng.integers(0, E, rows).astype(np.float32)
+    idx[::4] = 2
+    idx[3], idx[9] = -1, E
+    xt = _t(x).to(torch.bfloat16)
+    y = ctx.grouped_matmul(xt, _t(packed), _t(idx), 3, n, E)
+    torch.cuda.synchronize()
+    assert shape in ctx.last_kernel and "moexr" in ctx.last_kernel
+    got = y.cpu().numpy()
+    assert np.all(got[3] == 0.0) and np.all(got[9] == 0.0)
+    ok = np.array([r not in (3, 9) for r in range(rows)])
+    want = orc.grouped_matmul_f64(3, xt.float().cpu().numpy()[ok], packed, idx[ok], n, E)
+    assert rel_err(got[ok], want) <= TOL
+
+
+@pytest.mark.parametrize("route", ["table", "fused"])
+def test_register_path_matches_lds_path(ctx, orc, monkeypatch, route):
+    """EXPAND_SWIGLU over config-5-like shapes: the register-activation and
+    the LDS-record kernels agree within the bar."""
+    import torch
+    import rlxq
+
+    monkeypatch.setenv("RLXQ_MOE_ROUTE", route)
+    T, H, I, E, TOPK = 16, 2048, 768, 64, 8
+    announce(f"register vs lds route={route}")
+    rng = np.random.default_rng(5)
+    gate_up = _t(orc.synth_q4_1(rng, E * 2 * I, H))
+    xt = _t(rng.standard_normal((T, H)).astype(np.float32)).to(torch.bfloat16)
+    ids, probs = ctx.moe_route(_t(rng.standard_normal((T, E)).astype(np.float32)), TOPK, True)
+    out = {}
+    for kern in ("xr", "lds"):
+        monkeypatch.setenv("RLXQ_MOE_KERNEL", kern)
+        out[kern] = ctx.moe_grouped(xt, gate_up, ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_EXPAND_SWIGLU, 2 * I, E)
+        torch.cuda.synchronize()
+        assert ("moexr" in ctx.last_kernel) == (kern == "xr")
+    a, b = out["xr"].cpu().numpy(), out["lds"].cpu().numpy().astype(np.float64)
+    assert rel_err(a, b) <= TOL
+
+
+@pytest.mark.parametrize("route", ["table", "fused"])
+@pytest.mark.parametrize("k", [768, 2048, 4096])
+def test_grouped_register_path_q4_0(ctx, orc, monkeypatch, k, route):
+    """Register-activation kernels on Q4_0 (two blocks per unit)."""
+    import torch
+
+    monkeypatch.setenv("RLXQ_MOE_ROUTE", route)
+    rows, n, E = 19, 72, 5
+    announce(f"grouped register path q4_0 k={k} route={route}")
+    rng = np.random.default_rng(k + 7)
+    packed = orc.synth(2, rng, E * n, k)
+    xt = _t(rng.standard_normal((rows, k)).astype(np.float32)).to(torch.bfloat16)
+    idx = rng.integers(0, E, rows).astype(np.float32)
+    y = ctx.grouped_matmul(xt, _t(packed), _t(idx), 2, n, E)
+    torch.cuda.synchronize()
+    assert "moexr" in ctx.last_kernel
+    want = orc.grouped_matmul_f64(2, xt.float().cpu().numpy(), packed, idx, n, E)
+    assert rel_err(y.cpu().numpy(), want) <= TOL
+
+
+@pytest.mark.parametrize("sb", ["f32", "bf16"])
+@pytest.mark.parametrize("k,group", [(768, 32), (2048, 64), (4096, 128)])
+def test_grouped_register_path_mlx4(ctx, orc, k, group, sb):
+    """Register-activation kernels on MLX affine 4-bit codes with f32 or bf16
+    scale/bias slabs."""
+    import torch
+    import rlxq
+
+    rows, n, E = 11, 80, 4
+    announce(f"grouped register path mlx4 k={k} group={group} sb={sb}")
+    rng = np.random.default_rng(k + group)
+    codes = rng.integers(0, 16, (E * n, k)).astype(np.uint32)
+    wq = orc.mlx_pack(codes, 4)
+    sc = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(rng.uniform(0.01, 0.1, (E * n, k // group))))
+    bi = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(rng.uniform(-0.5, 0.1, (E * n, k // group))))
+    xt = _t(rng.standard_normal((rows, k)).astype(np.float32)).to(torch.bfloat16)
+    idx = (np.arange(rows) * 3 % E).astype(np.float32)
+    cast = (lambda a: _t(a).to(torch.bfloat16)) if sb == "bf16" else _t
+    y = ctx.grouped_matmul(xt, _t(wq.view(np.uint8)), _t(idx), rlxq.MLX_AFFINE4, n, E, group=group,
+                           scales=cast(sc), biases=cast(bi))
+    torch.cuda.synchronize()
+    assert "moexr" in ctx.last_kernel
+    xv = xt.float().cpu().numpy()
+    want = np.zeros((rows, n))
+    for r in range(rows):
+        e = int(idx[r])
+        sl = slice(e * n, (e + 1) * n)
+        want[r] = orc.mlx_matmul_f64(xv[r:r + 1], wq[sl], sc[sl], bi[sl], n, 4, group)[0]
+    assert rel_err(y.cpu().numpy(), want) <= TOL
