@@ -224,18 +224,24 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   char name[96];
   hipFunction_t fn;
 
-  // Single activation row, bf16, 4-bit codes, at most 4 unit chunks per row:
-  // activations held in registers (no LDS stage).  RLXQ_GEMV_XR="NU,D,W"
-  // picks the variant, "0" turns the path off (tuning).
+  // Single activation row, bf16, 4-bit codes, at most 4 unit chunks of 64 per
+  // row (6 for the one-block units): activations held in registers.  By
+  // default they reach the registers through LDS, once per 8-wave workgroup
+  // (the row of x then crosses L2 once per workgroup, not once per wave).
+  // RLXQ_GEMV_XR="NU,D,W[,XS]" picks the variant (XS=1: through LDS), "0"
+  // turns the path off (tuning).
   const bool xr_scheme = scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_MLX_AFFINE4;
   const int64_t nchunk64 = (units + 63) / 64;
-  int xr_nu = (int)nchunk64, xr_d = nchunk64 <= 2 ? 2 : (nchunk64 == 3 ? 2 : 1), xr_w = 4;
-  bool use_xr = m == 1 && xbf && xr_scheme && nchunk64 <= 4;
+  const int64_t xr_max = scheme == RLXQ_GGUF_Q4_0 ? 4 : 6;
+  int xr_nu = (int)(nchunk64 == 5 ? 6 : nchunk64), xr_d = nchunk64 <= 3 ? 2 : 1, xr_w = 8;
+  bool use_xr = m == 1 && xbf && xr_scheme && nchunk64 <= xr_max;
+  int xr_lds = 1;   // 1: the activations pass through LDS once per workgroup
   if (const char* e = std::getenv("RLXQ_GEMV_XR")) {
-    int nu, d, wv;
-    if (std::sscanf(e, "%d,%d,%d", &nu, &d, &wv) == 3) {
+    int nu, d, wv, xs = 0;
+    if (std::sscanf(e, "%d,%d,%d,%d", &nu, &d, &wv, &xs) >= 3) {
       xr_d = d;
       xr_w = wv;
+      xr_lds = xs;
       if (nu < xr_nu) use_xr = false;
       else xr_nu = nu;
     } else if (e[0] == '0') {
@@ -243,13 +249,15 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     }
   }
   if (use_xr) {
-    std::snprintf(name, sizeof name, "rlxq_gemvxr_%s_U%d_D%d_W%d", scheme_name(scheme), xr_nu, xr_d, xr_w);
+    std::snprintf(name, sizeof name, "rlxq_gemvx%s_%s_U%d_D%d_W%d", xr_lds ? "s" : "r", scheme_name(scheme), xr_nu,
+                  xr_d, xr_w);
     if ((rc = get_fn(ctx, name, &fn))) return rc;
-    const int per_cu = blocks_per_cu(ctx, name, fn, 64 * xr_w, 0);
+    const size_t lds = xr_lds ? (size_t)k * 2 : 0;
+    const int per_cu = blocks_per_cu(ctx, name, fn, 64 * xr_w, lds);
     const int64_t wgs_needed = (n + xr_w - 1) / xr_w;
     int64_t gx = (int64_t)ctx->cu_count * per_cu;
     if (gx > wgs_needed) gx = wgs_needed;
-    return launch(ctx, fn, dim3((unsigned)gx, 1, 1), dim3(64 * xr_w, 1, 1), 0, stream, args, name);
+    return launch(ctx, fn, dim3((unsigned)gx, 1, 1), dim3(64 * xr_w, 1, 1), lds, stream, args, name);
   }
 
   const int64_t rec_bytes = (xbf ? 20 : 36) * 4;

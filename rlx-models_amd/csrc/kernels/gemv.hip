@@ -222,7 +222,7 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
 // of D rows of weight loads in flight.
 // ---------------------------------------------------------------------------
 
-template <int SCH, int NU, int D, int WAVES>
+template <int SCH, int NU, int D, int WAVES, bool XLDS>
 RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   constexpr int BLOCKS = Unit<SCH>::BLOCKS;
   constexpr int DW = Unit<SCH>::DW;
@@ -248,21 +248,6 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     uc[c] = uok[c] ? u : U - 1;
   }
 
-  // activations of my units (raw bf16 pairs)
-  uint32_t X[NU][BLOCKS][16];
-  const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x);
-#pragma unroll
-  for (int c = 0; c < NU; c++)
-#pragma unroll
-    for (int bl = 0; bl < BLOCKS; bl++) {
-      const uint4* p = reinterpret_cast<const uint4*>(xb + (int64_t)(uc[c] * BLOCKS + bl) * 32);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint4 v = p[q];
-        X[c][bl][4 * q] = v.x; X[c][bl][4 * q + 1] = v.y; X[c][bl][4 * q + 2] = v.z; X[c][bl][4 * q + 3] = v.w;
-      }
-    }
-
   struct Buf {
     uint32_t dw[NU][DW];
     float sm[NU][BLOCKS], bm[NU][BLOCKS];
@@ -280,9 +265,48 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
       }
     }
   };
+
+  // activations of my units (raw bf16 pairs): straight from global memory, or
+  // (XLDS) copied once per workgroup into LDS and read from there, so the
+  // row of x crosses L2 once per workgroup rather than once per wave.  The
+  // first D rows of weights are requested right after the activations.
+  uint32_t X[NU][BLOCKS][16];
+  const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x);
   Buf ring[D];
+  if constexpr (XLDS) {
+    extern __shared__ __align__(16) uint16_t xs[];
+    constexpr int XCH = (4 * NU * BLOCKS + WAVES - 1) / WAVES;   // 16-byte chunks per thread
+    uint4 xv[XCH];
 #pragma unroll
-  for (int i = 0; i < D; i++) load(n0 + i * G, ring[i]);
+    for (int i = 0; i < XCH; i++) {
+      const int c = threadIdx.x + 64 * WAVES * i;
+      xv[i] = c < K / 8 ? *reinterpret_cast<const uint4*>(xb + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < D; i++) load(n0 + i * G, ring[i]);
+#pragma unroll
+    for (int i = 0; i < XCH; i++) {
+      const int c = threadIdx.x + 64 * WAVES * i;
+      if (c < K / 8) *reinterpret_cast<uint4*>(xs + 8 * c) = xv[i];
+    }
+    __syncthreads();
+    xb = xs;
+  }
+#pragma unroll
+  for (int c = 0; c < NU; c++)
+#pragma unroll
+    for (int bl = 0; bl < BLOCKS; bl++) {
+      const uint4* p = reinterpret_cast<const uint4*>(xb + (int64_t)(uc[c] * BLOCKS + bl) * 32);
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint4 v = p[q];
+        X[c][bl][4 * q] = v.x; X[c][bl][4 * q + 1] = v.y; X[c][bl][4 * q + 2] = v.z; X[c][bl][4 * q + 3] = v.w;
+      }
+    }
+  if constexpr (!XLDS) {
+#pragma unroll
+    for (int i = 0; i < D; i++) load(n0 + i * G, ring[i]);
+  }
 
   // pairs and block sums
   float S[NU][BLOCKS];
@@ -380,10 +404,15 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   RLXQ_GEMV_X(SNAME, SCH, bf16, true) \
   RLXQ_GEMV_X(SNAME, SCH, f32, false)
 
-// Register-activation variants: rlxq_gemvxr_<scheme>_U<NU>_D<D>_W<WAVES>.
+// Register-activation variants: rlxq_gemvxr_<scheme>_U<NU>_D<D>_W<WAVES>,
+// and rlxq_gemvxs_... with the activations passed through LDS.
 #define RLXQ_GEMVXR_INST(NAME, SCH, NU, D, W)                                         \
   extern "C" __global__ __launch_bounds__(64 * W) void NAME(rlxq_gemv_args a) {      \
-    rlxq::gemv_xr_body<SCH, NU, D, W>(a);                                             \
+    rlxq::gemv_xr_body<SCH, NU, D, W, false>(a);                                      \
+  }
+#define RLXQ_GEMVXS_INST(NAME, SCH, NU, D, W)                                         \
+  extern "C" __global__ __launch_bounds__(64 * W) void NAME(rlxq_gemv_args a) {      \
+    rlxq::gemv_xr_body<SCH, NU, D, W, true>(a);                                       \
   }
 #define RLXQ_GEMVXR_SCHEME(SNAME, SCH)                                  \
   RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U1_D2_W4, SCH, 1, 2, 4)       \
@@ -392,10 +421,32 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U2_D3_W4, SCH, 2, 3, 4)       \
   RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U2_D2_W2, SCH, 2, 2, 2)       \
   RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U3_D2_W4, SCH, 3, 2, 4)       \
-  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U4_D1_W4, SCH, 4, 1, 4)
+  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U4_D1_W4, SCH, 4, 1, 4)       \
+  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U4_D2_W4, SCH, 4, 2, 4)
+// six chunks (K up to 12288) for the one-block units only
+#define RLXQ_GEMVXR_WIDE(SNAME, SCH)                                    \
+  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U6_D1_W4, SCH, 6, 1, 4)       \
+  RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U6_D2_W4, SCH, 6, 2, 4)
 RLXQ_GEMVXR_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXR_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_GEMVXR_SCHEME(mlx4, SCH_MLX4)
+RLXQ_GEMVXR_WIDE(q4_1, SCH_Q4_1)
+RLXQ_GEMVXR_WIDE(mlx4, SCH_MLX4)
+#define RLXQ_GEMVXS_SCHEME(SNAME, SCH)                                  \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U1_D2_W8, SCH, 1, 2, 8)       \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8, SCH, 2, 2, 8)       \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U2_D2_W16, SCH, 2, 2, 16)     \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U3_D2_W8, SCH, 3, 2, 8)       \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U4_D1_W8, SCH, 4, 1, 8)       \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U4_D2_W8, SCH, 4, 2, 8)
+#define RLXQ_GEMVXS_WIDE(SNAME, SCH)                                    \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U6_D1_W8, SCH, 6, 1, 8)       \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U6_D2_W8, SCH, 6, 2, 8)
+RLXQ_GEMVXS_SCHEME(q4_1, SCH_Q4_1)
+RLXQ_GEMVXS_SCHEME(q4_0, SCH_Q4_0)
+RLXQ_GEMVXS_SCHEME(mlx4, SCH_MLX4)
+RLXQ_GEMVXS_WIDE(q4_1, SCH_Q4_1)
+RLXQ_GEMVXS_WIDE(mlx4, SCH_MLX4)
 
 RLXQ_GEMV_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMV_SCHEME(q4_0, SCH_Q4_0)
