@@ -18,6 +18,85 @@ namespace {
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 }  // namespace
 
+namespace {
+// x -> prepared f16 activations and row scales in the workspace (x16 at
+// the start, inv_s after it; `extra` more bytes follow for the caller).
+int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bool nibble, size_t extra,
+             rlxq_x16_args& xa, char** rest, void* stream) {
+  const size_t x16_bytes = round256((size_t)(m * k) * 2), s_bytes = round256((size_t)m * 4);
+  void* ws = nullptr;
+  int rc;
+  if ((rc = workspace(ctx, x16_bytes + s_bytes + extra, &ws))) return rc;
+  char* wsb = static_cast<char*>(ws);
+  std::memset(&xa, 0, sizeof xa);
+  xa.x = x;
+  xa.x16 = reinterpret_cast<uint16_t*>(wsb);
+  xa.inv_s = reinterpret_cast<float*>(wsb + x16_bytes);
+  xa.M = m;
+  xa.K = k;
+  xa.x_bf16 = x_dtype == RLXQ_BF16;
+  xa.nibble_order = nibble;
+  *rest = wsb + x16_bytes + s_bytes;
+  hipFunction_t fn;
+  if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
+  void* xargs[] = {&xa};
+  return launch(ctx, fn, dim3((unsigned)m), dim3(256), 0, stream, xargs, "rlxq_x16_prep");
+}
+
+// Register-streamed Q4_1 kernel: workgroups (NT x 16 weight rows, K split,
+// 16*MT-row chunk); K splits (powers of two, whole 128-element chunks) until
+// the grid holds about two workgroups per CU (RLXQ_SKINNY_WGS scales that).
+int skinny_xr_dispatch(rlxq_ctx* ctx, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m, int64_t k,
+                       int64_t n, void* y, int y_dtype, void* stream, int MT, int NT, int D) {
+  const int64_t tiles_n = (n + 16 * NT - 1) / (16 * NT), mch = (m + 16 * MT - 1) / (16 * MT);
+  const int64_t chunks = k / 128;
+  const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  int64_t target = 2 * cus;
+  if (const char* e = std::getenv("RLXQ_SKINNY_WGS")) target = (int64_t)(cus * std::atof(e));
+  int64_t splits = 1;
+  while (tiles_n * mch * splits < target && splits * 2 * 4 <= chunks && splits < 32) splits *= 2;
+  const int64_t kslice = ((chunks + splits - 1) / splits) * 128;
+  splits = (k + kslice - 1) / kslice;
+  if (tiles_n * mch * splits > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: batched-decode grid");
+  const size_t part_bytes = splits > 1 ? round256((size_t)(splits * m * n) * 4) : 0;
+  rlxq_x16_args xa;
+  char* rest = nullptr;
+  int rc;
+  if ((rc = prep_x16(ctx, x, x_dtype, m, k, true, part_bytes, xa, &rest, stream))) return rc;
+  rlxq_skinny_args a;
+  std::memset(&a, 0, sizeof a);
+  a.x16 = xa.x16;
+  a.inv_s = xa.inv_s;
+  a.w = static_cast<const uint8_t*>(w);
+  a.part = part_bytes ? reinterpret_cast<float*>(rest) : nullptr;
+  a.y = y;
+  a.M = m;
+  a.N = n;
+  a.K = k;
+  a.rb = rb;
+  a.y_ld = n;
+  a.kslice = (int32_t)kslice;
+  a.splits = (int32_t)splits;
+  a.tiles_n = (int32_t)tiles_n;
+  a.y_bf16 = y_dtype == RLXQ_BF16;
+  char name[64];
+  std::snprintf(name, sizeof name, "rlxq_skinnyxr_q4_1_mt%d_nt%d_d%d", MT, NT, D);
+  hipFunction_t fn;
+  if ((rc = get_fn(ctx, name, &fn))) return rc;
+  const size_t lds = 2 * (size_t)(MT * NT * 4) * 64 * 4;
+  void* args[] = {&a};
+  if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name))) return rc;
+  if (splits > 1) {
+    if ((rc = get_fn(ctx, "rlxq_skinny_reduce", &fn))) return rc;
+    const int64_t total = m * n;
+    void* rargs[] = {&a};
+    rc = launch(ctx, fn, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, rargs, "rlxq_skinny_reduce");
+    if (!rc) ctx->last_kernel = name;
+  }
+  return rc;
+}
+}  // namespace
+
 bool skinny_applies(int scheme, int64_t m, int64_t k) {
   return (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q4_1) && m >= 1 &&
          m <= 256 && k % 128 == 0;
@@ -29,6 +108,18 @@ bool skinny_applies(int scheme, int64_t m, int64_t k) {
 // [splits, M, N]) are added in split order.
 int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
                     int64_t k, int64_t n, void* y, int y_dtype, void* stream) {
+  // Q4_1: the register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR=
+  // "MT,NT,D" picks a compiled one, "0" the LDS-staged kernels below.
+  if (scheme == RLXQ_GGUF_Q4_1) {
+    int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = m <= 16 ? 2 : (m <= 32 ? 2 : 4), xd = m <= 16 ? 4 : (m <= 32 ? 3 : 1);
+    bool xr = true;
+    if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
+      int a1, a2, a3;
+      if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) xmt = a1, xnt = a2, xd = a3;
+      else if (e[0] == '0') xr = false;
+    }
+    if (xr) return skinny_xr_dispatch(ctx, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, xmt, xnt, xd);
+  }
   const int MT = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
   // blocks per thread per step (K per step = 64 * BPT); 2 measured fastest,
   // RLXQ_SKINNY_BPT selects another compiled one (2 or 8 for MT <= 2, 2 or 4

@@ -234,9 +234,20 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   const int K = a.K;
   const int bpr = K >> 5;
   const int U = bpr / BLOCKS;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  // the wave index through readfirstlane: the row loop below is then known
+  // to be wave-uniform (scalar branches), so the compiler's wait counts can
+  // keep the ring's loads in flight across iterations
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t G = (int64_t)gridDim.x * WAVES;
   const int64_t n0 = (int64_t)blockIdx.x * WAVES + wv;
+  // rows of this wave: n0 + s * G, s < cnt
+  const int64_t cnt = n0 < a.N ? (a.N - n0 + G - 1) / G : 0;
+  // output row and factor of the activation row (loop invariants, loaded
+  // before any weights so that waiting for them never waits for the ring)
+  int64_t yrow = 0;
+  float ysc = 1.f;
+  if (a.row_map) yrow = a.row_map[0];
+  if (a.row_scale) ysc = a.row_scale[0];
   const int gpr = MLX ? K / a.group : 0;
 
   int uc[NU];
@@ -253,7 +264,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     float sm[NU][BLOCKS], bm[NU][BLOCKS];
   };
   auto load = [&](int64_t n, Buf& bf) {
-    const int64_t nn = n < a.N ? n : 0;
+    const int64_t nn = (n >= 0 && n < a.N) ? n : 0;  // no rows (cnt = 0): row 0
     const uint8_t* rp = a.w + nn * a.rb;
 #pragma unroll
     for (int c = 0; c < NU; c++) {
@@ -283,7 +294,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
       xv[i] = c < K / 8 ? *reinterpret_cast<const uint4*>(xb + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
     }
 #pragma unroll
-    for (int i = 0; i < D; i++) load(n0 + i * G, ring[i]);
+    for (int i = 0; i < D; i++) load(n0 + (i < cnt ? i : cnt - 1) * G, ring[i]);
 #pragma unroll
     for (int i = 0; i < XCH; i++) {
       const int c = threadIdx.x + 64 * WAVES * i;
@@ -305,7 +316,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     }
   if constexpr (!XLDS) {
 #pragma unroll
-    for (int i = 0; i < D; i++) load(n0 + i * G, ring[i]);
+    for (int i = 0; i < D; i++) load(n0 + (i < cnt ? i : cnt - 1) * G, ring[i]);
   }
 
   // pairs and block sums
@@ -325,53 +336,63 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     }
 
   const UnpackK kc = unpack_consts();
-  int64_t n = n0;
-  while (n < a.N) {
+  // Row s of the wave uses ring slot s % D.  While D more rows follow a full
+  // group, each slot is refilled right after use with the row D later (no
+  // condition on the refill, so the compiler's wait counts keep the other
+  // slots' loads in flight); the last rows, already in the ring, are then
+  // computed without refills.
+  auto row = [&](int64_t st, const Buf& bf) {
+    const int64_t n = n0 + st * G;
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < NU; c++)
+#pragma unroll
+      for (int bl = 0; bl < BLOCKS; bl++) {
+        float d, mn;
+        if constexpr (MLX) {
+          d = bf.sm[c][bl];
+          mn = bf.bm[c][bl];
+        } else {
+          block_scales<SCH>(bf.dw[c], bl, d, mn);
+        }
+        if (!uok[c]) {
+          d = 0.f;
+          mn = 0.f;
+        }
+        uint32_t pw[16];
+        block_pairs<SCH>(bf.dw[c], bl, pw, kc);
+        float ch = -chain_bias<SCH>() * S[c][bl];
+#pragma unroll
+        for (int t = 0; t < 16; t++) ch = dot2_bf16(pw[t], X[c][bl][t], ch);
+        acc = fmaf(d, ch, acc);
+        if constexpr (HAS_MIN) acc = fmaf(mn, S[c][bl], acc);
+      }
+    const float v = lane_group_sum<64>(acc);
+    if (lane == 0 && yrow >= 0) {
+      const int64_t off = yrow * a.y_ld + n;
+      if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v * ysc);
+      else reinterpret_cast<float*>(a.y)[off] = v * ysc;
+    }
+  };
+  int64_t s0 = 0;
+  for (; s0 + 2 * D <= cnt; s0 += D) {
 #pragma unroll
     for (int i = 0; i < D; i++) {
-      if (n < a.N) {
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < NU; c++)
-#pragma unroll
-          for (int bl = 0; bl < BLOCKS; bl++) {
-            float d, mn;
-            if constexpr (MLX) {
-              d = ring[i].sm[c][bl];
-              mn = ring[i].bm[c][bl];
-            } else {
-              block_scales<SCH>(ring[i].dw[c], bl, d, mn);
-            }
-            if (!uok[c]) {
-              d = 0.f;
-              mn = 0.f;
-            }
-            uint32_t pw[16];
-            block_pairs<SCH>(ring[i].dw[c], bl, pw, kc);
-            float ch = -chain_bias<SCH>() * S[c][bl];
-#pragma unroll
-            for (int t = 0; t < 16; t++) ch = dot2_bf16(pw[t], X[c][bl][t], ch);
-            acc = fmaf(d, ch, acc);
-            if constexpr (HAS_MIN) acc = fmaf(mn, S[c][bl], acc);
-          }
-        const float v = lane_group_sum<64>(acc);
-        if (lane == 0) {
-          int64_t yrow = 0;
-          float sc = 1.f;
-          if (a.row_map) yrow = a.row_map[0];
-          if (a.row_scale) sc = a.row_scale[0];
-          if (yrow >= 0) {
-            const int64_t off = yrow * a.y_ld + n;
-            if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v * sc);
-            else reinterpret_cast<float*>(a.y)[off] = v * sc;
-          }
-        }
-        const int64_t nl = n + (int64_t)D * G;
-        if (nl < a.N) load(nl, ring[i]);
-        n += G;
-      }
+      row(s0 + i, ring[i]);
+      load(n0 + (s0 + i + D) * G, ring[i]);
     }
   }
+  // at most 2D - 1 rows remain: the first D of them may still refill
+#pragma unroll
+  for (int i = 0; i < D; i++) {
+    if (s0 + i < cnt) {
+      row(s0 + i, ring[i]);
+      if (s0 + i + D < cnt) load(n0 + (s0 + i + D) * G, ring[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < D; i++)
+    if (s0 + D + i < cnt) row(s0 + D + i, ring[i]);
 }
 
 }  // namespace rlxq

@@ -337,12 +337,12 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
 
   const UnpackK kc = unpack_consts();
   const int64_t base = (int64_t)wq * RP;  // the wave's first column (wave-uniform)
+  // column steps of this wave: base + s * cstride, s < cnt
+  const int64_t cnt = base < width ? (width - base + cstride - 1) / cstride : 0;
+  auto step_col = [&](int64_t st) { return base + (st < cnt ? st : (cnt > 0 ? cnt - 1 : 0)) * cstride + g; };
   for (int c0 = beg; c0 < end; c0 += MT) {
-    Buf ring[D];
-#pragma unroll
-    for (int i = 0; i < D; i++) load(base + i * cstride + g, ring[i]);
-
-    // activations of the MT entries: pairs and block sums of my units
+    // activations of the MT entries (raw bf16), requested before the ring so
+    // that waiting for them does not wait for the weights
     int ent[MT];
     uint32_t X[MT][NU][BLOCKS][16];
     float S[MT][NU][BLOCKS];
@@ -356,86 +356,114 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
 #pragma unroll
         for (int bl = 0; bl < BLOCKS; bl++) {
           const uint4* p = reinterpret_cast<const uint4*>(xb + (int64_t)(uc[c] * BLOCKS + bl) * 32);
-          uint32_t R[16];
 #pragma unroll
           for (int q = 0; q < 4; q++) {
             const uint4 v = p[q];
-            const bool live = ent[m] >= 0;
-            R[4 * q] = live ? v.x : 0u;
-            R[4 * q + 1] = live ? v.y : 0u;
-            R[4 * q + 2] = live ? v.z : 0u;
-            R[4 * q + 3] = live ? v.w : 0u;
+            X[m][c][bl][4 * q] = v.x;
+            X[m][c][bl][4 * q + 1] = v.y;
+            X[m][c][bl][4 * q + 2] = v.z;
+            X[m][c][bl][4 * q + 3] = v.w;
           }
+        }
+    }
+    // keep the activation loads ahead of the weight loads in the issue order
+    __builtin_amdgcn_sched_barrier(0);
+    Buf ring[D];
+#pragma unroll
+    for (int i = 0; i < D; i++) load(step_col(i), ring[i]);
+    // pairs and block sums of my units (zero for absent entries)
+#pragma unroll
+    for (int m = 0; m < MT; m++)
+#pragma unroll
+      for (int c = 0; c < NU; c++)
+#pragma unroll
+        for (int bl = 0; bl < BLOCKS; bl++) {
+          uint32_t R[16];
+#pragma unroll
+          for (int t = 0; t < 16; t++) R[t] = ent[m] >= 0 ? X[m][c][bl][t] : 0u;
           float sum = 0.f;
 #pragma unroll
           for (int t = 0; t < 16; t++) sum = dot2_bf16(R[t], 0x3F803F80u, sum);
           S[m][c][bl] = sum;
           pairs_from_raw<SCH>(R, X[m][c][bl]);
         }
-    }
 
-    int64_t col = base;
-    while (col < width) {
+    // Column step s uses ring slot s % D.  While D more steps follow a full
+    // group, each slot is refilled right after use with the step D later (no
+    // condition on the refill, so the wait counts keep the other slots'
+    // loads in flight); the last steps, already in the ring, follow.
+    auto step = [&](int64_t st, const Buf& rb) {
+      const int64_t col = base + st * cstride;
+      float acc[R2][MT];
 #pragma unroll
-      for (int i = 0; i < D; i++) {
-        if (col < width) {
-          float acc[R2][MT];
+      for (int r = 0; r < R2; r++)
 #pragma unroll
-          for (int r = 0; r < R2; r++)
+        for (int m = 0; m < MT; m++) acc[r][m] = 0.f;
 #pragma unroll
-            for (int m = 0; m < MT; m++) acc[r][m] = 0.f;
+      for (int r = 0; r < R2; r++)
 #pragma unroll
-          for (int r = 0; r < R2; r++)
+        for (int c = 0; c < NU; c++)
 #pragma unroll
-            for (int c = 0; c < NU; c++)
-#pragma unroll
-              for (int bl = 0; bl < BLOCKS; bl++) {
-                float d, mn;
-                if constexpr (MLX) {
-                  d = ring[i].sm[r][c];
-                  mn = ring[i].bm[r][c];
-                } else {
-                  block_scales<SCH>(ring[i].dw[r][c], bl, d, mn);
-                }
-                if (!uok[c]) {
-                  d = 0.f;
-                  mn = 0.f;
-                }
-                uint32_t pw[16];
-                block_pairs<SCH>(ring[i].dw[r][c], bl, pw, kc);
-#pragma unroll
-                for (int m = 0; m < MT; m++) {
-                  float ch = -chain_bias<SCH>() * S[m][c][bl];
-#pragma unroll
-                  for (int t = 0; t < 16; t++) ch = dot2_bf16(pw[t], X[m][c][bl][t], ch);
-                  acc[r][m] = fmaf(d, ch, acc[r][m]);
-                  if constexpr (HAS_MIN) acc[r][m] = fmaf(mn, S[m][c][bl], acc[r][m]);
-                }
-              }
-          float v[R2][MT];
-#pragma unroll
-          for (int r = 0; r < R2; r++)
-#pragma unroll
-            for (int m = 0; m < MT; m++) v[r][m] = lane_group_sum<L>(acc[r][m]);
-          const int64_t nl = col + (int64_t)D * cstride;
-          if (nl < width) load(nl + g, ring[i]);
-          const int64_t mycol = col + g;
-          if (li == 0 && mycol < width) {
+          for (int bl = 0; bl < BLOCKS; bl++) {
+            float d, mn;
+            if constexpr (MLX) {
+              d = rb.sm[r][c];
+              mn = rb.bm[r][c];
+            } else {
+              block_scales<SCH>(rb.dw[r][c], bl, d, mn);
+            }
+            if (!uok[c]) {
+              d = 0.f;
+              mn = 0.f;
+            }
+            uint32_t pw[16];
+            block_pairs<SCH>(rb.dw[r][c], bl, pw, kc);
 #pragma unroll
             for (int m = 0; m < MT; m++) {
-              if (ent[m] >= 0) {
-                float o = v[0][m];
-                if constexpr (SWIGLU) o = o / (1.f + expf(-o)) * v[1][m];  // silu(g) * u
-                const int64_t off = (int64_t)ent[m] * a.y_ld + mycol;
-                if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(o);
-                else reinterpret_cast<float*>(a.y)[off] = o;
-              }
+              float ch = -chain_bias<SCH>() * S[m][c][bl];
+#pragma unroll
+              for (int t = 0; t < 16; t++) ch = dot2_bf16(pw[t], X[m][c][bl][t], ch);
+              acc[r][m] = fmaf(d, ch, acc[r][m]);
+              if constexpr (HAS_MIN) acc[r][m] = fmaf(mn, S[m][c][bl], acc[r][m]);
             }
           }
-          col += cstride;
+      float v[R2][MT];
+#pragma unroll
+      for (int r = 0; r < R2; r++)
+#pragma unroll
+        for (int m = 0; m < MT; m++) v[r][m] = lane_group_sum<L>(acc[r][m]);
+      const int64_t mycol = col + g;
+      if (li == 0 && mycol < width) {
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+          if (ent[m] >= 0) {
+            float o = v[0][m];
+            if constexpr (SWIGLU) o = o / (1.f + expf(-o)) * v[1][m];  // silu(g) * u
+            const int64_t off = (int64_t)ent[m] * a.y_ld + mycol;
+            if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(o);
+            else reinterpret_cast<float*>(a.y)[off] = o;
+          }
         }
       }
+    };
+    int64_t s0 = 0;
+    for (; s0 + 2 * D <= cnt; s0 += D) {
+#pragma unroll
+      for (int i = 0; i < D; i++) {
+        step(s0 + i, ring[i]);
+        load(step_col(s0 + i + D), ring[i]);
+      }
     }
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+      if (s0 + i < cnt) {
+        step(s0 + i, ring[i]);
+        if (s0 + i + D < cnt) load(step_col(s0 + i + D), ring[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < D; i++)
+      if (s0 + D + i < cnt) step(s0 + D + i, ring[i]);
   }
 }
 
@@ -570,7 +598,8 @@ RLXQ_DEV void moe_gemv_body(const rlxq_moe_gemv_args& a) {
 template <int SCH, int L, int NU, int MT, int D, bool SWIGLU, bool FUSED>
 RLXQ_DEV void moe_xr_body(const rlxq_moe_gemv_args& a) {
   auto work = [&](int e, const int32_t* perm, int beg, int end, int tn) {
-    moe_xr_wave<SCH, L, NU, MT, D, SWIGLU>(a, e, perm, beg, end, tn * 4 + (int)(threadIdx.x >> 6), a.tiles_n * 4);
+    moe_xr_wave<SCH, L, NU, MT, D, SWIGLU>(a, e, perm, beg, end,
+                                           tn * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), a.tiles_n * 4);
   };
   if constexpr (FUSED) balanced_dispatch<MT>(a, work);
   else table_dispatch(a, work);

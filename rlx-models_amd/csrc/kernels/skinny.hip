@@ -433,6 +433,169 @@ RLXQ_DEV void skinny_dma_body(const rlxq_skinny_args& a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Register-streamed variant (Q4_1): no LDS stage and no barrier per step.
+// The four waves of a workgroup take the same NT tiles of 16 weight rows and
+// split their K range in 4-block chunks (chunk c -> wave c % 4).  Lane
+// (j, g) = (lane % 16, lane / 16) loads all 20 bytes of block 4c + g of row
+// j of each tile (one 4-byte and one 16-byte load) into a ring of D chunks,
+// so D * NT * 20 bytes per lane are in flight.  The four MFMA steps i of a
+// chunk each take code dword i of every lane's block: across the lane groups
+// g a step's 32 K positions are positions 8i .. 8i + 7 of blocks 4c .. 4c + 3
+// (prepared activation order), and the A fragment of lane (m, g) is the 16
+// bytes of row m at block 4c + g, positions 8i .. 8i + 7, loaded with the
+// chunk.  The waves' sums are added in the fixed order (w0 + w2) + (w1 + w3).
+// ---------------------------------------------------------------------------
+template <int MT, int NT, int D>
+RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
+  // wave index through readfirstlane: the chunk loop is wave-uniform
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int tn = blockIdx.x % a.tiles_n;
+  const int sp = (blockIdx.x / a.tiles_n) % a.splits;
+  const int mc = blockIdx.x / (a.tiles_n * a.splits);
+  const int64_t n0 = (int64_t)tn * 16 * NT, m0 = (int64_t)mc * 16 * MT;
+  const int64_t kb = (int64_t)sp * a.kslice;
+  const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
+  const int nchunk = (int)((ke - kb) / 128);
+  // chunks of this wave: wv + 4 it, it < cnt
+  const int cnt = nchunk > wv ? (nchunk - wv + 3) / 4 : 0;
+
+  const uint8_t* wrow[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int64_t n = n0 + 16 * t + j;
+    wrow[t] = a.w + (n < a.N ? n : a.N - 1) * a.rb + (kb / 32 + g) * 20;
+  }
+  const uint16_t* xrow[MT];
+  bool mok[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) {
+    const int64_t m = m0 + 16 * mt + j;
+    mok[mt] = m < a.M;
+    xrow[mt] = a.x16 + (mok[mt] ? m : 0) * a.K + kb + g * 32;
+  }
+
+  struct Stage {
+    uint32_t w[NT][5];
+    uint4 x[MT][4];
+  };
+  auto load = [&](int c, Stage& st) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const uint8_t* p = wrow[t] + (int64_t)c * 80;
+      st.w[t][0] = ld_u32(p);
+      const uint4 q = ld_u128(p + 4);
+      st.w[t][1] = q.x; st.w[t][2] = q.y; st.w[t][3] = q.z; st.w[t][4] = q.w;
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xrow[mt] + (int64_t)c * 128 + 8 * i);
+        st.x[mt][i] = mok[mt] ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
+  };
+
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Chunk it uses ring slot it % D.  While D more chunks follow a full
+  // group, each slot is refilled right after use with the chunk D later (no
+  // condition on the refill, so the wait counts keep the other slots' loads
+  // in flight); the last chunks, already in the ring, are computed after.
+  auto chunk_of = [&](int it) { return wv + 4 * it; };
+  auto compute = [&](const Stage& st) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const f16x8_t b = dequant_lane<SCH_Q4_1>(st.w[t], i);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, st.x[mt][i]), b, acc[mt][t],
+                                                             0, 0, 0);
+      }
+  };
+  // (slots past the wave's chunks repeat its last one: a few redundant
+  // loads when it has fewer than D chunks, none otherwise)
+  Stage ring[D];
+#pragma unroll
+  for (int d = 0; d < D; d++) load(chunk_of(d < cnt ? d : (cnt > 0 ? cnt - 1 : 0)), ring[d]);
+  int it0 = 0;
+  for (; it0 + 2 * D <= cnt; it0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      compute(ring[d]);
+      load(chunk_of(it0 + d + D), ring[d]);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D; d++) {
+    if (it0 + d < cnt) {
+      compute(ring[d]);
+      if (it0 + d + D < cnt) load(chunk_of(it0 + d + D), ring[d]);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D; d++)
+    if (it0 + D + d < cnt) compute(ring[d]);
+
+  // (w0 + w2) + (w1 + w3)
+  constexpr int E = MT * NT * 4;
+  extern __shared__ __align__(16) uint32_t sm[];
+  float* R = reinterpret_cast<float*>(sm);   // [2][E][64]
+  if (wv >= 2) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) R[((wv - 2) * E + (mt * NT + t) * 4 + r) * 64 + lane] = acc[mt][t][r];
+  }
+  __syncthreads();
+  if (wv < 2) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[mt][t][r] += R[(wv * E + (mt * NT + t) * 4 + r) * 64 + lane];
+  }
+  __syncthreads();
+  if (wv == 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) R[((mt * NT + t) * 4 + r) * 64 + lane] = acc[mt][t][r];
+  }
+  __syncthreads();
+  if (wv != 0) return;
+  // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int64_t m = m0 + 16 * mt + 4 * g + r;
+      if (m >= a.M) continue;
+      const float is = a.inv_s[m];
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const int64_t n = n0 + 16 * t + j;
+        if (n >= a.N) continue;
+        const float v = (acc[mt][t][r] + R[((mt * NT + t) * 4 + r) * 64 + lane]) * is;
+        if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
+        else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
+        else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+      }
+    }
+}
+
 }  // namespace rlxq
 
 // One workgroup of 256 per activation row; each thread owns whole 32-element
@@ -557,3 +720,17 @@ RLXQ_SKINNY_SCHEME(q8_0, SCH_Q8_0)
 RLXQ_SKINNY_DMA_INST(1)
 RLXQ_SKINNY_DMA_INST(2)
 RLXQ_SKINNY_DMA_INST(4)
+
+// Register-streamed Q4_1 variants: rlxq_skinnyxr_q4_1_mt<MT>_nt<NT>_d<D>.
+#define RLXQ_SKINNYXR_INST(MT, NT, D)                                                                  \
+  extern "C" __global__ __launch_bounds__(256) void rlxq_skinnyxr_q4_1_mt##MT##_nt##NT##_d##D(          \
+      rlxq_skinny_args a) {                                                                            \
+    rlxq::skinny_xr_body<MT, NT, D>(a);                                                                \
+  }
+RLXQ_SKINNYXR_INST(1, 2, 4)
+RLXQ_SKINNYXR_INST(1, 4, 2)
+RLXQ_SKINNYXR_INST(1, 4, 3)
+RLXQ_SKINNYXR_INST(2, 2, 3)
+RLXQ_SKINNYXR_INST(2, 4, 2)
+RLXQ_SKINNYXR_INST(4, 2, 2)
+RLXQ_SKINNYXR_INST(4, 4, 1)

@@ -28,7 +28,7 @@ def test_skinny_matches_oracle(ctx, orc, scheme, mkn, xdt):
     packed = orc.synth(scheme, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt=xdt)
-    assert ctx.last_kernel.startswith("rlxq_skinny_"), ctx.last_kernel
+    assert ctx.last_kernel.startswith("rlxq_skinny"), ctx.last_kernel
     assert rel_err(got, want) <= TOL_F32
 
 
@@ -67,19 +67,46 @@ def test_skinny_activation_range(ctx, orc, scheme):
         assert rel_err(got[r:r + 1], want[r:r + 1]) <= TOL_F32, r
 
 
-@pytest.mark.parametrize("dma", ["0", "1"])
+STAGINGS = {"register": {}, "lds": {"RLXQ_SKINNY_XR": "0", "RLXQ_SKINNY_DMA": "0"},
+            "dma": {"RLXQ_SKINNY_XR": "0", "RLXQ_SKINNY_DMA": "1"}}
+KERNEL_PREFIX = {"register": "rlxq_skinnyxr_", "lds": "rlxq_skinny_q4_1_mt", "dma": "rlxq_skinny_q4_1_mt"}
+
+
+@pytest.mark.parametrize("staging", list(STAGINGS))
 @pytest.mark.parametrize("mkn", [(5, 256, 136), (16, 4096, 512), (33, 768, 200), (64, 1024, 128)], ids=str)
-def test_skinny_q4_1_both_stagings(ctx, orc, monkeypatch, dma, mkn):
-    """Q4_1 through the register-staged and the LDS-DMA-staged kernels."""
-    monkeypatch.setenv("RLXQ_SKINNY_DMA", dma)
+def test_skinny_q4_1_every_staging(ctx, orc, monkeypatch, staging, mkn):
+    """Q4_1 through the register-streamed kernel (no LDS stage), the
+    register-staged LDS kernel and the LDS-DMA-staged kernel."""
+    for key, val in STAGINGS[staging].items():
+        monkeypatch.setenv(key, val)
     m, k, n = mkn
-    announce(f"skinny q4_1 dma={dma} {mkn}")
+    announce(f"skinny q4_1 staging={staging} {mkn}")
     rng = np.random.default_rng(k + n + m)
     packed = orc.synth_q4_1(rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, want = run_dense(ctx, orc, 3, x, packed, n, xdt="bf16")
-    assert ctx.last_kernel.endswith("_dma") == (dma == "1"), ctx.last_kernel
+    assert ctx.last_kernel.startswith(KERNEL_PREFIX[staging]), ctx.last_kernel
+    assert ctx.last_kernel.endswith("_dma") == (staging == "dma"), ctx.last_kernel
     assert rel_err(got, want) <= TOL_F32
+
+
+# every compiled register-streamed variant "MT,NT,D"; shapes with partial
+# row chunks, partial row tiles, several K splits and a single chunk of K
+XR_VARIANTS = ["1,2,4", "1,4,2", "1,4,3", "2,2,3", "2,4,2", "4,2,2", "4,4,1"]
+
+
+@pytest.mark.parametrize("cfg", XR_VARIANTS)
+def test_skinny_every_register_variant(ctx, orc, monkeypatch, cfg):
+    monkeypatch.setenv("RLXQ_SKINNY_XR", cfg)
+    mt, nt, d = (int(v) for v in cfg.split(","))
+    for (m, k, n) in [(5, 128, 7), (16 * mt + 3, 2048, 16 * nt * 3 + 5), (9, 12288, 200), (64, 1536, 96)]:
+        announce(f"skinny register {cfg} {(m, k, n)}")
+        rng = np.random.default_rng(m + k + n + mt)
+        packed = orc.synth_q4_1(rng, n, k)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        got, want = run_dense(ctx, orc, 3, x, packed, n, xdt="bf16")
+        assert ctx.last_kernel == f"rlxq_skinnyxr_q4_1_mt{mt}_nt{nt}_d{d}", ctx.last_kernel
+        assert rel_err(got, want) <= TOL_F32, (cfg, m, k, n)
 
 
 def test_f32_activations_stay_exact(ctx, orc, monkeypatch):
