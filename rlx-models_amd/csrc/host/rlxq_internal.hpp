@@ -25,6 +25,8 @@ struct rlxq_ctx {
   size_t ws_bytes = 0;
 };
 
+#include "skinny_args.h"
+
 namespace rlxq {
 
 // Records `msg` as the context's last error and returns `code`.
@@ -71,6 +73,10 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
                   const void* scales, const void* biases, int sb_dtype, int64_t m, int64_t k,
                   int64_t n, void* y, int y_dtype, void* stream);
 bool skinny_applies(int scheme, int64_t m, int64_t k);
+// x [m, k] -> prepared f16 activations (x16) and row factors (inv_s) at the
+// start of the workspace; `extra` further bytes follow at *rest.
+int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bool nibble, size_t extra,
+             rlxq_x16_args& xa, char** rest, void* stream);
 int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
                     int64_t k, int64_t n, void* y, int y_dtype, void* stream);
 int i8b_dispatch(rlxq_ctx* ctx, int group, const void* x, int x_dtype, const void* w, const void* scales,

@@ -18,7 +18,6 @@ namespace {
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 }  // namespace
 
-namespace {
 // x -> prepared f16 activations and row scales in the workspace (x16 at
 // the start, inv_s after it; `extra` more bytes follow for the caller).
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bool nibble, size_t extra,
@@ -42,6 +41,8 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bo
   void* xargs[] = {&xa};
   return launch(ctx, fn, dim3((unsigned)m), dim3(256), 0, stream, xargs, "rlxq_x16_prep");
 }
+
+namespace {
 
 // Register-streamed Q4_1 kernel: workgroups (NT x 16 weight rows, K split,
 // 16*MT-row chunk); K splits (powers of two, whole 128-element chunks) until

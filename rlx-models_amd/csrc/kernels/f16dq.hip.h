@@ -1,0 +1,78 @@
+// f16 dequantisation of packed 4/8-bit codes into MFMA operands, shared by
+// the batched-decode (skinny) and f16 prefill GEMM kernels.
+//
+// A lane's 8 consecutive operand positions 8g .. 8g + 7 of a 32-element
+// block hold, for the nibble formats, elements 4g .. 4g + 3 and
+// 16 + 4g .. 16 + 4g + 3 (the order in which code dword g unpacks); the
+// activations are stored in the same order (perm_k).
+#ifndef RLXQ_F16DQ_HIP_H
+#define RLXQ_F16DQ_HIP_H
+#include "common.hip.h"
+
+namespace rlxq {
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Element of a 32-block held at position p (see above).
+RLXQ_DEV int perm_k(int p, bool nibble) {
+  if (!nibble) return p;
+  const int g = p >> 3, e = p & 7;
+  return e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4);
+}
+
+
+// Normalised LDS block: scale dword (Q4_1: d | m << 16, else d) + code dwords.
+template <int SCH> constexpr int sk_bdw() { return SCH == SCH_Q8_0 ? 9 : 5; }
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8): wait on one counter, leave the others unconstrained.
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8); }
+constexpr int lgkmcnt0_imm() { return 0xF | (0x3 << 14) | (0x7 << 4); }
+
+RLXQ_DEV f16x2_t as_h2(uint32_t v) { return __builtin_bit_cast(f16x2_t, v); }
+RLXQ_DEV uint32_t as_u(f16x2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Two codes of bytes (b0, b1) or (b2, b3) of `u` as f16 1024 + code.
+RLXQ_DEV f16x2_t magic_lo(uint32_t u) { return as_h2(perm_b32(0x64646464u, u, 0x04010400u)); }
+RLXQ_DEV f16x2_t magic_hi(uint32_t u) { return as_h2(perm_b32(0x64646464u, u, 0x04030402u)); }
+
+// The lane's B operand: 8 f16 weights of one block of one row, positions
+// 8g .. 8g + 7.  `bp` points at the normalised block.
+template <int SCH>
+RLXQ_DEV f16x8_t dequant_lane(const uint32_t* bp, int g) {
+  const uint32_t dm = bp[0];
+  const f16x2_t d2 = as_h2(perm_b32(dm, dm, 0x01000100u));
+  f16x2_t w[4];
+  if constexpr (SCH == SCH_Q8_0) {
+    const uint32_t u0 = bp[1 + 2 * g] ^ 0x80808080u, u1 = bp[2 + 2 * g] ^ 0x80808080u;
+    const f16x2_t off = {(_Float16)-1152.f, (_Float16)-1152.f};
+    w[0] = (magic_lo(u0) + off) * d2;
+    w[1] = (magic_hi(u0) + off) * d2;
+    w[2] = (magic_lo(u1) + off) * d2;
+    w[3] = (magic_hi(u1) + off) * d2;
+  } else {
+    const uint32_t qs = bp[1 + g];
+    const uint32_t lo = qs & 0x0F0F0F0Fu, hi = (qs >> 4) & 0x0F0F0F0Fu;
+    if constexpr (SCH == SCH_Q4_1) {
+      const f16x2_t m2 = as_h2(perm_b32(dm, dm, 0x03020302u));
+      const f16x2_t off = {(_Float16)-1024.f, (_Float16)-1024.f};
+      w[0] = __builtin_elementwise_fma(magic_lo(lo) + off, d2, m2);
+      w[1] = __builtin_elementwise_fma(magic_hi(lo) + off, d2, m2);
+      w[2] = __builtin_elementwise_fma(magic_lo(hi) + off, d2, m2);
+      w[3] = __builtin_elementwise_fma(magic_hi(hi) + off, d2, m2);
+    } else {
+      const f16x2_t off = {(_Float16)-1032.f, (_Float16)-1032.f};
+      w[0] = (magic_lo(lo) + off) * d2;
+      w[1] = (magic_hi(lo) + off) * d2;
+      w[2] = (magic_lo(hi) + off) * d2;
+      w[3] = (magic_hi(hi) + off) * d2;
+    }
+  }
+  return f16x8_t{w[0].x, w[0].y, w[1].x, w[1].y, w[2].x, w[2].y, w[3].x, w[3].y};
+}
+
+}  // namespace rlxq
+
+#endif
