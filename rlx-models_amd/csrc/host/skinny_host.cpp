@@ -21,7 +21,7 @@ size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 // x -> prepared f16 activations and row scales in the workspace (x16 at
 // the start, inv_s after it; `extra` more bytes follow for the caller).
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bool nibble, size_t extra,
-             rlxq_x16_args& xa, char** rest, void* stream) {
+             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major) {
   const size_t x16_bytes = round256((size_t)(m * k) * 2), s_bytes = round256((size_t)m * 4);
   void* ws = nullptr;
   int rc;
@@ -35,6 +35,7 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bo
   xa.K = k;
   xa.x_bf16 = x_dtype == RLXQ_BF16;
   xa.nibble_order = nibble;
+  xa.frag_major = frag_major ? 1 : 0;
   *rest = wsb + x16_bytes + s_bytes;
   hipFunction_t fn;
   if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
@@ -63,7 +64,7 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, const void* x, int x_dtype, const void* w,
   rlxq_x16_args xa;
   char* rest = nullptr;
   int rc;
-  if ((rc = prep_x16(ctx, x, x_dtype, m, k, true, part_bytes, xa, &rest, stream))) return rc;
+  if ((rc = prep_x16(ctx, x, x_dtype, m, k, true, part_bytes, xa, &rest, stream, true))) return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
   a.x16 = xa.x16;
@@ -112,7 +113,7 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   // Q4_1: the register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR=
   // "MT,NT,D" picks a compiled one, "0" the LDS-staged kernels below.
   if (scheme == RLXQ_GGUF_Q4_1) {
-    int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = m <= 16 ? 2 : (m <= 32 ? 2 : 4), xd = m <= 16 ? 4 : (m <= 32 ? 3 : 1);
+    int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = 2, xd = m <= 16 ? 4 : (m <= 32 ? 3 : 2);
     bool xr = true;
     if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
       int a1, a2, a3;

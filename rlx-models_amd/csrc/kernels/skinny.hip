@@ -407,13 +407,16 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
     const int64_t n = n0 + 16 * t + j;
     wrow[t] = a.w + (n < a.N ? n : a.N - 1) * a.rb + (kb / 32 + g) * 20;
   }
-  const uint16_t* xrow[MT];
+  // activations in the fragment-major layout: piece i of chunk c for row m,
+  // lane group g at ((4 c + i) M + m) 4 + g (16-byte pieces), so the A
+  // fragment of 16 rows is one contiguous 1 KB read
+  const uint4* xrow[MT];
   bool mok[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; mt++) {
     const int64_t m = m0 + 16 * mt + j;
     mok[mt] = m < a.M;
-    xrow[mt] = a.x16 + (mok[mt] ? m : 0) * a.K + kb + g * 32;
+    xrow[mt] = reinterpret_cast<const uint4*>(a.x16) + ((kb / 32) * a.M + (mok[mt] ? m : 0)) * 4 + g;
   }
 
   struct Stage {
@@ -432,7 +435,7 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const uint4 v = *reinterpret_cast<const uint4*>(xrow[mt] + (int64_t)c * 128 + 8 * i);
+        const uint4 v = xrow[mt][((int64_t)c * 4 + i) * a.M * 4];
         st.x[mt][i] = mok[mt] ? v : make_uint4(0u, 0u, 0u, 0u);
       }
   };
@@ -609,9 +612,16 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
       const uint32_t h1 = f32_to_f16_bits(w[rlxq::perm_k(p + 1, nib)] * s);
       o[p / 2] = h0 | (h1 << 16);
     }
-    uint4* dst = reinterpret_cast<uint4*>(a.x16 + r * a.K + b * 32);
+    if (a.frag_major) {
+      uint4* dst = reinterpret_cast<uint4*>(a.x16);
 #pragma unroll
-    for (int q = 0; q < 4; q++) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+      for (int q = 0; q < 4; q++)
+        dst[(((b >> 2) * 4 + q) * a.M + r) * 4 + (b & 3)] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+    } else {
+      uint4* dst = reinterpret_cast<uint4*>(a.x16 + r * a.K + b * 32);
+#pragma unroll
+      for (int q = 0; q < 4; q++) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+    }
   };
 #pragma unroll
   for (int i = 0; i < RB; i++) {

@@ -4,15 +4,19 @@
 #define RLXQ_SKINNY_ARGS_H
 #include <stdint.h>
 
-/* Activation preparation: x [M, K] (f32 or bf16) -> x16 [M, K] f16 scaled by
- * a power of two per row (inv_s[m] = 1 / scale) and permuted within each
- * 32-element block to the order the packed codes unpack to. */
+/* Activation preparation: x [M, K] (f32 or bf16) -> x16 f16 scaled by a
+ * power of two per row (inv_s[m] = 1 / scale) and permuted within each
+ * 32-element block to the order the packed codes unpack to.  Row-major
+ * [M, K], or (frag_major) fragment-major: the 16-byte piece i (positions
+ * 8i .. 8i + 7) of block 4c + g of row m at piece ((4c + i) * M + m) * 4 + g,
+ * so the MFMA A fragments of 16 rows are 1 KB of contiguous memory. */
 typedef struct rlxq_x16_args {
   const void* x;
   uint16_t* x16;
   float* inv_s;
   int64_t M, K;
   int32_t x_bf16, nibble_order;
+  int32_t frag_major, pad;
 } rlxq_x16_args;
 
 typedef struct rlxq_skinny_args {
