@@ -45,11 +45,11 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bo
 
 namespace {
 
-// Register-streamed Q4_1 kernel: workgroups (NT x 16 weight rows, K split,
+// Register-streamed kernel: workgroups (NT x 16 weight rows, K split,
 // 16*MT-row chunk); K splits (powers of two, whole 128-element chunks) until
 // the grid holds about two workgroups per CU (RLXQ_SKINNY_WGS scales that).
-int skinny_xr_dispatch(rlxq_ctx* ctx, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m, int64_t k,
-                       int64_t n, void* y, int y_dtype, void* stream, int MT, int NT, int D) {
+int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
+                       int64_t k, int64_t n, void* y, int y_dtype, void* stream, int MT, int NT, int D) {
   const int64_t tiles_n = (n + 16 * NT - 1) / (16 * NT), mch = (m + 16 * MT - 1) / (16 * MT);
   const int64_t chunks = k / 128;
   const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
@@ -64,7 +64,7 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, const void* x, int x_dtype, const void* w,
   rlxq_x16_args xa;
   char* rest = nullptr;
   int rc;
-  if ((rc = prep_x16(ctx, x, x_dtype, m, k, true, part_bytes, xa, &rest, stream, true))) return rc;
+  if ((rc = prep_x16(ctx, x, x_dtype, m, k, scheme != RLXQ_GGUF_Q8_0, part_bytes, xa, &rest, stream, true))) return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
   a.x16 = xa.x16;
@@ -82,7 +82,7 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, const void* x, int x_dtype, const void* w,
   a.tiles_n = (int32_t)tiles_n;
   a.y_bf16 = y_dtype == RLXQ_BF16;
   char name[64];
-  std::snprintf(name, sizeof name, "rlxq_skinnyxr_q4_1_mt%d_nt%d_d%d", MT, NT, D);
+  std::snprintf(name, sizeof name, "rlxq_skinnyxr_%s_mt%d_nt%d_d%d", scheme_name(scheme), MT, NT, D);
   hipFunction_t fn;
   if ((rc = get_fn(ctx, name, &fn))) return rc;
   const size_t lds = 2 * (size_t)(MT * NT * 4) * 64 * 4;
@@ -110,9 +110,10 @@ bool skinny_applies(int scheme, int64_t m, int64_t k) {
 // [splits, M, N]) are added in split order.
 int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
                     int64_t k, int64_t n, void* y, int y_dtype, void* stream) {
-  // Q4_1: the register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR=
-  // "MT,NT,D" picks a compiled one, "0" the LDS-staged kernels below.
-  if (scheme == RLXQ_GGUF_Q4_1) {
+  // The register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR="MT,NT,D"
+  // picks a compiled one (every combination for Q4_1, the defaults for Q4_0
+  // and Q8_0), "0" the LDS-staged kernels below.
+  {
     int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = 2, xd = m <= 16 ? 4 : (m <= 32 ? 3 : 2);
     bool xr = true;
     if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
@@ -120,7 +121,7 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
       if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) xmt = a1, xnt = a2, xd = a3;
       else if (e[0] == '0') xr = false;
     }
-    if (xr) return skinny_xr_dispatch(ctx, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, xmt, xnt, xd);
+    if (xr) return skinny_xr_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, xmt, xnt, xd);
   }
   const int MT = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
   // blocks per thread per step (K per step = 64 * BPT); 2 measured fastest,

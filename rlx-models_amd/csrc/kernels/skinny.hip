@@ -374,20 +374,21 @@ RLXQ_DEV void skinny_dma_body(const rlxq_skinny_args& a) {
 }
 
 // ---------------------------------------------------------------------------
-// Register-streamed variant (Q4_1): no LDS stage and no barrier per step.
+// Register-streamed variant (GGUF Q4_1, Q4_0, Q8_0): no LDS stage and no
+// barrier per step.
 // The four waves of a workgroup take the same NT tiles of 16 weight rows and
 // split their K range in 4-block chunks (chunk c -> wave c % 4).  Lane
-// (j, g) = (lane % 16, lane / 16) loads all 20 bytes of block 4c + g of row
-// j of each tile (one 4-byte and one 16-byte load) into a ring of D chunks,
-// so D * NT * 20 bytes per lane are in flight.  The four MFMA steps i of a
-// chunk each take code dword i of every lane's block: across the lane groups
-// g a step's 32 K positions are positions 8i .. 8i + 7 of blocks 4c .. 4c + 3
-// (prepared activation order), and the A fragment of lane (m, g) is the 16
-// bytes of row m at block 4c + g, positions 8i .. 8i + 7, loaded with the
-// chunk.  The waves' sums are added in the fixed order (w0 + w2) + (w1 + w3).
-// ---------------------------------------------------------------------------
-template <int MT, int NT, int D>
+// (j, g) = (lane % 16, lane / 16) loads all the bytes of block 4c + g of row
+// j of each tile into a ring of D chunks, so D * NT blocks per lane are in
+// flight.  The four MFMA steps i of a chunk each take positions 8i .. 8i + 7
+// of every lane's block: across the lane groups g a step's 32 K positions
+// are positions 8i .. 8i + 7 of blocks 4c .. 4c + 3 (prepared activation
+// order), and the A fragment of lane (m, g) is the 16 bytes of row m at
+// block 4c + g, positions 8i .. 8i + 7, loaded with the chunk.  The waves'
+// sums are added in the fixed order (w0 + w2) + (w1 + w3).
+template <int SCH, int MT, int NT, int D>
 RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
+  constexpr int BDW = sk_bdw<SCH>();
   // wave index through readfirstlane: the chunk loop is wave-uniform
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
@@ -401,11 +402,21 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
   // chunks of this wave: wv + 4 it, it < cnt
   const int cnt = nchunk > wv ? (nchunk - wv + 3) / 4 : 0;
 
-  const uint8_t* wrow[NT];
+  rlxq_gemm_args ga;
+  ga.w = a.w;
+  ga.rb = a.rb;
+  ga.K = a.K;
+  ga.group = 32;
+  ga.sb_bf16 = 0;
+  ga.scales = nullptr;
+  ga.biases = nullptr;
+  int64_t wrow[NT];
+  bool wok[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     const int64_t n = n0 + 16 * t + j;
-    wrow[t] = a.w + (n < a.N ? n : a.N - 1) * a.rb + (kb / 32 + g) * 20;
+    wok[t] = n < a.N;
+    wrow[t] = wok[t] ? n : a.N - 1;
   }
   // activations in the fragment-major layout: piece i of chunk c for row m,
   // lane group g at ((4 c + i) M + m) 4 + g (16-byte pieces), so the A
@@ -420,17 +431,12 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
   }
 
   struct Stage {
-    uint32_t w[NT][5];
+    RawBlk<SCH> w[NT];
     uint4 x[MT][4];
   };
   auto load = [&](int c, Stage& st) {
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-      const uint8_t* p = wrow[t] + (int64_t)c * 80;
-      st.w[t][0] = ld_u32(p);
-      const uint4 q = ld_u128(p + 4);
-      st.w[t][1] = q.x; st.w[t][2] = q.y; st.w[t][3] = q.z; st.w[t][4] = q.w;
-    }
+    for (int t = 0; t < NT; t++) load_blk<SCH>(ga, wrow[t], kb / 32 + 4 * c + g, wok[t], st.w[t]);
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
@@ -452,11 +458,14 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
   // in flight); the last chunks, already in the ring, are computed after.
   auto chunk_of = [&](int it) { return wv + 4 * it; };
   auto compute = [&](const Stage& st) {
+    uint32_t o[NT][BDW];
+#pragma unroll
+    for (int t = 0; t < NT; t++) normalise<SCH>(st.w[t], o[t]);
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        const f16x8_t b = dequant_lane<SCH_Q4_1>(st.w[t], i);
+        const f16x8_t b = dequant_lane<SCH>(o[t], i);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
           acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, st.x[mt][i]), b, acc[mt][t],
@@ -671,16 +680,23 @@ RLXQ_SKINNY_DMA_INST(1)
 RLXQ_SKINNY_DMA_INST(2)
 RLXQ_SKINNY_DMA_INST(4)
 
-// Register-streamed Q4_1 variants: rlxq_skinnyxr_q4_1_mt<MT>_nt<NT>_d<D>.
-#define RLXQ_SKINNYXR_INST(MT, NT, D)                                                                  \
-  extern "C" __global__ __launch_bounds__(256) void rlxq_skinnyxr_q4_1_mt##MT##_nt##NT##_d##D(          \
+// Register-streamed variants: rlxq_skinnyxr_<scheme>_mt<MT>_nt<NT>_d<D>.
+#define RLXQ_SKINNYXR_INST(SNAME, SCH, MT, NT, D)                                                      \
+  extern "C" __global__ __launch_bounds__(256) void rlxq_skinnyxr_##SNAME##_mt##MT##_nt##NT##_d##D(     \
       rlxq_skinny_args a) {                                                                            \
-    rlxq::skinny_xr_body<MT, NT, D>(a);                                                                \
+    rlxq::skinny_xr_body<SCH, MT, NT, D>(a);                                                           \
   }
-RLXQ_SKINNYXR_INST(1, 2, 4)
-RLXQ_SKINNYXR_INST(1, 4, 2)
-RLXQ_SKINNYXR_INST(1, 4, 3)
-RLXQ_SKINNYXR_INST(2, 2, 3)
-RLXQ_SKINNYXR_INST(2, 4, 2)
-RLXQ_SKINNYXR_INST(4, 2, 2)
-RLXQ_SKINNYXR_INST(4, 4, 1)
+RLXQ_SKINNYXR_INST(q4_1, SCH_Q4_1, 1, 2, 4)
+RLXQ_SKINNYXR_INST(q4_1, SCH_Q4_1, 1, 4, 2)
+RLXQ_SKINNYXR_INST(q4_1, SCH_Q4_1, 1, 4, 3)
+RLXQ_SKINNYXR_INST(q4_1, SCH_Q4_1, 2, 2, 3)
+RLXQ_SKINNYXR_INST(q4_1, SCH_Q4_1, 2, 4, 2)
+RLXQ_SKINNYXR_INST(q4_1, SCH_Q4_1, 4, 2, 2)
+RLXQ_SKINNYXR_INST(q4_1, SCH_Q4_1, 4, 4, 1)
+// the defaults only for the other schemes
+RLXQ_SKINNYXR_INST(q4_0, SCH_Q4_0, 1, 2, 4)
+RLXQ_SKINNYXR_INST(q4_0, SCH_Q4_0, 2, 2, 3)
+RLXQ_SKINNYXR_INST(q4_0, SCH_Q4_0, 4, 2, 2)
+RLXQ_SKINNYXR_INST(q8_0, SCH_Q8_0, 1, 2, 4)
+RLXQ_SKINNYXR_INST(q8_0, SCH_Q8_0, 2, 2, 3)
+RLXQ_SKINNYXR_INST(q8_0, SCH_Q8_0, 4, 2, 2)

@@ -119,3 +119,20 @@ def test_f32_activations_stay_exact(ctx, orc, monkeypatch):
     got, want = run_dense(ctx, orc, 3, x, packed, 256)
     assert ctx.last_kernel.startswith("rlxq_gemv"), ctx.last_kernel
     assert rel_err(got, want) <= TOL_F32
+
+
+@pytest.mark.parametrize("kernel", ["register", "lds"])
+@pytest.mark.parametrize("scheme", [1, 2])
+def test_skinny_q8_0_q4_0_both_kernels(ctx, orc, monkeypatch, scheme, kernel):
+    """Q8_0 (34-byte blocks) and Q4_0 (18-byte blocks) through the
+    register-streamed kernel and the LDS-staged one."""
+    if kernel == "lds":
+        monkeypatch.setenv("RLXQ_SKINNY_XR", "0")
+    for (m, k, n) in [(6, 256, 40), (16, 2048, 300), (40, 640, 96), (64, 4096, 130)]:
+        announce(f"skinny scheme={scheme} kernel={kernel} {(m, k, n)}")
+        rng = np.random.default_rng(scheme * 100 + m + k)
+        packed = orc.synth(scheme, rng, n, k)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt="bf16")
+        assert ctx.last_kernel.startswith("rlxq_skinnyxr_" if kernel == "register" else "rlxq_skinny_"), ctx.last_kernel
+        assert rel_err(got, want) <= TOL_F32, (m, k, n)
