@@ -163,9 +163,10 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   ga.ids = ids;
   ga.idx_f32 = idx;
   ga.n_entries = (int32_t)n_entries;
-  // fused: chunks number at most min(E, n) + n / MT, plus the one that zeroes
-  // the rows of invalid entries
-  const int64_t slots = fused ? fired_est + (n_entries + MT - 1) / MT + 1 : fired_est;
+  // fused: chunks number at most min(n, min(E, n) + n / MT) (each holds an
+  // entry), plus the one that zeroes the rows of invalid entries
+  const int64_t chunk_bound = std::min<int64_t>(n_entries, fired_est + (n_entries + MT - 1) / MT);
+  const int64_t slots = fused ? chunk_bound + 1 : fired_est;
   const int64_t grid = slots * ga.tiles_n;
   if (grid > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": grid too large");
   const size_t lds = xr ? 0 : (size_t)2 * (k / 32) * (xbf ? 20 : 36) * 4;

@@ -413,11 +413,15 @@ int rlxq_moe_route(rlxq_ctx* ctx, const float* logits, int64_t rows, int64_t num
   DeviceGuard g(ctx->device);
   hipFunction_t fn;
   int rc;
-  if ((rc = get_fn(ctx, "rlxq_moe_route_k", &fn))) return rc;
+  // register slots per lane: the smallest compiled count covering E
+  const int nper = num_experts <= 64 ? 1 : num_experts <= 128 ? 2 : num_experts <= 256 ? 4 : num_experts <= 512 ? 8 : 16;
+  char name[32];
+  std::snprintf(name, sizeof name, "rlxq_moe_route_k%d", nper);
+  if ((rc = get_fn(ctx, name, &fn))) return rc;
   int64_t R = rows;
   int E = (int)num_experts, K = (int)top_k, rn = renorm ? 1 : 0;
   void* args[] = {(void*)&logits, &R, &E, &K, &rn, (void*)&ids, (void*)&probs};
-  return launch(ctx, fn, dim3((unsigned)rows), dim3(64), 0, stream, args, "moe_route");
+  return launch(ctx, fn, dim3((unsigned)rows), dim3(64), 0, stream, args, name);
 }
 
 }  // extern "C"

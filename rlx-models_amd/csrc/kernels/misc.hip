@@ -164,37 +164,37 @@ RLXQ_DEV void wave_argmax(float& v, int& e) {
 
 // Router: softmax over E logits then top-k by probability, ties to the lower
 // expert id; optional renormalisation of the kept probabilities.  One wave per
-// row, E <= 1024; the reductions use DPP row moves and readlane.
-extern "C" __global__ __launch_bounds__(64) void rlxq_moe_route_k(
-    const float* __restrict__ logits, int64_t rows, int E, int topk, int renorm,
-    int32_t* __restrict__ ids, float* __restrict__ probs) {
+// row, E <= 64 * NPER (lane l holds experts l, l + 64, ...); the reductions
+// use DPP row moves and readlane.
+namespace rlxq {
+template <int NPER>
+RLXQ_DEV void moe_route_body(const float* __restrict__ logits, int64_t rows, int E, int topk, int renorm,
+                             int32_t* __restrict__ ids, float* __restrict__ probs) {
   const int64_t r = blockIdx.x;
   if (r >= rows) return;
   const int lane = threadIdx.x;
   const float* l = logits + r * E;
-  constexpr int MAXE = 1024 / 64;
-  const int nper = (E + 63) / 64;   // experts per lane actually present
-  float p[MAXE];
+  float p[NPER];
   float mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < MAXE; i++) {
+  for (int i = 0; i < NPER; i++) {
     const int e = lane + 64 * i;
-    p[i] = (i < nper && e < E) ? l[e] : -INFINITY;
+    p[i] = e < E ? l[e] : -INFINITY;
     mx = fmaxf(mx, p[i]);
   }
-  mx = rlxq::wave_reduce(mx, [](float x, float y) { return fmaxf(x, y); });
+  mx = wave_reduce(mx, [](float x, float y) { return fmaxf(x, y); });
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < MAXE; i++) {
+  for (int i = 0; i < NPER; i++) {
     const int e = lane + 64 * i;
-    p[i] = (i < nper && e < E) ? expf(p[i] - mx) : 0.f;
+    p[i] = e < E ? expf(p[i] - mx) : 0.f;
     s += p[i];
   }
-  s = rlxq::wave_reduce(s, [](float x, float y) { return x + y; });
+  s = wave_reduce(s, [](float x, float y) { return x + y; });
 #pragma unroll
-  for (int i = 0; i < MAXE; i++) {
+  for (int i = 0; i < NPER; i++) {
     const int e = lane + 64 * i;
-    p[i] = (i < nper && e < E) ? p[i] / s : -1.f;
+    p[i] = e < E ? p[i] / s : -1.f;
   }
   float kept = 0.f, sel_p = 0.f;
   int sel_e = 0;
@@ -203,21 +203,21 @@ extern "C" __global__ __launch_bounds__(64) void rlxq_moe_route_k(
     float bv = -2.f;
     int be = 0x7fffffff;
 #pragma unroll
-    for (int i = 0; i < MAXE; i++) {
+    for (int i = 0; i < NPER; i++) {
       const int e = lane + 64 * i;
-      if (i < nper && (p[i] > bv || (p[i] == bv && e < be))) {
+      if (p[i] > bv || (p[i] == bv && e < be)) {
         bv = p[i];
         be = e;
       }
     }
-    rlxq::wave_argmax(bv, be);
+    wave_argmax(bv, be);
     if (lane == j) {
       sel_p = bv;
       sel_e = be;
     }
     kept += bv;
 #pragma unroll
-    for (int i = 0; i < MAXE; i++)
+    for (int i = 0; i < NPER; i++)
       if (lane + 64 * i == be) p[i] = -1.f;
   }
   if (lane < topk) {
@@ -225,3 +225,16 @@ extern "C" __global__ __launch_bounds__(64) void rlxq_moe_route_k(
     probs[r * topk + lane] = renorm ? sel_p / kept : sel_p;
   }
 }
+}  // namespace rlxq
+
+#define RLXQ_ROUTE_INST(NPER)                                                                         \
+  extern "C" __global__ __launch_bounds__(64) void rlxq_moe_route_k##NPER(                            \
+      const float* __restrict__ logits, int64_t rows, int E, int topk, int renorm,                      \
+      int32_t* __restrict__ ids, float* __restrict__ probs) {                                           \
+    rlxq::moe_route_body<NPER>(logits, rows, E, topk, renorm, ids, probs);                             \
+  }
+RLXQ_ROUTE_INST(1)
+RLXQ_ROUTE_INST(2)
+RLXQ_ROUTE_INST(4)
+RLXQ_ROUTE_INST(8)
+RLXQ_ROUTE_INST(16)
