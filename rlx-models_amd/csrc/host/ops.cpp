@@ -108,46 +108,6 @@ int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const 
 // Prefill dequant-GEMM launch.  256 x 256 tiles (one workgroup per CU, 4
 // waves of 128 x 128) for M >= 256, else 128 x 128 tiles (4 waves of 64 x 64).
 // RLXQ_GEMM_TILE=128|256 forces one of them (tests, sweeps).
-// Q4_1 prefill on the f16 kernel: activations prepared as scaled f16 rows,
-// raw weight blocks in LDS, f16 MFMA.
-int gemmh_dispatch(rlxq_ctx* ctx, const void* x, const void* w, int64_t rb, int64_t m, int64_t k, int64_t n,
-                   void* y, int y_dtype, void* stream) {
-  rlxq_x16_args xa;
-  char* rest = nullptr;
-  int rc;
-  if ((rc = prep_x16(ctx, x, RLXQ_BF16, m, k, true, 0, xa, &rest, stream))) return rc;
-  // 8 waves (2 x 4) with loads two steps ahead; RLXQ_GEMMH=t256p2|t256w8p1|t256w8p2
-  // selects another compiled variant
-  char name[48] = "rlxq_gemmh_q4_1_t256w8p2";
-  if (const char* e = std::getenv("RLXQ_GEMMH")) {
-    if (!std::strcmp(e, "t256p2") || !std::strcmp(e, "t256w8p1") || !std::strcmp(e, "t256w8p2"))
-      std::snprintf(name, sizeof name, "rlxq_gemmh_q4_1_%s", e);
-  }
-  const unsigned threads = std::strstr(name, "w8") ? 512 : 256;
-  hipFunction_t fn;
-  if ((rc = get_fn(ctx, name, &fn))) return rc;
-  rlxq_gemmh_args a;
-  std::memset(&a, 0, sizeof a);
-  a.x16 = xa.x16;
-  a.inv_s = xa.inv_s;
-  a.w = static_cast<const uint8_t*>(w);
-  a.y = y;
-  a.M = m;
-  a.N = n;
-  a.K = k;
-  a.rb = rb;
-  a.y_ld = n;
-  a.y_bf16 = y_dtype == RLXQ_BF16 ? 1 : 0;
-  const int64_t tiles_m = (m + 255) / 256, tiles_n = (n + 255) / 256;
-  if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
-  a.tiles_m = (int32_t)tiles_m;
-  a.tiles_n = (int32_t)tiles_n;
-  const size_t lds = 2 * 256 * 72 * 2 + 2 * 256 * 11 * 4;
-  const int64_t grid = 8 * ((tiles_m * tiles_n + 7) / 8);
-  void* args[] = {&a};
-  return launch(ctx, fn, dim3((unsigned)grid), dim3(threads), lds, stream, args, name);
-}
-
 int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const void* w, const void* scales,
                   const void* biases, int sb_dtype, int64_t rb, int64_t m, int64_t k, int64_t n, void* y,
                   int y_dtype, void* stream) {
@@ -166,16 +126,17 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
     tile = std::atoi(e) == 128 ? 128 : 256;
     var = tile == 128 ? "" : (std::strncmp(e, "256w8", 5) == 0 ? e + 3 : "");
   }
-  // Q4_1 with f32 output: the f16 kernel, whose f16 weights keep the output
-  // within 1e-3 (bf16 weights do not); RLXQ_GEMM_TILE=f16 forces it for bf16
-  // output too, any other value a bf16 tiling.
-  {
-    const char* e = std::getenv("RLXQ_GEMM_TILE");
-    const bool q41 = scheme == RLXQ_GGUF_Q4_1 && k % 64 == 0;
-    if (q41 && ((!e && y_dtype == RLXQ_F32) || (e && !std::strcmp(e, "f16"))))
-      return gemmh_dispatch(ctx, x, w, rb, m, k, n, y, y_dtype, stream);
+  // GGUF with f32 output: the f16 variant of the 256 tiles, whose f16 weights
+  // keep the output within 1e-3 (bf16 weights do not)
+  if (!std::getenv("RLXQ_GEMM_TILE") && y_dtype == RLXQ_F32 && !is_mlx(scheme)) {
+    tile = 256;
+    var = bit8 ? "w8f" : "w8p2f";
   }
   const bool w8 = tile == 256 && var[0] == 'w';
+  // "...f": f16 weights and MFMA on the prepared f16 activations (GGUF)
+  const size_t vl = std::strlen(var);
+  const bool f16 = vl > 0 && var[vl - 1] == 'f';
+  if (f16 && is_mlx(scheme)) return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: no f16 GEMM for MLX codes");
   char name[64];
   std::snprintf(name, sizeof name, "rlxq_gemm_%s_t%d%s", scheme_name(scheme), tile, var);
   hipFunction_t fn;
@@ -184,6 +145,13 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
   rlxq_gemm_args a;
   std::memset(&a, 0, sizeof a);
   a.x = x;
+  if (f16) {
+    rlxq_x16_args xa;
+    char* rest = nullptr;
+    if ((rc = prep_x16(ctx, x, RLXQ_BF16, m, k, scheme != RLXQ_GGUF_Q8_0, 0, xa, &rest, stream))) return rc;
+    a.x = xa.x16;
+    a.inv_s = xa.inv_s;
+  }
   a.w = static_cast<const uint8_t*>(w);
   a.scales = scales;
   a.biases = biases;
@@ -228,13 +196,13 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
 
   // Prefill: bf16 activations and bf16 output with at least 64 rows go to the
   // MFMA dequant-GEMM (weights rounded to bf16 in LDS, fp32 accumulation);
-  // Q4_1 with f32 output past the batched-decode sizes (more than 256 rows) to
-  // the f16 GEMM, which meets the 1e-3 bar.  Everything else stays on the
+  // GGUF with f32 output past the batched-decode sizes (more than 256 rows)
+  // to its f16 variant, which meets the 1e-3 bar.  Everything else stays on the
   // GEMV family, which keeps the products exact.
   // RLXQ_PREFILL=gemv|gemm forces one of them where both apply (tests).
   {
     bool gemm_ok = xbf && k % 64 == 0 && m >= 1;
-    bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (scheme == RLXQ_GGUF_Q4_1 && m > 256));
+    bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (!is_mlx(scheme) && m > 256));
     if (const char* e = std::getenv("RLXQ_PREFILL")) {
       if (!std::strcmp(e, "gemv")) use_gemm = false;
       if (!std::strcmp(e, "gemm")) use_gemm = gemm_ok;

@@ -8,6 +8,7 @@
 #ifndef RLXQ_F16DQ_HIP_H
 #define RLXQ_F16DQ_HIP_H
 #include "common.hip.h"
+#include "gemm_dq.hip.h"
 
 namespace rlxq {
 
@@ -71,6 +72,20 @@ RLXQ_DEV f16x8_t dequant_lane(const uint32_t* bp, int g) {
     }
   }
   return f16x8_t{w[0].x, w[0].y, w[1].x, w[1].y, w[2].x, w[2].y, w[3].x, w[3].y};
+}
+
+// Raw block -> normalised dwords.
+template <int SCH>
+RLXQ_DEV void normalise(const RawBlk<SCH>& r, uint32_t* o) {
+  if constexpr (SCH == SCH_Q4_1) {
+    o[0] = r.h;
+    o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;
+  } else {
+    constexpr int NQ = SCH == SCH_Q8_0 ? 8 : 4;
+    o[0] = r.off ? (r.w[0] >> 16) : (r.w[0] & 0xffffu);
+#pragma unroll
+    for (int i = 0; i < NQ; i++) o[1 + i] = r.off ? r.w[i + 1] : align_bytes(r.w[i + 1], r.w[i], 2);
+  }
 }
 
 }  // namespace rlxq

@@ -146,7 +146,7 @@ RLXQ_DEV void gemm_body(const rlxq_gemm_args& a) {
 // MFMAs.  The loop body has no branches (row bounds are clamped addresses plus
 // selects), and the next step's LDS stores and conversions sit between the
 // MFMA groups of the current step.
-template <int SCH, int WGM, int WGN, int PF>
+template <int SCH, int WGM, int WGN, int PF, bool F16>
 RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   constexpr int BM = 256, BN = 256;
   constexpr int NT = 64 * WGM * WGN;
@@ -206,12 +206,20 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
     }
   };
   auto store_b = [&](const Stage& P, int buf, int q) {
-    uint32_t o[16];
-    conv_blk<SCH>(P.b[q], o);
     uint16_t* dst = Bs + (buf * BN + brl) * GLD + ((tid >> 8) + q) * 32;
+    if constexpr (F16) {
+      // f16 weights d*q + m (one rounding) in the prepared activation order
+      uint32_t o[sk_bdw<SCH>()];
+      normalise<SCH>(P.b[q], o);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      *reinterpret_cast<uint4*>(dst + 8 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+      for (int g = 0; g < 4; g++) *reinterpret_cast<f16x8_t*>(dst + 8 * g) = dequant_lane<SCH>(o, g);
+    } else {
+      uint32_t o[16];
+      conv_blk<SCH>(P.b[q], o);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        *reinterpret_cast<uint4*>(dst + 8 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    }
   };
 
   f32x16_t acc[TM][TN];
@@ -225,16 +233,28 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   auto compute_ks = [&](int cur, int ks) {
     const uint16_t* Ab = As + (cur * BM + wm * WM) * GLD;
     const uint16_t* Bb = Bs + (cur * BN + wn * WN) * GLD;
-    bf16x8_t af[TM], bfr[TN];
     const int kof = ks * 16 + 8 * (lane >> 5);
+    if constexpr (F16) {
+      f16x8_t af[TM], bfr[TN];
 #pragma unroll
-    for (int i = 0; i < TM; i++) af[i] = *reinterpret_cast<const bf16x8_t*>(Ab + (i * 32 + (lane & 31)) * GLD + kof);
+      for (int i = 0; i < TM; i++) af[i] = *reinterpret_cast<const f16x8_t*>(Ab + (i * 32 + (lane & 31)) * GLD + kof);
 #pragma unroll
-    for (int j = 0; j < TN; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(Bb + (j * 32 + (lane & 31)) * GLD + kof);
+      for (int j = 0; j < TN; j++) bfr[j] = *reinterpret_cast<const f16x8_t*>(Bb + (j * 32 + (lane & 31)) * GLD + kof);
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+      for (int i = 0; i < TM; i++)
 #pragma unroll
-      for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    } else {
+      bf16x8_t af[TM], bfr[TN];
+#pragma unroll
+      for (int i = 0; i < TM; i++) af[i] = *reinterpret_cast<const bf16x8_t*>(Ab + (i * 32 + (lane & 31)) * GLD + kof);
+#pragma unroll
+      for (int j = 0; j < TN; j++) bfr[j] = *reinterpret_cast<const bf16x8_t*>(Bb + (j * 32 + (lane & 31)) * GLD + kof);
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
   };
   auto store_all = [&](const Stage& P, int buf) {
     store_a(P, buf, 0);
@@ -299,194 +319,7 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
       for (int r = 0; r < 16; r++) {
         const int64_t m = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
         if (m < a.M && n < a.N) {
-          const float v = acc[i][j][r];
-          if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
-          else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
-        }
-      }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// f16 prefill GEMM for Q4_1 weights (rlxq_gemmh_q4_1_*).  The LDS holds the
-// weights as raw blocks (10 KB per 64-K step instead of 32 KB of converted
-// weights) and each wave turns the codes of its own B fragments into f16
-// with packed f16 arithmetic (exact codes, then d*q + m with one rounding)
-// right before the MFMA; the activations are the f16 rows prepared by
-// rlxq_x16_prep (scaled by a power of two, in the order the codes unpack),
-// so one 16-byte LDS read is one MFMA A fragment.  LDS writes are the
-// expensive direction on gfx950 (about half the read rate per CU), so this
-// cuts the bytes written per step from 64 KB to 42 KB and the weight bytes
-// read from 64 KB to 24 KB.  256 x 256 tile, 4 waves of 128 x 128 (4 x 4
-// tiles of v_mfma_f32_32x32x16_f16, accumulators in AGPRs), one barrier per
-// step, global loads two steps ahead.
-// ---------------------------------------------------------------------------
-template <int WGM, int WGN, int PF>
-RLXQ_DEV void gemmh_q41_body(const rlxq_gemmh_args& a) {
-  constexpr int BM = 256, BN = 256, BK = 64;
-  constexpr int ALD = 72;   // f16 per activation row in LDS (144 B rows)
-  constexpr int BLD = 11;   // dwords per weight row in LDS: 2 blocks x 5 + 1
-  constexpr int NT = 64 * WGM * WGN;
-  constexpr int WM = BM / WGM, WN = BN / WGN;
-  constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int AP = 2048 / NT;   // 16-byte activation chunks per thread per step
-  constexpr int BPT = 512 / NT;   // weight blocks per thread per step
-  extern __shared__ uint16_t smem[];
-  uint16_t* As = smem;                                           // [2][BM][ALD]
-  uint32_t* Bs = reinterpret_cast<uint32_t*>(smem + 2 * BM * ALD);  // [2][BN][BLD]
-
-  int tm, tn;
-  if (!tile_of(blockIdx.x, a.tiles_m, a.tiles_n, 4, tm, tn)) return;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wv % WGM, wn = wv / WGM;
-  const int l32 = lane & 31, h = lane >> 5;
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int KT = (int)(a.K / BK);
-
-  // activations: 256 rows x 128 B per step, AP chunks of 16 B per thread
-  int64_t arow[AP];
-  bool aok[AP];
-#pragma unroll
-  for (int i = 0; i < AP; i++) {
-    const int c = tid + NT * i, r = c >> 3;
-    aok[i] = m0 + r < a.M;
-    arow[i] = (aok[i] ? m0 + r : a.M - 1) * a.K + (c & 7) * 8;
-  }
-  // weights: thread -> row n0 + (tid & 255), blocks (tid >> 8) + q (NT / 256)
-  const int brl = tid & 255, bb0 = tid >> 8;
-  const bool bok = n0 + brl < a.N;
-  const uint8_t* wrow = a.w + (bok ? n0 + brl : a.N - 1) * a.rb;
-
-  struct Stage {
-    uint4 x[AP];
-    uint32_t b[5 * BPT];
-  };
-  auto gload = [&](int kt, Stage& P) {
-#pragma unroll
-    for (int i = 0; i < AP; i++) {
-      const uint4 v = *reinterpret_cast<const uint4*>(a.x16 + arow[i] + (int64_t)kt * BK);
-      P.x[i] = aok[i] ? v : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int q = 0; q < BPT; q++) {
-      const uint8_t* p = wrow + (int64_t)(2 * kt + bb0 + q * (NT / 256)) * 20;
-      const uint32_t dm = ld_u32(p);
-      const uint4 v = ld_u128(p + 4);
-      P.b[5 * q] = bok ? dm : 0u;   // d = m = 0: the weights of a missing row are zero
-      P.b[5 * q + 1] = v.x;
-      P.b[5 * q + 2] = v.y;
-      P.b[5 * q + 3] = v.z;
-      P.b[5 * q + 4] = v.w;
-    }
-  };
-  auto store_x = [&](const Stage& P, int buf) {
-#pragma unroll
-    for (int i = 0; i < AP; i++) {
-      const int c = tid + NT * i;
-      *reinterpret_cast<uint4*>(As + (buf * BM + (c >> 3)) * ALD + (c & 7) * 8) = P.x[i];
-    }
-  };
-  auto store_w = [&](const Stage& P, int buf) {
-#pragma unroll
-    for (int q = 0; q < BPT; q++) {
-      uint32_t* dst = Bs + (buf * BN + brl) * BLD + (bb0 + q * (NT / 256)) * 5;
-#pragma unroll
-      for (int i = 0; i < 5; i++) dst[i] = P.b[5 * q + i];
-    }
-  };
-
-  f32x16_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; i++)
-#pragma unroll
-    for (int j = 0; j < TN; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-
-  // block blk of buffer cur: its two 16-K MFMA steps.  Lane (l32, h) of
-  // step kk carries positions 8g .. 8g + 7 with g = 2 kk + h: activation row
-  // l32 of each A tile and code dword g of weight row l32 of each B tile.
-  auto compute_blk = [&](int cur, int blk) {
-    const uint16_t* Ab = As + (cur * BM + wm * WM) * ALD + blk * 32;
-    const uint32_t* Bb = Bs + (cur * BN + wn * WN) * BLD + blk * 5;
-    uint32_t dm[TN];
-#pragma unroll
-    for (int j = 0; j < TN; j++) dm[j] = Bb[(j * 32 + l32) * BLD];
-#pragma unroll
-    for (int kk = 0; kk < 2; kk++) {
-      const int g = 2 * kk + h;
-      f16x8_t af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; i++) af[i] = *reinterpret_cast<const f16x8_t*>(Ab + (i * 32 + l32) * ALD + 8 * g);
-#pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const uint32_t blkw[2] = {dm[j], Bb[(j * 32 + l32) * BLD + 1 + g]};
-        bf[j] = dequant_lane<SCH_Q4_1>(blkw, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-  };
-  // one K step: MFMAs from buffer `cur` while stage Pn goes into cur ^ 1
-  auto step = [&](int cur, const Stage& Pn) {
-    compute_blk(cur, 0);
-    store_x(Pn, cur ^ 1);
-    compute_blk(cur, 1);
-    store_w(Pn, cur ^ 1);
-  };
-
-  if constexpr (PF == 1) {
-    Stage P;
-    gload(0, P);
-    store_x(P, 0);
-    store_w(P, 0);
-    __syncthreads();
-    for (int kt = 0; kt + 1 < KT; kt++) {
-      gload(kt + 1, P);
-      step(kt & 1, P);
-      __syncthreads();
-    }
-  } else {
-    // two register stages, the loop unrolled by two so each is a fixed set
-    Stage P0, P1;
-    gload(0, P0);
-    gload(KT > 1 ? 1 : 0, P1);
-    store_x(P0, 0);
-    store_w(P0, 0);
-    __syncthreads();
-    int kt = 0;
-    for (; kt + 2 < KT; kt += 2) {
-      gload(kt + 2, P0);
-      step(0, P1);
-      __syncthreads();
-      gload(kt + 3 < KT ? kt + 3 : KT - 1, P1);
-      step(1, P0);
-      __syncthreads();
-    }
-    if (kt + 1 < KT) {
-      step(0, P1);
-      __syncthreads();
-    }
-  }
-  compute_blk((KT - 1) & 1, 0);
-  compute_blk((KT - 1) & 1, 1);
-
-  // epilogue: C[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2), reg 4*(i/8) + i%4
-#pragma unroll
-  for (int i = 0; i < TM; i++)
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int64_t m = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-      if (m >= a.M) continue;
-      const float is = a.inv_s[m];
-#pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const int64_t n = n0 + wn * WN + j * 32 + l32;
-        if (n < a.N) {
-          const float v = acc[i][j][r] * is;
+          const float v = F16 ? acc[i][j][r] * a.inv_s[m] : acc[i][j][r];
           if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
           else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
         }
@@ -508,28 +341,25 @@ RLXQ_GEMM_INST(rlxq_gemm_mlx8_t128, SCH_MLX8)
 
 #define RLXQ_GEMM256_INST(SNAME, SCH)                                                        \
   extern "C" __global__ __launch_bounds__(256, 1) void rlxq_gemm_##SNAME##_t256(rlxq_gemm_args a) { \
-    rlxq::gemm256_body<SCH, 2, 2, 1>(a);                                                           \
+    rlxq::gemm256_body<SCH, 2, 2, 1, false>(a);                                                    \
   }                                                                                                \
   extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8(rlxq_gemm_args a) { \
-    rlxq::gemm256_body<SCH, 2, 4, 1>(a);                                                           \
+    rlxq::gemm256_body<SCH, 2, 4, 1, false>(a);                                                    \
   }                                                                                                \
   extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8p2(rlxq_gemm_args a) { \
-    rlxq::gemm256_body<SCH, 2, 4, 2>(a);                                                           \
+    rlxq::gemm256_body<SCH, 2, 4, 2, false>(a);                                                    \
+  }
+// f16 weights converted once per workgroup into LDS, f16 MFMA on the prepared
+// activations (GGUF schemes): rlxq_gemm_<scheme>_t256w8[p2]f
+#define RLXQ_GEMM256F_INST(SNAME, SCH, PF, SUFFIX)                                           \
+  extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8##SUFFIX##f(rlxq_gemm_args a) { \
+    rlxq::gemm256_body<SCH, 2, 4, PF, true>(a);                                                    \
   }
 RLXQ_GEMM256_INST(q4_1, SCH_Q4_1)
 RLXQ_GEMM256_INST(q4_0, SCH_Q4_0)
 RLXQ_GEMM256_INST(q8_0, SCH_Q8_0)
 RLXQ_GEMM256_INST(mlx4, SCH_MLX4)
 RLXQ_GEMM256_INST(mlx8, SCH_MLX8)
-
-// rlxq_gemmh_q4_1_t256[w8][p1|p2]: 4 waves (2 x 2) or 8 waves (2 x 4), global
-// loads one or two steps ahead
-extern "C" __global__ __launch_bounds__(256, 1) void rlxq_gemmh_q4_1_t256p2(rlxq_gemmh_args a) {
-  rlxq::gemmh_q41_body<2, 2, 2>(a);
-}
-extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemmh_q4_1_t256w8p1(rlxq_gemmh_args a) {
-  rlxq::gemmh_q41_body<2, 4, 1>(a);
-}
-extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemmh_q4_1_t256w8p2(rlxq_gemmh_args a) {
-  rlxq::gemmh_q41_body<2, 4, 2>(a);
-}
+RLXQ_GEMM256F_INST(q4_1, SCH_Q4_1, 2, p2)
+RLXQ_GEMM256F_INST(q4_0, SCH_Q4_0, 2, p2)
+RLXQ_GEMM256F_INST(q8_0, SCH_Q8_0, 1, )

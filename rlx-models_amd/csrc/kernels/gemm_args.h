@@ -5,7 +5,10 @@
 #include <stdint.h>
 
 typedef struct rlxq_gemm_args {
-  const void* x;          /* [M, K] bf16 activations                      */
+  const void* x;          /* [M, K] bf16 activations; f16 kernels: the f16
+                             rows prepared by rlxq_x16_prep (scaled by a
+                             power of two, in the code-unpacking order)    */
+  const float* inv_s;     /* f16 kernels: [M] factors undoing the scaling */
   const uint8_t* w;       /* packed weight rows, row stride rb bytes      */
   const void* scales;     /* MLX: [N, K/group] (f32 or bf16), else NULL   */
   const void* biases;     /* MLX: [N, K/group], else NULL                 */
@@ -15,15 +18,5 @@ typedef struct rlxq_gemm_args {
   int32_t tiles_m, tiles_n;   /* output tile grid (256 x 256 kernels)     */
 } rlxq_gemm_args;
 
-/* The f16 prefill GEMM (4-bit codes): activations prepared as f16 rows scaled
- * by a power of two (x16, inv_s) in the order the codes unpack to. */
-typedef struct rlxq_gemmh_args {
-  const uint16_t* x16;    /* [M, K] prepared activations                  */
-  const float* inv_s;     /* [M] row factors undoing the scaling          */
-  const uint8_t* w;       /* packed weight rows, row stride rb bytes      */
-  void* y;                /* [M, N] output, leading dimension y_ld        */
-  int64_t M, N, K, rb, y_ld;
-  int32_t tiles_m, tiles_n, y_bf16, pad;
-} rlxq_gemmh_args;
 
 #endif

@@ -28,19 +28,6 @@ namespace rlxq {
 
 constexpr int SK_BN = 128;          // weight rows per workgroup
 
-// Raw block -> normalised dwords.
-template <int SCH>
-RLXQ_DEV void normalise(const RawBlk<SCH>& r, uint32_t* o) {
-  if constexpr (SCH == SCH_Q4_1) {
-    o[0] = r.h;
-    o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;
-  } else {
-    constexpr int NQ = SCH == SCH_Q8_0 ? 8 : 4;
-    o[0] = r.off ? (r.w[0] >> 16) : (r.w[0] & 0xffffu);
-#pragma unroll
-    for (int i = 0; i < NQ; i++) o[1 + i] = r.off ? r.w[i + 1] : align_bytes(r.w[i + 1], r.w[i], 2);
-  }
-}
 
 // BPT blocks per thread per step: 2 threads per weight row, so a step spans
 // NB = 2 * BPT blocks (KS = 32 * NB of K) and wave w contracts blocks

@@ -1,8 +1,8 @@
 """Parity of the prefill dequant-GEMM against the CPU oracle, through the C
 ABI: the bf16 kernels (weights rounded to bf16 in LDS, bf16 MFMA) and, for
-Q4_1, the f16 kernel (raw blocks in LDS, weights d*q + m rounded once to f16,
-activations scaled by a power of two into f16, f16 MFMA); fp32 accumulation
-throughout.  Bar: max|got - want| / max|want| <= 2e-2 with bf16 output (the
+the GGUF schemes, their f16 variant (weights d*q + m rounded once to f16 in
+LDS, activations scaled by a power of two into f16, f16 MFMA); fp32
+accumulation throughout.  Bar: max|got - want| / max|want| <= 2e-2 with bf16 output (the
 prefill contract), 1e-3 for the f16 kernel with f32 output; `want` is the
 oracle's dequantized weights contracted in float64 with the bf16 activations
 the kernel saw."""
@@ -149,41 +149,35 @@ def test_every_gemm_tiling(ctx, orc, scheme, monkeypatch):
         assert np.allclose(outs["128"], outs[t], rtol=1e-6, atol=1e-6 * np.abs(outs["128"]).max())
 
 
-@pytest.mark.parametrize("variant", ["t256p2", "t256w8p1", "t256w8p2"])
-@pytest.mark.parametrize("mkn", [(256, 64, 256), (300, 128, 272), (513, 192, 300), (64, 640, 520),
-                                 (1000, 4096, 384), (77, 12288, 96)], ids=str)
-def test_gemm_f16_kernel_q4_1(ctx, orc, monkeypatch, mkn, variant):
-    """The f16 prefill kernels on ragged tiles, one to 192 K steps (odd and
-    even counts): f32 output within 1e-3, bf16 output within the prefill bar."""
-    monkeypatch.setenv("RLXQ_PREFILL", "gemm")
-    monkeypatch.setenv("RLXQ_GEMM_TILE", "f16")
-    monkeypatch.setenv("RLXQ_GEMMH", variant)
-    m, k, n = mkn
-    announce(f"gemm f16 kernel {variant} {mkn}")
-    rng = np.random.default_rng(m + 3 * k + n)
-    packed = orc.synth_q4_1(rng, n, k)
-    x = rng.standard_normal((m, k)).astype(np.float32)
-    x[1] *= 300.0   # rows of different magnitude: per-row scaling
-    x[2] *= 1e-3
-    wd = orc.dequantize(3, packed, k).astype(np.float64)
-    got, xv = run_gemm(ctx, orc, 3, x, packed, n, ydt="f32")
-    assert ctx.last_kernel == f"rlxq_gemmh_q4_1_{variant}", ctx.last_kernel
-    want = xv.astype(np.float64) @ wd.T
-    assert rel_err(got, want) <= 1e-3
-    for r in (1, 2):
-        assert rel_err(got[r:r + 1], want[r:r + 1]) <= 1e-3, r
-    got, xv = run_gemm(ctx, orc, 3, x, packed, n, ydt="bf16")
-    assert rel_err(got, want) <= TOL_PREFILL
-
-
-def test_f32_output_prefill_takes_the_f16_kernel(ctx, orc):
-    """Q4_1, bf16 activations, f32 output, past the batched-decode sizes: the
+@pytest.mark.parametrize("scheme", [1, 2, 3])
+def test_f32_output_prefill_takes_the_f16_kernel(ctx, orc, scheme):
+    """GGUF, bf16 activations, f32 output, past the batched-decode sizes: the
     dispatcher picks the f16 GEMM, and the output meets the 1e-3 bar."""
     m, k, n = 384, 1024, 520
-    rng = np.random.default_rng(11)
-    packed = orc.synth_q4_1(rng, n, k)
+    rng = np.random.default_rng(11 + scheme)
+    packed = orc.synth(scheme, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    got, xv = run_gemm(ctx, orc, 3, x, packed, n, ydt="f32")
-    assert ctx.last_kernel.startswith("rlxq_gemmh_q4_1_"), ctx.last_kernel
-    wd = orc.dequantize(3, packed, k).astype(np.float64)
+    got, xv = run_gemm(ctx, orc, scheme, x, packed, n, ydt="f32")
+    assert ctx.last_kernel.endswith("f"), ctx.last_kernel
+    wd = orc.dequantize(scheme, packed, k).astype(np.float64)
+    assert rel_err(got, xv.astype(np.float64) @ wd.T) <= 1e-3
+
+
+@pytest.mark.parametrize("scheme", [1, 2, 3])
+@pytest.mark.parametrize("mkn", [(256, 64, 256), (300, 640, 272), (513, 1280, 300), (1000, 4096, 520)], ids=str)
+def test_gemm_f16_shared_conversion(ctx, orc, monkeypatch, scheme, mkn):
+    """256 x 256 tiles with the weights converted once per workgroup to f16
+    and f16 MFMA on the prepared activations: f32 output within 1e-3."""
+    monkeypatch.setenv("RLXQ_PREFILL", "gemm")
+    tile = "256w8f" if scheme == 1 else "256w8p2f"
+    monkeypatch.setenv("RLXQ_GEMM_TILE", tile)
+    m, k, n = mkn
+    announce(f"gemm f16 shared conversion t{tile} scheme={scheme} {mkn}")
+    rng = np.random.default_rng(scheme * 7 + m + k + n)
+    packed = orc.synth(scheme, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[0] *= 500.0
+    got, xv = run_gemm(ctx, orc, scheme, x, packed, n, ydt="f32")
+    assert ctx.last_kernel.endswith(f"_t{tile}"), ctx.last_kernel
+    wd = orc.dequantize(scheme, packed, k).astype(np.float64)
     assert rel_err(got, xv.astype(np.float64) @ wd.T) <= 1e-3
