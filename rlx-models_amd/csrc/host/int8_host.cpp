@@ -28,7 +28,7 @@ struct W8a8Cfg {
 const W8a8Cfg kW8a8[] = {
     {"m128n128k64w22", 128, 128, 64, 2, 2},  {"m128n128k128w22", 128, 128, 128, 2, 2},
     {"m256n128k64w22", 256, 128, 64, 2, 2},  {"m128n256k64w22", 128, 256, 64, 2, 2},
-    {"m256n256k64w24", 256, 256, 64, 2, 4},
+    {"m256n256k64w24", 256, 256, 64, 2, 4},  {"m128n128k128w22_p2", 128, 128, 128, 2, 2},
 };
 
 // Tiling choice; RLXQ_W8A8_CFG=<name> selects one (tuning sweeps and the

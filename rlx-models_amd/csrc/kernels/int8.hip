@@ -63,7 +63,7 @@ RLXQ_DEV void w8a8_epilogue(const rlxq_w8a8_args& a, const i32x16_t (&acc)[TM][T
 // of BK bytes; each wave computes a (BM/WGM) x (BN/WGN) sub-tile from 32x32
 // MFMA tiles.  Global loads of step k+1 are in flight during the MFMAs of step
 // k; LDS tiles are double-buffered with one barrier per step.
-template <int BM, int BN, int BK, int WGM, int WGN, int GM>
+template <int BM, int BN, int BK, int WGM, int WGN, int GM, int PF>
 RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
   constexpr int NT = WGM * WGN * 64;
   constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -85,34 +85,59 @@ RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int KT = (int)((a.K + BK - 1) / BK);
 
-  uint4 ar[AP], br[BP];
-  auto load = [&](int kt) {
+  // Loads are branch-free: out-of-range chunks read a clamped, valid address
+  // and are replaced by zeros with selects (K and N are multiples of 16).
+  struct Stage {
+    uint4 a[AP], b[BP];
+  };
+  // loop-invariant parts of the chunk addresses: activation row (clamped),
+  // K offset of the chunk within the step; weight column (clamped), K row
+  // of the chunk within the step
+  const int8_t* abase[AP];
+  bool amok[AP];
+  int akof[AP];
+#pragma unroll
+  for (int i = 0; i < AP; i++) {
+    const int c = tid + NT * i, r = c / ACH, cc = c % ACH;
+    amok[i] = m0 + r < a.M;
+    abase[i] = a.qx + (amok[i] ? m0 + r : a.M - 1) * a.K;
+    akof[i] = 16 * cc;
+  }
+  const int8_t* bbase[BP];
+  bool bnok[BP];
+  int bkr[BP];
+#pragma unroll
+  for (int i = 0; i < BP; i++) {
+    const int c = tid + NT * i, r = c / BCH, cc = c % BCH;
+    bnok[i] = n0 + 16 * cc < a.N;
+    bbase[i] = a.wq + (bnok[i] ? n0 + 16 * cc : a.N - 16);
+    bkr[i] = r;
+  }
+  auto load = [&](int kt, Stage& P) {
     const int64_t k0 = (int64_t)kt * BK;
 #pragma unroll
     for (int i = 0; i < AP; i++) {
-      const int c = tid + NT * i, r = c / ACH, cc = c % ACH;
-      const int64_t m = m0 + r, k = k0 + 16 * cc;
-      ar[i] = make_uint4(0u, 0u, 0u, 0u);
-      if (m < a.M && k < a.K) ar[i] = *reinterpret_cast<const uint4*>(a.qx + m * a.K + k);
+      const int64_t k = k0 + akof[i];
+      const uint4 v = *reinterpret_cast<const uint4*>(abase[i] + (k < a.K ? k : a.K - 16));
+      P.a[i] = (amok[i] && k < a.K) ? v : make_uint4(0u, 0u, 0u, 0u);
     }
 #pragma unroll
     for (int i = 0; i < BP; i++) {
-      const int c = tid + NT * i, r = c / BCH, cc = c % BCH;
-      const int64_t k = k0 + r, n = n0 + 16 * cc;
-      br[i] = make_uint4(0u, 0u, 0u, 0u);
-      if (k < a.K && n < a.N) br[i] = *reinterpret_cast<const uint4*>(a.wq + k * a.N + n);
+      const int64_t k = k0 + bkr[i];
+      const uint4 v = *reinterpret_cast<const uint4*>(bbase[i] + (k < a.K ? k : a.K - 1) * a.N);
+      P.b[i] = (bnok[i] && k < a.K) ? v : make_uint4(0u, 0u, 0u, 0u);
     }
   };
-  auto store = [&](int buf) {
+  auto store = [&](const Stage& P, int buf) {
 #pragma unroll
     for (int i = 0; i < AP; i++) {
       const int c = tid + NT * i, r = c / ACH, cc = c % ACH;
-      *reinterpret_cast<uint4*>(As + (buf * BM + r) * AST + 16 * cc) = ar[i];
+      *reinterpret_cast<uint4*>(As + (buf * BM + r) * AST + 16 * cc) = P.a[i];
     }
 #pragma unroll
     for (int i = 0; i < BP; i++) {
       const int c = tid + NT * i, r = c / BCH, cc = c % BCH;
-      *reinterpret_cast<uint4*>(Bs + (buf * BK + r) * BST + 16 * cc) = br[i];
+      *reinterpret_cast<uint4*>(Bs + (buf * BK + r) * BST + 16 * cc) = P.b[i];
     }
   };
 
@@ -124,14 +149,8 @@ RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
-  load(0);
-  store(0);
-  __syncthreads();
   const int g = lane >> 4, s = lane & 15;
-  for (int kt = 0; kt < KT; kt++) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) load(kt + 1);
+  auto compute = [&](int cur) {
     const uint8_t* Ab = As + (cur * BM + wm * WM) * AST;
     const uint8_t* Bb = Bs + cur * BK * BST + wn * WN;
 #pragma unroll
@@ -153,8 +172,46 @@ RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bq[j], acc[i][j], 0, 0, 0);
     }
-    if (more) store(cur ^ 1);
+  };
+  if constexpr (PF == 1) {
+    Stage P;
+    load(0, P);
+    store(P, 0);
     __syncthreads();
+    for (int kt = 0; kt < KT; kt++) {
+      const bool more = kt + 1 < KT;
+      if (more) load(kt + 1, P);
+      compute(kt & 1);
+      if (more) store(P, (kt & 1) ^ 1);
+      __syncthreads();
+    }
+  } else {
+    // global loads two K steps ahead in two register stages, the loop
+    // unrolled by two so each stage is a fixed register set
+    Stage P0, P1;
+    load(0, P0);
+    load(KT > 1 ? 1 : 0, P1);
+    store(P0, 0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 2 < KT; kt += 2) {
+      load(kt + 2, P0);
+      compute(0);
+      store(P1, 1);
+      __syncthreads();
+      load(kt + 3 < KT ? kt + 3 : KT - 1, P1);
+      compute(1);
+      store(P0, 0);
+      __syncthreads();
+    }
+    if (kt + 1 < KT) {
+      compute(0);
+      store(P1, 1);
+      __syncthreads();
+      compute(1);
+    } else {
+      compute(0);
+    }
   }
   w8a8_epilogue<TM, TN>(a, acc, m0 + wm * WM, n0 + wn * WN, lane);
 }
@@ -298,13 +355,20 @@ RLXQ_DEV void i8b_body(const rlxq_i8b_args& a) {
 #define RLXQ_W8A8_INST(BM, BN, BK, WGM, WGN)                                                        \
   extern "C" __global__ __launch_bounds__(WGM * WGN * 64) void rlxq_w8a8_m##BM##n##BN##k##BK##w##WGM##WGN( \
       rlxq_w8a8_args a) {                                                                          \
-    rlxq::w8a8_body<BM, BN, BK, WGM, WGN, 8>(a);                                                   \
+    rlxq::w8a8_body<BM, BN, BK, WGM, WGN, 8, 1>(a);                                                \
+  }
+// global loads two K steps ahead: ..._p2
+#define RLXQ_W8A8_INST_P2(BM, BN, BK, WGM, WGN)                                                     \
+  extern "C" __global__ __launch_bounds__(WGM * WGN * 64, 1) void rlxq_w8a8_m##BM##n##BN##k##BK##w##WGM##WGN##_p2( \
+      rlxq_w8a8_args a) {                                                                          \
+    rlxq::w8a8_body<BM, BN, BK, WGM, WGN, 8, 2>(a);                                                \
   }
 RLXQ_W8A8_INST(128, 128, 64, 2, 2)
 RLXQ_W8A8_INST(128, 128, 128, 2, 2)
 RLXQ_W8A8_INST(256, 128, 64, 2, 2)
 RLXQ_W8A8_INST(128, 256, 64, 2, 2)
 RLXQ_W8A8_INST(256, 256, 64, 2, 4)
+RLXQ_W8A8_INST_P2(128, 128, 128, 2, 2)
 
 #define RLXQ_I8B_INST(MT, XN, XBF)                                                        \
   extern "C" __global__ __launch_bounds__(256) void rlxq_i8b_##XN##_mt##MT(rlxq_i8b_args a) { \
