@@ -364,8 +364,11 @@ int rlxq_quantize_act_int8(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m,
   int rc;
   if ((rc = get_fn(ctx, "rlxq_quant_act_i8", &fn))) return rc;
   int xb = x_dtype == RLXQ_BF16, K = (int)k;
+  // 16-element vector chunks need 16-byte aligned rows of x and q
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  int vec = (k % 16 == 0 && a16(x) && a16(q)) ? 1 : 0;
   int64_t M = m;
-  void* args[] = {(void*)&x, &xb, &M, &K, (void*)&q, (void*)&scales};
+  void* args[] = {(void*)&x, &xb, &M, &K, (void*)&q, (void*)&scales, &vec};
   return launch(ctx, fn, dim3((unsigned)m), dim3(256), 0, stream, args, "quantize_act_int8");
 }
 

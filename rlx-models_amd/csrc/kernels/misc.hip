@@ -87,29 +87,92 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_swiglu_k(
 // clamped to +-127.  One workgroup of 256 threads per row.
 extern "C" __global__ __launch_bounds__(256) void rlxq_quant_act_i8(
     const void* __restrict__ x, int x_bf16, int64_t M, int K, int8_t* __restrict__ q,
-    float* __restrict__ scales) {
+    float* __restrict__ scales, int vec) {
+  // 16-element chunks (vec: 16-byte aligned rows, else every element goes
+  // through the scalar loops): RB per thread stay in registers between the amax pass
+  // and the quantisation (one 16-byte store each); chunks past 256 * RB and
+  // the K % 16 tail are read again.  Per element the arithmetic is the
+  // scalar rule: q = clamp(round(x * (1 / (amax / 127))), -127, 127).
+  constexpr int RB = 3;
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
   if (r >= M) return;
-  auto ld = [&](int c) -> float {
+  const int t = threadIdx.x;
+  const int nch = vec ? K >> 4 : 0;
+  auto ld16 = [&](int c, float* v) {
+    if (x_bf16) {
+      const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + r * K + 16 * c);
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const uint4 u = p[h];
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          v[8 * h + 2 * e] = bf16_bits_to_f32(w[e] & 0xffffu);
+          v[8 * h + 2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+        }
+      }
+    } else {
+      const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + r * K + 16 * c);
+#pragma unroll
+      for (int h = 0; h < 4; h++) {
+        const float4 u = p[h];
+        v[4 * h] = u.x; v[4 * h + 1] = u.y; v[4 * h + 2] = u.z; v[4 * h + 3] = u.w;
+      }
+    }
+  };
+  auto ld1 = [&](int c) -> float {
     if (x_bf16) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(x)[r * K + c]);
     return reinterpret_cast<const float*>(x)[r * K + c];
   };
+  float v[RB][16];
   float amax = 0.f;
-  for (int c = threadIdx.x; c < K; c += blockDim.x) amax = fmaxf(amax, fabsf(ld(c)));
+#pragma unroll
+  for (int i = 0; i < RB; i++) {
+    const int c = t + 256 * i;
+    if (c < nch) {
+      ld16(c, v[i]);
+#pragma unroll
+      for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(v[i][e]));
+    }
+  }
+  for (int c = t + 256 * RB; c < nch; c += 256) {
+    float w[16];
+    ld16(c, w);
+#pragma unroll
+    for (int e = 0; e < 16; e++) amax = fmaxf(amax, fabsf(w[e]));
+  }
+  for (int c = 16 * nch + t; c < K; c += 256) amax = fmaxf(amax, fabsf(ld1(c)));
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  if ((t & 63) == 0) red[t >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float s = amax > 0.f ? __fdiv_rn(amax, 127.0f) : 1.0f;
   const float inv = __fdiv_rn(1.0f, s);
-  for (int c = threadIdx.x; c < K; c += blockDim.x) {
-    float v = roundf(__fmul_rn(ld(c), inv));
-    v = fminf(fmaxf(v, -127.f), 127.f);
-    q[r * K + c] = (int8_t)v;
+  auto quant = [&](float xv) -> uint32_t {
+    const float qv = fminf(fmaxf(roundf(__fmul_rn(xv, inv)), -127.f), 127.f);
+    return (uint32_t)(uint8_t)(int8_t)qv;
+  };
+  auto st16 = [&](int c, const float* w) {
+    uint32_t o[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+      o[d] = quant(w[4 * d]) | (quant(w[4 * d + 1]) << 8) | (quant(w[4 * d + 2]) << 16) | (quant(w[4 * d + 3]) << 24);
+    *reinterpret_cast<uint4*>(q + r * K + 16 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+  };
+#pragma unroll
+  for (int i = 0; i < RB; i++) {
+    const int c = t + 256 * i;
+    if (c < nch) st16(c, v[i]);
   }
-  if (threadIdx.x == 0) scales[r] = s;
+  for (int c = t + 256 * RB; c < nch; c += 256) {
+    float w[16];
+    ld16(c, w);
+    st16(c, w);
+  }
+  for (int c = 16 * nch + t; c < K; c += 256) q[r * K + c] = (int8_t)(int)fminf(fmaxf(roundf(__fmul_rn(ld1(c), inv)), -127.f), 127.f);
+  if (t == 0) scales[r] = s;
 }
 
 namespace rlxq {

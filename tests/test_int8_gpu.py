@@ -49,7 +49,7 @@ def _w8(rng, k, n):
 
 
 # ---------------------------------------------------------------- quantiser
-@pytest.mark.parametrize("m,k", [(1, 64), (3, 1000), (17, 4096), (64, 12288)])
+@pytest.mark.parametrize("m,k", [(1, 64), (3, 1000), (17, 4096), (64, 12288), (2, 12800), (5, 4104)])
 @pytest.mark.parametrize("xdt", ["f32", "bf16"])
 def test_quantize_act_int8_bit_exact(ctx, orc, rng, m, k, xdt):
     import torch
