@@ -2,6 +2,7 @@
 // int8 activation quantisation and the MoE router.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -111,32 +112,40 @@ int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const 
 int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const void* w, const void* scales,
                   const void* biases, int sb_dtype, int64_t rb, int64_t m, int64_t k, int64_t n, void* y,
                   int y_dtype, void* stream) {
-  // Tiling from a measured cost model: a round of resident 128 x 128 tiles
-  // (two workgroups per CU) takes ~0.65 of a round of 256 x 256 tiles (one
-  // per CU, 8 waves), per unit of K.
+  // 256 x 256 tiles, 8 waves, global loads two K steps ahead (one for the
+  // 8-bit schemes, whose larger raw blocks do not fit two stages in 256
+  // VGPRs).  When the tiles do not cover the CUs, K is split so that they do
+  // (at most 8 slices of at least 8 K steps) and the slices' f32 partial sums
+  // are added in slice order.  RLXQ_GEMM_TILE=128|256|256w8|256w8p2|...f
+  // forces a tiling (the 128 x 128 one never splits); RLXQ_GEMM_SPLITS=<n>
+  // forces the slice count.
   const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-  const int64_t t128 = ((m + 127) / 128) * ((n + 127) / 128), t256 = ((m + 255) / 256) * ((n + 255) / 256);
-  const double c128 = 0.7 * (double)((t128 + 2 * cus - 1) / (2 * cus)), c256 = (double)((t256 + cus - 1) / cus);
-  int tile = c256 < c128 ? 256 : 128;
-  // 256 tiles: 8 waves, global loads two K steps ahead, except for the 8-bit
-  // schemes whose larger raw blocks do not fit two stages in 256 VGPRs
+  int tile = 256;
   const bool bit8 = scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_MLX_AFFINE8;
-  const char* var = tile == 256 ? (bit8 ? "w8" : "w8p2") : "";
-  if (const char* e = std::getenv("RLXQ_GEMM_TILE")) {
-    tile = std::atoi(e) == 128 ? 128 : 256;
-    var = tile == 128 ? "" : (std::strncmp(e, "256w8", 5) == 0 ? e + 3 : "");
+  const char* var = bit8 ? "w8" : "w8p2";
+  const char* te = std::getenv("RLXQ_GEMM_TILE");
+  if (te) {
+    tile = std::atoi(te) == 128 ? 128 : 256;
+    var = tile == 128 ? "" : (std::strncmp(te, "256w8", 5) == 0 ? te + 3 : "");
   }
   // GGUF with f32 output: the f16 variant of the 256 tiles, whose f16 weights
   // keep the output within 1e-3 (bf16 weights do not)
-  if (!std::getenv("RLXQ_GEMM_TILE") && y_dtype == RLXQ_F32 && !is_mlx(scheme)) {
-    tile = 256;
-    var = bit8 ? "w8f" : "w8p2f";
-  }
+  if (!te && y_dtype == RLXQ_F32 && !is_mlx(scheme)) var = bit8 ? "w8f" : "w8p2f";
   const bool w8 = tile == 256 && var[0] == 'w';
   // "...f": f16 weights and MFMA on the prepared f16 activations (GGUF)
   const size_t vl = std::strlen(var);
   const bool f16 = vl > 0 && var[vl - 1] == 'f';
   if (f16 && is_mlx(scheme)) return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: no f16 GEMM for MLX codes");
+  const int64_t tiles_m = (m + tile - 1) / tile, tiles_n = (n + tile - 1) / tile;
+  if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
+  const int64_t tiles = tiles_m * tiles_n, ksteps = k / 64;
+  int64_t splits = 1;
+  if (tile == 256) {
+    while (tiles * splits * 2 <= cus && splits < 8 && ksteps / (splits * 2) >= 8) splits *= 2;
+    if (const char* e = std::getenv("RLXQ_GEMM_SPLITS")) splits = std::max<int64_t>(1, std::min<int64_t>(std::atoi(e), ksteps));
+  }
+  const int64_t kslice = ((ksteps + splits - 1) / splits) * 64;
+  splits = (k + kslice - 1) / kslice;
   char name[64];
   std::snprintf(name, sizeof name, "rlxq_gemm_%s_t%d%s", scheme_name(scheme), tile, var);
   hipFunction_t fn;
@@ -145,12 +154,17 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
   rlxq_gemm_args a;
   std::memset(&a, 0, sizeof a);
   a.x = x;
+  const size_t part_bytes = splits > 1 ? (((size_t)(splits * m * n) * 4 + 255) & ~(size_t)255) : 0;
+  char* part = nullptr;
   if (f16) {
     rlxq_x16_args xa;
-    char* rest = nullptr;
-    if ((rc = prep_x16(ctx, x, RLXQ_BF16, m, k, scheme != RLXQ_GGUF_Q8_0, 0, xa, &rest, stream))) return rc;
+    if ((rc = prep_x16(ctx, x, RLXQ_BF16, m, k, scheme != RLXQ_GGUF_Q8_0, part_bytes, xa, &part, stream))) return rc;
     a.x = xa.x16;
     a.inv_s = xa.inv_s;
+  } else if (part_bytes) {
+    void* ws = nullptr;
+    if ((rc = workspace(ctx, part_bytes, &ws))) return rc;
+    part = static_cast<char*>(ws);
   }
   a.w = static_cast<const uint8_t*>(w);
   a.scales = scales;
@@ -164,18 +178,38 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
   a.group = is_mlx(scheme) ? group : 32;
   a.sb_bf16 = sb_dtype == RLXQ_BF16 ? 1 : 0;
   a.y_bf16 = y_dtype == RLXQ_BF16 ? 1 : 0;
-  const int64_t tiles_m = (m + tile - 1) / tile, tiles_n = (n + tile - 1) / tile;
-  if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
   a.tiles_m = (int32_t)tiles_m;
   a.tiles_n = (int32_t)tiles_n;
+  a.part = splits > 1 ? reinterpret_cast<float*>(part) : nullptr;
+  a.kslice = (int32_t)kslice;
+  a.splits = (int32_t)splits;
   void* args[] = {&a};
   if (tile == 128) {
     const size_t lds = 2 * (128 + 128) * 72 * sizeof(uint16_t);
-    return launch(ctx, fn, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), lds, stream, args, name);
+    return launch(ctx, fn, dim3((unsigned)tiles), dim3(256), lds, stream, args, name);
   }
   const size_t lds = 2 * (256 + 256) * 72 * sizeof(uint16_t);
-  const int64_t grid = 8 * ((tiles_m * tiles_n + 7) / 8);
-  return launch(ctx, fn, dim3((unsigned)grid), dim3(w8 ? 512 : 256), lds, stream, args, name);
+  const int64_t grid = 8 * ((tiles + 7) / 8) * splits;
+  if ((rc = launch(ctx, fn, dim3((unsigned)grid), dim3(w8 ? 512 : 256), lds, stream, args, name))) return rc;
+  if (splits > 1) {
+    // slice partial sums, added in slice order (the batched-decode reduction)
+    rlxq_skinny_args r;
+    std::memset(&r, 0, sizeof r);
+    r.part = a.part;
+    r.y = y;
+    r.M = m;
+    r.N = n;
+    r.y_ld = n;
+    r.splits = (int32_t)splits;
+    r.y_bf16 = a.y_bf16;
+    hipFunction_t fr;
+    if ((rc = get_fn(ctx, "rlxq_skinny_reduce", &fr))) return rc;
+    void* rargs[] = {&r};
+    const int64_t total = m * n;
+    rc = launch(ctx, fr, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, rargs, "rlxq_skinny_reduce");
+    if (!rc) ctx->last_kernel = name;
+  }
+  return rc;
 }
 
 int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dtype, const void* w,

@@ -159,12 +159,19 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   uint16_t* As = smem;                // [2][BM][GLD]
   uint16_t* Bs = smem + 2 * BM * GLD;  // [2][BN][GLD]
 
+  // workgroup = (K slice, tile): the slice is the slowest index, so the
+  // tiles of one slice keep the XCD-aware order
+  const int tiles_pad = 8 * ((a.tiles_m * a.tiles_n + 7) / 8);
+  const int sp = blockIdx.x / tiles_pad;
   int tm, tn;
-  if (!tile_of(blockIdx.x, a.tiles_m, a.tiles_n, 4, tm, tn)) return;
+  if (!tile_of(blockIdx.x % tiles_pad, a.tiles_m, a.tiles_n, 4, tm, tn)) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wm = wv % WGM, wn = wv / WGM;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int KT = (int)(a.K / GBK);
+  const int64_t kbeg = (int64_t)sp * a.kslice;
+  const int64_t kend = kbeg + a.kslice < a.K ? kbeg + a.kslice : a.K;
+  const int KT = (int)((kend - kbeg) / GBK);
+  const int kt0 = (int)(kbeg / GBK);
   const uint16_t* xg = reinterpret_cast<const uint16_t*>(a.x);
 
   // activation tile: 256 rows x 128 B = 2048 chunks of 16 B
@@ -190,6 +197,7 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
     RawBlk<SCH> b[BPT];
   };
   auto gload = [&](int kt, Stage& P) {
+    kt += kt0;
 #pragma unroll
     for (int i = 0; i < AP; i++) {
       const uint4 v = *reinterpret_cast<const uint4*>(xg + arow[i] + (int64_t)kt * GBK);
@@ -320,7 +328,8 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
         const int64_t m = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
         if (m < a.M && n < a.N) {
           const float v = F16 ? acc[i][j][r] * a.inv_s[m] : acc[i][j][r];
-          if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
+          if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
+          else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
           else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
         }
       }

@@ -16,6 +16,11 @@ typedef struct rlxq_gemm_args {
   int64_t M, N, K, rb, y_ld;
   int32_t group, sb_bf16, y_bf16, pad;
   int32_t tiles_m, tiles_n;   /* output tile grid (256 x 256 kernels)     */
+  /* split-K (256 x 256 kernels): workgroup = (K slice, tile); slice sp
+   * covers K [sp * kslice, (sp + 1) * kslice) and, when splits > 1, writes
+   * f32 partial sums to part [splits, M, N] instead of y                  */
+  float* part;
+  int32_t kslice, splits;
 } rlxq_gemm_args;
 
 

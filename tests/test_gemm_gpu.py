@@ -181,3 +181,64 @@ def test_gemm_f16_shared_conversion(ctx, orc, monkeypatch, scheme, mkn):
     assert ctx.last_kernel.endswith(f"_t{tile}"), ctx.last_kernel
     wd = orc.dequantize(scheme, packed, k).astype(np.float64)
     assert rel_err(got, xv.astype(np.float64) @ wd.T) <= 1e-3
+
+
+@pytest.mark.parametrize("scheme", [1, 2, 3, 4])
+@pytest.mark.parametrize("tile_ydt", [("256w8p2", "bf16"), ("256w8", "f32"), ("256w8p2f", "f32"), ("256w8f", "f32")],
+                         ids=lambda t: f"{t[0]}-{t[1]}")
+@pytest.mark.parametrize("splits", [2, 3, 8])
+def test_gemm_split_k(ctx, orc, monkeypatch, scheme, tile_ydt, splits):
+    """K cut into slices (the last one shorter when the steps do not divide),
+    slice partial sums added in slice order: within the bar against the
+    oracle, and within 1e-5 of the unsplit kernel (f32 output)."""
+    import rlxq
+
+    tile, ydt = tile_ydt
+    if tile.endswith("f") and scheme == rlxq.MLX_AFFINE4:
+        pytest.skip("the f16 GEMM serves GGUF codes only")
+    if tile == "256w8f" and scheme != 1 or tile == "256w8p2f" and scheme == 1:
+        pytest.skip("one f16 tiling per scheme")
+    m, k, n = 300, 64 * 13, 520
+    rng = np.random.default_rng(31 * scheme + splits)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    kw = {}
+    if scheme == rlxq.MLX_AFFINE4:
+        codes = rng.integers(0, 16, (n, k)).astype(np.uint32)
+        wq = orc.mlx_pack(codes, 4)
+        sc = rng.uniform(0.01, 0.1, (n, k // 64)).astype(np.float32)
+        bi = rng.uniform(-0.5, 0.1, (n, k // 64)).astype(np.float32)
+        packed = wq.view(np.uint8)
+        kw = dict(group=64, scales=_t(sc), biases=_t(bi))
+        wd = orc.mlx_dequantize(wq, sc, bi, k, 4, 64).astype(np.float64)
+    else:
+        packed = orc.synth(scheme, rng, n, k)
+        wd = orc.dequantize(scheme, packed, k).astype(np.float64)
+    monkeypatch.setenv("RLXQ_PREFILL", "gemm")
+    monkeypatch.setenv("RLXQ_GEMM_TILE", tile)
+    outs = {}
+    for sp in (1, splits):
+        monkeypatch.setenv("RLXQ_GEMM_SPLITS", str(sp))
+        announce(f"gemm split-k t{tile} scheme={scheme} splits={sp} ydt={ydt}")
+        got, xv = run_gemm(ctx, orc, scheme, x, packed, n, ydt=ydt, **kw)
+        assert ctx.last_kernel.endswith(f"_t{tile}"), ctx.last_kernel
+        tol = 1e-3 if tile.endswith("f") else TOL_PREFILL
+        assert rel_err(got, xv.astype(np.float64) @ wd.T) <= tol
+        outs[sp] = got
+    if ydt == "f32":
+        assert rel_err(outs[splits], outs[1]) <= 1e-5
+
+
+@pytest.mark.parametrize("mkn", [(512, 12288, 4096), (2048, 12288, 4096), (256, 4096, 24576)], ids=str)
+def test_gemm_default_split_on_small_grids(ctx, orc, mkn):
+    """Prefill shapes whose 256 x 256 tiles do not cover the CUs: the
+    dispatcher splits K by itself; the output stays within the bar."""
+    m, k, n = mkn
+    announce(f"gemm default split {mkn}")
+    rng = np.random.default_rng(m + n)
+    packed = orc.synth_q4_1(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got, xv = run_gemm(ctx, orc, 3, x, packed, n)
+    assert ctx.last_kernel.startswith("rlxq_gemm_q4_1_t256"), ctx.last_kernel
+    w = orc.dequantize(3, packed, k).astype(np.float32)
+    want = (xv @ w.T).astype(np.float64)
+    assert rel_err(got, want) <= TOL_PREFILL
