@@ -202,11 +202,7 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
     r.y_ld = n;
     r.splits = (int32_t)splits;
     r.y_bf16 = a.y_bf16;
-    hipFunction_t fr;
-    if ((rc = get_fn(ctx, "rlxq_skinny_reduce", &fr))) return rc;
-    void* rargs[] = {&r};
-    const int64_t total = m * n;
-    rc = launch(ctx, fr, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, rargs, "rlxq_skinny_reduce");
+    rc = splits_reduce(ctx, r, stream);
     if (!rc) ctx->last_kernel = name;
   }
   return rc;
@@ -287,7 +283,7 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   const int64_t nchunk64 = (units + 63) / 64;
   const int64_t xr_max = scheme == RLXQ_GGUF_Q4_0 ? 4 : 6;
   int xr_nu = (int)(nchunk64 == 5 ? 6 : nchunk64), xr_d = nchunk64 <= 3 ? 2 : 1, xr_w = 8;
-  bool use_xr = m == 1 && xbf && xr_scheme && nchunk64 <= xr_max;
+  bool use_xr = m == 1 && xbf && xr_scheme && nchunk64 <= xr_max && n < (int64_t(1) << 31);
   int xr_lds = 1;   // 1: the activations pass through LDS once per workgroup
   if (const char* e = std::getenv("RLXQ_GEMV_XR")) {
     int nu, d, wv, xs = 0;
@@ -305,7 +301,7 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     std::snprintf(name, sizeof name, "rlxq_gemvx%s_%s_U%d_D%d_W%d", xr_lds ? "s" : "r", scheme_name(scheme), xr_nu,
                   xr_d, xr_w);
     if ((rc = get_fn(ctx, name, &fn))) return rc;
-    const size_t lds = xr_lds ? (size_t)k * 2 : 0;
+    const size_t lds = xr_lds ? (size_t)(k / 32) * 68 : 0;   // pair records + block sums
     const int per_cu = blocks_per_cu(ctx, name, fn, 64 * xr_w, lds);
     const int64_t wgs_needed = (n + xr_w - 1) / xr_w;
     int64_t gx = (int64_t)ctx->cu_count * per_cu;

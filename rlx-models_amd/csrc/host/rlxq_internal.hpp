@@ -73,6 +73,9 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
                   const void* scales, const void* biases, int sb_dtype, int64_t m, int64_t k,
                   int64_t n, void* y, int y_dtype, void* stream);
 bool skinny_applies(int scheme, int64_t m, int64_t k);
+// Adds the [splits, M, N] f32 partial sums in a.part into a.y (y_ld, y_bf16)
+// in slice order.
+int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream);
 // x [m, k] -> prepared f16 activations (x16) and row factors (inv_s) at the
 // start of the workspace; `extra` further bytes follow at *rest.
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bool nibble, size_t extra,

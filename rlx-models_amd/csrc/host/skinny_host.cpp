@@ -20,6 +20,15 @@ size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // x -> prepared f16 activations and row scales in the workspace (x16 at
 // the start, inv_s after it; `extra` more bytes follow for the caller).
+int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream) {
+  hipFunction_t fn;
+  int rc;
+  if ((rc = get_fn(ctx, "rlxq_skinny_reduce", &fn))) return rc;
+  const int64_t per = a.N % 4 == 0 ? 4 : 1, threads = (a.M * a.N + per - 1) / per;
+  void* rargs[] = {&a};
+  return launch(ctx, fn, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, rargs, "rlxq_skinny_reduce");
+}
+
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bool nibble, size_t extra,
              rlxq_x16_args& xa, char** rest, void* stream, bool frag_major) {
   const size_t x16_bytes = round256((size_t)(m * k) * 2), s_bytes = round256((size_t)m * 4);
@@ -89,10 +98,7 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   void* args[] = {&a};
   if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name))) return rc;
   if (splits > 1) {
-    if ((rc = get_fn(ctx, "rlxq_skinny_reduce", &fn))) return rc;
-    const int64_t total = m * n;
-    void* rargs[] = {&a};
-    rc = launch(ctx, fn, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, rargs, "rlxq_skinny_reduce");
+    rc = splits_reduce(ctx, a, stream);
     if (!rc) ctx->last_kernel = name;
   }
   return rc;
@@ -197,10 +203,7 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   void* args[] = {&a};
   if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name))) return rc;
   if (splits > 1) {
-    if ((rc = get_fn(ctx, "rlxq_skinny_reduce", &fn))) return rc;
-    const int64_t total = m * n;
-    void* rargs[] = {&a};
-    rc = launch(ctx, fn, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, rargs, "rlxq_skinny_reduce");
+    rc = splits_reduce(ctx, a, stream);
     if (!rc) ctx->last_kernel = name;
   }
   return rc;

@@ -238,16 +238,10 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   // to be wave-uniform (scalar branches), so the compiler's wait counts can
   // keep the ring's loads in flight across iterations
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t G = (int64_t)gridDim.x * WAVES;
-  const int64_t n0 = (int64_t)blockIdx.x * WAVES + wv;
-  // rows of this wave: n0 + s * G, s < cnt
-  const int64_t cnt = n0 < a.N ? (a.N - n0 + G - 1) / G : 0;
-  // output row and factor of the activation row (loop invariants, loaded
-  // before any weights so that waiting for them never waits for the ring)
-  int64_t yrow = 0;
-  float ysc = 1.f;
-  if (a.row_map) yrow = a.row_map[0];
-  if (a.row_scale) ysc = a.row_scale[0];
+  // rows of this wave: n0 + s * G, s < cnt (N < 2^31: 32-bit division)
+  const uint32_t G = gridDim.x * WAVES, n0u = blockIdx.x * WAVES + wv, N32 = (uint32_t)a.N;
+  const int64_t n0 = n0u;
+  const int64_t cnt = n0u < N32 ? (N32 - n0u + G - 1) / G : 0;
   const int gpr = MLX ? K / a.group : 0;
 
   int uc[NU];
@@ -277,63 +271,122 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     }
   };
 
-  // activations of my units (raw bf16 pairs): straight from global memory, or
-  // (XLDS) copied once per workgroup into LDS and read from there, so the
-  // row of x crosses L2 once per workgroup rather than once per wave.  The
-  // first D rows of weights are requested right after the activations.
+  // Activations of my units as bf16 pairs in the code-extraction order, and
+  // their block sums.  XR: each lane loads its units' raw activations from
+  // global memory and builds the pairs itself.  XLDS: the workgroup builds
+  // them once in LDS (so the row of x crosses L2 once per workgroup and each
+  // element is converted once): thread t takes half-blocks t, t + 64*WAVES,
+  // ...; half h of block b is the 16 elements whose pairs fill dwords
+  // 8h..8h+7 of the block's record (GGUF nibble order: elements 8h..8h+7 and
+  // 16+8h..16+8h+7; MLX order: 16h..16h+15), and the two halves' sums are
+  // added through a lane swap.  LDS: [bpr][16] pair dwords, then [bpr] sums.
+  // Either way the first D rows of weights are requested right after the
+  // activation loads.
   uint32_t X[NU][BLOCKS][16];
-  const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x);
+  float S[NU][BLOCKS];
+  const uint16_t* xg = reinterpret_cast<const uint16_t*>(a.x);
   Buf ring[D];
   if constexpr (XLDS) {
-    extern __shared__ __align__(16) uint16_t xs[];
-    constexpr int XCH = (4 * NU * BLOCKS + WAVES - 1) / WAVES;   // 16-byte chunks per thread
-    uint4 xv[XCH];
+    extern __shared__ __align__(16) uint32_t xs[];
+    float* xsum = reinterpret_cast<float*>(xs + bpr * 16);
+    constexpr int NT = 64 * WAVES;
+    constexpr int XH = (2 * 64 * NU * BLOCKS + NT - 1) / NT;   // half-blocks per thread
+    constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;
+    uint4 xa[XH], xc[XH];
 #pragma unroll
-    for (int i = 0; i < XCH; i++) {
-      const int c = threadIdx.x + 64 * WAVES * i;
-      xv[i] = c < K / 8 ? *reinterpret_cast<const uint4*>(xb + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int i = 0; i < D; i++) load(n0 + (i < cnt ? i : cnt - 1) * G, ring[i]);
-#pragma unroll
-    for (int i = 0; i < XCH; i++) {
-      const int c = threadIdx.x + 64 * WAVES * i;
-      if (c < K / 8) *reinterpret_cast<uint4*>(xs + 8 * c) = xv[i];
-    }
-    __syncthreads();
-    xb = xs;
-  }
-#pragma unroll
-  for (int c = 0; c < NU; c++)
-#pragma unroll
-    for (int bl = 0; bl < BLOCKS; bl++) {
-      const uint4* p = reinterpret_cast<const uint4*>(xb + (int64_t)(uc[c] * BLOCKS + bl) * 32);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint4 v = p[q];
-        X[c][bl][4 * q] = v.x; X[c][bl][4 * q + 1] = v.y; X[c][bl][4 * q + 2] = v.z; X[c][bl][4 * q + 3] = v.w;
+    for (int i = 0; i < XH; i++) {
+      const int hb = threadIdx.x + NT * i, b = hb >> 1, h = hb & 1;
+      xa[i] = xc[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (hb < 2 * bpr) {
+        const uint16_t* p = xg + (int64_t)b * 32;
+        xa[i] = *reinterpret_cast<const uint4*>(p + (MLX ? 16 * h : 8 * h));
+        xc[i] = *reinterpret_cast<const uint4*>(p + (MLX ? 16 * h + 8 : 16 + 8 * h));
       }
     }
-  if constexpr (!XLDS) {
 #pragma unroll
     for (int i = 0; i < D; i++) load(n0 + (i < cnt ? i : cnt - 1) * G, ring[i]);
+#pragma unroll
+    for (int i = 0; i < XH; i++) {
+      const int hb = threadIdx.x + NT * i, b = hb >> 1, h = hb & 1;
+      const uint32_t A[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w}, C[4] = {xc[i].x, xc[i].y, xc[i].z, xc[i].w};
+      uint32_t P[8];
+#pragma unroll
+      for (int t = 0; t < 2; t++) {
+        if constexpr (MLX) {
+          const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7
+          P[4 * t + 0] = perm_b32(R[2], R[0], LO);
+          P[4 * t + 1] = perm_b32(R[2], R[0], HI);
+          P[4 * t + 2] = perm_b32(R[3], R[1], LO);
+          P[4 * t + 3] = perm_b32(R[3], R[1], HI);
+        } else {
+          P[4 * t + 0] = perm_b32(A[2 * t + 1], A[2 * t], LO);
+          P[4 * t + 2] = perm_b32(A[2 * t + 1], A[2 * t], HI);
+          P[4 * t + 1] = perm_b32(C[2 * t + 1], C[2 * t], LO);
+          P[4 * t + 3] = perm_b32(C[2 * t + 1], C[2 * t], HI);
+        }
+      }
+      float sh = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; q++) sh = dot2_bf16(A[q], 0x3F803F80u, sh);
+#pragma unroll
+      for (int q = 0; q < 4; q++) sh = dot2_bf16(C[q], 0x3F803F80u, sh);
+      const float so = __shfl_xor(sh, 1, 64);
+      if (hb < 2 * bpr) {
+        uint4* dst = reinterpret_cast<uint4*>(xs + b * 16 + 8 * h);
+        dst[0] = make_uint4(P[0], P[1], P[2], P[3]);
+        dst[1] = make_uint4(P[4], P[5], P[6], P[7]);
+        if (h == 0) xsum[b] = sh + so;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NU; c++)
+#pragma unroll
+      for (int bl = 0; bl < BLOCKS; bl++) {
+        const int blk = uc[c] * BLOCKS + bl;
+        const uint4* p = reinterpret_cast<const uint4*>(xs + blk * 16);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const uint4 v = p[q];
+          X[c][bl][4 * q] = v.x; X[c][bl][4 * q + 1] = v.y; X[c][bl][4 * q + 2] = v.z; X[c][bl][4 * q + 3] = v.w;
+        }
+        S[c][bl] = xsum[blk];
+      }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NU; c++)
+#pragma unroll
+      for (int bl = 0; bl < BLOCKS; bl++) {
+        const uint4* p = reinterpret_cast<const uint4*>(xg + (int64_t)(uc[c] * BLOCKS + bl) * 32);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const uint4 v = p[q];
+          X[c][bl][4 * q] = v.x; X[c][bl][4 * q + 1] = v.y; X[c][bl][4 * q + 2] = v.z; X[c][bl][4 * q + 3] = v.w;
+        }
+      }
+#pragma unroll
+    for (int i = 0; i < D; i++) load(n0 + (i < cnt ? i : cnt - 1) * G, ring[i]);
+#pragma unroll
+    for (int c = 0; c < NU; c++)
+#pragma unroll
+      for (int bl = 0; bl < BLOCKS; bl++) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) s = dot2_bf16(X[c][bl][i], 0x3F803F80u, s);
+        S[c][bl] = s;
+        uint32_t R[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) R[i] = X[c][bl][i];
+        pairs_from_raw<SCH>(R, X[c][bl]);
+      }
   }
 
-  // pairs and block sums
-  float S[NU][BLOCKS];
-#pragma unroll
-  for (int c = 0; c < NU; c++)
-#pragma unroll
-    for (int bl = 0; bl < BLOCKS; bl++) {
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; i++) s = dot2_bf16(X[c][bl][i], 0x3F803F80u, s);
-      S[c][bl] = s;
-      uint32_t R[16];
-#pragma unroll
-      for (int i = 0; i < 16; i++) R[i] = X[c][bl][i];
-      pairs_from_raw<SCH>(R, X[c][bl]);
-    }
+  // output row and factor of the activation row (scalar loads, issued after
+  // the weights; used only by the stores)
+  int64_t yrow = 0;
+  float ysc = 1.f;
+  if (a.row_map) yrow = a.row_map[0];
+  if (a.row_scale) ysc = a.row_scale[0];
 
   const UnpackK kc = unpack_consts();
   // Row s of the wave uses ring slot s % D.  While D more rows follow a full

@@ -633,12 +633,47 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
 }
 
 // Split-K partial sums added in split order.
+// Four outputs per thread when N % 4 == 0 (up to eight slices' loads in
+// flight), one otherwise; either way each output adds the slices in slice
+// order, starting from zero.
 extern "C" __global__ __launch_bounds__(256) void rlxq_skinny_reduce(rlxq_skinny_args a) {
+  const int64_t mn = a.M * a.N;
+  if ((a.N & 3) == 0) {
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i >= mn) return;
+    const int64_t m = i / a.N, n = i - m * a.N;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < a.splits; s0 += 8) {
+      const int cnt = a.splits - s0 < 8 ? a.splits - s0 : 8;
+      float4 v[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++)
+        if (q < cnt) v[q] = *reinterpret_cast<const float4*>(a.part + (int64_t)(s0 + q) * mn + i);
+#pragma unroll
+      for (int q = 0; q < 8; q++)
+        if (q < cnt) {
+          s[0] += v[q].x;
+          s[1] += v[q].y;
+          s[2] += v[q].z;
+          s[3] += v[q].w;
+        }
+    }
+    if (a.y_bf16) {
+      uint16_t* yp = reinterpret_cast<uint16_t*>(a.y) + m * a.y_ld + n;
+#pragma unroll
+      for (int e = 0; e < 4; e++) yp[e] = (uint16_t)f32_to_bf16_bits(s[e]);
+    } else {
+      float* yp = reinterpret_cast<float*>(a.y) + m * a.y_ld + n;
+#pragma unroll
+      for (int e = 0; e < 4; e++) yp[e] = s[e];
+    }
+    return;
+  }
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= a.M * a.N) return;
+  if (i >= mn) return;
   const int64_t m = i / a.N, n = i - m * a.N;
   float v = 0.f;
-  for (int sp = 0; sp < a.splits; sp++) v += a.part[(int64_t)sp * a.M * a.N + i];
+  for (int sp = 0; sp < a.splits; sp++) v += a.part[(int64_t)sp * mn + i];
   if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
   else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
 }
