@@ -136,6 +136,28 @@ class Context:
     def last_kernel(self) -> str:
         return lib().rlxq_last_kernel(self.h).decode()
 
+    def bind_dequant_matmul(self, x, w, scheme: int, n: int, *, y, stream, group: int = 32, scales=None,
+                            biases=None):
+        """A zero-argument callable that runs dequant_matmul on these tensors.
+
+        The C arguments are converted once, as a compiled caller's FFI binding
+        holds them, so a call costs the C entry point and not this module's
+        argument handling (decode launches are a few microseconds each).  The
+        tensors must stay alive while the callable is used."""
+        m, k = x.shape
+        sb = _dt(scales) if scales is not None else F32
+        fn = lib().rlxq_dequant_matmul
+        args = (self.h, C.c_int(scheme), C.c_int(group), C.c_void_p(_ptr(x)), C.c_int(_dt(x)), C.c_void_p(_ptr(w)),
+                C.c_void_p(_ptr(scales)), C.c_void_p(_ptr(biases)), C.c_int(sb), C.c_int64(m), C.c_int64(k),
+                C.c_int64(n), C.c_void_p(_ptr(y)), C.c_int(_dt(y)), C.c_void_p(_stream(stream)))
+
+        def call():
+            rc = fn(*args)
+            if rc != OK:
+                self._check(rc, "dequant_matmul")
+
+        return call
+
     def dequant_matmul(self, x, w, scheme: int, n: int, *, group: int = 32, scales=None, biases=None,
                        y=None, y_dtype=None, stream=None):
         """y[m, n] = x[m, k] . dequant(w)^T; returns y (allocated if not given)."""

@@ -346,3 +346,23 @@ def test_every_xr_variant(ctx, orc, monkeypatch, cfg, scheme):
             packed = orc.synth(scheme, rng, n, k)
             got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt="bf16")
         assert rel_err(got, want) <= TOL_F32, (cfg, k, n)
+
+
+def test_bound_call_matches_plain_call(ctx, orc):
+    """The pre-bound launch (arguments converted once) writes the same output
+    as the plain call, on repeated calls."""
+    import torch
+    import rlxq
+
+    k, n = 4096, 1000
+    rng = np.random.default_rng(77)
+    packed = orc.synth_q4_1(rng, n, k)
+    x = _t(rng.standard_normal((1, k)).astype(np.float32)).to(torch.bfloat16)
+    w = _t(packed)
+    want = ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_1, n)
+    y = torch.full((1, n), float("nan"), device="cuda")
+    call = ctx.bind_dequant_matmul(x, w, rlxq.GGUF_Q4_1, n, y=y, stream=torch.cuda.current_stream().cuda_stream)
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    assert torch.equal(y, want)
