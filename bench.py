@@ -270,6 +270,103 @@ def batched_section(ctx, gen, sptr, stream) -> dict:
     return res
 
 
+def synth_q4_0_gpu(n: int, k: int, gen):
+    """Q4_0 rows on the device: codes ~U{0..15}, d ~U(0.005, 0.05) fp16."""
+    import torch
+
+    nb = n * (k // 32)
+    d = torch.empty(nb, device="cuda").uniform_(0.005, 0.05, generator=gen).half().view(torch.uint8).view(nb, 2)
+    q = torch.randint(0, 256, (nb, 16), device="cuda", dtype=torch.uint8, generator=gen)
+    return torch.cat([d, q], dim=1).contiguous().view(-1)
+
+
+def synth_mlx_gpu(n: int, k: int, bits: int, group: int, gen):
+    """MLX affine rows on the device: u32 code words (random bits), bf16 scale
+    ~U(0.01, 0.1) and bias ~U(-0.5, 0.1) slabs [n, k / group]."""
+    import torch
+
+    codes = torch.randint(0, 256, (n * k * bits // 8,), device="cuda", dtype=torch.uint8, generator=gen)
+    sc = torch.empty((n, k // group), device="cuda").uniform_(0.01, 0.1, generator=gen).to(torch.bfloat16)
+    bi = torch.empty((n, k // group), device="cuda").uniform_(-0.5, 0.1, generator=gen).to(torch.bfloat16)
+    return codes, sc, bi
+
+
+def schemes_section(ctx, gen, sptr, stream) -> dict:
+    """The other weight formats of the op at M=1 (bf16 activations, f32
+    output) on the gate_up shape 4096->24576, weights rotated past the MALL:
+    GGUF Q4_0, MLX affine 4/8-bit (group 64, bf16 slabs), Int8Block (i8
+    [K, N] with an f32 scale per column); the MLX 4-bit grouped op at the
+    MoE config's gate|up shape; and the bit-exact dequantisation kernel
+    (Q4_1 to f32).  Bytes: weights (+ scale slabs) + activations + outputs."""
+    import torch
+    import rlxq
+
+    res = {}
+    k, n = 4096, 24576
+    x = torch.randn((1, k), generator=gen, device="cuda").to(torch.bfloat16)
+    y = torch.empty((1, n), device="cuda")
+
+    def measure(label, wbytes, make, call):
+        ws = [make() for _ in range(_copies(wbytes))]
+        run = lambda i: call(ws[i % len(ws)])
+        for i in range(len(ws)):
+            run(i)
+        torch.cuda.synchronize()
+        us = _time_us(run, 4 * len(ws), stream)
+        b = wbytes + k * 2 + n * 4
+        res[label] = {"kernel": ctx.last_kernel, "us": round(us, 2), "GBps": round(b / us / 1e3, 1),
+                      "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        del ws
+        torch.cuda.empty_cache()
+
+    measure("q4_0_gemv_m1", n * k * 18 / 32, lambda: synth_q4_0_gpu(n, k, gen),
+            lambda w: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_0, n, y=y, stream=sptr))
+    for bits in (4, 8):
+        wb = n * k * bits / 8 + 2 * n * (k // 64) * 2
+        measure(f"mlx{bits}_g64_gemv_m1", wb, lambda bits=bits: synth_mlx_gpu(n, k, bits, 64, gen),
+                lambda w, bits=bits: ctx.dequant_matmul(x, w[0], rlxq.MLX_AFFINE4 if bits == 4 else rlxq.MLX_AFFINE8,
+                                                        n, group=64, scales=w[1], biases=w[2], y=y, stream=sptr))
+    measure("int8_block_gemv_m1", n * k + n * 4,
+            lambda: (torch.randint(-127, 128, (k, n), device="cuda", dtype=torch.int8, generator=gen),
+                     torch.rand((n,), device="cuda", generator=gen) * 0.01 + 1e-4),
+            lambda w: ctx.dequant_matmul(x, w[0], rlxq.INT8_BLOCK, n, group=k, scales=w[1], y=y, stream=sptr))
+
+    # MLX 4-bit grouped op: 128 (token, slot) rows over 128 experts of the
+    # MoE gate|up shape 2048->1536 (two banks alternate, 452 MB > MALL)
+    E, H, N2, R = 128, 2048, 1536, 128
+    banks = [synth_mlx_gpu(E * N2, H, 4, 64, gen) for _ in range(2)]
+    xg = torch.randn((R, H), generator=gen, device="cuda").to(torch.bfloat16)
+    idx = torch.randint(0, E, (R,), device="cuda", generator=gen).float()
+    yg = torch.empty((R, N2), device="cuda")
+    run = lambda i: ctx.grouped_matmul(xg, banks[i % 2][0], idx, rlxq.MLX_AFFINE4, N2, E, group=64,
+                                       scales=banks[i % 2][1], biases=banks[i % 2][2], y=yg, stream=sptr)
+    run(0)
+    run(1)
+    torch.cuda.synchronize()
+    us = _time_us(run, 20, stream)
+    uniq = int(torch.unique(idx).numel())
+    b = uniq * (N2 * H / 2 + 2 * N2 * (H // 64) * 2) + R * H * 2 + R * N2 * 4
+    res["mlx4_grouped_gate_up"] = {"kernel": ctx.last_kernel, "us": round(us, 2), "unique_experts": uniq,
+                                   "GBps": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                                   "launches": "device routing table from the f32 indices, then the grouped GEMV"}
+    del banks
+    torch.cuda.empty_cache()
+
+    # dequantisation to f32 (bytes: packed rows read + f32 written)
+    wq = [synth_q4_1_gpu(n, k, gen) for _ in range(2)]
+    out = torch.empty((n, k), device="cuda")
+    run = lambda i: ctx.dequantize(wq[i % 2], rlxq.GGUF_Q4_1, n, k, out=out, stream=sptr)
+    run(0)
+    torch.cuda.synchronize()
+    us = _time_us(run, 10, stream)
+    b = n * k * Q4_1_BPW + n * k * 4
+    res["dequantize_q4_1_f32"] = {"kernel": ctx.last_kernel, "us": round(us, 2), "GBps": round(b / us / 1e3, 1),
+                                  "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del wq, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def moe_section(ctx, gen, sptr, stream) -> dict:
     """Config 5: one MoE FFN of a Qwen3-30B-A3B-like layer for 16 tokens, as
     three launches: route (softmax of N(0,1) logits over 128 experts, top-8,
@@ -424,6 +521,7 @@ def main() -> int:
         out["prefill"] = prefill_section(ctx, gen, sptr, stream, a.quick)
         out["batched_decode"] = batched_section(ctx, gen, sptr, stream)
         out["moe"] = moe_section(ctx, gen, sptr, stream)
+        out["schemes"] = schemes_section(ctx, gen, sptr, stream)
         out["q8_gemv"] = q8_section(ctx, gen, sptr, stream)
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(a.cpu_seconds)

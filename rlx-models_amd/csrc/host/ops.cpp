@@ -357,8 +357,9 @@ int rlxq_dequantize(rlxq_ctx* ctx, int scheme, int group_size, const void* w, co
   int sch = scheme, sb = sb_dtype == RLXQ_BF16, grp = is_mlx(scheme) ? group_size : 32, K = (int)k;
   int64_t R = rows, RB = rb;
   void* args[] = {&sch, (void*)&w, (void*)&scales, (void*)&biases, &sb, &grp, &R, &K, &RB, (void*)&out};
-  const int64_t blocks = rows * (k / 32);
-  return launch(ctx, fn, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0, stream, args, "dequantize");
+  const int64_t quarters = rows * (k / 32) * 4;   // one thread per 8 weights
+  if ((quarters + 255) / 256 > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequantize: too many weights");
+  return launch(ctx, fn, dim3((unsigned)((quarters + 255) / 256)), dim3(256), 0, stream, args, "dequantize");
 }
 
 int rlxq_swiglu(rlxq_ctx* ctx, const void* gu, int gu_dtype, int64_t rows, int64_t inter, void* out,

@@ -65,7 +65,7 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
 
   struct Buf {
     uint32_t dw[P][C][DW];
-    float sm[P][C][BLOCKS], bm[P][C][BLOCKS];
+    SbRaw sm[P][C][BLOCKS], bm[P][C][BLOCKS];
   };
   auto load = [&](int64_t t, int jg, Buf& bf) {
 #pragma unroll
@@ -82,8 +82,8 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
 #pragma unroll
           for (int bl = 0; bl < BLOCKS; bl++) {
             const int64_t gi = n * gpr + ((uc * BLOCKS + bl) * 32) / a.group;
-            bf.sm[p][c][bl] = load_sb(a.scales, gi, a.sb_bf16 != 0);
-            bf.bm[p][c][bl] = load_sb(a.biases, gi, a.sb_bf16 != 0);
+            bf.sm[p][c][bl] = load_sb_raw(a.scales, gi, a.sb_bf16 != 0);
+            bf.bm[p][c][bl] = load_sb_raw(a.biases, gi, a.sb_bf16 != 0);
           }
         }
       }
@@ -111,8 +111,8 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
 #pragma unroll
         for (int p = 0; p < P; p++) {
           if constexpr (MLX) {
-            d[p] = bf.sm[p][c][bl];
-            mn[p] = bf.bm[p][c][bl];
+            d[p] = sb_decode(bf.sm[p][c][bl], a.sb_bf16 != 0);
+            mn[p] = sb_decode(bf.bm[p][c][bl], a.sb_bf16 != 0);
           } else {
             block_scales<SCH>(bf.dw[p][c], bl, d[p], mn[p]);
           }
@@ -255,7 +255,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
 
   struct Buf {
     uint32_t dw[NU][DW];
-    float sm[NU][BLOCKS], bm[NU][BLOCKS];
+    SbRaw sm[NU][BLOCKS], bm[NU][BLOCKS];
   };
   auto load = [&](int64_t n, Buf& bf) {
     const int64_t nn = (n >= 0 && n < a.N) ? n : 0;  // no rows (cnt = 0): row 0
@@ -265,8 +265,8 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
       load_unit<SCH>(bf.dw[c], rp + (int64_t)uc[c] * BYTES);
       if constexpr (MLX) {
         const int64_t gi = nn * gpr + (uc[c] * 32) / a.group;
-        bf.sm[c][0] = load_sb(a.scales, gi, a.sb_bf16 != 0);
-        bf.bm[c][0] = load_sb(a.biases, gi, a.sb_bf16 != 0);
+        bf.sm[c][0] = load_sb_raw(a.scales, gi, a.sb_bf16 != 0);
+        bf.bm[c][0] = load_sb_raw(a.biases, gi, a.sb_bf16 != 0);
       }
     }
   };
@@ -403,8 +403,8 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
       for (int bl = 0; bl < BLOCKS; bl++) {
         float d, mn;
         if constexpr (MLX) {
-          d = bf.sm[c][bl];
-          mn = bf.bm[c][bl];
+          d = sb_decode(bf.sm[c][bl], a.sb_bf16 != 0);
+          mn = sb_decode(bf.bm[c][bl], a.sb_bf16 != 0);
         } else {
           block_scales<SCH>(bf.dw[c], bl, d, mn);
         }

@@ -366,6 +366,22 @@ RLXQ_DEV float block_dot(const uint32_t* pw, const uint32_t* xr) {
   return c;
 }
 
+// Raw bits of MLX scale/bias idx for the register rings: two 16-bit loads
+// issued unconditionally (a bf16 slab: the element, twice; an f32 slab: its
+// two halves), so no branch on the slab dtype sits between the ring's loads
+// and the wait counts keep them in flight; sb_decode forms the value at use.
+struct SbRaw {
+  uint32_t lo, hi;
+};
+RLXQ_DEV SbRaw load_sb_raw(const void* p, int64_t idx, bool bf16) {
+  const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
+  const int64_t i0 = bf16 ? idx : 2 * idx;
+  return {q[i0], q[bf16 ? i0 : i0 + 1]};
+}
+RLXQ_DEV float sb_decode(SbRaw r, bool bf16) {
+  return __uint_as_float(bf16 ? (r.lo << 16) : (r.lo | (r.hi << 16)));
+}
+
 // MLX scale/bias for (row n, block b); sb_bf16 selects the slab dtype.
 RLXQ_DEV float load_sb(const void* p, int64_t idx, bool bf16) {
   if (bf16) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[idx]);

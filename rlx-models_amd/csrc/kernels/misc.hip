@@ -3,10 +3,11 @@
 // activation quantisation, and the MoE router (softmax + top-k).
 #include "common.hip.h"
 
-// One thread per 32-weight block.  Q8_0: d*q; Q4_0: d*(q-8); Q4_1: d*q + m
-// (d*q is exact in f32, so the single rounding is the add); MLX: scale*code
-// rounded, then + bias rounded (no contraction), as
-// crates/rlx-moshi/src/mlx_dequant.rs:66-71 evaluates it.
+// One thread per eight consecutive weights (a quarter of a 32-weight block),
+// so that a wave writes 2 KB of contiguous f32 with 16-byte stores.  Q8_0:
+// d*q; Q4_0: d*(q-8); Q4_1: d*q + m (d*q is exact in f32, so the single
+// rounding is the add); MLX: scale*code rounded, then + bias rounded (no
+// contraction), as crates/rlx-moshi/src/mlx_dequant.rs:66-71 evaluates it.
 extern "C" __global__ __launch_bounds__(256) void rlxq_dequant_rows(
     int scheme, const uint8_t* __restrict__ w, const void* __restrict__ scales,
     const void* __restrict__ biases, int sb_bf16, int group, int64_t rows, int K, int64_t rb,
@@ -15,48 +16,60 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_dequant_rows(
   // pragma governs the expressions written below.
 #pragma clang fp contract(off)
   const int bpr = K >> 5;
-  const int64_t blk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (blk >= rows * bpr) return;
+  const int64_t qid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (qid >= rows * bpr * 4) return;
+  const int64_t blk = qid >> 2;
+  const int q = (int)(qid & 3);
   const int64_t r = blk / bpr;
   const int b = (int)(blk - r * bpr);
-  float* o = out + r * (int64_t)K + (int64_t)b * 32;
+  float v[8];
   if (scheme == SCH_Q8_0 || scheme == SCH_Q4_0 || scheme == SCH_Q4_1) {
     const int bb = scheme == SCH_Q8_0 ? 34 : (scheme == SCH_Q4_0 ? 18 : 20);
     const uint8_t* p = w + r * rb + (int64_t)b * bb;
     const float d = f16_bits_to_f32((uint32_t)p[0] | ((uint32_t)p[1] << 8));
     if (scheme == SCH_Q8_0) {
-      for (int i = 0; i < 32; i++) o[i] = d * (float)(int8_t)p[2 + i];
-    } else if (scheme == SCH_Q4_0) {
-      for (int j = 0; j < 16; j++) {
-        o[j] = d * (float)((int)(p[2 + j] & 15) - 8);
-        o[j + 16] = d * (float)((int)(p[2 + j] >> 4) - 8);
-      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = d * (float)(int8_t)p[2 + 8 * q + i];
     } else {
-      const float m = f16_bits_to_f32((uint32_t)p[2] | ((uint32_t)p[3] << 8));
-      for (int j = 0; j < 16; j++) {
-        o[j] = d * (float)(p[4 + j] & 15) + m;
-        o[j + 16] = d * (float)(p[4 + j] >> 4) + m;
+      // element e = 8q + i: low nibble of byte e (e < 16), else high nibble of byte e - 16
+      const int hdr = scheme == SCH_Q4_0 ? 2 : 4;
+      const int byte0 = (8 * q) & 15, shift = q >= 2 ? 4 : 0;
+      const float m = scheme == SCH_Q4_1 ? f16_bits_to_f32((uint32_t)p[2] | ((uint32_t)p[3] << 8)) : 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int c = (p[hdr + byte0 + i] >> shift) & 15;
+        v[i] = scheme == SCH_Q4_0 ? d * (float)(c - 8) : d * (float)c + m;
       }
     }
-    return;
-  }
-  // MLX affine: 32 codes of this block; one scale/bias per group.
-  const int bits = scheme == SCH_MLX4 ? 4 : 8;
-  const int64_t gi = r * (int64_t)(K / group) + ((int64_t)b * 32) / group;
-  float s, bi;
-  if (sb_bf16) {
-    s = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(scales)[gi]);
-    bi = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(biases)[gi]);
   } else {
-    s = reinterpret_cast<const float*>(scales)[gi];
-    bi = reinterpret_cast<const float*>(biases)[gi];
+    // MLX affine: codes of this block; one scale/bias per group.
+    const int bits = scheme == SCH_MLX4 ? 4 : 8;
+    const int64_t gi = r * (int64_t)(K / group) + ((int64_t)b * 32) / group;
+    float s, bi;
+    if (sb_bf16) {
+      s = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(scales)[gi]);
+      bi = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(biases)[gi]);
+    } else {
+      s = reinterpret_cast<const float*>(scales)[gi];
+      bi = reinterpret_cast<const float*>(biases)[gi];
+    }
+    const uint32_t* wq = reinterpret_cast<const uint32_t*>(w + r * rb) + (b * 32 * bits) / 32;
+    const int per = 32 / bits;
+    const uint32_t mask = (1u << bits) - 1u;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int e = 8 * q + i;
+      const uint32_t code = (wq[e / per] >> ((e % per) * bits)) & mask;
+      v[i] = s * (float)code + bi;
+    }
   }
-  const uint32_t* wq = reinterpret_cast<const uint32_t*>(w + r * rb) + (b * 32 * bits) / 32;
-  const int per = 32 / bits;
-  const uint32_t mask = (1u << bits) - 1u;
-  for (int i = 0; i < 32; i++) {
-    const uint32_t code = (wq[i / per] >> ((i % per) * bits)) & mask;
-    o[i] = s * (float)code + bi;
+  float* o = out + r * (int64_t)K + (int64_t)b * 32 + 8 * q;
+  if ((reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+    reinterpret_cast<float4*>(o)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(o)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = v[i];
   }
 }
 

@@ -314,7 +314,7 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
 
   struct Buf {
     uint32_t dw[R2][NU][DW];
-    float sm[R2][NU], bm[R2][NU];
+    SbRaw sm[R2][NU], bm[R2][NU];
   };
   // rows of output column col: col (and width + col, the up row, for SwiGLU)
   auto load = [&](int64_t col, Buf& bf) {
@@ -328,8 +328,8 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
         load_unit<SCH>(bf.dw[r][c], rp + (int64_t)uc[c] * BYTES);
         if constexpr (MLX) {
           const int64_t gi = ((int64_t)e * a.N + n) * gpr + (uc[c] * 32) / a.group;
-          bf.sm[r][c] = load_sb(a.scales, gi, a.sb_bf16 != 0);
-          bf.bm[r][c] = load_sb(a.biases, gi, a.sb_bf16 != 0);
+          bf.sm[r][c] = load_sb_raw(a.scales, gi, a.sb_bf16 != 0);
+          bf.bm[r][c] = load_sb_raw(a.biases, gi, a.sb_bf16 != 0);
         }
       }
     }
@@ -407,8 +407,8 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
           for (int bl = 0; bl < BLOCKS; bl++) {
             float d, mn;
             if constexpr (MLX) {
-              d = rb.sm[r][c];
-              mn = rb.bm[r][c];
+              d = sb_decode(rb.sm[r][c], a.sb_bf16 != 0);
+              mn = sb_decode(rb.bm[r][c], a.sb_bf16 != 0);
             } else {
               block_scales<SCH>(rb.dw[r][c], bl, d, mn);
             }
@@ -652,7 +652,7 @@ RLXQ_MOE_SCHEME(mlx8, SCH_MLX8)
   RLXQ_MOEXR_INST(rlxq_moexrf_##SNAME##_L##L##_U##NU##_M##MT##_sw, SCH, L, NU, MT, D, true, true)
 #define RLXQ_MOEXR_SCHEME(SNAME, SCH)        \
   RLXQ_MOEXR_LU(SNAME, SCH, 64, 1, 1, 4)     \
-  RLXQ_MOEXR_LU(SNAME, SCH, 64, 1, 2, 4)     \
+  RLXQ_MOEXR_LU(SNAME, SCH, 64, 1, 2, 2)     \
   RLXQ_MOEXR_LU(SNAME, SCH, 64, 1, 4, 4)     \
   RLXQ_MOEXR_LU(SNAME, SCH, 64, 2, 1, 2)     \
   RLXQ_MOEXR_LU(SNAME, SCH, 64, 2, 2, 2)     \

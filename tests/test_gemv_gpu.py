@@ -213,7 +213,13 @@ def test_dequantize_bit_exact(ctx, orc, scheme):
     packed = orc.synth(scheme, rng, n, k)
     got = ctx.dequantize(_t(packed), scheme, n, k)
     torch.cuda.synchronize()
-    assert np.array_equal(got.cpu().numpy().view(np.uint32), orc.dequantize(scheme, packed, k).view(np.uint32))
+    want = orc.dequantize(scheme, packed, k).view(np.uint32)
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), want)
+    # an output that is only 4-byte aligned takes the scalar stores
+    buf = torch.full((n * k + 1,), float("nan"), device="cuda")
+    ctx.dequantize(_t(packed), scheme, n, k, out=buf[1:].view(n, k))
+    torch.cuda.synchronize()
+    assert np.array_equal(buf[1:].cpu().numpy().view(np.uint32).reshape(n, k), want)
 
 
 # ------------------------------------------------------------------ error paths
