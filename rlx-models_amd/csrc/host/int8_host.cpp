@@ -2,6 +2,7 @@
 // branch of rlxq_dequant_matmul.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -62,19 +63,32 @@ int i8b_dispatch(rlxq_ctx* ctx, int group, const void* x, int x_dtype, const voi
   if (k > ((int64_t)1 << 31) || n > ((int64_t)1 << 31) || m > ((int64_t)1 << 31))
     return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: Int8Block shape too large");
 
-  const int MT = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
-  const int64_t MC = 16 * MT;
-  const int64_t tiles_n = (n + 255) / 256, mch = (m + MC - 1) / MC;
-  const int64_t ksteps = (k + 127) / 128;
-  const int64_t base = tiles_n * mch;
-  const int64_t target = 4 * (int64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256);
-  int64_t splits = (target + base - 1) / base;
-  if (splits > ksteps) splits = ksteps;
+  // M = 1: the streaming GEMV (rlxq_i8bv_*, which also serves M <= 4 when
+  // RLXQ_I8B_GEMV=1; RLXQ_I8B_MFMA=1 forces the MFMA kernel); larger M: the
+  // MFMA kernel, which reads each weight once for up to 16 rows.
+  const char* force_mfma = std::getenv("RLXQ_I8B_MFMA");
   const int64_t cap = (int64_t)256 << 20;  // partial sums kept under 256 MiB
+  const char* force_gemv = std::getenv("RLXQ_I8B_GEMV");
+  const int64_t gemv_m = force_gemv && force_gemv[0] == '1' ? 4 : 1;
+  const bool gemv = m <= gemv_m && !(force_mfma && force_mfma[0] == '1') && ((k + 1023) / 1024) * m * n * 4 <= cap;
+  const int MT = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+  const int MR = m <= 1 ? 1 : (m <= 2 ? 2 : 4);
+  const int64_t MC = 16 * MT;
+  const int64_t tiles_n = gemv ? (n + 1023) / 1024 : (n + 255) / 256, mch = gemv ? 1 : (m + MC - 1) / MC;
+  const int64_t unit = gemv ? 16 : 128;   // K rows per slice granule
+  const int64_t ksteps = (k + unit - 1) / unit;
+  const int64_t base = tiles_n * mch;
+  // workgroups: four (of four waves) per CU for the MFMA kernel; one (of
+  // sixteen) per CU for the GEMV
+  const int64_t target = (gemv ? 1 : 4) * (int64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256);
+  int64_t splits = (target + base - 1) / base;
+  if (gemv) splits = std::max<int64_t>(splits, (k + 1023) / 1024);   // at most 1024 rows per slice
+  if (splits > ksteps) splits = ksteps;
   if (splits > 1 && splits * m * n * 4 > cap) splits = cap / (m * n * 4);
   if (splits < 1) splits = 1;
-  const int64_t kslice = ((ksteps + splits - 1) / splits) * 128;
+  const int64_t kslice = ((ksteps + splits - 1) / splits) * unit;
   splits = (k + kslice - 1) / kslice;
+  if (gemv && kslice > 1024) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: Int8Block decode slice");
   if (tiles_n * mch * splits > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: Int8Block grid");
 
   const size_t part_bytes = splits > 1 ? round256((size_t)(splits * m * n) * 4) : 0;
@@ -112,15 +126,17 @@ int i8b_dispatch(rlxq_ctx* ctx, int group, const void* x, int x_dtype, const voi
     if ((rc = launch(ctx, fn, dim3((unsigned)m), dim3(256), 0, stream, args, "rlxq_row_sum"))) return rc;
   }
   char name[48];
-  std::snprintf(name, sizeof name, "rlxq_i8b_%s_mt%d", a.x_bf16 ? "bf16" : "f32", MT);
+  if (gemv) std::snprintf(name, sizeof name, "rlxq_i8bv_%s_m%d", a.x_bf16 ? "bf16" : "f32", MR);
+  else std::snprintf(name, sizeof name, "rlxq_i8b_%s_mt%d", a.x_bf16 ? "bf16" : "f32", MT);
   if ((rc = get_fn(ctx, name, &fn))) return rc;
-  const size_t lds = 128 * (256 + 16) + 2 * (size_t)MC * (128 + 8) * 2;
+  const size_t lds = gemv ? 0 : 128 * (256 + 16) + 2 * (size_t)MC * (128 + 8) * 2;
   void* args[] = {&a};
-  if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name)))
+  if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(gemv ? 1024 : 256), lds, stream, args,
+                   name)))
     return rc;
   if (splits > 1) {
     if ((rc = get_fn(ctx, "rlxq_i8b_reduce", &fn))) return rc;
-    const int64_t total = m * n;
+    const int64_t total = (m * n + 3) / 4;   // threads: four outputs each (N % 16 == 0)
     if ((total + 255) / 256 > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: Int8Block output");
     void* rargs[] = {&a};
     // the last kernel launched names the path in rlxq_last_kernel: keep the

@@ -350,6 +350,127 @@ RLXQ_DEV void i8b_body(const rlxq_i8b_args& a) {
       }
 }
 
+// Decode-size Int8Block (M <= 4): a streaming GEMV over the [K, N] int8
+// rows, fp32 FMA on the exact integer values.  A lane owns 16 consecutive
+// columns (one 16-byte load per K row), a wave 1024 columns; the W waves of
+// a workgroup take interleaved rows kb + w, kb + w + W, ... of the
+// workgroup's K slice (the workgroup reads W rows' 1 KB pieces per step),
+// each with a ring of D rows of loads in flight, and their sums are added
+// in wave order through LDS, one activation row at a time.  K slices go to
+// the partial buffer (added in slice order by rlxq_i8b_reduce) unless there
+// is one.
+constexpr int I8BV_KMAX = 1024;  // most K rows per workgroup slice
+
+template <int MR, bool XBF16, int W, int D>
+RLXQ_DEV void i8b_gemv_body(const rlxq_i8b_args& a) {
+  __shared__ float red[W][1024];
+  __shared__ float xs[MR][I8BV_KMAX];   // the slice's activations, as f32
+  constexpr int NT = 64 * W;
+  const int tn = blockIdx.x % a.tiles_n;
+  const int sp = blockIdx.x / a.tiles_n;
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t n0 = (int64_t)tn * 1024 + 16 * lane;
+  const bool nok = n0 < a.N;
+  const int64_t kb = (int64_t)sp * a.kslice;
+  const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
+  const int klen = (int)(ke - kb);
+  // rows of this wave: kb + wv + W s, s < cnt
+  const int cnt = wv < klen ? (klen - wv + W - 1) / W : 0;
+  const int8_t* wp = a.wq + (nok ? n0 : 0) + (kb + wv) * a.N;
+
+  float acc[MR][16];
+#pragma unroll
+  for (int m = 0; m < MR; m++)
+#pragma unroll
+    for (int j = 0; j < 16; j++) acc[m][j] = 0.f;
+
+  auto load = [&](int st) {
+    const int s2 = st < cnt ? st : (cnt > 0 ? cnt - 1 : 0);
+    return *reinterpret_cast<const uint4*>(wp + (int64_t)s2 * W * a.N);
+  };
+  auto step = [&](int st, const uint4& w) {
+    const int kl = wv + W * st;
+    float xv[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) xv[m] = xs[m][kl];
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const float q = (float)(int)(int8_t)((wd[j >> 2] >> (8 * (j & 3))) & 0xffu);
+#pragma unroll
+      for (int m = 0; m < MR; m++) acc[m][j] = fmaf(xv[m], q, acc[m][j]);
+    }
+  };
+
+  // the slice's activations (issued first, so waiting for them does not
+  // wait for the ring), then D rows of weights
+  constexpr int XPT = (MR * I8BV_KMAX + NT - 1) / NT;
+  float xl[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; i++) {
+    const int e = threadIdx.x + NT * i, m = e / I8BV_KMAX, kl = e % I8BV_KMAX;
+    xl[i] = 0.f;
+    if (m < MR && m < a.M && kl < klen) {
+      const int64_t off = m * a.K + kb + kl;
+      if constexpr (XBF16) xl[i] = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(a.x)[off]);
+      else xl[i] = reinterpret_cast<const float*>(a.x)[off];
+    }
+  }
+  uint4 ring[D];
+#pragma unroll
+  for (int i = 0; i < D; i++) ring[i] = load(i);
+#pragma unroll
+  for (int i = 0; i < XPT; i++) {
+    const int e = threadIdx.x + NT * i;
+    if (e < MR * I8BV_KMAX) xs[e / I8BV_KMAX][e % I8BV_KMAX] = xl[i];
+  }
+  __syncthreads();
+  int s0 = 0;
+  for (; s0 + 2 * D <= cnt; s0 += D) {
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+      step(s0 + i, ring[i]);
+      ring[i] = load(s0 + i + D);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < D; i++) {
+    if (s0 + i < cnt) {
+      step(s0 + i, ring[i]);
+      if (s0 + i + D < cnt) ring[i] = load(s0 + i + D);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < D; i++)
+    if (s0 + D + i < cnt) step(s0 + D + i, ring[i]);
+
+  // the waves' sums, added in wave order, one activation row at a time
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+#pragma unroll
+    for (int j = 0; j < 16; j += 4)
+      *reinterpret_cast<float4*>(&red[wv][16 * lane + j]) =
+          make_float4(acc[m][j], acc[m][j + 1], acc[m][j + 2], acc[m][j + 3]);
+    __syncthreads();
+    for (int c = threadIdx.x; c < 1024; c += NT) {
+      const int64_t n = (int64_t)tn * 1024 + c;
+      float v = red[0][c];
+#pragma unroll
+      for (int w = 1; w < W; w++) v += red[w][c];
+      if (m < a.M && n < a.N) {
+        if (a.splits > 1) {
+          a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
+        } else {
+          const float o = i8b_finish(a, v, m, n);
+          if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(o);
+          else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = o;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace rlxq
 
 #define RLXQ_W8A8_INST(BM, BN, BK, WGM, WGN)                                                        \
@@ -381,13 +502,55 @@ RLXQ_I8B_INST(1, bf16, true)
 RLXQ_I8B_INST(2, bf16, true)
 RLXQ_I8B_INST(4, bf16, true)
 
-// Split-K reduction of the Int8Block partials, summed in split order.
+#define RLXQ_I8BV_INST(MR, XN, XBF)                                                           \
+  extern "C" __global__ __launch_bounds__(1024) void rlxq_i8bv_##XN##_m##MR(rlxq_i8b_args a) { \
+    rlxq::i8b_gemv_body<MR, XBF, 16, 8>(a);                                                     \
+  }
+RLXQ_I8BV_INST(1, f32, false)
+RLXQ_I8BV_INST(2, f32, false)
+RLXQ_I8BV_INST(4, f32, false)
+RLXQ_I8BV_INST(1, bf16, true)
+RLXQ_I8BV_INST(2, bf16, true)
+RLXQ_I8BV_INST(4, bf16, true)
+
+// Split-K reduction of the Int8Block partials, summed in split order.  Four
+// outputs per thread when N % 4 == 0, with sixteen slices' loads in flight
+// at a time (the sums stay in slice order).
 extern "C" __global__ __launch_bounds__(256) void rlxq_i8b_reduce(rlxq_i8b_args a) {
+  const int64_t mn = a.M * a.N;
+  if ((a.N & 3) == 0) {
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i >= mn) return;
+    const int64_t m = i / a.N, n = i - m * a.N;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < a.splits; s0 += 16) {
+      const int c = a.splits - s0 < 16 ? a.splits - s0 : 16;
+      float4 p[16];
+#pragma unroll
+      for (int q = 0; q < 16; q++)
+        if (q < c) p[q] = *reinterpret_cast<const float4*>(a.part + (int64_t)(s0 + q) * mn + i);
+#pragma unroll
+      for (int q = 0; q < 16; q++)
+        if (q < c) {
+          v[0] += p[q].x;
+          v[1] += p[q].y;
+          v[2] += p[q].z;
+          v[3] += p[q].w;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float o = rlxq::i8b_finish(a, v[e], m, n + e);
+      if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n + e] = (uint16_t)f32_to_bf16_bits(o);
+      else reinterpret_cast<float*>(a.y)[m * a.y_ld + n + e] = o;
+    }
+    return;
+  }
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= a.M * a.N) return;
+  if (i >= mn) return;
   const int64_t m = i / a.N, n = i - m * a.N;
   float v = 0.f;
-  for (int sp = 0; sp < a.splits; sp++) v += a.part[(int64_t)sp * a.M * a.N + i];
+  for (int sp = 0; sp < a.splits; sp++) v += a.part[(int64_t)sp * mn + i];
   const float o = rlxq::i8b_finish(a, v, m, n);
   if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(o);
   else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = o;

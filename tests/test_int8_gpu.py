@@ -251,3 +251,23 @@ def test_int8_block_host_checks(ctx):
     with pytest.raises(rlxq.RlxqError) as e:
         ctx.dequant_matmul(x, wq[:, :24].contiguous(), rlxq.INT8_BLOCK, 24, group=64, scales=sw[:24])
     assert e.value.status == rlxq.E_ALIGN
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 12288, 4096), (2, 1001, 1040), (3, 3000, 2064), (4, 4096, 24576 // 8),
+                                   (1, 5, 16)])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+@pytest.mark.parametrize("zp", [False, True])
+def test_int8_block_decode_gemv(ctx, orc, rng, monkeypatch, m, k, n, xdt, zp):
+    """The streaming GEMV (M = 1 by default, M <= 4 when forced; K slices of
+    at most 1024 rows, ragged column groups) and the MFMA kernel both meet
+    the f32 bar."""
+    announce(f"int8_block gemv m={m} k={k} n={n} x={xdt} zp={zp}")
+    monkeypatch.setenv("RLXQ_I8B_GEMV", "1")
+    seed = rng.integers(1 << 30)
+    got, want = _i8b_case(ctx, orc, np.random.default_rng(seed), m, k, n, xdt, zp=zp)
+    assert ctx.last_kernel.startswith("rlxq_i8bv_"), ctx.last_kernel
+    assert rel_err(got, want) <= TOL_F32
+    monkeypatch.setenv("RLXQ_I8B_MFMA", "1")
+    got2, want2 = _i8b_case(ctx, orc, np.random.default_rng(seed), m, k, n, xdt, zp=zp)
+    assert ctx.last_kernel.startswith("rlxq_i8b_"), ctx.last_kernel
+    assert rel_err(got2, want2) <= TOL_F32
