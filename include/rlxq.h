@@ -41,8 +41,12 @@ typedef enum rlxq_scheme {
     RLXQ_MLX_AFFINE4 = 4, /* MlxAffine{bits:4, group_size}: u32 LSB-first codes,
                              scale*code + bias, scales/biases [N, K/group]       */
     RLXQ_MLX_AFFINE8 = 5, /* MlxAffine{bits:8, group_size}                       */
-    RLXQ_INT8_BLOCK = 6   /* Int8Block{block_size: K}: i8 [K, N], scale [N],
+    RLXQ_INT8_BLOCK = 6,  /* Int8Block{block_size: K}: i8 [K, N], scale [N],
                              zp [N] (NULL = 0); y = x . ((Wq - zp) * scale)      */
+    RLXQ_GGUF_Q4_K = 7    /* GgufQ4K: 144 B / 256 w: f16 d, f16 dmin, 12 B of
+                             6-bit scales/mins, 128 nibble bytes;
+                             w = (d*sc)*q - dmin*mn.  Dense DequantMatMul and
+                             dequantize only; K % 256 == 0, w 16-byte aligned  */
 } rlxq_scheme;
 
 /* Element types of activations, outputs and MLX scale/bias slabs. */

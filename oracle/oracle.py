@@ -17,8 +17,8 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIBPATH = HERE / "liboracle.so"
 
-Q8_0, Q4_0, Q4_1, MLX4, MLX8, INT8_BLOCK = 1, 2, 3, 4, 5, 6
-BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20}
+Q8_0, Q4_0, Q4_1, MLX4, MLX8, INT8_BLOCK, Q4_K = 1, 2, 3, 4, 5, 6, 7
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20, Q4_K: 144}
 
 _lib = None
 
@@ -43,6 +43,7 @@ def lib() -> C.CDLL:
             "orc_row_bytes": (I64, [I, I64]),
             "orc_quantize": (I, [I, P, I64, P]),
             "orc_dequantize": (I, [I, P, I64, P]),
+            "orc_q4k_scale_min": (None, [P, I, C.POINTER(I), C.POINTER(I)]),
             "orc_mlx_pack": (I, [P, I64, I64, I, P]),
             "orc_mlx_dequantize": (I, [P, P, P, I64, I64, I, I, P]),
             "orc_matmul_f64": (I, [I, P, P, I64, I64, I64, P]),
@@ -292,5 +293,41 @@ def synth_q4_0(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
     return blk.reshape(n, -1)
 
 
+def synth_q4_k(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
+    """Q4_K rows (K % 256 == 0): codes ~U{0..15}, 6-bit scales and mins
+    ~U{0..63} packed as GGML does, d ~U(0.0005, 0.002) and dmin ~U(0.0005,
+    0.005) (fp16), so that d*sc spans Q4_1-like step sizes."""
+    nb = n * (k // 256)
+    blk = np.empty((nb, 144), np.uint8)
+    d = f32_to_f16_bits(rng.uniform(0.0005, 0.002, nb).astype(np.float32))
+    dm = f32_to_f16_bits(rng.uniform(0.0005, 0.005, nb).astype(np.float32))
+    blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blk[:, 2:4] = dm.view(np.uint8).reshape(nb, 2)
+    blk[:, 4:16] = q4k_pack_scales(rng.integers(0, 64, (nb, 8)), rng.integers(0, 64, (nb, 8)))
+    blk[:, 16:144] = rng.integers(0, 256, (nb, 128), dtype=np.uint8)
+    return blk.reshape(n, -1)
+
+
+def q4k_pack_scales(sc, mn) -> np.ndarray:
+    """The 12 bytes that hold eight 6-bit scales and mins ([..., 8] each), in
+    GGML's block_q4_K packing: bytes 0-3 sc[0..3] | (sc[4..7] >> 4) << 6,
+    bytes 4-7 mn[0..3] | (mn[4..7] >> 4) << 6, bytes 8-11 (sc[4..7] & 15) |
+    (mn[4..7] & 15) << 4."""
+    sc = np.asarray(sc, np.int64)
+    mn = np.asarray(mn, np.int64)
+    out = np.empty(sc.shape[:-1] + (12,), np.uint8)
+    out[..., 0:4] = (sc[..., 0:4] & 63) | ((sc[..., 4:8] >> 4) << 6)
+    out[..., 4:8] = (mn[..., 0:4] & 63) | ((mn[..., 4:8] >> 4) << 6)
+    out[..., 8:12] = (sc[..., 4:8] & 15) | ((mn[..., 4:8] & 15) << 4)
+    return out
+
+
+def q4k_scale_min(q12, s: int) -> tuple[int, int]:
+    q = np.ascontiguousarray(q12, dtype=np.uint8)
+    sc, mn = C.c_int(), C.c_int()
+    lib().orc_q4k_scale_min(_p(q), s, C.byref(sc), C.byref(mn))
+    return sc.value, mn.value
+
+
 def synth(scheme: int, rng: np.random.Generator, n: int, k: int) -> np.ndarray:
-    return {Q4_1: synth_q4_1, Q8_0: synth_q8_0, Q4_0: synth_q4_0}[scheme](rng, n, k)
+    return {Q4_1: synth_q4_1, Q8_0: synth_q8_0, Q4_0: synth_q4_0, Q4_K: synth_q4_k}[scheme](rng, n, k)

@@ -17,6 +17,7 @@
 #endif
 
 #define QK 32
+#define QKK 256 /* Q4_K super-block */
 
 /* ------------------------------------------------------------------------ */
 /* Scalar conversions                                                        */
@@ -124,14 +125,17 @@ int64_t orc_block_bytes(int scheme) {
         case ORC_GGUF_Q8_0: return 2 + QK;
         case ORC_GGUF_Q4_0: return 2 + QK / 2;
         case ORC_GGUF_Q4_1: return 4 + QK / 2;
+        case ORC_GGUF_Q4_K: return 2 + 2 + 12 + QKK / 2;
         default: return -1;
     }
 }
 
+int64_t orc_block_len(int scheme) { return scheme == ORC_GGUF_Q4_K ? QKK : QK; }
+
 int64_t orc_row_bytes(int scheme, int64_t k) {
-    int64_t bb = orc_block_bytes(scheme);
-    if (bb < 0 || k % QK) return -1;
-    return k / QK * bb;
+    int64_t bb = orc_block_bytes(scheme), len = orc_block_len(scheme);
+    if (bb < 0 || k % len) return -1;
+    return k / len * bb;
 }
 
 /* Rust `f32::round`: half away from zero (C roundf). */
@@ -198,7 +202,7 @@ static void quant_q4_1_block(const float* x, uint8_t* out) {
 
 int orc_quantize(int scheme, const float* src, int64_t n, uint8_t* dst) {
     int64_t bb = orc_block_bytes(scheme);
-    if (bb < 0 || n % QK) return -1;
+    if (bb < 0 || n % QK || scheme == ORC_GGUF_Q4_K) return -1;  /* no Q4_K encoder */
     for (int64_t b = 0; b < n / QK; b++) {
         const float* x = src + b * QK;
         uint8_t* o = dst + b * bb;
@@ -232,10 +236,52 @@ static void dequant_block(int scheme, const uint8_t* b, float* o) {
     }
 }
 
+/* GGUF Q4_K (GGML block_q4_K; QuantScheme::GgufQ4K, decoded by the absent
+ * rlx_gguf::dequant_q4_k): 256 weights in 144 bytes -- f16 d, f16 dmin, 12
+ * bytes packing eight 6-bit (scale, min) pairs, then 128 nibble bytes.  Byte
+ * j of the 32-byte group g holds weight 64g + j (low nibble, sub-block 2g)
+ * and weight 64g + 32 + j (high nibble, sub-block 2g + 1).  Sub-block s has
+ * scale sc and min mn taken from the 12 packed bytes q as
+ *   s < 4: sc = q[s] & 63,                       mn = q[s + 4] & 63;
+ *   s >= 4: sc = (q[s + 4] & 15) | (q[s - 4] >> 6) << 4,
+ *           mn = (q[s + 4] >> 4) | (q[s] >> 6) << 4;
+ * and w = (d * sc) * code - (dmin * mn): each product rounded to f32, then
+ * the subtraction rounded (no fused multiply-add). */
+void orc_q4k_scale_min(const uint8_t* q, int s, int* sc, int* mn) {
+    if (s < 4) {
+        *sc = q[s] & 63;
+        *mn = q[s + 4] & 63;
+    } else {
+        *sc = (q[s + 4] & 15) | ((q[s - 4] >> 6) << 4);
+        *mn = (q[s + 4] >> 4) | ((q[s] >> 6) << 4);
+    }
+}
+
+static void dequant_q4k_block(const uint8_t* b, float* o) {
+    const float d = rd_f16(b), dmin = rd_f16(b + 2);
+    const uint8_t* sc12 = b + 4;
+    const uint8_t* qs = b + 16;
+    for (int g = 0; g < 4; g++) {
+        for (int h = 0; h < 2; h++) {
+            int sc, mn;
+            orc_q4k_scale_min(sc12, 2 * g + h, &sc, &mn);
+            const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+            for (int j = 0; j < 32; j++) {
+                const int code = h == 0 ? (qs[32 * g + j] & 15) : (qs[32 * g + j] >> 4);
+                const float prod = d1 * (float)code;
+                o[64 * g + 32 * h + j] = prod - m1;
+            }
+        }
+    }
+}
+
 int orc_dequantize(int scheme, const uint8_t* src, int64_t n, float* dst) {
-    int64_t bb = orc_block_bytes(scheme);
-    if (bb < 0 || n % QK) return -1;
-    for (int64_t b = 0; b < n / QK; b++) dequant_block(scheme, src + b * bb, dst + b * QK);
+    int64_t bb = orc_block_bytes(scheme), len = orc_block_len(scheme);
+    if (bb < 0 || n % len) return -1;
+    for (int64_t b = 0; b < n / len; b++) {
+        if (scheme == ORC_GGUF_Q4_K) dequant_q4k_block(src + b * bb, dst + b * len);
+        else dequant_block(scheme, src + b * bb, dst + b * len);
+    }
     return 0;
 }
 
@@ -361,6 +407,7 @@ static float dot_refl(int scheme, const float* x, const uint8_t* row, int64_t k)
 
 int orc_matmul_refl(int scheme, const float* x, const uint8_t* w, int64_t m,
                     int64_t k, int64_t n, float* y) {
+    if (scheme == ORC_GGUF_Q4_K) return -1;  /* reference-order loop: legacy blocks only */
     int64_t rb = orc_row_bytes(scheme, k);
     if (rb < 0) return -1;
     for (int64_t r = 0; r < m; r++)
@@ -373,6 +420,7 @@ int orc_matmul_refl(int scheme, const float* x, const uint8_t* w, int64_t m,
 int orc_matmul_refl_par(int scheme, const float* x, const uint8_t* w,
                         int64_t m, int64_t k, int64_t n, float* y,
                         int nthreads) {
+    if (scheme == ORC_GGUF_Q4_K) return -1;
     int64_t rb = orc_row_bytes(scheme, k);
     if (rb < 0) return -1;
 #ifdef _OPENMP

@@ -22,6 +22,12 @@
  *                                  nibbles follows the public GGML block_q4_1
  *                                  layout (no reference code in the tree fixes
  *                                  it): "parity unpinned" at the byte level.
+ *   dequantize Q4_K ............. the public GGML block_q4_K layout (256-weight
+ *                                  super-blocks, 6-bit scales and mins); the
+ *                                  reference calls rlx_gguf::dequant_q4_k, which
+ *                                  is absent: pinned by closed forms and bit-level
+ *                                  probes of the scale packing, "parity unpinned"
+ *                                  against reference code.
  *   MLX affine dequant .......... pinned (mlx_dequant.rs:100-110 KAT,
  *                                  mlx_affine.rs:290-330 matmul test)
  *   matmul / grouped / MoE ...... pinned (closed forms, f64 brute force,
@@ -47,6 +53,7 @@ enum {
     ORC_MLX_AFFINE4 = 4,
     ORC_MLX_AFFINE8 = 5,
     ORC_INT8_BLOCK = 6,
+    ORC_GGUF_Q4_K = 7,
 };
 
 /* ---- scalar conversions (IEEE binary16 / bfloat16, round to nearest even) */
@@ -60,12 +67,15 @@ void orc_f32_to_bf16_n(const float* src, int64_t n, uint16_t* dst);
 void orc_bf16_to_f32_n(const uint16_t* src, int64_t n, float* dst);
 
 /* ---- GGUF legacy block codecs (32 weights per block) -------------------- */
-int64_t orc_block_bytes(int scheme);           /* 34 / 18 / 20, else -1 */
-int64_t orc_row_bytes(int scheme, int64_t k);  /* k/32 * block bytes, else -1 */
+int64_t orc_block_bytes(int scheme);           /* 34 / 18 / 20 / 144 (Q4_K), else -1 */
+int64_t orc_block_len(int scheme);             /* weights per block: 32, or 256 (Q4_K) */
+int64_t orc_row_bytes(int scheme, int64_t k);  /* k/len * block bytes, else -1 */
 /* Quantize n (multiple of 32) floats into packed blocks. 0 on success. */
 int orc_quantize(int scheme, const float* src, int64_t n, uint8_t* dst);
 /* Dequantize n (multiple of 32) weights. 0 on success. */
 int orc_dequantize(int scheme, const uint8_t* src, int64_t n, float* dst);
+/* Q4_K: the 6-bit (scale, min) of sub-block s (0..7) from the 12 packed bytes. */
+void orc_q4k_scale_min(const uint8_t* q, int s, int* sc, int* mn);
 
 /* ---- MLX affine (LSB-first u32 packing, w = scale*code + bias) ---------- */
 /* Pack row-major codes [rows, cols] into u32 words, LSB-first. */

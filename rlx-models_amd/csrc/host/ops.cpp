@@ -29,6 +29,7 @@ const char* scheme_name(int s) {
     case RLXQ_GGUF_Q4_1: return "q4_1";
     case RLXQ_MLX_AFFINE4: return "mlx4";
     case RLXQ_MLX_AFFINE8: return "mlx8";
+    case RLXQ_GGUF_Q4_K: return "q4_k";
     default: return nullptr;
   }
 }
@@ -59,7 +60,7 @@ int pick_lanes(int64_t units, const int* cands, int ncand) {
 // single-row family, RLXQ_GEMV_CFG="L,P,C,D,W" overrides it (tuning sweeps and
 // the per-variant parity test); a variant that was not compiled fails with
 // RLXQ_E_NOKERNEL.
-GemvCfg pick_gemv(int64_t m, int64_t units, int64_t lds_rec_bytes_m4, size_t max_lds) {
+GemvCfg pick_gemv(int64_t m, int64_t units, int64_t lds_rec_bytes_m4, size_t max_lds, bool wide_units) {
   GemvCfg c;
   if (m >= 2 && lds_rec_bytes_m4 <= (int64_t)max_lds) {
     static const int c4[] = {64, 8};
@@ -67,7 +68,9 @@ GemvCfg pick_gemv(int64_t m, int64_t units, int64_t lds_rec_bytes_m4, size_t max
   } else {
     static const int c1[] = {64, 32, 16, 8};
     const int L = pick_lanes(units, c1, 4);
-    c = L == 64 ? GemvCfg{64, 1, 2, 1, 2, 16} : GemvCfg{L, 2, 1, 1, 2, 8};
+    // 12-dword units (Q4_K) spill in the two-chunk 16-wave variant: one chunk,
+    // four steps in flight
+    c = L == 64 ? (wide_units ? GemvCfg{64, 1, 1, 1, 4, 16} : GemvCfg{64, 1, 2, 1, 2, 16}) : GemvCfg{L, 2, 1, 1, 2, 8};
   }
   const char* e = c.MT == 1 ? std::getenv("RLXQ_GEMV_CFG") : nullptr;
   if (e) {
@@ -84,6 +87,12 @@ GemvCfg pick_gemv(int64_t m, int64_t units, int64_t lds_rec_bytes_m4, size_t max
 int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const void* w,
                   const void* scales, const void* biases, int sb_dtype, int64_t k, int64_t* rb) {
   if (k % 32) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": K must be a multiple of 32");
+  if (scheme == RLXQ_GGUF_Q4_K) {
+    if (k % 256) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": Q4_K needs K % 256 == 0 (super-blocks)");
+    if (!aligned(w, 16)) return fail(ctx, RLXQ_E_ALIGN, std::string(what) + ": Q4_K rows must be 16-byte aligned");
+    *rb = k / 256 * 144;
+    return RLXQ_OK;
+  }
   if (is_gguf(scheme)) {
     if ((scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_0) && k % 64)
       return fail(ctx, RLXQ_E_ALIGN,
@@ -221,7 +230,7 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: K or N too large");
 
   const bool xbf = x_dtype == RLXQ_BF16;
-  const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0) ? 2 : 1;
+  const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_K) ? 2 : 1;
   const int64_t units = (k / 32) / blocks;
 
   // Prefill: bf16 activations and bf16 output with at least 64 rows go to the
@@ -231,7 +240,8 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // GEMV family, which keeps the products exact.
   // RLXQ_PREFILL=gemv|gemm forces one of them where both apply (tests).
   {
-    bool gemm_ok = xbf && k % 64 == 0 && m >= 1;
+    // (Q4_K: the GEMV family serves every M)
+    bool gemm_ok = xbf && k % 64 == 0 && m >= 1 && scheme != RLXQ_GGUF_Q4_K;
     bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (!is_mlx(scheme) && m > 256));
     if (const char* e = std::getenv("RLXQ_PREFILL")) {
       if (!std::strcmp(e, "gemv")) use_gemm = false;
@@ -279,10 +289,11 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // (the row of x then crosses L2 once per workgroup, not once per wave).
   // RLXQ_GEMV_XR="NU,D,W[,XS]" picks the variant (XS=1: through LDS), "0"
   // turns the path off (tuning).
-  const bool xr_scheme = scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_MLX_AFFINE4;
+  const bool q4k = scheme == RLXQ_GGUF_Q4_K;
+  const bool xr_scheme = scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_MLX_AFFINE4 || q4k;
   const int64_t nchunk64 = (units + 63) / 64;
-  const int64_t xr_max = scheme == RLXQ_GGUF_Q4_0 ? 4 : 6;
-  int xr_nu = (int)(nchunk64 == 5 ? 6 : nchunk64), xr_d = nchunk64 <= 3 ? 2 : 1, xr_w = 8;
+  const int64_t xr_max = scheme == RLXQ_GGUF_Q4_0 ? 4 : (q4k ? 3 : 6);
+  int xr_nu = (int)(nchunk64 == 5 ? 6 : nchunk64), xr_d = nchunk64 <= (q4k ? 2 : 3) ? 2 : 1, xr_w = 8;
   bool use_xr = m == 1 && xbf && xr_scheme && nchunk64 <= xr_max && n < (int64_t(1) << 31);
   int xr_lds = 1;   // 1: the activations pass through LDS once per workgroup
   if (const char* e = std::getenv("RLXQ_GEMV_XR")) {
@@ -311,7 +322,7 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
 
   const int64_t rec_bytes = (xbf ? 20 : 36) * 4;
   const int64_t bpr = k / 32;
-  const GemvCfg cfg = pick_gemv(m, units, 4 * bpr * rec_bytes, ctx->max_lds);
+  const GemvCfg cfg = pick_gemv(m, units, 4 * bpr * rec_bytes, ctx->max_lds, scheme == RLXQ_GGUF_Q4_K);
   const int waves = cfg.W;
   const int64_t tile = (int64_t)waves * cfg.P * (64 / cfg.L);
   const int64_t lds = cfg.MT * bpr * rec_bytes;

@@ -16,6 +16,7 @@ enum : int {
   SCH_Q4_1 = 3,
   SCH_MLX4 = 4,
   SCH_MLX8 = 5,
+  SCH_Q4_K = 7,
 };
 
 // D = a.lo*b.lo + a.hi*b.hi + c with bf16 pairs and an f32 accumulator

@@ -48,7 +48,7 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
   constexpr int RP = 64 / L;
   constexpr int TILE = WAVES * P * RP;
   constexpr bool MLX = (SCH == SCH_MLX4 || SCH == SCH_MLX8);
-  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || MLX);
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || MLX);
   extern __shared__ uint32_t lds[];
 
   const int K = a.K;
@@ -77,7 +77,7 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
       for (int c = 0; c < C; c++) {
         const int u = li + L * (jg * C + c);
         const int uc = u < U ? u : U - 1;
-        load_unit<SCH>(bf.dw[p][c], rp + (int64_t)uc * BYTES);
+        load_unit_at<SCH>(bf.dw[p][c], rp, uc);
         if constexpr (MLX) {
 #pragma unroll
           for (int bl = 0; bl < BLOCKS; bl++) {
@@ -114,7 +114,7 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
             d[p] = sb_decode(bf.sm[p][c][bl], a.sb_bf16 != 0);
             mn[p] = sb_decode(bf.bm[p][c][bl], a.sb_bf16 != 0);
           } else {
-            block_scales<SCH>(bf.dw[p][c], bl, d[p], mn[p]);
+            block_scales<SCH>(bf.dw[p][c], bl, d[p], mn[p], uc);
           }
           const bool rok = t * TILE + row_off + p * RP < a.N;
           if (!(rok && uok)) {
@@ -228,7 +228,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   constexpr int DW = Unit<SCH>::DW;
   constexpr int BYTES = Unit<SCH>::BYTES;
   constexpr bool MLX = SCH == SCH_MLX4;
-  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || MLX);
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || MLX);
   static_assert(!Unit<SCH>::BIT8, "register activations serve 4-bit codes");
 
   const int K = a.K;
@@ -262,7 +262,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     const uint8_t* rp = a.w + nn * a.rb;
 #pragma unroll
     for (int c = 0; c < NU; c++) {
-      load_unit<SCH>(bf.dw[c], rp + (int64_t)uc[c] * BYTES);
+      load_unit_at<SCH>(bf.dw[c], rp, uc[c]);
       if constexpr (MLX) {
         const int64_t gi = nn * gpr + (uc[c] * 32) / a.group;
         bf.sm[c][0] = load_sb_raw(a.scales, gi, a.sb_bf16 != 0);
@@ -292,6 +292,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     constexpr int NT = 64 * WAVES;
     constexpr int XH = (2 * 64 * NU * BLOCKS + NT - 1) / NT;   // half-blocks per thread
     constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;
+    constexpr bool LINEAR = MLX || SCH == SCH_Q4_K;   // half h = elements 16h..16h+15
     uint4 xa[XH], xc[XH];
 #pragma unroll
     for (int i = 0; i < XH; i++) {
@@ -299,8 +300,8 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
       xa[i] = xc[i] = make_uint4(0u, 0u, 0u, 0u);
       if (hb < 2 * bpr) {
         const uint16_t* p = xg + (int64_t)b * 32;
-        xa[i] = *reinterpret_cast<const uint4*>(p + (MLX ? 16 * h : 8 * h));
-        xc[i] = *reinterpret_cast<const uint4*>(p + (MLX ? 16 * h + 8 : 16 + 8 * h));
+        xa[i] = *reinterpret_cast<const uint4*>(p + (LINEAR ? 16 * h : 8 * h));
+        xc[i] = *reinterpret_cast<const uint4*>(p + (LINEAR ? 16 * h + 8 : 16 + 8 * h));
       }
     }
 #pragma unroll
@@ -312,7 +313,13 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
       uint32_t P[8];
 #pragma unroll
       for (int t = 0; t < 2; t++) {
-        if constexpr (MLX) {
+        if constexpr (SCH == SCH_Q4_K) {
+          const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7: pairs (4j+e, 4j+e+2)
+          P[4 * t + 0] = perm_b32(R[1], R[0], LO);
+          P[4 * t + 1] = perm_b32(R[1], R[0], HI);
+          P[4 * t + 2] = perm_b32(R[3], R[2], LO);
+          P[4 * t + 3] = perm_b32(R[3], R[2], HI);
+        } else if constexpr (MLX) {
           const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7
           P[4 * t + 0] = perm_b32(R[2], R[0], LO);
           P[4 * t + 1] = perm_b32(R[2], R[0], HI);
@@ -406,7 +413,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
           d = sb_decode(bf.sm[c][bl], a.sb_bf16 != 0);
           mn = sb_decode(bf.bm[c][bl], a.sb_bf16 != 0);
         } else {
-          block_scales<SCH>(bf.dw[c], bl, d, mn);
+          block_scales<SCH>(bf.dw[c], bl, d, mn, uc[c]);
         }
         if (!uok[c]) {
           d = 0.f;
@@ -516,6 +523,13 @@ RLXQ_GEMVXR_WIDE(mlx4, SCH_MLX4)
 #define RLXQ_GEMVXS_WIDE(SNAME, SCH)                                    \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U6_D1_W8, SCH, 6, 1, 8)       \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U6_D2_W8, SCH, 6, 2, 8)
+// Q4_K (64-weight units, 12 dwords each): up to three units per lane (K <= 12288)
+#define RLXQ_GEMVXS_Q4K                                                     \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U1_D2_W8, SCH_Q4_K, 1, 2, 8)          \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U2_D2_W8, SCH_Q4_K, 2, 2, 8)          \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U2_D1_W8, SCH_Q4_K, 2, 1, 8)          \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U3_D1_W8, SCH_Q4_K, 3, 1, 8)
+RLXQ_GEMVXS_Q4K
 RLXQ_GEMVXS_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXS_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_GEMVXS_SCHEME(mlx4, SCH_MLX4)
@@ -525,5 +539,6 @@ RLXQ_GEMVXS_WIDE(mlx4, SCH_MLX4)
 RLXQ_GEMV_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMV_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_GEMV_SCHEME(q8_0, SCH_Q8_0)
+RLXQ_GEMV_SCHEME(q4_k, SCH_Q4_K)
 RLXQ_GEMV_SCHEME(mlx4, SCH_MLX4)
 RLXQ_GEMV_SCHEME(mlx8, SCH_MLX8)

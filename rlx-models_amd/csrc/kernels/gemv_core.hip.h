@@ -34,6 +34,15 @@ struct Unit<SCH_MLX8> {
   static constexpr int BLOCKS = 1, BYTES = 32, DW = 8;
   static constexpr bool BIT8 = true;
 };
+// GGUF Q4_K: a unit is one 64-weight group of a 256-weight super-block (two
+// 32-weight sub-blocks sharing 32 code bytes): the super-block's 16-byte head
+// (f16 d, f16 dmin, 12 bytes of 6-bit scales and mins) plus the group's 32
+// code bytes.  BYTES is the row stride per unit (144 / 4).
+template <>
+struct Unit<SCH_Q4_K> {
+  static constexpr int BLOCKS = 2, BYTES = 36, DW = 12;
+  static constexpr bool BIT8 = false;
+};
 
 // Offset that the code -> float trick adds to each code, and the value the
 // dot chain starts from (in units of the block's plane sum) so that the chain
@@ -57,6 +66,13 @@ RLXQ_DEV void plane_pair(int t, int& a, int& b) {
     int base = 4 * i + ((e & 1) ? 16 : 0) + ((e & 2) ? 1 : 0);
     a = base;
     b = base + 2;
+  } else if constexpr (SCH == SCH_Q4_K) {
+    // code dword i = bytes 4i..4i+3 of the group: low nibbles are the first
+    // sub-block's elements 4i..4i+3 (the high ones the second's); extraction
+    // e = 0 -> (4i, 4i+2), e = 1 -> (4i+1, 4i+3).
+    int i = t >> 1, e = t & 1;
+    a = 4 * i + e;
+    b = 4 * i + e + 2;
   } else if constexpr (SCH == SCH_MLX4) {
     // u32 word i holds codes 8i..8i+7 LSB-first; extraction e -> (8i+e, 8i+e+4).
     int i = t >> 2, e = t & 3;
@@ -214,7 +230,7 @@ RLXQ_DEV void stage_store(uint32_t* lds, const XRaw<XBF16>& raw, int m, int K, i
       h1 = hi[1] | (hi[3] << 16);
       l0 = lo[0] | (lo[2] << 16);
       l1 = lo[1] | (lo[3] << 16);
-      if constexpr (BIT8) {
+      if constexpr (BIT8 || SCH == SCH_Q4_K) {
         t0 = 2 * q;
         t1 = 2 * q + 1;
       } else {
@@ -290,6 +306,8 @@ RLXQ_DEV void load_unit(uint32_t* dw, const uint8_t* p) {
   } else if constexpr (SCH == SCH_MLX4) {
     uint4 a = ld_u128(p);
     dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
+  } else if constexpr (SCH == SCH_Q4_K) {
+    static_assert(SCH != SCH_Q4_K, "Q4_K units are fetched with load_unit_at");
   } else {
     uint4 a = ld_u128(p), b = ld_u128(p + 16);
     dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
@@ -297,10 +315,49 @@ RLXQ_DEV void load_unit(uint32_t* dw, const uint8_t* p) {
   }
 }
 
-// Block scale terms of block `blk` of a fetched unit: d multiplies the dot
-// chain, m (Q4_1 min) multiplies the block sum of x.
+// Unit u of the packed row at rp.  Q4_K: super-block u / 4 (16-byte head)
+// and its 32 code bytes of group u % 4, all 16-byte aligned loads.
 template <int SCH>
-RLXQ_DEV void block_scales(const uint32_t* dw, int blk, float& d, float& m) {
+RLXQ_DEV void load_unit_at(uint32_t* dw, const uint8_t* rp, int u) {
+  if constexpr (SCH == SCH_Q4_K) {
+    const uint8_t* sb = rp + (int64_t)(u >> 2) * 144;
+    const uint4 h = ld_u128(sb), a = ld_u128(sb + 16 + 32 * (u & 3)), b = ld_u128(sb + 32 + 32 * (u & 3));
+    dw[0] = h.x; dw[1] = h.y; dw[2] = h.z; dw[3] = h.w;
+    dw[4] = a.x; dw[5] = a.y; dw[6] = a.z; dw[7] = a.w;
+    dw[8] = b.x; dw[9] = b.y; dw[10] = b.z; dw[11] = b.w;
+  } else {
+    load_unit<SCH>(dw, rp + (int64_t)u * Unit<SCH>::BYTES);
+  }
+}
+
+// Q4_K: 6-bit scale and min of sub-block s (0..7) from the head's 12 packed
+// bytes (dwords 1..3 of the head), GGML's packing.
+RLXQ_DEV void q4k_scale_min(const uint32_t* head, int s, float& sc, float& mn) {
+  auto byte = [&](int i) { return (head[1 + (i >> 2)] >> (8 * (i & 3))) & 0xffu; };
+  uint32_t a, b;
+  if (s < 4) {
+    a = byte(s) & 63u;
+    b = byte(s + 4) & 63u;
+  } else {
+    a = (byte(s + 4) & 15u) | ((byte(s - 4) >> 6) << 4);
+    b = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
+  }
+  sc = (float)a;
+  mn = (float)b;
+}
+
+// Block scale terms of block `blk` of a fetched unit: d multiplies the dot
+// chain, m (Q4_1 min; Q4_K minus dmin * min) multiplies the block sum of x.
+// u is the unit's index in its row (Q4_K: which group of the super-block).
+template <int SCH>
+RLXQ_DEV void block_scales(const uint32_t* dw, int blk, float& d, float& m, int u = 0) {
+  if constexpr (SCH == SCH_Q4_K) {
+    float sc, mn;
+    q4k_scale_min(dw, 2 * (u & 3) + blk, sc, mn);
+    d = f16_bits_to_f32(dw[0] & 0xffffu) * sc;
+    m = -(f16_bits_to_f32(dw[0] >> 16) * mn);
+    return;
+  }
   if constexpr (SCH == SCH_Q4_1) {
     d = f16_bits_to_f32(dw[0] & 0xffffu);
     m = f16_bits_to_f32(dw[0] >> 16);
@@ -341,6 +398,14 @@ RLXQ_DEV void block_pairs(const uint32_t* dw, int blk, uint32_t* pw, const Unpac
   } else if constexpr (SCH == SCH_MLX4) {
 #pragma unroll
     for (int i = 0; i < 4; i++) nib_pairs(dw[i], &pw[4 * i], k);
+  } else if constexpr (SCH == SCH_Q4_K) {
+    // sub-block blk: the low (0) or high (1) nibbles of the group's 32 bytes
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t w = dw[4 + i] >> (4 * blk);
+      pw[2 * i] = (w & k.mask) | k.magic;
+      pw[2 * i + 1] = ((w >> 8) & k.mask) | k.magic;
+    }
   } else {
 #pragma unroll
     for (int i = 0; i < 8; i++) byte_pairs(dw[i], &pw[2 * i]);
@@ -416,7 +481,13 @@ RLXQ_DEV void pairs_from_raw(const uint32_t* R, uint32_t* X) {
   constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;  // low / high halves of (R[a], R[b])
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    if constexpr (SCH == SCH_MLX4) {
+    if constexpr (SCH == SCH_Q4_K) {
+      // t = 2j + e holds (4j+e, 4j+e+2): R[2j] and R[2j+1], j = 2i, 2i+1
+      X[4 * i + 0] = perm_b32(R[4 * i + 1], R[4 * i], LO);
+      X[4 * i + 1] = perm_b32(R[4 * i + 1], R[4 * i], HI);
+      X[4 * i + 2] = perm_b32(R[4 * i + 3], R[4 * i + 2], LO);
+      X[4 * i + 3] = perm_b32(R[4 * i + 3], R[4 * i + 2], HI);
+    } else if constexpr (SCH == SCH_MLX4) {
       // t = 4i+e holds (8i+e, 8i+e+4): R[4i + e/2] and R[4i + 2 + e/2]
       X[4 * i + 0] = perm_b32(R[4 * i + 2], R[4 * i + 0], LO);
       X[4 * i + 1] = perm_b32(R[4 * i + 2], R[4 * i + 0], HI);

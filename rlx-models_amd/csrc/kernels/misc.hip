@@ -6,8 +6,9 @@
 // One thread per eight consecutive weights (a quarter of a 32-weight block),
 // so that a wave writes 2 KB of contiguous f32 with 16-byte stores.  Q8_0:
 // d*q; Q4_0: d*(q-8); Q4_1: d*q + m (d*q is exact in f32, so the single
-// rounding is the add); MLX: scale*code rounded, then + bias rounded (no
-// contraction), as crates/rlx-moshi/src/mlx_dequant.rs:66-71 evaluates it.
+// rounding is the add); Q4_K: (d*sc)*q - dmin*mn (GGML block_q4_K); MLX:
+// scale*code rounded, then + bias rounded (no contraction), as
+// crates/rlx-moshi/src/mlx_dequant.rs:66-71 evaluates it.
 extern "C" __global__ __launch_bounds__(256) void rlxq_dequant_rows(
     int scheme, const uint8_t* __restrict__ w, const void* __restrict__ scales,
     const void* __restrict__ biases, int sb_bf16, int group, int64_t rows, int K, int64_t rb,
@@ -23,7 +24,30 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_dequant_rows(
   const int64_t r = blk / bpr;
   const int b = (int)(blk - r * bpr);
   float v[8];
-  if (scheme == SCH_Q8_0 || scheme == SCH_Q4_0 || scheme == SCH_Q4_1) {
+  if (scheme == SCH_Q4_K) {
+    // sub-block s of super-block b / 8: the low (s even) or high nibbles of
+    // the 32 code bytes of group s / 2; w = (d*sc)*q - dmin*mn
+    const int s = b & 7, g = s >> 1;
+    const uint8_t* p = w + r * rb + (int64_t)(b >> 3) * 144;
+    const float d = f16_bits_to_f32((uint32_t)p[0] | ((uint32_t)p[1] << 8));
+    const float dmin = f16_bits_to_f32((uint32_t)p[2] | ((uint32_t)p[3] << 8));
+    const uint8_t* q12 = p + 4;
+    int sc, mn;
+    if (s < 4) {
+      sc = q12[s] & 63;
+      mn = q12[s + 4] & 63;
+    } else {
+      sc = (q12[s + 4] & 15) | ((q12[s - 4] >> 6) << 4);
+      mn = (q12[s + 4] >> 4) | ((q12[s] >> 6) << 4);
+    }
+    const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int byte = p[16 + 32 * g + 8 * q + i];
+      const float prod = d1 * (float)((s & 1) ? byte >> 4 : byte & 15);
+      v[i] = prod - m1;
+    }
+  } else if (scheme == SCH_Q8_0 || scheme == SCH_Q4_0 || scheme == SCH_Q4_1) {
     const int bb = scheme == SCH_Q8_0 ? 34 : (scheme == SCH_Q4_0 ? 18 : 20);
     const uint8_t* p = w + r * rb + (int64_t)b * bb;
     const float d = f16_bits_to_f32((uint32_t)p[0] | ((uint32_t)p[1] << 8));

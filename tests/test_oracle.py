@@ -334,3 +334,101 @@ def test_int8_block_matmul(orc, rng):
     zp = np.zeros(n, np.float32)
     want = x.astype(np.float64) @ ((wq.astype(np.float32) - zp) * s).astype(np.float64)
     assert np.allclose(orc.int8_block_matmul_f64(x, wq, s, zp), want, rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------- Q4_K
+# GGML block_q4_K (256 weights, 144 B).  The reference decodes it with the
+# absent rlx_gguf::dequant_q4_k, so these tests pin the restatement by bit
+# probes of the scale packing and closed forms built from scratch here.
+def _q4k_block(orc, d, dmin, sc, mn, codes):
+    """One packed block from explicit fields; codes [256] in weight order."""
+    b = np.zeros(144, np.uint8)
+    b[0:2] = orc.f32_to_f16_bits(np.float32([d])).view(np.uint8)
+    b[2:4] = orc.f32_to_f16_bits(np.float32([dmin])).view(np.uint8)
+    b[4:16] = orc.q4k_pack_scales(np.asarray(sc), np.asarray(mn))
+    codes = np.asarray(codes, np.uint8)
+    for g in range(4):
+        lo, hi = codes[64 * g:64 * g + 32], codes[64 * g + 32:64 * g + 64]
+        b[16 + 32 * g:48 + 32 * g] = lo | (hi << 4)
+    return b
+
+
+def test_q4k_scale_packing_round_trip(orc, rng):
+    """Every 6-bit (scale, min) value in every one of the eight slots comes
+    back from the packed 12 bytes, alone and mixed with random neighbours."""
+    for s in range(8):
+        for v in range(64):
+            sc = rng.integers(0, 64, 8)
+            mn = rng.integers(0, 64, 8)
+            sc[s], mn[s] = v, 63 - v
+            q = orc.q4k_pack_scales(sc, mn)
+            for t in range(8):
+                assert orc.q4k_scale_min(q, t) == (int(sc[t]), int(mn[t])), (s, v, t)
+
+
+def test_q4k_scale_bits_reach_the_right_slot(orc):
+    """Each of the 96 bits of the packed scales moves exactly one field of one
+    sub-block, by the power of two GGML's layout gives it (a transposed byte
+    index, a wrong shift or a swapped scale/min fails here)."""
+    want = {}
+    for byte in range(12):
+        for bit in range(8):
+            if byte < 4:
+                want[(byte, bit)] = ("sc", byte, 1 << bit) if bit < 6 else ("sc", byte + 4, 1 << (bit - 2))
+            elif byte < 8:
+                want[(byte, bit)] = ("mn", byte - 4, 1 << bit) if bit < 6 else ("mn", byte, 1 << (bit - 2))
+            else:
+                want[(byte, bit)] = ("sc", byte - 4, 1 << bit) if bit < 4 else ("mn", byte - 4, 1 << (bit - 4))
+    for (byte, bit), (field, slot, val) in want.items():
+        q = np.zeros(12, np.uint8)
+        q[byte] = 1 << bit
+        got = [orc.q4k_scale_min(q, s) for s in range(8)]
+        for s in range(8):
+            exp = (val if field == "sc" and s == slot else 0, val if field == "mn" and s == slot else 0)
+            assert got[s] == exp, (byte, bit, s)
+
+
+def test_q4k_code_layout_and_closed_form(orc, rng):
+    """d = 1, dmin = 0, unit scales: the weights are the codes, in GGML's
+    order (low nibbles of a 32-byte group = the group's first 32 weights);
+    then w = (d*sc)*q - dmin*mn per sub-block."""
+    codes = rng.integers(0, 16, 256)
+    b = _q4k_block(orc, 1.0, 0.0, [1] * 8, [0] * 8, codes)
+    np.testing.assert_array_equal(orc.dequantize(orc.Q4_K, b, 256)[0], codes.astype(np.float32))
+    sc, mn = rng.integers(1, 64, 8), rng.integers(0, 64, 8)
+    d, dmin = np.float32(0.01171875), np.float32(0.03125)   # exact in f16
+    b = _q4k_block(orc, d, dmin, sc, mn, codes)
+    got = orc.dequantize(orc.Q4_K, b, 256)[0]
+    for s in range(8):
+        d1, m1 = np.float32(d * np.float32(sc[s])), np.float32(dmin * np.float32(mn[s]))
+        want = (d1 * codes[32 * s:32 * s + 32].astype(np.float32)).astype(np.float32) - m1
+        np.testing.assert_array_equal(got[32 * s:32 * s + 32], want.astype(np.float32))
+
+
+def test_q4k_single_rounding(orc, rng):
+    """d and dmin are f16 (11 significant bits), scales and mins 6 bits, codes
+    4 bits: (d*sc)*q and dmin*mn are exact in f32, so every weight is the
+    exact value d*sc*q - dmin*mn rounded once to f32 (checked against float64
+    over random d, dmin and every scale, min and code)."""
+    for _ in range(6):
+        d = orc.f16_bits_to_f32(orc.f32_to_f16_bits(rng.uniform(1e-4, 0.05, 1).astype(np.float32)))[0]
+        dmin = orc.f16_bits_to_f32(orc.f32_to_f16_bits(rng.uniform(1e-4, 0.05, 1).astype(np.float32)))[0]
+        for base in range(0, 64, 8):
+            sc = np.arange(base, base + 8)
+            mn = rng.integers(0, 64, 8)
+            codes = rng.integers(0, 16, 256)
+            got = orc.dequantize(orc.Q4_K, _q4k_block(orc, d, dmin, sc, mn, codes), 256)[0]
+            s = np.repeat(np.arange(8), 32)
+            exact = float(d) * sc[s].astype(np.float64) * codes - float(dmin) * mn[s].astype(np.float64)
+            np.testing.assert_array_equal(got, exact.astype(np.float32))
+
+
+def test_q4k_rows_and_matmul(orc, rng):
+    """Row stride K/256*144; the f64 matmul is x @ dequant(W)^T."""
+    n, k = 7, 512
+    w = orc.synth_q4_k(rng, n, k)
+    assert w.shape == (n, k // 256 * 144) and orc.row_bytes(orc.Q4_K, k) == 288
+    assert orc.row_bytes(orc.Q4_K, 300) == -1
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    deq = orc.dequantize(orc.Q4_K, w, k).astype(np.float64)
+    np.testing.assert_allclose(orc.matmul_f64(orc.Q4_K, x, w, n), x.astype(np.float64) @ deq.T, rtol=1e-12)
