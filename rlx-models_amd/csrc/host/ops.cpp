@@ -115,9 +115,7 @@ int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const 
   return fail(ctx, RLXQ_E_SCHEME, std::string(what) + ": unsupported scheme " + std::to_string(scheme));
 }
 
-// Prefill dequant-GEMM launch.  256 x 256 tiles (one workgroup per CU, 4
-// waves of 128 x 128) for M >= 256, else 128 x 128 tiles (4 waves of 64 x 64).
-// RLXQ_GEMM_TILE=128|256 forces one of them (tests, sweeps).
+// Prefill dequant-GEMM launch (tilings and split-K below).
 int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const void* w, const void* scales,
                   const void* biases, int sb_dtype, int64_t rb, int64_t m, int64_t k, int64_t n, void* y,
                   int y_dtype, void* stream) {
