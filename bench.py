@@ -204,11 +204,12 @@ def decode_roofline(ctx, layers, xs, ys, calls, stream, reps: int) -> tuple[dict
 
 
 def prefill_section(ctx, gen, sptr, stream, quick: bool) -> dict:
-    """Config 4: Q4_1 dequant-GEMM and the W8A8 variant, bf16 in/out."""
+    """Config 4: Q4_1 dequant-GEMM (and GGUF Q4_K at M=4096) and the W8A8
+    variant, bf16 in/out."""
     import torch
     import rlxq
 
-    res = {"q4_1": {}, "w8a8": {}}
+    res = {"q4_1": {}, "q4_k": {}, "w8a8": {}}
     ms_list = (4096,) if quick else (512, 2048, 4096)
     for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):
         w = synth_q4_1_gpu(n, k, gen)
@@ -224,6 +225,19 @@ def prefill_section(ctx, gen, sptr, stream, quick: bool) -> dict:
                                            "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
             del x, y
         del w
+        # GGUF Q4_K on the same kernels (super-block head + group codes per K step)
+        w = synth_q4_k_gpu(n, k, gen)
+        m = 4096
+        x = torch.randn((m, k), generator=gen, device="cuda").to(torch.bfloat16)
+        y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+        run = lambda i: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_K, n, y=y, stream=sptr)
+        run(0)
+        torch.cuda.synchronize()
+        us = _time_us(run, 5, stream)
+        tf = 2.0 * m * n * k / us / 1e6
+        res["q4_k"][f"{name}_m{m}"] = {"m": m, "k": k, "n": n, "kernel": ctx.last_kernel, "us": round(us, 1),
+                                       "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+        del w, x, y
         m = 4096
         wq = torch.randint(-127, 128, (k, n), device="cuda", dtype=torch.int8, generator=gen)
         sw = torch.rand((n,), device="cuda", generator=gen) * 0.01 + 1e-4

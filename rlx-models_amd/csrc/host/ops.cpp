@@ -137,12 +137,13 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
   }
   // GGUF with f32 output: the f16 variant of the 256 tiles, whose f16 weights
   // keep the output within 1e-3 (bf16 weights do not)
-  if (!te && y_dtype == RLXQ_F32 && !is_mlx(scheme)) var = bit8 ? "w8f" : "w8p2f";
+  if (!te && y_dtype == RLXQ_F32 && !is_mlx(scheme) && scheme != RLXQ_GGUF_Q4_K) var = bit8 ? "w8f" : "w8p2f";
   const bool w8 = tile == 256 && var[0] == 'w';
   // "...f": f16 weights and MFMA on the prepared f16 activations (GGUF)
   const size_t vl = std::strlen(var);
   const bool f16 = vl > 0 && var[vl - 1] == 'f';
-  if (f16 && is_mlx(scheme)) return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: no f16 GEMM for MLX codes");
+  if (f16 && (is_mlx(scheme) || scheme == RLXQ_GGUF_Q4_K))
+    return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: no f16 GEMM for MLX or Q4_K codes");
   const int64_t tiles_m = (m + tile - 1) / tile, tiles_n = (n + tile - 1) / tile;
   if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
   const int64_t tiles = tiles_m * tiles_n, ksteps = k / 64;
@@ -238,9 +239,10 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // GEMV family, which keeps the products exact.
   // RLXQ_PREFILL=gemv|gemm forces one of them where both apply (tests).
   {
-    // (Q4_K: the GEMV family serves every M)
-    bool gemm_ok = xbf && k % 64 == 0 && m >= 1 && scheme != RLXQ_GGUF_Q4_K;
-    bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (!is_mlx(scheme) && m > 256));
+    // (Q4_K: bf16 output only; f32 output stays on the GEMV family)
+    bool gemm_ok = xbf && k % 64 == 0 && m >= 1;
+    const bool f16_gemm = !is_mlx(scheme) && scheme != RLXQ_GGUF_Q4_K;
+    bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (f16_gemm && m > 256));
     if (const char* e = std::getenv("RLXQ_PREFILL")) {
       if (!std::strcmp(e, "gemv")) use_gemm = false;
       if (!std::strcmp(e, "gemm")) use_gemm = gemm_ok;

@@ -19,6 +19,23 @@ enum : int {
   SCH_Q4_K = 7,
 };
 
+// GGUF Q4_K: 6-bit scale and min of sub-block s (0..7) from a super-block's
+// 16-byte head held as dwords (head[0] = f16 d | f16 dmin << 16, head[1..3] =
+// the 12 packed bytes), GGML's packing.
+RLXQ_DEV void q4k_scale_min(const uint32_t* head, int s, float& sc, float& mn) {
+  auto byte = [&](int i) { return (head[1 + (i >> 2)] >> (8 * (i & 3))) & 0xffu; };
+  uint32_t a, b;
+  if (s < 4) {
+    a = byte(s) & 63u;
+    b = byte(s + 4) & 63u;
+  } else {
+    a = (byte(s + 4) & 15u) | ((byte(s - 4) >> 6) << 4);
+    b = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
+  }
+  sc = (float)a;
+  mn = (float)b;
+}
+
 // D = a.lo*b.lo + a.hi*b.hi + c with bf16 pairs and an f32 accumulator
 // (v_dot2c_f32_bf16).  Products of two bf16 values are exact in f32.
 RLXQ_DEV float dot2_bf16(uint32_t a, uint32_t b, float c) {

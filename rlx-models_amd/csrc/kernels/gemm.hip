@@ -347,6 +347,7 @@ RLXQ_GEMM_INST(rlxq_gemm_q4_0_t128, SCH_Q4_0)
 RLXQ_GEMM_INST(rlxq_gemm_q8_0_t128, SCH_Q8_0)
 RLXQ_GEMM_INST(rlxq_gemm_mlx4_t128, SCH_MLX4)
 RLXQ_GEMM_INST(rlxq_gemm_mlx8_t128, SCH_MLX8)
+RLXQ_GEMM_INST(rlxq_gemm_q4_k_t128, SCH_Q4_K)
 
 #define RLXQ_GEMM256_INST(SNAME, SCH)                                                        \
   extern "C" __global__ __launch_bounds__(256, 1) void rlxq_gemm_##SNAME##_t256(rlxq_gemm_args a) { \
@@ -369,6 +370,7 @@ RLXQ_GEMM256_INST(q4_0, SCH_Q4_0)
 RLXQ_GEMM256_INST(q8_0, SCH_Q8_0)
 RLXQ_GEMM256_INST(mlx4, SCH_MLX4)
 RLXQ_GEMM256_INST(mlx8, SCH_MLX8)
+RLXQ_GEMM256_INST(q4_k, SCH_Q4_K)
 RLXQ_GEMM256F_INST(q4_1, SCH_Q4_1, 2, p2)
 RLXQ_GEMM256F_INST(q4_0, SCH_Q4_0, 2, p2)
 RLXQ_GEMM256F_INST(q8_0, SCH_Q8_0, 1, )

@@ -15,13 +15,24 @@ template <> struct RawBlk<SCH_Q4_0> { uint32_t w[5]; uint32_t off; };
 template <> struct RawBlk<SCH_Q8_0> { uint32_t w[9]; uint32_t off; };
 template <> struct RawBlk<SCH_MLX4> { uint4 q; float s, b; };
 template <> struct RawBlk<SCH_MLX8> { uint4 q0, q1; float s, b; };
+// Q4_K: block kb is sub-block kb % 8 of super-block kb / 8: the super-block's
+// head and the 32 code bytes of its group (low nibbles for even sub-blocks)
+template <> struct RawBlk<SCH_Q4_K> { uint4 hd; uint4 q0, q1; uint32_t sub; };
 
 // Loads block `kb` of weight row `row` (a valid row); `ok` = false zeroes it
 // with selects, so the caller's loop body stays free of branches.
 template <int SCH>
 RLXQ_DEV void load_blk(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok, RawBlk<SCH>& r) {
   const uint8_t* rp = a.w + row * a.rb;
-  if constexpr (SCH == SCH_Q4_1) {
+  if constexpr (SCH == SCH_Q4_K) {
+    const uint8_t* sb = rp + (kb >> 3) * 144;
+    const uint4 h = ld_u128(sb);
+    r.hd = ok ? h : make_uint4(0u, 0u, 0u, 0u);   // zero head: d = dmin = 0
+    const uint8_t* q = sb + 16 + 32 * ((kb & 7) >> 1);
+    r.q0 = ld_u128(q);
+    r.q1 = ld_u128(q + 16);
+    r.sub = (uint32_t)(kb & 7);
+  } else if constexpr (SCH == SCH_Q4_1) {
     const uint8_t* p = rp + kb * 20;
     r.h = ok ? ld_u32(p) : 0u;
     const uint4 q = ld_u128(p + 4);
@@ -67,7 +78,21 @@ RLXQ_DEV void load_blk(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok
 template <int SCH>
 RLXQ_DEV void conv_blk(const RawBlk<SCH>& r, uint32_t* out) {
   float v[32];
-  if constexpr (SCH == SCH_Q4_1 || SCH == SCH_Q4_0) {
+  if constexpr (SCH == SCH_Q4_K) {
+    const uint32_t hd[4] = {r.hd.x, r.hd.y, r.hd.z, r.hd.w};
+    float sc, mn;
+    q4k_scale_min(hd, (int)r.sub, sc, mn);
+    const float d1 = f16_bits_to_f32(hd[0] & 0xffffu) * sc, m1 = -(f16_bits_to_f32(hd[0] >> 16) * mn);
+    const uint32_t qs[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    const int sh = 4 * (int)(r.sub & 1u);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      uint32_t c = (qs[i] >> sh) & 0x0F0F0F0Fu;
+      asm volatile("" : "+v"(c));
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[4 * i + e] = fmaf(d1, (float)((c >> (8 * e)) & 0xffu), m1);
+    }
+  } else if constexpr (SCH == SCH_Q4_1 || SCH == SCH_Q4_0) {
     uint32_t qs[4];
     float d, m;
     if constexpr (SCH == SCH_Q4_1) {

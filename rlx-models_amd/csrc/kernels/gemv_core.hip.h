@@ -330,22 +330,6 @@ RLXQ_DEV void load_unit_at(uint32_t* dw, const uint8_t* rp, int u) {
   }
 }
 
-// Q4_K: 6-bit scale and min of sub-block s (0..7) from the head's 12 packed
-// bytes (dwords 1..3 of the head), GGML's packing.
-RLXQ_DEV void q4k_scale_min(const uint32_t* head, int s, float& sc, float& mn) {
-  auto byte = [&](int i) { return (head[1 + (i >> 2)] >> (8 * (i & 3))) & 0xffu; };
-  uint32_t a, b;
-  if (s < 4) {
-    a = byte(s) & 63u;
-    b = byte(s + 4) & 63u;
-  } else {
-    a = (byte(s + 4) & 15u) | ((byte(s - 4) >> 6) << 4);
-    b = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
-  }
-  sc = (float)a;
-  mn = (float)b;
-}
-
 // Block scale terms of block `blk` of a fetched unit: d multiplies the dot
 // chain, m (Q4_1 min; Q4_K minus dmin * min) multiplies the block sum of x.
 // u is the unit's index in its row (Q4_K: which group of the super-block).

@@ -121,3 +121,33 @@ def test_q4k_host_checks(ctx):
     with pytest.raises(rlxq.RlxqError) as e:
         ctx.grouped_matmul(x, wf[:4 * 288], idx, rlxq.GGUF_Q4_K, 4, 1)
     assert e.value.status == rlxq.E_SCHEME
+
+
+@pytest.mark.parametrize("mkn", [(64, 4096, 520), (300, 1280, 272), (512, 4096, 1024), (129, 12288, 300)], ids=str)
+@pytest.mark.parametrize("tile", [None, "128", "256", "256w8"])
+def test_q4k_prefill_gemm(ctx, orc, monkeypatch, mkn, tile):
+    """bf16 activations and output from 64 rows: the MFMA dequant-GEMM
+    (weights rounded to bf16 in LDS), every tiling, split-K where it applies;
+    the prefill bar 2e-2."""
+    import torch
+
+    if tile:
+        monkeypatch.setenv("RLXQ_GEMM_TILE", tile)
+    m, k, n = mkn
+    announce(f"q4_k gemm {mkn} tile={tile}")
+    rng = np.random.default_rng(m + k)
+    packed = orc.synth_q4_k(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got, want = _run(ctx, orc, x, packed, n, y_dtype=torch.bfloat16)
+    assert ctx.last_kernel.startswith("rlxq_gemm_q4_k_t" + (tile or "256")), ctx.last_kernel
+    assert rel_err(got, want) <= 2e-2
+
+
+def test_q4k_f32_output_prefill_stays_on_gemv(ctx, orc):
+    m, k, n = 300, 1024, 200
+    rng = np.random.default_rng(5)
+    packed = orc.synth_q4_k(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got, want = _run(ctx, orc, x, packed, n)
+    assert ctx.last_kernel.startswith("rlxq_gemv_q4_k_"), ctx.last_kernel
+    assert rel_err(got, want) <= TOL
