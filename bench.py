@@ -306,6 +306,18 @@ def synth_q4_k_gpu(n: int, k: int, gen):
     return torch.cat([d, dm, rest], dim=1).contiguous().view(-1)
 
 
+def synth_q6_k_gpu(n: int, k: int, gen):
+    """Q6_K rows on the device: random code bytes, int8 scales ~U{-64..63},
+    d ~U(0.0002, 0.001) fp16."""
+    import torch
+
+    nb = n * (k // 256)
+    q = torch.randint(0, 256, (nb, 192), device="cuda", dtype=torch.uint8, generator=gen)
+    sc = torch.randint(-64, 64, (nb, 16), device="cuda", dtype=torch.int8, generator=gen).view(torch.uint8)
+    d = torch.empty(nb, device="cuda").uniform_(0.0002, 0.001, generator=gen).half().view(torch.uint8).view(nb, 2)
+    return torch.cat([q, sc, d], dim=1).contiguous().view(-1)
+
+
 def synth_mlx_gpu(n: int, k: int, bits: int, group: int, gen):
     """MLX affine rows on the device: u32 code words (random bits), bf16 scale
     ~U(0.01, 0.1) and bias ~U(-0.5, 0.1) slabs [n, k / group]."""
@@ -320,7 +332,7 @@ def synth_mlx_gpu(n: int, k: int, bits: int, group: int, gen):
 def schemes_section(ctx, gen, sptr, stream) -> dict:
     """The other weight formats of the op at M=1 (bf16 activations, f32
     output) on the gate_up shape 4096->24576, weights rotated past the MALL:
-    GGUF Q4_0 and Q4_K, MLX affine 4/8-bit (group 64, bf16 slabs), Int8Block (i8
+    GGUF Q4_0, Q4_K and Q6_K, MLX affine 4/8-bit (group 64, bf16 slabs), Int8Block (i8
     [K, N] with an f32 scale per column); the MLX 4-bit grouped op at the
     MoE config's gate|up shape; and the bit-exact dequantisation kernel
     (Q4_1 to f32).  Bytes: weights (+ scale slabs) + activations + outputs."""
@@ -349,6 +361,8 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
             lambda w: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_0, n, y=y, stream=sptr))
     measure("q4_k_gemv_m1", n * k * 144 / 256, lambda: synth_q4_k_gpu(n, k, gen),
             lambda w: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_K, n, y=y, stream=sptr))
+    measure("q6_k_gemv_m1", n * k * 210 / 256, lambda: synth_q6_k_gpu(n, k, gen),
+            lambda w: ctx.dequant_matmul(x, w, rlxq.GGUF_Q6_K, n, y=y, stream=sptr))
     for bits in (4, 8):
         wb = n * k * bits / 8 + 2 * n * (k // 64) * 2
         measure(f"mlx{bits}_g64_gemv_m1", wb, lambda bits=bits: synth_mlx_gpu(n, k, bits, 64, gen),

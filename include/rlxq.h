@@ -43,12 +43,18 @@ typedef enum rlxq_scheme {
     RLXQ_MLX_AFFINE8 = 5, /* MlxAffine{bits:8, group_size}                       */
     RLXQ_INT8_BLOCK = 6,  /* Int8Block{block_size: K}: i8 [K, N], scale [N],
                              zp [N] (NULL = 0); y = x . ((Wq - zp) * scale)      */
-    RLXQ_GGUF_Q4_K = 7    /* GgufQ4K (weight_loader.rs:502; host twin
+    RLXQ_GGUF_Q4_K = 7,   /* GgufQ4K (weight_loader.rs:502; host twin
                              rlx_gguf::dequant_q4_k, crates/rlx-sam3/src/
                              packed_gguf.rs:50): 144 B / 256 w: f16 d, f16 dmin, 12 B of
                              6-bit scales/mins, 128 nibble bytes;
                              w = (d*sc)*q - dmin*mn.  Dense DequantMatMul and
                              dequantize only; K % 256 == 0, w 16-byte aligned  */
+    RLXQ_GGUF_Q6_K = 8    /* GgufQ6K (weight_loader.rs maps GgmlType::Q6K;
+                             host twin rlx_gguf::dequant_q6_k, crates/rlx-sam3/
+                             src/packed_gguf.rs): 210 B / 256 w: ql[128],
+                             qh[64], int8 scales[16], f16 d;
+                             w = (d*scale)*(code - 32).  Dense DequantMatMul
+                             (GEMV family) and dequantize; K % 256 == 0       */
 } rlxq_scheme;
 
 /* Element types of activations, outputs and MLX scale/bias slabs. */

@@ -17,8 +17,8 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIBPATH = HERE / "liboracle.so"
 
-Q8_0, Q4_0, Q4_1, MLX4, MLX8, INT8_BLOCK, Q4_K = 1, 2, 3, 4, 5, 6, 7
-BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20, Q4_K: 144}
+Q8_0, Q4_0, Q4_1, MLX4, MLX8, INT8_BLOCK, Q4_K, Q6_K = 1, 2, 3, 4, 5, 6, 7, 8
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20, Q4_K: 144, Q6_K: 210}
 
 _lib = None
 
@@ -308,6 +308,18 @@ def synth_q4_k(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
     return blk.reshape(n, -1)
 
 
+def synth_q6_k(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
+    """Q6_K rows (K % 256 == 0): random 6-bit codes (ql / qh bytes), int8
+    scales ~U{-64..63}, d ~U(0.0002, 0.001) fp16."""
+    nb = n * (k // 256)
+    blk = np.empty((nb, 210), np.uint8)
+    blk[:, 0:192] = rng.integers(0, 256, (nb, 192), dtype=np.uint8)
+    blk[:, 192:208] = rng.integers(-64, 64, (nb, 16), dtype=np.int8).view(np.uint8)
+    d = f32_to_f16_bits(rng.uniform(0.0002, 0.001, nb).astype(np.float32))
+    blk[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    return blk.reshape(n, -1)
+
+
 def q4k_pack_scales(sc, mn) -> np.ndarray:
     """The 12 bytes that hold eight 6-bit scales and mins ([..., 8] each), in
     GGML's block_q4_K packing: bytes 0-3 sc[0..3] | (sc[4..7] >> 4) << 6,
@@ -330,4 +342,4 @@ def q4k_scale_min(q12, s: int) -> tuple[int, int]:
 
 
 def synth(scheme: int, rng: np.random.Generator, n: int, k: int) -> np.ndarray:
-    return {Q4_1: synth_q4_1, Q8_0: synth_q8_0, Q4_0: synth_q4_0, Q4_K: synth_q4_k}[scheme](rng, n, k)
+    return {Q4_1: synth_q4_1, Q8_0: synth_q8_0, Q4_0: synth_q4_0, Q4_K: synth_q4_k, Q6_K: synth_q6_k}[scheme](rng, n, k)

@@ -126,11 +126,12 @@ int64_t orc_block_bytes(int scheme) {
         case ORC_GGUF_Q4_0: return 2 + QK / 2;
         case ORC_GGUF_Q4_1: return 4 + QK / 2;
         case ORC_GGUF_Q4_K: return 2 + 2 + 12 + QKK / 2;
+        case ORC_GGUF_Q6_K: return QKK / 2 + QKK / 4 + QKK / 16 + 2;
         default: return -1;
     }
 }
 
-int64_t orc_block_len(int scheme) { return scheme == ORC_GGUF_Q4_K ? QKK : QK; }
+int64_t orc_block_len(int scheme) { return (scheme == ORC_GGUF_Q4_K || scheme == ORC_GGUF_Q6_K) ? QKK : QK; }
 
 int64_t orc_row_bytes(int scheme, int64_t k) {
     int64_t bb = orc_block_bytes(scheme), len = orc_block_len(scheme);
@@ -202,7 +203,7 @@ static void quant_q4_1_block(const float* x, uint8_t* out) {
 
 int orc_quantize(int scheme, const float* src, int64_t n, uint8_t* dst) {
     int64_t bb = orc_block_bytes(scheme);
-    if (bb < 0 || n % QK || scheme == ORC_GGUF_Q4_K) return -1;  /* no Q4_K encoder */
+    if (bb < 0 || n % QK || scheme == ORC_GGUF_Q4_K || scheme == ORC_GGUF_Q6_K) return -1;  /* no K-quant encoders */
     for (int64_t b = 0; b < n / QK; b++) {
         const float* x = src + b * QK;
         uint8_t* o = dst + b * bb;
@@ -275,11 +276,37 @@ static void dequant_q4k_block(const uint8_t* b, float* o) {
     }
 }
 
+/* GGUF Q6_K (GGML block_q6_K; QuantScheme::GgufQ6K, decoded by the absent
+ * rlx_gguf::dequant_q6_k): 256 weights in 210 bytes -- ql[128] (low 4 bits
+ * of each 6-bit code), qh[64] (high 2 bits), int8 scales[16] (one per 16
+ * weights), f16 d.  In half h (weights 128h..128h+127; ql + 64h, qh + 32h,
+ * scales + 8h), for l < 32 and j < 4, weight 128h + 32j + l has
+ *   code = (ql[64h + l + 32 (j & 1)] >> 4 (j >> 1)) & 15
+ *          | ((qh[32h + l] >> 2j) & 3) << 4,
+ *   scale = scales[8h + 2j + l / 16],
+ * and w = (d * scale) * (code - 32), each product rounded to f32 in that
+ * order (d * scale is exact). */
+static void dequant_q6k_block(const uint8_t* b, float* o) {
+    const uint8_t* ql = b;
+    const uint8_t* qh = b + 128;
+    const int8_t* sc = (const int8_t*)(b + 192);
+    const float d = rd_f16(b + 208);
+    for (int h = 0; h < 2; h++)
+        for (int j = 0; j < 4; j++)
+            for (int l = 0; l < 32; l++) {
+                const int lo = (ql[64 * h + l + 32 * (j & 1)] >> (4 * (j >> 1))) & 15;
+                const int hi = (qh[32 * h + l] >> (2 * j)) & 3;
+                const float ds = d * (float)sc[8 * h + 2 * j + l / 16];
+                o[128 * h + 32 * j + l] = ds * (float)((lo | (hi << 4)) - 32);
+            }
+}
+
 int orc_dequantize(int scheme, const uint8_t* src, int64_t n, float* dst) {
     int64_t bb = orc_block_bytes(scheme), len = orc_block_len(scheme);
     if (bb < 0 || n % len) return -1;
     for (int64_t b = 0; b < n / len; b++) {
-        if (scheme == ORC_GGUF_Q4_K) dequant_q4k_block(src + b * bb, dst + b * len);
+        if (scheme == ORC_GGUF_Q6_K) dequant_q6k_block(src + b * bb, dst + b * len);
+        else if (scheme == ORC_GGUF_Q4_K) dequant_q4k_block(src + b * bb, dst + b * len);
         else dequant_block(scheme, src + b * bb, dst + b * len);
     }
     return 0;
@@ -407,7 +434,7 @@ static float dot_refl(int scheme, const float* x, const uint8_t* row, int64_t k)
 
 int orc_matmul_refl(int scheme, const float* x, const uint8_t* w, int64_t m,
                     int64_t k, int64_t n, float* y) {
-    if (scheme == ORC_GGUF_Q4_K) return -1;  /* reference-order loop: legacy blocks only */
+    if (scheme == ORC_GGUF_Q4_K || scheme == ORC_GGUF_Q6_K) return -1;  /* reference-order loop: legacy blocks only */
     int64_t rb = orc_row_bytes(scheme, k);
     if (rb < 0) return -1;
     for (int64_t r = 0; r < m; r++)
@@ -420,7 +447,7 @@ int orc_matmul_refl(int scheme, const float* x, const uint8_t* w, int64_t m,
 int orc_matmul_refl_par(int scheme, const float* x, const uint8_t* w,
                         int64_t m, int64_t k, int64_t n, float* y,
                         int nthreads) {
-    if (scheme == ORC_GGUF_Q4_K) return -1;
+    if (scheme == ORC_GGUF_Q4_K || scheme == ORC_GGUF_Q6_K) return -1;
     int64_t rb = orc_row_bytes(scheme, k);
     if (rb < 0) return -1;
 #ifdef _OPENMP

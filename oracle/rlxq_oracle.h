@@ -28,6 +28,11 @@
  *                                  is absent: pinned by closed forms and bit-level
  *                                  probes of the scale packing, "parity unpinned"
  *                                  against reference code.
+ *   dequantize Q6_K ............. the public GGML block_q6_K layout (ql / qh /
+ *                                  int8 scales per 16 weights / f16 d); absent
+ *                                  rlx_gguf::dequant_q6_k: pinned by bit probes
+ *                                  of the code layout and closed forms, "parity
+ *                                  unpinned" against reference code.
  *   MLX affine dequant .......... pinned (mlx_dequant.rs:100-110 KAT,
  *                                  mlx_affine.rs:290-330 matmul test)
  *   matmul / grouped / MoE ...... pinned (closed forms, f64 brute force,
@@ -54,6 +59,7 @@ enum {
     ORC_MLX_AFFINE8 = 5,
     ORC_INT8_BLOCK = 6,
     ORC_GGUF_Q4_K = 7,
+    ORC_GGUF_Q6_K = 8,
 };
 
 /* ---- scalar conversions (IEEE binary16 / bfloat16, round to nearest even) */
@@ -67,7 +73,7 @@ void orc_f32_to_bf16_n(const float* src, int64_t n, uint16_t* dst);
 void orc_bf16_to_f32_n(const uint16_t* src, int64_t n, float* dst);
 
 /* ---- GGUF legacy block codecs (32 weights per block) -------------------- */
-int64_t orc_block_bytes(int scheme);           /* 34 / 18 / 20 / 144 (Q4_K), else -1 */
+int64_t orc_block_bytes(int scheme);           /* 34 / 18 / 20 / 144 (Q4_K) / 210 (Q6_K), else -1 */
 int64_t orc_block_len(int scheme);             /* weights per block: 32, or 256 (Q4_K) */
 int64_t orc_row_bytes(int scheme, int64_t k);  /* k/len * block bytes, else -1 */
 /* Quantize n (multiple of 32) floats into packed blocks. 0 on success. */

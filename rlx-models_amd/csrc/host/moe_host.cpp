@@ -36,7 +36,8 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   if (x_dtype != RLXQ_F32 && x_dtype != RLXQ_BF16) return fail(ctx, RLXQ_E_DTYPE, std::string(what) + ": x_dtype");
   if (y_dtype != RLXQ_F32 && y_dtype != RLXQ_BF16) return fail(ctx, RLXQ_E_DTYPE, std::string(what) + ": y_dtype");
   int64_t rb = 0;
-  if (scheme == RLXQ_GGUF_Q4_K) return fail(ctx, RLXQ_E_SCHEME, std::string(what) + ": Q4_K serves dense calls only");
+  if (scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K)
+    return fail(ctx, RLXQ_E_SCHEME, std::string(what) + ": K-quants serve dense calls only");
   int rc = check_weights(ctx, what, scheme, group, bank, scales, biases, sb_dtype, k, &rb);
   if (rc) return rc;
   if (!aligned(x, 16)) return fail(ctx, RLXQ_E_ALIGN, std::string(what) + ": x must be 16-byte aligned");

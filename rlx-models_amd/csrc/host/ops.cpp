@@ -30,6 +30,7 @@ const char* scheme_name(int s) {
     case RLXQ_MLX_AFFINE4: return "mlx4";
     case RLXQ_MLX_AFFINE8: return "mlx8";
     case RLXQ_GGUF_Q4_K: return "q4_k";
+    case RLXQ_GGUF_Q6_K: return "q6_k";
     default: return nullptr;
   }
 }
@@ -60,7 +61,7 @@ int pick_lanes(int64_t units, const int* cands, int ncand) {
 // single-row family, RLXQ_GEMV_CFG="L,P,C,D,W" overrides it (tuning sweeps and
 // the per-variant parity test); a variant that was not compiled fails with
 // RLXQ_E_NOKERNEL.
-GemvCfg pick_gemv(int64_t m, int64_t units, int64_t lds_rec_bytes_m4, size_t max_lds, bool wide_units) {
+GemvCfg pick_gemv(int64_t m, int64_t units, int64_t lds_rec_bytes_m4, size_t max_lds, int scheme) {
   GemvCfg c;
   if (m >= 2 && lds_rec_bytes_m4 <= (int64_t)max_lds) {
     static const int c4[] = {64, 8};
@@ -68,9 +69,13 @@ GemvCfg pick_gemv(int64_t m, int64_t units, int64_t lds_rec_bytes_m4, size_t max
   } else {
     static const int c1[] = {64, 32, 16, 8};
     const int L = pick_lanes(units, c1, 4);
-    // 12-dword units (Q4_K) spill in the two-chunk 16-wave variant: one chunk,
-    // four steps in flight
-    c = L == 64 ? (wide_units ? GemvCfg{64, 1, 1, 1, 4, 16} : GemvCfg{64, 1, 2, 1, 2, 16}) : GemvCfg{L, 2, 1, 1, 2, 8};
+    // The K-quants' wide units (12 dwords for Q4_K, 21 for Q6_K) spill in the
+    // two-chunk 16-wave variant: Q4_K takes one chunk with four steps in
+    // flight, Q6_K the 8-wave variant.
+    c = L != 64 ? GemvCfg{L, 2, 1, 1, 2, 8}
+                : scheme == RLXQ_GGUF_Q4_K ? GemvCfg{64, 1, 1, 1, 4, 16}
+                : scheme == RLXQ_GGUF_Q6_K ? GemvCfg{64, 1, 2, 1, 2, 8}
+                                           : GemvCfg{64, 1, 2, 1, 2, 16};
   }
   const char* e = c.MT == 1 ? std::getenv("RLXQ_GEMV_CFG") : nullptr;
   if (e) {
@@ -91,6 +96,12 @@ int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const 
     if (k % 256) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": Q4_K needs K % 256 == 0 (super-blocks)");
     if (!aligned(w, 16)) return fail(ctx, RLXQ_E_ALIGN, std::string(what) + ": Q4_K rows must be 16-byte aligned");
     *rb = k / 256 * 144;
+    return RLXQ_OK;
+  }
+  if (scheme == RLXQ_GGUF_Q6_K) {
+    if (k % 256) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": Q6_K needs K % 256 == 0 (super-blocks)");
+    if (!aligned(w, 4)) return fail(ctx, RLXQ_E_ALIGN, std::string(what) + ": Q6_K weights must be 4-byte aligned");
+    *rb = k / 256 * 210;
     return RLXQ_OK;
   }
   if (is_gguf(scheme)) {
@@ -243,6 +254,7 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     bool gemm_ok = xbf && k % 64 == 0 && m >= 1;
     const bool f16_gemm = !is_mlx(scheme) && scheme != RLXQ_GGUF_Q4_K;
     bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (f16_gemm && m > 256));
+    if (scheme == RLXQ_GGUF_Q6_K) gemm_ok = use_gemm = false;   // (Q6_K: the GEMV family only)
     if (const char* e = std::getenv("RLXQ_PREFILL")) {
       if (!std::strcmp(e, "gemv")) use_gemm = false;
       if (!std::strcmp(e, "gemm")) use_gemm = gemm_ok;
@@ -322,7 +334,7 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
 
   const int64_t rec_bytes = (xbf ? 20 : 36) * 4;
   const int64_t bpr = k / 32;
-  const GemvCfg cfg = pick_gemv(m, units, 4 * bpr * rec_bytes, ctx->max_lds, scheme == RLXQ_GGUF_Q4_K);
+  const GemvCfg cfg = pick_gemv(m, units, 4 * bpr * rec_bytes, ctx->max_lds, scheme);
   const int waves = cfg.W;
   const int64_t tile = (int64_t)waves * cfg.P * (64 / cfg.L);
   const int64_t lds = cfg.MT * bpr * rec_bytes;

@@ -195,6 +195,7 @@ const char* rlxq_last_kernel(const rlxq_ctx* ctx) { return ctx ? ctx->last_kerne
 
 int64_t rlxq_row_bytes(int scheme, int64_t k) {
   if (scheme == RLXQ_GGUF_Q4_K) return (k <= 0 || k % 256) ? -1 : k / 256 * 144;
+  if (scheme == RLXQ_GGUF_Q6_K) return (k <= 0 || k % 256) ? -1 : k / 256 * 210;
   int64_t bb = gguf_block_bytes(scheme);
   if (bb < 0 || k <= 0 || k % 32) return -1;
   return k / 32 * bb;

@@ -17,6 +17,7 @@ enum : int {
   SCH_MLX4 = 4,
   SCH_MLX8 = 5,
   SCH_Q4_K = 7,
+  SCH_Q6_K = 8,
 };
 
 // GGUF Q4_K: 6-bit scale and min of sub-block s (0..7) from a super-block's

@@ -136,9 +136,13 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
           const float scl = __uint_as_float(xrec[NPL * 16 + 2]);
 #pragma unroll
           for (int p = 0; p < P; p++) {
-            const float cc = block_dot<SCH, NPL>(pw[p], xrec);
-            acc[p][m] = fmaf(BIT8 ? d[p] * scl : d[p], cc, acc[p][m]);
-            if constexpr (HAS_MIN) acc[p][m] = fmaf(mn[p], sx, acc[p][m]);
+            if constexpr (SCH == SCH_Q6_K) {
+              acc[p][m] += q6k_block_dot<NPL>(pw[p], xrec, d[p], mn[p]);   // mn: the second half's d
+            } else {
+              const float cc = block_dot<SCH, NPL>(pw[p], xrec);
+              acc[p][m] = fmaf(BIT8 ? d[p] * scl : d[p], cc, acc[p][m]);
+              if constexpr (HAS_MIN) acc[p][m] = fmaf(mn[p], sx, acc[p][m]);
+            }
           }
         }
       }
@@ -540,5 +544,6 @@ RLXQ_GEMV_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMV_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_GEMV_SCHEME(q8_0, SCH_Q8_0)
 RLXQ_GEMV_SCHEME(q4_k, SCH_Q4_K)
+RLXQ_GEMV_SCHEME(q6_k, SCH_Q6_K)
 RLXQ_GEMV_SCHEME(mlx4, SCH_MLX4)
 RLXQ_GEMV_SCHEME(mlx8, SCH_MLX8)

@@ -43,6 +43,16 @@ struct Unit<SCH_Q4_K> {
   static constexpr int BLOCKS = 2, BYTES = 36, DW = 12;
   static constexpr bool BIT8 = false;
 };
+// GGUF Q6_K: a unit is one 32-weight sub-block (half h, quarter j) of a
+// 210-byte super-block, which is only 2-byte aligned: the nine aligned dwords
+// covering its 32 ql bytes and the nine covering its 32 qh bytes, its two
+// int8 scales, the f16 d, and a word with the alignment and j (computed from
+// the address, not loaded).  BYTES is the row stride per unit (210 / 8).
+template <>
+struct Unit<SCH_Q6_K> {
+  static constexpr int BLOCKS = 1, BYTES = 26, DW = 21;
+  static constexpr bool BIT8 = false;
+};
 
 // Offset that the code -> float trick adds to each code, and the value the
 // dot chain starts from (in units of the block's plane sum) so that the chain
@@ -51,7 +61,8 @@ struct Unit<SCH_Q4_K> {
 //   Q8_0: q (bias 1024 + 128, codes stored as q ^ 0x80)   MLX8: code (1024)
 template <int SCH>
 RLXQ_DEV constexpr float chain_bias() {
-  return SCH == SCH_Q4_0 ? 136.f : (SCH == SCH_Q8_0 ? 1152.f : (SCH == SCH_MLX8 ? 1024.f : 128.f));
+  return SCH == SCH_Q4_0 ? 136.f
+         : (SCH == SCH_Q8_0 ? 1152.f : (SCH == SCH_MLX8 ? 1024.f : (SCH == SCH_Q6_K ? 160.f : 128.f)));
 }
 
 // Element pair (a, b) of a 32-element block that plane dword t carries.
@@ -66,7 +77,7 @@ RLXQ_DEV void plane_pair(int t, int& a, int& b) {
     int base = 4 * i + ((e & 1) ? 16 : 0) + ((e & 2) ? 1 : 0);
     a = base;
     b = base + 2;
-  } else if constexpr (SCH == SCH_Q4_K) {
+  } else if constexpr (SCH == SCH_Q4_K || SCH == SCH_Q6_K) {
     // code dword i = bytes 4i..4i+3 of the group: low nibbles are the first
     // sub-block's elements 4i..4i+3 (the high ones the second's); extraction
     // e = 0 -> (4i, 4i+2), e = 1 -> (4i+1, 4i+3).
@@ -99,6 +110,11 @@ RLXQ_DEV float group8_sum(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
   v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
   v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  return v;
+}
+RLXQ_DEV float group4_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
   return v;
 }
 RLXQ_DEV float group8_max(float v) {
@@ -201,6 +217,9 @@ RLXQ_DEV void stage_store(uint32_t* lds, const XRaw<XBF16>& raw, int m, int K, i
       }
     }
     const float S = (!BIT8 && XBF16) ? sx : group8_sum(ps);
+    // sum of the record's first 16 elements (lanes q < 4; Q6_K's halves)
+    float S_lo = 0.f;
+    if constexpr (SCH == SCH_Q6_K) S_lo = group4_sum((!BIT8 && XBF16) ? (v[0] + v[1]) + (v[2] + v[3]) : ps);
     // the two plane dwords of this lane and their positions t0, t1
     uint32_t h0, h1, l0 = 0u, l1 = 0u;
     int t0, t1;
@@ -230,7 +249,7 @@ RLXQ_DEV void stage_store(uint32_t* lds, const XRaw<XBF16>& raw, int m, int K, i
       h1 = hi[1] | (hi[3] << 16);
       l0 = lo[0] | (lo[2] << 16);
       l1 = lo[1] | (lo[3] << 16);
-      if constexpr (BIT8 || SCH == SCH_Q4_K) {
+      if constexpr (BIT8 || SCH == SCH_Q4_K || SCH == SCH_Q6_K) {
         t0 = 2 * q;
         t1 = 2 * q + 1;
       } else {
@@ -251,7 +270,7 @@ RLXQ_DEV void stage_store(uint32_t* lds, const XRaw<XBF16>& raw, int m, int K, i
         rec[NPL * 16 + 0] = __float_as_uint(S);
         rec[NPL * 16 + 1] = __float_as_uint(sx);
         rec[NPL * 16 + 2] = __float_as_uint(scl);
-        rec[NPL * 16 + 3] = 0u;
+        rec[NPL * 16 + 3] = __float_as_uint(S_lo);
       }
     }
   }
@@ -319,7 +338,20 @@ RLXQ_DEV void load_unit(uint32_t* dw, const uint8_t* p) {
 // and its 32 code bytes of group u % 4, all 16-byte aligned loads.
 template <int SCH>
 RLXQ_DEV void load_unit_at(uint32_t* dw, const uint8_t* rp, int u) {
-  if constexpr (SCH == SCH_Q4_K) {
+  if constexpr (SCH == SCH_Q6_K) {
+    const uint8_t* sb = rp + (int64_t)(u >> 3) * 210;
+    const int h = (u >> 2) & 1, j = u & 3;
+    const uint32_t off = (uint32_t)reinterpret_cast<uintptr_t>(sb) & 3u;   // 0 or 2
+    const uint8_t* ql = sb + 64 * h + 32 * (j & 1) - off;
+    const uint8_t* qh = sb + 128 + 32 * h - off;
+#pragma unroll
+    for (int i = 0; i < 9; i++) dw[i] = ld_u32(ql + 4 * i);
+#pragma unroll
+    for (int i = 0; i < 9; i++) dw[9 + i] = ld_u32(qh + 4 * i);
+    dw[18] = *reinterpret_cast<const uint16_t*>(sb + 192 + 8 * h + 2 * j);
+    dw[19] = *reinterpret_cast<const uint16_t*>(sb + 208);
+    dw[20] = off | ((uint32_t)j << 8);
+  } else if constexpr (SCH == SCH_Q4_K) {
     const uint8_t* sb = rp + (int64_t)(u >> 2) * 144;
     const uint4 h = ld_u128(sb), a = ld_u128(sb + 16 + 32 * (u & 3)), b = ld_u128(sb + 32 + 32 * (u & 3));
     dw[0] = h.x; dw[1] = h.y; dw[2] = h.z; dw[3] = h.w;
@@ -335,6 +367,13 @@ RLXQ_DEV void load_unit_at(uint32_t* dw, const uint8_t* rp, int u) {
 // u is the unit's index in its row (Q4_K: which group of the super-block).
 template <int SCH>
 RLXQ_DEV void block_scales(const uint32_t* dw, int blk, float& d, float& m, int u = 0) {
+  if constexpr (SCH == SCH_Q6_K) {
+    // d * scale of the block's first and second 16 weights (both exact)
+    const float dd = f16_bits_to_f32(dw[19] & 0xffffu);
+    d = dd * (float)(int8_t)(dw[18] & 0xffu);
+    m = dd * (float)(int8_t)((dw[18] >> 8) & 0xffu);
+    return;
+  }
   if constexpr (SCH == SCH_Q4_K) {
     float sc, mn;
     q4k_scale_min(dw, 2 * (u & 3) + blk, sc, mn);
@@ -382,6 +421,17 @@ RLXQ_DEV void block_pairs(const uint32_t* dw, int blk, uint32_t* pw, const Unpac
   } else if constexpr (SCH == SCH_MLX4) {
 #pragma unroll
     for (int i = 0; i < 4; i++) nib_pairs(dw[i], &pw[4 * i], k);
+  } else if constexpr (SCH == SCH_Q6_K) {
+    // code = (ql nibble j >> 1) | (qh bits 2j..2j+1) << 4, as bf16 128 + code
+    const uint32_t off = dw[20] & 3u, j = dw[20] >> 8;
+    const uint32_t ns = 4 * (j >> 1), hs = 2 * j;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t ql = off ? align_bytes(dw[i + 1], dw[i], 2) : dw[i];
+      const uint32_t qh = off ? align_bytes(dw[10 + i], dw[9 + i], 2) : dw[9 + i];
+      pw[2 * i] = ((ql >> ns) & k.mask) | (((qh >> hs) & 0x00030003u) << 4) | k.magic;
+      pw[2 * i + 1] = ((ql >> (ns + 8)) & k.mask) | (((qh >> (hs + 8)) & 0x00030003u) << 4) | k.magic;
+    }
   } else if constexpr (SCH == SCH_Q4_K) {
     // sub-block blk: the low (0) or high (1) nibbles of the group's 32 bytes
 #pragma unroll
@@ -394,6 +444,23 @@ RLXQ_DEV void block_pairs(const uint32_t* dw, int blk, uint32_t* pw, const Unpac
 #pragma unroll
     for (int i = 0; i < 8; i++) byte_pairs(dw[i], &pw[2 * i]);
   }
+}
+
+// Q6_K: the block's two 16-weight halves carry their own scale, so the
+// chain runs per half from -bias times the half's sum (record word
+// NPL*16+3 holds the first half's sum) and each half takes its d * scale.
+template <int NPL>
+RLXQ_DEV float q6k_block_dot(const uint32_t* pw, const uint32_t* xr, float d_lo, float d_hi) {
+  const float s = __uint_as_float(xr[NPL * 16 + 0]), s_lo = __uint_as_float(xr[NPL * 16 + 3]);
+  float lo = -160.f * s_lo, hi = -160.f * (s - s_lo);
+#pragma unroll
+  for (int t = 0; t < 8; t++) {
+    lo = dot2_bf16(pw[t], xr[t], lo);
+    if constexpr (NPL == 2) lo = dot2_bf16(pw[t], xr[16 + t], lo);
+    hi = dot2_bf16(pw[8 + t], xr[8 + t], hi);
+    if constexpr (NPL == 2) hi = dot2_bf16(pw[8 + t], xr[24 + t], hi);
+  }
+  return fmaf(d_lo, lo, d_hi * hi);
 }
 
 // sum over the block of (bias + code) * x, started at -bias * S so that it

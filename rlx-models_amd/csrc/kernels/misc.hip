@@ -24,7 +24,21 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_dequant_rows(
   const int64_t r = blk / bpr;
   const int b = (int)(blk - r * bpr);
   float v[8];
-  if (scheme == SCH_Q4_K) {
+  if (scheme == SCH_Q6_K) {
+    // weight 128h + 32j + l of super-block b / 8 (b % 8 = 4h + j):
+    // code = ql nibble | qh 2 bits << 4, w = (d * scale) * (code - 32)
+    const int h = (b >> 2) & 1, j = b & 3;
+    const uint8_t* p = w + r * rb + (int64_t)(b >> 3) * 210;
+    const float d = f16_bits_to_f32((uint32_t)p[208] | ((uint32_t)p[209] << 8));
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int l = 8 * q + i;
+      const int lo = (p[64 * h + l + 32 * (j & 1)] >> (4 * (j >> 1))) & 15;
+      const int hi = (p[128 + 32 * h + l] >> (2 * j)) & 3;
+      const float ds = d * (float)(int8_t)p[192 + 8 * h + 2 * j + l / 16];
+      v[i] = ds * (float)((lo | (hi << 4)) - 32);
+    }
+  } else if (scheme == SCH_Q4_K) {
     // sub-block s of super-block b / 8: the low (s even) or high nibbles of
     // the 32 code bytes of group s / 2; w = (d*sc)*q - dmin*mn
     const int s = b & 7, g = s >> 1;

@@ -14,7 +14,7 @@ PKG = Path(__file__).resolve().parent.parent
 LIBPATH = Path(os.environ.get("RLXQ_LIB", PKG / "lib" / "librlxq.so"))
 HEADER = PKG.parent / "include" / "rlxq.h"
 
-GGUF_Q8_0, GGUF_Q4_0, GGUF_Q4_1, MLX_AFFINE4, MLX_AFFINE8, INT8_BLOCK, GGUF_Q4_K = 1, 2, 3, 4, 5, 6, 7
+GGUF_Q8_0, GGUF_Q4_0, GGUF_Q4_1, MLX_AFFINE4, MLX_AFFINE8, INT8_BLOCK, GGUF_Q4_K, GGUF_Q6_K = 1, 2, 3, 4, 5, 6, 7, 8
 F32, BF16 = 0, 1
 MOE_EXPAND, MOE_COMBINE, MOE_EXPAND_SWIGLU = 0, 1, 2
 OK = 0

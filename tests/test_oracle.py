@@ -432,3 +432,103 @@ def test_q4k_rows_and_matmul(orc, rng):
     x = rng.standard_normal((3, k)).astype(np.float32)
     deq = orc.dequantize(orc.Q4_K, w, k).astype(np.float64)
     np.testing.assert_allclose(orc.matmul_f64(orc.Q4_K, x, w, n), x.astype(np.float64) @ deq.T, rtol=1e-12)
+
+
+# ------------------------------------------------------------------- Q6_K
+# GGML block_q6_K (256 weights, 210 B: ql[128], qh[64], int8 scales[16], f16
+# d).  The reference decodes it with the absent rlx_gguf::dequant_q6_k.
+def _q6k_zero(d=1.0):
+    b = np.zeros(210, np.uint8)
+    b[192:208] = 1                                   # unit scales
+    b[208:210] = np.array([d], np.float16).view(np.uint8)
+    return b
+
+
+def test_q6k_low_bits_reach_the_right_weight(orc):
+    """Each of the 1024 ql bits, alone: one weight moves from -32 by 2^bit,
+    at 128h + 32j + l with j = (byte % 64) // 32 for the low nibble and
+    j + 2 for the high one (GGML's q1..q4 order)."""
+    for byte in range(128):
+        for bit in range(8):
+            b = _q6k_zero()
+            b[byte] = 1 << bit
+            got = orc.dequantize(orc.Q6_K, b, 256)[0]
+            h, r = divmod(byte, 64)
+            j = r // 32 + (2 if bit >= 4 else 0)
+            e = 128 * h + 32 * j + r % 32
+            want = np.full(256, -32.0, np.float32)
+            want[e] += 1 << (bit % 4)
+            np.testing.assert_array_equal(got, want, err_msg=f"ql byte {byte} bit {bit}")
+
+
+def test_q6k_high_bits_reach_the_right_weight(orc):
+    """Each of the 512 qh bits: bit pair p of byte 32h + l holds code bits 4-5
+    of weight 128h + 32p + l."""
+    for byte in range(64):
+        for bit in range(8):
+            b = _q6k_zero()
+            b[128 + byte] = 1 << bit
+            got = orc.dequantize(orc.Q6_K, b, 256)[0]
+            h, l = divmod(byte, 32)
+            e = 128 * h + 32 * (bit // 2) + l
+            want = np.full(256, -32.0, np.float32)
+            want[e] += 16 << (bit % 2)
+            np.testing.assert_array_equal(got, want, err_msg=f"qh byte {byte} bit {bit}")
+
+
+def test_q6k_scales_cover_sixteen_weights_each(orc):
+    """scales[t] multiplies exactly weights 16t..16t+15 (signed), and d the
+    whole block: w = d * scale * (code - 32), exact in f32."""
+    for t in range(16):
+        b = _q6k_zero(d=0.5)
+        b[192:208] = 0
+        b[192 + t] = np.int8(-3).view(np.uint8)
+        got = orc.dequantize(orc.Q6_K, b, 256)[0]
+        want = np.zeros(256, np.float32)
+        want[16 * t:16 * t + 16] = 0.5 * -3 * -32
+        np.testing.assert_array_equal(got, want)
+
+
+def test_q6k_exact_products(orc, rng):
+    """d (f16, 11 bits) * scale (int8) * (code - 32) (6 bits) fits 24 bits: every
+    weight equals its exact value, over random blocks."""
+    w = orc.synth_q6_k(rng, 16, 256)
+    got = orc.dequantize(orc.Q6_K, w, 256)
+    for r in range(16):
+        b = w[r]
+        d = float(orc.f16_bits_to_f32(b[208:210].view(np.uint16))[0])
+        sc = b[192:208].view(np.int8).astype(np.float64)
+        for e in range(256):
+            h, rem = divmod(e, 128)
+            j, l = divmod(rem, 32)
+            lo = (int(b[64 * h + l + 32 * (j & 1)]) >> (4 * (j >> 1))) & 15
+            hi = (int(b[128 + 32 * h + l]) >> (2 * j)) & 3
+            exact = d * sc[8 * h + 2 * j + l // 16] * ((lo | hi << 4) - 32)
+            assert got[r, e] == np.float32(exact)
+
+
+def test_q6k_rows_and_matmul(orc, rng):
+    n, k = 5, 768
+    w = orc.synth_q6_k(rng, n, k)
+    assert w.shape == (n, 3 * 210) and orc.row_bytes(orc.Q6_K, k) == 630
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    deq = orc.dequantize(orc.Q6_K, w, k).astype(np.float64)
+    np.testing.assert_allclose(orc.matmul_f64(orc.Q6_K, x, w, n), x.astype(np.float64) @ deq.T, rtol=1e-12)
+
+
+def test_q6k_reference_probe_block(orc):
+    """The reference's own Q6_K probe block (crates/rlx-models-core/src/
+    weight_loader.rs:573-581: d = 1, scale byte 0 = 0xFF, ql[0] = 0x21,
+    qh[0] = 0x08), which it uses to reject decoders that read the scales
+    unsigned: with the signed scale -1, weight 0 is -1 * (1 - 32) = 31 and
+    weights 1..15 (code 0) are 32; every other scale is 0."""
+    b = np.zeros(210, np.uint8)
+    b[192] = 0xFF
+    b[0] = 0x21
+    b[128] = 0x08
+    b[208:210] = np.array([1.0], np.float16).view(np.uint8)
+    got = orc.dequantize(orc.Q6_K, b, 256)[0]
+    want = np.zeros(256, np.float32)
+    want[0] = 31.0
+    want[1:16] = 32.0
+    np.testing.assert_array_equal(got, want)

@@ -151,3 +151,19 @@ def test_q4k_f32_output_prefill_stays_on_gemv(ctx, orc):
     got, want = _run(ctx, orc, x, packed, n)
     assert ctx.last_kernel.startswith("rlxq_gemv_q4_k_"), ctx.last_kernel
     assert rel_err(got, want) <= TOL
+
+
+def test_q4k_device_matmul_session(orc):
+    """The reference's DeviceMatmul scheme table carries GgufQ4K
+    (crates/rlx-laguna/src/device_matmul.rs:64-76): the session API serves it."""
+    import rlxq
+
+    dm = rlxq.DeviceMatmul(0)
+    rng = np.random.default_rng(8)
+    m, k, n = 3, 1024, 333
+    packed = orc.synth_q4_k(rng, n, k).ravel()
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = dm.matmul(x, packed, m, k, n, rlxq.GGUF_Q4_K).reshape(m, n)
+    want = x.astype(np.float64) @ orc.dequantize(orc.Q4_K, packed, k).astype(np.float64).T
+    assert rel_err(y, want) <= TOL
+    dm.close()
