@@ -521,6 +521,8 @@ RLXQ_GEMVXR_WIDE(mlx4, SCH_MLX4)
   RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U1_D2_W8, SCH, 1, 2, 8)       \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8, SCH, 2, 2, 8)       \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U2_D2_W16, SCH, 2, 2, 16)     \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U2_D2_W4, SCH, 2, 2, 4)       \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U2_D1_W4, SCH, 2, 1, 4)       \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U3_D2_W8, SCH, 3, 2, 8)       \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U4_D1_W8, SCH, 4, 1, 8)       \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U4_D2_W8, SCH, 4, 2, 8)

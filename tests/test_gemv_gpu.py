@@ -319,7 +319,8 @@ def test_every_gemv_variant(ctx, orc, monkeypatch, cfg, scheme, xdt):
 # (masked chunks) and row counts that leave waves idle.  "NU,D,W" reads the
 # activations from global memory, "NU,D,W,1" through LDS.
 XR_VARIANTS = ["1,2,4", "2,2,4", "2,1,4", "2,3,4", "2,2,2", "3,2,4", "4,1,4", "4,2,4", "6,1,4", "6,2,4",
-               "1,2,8,1", "2,2,8,1", "2,2,16,1", "3,2,8,1", "4,1,8,1", "4,2,8,1", "6,1,8,1", "6,2,8,1"]
+               "1,2,8,1", "2,2,8,1", "2,2,16,1", "2,2,4,1", "2,1,4,1", "3,2,8,1", "4,1,8,1", "4,2,8,1", "6,1,8,1",
+               "6,2,8,1"]
 
 
 @pytest.mark.parametrize("cfg", XR_VARIANTS)
