@@ -18,7 +18,8 @@
 //    of v_mfma_f32_16x16x32_f16.  f16 weights keep the products within ~2^-12
 //    of the exact dequantised weights (bf16 weights would not meet a 1e-3
 //    output bound).  The four waves' partial sums are added in a fixed order.
-//  * rlxq_skinny_reduce: K splits added in split order (small N only).
+//  * rlxq_skinny_reduce: K splits added in split order (also the prefill
+//    GEMM's split-K reduction).
 #include "common.hip.h"
 #include "f16dq.hip.h"
 #include "gemm_dq.hip.h"
