@@ -200,7 +200,7 @@ int64_t rlxq_row_bytes(int scheme, int64_t k);
 
 /* ---- Host-side session API ----------------------------------------------
  * Mirrors rlx-laguna's DeviceMatmul (crates/rlx-laguna/src/device_matmul.rs:
- * 82-200): host slices in, host f32 out, weights uploaded once per distinct
+ * 82-296): host slices in, host f32 out, weights uploaded once per distinct
  * host pointer and length and kept resident (`uploaded_ptr`, :41-62,301-352),
  * shape mismatch and unknown scheme rejected (:129-146, :64-76). */
 typedef struct rlxq_device_matmul rlxq_device_matmul;
@@ -217,8 +217,22 @@ int rlxq_dm_grouped_matmul(rlxq_device_matmul* dm, const float* x,
                            const float* expert_idx, size_t idx_len, size_t m,
                            size_t k, size_t n, size_t num_experts, int scheme,
                            float* y);
+/* down(silu(gate(x)) * up(x)) per row with expert expert_idx[row]
+ * (DeviceMatmul::grouped_swiglu, crates/rlx-laguna/src/device_matmul.rs:221-296,
+ * graph :383-426): x [m, h]; gate and up stacks [E, inter, h], down stack
+ * [E, h, inter], each packed GGUF with its own scheme; y [m, h].  Gate and up
+ * of one scheme are kept as one gate|up bank on the device (one upload) and
+ * run as one launch with the SwiGLU fused. */
+int rlxq_dm_grouped_swiglu(rlxq_device_matmul* dm, const float* x,
+                           size_t x_len, const float* expert_idx,
+                           size_t idx_len, const uint8_t* w_gate,
+                           size_t gate_len, int gate_scheme,
+                           const uint8_t* w_up, size_t up_len, int up_scheme,
+                           const uint8_t* w_down, size_t down_len,
+                           int down_scheme, size_t m, size_t h, size_t inter,
+                           size_t num_experts, float* y);
 /* Number of weight uploads performed so far (re-upload is skipped when the
- * same host pointer and length come back). */
+ * same host pointers and lengths come back; a gate|up bank counts once). */
 int64_t rlxq_dm_upload_count(const rlxq_device_matmul* dm);
 
 #ifdef __cplusplus

@@ -59,6 +59,7 @@ def lib() -> C.CDLL:
         "rlxq_dm_last_error": (C.c_char_p, [P]),
         "rlxq_dm_matmul": (I, [P, P, S, P, S, S, S, S, I, P]),
         "rlxq_dm_grouped_matmul": (I, [P, P, S, P, S, P, S, S, S, S, S, I, P]),
+        "rlxq_dm_grouped_swiglu": (I, [P, P, S, P, S, P, S, I, P, S, I, P, S, I, S, S, S, S, P]),
         "rlxq_dm_upload_count": (I64, [P]),
     }
     for name, (res, args) in sig.items():
@@ -305,5 +306,22 @@ class DeviceMatmul:
         y = np.empty(m * n, np.float32)
         rc = lib().rlxq_dm_grouped_matmul(self.h, x.ctypes.data, x.size, w_bytes.ctypes.data, w_bytes.size,
                                           idx.ctypes.data, idx.size, m, k, n, num_experts, scheme, y.ctypes.data)
+        self._check(rc)
+        return y
+
+    def grouped_swiglu(self, x, expert_idx, w_gate, gate_scheme: int, w_up, up_scheme: int, w_down,
+                       down_scheme: int, m: int, h: int, inter: int, num_experts: int):
+        """down(silu(gate(x)) * up(x)) per row (DeviceMatmul::grouped_swiglu,
+        crates/rlx-laguna/src/device_matmul.rs:221-296): f32 [m * h]."""
+        import numpy as np
+
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        idx = np.ascontiguousarray(expert_idx, dtype=np.float32).ravel()
+        ws = [np.ascontiguousarray(w, dtype=np.uint8).ravel() for w in (w_gate, w_up, w_down)]
+        y = np.empty(m * h, np.float32)
+        rc = lib().rlxq_dm_grouped_swiglu(self.h, x.ctypes.data, x.size, idx.ctypes.data, idx.size,
+                                          ws[0].ctypes.data, ws[0].size, gate_scheme, ws[1].ctypes.data,
+                                          ws[1].size, up_scheme, ws[2].ctypes.data, ws[2].size, down_scheme,
+                                          m, h, inter, num_experts, y.ctypes.data)
         self._check(rc)
         return y

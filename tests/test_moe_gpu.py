@@ -230,6 +230,78 @@ def test_device_matmul_grouped_session(orc):
     dm.close()
 
 
+def _swiglu_f64(orc, x, idx, wg, gs, wu, us, wd, ds, h, inter, E):
+    g = orc.grouped_matmul_f64(gs, x, wg, idx, inter, E)
+    u = orc.grouped_matmul_f64(us, x, wu, idx, inter, E)
+    return orc.grouped_matmul_f64(ds, g / (1 + np.exp(-g)) * u, wd, idx, h, E)
+
+
+@pytest.mark.parametrize("schemes", [(3, 3, 3), (1, 1, 2), (2, 1, 3)], ids=lambda s: "-".join(map(str, s)))
+def test_device_matmul_grouped_swiglu(orc, schemes):
+    """DeviceMatmul::grouped_swiglu: down(silu(gate(x)) * up(x)) with the
+    expert of each row for all three projections (device_matmul.rs:221-296,
+    graph :383-426); gate and up of one scheme run as one gate|up launch."""
+    import torch
+    import rlxq
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    gs, us, ds = schemes
+    announce(f"DeviceMatmul grouped_swiglu schemes={schemes}")
+    dm = rlxq.DeviceMatmul(0)
+    rng = np.random.default_rng(21)
+    m, h, inter, E = 11, 512, 384, 6
+    wg = _bank(orc, gs, inter, h, E, 0.2, 0.7)
+    wu = _bank(orc, us, inter, h, E, 0.45, 0.9)
+    wd = _bank(orc, ds, h, inter, E, 0.65, 1.1)
+    x = rng.standard_normal((m, h)).astype(np.float32)
+    idx = (np.arange(m) * 5 % E).astype(np.float32)
+    y = dm.grouped_swiglu(x, idx, wg, gs, wu, us, wd, ds, m, h, inter, E).reshape(m, h)
+    assert rel_err(y, _swiglu_f64(orc, x, idx, wg, gs, wu, us, wd, ds, h, inter, E)) <= TOL
+    assert dm.uploads == (2 if gs == us else 3)
+    y2 = dm.grouped_swiglu(x[:4] * 0.5, idx[:4], wg, gs, wu, us, wd, ds, 4, h, inter, E).reshape(4, h)
+    assert dm.uploads == (2 if gs == us else 3)   # same host stacks: resident
+    assert rel_err(y2, _swiglu_f64(orc, x[:4] * 0.5, idx[:4], wg, gs, wu, us, wd, ds, h, inter, E)) <= TOL
+    bad = idx.copy()
+    bad[2] = -1
+    with pytest.raises(rlxq.RlxqError) as e:
+        dm.grouped_swiglu(x, bad, wg, gs, wu, us, wd, ds, m, h, inter, E)
+    assert e.value.status == rlxq.E_INDEX
+    with pytest.raises(rlxq.RlxqError) as e:
+        dm.grouped_swiglu(x, idx, wg, gs, wu, us, wd[:-1], ds, m, h, inter, E)
+    assert e.value.status == rlxq.E_SHAPE and "down weight bytes" in str(e.value)
+    with pytest.raises(rlxq.RlxqError) as e:
+        dm.grouped_swiglu(x[:, :9], idx, wg, gs, wu, us, wd, ds, m, h, inter, E)
+    assert e.value.status == rlxq.E_SHAPE and "x len" in str(e.value)
+    dm.close()
+
+
+def test_device_matmul_grouped_swiglu_bank_layout(ctx, orc):
+    """The session's gate|up bank (per expert: gate rows, then up rows) gives
+    exactly what the fused EXPAND_SWIGLU call gives on a bank built that way
+    on the host, followed by the grouped down projection."""
+    import torch
+    import rlxq
+
+    m, h, inter, E = 9, 256, 160, 5
+    announce("DeviceMatmul grouped_swiglu bank layout")
+    rng = np.random.default_rng(22)
+    wg = orc.synth_q4_1(rng, E * inter, h)
+    wu = orc.synth_q4_1(rng, E * inter, h)
+    wd = orc.synth_q4_1(rng, E * h, inter)
+    x = rng.standard_normal((m, h)).astype(np.float32)
+    idx = (np.arange(m) * 3 % E).astype(np.float32)
+    dm = rlxq.DeviceMatmul(0)
+    y = dm.grouped_swiglu(x, idx, wg, 3, wu, 3, wd, 3, m, h, inter, E).reshape(m, h)
+    dm.close()
+    gu = np.concatenate([wg.reshape(E, inter, -1), wu.reshape(E, inter, -1)], axis=1).reshape(-1)
+    ids = _t(idx.astype(np.int32).reshape(m, 1))
+    mid = ctx.moe_grouped(_t(x), _t(gu), ids, None, 3, rlxq.MOE_EXPAND_SWIGLU, 2 * inter, E)
+    want = ctx.grouped_matmul(mid, _t(wd), _t(idx), 3, h, E)
+    torch.cuda.synchronize()
+    assert np.array_equal(y, want.cpu().numpy())
+
+
 # ------------------------------------------------- routing variants and SwiGLU
 @pytest.mark.parametrize("route", ["table", "fused"])
 @pytest.mark.parametrize("scheme", [1, 3])
