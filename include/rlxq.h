@@ -74,7 +74,11 @@ typedef enum rlxq_status {
     RLXQ_E_NOMEM = -7,    /* device or host allocation failed               */
     RLXQ_E_INDEX = -8,    /* expert index outside [0, num_experts)          */
     RLXQ_E_NOKERNEL = -9, /* code object lacks the kernel for this variant  */
-    RLXQ_E_DEVICE = -10   /* device is not gfx950 or does not exist         */
+    RLXQ_E_DEVICE = -10,  /* device is not gfx950 or does not exist         */
+    RLXQ_E_IO = -11,      /* a checkpoint file cannot be opened or read     */
+    RLXQ_E_FORMAT = -12,  /* a checkpoint file is not valid GGUF            */
+    RLXQ_E_NOTFOUND = -13,/* no tensor or metadata key of that name         */
+    RLXQ_E_TAKEN = -14    /* the weight was already taken                   */
 } rlxq_status;
 
 typedef struct rlxq_ctx rlxq_ctx;
@@ -234,6 +238,69 @@ int rlxq_dm_grouped_swiglu(rlxq_device_matmul* dm, const float* x,
 /* Number of weight uploads performed so far (re-upload is skipped when the
  * same host pointers and lengths come back; a gate|up bank counts once). */
 int64_t rlxq_dm_upload_count(const rlxq_device_matmul* dm);
+
+/* ---- GGUF checkpoints: the on-disk step in front of the kernels ---------
+ * Replaces the reference's GgufLoader packed path
+ * (crates/rlx-models-core/src/weight_loader.rs:1360-1486, type map :497-565;
+ * container parser: external crate rlx_gguf ^0.2.19) and its streamed upload
+ * (crates/rlx-qwen3/src/high_level_runner.rs:474-499).  GGUF versions 2 and 3.
+ * Host code only, except rlxq_gguf_upload. */
+typedef struct rlxq_gguf rlxq_gguf;
+typedef struct rlxq_gguf_tensor {
+    const char* name;       /* valid until rlxq_gguf_close                    */
+    int32_t ggml_type;      /* ggml type id as stored (F32 0, Q4_0 2, Q4_1 3,
+                               Q8_0 8, Q4_K 12, Q6_K 14, BF16 30, ...)        */
+    int32_t n_dims;         /* 1..4                                           */
+    int64_t dims[4];        /* as stored: innermost first (unused dims = 1)   */
+    uint64_t offset;        /* absolute file offset of the tensor's bytes     */
+    int64_t nbytes;         /* -1 when the type has no fixed block layout here */
+    int32_t scheme;         /* rlxq_scheme the kernels read it as, 0 = none   */
+} rlxq_gguf_tensor;
+/* Parse the header (the data is read on demand).  *out is set even when the
+ * return is an error, so that rlxq_gguf_last_error can name the problem; the
+ * handle is then only good for that and rlxq_gguf_close. */
+int rlxq_gguf_open(const char* path, rlxq_gguf** out);
+void rlxq_gguf_close(rlxq_gguf* g);
+const char* rlxq_gguf_last_error(const rlxq_gguf* g);
+int rlxq_gguf_version(const rlxq_gguf* g);
+/* File offset of the aligned data section (general.alignment, default 32). */
+int64_t rlxq_gguf_data_offset(const rlxq_gguf* g);
+int64_t rlxq_gguf_tensor_count(const rlxq_gguf* g);
+/* Index of the tensor, or RLXQ_E_NOTFOUND. */
+int64_t rlxq_gguf_find_tensor(const rlxq_gguf* g, const char* name);
+int rlxq_gguf_tensor_info(const rlxq_gguf* g, int64_t i, rlxq_gguf_tensor* info);
+/* take_packed / take_packed_metadata (weight_loader.rs:1363-1486): the scheme
+ * and the shape reversed to outermost first ([out, in] for a projection, as
+ * the reference's `shape.reverse()`), and marks the weight taken; a second
+ * take is RLXQ_E_TAKEN ("weight already taken").  A tensor stored in a form
+ * the kernels do not read packed (F32, F16, BF16, other ggml types) gives
+ * *scheme = 0 and RLXQ_OK and is not taken (the reference's Ok(None)).
+ * Q4_1 always stays packed (the reference's RLX_GGUF_PACKED_Q4_1 opt-in
+ * exists because its GPU backends cannot dequantise Q4_1). */
+int rlxq_gguf_take_packed(rlxq_gguf* g, const char* name, int* scheme,
+                          int64_t shape[4], int* n_dims, int64_t* nbytes);
+/* The tensor's bytes as stored, into host memory of cap bytes (pread). */
+int rlxq_gguf_read(rlxq_gguf* g, const char* name, void* dst, size_t cap);
+/* The tensor's bytes as stored, into device memory of cap bytes: pread into
+ * two 32 MiB pinned staging buffers, each copied on `stream` while the other
+ * refills.  Returns when the last copy is queued; the bytes are on the device
+ * once `stream` has run it.  The staging buffers live until rlxq_gguf_close. */
+int rlxq_gguf_upload(rlxq_gguf* g, const char* name, void* dst, size_t cap,
+                     void* stream);
+/* Metadata: index of a key (or RLXQ_E_NOTFOUND), its name, its GGUF value
+ * type (0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32, 7 bool, 8 string,
+ * 9 array, 10 u64, 11 i64, 12 f64), element type and count (1 for a
+ * scalar); element j as an integer, a float or a string (RLXQ_E_DTYPE when
+ * the value is not of that kind). */
+int64_t rlxq_gguf_meta_count(const rlxq_gguf* g);
+int64_t rlxq_gguf_meta_find(const rlxq_gguf* g, const char* key);
+const char* rlxq_gguf_meta_key(const rlxq_gguf* g, int64_t i);
+int rlxq_gguf_meta_type(const rlxq_gguf* g, int64_t i, int* type,
+                        int* elem_type, uint64_t* count);
+int rlxq_gguf_meta_int(const rlxq_gguf* g, int64_t i, uint64_t j, int64_t* v);
+int rlxq_gguf_meta_float(const rlxq_gguf* g, int64_t i, uint64_t j, double* v);
+int rlxq_gguf_meta_str(const rlxq_gguf* g, int64_t i, uint64_t j,
+                       const char** s, uint64_t* len);
 
 #ifdef __cplusplus
 }

@@ -68,7 +68,7 @@ def build_host() -> Path:
     tmp = LIB / "librlxq.so.tmp"
     srcs = sorted(str(p) for p in HDIR.glob("*.cpp"))
     cmd = [
-        "g++", "-std=c++17", "-O2", "-fPIC", "-shared",
+        "g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-pthread",
         "-D__HIP_PLATFORM_AMD__", f"-DRLXQ_CO_DIR=\"{CO}\"",
         "-I", str(ROOT / "include"), "-I", str(HDIR), "-I", str(KDIR), "-I", str(ROCM / "include"),
         *srcs, "-o", str(tmp),

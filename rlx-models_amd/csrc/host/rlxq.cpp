@@ -185,6 +185,10 @@ const char* rlxq_strerror(int s) {
     case RLXQ_E_INDEX: return "expert index out of range";
     case RLXQ_E_NOKERNEL: return "kernel variant not available";
     case RLXQ_E_DEVICE: return "device is not gfx950";
+    case RLXQ_E_IO: return "checkpoint file cannot be opened or read";
+    case RLXQ_E_FORMAT: return "not a valid GGUF file";
+    case RLXQ_E_NOTFOUND: return "no tensor or key of that name";
+    case RLXQ_E_TAKEN: return "weight already taken";
     default: return "unknown status";
   }
 }

@@ -19,8 +19,15 @@ F32, BF16 = 0, 1
 MOE_EXPAND, MOE_COMBINE, MOE_EXPAND_SWIGLU = 0, 1, 2
 OK = 0
 E_NULL, E_SHAPE, E_SCHEME, E_ALIGN, E_DTYPE, E_HIP, E_NOMEM, E_INDEX, E_NOKERNEL, E_DEVICE = range(-1, -11, -1)
+E_IO, E_FORMAT, E_NOTFOUND, E_TAKEN = range(-11, -15, -1)
 
 _lib = None
+
+
+class GgufTensorInfo(C.Structure):
+    """rlxq_gguf_tensor."""
+    _fields_ = [("name", C.c_char_p), ("ggml_type", C.c_int32), ("n_dims", C.c_int32),
+                ("dims", C.c_int64 * 4), ("offset", C.c_uint64), ("nbytes", C.c_int64), ("scheme", C.c_int32)]
 
 
 class RlxqError(RuntimeError):
@@ -61,6 +68,25 @@ def lib() -> C.CDLL:
         "rlxq_dm_grouped_matmul": (I, [P, P, S, P, S, P, S, S, S, S, S, I, P]),
         "rlxq_dm_grouped_swiglu": (I, [P, P, S, P, S, P, S, I, P, S, I, P, S, I, S, S, S, S, P]),
         "rlxq_dm_upload_count": (I64, [P]),
+        "rlxq_gguf_open": (I, [C.c_char_p, C.POINTER(P)]),
+        "rlxq_gguf_close": (None, [P]),
+        "rlxq_gguf_last_error": (C.c_char_p, [P]),
+        "rlxq_gguf_version": (I, [P]),
+        "rlxq_gguf_data_offset": (I64, [P]),
+        "rlxq_gguf_tensor_count": (I64, [P]),
+        "rlxq_gguf_find_tensor": (I64, [P, C.c_char_p]),
+        "rlxq_gguf_tensor_info": (I, [P, I64, C.POINTER(GgufTensorInfo)]),
+        "rlxq_gguf_take_packed": (I, [P, C.c_char_p, C.POINTER(I), C.POINTER(I64), C.POINTER(I),
+                                      C.POINTER(I64)]),
+        "rlxq_gguf_read": (I, [P, C.c_char_p, P, S]),
+        "rlxq_gguf_upload": (I, [P, C.c_char_p, P, S, P]),
+        "rlxq_gguf_meta_count": (I64, [P]),
+        "rlxq_gguf_meta_find": (I64, [P, C.c_char_p]),
+        "rlxq_gguf_meta_key": (C.c_char_p, [P, I64]),
+        "rlxq_gguf_meta_type": (I, [P, I64, C.POINTER(I), C.POINTER(I), C.POINTER(C.c_uint64)]),
+        "rlxq_gguf_meta_int": (I, [P, I64, C.c_uint64, C.POINTER(I64)]),
+        "rlxq_gguf_meta_float": (I, [P, I64, C.c_uint64, C.POINTER(C.c_double)]),
+        "rlxq_gguf_meta_str": (I, [P, I64, C.c_uint64, C.POINTER(C.c_char_p), C.POINTER(C.c_uint64)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -325,3 +351,114 @@ class DeviceMatmul:
                                           m, h, inter, num_experts, y.ctypes.data)
         self._check(rc)
         return y
+
+
+class GgufTensor:
+    """One tensor info of a GGUF file: `shape` innermost first, as stored."""
+
+    def __init__(self, ti: GgufTensorInfo):
+        self.name = ti.name.decode()
+        self.dtype = int(ti.ggml_type)
+        self.shape = [int(ti.dims[d]) for d in range(ti.n_dims)]
+        self.offset = int(ti.offset)
+        self.nbytes = int(ti.nbytes)
+        self.scheme = int(ti.scheme)
+
+    def __repr__(self):
+        return f"GgufTensor({self.name!r}, type={self.dtype}, shape={self.shape}, nbytes={self.nbytes})"
+
+
+class GgufFile:
+    """A GGUF checkpoint through rlxq_gguf_* (GgufFile / GgufLoader's packed
+    path: crates/rlx-models-core/src/weight_loader.rs:1360-1486)."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        rc = lib().rlxq_gguf_open(str(path).encode(), C.byref(h))
+        if rc != OK:
+            msg = lib().rlxq_gguf_last_error(h).decode() if h else strerror(rc)
+            lib().rlxq_gguf_close(h)
+            raise RlxqError(rc, msg)
+        self.h = h
+        L = lib()
+        self.version = int(L.rlxq_gguf_version(h))
+        self.data_offset = int(L.rlxq_gguf_data_offset(h))
+        self.tensors = {}
+        for i in range(int(L.rlxq_gguf_tensor_count(h))):
+            ti = GgufTensorInfo()
+            self._check(L.rlxq_gguf_tensor_info(h, i, C.byref(ti)))
+            t = GgufTensor(ti)
+            self.tensors[t.name] = t
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().rlxq_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc: int) -> None:
+        if rc != OK:
+            raise RlxqError(rc, lib().rlxq_gguf_last_error(self.h).decode() or strerror(rc))
+
+    def get(self, name: str):
+        return self.tensors.get(name)
+
+    def keys(self) -> list:
+        L = lib()
+        return [L.rlxq_gguf_meta_key(self.h, i).decode() for i in range(int(L.rlxq_gguf_meta_count(self.h)))]
+
+    def meta(self, key: str):
+        """The value of a metadata key: int, float, bool, str or a list of them."""
+        L = lib()
+        i = int(L.rlxq_gguf_meta_find(self.h, key.encode()))
+        if i < 0:
+            raise KeyError(key)
+        ty, el, cnt = C.c_int(), C.c_int(), C.c_uint64()
+        self._check(L.rlxq_gguf_meta_type(self.h, i, C.byref(ty), C.byref(el), C.byref(cnt)))
+
+        def one(j):
+            if el.value == 8:
+                sp, n = C.c_char_p(), C.c_uint64()
+                self._check(L.rlxq_gguf_meta_str(self.h, i, j, C.byref(sp), C.byref(n)))
+                return C.string_at(sp, n.value).decode("utf-8", "replace")
+            if el.value in (6, 12):
+                v = C.c_double()
+                self._check(L.rlxq_gguf_meta_float(self.h, i, j, C.byref(v)))
+                return v.value
+            v = C.c_int64()
+            self._check(L.rlxq_gguf_meta_int(self.h, i, j, C.byref(v)))
+            return bool(v.value) if el.value == 7 else v.value
+
+        if ty.value == 9:
+            return [one(j) for j in range(cnt.value)]
+        return one(0)
+
+    def take_packed(self, name: str):
+        """(scheme, shape outermost first, nbytes), or None for a tensor the
+        kernels do not read packed (not taken then); raises on a second take."""
+        sch, nd, nb = C.c_int(), C.c_int(), C.c_int64()
+        shape = (C.c_int64 * 4)()
+        self._check(lib().rlxq_gguf_take_packed(self.h, name.encode(), C.byref(sch), shape, C.byref(nd),
+                                                C.byref(nb)))
+        if sch.value == 0:
+            return None
+        return sch.value, [int(shape[d]) for d in range(nd.value)], int(nb.value)
+
+    def read(self, name: str):
+        import numpy as np
+
+        t = self.tensors[name]
+        out = np.empty(max(t.nbytes, 0), np.uint8)
+        self._check(lib().rlxq_gguf_read(self.h, name.encode(), out.ctypes.data, out.size))
+        return out
+
+    def upload(self, name: str, dst, *, stream=None):
+        """The tensor's bytes into the device tensor `dst` (pread + pinned staging)."""
+        nbytes = dst.numel() * dst.element_size()
+        self._check(lib().rlxq_gguf_upload(self.h, name.encode(), _ptr(dst), nbytes, _stream(stream)))
+        return dst
