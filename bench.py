@@ -330,11 +330,24 @@ def synth_mlx_gpu(n: int, k: int, bits: int, group: int, gen):
     return codes, sc, bi
 
 
+def synth_mxfp4_gpu(n: int, k: int, gen, decoded: bool = False):
+    """MXFP4 rows on the device: random code bytes and E8M0 scale bytes in
+    [115, 125] ([n, k / 32] uint8), or those scales decoded to bf16."""
+    import torch
+
+    codes = torch.randint(0, 256, (n * k // 2,), device="cuda", dtype=torch.uint8, generator=gen)
+    eb = torch.randint(115, 126, (n, k // 32), device="cuda", dtype=torch.uint8, generator=gen)
+    if decoded:
+        return codes, (eb.to(torch.int16) << 7).view(torch.bfloat16)
+    return codes, eb
+
+
 def schemes_section(ctx, gen, sptr, stream) -> dict:
     """The other weight formats of the op at M=1 (bf16 activations, f32
     output) on the gate_up shape 4096->24576, weights rotated past the MALL:
-    GGUF Q4_0, Q4_K and Q6_K, MLX affine 4/8-bit (group 64, bf16 slabs), Int8Block (i8
-    [K, N] with an f32 scale per column); the MLX 4-bit grouped op at the
+    GGUF Q4_0, Q4_K and Q6_K, MLX affine 4/8-bit (group 64, bf16 slabs), MXFP4
+    (E8M0 byte scales), Int8Block (i8 [K, N] with an f32 scale per column); the
+    MLX 4-bit and MXFP4 (bf16 decoded scales) grouped ops at the
     MoE config's gate|up shape; and the bit-exact dequantisation kernel
     (Q4_1 to f32).  Bytes: weights (+ scale slabs) + activations + outputs."""
     import torch
@@ -369,6 +382,8 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
         measure(f"mlx{bits}_g64_gemv_m1", wb, lambda bits=bits: synth_mlx_gpu(n, k, bits, 64, gen),
                 lambda w, bits=bits: ctx.dequant_matmul(x, w[0], rlxq.MLX_AFFINE4 if bits == 4 else rlxq.MLX_AFFINE8,
                                                         n, group=64, scales=w[1], biases=w[2], y=y, stream=sptr))
+    measure("mxfp4_gemv_m1", n * k / 2 + n * k / 32, lambda: synth_mxfp4_gpu(n, k, gen),
+            lambda w: ctx.dequant_matmul(x, w[0], rlxq.MLX_MXFP4, n, scales=w[1], y=y, stream=sptr))
     measure("int8_block_gemv_m1", n * k + n * 4,
             lambda: (torch.randint(-127, 128, (k, n), device="cuda", dtype=torch.int8, generator=gen),
                      torch.rand((n,), device="cuda", generator=gen) * 0.01 + 1e-4),
@@ -392,6 +407,20 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
     res["mlx4_grouped_gate_up"] = {"kernel": ctx.last_kernel, "us": round(us, 2), "unique_experts": uniq,
                                    "GBps": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                                    "launches": "device routing table from the f32 indices, then the grouped GEMV"}
+    del banks
+    torch.cuda.empty_cache()
+    # the same with MXFP4 experts (codes + decoded bf16 scales, no bias slab)
+    banks = [synth_mxfp4_gpu(E * N2, H, gen, decoded=True) for _ in range(2)]
+    run = lambda i: ctx.grouped_matmul(xg, banks[i % 2][0], idx, rlxq.MLX_MXFP4, N2, E, scales=banks[i % 2][1],
+                                       y=yg, stream=sptr)
+    run(0)
+    run(1)
+    torch.cuda.synchronize()
+    us = _time_us(run, 20, stream)
+    b = uniq * (N2 * H / 2 + N2 * (H // 32) * 2) + R * H * 2 + R * N2 * 4
+    res["mxfp4_grouped_gate_up"] = {"kernel": ctx.last_kernel, "us": round(us, 2), "unique_experts": uniq,
+                                    "GBps": round(b / us / 1e3, 1),
+                                    "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
     del banks
     torch.cuda.empty_cache()
 

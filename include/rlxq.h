@@ -49,18 +49,28 @@ typedef enum rlxq_scheme {
                              6-bit scales/mins, 128 nibble bytes;
                              w = (d*sc)*q - dmin*mn.  Dense DequantMatMul and
                              dequantize only; K % 256 == 0, w 16-byte aligned  */
-    RLXQ_GGUF_Q6_K = 8    /* GgufQ6K (weight_loader.rs maps GgmlType::Q6K;
+    RLXQ_GGUF_Q6_K = 8,   /* GgufQ6K (weight_loader.rs maps GgmlType::Q6K;
                              host twin rlx_gguf::dequant_q6_k, crates/rlx-sam3/
                              src/packed_gguf.rs): 210 B / 256 w: ql[128],
                              qh[64], int8 scales[16], f16 d;
                              w = (d*scale)*(code - 32).  Dense DequantMatMul
                              (GEMV family) and dequantize; K % 256 == 0       */
+    RLXQ_MLX_MXFP4 = 9    /* MlxMxfp4{group_size: 32} (crates/rlx-models-core/
+                             src/mxfp4_pack.rs:16-50): codes [N, K/2], two E2M1
+                             codes per byte, low nibble = even element; one
+                             scale per 32: E8M0 bytes [N, K/32] (RLXQ_U8, the
+                             dense op's operand; 2^(b-127), b = 0 -> 0) or the
+                             decoded value as BF16 (the grouped op's [E, N, G]
+                             operand).  No bias (biases are not read).
+                             w = E2M1(code) * scale.  GEMV family, grouped ops
+                             and dequantize                                    */
 } rlxq_scheme;
 
 /* Element types of activations, outputs and MLX scale/bias slabs. */
 typedef enum rlxq_dtype {
     RLXQ_F32 = 0,
-    RLXQ_BF16 = 1
+    RLXQ_BF16 = 1,
+    RLXQ_U8 = 2           /* raw bytes: MXFP4's E8M0 scale slab              */
 } rlxq_dtype;
 
 typedef enum rlxq_status {

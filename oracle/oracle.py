@@ -343,3 +343,82 @@ def q4k_scale_min(q12, s: int) -> tuple[int, int]:
 
 def synth(scheme: int, rng: np.random.Generator, n: int, k: int) -> np.ndarray:
     return {Q4_1: synth_q4_1, Q8_0: synth_q8_0, Q4_0: synth_q4_0, Q4_K: synth_q4_k, Q6_K: synth_q6_k}[scheme](rng, n, k)
+
+
+# ---- MXFP4 (QuantScheme::MlxMxfp4), in numpy ---------------------------------
+# crates/rlx-models-core/src/mxfp4_pack.rs: layout :26-33 (codes [rows, k/2],
+# element c in byte c/2, low nibble when c is even; E8M0 exponent bytes
+# [rows, k/32], b meaning 2^(b-127)), E2M1 table :56-58, encoder :64-128 and
+# :196-250, decoder :263-281 (exp2 with the exponent clamped, :130-135).
+MXFP4 = 9
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0])
+
+
+def e8m0_value(b) -> np.ndarray:
+    """2^(b-127) as the reference decodes it: (b clamped to 0..254) << 7 as
+    bf16 bits, so b = 0 is 0.0 and b = 255 is 2^127 (mxfp4_pack.rs:130-135)."""
+    e = np.clip(np.asarray(b, np.int64), 0, 254)
+    return np.where(e == 0, 0.0, np.ldexp(1.0, (e - 127).astype(np.int64)))
+
+
+def mxfp4_nibbles(codes, rows: int, k: int) -> np.ndarray:
+    c = np.asarray(codes, np.uint8).reshape(rows, k // 2)
+    return np.stack([c & 15, c >> 4], axis=-1).reshape(rows, k)
+
+
+def mxfp4_dequantize(codes, scales, rows: int, k: int) -> np.ndarray:
+    """f64 [rows, k]: E2M1(code) * scale; `scales` are E8M0 bytes (uint8) or
+    the decoded scales as bf16 bits (uint16)."""
+    s = np.asarray(scales).reshape(rows, k // 32)
+    sc = e8m0_value(s) if s.dtype == np.uint8 else bf16_bits_to_f32(s).astype(np.float64)
+    return E2M1[mxfp4_nibbles(codes, rows, k)] * np.repeat(sc, 32, axis=1)
+
+
+def e8m0_exponent(amax) -> np.ndarray:
+    """Smallest b with 6 * 2^(b-127) >= amax, 127 for a zero, negative or
+    non-finite amax (mxfp4_pack.rs:116-128)."""
+    a = np.asarray(amax, np.float32).astype(np.float64)
+    ok = np.isfinite(a) & (a > 0)
+    safe = np.where(ok, a, 1.0)
+    e = np.clip(np.ceil(np.log2(safe / 6.0)), -127, 127).astype(np.int64)
+    for _ in range(3):
+        e = np.where((e < 127) & (np.ldexp(6.0, e) < safe), e + 1, e)
+        e = np.where((e > -127) & (np.ldexp(6.0, e - 1) >= safe), e - 1, e)
+    return np.where(ok, e + 127, 127).astype(np.uint8)
+
+
+def e2m1_code(v, scale) -> np.ndarray:
+    """Nearest E2M1 code of v / scale, ties to even, sign kept (also for
+    -0.0); a non-finite ratio saturates to +-6 (mxfp4_pack.rs:64-112)."""
+    v = np.asarray(v, np.float32)
+    scale = np.asarray(scale, np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.where(scale > 0, v / np.where(scale > 0, scale, 1), np.float32(0.0)).astype(np.float32)
+    a = np.abs(r)
+    mag = np.select([a <= 0.25, a < 0.75, a <= 1.25, a < 1.75, a <= 2.5, a < 3.5, a <= 5.0],
+                    [0, 1, 2, 3, 4, 5, 6], 7).astype(np.uint8)
+    code = np.where(np.signbit(r), mag | 8, mag).astype(np.uint8)
+    return np.where(np.isfinite(r), code, np.where(np.signbit(r), 0x0F, 0x07)).astype(np.uint8)
+
+
+def mxfp4_quantize(w) -> tuple[np.ndarray, np.ndarray]:
+    """Row-major f32 [rows, k] -> (codes uint8 [rows, k/2], E8M0 bytes uint8
+    [rows, k/32]), the reference encoder (mxfp4_pack.rs:196-250)."""
+    w = np.asarray(w, np.float32)
+    rows, k = w.shape
+    g = w.reshape(rows, k // 32, 32)
+    eb = e8m0_exponent(np.max(np.abs(g), axis=2))
+    scale = e8m0_value(eb).astype(np.float32)
+    nib = e2m1_code(g, scale[:, :, None]).reshape(rows, k)
+    codes = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    return codes, eb
+
+
+def mxfp4_matmul_f64(x, codes, scales, n: int) -> np.ndarray:
+    x = np.asarray(x, np.float64)
+    return x @ mxfp4_dequantize(codes, scales, n, x.shape[1]).T
+
+
+def synth_mxfp4(rng: np.random.Generator, n: int, k: int) -> tuple[np.ndarray, np.ndarray]:
+    """MXFP4 rows from N(0, 0.02) weights through the reference encoder."""
+    return mxfp4_quantize((rng.standard_normal((n, k)) * 0.02).astype(np.float32))

@@ -72,7 +72,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   // units cover a row with the least padding, MT entries are served per
   // weight pass.  The LDS-record kernels serve everything else.
   const bool q40 = scheme == RLXQ_GGUF_Q4_0;   // two blocks per unit
-  bool xr = xbf && (scheme == RLXQ_GGUF_Q4_1 || q40 || scheme == RLXQ_MLX_AFFINE4) &&
+  bool xr = xbf && (scheme == RLXQ_GGUF_Q4_1 || q40 || scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_MXFP4) &&
             units <= (q40 ? 128 : 256) && !(is_mlx(scheme) && group % 32);
   if (const char* ev = std::getenv("RLXQ_MOE_KERNEL")) {
     if (!std::strcmp(ev, "lds")) xr = false;
@@ -158,7 +158,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   ga.K = (int32_t)k;
   ga.E = (int32_t)num_experts;
   ga.group = is_mlx(scheme) ? group : 32;
-  ga.sb_bf16 = sb_dtype == RLXQ_BF16 ? 1 : 0;
+  ga.sb_bf16 = sb_code(sb_dtype);
   ga.y_bf16 = (!combine && y_dtype == RLXQ_BF16) ? 1 : 0;
   ga.x_div = x_div;
   ga.swiglu = swiglu ? 1 : 0;

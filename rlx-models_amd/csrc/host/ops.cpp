@@ -31,6 +31,7 @@ const char* scheme_name(int s) {
     case RLXQ_MLX_AFFINE8: return "mlx8";
     case RLXQ_GGUF_Q4_K: return "q4_k";
     case RLXQ_GGUF_Q6_K: return "q6_k";
+    case RLXQ_MLX_MXFP4: return "mxfp4";
     default: return nullptr;
   }
 }
@@ -110,6 +111,18 @@ int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const 
                   std::string(what) + ": Q8_0/Q4_0 need K % 64 == 0 (block pairs are read dword aligned)");
     if (!aligned(w, 4)) return fail(ctx, RLXQ_E_ALIGN, std::string(what) + ": w must be 4-byte aligned");
     *rb = k / 32 * gguf_block_bytes(scheme);
+    return RLXQ_OK;
+  }
+  if (scheme == RLXQ_MLX_MXFP4) {
+    // MlxMxfp4 (crates/rlx-models-core/src/mxfp4_pack.rs:16-50): codes [N, K/2],
+    // one scale per 32 codes (E8M0 bytes, the dense op's U8 operand, or the
+    // decoded bf16 the grouped op takes); no bias (biases are not read)
+    if (group != 32) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": MXFP4 group_size must be 32");
+    if (!scales) return fail(ctx, RLXQ_E_NULL, std::string(what) + ": MXFP4 needs scales");
+    if (sb_dtype != RLXQ_U8 && sb_dtype != RLXQ_BF16)
+      return fail(ctx, RLXQ_E_DTYPE, std::string(what) + ": MXFP4 scales are U8 (E8M0) or BF16");
+    if (!aligned(w, 16)) return fail(ctx, RLXQ_E_ALIGN, std::string(what) + ": MXFP4 codes must be 16-byte aligned");
+    *rb = k / 2;
     return RLXQ_OK;
   }
   if (is_mlx(scheme)) {
@@ -195,7 +208,7 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
   a.rb = rb;
   a.y_ld = n;
   a.group = is_mlx(scheme) ? group : 32;
-  a.sb_bf16 = sb_dtype == RLXQ_BF16 ? 1 : 0;
+  a.sb_bf16 = sb_code(sb_dtype);
   a.y_bf16 = y_dtype == RLXQ_BF16 ? 1 : 0;
   a.tiles_m = (int32_t)tiles_m;
   a.tiles_n = (int32_t)tiles_n;
@@ -254,7 +267,8 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     bool gemm_ok = xbf && k % 64 == 0 && m >= 1;
     const bool f16_gemm = !is_mlx(scheme) && scheme != RLXQ_GGUF_Q4_K;
     bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (f16_gemm && m > 256));
-    if (scheme == RLXQ_GGUF_Q6_K) gemm_ok = use_gemm = false;   // (Q6_K: the GEMV family only)
+    if (scheme == RLXQ_GGUF_Q6_K || scheme == RLXQ_MLX_MXFP4)
+      gemm_ok = use_gemm = false;   // (Q6_K, MXFP4: the GEMV family only)
     if (const char* e = std::getenv("RLXQ_PREFILL")) {
       if (!std::strcmp(e, "gemv")) use_gemm = false;
       if (!std::strcmp(e, "gemm")) use_gemm = gemm_ok;
@@ -289,7 +303,7 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   a.y_ld = n;
   a.K = (int32_t)k;
   a.group = is_mlx(scheme) ? group : 32;
-  a.sb_bf16 = sb_dtype == RLXQ_BF16 ? 1 : 0;
+  a.sb_bf16 = sb_code(sb_dtype);
   a.y_bf16 = y_dtype == RLXQ_BF16 ? 1 : 0;
   void* args[] = {&a};
   char name[96];
@@ -302,7 +316,8 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // RLXQ_GEMV_XR="NU,D,W[,XS]" picks the variant (XS=1: through LDS), "0"
   // turns the path off (tuning).
   const bool q4k = scheme == RLXQ_GGUF_Q4_K;
-  const bool xr_scheme = scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_MLX_AFFINE4 || q4k;
+  const bool xr_scheme = scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_MLX_AFFINE4 ||
+                         scheme == RLXQ_MLX_MXFP4 || q4k;
   const int64_t nchunk64 = (units + 63) / 64;
   const int64_t xr_max = scheme == RLXQ_GGUF_Q4_0 ? 4 : (q4k ? 3 : 6);
   // two chunks (K = 4096 for the one-block units): 4-wave workgroups with one
@@ -381,7 +396,7 @@ int rlxq_dequantize(rlxq_ctx* ctx, int scheme, int group_size, const void* w, co
   DeviceGuard g(ctx->device);
   hipFunction_t fn;
   if ((rc = get_fn(ctx, "rlxq_dequant_rows", &fn))) return rc;
-  int sch = scheme, sb = sb_dtype == RLXQ_BF16, grp = is_mlx(scheme) ? group_size : 32, K = (int)k;
+  int sch = scheme, sb = sb_code(sb_dtype), grp = is_mlx(scheme) ? group_size : 32, K = (int)k;
   int64_t R = rows, RB = rb;
   void* args[] = {&sch, (void*)&w, (void*)&scales, (void*)&biases, &sb, &grp, &R, &K, &RB, (void*)&out};
   const int64_t quarters = rows * (k / 32) * 4;   // one thread per 8 weights

@@ -60,6 +60,8 @@ int workspace(rlxq_ctx* ctx, size_t bytes, void** out);
 
 bool is_gguf(int scheme);
 bool is_mlx(int scheme);
+// Slab dtype as the kernels read it (sb_bf16 field): 0 f32, 1 bf16, 2 bytes.
+inline int sb_code(int sb_dtype) { return sb_dtype == RLXQ_BF16 ? 1 : (sb_dtype == RLXQ_U8 ? 2 : 0); }
 int64_t gguf_block_bytes(int scheme);
 
 // Validates a weight operand (scheme, alignment, MLX scale slabs) and returns

@@ -18,7 +18,21 @@ enum : int {
   SCH_MLX8 = 5,
   SCH_Q4_K = 7,
   SCH_Q6_K = 8,
+  SCH_MXFP4 = 9,
 };
+
+// MXFP4 (OCP microscaling FP4): E2M1 codes, two per byte (low nibble = even
+// element), and one E8M0 exponent byte b per 32 codes, scale 2^(b - 127).
+// b = 0 reads as 0 and b = 255 as 2^127, as the reference decoder's clamped
+// exponent (crates/rlx-models-core/src/mxfp4_pack.rs:130-135, 263-281).
+RLXQ_DEV float e8m0_to_f32(uint32_t b) { return __uint_as_float((b < 254u ? b : 254u) << 23); }
+
+// The two E2M1 codes of byte SEL of w as a bf16 pair (low nibble in the low
+// half), exact: v_cvt_scalef32_pk_bf16_fp4 with scale 1.
+template <int SEL>
+RLXQ_DEV uint32_t fp4x2_to_bf16x2(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, SEL));
+}
 
 // GGUF Q4_K: 6-bit scale and min of sub-block s (0..7) from a super-block's
 // 16-byte head held as dwords (head[0] = f16 d | f16 dmin << 16, head[1..3] =

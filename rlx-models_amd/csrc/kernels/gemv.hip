@@ -1,6 +1,6 @@
 // Dequant-GEMV for decode (M = 1..few rows): y[m, n] = sum_k x[m, k] * W[n, k]
-// over packed GGUF Q4_1 / Q4_0 / Q8_0 blocks or MLX affine 4/8-bit codes,
-// with fp32 accumulation.  Replaces the backend kernel of Op::DequantMatMul
+// over packed GGUF Q4_1 / Q4_0 / Q8_0 / Q4_K / Q6_K blocks, MLX affine 4/8-bit
+// codes or MXFP4 codes, with fp32 accumulation.  Replaces the backend kernel of Op::DequantMatMul
 // (crates/rlx-models-core/src/standard_decoder.rs:727-738).
 //
 // Work split (one wave64 = 64 lanes):
@@ -16,7 +16,9 @@
 //     (4-bit codes) or f16 (8-bit codes) pairs in exactly the order the code
 //     extraction below yields them, plus the block sums.
 //   * 4-bit codes become bf16 (128 + q) with one and-or per pair; 8-bit codes
-//     become f16 (1024 + u) with one byte permute per pair.  v_dot2c
+//     become f16 (1024 + u) with one byte permute per pair; MXFP4 code bytes
+//     become bf16 pairs of their signed E2M1 values with one
+//     v_cvt_scalef32_pk_bf16_fp4 each (no offset to remove).  v_dot2c
 //     accumulates pairs in f32 starting from -bias * (block sum of x), which
 //     removes the 128 / 1024 offset, so the block dot is sum(q * x).
 //   * f32 activations are split into hi + lo planes so the products keep
@@ -47,8 +49,8 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
   constexpr int BYTES = Unit<SCH>::BYTES;
   constexpr int RP = 64 / L;
   constexpr int TILE = WAVES * P * RP;
-  constexpr bool MLX = (SCH == SCH_MLX4 || SCH == SCH_MLX8);
-  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || MLX);
+  constexpr bool SLAB = slab_scales<SCH>(), SBIAS = slab_bias<SCH>();
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SBIAS);
   extern __shared__ uint32_t lds[];
 
   const int K = a.K;
@@ -60,7 +62,7 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
   const int64_t m0 = (int64_t)blockIdx.y * MT;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane / L, li = lane % L;
-  const int gpr = MLX ? K / a.group : 0;  // MLX groups per row
+  const int gpr = SLAB ? K / a.group : 0;  // slab groups per row
   const int64_t row_off = wv * (P * RP) + g;
 
   struct Buf {
@@ -78,12 +80,12 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
         const int u = li + L * (jg * C + c);
         const int uc = u < U ? u : U - 1;
         load_unit_at<SCH>(bf.dw[p][c], rp, uc);
-        if constexpr (MLX) {
+        if constexpr (SLAB) {
 #pragma unroll
           for (int bl = 0; bl < BLOCKS; bl++) {
             const int64_t gi = n * gpr + ((uc * BLOCKS + bl) * 32) / a.group;
-            bf.sm[p][c][bl] = load_sb_raw(a.scales, gi, a.sb_bf16 != 0);
-            bf.bm[p][c][bl] = load_sb_raw(a.biases, gi, a.sb_bf16 != 0);
+            bf.sm[p][c][bl] = load_scale_raw<SCH>(a.scales, gi, a.sb_bf16);
+            if constexpr (SBIAS) bf.bm[p][c][bl] = load_sb_raw(a.biases, gi, a.sb_bf16 != 0);
           }
         }
       }
@@ -110,9 +112,9 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
         uint32_t pw[P][16];
 #pragma unroll
         for (int p = 0; p < P; p++) {
-          if constexpr (MLX) {
-            d[p] = sb_decode(bf.sm[p][c][bl], a.sb_bf16 != 0);
-            mn[p] = sb_decode(bf.bm[p][c][bl], a.sb_bf16 != 0);
+          if constexpr (SLAB) {
+            d[p] = scale_decode<SCH>(bf.sm[p][c][bl], a.sb_bf16);
+            mn[p] = SBIAS ? sb_decode(bf.bm[p][c][bl], a.sb_bf16 != 0) : 0.f;
           } else {
             block_scales<SCH>(bf.dw[p][c], bl, d[p], mn[p], uc);
           }
@@ -232,6 +234,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   constexpr int DW = Unit<SCH>::DW;
   constexpr int BYTES = Unit<SCH>::BYTES;
   constexpr bool MLX = SCH == SCH_MLX4;
+  constexpr bool MX = SCH == SCH_MXFP4;
   constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || MLX);
   static_assert(!Unit<SCH>::BIT8, "register activations serve 4-bit codes");
 
@@ -246,7 +249,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   const uint32_t G = gridDim.x * WAVES, n0u = blockIdx.x * WAVES + wv, N32 = (uint32_t)a.N;
   const int64_t n0 = n0u;
   const int64_t cnt = n0u < N32 ? (N32 - n0u + G - 1) / G : 0;
-  const int gpr = MLX ? K / a.group : 0;
+  const int gpr = (MLX || MX) ? K / a.group : 0;
 
   int uc[NU];
   bool uok[NU];
@@ -267,10 +270,10 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
 #pragma unroll
     for (int c = 0; c < NU; c++) {
       load_unit_at<SCH>(bf.dw[c], rp, uc[c]);
-      if constexpr (MLX) {
+      if constexpr (MLX || MX) {
         const int64_t gi = nn * gpr + (uc[c] * 32) / a.group;
-        bf.sm[c][0] = load_sb_raw(a.scales, gi, a.sb_bf16 != 0);
-        bf.bm[c][0] = load_sb_raw(a.biases, gi, a.sb_bf16 != 0);
+        bf.sm[c][0] = load_scale_raw<SCH>(a.scales, gi, a.sb_bf16);
+        if constexpr (MLX) bf.bm[c][0] = load_sb_raw(a.biases, gi, a.sb_bf16 != 0);
       }
     }
   };
@@ -296,7 +299,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     constexpr int NT = 64 * WAVES;
     constexpr int XH = (2 * 64 * NU * BLOCKS + NT - 1) / NT;   // half-blocks per thread
     constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;
-    constexpr bool LINEAR = MLX || SCH == SCH_Q4_K;   // half h = elements 16h..16h+15
+    constexpr bool LINEAR = MLX || MX || SCH == SCH_Q4_K;   // half h = elements 16h..16h+15
     uint4 xa[XH], xc[XH];
 #pragma unroll
     for (int i = 0; i < XH; i++) {
@@ -317,7 +320,13 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
       uint32_t P[8];
 #pragma unroll
       for (int t = 0; t < 2; t++) {
-        if constexpr (SCH == SCH_Q4_K) {
+        if constexpr (MX) {
+          const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7: pairs (2j, 2j+1) as loaded
+          P[4 * t + 0] = R[0];
+          P[4 * t + 1] = R[1];
+          P[4 * t + 2] = R[2];
+          P[4 * t + 3] = R[3];
+        } else if constexpr (SCH == SCH_Q4_K) {
           const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7: pairs (4j+e, 4j+e+2)
           P[4 * t + 0] = perm_b32(R[1], R[0], LO);
           P[4 * t + 1] = perm_b32(R[1], R[0], HI);
@@ -416,6 +425,9 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
         if constexpr (MLX) {
           d = sb_decode(bf.sm[c][bl], a.sb_bf16 != 0);
           mn = sb_decode(bf.bm[c][bl], a.sb_bf16 != 0);
+        } else if constexpr (MX) {
+          d = scale_decode<SCH>(bf.sm[c][bl], a.sb_bf16);
+          mn = 0.f;
         } else {
           block_scales<SCH>(bf.dw[c], bl, d, mn, uc[c]);
         }
@@ -425,7 +437,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
         }
         uint32_t pw[16];
         block_pairs<SCH>(bf.dw[c], bl, pw, kc);
-        float ch = -chain_bias<SCH>() * S[c][bl];
+        float ch = chain_start<SCH>(S[c][bl]);
 #pragma unroll
         for (int t = 0; t < 16; t++) ch = dot2_bf16(pw[t], X[c][bl][t], ch);
         acc = fmaf(d, ch, acc);
@@ -539,8 +551,10 @@ RLXQ_GEMVXS_Q4K
 RLXQ_GEMVXS_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXS_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_GEMVXS_SCHEME(mlx4, SCH_MLX4)
+RLXQ_GEMVXS_SCHEME(mxfp4, SCH_MXFP4)
 RLXQ_GEMVXS_WIDE(q4_1, SCH_Q4_1)
 RLXQ_GEMVXS_WIDE(mlx4, SCH_MLX4)
+RLXQ_GEMVXS_WIDE(mxfp4, SCH_MXFP4)
 
 RLXQ_GEMV_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMV_SCHEME(q4_0, SCH_Q4_0)
@@ -549,3 +563,4 @@ RLXQ_GEMV_SCHEME(q4_k, SCH_Q4_K)
 RLXQ_GEMV_SCHEME(q6_k, SCH_Q6_K)
 RLXQ_GEMV_SCHEME(mlx4, SCH_MLX4)
 RLXQ_GEMV_SCHEME(mlx8, SCH_MLX8)
+RLXQ_GEMV_SCHEME(mxfp4, SCH_MXFP4)

@@ -34,6 +34,24 @@ struct Unit<SCH_MLX8> {
   static constexpr int BLOCKS = 1, BYTES = 32, DW = 8;
   static constexpr bool BIT8 = true;
 };
+// MXFP4: 16 code bytes per 32 weights (the MLX 4-bit code layout), the E8M0
+// scale in a slab of its own.
+template <>
+struct Unit<SCH_MXFP4> {
+  static constexpr int BLOCKS = 1, BYTES = 16, DW = 4;
+  static constexpr bool BIT8 = false;
+};
+
+// Schemes whose scales live in a slab of their own (MLX affine: scale and
+// bias; MXFP4: scale only).
+template <int SCH>
+RLXQ_DEV constexpr bool slab_scales() {
+  return SCH == SCH_MLX4 || SCH == SCH_MLX8 || SCH == SCH_MXFP4;
+}
+template <int SCH>
+RLXQ_DEV constexpr bool slab_bias() {
+  return SCH == SCH_MLX4 || SCH == SCH_MLX8;
+}
 // GGUF Q4_K: a unit is one 64-weight group of a 256-weight super-block (two
 // 32-weight sub-blocks sharing 32 code bytes): the super-block's 16-byte head
 // (f16 d, f16 dmin, 12 bytes of 6-bit scales and mins) plus the group's 32
@@ -59,10 +77,18 @@ struct Unit<SCH_Q6_K> {
 // ends at sum(w_int * x) where w_int is the scheme's integer weight:
 //   Q4_1/MLX4: q (bias 128)    Q4_0: q - 8 (bias 136)
 //   Q8_0: q (bias 1024 + 128, codes stored as q ^ 0x80)   MLX8: code (1024)
+//   MXFP4: none (the pairs carry the signed E2M1 values themselves)
 template <int SCH>
 RLXQ_DEV constexpr float chain_bias() {
-  return SCH == SCH_Q4_0 ? 136.f
-         : (SCH == SCH_Q8_0 ? 1152.f : (SCH == SCH_MLX8 ? 1024.f : (SCH == SCH_Q6_K ? 160.f : 128.f)));
+  return SCH == SCH_MXFP4 ? 0.f
+         : (SCH == SCH_Q4_0 ? 136.f
+            : (SCH == SCH_Q8_0 ? 1152.f : (SCH == SCH_MLX8 ? 1024.f : (SCH == SCH_Q6_K ? 160.f : 128.f))));
+}
+// Start of a block's dot chain: -bias * (sum of the block's x).
+template <int SCH>
+RLXQ_DEV float chain_start(float s) {
+  if constexpr (SCH == SCH_MXFP4) return 0.f;
+  return -chain_bias<SCH>() * s;
 }
 
 // Element pair (a, b) of a 32-element block that plane dword t carries.
@@ -89,6 +115,10 @@ RLXQ_DEV void plane_pair(int t, int& a, int& b) {
     int i = t >> 2, e = t & 3;
     a = 8 * i + e;
     b = 8 * i + e + 4;
+  } else if constexpr (SCH == SCH_MXFP4) {
+    // code byte t converts to (2t, 2t+1)
+    a = 2 * t;
+    b = 2 * t + 1;
   } else {
     // byte codes, dword i = codes 4i..4i+3; e=0 -> (4i, 4i+2), e=1 -> (4i+1, 4i+3).
     int i = t >> 1, e = t & 1;
@@ -223,7 +253,15 @@ RLXQ_DEV void stage_store(uint32_t* lds, const XRaw<XBF16>& raw, int m, int K, i
     // the two plane dwords of this lane and their positions t0, t1
     uint32_t h0, h1, l0 = 0u, l1 = 0u;
     int t0, t1;
-    if constexpr (SCH == SCH_MLX4) {
+    if constexpr (SCH == SCH_MXFP4) {
+      // pairs (4q, 4q+1) and (4q+2, 4q+3)
+      h0 = hi[0] | (hi[1] << 16);
+      h1 = hi[2] | (hi[3] << 16);
+      l0 = lo[0] | (lo[1] << 16);
+      l1 = lo[2] | (lo[3] << 16);
+      t0 = 2 * q;
+      t1 = 2 * q + 1;
+    } else if constexpr (SCH == SCH_MLX4) {
       // pairs (8j+e, 8j+e+4): even lanes hold 8j..8j+3, odd lanes 8j+4..8j+7
       const uint32_t hp01 = swap_lane_pair(hi[0] | (hi[1] << 16)), hp23 = swap_lane_pair(hi[2] | (hi[3] << 16));
       const uint32_t lp01 = swap_lane_pair(lo[0] | (lo[1] << 16)), lp23 = swap_lane_pair(lo[2] | (lo[3] << 16));
@@ -322,7 +360,7 @@ RLXQ_DEV void load_unit(uint32_t* dw, const uint8_t* p) {
       dw[4 * q] = a.x; dw[4 * q + 1] = a.y; dw[4 * q + 2] = a.z; dw[4 * q + 3] = a.w;
     }
     dw[16] = ld_u32(p + 64);
-  } else if constexpr (SCH == SCH_MLX4) {
+  } else if constexpr (SCH == SCH_MLX4 || SCH == SCH_MXFP4) {
     uint4 a = ld_u128(p);
     dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
   } else if constexpr (SCH == SCH_Q4_K) {
@@ -421,6 +459,15 @@ RLXQ_DEV void block_pairs(const uint32_t* dw, int blk, uint32_t* pw, const Unpac
   } else if constexpr (SCH == SCH_MLX4) {
 #pragma unroll
     for (int i = 0; i < 4; i++) nib_pairs(dw[i], &pw[4 * i], k);
+  } else if constexpr (SCH == SCH_MXFP4) {
+    // byte t of the 16 code bytes -> the E2M1 values of elements (2t, 2t+1)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      pw[4 * i + 0] = fp4x2_to_bf16x2<0>(dw[i]);
+      pw[4 * i + 1] = fp4x2_to_bf16x2<1>(dw[i]);
+      pw[4 * i + 2] = fp4x2_to_bf16x2<2>(dw[i]);
+      pw[4 * i + 3] = fp4x2_to_bf16x2<3>(dw[i]);
+    }
   } else if constexpr (SCH == SCH_Q6_K) {
     // code = (ql nibble j >> 1) | (qh bits 2j..2j+1) << 4, as bf16 128 + code
     const uint32_t off = dw[20] & 3u, j = dw[20] >> 8;
@@ -468,7 +515,7 @@ RLXQ_DEV float q6k_block_dot(const uint32_t* pw, const uint32_t* xr, float d_lo,
 template <int SCH, int NPL>
 RLXQ_DEV float block_dot(const uint32_t* pw, const uint32_t* xr) {
   constexpr bool BIT8 = Unit<SCH>::BIT8;
-  float c = -chain_bias<SCH>() * __uint_as_float(xr[NPL * 16 + 0]);
+  float c = chain_start<SCH>(__uint_as_float(xr[NPL * 16 + 0]));
 #pragma unroll
   for (int t = 0; t < 16; t++) {
     if constexpr (BIT8) {
@@ -496,6 +543,25 @@ RLXQ_DEV SbRaw load_sb_raw(const void* p, int64_t idx, bool bf16) {
 }
 RLXQ_DEV float sb_decode(SbRaw r, bool bf16) {
   return __uint_as_float(bf16 ? (r.lo << 16) : (r.lo | (r.hi << 16)));
+}
+
+// Slab scale of a scheme at idx for the register rings, raw: MLX (f32 or
+// bf16, load_sb_raw); MXFP4 (sbt 2: E8M0 bytes, 1: bf16) as two byte loads
+// from addresses chosen without a branch, both in bounds either way.
+template <int SCH>
+RLXQ_DEV SbRaw load_scale_raw(const void* p, int64_t idx, int sbt) {
+  if constexpr (SCH == SCH_MXFP4) {
+    const uint8_t* b = reinterpret_cast<const uint8_t*>(p);
+    const int64_t i0 = sbt == 2 ? idx : 2 * idx;
+    return {b[i0], b[sbt == 2 ? i0 : i0 + 1]};
+  } else {
+    return load_sb_raw(p, idx, sbt == 1);
+  }
+}
+template <int SCH>
+RLXQ_DEV float scale_decode(SbRaw r, int sbt) {
+  if constexpr (SCH == SCH_MXFP4) return sbt == 2 ? e8m0_to_f32(r.lo) : bf16_bits_to_f32(r.lo | (r.hi << 8));
+  return sb_decode(r, sbt == 1);
 }
 
 // MLX scale/bias for (row n, block b); sb_bf16 selects the slab dtype.
@@ -538,6 +604,12 @@ RLXQ_DEV void pairs_from_raw(const uint32_t* R, uint32_t* X) {
       X[4 * i + 1] = perm_b32(R[4 * i + 1], R[4 * i], HI);
       X[4 * i + 2] = perm_b32(R[4 * i + 3], R[4 * i + 2], LO);
       X[4 * i + 3] = perm_b32(R[4 * i + 3], R[4 * i + 2], HI);
+    } else if constexpr (SCH == SCH_MXFP4) {
+      // t holds (2t, 2t+1): the raw pairs as they are
+      X[4 * i + 0] = R[4 * i + 0];
+      X[4 * i + 1] = R[4 * i + 1];
+      X[4 * i + 2] = R[4 * i + 2];
+      X[4 * i + 3] = R[4 * i + 3];
     } else if constexpr (SCH == SCH_MLX4) {
       // t = 4i+e holds (8i+e, 8i+e+4): R[4i + e/2] and R[4i + 2 + e/2]
       X[4 * i + 0] = perm_b32(R[4 * i + 2], R[4 * i + 0], LO);

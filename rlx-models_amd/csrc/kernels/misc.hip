@@ -6,7 +6,8 @@
 // One thread per eight consecutive weights (a quarter of a 32-weight block),
 // so that a wave writes 2 KB of contiguous f32 with 16-byte stores.  Q8_0:
 // d*q; Q4_0: d*(q-8); Q4_1: d*q + m (d*q is exact in f32, so the single
-// rounding is the add); Q4_K: (d*sc)*q - dmin*mn (GGML block_q4_K); MLX:
+// rounding is the add); Q4_K: (d*sc)*q - dmin*mn (GGML block_q4_K); MXFP4:
+// E2M1(code) * 2^(e - 127) (exact); MLX:
 // scale*code rounded, then + bias rounded (no contraction), as
 // crates/rlx-moshi/src/mlx_dequant.rs:66-71 evaluates it.
 extern "C" __global__ __launch_bounds__(256) void rlxq_dequant_rows(
@@ -60,6 +61,21 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_dequant_rows(
       const int byte = p[16 + 32 * g + 8 * q + i];
       const float prod = d1 * (float)((s & 1) ? byte >> 4 : byte & 15);
       v[i] = prod - m1;
+    }
+  } else if (scheme == SCH_MXFP4) {
+    // codes 8q..8q+7 of the block are dword 4b + q of the row (low nibble =
+    // even element); w = E2M1(code) * scale, exact.  sb_bf16: 2 = E8M0 bytes,
+    // 1 = the decoded scales as bf16.
+    const int64_t gi = r * (int64_t)bpr + b;
+    const float sc = sb_bf16 == 2 ? e8m0_to_f32(reinterpret_cast<const uint8_t*>(scales)[gi])
+                                  : bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(scales)[gi]);
+    const uint32_t cw = reinterpret_cast<const uint32_t*>(w + r * rb)[4 * b + q];
+    const uint32_t pr[4] = {fp4x2_to_bf16x2<0>(cw), fp4x2_to_bf16x2<1>(cw), fp4x2_to_bf16x2<2>(cw),
+                            fp4x2_to_bf16x2<3>(cw)};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      v[2 * i] = bf16_bits_to_f32(pr[i] & 0xffffu) * sc;
+      v[2 * i + 1] = bf16_bits_to_f32(pr[i] >> 16) * sc;
     }
   } else if (scheme == SCH_Q8_0 || scheme == SCH_Q4_0 || scheme == SCH_Q4_1) {
     const int bb = scheme == SCH_Q8_0 ? 34 : (scheme == SCH_Q4_0 ? 18 : 20);

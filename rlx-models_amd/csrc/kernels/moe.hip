@@ -139,8 +139,8 @@ RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, 
   constexpr int RP = 64 / L;
   const int NPASS = a.tile_rows / 4 / RP;  // row passes per wave
   constexpr int D = MOE_RING;
-  constexpr bool MLX = (SCH == SCH_MLX4 || SCH == SCH_MLX8);
-  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || MLX);
+  constexpr bool SLAB = slab_scales<SCH>(), SBIAS = slab_bias<SCH>();
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SBIAS);
   extern __shared__ uint32_t lds[];
   __shared__ float res[SWIGLU ? MT * MOE_TILE_MAX : 1];
 
@@ -152,7 +152,7 @@ RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane / L, li = lane % L;
   const uint8_t* wbase = a.bank + (int64_t)e * a.N * a.rb;
-  const int gpr = MLX ? K / a.group : 0;
+  const int gpr = SLAB ? K / a.group : 0;
   const UnpackK kc = unpack_consts();
 
   auto step_row = [&](int s, int& lr, int& j) {
@@ -208,10 +208,10 @@ RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, 
 #pragma unroll
           for (int bl = 0; bl < BLOCKS; bl++) {
             float dd, mn;
-            if constexpr (MLX) {
+            if constexpr (SLAB) {
               const int64_t gi = ((int64_t)e * a.N + nn) * gpr + ((uc * BLOCKS + bl) * 32) / a.group;
-              dd = load_sb(a.scales, gi, a.sb_bf16 != 0);
-              mn = load_sb(a.biases, gi, a.sb_bf16 != 0);
+              dd = scale_decode<SCH>(load_scale_raw<SCH>(a.scales, gi, a.sb_bf16), a.sb_bf16);
+              mn = SBIAS ? load_sb(a.biases, gi, a.sb_bf16 != 0) : 0.f;
             } else {
               block_scales<SCH>(ring[d], bl, dd, mn);
             }
@@ -292,6 +292,7 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
   constexpr int RP = 64 / L;
   constexpr int R2 = SWIGLU ? 2 : 1;
   constexpr bool MLX = SCH == SCH_MLX4;
+  constexpr bool MX = SCH == SCH_MXFP4;
   constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || MLX);
   static_assert(!Unit<SCH>::BIT8, "register activations serve 4-bit codes");
 
@@ -300,7 +301,7 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
   const int lane = threadIdx.x & 63, g = lane / L, li = lane % L;
   const int64_t width = SWIGLU ? a.N / 2 : a.N;
   const uint8_t* wbase = a.bank + (int64_t)e * a.N * a.rb;
-  const int gpr = MLX ? K / a.group : 0;
+  const int gpr = (MLX || MX) ? K / a.group : 0;
   const int64_t cstride = (int64_t)nw * RP;
 
   int uc[NU];
@@ -326,10 +327,10 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
 #pragma unroll
       for (int c = 0; c < NU; c++) {
         load_unit<SCH>(bf.dw[r][c], rp + (int64_t)uc[c] * BYTES);
-        if constexpr (MLX) {
+        if constexpr (MLX || MX) {
           const int64_t gi = ((int64_t)e * a.N + n) * gpr + (uc[c] * 32) / a.group;
-          bf.sm[r][c] = load_sb_raw(a.scales, gi, a.sb_bf16 != 0);
-          bf.bm[r][c] = load_sb_raw(a.biases, gi, a.sb_bf16 != 0);
+          bf.sm[r][c] = load_scale_raw<SCH>(a.scales, gi, a.sb_bf16);
+          if constexpr (MLX) bf.bm[r][c] = load_sb_raw(a.biases, gi, a.sb_bf16 != 0);
         }
       }
     }
@@ -409,6 +410,9 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
             if constexpr (MLX) {
               d = sb_decode(rb.sm[r][c], a.sb_bf16 != 0);
               mn = sb_decode(rb.bm[r][c], a.sb_bf16 != 0);
+            } else if constexpr (MX) {
+              d = scale_decode<SCH>(rb.sm[r][c], a.sb_bf16);
+              mn = 0.f;
             } else {
               block_scales<SCH>(rb.dw[r][c], bl, d, mn);
             }
@@ -420,7 +424,7 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
             block_pairs<SCH>(rb.dw[r][c], bl, pw, kc);
 #pragma unroll
             for (int m = 0; m < MT; m++) {
-              float ch = -chain_bias<SCH>() * S[m][c][bl];
+              float ch = chain_start<SCH>(S[m][c][bl]);
 #pragma unroll
               for (int t = 0; t < 16; t++) ch = dot2_bf16(pw[t], X[m][c][bl][t], ch);
               acc[r][m] = fmaf(d, ch, acc[r][m]);
@@ -637,6 +641,7 @@ RLXQ_MOE_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_MOE_SCHEME(q8_0, SCH_Q8_0)
 RLXQ_MOE_SCHEME(mlx4, SCH_MLX4)
 RLXQ_MOE_SCHEME(mlx8, SCH_MLX8)
+RLXQ_MOE_SCHEME(mxfp4, SCH_MXFP4)
 
 // Register-activation variants (4-bit codes, bf16 activations):
 // rlxq_moexr[f]_<scheme>_L<L>_U<NU>_M<MT>[_sw]; f = routing in the workgroup.
@@ -671,6 +676,7 @@ RLXQ_MOE_SCHEME(mlx8, SCH_MLX8)
   RLXQ_MOEXR_LU(SNAME, SCH, 8, 4, 2, 1)
 RLXQ_MOEXR_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_MOEXR_SCHEME(mlx4, SCH_MLX4)
+RLXQ_MOEXR_SCHEME(mxfp4, SCH_MXFP4)
 // Q4_0 units hold two blocks: at most four blocks of activations per lane
 // and entry (NU * MT <= 2).
 RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 64, 1, 1, 4)

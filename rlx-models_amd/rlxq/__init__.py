@@ -15,7 +15,8 @@ LIBPATH = Path(os.environ.get("RLXQ_LIB", PKG / "lib" / "librlxq.so"))
 HEADER = PKG.parent / "include" / "rlxq.h"
 
 GGUF_Q8_0, GGUF_Q4_0, GGUF_Q4_1, MLX_AFFINE4, MLX_AFFINE8, INT8_BLOCK, GGUF_Q4_K, GGUF_Q6_K = 1, 2, 3, 4, 5, 6, 7, 8
-F32, BF16 = 0, 1
+MLX_MXFP4 = 9
+F32, BF16, U8 = 0, 1, 2
 MOE_EXPAND, MOE_COMBINE, MOE_EXPAND_SWIGLU = 0, 1, 2
 OK = 0
 E_NULL, E_SHAPE, E_SCHEME, E_ALIGN, E_DTYPE, E_HIP, E_NOMEM, E_INDEX, E_NOKERNEL, E_DEVICE = range(-1, -11, -1)
@@ -130,6 +131,8 @@ def _dt(t) -> int:
         return F32
     if t.dtype == torch.bfloat16:
         return BF16
+    if t.dtype == torch.uint8:
+        return U8
     raise TypeError(f"unsupported dtype {t.dtype}")
 
 

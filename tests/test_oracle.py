@@ -532,3 +532,91 @@ def test_q6k_reference_probe_block(orc):
     want[0] = 31.0
     want[1:16] = 32.0
     np.testing.assert_array_equal(got, want)
+
+
+# ------------------------------------------------------------------ MXFP4
+# The oracle's MXFP4 codec against the reference's own tests of its encoder
+# and decoder (crates/rlx-models-core/src/mxfp4_pack.rs:290-398) and the E8M0
+# known answers of crates/rlx-models-core/src/dsv4_quant.rs:184-188.
+def test_mxfp4_e8m0_known_answers(orc):
+    assert list(orc.e8m0_value([127, 128, 126])) == [1.0, 2.0, 0.5]
+    assert orc.e8m0_value(0) == 0.0 and orc.e8m0_value(255) == 2.0 ** 127 and orc.e8m0_value(254) == 2.0 ** 127
+    assert orc.e8m0_value(1) == 2.0 ** -126
+
+
+def test_mxfp4_layout_low_nibble_is_the_even_element(orc):
+    """mxfp4_pack.rs:30-31: element c of row r is byte r*k/2 + c/2, low
+    nibble when c is even."""
+    rows, k = 2, 64
+    codes = np.zeros((rows, k // 2), np.uint8)
+    scales = np.full((rows, k // 32), 127, np.uint8)
+    codes[1, 5] = 0x72        # element 10: code 2 (1.0), element 11: code 7 (6.0)
+    d = orc.mxfp4_dequantize(codes, scales, rows, k)
+    want = np.zeros((rows, k))
+    want[1, 10], want[1, 11] = 1.0, 6.0
+    assert np.array_equal(d, want)
+    scales[1, 0] = 129        # group 0 of row 1 scaled by 4
+    assert orc.mxfp4_dequantize(codes, scales, rows, k)[1, 11] == 24.0
+
+
+def test_mxfp4_exact_grid_round_trip(orc):
+    """mxfp4_pack.rs:294-308: quantization is the identity on its own grid,
+    bit for bit (signed zero included)."""
+    for e in (-8, -2, 0, 5):
+        row = (orc.E2M1[np.arange(32) % 16] * 2.0 ** e).astype(np.float32)[None, :]
+        codes, eb = orc.mxfp4_quantize(row)
+        back = orc.mxfp4_dequantize(codes, eb, 1, 32).astype(np.float32)
+        assert np.array_equal(back.view(np.uint32), row.view(np.uint32)), e
+
+
+def test_mxfp4_saturation_never_happens(orc):
+    """mxfp4_pack.rs:310-335."""
+    for amax in (1e-6, 0.017, 1.0, 1.9, 6.0, 7.9, 1e4):
+        row = np.zeros((1, 32), np.float32)
+        row[0, 7] = amax
+        codes, eb = orc.mxfp4_quantize(row)
+        scale = orc.e8m0_value(eb[0, 0])
+        assert scale * 6.0 >= np.float32(amax)
+        assert (codes[0, 3] >> 4) <= 7      # element 7: byte 3, high nibble, positive
+        back = orc.mxfp4_dequantize(codes, eb, 1, 32)[0, 7]
+        assert abs(back - np.float32(amax)) <= 0.2 * np.float32(amax)
+
+
+def test_mxfp4_zero_group(orc):
+    """mxfp4_pack.rs:337-343."""
+    codes, eb = orc.mxfp4_quantize(np.zeros((1, 32), np.float32))
+    assert (orc.mxfp4_dequantize(codes, eb, 1, 32) == 0).all() and (eb != 0xFF).all()
+
+
+def test_mxfp4_ties_to_even(orc):
+    """mxfp4_pack.rs:345-361."""
+    for v, want in ((0.25, 0.0), (0.75, 1.0), (1.25, 1.0), (1.75, 2.0), (2.5, 2.0), (3.5, 4.0), (5.0, 4.0)):
+        assert orc.E2M1[orc.e2m1_code(np.float32(v), np.float32(1.0))] == want, v
+
+
+def test_mxfp4_gaussian_cosine(orc):
+    """mxfp4_pack.rs:363-388: the reference's LCG weights (64 x 256, scaled
+    by 0.02) keep cosine > 0.99 through a round trip."""
+    rows, k = 64, 256
+    s = 0x12345678
+    w = np.empty(rows * k, np.float32)
+    for i in range(rows * k):
+        s = (s * 6364136223846793005 + 1) & 0xFFFFFFFFFFFFFFFF
+        u = np.float32(s >> 33) / np.float32(np.float32(0xFFFFFFFF) / np.float32(2.0)) - np.float32(1.0)
+        w[i] = u * np.float32(0.02)
+    w = w.reshape(rows, k)
+    codes, eb = orc.mxfp4_quantize(w)
+    back = orc.mxfp4_dequantize(codes, eb, rows, k)
+    cos = float((w.astype(np.float64) * back).sum() / np.sqrt((w.astype(np.float64) ** 2).sum() * (back ** 2).sum()))
+    assert cos > 0.99
+
+
+def test_mxfp4_exponent_is_the_smallest(orc):
+    """e8m0_exponent's contract (mxfp4_pack.rs:114-128) against brute force:
+    the smallest b with 6 * 2^(b-127) >= amax, powers of two included."""
+    rng = np.random.default_rng(3)
+    amax = np.concatenate([6.0 * 2.0 ** np.arange(-20, 20), rng.uniform(1e-6, 1e3, 200)]).astype(np.float32)
+    got = orc.e8m0_exponent(amax)
+    for a, b in zip(amax, got):
+        want = next(bb for bb in range(1, 255) if 6.0 * 2.0 ** (bb - 127) >= float(a))
+        assert b == want, (a, b, want)
