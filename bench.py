@@ -21,6 +21,7 @@ Extra keys of the same JSON line:
                   activations computed on the fly x per-channel int8 weights)
   batched_decode  config 3: Q4_1 and Q8_0, M in {1, 4, 16, 64}
   moe             config 5: routed-expert grouped GEMV, 16 tokens, top-8 of 128
+  moe_q4_k        the same with Q4_K expert banks (a Q4_K_M MoE checkpoint)
   q8_gemv         config 1: Q8_0 2048->2048, f32 activations
   gguf_upload     a 537 MB GGUF checkpoint streamed from the page cache to HBM
   cpu_baseline    the C restatement of the reference CPU algorithm timed on
@@ -439,7 +440,7 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
     return res
 
 
-def moe_section(ctx, gen, sptr, stream) -> dict:
+def moe_section(ctx, gen, sptr, stream, scheme: str = "q4_1") -> dict:
     """Config 5: one MoE FFN of a Qwen3-30B-A3B-like layer for 16 tokens, as
     three launches: route (softmax of N(0,1) logits over 128 experts, top-8,
     renormalised), the fused gate|up 2048->1536 + SwiGLU per (token, slot),
@@ -449,7 +450,9 @@ def moe_section(ctx, gen, sptr, stream) -> dict:
     import rlxq
 
     E, H, I, TOPK, T = 128, 2048, 768, 8, 16
-    banks = [(synth_q4_1_gpu(E * 2 * I, H, gen), synth_q4_1_gpu(E * H, I, gen)) for _ in range(2)]
+    synth, sch, bpw = {"q4_1": (synth_q4_1_gpu, rlxq.GGUF_Q4_1, Q4_1_BPW),
+                       "q4_k": (synth_q4_k_gpu, rlxq.GGUF_Q4_K, 144 / 256)}[scheme]
+    banks = [(synth(E * 2 * I, H, gen), synth(E * H, I, gen)) for _ in range(2)]
     logits = [torch.randn((T, E), generator=gen, device="cuda") for _ in range(2)]
     x = torch.randn((T, H), generator=gen, device="cuda").to(torch.bfloat16)
     act = torch.empty((T * TOPK, I), device="cuda", dtype=torch.bfloat16)
@@ -460,8 +463,8 @@ def moe_section(ctx, gen, sptr, stream) -> dict:
         bgu, bdn = banks[i % 2]
         ids, probs = ctx.moe_route(logits[i % 2], TOPK, True, stream=sptr)
         routes[i % 2] = ids
-        ctx.moe_grouped(x, bgu, ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_EXPAND_SWIGLU, 2 * I, E, y=act, stream=sptr)
-        ctx.moe_grouped(act, bdn, ids, probs, rlxq.GGUF_Q4_1, rlxq.MOE_COMBINE, H, E, y=y, stream=sptr)
+        ctx.moe_grouped(x, bgu, ids, probs, sch, rlxq.MOE_EXPAND_SWIGLU, 2 * I, E, y=act, stream=sptr)
+        ctx.moe_grouped(act, bdn, ids, probs, sch, rlxq.MOE_COMBINE, H, E, y=y, stream=sptr)
 
     for i in range(4):
         layer(i)
@@ -469,11 +472,11 @@ def moe_section(ctx, gen, sptr, stream) -> dict:
     us = _time_us(layer, 40, stream)
     uniq = [int(torch.unique(r).numel()) for r in routes]
     u = sum(uniq) / len(uniq)
-    per_expert = 2 * I * H * Q4_1_BPW + H * I * Q4_1_BPW
+    per_expert = 2 * I * H * bpw + H * I * bpw
     b = u * per_expert + T * H * 2 + T * TOPK * I * 2 * 2 + T * H * 4
     return {"us_per_layer": round(us, 2), "unique_experts": u, "GBps": round(b / us / 1e3, 1),
             "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-            "bytes_model": "unique experts x (1,966,080 + 983,040) B + activations",
+            "bytes_model": f"unique experts x {int(per_expert):,} B + activations",
             "launches_per_layer": "route, gate|up + SwiGLU (routing in the workgroups), down + combine"}
 
 
@@ -635,6 +638,7 @@ def main() -> int:
         out["prefill"] = prefill_section(ctx, gen, sptr, stream, a.quick)
         out["batched_decode"] = batched_section(ctx, gen, sptr, stream)
         out["moe"] = moe_section(ctx, gen, sptr, stream)
+        out["moe_q4_k"] = moe_section(ctx, gen, sptr, stream, "q4_k")
         out["schemes"] = schemes_section(ctx, gen, sptr, stream)
         out["q8_gemv"] = q8_section(ctx, gen, sptr, stream)
         out["gguf_upload"] = gguf_section(ctx, gen, sptr, stream)

@@ -47,14 +47,14 @@ typedef enum rlxq_scheme {
                              rlx_gguf::dequant_q4_k, crates/rlx-sam3/src/
                              packed_gguf.rs:50): 144 B / 256 w: f16 d, f16 dmin, 12 B of
                              6-bit scales/mins, 128 nibble bytes;
-                             w = (d*sc)*q - dmin*mn.  Dense DequantMatMul and
-                             dequantize only; K % 256 == 0, w 16-byte aligned  */
+                             w = (d*sc)*q - dmin*mn.  Dense and grouped ops,
+                             dequantize; K % 256 == 0, w 16-byte aligned       */
     RLXQ_GGUF_Q6_K = 8,   /* GgufQ6K (weight_loader.rs maps GgmlType::Q6K;
                              host twin rlx_gguf::dequant_q6_k, crates/rlx-sam3/
                              src/packed_gguf.rs): 210 B / 256 w: ql[128],
                              qh[64], int8 scales[16], f16 d;
-                             w = (d*scale)*(code - 32).  Dense DequantMatMul
-                             (GEMV family) and dequantize; K % 256 == 0       */
+                             w = (d*scale)*(code - 32).  Dense (GEMV family)
+                             and grouped ops, dequantize; K % 256 == 0        */
     RLXQ_MLX_MXFP4 = 9    /* MlxMxfp4{group_size: 32} (crates/rlx-models-core/
                              src/mxfp4_pack.rs:16-50): codes [N, K/2], two E2M1
                              codes per byte, low nibble = even element; one
@@ -159,7 +159,7 @@ int rlxq_dequant_grouped_matmul(rlxq_ctx* ctx, int scheme, int group_size,
  *                     expert slabs hold gate rows [0, N/2) then up rows
  *                     [N/2, N); y [rows*top_k, N/2] = silu(g) * u with
  *                     g, u = x[r] . W^T rows, silu(g) = g / (1 + exp(-g))
- * GGUF schemes only (scales/biases NULL).  An id outside [0, num_experts)
+ * GGUF schemes only, K-quants included (scales/biases NULL).  An id outside [0, num_experts)
  * gives a zero output row (EXPAND) or a zero contribution (COMBINE). */
 typedef enum rlxq_moe_mode {
     RLXQ_MOE_EXPAND = 0,

@@ -36,8 +36,6 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   if (x_dtype != RLXQ_F32 && x_dtype != RLXQ_BF16) return fail(ctx, RLXQ_E_DTYPE, std::string(what) + ": x_dtype");
   if (y_dtype != RLXQ_F32 && y_dtype != RLXQ_BF16) return fail(ctx, RLXQ_E_DTYPE, std::string(what) + ": y_dtype");
   int64_t rb = 0;
-  if (scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K)
-    return fail(ctx, RLXQ_E_SCHEME, std::string(what) + ": K-quants serve dense calls only");
   int rc = check_weights(ctx, what, scheme, group, bank, scales, biases, sb_dtype, k, &rb);
   if (rc) return rc;
   if (!aligned(x, 16)) return fail(ctx, RLXQ_E_ALIGN, std::string(what) + ": x must be 16-byte aligned");
@@ -58,7 +56,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     if (!std::strcmp(e, "fused")) fused = fusable, route_forced = true;
   }
   // kernel choice
-  const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0) ? 2 : 1;
+  const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_K) ? 2 : 1;
   const int64_t units = (k / 32) / blocks;
   const bool xbf = x_dtype == RLXQ_BF16;
   const int64_t fired_est = num_experts < n_entries ? num_experts : n_entries;
@@ -67,10 +65,11 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   std::memset(&ga, 0, sizeof ga);
   char name[80];
   int MT = 2;   // entries served per weight pass
-  // Register-activation kernels (4-bit codes: Q4_1, Q4_0, MLX affine 4-bit;
-  // bf16 activations; up to 256 units per row): lane groups of L lanes x NU
-  // units cover a row with the least padding, MT entries are served per
-  // weight pass.  The LDS-record kernels serve everything else.
+  // Register-activation kernels (4-bit codes: Q4_1, Q4_0, MLX affine 4-bit,
+  // MXFP4; bf16 activations; up to 256 units per row): lane groups of L lanes
+  // x NU units cover a row with the least padding, MT entries are served per
+  // weight pass.  The LDS-record kernels serve everything else (Q8_0, MLX
+  // 8-bit, the K-quants, f32 activations).
   const bool q40 = scheme == RLXQ_GGUF_Q4_0;   // two blocks per unit
   bool xr = xbf && (scheme == RLXQ_GGUF_Q4_1 || q40 || scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_MXFP4) &&
             units <= (q40 ? 128 : 256) && !(is_mlx(scheme) && group % 32);
@@ -216,7 +215,8 @@ int rlxq_moe_grouped(rlxq_ctx* ctx, int scheme, int mode, const void* x, int x_d
   if (!ctx) return RLXQ_E_NULL;
   ctx->last_error.clear();
   if (!ids) return fail(ctx, RLXQ_E_NULL, "moe_grouped: ids is null");
-  if (!is_gguf(scheme)) return fail(ctx, RLXQ_E_SCHEME, "moe_grouped: GGUF schemes only");
+  if (!is_gguf(scheme) && scheme != RLXQ_GGUF_Q4_K && scheme != RLXQ_GGUF_Q6_K)
+    return fail(ctx, RLXQ_E_SCHEME, "moe_grouped: GGUF schemes only");
   if (rows < 0 || top_k <= 0 || top_k > 64) return fail(ctx, RLXQ_E_SHAPE, "moe_grouped: need 0 < top_k <= 64");
   if (mode == RLXQ_MOE_EXPAND || mode == RLXQ_MOE_EXPAND_SWIGLU) {
     const bool sw = mode == RLXQ_MOE_EXPAND_SWIGLU;

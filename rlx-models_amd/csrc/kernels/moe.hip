@@ -140,7 +140,7 @@ RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, 
   const int NPASS = a.tile_rows / 4 / RP;  // row passes per wave
   constexpr int D = MOE_RING;
   constexpr bool SLAB = slab_scales<SCH>(), SBIAS = slab_bias<SCH>();
-  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SBIAS);
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SBIAS);
   extern __shared__ uint32_t lds[];
   __shared__ float res[SWIGLU ? MT * MOE_TILE_MAX : 1];
 
@@ -166,7 +166,7 @@ RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, 
     bool rok;
     const int64_t n = tile_row<SWIGLU>(a, tn, lr, rok);
     const int u = li + L * j;
-    load_unit<SCH>(dw, wbase + (rok ? n : 0) * a.rb + (int64_t)(u < U ? u : U - 1) * BYTES);
+    load_unit_at<SCH>(dw, wbase + (rok ? n : 0) * a.rb, u < U ? u : U - 1);
   };
 
   for (int c0 = beg; c0 < end; c0 += MT) {
@@ -213,7 +213,7 @@ RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, 
               dd = scale_decode<SCH>(load_scale_raw<SCH>(a.scales, gi, a.sb_bf16), a.sb_bf16);
               mn = SBIAS ? load_sb(a.biases, gi, a.sb_bf16 != 0) : 0.f;
             } else {
-              block_scales<SCH>(ring[d], bl, dd, mn);
+              block_scales<SCH>(ring[d], bl, dd, mn, uc);
             }
             if (!(rok && uok)) {
               dd = 0.f;
@@ -230,6 +230,10 @@ RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, 
               for (int q = 0; q < RS; q += 4) {
                 const uint4 v = *reinterpret_cast<const uint4*>(xr + q);
                 xrec[q] = v.x; xrec[q + 1] = v.y; xrec[q + 2] = v.z; xrec[q + 3] = v.w;
+              }
+              if constexpr (SCH == SCH_Q6_K) {   // per-half scales: dd, mn = d * scale of each half
+                acc[m] += q6k_block_dot<NPL>(pw, xrec, dd, mn);
+                continue;
               }
               const float cc = block_dot<SCH, NPL>(pw, xrec);
               const float scl = __uint_as_float(xrec[NPL * 16 + 2]);
@@ -642,6 +646,8 @@ RLXQ_MOE_SCHEME(q8_0, SCH_Q8_0)
 RLXQ_MOE_SCHEME(mlx4, SCH_MLX4)
 RLXQ_MOE_SCHEME(mlx8, SCH_MLX8)
 RLXQ_MOE_SCHEME(mxfp4, SCH_MXFP4)
+RLXQ_MOE_SCHEME(q4_k, SCH_Q4_K)
+RLXQ_MOE_SCHEME(q6_k, SCH_Q6_K)
 
 // Register-activation variants (4-bit codes, bf16 activations):
 // rlxq_moexr[f]_<scheme>_L<L>_U<NU>_M<MT>[_sw]; f = routing in the workgroup.

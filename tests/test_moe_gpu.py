@@ -498,3 +498,55 @@ def test_grouped_register_path_mlx4(ctx, orc, k, group, sb):
         sl = slice(e * n, (e + 1) * n)
         want[r] = orc.mlx_matmul_f64(xv[r:r + 1], wq[sl], sc[sl], bi[sl], n, 4, group)[0]
     assert rel_err(y.cpu().numpy(), want) <= TOL
+
+
+# ----------------------------------------- K-quant experts (Q4_K_M MoE files)
+@pytest.mark.parametrize("scheme", [7, 8], ids=["q4_k", "q6_k"])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_grouped_k_quants(ctx, orc, scheme, xdt):
+    """GGUF Q4_K / Q6_K expert stacks through the grouped op (the formats of
+    Q4_K_M MoE checkpoints), on the LDS-record kernels."""
+    import torch
+
+    rows, k, n, E = 20, 1024, 320, 6
+    announce(f"grouped k-quant scheme={scheme} x={xdt}")
+    rng = np.random.default_rng(50 + scheme)
+    bank = orc.synth(scheme, rng, E * n, k)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    xt = _t(x) if xdt == "f32" else _t(x).to(torch.bfloat16)
+    xv = xt.float().cpu().numpy()
+    idx = ((np.arange(rows) * 5 + 1) % E).astype(np.float32)
+    y = ctx.grouped_matmul(xt, _t(bank), _t(idx), scheme, n, E)
+    torch.cuda.synchronize()
+    assert ("q4_k" if scheme == 7 else "q6_k") in ctx.last_kernel
+    assert rel_err(y.cpu().numpy(), orc.grouped_matmul_f64(scheme, xv, bank, idx, n, E)) <= TOL
+
+
+@pytest.mark.parametrize("scheme", [7, 8], ids=["q4_k", "q6_k"])
+def test_moe_ffn_k_quants(ctx, orc, scheme):
+    """Route, EXPAND_SWIGLU and COMBINE over K-quant banks (Qwen3-30B-A3B's
+    expert shapes, 32 experts) against the float64 chain."""
+    import torch
+    import rlxq
+
+    T, H, I, E, TOPK = 6, 2048, 768, 32, 8
+    announce(f"moe ffn k-quant scheme={scheme}")
+    rng = np.random.default_rng(60 + scheme)
+    gate_up = orc.synth(scheme, rng, E * 2 * I, H)
+    down = orc.synth(scheme, rng, E * H, I)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    xt = _t(x).to(torch.bfloat16)
+    xv = xt.float().cpu().numpy()
+    ids, probs = ctx.moe_route(_t(rng.standard_normal((T, E)).astype(np.float32)), TOPK, True)
+    act = ctx.moe_grouped(xt, _t(gate_up), ids, probs, scheme, rlxq.MOE_EXPAND_SWIGLU, 2 * I, E)
+    y = ctx.moe_grouped(act, _t(down), ids, probs, scheme, rlxq.MOE_COMBINE, H, E)
+    torch.cuda.synchronize()
+    flat = ids.cpu().numpy().ravel().astype(np.float32)
+    gu = orc.grouped_matmul_f64(scheme, np.repeat(xv, TOPK, axis=0), gate_up, flat, 2 * I, E)
+    g, u = gu[:, :I], gu[:, I:]
+    a64 = g / (1.0 + np.exp(-g)) * u
+    assert rel_err(act.cpu().numpy(), a64) <= TOL
+    dn = orc.grouped_matmul_f64(scheme, act.cpu().numpy(), down, flat, H, E)
+    pv = probs.cpu().numpy()
+    want = np.stack([sum(pv[r, j] * dn[r * TOPK + j] for j in range(TOPK)) for r in range(T)])
+    assert rel_err(y.cpu().numpy(), want) <= TOL

@@ -118,9 +118,12 @@ def test_q4k_host_checks(ctx):
         ctx.dequant_matmul(x, wf[4:4 + 4 * 288], rlxq.GGUF_Q4_K, 4)
     assert e.value.status == rlxq.E_ALIGN
     idx = torch.zeros((1,), device="cuda")
+    with pytest.raises(rlxq.RlxqError) as e:   # the grouped op checks the same way
+        ctx.grouped_matmul(x[:, :288].contiguous(), wf[:4 * 288], idx, rlxq.GGUF_Q4_K, 4, 1)
+    assert e.value.status == rlxq.E_SHAPE
     with pytest.raises(rlxq.RlxqError) as e:
-        ctx.grouped_matmul(x, wf[:4 * 288], idx, rlxq.GGUF_Q4_K, 4, 1)
-    assert e.value.status == rlxq.E_SCHEME
+        ctx.grouped_matmul(x, wf[4:4 + 4 * 288], idx, rlxq.GGUF_Q4_K, 4, 1)
+    assert e.value.status == rlxq.E_ALIGN
 
 
 @pytest.mark.parametrize("mkn", [(64, 4096, 520), (300, 1280, 272), (512, 4096, 1024), (129, 12288, 300)], ids=str)
