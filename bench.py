@@ -407,7 +407,7 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
     b = uniq * (N2 * H / 2 + 2 * N2 * (H // 64) * 2) + R * H * 2 + R * N2 * 4
     res["mlx4_grouped_gate_up"] = {"kernel": ctx.last_kernel, "us": round(us, 2), "unique_experts": uniq,
                                    "GBps": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-                                   "launches": "device routing table from the f32 indices, then the grouped GEMV"}
+                                   "launches": "one: the f32 indices routed inside the grouped GEMV's workgroups"}
     del banks
     torch.cuda.empty_cache()
     # the same with MXFP4 experts (codes + decoded bf16 scales, no bias slab)
