@@ -65,26 +65,35 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   std::memset(&ga, 0, sizeof ga);
   char name[80];
   int MT = 2;   // entries served per weight pass
-  // Register-activation kernels (4-bit codes: Q4_1, Q4_0, MLX affine 4-bit,
-  // MXFP4; bf16 activations; up to 256 units per row): lane groups of L lanes
-  // x NU units cover a row with the least padding, MT entries are served per
-  // weight pass.  The LDS-record kernels serve everything else (Q8_0, MLX
-  // 8-bit, the K-quants, f32 activations).
+  // Register-activation kernels (4-bit codes: Q4_1, Q4_0, Q4_K, MLX affine
+  // 4-bit, MXFP4; bf16 activations; up to 256 units per row): lane groups of L
+  // lanes x NU units cover a row with the least padding, MT entries are served
+  // per weight pass.  The LDS-record kernels serve everything else (Q8_0, MLX
+  // 8-bit, Q6_K, f32 activations).
   const bool q40 = scheme == RLXQ_GGUF_Q4_0;   // two blocks per unit
-  bool xr = xbf && (scheme == RLXQ_GGUF_Q4_1 || q40 || scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_MXFP4) &&
-            units <= (q40 ? 128 : 256) && !(is_mlx(scheme) && group % 32);
+  const bool q4k = scheme == RLXQ_GGUF_Q4_K;   // two blocks per unit (64 weights)
+  const bool wide = q40 || q4k;                // units of two blocks: at most two per lane
+  bool xr = xbf &&
+            (scheme == RLXQ_GGUF_Q4_1 || wide || scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_MXFP4) &&
+            units <= (wide ? 128 : 256) && !(is_mlx(scheme) && group % 32);
+  // lane groups: L lanes x NU units, the least padding over the instantiated shapes
+  static const int cand[][2] = {{64, 1}, {64, 2}, {64, 4}, {8, 1}, {8, 2}, {8, 3}, {8, 4}};
+  int L = 0, NU = 0;
+  for (const auto& c : cand)
+    if (!(wide && c[1] > 2) && c[0] * c[1] >= units && (L == 0 || c[0] * c[1] < L * NU)) L = c[0], NU = c[1];
+  // Q4_K with under 70% of the lanes holding a unit (K = 2048: 32 units on 64
+  // lanes) measured slower than the LDS-record kernel (gate|up 79 against
+  // 58 us at config 5); RLXQ_MOE_KERNEL=xr|lds forces one (tests)
+  if (q4k && units * 10 < 7 * (int64_t)L * NU) xr = false;
   if (const char* ev = std::getenv("RLXQ_MOE_KERNEL")) {
     if (!std::strcmp(ev, "lds")) xr = false;
+    if (!std::strcmp(ev, "xr") && q4k && xbf && units <= 128) xr = true;
   }
   // The balanced in-workgroup routing pays for the register kernels (every
   // workgroup one chunk of MT entries); the LDS-record kernels measure faster
   // with the device table.
   if (!xr && fused && !route_forced) fused = false;
   if (xr) {
-    static const int cand[][2] = {{64, 1}, {64, 2}, {64, 4}, {8, 1}, {8, 2}, {8, 3}, {8, 4}};
-    int L = 0, NU = 0;
-    for (const auto& c : cand)
-      if (!(q40 && c[1] > 2) && c[0] * c[1] >= units && (L == 0 || c[0] * c[1] < L * NU)) L = c[0], NU = c[1];
     // one entry per pass while experts hold few entries: the chunks of one
     // expert then run side by side and share its rows through the caches
     const double avg = (double)n_entries / (double)fired_est;
@@ -92,7 +101,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     if (const char* ev = std::getenv("RLXQ_MOE_MT")) MT = std::atoi(ev);
     if (MT != 1 && MT != 2 && MT != 4) MT = 2;
     if (NU >= 3 && MT > 2) MT = 2;          // register budget of the instantiated kernels
-    if (q40) MT = std::min(MT, 2 / NU);
+    if (wide) MT = std::min(MT, 2 / NU);
     // workgroups (4 waves) per expert: about 16 waves per CU over the fired
     // experts, and no more waves than column steps
     const int64_t rp = 64 / L;
@@ -104,7 +113,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     std::snprintf(name, sizeof name, "rlxq_moexr%s_%s_L%d_U%d_M%d%s", fused ? "f" : "", scheme_name(scheme), L, NU,
                   MT, swiglu ? "_sw" : "");
   } else {
-    const int L = units >= 48 ? 64 : 8;
+    L = units >= 48 ? 64 : 8;
     std::snprintf(name, sizeof name, "rlxq_moe_gemv%s_%s_%s_L%d_M%d%s", fused ? "f" : "", scheme_name(scheme),
                   xbf ? "bf16" : "f32", L, MT, swiglu ? "_sw" : "");
     // Rows per workgroup tile; RLXQ_MOE_TILE=64|128|192|256 forces it.

@@ -297,7 +297,7 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
   constexpr int R2 = SWIGLU ? 2 : 1;
   constexpr bool MLX = SCH == SCH_MLX4;
   constexpr bool MX = SCH == SCH_MXFP4;
-  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || MLX);
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || MLX);
   static_assert(!Unit<SCH>::BIT8, "register activations serve 4-bit codes");
 
   const int K = a.K;
@@ -330,7 +330,7 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
       const uint8_t* rp = wbase + n * a.rb;
 #pragma unroll
       for (int c = 0; c < NU; c++) {
-        load_unit<SCH>(bf.dw[r][c], rp + (int64_t)uc[c] * BYTES);
+        load_unit_at<SCH>(bf.dw[r][c], rp, uc[c]);
         if constexpr (MLX || MX) {
           const int64_t gi = ((int64_t)e * a.N + n) * gpr + (uc[c] * 32) / a.group;
           bf.sm[r][c] = load_scale_raw<SCH>(a.scales, gi, a.sb_bf16);
@@ -418,7 +418,7 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
               d = scale_decode<SCH>(rb.sm[r][c], a.sb_bf16);
               mn = 0.f;
             } else {
-              block_scales<SCH>(rb.dw[r][c], bl, d, mn);
+              block_scales<SCH>(rb.dw[r][c], bl, d, mn, uc[c]);
             }
             if (!uok[c]) {
               d = 0.f;
@@ -683,6 +683,13 @@ RLXQ_MOE_SCHEME(q6_k, SCH_Q6_K)
 RLXQ_MOEXR_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_MOEXR_SCHEME(mlx4, SCH_MLX4)
 RLXQ_MOEXR_SCHEME(mxfp4, SCH_MXFP4)
+// Q4_K: 64-weight units (two blocks, 12 dwords): at most two units per lane
+RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 64, 1, 1, 4)
+RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 64, 1, 2, 2)
+RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 64, 2, 1, 2)
+RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 8, 1, 1, 4)
+RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 8, 1, 2, 4)
+RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 8, 2, 1, 2)
 // Q4_0 units hold two blocks: at most four blocks of activations per lane
 // and entry (NU * MT <= 2).
 RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 64, 1, 1, 4)

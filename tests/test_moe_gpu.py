@@ -550,3 +550,39 @@ def test_moe_ffn_k_quants(ctx, orc, scheme):
     pv = probs.cpu().numpy()
     want = np.stack([sum(pv[r, j] * dn[r * TOPK + j] for j in range(TOPK)) for r in range(T)])
     assert rel_err(y.cpu().numpy(), want) <= TOL
+
+
+# (k, lane-group shape the register path picks for Q4_K's 64-weight units)
+XR_Q4K_SHAPES = [(256, "L8_U1"), (768, "L8_U2"), (1024, "L8_U2"), (2048, "L64_U1"), (4096, "L64_U1"),
+                 (8192, "L64_U2")]
+
+
+@pytest.mark.parametrize("mt", ["1", "2"])
+@pytest.mark.parametrize("route", ["table", "fused"])
+@pytest.mark.parametrize("k,shape", XR_Q4K_SHAPES, ids=[str(k) for k, _ in XR_Q4K_SHAPES])
+def test_grouped_register_path_q4_k(ctx, orc, monkeypatch, k, shape, route, mt):
+    """Register-activation kernels over Q4_K expert banks (bf16 activations):
+    every lane-group shape, both routings, 1/2 entries per weight pass, a
+    crowded expert and invalid indices (zero rows)."""
+    import torch
+
+    monkeypatch.setenv("RLXQ_MOE_ROUTE", route)
+    monkeypatch.setenv("RLXQ_MOE_MT", mt)
+    monkeypatch.setenv("RLXQ_MOE_KERNEL", "xr")   # also where the host would pick the LDS kernel
+    rows, n, E = 19, 72, 5
+    announce(f"grouped register path q4_k k={k} route={route} mt={mt}")
+    rng = np.random.default_rng(k + 7 * int(mt))
+    packed = orc.synth_q4_k(rng, E * n, k)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    idx = rng.integers(0, E, rows).astype(np.float32)
+    idx[::4] = 1
+    idx[2], idx[7] = -1, E
+    xt = _t(x).to(torch.bfloat16)
+    y = ctx.grouped_matmul(xt, _t(packed), _t(idx), 7, n, E)
+    torch.cuda.synchronize()
+    assert shape in ctx.last_kernel and "moexr" in ctx.last_kernel and "q4_k" in ctx.last_kernel
+    got = y.cpu().numpy()
+    assert np.all(got[2] == 0.0) and np.all(got[7] == 0.0)
+    ok = np.array([r not in (2, 7) for r in range(rows)])
+    want = orc.grouped_matmul_f64(7, xt.float().cpu().numpy()[ok], packed, idx[ok], n, E)
+    assert rel_err(got[ok], want) <= TOL
