@@ -382,10 +382,14 @@ RLXQ_DEV void load_unit_at(uint32_t* dw, const uint8_t* rp, int u) {
     const uint32_t off = (uint32_t)reinterpret_cast<uintptr_t>(sb) & 3u;   // 0 or 2
     const uint8_t* ql = sb + 64 * h + 32 * (j & 1) - off;
     const uint8_t* qh = sb + 128 + 32 * h - off;
-#pragma unroll
-    for (int i = 0; i < 9; i++) dw[i] = ld_u32(ql + 4 * i);
-#pragma unroll
-    for (int i = 0; i < 9; i++) dw[9 + i] = ld_u32(qh + 4 * i);
+    // 4-byte aligned: two 16-byte loads and a dword each
+    const uint4 l0 = ld_u128(ql), l1 = ld_u128(ql + 16), h0 = ld_u128(qh), h1 = ld_u128(qh + 16);
+    dw[0] = l0.x; dw[1] = l0.y; dw[2] = l0.z; dw[3] = l0.w;
+    dw[4] = l1.x; dw[5] = l1.y; dw[6] = l1.z; dw[7] = l1.w;
+    dw[8] = ld_u32(ql + 32);
+    dw[9] = h0.x; dw[10] = h0.y; dw[11] = h0.z; dw[12] = h0.w;
+    dw[13] = h1.x; dw[14] = h1.y; dw[15] = h1.z; dw[16] = h1.w;
+    dw[17] = ld_u32(qh + 32);
     dw[18] = *reinterpret_cast<const uint16_t*>(sb + 192 + 8 * h + 2 * j);
     dw[19] = *reinterpret_cast<const uint16_t*>(sb + 208);
     dw[20] = off | ((uint32_t)j << 8);
