@@ -69,7 +69,7 @@ struct Unit<SCH_Q4_K> {
 template <>
 struct Unit<SCH_Q6_K> {
   static constexpr int BLOCKS = 1, BYTES = 26, DW = 21;
-  static constexpr bool BIT8 = false;
+  static constexpr bool BIT8 = true;   // 6-bit codes take the byte path (f16 1024 + code)
 };
 
 // Offset that the code -> float trick adds to each code, and the value the
@@ -77,12 +77,13 @@ struct Unit<SCH_Q6_K> {
 // ends at sum(w_int * x) where w_int is the scheme's integer weight:
 //   Q4_1/MLX4: q (bias 128)    Q4_0: q - 8 (bias 136)
 //   Q8_0: q (bias 1024 + 128, codes stored as q ^ 0x80)   MLX8: code (1024)
+//   Q6_K: code - 32 (bias 1024 + 32)
 //   MXFP4: none (the pairs carry the signed E2M1 values themselves)
 template <int SCH>
 RLXQ_DEV constexpr float chain_bias() {
   return SCH == SCH_MXFP4 ? 0.f
          : (SCH == SCH_Q4_0 ? 136.f
-            : (SCH == SCH_Q8_0 ? 1152.f : (SCH == SCH_MLX8 ? 1024.f : (SCH == SCH_Q6_K ? 160.f : 128.f))));
+            : (SCH == SCH_Q8_0 ? 1152.f : (SCH == SCH_MLX8 ? 1024.f : (SCH == SCH_Q6_K ? 1056.f : 128.f))));
 }
 // Start of a block's dot chain: -bias * (sum of the block's x).
 template <int SCH>
@@ -473,15 +474,15 @@ RLXQ_DEV void block_pairs(const uint32_t* dw, int blk, uint32_t* pw, const Unpac
       pw[4 * i + 3] = fp4x2_to_bf16x2<3>(dw[i]);
     }
   } else if constexpr (SCH == SCH_Q6_K) {
-    // code = (ql nibble j >> 1) | (qh bits 2j..2j+1) << 4, as bf16 128 + code
+    // code = (ql nibble j >> 1) | (qh bits 2j..2j+1) << 4 for four elements
+    // at once (one byte each), then f16 (1024 + code) pairs
     const uint32_t off = dw[20] & 3u, j = dw[20] >> 8;
     const uint32_t ns = 4 * (j >> 1), hs = 2 * j;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const uint32_t ql = off ? align_bytes(dw[i + 1], dw[i], 2) : dw[i];
       const uint32_t qh = off ? align_bytes(dw[10 + i], dw[9 + i], 2) : dw[9 + i];
-      pw[2 * i] = ((ql >> ns) & k.mask) | (((qh >> hs) & 0x00030003u) << 4) | k.magic;
-      pw[2 * i + 1] = ((ql >> (ns + 8)) & k.mask) | (((qh >> (hs + 8)) & 0x00030003u) << 4) | k.magic;
+      byte_pairs(((ql >> ns) & 0x0F0F0F0Fu) | (((qh >> hs) & 0x03030303u) << 4), &pw[2 * i]);
     }
   } else if constexpr (SCH == SCH_Q4_K) {
     // sub-block blk: the low (0) or high (1) nibbles of the group's 32 bytes
@@ -499,19 +500,21 @@ RLXQ_DEV void block_pairs(const uint32_t* dw, int blk, uint32_t* pw, const Unpac
 
 // Q6_K: the block's two 16-weight halves carry their own scale, so the
 // chain runs per half from -bias times the half's sum (record word
-// NPL*16+3 holds the first half's sum) and each half takes its d * scale.
+// NPL*16+3 holds the first half's sum) and each half takes its d * scale;
+// the record's power-of-two block factor scales the result.
 template <int NPL>
 RLXQ_DEV float q6k_block_dot(const uint32_t* pw, const uint32_t* xr, float d_lo, float d_hi) {
   const float s = __uint_as_float(xr[NPL * 16 + 0]), s_lo = __uint_as_float(xr[NPL * 16 + 3]);
-  float lo = -160.f * s_lo, hi = -160.f * (s - s_lo);
+  const float scl = __uint_as_float(xr[NPL * 16 + 2]);
+  float lo = -chain_bias<SCH_Q6_K>() * s_lo, hi = -chain_bias<SCH_Q6_K>() * (s - s_lo);
 #pragma unroll
   for (int t = 0; t < 8; t++) {
-    lo = dot2_bf16(pw[t], xr[t], lo);
-    if constexpr (NPL == 2) lo = dot2_bf16(pw[t], xr[16 + t], lo);
-    hi = dot2_bf16(pw[8 + t], xr[8 + t], hi);
-    if constexpr (NPL == 2) hi = dot2_bf16(pw[8 + t], xr[24 + t], hi);
+    lo = dot2_f16(pw[t], xr[t], lo);
+    if constexpr (NPL == 2) lo = dot2_f16(pw[t], xr[16 + t], lo);
+    hi = dot2_f16(pw[8 + t], xr[8 + t], hi);
+    if constexpr (NPL == 2) hi = dot2_f16(pw[8 + t], xr[24 + t], hi);
   }
-  return fmaf(d_lo, lo, d_hi * hi);
+  return scl * fmaf(d_lo, lo, d_hi * hi);
 }
 
 // sum over the block of (bias + code) * x, started at -bias * S so that it
