@@ -77,13 +77,15 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
             (scheme == RLXQ_GGUF_Q4_1 || wide || scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_MXFP4) &&
             units <= (wide ? 128 : 256) && !(is_mlx(scheme) && group % 32);
   // lane groups: L lanes x NU units, the least padding over the instantiated shapes
-  static const int cand[][2] = {{64, 1}, {64, 2}, {64, 4}, {8, 1}, {8, 2}, {8, 3}, {8, 4}};
+  // (32-lane groups: Q4_K only)
+  static const int cand[][2] = {{64, 1}, {64, 2}, {64, 4}, {8, 1}, {8, 2}, {8, 3}, {8, 4}, {32, 1}};
   int L = 0, NU = 0;
   for (const auto& c : cand)
-    if (!(wide && c[1] > 2) && c[0] * c[1] >= units && (L == 0 || c[0] * c[1] < L * NU)) L = c[0], NU = c[1];
-  // Q4_K with under 70% of the lanes holding a unit (K = 2048: 32 units on 64
-  // lanes) measured slower than the LDS-record kernel (gate|up 79 against
-  // 58 us at config 5); RLXQ_MOE_KERNEL=xr|lds forces one (tests)
+    if (!(wide && c[1] > 2) && !(c[0] == 32 && !q4k) && c[0] * c[1] >= units && (L == 0 || c[0] * c[1] < L * NU))
+      L = c[0], NU = c[1];
+  // Q4_K with under 70% of the lanes holding a unit (K = 2048 on 64-lane
+  // groups: 32 units) measured slower than the LDS-record kernel (gate|up 79
+  // against 58 us at config 5); RLXQ_MOE_KERNEL=xr|lds forces one (tests)
   if (q4k && units * 10 < 7 * (int64_t)L * NU) xr = false;
   if (const char* ev = std::getenv("RLXQ_MOE_KERNEL")) {
     if (!std::strcmp(ev, "lds")) xr = false;

@@ -683,7 +683,10 @@ RLXQ_MOE_SCHEME(q6_k, SCH_Q6_K)
 RLXQ_MOEXR_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_MOEXR_SCHEME(mlx4, SCH_MLX4)
 RLXQ_MOEXR_SCHEME(mxfp4, SCH_MXFP4)
-// Q4_K: 64-weight units (two blocks, 12 dwords): at most two units per lane
+// Q4_K: 64-weight units (two blocks, 12 dwords): at most two units per lane;
+// 32-lane groups for the 32 units of K = 2048
+RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 32, 1, 1, 4)
+RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 32, 1, 2, 2)
 RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 64, 1, 1, 4)
 RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 64, 1, 2, 2)
 RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 64, 2, 1, 2)

@@ -553,7 +553,7 @@ def test_moe_ffn_k_quants(ctx, orc, scheme):
 
 
 # (k, lane-group shape the register path picks for Q4_K's 64-weight units)
-XR_Q4K_SHAPES = [(256, "L8_U1"), (768, "L8_U2"), (1024, "L8_U2"), (2048, "L64_U1"), (4096, "L64_U1"),
+XR_Q4K_SHAPES = [(256, "L8_U1"), (768, "L8_U2"), (1024, "L8_U2"), (2048, "L32_U1"), (4096, "L64_U1"),
                  (8192, "L64_U2")]
 
 
