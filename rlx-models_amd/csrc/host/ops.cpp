@@ -353,6 +353,32 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     return launch(ctx, fn, dim3((unsigned)gx, 1, 1), dim3(64 * xr_w, 1, 1), lds, stream, args, name);
   }
 
+  // Two to four activation rows (bf16, Q4_1): the same register kernel with
+  // the rows' activations side by side in registers (MT = 2 or 4 rows, at
+  // most 8 units of activations per lane), so every weight row is fetched
+  // once for all of them.  RLXQ_GEMV_XR=0 turns it off as well.
+  {
+    const char* e = std::getenv("RLXQ_GEMV_XR");
+    const int mt = m <= 2 ? 2 : 4;
+    if (m >= 2 && m <= 4 && xbf && scheme == RLXQ_GGUF_Q4_1 && n < (int64_t(1) << 31) && !(e && e[0] == '0') &&
+        nchunk64 <= (mt == 2 ? 4 : 2)) {
+      // (two steps in flight up to two chunks; 4-wave groups for two rows at
+      // K = 4096: gate_up 15.5 us at M = 2, 23.4 at M = 4 on 8 waves)
+      const int nu = (int)nchunk64;
+      int d = nu <= 2 ? 2 : 1, wv = (nu == 2 && mt == 2) ? 4 : 8;
+      if (const char* t = std::getenv("RLXQ_GEMV_XSM")) std::sscanf(t, "%d,%d", &d, &wv);   // "D,W" (tuning)
+      std::snprintf(name, sizeof name, "rlxq_gemvxs_%s_U%d_D%d_W%d_M%d", scheme_name(scheme), nu, d, wv, mt);
+      if ((rc = get_fn(ctx, name, &fn))) return rc;
+      const size_t lds = (size_t)mt * (k / 32) * 68;
+      if (lds <= ctx->max_lds) {
+        const int per_cu = blocks_per_cu(ctx, name, fn, 64 * wv, lds);
+        int64_t gx = (int64_t)ctx->cu_count * per_cu;
+        gx = std::min<int64_t>(gx, (n + wv - 1) / wv);
+        return launch(ctx, fn, dim3((unsigned)gx, 1, 1), dim3(64 * wv, 1, 1), lds, stream, args, name);
+      }
+    }
+  }
+
   const int64_t rec_bytes = (xbf ? 20 : 36) * 4;
   const int64_t bpr = k / 32;
   const GemvCfg cfg = pick_gemv(m, units, 4 * bpr * rec_bytes, ctx->max_lds, scheme);

@@ -228,7 +228,7 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
 // of D rows of weight loads in flight.
 // ---------------------------------------------------------------------------
 
-template <int SCH, int NU, int D, int WAVES, bool XLDS>
+template <int SCH, int NU, int D, int WAVES, bool XLDS, int MT = 1>
 RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   constexpr int BLOCKS = Unit<SCH>::BLOCKS;
   constexpr int DW = Unit<SCH>::DW;
@@ -289,90 +289,107 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   // added through a lane swap.  LDS: [bpr][16] pair dwords, then [bpr] sums.
   // Either way the first D rows of weights are requested right after the
   // activation loads.
-  uint32_t X[NU][BLOCKS][16];
-  float S[NU][BLOCKS];
-  const uint16_t* xg = reinterpret_cast<const uint16_t*>(a.x);
+  // MT activation rows (M <= MT; rows past M read row 0 and are not stored)
+  uint32_t X[MT][NU][BLOCKS][16];
+  float S[MT][NU][BLOCKS];
   Buf ring[D];
   if constexpr (XLDS) {
-    extern __shared__ __align__(16) uint32_t xs[];
-    float* xsum = reinterpret_cast<float*>(xs + bpr * 16);
+    extern __shared__ __align__(16) uint32_t xlds[];
     constexpr int NT = 64 * WAVES;
-    constexpr int XH = (2 * 64 * NU * BLOCKS + NT - 1) / NT;   // half-blocks per thread
+    constexpr int XH = (2 * 64 * NU * BLOCKS + NT - 1) / NT;   // half-blocks per thread and row
     constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;
     constexpr bool LINEAR = MLX || MX || SCH == SCH_Q4_K;   // half h = elements 16h..16h+15
-    uint4 xa[XH], xc[XH];
+    uint4 xa[MT][XH], xc[MT][XH];
 #pragma unroll
-    for (int i = 0; i < XH; i++) {
-      const int hb = threadIdx.x + NT * i, b = hb >> 1, h = hb & 1;
-      xa[i] = xc[i] = make_uint4(0u, 0u, 0u, 0u);
-      if (hb < 2 * bpr) {
-        const uint16_t* p = xg + (int64_t)b * 32;
-        xa[i] = *reinterpret_cast<const uint4*>(p + (LINEAR ? 16 * h : 8 * h));
-        xc[i] = *reinterpret_cast<const uint4*>(p + (LINEAR ? 16 * h + 8 : 16 + 8 * h));
+    for (int m = 0; m < MT; m++) {
+      const uint16_t* xg = reinterpret_cast<const uint16_t*>(a.x) + (int64_t)(m < a.M ? m : 0) * K;
+#pragma unroll
+      for (int i = 0; i < XH; i++) {
+        const int hb = threadIdx.x + NT * i, b = hb >> 1, h = hb & 1;
+        xa[m][i] = xc[m][i] = make_uint4(0u, 0u, 0u, 0u);
+        if (hb < 2 * bpr) {
+          const uint16_t* p = xg + (int64_t)b * 32;
+          xa[m][i] = *reinterpret_cast<const uint4*>(p + (LINEAR ? 16 * h : 8 * h));
+          xc[m][i] = *reinterpret_cast<const uint4*>(p + (LINEAR ? 16 * h + 8 : 16 + 8 * h));
+        }
       }
     }
 #pragma unroll
     for (int i = 0; i < D; i++) load(n0 + (i < cnt ? i : cnt - 1) * G, ring[i]);
 #pragma unroll
-    for (int i = 0; i < XH; i++) {
-      const int hb = threadIdx.x + NT * i, b = hb >> 1, h = hb & 1;
-      const uint32_t A[4] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w}, C[4] = {xc[i].x, xc[i].y, xc[i].z, xc[i].w};
-      uint32_t P[8];
+    for (int m = 0; m < MT; m++) {
+      uint32_t* xs = xlds + (size_t)m * bpr * 17;
+      float* xsum = reinterpret_cast<float*>(xs + bpr * 16);
 #pragma unroll
-      for (int t = 0; t < 2; t++) {
-        if constexpr (MX) {
-          const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7: pairs (2j, 2j+1) as loaded
-          P[4 * t + 0] = R[0];
-          P[4 * t + 1] = R[1];
-          P[4 * t + 2] = R[2];
-          P[4 * t + 3] = R[3];
-        } else if constexpr (SCH == SCH_Q4_K) {
-          const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7: pairs (4j+e, 4j+e+2)
-          P[4 * t + 0] = perm_b32(R[1], R[0], LO);
-          P[4 * t + 1] = perm_b32(R[1], R[0], HI);
-          P[4 * t + 2] = perm_b32(R[3], R[2], LO);
-          P[4 * t + 3] = perm_b32(R[3], R[2], HI);
-        } else if constexpr (MLX) {
-          const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7
-          P[4 * t + 0] = perm_b32(R[2], R[0], LO);
-          P[4 * t + 1] = perm_b32(R[2], R[0], HI);
-          P[4 * t + 2] = perm_b32(R[3], R[1], LO);
-          P[4 * t + 3] = perm_b32(R[3], R[1], HI);
-        } else {
-          P[4 * t + 0] = perm_b32(A[2 * t + 1], A[2 * t], LO);
-          P[4 * t + 2] = perm_b32(A[2 * t + 1], A[2 * t], HI);
-          P[4 * t + 1] = perm_b32(C[2 * t + 1], C[2 * t], LO);
-          P[4 * t + 3] = perm_b32(C[2 * t + 1], C[2 * t], HI);
+      for (int i = 0; i < XH; i++) {
+        const int hb = threadIdx.x + NT * i, b = hb >> 1, h = hb & 1;
+        const uint32_t A[4] = {xa[m][i].x, xa[m][i].y, xa[m][i].z, xa[m][i].w};
+        const uint32_t C[4] = {xc[m][i].x, xc[m][i].y, xc[m][i].z, xc[m][i].w};
+        uint32_t P[8];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          if constexpr (MX) {
+            const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7: pairs (2j, 2j+1) as loaded
+            P[4 * t + 0] = R[0];
+            P[4 * t + 1] = R[1];
+            P[4 * t + 2] = R[2];
+            P[4 * t + 3] = R[3];
+          } else if constexpr (SCH == SCH_Q4_K) {
+            const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7: pairs (4j+e, 4j+e+2)
+            P[4 * t + 0] = perm_b32(R[1], R[0], LO);
+            P[4 * t + 1] = perm_b32(R[1], R[0], HI);
+            P[4 * t + 2] = perm_b32(R[3], R[2], LO);
+            P[4 * t + 3] = perm_b32(R[3], R[2], HI);
+          } else if constexpr (MLX) {
+            const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7
+            P[4 * t + 0] = perm_b32(R[2], R[0], LO);
+            P[4 * t + 1] = perm_b32(R[2], R[0], HI);
+            P[4 * t + 2] = perm_b32(R[3], R[1], LO);
+            P[4 * t + 3] = perm_b32(R[3], R[1], HI);
+          } else {
+            P[4 * t + 0] = perm_b32(A[2 * t + 1], A[2 * t], LO);
+            P[4 * t + 2] = perm_b32(A[2 * t + 1], A[2 * t], HI);
+            P[4 * t + 1] = perm_b32(C[2 * t + 1], C[2 * t], LO);
+            P[4 * t + 3] = perm_b32(C[2 * t + 1], C[2 * t], HI);
+          }
         }
-      }
-      float sh = 0.f;
+        float sh = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; q++) sh = dot2_bf16(A[q], 0x3F803F80u, sh);
+        for (int q = 0; q < 4; q++) sh = dot2_bf16(A[q], 0x3F803F80u, sh);
 #pragma unroll
-      for (int q = 0; q < 4; q++) sh = dot2_bf16(C[q], 0x3F803F80u, sh);
-      const float so = __shfl_xor(sh, 1, 64);
-      if (hb < 2 * bpr) {
-        uint4* dst = reinterpret_cast<uint4*>(xs + b * 16 + 8 * h);
-        dst[0] = make_uint4(P[0], P[1], P[2], P[3]);
-        dst[1] = make_uint4(P[4], P[5], P[6], P[7]);
-        if (h == 0) xsum[b] = sh + so;
+        for (int q = 0; q < 4; q++) sh = dot2_bf16(C[q], 0x3F803F80u, sh);
+        const float so = __shfl_xor(sh, 1, 64);
+        if (hb < 2 * bpr) {
+          uint4* dst = reinterpret_cast<uint4*>(xs + b * 16 + 8 * h);
+          dst[0] = make_uint4(P[0], P[1], P[2], P[3]);
+          dst[1] = make_uint4(P[4], P[5], P[6], P[7]);
+          if (h == 0) xsum[b] = sh + so;
+        }
       }
     }
     __syncthreads();
 #pragma unroll
-    for (int c = 0; c < NU; c++)
+    for (int m = 0; m < MT; m++) {
+      const uint32_t* xs = xlds + (size_t)m * bpr * 17;
+      const float* xsum = reinterpret_cast<const float*>(xs + bpr * 16);
 #pragma unroll
-      for (int bl = 0; bl < BLOCKS; bl++) {
-        const int blk = uc[c] * BLOCKS + bl;
-        const uint4* p = reinterpret_cast<const uint4*>(xs + blk * 16);
+      for (int c = 0; c < NU; c++)
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const uint4 v = p[q];
-          X[c][bl][4 * q] = v.x; X[c][bl][4 * q + 1] = v.y; X[c][bl][4 * q + 2] = v.z; X[c][bl][4 * q + 3] = v.w;
+        for (int bl = 0; bl < BLOCKS; bl++) {
+          const int blk = uc[c] * BLOCKS + bl;
+          const uint4* p = reinterpret_cast<const uint4*>(xs + blk * 16);
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const uint4 v = p[q];
+            X[m][c][bl][4 * q] = v.x; X[m][c][bl][4 * q + 1] = v.y;
+            X[m][c][bl][4 * q + 2] = v.z; X[m][c][bl][4 * q + 3] = v.w;
+          }
+          S[m][c][bl] = xsum[blk];
         }
-        S[c][bl] = xsum[blk];
-      }
+    }
   } else {
+    static_assert(MT == 1 || XLDS, "several activation rows go through LDS");
+    const uint16_t* xg = reinterpret_cast<const uint16_t*>(a.x);
 #pragma unroll
     for (int c = 0; c < NU; c++)
 #pragma unroll
@@ -381,7 +398,8 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
           const uint4 v = p[q];
-          X[c][bl][4 * q] = v.x; X[c][bl][4 * q + 1] = v.y; X[c][bl][4 * q + 2] = v.z; X[c][bl][4 * q + 3] = v.w;
+          X[0][c][bl][4 * q] = v.x; X[0][c][bl][4 * q + 1] = v.y;
+          X[0][c][bl][4 * q + 2] = v.z; X[0][c][bl][4 * q + 3] = v.w;
         }
       }
 #pragma unroll
@@ -392,12 +410,12 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
       for (int bl = 0; bl < BLOCKS; bl++) {
         float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) s = dot2_bf16(X[c][bl][i], 0x3F803F80u, s);
-        S[c][bl] = s;
+        for (int i = 0; i < 16; i++) s = dot2_bf16(X[0][c][bl][i], 0x3F803F80u, s);
+        S[0][c][bl] = s;
         uint32_t R[16];
 #pragma unroll
-        for (int i = 0; i < 16; i++) R[i] = X[c][bl][i];
-        pairs_from_raw<SCH>(R, X[c][bl]);
+        for (int i = 0; i < 16; i++) R[i] = X[0][c][bl][i];
+        pairs_from_raw<SCH>(R, X[0][c][bl]);
       }
   }
 
@@ -416,7 +434,9 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   // computed without refills.
   auto row = [&](int64_t st, const Buf& bf) {
     const int64_t n = n0 + st * G;
-    float acc = 0.f;
+    float acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; m++) acc[m] = 0.f;
 #pragma unroll
     for (int c = 0; c < NU; c++)
 #pragma unroll
@@ -437,17 +457,23 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
         }
         uint32_t pw[16];
         block_pairs<SCH>(bf.dw[c], bl, pw, kc);
-        float ch = chain_start<SCH>(S[c][bl]);
 #pragma unroll
-        for (int t = 0; t < 16; t++) ch = dot2_bf16(pw[t], X[c][bl][t], ch);
-        acc = fmaf(d, ch, acc);
-        if constexpr (HAS_MIN) acc = fmaf(mn, S[c][bl], acc);
+        for (int m = 0; m < MT; m++) {
+          float ch = chain_start<SCH>(S[m][c][bl]);
+#pragma unroll
+          for (int t = 0; t < 16; t++) ch = dot2_bf16(pw[t], X[m][c][bl][t], ch);
+          acc[m] = fmaf(d, ch, acc[m]);
+          if constexpr (HAS_MIN) acc[m] = fmaf(mn, S[m][c][bl], acc[m]);
+        }
       }
-    const float v = lane_group_sum<64>(acc);
-    if (lane == 0 && yrow >= 0) {
-      const int64_t off = yrow * a.y_ld + n;
-      if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v * ysc);
-      else reinterpret_cast<float*>(a.y)[off] = v * ysc;
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+      const float v = lane_group_sum<64>(acc[m]);
+      if (lane == 0 && yrow >= 0 && m < a.M) {
+        const int64_t off = (yrow + m) * a.y_ld + n;
+        if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v * ysc);
+        else reinterpret_cast<float*>(a.y)[off] = v * ysc;
+      }
     }
   };
   int64_t s0 = 0;
@@ -548,6 +574,26 @@ RLXQ_GEMVXR_WIDE(mlx4, SCH_MLX4)
   RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U2_D1_W8, SCH_Q4_K, 2, 1, 8)          \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U3_D1_W8, SCH_Q4_K, 3, 1, 8)
 RLXQ_GEMVXS_Q4K
+// several activation rows (M = 2..4): rlxq_gemvxs_<scheme>_U<NU>_D<D>_W<W>_M<MT>,
+// NU * MT <= 8 units of activations per lane
+#define RLXQ_GEMVXSM_INST(NAME, SCH, NU, D, W, MT)                                    \
+  extern "C" __global__ __launch_bounds__(64 * W) void NAME(rlxq_gemv_args a) {      \
+    rlxq::gemv_xr_body<SCH, NU, D, W, true, MT>(a);                                   \
+  }
+#define RLXQ_GEMVXSM_SCHEME(SNAME, SCH)                                       \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U1_D2_W8_M2, SCH, 1, 2, 8, 2)      \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D1_W4_M2, SCH, 2, 1, 4, 2)      \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D2_W4_M2, SCH, 2, 2, 4, 2)      \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U3_D1_W8_M2, SCH, 3, 1, 8, 2)      \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U4_D1_W8_M2, SCH, 4, 1, 8, 2)      \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U1_D2_W8_M4, SCH, 1, 2, 8, 4)      \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D1_W4_M4, SCH, 2, 1, 4, 4)      \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D2_W4_M4, SCH, 2, 2, 4, 4)      \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D1_W8_M2, SCH, 2, 1, 8, 2)      \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8_M2, SCH, 2, 2, 8, 2)      \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D1_W8_M4, SCH, 2, 1, 8, 4)      \
+  RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8_M4, SCH, 2, 2, 8, 4)
+RLXQ_GEMVXSM_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXS_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXS_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_GEMVXS_SCHEME(mlx4, SCH_MLX4)

@@ -373,3 +373,34 @@ def test_bound_call_matches_plain_call(ctx, orc):
         call()
     torch.cuda.synchronize()
     assert torch.equal(y, want)
+
+
+@pytest.mark.parametrize("m", [2, 3, 4])
+@pytest.mark.parametrize("k,n", [(2048, 1000), (4096, 4096), (4096, 777), (8192, 640), (1536, 320)], ids=str)
+def test_multi_row_register_path(ctx, orc, monkeypatch, m, k, n):
+    """Q4_1, bf16 activations, M = 2..4: the register-activation kernel with
+    the rows side by side (MT = 2 or 4) where it applies, against the oracle
+    and against the LDS-record kernel (RLXQ_GEMV_XR=0)."""
+    import torch
+
+    announce(f"multi-row register gemv m={m} k={k} n={n}")
+    rng = np.random.default_rng(m * 7 + k + n)
+    packed = orc.synth_q4_1(rng, n, k)
+    x32 = rng.standard_normal((m, k)).astype(np.float32)
+    xt, xv = _x_as(x32, "bf16")
+    y = ctx.dequant_matmul(xt, _t(packed), 3, n)
+    torch.cuda.synchronize()
+    mt = 2 if m <= 2 else 4
+    chunks = (k // 32 + 63) // 64
+    if chunks <= (4 if mt == 2 else 2):
+        assert ctx.last_kernel.endswith(f"_M{mt}"), ctx.last_kernel
+    got = y.cpu().numpy()
+    assert rel_err(got, want_f64(orc, 3, xv, packed, k)) <= 1e-3
+    yb = ctx.dequant_matmul(xt, _t(packed), 3, n, y_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert rel_err(yb.float().cpu().numpy(), want_f64(orc, 3, xv, packed, k)) <= 1e-2
+    monkeypatch.setenv("RLXQ_GEMV_XR", "0")
+    y2 = ctx.dequant_matmul(xt, _t(packed), 3, n)
+    torch.cuda.synchronize()
+    assert "gemvxs" not in ctx.last_kernel
+    assert rel_err(got, y2.cpu().numpy().astype(np.float64)) <= 1e-3
