@@ -21,7 +21,8 @@
  *     dtype, alignment and null-pointer problems are rejected on the host
  *     before any kernel is launched; rlxq_last_error() names the argument.
  *   - A context is used by one host thread at a time (the reference's
- *     CompiledGraph is &mut self); calls on different streams may overlap.
+ *     CompiledGraph is &mut self); calls on different streams may overlap
+ *     (the library's scratch is kept per stream).
  */
 #ifndef RLXQ_H
 #define RLXQ_H

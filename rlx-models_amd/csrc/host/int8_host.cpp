@@ -95,7 +95,7 @@ int i8b_dispatch(rlxq_ctx* ctx, int group, const void* x, int x_dtype, const voi
   const size_t xsum_bytes = zp ? round256((size_t)m * 4) : 0;
   void* ws = nullptr;
   int rc;
-  if (part_bytes + xsum_bytes && (rc = workspace(ctx, part_bytes + xsum_bytes, &ws))) return rc;
+  if (part_bytes + xsum_bytes && (rc = workspace(ctx, part_bytes + xsum_bytes, &ws, stream))) return rc;
 
   rlxq_i8b_args a;
   std::memset(&a, 0, sizeof a);
@@ -178,7 +178,7 @@ int rlxq_w8a8_gemm(rlxq_ctx* ctx, const void* x, int x_dtype, const int8_t* wq, 
   const size_t q_bytes = round256((size_t)(m * k));
   void* ws = nullptr;
   int rc;
-  if ((rc = workspace(ctx, q_bytes + round256((size_t)m * 4), &ws))) return rc;
+  if ((rc = workspace(ctx, q_bytes + round256((size_t)m * 4), &ws, stream))) return rc;
   int8_t* qx = static_cast<int8_t*>(ws);
   float* sx = reinterpret_cast<float*>(static_cast<char*>(ws) + q_bytes);
   if ((rc = rlxq_quantize_act_int8(ctx, x, x_dtype, m, k, qx, sx, stream))) return rc;

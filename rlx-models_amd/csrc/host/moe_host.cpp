@@ -130,7 +130,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   const size_t table_bytes = fused ? 0 : ((size_t)(2 + 2 * num_experts + n_entries) * 4 + 255) & ~size_t(255);
   const size_t tmp_bytes = combine ? (size_t)n_entries * width * 4 : 0;
   void* ws = nullptr;
-  if (table_bytes + tmp_bytes && (rc = workspace(ctx, table_bytes + tmp_bytes, &ws))) return rc;
+  if (table_bytes + tmp_bytes && (rc = workspace(ctx, table_bytes + tmp_bytes, &ws, stream))) return rc;
   int32_t* table = fused ? nullptr : static_cast<int32_t*>(ws);
   float* tmp = combine ? reinterpret_cast<float*>(static_cast<char*>(ws) + table_bytes) : nullptr;
 

@@ -197,7 +197,7 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
     a.inv_s = xa.inv_s;
   } else if (part_bytes) {
     void* ws = nullptr;
-    if ((rc = workspace(ctx, part_bytes, &ws))) return rc;
+    if ((rc = workspace(ctx, part_bytes, &ws, stream))) return rc;
     part = static_cast<char*>(ws);
   }
   a.w = static_cast<const uint8_t*>(w);

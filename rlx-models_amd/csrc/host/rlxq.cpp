@@ -127,28 +127,30 @@ int launch(rlxq_ctx* ctx, hipFunction_t fn, dim3 grid, dim3 block, size_t lds, v
   return RLXQ_OK;
 }
 
-int workspace(rlxq_ctx* ctx, size_t bytes, void** out) {
-  if (bytes <= ctx->ws_bytes) {
-    *out = ctx->ws;
+int workspace(rlxq_ctx* ctx, size_t bytes, void** out, void* stream) {
+  rlxq_ctx::Scratch& w = ctx->ws[stream];
+  if (bytes <= w.bytes) {
+    *out = w.p;
     return RLXQ_OK;
   }
-  // Growing frees the old buffer, which other streams may still use: wait.
-  if (ctx->ws) {
+  // Growing frees the old buffer, which earlier work may still use: wait for
+  // the device (the null stream's work included).
+  if (w.p) {
     hipError_t e = hipDeviceSynchronize();
     if (e != hipSuccess) return fail(ctx, RLXQ_E_HIP, "workspace: sync: " + hip_msg(e));
-    (void)hipFree(ctx->ws);
-    ctx->ws = nullptr;
-    ctx->ws_bytes = 0;
+    (void)hipFree(w.p);
+    w.p = nullptr;
+    w.bytes = 0;
   }
   size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
   want = (want + 4095) & ~size_t(4095);
-  hipError_t e = hipMalloc(&ctx->ws, want);
+  hipError_t e = hipMalloc(&w.p, want);
   if (e != hipSuccess) {
-    ctx->ws = nullptr;
+    w.p = nullptr;
     return fail(ctx, RLXQ_E_NOMEM, "workspace: hipMalloc(" + std::to_string(want) + "): " + hip_msg(e));
   }
-  ctx->ws_bytes = want;
-  *out = ctx->ws;
+  w.bytes = want;
+  *out = w.p;
   return RLXQ_OK;
 }
 
@@ -243,10 +245,9 @@ int rlxq_destroy(rlxq_ctx* ctx) {
   if (!ctx) return RLXQ_E_NULL;
   {
     DeviceGuard g(ctx->device);
-    if (ctx->ws) {
-      (void)hipDeviceSynchronize();
-      (void)hipFree(ctx->ws);
-    }
+    if (!ctx->ws.empty()) (void)hipDeviceSynchronize();
+    for (auto& kv : ctx->ws)
+      if (kv.second.p) (void)hipFree(kv.second.p);
     for (hipModule_t m : ctx->modules) (void)hipModuleUnload(m);
   }
   delete ctx;

@@ -20,9 +20,13 @@ struct rlxq_ctx {
   int cu_count = 0;
   size_t max_lds = 65536;
   // Library-owned scratch (routing tables, quantised activations, split-K
-  // partials).  Grown on demand; freed by rlxq_destroy.
-  void* ws = nullptr;
-  size_t ws_bytes = 0;
+  // partials), one buffer per stream so that calls on different streams can
+  // overlap.  Grown on demand; freed by rlxq_destroy.
+  struct Scratch {
+    void* p = nullptr;
+    size_t bytes = 0;
+  };
+  std::unordered_map<void*, Scratch> ws;
 };
 
 #include "skinny_args.h"
@@ -55,8 +59,9 @@ int blocks_per_cu(rlxq_ctx* ctx, const std::string& name, hipFunction_t fn, int 
 int launch(rlxq_ctx* ctx, hipFunction_t fn, dim3 grid, dim3 block, size_t lds, void* stream,
            void** args, const char* what);
 
-// Ensures at least `bytes` of context scratch; returns its device pointer.
-int workspace(rlxq_ctx* ctx, size_t bytes, void** out);
+// Ensures at least `bytes` of context scratch for `stream`; returns its
+// device pointer.
+int workspace(rlxq_ctx* ctx, size_t bytes, void** out, void* stream);
 
 bool is_gguf(int scheme);
 bool is_mlx(int scheme);

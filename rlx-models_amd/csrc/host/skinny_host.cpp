@@ -34,7 +34,7 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bo
   const size_t x16_bytes = round256((size_t)(m * k) * 2), s_bytes = round256((size_t)m * 4);
   void* ws = nullptr;
   int rc;
-  if ((rc = workspace(ctx, x16_bytes + s_bytes + extra, &ws))) return rc;
+  if ((rc = workspace(ctx, x16_bytes + s_bytes + extra, &ws, stream))) return rc;
   char* wsb = static_cast<char*>(ws);
   std::memset(&xa, 0, sizeof xa);
   xa.x = x;
@@ -158,7 +158,7 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   const size_t part_bytes = splits > 1 ? round256((size_t)(splits * m * n) * 4) : 0;
   void* ws = nullptr;
   int rc;
-  if ((rc = workspace(ctx, x16_bytes + s_bytes + part_bytes, &ws))) return rc;
+  if ((rc = workspace(ctx, x16_bytes + s_bytes + part_bytes, &ws, stream))) return rc;
   char* wsb = static_cast<char*>(ws);
 
   rlxq_x16_args xa;

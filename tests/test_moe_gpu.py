@@ -586,3 +586,30 @@ def test_grouped_register_path_q4_k(ctx, orc, monkeypatch, k, shape, route, mt):
     ok = np.array([r not in (2, 7) for r in range(rows)])
     want = orc.grouped_matmul_f64(7, xt.float().cpu().numpy()[ok], packed, idx[ok], n, E)
     assert rel_err(got[ok], want) <= TOL
+
+
+def test_two_streams_use_their_own_workspace(ctx, orc):
+    """Calls that use the library's scratch (the routing table and per-entry
+    rows here) on two streams at once: each stream has its own workspace, so
+    both results stay right."""
+    import torch
+
+    announce("two streams, grouped op with device tables")
+    rng = np.random.default_rng(77)
+    rows, k, n, E = 300, 1024, 512, 16
+    bank = orc.synth_q4_1(rng, E * n, k)
+    xs = [rng.standard_normal((rows, k)).astype(np.float32) for _ in range(2)]
+    idxs = [rng.integers(0, E, rows).astype(np.float32) for _ in range(2)]
+    bt = _t(bank)
+    xt = [_t(x) for x in xs]
+    it = [_t(i) for i in idxs]
+    ys = [torch.empty((rows, n), device="cuda") for _ in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for _ in range(4):
+        for j in range(2):
+            with torch.cuda.stream(streams[j]):
+                ctx.grouped_matmul(xt[j], bt, it[j], 3, n, E, y=ys[j], stream=streams[j].cuda_stream)
+    torch.cuda.synchronize()
+    for j in range(2):
+        assert rel_err(ys[j].cpu().numpy(), orc.grouped_matmul_f64(3, xs[j], bank, idxs[j], n, E)) <= TOL
