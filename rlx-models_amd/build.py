@@ -80,6 +80,20 @@ def build_host() -> Path:
     return out
 
 
+def build_examples() -> list[Path]:
+    """The plain-C callers of the ABI in examples/, linked against librlxq.so."""
+    outs = []
+    (LIB / "examples").mkdir(parents=True, exist_ok=True)
+    for src in sorted((PKG / "examples").glob("*.c")):
+        out = LIB / "examples" / src.stem
+        cmd = ["gcc", "-std=c99", "-O2", "-Wall", "-D__HIP_PLATFORM_AMD__", "-I", str(ROOT / "include"),
+               "-I", str(ROCM / "include"), str(src), "-o", str(out), "-L", str(LIB), "-lrlxq",
+               f"-Wl,-rpath,{LIB}", "-L", str(ROCM / "lib"), "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}", "-lm"]
+        _run(cmd, f"gcc {src.name}")
+        outs.append(out)
+    return outs
+
+
 def build_oracle() -> Path:
     odir = ROOT / "oracle"
     out = odir / "liboracle.so"
@@ -104,6 +118,7 @@ def main(argv: list[str] | None = None) -> int:
     if not a.host_only:
         build_code_objects()
     build_host()
+    build_examples()
     if not a.no_oracle:
         build_oracle()
     return 0

@@ -54,3 +54,18 @@ def test_init_without_gfx950_fails_cleanly():
     h = C.c_void_p()
     rc = rlxq.lib().rlxq_init(0, C.byref(h))
     assert rc in (rlxq.E_DEVICE, rlxq.E_HIP) and not h.value
+
+
+EXAMPLE = rlxq.PKG / "lib" / "examples" / "decode_gemv"
+
+
+def test_plain_c_caller_links_and_runs():
+    """examples/decode_gemv.c: the ABI from plain C (no Python, no torch).
+    Without a gfx950 device it must stop cleanly with status 77."""
+    import torch
+
+    assert EXAMPLE.exists(), "build the package first (python rlx-models_amd/build.py)"
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present: tests/test_gemv_gpu.py runs it for real")
+    r = subprocess.run([str(EXAMPLE)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 77, r.stdout + r.stderr

@@ -404,3 +404,18 @@ def test_multi_row_register_path(ctx, orc, monkeypatch, m, k, n):
     torch.cuda.synchronize()
     assert "gemvxs" not in ctx.last_kernel
     assert rel_err(got, y2.cpu().numpy().astype(np.float64)) <= 1e-3
+
+
+def test_plain_c_caller_on_the_gpu():
+    """examples/decode_gemv.c run as its own process: a Q4_1 decode GEMV
+    called from C, checked against its double-precision loop (1e-3)."""
+    import subprocess
+
+    import rlxq
+
+    announce("plain C caller")
+    exe = rlxq.PKG / "lib" / "examples" / "decode_gemv"
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=100)
+    print(r.stdout, flush=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "rlxq_gemv" in r.stdout
