@@ -594,6 +594,8 @@ RLXQ_GEMVXS_Q4K
   RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D1_W8_M4, SCH, 2, 1, 8, 4)      \
   RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8_M4, SCH, 2, 2, 8, 4)
 RLXQ_GEMVXSM_SCHEME(q4_1, SCH_Q4_1)
+RLXQ_GEMVXSM_SCHEME(mlx4, SCH_MLX4)
+RLXQ_GEMVXSM_SCHEME(mxfp4, SCH_MXFP4)
 RLXQ_GEMVXS_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXS_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_GEMVXS_SCHEME(mlx4, SCH_MLX4)

@@ -419,3 +419,32 @@ def test_plain_c_caller_on_the_gpu():
     print(r.stdout, flush=True)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "rlxq_gemv" in r.stdout
+
+
+@pytest.mark.parametrize("scheme", ["mlx4", "mxfp4"])
+@pytest.mark.parametrize("m", [2, 4])
+def test_multi_row_register_path_mlx_mxfp4(ctx, orc, m, scheme):
+    """M = 2..4 on the register kernel for the other one-block 4-bit formats:
+    MLX affine 4-bit (group 64, bf16 slabs) and MXFP4 (E8M0 scales)."""
+    import torch
+    import rlxq
+
+    k, n = 4096, 1000
+    announce(f"multi-row register gemv {scheme} m={m}")
+    rng = np.random.default_rng(90 + m)
+    x32 = rng.standard_normal((m, k)).astype(np.float32)
+    xt, xv = _x_as(x32, "bf16")
+    if scheme == "mlx4":
+        codes = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint32)
+        sc = (rng.uniform(0.01, 0.1, (n, k // 64))).astype(np.float32)
+        bi = (rng.uniform(-0.5, 0.1, (n, k // 64))).astype(np.float32)
+        sct, bit = _t(sc).to(torch.bfloat16), _t(bi).to(torch.bfloat16)
+        y = ctx.dequant_matmul(xt, _t(codes.view(np.uint8)), rlxq.MLX_AFFINE4, n, group=64, scales=sct, biases=bit)
+        want = orc.mlx_matmul_f64(xv, codes, sct.float().cpu().numpy(), bit.float().cpu().numpy(), n, 4, 64)
+    else:
+        codes, eb = orc.synth_mxfp4(rng, n, k)
+        y = ctx.dequant_matmul(xt, _t(codes), rlxq.MLX_MXFP4, n, scales=_t(eb))
+        want = orc.mxfp4_matmul_f64(xv, codes, eb, n)
+    torch.cuda.synchronize()
+    assert ctx.last_kernel.endswith(f"_M{m}"), ctx.last_kernel
+    assert rel_err(y.cpu().numpy(), want) <= 1e-3
