@@ -353,8 +353,8 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     return launch(ctx, fn, dim3((unsigned)gx, 1, 1), dim3(64 * xr_w, 1, 1), lds, stream, args, name);
   }
 
-  // Two to four activation rows (bf16; Q4_1, MLX 4-bit, MXFP4: one-block
-  // units): the same register kernel with
+  // Two to four activation rows (bf16; Q4_1, MLX 4-bit, MXFP4, Q4_K): the
+  // same register kernel with
   // the rows' activations side by side in registers (MT = 2 or 4 rows, at
   // most 8 units of activations per lane), so every weight row is fetched
   // once for all of them.  RLXQ_GEMV_XR=0 turns it off as well.
@@ -362,12 +362,15 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     const char* e = std::getenv("RLXQ_GEMV_XR");
     const int mt = m <= 2 ? 2 : 4;
     const bool one_block4 = scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_MXFP4;
-    if (m >= 2 && m <= 4 && xbf && one_block4 && n < (int64_t(1) << 31) && !(e && e[0] == '0') &&
-        nchunk64 <= (mt == 2 ? 4 : 2)) {
+    // Q4_K's 64-weight units hold twice the activations: NU * MT <= 4
+    const int64_t max_nu = q4k ? (mt == 2 ? 2 : 1) : (mt == 2 ? 4 : 2);
+    if (m >= 2 && m <= 4 && xbf && (one_block4 || q4k) && n < (int64_t(1) << 31) && !(e && e[0] == '0') &&
+        nchunk64 <= max_nu) {
       // (two steps in flight up to two chunks; 4-wave groups for two rows at
       // K = 4096: gate_up 15.5 us at M = 2, 23.4 at M = 4 on 8 waves)
       const int nu = (int)nchunk64;
       int d = nu <= 2 ? 2 : 1, wv = (nu == 2 && mt == 2) ? 4 : 8;
+      if (q4k) d = nu == 1 ? 2 : 1, wv = 8;
       if (const char* t = std::getenv("RLXQ_GEMV_XSM")) std::sscanf(t, "%d,%d", &d, &wv);   // "D,W" (tuning)
       std::snprintf(name, sizeof name, "rlxq_gemvxs_%s_U%d_D%d_W%d_M%d", scheme_name(scheme), nu, d, wv, mt);
       if ((rc = get_fn(ctx, name, &fn))) return rc;

@@ -596,6 +596,10 @@ RLXQ_GEMVXS_Q4K
 RLXQ_GEMVXSM_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXSM_SCHEME(mlx4, SCH_MLX4)
 RLXQ_GEMVXSM_SCHEME(mxfp4, SCH_MXFP4)
+// Q4_K (two-block units): NU * MT <= 4
+RLXQ_GEMVXSM_INST(rlxq_gemvxs_q4_k_U1_D2_W8_M2, SCH_Q4_K, 1, 2, 8, 2)
+RLXQ_GEMVXSM_INST(rlxq_gemvxs_q4_k_U2_D1_W8_M2, SCH_Q4_K, 2, 1, 8, 2)
+RLXQ_GEMVXSM_INST(rlxq_gemvxs_q4_k_U1_D2_W8_M4, SCH_Q4_K, 1, 2, 8, 4)
 RLXQ_GEMVXS_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXS_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_GEMVXS_SCHEME(mlx4, SCH_MLX4)

@@ -421,11 +421,11 @@ def test_plain_c_caller_on_the_gpu():
     assert "rlxq_gemv" in r.stdout
 
 
-@pytest.mark.parametrize("scheme", ["mlx4", "mxfp4"])
+@pytest.mark.parametrize("scheme", ["mlx4", "mxfp4", "q4_k"])
 @pytest.mark.parametrize("m", [2, 4])
 def test_multi_row_register_path_mlx_mxfp4(ctx, orc, m, scheme):
-    """M = 2..4 on the register kernel for the other one-block 4-bit formats:
-    MLX affine 4-bit (group 64, bf16 slabs) and MXFP4 (E8M0 scales)."""
+    """M = 2..4 on the register kernel for the other 4-bit formats: MLX
+    affine 4-bit (group 64, bf16 slabs), MXFP4 (E8M0 scales) and Q4_K."""
     import torch
     import rlxq
 
@@ -441,10 +441,14 @@ def test_multi_row_register_path_mlx_mxfp4(ctx, orc, m, scheme):
         sct, bit = _t(sc).to(torch.bfloat16), _t(bi).to(torch.bfloat16)
         y = ctx.dequant_matmul(xt, _t(codes.view(np.uint8)), rlxq.MLX_AFFINE4, n, group=64, scales=sct, biases=bit)
         want = orc.mlx_matmul_f64(xv, codes, sct.float().cpu().numpy(), bit.float().cpu().numpy(), n, 4, 64)
-    else:
+    elif scheme == "mxfp4":
         codes, eb = orc.synth_mxfp4(rng, n, k)
         y = ctx.dequant_matmul(xt, _t(codes), rlxq.MLX_MXFP4, n, scales=_t(eb))
         want = orc.mxfp4_matmul_f64(xv, codes, eb, n)
+    else:
+        packed = orc.synth_q4_k(rng, n, k)
+        y = ctx.dequant_matmul(xt, _t(packed), rlxq.GGUF_Q4_K, n)
+        want = want_f64(orc, rlxq.GGUF_Q4_K, xv, packed, k)
     torch.cuda.synchronize()
     assert ctx.last_kernel.endswith(f"_M{m}"), ctx.last_kernel
     assert rel_err(y.cpu().numpy(), want) <= 1e-3
