@@ -683,6 +683,10 @@ RLXQ_MOE_SCHEME(q6_k, SCH_Q6_K)
 RLXQ_MOEXR_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_MOEXR_SCHEME(mlx4, SCH_MLX4)
 RLXQ_MOEXR_SCHEME(mxfp4, SCH_MXFP4)
+// Q4_1 at 33..64 units (K = 2048): 32-lane groups of two units
+RLXQ_MOEXR_LU(q4_1, SCH_Q4_1, 32, 2, 1, 2)
+RLXQ_MOEXR_LU(q4_1, SCH_Q4_1, 32, 2, 2, 2)
+RLXQ_MOEXR_LU(q4_1, SCH_Q4_1, 32, 2, 4, 2)
 // Q4_K: 64-weight units (two blocks, 12 dwords): at most two units per lane;
 // 32-lane groups for the 32 units of K = 2048
 RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 32, 1, 1, 4)

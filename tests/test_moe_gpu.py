@@ -391,7 +391,7 @@ def test_moe_ffn_config5_fused_swiglu(ctx, orc):
 
 
 # (k, lane-group shape the register path picks for Q4_1: L lanes x NU units)
-XR_SHAPES = [(96, "L8_U1"), (512, "L8_U2"), (768, "L8_U3"), (1024, "L8_U4"), (2048, "L64_U1"),
+XR_SHAPES = [(96, "L8_U1"), (512, "L8_U2"), (768, "L8_U3"), (1024, "L8_U4"), (2048, "L32_U2"),
              (2560, "L64_U2"), (8192, "L64_U4")]
 
 
