@@ -83,9 +83,11 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   for (const auto& c : cand)
     if (!(wide && c[1] > 2) && !(c[0] == 32 && !q4k) && c[0] * c[1] >= units && (L == 0 || c[0] * c[1] < L * NU))
       L = c[0], NU = c[1];
-  // Q4_1 at 33..64 units: 32-lane groups of two units rather than 64 lanes of
-  // one (config 5's gate|up, K = 2048: 40.4 against 44.1 us)
-  if (scheme == RLXQ_GGUF_Q4_1 && units > 32 && units <= 64) L = 32, NU = 2;
+  // one-block 4-bit units, 33..64 of them: 32-lane groups of two units rather
+  // than 64 lanes of one (config 5's Q4_1 gate|up, K = 2048: 40.4 against
+  // 44.1 us)
+  const bool one_block4 = scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_MXFP4;
+  if (one_block4 && units > 32 && units <= 64) L = 32, NU = 2;
   // Q4_K with under 70% of the lanes holding a unit (K = 2048 on 64-lane
   // groups: 32 units) measured slower than the LDS-record kernel (gate|up 79
   // against 58 us at config 5); RLXQ_MOE_KERNEL=xr|lds forces one (tests)

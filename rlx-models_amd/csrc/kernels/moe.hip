@@ -687,6 +687,12 @@ RLXQ_MOEXR_SCHEME(mxfp4, SCH_MXFP4)
 RLXQ_MOEXR_LU(q4_1, SCH_Q4_1, 32, 2, 1, 2)
 RLXQ_MOEXR_LU(q4_1, SCH_Q4_1, 32, 2, 2, 2)
 RLXQ_MOEXR_LU(q4_1, SCH_Q4_1, 32, 2, 4, 2)
+RLXQ_MOEXR_LU(mlx4, SCH_MLX4, 32, 2, 1, 2)
+RLXQ_MOEXR_LU(mlx4, SCH_MLX4, 32, 2, 2, 2)
+RLXQ_MOEXR_LU(mlx4, SCH_MLX4, 32, 2, 4, 2)
+RLXQ_MOEXR_LU(mxfp4, SCH_MXFP4, 32, 2, 1, 2)
+RLXQ_MOEXR_LU(mxfp4, SCH_MXFP4, 32, 2, 2, 2)
+RLXQ_MOEXR_LU(mxfp4, SCH_MXFP4, 32, 2, 4, 2)
 // Q4_K: 64-weight units (two blocks, 12 dwords): at most two units per lane;
 // 32-lane groups for the 32 units of K = 2048
 RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 32, 1, 1, 4)
