@@ -23,6 +23,13 @@
  *   - A context is used by one host thread at a time (the reference's
  *     CompiledGraph is &mut self); calls on different streams may overlap
  *     (the library's scratch is kept per stream).
+ *   - Scratch: some paths (batched decode, split-K, MoE routing, W8A8) use
+ *     device scratch that the context allocates per stream and grows on
+ *     demand.  A buffer replaced by growth is kept until
+ *     rlxq_release_stream or rlxq_destroy, so a HIP graph captured earlier
+ *     stays valid.  A call under stream capture must not need growth (the
+ *     allocation fails under global capture): size the stream's scratch
+ *     first with rlxq_reserve_workspace, or run the call once uncaptured.
  */
 #ifndef RLXQ_H
 #define RLXQ_H
@@ -108,6 +115,15 @@ const char* rlxq_last_error(const rlxq_ctx* ctx);
 const char* rlxq_last_kernel(const rlxq_ctx* ctx);
 /* Library version string, e.g. "rlxq 0.1.0 gfx950". */
 const char* rlxq_version(void);
+/* Scratch management (no counterpart in the reference, whose runtime owns
+ * its arena): make the scratch of `stream` at least `bytes`; report its
+ * size (0 if the stream has none); and free every scratch buffer the stream
+ * holds after waiting for the stream (graphs that captured calls on it must
+ * not be replayed afterwards).  For callers that capture graphs or use many
+ * streams (per-request streams, torch's stream pool). */
+int rlxq_reserve_workspace(rlxq_ctx* ctx, void* stream, size_t bytes);
+int64_t rlxq_workspace_bytes(const rlxq_ctx* ctx, void* stream);
+int rlxq_release_stream(rlxq_ctx* ctx, void* stream);
 
 /* Dense DequantMatMul: y[m, n] = sum_k x[m, k] * dequant(W)[n, k].
  * Replaces the backend kernel of Op::DequantMatMul{scheme} (the IR op is

@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import argparse
 import concurrent.futures as cf
+import hashlib
 import os
 import shutil
 import subprocess
@@ -27,9 +28,11 @@ CO = LIB / "co"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 
-# Code objects the host library embeds (rlxq.cpp RLXQ_EMBED lines).  A name
-# without a source file is embedded empty and skipped at load time.
-CODE_OBJECTS = ("gemv", "misc", "gemm", "moe", "int8", "skinny")
+# Code objects the host library embeds (rlxq.cpp RLXQ_EMBED lines), with the
+# number of parts each kernel file is compiled in (-DRLXQ_PART=i gives
+# <name><i>.co; the parts build in parallel).  A name without a source file is
+# embedded empty and skipped at load time.
+CODE_OBJECTS = (("gemv", 4), ("misc", 1), ("gemm", 1), ("moe", 4), ("int8", 1), ("skinny", 1))
 
 HIP_FLAGS = [
     "--genco", "--offload-arch=gfx950", "-O3", "-std=c++17",
@@ -46,19 +49,43 @@ def _run(cmd: list[str], what: str) -> None:
         raise RuntimeError(f"{what} failed ({r.returncode}):\n{' '.join(cmd)}\n{out}")
 
 
-def build_code_objects() -> None:
+def _inputs_digest(src: Path, defs: list[str]) -> str:
+    h = hashlib.sha256()
+    h.update(" ".join([*HIP_FLAGS, *defs]).encode())
+    for p in [src, *sorted(KDIR.glob("*.h"))]:
+        h.update(p.name.encode())
+        h.update(p.read_bytes())
+    return h.hexdigest()
+
+
+def build_code_objects(cached: bool = False) -> None:
+    """hipcc --genco of every kernel part.  With cached=True (development
+    only) a part whose source, kernel headers and flags are unchanged since its
+    last build is kept."""
     CO.mkdir(parents=True, exist_ok=True)
     jobs = []
-    for name in CODE_OBJECTS:
+    for name, parts in CODE_OBJECTS:
         src = KDIR / f"{name}.hip"
-        dst = CO / f"{name}.co"
-        if not src.exists():
-            dst.write_bytes(b"")
-            continue
-        jobs.append((name, [HIPCC, *HIP_FLAGS, "-I", str(KDIR), str(src), "-o", str(dst)]))
+        for i in range(parts):
+            dst = CO / (f"{name}{i}.co" if parts > 1 else f"{name}.co")
+            if not src.exists():
+                dst.write_bytes(b"")
+                continue
+            defs = [f"-DRLXQ_PART={i}"] if parts > 1 else []
+            stamp = dst.with_suffix(".sha256")
+            digest = _inputs_digest(src, defs)
+            if cached and dst.exists() and stamp.exists() and stamp.read_text() == digest:
+                continue
+            jobs.append((dst.stem, [HIPCC, *HIP_FLAGS, *defs, "-I", str(KDIR), str(src), "-o", str(dst)], stamp, digest))
+
+    def one(job):
+        stem, cmd, stamp, digest = job
+        stamp.unlink(missing_ok=True)
+        _run(cmd, f"hipcc {stem}")
+        stamp.write_text(digest)
+
     with cf.ThreadPoolExecutor(max_workers=min(8, max(1, len(jobs)))) as ex:
-        futs = [ex.submit(_run, cmd, f"hipcc {name}") for name, cmd in jobs]
-        for f in futs:
+        for f in [ex.submit(one, j) for j in jobs]:
             f.result()
 
 
@@ -112,11 +139,12 @@ def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--no-oracle", action="store_true")
     ap.add_argument("--host-only", action="store_true", help="relink librlxq.so from existing code objects")
+    ap.add_argument("--cached", action="store_true", help="keep code objects whose inputs are unchanged (development)")
     a = ap.parse_args(argv)
     if shutil.which("g++") is None or not Path(HIPCC).exists():
         raise RuntimeError("need g++ and hipcc")
     if not a.host_only:
-        build_code_objects()
+        build_code_objects(cached=a.cached)
     build_host()
     build_examples()
     if not a.no_oracle:

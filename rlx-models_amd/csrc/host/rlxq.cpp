@@ -4,7 +4,8 @@
 // The gfx950 code objects are assembled into this shared library at build
 // time (.incbin) and loaded with hipModuleLoadData; kernels are launched with
 // hipModuleLaunchKernel.  Nothing here allocates on the hot path except the
-// context scratch, which grows once to the largest size a call has needed.
+// per-stream context scratch, which grows to the largest size a call on that
+// stream has needed (rlxq_reserve_workspace sizes it ahead).
 #include <hip/hip_runtime_api.h>
 
 #include <cstdio>
@@ -31,10 +32,16 @@
   extern "C" __attribute__((visibility("hidden"))) const unsigned char sym##_begin[];         \
   extern "C" __attribute__((visibility("hidden"))) const unsigned char sym##_end[];
 
-RLXQ_EMBED(rlxq_co_gemv, "gemv.co")
+RLXQ_EMBED(rlxq_co_gemv0, "gemv0.co")
+RLXQ_EMBED(rlxq_co_gemv1, "gemv1.co")
+RLXQ_EMBED(rlxq_co_gemv2, "gemv2.co")
+RLXQ_EMBED(rlxq_co_gemv3, "gemv3.co")
 RLXQ_EMBED(rlxq_co_misc, "misc.co")
 RLXQ_EMBED(rlxq_co_gemm, "gemm.co")
-RLXQ_EMBED(rlxq_co_moe, "moe.co")
+RLXQ_EMBED(rlxq_co_moe0, "moe0.co")
+RLXQ_EMBED(rlxq_co_moe1, "moe1.co")
+RLXQ_EMBED(rlxq_co_moe2, "moe2.co")
+RLXQ_EMBED(rlxq_co_moe3, "moe3.co")
 RLXQ_EMBED(rlxq_co_int8, "int8.co")
 RLXQ_EMBED(rlxq_co_skinny, "skinny.co")
 
@@ -47,10 +54,16 @@ struct Image {
 };
 
 const Image kImages[] = {
-    {rlxq_co_gemv_begin, rlxq_co_gemv_end, "gemv"},
+    {rlxq_co_gemv0_begin, rlxq_co_gemv0_end, "gemv0"},
+    {rlxq_co_gemv1_begin, rlxq_co_gemv1_end, "gemv1"},
+    {rlxq_co_gemv2_begin, rlxq_co_gemv2_end, "gemv2"},
+    {rlxq_co_gemv3_begin, rlxq_co_gemv3_end, "gemv3"},
     {rlxq_co_misc_begin, rlxq_co_misc_end, "misc"},
     {rlxq_co_gemm_begin, rlxq_co_gemm_end, "gemm"},
-    {rlxq_co_moe_begin, rlxq_co_moe_end, "moe"},
+    {rlxq_co_moe0_begin, rlxq_co_moe0_end, "moe0"},
+    {rlxq_co_moe1_begin, rlxq_co_moe1_end, "moe1"},
+    {rlxq_co_moe2_begin, rlxq_co_moe2_end, "moe2"},
+    {rlxq_co_moe3_begin, rlxq_co_moe3_end, "moe3"},
     {rlxq_co_int8_begin, rlxq_co_int8_end, "int8"},
     {rlxq_co_skinny_begin, rlxq_co_skinny_end, "skinny"},
 };
@@ -133,22 +146,21 @@ int workspace(rlxq_ctx* ctx, size_t bytes, void** out, void* stream) {
     *out = w.p;
     return RLXQ_OK;
   }
-  // Growing frees the old buffer, which earlier work may still use: wait for
-  // the device (the null stream's work included).
-  if (w.p) {
-    hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) return fail(ctx, RLXQ_E_HIP, "workspace: sync: " + hip_msg(e));
-    (void)hipFree(w.p);
-    w.p = nullptr;
-    w.bytes = 0;
-  }
+  // The buffer being replaced may still be read by queued work or named by a
+  // captured graph: keep it until the stream is released or the context
+  // destroyed.  Nothing waits here.
   size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
   want = (want + 4095) & ~size_t(4095);
-  hipError_t e = hipMalloc(&w.p, want);
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, want);
   if (e != hipSuccess) {
-    w.p = nullptr;
-    return fail(ctx, RLXQ_E_NOMEM, "workspace: hipMalloc(" + std::to_string(want) + "): " + hip_msg(e));
+    (void)hipGetLastError();
+    return fail(ctx, RLXQ_E_NOMEM,
+                "workspace: hipMalloc(" + std::to_string(want) + "): " + hip_msg(e) +
+                    " (under stream capture, size the scratch first with rlxq_reserve_workspace)");
   }
+  if (w.p) w.retired.push_back(w.p);
+  w.p = p;
   w.bytes = want;
   *out = w.p;
   return RLXQ_OK;
@@ -246,11 +258,44 @@ int rlxq_destroy(rlxq_ctx* ctx) {
   {
     DeviceGuard g(ctx->device);
     if (!ctx->ws.empty()) (void)hipDeviceSynchronize();
-    for (auto& kv : ctx->ws)
+    for (auto& kv : ctx->ws) {
       if (kv.second.p) (void)hipFree(kv.second.p);
+      for (void* p : kv.second.retired) (void)hipFree(p);
+    }
     for (hipModule_t m : ctx->modules) (void)hipModuleUnload(m);
   }
   delete ctx;
+  return RLXQ_OK;
+}
+
+int rlxq_reserve_workspace(rlxq_ctx* ctx, void* stream, size_t bytes) {
+  if (!ctx) return RLXQ_E_NULL;
+  ctx->last_error.clear();
+  DeviceGuard g(ctx->device);
+  if (!g.ok()) return fail(ctx, RLXQ_E_HIP, "reserve_workspace: hipSetDevice");
+  void* p = nullptr;
+  return workspace(ctx, bytes, &p, stream);
+}
+
+int64_t rlxq_workspace_bytes(const rlxq_ctx* ctx, void* stream) {
+  if (!ctx) return RLXQ_E_NULL;
+  auto it = ctx->ws.find(stream);
+  return it == ctx->ws.end() ? 0 : (int64_t)it->second.bytes;
+}
+
+int rlxq_release_stream(rlxq_ctx* ctx, void* stream) {
+  if (!ctx) return RLXQ_E_NULL;
+  ctx->last_error.clear();
+  auto it = ctx->ws.find(stream);
+  if (it == ctx->ws.end()) return RLXQ_OK;
+  DeviceGuard g(ctx->device);
+  if (!g.ok()) return fail(ctx, RLXQ_E_HIP, "release_stream: hipSetDevice");
+  // Work queued on the stream may still use its buffers.
+  hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(ctx, RLXQ_E_HIP, "release_stream: sync: " + hip_msg(e));
+  if (it->second.p) (void)hipFree(it->second.p);
+  for (void* p : it->second.retired) (void)hipFree(p);
+  ctx->ws.erase(it);
   return RLXQ_OK;
 }
 

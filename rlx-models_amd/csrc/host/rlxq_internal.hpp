@@ -21,10 +21,14 @@ struct rlxq_ctx {
   size_t max_lds = 65536;
   // Library-owned scratch (routing tables, quantised activations, split-K
   // partials), one buffer per stream so that calls on different streams can
-  // overlap.  Grown on demand; freed by rlxq_destroy.
+  // overlap.  Grown on demand.  A buffer that growth replaces is never freed
+  // while the context lives (a HIP graph captured earlier may still name it):
+  // it moves to `retired` and is freed by rlxq_release_stream or
+  // rlxq_destroy.
   struct Scratch {
     void* p = nullptr;
     size_t bytes = 0;
+    std::vector<void*> retired;
   };
   std::unordered_map<void*, Scratch> ws;
 };

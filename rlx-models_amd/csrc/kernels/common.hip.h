@@ -6,6 +6,15 @@
 
 #define RLXQ_DEV __device__ __forceinline__
 
+// A large kernel file is compiled as several code objects, each holding the
+// instantiations of one part (-DRLXQ_PART=i); without RLXQ_PART a file holds
+// all of them.
+#ifdef RLXQ_PART
+#define RLXQ_PART_IS(i) (RLXQ_PART == (i))
+#else
+#define RLXQ_PART_IS(i) 1
+#endif
+
 typedef __bf16 rlxq_bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 rlxq_f16x2_t __attribute__((ext_vector_type(2)));
 

@@ -550,11 +550,13 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
 #define RLXQ_GEMVXR_WIDE(SNAME, SCH)                                    \
   RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U6_D1_W4, SCH, 6, 1, 4)       \
   RLXQ_GEMVXR_INST(rlxq_gemvxr_##SNAME##_U6_D2_W4, SCH, 6, 2, 4)
+#if RLXQ_PART_IS(0)
 RLXQ_GEMVXR_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXR_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_GEMVXR_SCHEME(mlx4, SCH_MLX4)
 RLXQ_GEMVXR_WIDE(q4_1, SCH_Q4_1)
 RLXQ_GEMVXR_WIDE(mlx4, SCH_MLX4)
+#endif
 #define RLXQ_GEMVXS_SCHEME(SNAME, SCH)                                  \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U1_D2_W8, SCH, 1, 2, 8)       \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8, SCH, 2, 2, 8)       \
@@ -573,7 +575,9 @@ RLXQ_GEMVXR_WIDE(mlx4, SCH_MLX4)
   RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U2_D2_W8, SCH_Q4_K, 2, 2, 8)          \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U2_D1_W8, SCH_Q4_K, 2, 1, 8)          \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U3_D1_W8, SCH_Q4_K, 3, 1, 8)
+#if RLXQ_PART_IS(0)
 RLXQ_GEMVXS_Q4K
+#endif
 // several activation rows (M = 2..4): rlxq_gemvxs_<scheme>_U<NU>_D<D>_W<W>_M<MT>,
 // NU * MT <= 8 units of activations per lane
 #define RLXQ_GEMVXSM_INST(NAME, SCH, NU, D, W, MT)                                    \
@@ -593,6 +597,7 @@ RLXQ_GEMVXS_Q4K
   RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8_M2, SCH, 2, 2, 8, 2)      \
   RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D1_W8_M4, SCH, 2, 1, 8, 4)      \
   RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8_M4, SCH, 2, 2, 8, 4)
+#if RLXQ_PART_IS(1)
 RLXQ_GEMVXSM_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXSM_SCHEME(mlx4, SCH_MLX4)
 RLXQ_GEMVXSM_SCHEME(mxfp4, SCH_MXFP4)
@@ -600,6 +605,8 @@ RLXQ_GEMVXSM_SCHEME(mxfp4, SCH_MXFP4)
 RLXQ_GEMVXSM_INST(rlxq_gemvxs_q4_k_U1_D2_W8_M2, SCH_Q4_K, 1, 2, 8, 2)
 RLXQ_GEMVXSM_INST(rlxq_gemvxs_q4_k_U2_D1_W8_M2, SCH_Q4_K, 2, 1, 8, 2)
 RLXQ_GEMVXSM_INST(rlxq_gemvxs_q4_k_U1_D2_W8_M4, SCH_Q4_K, 1, 2, 8, 4)
+#endif
+#if RLXQ_PART_IS(0)
 RLXQ_GEMVXS_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXS_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_GEMVXS_SCHEME(mlx4, SCH_MLX4)
@@ -608,11 +615,16 @@ RLXQ_GEMVXS_WIDE(q4_1, SCH_Q4_1)
 RLXQ_GEMVXS_WIDE(mlx4, SCH_MLX4)
 RLXQ_GEMVXS_WIDE(mxfp4, SCH_MXFP4)
 
+#endif
+#if RLXQ_PART_IS(2)
 RLXQ_GEMV_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMV_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_GEMV_SCHEME(q8_0, SCH_Q8_0)
 RLXQ_GEMV_SCHEME(q4_k, SCH_Q4_K)
 RLXQ_GEMV_SCHEME(q6_k, SCH_Q6_K)
+#endif
+#if RLXQ_PART_IS(3)
 RLXQ_GEMV_SCHEME(mlx4, SCH_MLX4)
 RLXQ_GEMV_SCHEME(mlx8, SCH_MLX8)
 RLXQ_GEMV_SCHEME(mxfp4, SCH_MXFP4)
+#endif

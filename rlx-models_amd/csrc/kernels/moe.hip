@@ -16,6 +16,7 @@
 #include "gemv_core.hip.h"
 #include "moe_args.h"
 
+#if RLXQ_PART_IS(0)
 // One workgroup of 1024 threads.  E <= 1024.
 extern "C" __global__ __launch_bounds__(1024) void rlxq_moe_table_k(rlxq_moe_table_args a) {
   __shared__ int32_t cnt[1024], cur[1024], scan[1024];
@@ -99,6 +100,7 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_moe_combine_k(const float
   if (y_bf16) reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)f32_to_bf16_bits(s);
   else reinterpret_cast<float*>(y)[i] = s;
 }
+#endif
 
 namespace rlxq {
 
@@ -640,14 +642,18 @@ RLXQ_DEV void moe_xr_body(const rlxq_moe_gemv_args& a) {
   RLXQ_MOE_X(SNAME, SCH, bf16, true) \
   RLXQ_MOE_X(SNAME, SCH, f32, false)
 
+#if RLXQ_PART_IS(0)
 RLXQ_MOE_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_MOE_SCHEME(q4_0, SCH_Q4_0)
 RLXQ_MOE_SCHEME(q8_0, SCH_Q8_0)
 RLXQ_MOE_SCHEME(mlx4, SCH_MLX4)
+#endif
+#if RLXQ_PART_IS(1)
 RLXQ_MOE_SCHEME(mlx8, SCH_MLX8)
 RLXQ_MOE_SCHEME(mxfp4, SCH_MXFP4)
 RLXQ_MOE_SCHEME(q4_k, SCH_Q4_K)
 RLXQ_MOE_SCHEME(q6_k, SCH_Q6_K)
+#endif
 
 // Register-activation variants (4-bit codes, bf16 activations):
 // rlxq_moexr[f]_<scheme>_L<L>_U<NU>_M<MT>[_sw]; f = routing in the workgroup.
@@ -680,9 +686,14 @@ RLXQ_MOE_SCHEME(q6_k, SCH_Q6_K)
   RLXQ_MOEXR_LU(SNAME, SCH, 8, 3, 2, 2)      \
   RLXQ_MOEXR_LU(SNAME, SCH, 8, 4, 1, 1)      \
   RLXQ_MOEXR_LU(SNAME, SCH, 8, 4, 2, 1)
+#if RLXQ_PART_IS(2)
 RLXQ_MOEXR_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_MOEXR_SCHEME(mlx4, SCH_MLX4)
+#endif
+#if RLXQ_PART_IS(3)
 RLXQ_MOEXR_SCHEME(mxfp4, SCH_MXFP4)
+#endif
+#if RLXQ_PART_IS(2)
 // Q4_1 at 33..64 units (K = 2048): 32-lane groups of two units
 RLXQ_MOEXR_LU(q4_1, SCH_Q4_1, 32, 2, 1, 2)
 RLXQ_MOEXR_LU(q4_1, SCH_Q4_1, 32, 2, 2, 2)
@@ -693,6 +704,8 @@ RLXQ_MOEXR_LU(mlx4, SCH_MLX4, 32, 2, 4, 2)
 RLXQ_MOEXR_LU(mxfp4, SCH_MXFP4, 32, 2, 1, 2)
 RLXQ_MOEXR_LU(mxfp4, SCH_MXFP4, 32, 2, 2, 2)
 RLXQ_MOEXR_LU(mxfp4, SCH_MXFP4, 32, 2, 4, 2)
+#endif
+#if RLXQ_PART_IS(3)
 // Q4_K: 64-weight units (two blocks, 12 dwords): at most two units per lane;
 // 32-lane groups for the 32 units of K = 2048
 RLXQ_MOEXR_LU(q4_k, SCH_Q4_K, 32, 1, 1, 4)
@@ -711,3 +724,4 @@ RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 64, 2, 1, 2)
 RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 8, 1, 1, 4)
 RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 8, 1, 2, 4)
 RLXQ_MOEXR_LU(q4_0, SCH_Q4_0, 8, 2, 1, 2)
+#endif

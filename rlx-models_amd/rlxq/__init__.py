@@ -54,6 +54,9 @@ def lib() -> C.CDLL:
         "rlxq_last_kernel": (C.c_char_p, [P]),
         "rlxq_version": (C.c_char_p, []),
         "rlxq_row_bytes": (I64, [I, I64]),
+        "rlxq_reserve_workspace": (I, [P, P, S]),
+        "rlxq_workspace_bytes": (I64, [P, P]),
+        "rlxq_release_stream": (I, [P, P]),
         "rlxq_dequant_matmul": (I, [P, I, I, P, I, P, P, P, I, I64, I64, I64, P, I, P]),
         "rlxq_dequant_grouped_matmul": (I, [P, I, I, P, I, P, P, P, I, P, I64, I64, I64, I64, P, I, P]),
         "rlxq_moe_grouped": (I, [P, I, I, P, I, P, P, P, I64, I64, I64, I64, I64, P, I, P]),
@@ -136,6 +139,166 @@ def _dt(t) -> int:
     raise TypeError(f"unsupported dtype {t.dtype}")
 
 
+# ---- argument checks -------------------------------------------------------
+# The C entry points check shapes, schemes and alignment, but they receive raw
+# device pointers: they cannot see a tensor's size, layout or device.  These
+# checks run before every call of the wrappers below and raise ValueError, so
+# a wrong n, num_experts or output buffer never reaches a kernel.
+
+_PACKED = (GGUF_Q8_0, GGUF_Q4_0, GGUF_Q4_1, MLX_AFFINE4, MLX_AFFINE8, GGUF_Q4_K, GGUF_Q6_K, MLX_MXFP4)
+
+
+def packed_row_bytes(scheme: int, k: int) -> int:
+    """Bytes of one packed weight row of K elements (-1 if K does not fit
+    the scheme): GGUF blocks, MLX u32 codes, MXFP4 code bytes."""
+    if scheme == MLX_AFFINE4 or scheme == MLX_MXFP4:
+        return k // 2 if k > 0 and k % 32 == 0 else -1
+    if scheme == MLX_AFFINE8:
+        return k if k > 0 and k % 32 == 0 else -1
+    return int(lib().rlxq_row_bytes(scheme, k))
+
+
+def _need(cond, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _nbytes(t) -> int:
+    return t.numel() * t.element_size()
+
+
+def _tensor(t, name: str, dtypes=None, ndim=None):
+    _need(t is not None, f"{name} is required")
+    _need(hasattr(t, "data_ptr") and hasattr(t, "is_contiguous"), f"{name} must be a tensor")
+    _need(t.is_contiguous(), f"{name} must be contiguous (got strides {tuple(t.stride())})")
+    if dtypes is not None:
+        _need(t.dtype in dtypes, f"{name} has dtype {t.dtype}, expected one of {[str(d) for d in dtypes]}")
+    if ndim is not None:
+        _need(t.dim() == ndim, f"{name} must be {ndim}-D (got shape {tuple(t.shape)})")
+
+
+def _on_device(device: int, **tensors) -> None:
+    for name, t in tensors.items():
+        if t is not None:
+            _need(t.is_cuda and (t.device.index or 0) == device,
+                  f"{name} is on {t.device}, the context is on cuda:{device}")
+
+
+def _act_dtypes():
+    import torch
+
+    return (torch.float32, torch.bfloat16)
+
+
+def _check_weights(scheme: int, group: int, w, scales, biases, rows: int, k: int, what: str) -> None:
+    """w (and the MLX / MXFP4 / Int8Block slabs) hold at least `rows` packed
+    rows of K weights (rows = N, or E * N for an expert bank).  What the C
+    entry point checks itself (scheme, K against the scheme, group size, slab
+    dtypes, NULL slabs) is left to it, so its status codes reach the caller."""
+    import torch
+
+    _tensor(w, f"{what}: w")
+    if scheme == INT8_BLOCK:
+        _need(w.dtype in (torch.int8, torch.uint8), f"{what}: Int8Block weights are int8 [K, N]")
+        _need(_nbytes(w) >= k * rows, f"{what}: w holds {_nbytes(w)} B, [K={k}, N={rows}] int8 needs {k * rows}")
+        for nm, t in (("scales", scales), ("zero points", biases)):
+            if t is not None:
+                _tensor(t, f"{what}: {nm}")
+                _need(t.numel() >= rows, f"{what}: {nm} have {t.numel()} elements, N = {rows}")
+        return
+    if scheme not in _PACKED:
+        return
+    rb = packed_row_bytes(scheme, k)
+    if rb <= 0:
+        return
+    _need(_nbytes(w) >= rows * rb, f"{what}: w holds {_nbytes(w)} B, {rows} rows of {rb} B need {rows * rb}")
+    if scheme in (MLX_AFFINE4, MLX_AFFINE8, MLX_MXFP4):
+        g = 32 if scheme == MLX_MXFP4 else group
+        if g <= 0 or k % g:
+            return
+        per = rows * (k // g)
+        slabs = (("scales", scales),) if scheme == MLX_MXFP4 else (("scales", scales), ("biases", biases))
+        for nm, t in slabs:
+            if t is not None:
+                _tensor(t, f"{what}: {nm}")
+                _need(t.numel() >= per, f"{what}: {nm} has {t.numel()} elements, [{rows}, {k // g}] needs {per}")
+        if scheme != MLX_MXFP4 and scales is not None and biases is not None:
+            _need(scales.dtype == biases.dtype, f"{what}: scales and biases must share a dtype")
+
+
+def _check_out(y, shape, what: str) -> None:
+    _tensor(y, f"{what}: y", _act_dtypes())
+    _need(tuple(y.shape) == tuple(shape), f"{what}: y has shape {tuple(y.shape)}, expected {tuple(shape)}")
+
+
+def check_dense(x, w, scheme: int, n: int, *, group: int = 32, scales=None, biases=None, y=None,
+                device=None) -> None:
+    """Raises ValueError unless the dense call's tensors fit each other."""
+    _tensor(x, "dequant_matmul: x", _act_dtypes(), 2)
+    m, k = x.shape
+    _need(n >= 0, "dequant_matmul: n must be >= 0")
+    _check_weights(scheme, group, w, scales, biases, n, k, "dequant_matmul")
+    if y is not None:
+        _check_out(y, (m, n), "dequant_matmul")
+    if device is not None:
+        _on_device(device, x=x, w=w, scales=scales, biases=biases, y=y)
+
+
+def check_grouped(x, bank, expert_idx, scheme: int, n: int, num_experts: int, *, group: int = 32, scales=None,
+                  biases=None, y=None, device=None) -> None:
+    import torch
+
+    _tensor(x, "grouped_matmul: x", _act_dtypes(), 2)
+    rows, k = x.shape
+    _need(num_experts > 0 and n >= 0, "grouped_matmul: need num_experts > 0 and n >= 0")
+    _check_weights(scheme, group, bank, scales, biases, num_experts * n, k, "grouped_matmul")
+    _tensor(expert_idx, "grouped_matmul: expert_idx", (torch.float32,))
+    _need(expert_idx.numel() == rows, f"grouped_matmul: expert_idx has {expert_idx.numel()} entries, rows = {rows}")
+    if y is not None:
+        _check_out(y, (rows, n), "grouped_matmul")
+    if device is not None:
+        _on_device(device, x=x, bank=bank, expert_idx=expert_idx, scales=scales, biases=biases, y=y)
+
+
+def check_moe(x, bank, ids, probs, scheme: int, mode: int, n: int, num_experts: int, *, y=None,
+              device=None) -> None:
+    import torch
+
+    _need(mode in (MOE_EXPAND, MOE_COMBINE, MOE_EXPAND_SWIGLU), f"moe_grouped: unknown mode {mode}")
+    _tensor(ids, "moe_grouped: ids", (torch.int32,), 2)
+    rows, top_k = ids.shape
+    _tensor(x, "moe_grouped: x", _act_dtypes(), 2)
+    k = x.shape[1]
+    want_rows = rows * top_k if mode == MOE_COMBINE else rows
+    _need(x.shape[0] == want_rows, f"moe_grouped: x has {x.shape[0]} rows, this mode needs {want_rows}")
+    _need(num_experts > 0 and n >= 0, "moe_grouped: need num_experts > 0 and n >= 0")
+    _need(mode != MOE_EXPAND_SWIGLU or n % 2 == 0, "moe_grouped: EXPAND_SWIGLU needs an even n (gate|up)")
+    _check_weights(scheme, 32, bank, None, None, num_experts * n, k, "moe_grouped")
+    if mode == MOE_COMBINE:
+        _tensor(probs, "moe_grouped: probs", (torch.float32,), 2)
+        _need(tuple(probs.shape) == (rows, top_k), f"moe_grouped: probs has shape {tuple(probs.shape)}")
+    if y is not None:
+        width = n // 2 if mode == MOE_EXPAND_SWIGLU else n
+        _check_out(y, (rows if mode == MOE_COMBINE else rows * top_k, width), "moe_grouped")
+    if device is not None:
+        _on_device(device, x=x, bank=bank, ids=ids, probs=probs if mode == MOE_COMBINE else None, y=y)
+
+
+def check_w8a8(x, wq, w_scale, n: int, *, y=None, device=None) -> None:
+    import torch
+
+    _tensor(x, "w8a8_gemm: x", _act_dtypes(), 2)
+    m, k = x.shape
+    _tensor(wq, "w8a8_gemm: wq", (torch.int8,))
+    _need(wq.numel() >= k * n, f"w8a8_gemm: wq has {wq.numel()} elements, [K={k}, N={n}] needs {k * n}")
+    _tensor(w_scale, "w8a8_gemm: w_scale", (torch.float32,))
+    _need(w_scale.numel() >= n, f"w8a8_gemm: w_scale has {w_scale.numel()} elements, N = {n}")
+    if y is not None:
+        _check_out(y, (m, n), "w8a8_gemm")
+    if device is not None:
+        _on_device(device, x=x, wq=wq, w_scale=w_scale, y=y)
+
+
 class Context:
     """Owns an rlxq_ctx on one device (rlxq_init / rlxq_destroy)."""
 
@@ -166,6 +329,18 @@ class Context:
     def last_kernel(self) -> str:
         return lib().rlxq_last_kernel(self.h).decode()
 
+    def reserve_workspace(self, nbytes: int, *, stream=None) -> None:
+        """Sizes the context scratch of `stream` to at least nbytes (before a
+        graph capture)."""
+        self._check(lib().rlxq_reserve_workspace(self.h, _stream(stream), nbytes), "reserve_workspace")
+
+    def workspace_bytes(self, *, stream=None) -> int:
+        return int(lib().rlxq_workspace_bytes(self.h, _stream(stream)))
+
+    def release_stream(self, *, stream=None) -> None:
+        """Frees the scratch buffers of `stream` after waiting for it."""
+        self._check(lib().rlxq_release_stream(self.h, _stream(stream)), "release_stream")
+
     def bind_dequant_matmul(self, x, w, scheme: int, n: int, *, y, stream, group: int = 32, scales=None,
                             biases=None):
         """A zero-argument callable that runs dequant_matmul on these tensors.
@@ -174,6 +349,7 @@ class Context:
         holds them, so a call costs the C entry point and not this module's
         argument handling (decode launches are a few microseconds each).  The
         tensors must stay alive while the callable is used."""
+        check_dense(x, w, scheme, n, group=group, scales=scales, biases=biases, y=y, device=self.device)
         m, k = x.shape
         sb = _dt(scales) if scales is not None else F32
         fn = lib().rlxq_dequant_matmul
@@ -193,6 +369,7 @@ class Context:
         """y[m, n] = x[m, k] . dequant(w)^T; returns y (allocated if not given)."""
         import torch
 
+        check_dense(x, w, scheme, n, group=group, scales=scales, biases=biases, y=y, device=self.device)
         m, k = x.shape
         if y is None:
             y = torch.empty((m, n), dtype=y_dtype or torch.float32, device=x.device)
@@ -206,8 +383,14 @@ class Context:
                    out=None, stream=None):
         import torch
 
+        _need(rows >= 0 and k > 0, "dequantize: need rows >= 0 and k > 0")
+        _need(scheme != INT8_BLOCK, "dequantize: Int8Block has no packed rows")
+        _check_weights(scheme, group, w, scales, biases, rows, k, "dequantize")
         if out is None:
             out = torch.empty((rows, k), dtype=torch.float32, device=w.device)
+        _tensor(out, "dequantize: out", (torch.float32,))
+        _need(tuple(out.shape) == (rows, k), f"dequantize: out has shape {tuple(out.shape)}, expected {(rows, k)}")
+        _on_device(self.device, w=w, scales=scales, biases=biases, out=out)
         sb = _dt(scales) if scales is not None else F32
         rc = lib().rlxq_dequantize(self.h, scheme, group, _ptr(w), _ptr(scales), _ptr(biases), sb, rows, k,
                                    _ptr(out), _stream(stream))
@@ -218,6 +401,8 @@ class Context:
                        scales=None, biases=None, y=None, y_dtype=None, stream=None):
         import torch
 
+        check_grouped(x, bank, expert_idx, scheme, n, num_experts, group=group, scales=scales, biases=biases, y=y,
+                      device=self.device)
         rows, k = x.shape
         if y is None:
             y = torch.empty((rows, n), dtype=y_dtype or torch.float32, device=x.device)
@@ -232,6 +417,7 @@ class Context:
                     y=None, y_dtype=None, stream=None):
         import torch
 
+        check_moe(x, bank, ids, probs, scheme, mode, n, num_experts, y=y, device=self.device)
         rows, top_k = ids.shape
         k = x.shape[1]
         out_rows = rows if mode == MOE_COMBINE else rows * top_k
@@ -246,6 +432,8 @@ class Context:
     def moe_route(self, logits, top_k: int, renorm: bool, *, stream=None):
         import torch
 
+        _tensor(logits, "moe_route: logits", (torch.float32,), 2)
+        _on_device(self.device, logits=logits)
         rows, e = logits.shape
         ids = torch.empty((rows, top_k), dtype=torch.int32, device=logits.device)
         probs = torch.empty((rows, top_k), dtype=torch.float32, device=logits.device)
@@ -257,9 +445,13 @@ class Context:
     def swiglu(self, gu, inter: int, *, out=None, out_dtype=None, stream=None):
         import torch
 
+        _tensor(gu, "swiglu: gu", _act_dtypes(), 2)
+        _need(gu.shape[1] == 2 * inter, f"swiglu: gu has {gu.shape[1]} columns, 2 * inter = {2 * inter}")
         rows = gu.shape[0]
         if out is None:
             out = torch.empty((rows, inter), dtype=out_dtype or gu.dtype, device=gu.device)
+        _check_out(out, (rows, inter), "swiglu")
+        _on_device(self.device, gu=gu, out=out)
         rc = lib().rlxq_swiglu(self.h, _ptr(gu), _dt(gu), rows, inter, _ptr(out), _dt(out), _stream(stream))
         self._check(rc, "swiglu")
         return out
@@ -267,6 +459,8 @@ class Context:
     def quantize_act_int8(self, x, *, stream=None):
         import torch
 
+        _tensor(x, "quantize_act_int8: x", _act_dtypes(), 2)
+        _on_device(self.device, x=x)
         m, k = x.shape
         q = torch.empty((m, k), dtype=torch.int8, device=x.device)
         s = torch.empty((m,), dtype=torch.float32, device=x.device)
@@ -277,6 +471,7 @@ class Context:
     def w8a8_gemm(self, x, wq, w_scale, n: int, *, y=None, y_dtype=None, stream=None):
         import torch
 
+        check_w8a8(x, wq, w_scale, n, y=y, device=self.device)
         m, k = x.shape
         if y is None:
             y = torch.empty((m, n), dtype=y_dtype or torch.float32, device=x.device)
