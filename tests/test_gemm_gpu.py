@@ -2,8 +2,9 @@
 ABI: the bf16 kernels (weights rounded to bf16 in LDS, bf16 MFMA) and, for
 the GGUF schemes, their f16 variant (weights d*q + m rounded once to f16 in
 LDS, activations scaled by a power of two into f16, f16 MFMA); fp32
-accumulation throughout.  Bar: max|got - want| / max|want| <= 2e-2 with bf16 output (the
-prefill contract), 1e-3 for the f16 kernel with f32 output; `want` is the
+accumulation throughout.  Bar: max|got - want| / max|want| <= 8e-3 with bf16 output
+(tighter than the 2e-2 prefill contract: bf16 weights and the bf16 output
+rounding account for about 4e-3), 1e-3 for the f16 kernel with f32 output; `want` is the
 oracle's dequantized weights contracted in float64 with the bf16 activations
 the kernel saw."""
 import numpy as np
@@ -14,7 +15,7 @@ from test_gemv_gpu import _t, rel_err
 
 pytestmark = pytest.mark.gpu
 
-TOL_PREFILL = 2e-2
+TOL_PREFILL = 8e-3
 
 
 def run_gemm(ctx, orc, scheme, x32, packed, n, ydt="bf16", **kw):
@@ -242,3 +243,34 @@ def test_gemm_default_split_on_small_grids(ctx, orc, mkn):
     w = orc.dequantize(3, packed, k).astype(np.float32)
     want = (xv @ w.T).astype(np.float64)
     assert rel_err(got, want) <= TOL_PREFILL
+
+
+@pytest.mark.parametrize("m,k,n", [(2048, 4096, 24576), (4096, 4096, 24576), (2048, 12288, 4096),
+                                   (4096, 12288, 4096)], ids=str)
+@pytest.mark.parametrize("ydt", ["bf16", "f32"])
+def test_gemm_config4_full_size_sampled(ctx, orc, m, k, n, ydt):
+    """The bench's prefill cells at full size (Q4_1, Qwen3-8B gate|up and
+    down, M = 2048 and 4096; 12288->4096 at M=4096 is the unsplit path), with
+    the output dtype the bench reports (bf16) and the f32-output f16 kernel:
+    48 rows x 384 columns of the output against the float64 oracle."""
+    import torch
+    import rlxq
+    from bench import synth_q4_1_gpu
+
+    announce(f"gemm config4 full size m={m} k={k} n={n} y={ydt}")
+    g = torch.Generator(device="cuda").manual_seed(m + k + n)
+    w = synth_q4_1_gpu(n, k, g)
+    x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+    y = ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_1, n, y_dtype=torch.bfloat16 if ydt == "bf16" else torch.float32)
+    kern = ctx.last_kernel
+    torch.cuda.synchronize()
+    assert kern.startswith("rlxq_gemm_q4_1_t256"), kern
+    rs = np.random.default_rng(m + n)
+    rows = np.sort(rs.choice(m, 48, replace=False))
+    cols = np.sort(rs.choice(n, 384, replace=False))
+    wsub = w.view(n, -1)[torch.from_numpy(cols).cuda()].cpu().numpy()
+    wd = orc.dequantize(3, wsub, k).astype(np.float64)
+    want = x[torch.from_numpy(rows).cuda()].float().cpu().numpy().astype(np.float64) @ wd.T
+    got = y.float().cpu().numpy()[np.ix_(rows, cols)]
+    # the sampled block's own max is the scale (a subset of the full output's)
+    assert rel_err(got, want) <= (TOL_PREFILL if ydt == "bf16" else 1e-3), kern

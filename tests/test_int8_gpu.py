@@ -133,13 +133,15 @@ def test_every_w8a8_tiling(ctx, orc, rng, cfg, monkeypatch):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-def test_w8a8_prefill_config_sampled(ctx, orc):
-    """The prefill W8A8 shape at full size (M=4096, 4096 -> 24576, Qwen3-8B
-    gate|up): the oracle checks a sample of 64 rows x 256 columns, plus the
-    activation quantiser on every row."""
+@pytest.mark.parametrize("k,n", [(4096, 24576), (12288, 4096)], ids=lambda s: str(s))
+def test_w8a8_prefill_config_sampled(ctx, orc, k, n):
+    """The prefill W8A8 shapes at full size (M=4096; Qwen3-8B gate|up
+    4096 -> 24576 and down 12288 -> 4096): the oracle checks a sample of 64
+    rows x 256 columns bit for bit, plus the activation quantiser on every
+    row."""
     import torch
 
-    m, k, n = 4096, 4096, 24576
+    m = 4096
     g = torch.Generator(device="cuda").manual_seed(0)
     announce(f"w8a8 prefill m={m} k={k} n={n}")
     x = torch.randn((m, k), device="cuda", generator=g, dtype=torch.float32).to(torch.bfloat16)
