@@ -96,7 +96,9 @@ typedef enum rlxq_status {
     RLXQ_E_IO = -11,      /* a checkpoint file cannot be opened or read     */
     RLXQ_E_FORMAT = -12,  /* a checkpoint file is not valid GGUF            */
     RLXQ_E_NOTFOUND = -13,/* no tensor or metadata key of that name         */
-    RLXQ_E_TAKEN = -14    /* the weight was already taken                   */
+    RLXQ_E_TAKEN = -14,   /* the weight was already taken                   */
+    RLXQ_E_SCRATCH = -15  /* call needs more scratch than the no-allocation
+                             entry point holds (RLXQ_NOALLOC_SCRATCH_BYTES)  */
 } rlxq_status;
 
 typedef struct rlxq_ctx rlxq_ctx;
@@ -143,6 +145,22 @@ int rlxq_dequant_matmul(rlxq_ctx* ctx, int scheme, int group_size,
                         const void* scales, const void* biases, int sb_dtype,
                         int64_t m, int64_t k, int64_t n, void* y, int y_dtype,
                         void* stream);
+
+/* The dense op for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Same arguments, kernels and results as
+ * rlxq_dequant_matmul, but it calls no hipMalloc / hipFree: the scratch that
+ * batched decode and split-K need is a static device array of
+ * RLXQ_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends.  A call
+ * that would need more returns RLXQ_E_SCRATCH before any launch.  Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, contexts or threads) race and must be serialised by the caller. */
+#define RLXQ_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int rlxq_dequant_matmul_noalloc(rlxq_ctx* ctx, int scheme, int group_size,
+                                const void* x, int x_dtype, const void* w,
+                                const void* scales, const void* biases,
+                                int sb_dtype, int64_t m, int64_t k, int64_t n,
+                                void* y, int y_dtype, void* stream);
 
 /* Grouped expert DequantMatMul: out[r, :] = x[r, :] . dequant(bank[e[r]])^T.
  * Replaces Op::DequantGroupedMatMul{scheme} (crates/rlx-qwen35/src/builder.rs:2955-2973;

@@ -89,11 +89,28 @@ def build_code_objects(cached: bool = False) -> None:
             f.result()
 
 
+def build_host_hip_objects() -> list[str]:
+    """Host translation units that also hold device data (noalloc.hip: the
+    static scratch array of the no-allocation entry point), compiled by hipcc
+    into position-independent objects for the g++ link."""
+    odir = LIB / "obj"
+    odir.mkdir(parents=True, exist_ok=True)
+    objs = []
+    for src in sorted(HDIR.glob("*.hip")):
+        obj = odir / f"{src.stem}.o"
+        cmd = [HIPCC, "-c", "-fPIC", "--offload-arch=gfx950", "-O2", "-std=c++17",
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               "-I", str(ROOT / "include"), "-I", str(HDIR), "-I", str(KDIR), str(src), "-o", str(obj)]
+        _run(cmd, f"hipcc -c {src.name}")
+        objs.append(str(obj))
+    return objs
+
+
 def build_host() -> Path:
     LIB.mkdir(parents=True, exist_ok=True)
     out = LIB / "librlxq.so"
     tmp = LIB / "librlxq.so.tmp"
-    srcs = sorted(str(p) for p in HDIR.glob("*.cpp"))
+    srcs = sorted(str(p) for p in HDIR.glob("*.cpp")) + build_host_hip_objects()
     cmd = [
         "g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-pthread",
         "-D__HIP_PLATFORM_AMD__", f"-DRLXQ_CO_DIR=\"{CO}\"",

@@ -67,7 +67,10 @@ int i8b_dispatch(rlxq_ctx* ctx, int group, const void* x, int x_dtype, const voi
   // RLXQ_I8B_GEMV=1; RLXQ_I8B_MFMA=1 forces the MFMA kernel); larger M: the
   // MFMA kernel, which reads each weight once for up to 16 rows.
   const char* force_mfma = std::getenv("RLXQ_I8B_MFMA");
-  const int64_t cap = (int64_t)256 << 20;  // partial sums kept under 256 MiB
+  // partial sums kept under 256 MiB (under the fixed scratch of the
+  // no-allocation entry point, less room for the zero-point row sums)
+  const int64_t cap = ctx->fixed_active ? std::min<int64_t>((int64_t)256 << 20, (int64_t)ctx->fixed_bytes / 2)
+                                        : (int64_t)256 << 20;
   const char* force_gemv = std::getenv("RLXQ_I8B_GEMV");
   const int64_t gemv_m = force_gemv && force_gemv[0] == '1' ? 4 : 1;
   const bool gemv = m <= gemv_m && !(force_mfma && force_mfma[0] == '1') && ((k + 1023) / 1024) * m * n * 4 <= cap;

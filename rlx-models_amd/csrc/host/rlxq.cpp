@@ -141,6 +141,14 @@ int launch(rlxq_ctx* ctx, hipFunction_t fn, dim3 grid, dim3 block, size_t lds, v
 }
 
 int workspace(rlxq_ctx* ctx, size_t bytes, void** out, void* stream) {
+  if (ctx->fixed_active) {
+    if (bytes > ctx->fixed_bytes)
+      return fail(ctx, RLXQ_E_SCRATCH,
+                  "this call needs " + std::to_string(bytes) + " B of scratch; the no-allocation entry point holds " +
+                      std::to_string(ctx->fixed_bytes) + " B");
+    *out = ctx->fixed_p;
+    return RLXQ_OK;
+  }
   rlxq_ctx::Scratch& w = ctx->ws[stream];
   if (bytes <= w.bytes) {
     *out = w.p;
@@ -203,6 +211,7 @@ const char* rlxq_strerror(int s) {
     case RLXQ_E_FORMAT: return "not a valid GGUF file";
     case RLXQ_E_NOTFOUND: return "no tensor or key of that name";
     case RLXQ_E_TAKEN: return "weight already taken";
+    case RLXQ_E_SCRATCH: return "call needs more scratch than the no-allocation entry point holds";
     default: return "unknown status";
   }
 }
@@ -237,6 +246,7 @@ int rlxq_init(int device, rlxq_ctx** out) {
   ctx->device = device;
   ctx->cu_count = prop.multiProcessorCount;
   ctx->max_lds = prop.sharedMemPerBlock;
+  noalloc_setup(ctx);
   for (const Image& im : kImages) {
     if (im.end - im.begin <= 1) continue;  // component not built into this library
     hipModule_t m = nullptr;

@@ -31,6 +31,14 @@ struct rlxq_ctx {
     std::vector<void*> retired;
   };
   std::unordered_map<void*, Scratch> ws;
+  // The no-allocation entry point's scratch: the device address of a static
+  // device array (RLXQ_NOALLOC_SCRATCH_BYTES), looked up at init.  While
+  // fixed_active, workspace() returns it instead of the per-stream buffers.
+  void* fixed_p = nullptr;
+  size_t fixed_bytes = 0;
+  bool fixed_active = false;
+  int fixed_status = RLXQ_E_HIP;
+  std::string fixed_msg = "not set up";
 };
 
 #include "skinny_args.h"
@@ -54,6 +62,9 @@ class DeviceGuard {
 
 // Looks a kernel up by name across the loaded code objects.
 int get_fn(rlxq_ctx* ctx, const std::string& name, hipFunction_t* out);
+
+// Looks up the no-allocation scratch of ctx->device (device current).
+void noalloc_setup(rlxq_ctx* ctx);
 
 // Workgroups of `threads` threads and `lds` bytes of LDS that one CU holds
 // at once (cached per kernel and LDS size; at least 1).

@@ -20,7 +20,8 @@ F32, BF16, U8 = 0, 1, 2
 MOE_EXPAND, MOE_COMBINE, MOE_EXPAND_SWIGLU = 0, 1, 2
 OK = 0
 E_NULL, E_SHAPE, E_SCHEME, E_ALIGN, E_DTYPE, E_HIP, E_NOMEM, E_INDEX, E_NOKERNEL, E_DEVICE = range(-1, -11, -1)
-E_IO, E_FORMAT, E_NOTFOUND, E_TAKEN = range(-11, -15, -1)
+E_IO, E_FORMAT, E_NOTFOUND, E_TAKEN, E_SCRATCH = range(-11, -16, -1)
+NOALLOC_SCRATCH_BYTES = 64 << 20   # RLXQ_NOALLOC_SCRATCH_BYTES
 
 _lib = None
 
@@ -58,6 +59,7 @@ def lib() -> C.CDLL:
         "rlxq_workspace_bytes": (I64, [P, P]),
         "rlxq_release_stream": (I, [P, P]),
         "rlxq_dequant_matmul": (I, [P, I, I, P, I, P, P, P, I, I64, I64, I64, P, I, P]),
+        "rlxq_dequant_matmul_noalloc": (I, [P, I, I, P, I, P, P, P, I, I64, I64, I64, P, I, P]),
         "rlxq_dequant_grouped_matmul": (I, [P, I, I, P, I, P, P, P, I, P, I64, I64, I64, I64, P, I, P]),
         "rlxq_moe_grouped": (I, [P, I, I, P, I, P, P, P, I64, I64, I64, I64, I64, P, I, P]),
         "rlxq_moe_route": (I, [P, P, I64, I64, I64, I, P, P, P]),
@@ -377,6 +379,18 @@ class Context:
         rc = lib().rlxq_dequant_matmul(self.h, scheme, group, _ptr(x), _dt(x), _ptr(w), _ptr(scales), _ptr(biases),
                                        sb, m, k, n, _ptr(y), _dt(y), _stream(stream))
         self._check(rc, "dequant_matmul")
+        return y
+
+    def dequant_matmul_noalloc(self, x, w, scheme: int, n: int, *, y, group: int = 32, scales=None, biases=None,
+                               stream=None):
+        """rlxq_dequant_matmul_noalloc into the caller's y: no device memory is
+        allocated (the scratch is the library's static per-GPU array)."""
+        check_dense(x, w, scheme, n, group=group, scales=scales, biases=biases, y=y, device=self.device)
+        m, k = x.shape
+        sb = _dt(scales) if scales is not None else F32
+        rc = lib().rlxq_dequant_matmul_noalloc(self.h, scheme, group, _ptr(x), _dt(x), _ptr(w), _ptr(scales),
+                                               _ptr(biases), sb, m, k, n, _ptr(y), _dt(y), _stream(stream))
+        self._check(rc, "dequant_matmul_noalloc")
         return y
 
     def dequantize(self, w, scheme: int, rows: int, k: int, *, group: int = 32, scales=None, biases=None,
