@@ -16,16 +16,19 @@ Extra keys of the same JSON line:
                   durations from HIP events on the launch stream around runs
                   of the step's launches of one shape, back to back
   per_shape       per-projection microseconds and GB/s (same runs)
-  prefill         config 4: Q4_1 dequant-GEMM, M in {512, 2048, 4096}, bf16
-                  in/out, TFLOP/s; and the W8A8 variant (per-row int8
-                  activations computed on the fly x per-channel int8 weights)
+  prefill         config 4 headline: Q4_1 dequant-GEMM TFLOP/s at M=4096 over
+                  gate|up + down (bf16 in/out), with prefill_roofline (MFMA)
+  prefill_detail  config 4: Q4_1 dequant-GEMM, M in {512, 2048, 4096}, Q4_K
+                  at M=4096, and the W8A8 variant (per-row int8 activations
+                  computed on the fly x per-channel int8 weights)
   batched_decode  config 3: Q4_1 and Q8_0, M in {1, 4, 16, 64}
   moe             config 5: routed-expert grouped GEMV, 16 tokens, top-8 of 128
   moe_q4_k        the same with Q4_K expert banks (a Q4_K_M MoE checkpoint)
   q8_gemv         config 1: Q8_0 2048->2048, f32 activations
   gguf_upload     a 537 MB GGUF checkpoint streamed from the page cache to HBM
   cpu_baseline    the C restatement of the reference CPU algorithm timed on
-                  this host's cores over a bounded sample
+                  this host's cores over bounded samples: config 2 on all
+                  threads (value) and one, config 1 on all threads and one
 Weights in the extra sections rotate over enough copies to exceed the MALL.
 """
 from __future__ import annotations
@@ -108,30 +111,82 @@ def _time_us(fn, reps: int, stream) -> float:
     return ev0.elapsed_time(ev1) * 1e3 / reps
 
 
-def cpu_baseline(seconds: float = 10.0) -> dict:
-    """The oracle's reference-order Q4_1 GEMV (C, OpenMP over output rows, like
-    gguf_matmul_bt_parallel) on this host, over the four Qwen3-8B shapes, for
-    a bounded time."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def _cpu_threads() -> int:
+    """Host threads this process may use: OMP_NUM_THREADS if set (the GPU
+    box sets it to its CPU share), else the affinity mask."""
+    try:
+        n = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        n = 0
+    return n if n > 0 else len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(seconds: float = 16.0) -> dict:
+    """The oracle's reference-order GEMV (C, flint-style 8-lane block dot,
+    OpenMP over output rows like gguf_matmul_bt_parallel) on this host's
+    cores, over bounded samples of the same workloads: config 2 (the four
+    Qwen3-8B Q4_1 shapes at M=1) with all threads and with one, and config 1
+    (Q8_0 2048 -> 2048, f32 x, the bench_matmul_rlx shape) with all threads and
+    with one.  `value` is config 2 on all threads."""
     import numpy as np
     from oracle import oracle as orc
 
     rng = np.random.default_rng(0)
-    threads = os.cpu_count() or 1
+    threads = _cpu_threads()
     ws = [(k, n, orc.synth_q4_1(rng, n, k)) for _, k, n in SHAPES]
     xs = {k: rng.standard_normal((1, k)).astype(np.float32) for k in (4096, 12288)}
-    done_bytes, reps = 0.0, 0
-    t0 = time.perf_counter()
-    while True:
-        for k, n, w in ws:
-            orc.matmul_refl(orc.Q4_1, xs[k], w, n, threads=threads)
-            done_bytes += gemv_bytes(k, n, xsize=4)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": round(done_bytes / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} layer(s) of the 4 Qwen3-8B Q4_1 GEMVs at M=1 (f32 x), "
-                      f"{el:.1f} s, reference-order C restatement (OpenMP)"}
+    w1 = orc.synth_q8_0(rng, 2048, 2048)
+    x1 = rng.standard_normal((1, 2048)).astype(np.float32)
+
+    def run_layers(nthreads: int, budget: float):
+        done_bytes, reps = 0.0, 0
+        t0 = time.perf_counter()
+        while True:
+            for k, n, w in ws:
+                orc.matmul_refl(orc.Q4_1, xs[k], w, n, threads=nthreads)
+                done_bytes += gemv_bytes(k, n, xsize=4)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return done_bytes / el / 1e9, reps, el
+
+    def run_q8(nthreads: int, budget: float):
+        calls = 0
+        t0 = time.perf_counter()
+        while True:
+            orc.matmul_refl(orc.Q8_0, x1, w1, 2048, threads=nthreads)
+            calls += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                us = el / calls * 1e6
+                return {"us_per_call": round(us, 2), "GBps": round(gemv_bytes(2048, 2048, bpw=Q8_0_BPW, xsize=4) /
+                                                                   us / 1e3, 3), "calls": calls}
+
+    share = seconds / 8.0
+    v_all, reps_all, el_all = run_layers(threads, 3 * share)
+    v_one, reps_one, el_one = run_layers(1, 3 * share)
+    return {"value": round(v_all, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(),
+            "sample": f"{reps_all} layer(s) of the 4 Qwen3-8B Q4_1 GEMVs at M=1 (f32 x) in {el_all:.1f} s on "
+                      f"{threads} threads; reference-order C restatement of the reference CPU path (flint block "
+                      f"dot, OpenMP over output rows), not the Rust binary",
+            "one_core": {"value": round(v_one, 3), "unit": "GB/s", "cores": 1,
+                         "sample": f"{reps_one} layer(s) in {el_one:.1f} s"},
+            "config1_q8_0_2048": {"all_cores": run_q8(threads, share), "one_core": run_q8(1, share),
+                                  "workload": "Q8_0 GEMV 2048->2048, f32 x [1, 2048] (bench_matmul_rlx shape)"}}
 
 
 # ---------------------------------------------------------------- sections
@@ -256,6 +311,23 @@ def prefill_section(ctx, gen, sptr, stream, quick: bool) -> dict:
         del wq, sw, x, y
         torch.cuda.empty_cache()
     return res
+
+
+def prefill_headline(detail: dict) -> dict:
+    """The metric's second half as flat scalars: Q4_1 dequant-GEMM TFLOP/s at
+    M=4096 over one layer's gate|up and down (total flops / total time), with
+    the per-shape figures."""
+    q = detail["q4_1"]
+    gu, dn = q["gate_up_m4096"], q["down_m4096"]
+    flops = 2.0 * 4096 * (gu["n"] * gu["k"] + dn["n"] * dn["k"])
+    tf = flops / (gu["us"] + dn["us"]) / 1e6
+    return {"TFLOPs": round(tf, 1), "unit": "TFLOP/s", "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+            "workload": "Q4_1 group-32 dequant-GEMM, bf16 x and y, f32 accumulate, M=4096: Qwen3-8B gate_up "
+                        "4096->24576 + down 12288->4096",
+            "kernel": gu["kernel"], "gate_up_m4096_TFLOPs": gu["TFLOPs"], "down_m4096_TFLOPs": dn["TFLOPs"],
+            "gate_up_m4096_us": gu["us"], "down_m4096_us": dn["us"],
+            "w8a8_gate_up_m4096_TOPs": detail["w8a8"]["gate_up_m4096"]["TOPs"],
+            "w8a8_down_m4096_TOPs": detail["w8a8"]["down_m4096"]["TOPs"]}
 
 
 def batched_section(ctx, gen, sptr, stream) -> dict:
@@ -552,7 +624,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="only the decode step and its roofline")
     ap.add_argument("--quick", action="store_true", help="prefill at M=4096 only")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=16.0)
+    ap.add_argument("--section", choices=["prefill", "batched", "moe", "moe_q4_k", "schemes", "q8", "gguf"],
+                    help="profiling mode: run only this section (no decode step, no CPU baseline) and print its "
+                         "figures as one JSON object")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy 3 times (the reference for FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
@@ -578,6 +653,18 @@ def main() -> int:
     sptr = stream.cuda_stream
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0)
+
+    if a.section:
+        run = {"prefill": lambda: prefill_section(ctx, gen, sptr, stream, a.quick),
+               "batched": lambda: batched_section(ctx, gen, sptr, stream),
+               "moe": lambda: moe_section(ctx, gen, sptr, stream),
+               "moe_q4_k": lambda: moe_section(ctx, gen, sptr, stream, "q4_k"),
+               "schemes": lambda: schemes_section(ctx, gen, sptr, stream),
+               "q8": lambda: q8_section(ctx, gen, sptr, stream),
+               "gguf": lambda: gguf_section(ctx, gen, sptr, stream)}[a.section]
+        print(json.dumps({"section": a.section, "result": run()}), flush=True)
+        ctx.close()
+        return 0
 
     # ---- resident inputs: 36 layers of weights, activations, outputs -------
     layers = [{name: synth_q4_1_gpu(n, k, gen) for name, k, n in SHAPES} for _ in range(LAYERS)]
@@ -635,7 +722,13 @@ def main() -> int:
         "roofline": roofline,
     }
     if not a.no_extra:
-        out["prefill"] = prefill_section(ctx, gen, sptr, stream, a.quick)
+        detail = prefill_section(ctx, gen, sptr, stream, a.quick)
+        out["prefill"] = prefill_headline(detail)
+        out["prefill_roofline"] = {"bound": "mfma", "kernel": out["prefill"]["kernel"],
+                                   "achieved": out["prefill"]["TFLOPs"], "peak": BF16_PEAK_TFLOPS,
+                                   "unit": "TFLOP/s", "frac": out["prefill"]["frac_bf16_peak"],
+                                   "traffic": None}
+        out["prefill_detail"] = detail
         out["batched_decode"] = batched_section(ctx, gen, sptr, stream)
         out["moe"] = moe_section(ctx, gen, sptr, stream)
         out["moe_q4_k"] = moe_section(ctx, gen, sptr, stream, "q4_k")

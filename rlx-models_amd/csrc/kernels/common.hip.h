@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 #define RLXQ_DEV __device__ __forceinline__
 
 // A large kernel file is compiled as several code objects, each holding the
@@ -17,6 +19,18 @@
 
 typedef __bf16 rlxq_bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 rlxq_f16x2_t __attribute__((ext_vector_type(2)));
+
+namespace rlxq {
+// f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N - 1>{})
+template <class F, int... I>
+RLXQ_DEV void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+RLXQ_DEV void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+}  // namespace rlxq
 
 // Scheme ids (same numbering as include/rlxq.h).
 enum : int {

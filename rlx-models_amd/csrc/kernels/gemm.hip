@@ -317,23 +317,26 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
 #pragma unroll
   for (int ks = 0; ks < GBK / 16; ks++) compute_ks((KT - 1) & 1, ks);
 
-  // epilogue: C[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2), reg 4*(i/8) + i%4
-#pragma unroll
-  for (int i = 0; i < TM; i++)
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
-      const int64_t n = n0 + wn * WN + j * 32 + (lane & 31);
+  // epilogue: C[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2), reg
+  // 4*(i/8) + i%4.  The tiles are walked with compile-time indices: a runtime
+  // loop over them would index the accumulators dynamically and move them to
+  // scratch memory.
+  static_for<TM>([&](auto I) {
+    static_for<TN>([&](auto J) {
+      const int64_t n = n0 + wn * WN + J.value * 32 + (lane & 31);
+      const f32x16_t v = acc[I.value][J.value];
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int64_t m = m0 + wm * WM + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+        const int64_t m = m0 + wm * WM + I.value * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
         if (m < a.M && n < a.N) {
-          const float v = F16 ? acc[i][j][r] * a.inv_s[m] : acc[i][j][r];
-          if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
-          else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
-          else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+          const float o = F16 ? v[r] * a.inv_s[m] : v[r];
+          if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = o;
+          else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(o);
+          else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = o;
         }
       }
-    }
+    });
+  });
 }
 
 }  // namespace rlxq

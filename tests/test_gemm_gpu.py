@@ -274,3 +274,4 @@ def test_gemm_config4_full_size_sampled(ctx, orc, m, k, n, ydt):
     got = y.float().cpu().numpy()[np.ix_(rows, cols)]
     # the sampled block's own max is the scale (a subset of the full output's)
     assert rel_err(got, want) <= (TOL_PREFILL if ydt == "bf16" else 1e-3), kern
+
