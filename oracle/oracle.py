@@ -10,12 +10,13 @@ reference file:line each routine restates.  Arrays are numpy, C-contiguous.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIBPATH = HERE / "liboracle.so"
+LIBPATH = Path(os.environ.get("RLXQ_ORACLE_LIB", HERE / "liboracle.so"))
 
 Q8_0, Q4_0, Q4_1, MLX4, MLX8, INT8_BLOCK, Q4_K, Q6_K = 1, 2, 3, 4, 5, 6, 7, 8
 BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20, Q4_K: 144, Q6_K: 210}

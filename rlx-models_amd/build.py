@@ -106,13 +106,22 @@ def build_host_hip_objects() -> list[str]:
     return objs
 
 
-def build_host() -> Path:
-    LIB.mkdir(parents=True, exist_ok=True)
-    out = LIB / "librlxq.so"
-    tmp = LIB / "librlxq.so.tmp"
+# CPU sanitizer build of the host code (tests/sanitize_run.py): AddressSanitizer
+# and UndefinedBehaviorSanitizer on the g++ translation units only (the
+# code objects are embedded unchanged).
+SANITIZE_FLAGS = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-fno-sanitize-recover=undefined",
+                  "-g", "-O1"]
+SANDIR = LIB / "sanitize"
+
+
+def build_host(sanitize: bool = False) -> Path:
+    outdir = SANDIR if sanitize else LIB
+    outdir.mkdir(parents=True, exist_ok=True)
+    out = outdir / "librlxq.so"
+    tmp = outdir / "librlxq.so.tmp"
     srcs = sorted(str(p) for p in HDIR.glob("*.cpp")) + build_host_hip_objects()
     cmd = [
-        "g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-pthread",
+        "g++", "-std=c++17", *(SANITIZE_FLAGS if sanitize else ["-O2"]), "-fPIC", "-shared", "-pthread",
         "-D__HIP_PLATFORM_AMD__", f"-DRLXQ_CO_DIR=\"{CO}\"",
         "-I", str(ROOT / "include"), "-I", str(HDIR), "-I", str(KDIR), "-I", str(ROCM / "include"),
         *srcs, "-o", str(tmp),
@@ -138,15 +147,17 @@ def build_examples() -> list[Path]:
     return outs
 
 
-def build_oracle() -> Path:
+def build_oracle(sanitize: bool = False) -> Path:
     odir = ROOT / "oracle"
-    out = odir / "liboracle.so"
-    tmp = odir / "liboracle.so.tmp"
+    outdir = SANDIR if sanitize else odir
+    outdir.mkdir(parents=True, exist_ok=True)
+    out = outdir / "liboracle.so"
+    tmp = outdir / "liboracle.so.tmp"
     # -ffp-contract=off keeps every multiply-add rounded where the restated
     # reference rounds; x86-64-v3 (AVX2 + FMA) so fmaf() is one instruction on
     # any host the GPU box may have.
-    cmd = ["gcc", "-std=c11", "-O3", "-march=x86-64-v3", "-ffp-contract=off", "-fopenmp",
-           "-fPIC", "-shared", str(odir / "rlxq_oracle.c"), "-o", str(tmp), "-lm"]
+    cmd = ["gcc", "-std=c11", *(SANITIZE_FLAGS if sanitize else ["-O3"]), "-march=x86-64-v3", "-ffp-contract=off",
+           "-fopenmp", "-fPIC", "-shared", str(odir / "rlxq_oracle.c"), "-o", str(tmp), "-lm"]
     _run(cmd, "gcc liboracle")
     os.replace(tmp, out)
     return out
@@ -157,9 +168,16 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--no-oracle", action="store_true")
     ap.add_argument("--host-only", action="store_true", help="relink librlxq.so from existing code objects")
     ap.add_argument("--cached", action="store_true", help="keep code objects whose inputs are unchanged (development)")
+    ap.add_argument("--sanitize", action="store_true",
+                    help="only the CPU sanitizer build of librlxq and the oracle, into lib/sanitize/ "
+                         "(needs the code objects of a normal build)")
     a = ap.parse_args(argv)
     if shutil.which("g++") is None or not Path(HIPCC).exists():
         raise RuntimeError("need g++ and hipcc")
+    if a.sanitize:
+        build_host(sanitize=True)
+        build_oracle(sanitize=True)
+        return 0
     if not a.host_only:
         build_code_objects(cached=a.cached)
     build_host()

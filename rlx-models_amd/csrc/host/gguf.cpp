@@ -259,7 +259,13 @@ int parse(rlxq_gguf* g) {
     if (big || elems >= (uint64_t(1) << 62)) return g->fail(RLXQ_E_FORMAT, "gguf: tensor " + t.name + " is too large");
     t.type = (int32_t)ty;
     if (const TypeLayout* l = layout_of(t.type)) {
-      if (t.dims[0] % l->block == 0) t.nbytes = (int64_t)(elems / l->block * l->bytes);
+      // (blocks x bytes per block, checked: 8-byte types could wrap)
+      uint64_t nb = 0;
+      if (t.dims[0] % l->block == 0 &&
+          !__builtin_mul_overflow(elems / l->block, (uint64_t)l->bytes, &nb) && nb < (uint64_t(1) << 62))
+        t.nbytes = (int64_t)nb;
+      else if (t.dims[0] % l->block == 0)
+        return g->fail(RLXQ_E_FORMAT, "gguf: tensor " + t.name + " is too large");
     }
     if (!g->tensor_idx.emplace(t.name, i).second) return g->fail(RLXQ_E_FORMAT, "gguf: duplicate tensor " + t.name);
   }

@@ -1,0 +1,95 @@
+"""Bounded corruption loop over the reference's GGUF header fixture
+(tests/golden/bonsai2_manifest.gguf): every truncation at a spread of
+lengths and random single-byte flips, each opened and walked through the
+reader's whole API (tensor infos, take_packed, metadata values).  A corrupt
+file must give an error status, never a crash.  Run by
+tests/sanitize_run.py under AddressSanitizer and UBSan; also runnable alone:
+
+    python tests/gguf_fuzz.py [--flips N] [--cuts N]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import os
+import sys
+import tempfile
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(ROOT / "rlx-models_amd"))
+FIXTURE = ROOT / "tests" / "golden" / "bonsai2_manifest.gguf"
+
+
+def walk(path: str) -> str:
+    """Opens `path` and reads everything the API exposes; returns 'ok' or the
+    error status of the first failure."""
+    import rlxq
+
+    L = rlxq.lib()
+    h = C.c_void_p()
+    rc = L.rlxq_gguf_open(path.encode(), C.byref(h))
+    try:
+        if rc != 0:
+            L.rlxq_gguf_last_error(h)
+            return f"open:{rc}"
+        L.rlxq_gguf_version(h)
+        L.rlxq_gguf_data_offset(h)
+        for i in range(int(L.rlxq_gguf_tensor_count(h))):
+            ti = rlxq.GgufTensorInfo()
+            if L.rlxq_gguf_tensor_info(h, i, C.byref(ti)) != 0:
+                continue
+            sch, nd, nb = C.c_int(), C.c_int(), C.c_int64()
+            shape = (C.c_int64 * 4)()
+            L.rlxq_gguf_take_packed(h, ti.name, C.byref(sch), shape, C.byref(nd), C.byref(nb))
+            L.rlxq_gguf_find_tensor(h, ti.name)
+            if 0 <= ti.nbytes <= 1 << 16:
+                buf = (C.c_uint8 * max(int(ti.nbytes), 1))()
+                L.rlxq_gguf_read(h, ti.name, buf, ti.nbytes)
+        for i in range(int(L.rlxq_gguf_meta_count(h))):
+            ty, el, cnt = C.c_int(), C.c_int(), C.c_uint64()
+            if L.rlxq_gguf_meta_type(h, i, C.byref(ty), C.byref(el), C.byref(cnt)) != 0:
+                continue
+            L.rlxq_gguf_meta_key(h, i)
+            for j in list(range(min(cnt.value, 4))) + [cnt.value]:   # the last probe is out of range
+                v, f = C.c_int64(), C.c_double()
+                s, n = C.c_char_p(), C.c_uint64()
+                L.rlxq_gguf_meta_int(h, i, j, C.byref(v))
+                L.rlxq_gguf_meta_float(h, i, j, C.byref(f))
+                L.rlxq_gguf_meta_str(h, i, j, C.byref(s), C.byref(n))
+        return "ok"
+    finally:
+        L.rlxq_gguf_close(h)
+
+
+def main(argv=None) -> int:
+    import numpy as np
+
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--flips", type=int, default=300)
+    ap.add_argument("--cuts", type=int, default=300)
+    a = ap.parse_args(argv)
+    data = FIXTURE.read_bytes()
+    rng = np.random.default_rng(0)
+    outcomes: dict[str, int] = {}
+    with tempfile.TemporaryDirectory() as d:
+        p = os.path.join(d, "f.gguf")
+        cuts = sorted(set(np.linspace(0, len(data), a.cuts, dtype=np.int64).tolist()) | set(range(0, 64)))
+        for n in cuts:
+            Path(p).write_bytes(data[:n])
+            r = walk(p)
+            outcomes[r] = outcomes.get(r, 0) + 1
+        for _ in range(a.flips):
+            b = bytearray(data)
+            pos = int(rng.integers(0, min(len(b), 1 << 20)))
+            b[pos] ^= int(rng.integers(1, 256))
+            Path(p).write_bytes(bytes(b))
+            r = walk(p)
+            outcomes[r] = outcomes.get(r, 0) + 1
+    assert walk(str(FIXTURE)) == "ok"
+    print(f"gguf fuzz: {len(cuts)} truncations + {a.flips} byte flips of {FIXTURE.name}; outcomes {outcomes}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -292,6 +292,11 @@ def test_open_errors(tmp_path):
         if data is not None:
             p.write_bytes(data)
         _expect_open_error(p, *want[name])
+    # an 8-byte element type whose byte size wraps 64 bits: elements below
+    # 2^62, elements x 8 past 2^64 (it would wrap to 8 bytes)
+    p = tmp_path / "wrap.gguf"
+    p.write_bytes(gguf_bytes([], [("w", 28, [(1 << 61) + 1], b"\0" * 8)])[0])
+    _expect_open_error(p, rlxq.E_FORMAT, "too large")
     # a huge count is rejected before anything is allocated for it
     bad = bytearray(good)
     bad[8:16] = (1 << 60).to_bytes(8, "little")
