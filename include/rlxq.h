@@ -347,6 +347,75 @@ int rlxq_gguf_meta_float(const rlxq_gguf* g, int64_t i, uint64_t j, double* v);
 int rlxq_gguf_meta_str(const rlxq_gguf* g, int64_t i, uint64_t j,
                        const char** s, uint64_t* len);
 
+/* ---- MLX checkpoints (mlx-community safetensors) --------------------------
+ * Replaces the reference's MlxLoader and its take_packed_mlx
+ * (crates/rlx-models-core/src/weight_loader.rs:906-1012, consumed by
+ * load_proj, crates/rlx-models-core/src/standard_decoder.rs:590-645; reader
+ * crate rlx-mlx-io, absent).  rlxq_mlx_open takes a checkpoint directory
+ * (config.json with its "quantization" block, and model.safetensors.index.json
+ * shards or every *.safetensors file) or one .safetensors file (config.json
+ * from its directory when present).  Host code only, except rlxq_mlx_upload. */
+typedef struct rlxq_mlx rlxq_mlx;
+typedef enum rlxq_st_dtype {   /* safetensors element types */
+    RLXQ_ST_BOOL = 1, RLXQ_ST_U8, RLXQ_ST_I8, RLXQ_ST_U16, RLXQ_ST_I16,
+    RLXQ_ST_F16, RLXQ_ST_BF16, RLXQ_ST_U32, RLXQ_ST_I32, RLXQ_ST_F32,
+    RLXQ_ST_U64, RLXQ_ST_I64, RLXQ_ST_F64, RLXQ_ST_F8_E4M3, RLXQ_ST_F8_E5M2
+} rlxq_st_dtype;
+typedef enum rlxq_mlx_mode {
+    RLXQ_MLX_MODE_NONE = 0, RLXQ_MLX_MODE_AFFINE = 1, RLXQ_MLX_MODE_MXFP4 = 2
+} rlxq_mlx_mode;
+typedef struct rlxq_mlx_tensor {
+    const char* name;       /* valid until rlxq_mlx_close                      */
+    int32_t dtype;          /* rlxq_st_dtype                                   */
+    int32_t n_dims;         /* 0..8                                            */
+    int64_t shape[8];       /* outermost first (unused dims = 1)               */
+    int64_t nbytes;
+    const char* file;       /* the safetensors file holding it                 */
+    uint64_t offset;        /* absolute file offset of its bytes               */
+} rlxq_mlx_tensor;
+/* A quantized Linear as the kernels read it (the reference's
+ * MlxPackedLinear): codes [out, in * bits / 32] u32 LSB first, scales and
+ * biases [out, in / group_size] of slab_dtype (BF16, F16 or F32; MXFP4: U8
+ * E8M0 scales, no biases).  Tensor names point into the handle. */
+typedef struct rlxq_mlx_packed {
+    int32_t scheme;         /* RLXQ_MLX_AFFINE4 / 8, RLXQ_MLX_MXFP4; 0 = not packed */
+    int32_t bits, group_size;
+    int64_t out_features, in_features;
+    const char* codes;
+    const char* scales;
+    const char* biases;     /* NULL for MXFP4                                  */
+    int64_t codes_nbytes, scales_nbytes, biases_nbytes;
+    int32_t slab_dtype;     /* rlxq_st_dtype of scales (and biases)            */
+} rlxq_mlx_packed;
+/* *out is set even when the return is an error (for rlxq_mlx_last_error). */
+int rlxq_mlx_open(const char* path, rlxq_mlx** out);
+void rlxq_mlx_close(rlxq_mlx* h);
+const char* rlxq_mlx_last_error(const rlxq_mlx* h);
+/* The checkpoint-wide quantization block (bits = group_size = 0 and
+ * RLXQ_MLX_MODE_NONE when there is none). */
+int rlxq_mlx_quantization(const rlxq_mlx* h, int* bits, int* group_size,
+                          int* mode);
+int64_t rlxq_mlx_tensor_count(const rlxq_mlx* h);
+int64_t rlxq_mlx_find_tensor(const rlxq_mlx* h, const char* name);
+int rlxq_mlx_tensor_info(const rlxq_mlx* h, int64_t i, rlxq_mlx_tensor* info);
+/* take_packed_mlx(key): the Linear `key` (tensors key.weight, key.scales,
+ * key.biases) under the quantization that applies to it (a per-layer entry
+ * of the block, else the block itself).  A Linear stored dense, switched off
+ * by a `false` entry, or packed in a form these kernels do not read (bits
+ * other than 4 and 8, group sizes other than 32/64/128, MXFP4 other than
+ * 4-bit group 32) gives scheme 0 and RLXQ_OK and is not taken (the
+ * reference's Ok(None)); a second take is RLXQ_E_TAKEN. */
+int rlxq_mlx_take_packed(rlxq_mlx* h, const char* key, rlxq_mlx_packed* out);
+/* A tensor's bytes as stored, into host memory of cap bytes (pread). */
+int rlxq_mlx_read(rlxq_mlx* h, const char* name, void* dst, size_t cap);
+/* An F32 / F16 / BF16 tensor as f32, into count floats (F16 scale slabs:
+ * the kernels take F32 or BF16 slabs). */
+int rlxq_mlx_read_f32(rlxq_mlx* h, const char* name, float* dst, size_t count);
+/* A tensor's bytes as stored, into device memory of cap bytes (pread into two
+ * 32 MiB pinned staging buffers copied on `stream`, as rlxq_gguf_upload). */
+int rlxq_mlx_upload(rlxq_mlx* h, const char* name, void* dst, size_t cap,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

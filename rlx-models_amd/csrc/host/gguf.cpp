@@ -37,9 +37,12 @@
 #include <unordered_map>
 #include <vector>
 
+#include "file_io.hpp"
 #include "rlxq.h"
 
 namespace {
+
+using rlxq::pread_all;
 
 enum : uint32_t {
   GT_U8 = 0, GT_I8 = 1, GT_U16 = 2, GT_I16 = 3, GT_U32 = 4, GT_I32 = 5, GT_F32 = 6, GT_BOOL = 7,
@@ -123,7 +126,6 @@ struct Tensor {
   bool taken = false;
 };
 
-constexpr size_t kStageBytes = size_t(32) << 20;   // per staging buffer
 
 }  // namespace
 
@@ -138,9 +140,7 @@ struct rlxq_gguf {
   std::vector<Tensor> tensors;
   std::unordered_map<std::string, size_t> tensor_idx;
   std::string err;
-  void* stage[2] = {nullptr, nullptr};
-  hipEvent_t ev[2] = {nullptr, nullptr};
-  bool ev_live[2] = {false, false};
+  rlxq::StagedUpload up;
 
   int fail(int code, const std::string& msg) {
     err = msg;
@@ -302,45 +302,6 @@ int data_range(rlxq_gguf* g, const Tensor& t, uint64_t* off, uint64_t* len) {
   return RLXQ_OK;
 }
 
-bool pread_all(int fd, void* dst, uint64_t n, uint64_t off) {
-  uint8_t* d = static_cast<uint8_t*>(dst);
-  while (n) {
-    const size_t want = (size_t)std::min<uint64_t>(n, uint64_t(1) << 30);
-    const ssize_t r = pread(fd, d, want, (off_t)off);
-    if (r < 0 && errno == EINTR) continue;
-    if (r <= 0) return false;
-    d += r;
-    off += (uint64_t)r;
-    n -= (uint64_t)r;
-  }
-  return true;
-}
-
-// pread_all split over up to 8 threads in parts of at least 4 MiB: one
-// thread copying out of the page cache is slower than the copy to the device.
-bool pread_par(int fd, uint8_t* dst, uint64_t n, uint64_t off) {
-  constexpr uint64_t kPart = uint64_t(4) << 20;
-  const int parts = (int)std::min<uint64_t>(8, (n + kPart - 1) / kPart);
-  if (parts <= 1) return pread_all(fd, dst, n, off);
-  const uint64_t step = (n + parts - 1) / parts;
-  std::atomic<bool> ok{true};
-  std::vector<std::thread> th;
-  uint64_t lo = step;   // part 0 runs on this thread
-  try {
-    for (; lo < n; lo += step) {
-      const uint64_t len = std::min(step, n - lo);
-      th.emplace_back([&ok, fd, dst, off, lo, len] {
-        if (!pread_all(fd, dst + lo, len, off + lo)) ok = false;
-      });
-    }
-  } catch (...) {   // no thread: read the remaining parts here
-    if (!pread_all(fd, dst + lo, n - lo, off + lo)) ok = false;
-  }
-  if (!pread_all(fd, dst, std::min(step, n), off)) ok = false;
-  for (auto& t : th) t.join();
-  return ok;
-}
-
 const Meta* meta_at(const rlxq_gguf* g, int64_t i) {
   return (g && i >= 0 && (uint64_t)i < g->meta.size()) ? &g->meta[(size_t)i] : nullptr;
 }
@@ -397,15 +358,8 @@ int rlxq_gguf_open(const char* path, rlxq_gguf** out) {
 
 void rlxq_gguf_close(rlxq_gguf* g) {
   if (!g) return;
-  for (int b = 0; b < 2; b++) {
-    if (g->ev[b]) {
-      if (g->ev_live[b]) (void)hipEventSynchronize(g->ev[b]);
-      (void)hipEventDestroy(g->ev[b]);
-    }
-    if (g->stage[b]) (void)hipHostFree(g->stage[b]);
-  }
   if (g->fd >= 0) close(g->fd);
-  delete g;
+  delete g;   // (the staging buffers wait for their last copies)
 }
 
 const char* rlxq_gguf_last_error(const rlxq_gguf* g) { return g ? g->err.c_str() : ""; }
@@ -480,32 +434,9 @@ int rlxq_gguf_upload(rlxq_gguf* g, const char* name, void* dst, size_t cap, void
   uint64_t off, len;
   if ((rc = data_range(g, *t, &off, &len))) return rc;
   if (len > cap) return g->fail(RLXQ_E_SHAPE, std::string("gguf: ") + name + " needs " + std::to_string(len) + " bytes");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  for (int b = 0; b < 2; b++) {
-    if (!g->stage[b] && hipHostMalloc(&g->stage[b], kStageBytes, hipHostMallocDefault) != hipSuccess) {
-      g->stage[b] = nullptr;
-      return g->fail(RLXQ_E_NOMEM, "gguf: pinned staging allocation failed");
-    }
-    if (!g->ev[b] && hipEventCreateWithFlags(&g->ev[b], hipEventDisableTiming) != hipSuccess) {
-      g->ev[b] = nullptr;
-      return g->fail(RLXQ_E_HIP, "gguf: event creation failed");
-    }
-  }
-  uint8_t* d = static_cast<uint8_t*>(dst);
-  int b = 0;
-  for (uint64_t done = 0; done < len; done += kStageBytes, b ^= 1) {
-    const uint64_t n = std::min<uint64_t>(kStageBytes, len - done);
-    // the copy that last read this buffer must be finished before refilling it
-    if (g->ev_live[b] && hipEventSynchronize(g->ev[b]) != hipSuccess)
-      return g->fail(RLXQ_E_HIP, "gguf: waiting for a staging copy failed");
-    g->ev_live[b] = false;
-    if (!pread_par(g->fd, static_cast<uint8_t*>(g->stage[b]), n, off + done))
-      return g->fail(RLXQ_E_IO, std::string("gguf: read failed for ") + name);
-    if (hipMemcpyAsync(d + done, g->stage[b], n, hipMemcpyHostToDevice, s) != hipSuccess ||
-        hipEventRecord(g->ev[b], s) != hipSuccess)
-      return g->fail(RLXQ_E_HIP, std::string("gguf: copy to the device failed for ") + name);
-    g->ev_live[b] = true;
-  }
+  std::string why;
+  if ((rc = g->up.run(g->fd, off, len, dst, stream, &why)))
+    return g->fail(rc, std::string("gguf: ") + name + ": " + why);
   return RLXQ_OK;
 }
 

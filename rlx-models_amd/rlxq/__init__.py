@@ -32,6 +32,25 @@ class GgufTensorInfo(C.Structure):
                 ("dims", C.c_int64 * 4), ("offset", C.c_uint64), ("nbytes", C.c_int64), ("scheme", C.c_int32)]
 
 
+class MlxTensorInfo(C.Structure):
+    """rlxq_mlx_tensor."""
+    _fields_ = [("name", C.c_char_p), ("dtype", C.c_int32), ("n_dims", C.c_int32), ("shape", C.c_int64 * 8),
+                ("nbytes", C.c_int64), ("file", C.c_char_p), ("offset", C.c_uint64)]
+
+
+class MlxPacked(C.Structure):
+    """rlxq_mlx_packed."""
+    _fields_ = [("scheme", C.c_int32), ("bits", C.c_int32), ("group_size", C.c_int32),
+                ("out_features", C.c_int64), ("in_features", C.c_int64), ("codes", C.c_char_p),
+                ("scales", C.c_char_p), ("biases", C.c_char_p), ("codes_nbytes", C.c_int64),
+                ("scales_nbytes", C.c_int64), ("biases_nbytes", C.c_int64), ("slab_dtype", C.c_int32)]
+
+
+ST_DTYPES = {1: "BOOL", 2: "U8", 3: "I8", 4: "U16", 5: "I16", 6: "F16", 7: "BF16", 8: "U32", 9: "I32", 10: "F32",
+             11: "U64", 12: "I64", 13: "F64", 14: "F8_E4M3", 15: "F8_E5M2"}
+MLX_MODE_NONE, MLX_MODE_AFFINE, MLX_MODE_MXFP4 = 0, 1, 2
+
+
 class RlxqError(RuntimeError):
     def __init__(self, status: int, msg: str):
         super().__init__(f"rlxq status {status}: {msg}")
@@ -93,6 +112,17 @@ def lib() -> C.CDLL:
         "rlxq_gguf_meta_int": (I, [P, I64, C.c_uint64, C.POINTER(I64)]),
         "rlxq_gguf_meta_float": (I, [P, I64, C.c_uint64, C.POINTER(C.c_double)]),
         "rlxq_gguf_meta_str": (I, [P, I64, C.c_uint64, C.POINTER(C.c_char_p), C.POINTER(C.c_uint64)]),
+        "rlxq_mlx_open": (I, [C.c_char_p, C.POINTER(P)]),
+        "rlxq_mlx_close": (None, [P]),
+        "rlxq_mlx_last_error": (C.c_char_p, [P]),
+        "rlxq_mlx_quantization": (I, [P, C.POINTER(I), C.POINTER(I), C.POINTER(I)]),
+        "rlxq_mlx_tensor_count": (I64, [P]),
+        "rlxq_mlx_find_tensor": (I64, [P, C.c_char_p]),
+        "rlxq_mlx_tensor_info": (I, [P, I64, C.POINTER(MlxTensorInfo)]),
+        "rlxq_mlx_take_packed": (I, [P, C.c_char_p, C.POINTER(MlxPacked)]),
+        "rlxq_mlx_read": (I, [P, C.c_char_p, P, S]),
+        "rlxq_mlx_read_f32": (I, [P, C.c_char_p, P, S]),
+        "rlxq_mlx_upload": (I, [P, C.c_char_p, P, S, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -673,4 +703,79 @@ class GgufFile:
         """The tensor's bytes into the device tensor `dst` (pread + pinned staging)."""
         nbytes = dst.numel() * dst.element_size()
         self._check(lib().rlxq_gguf_upload(self.h, name.encode(), _ptr(dst), nbytes, _stream(stream)))
+        return dst
+
+
+class MlxFile:
+    """An MLX (mlx-community) checkpoint through rlxq_mlx_*: a directory or
+    one .safetensors file (MlxLoader and take_packed_mlx:
+    crates/rlx-models-core/src/weight_loader.rs:906-1012)."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        rc = lib().rlxq_mlx_open(str(path).encode(), C.byref(h))
+        if rc != OK:
+            msg = lib().rlxq_mlx_last_error(h).decode() if h else strerror(rc)
+            lib().rlxq_mlx_close(h)
+            raise RlxqError(rc, msg)
+        self.h = h
+        L = lib()
+        self.tensors = {}
+        for i in range(int(L.rlxq_mlx_tensor_count(h))):
+            ti = MlxTensorInfo()
+            self._check(L.rlxq_mlx_tensor_info(h, i, C.byref(ti)))
+            self.tensors[ti.name.decode()] = {"dtype": ST_DTYPES[ti.dtype],
+                                              "shape": [int(ti.shape[d]) for d in range(ti.n_dims)],
+                                              "nbytes": int(ti.nbytes), "file": ti.file.decode(),
+                                              "offset": int(ti.offset)}
+        b, g, m = C.c_int(), C.c_int(), C.c_int()
+        self._check(L.rlxq_mlx_quantization(h, C.byref(b), C.byref(g), C.byref(m)))
+        self.quantization = (b.value, g.value, m.value)
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().rlxq_mlx_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc: int) -> None:
+        if rc != OK:
+            raise RlxqError(rc, lib().rlxq_mlx_last_error(self.h).decode() or strerror(rc))
+
+    def take_packed(self, key: str):
+        """The packed Linear as a dict, or None when `key` is not packed in a
+        form the kernels read (not taken then); raises on a second take."""
+        p = MlxPacked()
+        self._check(lib().rlxq_mlx_take_packed(self.h, key.encode(), C.byref(p)))
+        if p.scheme == 0:
+            return None
+        return {"scheme": p.scheme, "bits": p.bits, "group_size": p.group_size, "n": p.out_features,
+                "k": p.in_features, "codes": p.codes.decode(), "scales": p.scales.decode(),
+                "biases": p.biases.decode() if p.biases else None, "codes_nbytes": p.codes_nbytes,
+                "scales_nbytes": p.scales_nbytes, "biases_nbytes": p.biases_nbytes,
+                "slab_dtype": ST_DTYPES[p.slab_dtype]}
+
+    def read(self, name: str):
+        import numpy as np
+
+        out = np.empty(self.tensors[name]["nbytes"], np.uint8)
+        self._check(lib().rlxq_mlx_read(self.h, name.encode(), out.ctypes.data, out.size))
+        return out
+
+    def read_f32(self, name: str):
+        import numpy as np
+
+        t = self.tensors[name]
+        out = np.empty(int(np.prod(t["shape"])) if t["shape"] else 1, np.float32)
+        self._check(lib().rlxq_mlx_read_f32(self.h, name.encode(), out.ctypes.data, out.size))
+        return out.reshape(t["shape"])
+
+    def upload(self, name: str, dst, *, stream=None):
+        nbytes = dst.numel() * dst.element_size()
+        self._check(lib().rlxq_mlx_upload(self.h, name.encode(), _ptr(dst), nbytes, _stream(stream)))
         return dst

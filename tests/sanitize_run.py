@@ -5,8 +5,8 @@ runs, with those libraries loaded through RLXQ_LIB / RLXQ_ORACLE_LIB and the
 ASan runtime preloaded into Python:
   * the CPU tests of the GGUF reader, the C ABI, the oracle, the golden
     fixtures and the binding's argument checks;
-  * tests/gguf_fuzz.py (truncations and byte flips of the reference's GGUF
-    fixture).
+  * tests/checkpoint_fuzz.py (truncations and byte flips of the reference's
+    GGUF and safetensors fixtures).
 No GPU is used.  Exit status 0 means every step passed with no sanitizer
 report (reports abort the process: halt_on_error).
 
@@ -43,8 +43,8 @@ def main() -> int:
     steps = [
         [sys.executable, "-m", "pytest", "-q", "-p", "no:cacheprovider", "-m", "not gpu",
          "tests/test_gguf.py", "tests/test_abi.py", "tests/test_oracle.py", "tests/test_golden.py",
-         "tests/test_wrapper_checks.py"],
-        [sys.executable, "tests/gguf_fuzz.py"],
+         "tests/test_wrapper_checks.py", "tests/test_mlx_loader.py"],
+        [sys.executable, "tests/checkpoint_fuzz.py"],
     ]
     for cmd in steps:
         print("[sanitize]", " ".join(cmd[1:]), flush=True)
