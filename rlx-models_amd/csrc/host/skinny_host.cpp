@@ -30,8 +30,9 @@ int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream) {
 }
 
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bool nibble, size_t extra,
-             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major) {
-  const size_t x16_bytes = round256((size_t)(m * k) * 2), s_bytes = round256((size_t)m * 4);
+             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major, int64_t mp) {
+  if (!frag_major || mp < m) mp = m;
+  const size_t x16_bytes = round256((size_t)(mp * k) * 2), s_bytes = round256((size_t)m * 4);
   void* ws = nullptr;
   int rc;
   if ((rc = workspace(ctx, x16_bytes + s_bytes + extra, &ws, stream))) return rc;
@@ -42,6 +43,7 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bo
   xa.inv_s = reinterpret_cast<float*>(wsb + x16_bytes);
   xa.M = m;
   xa.K = k;
+  xa.Mp = mp;
   xa.x_bf16 = x_dtype == RLXQ_BF16;
   xa.nibble_order = nibble;
   xa.frag_major = frag_major ? 1 : 0;
@@ -49,7 +51,7 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bo
   hipFunction_t fn;
   if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
   void* xargs[] = {&xa};
-  return launch(ctx, fn, dim3((unsigned)m), dim3(256), 0, stream, xargs, "rlxq_x16_prep");
+  return launch(ctx, fn, dim3((unsigned)mp), dim3(256), 0, stream, xargs, "rlxq_x16_prep");
 }
 
 namespace {
@@ -73,7 +75,9 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   rlxq_x16_args xa;
   char* rest = nullptr;
   int rc;
-  if ((rc = prep_x16(ctx, x, x_dtype, m, k, scheme != RLXQ_GGUF_Q8_0, part_bytes, xa, &rest, stream, true))) return rc;
+  const int64_t mp = mch * 16 * MT;
+  if ((rc = prep_x16(ctx, x, x_dtype, m, k, scheme != RLXQ_GGUF_Q8_0, part_bytes, xa, &rest, stream, true, mp)))
+    return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
   a.x16 = xa.x16;
@@ -86,6 +90,7 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   a.K = k;
   a.rb = rb;
   a.y_ld = n;
+  a.Mp = mp;
   a.kslice = (int32_t)kslice;
   a.splits = (int32_t)splits;
   a.tiles_n = (int32_t)tiles_n;
@@ -95,6 +100,58 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   hipFunction_t fn;
   if ((rc = get_fn(ctx, name, &fn))) return rc;
   const size_t lds = 2 * (size_t)(MT * NT * 4) * 64 * 4;
+  void* args[] = {&a};
+  if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name))) return rc;
+  if (splits > 1) {
+    rc = splits_reduce(ctx, a, stream);
+    if (!rc) ctx->last_kernel = name;
+  }
+  return rc;
+}
+// N-split kernel: workgroups (4 NT x 16 weight rows, K split, 16*MT-row
+// chunk), the activations of a step shared by the four waves through LDS; K
+// splits as for the register-streamed kernel.
+int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
+                       int64_t k, int64_t n, void* y, int y_dtype, void* stream, int MT, int NT, int D) {
+  const int64_t tiles_n = (n + 64 * NT - 1) / (64 * NT), mch = (m + 16 * MT - 1) / (16 * MT);
+  const int64_t chunks = k / 128;
+  const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  int64_t target = 2 * cus;
+  if (const char* e = std::getenv("RLXQ_SKINNY_WGS")) target = (int64_t)(cus * std::atof(e));
+  int64_t splits = 1;
+  while (tiles_n * mch * splits < target && splits * 2 * 4 <= chunks && splits < 32) splits *= 2;
+  const int64_t kslice = ((chunks + splits - 1) / splits) * 128;
+  splits = (k + kslice - 1) / kslice;
+  if (tiles_n * mch * splits > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: batched-decode grid");
+  const size_t part_bytes = splits > 1 ? round256((size_t)(splits * m * n) * 4) : 0;
+  rlxq_x16_args xa;
+  char* rest = nullptr;
+  int rc;
+  const int64_t mp = mch * 16 * MT;
+  if ((rc = prep_x16(ctx, x, x_dtype, m, k, scheme != RLXQ_GGUF_Q8_0, part_bytes, xa, &rest, stream, true, mp)))
+    return rc;
+  rlxq_skinny_args a;
+  std::memset(&a, 0, sizeof a);
+  a.x16 = xa.x16;
+  a.inv_s = xa.inv_s;
+  a.w = static_cast<const uint8_t*>(w);
+  a.part = part_bytes ? reinterpret_cast<float*>(rest) : nullptr;
+  a.y = y;
+  a.M = m;
+  a.N = n;
+  a.K = k;
+  a.rb = rb;
+  a.y_ld = n;
+  a.Mp = mp;
+  a.kslice = (int32_t)kslice;
+  a.splits = (int32_t)splits;
+  a.tiles_n = (int32_t)tiles_n;
+  a.y_bf16 = y_dtype == RLXQ_BF16;
+  char name[64];
+  std::snprintf(name, sizeof name, "rlxq_skinnyns_%s_mt%d_nt%d_d%d", scheme_name(scheme), MT, NT, D);
+  hipFunction_t fn;
+  if ((rc = get_fn(ctx, name, &fn))) return rc;
+  const size_t lds = 2 * (size_t)(4 * 16 * MT * 64);
   void* args[] = {&a};
   if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name))) return rc;
   if (splits > 1) {
@@ -119,6 +176,21 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   // The register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR="MT,NT,D"
   // picks a compiled one (every combination for Q4_1, the defaults for Q4_0
   // and Q8_0), "0" the LDS-staged kernels below.
+  // The N-split kernel (activations shared through LDS): Q4_1 past 16 rows,
+  // where it measured 5-13% faster than the register-streamed one (at 16 rows
+  // and below, and for Q8_0, it was slower).  RLXQ_SKINNY_NS="MT,NT,D" picks
+  // a compiled one for any scheme, "0" turns the default off.
+  {
+    int nmt = m <= 32 ? 2 : 4, nnt = 1, nd = 3;
+    bool ns = scheme == RLXQ_GGUF_Q4_1 && m > 16;
+    if (const char* e = std::getenv("RLXQ_SKINNY_NS")) {
+      int a1, a2, a3;
+      if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) nmt = a1, nnt = a2, nd = a3, ns = true;
+      else if (e[0] == '0') ns = false;
+    }
+    if (std::getenv("RLXQ_SKINNY_XR") && !std::getenv("RLXQ_SKINNY_NS")) ns = false;
+    if (ns) return skinny_ns_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, nmt, nnt, nd);
+  }
   {
     int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = 2, xd = m <= 16 ? 4 : (m <= 32 ? 3 : 2);
     bool xr = true;

@@ -407,16 +407,13 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
     wrow[t] = wok[t] ? n : a.N - 1;
   }
   // activations in the fragment-major layout: piece i of chunk c for row m,
-  // lane group g at ((4 c + i) M + m) 4 + g (16-byte pieces), so the A
-  // fragment of 16 rows is one contiguous 1 KB read
+  // lane group g at ((4 c + i) Mp + m) 4 + g (16-byte pieces), so the A
+  // fragment of 16 rows is one contiguous 1 KB read; the Mp rows cover every
+  // 16 MT-row chunk (padding rows zero)
   const uint4* xrow[MT];
-  bool mok[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; mt++) {
-    const int64_t m = m0 + 16 * mt + j;
-    mok[mt] = m < a.M;
-    xrow[mt] = reinterpret_cast<const uint4*>(a.x16) + ((kb / 32) * a.M + (mok[mt] ? m : 0)) * 4 + g;
-  }
+  for (int mt = 0; mt < MT; mt++)
+    xrow[mt] = reinterpret_cast<const uint4*>(a.x16) + ((kb / 32) * a.Mp + m0 + 16 * mt + j) * 4 + g;
 
   struct Stage {
     RawBlk<SCH> w[NT];
@@ -428,10 +425,7 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint4 v = xrow[mt][((int64_t)c * 4 + i) * a.M * 4];
-        st.x[mt][i] = mok[mt] ? v : make_uint4(0u, 0u, 0u, 0u);
-      }
+      for (int i = 0; i < 4; i++) st.x[mt][i] = xrow[mt][((int64_t)c * 4 + i) * a.Mp * 4];
   };
 
   f32x4_t acc[MT][NT];
@@ -536,18 +530,169 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// N-split variant (GGUF Q4_1, Q4_0, Q8_0): the four waves of a workgroup take
+// different weight rows (wave w: NT tiles of 16 rows) over the same K range,
+// so each step's activations are loaded once per workgroup and shared through
+// LDS; the weights stream into registers as in the register-streamed variant
+// (lane (j, g): block 4c + g of row j of each tile).  A step is a
+// 128-element K chunk c.  Both the weights and the activation pieces of a
+// step are loaded D steps ahead into register rings (plain loads only, so
+// the compiler's load-count waits stay exact); the activations of step s + 1
+// go to LDS at the start of step s, into the slot step s - 1 read (two slots),
+// and one barrier per step publishes them.
+//
+// LDS slot layout: group q = i MT + mt (piece i of the chunk's blocks, m-tile
+// mt) is 1 KB, position g 16 + j holding the 16-byte piece of row 16 mt + j,
+// block 4c + g, so an A fragment read is 1 KB of consecutive LDS (no bank
+// conflicts).  Thread (w, lane) loads and stores piece i = w of every m-tile.
+template <int SCH, int MT, int NT, int D>
+RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
+  constexpr int MC = 16 * MT;
+  constexpr int AST = 4 * MC * 64;   // bytes of one activation slot
+  constexpr int BDW = sk_bdw<SCH>();
+  extern __shared__ __align__(16) uint8_t sma[];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int tn = blockIdx.x % a.tiles_n;
+  const int sp = (blockIdx.x / a.tiles_n) % a.splits;
+  const int mc = blockIdx.x / (a.tiles_n * a.splits);
+  const int64_t n0 = (int64_t)tn * 64 * NT + 16 * NT * wv, m0 = (int64_t)mc * MC;
+  const int64_t kb = (int64_t)sp * a.kslice;
+  const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
+  const int nsteps = (int)((ke - kb) / 128);
+
+  rlxq_gemm_args ga;
+  ga.w = a.w;
+  ga.rb = a.rb;
+  ga.K = a.K;
+  ga.group = 32;
+  ga.sb_bf16 = 0;
+  ga.scales = nullptr;
+  ga.biases = nullptr;
+  int64_t wrow[NT];
+  bool wok[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int64_t n = n0 + 16 * t + j;
+    wok[t] = n < a.N;
+    wrow[t] = wok[t] ? n : a.N - 1;
+  }
+  // this thread's activation piece: row 16 u + j of the m-chunk, block 4c + g,
+  // positions 8 wv .. 8 wv + 7 (fragment-major source; the Mp rows cover
+  // every m-chunk)
+  const uint4* xsrc = reinterpret_cast<const uint4*>(a.x16) + (wv * a.Mp + m0 + j) * 4 + g;
+
+  struct Stage {
+    RawBlk<SCH> w[NT];
+    uint4 x[MT];
+  };
+  // steps past the last repeat it (their data is never used), so every step
+  // issues the same loads
+  auto load = [&](int s, Stage& st) {
+    const int64_t c = kb / 128 + (s < nsteps ? s : nsteps - 1);
+#pragma unroll
+    for (int u = 0; u < MT; u++) st.x[u] = xsrc[(4 * c * a.Mp + 16 * u) * 4];
+#pragma unroll
+    for (int t = 0; t < NT; t++) load_blk<SCH>(ga, wrow[t], 4 * c + g, wok[t], st.w[t]);
+  };
+  auto put = [&](int s, const Stage& st) {
+    uint8_t* slot = sma + (s & 1) * AST;
+#pragma unroll
+    for (int u = 0; u < MT; u++) *reinterpret_cast<uint4*>(slot + (wv * MT + u) * 1024 + lane * 16) = st.x[u];
+  };
+  // the LDS stores of this wave have completed; then every wave's have
+  auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int s, const Stage& st) {
+    const uint8_t* slot = sma + (s & 1) * AST;
+    uint32_t o[NT][BDW];
+#pragma unroll
+    for (int t = 0; t < NT; t++) normalise<SCH>(st.w[t], o[t]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      f16x8_t af[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) af[mt] = *reinterpret_cast<const f16x8_t*>(slot + (i * MT + mt) * 1024 + lane * 16);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const f16x8_t b = dequant_lane<SCH>(o[t], i);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mt], b, acc[mt][t], 0, 0, 0);
+      }
+    }
+  };
+  // step s: ring slot s % D holds step s's weights (and step s's
+  // activations, already in LDS slot s & 1); slot (s + 1) % D holds step
+  // s + 1's activations, stored now into LDS slot (s + 1) & 1
+  Stage ring[D];
+  auto step = [&](int s, int d) {
+    put(s + 1, ring[(d + 1) % D]);
+    compute(s, ring[d]);
+    load(s + D, ring[d]);
+    barrier();
+  };
+
+#pragma unroll
+  for (int d = 0; d < D; d++) load(d, ring[d]);
+  put(0, ring[0]);
+  barrier();
+  int s0 = 0;
+  for (; s0 + D <= nsteps; s0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; d++) step(s0 + d, d);
+  }
+#pragma unroll
+  for (int d = 0; d < D; d++)
+    if (s0 + d < nsteps) step(s0 + d, d);
+
+  // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int64_t m = m0 + 16 * mt + 4 * g + r;
+      if (m >= a.M) continue;
+      const float is = a.inv_s[m];
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const int64_t n = n0 + 16 * t + j;
+        if (n >= a.N) continue;
+        const float v = acc[mt][t][r] * is;
+        if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
+        else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
+        else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+      }
+    }
+}
+
 }  // namespace rlxq
 
-// One workgroup of 256 per activation row; each thread owns whole 32-element
-// blocks (held in registers, so the permutation is local): blocks t, t + 256,
-// t + 512 (K <= 24576 keeps a row in registers; longer rows are read twice).
+// One workgroup of 256 per activation row (per padded row in the
+// fragment-major layout); each thread owns whole 32-element blocks (held in
+// registers, so the permutation is local): blocks t, t + 256, t + 512
+// (K <= 24576 keeps a row in registers; longer rows are read twice).
 extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a) {
   constexpr int RB = 3;   // register-resident blocks per thread
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
-  if (r >= a.M) return;
   const int64_t nblk = a.K >> 5;
   const int t = threadIdx.x;
+  if (r >= a.M) {
+    // padding rows of the fragment-major layout: zeros
+    if (!a.frag_major || r >= a.Mp) return;
+    uint4* dst = reinterpret_cast<uint4*>(a.x16);
+    for (int64_t b = t; b < nblk; b += 256)
+#pragma unroll
+      for (int q = 0; q < 4; q++) dst[(((b >> 2) * 4 + q) * a.Mp + r) * 4 + (b & 3)] = make_uint4(0u, 0u, 0u, 0u);
+    return;
+  }
   auto load_blk32 = [&](int64_t b, float* v) {
     if (a.x_bf16) {
       const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + r * a.K + b * 32);
@@ -613,7 +758,7 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
       uint4* dst = reinterpret_cast<uint4*>(a.x16);
 #pragma unroll
       for (int q = 0; q < 4; q++)
-        dst[(((b >> 2) * 4 + q) * a.M + r) * 4 + (b & 3)] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+        dst[(((b >> 2) * 4 + q) * a.Mp + r) * 4 + (b & 3)] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
     } else {
       uint4* dst = reinterpret_cast<uint4*>(a.x16 + r * a.K + b * 32);
 #pragma unroll
@@ -723,3 +868,17 @@ RLXQ_SKINNYXR_INST(q4_0, SCH_Q4_0, 4, 2, 2)
 RLXQ_SKINNYXR_INST(q8_0, SCH_Q8_0, 1, 2, 4)
 RLXQ_SKINNYXR_INST(q8_0, SCH_Q8_0, 2, 2, 3)
 RLXQ_SKINNYXR_INST(q8_0, SCH_Q8_0, 4, 2, 2)
+
+// N-split variants: rlxq_skinnyns_<scheme>_mt<MT>_nt<NT>_d<D>.
+#define RLXQ_SKINNYNS_INST(SNAME, SCH, MT, NT, D)                                                      \
+  extern "C" __global__ __launch_bounds__(256) void rlxq_skinnyns_##SNAME##_mt##MT##_nt##NT##_d##D(     \
+      rlxq_skinny_args a) {                                                                            \
+    rlxq::skinny_ns_body<SCH, MT, NT, D>(a);                                                           \
+  }
+RLXQ_SKINNYNS_INST(q4_1, SCH_Q4_1, 1, 1, 3)
+RLXQ_SKINNYNS_INST(q4_1, SCH_Q4_1, 2, 1, 3)
+RLXQ_SKINNYNS_INST(q4_1, SCH_Q4_1, 2, 2, 3)
+RLXQ_SKINNYNS_INST(q4_1, SCH_Q4_1, 4, 1, 3)
+RLXQ_SKINNYNS_INST(q4_1, SCH_Q4_1, 4, 2, 2)
+RLXQ_SKINNYNS_INST(q8_0, SCH_Q8_0, 4, 2, 2)
+RLXQ_SKINNYNS_INST(q4_0, SCH_Q4_0, 4, 1, 3)

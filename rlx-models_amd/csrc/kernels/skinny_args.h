@@ -7,14 +7,15 @@
 /* Activation preparation: x [M, K] (f32 or bf16) -> x16 f16 scaled by a
  * power of two per row (inv_s[m] = 1 / scale) and permuted within each
  * 32-element block to the order the packed codes unpack to.  Row-major
- * [M, K], or (frag_major) fragment-major: the 16-byte piece i (positions
- * 8i .. 8i + 7) of block 4c + g of row m at piece ((4c + i) * M + m) * 4 + g,
- * so the MFMA A fragments of 16 rows are 1 KB of contiguous memory. */
+ * [M, K], or (frag_major) fragment-major over Mp >= M rows (rows M .. Mp - 1
+ * zero): the 16-byte piece i (positions 8i .. 8i + 7) of block 4c + g of row
+ * m at piece ((4c + i) * Mp + m) * 4 + g, so the MFMA A fragments of 16 rows
+ * are 1 KB of contiguous memory. */
 typedef struct rlxq_x16_args {
   const void* x;
   uint16_t* x16;
   float* inv_s;
-  int64_t M, K;
+  int64_t M, K, Mp;
   int32_t x_bf16, nibble_order;
   int32_t frag_major, pad;
 } rlxq_x16_args;
@@ -26,6 +27,7 @@ typedef struct rlxq_skinny_args {
   float* part;            /* [splits, M, N] partial sums (splits > 1)     */
   void* y;                /* [M, N] output (splits == 1)                  */
   int64_t M, N, K, rb, y_ld;
+  int64_t Mp;             /* rows of the fragment-major x16 (>= M)        */
   int32_t kslice;         /* K per split, a multiple of 128               */
   int32_t splits, tiles_n, y_bf16;
 } rlxq_skinny_args;

@@ -67,7 +67,8 @@ def test_skinny_activation_range(ctx, orc, scheme):
         assert rel_err(got[r:r + 1], want[r:r + 1]) <= TOL_F32, r
 
 
-STAGINGS = {"register": {}, "lds": {"RLXQ_SKINNY_XR": "0", "RLXQ_SKINNY_DMA": "0"},
+STAGINGS = {"default": {}, "register": {"RLXQ_SKINNY_NS": "0"},
+            "lds": {"RLXQ_SKINNY_XR": "0", "RLXQ_SKINNY_DMA": "0"},
             "dma": {"RLXQ_SKINNY_XR": "0", "RLXQ_SKINNY_DMA": "1"}}
 KERNEL_PREFIX = {"register": "rlxq_skinnyxr_", "lds": "rlxq_skinny_q4_1_mt", "dma": "rlxq_skinny_q4_1_mt"}
 
@@ -75,7 +76,8 @@ KERNEL_PREFIX = {"register": "rlxq_skinnyxr_", "lds": "rlxq_skinny_q4_1_mt", "dm
 @pytest.mark.parametrize("staging", list(STAGINGS))
 @pytest.mark.parametrize("mkn", [(5, 256, 136), (16, 4096, 512), (33, 768, 200), (64, 1024, 128)], ids=str)
 def test_skinny_q4_1_every_staging(ctx, orc, monkeypatch, staging, mkn):
-    """Q4_1 through the register-streamed kernel (no LDS stage), the
+    """Q4_1 through the default choice (register-streamed up to 16 rows,
+    N-split above), the register-streamed kernel (no LDS stage), the
     register-staged LDS kernel and the LDS-DMA-staged kernel."""
     for key, val in STAGINGS[staging].items():
         monkeypatch.setenv(key, val)
@@ -85,7 +87,8 @@ def test_skinny_q4_1_every_staging(ctx, orc, monkeypatch, staging, mkn):
     packed = orc.synth_q4_1(rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, want = run_dense(ctx, orc, 3, x, packed, n, xdt="bf16")
-    assert ctx.last_kernel.startswith(KERNEL_PREFIX[staging]), ctx.last_kernel
+    prefix = KERNEL_PREFIX.get(staging, "rlxq_skinnyxr_" if m <= 16 else "rlxq_skinnyns_q4_1_")
+    assert ctx.last_kernel.startswith(prefix), ctx.last_kernel
     assert ctx.last_kernel.endswith("_dma") == (staging == "dma"), ctx.last_kernel
     assert rel_err(got, want) <= TOL_F32
 
@@ -136,3 +139,27 @@ def test_skinny_q8_0_q4_0_both_kernels(ctx, orc, monkeypatch, scheme, kernel):
         got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt="bf16")
         assert ctx.last_kernel.startswith("rlxq_skinnyxr_" if kernel == "register" else "rlxq_skinny_"), ctx.last_kernel
         assert rel_err(got, want) <= TOL_F32, (m, k, n)
+
+
+# every compiled N-split variant "scheme:MT,NT,D" (activations shared through
+# LDS, the four waves on different weight rows); shapes with partial row
+# chunks and tiles, several K splits, one K chunk, and a long K
+NS_VARIANTS = ["3:1,1,3", "3:2,1,3", "3:2,2,3", "3:4,1,3", "3:4,2,2", "1:4,2,2", "2:4,1,3"]
+
+
+@pytest.mark.parametrize("cfg", NS_VARIANTS)
+def test_skinny_every_nsplit_variant(ctx, orc, monkeypatch, cfg):
+    scheme, rest = int(cfg.split(":")[0]), cfg.split(":")[1]
+    monkeypatch.setenv("RLXQ_SKINNY_NS", rest)
+    mt, nt, d = (int(v) for v in rest.split(","))
+    name = {1: "q8_0", 2: "q4_0", 3: "q4_1"}[scheme]
+    for (m, k, n) in [(5, 128, 7), (16 * mt + 3, 2048, 64 * nt * 3 + 5), (9, 12288, 200), (64, 1536, 96),
+                      (3, 640, 64 * nt)]:
+        announce(f"skinny n-split {cfg} {(m, k, n)}")
+        rng = np.random.default_rng(m + k + n + mt + scheme)
+        packed = orc.synth(scheme, rng, n, k)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt="bf16")
+        assert ctx.last_kernel == f"rlxq_skinnyns_{name}_mt{mt}_nt{nt}_d{d}", ctx.last_kernel
+        assert rel_err(got, want) <= TOL_F32, (cfg, m, k, n)
+
