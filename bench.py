@@ -380,6 +380,27 @@ def synth_q4_k_gpu(n: int, k: int, gen):
     return torch.cat([d, dm, rest], dim=1).contiguous().view(-1)
 
 
+def synth_kq_gpu(scheme: str, n: int, k: int, gen):
+    """Q5_K / Q3_K / Q2_K / Q8_K rows on the device: random code and scale
+    bytes, with the super-block scales set to the sizes of the oracle's
+    synthetic rows (fp16 d (and dmin) at their offsets, Q8_K's f32 d)."""
+    import torch
+
+    sb, fields = {"q5_k": (176, [(0, 0.0003, 0.001), (2, 0.0005, 0.005)]),
+                  "q3_k": (110, [(108, 0.0002, 0.001)]),
+                  "q2_k": (84, [(80, 0.001, 0.004), (82, 0.0005, 0.002)]),
+                  "q8_k": (292, [])}[scheme]
+    nb = n * (k // 256)
+    blk = torch.randint(0, 256, (nb, sb), device="cuda", dtype=torch.uint8, generator=gen)
+    for off, lo, hi in fields:
+        v = torch.empty(nb, device="cuda").uniform_(lo, hi, generator=gen).half().view(torch.uint8).view(nb, 2)
+        blk[:, off:off + 2] = v
+    if scheme == "q8_k":
+        d = torch.empty(nb, device="cuda").uniform_(0.0002, 0.001, generator=gen).view(torch.uint8).view(nb, 4)
+        blk[:, 0:4] = d
+    return blk.contiguous().view(-1)
+
+
 def synth_q6_k_gpu(n: int, k: int, gen):
     """Q6_K rows on the device: random code bytes, int8 scales ~U{-64..63},
     d ~U(0.0002, 0.001) fp16."""
@@ -418,7 +439,8 @@ def synth_mxfp4_gpu(n: int, k: int, gen, decoded: bool = False):
 def schemes_section(ctx, gen, sptr, stream) -> dict:
     """The other weight formats of the op at M=1 (bf16 activations, f32
     output) on the gate_up shape 4096->24576, weights rotated past the MALL:
-    GGUF Q4_0, Q4_K and Q6_K, MLX affine 4/8-bit (group 64, bf16 slabs), MXFP4
+    GGUF Q4_0, Q4_K, Q6_K, Q5_K, Q3_K, Q2_K and Q8_K, MLX affine 4/8-bit
+    (group 64, bf16 slabs), MXFP4
     (E8M0 byte scales), Int8Block (i8 [K, N] with an f32 scale per column); the
     MLX 4-bit and MXFP4 (bf16 decoded scales) grouped ops at the
     MoE config's gate|up shape; and the bit-exact dequantisation kernel
@@ -450,6 +472,10 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
             lambda w: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_K, n, y=y, stream=sptr))
     measure("q6_k_gemv_m1", n * k * 210 / 256, lambda: synth_q6_k_gpu(n, k, gen),
             lambda w: ctx.dequant_matmul(x, w, rlxq.GGUF_Q6_K, n, y=y, stream=sptr))
+    for name, sch, sb in (("q5_k", rlxq.GGUF_Q5_K, 176), ("q3_k", rlxq.GGUF_Q3_K, 110),
+                          ("q2_k", rlxq.GGUF_Q2_K, 84), ("q8_k", rlxq.GGUF_Q8_K, 292)):
+        measure(f"{name}_gemv_m1", n * k * sb / 256, lambda name=name: synth_kq_gpu(name, n, k, gen),
+                lambda w, sch=sch: ctx.dequant_matmul(x, w, sch, n, y=y, stream=sptr))
     for bits in (4, 8):
         wb = n * k * bits / 8 + 2 * n * (k // 64) * 2
         measure(f"mlx{bits}_g64_gemv_m1", wb, lambda bits=bits: synth_mlx_gpu(n, k, bits, 64, gen),

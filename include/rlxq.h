@@ -63,7 +63,7 @@ typedef enum rlxq_scheme {
                              qh[64], int8 scales[16], f16 d;
                              w = (d*scale)*(code - 32).  Dense (GEMV family)
                              and grouped ops, dequantize; K % 256 == 0        */
-    RLXQ_MLX_MXFP4 = 9    /* MlxMxfp4{group_size: 32} (crates/rlx-models-core/
+    RLXQ_MLX_MXFP4 = 9,   /* MlxMxfp4{group_size: 32} (crates/rlx-models-core/
                              src/mxfp4_pack.rs:16-50): codes [N, K/2], two E2M1
                              codes per byte, low nibble = even element; one
                              scale per 32: E8M0 bytes [N, K/32] (RLXQ_U8, the
@@ -72,6 +72,24 @@ typedef enum rlxq_scheme {
                              operand).  No bias (biases are not read).
                              w = E2M1(code) * scale.  GEMV family, grouped ops
                              and dequantize                                    */
+    /* The other K-quants of the reference's DeviceMatmul table
+     * (crates/rlx-laguna/src/device_matmul.rs:64-76) and of its GGUF scheme
+     * map (crates/rlx-models-core/src/weight_loader.rs:497-505; host twins
+     * rlx_gguf::dequant_q5_k / q3_k / q2_k / q8_k, crates/rlx-sam3/src/
+     * packed_gguf.rs:46-56).  256 weights per super-block, K % 256 == 0; the
+     * GEMV family (every M), grouped ops and dequantize.                     */
+    RLXQ_GGUF_Q5_K = 10,  /* 176 B: f16 d, f16 dmin, the 12 Q4_K scale bytes,
+                             qh[32], qs[128]; code = nibble | qh bit << 4;
+                             w = (d*sc)*code - dmin*mn; w 16-byte aligned      */
+    RLXQ_GGUF_Q3_K = 11,  /* 110 B: hmask[32], qs[64], 12 B of sixteen 6-bit
+                             scales, f16 d; code = 2 bits - (hmask bit ? 0 : 4);
+                             w = (d*(scale-32))*code; w 4-byte aligned (its
+                             110-byte rows are 2-byte aligned)                */
+    RLXQ_GGUF_Q2_K = 12,  /* 84 B: scales[16] (scale | min << 4), qs[64], f16
+                             d, f16 dmin; w = (d*sc)*code - dmin*mn;
+                             w 4-byte aligned                                  */
+    RLXQ_GGUF_Q8_K = 13   /* 292 B: f32 d, int8 qs[256], int16 bsums[16];
+                             w = d*q; w 4-byte aligned                         */
 } rlxq_scheme;
 
 /* Element types of activations, outputs and MLX scale/bias slabs. */

@@ -19,7 +19,9 @@ HERE = Path(__file__).resolve().parent
 LIBPATH = Path(os.environ.get("RLXQ_ORACLE_LIB", HERE / "liboracle.so"))
 
 Q8_0, Q4_0, Q4_1, MLX4, MLX8, INT8_BLOCK, Q4_K, Q6_K = 1, 2, 3, 4, 5, 6, 7, 8
-BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20, Q4_K: 144, Q6_K: 210}
+Q5_K, Q3_K, Q2_K, Q8_K = 10, 11, 12, 13
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, Q4_1: 20, Q4_K: 144, Q6_K: 210, Q5_K: 176, Q3_K: 110, Q2_K: 84, Q8_K: 292}
+KQUANTS = (Q4_K, Q6_K, Q5_K, Q3_K, Q2_K, Q8_K)
 
 _lib = None
 
@@ -45,6 +47,7 @@ def lib() -> C.CDLL:
             "orc_quantize": (I, [I, P, I64, P]),
             "orc_dequantize": (I, [I, P, I64, P]),
             "orc_q4k_scale_min": (None, [P, I, C.POINTER(I), C.POINTER(I)]),
+            "orc_q3k_scale": (I, [P, I]),
             "orc_mlx_pack": (I, [P, I64, I64, I, P]),
             "orc_mlx_dequantize": (I, [P, P, P, I64, I64, I, I, P]),
             "orc_matmul_f64": (I, [I, P, P, I64, I64, I64, P]),
@@ -321,6 +324,76 @@ def synth_q6_k(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
     return blk.reshape(n, -1)
 
 
+def synth_q5_k(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
+    """Q5_K rows (K % 256 == 0): random qh / qs bytes (5-bit codes), 6-bit
+    scales and mins ~U{0..63} in the Q4_K packing, d ~U(0.0003, 0.001) and
+    dmin ~U(0.0005, 0.005) fp16."""
+    nb = n * (k // 256)
+    blk = np.empty((nb, 176), np.uint8)
+    d = f32_to_f16_bits(rng.uniform(0.0003, 0.001, nb).astype(np.float32))
+    dm = f32_to_f16_bits(rng.uniform(0.0005, 0.005, nb).astype(np.float32))
+    blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blk[:, 2:4] = dm.view(np.uint8).reshape(nb, 2)
+    blk[:, 4:16] = q4k_pack_scales(rng.integers(0, 64, (nb, 8)), rng.integers(0, 64, (nb, 8)))
+    blk[:, 16:176] = rng.integers(0, 256, (nb, 160), dtype=np.uint8)
+    return blk.reshape(n, -1)
+
+
+def synth_q3_k(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
+    """Q3_K rows (K % 256 == 0): random hmask / qs bytes, sixteen 6-bit
+    scales ~U{0..63} in GGML's block_q3_K packing, d ~U(0.0002, 0.001) fp16."""
+    nb = n * (k // 256)
+    blk = np.empty((nb, 110), np.uint8)
+    blk[:, 0:96] = rng.integers(0, 256, (nb, 96), dtype=np.uint8)
+    blk[:, 96:108] = q3k_pack_scales(rng.integers(0, 64, (nb, 16)))
+    d = f32_to_f16_bits(rng.uniform(0.0002, 0.001, nb).astype(np.float32))
+    blk[:, 108:110] = d.view(np.uint8).reshape(nb, 2)
+    return blk.reshape(n, -1)
+
+
+def synth_q2_k(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
+    """Q2_K rows (K % 256 == 0): random scale bytes (4-bit scale and min),
+    random 2-bit codes, d ~U(0.001, 0.004) and dmin ~U(0.0005, 0.002) fp16."""
+    nb = n * (k // 256)
+    blk = np.empty((nb, 84), np.uint8)
+    blk[:, 0:80] = rng.integers(0, 256, (nb, 80), dtype=np.uint8)
+    d = f32_to_f16_bits(rng.uniform(0.001, 0.004, nb).astype(np.float32))
+    dm = f32_to_f16_bits(rng.uniform(0.0005, 0.002, nb).astype(np.float32))
+    blk[:, 80:82] = d.view(np.uint8).reshape(nb, 2)
+    blk[:, 82:84] = dm.view(np.uint8).reshape(nb, 2)
+    return blk.reshape(n, -1)
+
+
+def synth_q8_k(rng: np.random.Generator, n: int, k: int) -> np.ndarray:
+    """Q8_K rows (K % 256 == 0): f32 d ~U(0.0002, 0.001), int8 codes
+    ~U{-127..127}, and the 16 int16 sums of 16 codes that the format carries."""
+    nb = n * (k // 256)
+    blk = np.empty((nb, 292), np.uint8)
+    blk[:, 0:4] = rng.uniform(0.0002, 0.001, nb).astype(np.float32).view(np.uint8).reshape(nb, 4)
+    q = rng.integers(-127, 128, (nb, 256)).astype(np.int8)
+    blk[:, 4:260] = q.view(np.uint8)
+    blk[:, 260:292] = q.astype(np.int16).reshape(nb, 16, 16).sum(-1).astype(np.int16).view(np.uint8).reshape(nb, 32)
+    return blk.reshape(n, -1)
+
+
+def q3k_pack_scales(sc) -> np.ndarray:
+    """The 12 bytes that hold sixteen 6-bit Q3_K scales ([..., 16], 0..63), in
+    GGML's block_q3_K packing: byte t < 8 holds the low nibbles of scales t
+    (bits 0-3) and t + 8 (bits 4-7); byte 8 + t holds bits 4-5 of scales t,
+    t + 4, t + 8, t + 12 at bits 0-1, 2-3, 4-5, 6-7."""
+    sc = np.asarray(sc, np.int64)
+    out = np.empty(sc.shape[:-1] + (12,), np.uint8)
+    out[..., 0:8] = (sc[..., 0:8] & 15) | ((sc[..., 8:16] & 15) << 4)
+    hi = sc >> 4
+    out[..., 8:12] = hi[..., 0:4] | (hi[..., 4:8] << 2) | (hi[..., 8:12] << 4) | (hi[..., 12:16] << 6)
+    return out
+
+
+def q3k_scale(q12, s: int) -> int:
+    q = np.ascontiguousarray(q12, dtype=np.uint8)
+    return int(lib().orc_q3k_scale(_p(q), s))
+
+
 def q4k_pack_scales(sc, mn) -> np.ndarray:
     """The 12 bytes that hold eight 6-bit scales and mins ([..., 8] each), in
     GGML's block_q4_K packing: bytes 0-3 sc[0..3] | (sc[4..7] >> 4) << 6,
@@ -343,7 +416,8 @@ def q4k_scale_min(q12, s: int) -> tuple[int, int]:
 
 
 def synth(scheme: int, rng: np.random.Generator, n: int, k: int) -> np.ndarray:
-    return {Q4_1: synth_q4_1, Q8_0: synth_q8_0, Q4_0: synth_q4_0, Q4_K: synth_q4_k, Q6_K: synth_q6_k}[scheme](rng, n, k)
+    return {Q4_1: synth_q4_1, Q8_0: synth_q8_0, Q4_0: synth_q4_0, Q4_K: synth_q4_k, Q6_K: synth_q6_k,
+            Q5_K: synth_q5_k, Q3_K: synth_q3_k, Q2_K: synth_q2_k, Q8_K: synth_q8_k}[scheme](rng, n, k)
 
 
 # ---- MXFP4 (QuantScheme::MlxMxfp4), in numpy ---------------------------------

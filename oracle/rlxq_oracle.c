@@ -127,11 +127,20 @@ int64_t orc_block_bytes(int scheme) {
         case ORC_GGUF_Q4_1: return 4 + QK / 2;
         case ORC_GGUF_Q4_K: return 2 + 2 + 12 + QKK / 2;
         case ORC_GGUF_Q6_K: return QKK / 2 + QKK / 4 + QKK / 16 + 2;
+        case ORC_GGUF_Q5_K: return 2 + 2 + 12 + QKK / 8 + QKK / 2;
+        case ORC_GGUF_Q3_K: return QKK / 8 + QKK / 4 + 12 + 2;
+        case ORC_GGUF_Q2_K: return QKK / 16 + QKK / 4 + 2 + 2;
+        case ORC_GGUF_Q8_K: return 4 + QKK + 2 * (QKK / 16);
         default: return -1;
     }
 }
 
-int64_t orc_block_len(int scheme) { return (scheme == ORC_GGUF_Q4_K || scheme == ORC_GGUF_Q6_K) ? QKK : QK; }
+static int is_kquant(int scheme) {
+    return scheme == ORC_GGUF_Q4_K || scheme == ORC_GGUF_Q6_K || scheme == ORC_GGUF_Q5_K ||
+           scheme == ORC_GGUF_Q3_K || scheme == ORC_GGUF_Q2_K || scheme == ORC_GGUF_Q8_K;
+}
+
+int64_t orc_block_len(int scheme) { return is_kquant(scheme) ? QKK : QK; }
 
 int64_t orc_row_bytes(int scheme, int64_t k) {
     int64_t bb = orc_block_bytes(scheme), len = orc_block_len(scheme);
@@ -203,7 +212,7 @@ static void quant_q4_1_block(const float* x, uint8_t* out) {
 
 int orc_quantize(int scheme, const float* src, int64_t n, uint8_t* dst) {
     int64_t bb = orc_block_bytes(scheme);
-    if (bb < 0 || n % QK || scheme == ORC_GGUF_Q4_K || scheme == ORC_GGUF_Q6_K) return -1;  /* no K-quant encoders */
+    if (bb < 0 || n % QK || is_kquant(scheme)) return -1;  /* no K-quant encoders */
     for (int64_t b = 0; b < n / QK; b++) {
         const float* x = src + b * QK;
         uint8_t* o = dst + b * bb;
@@ -301,13 +310,117 @@ static void dequant_q6k_block(const uint8_t* b, float* o) {
             }
 }
 
+/* GGUF Q5_K (GGML block_q5_K; QuantScheme::GgufQ5K, decoded by the absent
+ * rlx_gguf::dequant_q5_k): 256 weights in 176 bytes -- f16 d, f16 dmin, the
+ * 12 scale/min bytes of Q4_K, qh[32], qs[128].  Group g (weights
+ * 64g..64g+63) reads qs[32g..32g+31]; weight 64g + 32h + l has
+ *   code = (qs[32g + l] >> 4h) & 15 | ((qh[l] >> (2g + h)) & 1) << 4,
+ * sub-block s = 2g + h, and w = (d * sc) * code - (dmin * mn) as for Q4_K. */
+static void dequant_q5k_block(const uint8_t* b, float* o) {
+    const float d = rd_f16(b), dmin = rd_f16(b + 2);
+    const uint8_t* sc12 = b + 4;
+    const uint8_t* qh = b + 16;
+    const uint8_t* qs = b + 48;
+    for (int g = 0; g < 4; g++)
+        for (int h = 0; h < 2; h++) {
+            int sc, mn;
+            orc_q4k_scale_min(sc12, 2 * g + h, &sc, &mn);
+            const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+            for (int l = 0; l < 32; l++) {
+                const int code = ((qs[32 * g + l] >> (4 * h)) & 15) | (((qh[l] >> (2 * g + h)) & 1) << 4);
+                const float prod = d1 * (float)code;
+                o[64 * g + 32 * h + l] = prod - m1;
+            }
+        }
+}
+
+/* GGUF Q3_K (GGML block_q3_K; QuantScheme::GgufQ3K, absent
+ * rlx_gguf::dequant_q3_k): 256 weights in 110 bytes -- hmask[32], qs[64]
+ * (2-bit codes), 12 bytes packing sixteen 6-bit scales, f16 d.  Scale s
+ * (16 weights each) from the 12 bytes q:
+ *   s < 4:  q[s] & 15       | ((q[8 + s] >> 0) & 3) << 4
+ *   s < 8:  q[s] & 15       | ((q[4 + s] >> 2) & 3) << 4      (q[s], s = 4..7)
+ *   s < 12: q[s - 8] >> 4   | ((q[s] >> 4) & 3) << 4          (q[8 + (s - 8)])
+ *   else:   q[s - 8] >> 4   | ((q[s - 4] >> 6) & 3) << 4      (q[8 + (s - 12)])
+ * In half n (weights 128n..128n+127; qs + 32n) and quarter j, weight
+ * 128n + 32j + 16i + l (i, l < 16) has
+ *   code = (qs[32n + 16i + l] >> 2j) & 3, minus 4 unless bit 4n + j of
+ *   hmask[16i + l] is set,
+ *   scale = scale[8n + 2j + i] - 32,
+ * and w = (d * scale) * code, each product rounded to f32 (d * scale exact). */
+int orc_q3k_scale(const uint8_t* q, int s) {
+    if (s < 4) return (q[s] & 15) | (((q[8 + s] >> 0) & 3) << 4);
+    if (s < 8) return (q[s] & 15) | (((q[4 + s] >> 2) & 3) << 4);
+    if (s < 12) return (q[s - 8] >> 4) | (((q[s] >> 4) & 3) << 4);
+    return (q[s - 8] >> 4) | (((q[s - 4] >> 6) & 3) << 4);
+}
+
+static void dequant_q3k_block(const uint8_t* b, float* o) {
+    const uint8_t* hm = b;
+    const uint8_t* qs = b + 32;
+    const uint8_t* sc12 = b + 96;
+    const float d = rd_f16(b + 108);
+    for (int n = 0; n < 2; n++)
+        for (int j = 0; j < 4; j++)
+            for (int i = 0; i < 2; i++) {
+                const float dl = d * (float)(orc_q3k_scale(sc12, 8 * n + 2 * j + i) - 32);
+                for (int l = 0; l < 16; l++) {
+                    const int lo = (qs[32 * n + 16 * i + l] >> (2 * j)) & 3;
+                    const int hi = (hm[16 * i + l] >> (4 * n + j)) & 1;
+                    o[128 * n + 32 * j + 16 * i + l] = dl * (float)(lo - (hi ? 0 : 4));
+                }
+            }
+}
+
+/* GGUF Q2_K (GGML block_q2_K; QuantScheme::GgufQ2K, absent
+ * rlx_gguf::dequant_q2_k): 256 weights in 84 bytes -- scales[16] (low
+ * nibble scale, high nibble min, per 16 weights), qs[64] (2-bit codes), f16
+ * d, f16 dmin.  Weight 128n + 32j + 16i + l has
+ *   code = (qs[32n + 16i + l] >> 2j) & 3, byte c = scales[8n + 2j + i],
+ * and w = (d * (c & 15)) * code - (dmin * (c >> 4)), each product rounded
+ * to f32, then the subtraction. */
+static void dequant_q2k_block(const uint8_t* b, float* o) {
+    const uint8_t* sc = b;
+    const uint8_t* qs = b + 16;
+    const float d = rd_f16(b + 80), dmin = rd_f16(b + 82);
+    for (int n = 0; n < 2; n++)
+        for (int j = 0; j < 4; j++)
+            for (int i = 0; i < 2; i++) {
+                const int c = sc[8 * n + 2 * j + i];
+                const float dl = d * (float)(c & 15), ml = dmin * (float)(c >> 4);
+                for (int l = 0; l < 16; l++) {
+                    const int code = (qs[32 * n + 16 * i + l] >> (2 * j)) & 3;
+                    const float prod = dl * (float)code;
+                    o[128 * n + 32 * j + 16 * i + l] = prod - ml;
+                }
+            }
+}
+
+/* GGUF Q8_K (GGML block_q8_K; QuantScheme::GgufQ8K, absent
+ * rlx_gguf::dequant_q8_k): 256 weights in 292 bytes -- f32 d, int8 qs[256],
+ * int16 bsums[16] (sums of 16 codes, not needed to decode); w = d * q. */
+static void dequant_q8k_block(const uint8_t* b, float* o) {
+    float d;
+    memcpy(&d, b, 4);
+    const int8_t* qs = (const int8_t*)(b + 4);
+    for (int l = 0; l < 256; l++) o[l] = d * (float)qs[l];
+}
+
 int orc_dequantize(int scheme, const uint8_t* src, int64_t n, float* dst) {
     int64_t bb = orc_block_bytes(scheme), len = orc_block_len(scheme);
     if (bb < 0 || n % len) return -1;
     for (int64_t b = 0; b < n / len; b++) {
-        if (scheme == ORC_GGUF_Q6_K) dequant_q6k_block(src + b * bb, dst + b * len);
-        else if (scheme == ORC_GGUF_Q4_K) dequant_q4k_block(src + b * bb, dst + b * len);
-        else dequant_block(scheme, src + b * bb, dst + b * len);
+        const uint8_t* s = src + b * bb;
+        float* o = dst + b * len;
+        switch (scheme) {
+            case ORC_GGUF_Q6_K: dequant_q6k_block(s, o); break;
+            case ORC_GGUF_Q4_K: dequant_q4k_block(s, o); break;
+            case ORC_GGUF_Q5_K: dequant_q5k_block(s, o); break;
+            case ORC_GGUF_Q3_K: dequant_q3k_block(s, o); break;
+            case ORC_GGUF_Q2_K: dequant_q2k_block(s, o); break;
+            case ORC_GGUF_Q8_K: dequant_q8k_block(s, o); break;
+            default: dequant_block(scheme, s, o);
+        }
     }
     return 0;
 }
@@ -434,7 +547,7 @@ static float dot_refl(int scheme, const float* x, const uint8_t* row, int64_t k)
 
 int orc_matmul_refl(int scheme, const float* x, const uint8_t* w, int64_t m,
                     int64_t k, int64_t n, float* y) {
-    if (scheme == ORC_GGUF_Q4_K || scheme == ORC_GGUF_Q6_K) return -1;  /* reference-order loop: legacy blocks only */
+    if (is_kquant(scheme)) return -1;  /* reference-order loop: legacy blocks only */
     int64_t rb = orc_row_bytes(scheme, k);
     if (rb < 0) return -1;
     for (int64_t r = 0; r < m; r++)
@@ -447,7 +560,7 @@ int orc_matmul_refl(int scheme, const float* x, const uint8_t* w, int64_t m,
 int orc_matmul_refl_par(int scheme, const float* x, const uint8_t* w,
                         int64_t m, int64_t k, int64_t n, float* y,
                         int nthreads) {
-    if (scheme == ORC_GGUF_Q4_K || scheme == ORC_GGUF_Q6_K) return -1;
+    if (is_kquant(scheme)) return -1;
     int64_t rb = orc_row_bytes(scheme, k);
     if (rb < 0) return -1;
 #ifdef _OPENMP

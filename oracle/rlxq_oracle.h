@@ -60,6 +60,10 @@ enum {
     ORC_INT8_BLOCK = 6,
     ORC_GGUF_Q4_K = 7,
     ORC_GGUF_Q6_K = 8,
+    ORC_GGUF_Q5_K = 10,
+    ORC_GGUF_Q3_K = 11,
+    ORC_GGUF_Q2_K = 12,
+    ORC_GGUF_Q8_K = 13,
 };
 
 /* ---- scalar conversions (IEEE binary16 / bfloat16, round to nearest even) */
@@ -73,15 +77,19 @@ void orc_f32_to_bf16_n(const float* src, int64_t n, uint16_t* dst);
 void orc_bf16_to_f32_n(const uint16_t* src, int64_t n, float* dst);
 
 /* ---- GGUF legacy block codecs (32 weights per block) -------------------- */
-int64_t orc_block_bytes(int scheme);           /* 34 / 18 / 20 / 144 (Q4_K) / 210 (Q6_K), else -1 */
-int64_t orc_block_len(int scheme);             /* weights per block: 32, or 256 (Q4_K) */
+int64_t orc_block_bytes(int scheme);           /* 34 / 18 / 20; K-quants 144 (Q4_K) / 210 (Q6_K) /
+                                                  176 (Q5_K) / 110 (Q3_K) / 84 (Q2_K) / 292 (Q8_K); else -1 */
+int64_t orc_block_len(int scheme);             /* weights per block: 32, or 256 (the K-quants) */
 int64_t orc_row_bytes(int scheme, int64_t k);  /* k/len * block bytes, else -1 */
 /* Quantize n (multiple of 32) floats into packed blocks. 0 on success. */
 int orc_quantize(int scheme, const float* src, int64_t n, uint8_t* dst);
 /* Dequantize n (multiple of 32) weights. 0 on success. */
 int orc_dequantize(int scheme, const uint8_t* src, int64_t n, float* dst);
-/* Q4_K: the 6-bit (scale, min) of sub-block s (0..7) from the 12 packed bytes. */
+/* Q4_K / Q5_K: the 6-bit (scale, min) of sub-block s (0..7) from the 12 packed bytes. */
 void orc_q4k_scale_min(const uint8_t* q, int s, int* sc, int* mn);
+/* Q3_K: the 6-bit scale of 16-weight group s (0..15) from the 12 packed bytes
+ * (unsigned, 0..63; the weight uses scale - 32). */
+int orc_q3k_scale(const uint8_t* q, int s);
 
 /* ---- MLX affine (LSB-first u32 packing, w = scale*code + bias) ---------- */
 /* Pack row-major codes [rows, cols] into u32 words, LSB-first. */

@@ -32,7 +32,7 @@ HIPCC = str(ROCM / "bin" / "hipcc")
 # number of parts each kernel file is compiled in (-DRLXQ_PART=i gives
 # <name><i>.co; the parts build in parallel).  A name without a source file is
 # embedded empty and skipped at load time.
-CODE_OBJECTS = (("gemv", 4), ("misc", 1), ("gemm", 1), ("moe", 4), ("int8", 1), ("skinny", 1))
+CODE_OBJECTS = (("gemv", 6), ("misc", 1), ("gemm", 1), ("moe", 5), ("int8", 1), ("skinny", 1))
 
 HIP_FLAGS = [
     "--genco", "--offload-arch=gfx950", "-O3", "-std=c++17",

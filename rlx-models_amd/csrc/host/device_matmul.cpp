@@ -222,9 +222,7 @@ class DeviceMatmul {
   // The schemes whose packed bytes are self-describing (device_matmul.rs:64-76
   // lists the GGUF tags; anything else is "unsupported scheme").
   int check_scheme(int scheme) {
-    if (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_K ||
-        scheme == RLXQ_GGUF_Q6_K)
-      return RLXQ_OK;
+    if (rlxq_row_bytes(scheme, 256) > 0) return RLXQ_OK;   // the GGUF block and K-quant schemes
     return bail(RLXQ_E_SCHEME, "DeviceMatmul: unsupported scheme " + std::to_string(scheme));
   }
 

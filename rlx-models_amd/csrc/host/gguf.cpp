@@ -101,8 +101,12 @@ int scheme_of(int32_t t) {
     case 2: return RLXQ_GGUF_Q4_0;
     case 3: return RLXQ_GGUF_Q4_1;
     case 8: return RLXQ_GGUF_Q8_0;
+    case 10: return RLXQ_GGUF_Q2_K;
+    case 11: return RLXQ_GGUF_Q3_K;
     case 12: return RLXQ_GGUF_Q4_K;
+    case 13: return RLXQ_GGUF_Q5_K;
     case 14: return RLXQ_GGUF_Q6_K;
+    case 15: return RLXQ_GGUF_Q8_K;
     default: return 0;
   }
 }

@@ -56,7 +56,8 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     if (!std::strcmp(e, "fused")) fused = fusable, route_forced = true;
   }
   // kernel choice
-  const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_K) ? 2 : 1;
+  const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_K ||
+                      scheme == RLXQ_GGUF_Q5_K) ? 2 : 1;
   const int64_t units = (k / 32) / blocks;
   const bool xbf = x_dtype == RLXQ_BF16;
   const int64_t fired_est = num_experts < n_entries ? num_experts : n_entries;
@@ -231,7 +232,7 @@ int rlxq_moe_grouped(rlxq_ctx* ctx, int scheme, int mode, const void* x, int x_d
   if (!ctx) return RLXQ_E_NULL;
   ctx->last_error.clear();
   if (!ids) return fail(ctx, RLXQ_E_NULL, "moe_grouped: ids is null");
-  if (!is_gguf(scheme) && scheme != RLXQ_GGUF_Q4_K && scheme != RLXQ_GGUF_Q6_K)
+  if (!is_gguf(scheme) && kquant_bytes(scheme) < 0)
     return fail(ctx, RLXQ_E_SCHEME, "moe_grouped: GGUF schemes only");
   if (rows < 0 || top_k <= 0 || top_k > 64) return fail(ctx, RLXQ_E_SHAPE, "moe_grouped: need 0 < top_k <= 64");
   if (mode == RLXQ_MOE_EXPAND || mode == RLXQ_MOE_EXPAND_SWIGLU) {

@@ -32,6 +32,10 @@ const char* scheme_name(int s) {
     case RLXQ_GGUF_Q4_K: return "q4_k";
     case RLXQ_GGUF_Q6_K: return "q6_k";
     case RLXQ_MLX_MXFP4: return "mxfp4";
+    case RLXQ_GGUF_Q5_K: return "q5_k";
+    case RLXQ_GGUF_Q3_K: return "q3_k";
+    case RLXQ_GGUF_Q2_K: return "q2_k";
+    case RLXQ_GGUF_Q8_K: return "q8_k";
     default: return nullptr;
   }
 }
@@ -75,10 +79,17 @@ GemvCfg pick_gemv(int64_t m, int64_t units, int64_t lds_rec_bytes_m4, size_t max
     // chunk with four steps in flight, Q6_K two chunks with one step (97
     // VGPRs; 30.6 us against 35.1 for the 8-wave two-step variant on
     // 4096->24576, 16.9 against 18.4 on 12288->4096).
+    // The other K-quants, measured on 4096->24576 and 12288->4096: Q3_K, Q2_K
+    // and Q8_K also run best on Q6_K's variant (Q3_K's 22-dword units spill
+    // in the two-step one); Q5_K on two rows per wave of 8-wave workgroups
+    // (28.8 against 38.1 us for gate_up).
     c = L != 64 ? GemvCfg{L, 2, 1, 1, 2, 8}
                 : scheme == RLXQ_GGUF_Q4_K ? GemvCfg{64, 1, 1, 1, 4, 16}
-                : scheme == RLXQ_GGUF_Q6_K ? GemvCfg{64, 1, 2, 1, 1, 16}
-                                           : GemvCfg{64, 1, 2, 1, 2, 16};
+                : scheme == RLXQ_GGUF_Q5_K ? GemvCfg{64, 2, 1, 1, 2, 8}
+                : (scheme == RLXQ_GGUF_Q6_K || scheme == RLXQ_GGUF_Q3_K || scheme == RLXQ_GGUF_Q2_K ||
+                   scheme == RLXQ_GGUF_Q8_K)
+                    ? GemvCfg{64, 1, 2, 1, 1, 16}
+                    : GemvCfg{64, 1, 2, 1, 2, 16};
   }
   const char* e = c.MT == 1 ? std::getenv("RLXQ_GEMV_CFG") : nullptr;
   if (e) {
@@ -101,10 +112,16 @@ int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const 
     *rb = k / 256 * 144;
     return RLXQ_OK;
   }
-  if (scheme == RLXQ_GGUF_Q6_K) {
-    if (k % 256) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": Q6_K needs K % 256 == 0 (super-blocks)");
-    if (!aligned(w, 4)) return fail(ctx, RLXQ_E_ALIGN, std::string(what) + ": Q6_K weights must be 4-byte aligned");
-    *rb = k / 256 * 210;
+  if (const int64_t sb = kquant_bytes(scheme); sb > 0) {
+    // Q6_K, Q5_K, Q3_K, Q2_K, Q8_K (Q5_K's 176-byte super-blocks are read
+    // with 16-byte loads; the others with dword-aligned ones)
+    const char* nm = scheme_name(scheme);
+    if (k % 256) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": " + nm + " needs K % 256 == 0 (super-blocks)");
+    const uintptr_t al = scheme == RLXQ_GGUF_Q5_K ? 16 : 4;
+    if (!aligned(w, al))
+      return fail(ctx, RLXQ_E_ALIGN, std::string(what) + ": " + nm + " weights must be " + std::to_string(al) +
+                                         "-byte aligned");
+    *rb = k / 256 * sb;
     return RLXQ_OK;
   }
   if (is_gguf(scheme)) {
@@ -255,7 +272,8 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: K or N too large");
 
   const bool xbf = x_dtype == RLXQ_BF16;
-  const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_K) ? 2 : 1;
+  const int blocks = (scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_K ||
+                      scheme == RLXQ_GGUF_Q5_K) ? 2 : 1;
   const int64_t units = (k / 32) / blocks;
 
   // Prefill: bf16 activations and bf16 output with at least 64 rows go to the
@@ -269,8 +287,8 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     bool gemm_ok = xbf && k % 64 == 0 && m >= 1;
     const bool f16_gemm = !is_mlx(scheme) && scheme != RLXQ_GGUF_Q4_K;
     bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (f16_gemm && m > 256));
-    if (scheme == RLXQ_GGUF_Q6_K || scheme == RLXQ_MLX_MXFP4)
-      gemm_ok = use_gemm = false;   // (Q6_K, MXFP4: the GEMV family only)
+    if (scheme == RLXQ_MLX_MXFP4 || (kquant_bytes(scheme) > 0 && scheme != RLXQ_GGUF_Q4_K))
+      gemm_ok = use_gemm = false;   // (MXFP4 and the K-quants but Q4_K: the GEMV family only)
     if (const char* e = std::getenv("RLXQ_PREFILL")) {
       if (!std::strcmp(e, "gemv")) use_gemm = false;
       if (!std::strcmp(e, "gemm")) use_gemm = gemm_ok;

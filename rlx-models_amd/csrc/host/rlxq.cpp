@@ -36,12 +36,15 @@ RLXQ_EMBED(rlxq_co_gemv0, "gemv0.co")
 RLXQ_EMBED(rlxq_co_gemv1, "gemv1.co")
 RLXQ_EMBED(rlxq_co_gemv2, "gemv2.co")
 RLXQ_EMBED(rlxq_co_gemv3, "gemv3.co")
+RLXQ_EMBED(rlxq_co_gemv4, "gemv4.co")
+RLXQ_EMBED(rlxq_co_gemv5, "gemv5.co")
 RLXQ_EMBED(rlxq_co_misc, "misc.co")
 RLXQ_EMBED(rlxq_co_gemm, "gemm.co")
 RLXQ_EMBED(rlxq_co_moe0, "moe0.co")
 RLXQ_EMBED(rlxq_co_moe1, "moe1.co")
 RLXQ_EMBED(rlxq_co_moe2, "moe2.co")
 RLXQ_EMBED(rlxq_co_moe3, "moe3.co")
+RLXQ_EMBED(rlxq_co_moe4, "moe4.co")
 RLXQ_EMBED(rlxq_co_int8, "int8.co")
 RLXQ_EMBED(rlxq_co_skinny, "skinny.co")
 
@@ -58,12 +61,15 @@ const Image kImages[] = {
     {rlxq_co_gemv1_begin, rlxq_co_gemv1_end, "gemv1"},
     {rlxq_co_gemv2_begin, rlxq_co_gemv2_end, "gemv2"},
     {rlxq_co_gemv3_begin, rlxq_co_gemv3_end, "gemv3"},
+    {rlxq_co_gemv4_begin, rlxq_co_gemv4_end, "gemv4"},
+    {rlxq_co_gemv5_begin, rlxq_co_gemv5_end, "gemv5"},
     {rlxq_co_misc_begin, rlxq_co_misc_end, "misc"},
     {rlxq_co_gemm_begin, rlxq_co_gemm_end, "gemm"},
     {rlxq_co_moe0_begin, rlxq_co_moe0_end, "moe0"},
     {rlxq_co_moe1_begin, rlxq_co_moe1_end, "moe1"},
     {rlxq_co_moe2_begin, rlxq_co_moe2_end, "moe2"},
     {rlxq_co_moe3_begin, rlxq_co_moe3_end, "moe3"},
+    {rlxq_co_moe4_begin, rlxq_co_moe4_end, "moe4"},
     {rlxq_co_int8_begin, rlxq_co_int8_end, "int8"},
     {rlxq_co_skinny_begin, rlxq_co_skinny_end, "skinny"},
 };
@@ -177,6 +183,18 @@ int workspace(rlxq_ctx* ctx, size_t bytes, void** out, void* stream) {
 bool is_gguf(int s) { return s == RLXQ_GGUF_Q8_0 || s == RLXQ_GGUF_Q4_0 || s == RLXQ_GGUF_Q4_1; }
 bool is_mlx(int s) { return s == RLXQ_MLX_AFFINE4 || s == RLXQ_MLX_AFFINE8; }
 
+int64_t kquant_bytes(int s) {
+  switch (s) {
+    case RLXQ_GGUF_Q4_K: return 144;
+    case RLXQ_GGUF_Q6_K: return 210;
+    case RLXQ_GGUF_Q5_K: return 176;
+    case RLXQ_GGUF_Q3_K: return 110;
+    case RLXQ_GGUF_Q2_K: return 84;
+    case RLXQ_GGUF_Q8_K: return 292;
+    default: return -1;
+  }
+}
+
 int64_t gguf_block_bytes(int s) {
   switch (s) {
     case RLXQ_GGUF_Q8_0: return 34;
@@ -221,8 +239,7 @@ const char* rlxq_last_error(const rlxq_ctx* ctx) { return ctx ? ctx->last_error.
 const char* rlxq_last_kernel(const rlxq_ctx* ctx) { return ctx ? ctx->last_kernel.c_str() : ""; }
 
 int64_t rlxq_row_bytes(int scheme, int64_t k) {
-  if (scheme == RLXQ_GGUF_Q4_K) return (k <= 0 || k % 256) ? -1 : k / 256 * 144;
-  if (scheme == RLXQ_GGUF_Q6_K) return (k <= 0 || k % 256) ? -1 : k / 256 * 210;
+  if (const int64_t sb = kquant_bytes(scheme); sb > 0) return (k <= 0 || k % 256) ? -1 : k / 256 * sb;
   int64_t bb = gguf_block_bytes(scheme);
   if (bb < 0 || k <= 0 || k % 32) return -1;
   return k / 32 * bb;

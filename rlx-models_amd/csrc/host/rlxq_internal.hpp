@@ -80,6 +80,9 @@ int workspace(rlxq_ctx* ctx, size_t bytes, void** out, void* stream);
 
 bool is_gguf(int scheme);
 bool is_mlx(int scheme);
+// GGUF K-quant super-block bytes (256 weights): Q4_K 144, Q6_K 210, Q5_K
+// 176, Q3_K 110, Q2_K 84, Q8_K 292; -1 for the other schemes.
+int64_t kquant_bytes(int scheme);
 // Slab dtype as the kernels read it (sb_bf16 field): 0 f32, 1 bf16, 2 bytes.
 inline int sb_code(int sb_dtype) { return sb_dtype == RLXQ_BF16 ? 1 : (sb_dtype == RLXQ_U8 ? 2 : 0); }
 int64_t gguf_block_bytes(int scheme);

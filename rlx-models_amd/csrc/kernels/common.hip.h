@@ -42,6 +42,10 @@ enum : int {
   SCH_Q4_K = 7,
   SCH_Q6_K = 8,
   SCH_MXFP4 = 9,
+  SCH_Q5_K = 10,
+  SCH_Q3_K = 11,
+  SCH_Q2_K = 12,
+  SCH_Q8_K = 13,
 };
 
 // MXFP4 (OCP microscaling FP4): E2M1 codes, two per byte (low nibble = even

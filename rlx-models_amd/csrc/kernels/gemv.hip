@@ -1,5 +1,6 @@
 // Dequant-GEMV for decode (M = 1..few rows): y[m, n] = sum_k x[m, k] * W[n, k]
-// over packed GGUF Q4_1 / Q4_0 / Q8_0 / Q4_K / Q6_K blocks, MLX affine 4/8-bit
+// over packed GGUF Q4_1 / Q4_0 / Q8_0 / Q4_K / Q6_K / Q5_K / Q3_K / Q2_K / Q8_K
+// blocks, MLX affine 4/8-bit
 // codes or MXFP4 codes, with fp32 accumulation.  Replaces the backend kernel of Op::DequantMatMul
 // (crates/rlx-models-core/src/standard_decoder.rs:727-738).
 //
@@ -50,7 +51,8 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
   constexpr int RP = 64 / L;
   constexpr int TILE = WAVES * P * RP;
   constexpr bool SLAB = slab_scales<SCH>(), SBIAS = slab_bias<SCH>();
-  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SBIAS);
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SCH == SCH_Q5_K || SBIAS);
+  constexpr bool HALF2 = SCH == SCH_Q2_K || SCH == SCH_Q3_K;   // two scales (and mins) per block
   extern __shared__ uint32_t lds[];
 
   const int K = a.K;
@@ -108,13 +110,16 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
 #pragma unroll
       for (int bl = 0; bl < BLOCKS; bl++) {
         const int b = uc * BLOCKS + bl;
-        float d[P], mn[P];
+        float d[P], mn[P], d2[P], m2[P];
         uint32_t pw[P][16];
 #pragma unroll
         for (int p = 0; p < P; p++) {
+          d2[p] = m2[p] = 0.f;
           if constexpr (SLAB) {
             d[p] = scale_decode<SCH>(bf.sm[p][c][bl], a.sb_bf16);
             mn[p] = SBIAS ? sb_decode(bf.bm[p][c][bl], a.sb_bf16 != 0) : 0.f;
+          } else if constexpr (HALF2) {
+            block_scales_half<SCH>(bf.dw[p][c], d[p], d2[p], mn[p], m2[p]);
           } else {
             block_scales<SCH>(bf.dw[p][c], bl, d[p], mn[p], uc);
           }
@@ -122,6 +127,8 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
           if (!(rok && uok)) {
             d[p] = 0.f;
             mn[p] = 0.f;
+            d2[p] = 0.f;
+            m2[p] = 0.f;
           }
           block_pairs<SCH>(bf.dw[p][c], bl, pw[p], kc);
         }
@@ -140,6 +147,8 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
           for (int p = 0; p < P; p++) {
             if constexpr (SCH == SCH_Q6_K) {
               acc[p][m] += q6k_block_dot<NPL>(pw[p], xrec, d[p], mn[p]);   // mn: the second half's d
+            } else if constexpr (HALF2) {
+              acc[p][m] += khalf_block_dot<SCH, NPL>(pw[p], xrec, d[p], d2[p], mn[p], m2[p]);
             } else {
               const float cc = block_dot<SCH, NPL>(pw[p], xrec);
               acc[p][m] = fmaf(BIT8 ? d[p] * scl : d[p], cc, acc[p][m]);
@@ -627,4 +636,12 @@ RLXQ_GEMV_SCHEME(q6_k, SCH_Q6_K)
 RLXQ_GEMV_SCHEME(mlx4, SCH_MLX4)
 RLXQ_GEMV_SCHEME(mlx8, SCH_MLX8)
 RLXQ_GEMV_SCHEME(mxfp4, SCH_MXFP4)
+#endif
+#if RLXQ_PART_IS(4)
+RLXQ_GEMV_SCHEME(q5_k, SCH_Q5_K)
+RLXQ_GEMV_SCHEME(q8_k, SCH_Q8_K)
+#endif
+#if RLXQ_PART_IS(5)
+RLXQ_GEMV_SCHEME(q3_k, SCH_Q3_K)
+RLXQ_GEMV_SCHEME(q2_k, SCH_Q2_K)
 #endif

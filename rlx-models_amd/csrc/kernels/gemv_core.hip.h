@@ -72,18 +72,64 @@ struct Unit<SCH_Q6_K> {
   static constexpr bool BIT8 = true;   // 6-bit codes take the byte path (f16 1024 + code)
 };
 
+// GGUF Q5_K: a unit is one 64-weight group (sub-blocks 2g, 2g + 1) of a
+// 176-byte super-block: the 16-byte head (f16 d, f16 dmin, the Q4_K scale
+// bytes), the 32 qh bytes (the fifth code bit of every weight, bit 2g + h),
+// the group's 32 qs bytes, and g (computed).  BYTES is the row stride per
+// unit (176 / 4).
+template <>
+struct Unit<SCH_Q5_K> {
+  static constexpr int BLOCKS = 2, BYTES = 44, DW = 21;
+  static constexpr bool BIT8 = false;
+};
+// GGUF Q8_K: a unit is one 32-weight block of a 292-byte super-block: its 32
+// int8 codes and the super-block's f32 d (load_unit_at addresses the
+// super-block; 292 / 8 is not a whole byte count).
+template <>
+struct Unit<SCH_Q8_K> {
+  static constexpr int BLOCKS = 1, BYTES = 36, DW = 9;
+  static constexpr bool BIT8 = true;
+};
+// GGUF Q2_K: a unit is one 32-weight block (n, j) = (b / 4, b % 4) of an
+// 84-byte super-block: the 32 qs bytes of half n (2-bit codes at bit 2j),
+// the dword holding its two scale bytes (scale | min << 4 for its two
+// 16-weight halves), the f16 d | f16 dmin dword, and j (computed).
+template <>
+struct Unit<SCH_Q2_K> {
+  static constexpr int BLOCKS = 1, BYTES = 10, DW = 11;
+  static constexpr bool BIT8 = false;
+};
+// GGUF Q3_K: a unit is one 32-weight block (n, j) of a 110-byte super-block,
+// which is only 2-byte aligned: the nine aligned dwords covering the 32
+// hmask bytes (bit 4n + j) and the nine covering its 32 qs bytes (bit 2j),
+// its two scales' low-nibble bytes and high-bit bytes (16-bit loads), the f16
+// d, and a word with the alignment, j and n (computed).
+template <>
+struct Unit<SCH_Q3_K> {
+  static constexpr int BLOCKS = 1, BYTES = 13, DW = 22;
+  static constexpr bool BIT8 = false;
+};
+// K-quants whose 32-weight blocks carry a scale per 16 weights.
+template <int SCH>
+RLXQ_DEV constexpr bool half_scales() {
+  return SCH == SCH_Q6_K || SCH == SCH_Q2_K || SCH == SCH_Q3_K;
+}
+
 // Offset that the code -> float trick adds to each code, and the value the
 // dot chain starts from (in units of the block's plane sum) so that the chain
 // ends at sum(w_int * x) where w_int is the scheme's integer weight:
 //   Q4_1/MLX4: q (bias 128)    Q4_0: q - 8 (bias 136)
 //   Q8_0: q (bias 1024 + 128, codes stored as q ^ 0x80)   MLX8: code (1024)
 //   Q6_K: code - 32 (bias 1024 + 32)
+//   Q8_K: q (bias 1024 + 128, as Q8_0)   Q5_K, Q2_K: code (128)
+//   Q3_K: (2 bits + 4 * hmask bit) - 4 (bias 132)
 //   MXFP4: none (the pairs carry the signed E2M1 values themselves)
 template <int SCH>
 RLXQ_DEV constexpr float chain_bias() {
   return SCH == SCH_MXFP4 ? 0.f
          : (SCH == SCH_Q4_0 ? 136.f
-            : (SCH == SCH_Q8_0 ? 1152.f : (SCH == SCH_MLX8 ? 1024.f : (SCH == SCH_Q6_K ? 1056.f : 128.f))));
+            : ((SCH == SCH_Q8_0 || SCH == SCH_Q8_K) ? 1152.f
+               : (SCH == SCH_MLX8 ? 1024.f : (SCH == SCH_Q6_K ? 1056.f : (SCH == SCH_Q3_K ? 132.f : 128.f)))));
 }
 // Start of a block's dot chain: -bias * (sum of the block's x).
 template <int SCH>
@@ -104,7 +150,7 @@ RLXQ_DEV void plane_pair(int t, int& a, int& b) {
     int base = 4 * i + ((e & 1) ? 16 : 0) + ((e & 2) ? 1 : 0);
     a = base;
     b = base + 2;
-  } else if constexpr (SCH == SCH_Q4_K || SCH == SCH_Q6_K) {
+  } else if constexpr (SCH == SCH_Q4_K || SCH == SCH_Q6_K || SCH == SCH_Q5_K || SCH == SCH_Q2_K || SCH == SCH_Q3_K) {
     // code dword i = bytes 4i..4i+3 of the group: low nibbles are the first
     // sub-block's elements 4i..4i+3 (the high ones the second's); extraction
     // e = 0 -> (4i, 4i+2), e = 1 -> (4i+1, 4i+3).
@@ -248,9 +294,10 @@ RLXQ_DEV void stage_store(uint32_t* lds, const XRaw<XBF16>& raw, int m, int K, i
       }
     }
     const float S = (!BIT8 && XBF16) ? sx : group8_sum(ps);
-    // sum of the record's first 16 elements (lanes q < 4; Q6_K's halves)
+    // sum of the record's first 16 elements (lanes q < 4; the per-half
+    // scales of Q6_K, Q2_K, Q3_K)
     float S_lo = 0.f;
-    if constexpr (SCH == SCH_Q6_K) S_lo = group4_sum((!BIT8 && XBF16) ? (v[0] + v[1]) + (v[2] + v[3]) : ps);
+    if constexpr (half_scales<SCH>()) S_lo = group4_sum((!BIT8 && XBF16) ? (v[0] + v[1]) + (v[2] + v[3]) : ps);
     // the two plane dwords of this lane and their positions t0, t1
     uint32_t h0, h1, l0 = 0u, l1 = 0u;
     int t0, t1;
@@ -288,7 +335,8 @@ RLXQ_DEV void stage_store(uint32_t* lds, const XRaw<XBF16>& raw, int m, int K, i
       h1 = hi[1] | (hi[3] << 16);
       l0 = lo[0] | (lo[2] << 16);
       l1 = lo[1] | (lo[3] << 16);
-      if constexpr (BIT8 || SCH == SCH_Q4_K || SCH == SCH_Q6_K) {
+      if constexpr (BIT8 || SCH == SCH_Q4_K || SCH == SCH_Q6_K || SCH == SCH_Q5_K || SCH == SCH_Q2_K ||
+                    SCH == SCH_Q3_K) {
         t0 = 2 * q;
         t1 = 2 * q + 1;
       } else {
@@ -377,7 +425,53 @@ RLXQ_DEV void load_unit(uint32_t* dw, const uint8_t* p) {
 // and its 32 code bytes of group u % 4, all 16-byte aligned loads.
 template <int SCH>
 RLXQ_DEV void load_unit_at(uint32_t* dw, const uint8_t* rp, int u) {
-  if constexpr (SCH == SCH_Q6_K) {
+  if constexpr (SCH == SCH_Q5_K) {
+    const uint8_t* sb = rp + (int64_t)(u >> 2) * 176;
+    const int g = u & 3;
+    const uint4 h = ld_u128(sb), qh0 = ld_u128(sb + 16), qh1 = ld_u128(sb + 32);
+    const uint4 q0 = ld_u128(sb + 48 + 32 * g), q1 = ld_u128(sb + 64 + 32 * g);
+    dw[0] = h.x; dw[1] = h.y; dw[2] = h.z; dw[3] = h.w;
+    dw[4] = qh0.x; dw[5] = qh0.y; dw[6] = qh0.z; dw[7] = qh0.w;
+    dw[8] = qh1.x; dw[9] = qh1.y; dw[10] = qh1.z; dw[11] = qh1.w;
+    dw[12] = q0.x; dw[13] = q0.y; dw[14] = q0.z; dw[15] = q0.w;
+    dw[16] = q1.x; dw[17] = q1.y; dw[18] = q1.z; dw[19] = q1.w;
+    dw[20] = (uint32_t)g;
+  } else if constexpr (SCH == SCH_Q8_K) {
+    const uint8_t* sb = rp + (int64_t)(u >> 3) * 292;
+    const uint8_t* c = sb + 4 + 32 * (u & 7);
+    const uint4 a = ld_u128(c), b = ld_u128(c + 16);
+    dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
+    dw[4] = b.x; dw[5] = b.y; dw[6] = b.z; dw[7] = b.w;
+    dw[8] = ld_u32(sb);
+  } else if constexpr (SCH == SCH_Q2_K) {
+    const uint8_t* sb = rp + (int64_t)(u >> 3) * 84;
+    const int n = (u >> 2) & 1, j = u & 3;
+    const uint4 a = ld_u128(sb + 16 + 32 * n), b = ld_u128(sb + 32 + 32 * n);
+    dw[0] = a.x; dw[1] = a.y; dw[2] = a.z; dw[3] = a.w;
+    dw[4] = b.x; dw[5] = b.y; dw[6] = b.z; dw[7] = b.w;
+    dw[8] = ld_u32(sb + 8 * n + 4 * (j >> 1));   // scale bytes 8n + 2j, 8n + 2j + 1
+    dw[9] = ld_u32(sb + 80);                      // f16 d | f16 dmin
+    dw[10] = (uint32_t)j;
+  } else if constexpr (SCH == SCH_Q3_K) {
+    const uint8_t* sb = rp + (int64_t)(u >> 3) * 110;
+    const int n = (u >> 2) & 1, j = u & 3;
+    const uint32_t off = (uint32_t)reinterpret_cast<uintptr_t>(sb) & 3u;   // 0 or 2
+    const uint8_t* hm = sb - off;
+    const uint8_t* qs = sb + 32 + 32 * n - off;
+    const uint4 h0 = ld_u128(hm), h1 = ld_u128(hm + 16), q0 = ld_u128(qs), q1 = ld_u128(qs + 16);
+    dw[0] = h0.x; dw[1] = h0.y; dw[2] = h0.z; dw[3] = h0.w;
+    dw[4] = h1.x; dw[5] = h1.y; dw[6] = h1.z; dw[7] = h1.w;
+    dw[8] = ld_u32(hm + 32);
+    dw[9] = q0.x; dw[10] = q0.y; dw[11] = q0.z; dw[12] = q0.w;
+    dw[13] = q1.x; dw[14] = q1.y; dw[15] = q1.z; dw[16] = q1.w;
+    dw[17] = ld_u32(qs + 32);
+    // scales 8n + 2j and 8n + 2j + 1: low nibbles in bytes 2j, 2j + 1 (the
+    // high nibbles for n = 1), bits 4..5 in bytes 8 + 2 (j & 1), + 1
+    dw[18] = *reinterpret_cast<const uint16_t*>(sb + 96 + 2 * j);
+    dw[19] = *reinterpret_cast<const uint16_t*>(sb + 104 + 2 * (j & 1));
+    dw[20] = *reinterpret_cast<const uint16_t*>(sb + 108);
+    dw[21] = off | ((uint32_t)j << 8) | ((uint32_t)n << 16);
+  } else if constexpr (SCH == SCH_Q6_K) {
     const uint8_t* sb = rp + (int64_t)(u >> 3) * 210;
     const int h = (u >> 2) & 1, j = u & 3;
     const uint32_t off = (uint32_t)reinterpret_cast<uintptr_t>(sb) & 3u;   // 0 or 2
@@ -405,11 +499,55 @@ RLXQ_DEV void load_unit_at(uint32_t* dw, const uint8_t* rp, int u) {
   }
 }
 
+// Q2_K / Q3_K: the two 16-weight halves' multipliers of the code chains (d,
+// d2) and of the halves' x sums (m, m2; Q2_K: minus dmin * min, Q3_K: 0).
+template <int SCH>
+RLXQ_DEV void block_scales_half(const uint32_t* dw, float& d, float& d2, float& m, float& m2) {
+  if constexpr (SCH == SCH_Q2_K) {
+    const uint32_t c = (dw[8] >> (16 * (dw[10] & 1))) & 0xffffu;   // bytes 8n + 2j, + 1
+    const float dd = f16_bits_to_f32(dw[9] & 0xffffu), dm = f16_bits_to_f32(dw[9] >> 16);
+    d = dd * (float)(c & 15u);
+    m = -(dm * (float)((c >> 4) & 15u));
+    d2 = dd * (float)((c >> 8) & 15u);
+    m2 = -(dm * (float)(c >> 12));
+  } else {
+    const uint32_t j = (dw[21] >> 8) & 3u, n = dw[21] >> 16;
+    const uint32_t ls = 4 * n, hs = 2 * (2 * n + (j >> 1));
+    const int s0 = (int)(((dw[18] >> ls) & 15u) | (((dw[19] >> hs) & 3u) << 4));
+    const int s1 = (int)(((dw[18] >> (8 + ls)) & 15u) | (((dw[19] >> (8 + hs)) & 3u) << 4));
+    const float dd = f16_bits_to_f32(dw[20] & 0xffffu);
+    d = dd * (float)(s0 - 32);
+    d2 = dd * (float)(s1 - 32);
+    m = 0.f;
+    m2 = 0.f;
+  }
+}
+
 // Block scale terms of block `blk` of a fetched unit: d multiplies the dot
 // chain, m (Q4_1 min; Q4_K minus dmin * min) multiplies the block sum of x.
 // u is the unit's index in its row (Q4_K: which group of the super-block).
 template <int SCH>
 RLXQ_DEV void block_scales(const uint32_t* dw, int blk, float& d, float& m, int u = 0) {
+  if constexpr (SCH == SCH_Q5_K) {
+    // (the head copied out: a runtime index into the 21-dword unit would
+    // keep the whole unit in scratch memory)
+    const uint32_t head[4] = {dw[0], dw[1], dw[2], dw[3]};
+    float sc, mn;
+    q4k_scale_min(head, 2 * (int)dw[20] + blk, sc, mn);
+    d = f16_bits_to_f32(dw[0] & 0xffffu) * sc;
+    m = -(f16_bits_to_f32(dw[0] >> 16) * mn);
+    return;
+  }
+  if constexpr (SCH == SCH_Q8_K) {
+    d = __uint_as_float(dw[8]);
+    m = 0.f;
+    return;
+  }
+  if constexpr (SCH == SCH_Q2_K || SCH == SCH_Q3_K) {
+    float d2, m2;
+    block_scales_half<SCH>(dw, d, d2, m, m2);
+    return;
+  }
   if constexpr (SCH == SCH_Q6_K) {
     // d * scale of the block's first and second 16 weights (both exact)
     const float dd = f16_bits_to_f32(dw[19] & 0xffffu);
@@ -484,6 +622,40 @@ RLXQ_DEV void block_pairs(const uint32_t* dw, int blk, uint32_t* pw, const Unpac
       const uint32_t qh = off ? align_bytes(dw[10 + i], dw[9 + i], 2) : dw[9 + i];
       byte_pairs(((ql >> ns) & 0x0F0F0F0Fu) | (((qh >> hs) & 0x03030303u) << 4), &pw[2 * i]);
     }
+  } else if constexpr (SCH == SCH_Q5_K) {
+    // sub-block 2g + blk: nibble blk of the group's qs bytes, fifth bit from
+    // bit 2g + blk of the qh bytes; bf16 (128 + code) pairs
+    const uint32_t hs = 2 * dw[20] + blk;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t c = ((dw[12 + i] >> (4 * blk)) & 0x0F0F0F0Fu) | (((dw[4 + i] >> hs) & 0x01010101u) << 4);
+      pw[2 * i] = (c & 0x001F001Fu) | 0x43004300u;
+      pw[2 * i + 1] = ((c >> 8) & 0x001F001Fu) | 0x43004300u;
+    }
+  } else if constexpr (SCH == SCH_Q8_K) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) byte_pairs(dw[i] ^ 0x80808080u, &pw[2 * i]);
+  } else if constexpr (SCH == SCH_Q2_K) {
+    // bits 2j..2j+1 of the half's 32 qs bytes (elements 0..15: bytes 0..15)
+    const uint32_t sh = 2 * dw[10];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t c = (dw[i] >> sh) & 0x03030303u;
+      pw[2 * i] = (c & 0x00030003u) | 0x43004300u;
+      pw[2 * i + 1] = ((c >> 8) & 0x00030003u) | 0x43004300u;
+    }
+  } else if constexpr (SCH == SCH_Q3_K) {
+    // 2 bits (qs bit 2j) + 4 * (hmask bit 4n + j): 0..7 = code + 4
+    const uint32_t off = dw[21] & 3u, j = (dw[21] >> 8) & 3u, n = dw[21] >> 16;
+    const uint32_t qsh = 2 * j, hsh = 4 * n + j;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t hm = off ? align_bytes(dw[i + 1], dw[i], 2) : dw[i];
+      const uint32_t qv = off ? align_bytes(dw[10 + i], dw[9 + i], 2) : dw[9 + i];
+      const uint32_t c = ((qv >> qsh) & 0x03030303u) | (((hm >> hsh) & 0x01010101u) << 2);
+      pw[2 * i] = (c & 0x00070007u) | 0x43004300u;
+      pw[2 * i + 1] = ((c >> 8) & 0x00070007u) | 0x43004300u;
+    }
   } else if constexpr (SCH == SCH_Q4_K) {
     // sub-block blk: the low (0) or high (1) nibbles of the group's 32 bytes
 #pragma unroll
@@ -515,6 +687,27 @@ RLXQ_DEV float q6k_block_dot(const uint32_t* pw, const uint32_t* xr, float d_lo,
     if constexpr (NPL == 2) hi = dot2_f16(pw[8 + t], xr[24 + t], hi);
   }
   return scl * fmaf(d_lo, lo, d_hi * hi);
+}
+
+// Q2_K / Q3_K (bf16 pairs, bias chain_bias): each 16-weight half's chain
+// runs from -bias times the half's x sum (record word NPL*16+3 holds the
+// first half's) and takes its own multiplier; the mins multiply the halves'
+// x sums.
+template <int SCH, int NPL>
+RLXQ_DEV float khalf_block_dot(const uint32_t* pw, const uint32_t* xr, float d_lo, float d_hi, float m_lo,
+                               float m_hi) {
+  const float s = __uint_as_float(xr[NPL * 16 + 0]), s_lo = __uint_as_float(xr[NPL * 16 + 3]);
+  float lo = -chain_bias<SCH>() * s_lo, hi = -chain_bias<SCH>() * (s - s_lo);
+#pragma unroll
+  for (int t = 0; t < 8; t++) {
+    lo = dot2_bf16(pw[t], xr[t], lo);
+    if constexpr (NPL == 2) lo = dot2_bf16(pw[t], xr[16 + t], lo);
+    hi = dot2_bf16(pw[8 + t], xr[8 + t], hi);
+    if constexpr (NPL == 2) hi = dot2_bf16(pw[8 + t], xr[24 + t], hi);
+  }
+  float r = fmaf(d_lo, lo, d_hi * hi);
+  if constexpr (SCH == SCH_Q2_K) r = fmaf(m_lo, s_lo, fmaf(m_hi, s - s_lo, r));
+  return r;
 }
 
 // sum over the block of (bias + code) * x, started at -bias * S so that it

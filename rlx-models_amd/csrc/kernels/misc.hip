@@ -6,7 +6,8 @@
 // One thread per eight consecutive weights (a quarter of a 32-weight block),
 // so that a wave writes 2 KB of contiguous f32 with 16-byte stores.  Q8_0:
 // d*q; Q4_0: d*(q-8); Q4_1: d*q + m (d*q is exact in f32, so the single
-// rounding is the add); Q4_K: (d*sc)*q - dmin*mn (GGML block_q4_K); MXFP4:
+// rounding is the add); Q4_K, Q5_K, Q2_K: (d*sc)*q - dmin*mn (GGML block_q4_K
+// / q5_K / q2_K); Q3_K: (d*(sc-32))*q; Q8_K: d*q; MXFP4:
 // E2M1(code) * 2^(e - 127) (exact); MLX:
 // scale*code rounded, then + bias rounded (no contraction), as
 // crates/rlx-moshi/src/mlx_dequant.rs:66-71 evaluates it.
@@ -62,6 +63,70 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_dequant_rows(
       const float prod = d1 * (float)((s & 1) ? byte >> 4 : byte & 15);
       v[i] = prod - m1;
     }
+  } else if (scheme == SCH_Q5_K) {
+    // sub-block s of super-block b / 8: nibble s & 1 of the group's qs
+    // bytes, fifth bit from qh bit s; w = (d*sc)*code - dmin*mn
+    const int s = b & 7, g = s >> 1;
+    const uint8_t* p = w + r * rb + (int64_t)(b >> 3) * 176;
+    const float d = f16_bits_to_f32((uint32_t)p[0] | ((uint32_t)p[1] << 8));
+    const float dmin = f16_bits_to_f32((uint32_t)p[2] | ((uint32_t)p[3] << 8));
+    const uint8_t* q12 = p + 4;
+    int sc, mn;
+    if (s < 4) {
+      sc = q12[s] & 63;
+      mn = q12[s + 4] & 63;
+    } else {
+      sc = (q12[s + 4] & 15) | ((q12[s - 4] >> 6) << 4);
+      mn = (q12[s + 4] >> 4) | ((q12[s] >> 6) << 4);
+    }
+    const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int l = 8 * q + i;
+      const int code = ((p[48 + 32 * g + l] >> (4 * (s & 1))) & 15) | (((p[16 + l] >> s) & 1) << 4);
+      const float prod = d1 * (float)code;
+      v[i] = prod - m1;
+    }
+  } else if (scheme == SCH_Q3_K || scheme == SCH_Q2_K) {
+    // block (n, j) = (b % 8 / 4, b % 4) of super-block b / 8; its weights
+    // 16i + l (i < 2) have code bits 2j of qs byte 32n + 16i + l and
+    // scale 8n + 2j + i
+    const int bb = b & 7, n = bb >> 2, j = bb & 3, i = q >> 1;
+    const int s = 8 * n + 2 * j + i;
+    if (scheme == SCH_Q3_K) {
+      // w = (d * (scale - 32)) * (2 bits - (hmask bit 4n + j ? 0 : 4))
+      const uint8_t* p = w + r * rb + (int64_t)(b >> 3) * 110;
+      const uint8_t* sc12 = p + 96;
+      const int sc = ((sc12[s & 7] >> (4 * (s >> 3))) & 15) | (((sc12[8 + (s & 3)] >> (2 * (s >> 2))) & 3) << 4);
+      const float dl = f16_bits_to_f32((uint32_t)p[108] | ((uint32_t)p[109] << 8)) * (float)(sc - 32);
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const int l = 8 * (q & 1) + t;
+        const int lo = (p[32 + 32 * n + 16 * i + l] >> (2 * j)) & 3;
+        const int hi = (p[16 * i + l] >> (4 * n + j)) & 1;
+        v[t] = dl * (float)(lo - (hi ? 0 : 4));
+      }
+    } else {
+      // w = (d * (c & 15)) * code - dmin * (c >> 4), c = scales[s]
+      const uint8_t* p = w + r * rb + (int64_t)(b >> 3) * 84;
+      const int c = p[s];
+      const float d = f16_bits_to_f32((uint32_t)p[80] | ((uint32_t)p[81] << 8));
+      const float dmin = f16_bits_to_f32((uint32_t)p[82] | ((uint32_t)p[83] << 8));
+      const float dl = d * (float)(c & 15), ml = dmin * (float)(c >> 4);
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const int l = 8 * (q & 1) + t;
+        const float prod = dl * (float)((p[16 + 32 * n + 16 * i + l] >> (2 * j)) & 3);
+        v[t] = prod - ml;
+      }
+    }
+  } else if (scheme == SCH_Q8_K) {
+    // w = d * q, d the super-block's f32
+    const uint8_t* p = w + r * rb + (int64_t)(b >> 3) * 292;
+    const float d = __uint_as_float((uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
+                                    ((uint32_t)p[3] << 24));
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = d * (float)(int8_t)p[4 + 32 * (b & 7) + 8 * q + i];
   } else if (scheme == SCH_MXFP4) {
     // codes 8q..8q+7 of the block are dword 4b + q of the row (low nibble =
     // even element); w = E2M1(code) * scale, exact.  sb_bf16: 2 = E8M0 bytes,

@@ -142,7 +142,8 @@ RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, 
   const int NPASS = a.tile_rows / 4 / RP;  // row passes per wave
   constexpr int D = MOE_RING;
   constexpr bool SLAB = slab_scales<SCH>(), SBIAS = slab_bias<SCH>();
-  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SBIAS);
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SCH == SCH_Q5_K || SBIAS);
+  constexpr bool HALF2 = SCH == SCH_Q2_K || SCH == SCH_Q3_K;   // two scales (and mins) per block
   extern __shared__ uint32_t lds[];
   __shared__ float res[SWIGLU ? MT * MOE_TILE_MAX : 1];
 
@@ -209,17 +210,21 @@ RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, 
           }
 #pragma unroll
           for (int bl = 0; bl < BLOCKS; bl++) {
-            float dd, mn;
+            float dd, mn, d2 = 0.f, m2 = 0.f;
             if constexpr (SLAB) {
               const int64_t gi = ((int64_t)e * a.N + nn) * gpr + ((uc * BLOCKS + bl) * 32) / a.group;
               dd = scale_decode<SCH>(load_scale_raw<SCH>(a.scales, gi, a.sb_bf16), a.sb_bf16);
               mn = SBIAS ? load_sb(a.biases, gi, a.sb_bf16 != 0) : 0.f;
+            } else if constexpr (HALF2) {
+              block_scales_half<SCH>(ring[d], dd, d2, mn, m2);
             } else {
               block_scales<SCH>(ring[d], bl, dd, mn, uc);
             }
             if (!(rok && uok)) {
               dd = 0.f;
               mn = 0.f;
+              d2 = 0.f;
+              m2 = 0.f;
             }
             uint32_t pw[16];
             block_pairs<SCH>(ring[d], bl, pw, kc);
@@ -235,6 +240,10 @@ RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, 
               }
               if constexpr (SCH == SCH_Q6_K) {   // per-half scales: dd, mn = d * scale of each half
                 acc[m] += q6k_block_dot<NPL>(pw, xrec, dd, mn);
+                continue;
+              }
+              if constexpr (HALF2) {
+                acc[m] += khalf_block_dot<SCH, NPL>(pw, xrec, dd, d2, mn, m2);
                 continue;
               }
               const float cc = block_dot<SCH, NPL>(pw, xrec);
@@ -653,6 +662,12 @@ RLXQ_MOE_SCHEME(mlx8, SCH_MLX8)
 RLXQ_MOE_SCHEME(mxfp4, SCH_MXFP4)
 RLXQ_MOE_SCHEME(q4_k, SCH_Q4_K)
 RLXQ_MOE_SCHEME(q6_k, SCH_Q6_K)
+#endif
+#if RLXQ_PART_IS(4)
+RLXQ_MOE_SCHEME(q5_k, SCH_Q5_K)
+RLXQ_MOE_SCHEME(q8_k, SCH_Q8_K)
+RLXQ_MOE_SCHEME(q3_k, SCH_Q3_K)
+RLXQ_MOE_SCHEME(q2_k, SCH_Q2_K)
 #endif
 
 // Register-activation variants (4-bit codes, bf16 activations):

@@ -16,6 +16,7 @@ HEADER = PKG.parent / "include" / "rlxq.h"
 
 GGUF_Q8_0, GGUF_Q4_0, GGUF_Q4_1, MLX_AFFINE4, MLX_AFFINE8, INT8_BLOCK, GGUF_Q4_K, GGUF_Q6_K = 1, 2, 3, 4, 5, 6, 7, 8
 MLX_MXFP4 = 9
+GGUF_Q5_K, GGUF_Q3_K, GGUF_Q2_K, GGUF_Q8_K = 10, 11, 12, 13
 F32, BF16, U8 = 0, 1, 2
 MOE_EXPAND, MOE_COMBINE, MOE_EXPAND_SWIGLU = 0, 1, 2
 OK = 0
@@ -177,7 +178,8 @@ def _dt(t) -> int:
 # checks run before every call of the wrappers below and raise ValueError, so
 # a wrong n, num_experts or output buffer never reaches a kernel.
 
-_PACKED = (GGUF_Q8_0, GGUF_Q4_0, GGUF_Q4_1, MLX_AFFINE4, MLX_AFFINE8, GGUF_Q4_K, GGUF_Q6_K, MLX_MXFP4)
+_PACKED = (GGUF_Q8_0, GGUF_Q4_0, GGUF_Q4_1, MLX_AFFINE4, MLX_AFFINE8, GGUF_Q4_K, GGUF_Q6_K, MLX_MXFP4,
+           GGUF_Q5_K, GGUF_Q3_K, GGUF_Q2_K, GGUF_Q8_K)
 
 
 def packed_row_bytes(scheme: int, k: int) -> int:

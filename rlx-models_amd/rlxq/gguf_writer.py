@@ -19,6 +19,7 @@ _FMT = {0: "B", 1: "b", 2: "H", 3: "h", 4: "I", 5: "i", 6: "f", 7: "?", 10: "Q",
 
 # ggml type ids used by the tests
 F32, F16, Q4_0, Q4_1, Q8_0, Q4_K, Q6_K, Q5_K, BF16 = 0, 1, 2, 3, 8, 12, 14, 13, 30
+Q2_K, Q3_K, Q8_K = 10, 11, 15
 
 
 def _str(s: str) -> bytes:

@@ -18,7 +18,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from rlxq.gguf_writer import BF16, F16, F32, Q4_0, Q4_1, Q4_K, Q5_K, Q6_K, Q8_0, gguf_bytes, write_gguf
+from rlxq.gguf_writer import BF16, F16, F32, Q2_K, Q3_K, Q4_0, Q4_1, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K, gguf_bytes, write_gguf
 
 FIXTURE = Path(__file__).parent / "golden" / "bonsai2_manifest.gguf"
 FIXTURE_SHA256 = "a5f3ba541001c302e16a2005bb5aa7d4464ca71ad384f109cbc3a9d2ecdc7726"
@@ -142,6 +142,10 @@ LAYOUT = [
     ("token_embd.weight", F16, [32, 10], 2, 1),
     ("blk.1.attn_q.weight", Q5_K, [256, 8], 176, 256),
     ("output.weight", BF16, [32, 7], 2, 1),
+    ("blk.1.attn_k.weight", 6, [64, 4], 22, 32),          # Q5_0: not served, stays unpacked
+    ("blk.1.ffn_up.weight", Q3_K, [256, 6], 110, 256),
+    ("blk.1.ffn_down.weight", Q2_K, [512, 3], 84, 256),
+    ("blk.1.ffn_gate.weight", Q8_K, [256, 5], 292, 256),
 ]
 
 
@@ -218,6 +222,10 @@ def test_take_packed_rules(tmp_path):
         "blk.0.ffn_up.weight": (rlxq.GGUF_Q4_K, [24, 512], 24 * 2 * 144),
         "blk.0.ffn_gate.weight": (rlxq.GGUF_Q6_K, [40, 256], 40 * 210),
         "blk.0.ffn_gate_exps.weight": (rlxq.GGUF_Q4_1, [3, 24, 64], 3 * 24 * 2 * 20),
+        "blk.1.attn_q.weight": (rlxq.GGUF_Q5_K, [8, 256], 8 * 176),
+        "blk.1.ffn_up.weight": (rlxq.GGUF_Q3_K, [6, 256], 6 * 110),
+        "blk.1.ffn_down.weight": (rlxq.GGUF_Q2_K, [3, 512], 3 * 2 * 84),
+        "blk.1.ffn_gate.weight": (rlxq.GGUF_Q8_K, [5, 256], 5 * 292),
     }
     for name, w in want.items():
         assert f.get(name).scheme == w[0]
@@ -226,7 +234,7 @@ def test_take_packed_rules(tmp_path):
             f.take_packed(name)
         assert e.value.status == rlxq.E_TAKEN and "already taken" in str(e.value)
         assert f.read(name).size == w[2]   # reading bytes does not depend on the taken mark
-    for name in ("blk.0.attn_norm.weight", "token_embd.weight", "output.weight", "blk.1.attn_q.weight"):
+    for name in ("blk.0.attn_norm.weight", "token_embd.weight", "output.weight", "blk.1.attn_k.weight"):
         assert f.get(name).scheme == 0
         assert f.take_packed(name) is None
         assert f.take_packed(name) is None   # not taken
@@ -238,9 +246,10 @@ def test_take_packed_rules(tmp_path):
 
 def test_block_layouts_match_the_kernels(tmp_path):
     """Packed bytes per row agree with rlxq_row_bytes for the schemes the
-    kernels read (Q4_0 18, Q4_1 20, Q8_0 34 B per 32; Q4_K 144, Q6_K 210 B
-    per 256: block_q6_K is ql[128] + qh[64] + scales[16] + d, the
-    reference's probe block, weight_loader.rs:573-581)."""
+    kernels read (Q4_0 18, Q4_1 20, Q8_0 34 B per 32; Q4_K 144, Q6_K 210,
+    Q5_K 176, Q3_K 110, Q2_K 84, Q8_K 292 B per 256: block_q6_K is ql[128] +
+    qh[64] + scales[16] + d, the reference's probe block,
+    weight_loader.rs:573-581)."""
     import rlxq
 
     path = tmp_path / "m.gguf"

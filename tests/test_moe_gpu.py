@@ -501,11 +501,15 @@ def test_grouped_register_path_mlx4(ctx, orc, k, group, sb):
 
 
 # ----------------------------------------- K-quant experts (Q4_K_M MoE files)
-@pytest.mark.parametrize("scheme", [7, 8], ids=["q4_k", "q6_k"])
+KQ_NAMES = {7: "q4_k", 8: "q6_k", 10: "q5_k", 11: "q3_k", 12: "q2_k", 13: "q8_k"}
+
+
+@pytest.mark.parametrize("scheme", list(KQ_NAMES), ids=list(KQ_NAMES.values()))
 @pytest.mark.parametrize("xdt", ["f32", "bf16"])
 def test_grouped_k_quants(ctx, orc, scheme, xdt):
-    """GGUF Q4_K / Q6_K expert stacks through the grouped op (the formats of
-    Q4_K_M MoE checkpoints), on the LDS-record kernels."""
+    """GGUF K-quant expert stacks through the grouped op (Q4_K / Q6_K: the
+    formats of Q4_K_M MoE checkpoints; Q5_K, Q3_K, Q2_K, Q8_K: the rest of
+    the reference's DeviceMatmul table), on the LDS-record kernels."""
     import torch
 
     rows, k, n, E = 20, 1024, 320, 6
@@ -518,11 +522,11 @@ def test_grouped_k_quants(ctx, orc, scheme, xdt):
     idx = ((np.arange(rows) * 5 + 1) % E).astype(np.float32)
     y = ctx.grouped_matmul(xt, _t(bank), _t(idx), scheme, n, E)
     torch.cuda.synchronize()
-    assert ("q4_k" if scheme == 7 else "q6_k") in ctx.last_kernel
+    assert KQ_NAMES[scheme] in ctx.last_kernel, ctx.last_kernel
     assert rel_err(y.cpu().numpy(), orc.grouped_matmul_f64(scheme, xv, bank, idx, n, E)) <= TOL
 
 
-@pytest.mark.parametrize("scheme", [7, 8], ids=["q4_k", "q6_k"])
+@pytest.mark.parametrize("scheme", list(KQ_NAMES), ids=list(KQ_NAMES.values()))
 def test_moe_ffn_k_quants(ctx, orc, scheme):
     """Route, EXPAND_SWIGLU and COMBINE over K-quant banks (Qwen3-30B-A3B's
     expert shapes, 32 experts) against the float64 chain."""

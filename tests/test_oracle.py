@@ -534,6 +534,246 @@ def test_q6k_reference_probe_block(orc):
     np.testing.assert_array_equal(got, want)
 
 
+# ------------------------------------------------------------------ Q5_K
+# GGML block_q5_K (the reference maps GgmlType::Q5K to QuantScheme::GgufQ5K,
+# crates/rlx-models-core/src/weight_loader.rs:503, and decodes it with the
+# absent rlx_gguf::dequant_q5_k): f16 d, f16 dmin, the 12 Q4_K scale bytes,
+# qh[32], qs[128].  Probes: every code bit alone moves one weight by its
+# place value, at the weight the layout names.
+
+def _q5k_unit(d=1.0, dmin=0.0):
+    b = np.zeros(176, np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    b[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    return b
+
+
+def _set_q4k_scales(b, off, sc, mn, orc):
+    b[off:off + 12] = orc.q4k_pack_scales(np.asarray(sc), np.asarray(mn))
+
+
+def test_q5k_low_bits_reach_the_right_weight(orc):
+    """qs byte 32g + l, bit t: weight 64g + 32 (t >= 4) + l moves by
+    2^(t % 4), all scales 1."""
+    for byte in range(128):
+        for bit in range(8):
+            b = _q5k_unit()
+            _set_q4k_scales(b, 4, [1] * 8, [0] * 8, orc)
+            b[48 + byte] = 1 << bit
+            got = orc.dequantize(orc.Q5_K, b, 256)[0]
+            g, l = divmod(byte, 32)
+            want = np.zeros(256, np.float32)
+            want[64 * g + 32 * (bit // 4) + l] = 1 << (bit % 4)
+            np.testing.assert_array_equal(got, want, err_msg=f"qs byte {byte} bit {bit}")
+
+
+def test_q5k_high_bits_reach_the_right_weight(orc):
+    """qh byte l, bit t: the fifth code bit (16) of weight 32t + l."""
+    for byte in range(32):
+        for bit in range(8):
+            b = _q5k_unit()
+            _set_q4k_scales(b, 4, [1] * 8, [0] * 8, orc)
+            b[16 + byte] = 1 << bit
+            got = orc.dequantize(orc.Q5_K, b, 256)[0]
+            want = np.zeros(256, np.float32)
+            want[32 * bit + byte] = 16.0
+            np.testing.assert_array_equal(got, want, err_msg=f"qh byte {byte} bit {bit}")
+
+
+def test_q5k_scales_and_mins_per_sub_block(orc, rng):
+    """Sub-block s (weights 32s..32s+31) takes scale s and min s of the
+    Q4_K packing: w = (d * sc) * code - dmin * mn, products rounded to f32,
+    then the subtraction."""
+    for _ in range(8):
+        b = _q5k_unit(d=0.25, dmin=0.125)
+        sc = rng.integers(0, 64, 8)
+        mn = rng.integers(0, 64, 8)
+        _set_q4k_scales(b, 4, sc, mn, orc)
+        b[16:176] = rng.integers(0, 256, 160, dtype=np.uint8)
+        got = orc.dequantize(orc.Q5_K, b, 256)[0]
+        for e in range(256):
+            s, l = divmod(e, 32)
+            g, h = divmod(s, 2)
+            code = ((int(b[48 + 32 * g + l]) >> (4 * h)) & 15) | (((int(b[16 + l]) >> s) & 1) << 4)
+            want = np.float32(np.float32(0.25 * sc[s]) * np.float32(code)) - np.float32(0.125 * mn[s])
+            assert got[e] == want, (e, got[e], want)
+
+
+def test_q5k_rows_and_matmul(orc, rng):
+    n, k = 5, 768
+    w = orc.synth_q5_k(rng, n, k)
+    assert w.shape == (n, 3 * 176) and orc.row_bytes(orc.Q5_K, k) == 528
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    deq = orc.dequantize(orc.Q5_K, w, k).astype(np.float64)
+    np.testing.assert_allclose(orc.matmul_f64(orc.Q5_K, x, w, n), x.astype(np.float64) @ deq.T, rtol=1e-12)
+
+
+# ------------------------------------------------------------------ Q3_K
+# GGML block_q3_K (GgmlType::Q3K -> QuantScheme::GgufQ3K,
+# weight_loader.rs:500; absent rlx_gguf::dequant_q3_k): hmask[32], qs[64],
+# 12 bytes of sixteen 6-bit scales, f16 d; w = d * (scale - 32) * code with
+# code = 2 low bits - (4 unless the hmask bit is set).
+
+def _q3k_unit(scales=None, d=1.0):
+    from oracle import oracle as o
+
+    b = np.zeros(110, np.uint8)
+    b[96:108] = o.q3k_pack_scales(np.full(16, 33) if scales is None else np.asarray(scales))
+    b[108:110] = np.array([d], np.float16).view(np.uint8)
+    return b
+
+
+def test_q3k_scale_bits_reach_the_right_scale(orc):
+    """Each of the 96 scale bits alone: byte t < 8, bit i sets bit i % 4 of
+    scale t + 8 (i // 4); byte 8 + t, bit i sets bit 4 + i % 2 of scale
+    t + 4 (i // 2) -- GGML's aux[] unpacking of block_q3_K.scales."""
+    for byte in range(12):
+        for bit in range(8):
+            q = np.zeros(12, np.uint8)
+            q[byte] = 1 << bit
+            got = [orc.q3k_scale(q, s) for s in range(16)]
+            want = [0] * 16
+            if byte < 8:
+                want[byte + 8 * (bit // 4)] = 1 << (bit % 4)
+            else:
+                want[(byte - 8) + 4 * (bit // 2)] = 1 << (4 + bit % 2)
+            assert got == want, (byte, bit, got)
+
+
+def test_q3k_scale_packing_round_trip(orc, rng):
+    for _ in range(50):
+        sc = rng.integers(0, 64, 16)
+        q = orc.q3k_pack_scales(sc)
+        assert [orc.q3k_scale(q, s) for s in range(16)] == list(sc)
+
+
+def test_q3k_low_bits_reach_the_right_weight(orc):
+    """qs byte 32n + 16i + l, bit pair j: weight 128n + 32j + 16i + l, the
+    hmask bits all set (no -4), all scales 33 (scale - 32 = 1)."""
+    for byte in range(64):
+        for bit in range(8):
+            b = _q3k_unit()
+            b[0:32] = 0xFF
+            b[32 + byte] = 1 << bit
+            got = orc.dequantize(orc.Q3_K, b, 256)[0]
+            n, r = divmod(byte, 32)
+            i, l = divmod(r, 16)
+            want = np.zeros(256, np.float32)
+            want[128 * n + 32 * (bit // 2) + 16 * i + l] = 1 << (bit % 2)
+            np.testing.assert_array_equal(got, want, err_msg=f"qs byte {byte} bit {bit}")
+
+
+def test_q3k_hmask_bits_reach_the_right_weight(orc):
+    """hmask byte 16i + l, bit t (t = 4n + j): only weight 128n + 32j + 16i + l
+    escapes the -4 offset (codes 0, scales 33)."""
+    for byte in range(32):
+        for bit in range(8):
+            b = _q3k_unit()
+            b[byte] = 1 << bit
+            got = orc.dequantize(orc.Q3_K, b, 256)[0]
+            n, j = divmod(bit, 4)
+            i, l = divmod(byte, 16)
+            want = np.full(256, -4.0, np.float32)
+            want[128 * n + 32 * j + 16 * i + l] = 0.0
+            np.testing.assert_array_equal(got, want, err_msg=f"hmask byte {byte} bit {bit}")
+
+
+def test_q3k_scales_cover_sixteen_weights_each(orc):
+    """Scale s multiplies weights 16s..16s+15, signed (scale - 32)."""
+    for s in range(16):
+        sc = np.full(16, 32)
+        sc[s] = 29                                     # -3
+        b = _q3k_unit(scales=sc, d=0.5)
+        got = orc.dequantize(orc.Q3_K, b, 256)[0]     # codes 0, hmask 0: code -4
+        want = np.zeros(256, np.float32)
+        want[16 * s:16 * s + 16] = 0.5 * -3 * -4
+        np.testing.assert_array_equal(got, want)
+
+
+def test_q3k_rows_and_matmul(orc, rng):
+    n, k = 4, 512
+    w = orc.synth_q3_k(rng, n, k)
+    assert w.shape == (n, 2 * 110) and orc.row_bytes(orc.Q3_K, k) == 220
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    deq = orc.dequantize(orc.Q3_K, w, k).astype(np.float64)
+    np.testing.assert_allclose(orc.matmul_f64(orc.Q3_K, x, w, n), x.astype(np.float64) @ deq.T, rtol=1e-12)
+
+
+# ------------------------------------------------------------------ Q2_K
+# GGML block_q2_K (GgmlType::Q2K -> QuantScheme::GgufQ2K,
+# weight_loader.rs:499; absent rlx_gguf::dequant_q2_k): scales[16] (scale
+# nibble, min nibble), qs[64], f16 d, f16 dmin.
+
+def _q2k_unit(d=1.0, dmin=0.0, sc=0x01):
+    b = np.zeros(84, np.uint8)
+    b[0:16] = sc
+    b[80:82] = np.array([d], np.float16).view(np.uint8)
+    b[82:84] = np.array([dmin], np.float16).view(np.uint8)
+    return b
+
+
+def test_q2k_code_bits_reach_the_right_weight(orc):
+    """qs byte 32n + 16i + l, bit pair j: weight 128n + 32j + 16i + l."""
+    for byte in range(64):
+        for bit in range(8):
+            b = _q2k_unit()
+            b[16 + byte] = 1 << bit
+            got = orc.dequantize(orc.Q2_K, b, 256)[0]
+            n, r = divmod(byte, 32)
+            i, l = divmod(r, 16)
+            want = np.zeros(256, np.float32)
+            want[128 * n + 32 * (bit // 2) + 16 * i + l] = 1 << (bit % 2)
+            np.testing.assert_array_equal(got, want, err_msg=f"qs byte {byte} bit {bit}")
+
+
+def test_q2k_scale_and_min_per_sixteen(orc):
+    """scales[t]: low nibble times d scales weights 16t..16t+15, high nibble
+    times dmin is subtracted from them."""
+    for t in range(16):
+        b = _q2k_unit(d=0.5, dmin=0.25, sc=0)
+        b[t] = 0x3 | (0x5 << 4)
+        b[16:80] = 0xFF                                # every code 3
+        got = orc.dequantize(orc.Q2_K, b, 256)[0]
+        want = np.zeros(256, np.float32)
+        want[16 * t:16 * t + 16] = 0.5 * 3 * 3 - 0.25 * 5
+        np.testing.assert_array_equal(got, want)
+
+
+def test_q2k_rows_and_matmul(orc, rng):
+    n, k = 4, 512
+    w = orc.synth_q2_k(rng, n, k)
+    assert w.shape == (n, 2 * 84) and orc.row_bytes(orc.Q2_K, k) == 168
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    deq = orc.dequantize(orc.Q2_K, w, k).astype(np.float64)
+    np.testing.assert_allclose(orc.matmul_f64(orc.Q2_K, x, w, n), x.astype(np.float64) @ deq.T, rtol=1e-12)
+
+
+# ------------------------------------------------------------------ Q8_K
+# GGML block_q8_K (GgmlType::Q8K -> QuantScheme::GgufQ8K,
+# weight_loader.rs:504): f32 d, int8 qs[256], int16 bsums[16].
+
+def test_q8k_is_f32_scale_times_int8(orc, rng):
+    w = orc.synth_q8_k(rng, 3, 512)
+    got = orc.dequantize(orc.Q8_K, w, 512)
+    for r in range(3):
+        for sb in range(2):
+            blk = w[r, 292 * sb:292 * (sb + 1)]
+            d = blk[0:4].view(np.float32)[0]
+            q = blk[4:260].view(np.int8).astype(np.float32)
+            np.testing.assert_array_equal(got[r, 256 * sb:256 * (sb + 1)], d * q)
+            # the synthetic bsums are the format's own sums of 16 codes
+            np.testing.assert_array_equal(blk[260:292].view(np.int16), q.reshape(16, 16).sum(1).astype(np.int16))
+
+
+def test_q8k_rows_and_matmul(orc, rng):
+    n, k = 4, 256
+    w = orc.synth_q8_k(rng, n, k)
+    assert orc.row_bytes(orc.Q8_K, k) == 292
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    deq = orc.dequantize(orc.Q8_K, w, k).astype(np.float64)
+    np.testing.assert_allclose(orc.matmul_f64(orc.Q8_K, x, w, n), x.astype(np.float64) @ deq.T, rtol=1e-12)
+
+
 # ------------------------------------------------------------------ MXFP4
 # The oracle's MXFP4 codec against the reference's own tests of its encoder
 # and decoder (crates/rlx-models-core/src/mxfp4_pack.rs:290-398) and the E8M0
