@@ -205,7 +205,7 @@ int rlxq_w8a8_gemm(rlxq_ctx* ctx, const void* x, int x_dtype, const int8_t* wq, 
   a.tiles_n = (int32_t)tiles_n;
   a.y_bf16 = y_dtype == RLXQ_BF16;
   const int64_t grid = 8 * ((tiles_m * tiles_n + 7) / 8);
-  const size_t lds = 2 * (size_t)c->BM * (c->BK + 16) + 2 * (size_t)c->BK * (c->BN + 16);
+  const size_t lds = 2 * (size_t)c->BM * (c->BK + 16) + 2 * (size_t)c->BK * (c->BN + 32);
   void* args[] = {&a};
   return launch(ctx, fn, dim3((unsigned)grid), dim3(64 * c->WGM * c->WGN), lds, stream, args, name);
 }

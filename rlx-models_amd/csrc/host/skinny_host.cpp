@@ -163,8 +163,9 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
 }  // namespace
 
 bool skinny_applies(int scheme, int64_t m, int64_t k) {
-  return (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q4_1) && m >= 1 &&
-         m <= 256 && k % 128 == 0;
+  return (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q4_1 ||
+          (scheme == RLXQ_GGUF_Q4_K && k % 256 == 0)) &&
+         m >= 1 && m <= 256 && k % 128 == 0;
 }
 
 // Workgroups: (128 weight rows, K split, 64-row chunk).  K splits only where
@@ -176,13 +177,13 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   // The register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR="MT,NT,D"
   // picks a compiled one (every combination for Q4_1, the defaults for Q4_0
   // and Q8_0), "0" the LDS-staged kernels below.
-  // The N-split kernel (activations shared through LDS): Q4_1 past 16 rows,
+  // The N-split kernel (activations shared through LDS): Q4_1 (and Q4_K) past 16 rows,
   // where it measured 5-13% faster than the register-streamed one (at 16 rows
   // and below, and for Q8_0, it was slower).  RLXQ_SKINNY_NS="MT,NT,D" picks
   // a compiled one for any scheme, "0" turns the default off.
   {
     int nmt = m <= 32 ? 2 : 4, nnt = 1, nd = 3;
-    bool ns = scheme == RLXQ_GGUF_Q4_1 && m > 16;
+    bool ns = (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_K) && m > 16;
     if (const char* e = std::getenv("RLXQ_SKINNY_NS")) {
       int a1, a2, a3;
       if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) nmt = a1, nnt = a2, nd = a3, ns = true;
@@ -193,11 +194,12 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   }
   {
     int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = 2, xd = m <= 16 ? 4 : (m <= 32 ? 3 : 2);
+    if (scheme == RLXQ_GGUF_Q4_K) xd = m <= 16 ? 3 : 2;   // its 13-dword raw blocks
     bool xr = true;
     if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
       int a1, a2, a3;
       if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) xmt = a1, xnt = a2, xd = a3;
-      else if (e[0] == '0') xr = false;
+      else if (e[0] == '0') xr = scheme == RLXQ_GGUF_Q4_K;   // (Q4_K has no LDS-staged kernel)
     }
     if (xr) return skinny_xr_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, xmt, xnt, xd);
   }

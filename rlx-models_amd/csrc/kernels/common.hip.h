@@ -65,7 +65,13 @@ RLXQ_DEV uint32_t fp4x2_to_bf16x2(uint32_t w) {
 // 16-byte head held as dwords (head[0] = f16 d | f16 dmin << 16, head[1..3] =
 // the 12 packed bytes), GGML's packing.
 RLXQ_DEV void q4k_scale_min(const uint32_t* head, int s, float& sc, float& mn) {
-  auto byte = [&](int i) { return (head[1 + (i >> 2)] >> (8 * (i & 3))) & 0xffu; };
+  // (the dword picked by selects, not by a runtime array index, which would
+  // keep the caller's copy of the head in scratch memory)
+  const uint32_t h1 = head[1], h2 = head[2], h3 = head[3];
+  auto byte = [&](int i) {
+    const uint32_t w = i < 4 ? h1 : (i < 8 ? h2 : h3);
+    return (w >> (8 * (i & 3))) & 0xffu;
+  };
   uint32_t a, b;
   if (s < 4) {
     a = byte(s) & 63u;

@@ -15,6 +15,7 @@ namespace rlxq {
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // Element of a 32-block held at position p (see above).
 RLXQ_DEV int perm_k(int p, bool nibble) {
@@ -24,7 +25,10 @@ RLXQ_DEV int perm_k(int p, bool nibble) {
 }
 
 
-// Normalised LDS block: scale dword (Q4_1: d | m << 16, else d) + code dwords.
+// Normalised block: scale dword (Q4_1, Q4_K: d | m << 16, else d) + code
+// dwords.  A Q4_K sub-block normalises to the Q4_1 form: d = d * sc and
+// m = -dmin * mn rounded to f16, and code dword g holding elements 4g..4g+3
+// (low nibbles) and 16 + 4g.. (high nibbles) of the sub-block.
 template <int SCH> constexpr int sk_bdw() { return SCH == SCH_Q8_0 ? 9 : 5; }
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
@@ -56,7 +60,7 @@ RLXQ_DEV f16x8_t dequant_lane(const uint32_t* bp, int g) {
   } else {
     const uint32_t qs = bp[1 + g];
     const uint32_t lo = qs & 0x0F0F0F0Fu, hi = (qs >> 4) & 0x0F0F0F0Fu;
-    if constexpr (SCH == SCH_Q4_1) {
+    if constexpr (SCH == SCH_Q4_1 || SCH == SCH_Q4_K) {
       const f16x2_t m2 = as_h2(perm_b32(dm, dm, 0x03020302u));
       const f16x2_t off = {(_Float16)-1024.f, (_Float16)-1024.f};
       w[0] = __builtin_elementwise_fma(magic_lo(lo) + off, d2, m2);
@@ -77,7 +81,18 @@ RLXQ_DEV f16x8_t dequant_lane(const uint32_t* bp, int g) {
 // Raw block -> normalised dwords.
 template <int SCH>
 RLXQ_DEV void normalise(const RawBlk<SCH>& r, uint32_t* o) {
-  if constexpr (SCH == SCH_Q4_1) {
+  if constexpr (SCH == SCH_Q4_K) {
+    const uint32_t hd[4] = {r.hd.x, r.hd.y, r.hd.z, r.hd.w};
+    float sc, mn;
+    q4k_scale_min(hd, (int)r.sub, sc, mn);
+    const uint32_t d1 = f32_to_f16_bits(f16_bits_to_f32(hd[0] & 0xffffu) * sc);
+    const uint32_t m1 = f32_to_f16_bits(-(f16_bits_to_f32(hd[0] >> 16) * mn));
+    o[0] = d1 | (m1 << 16);
+    const uint32_t qs[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    const uint32_t sh = 4 * (r.sub & 1u);
+#pragma unroll
+    for (int g = 0; g < 4; g++) o[1 + g] = ((qs[g] >> sh) & 0x0F0F0F0Fu) | (((qs[4 + g] >> sh) & 0x0F0F0F0Fu) << 4);
+  } else if constexpr (SCH == SCH_Q4_1) {
     o[0] = r.h;
     o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;
   } else {

@@ -69,7 +69,11 @@ RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int AST = BK + 16;  // A row stride (bytes): 16-byte reads of 8 rows hit distinct banks
-  constexpr int BST = BN + 16;  // B row stride: transpose reads of 8 rows hit distinct banks
+  // B row stride: a transpose read covers 8 rows x 32 bytes per 32 lanes, so
+  // the stride is an odd multiple of 32 bytes (8 banks per row, the 8 rows on
+  // distinct banks); BN + 16 had each row's second 16 bytes on the next
+  // row's banks
+  constexpr int BST = BN + 32;
   constexpr int ACH = BK / 16, BCH = BN / 16;
   constexpr int AP = BM * ACH / NT, BP = BK * BCH / NT;
   static_assert((BM * ACH) % NT == 0 && (BK * BCH) % NT == 0, "tile / threads");

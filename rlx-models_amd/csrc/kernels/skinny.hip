@@ -1,6 +1,7 @@
 // Batched-decode dequant-GEMM for small M (the multi-row decode path):
 // y[m, n] = sum_k x[m, k] * dequant(W)[n, k] for up to 64 activation rows and
-// GGUF Q8_0 / Q4_0 / Q4_1 weights, streaming every weight once for all rows.
+// GGUF Q8_0 / Q4_0 / Q4_1 / Q4_K weights, streaming every weight once for all
+// rows.
 // Replaces the backend kernel of Op::DequantMatMul at decode batch sizes
 // (crates/rlx-models-core/src/standard_decoder.rs:727-738, M rows per call).
 //
@@ -581,25 +582,26 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
   // this thread's activation piece: row 16 u + j of the m-chunk, block 4c + g,
   // positions 8 wv .. 8 wv + 7 (fragment-major source; the Mp rows cover
   // every m-chunk)
-  const uint4* xsrc = reinterpret_cast<const uint4*>(a.x16) + (wv * a.Mp + m0 + j) * 4 + g;
+  const u32x4_t* xsrc = reinterpret_cast<const u32x4_t*>(a.x16) + (wv * a.Mp + m0 + j) * 4 + g;
 
-  struct Stage {
-    RawBlk<SCH> w[NT];
-    uint4 x[MT];
-  };
+  // ring slot d: a step's weight blocks wr[d] and activation pieces xr[d]
+  // (pieces held as a clang vector type: a ring of HIP's uint4 struct, or
+  // one struct of both rings, stayed in scratch memory for some schemes)
+  RawBlk<SCH> wr[D][NT];
+  u32x4_t xr[D][MT];
   // steps past the last repeat it (their data is never used), so every step
   // issues the same loads
-  auto load = [&](int s, Stage& st) {
+  auto load = [&](int s, int d) {
     const int64_t c = kb / 128 + (s < nsteps ? s : nsteps - 1);
 #pragma unroll
-    for (int u = 0; u < MT; u++) st.x[u] = xsrc[(4 * c * a.Mp + 16 * u) * 4];
+    for (int u = 0; u < MT; u++) xr[d][u] = xsrc[(4 * c * a.Mp + 16 * u) * 4];
 #pragma unroll
-    for (int t = 0; t < NT; t++) load_blk<SCH>(ga, wrow[t], 4 * c + g, wok[t], st.w[t]);
+    for (int t = 0; t < NT; t++) load_blk<SCH>(ga, wrow[t], 4 * c + g, wok[t], wr[d][t]);
   };
-  auto put = [&](int s, const Stage& st) {
+  auto put = [&](int s, int d) {
     uint8_t* slot = sma + (s & 1) * AST;
 #pragma unroll
-    for (int u = 0; u < MT; u++) *reinterpret_cast<uint4*>(slot + (wv * MT + u) * 1024 + lane * 16) = st.x[u];
+    for (int u = 0; u < MT; u++) *reinterpret_cast<u32x4_t*>(slot + (wv * MT + u) * 1024 + lane * 16) = xr[d][u];
   };
   // the LDS stores of this wave have completed; then every wave's have
   auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
@@ -610,11 +612,11 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
 #pragma unroll
     for (int t = 0; t < NT; t++) acc[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int s, const Stage& st) {
+  auto compute = [&](int s, int d) {
     const uint8_t* slot = sma + (s & 1) * AST;
     uint32_t o[NT][BDW];
 #pragma unroll
-    for (int t = 0; t < NT; t++) normalise<SCH>(st.w[t], o[t]);
+    for (int t = 0; t < NT; t++) normalise<SCH>(wr[d][t], o[t]);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       f16x8_t af[MT];
@@ -631,17 +633,16 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
   // step s: ring slot s % D holds step s's weights (and step s's
   // activations, already in LDS slot s & 1); slot (s + 1) % D holds step
   // s + 1's activations, stored now into LDS slot (s + 1) & 1
-  Stage ring[D];
   auto step = [&](int s, int d) {
-    put(s + 1, ring[(d + 1) % D]);
-    compute(s, ring[d]);
-    load(s + D, ring[d]);
+    put(s + 1, (d + 1) % D);
+    compute(s, d);
+    load(s + D, d);
     barrier();
   };
 
 #pragma unroll
-  for (int d = 0; d < D; d++) load(d, ring[d]);
-  put(0, ring[0]);
+  for (int d = 0; d < D; d++) load(d, d);
+  put(0, 0);
   barrier();
   int s0 = 0;
   for (; s0 + D <= nsteps; s0 += D) {
@@ -868,6 +869,10 @@ RLXQ_SKINNYXR_INST(q4_0, SCH_Q4_0, 4, 2, 2)
 RLXQ_SKINNYXR_INST(q8_0, SCH_Q8_0, 1, 2, 4)
 RLXQ_SKINNYXR_INST(q8_0, SCH_Q8_0, 2, 2, 3)
 RLXQ_SKINNYXR_INST(q8_0, SCH_Q8_0, 4, 2, 2)
+// Q4_K sub-blocks (13-dword raw blocks: shallower rings)
+RLXQ_SKINNYXR_INST(q4_k, SCH_Q4_K, 1, 2, 3)
+RLXQ_SKINNYXR_INST(q4_k, SCH_Q4_K, 2, 2, 2)
+RLXQ_SKINNYXR_INST(q4_k, SCH_Q4_K, 4, 2, 2)
 
 // N-split variants: rlxq_skinnyns_<scheme>_mt<MT>_nt<NT>_d<D>.
 #define RLXQ_SKINNYNS_INST(SNAME, SCH, MT, NT, D)                                                      \
@@ -882,3 +887,6 @@ RLXQ_SKINNYNS_INST(q4_1, SCH_Q4_1, 4, 1, 3)
 RLXQ_SKINNYNS_INST(q4_1, SCH_Q4_1, 4, 2, 2)
 RLXQ_SKINNYNS_INST(q8_0, SCH_Q8_0, 4, 2, 2)
 RLXQ_SKINNYNS_INST(q4_0, SCH_Q4_0, 4, 1, 3)
+RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 1, 1, 3)
+RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 2, 1, 3)
+RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 4, 1, 3)

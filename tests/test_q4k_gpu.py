@@ -78,10 +78,12 @@ def test_q4k_every_register_variant(ctx, orc, monkeypatch, cfg, k):
 @pytest.mark.parametrize("xdt", ["f32", "bf16"])
 def test_q4k_record_path(ctx, orc, monkeypatch, m, xdt):
     """The LDS-record GEMV: f32 activations, and every M > 1 (bf16 M = 2..4
-    take the register kernel by default; RLXQ_GEMV_XR=0 keeps them here)."""
+    take the register kernel by default, bf16 M >= 5 the batched-decode MFMA
+    kernels; RLXQ_GEMV_XR=0 and RLXQ_DECODE=gemv keep them here)."""
     if m == 1 and xdt == "bf16":
         pytest.skip("register path")
     monkeypatch.setenv("RLXQ_GEMV_XR", "0")
+    monkeypatch.setenv("RLXQ_DECODE", "gemv")
     k, n = 4096, 520
     announce(f"q4_k gemv m={m} x={xdt}")
     rng = np.random.default_rng(m)

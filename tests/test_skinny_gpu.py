@@ -163,3 +163,63 @@ def test_skinny_every_nsplit_variant(ctx, orc, monkeypatch, cfg):
         assert ctx.last_kernel == f"rlxq_skinnyns_{name}_mt{mt}_nt{nt}_d{d}", ctx.last_kernel
         assert rel_err(got, want) <= TOL_F32, (cfg, m, k, n)
 
+
+
+# Q4_K (GGML block_q4_K, 144-byte super-blocks of 256): the same f16-MFMA
+# kernels after each 32-value sub-block's 6-bit scale and min are folded into
+# one f16 d*sc and m*mn (the Q4_1 form)
+Q4K_XR = ["1,2,3", "2,2,2", "4,2,2"]
+Q4K_NS = ["1,1,3", "2,1,3", "4,1,3"]
+
+
+@pytest.mark.parametrize("mkn", [(5, 256, 7), (16, 4096, 512), (17, 1024, 300), (33, 512, 129),
+                                 (64, 4096, 256), (100, 768, 200), (256, 256, 40)], ids=str)
+def test_skinny_q4_k_default(ctx, orc, mkn):
+    m, k, n = mkn
+    announce(f"skinny q4_k default {mkn}")
+    rng = np.random.default_rng(m * 3 + k + n)
+    packed = orc.synth(7, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[0] *= 300.0
+    got, want = run_dense(ctx, orc, 7, x, packed, n, xdt="bf16")
+    prefix = "rlxq_skinnyxr_q4_k_" if m <= 16 else "rlxq_skinnyns_q4_k_"
+    assert ctx.last_kernel.startswith(prefix), ctx.last_kernel
+    assert rel_err(got, want) <= TOL_F32
+    got, want = run_dense(ctx, orc, 7, x, packed, n, xdt="bf16", ydt="bf16")
+    assert rel_err(got, want) <= TOL_BF16
+
+
+@pytest.mark.parametrize("cfg", [("xr", c) for c in Q4K_XR] + [("ns", c) for c in Q4K_NS], ids=str)
+def test_skinny_q4_k_every_variant(ctx, orc, monkeypatch, cfg):
+    kind, rest = cfg
+    monkeypatch.setenv("RLXQ_SKINNY_XR" if kind == "xr" else "RLXQ_SKINNY_NS", rest)
+    mt, nt, d = (int(v) for v in rest.split(","))
+    for (m, k, n) in [(5, 256, 7), (16 * mt + 3, 2048, 64 * nt * 3 + 5), (9, 12288, 200), (64, 1536, 96),
+                      (3, 768, 64 * nt)]:
+        announce(f"skinny q4_k {kind} {rest} {(m, k, n)}")
+        rng = np.random.default_rng(m + k + n + mt)
+        packed = orc.synth(7, rng, n, k)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        got, want = run_dense(ctx, orc, 7, x, packed, n, xdt="bf16")
+        assert ctx.last_kernel == f"rlxq_skinny{kind}_q4_k_mt{mt}_nt{nt}_d{d}", ctx.last_kernel
+        assert rel_err(got, want) <= TOL_F32, (cfg, m, k, n)
+
+
+def test_skinny_q4_k_activation_range_and_no_staged_kernel(ctx, orc, monkeypatch):
+    """Rows far outside the f16 range; RLXQ_SKINNY_XR=0 (the LDS-staged
+    kernels, which Q4_K lacks) keeps Q4_K on the register-streamed kernel."""
+    monkeypatch.setenv("RLXQ_SKINNY_XR", "0")
+    m, k, n = 8, 512, 96
+    rng = np.random.default_rng(27)
+    packed = orc.synth(7, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[0] *= 1e6
+    x[1] *= 1e-6
+    x[3] = 0.0
+    got, want = run_dense(ctx, orc, 7, x, packed, n, xdt="bf16")
+    assert ctx.last_kernel.startswith("rlxq_skinnyxr_q4_k_"), ctx.last_kernel
+    for r in range(m):
+        if r == 3:
+            assert np.all(got[r] == 0.0)
+            continue
+        assert rel_err(got[r:r + 1], want[r:r + 1]) <= TOL_F32, r
