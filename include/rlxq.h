@@ -30,6 +30,9 @@
  *     stays valid.  A call under stream capture must not need growth (the
  *     allocation fails under global capture): size the stream's scratch
  *     first with rlxq_reserve_workspace, or run the call once uncaptured.
+ *     The MoE combine fused into the down launch also takes 64 KB of
+ *     per-stream counters, zeroed once when first used (or by
+ *     rlxq_reserve_workspace) and left at zero by every call.
  */
 #ifndef RLXQ_H
 #define RLXQ_H
@@ -136,7 +139,8 @@ const char* rlxq_last_kernel(const rlxq_ctx* ctx);
 /* Library version string, e.g. "rlxq 0.1.0 gfx950". */
 const char* rlxq_version(void);
 /* Scratch management (no counterpart in the reference, whose runtime owns
- * its arena): make the scratch of `stream` at least `bytes`; report its
+ * its arena): make the scratch of `stream` at least `bytes` (and create
+ * its zeroed counters); report its
  * size (0 if the stream has none); and free every scratch buffer the stream
  * holds after waiting for the stream (graphs that captured calls on it must
  * not be replayed afterwards).  For callers that capture graphs or use many

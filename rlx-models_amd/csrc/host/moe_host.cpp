@@ -187,12 +187,26 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   const int64_t slots = fused ? chunk_bound + 1 : fired_est;
   const int64_t grid = slots * ga.tiles_n;
   if (grid > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": grid too large");
+  // The combine in the down launch itself (register kernels with the
+  // routing in the workgroups): the workgroup completing a (token row, tile)
+  // sums it.  RLXQ_MOE_COMBINE=launch keeps the separate combine kernel.
+  bool fuse_combine = combine && xr && fused && rows * ga.tiles_n <= rlxq_ctx::kCounterSlots;
+  if (const char* ev = std::getenv("RLXQ_MOE_COMBINE"))
+    if (!std::strcmp(ev, "launch")) fuse_combine = false;
+  if (fuse_combine) {
+    if ((rc = zeroed_counters(ctx, stream, &ga.counters))) return rc;
+    ga.probs = probs;
+    ga.out = y;
+    ga.top_k = top_k;
+    ga.out_bf16 = y_dtype == RLXQ_BF16 ? 1 : 0;
+  }
   const size_t lds = xr ? 0 : (size_t)2 * (k / 32) * (xbf ? 20 : 36) * 4;
   void* gargs[] = {&ga};
   if ((rc = launch(ctx, fg, dim3((unsigned)grid), dim3(256), lds, stream, gargs, name))) return rc;
 
-  // 3. probability-weighted sum over the top-k slots
-  if (combine) {
+  // 3. probability-weighted sum over the top-k slots (in the GEMV launch
+  // above when it took the counters)
+  if (combine && !ga.counters) {
     hipFunction_t fc;
     if ((rc = get_fn(ctx, "rlxq_moe_combine_k", &fc))) return rc;
     int64_t R = rows, N = width;

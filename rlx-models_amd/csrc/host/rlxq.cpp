@@ -180,6 +180,31 @@ int workspace(rlxq_ctx* ctx, size_t bytes, void** out, void* stream) {
   return RLXQ_OK;
 }
 
+int zeroed_counters(rlxq_ctx* ctx, void* stream, int32_t** out) {
+  rlxq_ctx::Scratch& w = ctx->ws[stream];
+  if (!w.counters) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &st) != hipSuccess ||
+        st != hipStreamCaptureStatusNone) {
+      (void)hipGetLastError();
+      return fail(ctx, RLXQ_E_SCRATCH,
+                  "counters: first use under stream capture (call rlxq_reserve_workspace on the stream first)");
+    }
+    void* p = nullptr;
+    const size_t bytes = (size_t)rlxq_ctx::kCounterSlots * sizeof(int32_t);
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(p, 0, bytes, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      if (p) (void)hipFree(p);
+      return fail(ctx, RLXQ_E_NOMEM, "counters: " + hip_msg(e));
+    }
+    w.counters = static_cast<int32_t*>(p);
+  }
+  *out = w.counters;
+  return RLXQ_OK;
+}
+
 bool is_gguf(int s) { return s == RLXQ_GGUF_Q8_0 || s == RLXQ_GGUF_Q4_0 || s == RLXQ_GGUF_Q4_1; }
 bool is_mlx(int s) { return s == RLXQ_MLX_AFFINE4 || s == RLXQ_MLX_AFFINE8; }
 
@@ -287,6 +312,7 @@ int rlxq_destroy(rlxq_ctx* ctx) {
     if (!ctx->ws.empty()) (void)hipDeviceSynchronize();
     for (auto& kv : ctx->ws) {
       if (kv.second.p) (void)hipFree(kv.second.p);
+      if (kv.second.counters) (void)hipFree(kv.second.counters);
       for (void* p : kv.second.retired) (void)hipFree(p);
     }
     for (hipModule_t m : ctx->modules) (void)hipModuleUnload(m);
@@ -301,7 +327,9 @@ int rlxq_reserve_workspace(rlxq_ctx* ctx, void* stream, size_t bytes) {
   DeviceGuard g(ctx->device);
   if (!g.ok()) return fail(ctx, RLXQ_E_HIP, "reserve_workspace: hipSetDevice");
   void* p = nullptr;
-  return workspace(ctx, bytes, &p, stream);
+  int32_t* c = nullptr;
+  const int rc = workspace(ctx, bytes, &p, stream);
+  return rc ? rc : zeroed_counters(ctx, stream, &c);
 }
 
 int64_t rlxq_workspace_bytes(const rlxq_ctx* ctx, void* stream) {
@@ -321,6 +349,7 @@ int rlxq_release_stream(rlxq_ctx* ctx, void* stream) {
   hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(ctx, RLXQ_E_HIP, "release_stream: sync: " + hip_msg(e));
   if (it->second.p) (void)hipFree(it->second.p);
+  if (it->second.counters) (void)hipFree(it->second.counters);
   for (void* p : it->second.retired) (void)hipFree(p);
   ctx->ws.erase(it);
   return RLXQ_OK;

@@ -29,7 +29,11 @@ struct rlxq_ctx {
     void* p = nullptr;
     size_t bytes = 0;
     std::vector<void*> retired;
+    // kCounterSlots int32 counters, zeroed when allocated; kernels that take
+    // them leave them at zero (the fused MoE combine)
+    int32_t* counters = nullptr;
   };
+  static constexpr int64_t kCounterSlots = 16384;
   std::unordered_map<void*, Scratch> ws;
   // The no-allocation entry point's scratch: the device address of a static
   // device array (RLXQ_NOALLOC_SCRATCH_BYTES), looked up at init.  While
@@ -77,6 +81,9 @@ int launch(rlxq_ctx* ctx, hipFunction_t fn, dim3 grid, dim3 block, size_t lds, v
 // Ensures at least `bytes` of context scratch for `stream`; returns its
 // device pointer.
 int workspace(rlxq_ctx* ctx, size_t bytes, void** out, void* stream);
+// The stream's zeroed counters (rlxq_ctx::kCounterSlots), allocated and
+// cleared on the stream at first use (not under stream capture).
+int zeroed_counters(rlxq_ctx* ctx, void* stream, int32_t** out);
 
 bool is_gguf(int scheme);
 bool is_mlx(int scheme);

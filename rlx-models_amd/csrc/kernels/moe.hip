@@ -459,7 +459,9 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
             float o = v[0][m];
             if constexpr (SWIGLU) o = o / (1.f + expf(-o)) * v[1][m];  // silu(g) * u
             const int64_t off = (int64_t)ent[m] * a.y_ld + mycol;
-            if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(o);
+            if (a.counters)   // (combine in this launch: written through to the device-coherent level)
+              __hip_atomic_store(reinterpret_cast<float*>(a.y) + off, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(o);
             else reinterpret_cast<float*>(a.y)[off] = o;
           }
         }
@@ -534,8 +536,8 @@ RLXQ_DEV int block_exclusive_sum(int v, int32_t* ws, int& total) {
 // Chunk number C (the count of chunks; the grid always holds it) zeroes the
 // output rows of invalid entries, its tiles splitting the rows.  Chunks past
 // C exit.  E <= 1024, n_entries <= 1024, 256 threads.
-template <int MT, class Work>
-RLXQ_DEV void balanced_dispatch(const rlxq_moe_gemv_args& a, Work work) {
+template <int MT, class Work, class After>
+RLXQ_DEV void balanced_dispatch(const rlxq_moe_gemv_args& a, Work work, After after) {
   __shared__ int32_t cnt[1024];
   __shared__ int32_t ent[1024];
   __shared__ int32_t ws0[4], ws1[4], pick[2];
@@ -592,6 +594,12 @@ RLXQ_DEV void balanced_dispatch(const rlxq_moe_gemv_args& a, Work work) {
     if (q < c) ent[first + q] = mine[q];
   __syncthreads();
   if (e == E) {
+    // (with the combine in this launch the rows of invalid entries are not
+    // read: only their counts are needed)
+    if (a.counters) {
+      after(ent, 0, total, tn);
+      return;
+    }
     const int64_t width = a.swiglu ? a.N / 2 : a.N;
     for (int64_t idx = (int64_t)tn * blockDim.x + t; idx < (int64_t)total * width;
          idx += (int64_t)blockDim.x * a.tiles_n) {
@@ -602,7 +610,65 @@ RLXQ_DEV void balanced_dispatch(const rlxq_moe_gemv_args& a, Work work) {
     return;
   }
   const int beg = j * MT;
-  work(e, ent, beg, beg + MT < total ? beg + MT : total, tn);
+  const int end = beg + MT < total ? beg + MT : total;
+  work(e, ent, beg, end, tn);
+  if (a.counters) after(ent, beg, end, tn);
+}
+
+// The combine step of a fused down launch (see rlxq_moe_gemv_args): this
+// workgroup has written the rows of entries ent[beg .. end) for the columns
+// of tile tn (waves 4 tn .. 4 tn + 3 of nw = 4 tiles_n, RP columns per wave
+// step, steps nw * RP apart).  Each entry counts once for its (token row,
+// tile); the workgroup that brings a count to top_k sums the row's entries
+// over the tile's columns in slot order and resets the count.
+// Visibility across the XCDs' L2 caches without a cache-wide write-back or
+// invalidate per workgroup: the entry rows are stored and read with
+// device-scope (write-through, coherent-level) accesses, every thread waits
+// for its stores to complete before the barrier that precedes the counts,
+// and the sum's loads are issued only after the count that completes the row
+// has returned.
+template <int RP>
+RLXQ_DEV void combine_tail(const rlxq_moe_gemv_args& a, const int32_t* ent, int beg, int end, int tn) {
+  __shared__ int32_t done[1024];
+  __shared__ int32_t ndone;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int nd = 0;
+    for (int i = beg; i < end; i++) {
+      const int r = ent[i] / a.top_k;
+      int32_t* c = a.counters + (int64_t)r * a.tiles_n + tn;
+      if (atomicAdd(c, 1) == a.top_k - 1) {
+        atomicExch(c, 0);
+        done[nd++] = r;
+      }
+    }
+    ndone = nd;
+  }
+  __syncthreads();
+  const int nd = ndone;
+  if (nd == 0) return;
+  const int64_t width = a.N;
+  const int64_t nw = 4 * (int64_t)a.tiles_n;
+  float* tmp = reinterpret_cast<float*>(a.y);
+  for (int d = 0; d < nd; d++) {
+    const int64_t r = done[d];
+    for (int64_t jj = threadIdx.x;; jj += blockDim.x) {
+      const int64_t st = jj / (4 * RP), rem = jj % (4 * RP);
+      if ((st * nw + 4 * tn) * RP >= width) break;
+      const int64_t col = (st * nw + 4 * tn + rem / RP) * RP + rem % RP;
+      if (col >= width) continue;
+      float acc = 0.f;
+      for (int q = 0; q < a.top_k; q++) {
+        const int64_t en = r * a.top_k + q;
+        if (entry_expert(a, (int)en) < 0) continue;
+        acc = fmaf(a.probs[en], __hip_atomic_load(tmp + en * a.y_ld + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                   acc);
+      }
+      if (a.out_bf16) reinterpret_cast<uint16_t*>(a.out)[r * width + col] = (uint16_t)f32_to_bf16_bits(acc);
+      else reinterpret_cast<float*>(a.out)[r * width + col] = acc;
+    }
+  }
 }
 
 template <int SCH, bool XBF16, int L, int MT, bool SWIGLU, bool FUSED>
@@ -610,7 +676,7 @@ RLXQ_DEV void moe_gemv_body(const rlxq_moe_gemv_args& a) {
   auto work = [&](int e, const int32_t* perm, int beg, int end, int tn) {
     moe_tile<SCH, XBF16, L, MT, SWIGLU>(a, e, perm, beg, end, tn);
   };
-  if constexpr (FUSED) balanced_dispatch<MT>(a, work);
+  if constexpr (FUSED) balanced_dispatch<MT>(a, work, [](const int32_t*, int, int, int) {});
   else table_dispatch(a, work);
 }
 
@@ -620,7 +686,10 @@ RLXQ_DEV void moe_xr_body(const rlxq_moe_gemv_args& a) {
     moe_xr_wave<SCH, L, NU, MT, D, SWIGLU>(a, e, perm, beg, end,
                                            tn * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), a.tiles_n * 4);
   };
-  if constexpr (FUSED) balanced_dispatch<MT>(a, work);
+  auto after = [&](const int32_t* perm, int beg, int end, int tn) {
+    if constexpr (!SWIGLU) combine_tail<64 / L>(a, perm, beg, end, tn);
+  };
+  if constexpr (FUSED) balanced_dispatch<MT>(a, work, after);
   else table_dispatch(a, work);
 }
 

@@ -39,6 +39,16 @@ typedef struct rlxq_moe_gemv_args {
   const int32_t* ids;
   const float* idx_f32;
   int32_t n_entries;
+  /* COMBINE in the same launch (register kernels, routing in the
+   * workgroups): y above holds the per-entry rows; the workgroup that
+   * completes a (token row, tile) sums that row's top_k entry rows in slot
+   * order, weighted by probs [rows, top_k], into out [rows, N] (entries with
+   * an invalid expert id contribute nothing).  counters [rows, tiles_n] are
+   * zero on entry and left at zero.  counters == NULL: no combine here.   */
+  const float* probs;
+  void* out;
+  int32_t* counters;
+  int32_t top_k, out_bf16;
 } rlxq_moe_gemv_args;
 
 #endif

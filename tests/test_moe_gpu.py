@@ -617,3 +617,45 @@ def test_two_streams_use_their_own_workspace(ctx, orc):
     torch.cuda.synchronize()
     for j in range(2):
         assert rel_err(ys[j].cpu().numpy(), orc.grouped_matmul_f64(3, xs[j], bank, idxs[j], n, E)) <= TOL
+
+
+@pytest.mark.parametrize("tokens", [16, 64, 128])
+@pytest.mark.parametrize("ydt", ["f32", "bf16"])
+def test_combine_in_down_launch_matches_combine_kernel(ctx, orc, monkeypatch, tokens, ydt):
+    """COMBINE on the register kernels with the routing in the workgroups
+    sums each token's top-k rows in the down launch itself (the workgroup
+    that completes a (token, tile) does it).  It must equal the separate
+    combine kernel bit for bit, with invalid expert ids in some rows (they
+    contribute nothing), over consecutive calls (the counters reset), and
+    against the float64 oracle."""
+    import torch
+    import rlxq
+
+    H, I, E, TOPK = 2048, 768, 128, 8
+    announce(f"moe fused combine tokens={tokens} y={ydt}")
+    rng = np.random.default_rng(tokens)
+    down = orc.synth_q4_1(rng, E * H, I)
+    dt = _t(down)
+    ydtype = torch.bfloat16 if ydt == "bf16" else torch.float32
+    for call in range(6):
+        act = rng.standard_normal((tokens * TOPK, I)).astype(np.float32)
+        at = _t(act).to(torch.bfloat16)
+        ids = np.stack([rng.choice(E, TOPK, replace=False) for _ in range(tokens)]).astype(np.int32)
+        ids[1, 3] = -1
+        ids[tokens - 1, 0] = E + 5
+        probs = rng.uniform(0.01, 0.3, (tokens, TOPK)).astype(np.float32)
+        it, pt = _t(ids), _t(probs)
+        monkeypatch.delenv("RLXQ_MOE_COMBINE", raising=False)
+        y = ctx.moe_grouped(at, dt, it, pt, rlxq.GGUF_Q4_1, rlxq.MOE_COMBINE, H, E, y_dtype=ydtype)
+        torch.cuda.synchronize()
+        assert ctx.last_kernel.startswith("rlxq_moexrf_q4_1_"), ctx.last_kernel
+        monkeypatch.setenv("RLXQ_MOE_COMBINE", "launch")
+        y2 = ctx.moe_grouped(at, dt, it, pt, rlxq.GGUF_Q4_1, rlxq.MOE_COMBINE, H, E, y_dtype=ydtype)
+        torch.cuda.synchronize()
+        assert ctx.last_kernel == "rlxq_moe_combine_k", ctx.last_kernel
+        assert torch.equal(y, y2), call
+        valid = (ids >= 0) & (ids < E)
+        av = at.float().cpu().numpy()
+        dn = orc.grouped_matmul_f64(3, av, down, np.where(valid, ids, 0).ravel().astype(np.float32), H, E)
+        want = np.einsum("tk,tkh->th", np.where(valid, probs, 0.0).astype(np.float64), dn.reshape(tokens, TOPK, H))
+        assert rel_err(y.float().cpu().numpy(), want) <= (1e-2 if ydt == "bf16" else TOL), call
