@@ -171,7 +171,9 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
   // forces the slice count.
   const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   int tile = 256;
-  const bool bit8 = scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_MLX_AFFINE8;
+  // (and Q6_K, Q8_K: larger raw blocks, one register stage)
+  const bool bit8 = scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_MLX_AFFINE8 || scheme == RLXQ_GGUF_Q6_K ||
+                    scheme == RLXQ_GGUF_Q8_K;
   const char* var = bit8 ? "w8" : "w8p2";
   const char* te = std::getenv("RLXQ_GEMM_TILE");
   if (te) {
@@ -180,13 +182,13 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
   }
   // GGUF with f32 output: the f16 variant of the 256 tiles, whose f16 weights
   // keep the output within 1e-3 (bf16 weights do not)
-  if (!te && y_dtype == RLXQ_F32 && !is_mlx(scheme) && scheme != RLXQ_GGUF_Q4_K) var = bit8 ? "w8f" : "w8p2f";
+  const bool has_f16 = is_gguf(scheme);   // Q8_0, Q4_0, Q4_1
+  if (!te && y_dtype == RLXQ_F32 && has_f16) var = bit8 ? "w8f" : "w8p2f";
   const bool w8 = tile == 256 && var[0] == 'w';
   // "...f": f16 weights and MFMA on the prepared f16 activations (GGUF)
   const size_t vl = std::strlen(var);
   const bool f16 = vl > 0 && var[vl - 1] == 'f';
-  if (f16 && (is_mlx(scheme) || scheme == RLXQ_GGUF_Q4_K))
-    return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: no f16 GEMM for MLX or Q4_K codes");
+  if (f16 && !has_f16) return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: the f16 GEMM serves Q8_0, Q4_0 and Q4_1");
   const int64_t tiles_m = (m + tile - 1) / tile, tiles_n = (n + tile - 1) / tile;
   if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
   const int64_t tiles = tiles_m * tiles_n, ksteps = k / 64;
@@ -283,12 +285,13 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // GEMV family, which keeps the products exact.
   // RLXQ_PREFILL=gemv|gemm forces one of them where both apply (tests).
   {
-    // (Q4_K: bf16 output only; f32 output stays on the GEMV family)
+    // (MLX, MXFP4, Q4_K, Q6_K, Q8_K: bf16 output only; f32 output stays on
+    // the GEMV family, whose weights are not rounded to bf16)
     bool gemm_ok = xbf && k % 64 == 0 && m >= 1;
-    const bool f16_gemm = !is_mlx(scheme) && scheme != RLXQ_GGUF_Q4_K;
+    const bool f16_gemm = is_gguf(scheme);
     bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (f16_gemm && m > 256));
-    if (scheme == RLXQ_MLX_MXFP4 || (kquant_bytes(scheme) > 0 && scheme != RLXQ_GGUF_Q4_K))
-      gemm_ok = use_gemm = false;   // (MXFP4 and the K-quants but Q4_K: the GEMV family only)
+    if (scheme == RLXQ_GGUF_Q5_K || scheme == RLXQ_GGUF_Q3_K || scheme == RLXQ_GGUF_Q2_K)
+      gemm_ok = use_gemm = false;   // (these K-quants: the GEMV family only)
     if (const char* e = std::getenv("RLXQ_PREFILL")) {
       if (!std::strcmp(e, "gemv")) use_gemm = false;
       if (!std::strcmp(e, "gemm")) use_gemm = gemm_ok;

@@ -174,43 +174,41 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   const int kt0 = (int)(kbeg / GBK);
   const uint16_t* xg = reinterpret_cast<const uint16_t*>(a.x);
 
-  // activation tile: 256 rows x 128 B = 2048 chunks of 16 B
+  // activation tile: 256 rows x 128 B = 2048 chunks of 16 B.  Rows past M
+  // read row M - 1 and weight rows past N read row N - 1: they only feed
+  // output rows and columns that are not stored, so no select zeroes them.
   int64_t arow[AP];
-  bool aok[AP];
 #pragma unroll
   for (int i = 0; i < AP; i++) {
     const int c = tid + NT * i, r = c >> 3;
-    aok[i] = m0 + r < a.M;
-    arow[i] = (aok[i] ? m0 + r : a.M - 1) * a.K + (c & 7) * 8;
+    arow[i] = (m0 + r < a.M ? m0 + r : a.M - 1) * a.K + (c & 7) * 8;
   }
   // weight tile: 256 rows x 2 blocks; thread -> row n0 + (tid & 255), blocks
   // (tid >> 8) + q * (NT / 256)
   const int brl = tid & 255;
-  const bool bok = n0 + brl < a.N;
-  const int64_t brow = bok ? n0 + brl : a.N - 1;
+  const int64_t brow = n0 + brl < a.N ? n0 + brl : a.N - 1;
 
   // Global loads run PF steps ahead of the MFMAs (PF register stages); the
   // LDS stores and conversions of the next step sit between the MFMA groups
   // of the current one.
+  // (activation chunks as a clang vector type: HIP's uint4 struct copied in
+  // from memory kept the stages in scratch memory)
   struct Stage {
-    uint4 a[AP];
+    u32x4_t a[AP];
     RawBlk<SCH> b[BPT];
   };
   auto gload = [&](int kt, Stage& P) {
     kt += kt0;
 #pragma unroll
-    for (int i = 0; i < AP; i++) {
-      const uint4 v = *reinterpret_cast<const uint4*>(xg + arow[i] + (int64_t)kt * GBK);
-      P.a[i] = aok[i] ? v : make_uint4(0u, 0u, 0u, 0u);
-    }
+    for (int i = 0; i < AP; i++) P.a[i] = *reinterpret_cast<const u32x4_t*>(xg + arow[i] + (int64_t)kt * GBK);
 #pragma unroll
-    for (int q = 0; q < BPT; q++) load_blk<SCH>(a, brow, 2 * (int64_t)kt + (tid >> 8) + q, bok, P.b[q]);
+    for (int q = 0; q < BPT; q++) load_blk<SCH>(a, brow, 2 * (int64_t)kt + (tid >> 8) + q, true, P.b[q]);
   };
   auto store_a = [&](const Stage& P, int buf, int half) {
 #pragma unroll
     for (int i = half * AP / 2; i < (half + 1) * AP / 2; i++) {
       const int c = tid + NT * i;
-      *reinterpret_cast<uint4*>(As + (buf * BM + (c >> 3)) * GLD + (c & 7) * 8) = P.a[i];
+      *reinterpret_cast<u32x4_t*>(As + (buf * BM + (c >> 3)) * GLD + (c & 7) * 8) = P.a[i];
     }
   };
   auto store_b = [&](const Stage& P, int buf, int q) {
@@ -351,6 +349,9 @@ RLXQ_GEMM_INST(rlxq_gemm_q8_0_t128, SCH_Q8_0)
 RLXQ_GEMM_INST(rlxq_gemm_mlx4_t128, SCH_MLX4)
 RLXQ_GEMM_INST(rlxq_gemm_mlx8_t128, SCH_MLX8)
 RLXQ_GEMM_INST(rlxq_gemm_q4_k_t128, SCH_Q4_K)
+RLXQ_GEMM_INST(rlxq_gemm_q6_k_t128, SCH_Q6_K)
+RLXQ_GEMM_INST(rlxq_gemm_q8_k_t128, SCH_Q8_K)
+RLXQ_GEMM_INST(rlxq_gemm_mxfp4_t128, SCH_MXFP4)
 
 #define RLXQ_GEMM256_INST(SNAME, SCH)                                                        \
   extern "C" __global__ __launch_bounds__(256, 1) void rlxq_gemm_##SNAME##_t256(rlxq_gemm_args a) { \
@@ -374,6 +375,9 @@ RLXQ_GEMM256_INST(q8_0, SCH_Q8_0)
 RLXQ_GEMM256_INST(mlx4, SCH_MLX4)
 RLXQ_GEMM256_INST(mlx8, SCH_MLX8)
 RLXQ_GEMM256_INST(q4_k, SCH_Q4_K)
+RLXQ_GEMM256_INST(q6_k, SCH_Q6_K)
+RLXQ_GEMM256_INST(q8_k, SCH_Q8_K)
+RLXQ_GEMM256_INST(mxfp4, SCH_MXFP4)
 RLXQ_GEMM256F_INST(q4_1, SCH_Q4_1, 2, p2)
 RLXQ_GEMM256F_INST(q4_0, SCH_Q4_0, 2, p2)
 RLXQ_GEMM256F_INST(q8_0, SCH_Q8_0, 1, )

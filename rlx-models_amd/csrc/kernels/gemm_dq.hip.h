@@ -18,13 +18,61 @@ template <> struct RawBlk<SCH_MLX8> { uint4 q0, q1; float s, b; };
 // Q4_K: block kb is sub-block kb % 8 of super-block kb / 8: the super-block's
 // head and the 32 code bytes of its group (low nibbles for even sub-blocks)
 template <> struct RawBlk<SCH_Q4_K> { uint4 hd; uint4 q0, q1; uint32_t sub; };
+// Q6_K: block kb is quarter (kb & 3) of half (kb >> 2) & 1 of super-block
+// kb / 8: 32 ql bytes and the half's 32 qh bytes as 9 aligned dwords each
+// (210-byte super-blocks start 2-byte aligned; `off` is 0 or 2), the dword
+// holding the two int8 scales and the one holding f16 d.
+template <> struct RawBlk<SCH_Q6_K> { uint32_t ql[9], qh[9], sc, d; uint32_t off, q; };
+// Q8_K: f32 d and the 32 int8 codes of sub-block kb % 8 of super-block kb / 8.
+template <> struct RawBlk<SCH_Q8_K> { uint4 q0, q1; float d; };
+// MXFP4: 16 bytes of E2M1 codes and the block's slab scale, raw.
+template <> struct RawBlk<SCH_MXFP4> { uint4 q; float s; };
 
 // Loads block `kb` of weight row `row` (a valid row); `ok` = false zeroes it
 // with selects, so the caller's loop body stays free of branches.
 template <int SCH>
 RLXQ_DEV void load_blk(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok, RawBlk<SCH>& r) {
   const uint8_t* rp = a.w + row * a.rb;
-  if constexpr (SCH == SCH_Q4_K) {
+  if constexpr (SCH == SCH_Q6_K) {
+    // GGML block_q6_K: ql[128], qh[64], int8 scales[16], f16 d (offset 208)
+    const uint8_t* sb = rp + (kb >> 3) * 210;
+    const int h = (int)((kb >> 2) & 1), q = (int)(kb & 3);
+    const uint32_t off = (uint32_t)reinterpret_cast<uintptr_t>(sb) & 3u;
+    const uint8_t* al = sb - off;   // aligned: every read below stays in the super-block or the one before
+    const uint8_t* pl = al + 64 * h + 32 * (q & 1);
+    const uint8_t* ph = al + 128 + 32 * h;
+#pragma unroll
+    for (int i = 0; i < 9; i++) {
+      r.ql[i] = ld_u32(pl + 4 * i);
+      r.qh[i] = ld_u32(ph + 4 * i);
+    }
+    // the two scales and d, each read from the aligned dword that holds it
+    const uint32_t po = off + 192 + 8 * h + 2 * q;
+    r.sc = (ld_u32(al + (po & ~3u)) >> (8 * (po & 3u))) & 0xffffu;
+    // (the load is not left to the select: the compiler would move it into a
+    // branch and wait for it there)
+    uint32_t dw = ld_u32(al + 208);
+    asm volatile("" : "+v"(dw));
+    r.d = ok ? (dw >> (8 * off)) & 0xffffu : 0u;   // zero d: no weight
+    r.off = off;
+    r.q = (uint32_t)q;
+  } else if constexpr (SCH == SCH_Q8_K) {
+    const uint8_t* sb = rp + (kb >> 3) * 292;
+    const float d = *reinterpret_cast<const float*>(sb);
+    r.d = ok ? d : 0.f;
+    r.q0 = ld_u128(sb + 4 + 32 * (kb & 7));
+    r.q1 = ld_u128(sb + 20 + 32 * (kb & 7));
+  } else if constexpr (SCH == SCH_MXFP4) {
+    r.q = ld_u128(rp + kb * 16);
+    const int64_t gi = row * (int64_t)(a.K / 32) + kb;
+    const uint8_t* sp = reinterpret_cast<const uint8_t*>(a.scales);
+    // E8M0 byte (sb_bf16 == 2) or bf16 (1): two byte loads from addresses
+    // chosen without a branch, both in bounds either way
+    const int64_t i0 = a.sb_bf16 == 2 ? gi : 2 * gi;
+    const uint32_t lo = sp[i0], hi = sp[a.sb_bf16 == 2 ? i0 : i0 + 1];
+    const float s = a.sb_bf16 == 2 ? e8m0_to_f32(lo) : bf16_bits_to_f32(lo | (hi << 8));
+    r.s = ok ? s : 0.f;
+  } else if constexpr (SCH == SCH_Q4_K) {
     const uint8_t* sb = rp + (kb >> 3) * 144;
     const uint4 h = ld_u128(sb);
     r.hd = ok ? h : make_uint4(0u, 0u, 0u, 0u);   // zero head: d = dmin = 0
@@ -77,8 +125,42 @@ RLXQ_DEV void load_blk(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok
 // f32 d*q + m (the CPU decoder's arithmetic), rounded to bf16 (nearest even).
 template <int SCH>
 RLXQ_DEV void conv_blk(const RawBlk<SCH>& r, uint32_t* out) {
+  if constexpr (SCH == SCH_MXFP4) {
+    // E2M1 x scale, one conversion per code pair: exact in bf16 for E8M0
+    // scales (powers of two); with a bf16 scale the f32 product is rounded
+    const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      out[4 * i + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q[i], r.s, 0));
+      out[4 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q[i], r.s, 1));
+      out[4 * i + 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q[i], r.s, 2));
+      out[4 * i + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q[i], r.s, 3));
+    }
+  } else {
   float v[32];
-  if constexpr (SCH == SCH_Q4_K) {
+  if constexpr (SCH == SCH_Q6_K) {
+    // code = (ql >> 4 (q >> 1) & 15) | (qh >> 2q & 3) << 4 for each byte;
+    // w = (d * sc) * (code - 32), computed as fma(d * sc, code, -32 (d * sc))
+    // (exact: -32 (d * sc) is)
+    const float d = f16_bits_to_f32(r.d);
+    const float ds0 = d * (float)(int8_t)(r.sc & 0xffu), ds1 = d * (float)(int8_t)(r.sc >> 8);
+    const uint32_t s1 = 4u * (r.q >> 1), s2 = 2u * r.q;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t l = align_bytes(r.ql[i + 1], r.ql[i], r.off), hq = align_bytes(r.qh[i + 1], r.qh[i], r.off);
+      uint32_t c = ((l >> s1) & 0x0F0F0F0Fu) | (((hq >> s2) & 0x03030303u) << 4);
+      asm volatile("" : "+v"(c));
+      const float ds = i < 4 ? ds0 : ds1;
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[4 * i + e] = fmaf(ds, (float)((c >> (8 * e)) & 0xffu), -32.f * ds);
+    }
+  } else if constexpr (SCH == SCH_Q8_K) {
+    const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[4 * i + e] = r.d * (float)(int8_t)((q[i] >> (8 * e)) & 0xffu);
+  } else if constexpr (SCH == SCH_Q4_K) {
     const uint32_t hd[4] = {r.hd.x, r.hd.y, r.hd.z, r.hd.w};
     float sc, mn;
     q4k_scale_min(hd, (int)r.sub, sc, mn);
@@ -148,6 +230,7 @@ RLXQ_DEV void conv_blk(const RawBlk<SCH>& r, uint32_t* out) {
   }
 #pragma unroll
   for (int i = 0; i < 16; i++) out[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+  }
 }
 
 // Dequantize one 32-weight block of row `row` (K-block `kb`) into 16 dwords of

@@ -89,13 +89,19 @@ def test_q6k_every_record_variant(ctx, orc, monkeypatch, cfg):
     assert rel_err(got, want) <= TOL
 
 
-def test_q6k_bf16_output_and_prefill_rows(ctx, orc):
+def test_q6k_bf16_output_and_prefill_rows(ctx, orc, monkeypatch):
+    """bf16 output from 64 rows: the MFMA GEMM by default, the GEMV's
+    multi-row path when forced."""
     import torch
 
     k, n, m = 1024, 300, 80
     rng = np.random.default_rng(4)
     packed = orc.synth_q6_k(rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
+    got, want = _run(ctx, orc, x, packed, n, y_dtype=torch.bfloat16)
+    assert ctx.last_kernel.startswith("rlxq_gemm_q6_k_t256"), ctx.last_kernel
+    assert rel_err(got, want) <= 2e-2
+    monkeypatch.setenv("RLXQ_PREFILL", "gemv")
     got, want = _run(ctx, orc, x, packed, n, y_dtype=torch.bfloat16)
     assert ctx.last_kernel.startswith("rlxq_gemv_q6_k_"), ctx.last_kernel
     assert rel_err(got, want) <= 2e-2
