@@ -162,19 +162,19 @@ int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const 
 int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const void* w, const void* scales,
                   const void* biases, int sb_dtype, int64_t rb, int64_t m, int64_t k, int64_t n, void* y,
                   int y_dtype, void* stream) {
-  // 256 x 256 tiles, 8 waves, global loads two K steps ahead (one for the
-  // 8-bit schemes, whose larger raw blocks do not fit two stages in 256
-  // VGPRs).  When the tiles do not cover the CUs, K is split so that they do
+  // 256 x 256 tiles, 8 waves, global loads two K steps ahead (one for Q6_K
+  // and Q3_K, whose larger raw blocks do not fit two stages in 256 VGPRs;
+  // Q6_K with its LDS stores after the step's MFMAs, which measured 15%
+  // faster for it and slower for the others).  When the tiles do not cover the CUs, K is split so that they do
   // (at most 8 slices of at least 8 K steps) and the slices' f32 partial sums
-  // are added in slice order.  RLXQ_GEMM_TILE=128|256|256w8|256w8p2|...f
+  // are added in slice order.  RLXQ_GEMM_TILE=128|256|256w8|256w8l|256w8p2|...f
   // forces a tiling (the 128 x 128 one never splits); RLXQ_GEMM_SPLITS=<n>
   // forces the slice count.
   const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   int tile = 256;
-  // (and Q6_K, Q8_K: larger raw blocks, one register stage)
-  const bool bit8 = scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_MLX_AFFINE8 || scheme == RLXQ_GGUF_Q6_K ||
-                    scheme == RLXQ_GGUF_Q8_K;
-  const char* var = bit8 ? "w8" : "w8p2";
+  const bool one_stage = scheme == RLXQ_GGUF_Q6_K || scheme == RLXQ_GGUF_Q3_K;
+  const char* var = scheme == RLXQ_GGUF_Q6_K ? "w8l" : (one_stage ? "w8" : "w8p2");
+  const bool bit8 = scheme == RLXQ_GGUF_Q8_0;   // (its f16 variant keeps one stage)
   const char* te = std::getenv("RLXQ_GEMM_TILE");
   if (te) {
     tile = std::atoi(te) == 128 ? 128 : 256;
@@ -285,13 +285,11 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // GEMV family, which keeps the products exact.
   // RLXQ_PREFILL=gemv|gemm forces one of them where both apply (tests).
   {
-    // (MLX, MXFP4, Q4_K, Q6_K, Q8_K: bf16 output only; f32 output stays on
+    // (MLX, MXFP4 and the K-quants: bf16 output only; f32 output stays on
     // the GEMV family, whose weights are not rounded to bf16)
-    bool gemm_ok = xbf && k % 64 == 0 && m >= 1;
+    const bool gemm_ok = xbf && k % 64 == 0 && m >= 1;
     const bool f16_gemm = is_gguf(scheme);
     bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (f16_gemm && m > 256));
-    if (scheme == RLXQ_GGUF_Q5_K || scheme == RLXQ_GGUF_Q3_K || scheme == RLXQ_GGUF_Q2_K)
-      gemm_ok = use_gemm = false;   // (these K-quants: the GEMV family only)
     if (const char* e = std::getenv("RLXQ_PREFILL")) {
       if (!std::strcmp(e, "gemv")) use_gemm = false;
       if (!std::strcmp(e, "gemm")) use_gemm = gemm_ok;

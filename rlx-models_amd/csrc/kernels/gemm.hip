@@ -146,7 +146,7 @@ RLXQ_DEV void gemm_body(const rlxq_gemm_args& a) {
 // MFMAs.  The loop body has no branches (row bounds are clamped addresses plus
 // selects), and the next step's LDS stores and conversions sit between the
 // MFMA groups of the current step.
-template <int SCH, int WGM, int WGN, int PF, bool F16>
+template <int SCH, int WGM, int WGN, int PF, bool F16, bool LATE = false>
 RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   constexpr int BM = 256, BN = 256;
   constexpr int NT = 64 * WGM * WGN;
@@ -288,7 +288,15 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
     __syncthreads();
     for (int kt = 0; kt + 1 < KT; kt++) {
       gload(kt + 1, P);
-      step(kt & 1, P);
+      if constexpr (LATE) {
+        // the stage's LDS stores after all four MFMA groups: the loads have
+        // the whole step to arrive
+#pragma unroll
+        for (int ks = 0; ks < GBK / 16; ks++) compute_ks(kt & 1, ks);
+        store_all(P, (kt & 1) ^ 1);
+      } else {
+        step(kt & 1, P);
+      }
       __syncthreads();
     }
   } else {
@@ -352,6 +360,9 @@ RLXQ_GEMM_INST(rlxq_gemm_q4_k_t128, SCH_Q4_K)
 RLXQ_GEMM_INST(rlxq_gemm_q6_k_t128, SCH_Q6_K)
 RLXQ_GEMM_INST(rlxq_gemm_q8_k_t128, SCH_Q8_K)
 RLXQ_GEMM_INST(rlxq_gemm_mxfp4_t128, SCH_MXFP4)
+RLXQ_GEMM_INST(rlxq_gemm_q5_k_t128, SCH_Q5_K)
+RLXQ_GEMM_INST(rlxq_gemm_q3_k_t128, SCH_Q3_K)
+RLXQ_GEMM_INST(rlxq_gemm_q2_k_t128, SCH_Q2_K)
 
 #define RLXQ_GEMM256_INST(SNAME, SCH)                                                        \
   extern "C" __global__ __launch_bounds__(256, 1) void rlxq_gemm_##SNAME##_t256(rlxq_gemm_args a) { \
@@ -362,6 +373,9 @@ RLXQ_GEMM_INST(rlxq_gemm_mxfp4_t128, SCH_MXFP4)
   }                                                                                                \
   extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8p2(rlxq_gemm_args a) { \
     rlxq::gemm256_body<SCH, 2, 4, 2, false>(a);                                                    \
+  }                                                                                                \
+  extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8l(rlxq_gemm_args a) { \
+    rlxq::gemm256_body<SCH, 2, 4, 1, false, true>(a);                                              \
   }
 // f16 weights converted once per workgroup into LDS, f16 MFMA on the prepared
 // activations (GGUF schemes): rlxq_gemm_<scheme>_t256w8[p2]f
@@ -378,6 +392,9 @@ RLXQ_GEMM256_INST(q4_k, SCH_Q4_K)
 RLXQ_GEMM256_INST(q6_k, SCH_Q6_K)
 RLXQ_GEMM256_INST(q8_k, SCH_Q8_K)
 RLXQ_GEMM256_INST(mxfp4, SCH_MXFP4)
+RLXQ_GEMM256_INST(q5_k, SCH_Q5_K)
+RLXQ_GEMM256_INST(q3_k, SCH_Q3_K)
+RLXQ_GEMM256_INST(q2_k, SCH_Q2_K)
 RLXQ_GEMM256F_INST(q4_1, SCH_Q4_1, 2, p2)
 RLXQ_GEMM256F_INST(q4_0, SCH_Q4_0, 2, p2)
 RLXQ_GEMM256F_INST(q8_0, SCH_Q8_0, 1, )

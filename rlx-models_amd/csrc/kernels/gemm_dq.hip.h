@@ -23,6 +23,17 @@ template <> struct RawBlk<SCH_Q4_K> { uint4 hd; uint4 q0, q1; uint32_t sub; };
 // (210-byte super-blocks start 2-byte aligned; `off` is 0 or 2), the dword
 // holding the two int8 scales and the one holding f16 d.
 template <> struct RawBlk<SCH_Q6_K> { uint32_t ql[9], qh[9], sc, d; uint32_t off, q; };
+// Q5_K: the super-block's 16-byte head (as Q4_K's), the 32 qs bytes of the
+// sub-block's pair and qh[32]; `sub` = kb % 8.
+template <> struct RawBlk<SCH_Q5_K> { uint4 hd, q0, q1, h0, h1; uint32_t sub; };
+// Q3_K: block kb is quarter j = kb % 4 of half n = (kb / 4) % 2 of super-block
+// kb / 8: the half's 32 qs bytes and hmask[32] as 9 aligned dwords each
+// (110-byte super-blocks start 2-byte aligned; `off` is 0 or 2) and the 4
+// aligned dwords holding the 12 scale bytes and f16 d.
+template <> struct RawBlk<SCH_Q3_K> { uint32_t qs[9], hm[9], sd[4]; uint32_t off, sub; };
+// Q2_K: the half's 32 qs bytes, the two scale/min bytes of the block and the
+// dword of f16 d | f16 dmin; `sub` = kb % 8.
+template <> struct RawBlk<SCH_Q2_K> { uint4 q0, q1; uint32_t sc, dd, sub; };
 // Q8_K: f32 d and the 32 int8 codes of sub-block kb % 8 of super-block kb / 8.
 template <> struct RawBlk<SCH_Q8_K> { uint4 q0, q1; float d; };
 // MXFP4: 16 bytes of E2M1 codes and the block's slab scale, raw.
@@ -56,6 +67,46 @@ RLXQ_DEV void load_blk(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok
     r.d = ok ? (dw >> (8 * off)) & 0xffffu : 0u;   // zero d: no weight
     r.off = off;
     r.q = (uint32_t)q;
+  } else if constexpr (SCH == SCH_Q5_K) {
+    // GGML block_q5_K: f16 d, f16 dmin, scales[12], qh[32] (16), qs[128] (48)
+    const uint8_t* sb = rp + (kb >> 3) * 176;
+    const uint4 h = ld_u128(sb);
+    r.hd = ok ? h : make_uint4(0u, 0u, 0u, 0u);   // zero head: d = dmin = 0
+    const uint8_t* q = sb + 48 + 32 * ((kb & 7) >> 1);
+    r.q0 = ld_u128(q);
+    r.q1 = ld_u128(q + 16);
+    r.h0 = ld_u128(sb + 16);
+    r.h1 = ld_u128(sb + 32);
+    r.sub = (uint32_t)(kb & 7);
+  } else if constexpr (SCH == SCH_Q3_K) {
+    // GGML block_q3_K: hmask[32], qs[64] (32), scales[12] (96), f16 d (108)
+    const uint8_t* sb = rp + (kb >> 3) * 110;
+    const int n = (int)((kb >> 2) & 1);
+    const uint32_t off = (uint32_t)reinterpret_cast<uintptr_t>(sb) & 3u;
+    const uint8_t* al = sb - off;   // aligned: every read below stays in the super-block or the one before
+#pragma unroll
+    for (int i = 0; i < 9; i++) {
+      r.qs[i] = ld_u32(al + 32 + 32 * n + 4 * i);
+      r.hm[i] = ld_u32(al + 4 * i);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.sd[i] = ld_u32(al + 96 + 4 * i);
+    // (d is the last two bytes; a zero d zeroes the block)
+    if (!ok) r.sd[3] = 0u;
+    r.off = off;
+    r.sub = (uint32_t)(kb & 7);
+  } else if constexpr (SCH == SCH_Q2_K) {
+    // GGML block_q2_K: scales[16], qs[64] (16), f16 d (80), f16 dmin (82)
+    const uint8_t* sb = rp + (kb >> 3) * 84;
+    const int blk = (int)(kb & 7), n = blk >> 2, j = blk & 3;
+    r.q0 = ld_u128(sb + 16 + 32 * n);
+    r.q1 = ld_u128(sb + 32 + 32 * n);
+    const uint32_t so = 8 * n + 2 * j;   // scale bytes so, so + 1
+    r.sc = (ld_u32(sb + (so & ~3u)) >> (8 * (so & 3u))) & 0xffffu;
+    uint32_t dd = ld_u32(sb + 80);
+    asm volatile("" : "+v"(dd));
+    r.dd = ok ? dd : 0u;
+    r.sub = (uint32_t)blk;
   } else if constexpr (SCH == SCH_Q8_K) {
     const uint8_t* sb = rp + (kb >> 3) * 292;
     const float d = *reinterpret_cast<const float*>(sb);
@@ -153,6 +204,66 @@ RLXQ_DEV void conv_blk(const RawBlk<SCH>& r, uint32_t* out) {
       const float ds = i < 4 ? ds0 : ds1;
 #pragma unroll
       for (int e = 0; e < 4; e++) v[4 * i + e] = fmaf(ds, (float)((c >> (8 * e)) & 0xffu), -32.f * ds);
+    }
+  } else if constexpr (SCH == SCH_Q5_K) {
+    // code = (qs >> 4 (sub & 1) & 15) | (qh >> sub & 1) << 4; w = (d sc) code -
+    // dmin mn with the products exact in f32, so one fma
+    const uint32_t hd[4] = {r.hd.x, r.hd.y, r.hd.z, r.hd.w};
+    float sc, mn;
+    q4k_scale_min(hd, (int)r.sub, sc, mn);
+    const float d1 = f16_bits_to_f32(hd[0] & 0xffffu) * sc, m1 = f16_bits_to_f32(hd[0] >> 16) * mn;
+    const uint32_t qs[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    const uint32_t qh[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+    const uint32_t sh = 4u * (r.sub & 1u);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      uint32_t c = ((qs[i] >> sh) & 0x0F0F0F0Fu) | (((qh[i] >> r.sub) & 0x01010101u) << 4);
+      asm volatile("" : "+v"(c));
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[4 * i + e] = fmaf(d1, (float)((c >> (8 * e)) & 0xffu), -m1);
+    }
+  } else if constexpr (SCH == SCH_Q3_K) {
+    // code = (qs >> 2j & 3) - (hmask bit 4n + j ? 0 : 4), scale s = 8n + 2j + i
+    // (i: the block's two 16-weight halves), w = (d (scale - 32)) code, exact
+    // products rounded once
+    const uint32_t w0 = align_bytes(r.sd[1], r.sd[0], r.off), w1 = align_bytes(r.sd[2], r.sd[1], r.off),
+                   w2 = align_bytes(r.sd[3], r.sd[2], r.off);
+    const float d = f16_bits_to_f32((r.sd[3] >> (8 * r.off)) & 0xffffu);
+    // byte i of the 12 scale bytes (selects, not a runtime array index)
+    auto byte = [&](uint32_t i) { return ((i < 4 ? w0 : (i < 8 ? w1 : w2)) >> (8 * (i & 3))) & 0xffu; };
+    // 6-bit scale s: low nibble of byte s % 8 (high nibble past 7), bits
+    // 2 (s / 4) .. + 1 of byte 8 + s % 4
+    auto scale = [&](uint32_t s6) {
+      return (int)(((byte(s6 & 7) >> (4 * (s6 >> 3))) & 15) | (((byte(8 + (s6 & 3)) >> (2 * (s6 >> 2))) & 3) << 4));
+    };
+    const uint32_t n = r.sub >> 2, j = r.sub & 3, s0 = 8 * n + 2 * j;
+    const float dl0 = d * (float)(scale(s0) - 32), dl1 = d * (float)(scale(s0 + 1) - 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t q = align_bytes(r.qs[i + 1], r.qs[i], r.off), hm = align_bytes(r.hm[i + 1], r.hm[i], r.off);
+      // code + 4 = low bits | 4 (mask bit set)
+      uint32_t c = ((q >> (2 * j)) & 0x03030303u) | (((hm >> (4 * n + j)) & 0x01010101u) << 2);
+      asm volatile("" : "+v"(c));
+      const float dl = i < 4 ? dl0 : dl1;
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[4 * i + e] = fmaf(dl, (float)((c >> (8 * e)) & 0xffu), -4.f * dl);
+    }
+  } else if constexpr (SCH == SCH_Q2_K) {
+    // code = qs >> 2j & 3; w = (d (c & 15)) code - dmin (c >> 4), the products
+    // exact, so one fma
+    const float d = f16_bits_to_f32(r.dd & 0xffffu), dmin = f16_bits_to_f32(r.dd >> 16);
+    const uint32_t j = r.sub & 3;
+    const uint32_t c0 = r.sc & 0xffu, c1 = (r.sc >> 8) & 0xffu;
+    const float dl0 = d * (float)(c0 & 15u), ml0 = dmin * (float)(c0 >> 4);
+    const float dl1 = d * (float)(c1 & 15u), ml1 = dmin * (float)(c1 >> 4);
+    const uint32_t qs[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      uint32_t c = (qs[i] >> (2 * j)) & 0x03030303u;
+      asm volatile("" : "+v"(c));
+      const float dl = i < 4 ? dl0 : dl1, ml = i < 4 ? ml0 : ml1;
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[4 * i + e] = fmaf(dl, (float)((c >> (8 * e)) & 0xffu), -ml);
     }
   } else if constexpr (SCH == SCH_Q8_K) {
     const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};

@@ -139,14 +139,14 @@ def test_every_gemm_tiling(ctx, orc, scheme, monkeypatch):
         wd = orc.dequantize(scheme, packed, k).astype(np.float64)
     outs = {}
     monkeypatch.setenv("RLXQ_PREFILL", "gemm")
-    for tile in ("128", "256", "256w8", "256w8p2"):
+    for tile in ("128", "256", "256w8", "256w8l", "256w8p2"):
         monkeypatch.setenv("RLXQ_GEMM_TILE", tile)
         announce(f"gemm tiling t{tile} scheme={scheme} m={m} k={k} n={n}")
         got, xv = run_gemm(ctx, orc, scheme, x, packed, n, ydt="f32", **kw)
         assert ctx.last_kernel.endswith(f"_t{tile}")
         assert rel_err(got, xv.astype(np.float64) @ wd.T) <= TOL_PREFILL
         outs[tile] = got
-    for t in ("256", "256w8", "256w8p2"):
+    for t in ("256", "256w8", "256w8l", "256w8p2"):
         assert np.allclose(outs["128"], outs[t], rtol=1e-6, atol=1e-6 * np.abs(outs["128"]).max())
 
 

@@ -1,8 +1,9 @@
 """Prefill dequant-GEMM (bf16 MFMA, weights rounded to bf16 in LDS) for the
-GGUF Q6_K and Q8_K super-blocks and MLX MXFP4 codes, through the C ABI,
-against the float64 oracle on the activations the kernel saw.  Q6_K's
-210-byte super-blocks start 2-byte aligned every other time (and whole rows
-do when K / 256 is odd); the kernel reads them through aligned dwords.  Bar:
+GGUF K-quant super-blocks Q6_K, Q5_K, Q3_K, Q2_K and Q8_K and MLX MXFP4
+codes, through the C ABI, against the float64 oracle on the activations the
+kernel saw.  Q6_K's 210-byte and Q3_K's 110-byte super-blocks start 2-byte
+aligned every other time (and whole rows do when K / 256 is odd); the kernel
+reads them through aligned dwords.  Bar:
 the prefill bar 2e-2 (bf16 output); every tiling agrees with the 128 x 128
 one to ~1e-6 on f32 output."""
 import numpy as np
@@ -14,8 +15,9 @@ from test_gemv_gpu import _t, rel_err
 pytestmark = pytest.mark.gpu
 
 TOL_PREFILL = 2e-2
-Q6_K, Q8_K, MXFP4 = 8, 13, 9
-NAMES = {Q6_K: "q6_k", Q8_K: "q8_k", MXFP4: "mxfp4"}
+Q6_K, Q8_K, MXFP4, Q5_K, Q3_K, Q2_K = 8, 13, 9, 10, 11, 12
+NAMES = {Q6_K: "q6_k", Q8_K: "q8_k", MXFP4: "mxfp4", Q5_K: "q5_k", Q3_K: "q3_k", Q2_K: "q2_k"}
+ALL = [Q6_K, Q5_K, Q3_K, Q2_K, Q8_K, MXFP4]
 
 
 def _weights(orc, scheme, rng, n, k, mx_scales="u8"):
@@ -44,7 +46,7 @@ def _run(ctx, scheme, x32, packed, kw, n, ydt):
     return y.float().cpu().numpy(), xt.float().cpu().numpy().astype(np.float64)
 
 
-@pytest.mark.parametrize("scheme", [Q6_K, Q8_K, MXFP4], ids=lambda s: NAMES[s])
+@pytest.mark.parametrize("scheme", ALL, ids=lambda s: NAMES[s])
 @pytest.mark.parametrize("mkn", [(64, 4096, 520), (300, 1280, 272), (512, 4096, 1024), (129, 12288, 300)], ids=str)
 def test_prefill_default_kernel(ctx, orc, scheme, mkn):
     """bf16 activations and output from 64 rows take the 256 x 256 GEMM
@@ -59,10 +61,11 @@ def test_prefill_default_kernel(ctx, orc, scheme, mkn):
     assert rel_err(got, xv @ wd.T) <= TOL_PREFILL
 
 
-@pytest.mark.parametrize("scheme", [Q6_K, Q8_K, MXFP4], ids=lambda s: NAMES[s])
+@pytest.mark.parametrize("scheme", ALL, ids=lambda s: NAMES[s])
 def test_every_tiling_agrees(ctx, orc, monkeypatch, scheme):
     """Every tiling on a ragged shape with an odd super-block count (Q6_K rows
-    alternate 4- and 2-byte alignment), f32 output forced onto the GEMM: each
+    and Q3_K rows alternate 4- and 2-byte alignment), f32 output forced onto
+    the GEMM: each
     within the bar, all within ~1e-6 of the 128 x 128 tiling."""
     m, k, n = 300, 1280, 272
     rng = np.random.default_rng(17 + scheme)
@@ -70,9 +73,9 @@ def test_every_tiling_agrees(ctx, orc, monkeypatch, scheme):
     x = rng.standard_normal((m, k)).astype(np.float32)
     monkeypatch.setenv("RLXQ_PREFILL", "gemm")
     outs = {}
-    for tile in ("128", "256", "256w8", "256w8p2"):
-        if tile == "256w8p2" and scheme == Q6_K:
-            continue   # (its two register stages do not fit Q6_K's raw blocks)
+    for tile in ("128", "256", "256w8", "256w8l", "256w8p2"):
+        if tile == "256w8p2" and scheme in (Q6_K, Q3_K):
+            continue   # (its two register stages do not fit these raw blocks)
         monkeypatch.setenv("RLXQ_GEMM_TILE", tile)
         announce(f"gemm tiling {NAMES[scheme]} t{tile}")
         got, xv = _run(ctx, scheme, x, packed, kw, n, "f32")
@@ -96,7 +99,7 @@ def test_mxfp4_bf16_scales_and_split_k(ctx, orc, monkeypatch):
         assert rel_err(got, xv @ wd.T) <= TOL_PREFILL, sp
 
 
-@pytest.mark.parametrize("scheme", [Q6_K, Q8_K, MXFP4], ids=lambda s: NAMES[s])
+@pytest.mark.parametrize("scheme", ALL, ids=lambda s: NAMES[s])
 def test_f32_output_prefill_stays_on_gemv(ctx, orc, scheme):
     """f32 output is not routed to the bf16-weight GEMM: the GEMV family keeps
     the 1e-3 bar."""

@@ -117,10 +117,9 @@ def test_kquant_bf16_output_and_prefill_rows(ctx, orc, name):
     packed = orc.synth(scheme, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, want = _run(ctx, orc, scheme, x, packed, n, y_dtype=torch.bfloat16)
-    # (Q8_K's bf16-output prefill runs on the MFMA GEMM, the others on the GEMV)
-    prefix = "rlxq_gemm_q8_k_t256" if name == "q8_k" else f"rlxq_gemv_{name}_"
-    assert ctx.last_kernel.startswith(prefix), ctx.last_kernel
-    assert rel_err(got, want) <= 1e-2
+    # bf16-output prefill runs on the MFMA GEMM (weights rounded to bf16)
+    assert ctx.last_kernel.startswith(f"rlxq_gemm_{name}_t256"), ctx.last_kernel
+    assert rel_err(got, want) <= 2e-2
 
 
 @pytest.mark.parametrize("name", list(SCHEMES))
