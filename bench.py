@@ -24,6 +24,7 @@ Extra keys of the same JSON line:
   batched_decode  config 3: Q4_1 and Q8_0 (and Q4_K), M in {1, 4, 16, 64}
   moe             config 5: routed-expert grouped GEMV, 16 tokens, top-8 of 128
   moe_q4_k        the same with Q4_K expert banks (a Q4_K_M MoE checkpoint)
+  moe_prefill     the config-5 layer at 256 tokens (grouped MFMA kernels)
   q8_gemv         config 1: Q8_0 2048->2048, f32 activations
   gguf_upload     a 537 MB GGUF checkpoint streamed from the page cache to HBM
   cpu_baseline    the C restatement of the reference CPU algorithm timed on
@@ -540,16 +541,17 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
     return res
 
 
-def moe_section(ctx, gen, sptr, stream, scheme: str = "q4_1") -> dict:
+def moe_section(ctx, gen, sptr, stream, scheme: str = "q4_1", tokens: int = 16) -> dict:
     """Config 5: one MoE FFN of a Qwen3-30B-A3B-like layer for 16 tokens, as
-    three launches: route (softmax of N(0,1) logits over 128 experts, top-8,
+    three calls: route (softmax of N(0,1) logits over 128 experts, top-8,
     renormalised), the fused gate|up 2048->1536 + SwiGLU per (token, slot),
     and down 768->2048 with the probability-weighted combine.  Two layers with
-    their own expert banks and logits alternate (755 MB of banks)."""
+    their own expert banks and logits alternate (755 MB of banks).  `tokens`
+    = 256: the same layer at a prefill size (the grouped MFMA kernels)."""
     import torch
     import rlxq
 
-    E, H, I, TOPK, T = 128, 2048, 768, 8, 16
+    E, H, I, TOPK, T = 128, 2048, 768, 8, tokens
     synth, sch, bpw = {"q4_1": (synth_q4_1_gpu, rlxq.GGUF_Q4_1, Q4_1_BPW),
                        "q4_k": (synth_q4_k_gpu, rlxq.GGUF_Q4_K, 144 / 256)}[scheme]
     banks = [(synth(E * 2 * I, H, gen), synth(E * H, I, gen)) for _ in range(2)]
@@ -574,10 +576,16 @@ def moe_section(ctx, gen, sptr, stream, scheme: str = "q4_1") -> dict:
     u = sum(uniq) / len(uniq)
     per_expert = 2 * I * H * bpw + H * I * bpw
     b = u * per_expert + T * H * 2 + T * TOPK * I * 2 * 2 + T * H * 4
-    return {"us_per_layer": round(us, 2), "unique_experts": u, "GBps": round(b / us / 1e3, 1),
-            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-            "bytes_model": f"unique experts x {int(per_expert):,} B + activations",
-            "launches_per_layer": "route, gate|up + SwiGLU (routing in the workgroups), down + combine"}
+    out = {"tokens": T, "us_per_layer": round(us, 2), "unique_experts": u, "GBps": round(b / us / 1e3, 1),
+           "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+           "bytes_model": f"unique experts x {int(per_expert):,} B + activations", "kernel_down": ctx.last_kernel}
+    if T <= 64:
+        out["launches_per_layer"] = "route, gate|up + SwiGLU (routing in the workgroups), down + combine"
+    else:
+        out["launches_per_layer"] = ("route, then per grouped call: routing table, gathered-row layout, f16 rows, "
+                                     "grouped MFMA kernel (+ combine kernel for down)")
+        out["TFLOPs"] = round(2.0 * T * TOPK * (2 * I * H + H * I) / us / 1e6, 1)
+    return out
 
 
 def gguf_section(ctx, gen, sptr, stream) -> dict:
@@ -653,7 +661,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="only the decode step and its roofline")
     ap.add_argument("--quick", action="store_true", help="prefill at M=4096 only")
     ap.add_argument("--cpu-seconds", type=float, default=16.0)
-    ap.add_argument("--section", choices=["prefill", "batched", "moe", "moe_q4_k", "schemes", "q8", "gguf"],
+    ap.add_argument("--section", choices=["prefill", "batched", "moe", "moe_q4_k", "moe_prefill", "schemes", "q8",
+                                          "gguf"],
                     help="profiling mode: run only this section (no decode step, no CPU baseline) and print its "
                          "figures as one JSON object")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -687,6 +696,7 @@ def main() -> int:
                "batched": lambda: batched_section(ctx, gen, sptr, stream),
                "moe": lambda: moe_section(ctx, gen, sptr, stream),
                "moe_q4_k": lambda: moe_section(ctx, gen, sptr, stream, "q4_k"),
+               "moe_prefill": lambda: moe_section(ctx, gen, sptr, stream, "q4_1", 256),
                "schemes": lambda: schemes_section(ctx, gen, sptr, stream),
                "q8": lambda: q8_section(ctx, gen, sptr, stream),
                "gguf": lambda: gguf_section(ctx, gen, sptr, stream)}[a.section]
@@ -760,6 +770,7 @@ def main() -> int:
         out["batched_decode"] = batched_section(ctx, gen, sptr, stream)
         out["moe"] = moe_section(ctx, gen, sptr, stream)
         out["moe_q4_k"] = moe_section(ctx, gen, sptr, stream, "q4_k")
+        out["moe_prefill"] = moe_section(ctx, gen, sptr, stream, "q4_1", 256)
         out["schemes"] = schemes_section(ctx, gen, sptr, stream)
         out["q8_gemv"] = q8_section(ctx, gen, sptr, stream)
         out["gguf_upload"] = gguf_section(ctx, gen, sptr, stream)

@@ -13,6 +13,7 @@
 
 #include "moe_args.h"
 #include "rlxq.h"
+#include "skinny_args.h"
 #include "rlxq_internal.hpp"
 
 namespace rlxq {
@@ -101,6 +102,24 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   // workgroup one chunk of MT entries); the LDS-record kernels measure faster
   // with the device table.
   if (!xr && fused && !route_forced) fused = false;
+  // Prefill-sized calls (at least 8 entries per fired expert on average) on
+  // GGUF Q4_1, Q4_0, Q8_0 or Q4_K codes with bf16 activations: the grouped
+  // f16-MFMA kernels over gathered activation rows, one weight pass per chunk
+  // of 16 MT entries of an expert (device table, then the gathered-row
+  // layout, then the prepared rows).  RLXQ_MOE_KERNEL=sk forces them where
+  // they apply; xr or lds keeps the GEMV kernels.
+  const bool sk_ok = xbf && k % 128 == 0 &&
+                     (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0 ||
+                      (q4k && k % 256 == 0));
+  bool sk = sk_ok && n_entries >= 8 * fired_est;
+  if (const char* ev = std::getenv("RLXQ_MOE_KERNEL")) {
+    if (!std::strcmp(ev, "sk")) sk = sk_ok;
+    else sk = false;
+  }
+  if (sk) {
+    fused = false;
+    xr = false;
+  }
   if (xr) {
     // one entry per pass while experts hold few entries: the chunks of one
     // expert then run side by side and share its rows through the caches
@@ -134,11 +153,28 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     ga.tiles_n = (int32_t)(swiglu ? (width + tile / 2 - 1) / (tile / 2) : (n + tile - 1) / tile);
   }
   const size_t table_bytes = fused ? 0 : ((size_t)(2 + 2 * num_experts + n_entries) * 4 + 255) & ~size_t(255);
-  const size_t tmp_bytes = combine ? (size_t)n_entries * width * 4 : 0;
+  const size_t tmp_bytes = combine ? (((size_t)n_entries * width * 4 + 255) & ~size_t(255)) : 0;
+  // grouped MFMA path: chunks of RPC gathered rows, each expert's entries
+  // padded to whole chunks
+  const double avg_e = (double)n_entries / (double)fired_est;
+  // (chunks of 16 rows with 4 weight tiles measured best at 16 entries per
+  // expert: gate|up 115 us and down 83 us at config 5 with 256 tokens,
+  // against 131 and 130 with 2 tiles; 64-row chunks keep 2 tiles)
+  int sk_mt = avg_e <= 24.0 ? 1 : (avg_e <= 48.0 ? 2 : 4), sk_nt = 0, sk_d = 0;
+  if (const char* ev = std::getenv("RLXQ_MOE_SK")) std::sscanf(ev, "%d,%d,%d", &sk_mt, &sk_nt, &sk_d);   // tuning
+  if (sk_mt != 1 && sk_mt != 2 && sk_mt != 4) sk_mt = 1;
+  if (sk_nt != 2 && sk_nt != 4 && sk_nt != 8) sk_nt = sk_mt == 4 ? 2 : 4;
+  const int64_t rpc = 16 * sk_mt;
+  const int64_t sk_mp = sk ? ((n_entries + fired_est * (rpc - 1) + rpc - 1) / rpc) * rpc : 0;
+  auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
+  const size_t cmap_bytes = sk ? r256((size_t)(1 + sk_mp / rpc) * 4) : 0, emap_bytes = sk ? r256((size_t)sk_mp * 4) : 0;
+  const size_t x16_bytes = sk ? r256((size_t)sk_mp * k * 2) : 0, is_bytes = sk ? r256((size_t)sk_mp * 4) : 0;
+  const size_t total_ws = table_bytes + tmp_bytes + cmap_bytes + emap_bytes + x16_bytes + is_bytes;
   void* ws = nullptr;
-  if (table_bytes + tmp_bytes && (rc = workspace(ctx, table_bytes + tmp_bytes, &ws, stream))) return rc;
+  if (total_ws && (rc = workspace(ctx, total_ws, &ws, stream))) return rc;
   int32_t* table = fused ? nullptr : static_cast<int32_t*>(ws);
   float* tmp = combine ? reinterpret_cast<float*>(static_cast<char*>(ws) + table_bytes) : nullptr;
+  char* skb = static_cast<char*>(ws) + table_bytes + tmp_bytes;
 
   // 1. routing table
   if (!fused) {
@@ -158,6 +194,70 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     if ((rc = launch(ctx, ft, dim3(1), dim3(1024), 0, stream, targs, "rlxq_moe_table_k"))) return rc;
   }
 
+  if (sk) {
+    // 2a. gathered-row layout of the table's entries
+    rlxq_moe_pad_args pa;
+    pa.table = table;
+    pa.cmap = reinterpret_cast<int32_t*>(skb);
+    pa.emap = reinterpret_cast<int32_t*>(skb + cmap_bytes);
+    pa.Mp = sk_mp;
+    pa.E = (int32_t)num_experts;
+    pa.rows_per_chunk = (int32_t)rpc;
+    hipFunction_t fp;
+    if ((rc = get_fn(ctx, "rlxq_moe_pad_k", &fp))) return rc;
+    void* pargs[] = {&pa};
+    if ((rc = launch(ctx, fp, dim3(1), dim3(1024), 0, stream, pargs, "rlxq_moe_pad_k"))) return rc;
+    // 2b. the gathered rows to f16 (scaled per row, code-unpacking order)
+    rlxq_x16_args xa;
+    std::memset(&xa, 0, sizeof xa);
+    xa.x = x;
+    xa.x16 = reinterpret_cast<uint16_t*>(skb + cmap_bytes + emap_bytes);
+    xa.inv_s = reinterpret_cast<float*>(skb + cmap_bytes + emap_bytes + x16_bytes);
+    xa.M = sk_mp;
+    xa.K = k;
+    xa.Mp = sk_mp;
+    xa.x_bf16 = 1;
+    xa.nibble_order = scheme != RLXQ_GGUF_Q8_0;
+    xa.frag_major = 1;
+    xa.rdiv = x_div;
+    xa.rmap = pa.emap;
+    hipFunction_t fx;
+    if ((rc = get_fn(ctx, "rlxq_x16_prep", &fx))) return rc;
+    void* xargs[] = {&xa};
+    if ((rc = launch(ctx, fx, dim3((unsigned)sk_mp), dim3(256), 0, stream, xargs, "rlxq_x16_prep"))) return rc;
+    // 2c. the grouped MFMA kernel over (chunk, tile): NT weight tiles of 16
+    // rows (SwiGLU: NT / 2 gate tiles and their up tiles)
+    const int NT = sk_nt;
+    const int nh = swiglu ? NT / 2 : NT;
+    int D = sk_d;
+    if (D <= 0) D = NT >= 4 ? (NT == 8 && sk_mt == 2 ? 1 : (sk_mt == 4 ? 1 : 2))
+                            : (sk_mt == 1 ? (q4k ? 3 : 4) : (sk_mt == 2 ? 3 : 2));
+    rlxq_moe_sk_args ka;
+    std::memset(&ka, 0, sizeof ka);
+    ka.x16 = xa.x16;
+    ka.inv_s = xa.inv_s;
+    ka.cmap = pa.cmap;
+    ka.emap = pa.emap;
+    ka.bank = static_cast<const uint8_t*>(bank);
+    ka.y = combine ? static_cast<void*>(tmp) : y;
+    ka.N = n;
+    ka.K = k;
+    ka.rb = rb;
+    ka.y_ld = width;
+    ka.Mp = sk_mp;
+    ka.tiles_n = (int32_t)((width + 16 * nh - 1) / (16 * nh));
+    ka.y_bf16 = (!combine && y_dtype == RLXQ_BF16) ? 1 : 0;
+    ka.swiglu = swiglu ? 1 : 0;
+    std::snprintf(name, sizeof name, "rlxq_moesk_%s_mt%d_nt%d_d%d%s", scheme_name(scheme), sk_mt, NT, D,
+                  swiglu ? "_sw" : "");
+    hipFunction_t fk;
+    if ((rc = get_fn(ctx, name, &fk))) return rc;
+    const int64_t grid = (sk_mp / rpc) * ka.tiles_n;
+    if (grid > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": grid too large");
+    const size_t lds = 2 * (size_t)(sk_mt * NT * 4) * 64 * 4;
+    void* kargs[] = {&ka};
+    if ((rc = launch(ctx, fk, dim3((unsigned)grid), dim3(256), lds, stream, kargs, name))) return rc;
+  } else {
   // 2. grouped GEMV over (expert or chunk, tile)
   hipFunction_t fg;
   if ((rc = get_fn(ctx, name, &fg))) return rc;
@@ -203,6 +303,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   const size_t lds = xr ? 0 : (size_t)2 * (k / 32) * (xbf ? 20 : 36) * 4;
   void* gargs[] = {&ga};
   if ((rc = launch(ctx, fg, dim3((unsigned)grid), dim3(256), lds, stream, gargs, name))) return rc;
+  }
 
   // 3. probability-weighted sum over the top-k slots (in the GEMV launch
   // above when it took the counters)

@@ -51,4 +51,31 @@ typedef struct rlxq_moe_gemv_args {
   int32_t top_k, out_bf16;
 } rlxq_moe_gemv_args;
 
+/* Grouped batched-decode MFMA path (prefill-sized MoE calls): the entries of
+ * each fired expert (table order) are laid out in gathered activation rows,
+ * each expert's run padded to whole chunks of rows_per_chunk rows.
+ * rlxq_moe_pad_k writes cmap ([0]: chunks, [1 + c]: expert of chunk c) and
+ * emap ([Mp]: entry of gathered row, -1 for padding).                     */
+typedef struct rlxq_moe_pad_args {
+  const int32_t* table;
+  int32_t* cmap;
+  int32_t* emap;
+  int64_t Mp;
+  int32_t E, rows_per_chunk;
+} rlxq_moe_pad_args;
+
+typedef struct rlxq_moe_sk_args {
+  const uint16_t* x16;    /* gathered f16 rows, fragment-major over Mp    */
+  const float* inv_s;     /* [Mp] factors undoing the row scaling         */
+  const int32_t* cmap;
+  const int32_t* emap;
+  const uint8_t* bank;    /* E contiguous [N, K] packed slabs             */
+  void* y;                /* entry rows, leading dimension y_ld           */
+  int64_t N, K, rb, y_ld, Mp;
+  int32_t tiles_n, y_bf16;
+  int32_t swiglu;         /* 1: rows [0, N/2) gate, [N/2, N) up; y [entries, N/2]
+                             = silu(x.Wg^T) * (x.Wu^T)                     */
+  int32_t pad;
+} rlxq_moe_sk_args;
+
 #endif

@@ -25,6 +25,7 @@
 #include "f16dq.hip.h"
 #include "gemm_dq.hip.h"
 #include "skinny_args.h"
+#include "moe_args.h"
 
 namespace rlxq {
 
@@ -375,38 +376,30 @@ RLXQ_DEV void skinny_dma_body(const rlxq_skinny_args& a) {
 // order), and the A fragment of lane (m, g) is the 16 bytes of row m at
 // block 4c + g, positions 8i .. 8i + 7, loaded with the chunk.  The waves'
 // sums are added in the fixed order (w0 + w2) + (w1 + w3).
+// The contraction of the register-streamed kernel for 16 MT activation rows
+// from m0 (fragment-major x16 over Mp rows) against NT 16-row weight tiles
+// (lane j of tile t reads weight row wrow[t] of the rows at w, stride rb)
+// over K [kb, ke).  Returns true in wave 0, whose acc then holds the sums.
 template <int SCH, int MT, int NT, int D>
-RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
+RLXQ_DEV bool skinny_xr_core(const uint16_t* x16, int64_t Mp, int64_t m0, const uint8_t* w, int64_t rb, int64_t K,
+                             int64_t kb, int64_t ke, const int64_t (&wrow)[NT], const bool (&wok)[NT],
+                             f32x4_t (&acc)[MT][NT]) {
   constexpr int BDW = sk_bdw<SCH>();
   // wave index through readfirstlane: the chunk loop is wave-uniform
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
-  const int tn = blockIdx.x % a.tiles_n;
-  const int sp = (blockIdx.x / a.tiles_n) % a.splits;
-  const int mc = blockIdx.x / (a.tiles_n * a.splits);
-  const int64_t n0 = (int64_t)tn * 16 * NT, m0 = (int64_t)mc * 16 * MT;
-  const int64_t kb = (int64_t)sp * a.kslice;
-  const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
   const int nchunk = (int)((ke - kb) / 128);
   // chunks of this wave: wv + 4 it, it < cnt
   const int cnt = nchunk > wv ? (nchunk - wv + 3) / 4 : 0;
 
   rlxq_gemm_args ga;
-  ga.w = a.w;
-  ga.rb = a.rb;
-  ga.K = a.K;
+  ga.w = w;
+  ga.rb = rb;
+  ga.K = K;
   ga.group = 32;
   ga.sb_bf16 = 0;
   ga.scales = nullptr;
   ga.biases = nullptr;
-  int64_t wrow[NT];
-  bool wok[NT];
-#pragma unroll
-  for (int t = 0; t < NT; t++) {
-    const int64_t n = n0 + 16 * t + j;
-    wok[t] = n < a.N;
-    wrow[t] = wok[t] ? n : a.N - 1;
-  }
   // activations in the fragment-major layout: piece i of chunk c for row m,
   // lane group g at ((4 c + i) Mp + m) 4 + g (16-byte pieces), so the A
   // fragment of 16 rows is one contiguous 1 KB read; the Mp rows cover every
@@ -414,7 +407,7 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
   const uint4* xrow[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; mt++)
-    xrow[mt] = reinterpret_cast<const uint4*>(a.x16) + ((kb / 32) * a.Mp + m0 + 16 * mt + j) * 4 + g;
+    xrow[mt] = reinterpret_cast<const uint4*>(x16) + ((kb / 32) * Mp + m0 + 16 * mt + j) * 4 + g;
 
   struct Stage {
     RawBlk<SCH> w[NT];
@@ -426,10 +419,9 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) st.x[mt][i] = xrow[mt][((int64_t)c * 4 + i) * a.Mp * 4];
+      for (int i = 0; i < 4; i++) st.x[mt][i] = xrow[mt][((int64_t)c * 4 + i) * Mp * 4];
   };
 
-  f32x4_t acc[MT][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; mt++)
 #pragma unroll
@@ -456,10 +448,11 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
       }
   };
   // (slots past the wave's chunks repeat its last one: a few redundant
-  // loads when it has fewer than D chunks, none otherwise)
+  // loads when it has fewer than D chunks, none otherwise; a wave with no
+  // chunk at all (K under 512) loads chunk 0, never one past K)
   Stage ring[D];
 #pragma unroll
-  for (int d = 0; d < D; d++) load(chunk_of(d < cnt ? d : (cnt > 0 ? cnt - 1 : 0)), ring[d]);
+  for (int d = 0; d < D; d++) load(cnt > 0 ? chunk_of(d < cnt ? d : cnt - 1) : 0, ring[d]);
   int it0 = 0;
   for (; it0 + 2 * D <= cnt; it0 += D) {
 #pragma unroll
@@ -510,7 +503,36 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
         for (int r = 0; r < 4; r++) R[((mt * NT + t) * 4 + r) * 64 + lane] = acc[mt][t][r];
   }
   __syncthreads();
-  if (wv != 0) return;
+  if (wv != 0) return false;
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[mt][t][r] += R[((mt * NT + t) * 4 + r) * 64 + lane];
+  return true;
+}
+
+template <int SCH, int MT, int NT, int D>
+RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 15, g = lane >> 4;
+  const int tn = blockIdx.x % a.tiles_n;
+  const int sp = (blockIdx.x / a.tiles_n) % a.splits;
+  const int mc = blockIdx.x / (a.tiles_n * a.splits);
+  const int64_t n0 = (int64_t)tn * 16 * NT, m0 = (int64_t)mc * 16 * MT;
+  const int64_t kb = (int64_t)sp * a.kslice;
+  const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
+  int64_t wrow[NT];
+  bool wok[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int64_t n = n0 + 16 * t + j;
+    wok[t] = n < a.N;
+    wrow[t] = wok[t] ? n : a.N - 1;
+  }
+  f32x4_t acc[MT][NT];
+  if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.Mp, m0, a.w, a.rb, a.K, kb, ke, wrow, wok, acc)) return;
   // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
 #pragma unroll
   for (int mt = 0; mt < MT; mt++)
@@ -523,10 +545,66 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
       for (int t = 0; t < NT; t++) {
         const int64_t n = n0 + 16 * t + j;
         if (n >= a.N) continue;
-        const float v = (acc[mt][t][r] + R[((mt * NT + t) * 4 + r) * 64 + lane]) * is;
+        const float v = acc[mt][t][r] * is;
         if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
         else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
         else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped (MoE) variant of the register-streamed kernel for prefill-sized
+// calls: a workgroup takes one chunk of 16 MT gathered rows, all of one
+// expert, and NT 16-row weight tiles of that expert's slab; with SwiGLU the
+// first NT / 2 tiles are gate rows and the rest the matching up rows N / 2
+// further on, and the epilogue writes silu(g) * u.  Output rows go to the
+// rows' entries.  Replaces the backend kernel of Op::DequantGroupedMatMul
+// and the MoE expert FFN (crates/rlx-models-core/src/standard_decoder.rs:
+// 12634-12760) at prefill sizes.
+template <int SCH, int MT, int NT, int D, bool SW>
+RLXQ_DEV void moe_sk_body(const rlxq_moe_sk_args& a) {
+  constexpr int NH = SW ? NT / 2 : NT;   // output column tiles
+  static_assert(!SW || NT % 2 == 0, "gate/up tile pairs");
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 15, g = lane >> 4;
+  const int chunk = blockIdx.x / a.tiles_n, tn = blockIdx.x % a.tiles_n;
+  if (chunk >= a.cmap[0]) return;
+  const int e = a.cmap[1 + chunk];
+  const int64_t m0 = (int64_t)chunk * 16 * MT;
+  const int64_t width = SW ? a.N / 2 : a.N;
+  const int64_t n0 = (int64_t)tn * 16 * NH;
+  int64_t wrow[NT];
+  bool wok[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) {
+    const int64_t c = n0 + 16 * (t % NH) + j;
+    wok[t] = c < width;
+    const int64_t cc = wok[t] ? c : width - 1;
+    wrow[t] = (SW && t >= NH) ? width + cc : cc;
+  }
+  f32x4_t acc[MT][NT];
+  if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.Mp, m0, a.bank + (int64_t)e * a.N * a.rb, a.rb, a.K, 0, a.K, wrow,
+                                      wok, acc))
+    return;
+  // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int64_t m = m0 + 16 * mt + 4 * g + r;
+      const int32_t ent = a.emap[m];
+      if (ent < 0) continue;
+      const float is = a.inv_s[m];
+#pragma unroll
+      for (int t = 0; t < NH; t++) {
+        const int64_t c = n0 + 16 * t + j;
+        if (c >= width) continue;
+        float o = acc[mt][t][r] * is;
+        if constexpr (SW) o = o / (1.f + expf(-o)) * (acc[mt][t + NH][r] * is);   // silu(g) * u
+        const int64_t off = (int64_t)ent * a.y_ld + c;
+        if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(o);
+        else reinterpret_cast<float*>(a.y)[off] = o;
       }
     }
 }
@@ -685,7 +763,9 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
   const int64_t r = blockIdx.x;
   const int64_t nblk = a.K >> 5;
   const int t = threadIdx.x;
-  if (r >= a.M) {
+  const int32_t ent = a.rmap ? (r < a.Mp ? a.rmap[r] : -1) : 0;
+  const int64_t src = a.rmap ? (int64_t)(ent >= 0 ? ent : 0) / a.rdiv : r;   // x row of x16 row r
+  if (a.rmap ? ent < 0 : r >= a.M) {
     // padding rows of the fragment-major layout: zeros
     if (!a.frag_major || r >= a.Mp) return;
     uint4* dst = reinterpret_cast<uint4*>(a.x16);
@@ -696,7 +776,7 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
   }
   auto load_blk32 = [&](int64_t b, float* v) {
     if (a.x_bf16) {
-      const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + r * a.K + b * 32);
+      const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + src * a.K + b * 32);
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         const uint4 u = p[q];
@@ -708,7 +788,7 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
         }
       }
     } else {
-      const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.x) + r * a.K + b * 32);
+      const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.x) + src * a.K + b * 32);
 #pragma unroll
       for (int q = 0; q < 8; q++) {
         const float4 u = p[q];
@@ -890,3 +970,85 @@ RLXQ_SKINNYNS_INST(q4_0, SCH_Q4_0, 4, 1, 3)
 RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 1, 1, 3)
 RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 2, 1, 3)
 RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 4, 1, 3)
+
+// Gathered-row layout of the grouped MFMA path (see rlxq_moe_pad_args): one
+// workgroup of 1024 threads, thread f for fired-expert slot f (E <= 1024).
+extern "C" __global__ __launch_bounds__(1024) void rlxq_moe_pad_k(rlxq_moe_pad_args a) {
+  __shared__ int32_t wsum[16];
+  __shared__ int32_t cstart[1025];   // first chunk of each slot, then the total
+  const int f = threadIdx.x, lane = f & 63, wv = f >> 6;
+  const int F = a.table[0];
+  const int32_t* off = a.table + 1 + a.E;
+  const int32_t* perm = a.table + 2 + 2 * a.E;
+  const int R = a.rows_per_chunk;
+  const int cnt = f < F ? off[f + 1] - off[f] : 0;
+  const int ch = (cnt + R - 1) / R;
+  // exclusive sum of the chunk counts over the 1024 threads
+  int inc = ch;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += o;
+  }
+  if (lane == 63) wsum[wv] = inc;
+  __syncthreads();
+  int base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < 16; w++) {
+    base += w < wv ? wsum[w] : 0;
+    total += wsum[w];
+  }
+  const int first = base + inc - ch;
+  if (f < F) cstart[f] = first;
+  if (f == 0) {
+    a.cmap[0] = total;
+    cstart[F] = total;
+  }
+  __syncthreads();
+  // every gathered row (and chunk) by all threads: the slot of chunk c is the
+  // last slot whose first chunk is at most c
+  auto slot_of = [&](int c) {
+    int lo = 0, hi = F - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (cstart[mid] <= c) lo = mid;
+      else hi = mid - 1;
+    }
+    return lo;
+  };
+  for (int c = f; c < total; c += 1024) a.cmap[1 + c] = a.table[1 + slot_of(c)];
+  for (int64_t p = f; p < a.Mp; p += 1024) {
+    const int c = (int)(p / R);
+    int32_t v = -1;
+    if (c < total) {
+      const int s = slot_of(c);
+      const int64_t local = p - (int64_t)cstart[s] * R;
+      if (local < off[s + 1] - off[s]) v = perm[off[s] + local];
+    }
+    a.emap[p] = v;
+  }
+}
+
+// Grouped MFMA variants: rlxq_moesk_<scheme>_mt<MT>_nt<NT>_d<D>[_sw].
+#define RLXQ_MOESK_INST(SNAME, SCH, MT, NT, D)                                                         \
+  extern "C" __global__ __launch_bounds__(256) void rlxq_moesk_##SNAME##_mt##MT##_nt##NT##_d##D(        \
+      rlxq_moe_sk_args a) {                                                                            \
+    rlxq::moe_sk_body<SCH, MT, NT, D, false>(a);                                                       \
+  }                                                                                                    \
+  extern "C" __global__ __launch_bounds__(256) void rlxq_moesk_##SNAME##_mt##MT##_nt##NT##_d##D##_sw(   \
+      rlxq_moe_sk_args a) {                                                                            \
+    rlxq::moe_sk_body<SCH, MT, NT, D, true>(a);                                                        \
+  }
+#define RLXQ_MOESK_SCHEME(SNAME, SCH, D1)   \
+  RLXQ_MOESK_INST(SNAME, SCH, 1, 2, D1)     \
+  RLXQ_MOESK_INST(SNAME, SCH, 1, 4, 2)      \
+  RLXQ_MOESK_INST(SNAME, SCH, 1, 8, 2)      \
+  RLXQ_MOESK_INST(SNAME, SCH, 2, 2, 3)      \
+  RLXQ_MOESK_INST(SNAME, SCH, 2, 4, 2)      \
+  RLXQ_MOESK_INST(SNAME, SCH, 2, 8, 1)      \
+  RLXQ_MOESK_INST(SNAME, SCH, 4, 2, 2)      \
+  RLXQ_MOESK_INST(SNAME, SCH, 4, 4, 1)
+RLXQ_MOESK_SCHEME(q4_1, SCH_Q4_1, 4)
+RLXQ_MOESK_SCHEME(q4_0, SCH_Q4_0, 4)
+RLXQ_MOESK_SCHEME(q8_0, SCH_Q8_0, 4)
+RLXQ_MOESK_SCHEME(q4_k, SCH_Q4_K, 3)

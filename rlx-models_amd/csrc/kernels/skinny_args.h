@@ -17,7 +17,10 @@ typedef struct rlxq_x16_args {
   float* inv_s;
   int64_t M, K, Mp;
   int32_t x_bf16, nibble_order;
-  int32_t frag_major, pad;
+  int32_t frag_major, rdiv;
+  /* gathered rows (fragment-major only): x16 row r is x row rmap[r] / rdiv,
+   * a zero row where rmap[r] < 0; NULL: x16 row r is x row r             */
+  const int32_t* rmap;
 } rlxq_x16_args;
 
 typedef struct rlxq_skinny_args {

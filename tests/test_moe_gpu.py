@@ -633,6 +633,7 @@ def test_combine_in_down_launch_matches_combine_kernel(ctx, orc, monkeypatch, to
 
     H, I, E, TOPK = 2048, 768, 128, 8
     announce(f"moe fused combine tokens={tokens} y={ydt}")
+    monkeypatch.setenv("RLXQ_MOE_KERNEL", "xr")   # (128 tokens would take the grouped MFMA path)
     rng = np.random.default_rng(tokens)
     down = orc.synth_q4_1(rng, E * H, I)
     dt = _t(down)
