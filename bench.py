@@ -21,7 +21,7 @@ Extra keys of the same JSON line:
   prefill_detail  config 4: Q4_1 dequant-GEMM, M in {512, 2048, 4096}, Q4_K
                   at M=4096, and the W8A8 variant (per-row int8 activations
                   computed on the fly x per-channel int8 weights)
-  batched_decode  config 3: Q4_1 and Q8_0 (and Q4_K), M in {1, 4, 16, 64}
+  batched_decode  config 3: Q4_1 and Q8_0 (and Q4_K, Q6_K), M in {1, 4, 16, 64}
   moe             config 5: routed-expert grouped GEMV, 16 tokens, top-8 of 128
   moe_q4_k        the same with Q4_K expert banks (a Q4_K_M MoE checkpoint)
   moe_prefill     the config-5 layer at 256 tokens (grouped MFMA kernels)
@@ -332,15 +332,16 @@ def prefill_headline(detail: dict) -> dict:
 
 
 def batched_section(ctx, gen, sptr, stream) -> dict:
-    """Config 3: batched decode, Q4_1 and Q8_0 (and Q4_K beside them), M in
-    {1, 4, 16, 64}, bf16 x, f32 y."""
+    """Config 3: batched decode, Q4_1 and Q8_0 (and Q4_K, Q6_K beside them), M
+    in {1, 4, 16, 64}, bf16 x, f32 y."""
     import torch
     import rlxq
 
     res = {}
     for sname, scheme, bpw, synth in (("q4_1", rlxq.GGUF_Q4_1, Q4_1_BPW, synth_q4_1_gpu),
                                       ("q8_0", rlxq.GGUF_Q8_0, Q8_0_BPW, synth_q8_0_gpu),
-                                      ("q4_k", rlxq.GGUF_Q4_K, 144 / 256, synth_q4_k_gpu)):
+                                      ("q4_k", rlxq.GGUF_Q4_K, 144 / 256, synth_q4_k_gpu),
+                                      ("q6_k", rlxq.GGUF_Q6_K, 210 / 256, synth_q6_k_gpu)):
         for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):
             wb = n * k * bpw
             ws = [synth(n, k, gen) for _ in range(_copies(wb))]

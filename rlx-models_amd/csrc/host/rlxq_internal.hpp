@@ -105,6 +105,9 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
                   const void* scales, const void* biases, int sb_dtype, int64_t m, int64_t k,
                   int64_t n, void* y, int y_dtype, void* stream);
 bool skinny_applies(int scheme, int64_t m, int64_t k);
+// Whether the batched-decode activations take the nibble-unpacking order
+// (4-bit code formats) or stay in natural order (Q8_0, Q6_K).
+bool sk_nibble(int scheme);
 // Adds the [splits, M, N] f32 partial sums in a.part into a.y (y_ld, y_bf16)
 // in slice order.
 int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream);

@@ -76,7 +76,7 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   char* rest = nullptr;
   int rc;
   const int64_t mp = mch * 16 * MT;
-  if ((rc = prep_x16(ctx, x, x_dtype, m, k, scheme != RLXQ_GGUF_Q8_0, part_bytes, xa, &rest, stream, true, mp)))
+  if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_nibble(scheme), part_bytes, xa, &rest, stream, true, mp)))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
@@ -128,7 +128,7 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   char* rest = nullptr;
   int rc;
   const int64_t mp = mch * 16 * MT;
-  if ((rc = prep_x16(ctx, x, x_dtype, m, k, scheme != RLXQ_GGUF_Q8_0, part_bytes, xa, &rest, stream, true, mp)))
+  if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_nibble(scheme), part_bytes, xa, &rest, stream, true, mp)))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
@@ -162,9 +162,11 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
 }
 }  // namespace
 
+bool sk_nibble(int scheme) { return scheme != RLXQ_GGUF_Q8_0 && scheme != RLXQ_GGUF_Q6_K; }
+
 bool skinny_applies(int scheme, int64_t m, int64_t k) {
   return (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q4_1 ||
-          (scheme == RLXQ_GGUF_Q4_K && k % 256 == 0)) &&
+          ((scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K) && k % 256 == 0)) &&
          m >= 1 && m <= 256 && k % 128 == 0;
 }
 
@@ -182,8 +184,9 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   // and below, and for Q8_0, it was slower).  RLXQ_SKINNY_NS="MT,NT,D" picks
   // a compiled one for any scheme, "0" turns the default off.
   {
-    int nmt = m <= 32 ? 2 : 4, nnt = 1, nd = 3;
-    bool ns = (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_K) && m > 16;
+    const bool q6k = scheme == RLXQ_GGUF_Q6_K;
+    int nmt = m <= 32 ? 2 : 4, nnt = 1, nd = q6k && m > 32 ? 2 : 3;
+    bool ns = (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_K || q6k) && m > 16;
     if (const char* e = std::getenv("RLXQ_SKINNY_NS")) {
       int a1, a2, a3;
       if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) nmt = a1, nnt = a2, nd = a3, ns = true;
@@ -195,11 +198,13 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   {
     int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = 2, xd = m <= 16 ? 4 : (m <= 32 ? 3 : 2);
     if (scheme == RLXQ_GGUF_Q4_K) xd = m <= 16 ? 3 : 2;   // its 13-dword raw blocks
+    if (scheme == RLXQ_GGUF_Q6_K) xd = m <= 32 ? 2 : 1;   // its 22-dword raw blocks
     bool xr = true;
     if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
       int a1, a2, a3;
       if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) xmt = a1, xnt = a2, xd = a3;
-      else if (e[0] == '0') xr = scheme == RLXQ_GGUF_Q4_K;   // (Q4_K has no LDS-staged kernel)
+      else if (e[0] == '0')   // (Q4_K and Q6_K have no LDS-staged kernel)
+        xr = scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K;
     }
     if (xr) return skinny_xr_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, xmt, xnt, xd);
   }
@@ -243,7 +248,7 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   xa.M = m;
   xa.K = k;
   xa.x_bf16 = x_dtype == RLXQ_BF16;
-  xa.nibble_order = scheme != RLXQ_GGUF_Q8_0;
+  xa.nibble_order = sk_nibble(scheme);
   hipFunction_t fn;
   if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
   void* xargs[] = {&xa};

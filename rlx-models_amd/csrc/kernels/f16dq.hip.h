@@ -29,7 +29,11 @@ RLXQ_DEV int perm_k(int p, bool nibble) {
 // dwords.  A Q4_K sub-block normalises to the Q4_1 form: d = d * sc and
 // m = -dmin * mn rounded to f16, and code dword g holding elements 4g..4g+3
 // (low nibbles) and 16 + 4g.. (high nibbles) of the sub-block.
-template <int SCH> constexpr int sk_bdw() { return SCH == SCH_Q8_0 ? 9 : 5; }
+// A Q6_K block normalises to the int8 form of Q8_0 with one f16 scale per
+// 16 weights: scale dword d0 | d1 << 16 (d * sc of the two halves, rounded
+// to f16) and code bytes code + 96, so that code - 32 = byte - 128 as for
+// Q8_0's sign-flipped bytes; its activations stay in natural order.
+template <int SCH> constexpr int sk_bdw() { return (SCH == SCH_Q8_0 || SCH == SCH_Q6_K) ? 9 : 5; }
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
 // 6:4, lgkmcnt 11:8): wait on one counter, leave the others unconstrained.
@@ -50,13 +54,16 @@ RLXQ_DEV f16x8_t dequant_lane(const uint32_t* bp, int g) {
   const uint32_t dm = bp[0];
   const f16x2_t d2 = as_h2(perm_b32(dm, dm, 0x01000100u));
   f16x2_t w[4];
-  if constexpr (SCH == SCH_Q8_0) {
-    const uint32_t u0 = bp[1 + 2 * g] ^ 0x80808080u, u1 = bp[2 + 2 * g] ^ 0x80808080u;
+  if constexpr (SCH == SCH_Q8_0 || SCH == SCH_Q6_K) {
+    const uint32_t flip = SCH == SCH_Q8_0 ? 0x80808080u : 0u;
+    const uint32_t u0 = bp[1 + 2 * g] ^ flip, u1 = bp[2 + 2 * g] ^ flip;
+    // (Q6_K: positions 8g.. lie in half g / 2 of the block)
+    const f16x2_t dd = SCH == SCH_Q6_K ? as_h2(perm_b32(dm, dm, g < 2 ? 0x01000100u : 0x03020302u)) : d2;
     const f16x2_t off = {(_Float16)-1152.f, (_Float16)-1152.f};
-    w[0] = (magic_lo(u0) + off) * d2;
-    w[1] = (magic_hi(u0) + off) * d2;
-    w[2] = (magic_lo(u1) + off) * d2;
-    w[3] = (magic_hi(u1) + off) * d2;
+    w[0] = (magic_lo(u0) + off) * dd;
+    w[1] = (magic_hi(u0) + off) * dd;
+    w[2] = (magic_lo(u1) + off) * dd;
+    w[3] = (magic_hi(u1) + off) * dd;
   } else {
     const uint32_t qs = bp[1 + g];
     const uint32_t lo = qs & 0x0F0F0F0Fu, hi = (qs >> 4) & 0x0F0F0F0Fu;
@@ -81,7 +88,18 @@ RLXQ_DEV f16x8_t dequant_lane(const uint32_t* bp, int g) {
 // Raw block -> normalised dwords.
 template <int SCH>
 RLXQ_DEV void normalise(const RawBlk<SCH>& r, uint32_t* o) {
-  if constexpr (SCH == SCH_Q4_K) {
+  if constexpr (SCH == SCH_Q6_K) {
+    const float d = f16_bits_to_f32(r.d);
+    const float ds0 = d * (float)(int8_t)(r.sc & 0xffu), ds1 = d * (float)(int8_t)(r.sc >> 8);
+    o[0] = f32_to_f16_bits(ds0) | (f32_to_f16_bits(ds1) << 16);
+    const uint32_t s1 = 4u * (r.q >> 1), s2 = 2u * r.q;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t l = align_bytes(r.ql[i + 1], r.ql[i], r.off), hq = align_bytes(r.qh[i + 1], r.qh[i], r.off);
+      // code (0..63) + 96 per byte: no carry between bytes
+      o[1 + i] = (((l >> s1) & 0x0F0F0F0Fu) | (((hq >> s2) & 0x03030303u) << 4)) + 0x60606060u;
+    }
+  } else if constexpr (SCH == SCH_Q4_K) {
     const uint32_t hd[4] = {r.hd.x, r.hd.y, r.hd.z, r.hd.w};
     float sc, mn;
     q4k_scale_min(hd, (int)r.sub, sc, mn);

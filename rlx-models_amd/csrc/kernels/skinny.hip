@@ -953,6 +953,10 @@ RLXQ_SKINNYXR_INST(q8_0, SCH_Q8_0, 4, 2, 2)
 RLXQ_SKINNYXR_INST(q4_k, SCH_Q4_K, 1, 2, 3)
 RLXQ_SKINNYXR_INST(q4_k, SCH_Q4_K, 2, 2, 2)
 RLXQ_SKINNYXR_INST(q4_k, SCH_Q4_K, 4, 2, 2)
+// Q6_K (22-dword raw blocks)
+RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 1, 2, 2)
+RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 2, 2, 2)
+RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 4, 2, 1)
 
 // N-split variants: rlxq_skinnyns_<scheme>_mt<MT>_nt<NT>_d<D>.
 #define RLXQ_SKINNYNS_INST(SNAME, SCH, MT, NT, D)                                                      \
@@ -970,6 +974,9 @@ RLXQ_SKINNYNS_INST(q4_0, SCH_Q4_0, 4, 1, 3)
 RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 1, 1, 3)
 RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 2, 1, 3)
 RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 4, 1, 3)
+RLXQ_SKINNYNS_INST(q6_k, SCH_Q6_K, 1, 1, 3)
+RLXQ_SKINNYNS_INST(q6_k, SCH_Q6_K, 2, 1, 3)
+RLXQ_SKINNYNS_INST(q6_k, SCH_Q6_K, 4, 1, 2)
 
 // Gathered-row layout of the grouped MFMA path (see rlxq_moe_pad_args): one
 // workgroup of 1024 threads, thread f for fired-expert slot f (E <= 1024).

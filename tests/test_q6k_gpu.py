@@ -91,7 +91,8 @@ def test_q6k_every_record_variant(ctx, orc, monkeypatch, cfg):
 
 def test_q6k_bf16_output_and_prefill_rows(ctx, orc, monkeypatch):
     """bf16 output from 64 rows: the MFMA GEMM by default, the GEMV's
-    multi-row path when forced."""
+    multi-row path when forced (RLXQ_PREFILL and RLXQ_DECODE: 80 rows would
+    otherwise take the batched-decode MFMA kernels)."""
     import torch
 
     k, n, m = 1024, 300, 80
@@ -102,6 +103,7 @@ def test_q6k_bf16_output_and_prefill_rows(ctx, orc, monkeypatch):
     assert ctx.last_kernel.startswith("rlxq_gemm_q6_k_t256"), ctx.last_kernel
     assert rel_err(got, want) <= 2e-2
     monkeypatch.setenv("RLXQ_PREFILL", "gemv")
+    monkeypatch.setenv("RLXQ_DECODE", "gemv")
     got, want = _run(ctx, orc, x, packed, n, y_dtype=torch.bfloat16)
     assert ctx.last_kernel.startswith("rlxq_gemv_q6_k_"), ctx.last_kernel
     assert rel_err(got, want) <= 2e-2

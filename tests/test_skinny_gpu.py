@@ -223,3 +223,40 @@ def test_skinny_q4_k_activation_range_and_no_staged_kernel(ctx, orc, monkeypatch
             assert np.all(got[r] == 0.0)
             continue
         assert rel_err(got[r:r + 1], want[r:r + 1]) <= TOL_F32, r
+
+
+# Q6_K (GGML block_q6_K, 210-byte super-blocks, 2-byte aligned every other
+# time): the int8 form of Q8_0 with one f16 scale d * sc per 16 weights
+Q6K_XR = ["1,2,2", "2,2,2", "4,2,1"]
+Q6K_NS = ["1,1,3", "2,1,3", "4,1,2"]
+
+
+@pytest.mark.parametrize("mkn", [(5, 256, 7), (16, 4096, 512), (17, 1280, 300), (33, 2304, 129),
+                                 (64, 4096, 256), (100, 768, 200)], ids=str)
+def test_skinny_q6_k_default(ctx, orc, mkn):
+    m, k, n = mkn
+    announce(f"skinny q6_k default {mkn}")
+    rng = np.random.default_rng(m * 5 + k + n)
+    packed = orc.synth(8, rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[0] *= 300.0
+    got, want = run_dense(ctx, orc, 8, x, packed, n, xdt="bf16")
+    prefix = "rlxq_skinnyxr_q6_k_" if m <= 16 else "rlxq_skinnyns_q6_k_"
+    assert ctx.last_kernel.startswith(prefix), ctx.last_kernel
+    assert rel_err(got, want) <= TOL_F32
+
+
+@pytest.mark.parametrize("cfg", [("xr", c) for c in Q6K_XR] + [("ns", c) for c in Q6K_NS], ids=str)
+def test_skinny_q6_k_every_variant(ctx, orc, monkeypatch, cfg):
+    kind, rest = cfg
+    monkeypatch.setenv("RLXQ_SKINNY_XR" if kind == "xr" else "RLXQ_SKINNY_NS", rest)
+    mt, nt, d = (int(v) for v in rest.split(","))
+    for (m, k, n) in [(5, 256, 7), (16 * mt + 3, 2304, 64 * nt * 3 + 5), (9, 12288, 200), (64, 1536, 96),
+                      (3, 768, 64 * nt)]:
+        announce(f"skinny q6_k {kind} {rest} {(m, k, n)}")
+        rng = np.random.default_rng(m + k + n + mt + 1)
+        packed = orc.synth(8, rng, n, k)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        got, want = run_dense(ctx, orc, 8, x, packed, n, xdt="bf16")
+        assert ctx.last_kernel == f"rlxq_skinny{kind}_q6_k_mt{mt}_nt{nt}_d{d}", ctx.last_kernel
+        assert rel_err(got, want) <= TOL_F32, (cfg, m, k, n)
