@@ -108,9 +108,10 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   // of 16 MT entries of an expert (device table, then the gathered-row
   // layout, then the prepared rows).  RLXQ_MOE_KERNEL=sk forces them where
   // they apply; xr or lds keeps the GEMV kernels.
+  const bool q6k = scheme == RLXQ_GGUF_Q6_K;
   const bool sk_ok = xbf && k % 128 == 0 &&
                      (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0 ||
-                      (q4k && k % 256 == 0));
+                      ((q4k || q6k) && k % 256 == 0));
   bool sk = sk_ok && n_entries >= 8 * fired_est;
   if (const char* ev = std::getenv("RLXQ_MOE_KERNEL")) {
     if (!std::strcmp(ev, "sk")) sk = sk_ok;
@@ -229,9 +230,12 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     // rows (SwiGLU: NT / 2 gate tiles and their up tiles)
     const int NT = sk_nt;
     const int nh = swiglu ? NT / 2 : NT;
+    // ring depth of the compiled variant (Q6_K's larger raw blocks: one
+    // shallower)
     int D = sk_d;
     if (D <= 0) D = NT >= 4 ? (NT == 8 && sk_mt == 2 ? 1 : (sk_mt == 4 ? 1 : 2))
                             : (sk_mt == 1 ? (q4k ? 3 : 4) : (sk_mt == 2 ? 3 : 2));
+    if (sk_d <= 0 && q6k) D = NT >= 4 || sk_mt == 4 ? 1 : 2;
     rlxq_moe_sk_args ka;
     std::memset(&ka, 0, sizeof ka);
     ka.x16 = xa.x16;

@@ -1059,3 +1059,9 @@ RLXQ_MOESK_SCHEME(q4_1, SCH_Q4_1, 4)
 RLXQ_MOESK_SCHEME(q4_0, SCH_Q4_0, 4)
 RLXQ_MOESK_SCHEME(q8_0, SCH_Q8_0, 4)
 RLXQ_MOESK_SCHEME(q4_k, SCH_Q4_K, 3)
+// Q6_K (22-dword raw blocks: shallower rings)
+RLXQ_MOESK_INST(q6_k, SCH_Q6_K, 1, 2, 2)
+RLXQ_MOESK_INST(q6_k, SCH_Q6_K, 1, 4, 1)
+RLXQ_MOESK_INST(q6_k, SCH_Q6_K, 2, 2, 2)
+RLXQ_MOESK_INST(q6_k, SCH_Q6_K, 2, 4, 1)
+RLXQ_MOESK_INST(q6_k, SCH_Q6_K, 4, 2, 1)

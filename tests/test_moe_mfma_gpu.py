@@ -1,5 +1,5 @@
 """The grouped f16-MFMA path of the expert ops for prefill-sized calls
-(GGUF Q4_1, Q4_0, Q8_0, Q4_K codes, bf16 activations, at least 8 entries per
+(GGUF Q4_1, Q4_0, Q8_0, Q4_K, Q6_K codes, bf16 activations, at least 8 entries per
 fired expert): the device table, the gathered-row layout (each expert's
 entries padded to whole chunks), the prepared f16 rows and the grouped
 kernel, through the C ABI.  Against the float64 oracle on the activations
@@ -14,7 +14,7 @@ from test_gemv_gpu import _t, rel_err
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
-SCHEMES = {"q4_1": 3, "q4_0": 2, "q8_0": 1, "q4_k": 7}
+SCHEMES = {"q4_1": 3, "q4_0": 2, "q8_0": 1, "q4_k": 7, "q6_k": 8}
 
 
 @pytest.mark.parametrize("name", list(SCHEMES))
