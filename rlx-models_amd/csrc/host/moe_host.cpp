@@ -112,9 +112,12 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   const bool sk_ok = xbf && k % 128 == 0 &&
                      (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0 ||
                       ((q4k || q6k) && k % 256 == 0));
-  bool sk = sk_ok && n_entries >= 8 * fired_est;
+  // (the gathered f16 rows take about 2 K bytes per entry: calls needing
+  // more than 1 GiB of them stay on the GEMV kernels)
+  const bool sk_fits = (double)(n_entries + fired_est * 63) * (double)k * 2.0 <= (double)(1u << 30);
+  bool sk = sk_ok && sk_fits && n_entries >= 8 * fired_est;
   if (const char* ev = std::getenv("RLXQ_MOE_KERNEL")) {
-    if (!std::strcmp(ev, "sk")) sk = sk_ok;
+    if (!std::strcmp(ev, "sk")) sk = sk_ok && sk_fits;
     else sk = false;
   }
   if (sk) {
