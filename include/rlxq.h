@@ -30,9 +30,9 @@
  *     stays valid.  A call under stream capture must not need growth (the
  *     allocation fails under global capture): size the stream's scratch
  *     first with rlxq_reserve_workspace, or run the call once uncaptured.
- *     The MoE combine fused into the down launch also takes 64 KB of
- *     per-stream counters, zeroed once when first used (or by
- *     rlxq_reserve_workspace) and left at zero by every call.
+ *     The MoE combine fused into the down launch (when selected) also
+ *     takes 64 KB of per-stream counters, zeroed once when first used (or
+ *     by rlxq_reserve_workspace) and left at zero by every call.
  */
 #ifndef RLXQ_H
 #define RLXQ_H

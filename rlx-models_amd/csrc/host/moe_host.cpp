@@ -295,11 +295,14 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   const int64_t grid = slots * ga.tiles_n;
   if (grid > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": grid too large");
   // The combine in the down launch itself (register kernels with the
-  // routing in the workgroups): the workgroup completing a (token row, tile)
-  // sums it.  RLXQ_MOE_COMBINE=launch keeps the separate combine kernel.
-  bool fuse_combine = combine && xr && fused && rows * ga.tiles_n <= rlxq_ctx::kCounterSlots;
+  // routing in the workgroups: the workgroup completing a (token row, tile)
+  // sums it) is selected by RLXQ_MOE_COMBINE=fused.  The separate combine
+  // kernel stays the default: on one box, three runs each, the config-5
+  // layer took 75.6-77.8 us fused against 72.3-76.6 with the extra launch
+  // (the last workgroup of each token adds the sum to the kernel's tail).
+  bool fuse_combine = false;
   if (const char* ev = std::getenv("RLXQ_MOE_COMBINE"))
-    if (!std::strcmp(ev, "launch")) fuse_combine = false;
+    if (!std::strcmp(ev, "fused")) fuse_combine = combine && xr && fused && rows * ga.tiles_n <= rlxq_ctx::kCounterSlots;
   if (fuse_combine) {
     if ((rc = zeroed_counters(ctx, stream, &ga.counters))) return rc;
     ga.probs = probs;

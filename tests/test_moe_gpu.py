@@ -623,8 +623,9 @@ def test_two_streams_use_their_own_workspace(ctx, orc):
 @pytest.mark.parametrize("ydt", ["f32", "bf16"])
 def test_combine_in_down_launch_matches_combine_kernel(ctx, orc, monkeypatch, tokens, ydt):
     """COMBINE on the register kernels with the routing in the workgroups
-    sums each token's top-k rows in the down launch itself (the workgroup
-    that completes a (token, tile) does it).  It must equal the separate
+    can sum each token's top-k rows in the down launch itself
+    (RLXQ_MOE_COMBINE=fused: the workgroup that completes a (token, tile)
+    does it).  It must equal the separate
     combine kernel bit for bit, with invalid expert ids in some rows (they
     contribute nothing), over consecutive calls (the counters reset), and
     against the float64 oracle."""
@@ -646,7 +647,7 @@ def test_combine_in_down_launch_matches_combine_kernel(ctx, orc, monkeypatch, to
         ids[tokens - 1, 0] = E + 5
         probs = rng.uniform(0.01, 0.3, (tokens, TOPK)).astype(np.float32)
         it, pt = _t(ids), _t(probs)
-        monkeypatch.delenv("RLXQ_MOE_COMBINE", raising=False)
+        monkeypatch.setenv("RLXQ_MOE_COMBINE", "fused")
         y = ctx.moe_grouped(at, dt, it, pt, rlxq.GGUF_Q4_1, rlxq.MOE_COMBINE, H, E, y_dtype=ydtype)
         torch.cuda.synchronize()
         assert ctx.last_kernel.startswith("rlxq_moexrf_q4_1_"), ctx.last_kernel
