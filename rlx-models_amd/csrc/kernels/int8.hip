@@ -35,27 +35,41 @@ RLXQ_DEV i32x2_t lds_tr8(const uint8_t* p) {
 
 // ---------------------------------------------------------------- W8A8 GEMM
 
-// y[m, n] = (float(acc) * sx[m]) * sw[n], two roundings in this order.
+// y[m, n] = (float(acc) * sx[m]) * sw[n], two roundings in this order.  The
+// output dtype and whether the workgroup's tile lies wholly inside M x N are
+// decided once; a lane stores through one base pointer at wave-uniform
+// offsets, so a whole tile needs no per-element bounds checks or 64-bit
+// multiplies.
 template <int TM, int TN>
 RLXQ_DEV void w8a8_epilogue(const rlxq_w8a8_args& a, const i32x16_t (&acc)[TM][TN], int64_t mb, int64_t nb,
-                            int lane) {
+                            int lane, bool whole) {
 #pragma clang fp contract(off)
+  const int64_t m1 = mb + 4 * (lane >> 5), n1 = nb + (lane & 31);   // the lane's first row, column
+  auto epi = [&](auto put, auto checked) {
 #pragma unroll
-  for (int j = 0; j < TN; j++) {
-    const int64_t n = nb + j * 32 + (lane & 31);
-    if (n >= a.N) continue;
-    const float sw = a.sw[n];
+    for (int j = 0; j < TN; j++) {
+      const int64_t n = n1 + j * 32;
+      if (checked.value && n >= a.N) continue;
+      const float sw = a.sw[n];
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+      for (int i = 0; i < TM; i++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int64_t m = mb + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-        if (m < a.M) {
-          const float v = ((float)acc[i][j][r] * a.sx[m]) * sw;
-          if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
-          else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
+        for (int r = 0; r < 16; r++) {
+          const int dm = i * 32 + 8 * (r / 4) + (r % 4);
+          if (!checked.value || m1 + dm < a.M) put(dm, j * 32, ((float)acc[i][j][r] * a.sx[m1 + dm]) * sw);
         }
-      }
+    }
+  };
+  auto epi_any = [&](auto put) {
+    if (whole) epi(put, std::false_type{});
+    else epi(put, std::true_type{});
+  };
+  if (a.y_bf16) {
+    uint16_t* p = reinterpret_cast<uint16_t*>(a.y) + m1 * a.y_ld + n1;
+    epi_any([&](int dm, int dn, float v) { p[(int64_t)dm * a.y_ld + dn] = (uint16_t)f32_to_bf16_bits(v); });
+  } else {
+    float* p = reinterpret_cast<float*>(a.y) + m1 * a.y_ld + n1;
+    epi_any([&](int dm, int dn, float v) { p[(int64_t)dm * a.y_ld + dn] = v; });
   }
 }
 
@@ -217,7 +231,7 @@ RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
       compute(0);
     }
   }
-  w8a8_epilogue<TM, TN>(a, acc, m0 + wm * WM, n0 + wn * WN, lane);
+  w8a8_epilogue<TM, TN>(a, acc, m0 + wm * WM, n0 + wn * WN, lane, m0 + BM <= a.M && n0 + BN <= a.N);
 }
 
 // ------------------------------------------------------------- Int8Block
