@@ -30,19 +30,24 @@ const W8a8Cfg kW8a8[] = {
     {"m128n128k64w22", 128, 128, 64, 2, 2},  {"m128n128k128w22", 128, 128, 128, 2, 2},
     {"m256n128k64w22", 256, 128, 64, 2, 2},  {"m128n256k64w22", 128, 256, 64, 2, 2},
     {"m256n256k64w24", 256, 256, 64, 2, 4},  {"m128n128k128w22_p2", 128, 128, 128, 2, 2},
+    {"m256n256k128w24", 256, 256, 128, 2, 4},
 };
 
 // Tiling choice; RLXQ_W8A8_CFG=<name> selects one (tuning sweeps and the
 // per-variant parity test).
-// Default: 256 x 256 tiles (8 waves) once they cover the CUs, else 128 x 128.
-const W8a8Cfg* pick_w8a8(int64_t m, int64_t n, int cus) {
+// Default: 256 x 256 tiles (8 waves) once they cover the CUs, else 128 x 128;
+// the 256 x 256 tiles take 128-byte K steps from K = 8192 (Qwen3-8B down at
+// M=4096: 244 us against 254 with 64-byte steps; gate_up, K = 4096, the
+// same either way; the two-stage variants of both measured 5-30% slower).
+const W8a8Cfg* pick_w8a8(int64_t m, int64_t n, int64_t k, int cus) {
   if (const char* e = std::getenv("RLXQ_W8A8_CFG")) {
     for (const auto& c : kW8a8)
       if (std::strcmp(c.name, e) == 0) return &c;
     return nullptr;
   }
   const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256);
-  return t256 >= (cus > 0 ? cus : 256) ? &kW8a8[4] : &kW8a8[0];
+  if (t256 < (cus > 0 ? cus : 256)) return &kW8a8[0];
+  return k >= 8192 && k % 128 == 0 ? &kW8a8[6] : &kW8a8[4];
 }
 
 }  // namespace
@@ -172,7 +177,7 @@ int rlxq_w8a8_gemm(rlxq_ctx* ctx, const void* x, int x_dtype, const int8_t* wq, 
   if (!aligned16(wq)) return fail(ctx, RLXQ_E_ALIGN, "w8a8_gemm: wq must be 16-byte aligned");
   if (m == 0) return RLXQ_OK;
 
-  const W8a8Cfg* c = pick_w8a8(m, n, ctx->cu_count);
+  const W8a8Cfg* c = pick_w8a8(m, n, k, ctx->cu_count);
   if (!c) return fail(ctx, RLXQ_E_NOKERNEL, "w8a8_gemm: RLXQ_W8A8_CFG names no compiled tiling");
   const int64_t tiles_m = (m + c->BM - 1) / c->BM, tiles_n = (n + c->BN - 1) / c->BN;
   if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "w8a8_gemm: too many tiles");

@@ -508,6 +508,7 @@ RLXQ_W8A8_INST(256, 128, 64, 2, 2)
 RLXQ_W8A8_INST(128, 256, 64, 2, 2)
 RLXQ_W8A8_INST(256, 256, 64, 2, 4)
 RLXQ_W8A8_INST_P2(128, 128, 128, 2, 2)
+RLXQ_W8A8_INST(256, 256, 128, 2, 4)
 
 #define RLXQ_I8B_INST(MT, XN, XBF)                                                        \
   extern "C" __global__ __launch_bounds__(256) void rlxq_i8b_##XN##_mt##MT(rlxq_i8b_args a) { \

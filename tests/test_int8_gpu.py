@@ -120,7 +120,7 @@ def test_w8a8_bf16_output_bit_exact(ctx, orc, rng):
 
 
 W8A8_CFGS = ["m128n128k64w22", "m128n128k128w22", "m256n128k64w22", "m128n256k64w22", "m256n256k64w24",
-             "m128n128k128w22_p2"]
+             "m128n128k128w22_p2", "m256n256k128w24"]
 
 
 @pytest.mark.parametrize("cfg", W8A8_CFGS)
