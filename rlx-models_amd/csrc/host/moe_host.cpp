@@ -156,6 +156,48 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     ga.tile_rows = tile;
     ga.tiles_n = (int32_t)(swiglu ? (width + tile / 2 - 1) / (tile / 2) : (n + tile - 1) / tile);
   }
+  // COMBINE on the register kernels at decode sizes: down and combine in one
+  // token-major launch (rlxq_moexc_*: workgroup = token row and column tile,
+  // wave = top-k slot, the slots summed in slot order in the workgroup; the
+  // same bits as the expert-major kernel plus rlxq_moe_combine_k).
+  // RLXQ_MOE_COMBINE=launch keeps the two launches, =fused the combine in the
+  // expert-major launch (counters); RLXQ_MOE_XC_TILE=<columns> sets the tile.
+  bool xc = combine && xr && fused && top_k <= 8 && x_div == 1 && rows <= 0x7fffffff;
+  if (const char* ev = std::getenv("RLXQ_MOE_COMBINE"))
+    if (!std::strcmp(ev, "launch") || !std::strcmp(ev, "fused")) xc = false;
+  if (xc) {
+    int64_t tc = 128;
+    if (const char* ev = std::getenv("RLXQ_MOE_XC_TILE")) tc = std::max<int64_t>(16, std::min<int64_t>(1024, std::atoi(ev)));
+    tc = std::min<int64_t>(tc, ((n + 15) / 16) * 16);
+    std::snprintf(name, sizeof name, "rlxq_moexc_%s_L%d_U%d", scheme_name(scheme), L, NU);
+    hipFunction_t fx;
+    if ((rc = get_fn(ctx, name, &fx))) return rc;
+    ga.x = x;
+    ga.bank = static_cast<const uint8_t*>(bank);
+    ga.N = n;
+    ga.rb = rb;
+    ga.x_ld = k;
+    ga.K = (int32_t)k;
+    ga.E = (int32_t)num_experts;
+    ga.group = is_mlx(scheme) ? group : 32;
+    ga.sb_bf16 = sb_code(sb_dtype);
+    ga.scales = scales;
+    ga.biases = biases;
+    ga.x_div = 1;
+    ga.ids = ids;
+    ga.idx_f32 = idx;
+    ga.n_entries = (int32_t)n_entries;
+    ga.probs = probs;
+    ga.out = y;
+    ga.out_bf16 = y_dtype == RLXQ_BF16 ? 1 : 0;
+    ga.top_k = top_k;
+    ga.tile_rows = (int32_t)tc;
+    ga.tiles_n = (int32_t)((n + tc - 1) / tc);
+    const int64_t grid = rows * ga.tiles_n;
+    if (grid > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": grid too large");
+    void* xargs[] = {&ga};
+    return launch(ctx, fx, dim3((unsigned)grid), dim3(64 * top_k), (size_t)top_k * tc * 4, stream, xargs, name);
+  }
   const size_t table_bytes = fused ? 0 : ((size_t)(2 + 2 * num_experts + n_entries) * 4 + 255) & ~size_t(255);
   const size_t tmp_bytes = combine ? (((size_t)n_entries * width * 4 + 255) & ~size_t(255)) : 0;
   // grouped MFMA path: chunks of RPC gathered rows, each expert's entries

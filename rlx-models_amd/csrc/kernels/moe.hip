@@ -300,7 +300,7 @@ RLXQ_DEV void moe_tile(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, 
 // ---------------------------------------------------------------------------
 template <int SCH, int L, int NU, int MT, int D, bool SWIGLU>
 RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* perm, int beg, int end, int wq,
-                          int nw) {
+                          int nw, int64_t cb = 0, int64_t ce = -1, float* vout = nullptr) {
   constexpr int BLOCKS = Unit<SCH>::BLOCKS;
   constexpr int DW = Unit<SCH>::DW;
   constexpr int BYTES = Unit<SCH>::BYTES;
@@ -315,6 +315,9 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
   const int U = (K >> 5) / BLOCKS;
   const int lane = threadIdx.x & 63, g = lane / L, li = lane % L;
   const int64_t width = SWIGLU ? a.N / 2 : a.N;
+  // output columns [cb, ce) (default: all); vout != NULL: the single entry's
+  // values go to vout[col - cb] instead of y
+  if (ce < 0) ce = width;
   const uint8_t* wbase = a.bank + (int64_t)e * a.N * a.rb;
   const int gpr = (MLX || MX) ? K / a.group : 0;
   const int64_t cstride = (int64_t)nw * RP;
@@ -334,7 +337,7 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
   };
   // rows of output column col: col (and width + col, the up row, for SwiGLU)
   auto load = [&](int64_t col, Buf& bf) {
-    const int64_t cc = col < width ? col : 0;
+    const int64_t cc = col < ce ? col : cb;
 #pragma unroll
     for (int r = 0; r < R2; r++) {
       const int64_t n = r == 0 ? cc : width + cc;
@@ -352,9 +355,9 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
   };
 
   const UnpackK kc = unpack_consts();
-  const int64_t base = (int64_t)wq * RP;  // the wave's first column (wave-uniform)
+  const int64_t base = cb + (int64_t)wq * RP;  // the wave's first column (wave-uniform)
   // column steps of this wave: base + s * cstride, s < cnt
-  const int64_t cnt = base < width ? (width - base + cstride - 1) / cstride : 0;
+  const int64_t cnt = base < ce ? (ce - base + cstride - 1) / cstride : 0;
   auto step_col = [&](int64_t st) { return base + (st < cnt ? st : (cnt > 0 ? cnt - 1 : 0)) * cstride + g; };
   for (int c0 = beg; c0 < end; c0 += MT) {
     // activations of the MT entries (raw bf16), requested before the ring so
@@ -452,7 +455,9 @@ RLXQ_DEV void moe_xr_wave(const rlxq_moe_gemv_args& a, int e, const int32_t* per
 #pragma unroll
         for (int m = 0; m < MT; m++) v[r][m] = lane_group_sum<L>(acc[r][m]);
       const int64_t mycol = col + g;
-      if (li == 0 && mycol < width) {
+      if (vout) {
+        if (li == 0 && mycol < ce) vout[mycol - cb] = v[0][0];
+      } else if (li == 0 && mycol < ce) {
 #pragma unroll
         for (int m = 0; m < MT; m++) {
           if (ent[m] >= 0) {
@@ -693,6 +698,43 @@ RLXQ_DEV void moe_xr_body(const rlxq_moe_gemv_args& a) {
   else table_dispatch(a, work);
 }
 
+// Down projection and combine of decode-sized MoE calls in one launch,
+// token-major: workgroup = (token row r, tile of tile_rows output columns),
+// wave j = top-k slot j (64 * top_k threads, top_k <= 8).  Wave j computes
+// entry r * top_k + j's values for the tile's columns exactly as the
+// expert-major register kernel computes them for one entry (the same
+// moe_xr_wave, one entry per pass) into LDS, then the workgroup sums the
+// slots in slot order, y[r, c] = fma(probs[r, j], v[j][c], ...) for j = 0,
+// 1, ... as rlxq_moe_combine_k does, so the output matches the two-launch
+// path bit for bit.  An invalid expert id contributes zero (as its zeroed
+// row does there).  No per-entry rows in memory, no counters, no atomics.
+template <int SCH, int L, int NU, int D>
+RLXQ_DEV void moe_xc_body(const rlxq_moe_gemv_args& a) {
+  extern __shared__ float vals[];   // [top_k][tile_rows]
+  __shared__ int32_t ents[8];
+  const int tk = a.top_k, TC = a.tile_rows;
+  const int64_t r = blockIdx.x / a.tiles_n;
+  const int tn = blockIdx.x % a.tiles_n;
+  const int64_t cb = (int64_t)tn * TC, ce = cb + TC < a.N ? cb + TC : a.N;
+  const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (threadIdx.x < tk) ents[threadIdx.x] = (int32_t)(r * tk + threadIdx.x);
+  __syncthreads();
+  float* vj = vals + j * TC;
+  const int e = entry_expert(a, (int)(r * tk + j));
+  if (e >= 0) {
+    moe_xr_wave<SCH, L, NU, 1, D, false>(a, e, ents, j, j + 1, 0, 1, cb, ce, vj);
+  } else {
+    for (int64_t c = threadIdx.x & 63; c < ce - cb; c += 64) vj[c] = 0.f;
+  }
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < ce - cb; c += blockDim.x) {
+    float acc = 0.f;
+    for (int q = 0; q < tk; q++) acc = fmaf(a.probs[r * tk + q], vals[q * TC + c], acc);
+    if (a.out_bf16) reinterpret_cast<uint16_t*>(a.out)[r * a.N + cb + c] = (uint16_t)f32_to_bf16_bits(acc);
+    else reinterpret_cast<float*>(a.out)[r * a.N + cb + c] = acc;
+  }
+}
+
 }  // namespace rlxq
 
 #define RLXQ_MOE_INST(NAME, SCH, XBF, L, MT, SW)                                        \
@@ -751,6 +793,20 @@ RLXQ_MOE_SCHEME(q2_k, SCH_Q2_K)
   RLXQ_MOEXR_INST(rlxq_moexr_##SNAME##_L##L##_U##NU##_M##MT##_sw, SCH, L, NU, MT, D, true, false)    \
   RLXQ_MOEXR_INST(rlxq_moexrf_##SNAME##_L##L##_U##NU##_M##MT, SCH, L, NU, MT, D, false, true)        \
   RLXQ_MOEXR_INST(rlxq_moexrf_##SNAME##_L##L##_U##NU##_M##MT##_sw, SCH, L, NU, MT, D, true, true)
+// Token-major down + combine: rlxq_moexc_<scheme>_L<L>_U<NU> (the lane
+// groups and ring depths of the one-entry register kernels)
+#define RLXQ_MOEXC_INST(SNAME, SCH, L, NU, D)                                                  \
+  extern "C" __global__ __launch_bounds__(512) void rlxq_moexc_##SNAME##_L##L##_U##NU(rlxq_moe_gemv_args a) { \
+    rlxq::moe_xc_body<SCH, L, NU, D>(a);                                                         \
+  }
+#define RLXQ_MOEXC_SCHEME(SNAME, SCH)   \
+  RLXQ_MOEXC_INST(SNAME, SCH, 64, 1, 4) \
+  RLXQ_MOEXC_INST(SNAME, SCH, 64, 2, 2) \
+  RLXQ_MOEXC_INST(SNAME, SCH, 64, 4, 1) \
+  RLXQ_MOEXC_INST(SNAME, SCH, 8, 1, 4)  \
+  RLXQ_MOEXC_INST(SNAME, SCH, 8, 2, 2)  \
+  RLXQ_MOEXC_INST(SNAME, SCH, 8, 3, 2)  \
+  RLXQ_MOEXC_INST(SNAME, SCH, 8, 4, 1)
 #define RLXQ_MOEXR_SCHEME(SNAME, SCH)        \
   RLXQ_MOEXR_LU(SNAME, SCH, 64, 1, 1, 4)     \
   RLXQ_MOEXR_LU(SNAME, SCH, 64, 1, 2, 2)     \
@@ -776,6 +832,23 @@ RLXQ_MOEXR_SCHEME(mlx4, SCH_MLX4)
 #endif
 #if RLXQ_PART_IS(3)
 RLXQ_MOEXR_SCHEME(mxfp4, SCH_MXFP4)
+#endif
+#if RLXQ_PART_IS(4)
+RLXQ_MOEXC_SCHEME(q4_1, SCH_Q4_1)
+RLXQ_MOEXC_SCHEME(mlx4, SCH_MLX4)
+RLXQ_MOEXC_SCHEME(mxfp4, SCH_MXFP4)
+RLXQ_MOEXC_INST(q4_1, SCH_Q4_1, 32, 2, 2)
+RLXQ_MOEXC_INST(mlx4, SCH_MLX4, 32, 2, 2)
+RLXQ_MOEXC_INST(mxfp4, SCH_MXFP4, 32, 2, 2)
+RLXQ_MOEXC_INST(q4_k, SCH_Q4_K, 32, 1, 4)
+RLXQ_MOEXC_INST(q4_k, SCH_Q4_K, 64, 1, 4)
+RLXQ_MOEXC_INST(q4_k, SCH_Q4_K, 64, 2, 2)
+RLXQ_MOEXC_INST(q4_k, SCH_Q4_K, 8, 1, 4)
+RLXQ_MOEXC_INST(q4_k, SCH_Q4_K, 8, 2, 2)
+RLXQ_MOEXC_INST(q4_0, SCH_Q4_0, 64, 1, 4)
+RLXQ_MOEXC_INST(q4_0, SCH_Q4_0, 64, 2, 2)
+RLXQ_MOEXC_INST(q4_0, SCH_Q4_0, 8, 1, 4)
+RLXQ_MOEXC_INST(q4_0, SCH_Q4_0, 8, 2, 2)
 #endif
 #if RLXQ_PART_IS(2)
 // Q4_1 at 33..64 units (K = 2048): 32-lane groups of two units

@@ -661,3 +661,53 @@ def test_combine_in_down_launch_matches_combine_kernel(ctx, orc, monkeypatch, to
         dn = orc.grouped_matmul_f64(3, av, down, np.where(valid, ids, 0).ravel().astype(np.float32), H, E)
         want = np.einsum("tk,tkh->th", np.where(valid, probs, 0.0).astype(np.float64), dn.reshape(tokens, TOPK, H))
         assert rel_err(y.float().cpu().numpy(), want) <= (1e-2 if ydt == "bf16" else TOL), call
+
+
+# (scheme, K, tokens, top_k): config 5's down (Q4_1 K=768: 8-lane groups of
+# three units; Q4_K: 8-lane groups of two), K=2048 (32-lane groups), Q4_0,
+# one token, top-1 and top-2, 64 tokens
+XC_CASES = [(3, 768, 16, 8), (7, 768, 16, 8), (3, 2048, 16, 8), (2, 512, 7, 4), (3, 768, 1, 8), (3, 256, 5, 1),
+            (7, 1024, 3, 2), (3, 768, 64, 8)]
+
+
+@pytest.mark.parametrize("ydt", ["f32", "bf16"])
+@pytest.mark.parametrize("case", XC_CASES, ids=lambda c: "_".join(map(str, c)))
+def test_token_major_down_matches_two_launches(ctx, orc, monkeypatch, case, ydt):
+    """COMBINE at decode sizes runs down and combine in one token-major launch
+    (rlxq_moexc_*: a workgroup per token and column tile, a wave per slot,
+    the slots summed in slot order in the workgroup).  It must equal the
+    expert-major kernel plus rlxq_moe_combine_k bit for bit, with invalid
+    expert ids contributing nothing, and match the float64 oracle."""
+    import torch
+    import rlxq
+
+    scheme, K, tokens, topk = case
+    H, E = 1000 if scheme == 2 else 2048, 40
+    announce(f"moe token-major down {case} y={ydt}")
+    rng = np.random.default_rng(K + tokens + topk)
+    down = orc.synth(scheme, rng, E * H, K)
+    dt = _t(down)
+    ydtype = torch.bfloat16 if ydt == "bf16" else torch.float32
+    act = rng.standard_normal((tokens * topk, K)).astype(np.float32)
+    at = _t(act).to(torch.bfloat16)
+    ids = np.stack([rng.choice(E, topk, replace=False) for _ in range(tokens)]).astype(np.int32)
+    if tokens > 2:
+        ids[1, topk - 1] = -1
+        ids[tokens - 1, 0] = E + 5
+    probs = rng.uniform(0.01, 0.3, (tokens, topk)).astype(np.float32)
+    it, pt = _t(ids), _t(probs)
+    monkeypatch.setenv("RLXQ_MOE_KERNEL", "xr")   # (64 tokens of 40 experts would take the grouped MFMA path)
+    monkeypatch.delenv("RLXQ_MOE_COMBINE", raising=False)
+    y = ctx.moe_grouped(at, dt, it, pt, scheme, rlxq.MOE_COMBINE, H, E, y_dtype=ydtype)
+    torch.cuda.synchronize()
+    assert ctx.last_kernel.startswith("rlxq_moexc_"), ctx.last_kernel
+    monkeypatch.setenv("RLXQ_MOE_COMBINE", "launch")
+    y2 = ctx.moe_grouped(at, dt, it, pt, scheme, rlxq.MOE_COMBINE, H, E, y_dtype=ydtype)
+    torch.cuda.synchronize()
+    assert ctx.last_kernel == "rlxq_moe_combine_k", ctx.last_kernel
+    assert torch.equal(y, y2)
+    valid = (ids >= 0) & (ids < E)
+    av = at.float().cpu().numpy()
+    dn = orc.grouped_matmul_f64(scheme, av, down, np.where(valid, ids, 0).ravel().astype(np.float32), H, E)
+    want = np.einsum("tk,tkh->th", np.where(valid, probs, 0.0).astype(np.float64), dn.reshape(tokens, topk, H))
+    assert rel_err(y.float().cpu().numpy(), want) <= (1e-2 if ydt == "bf16" else TOL)
