@@ -581,7 +581,8 @@ def moe_section(ctx, gen, sptr, stream, scheme: str = "q4_1", tokens: int = 16) 
            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
            "bytes_model": f"unique experts x {int(per_expert):,} B + activations", "kernel_down": ctx.last_kernel}
     if T <= 64:
-        out["launches_per_layer"] = "route, gate|up + SwiGLU (routing in the workgroups), down + combine"
+        out["launches_per_layer"] = ("route, gate|up + SwiGLU (routing in the workgroups), down and combine in one "
+                                     "token-major launch")
     else:
         out["launches_per_layer"] = ("route, then per grouped call: routing table, gathered-row layout, f16 rows, "
                                      "grouped MFMA kernel (+ combine kernel for down)")
