@@ -332,23 +332,32 @@ def prefill_headline(detail: dict) -> dict:
 
 
 def batched_section(ctx, gen, sptr, stream) -> dict:
-    """Config 3: batched decode, Q4_1 and Q8_0 (and Q4_K, Q6_K beside them), M
-    in {1, 4, 16, 64}, bf16 x, f32 y."""
+    """Config 3: batched decode, Q4_1 and Q8_0 (and Q4_K, Q6_K and MLX affine
+    4-bit, group 64 with bf16 slabs, beside them), M in {1, 4, 16, 64}, bf16
+    x, f32 y."""
     import torch
     import rlxq
 
     res = {}
+    mlx_synth = lambda n, k, g: synth_mlx_gpu(n, k, 4, 64, g)
     for sname, scheme, bpw, synth in (("q4_1", rlxq.GGUF_Q4_1, Q4_1_BPW, synth_q4_1_gpu),
                                       ("q8_0", rlxq.GGUF_Q8_0, Q8_0_BPW, synth_q8_0_gpu),
                                       ("q4_k", rlxq.GGUF_Q4_K, 144 / 256, synth_q4_k_gpu),
-                                      ("q6_k", rlxq.GGUF_Q6_K, 210 / 256, synth_q6_k_gpu)):
+                                      ("q6_k", rlxq.GGUF_Q6_K, 210 / 256, synth_q6_k_gpu),
+                                      ("mlx4", rlxq.MLX_AFFINE4, 0.5 + 4 / 64, mlx_synth)):
         for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):
             wb = n * k * bpw
             ws = [synth(n, k, gen) for _ in range(_copies(wb))]
             for m in (1, 4, 16, 64):
                 x = torch.randn((m, k), generator=gen, device="cuda").to(torch.bfloat16)
                 y = torch.empty((m, n), device="cuda")
-                run = lambda i: ctx.dequant_matmul(x, ws[i % len(ws)], scheme, n, y=y, stream=sptr)
+
+                def run(i, x=x, y=y, ws=ws, scheme=scheme, n=n):
+                    w = ws[i % len(ws)]
+                    if isinstance(w, tuple):
+                        return ctx.dequant_matmul(x, w[0], scheme, n, group=64, scales=w[1], biases=w[2], y=y,
+                                                  stream=sptr)
+                    return ctx.dequant_matmul(x, w, scheme, n, y=y, stream=sptr)
                 for i in range(len(ws)):
                     run(i)
                 torch.cuda.synchronize()

@@ -263,7 +263,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     xa.K = k;
     xa.Mp = sk_mp;
     xa.x_bf16 = 1;
-    xa.nibble_order = sk_nibble(scheme);
+    xa.nibble_order = sk_order(scheme);
     xa.frag_major = 1;
     xa.rdiv = x_div;
     xa.rmap = pa.emap;

@@ -211,7 +211,8 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
   char* part = nullptr;
   if (f16) {
     rlxq_x16_args xa;
-    if ((rc = prep_x16(ctx, x, RLXQ_BF16, m, k, scheme != RLXQ_GGUF_Q8_0, part_bytes, xa, &part, stream))) return rc;
+    if ((rc = prep_x16(ctx, x, RLXQ_BF16, m, k, scheme != RLXQ_GGUF_Q8_0 ? 1 : 0, part_bytes, xa, &part, stream)))
+      return rc;
     a.x = xa.x16;
     a.inv_s = xa.inv_s;
   } else if (part_bytes) {
@@ -297,17 +298,25 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     if (use_gemm) return gemm_dispatch(ctx, scheme, group, x, w, scales, biases, sb_dtype, rb, m, k, n, y, y_dtype, stream);
   }
   // Batched decode: from 5 rows of bf16 activations (exact in f16 once scaled),
-  // GGUF weights stream once for all rows through the f16-MFMA kernel; f32
-  // activations would lose bits in f16 and stay on the GEMV.
+  // GGUF and MLX affine 4-bit weights stream once for all rows through the
+  // f16-MFMA kernel; f32 activations would lose bits in f16 and stay on the
+  // GEMV.
   // RLXQ_DECODE=gemv|skinny forces one where both apply.
   {
-    const bool sk_ok = skinny_applies(scheme, m, k) && xbf;
+    const bool sk_ok = skinny_applies(scheme, group, m, k) && xbf;
     bool use_sk = sk_ok && m >= 5;
     if (const char* e = std::getenv("RLXQ_DECODE")) {
       if (!std::strcmp(e, "gemv")) use_sk = false;
       if (!std::strcmp(e, "skinny")) use_sk = sk_ok;
     }
-    if (use_sk) return skinny_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream);
+    if (use_sk) {
+      SkinnySb sb;
+      sb.scales = scales;
+      sb.biases = biases;
+      sb.group = is_mlx(scheme) ? group : 32;
+      sb.sb_bf16 = sb_code(sb_dtype);
+      return skinny_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, sb);
+    }
   }
 
   rlxq_gemv_args a;

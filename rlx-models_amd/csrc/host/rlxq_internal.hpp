@@ -104,20 +104,28 @@ const char* scheme_name(int scheme);
 int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dtype, const void* w,
                   const void* scales, const void* biases, int sb_dtype, int64_t m, int64_t k,
                   int64_t n, void* y, int y_dtype, void* stream);
-bool skinny_applies(int scheme, int64_t m, int64_t k);
-// Whether the batched-decode activations take the nibble-unpacking order
-// (4-bit code formats) or stay in natural order (Q8_0, Q6_K).
-bool sk_nibble(int scheme);
+bool skinny_applies(int scheme, int group, int64_t m, int64_t k);
+// Order of the batched-decode activations within a 32-block: 1 the GGUF
+// nibble-unpacking order, 2 MLX's, 0 natural (Q8_0, Q6_K).
+int sk_order(int scheme);
+// MLX per-group scales and biases for the batched-decode kernels (unused by
+// the GGUF formats).
+struct SkinnySb {
+  const void* scales = nullptr;
+  const void* biases = nullptr;
+  int64_t group = 32;
+  int32_t sb_bf16 = 0;
+};
 // Adds the [splits, M, N] f32 partial sums in a.part into a.y (y_ld, y_bf16)
 // in slice order.
 int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream);
 // x [m, k] -> prepared f16 activations (x16) and row factors (inv_s) at the
 // start of the workspace; `extra` further bytes follow at *rest.  The
 // fragment-major layout holds mp >= m rows (the rows past m zero).
-int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bool nibble, size_t extra,
+int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, int order, size_t extra,
              rlxq_x16_args& xa, char** rest, void* stream, bool frag_major = false, int64_t mp = 0);
 int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
-                    int64_t k, int64_t n, void* y, int y_dtype, void* stream);
+                    int64_t k, int64_t n, void* y, int y_dtype, void* stream, const SkinnySb& sb = SkinnySb());
 int i8b_dispatch(rlxq_ctx* ctx, int group, const void* x, int x_dtype, const void* w, const void* scales,
                  const void* zp, int sb_dtype, int64_t m, int64_t k, int64_t n, void* y, int y_dtype,
                  void* stream);

@@ -29,7 +29,7 @@ int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream) {
   return launch(ctx, fn, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, rargs, "rlxq_skinny_reduce");
 }
 
-int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bool nibble, size_t extra,
+int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, int order, size_t extra,
              rlxq_x16_args& xa, char** rest, void* stream, bool frag_major, int64_t mp) {
   if (!frag_major || mp < m) mp = m;
   const size_t x16_bytes = round256((size_t)(mp * k) * 2), s_bytes = round256((size_t)m * 4);
@@ -45,7 +45,7 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, bo
   xa.K = k;
   xa.Mp = mp;
   xa.x_bf16 = x_dtype == RLXQ_BF16;
-  xa.nibble_order = nibble;
+  xa.nibble_order = order;
   xa.frag_major = frag_major ? 1 : 0;
   *rest = wsb + x16_bytes + s_bytes;
   hipFunction_t fn;
@@ -60,7 +60,8 @@ namespace {
 // 16*MT-row chunk); K splits (powers of two, whole 128-element chunks) until
 // the grid holds about two workgroups per CU (RLXQ_SKINNY_WGS scales that).
 int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
-                       int64_t k, int64_t n, void* y, int y_dtype, void* stream, int MT, int NT, int D) {
+                       int64_t k, int64_t n, void* y, int y_dtype, void* stream, int MT, int NT, int D,
+                       const SkinnySb& sb) {
   const int64_t tiles_n = (n + 16 * NT - 1) / (16 * NT), mch = (m + 16 * MT - 1) / (16 * MT);
   const int64_t chunks = k / 128;
   const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
@@ -76,7 +77,7 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   char* rest = nullptr;
   int rc;
   const int64_t mp = mch * 16 * MT;
-  if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_nibble(scheme), part_bytes, xa, &rest, stream, true, mp)))
+  if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp)))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
@@ -95,6 +96,10 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   a.splits = (int32_t)splits;
   a.tiles_n = (int32_t)tiles_n;
   a.y_bf16 = y_dtype == RLXQ_BF16;
+  a.scales = sb.scales;
+  a.biases = sb.biases;
+  a.group = sb.group;
+  a.sb_bf16 = sb.sb_bf16;
   char name[64];
   std::snprintf(name, sizeof name, "rlxq_skinnyxr_%s_mt%d_nt%d_d%d", scheme_name(scheme), MT, NT, D);
   hipFunction_t fn;
@@ -112,7 +117,8 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
 // chunk), the activations of a step shared by the four waves through LDS; K
 // splits as for the register-streamed kernel.
 int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
-                       int64_t k, int64_t n, void* y, int y_dtype, void* stream, int MT, int NT, int D) {
+                       int64_t k, int64_t n, void* y, int y_dtype, void* stream, int MT, int NT, int D,
+                       const SkinnySb& sb) {
   const int64_t tiles_n = (n + 64 * NT - 1) / (64 * NT), mch = (m + 16 * MT - 1) / (16 * MT);
   const int64_t chunks = k / 128;
   const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
@@ -128,7 +134,7 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   char* rest = nullptr;
   int rc;
   const int64_t mp = mch * 16 * MT;
-  if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_nibble(scheme), part_bytes, xa, &rest, stream, true, mp)))
+  if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp)))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
@@ -147,6 +153,10 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   a.splits = (int32_t)splits;
   a.tiles_n = (int32_t)tiles_n;
   a.y_bf16 = y_dtype == RLXQ_BF16;
+  a.scales = sb.scales;
+  a.biases = sb.biases;
+  a.group = sb.group;
+  a.sb_bf16 = sb.sb_bf16;
   char name[64];
   std::snprintf(name, sizeof name, "rlxq_skinnyns_%s_mt%d_nt%d_d%d", scheme_name(scheme), MT, NT, D);
   hipFunction_t fn;
@@ -162,11 +172,15 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
 }
 }  // namespace
 
-bool sk_nibble(int scheme) { return scheme != RLXQ_GGUF_Q8_0 && scheme != RLXQ_GGUF_Q6_K; }
+int sk_order(int scheme) {
+  if (scheme == RLXQ_MLX_AFFINE4) return 2;
+  return scheme != RLXQ_GGUF_Q8_0 && scheme != RLXQ_GGUF_Q6_K ? 1 : 0;
+}
 
-bool skinny_applies(int scheme, int64_t m, int64_t k) {
+bool skinny_applies(int scheme, int group, int64_t m, int64_t k) {
   return (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q4_1 ||
-          ((scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K) && k % 256 == 0)) &&
+          ((scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K) && k % 256 == 0) ||
+          (scheme == RLXQ_MLX_AFFINE4 && group >= 32 && group % 32 == 0 && k % group == 0)) &&
          m >= 1 && m <= 256 && k % 128 == 0;
 }
 
@@ -175,7 +189,8 @@ bool skinny_applies(int scheme, int64_t m, int64_t k) {
 // at most 32 and at most one split per K step; their partial sums (f32,
 // [splits, M, N]) are added in split order.
 int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
-                    int64_t k, int64_t n, void* y, int y_dtype, void* stream) {
+                    int64_t k, int64_t n, void* y, int y_dtype, void* stream, const SkinnySb& sb) {
+  const bool mlx = scheme == RLXQ_MLX_AFFINE4;
   // The register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR="MT,NT,D"
   // picks a compiled one (every combination for Q4_1, the defaults for Q4_0
   // and Q8_0), "0" the LDS-staged kernels below.
@@ -186,14 +201,14 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   {
     const bool q6k = scheme == RLXQ_GGUF_Q6_K;
     int nmt = m <= 32 ? 2 : 4, nnt = 1, nd = q6k && m > 32 ? 2 : 3;
-    bool ns = (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_K || q6k) && m > 16;
+    bool ns = (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_K || q6k || mlx) && m > 16;
     if (const char* e = std::getenv("RLXQ_SKINNY_NS")) {
       int a1, a2, a3;
       if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) nmt = a1, nnt = a2, nd = a3, ns = true;
       else if (e[0] == '0') ns = false;
     }
     if (std::getenv("RLXQ_SKINNY_XR") && !std::getenv("RLXQ_SKINNY_NS")) ns = false;
-    if (ns) return skinny_ns_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, nmt, nnt, nd);
+    if (ns) return skinny_ns_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, nmt, nnt, nd, sb);
   }
   {
     int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = 2, xd = m <= 16 ? 4 : (m <= 32 ? 3 : 2);
@@ -203,10 +218,10 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
     if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
       int a1, a2, a3;
       if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) xmt = a1, xnt = a2, xd = a3;
-      else if (e[0] == '0')   // (Q4_K and Q6_K have no LDS-staged kernel)
-        xr = scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K;
+      else if (e[0] == '0')   // (Q4_K, Q6_K and MLX4 have no LDS-staged kernel)
+        xr = scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K || mlx;
     }
-    if (xr) return skinny_xr_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, xmt, xnt, xd);
+    if (xr) return skinny_xr_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, xmt, xnt, xd, sb);
   }
   const int MT = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
   // blocks per thread per step (K per step = 64 * BPT); 2 measured fastest,
@@ -248,7 +263,7 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   xa.M = m;
   xa.K = k;
   xa.x_bf16 = x_dtype == RLXQ_BF16;
-  xa.nibble_order = sk_nibble(scheme);
+  xa.nibble_order = sk_order(scheme);
   hipFunction_t fn;
   if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
   void* xargs[] = {&xa};

@@ -2,9 +2,11 @@
 // the batched-decode (skinny) and f16 prefill GEMM kernels.
 //
 // A lane's 8 consecutive operand positions 8g .. 8g + 7 of a 32-element
-// block hold, for the nibble formats, elements 4g .. 4g + 3 and
-// 16 + 4g .. 16 + 4g + 3 (the order in which code dword g unpacks); the
-// activations are stored in the same order (perm_k).
+// block hold, for the GGUF nibble formats, elements 4g .. 4g + 3 and
+// 16 + 4g .. 16 + 4g + 3, for MLX's 4-bit codes (eight per little-endian
+// word, low nibble first) elements 8g, 8g + 2, 8g + 4, 8g + 6, 8g + 1, ..,
+// 8g + 7 (the orders in which code dword g unpacks); the activations are
+// stored in the same order (perm_k).
 #ifndef RLXQ_F16DQ_HIP_H
 #define RLXQ_F16DQ_HIP_H
 #include "common.hip.h"
@@ -17,18 +19,23 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-// Element of a 32-block held at position p (see above).
-RLXQ_DEV int perm_k(int p, bool nibble) {
-  if (!nibble) return p;
+// Element of a 32-block held at position p (see above); order 0 natural,
+// 1 GGUF nibbles, 2 MLX nibbles.
+RLXQ_DEV int perm_k(int p, int order) {
+  if (order == 0) return p;
   const int g = p >> 3, e = p & 7;
+  if (order == 2) return 8 * g + (e < 4 ? 2 * e : 2 * (e - 4) + 1);
   return e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4);
 }
 
 
-// Normalised block: scale dword (Q4_1, Q4_K: d | m << 16, else d) + code
-// dwords.  A Q4_K sub-block normalises to the Q4_1 form: d = d * sc and
+// Normalised block: scale dword (Q4_1, Q4_K, MLX4: d | m << 16, else d) +
+// code dwords.  A Q4_K sub-block normalises to the Q4_1 form: d = d * sc and
 // m = -dmin * mn rounded to f16, and code dword g holding elements 4g..4g+3
 // (low nibbles) and 16 + 4g.. (high nibbles) of the sub-block.
+// An MLX4 block: the group's f32 scale and bias rounded to f16 (the f16
+// range covers the scales of real weight slabs; scales below 2^-14 lose bits
+// as f16 subnormals) and its four code words as they are.
 // A Q6_K block normalises to the int8 form of Q8_0 with one f16 scale per
 // 16 weights: scale dword d0 | d1 << 16 (d * sc of the two halves, rounded
 // to f16) and code bytes code + 96, so that code - 32 = byte - 128 as for
@@ -67,7 +74,7 @@ RLXQ_DEV f16x8_t dequant_lane(const uint32_t* bp, int g) {
   } else {
     const uint32_t qs = bp[1 + g];
     const uint32_t lo = qs & 0x0F0F0F0Fu, hi = (qs >> 4) & 0x0F0F0F0Fu;
-    if constexpr (SCH == SCH_Q4_1 || SCH == SCH_Q4_K) {
+    if constexpr (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SCH == SCH_MLX4) {
       const f16x2_t m2 = as_h2(perm_b32(dm, dm, 0x03020302u));
       const f16x2_t off = {(_Float16)-1024.f, (_Float16)-1024.f};
       w[0] = __builtin_elementwise_fma(magic_lo(lo) + off, d2, m2);
@@ -110,6 +117,9 @@ RLXQ_DEV void normalise(const RawBlk<SCH>& r, uint32_t* o) {
     const uint32_t sh = 4 * (r.sub & 1u);
 #pragma unroll
     for (int g = 0; g < 4; g++) o[1 + g] = ((qs[g] >> sh) & 0x0F0F0F0Fu) | (((qs[4 + g] >> sh) & 0x0F0F0F0Fu) << 4);
+  } else if constexpr (SCH == SCH_MLX4) {
+    o[0] = f32_to_f16_bits(r.s) | (f32_to_f16_bits(r.b) << 16);
+    o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;
   } else if constexpr (SCH == SCH_Q4_1) {
     o[0] = r.h;
     o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;

@@ -1,6 +1,6 @@
 // Batched-decode dequant-GEMM for small M (the multi-row decode path):
 // y[m, n] = sum_k x[m, k] * dequant(W)[n, k] for up to 64 activation rows and
-// GGUF Q8_0 / Q4_0 / Q4_1 / Q4_K weights, streaming every weight once for all
+// GGUF Q8_0 / Q4_0 / Q4_1 / Q4_K / Q6_K and MLX affine 4-bit weights, streaming every weight once for all
 // rows.
 // Replaces the backend kernel of Op::DequantMatMul at decode batch sizes
 // (crates/rlx-models-core/src/standard_decoder.rs:727-738, M rows per call).
@@ -8,8 +8,9 @@
 //  * rlxq_x16_prep: each activation row to f16, scaled by a power of two so
 //    its largest element lies in [2^13, 2^14) (exact; undone in the
 //    epilogue), and permuted within each 32-element block to the order in
-//    which a lane unpacks the codes: for the nibble formats position
-//    8g + e holds element 4g + e (e < 4) or 16 + 4g + e - 4.
+//    which a lane unpacks the codes: for the GGUF nibble formats position
+//    8g + e holds element 4g + e (e < 4) or 16 + 4g + e - 4, for MLX's
+//    element 8g + 2e (e < 4) or 8g + 2(e - 4) + 1.
 //  * rlxq_skinny_*: a workgroup takes 128 weight rows, a K split and all M
 //    rows.  Per step the raw blocks are staged in LDS (a run of blocks per
 //    thread, normalised to a dword scale word plus the code dwords) and the
@@ -383,7 +384,8 @@ RLXQ_DEV void skinny_dma_body(const rlxq_skinny_args& a) {
 template <int SCH, int MT, int NT, int D>
 RLXQ_DEV bool skinny_xr_core(const uint16_t* x16, int64_t Mp, int64_t m0, const uint8_t* w, int64_t rb, int64_t K,
                              int64_t kb, int64_t ke, const int64_t (&wrow)[NT], const bool (&wok)[NT],
-                             f32x4_t (&acc)[MT][NT]) {
+                             f32x4_t (&acc)[MT][NT], const void* scales = nullptr,
+                             const void* biases = nullptr, int64_t group = 32, int32_t sb_bf16 = 0) {
   constexpr int BDW = sk_bdw<SCH>();
   // wave index through readfirstlane: the chunk loop is wave-uniform
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -396,10 +398,10 @@ RLXQ_DEV bool skinny_xr_core(const uint16_t* x16, int64_t Mp, int64_t m0, const 
   ga.w = w;
   ga.rb = rb;
   ga.K = K;
-  ga.group = 32;
-  ga.sb_bf16 = 0;
-  ga.scales = nullptr;
-  ga.biases = nullptr;
+  ga.group = group;
+  ga.sb_bf16 = sb_bf16;
+  ga.scales = scales;
+  ga.biases = biases;
   // activations in the fragment-major layout: piece i of chunk c for row m,
   // lane group g at ((4 c + i) Mp + m) 4 + g (16-byte pieces), so the A
   // fragment of 16 rows is one contiguous 1 KB read; the Mp rows cover every
@@ -532,7 +534,9 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
     wrow[t] = wok[t] ? n : a.N - 1;
   }
   f32x4_t acc[MT][NT];
-  if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.Mp, m0, a.w, a.rb, a.K, kb, ke, wrow, wok, acc)) return;
+  if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.Mp, m0, a.w, a.rb, a.K, kb, ke, wrow, wok, acc, a.scales, a.biases,
+                                      a.group, a.sb_bf16))
+    return;
   // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
 #pragma unroll
   for (int mt = 0; mt < MT; mt++)
@@ -645,10 +649,10 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
   ga.w = a.w;
   ga.rb = a.rb;
   ga.K = a.K;
-  ga.group = 32;
-  ga.sb_bf16 = 0;
-  ga.scales = nullptr;
-  ga.biases = nullptr;
+  ga.group = a.group;
+  ga.sb_bf16 = a.sb_bf16;
+  ga.scales = a.scales;
+  ga.biases = a.biases;
   int64_t wrow[NT];
   bool wok[NT];
 #pragma unroll
@@ -826,7 +830,7 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
     s = ldexpf(1.f, sh);
     inv = ldexpf(1.f, -sh);
   }
-  const bool nib = a.nibble_order != 0;
+  const int nib = a.nibble_order;
   auto store_blk32 = [&](int64_t b, const float* w) {
     uint32_t o[16];
 #pragma unroll
@@ -954,6 +958,9 @@ RLXQ_SKINNYXR_INST(q4_k, SCH_Q4_K, 1, 2, 3)
 RLXQ_SKINNYXR_INST(q4_k, SCH_Q4_K, 2, 2, 2)
 RLXQ_SKINNYXR_INST(q4_k, SCH_Q4_K, 4, 2, 2)
 // Q6_K (22-dword raw blocks)
+RLXQ_SKINNYXR_INST(mlx4, SCH_MLX4, 1, 2, 4)
+RLXQ_SKINNYXR_INST(mlx4, SCH_MLX4, 2, 2, 3)
+RLXQ_SKINNYXR_INST(mlx4, SCH_MLX4, 4, 2, 2)
 RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 1, 2, 2)
 RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 2, 2, 2)
 RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 4, 2, 1)
@@ -974,6 +981,9 @@ RLXQ_SKINNYNS_INST(q4_0, SCH_Q4_0, 4, 1, 3)
 RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 1, 1, 3)
 RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 2, 1, 3)
 RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 4, 1, 3)
+RLXQ_SKINNYNS_INST(mlx4, SCH_MLX4, 1, 1, 3)
+RLXQ_SKINNYNS_INST(mlx4, SCH_MLX4, 2, 1, 3)
+RLXQ_SKINNYNS_INST(mlx4, SCH_MLX4, 4, 1, 3)
 RLXQ_SKINNYNS_INST(q6_k, SCH_Q6_K, 1, 1, 3)
 RLXQ_SKINNYNS_INST(q6_k, SCH_Q6_K, 2, 1, 3)
 RLXQ_SKINNYNS_INST(q6_k, SCH_Q6_K, 4, 1, 2)

@@ -16,7 +16,8 @@ typedef struct rlxq_x16_args {
   uint16_t* x16;
   float* inv_s;
   int64_t M, K, Mp;
-  int32_t x_bf16, nibble_order;
+  int32_t x_bf16;
+  int32_t nibble_order;   /* 0 natural, 1 GGUF nibbles, 2 MLX nibbles    */
   int32_t frag_major, rdiv;
   /* gathered rows (fragment-major only): x16 row r is x row rmap[r] / rdiv,
    * a zero row where rmap[r] < 0; NULL: x16 row r is x row r             */
@@ -26,13 +27,19 @@ typedef struct rlxq_x16_args {
 typedef struct rlxq_skinny_args {
   const uint16_t* x16;    /* prepared activations [M, K] f16              */
   const float* inv_s;     /* [M]                                          */
-  const uint8_t* w;       /* packed GGUF rows, row stride rb bytes        */
+  const uint8_t* w;       /* packed rows, row stride rb bytes             */
   float* part;            /* [splits, M, N] partial sums (splits > 1)     */
   void* y;                /* [M, N] output (splits == 1)                  */
   int64_t M, N, K, rb, y_ld;
   int64_t Mp;             /* rows of the fragment-major x16 (>= M)        */
   int32_t kslice;         /* K per split, a multiple of 128               */
   int32_t splits, tiles_n, y_bf16;
+  /* MLX affine 4-bit: per-group scales and biases [N, K / group] (f32, or
+   * bf16 where sb_bf16); unused by the GGUF formats                     */
+  const void* scales;
+  const void* biases;
+  int64_t group;
+  int32_t sb_bf16;
 } rlxq_skinny_args;
 
 #endif

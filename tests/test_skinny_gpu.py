@@ -260,3 +260,82 @@ def test_skinny_q6_k_every_variant(ctx, orc, monkeypatch, cfg):
         got, want = run_dense(ctx, orc, 8, x, packed, n, xdt="bf16")
         assert ctx.last_kernel == f"rlxq_skinny{kind}_q6_k_mt{mt}_nt{nt}_d{d}", ctx.last_kernel
         assert rel_err(got, want) <= TOL_F32, (cfg, m, k, n)
+
+
+# MLX affine 4-bit (eight codes per little-endian word, per-group f32 or
+# bf16 scale and bias): the Q4_1 form with the group's scale and bias rounded
+# to f16, activations in MLX's unpacking order
+MLX_XR = ["1,2,4", "2,2,3", "4,2,2"]
+MLX_NS = ["1,1,3", "2,1,3", "4,1,3"]
+
+
+def _mlx_case(ctx, orc, rng, m, k, n, group, sb, ydt="f32", x_scale=None):
+    import torch
+    import rlxq
+    from test_gemv_gpu import _t, _x_as
+
+    codes = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint32)
+    sc = rng.uniform(0.01, 0.1, (n, k // group)).astype(np.float32)
+    bi = rng.uniform(-0.5, 0.1, (n, k // group)).astype(np.float32)
+    if sb == "bf16":
+        sc = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(sc))
+        bi = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(bi))
+        st, bt = _t(sc).to(torch.bfloat16), _t(bi).to(torch.bfloat16)
+    else:
+        st, bt = _t(sc), _t(bi)
+    x32 = rng.standard_normal((m, k)).astype(np.float32)
+    if x_scale is not None:
+        x32 *= x_scale[:, None]
+    xt, xv = _x_as(x32, "bf16")
+    y = ctx.dequant_matmul(xt, _t(codes.view(np.uint8)), rlxq.MLX_AFFINE4, n, group=group, scales=st, biases=bt,
+                           y_dtype=torch.bfloat16 if ydt == "bf16" else torch.float32)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy(), orc.mlx_matmul_f64(xv, codes, sc, bi, n, 4, group)
+
+
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("sb", ["f32", "bf16"])
+@pytest.mark.parametrize("mkn", [(5, 256, 7), (16, 4096, 512), (17, 1024, 300), (33, 768, 129),
+                                 (64, 4096, 256), (100, 768, 200), (256, 384, 40)], ids=str)
+def test_skinny_mlx4_default(ctx, orc, mkn, group, sb):
+    m, k, n = mkn
+    if k % group:
+        pytest.skip("K not a multiple of the group")
+    announce(f"skinny mlx4 default {mkn} group={group} sb={sb}")
+    rng = np.random.default_rng(m * 11 + k + n + group)
+    got, want = _mlx_case(ctx, orc, rng, m, k, n, group, sb)
+    prefix = "rlxq_skinnyxr_mlx4_" if m <= 16 else "rlxq_skinnyns_mlx4_"
+    assert ctx.last_kernel.startswith(prefix), ctx.last_kernel
+    assert rel_err(got, want) <= TOL_F32
+    got, want = _mlx_case(ctx, orc, np.random.default_rng(m * 11 + k + n + group), m, k, n, group, sb, ydt="bf16")
+    assert rel_err(got, want) <= TOL_BF16
+
+
+@pytest.mark.parametrize("cfg", [("xr", c) for c in MLX_XR] + [("ns", c) for c in MLX_NS], ids=str)
+def test_skinny_mlx4_every_variant(ctx, orc, monkeypatch, cfg):
+    kind, rest = cfg
+    monkeypatch.setenv("RLXQ_SKINNY_XR" if kind == "xr" else "RLXQ_SKINNY_NS", rest)
+    mt, nt, d = (int(v) for v in rest.split(","))
+    for (m, k, n, group) in [(5, 256, 7, 32), (16 * mt + 3, 2048, 64 * nt * 3 + 5, 64), (9, 12288, 200, 64),
+                             (64, 1536, 96, 128), (3, 768, 64 * nt, 32)]:
+        announce(f"skinny mlx4 {kind} {rest} {(m, k, n, group)}")
+        rng = np.random.default_rng(m + k + n + mt + 2)
+        got, want = _mlx_case(ctx, orc, rng, m, k, n, group, "bf16")
+        assert ctx.last_kernel == f"rlxq_skinny{kind}_mlx4_mt{mt}_nt{nt}_d{d}", ctx.last_kernel
+        assert rel_err(got, want) <= TOL_F32, (cfg, m, k, n)
+
+
+def test_skinny_mlx4_activation_range_and_no_staged_kernel(ctx, orc, monkeypatch):
+    """Rows far outside the f16 range and a zero row; RLXQ_SKINNY_XR=0 keeps
+    MLX4 (no LDS-staged kernel) on the register-streamed kernel."""
+    monkeypatch.setenv("RLXQ_SKINNY_XR", "0")
+    m, k, n = 8, 512, 96
+    xs = np.ones(m, dtype=np.float32)
+    xs[0], xs[1], xs[3] = 1e6, 1e-6, 0.0
+    got, want = _mlx_case(ctx, orc, np.random.default_rng(31), m, k, n, 64, "f32", x_scale=xs)
+    assert ctx.last_kernel.startswith("rlxq_skinnyxr_mlx4_"), ctx.last_kernel
+    for r in range(m):
+        if r == 3:
+            assert np.all(got[r] == 0.0)
+            continue
+        assert rel_err(got[r:r + 1], want[r:r + 1]) <= TOL_F32, r
