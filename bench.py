@@ -332,9 +332,9 @@ def prefill_headline(detail: dict) -> dict:
 
 
 def batched_section(ctx, gen, sptr, stream) -> dict:
-    """Config 3: batched decode, Q4_1 and Q8_0 (and Q4_K, Q6_K and MLX affine
-    4-bit, group 64 with bf16 slabs, beside them), M in {1, 4, 16, 64}, bf16
-    x, f32 y."""
+    """Config 3: batched decode, Q4_1 and Q8_0 (and Q4_K, Q6_K, MLX affine
+    4-bit, group 64 with bf16 slabs, and MXFP4 with E8M0 scale bytes beside
+    them), M in {1, 4, 16, 64}, bf16 x, f32 y."""
     import torch
     import rlxq
 
@@ -344,7 +344,8 @@ def batched_section(ctx, gen, sptr, stream) -> dict:
                                       ("q8_0", rlxq.GGUF_Q8_0, Q8_0_BPW, synth_q8_0_gpu),
                                       ("q4_k", rlxq.GGUF_Q4_K, 144 / 256, synth_q4_k_gpu),
                                       ("q6_k", rlxq.GGUF_Q6_K, 210 / 256, synth_q6_k_gpu),
-                                      ("mlx4", rlxq.MLX_AFFINE4, 0.5 + 4 / 64, mlx_synth)):
+                                      ("mlx4", rlxq.MLX_AFFINE4, 0.5 + 4 / 64, mlx_synth),
+                                      ("mxfp4", rlxq.MLX_MXFP4, 0.5 + 1 / 32, synth_mxfp4_gpu)):
         for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):
             wb = n * k * bpw
             ws = [synth(n, k, gen) for _ in range(_copies(wb))]
@@ -354,9 +355,11 @@ def batched_section(ctx, gen, sptr, stream) -> dict:
 
                 def run(i, x=x, y=y, ws=ws, scheme=scheme, n=n):
                     w = ws[i % len(ws)]
-                    if isinstance(w, tuple):
+                    if isinstance(w, tuple) and len(w) == 3:
                         return ctx.dequant_matmul(x, w[0], scheme, n, group=64, scales=w[1], biases=w[2], y=y,
                                                   stream=sptr)
+                    if isinstance(w, tuple):
+                        return ctx.dequant_matmul(x, w[0], scheme, n, scales=w[1], y=y, stream=sptr)
                     return ctx.dequant_matmul(x, w, scheme, n, y=y, stream=sptr)
                 for i in range(len(ws)):
                     run(i)

@@ -299,11 +299,11 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   }
   // Batched decode: from 5 rows of bf16 activations (exact in f16 once scaled),
   // GGUF and MLX affine 4-bit weights stream once for all rows through the
-  // f16-MFMA kernel; f32 activations would lose bits in f16 and stay on the
-  // GEMV.
+  // f16-MFMA kernel (MXFP4 with E8M0 scales through its bf16-MFMA twin); f32
+  // activations would lose bits in f16 and stay on the GEMV.
   // RLXQ_DECODE=gemv|skinny forces one where both apply.
   {
-    const bool sk_ok = skinny_applies(scheme, group, m, k) && xbf;
+    const bool sk_ok = skinny_applies(scheme, group, sb_dtype, m, k) && xbf;
     bool use_sk = sk_ok && m >= 5;
     if (const char* e = std::getenv("RLXQ_DECODE")) {
       if (!std::strcmp(e, "gemv")) use_sk = false;

@@ -104,12 +104,12 @@ const char* scheme_name(int scheme);
 int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dtype, const void* w,
                   const void* scales, const void* biases, int sb_dtype, int64_t m, int64_t k,
                   int64_t n, void* y, int y_dtype, void* stream);
-bool skinny_applies(int scheme, int group, int64_t m, int64_t k);
+bool skinny_applies(int scheme, int group, int sb_dtype, int64_t m, int64_t k);
 // Order of the batched-decode activations within a 32-block: 1 the GGUF
-// nibble-unpacking order, 2 MLX's, 0 natural (Q8_0, Q6_K).
+// nibble-unpacking order, 2 MLX's, 0 natural (Q8_0, Q6_K, MXFP4).
 int sk_order(int scheme);
-// MLX per-group scales and biases for the batched-decode kernels (unused by
-// the GGUF formats).
+// MLX per-group scales and biases, or MXFP4's E8M0 scale bytes, for the
+// batched-decode kernels (unused by the GGUF formats).
 struct SkinnySb {
   const void* scales = nullptr;
   const void* biases = nullptr;
@@ -121,9 +121,11 @@ struct SkinnySb {
 int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream);
 // x [m, k] -> prepared f16 activations (x16) and row factors (inv_s) at the
 // start of the workspace; `extra` further bytes follow at *rest.  The
-// fragment-major layout holds mp >= m rows (the rows past m zero).
+// fragment-major layout holds mp >= m rows (the rows past m zero); out_bf16
+// stores bf16 instead of f16.
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, int order, size_t extra,
-             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major = false, int64_t mp = 0);
+             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major = false, int64_t mp = 0,
+             bool out_bf16 = false);
 int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
                     int64_t k, int64_t n, void* y, int y_dtype, void* stream, const SkinnySb& sb = SkinnySb());
 int i8b_dispatch(rlxq_ctx* ctx, int group, const void* x, int x_dtype, const void* w, const void* scales,

@@ -30,7 +30,7 @@ int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream) {
 }
 
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, int order, size_t extra,
-             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major, int64_t mp) {
+             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major, int64_t mp, bool out_bf16) {
   if (!frag_major || mp < m) mp = m;
   const size_t x16_bytes = round256((size_t)(mp * k) * 2), s_bytes = round256((size_t)m * 4);
   void* ws = nullptr;
@@ -47,6 +47,7 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, in
   xa.x_bf16 = x_dtype == RLXQ_BF16;
   xa.nibble_order = order;
   xa.frag_major = frag_major ? 1 : 0;
+  xa.out_bf16 = out_bf16 ? 1 : 0;
   *rest = wsb + x16_bytes + s_bytes;
   hipFunction_t fn;
   if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
@@ -77,7 +78,8 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   char* rest = nullptr;
   int rc;
   const int64_t mp = mch * 16 * MT;
-  if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp)))
+  if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp,
+                     scheme == RLXQ_MLX_MXFP4)))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
@@ -134,7 +136,8 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   char* rest = nullptr;
   int rc;
   const int64_t mp = mch * 16 * MT;
-  if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp)))
+  if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp,
+                     scheme == RLXQ_MLX_MXFP4)))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
@@ -174,13 +177,15 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
 
 int sk_order(int scheme) {
   if (scheme == RLXQ_MLX_AFFINE4) return 2;
-  return scheme != RLXQ_GGUF_Q8_0 && scheme != RLXQ_GGUF_Q6_K ? 1 : 0;
+  return scheme != RLXQ_GGUF_Q8_0 && scheme != RLXQ_GGUF_Q6_K && scheme != RLXQ_MLX_MXFP4 ? 1 : 0;
 }
 
-bool skinny_applies(int scheme, int group, int64_t m, int64_t k) {
+bool skinny_applies(int scheme, int group, int sb_dtype, int64_t m, int64_t k) {
   return (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q4_1 ||
           ((scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K) && k % 256 == 0) ||
-          (scheme == RLXQ_MLX_AFFINE4 && group >= 32 && group % 32 == 0 && k % group == 0)) &&
+          (scheme == RLXQ_MLX_AFFINE4 && group >= 32 && group % 32 == 0 && k % group == 0) ||
+          // (E8M0 scales only: a bf16 scale times a code is not exact in bf16)
+          (scheme == RLXQ_MLX_MXFP4 && sb_dtype == RLXQ_U8)) &&
          m >= 1 && m <= 256 && k % 128 == 0;
 }
 
@@ -190,7 +195,7 @@ bool skinny_applies(int scheme, int group, int64_t m, int64_t k) {
 // [splits, M, N]) are added in split order.
 int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
                     int64_t k, int64_t n, void* y, int y_dtype, void* stream, const SkinnySb& sb) {
-  const bool mlx = scheme == RLXQ_MLX_AFFINE4;
+  const bool mlx = scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_MXFP4;
   // The register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR="MT,NT,D"
   // picks a compiled one (every combination for Q4_1, the defaults for Q4_0
   // and Q8_0), "0" the LDS-staged kernels below.
@@ -218,7 +223,7 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
     if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
       int a1, a2, a3;
       if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) xmt = a1, xnt = a2, xd = a3;
-      else if (e[0] == '0')   // (Q4_K, Q6_K and MLX4 have no LDS-staged kernel)
+      else if (e[0] == '0')   // (Q4_K, Q6_K, MLX4 and MXFP4 have no LDS-staged kernel)
         xr = scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K || mlx;
     }
     if (xr) return skinny_xr_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, xmt, xnt, xd, sb);

@@ -18,6 +18,7 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 // Element of a 32-block held at position p (see above); order 0 natural,
 // 1 GGUF nibbles, 2 MLX nibbles.
@@ -33,6 +34,7 @@ RLXQ_DEV int perm_k(int p, int order) {
 // code dwords.  A Q4_K sub-block normalises to the Q4_1 form: d = d * sc and
 // m = -dmin * mn rounded to f16, and code dword g holding elements 4g..4g+3
 // (low nibbles) and 16 + 4g.. (high nibbles) of the sub-block.
+// An MXFP4 block: its f32 scale (a power of two) and its four code words.
 // An MLX4 block: the group's f32 scale and bias rounded to f16 (the f16
 // range covers the scales of real weight slabs; scales below 2^-14 lose bits
 // as f16 subnormals) and its four code words as they are.
@@ -92,6 +94,37 @@ RLXQ_DEV f16x8_t dequant_lane(const uint32_t* bp, int g) {
   return f16x8_t{w[0].x, w[0].y, w[1].x, w[1].y, w[2].x, w[2].y, w[3].x, w[3].y};
 }
 
+// The B operand of one MFMA step and the step itself.  MXFP4 takes bf16
+// MFMA: E2M1 codes times an E8M0 scale (a power of two) are exact in bf16
+// (v_cvt_scalef32_pk_bf16_fp4, one per code pair), as are the bf16
+// activations scaled by a power of two, and its codes unpack in natural
+// order.  The other formats take f16 MFMA with dequant_lane's weights.
+template <int SCH> struct SkOp { typedef f16x8_t type; };
+template <> struct SkOp<SCH_MXFP4> { typedef bf16x8_t type; };
+
+template <int SCH>
+RLXQ_DEV typename SkOp<SCH>::type sk_b(const uint32_t* bp, int g) {
+  if constexpr (SCH == SCH_MXFP4) {
+    const float sc = __uint_as_float(bp[0]);
+    const uint32_t q = bp[1 + g];
+    const u32x4_t b = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 0)),
+                       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 1)),
+                       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 2)),
+                       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 3))};
+    return __builtin_bit_cast(bf16x8_t, b);
+  } else {
+    return dequant_lane<SCH>(bp, g);
+  }
+}
+
+template <int SCH>
+RLXQ_DEV f32x4_t sk_mfma(f16x8_t a, typename SkOp<SCH>::type b, f32x4_t c) {
+  if constexpr (SCH == SCH_MXFP4)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), b, c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
 // Raw block -> normalised dwords.
 template <int SCH>
 RLXQ_DEV void normalise(const RawBlk<SCH>& r, uint32_t* o) {
@@ -117,6 +150,9 @@ RLXQ_DEV void normalise(const RawBlk<SCH>& r, uint32_t* o) {
     const uint32_t sh = 4 * (r.sub & 1u);
 #pragma unroll
     for (int g = 0; g < 4; g++) o[1 + g] = ((qs[g] >> sh) & 0x0F0F0F0Fu) | (((qs[4 + g] >> sh) & 0x0F0F0F0Fu) << 4);
+  } else if constexpr (SCH == SCH_MXFP4) {
+    o[0] = __float_as_uint(r.s);
+    o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;
   } else if constexpr (SCH == SCH_MLX4) {
     o[0] = f32_to_f16_bits(r.s) | (f32_to_f16_bits(r.b) << 16);
     o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;

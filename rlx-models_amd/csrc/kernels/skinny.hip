@@ -1,6 +1,7 @@
 // Batched-decode dequant-GEMM for small M (the multi-row decode path):
 // y[m, n] = sum_k x[m, k] * dequant(W)[n, k] for up to 64 activation rows and
-// GGUF Q8_0 / Q4_0 / Q4_1 / Q4_K / Q6_K and MLX affine 4-bit weights, streaming every weight once for all
+// GGUF Q8_0 / Q4_0 / Q4_1 / Q4_K / Q6_K, MLX affine 4-bit and MXFP4 weights,
+// streaming every weight once for all
 // rows.
 // Replaces the backend kernel of Op::DequantMatMul at decode batch sizes
 // (crates/rlx-models-core/src/standard_decoder.rs:727-738, M rows per call).
@@ -442,11 +443,10 @@ RLXQ_DEV bool skinny_xr_core(const uint16_t* x16, int64_t Mp, int64_t m0, const 
     for (int i = 0; i < 4; i++)
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        const f16x8_t b = dequant_lane<SCH>(o[t], i);
+        const auto b = sk_b<SCH>(o[t], i);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
-          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, st.x[mt][i]), b, acc[mt][t],
-                                                             0, 0, 0);
+          acc[mt][t] = sk_mfma<SCH>(__builtin_bit_cast(f16x8_t, st.x[mt][i]), b, acc[mt][t]);
       }
   };
   // (slots past the wave's chunks repeat its last one: a few redundant
@@ -706,9 +706,9 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
       for (int mt = 0; mt < MT; mt++) af[mt] = *reinterpret_cast<const f16x8_t*>(slot + (i * MT + mt) * 1024 + lane * 16);
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        const f16x8_t b = dequant_lane<SCH>(o[t], i);
+        const auto b = sk_b<SCH>(o[t], i);
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mt], b, acc[mt][t], 0, 0, 0);
+        for (int mt = 0; mt < MT; mt++) acc[mt][t] = sk_mfma<SCH>(af[mt], b, acc[mt][t]);
       }
     }
   };
@@ -835,8 +835,9 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
     uint32_t o[16];
 #pragma unroll
     for (int p = 0; p < 32; p += 2) {
-      const uint32_t h0 = f32_to_f16_bits(w[rlxq::perm_k(p, nib)] * s);
-      const uint32_t h1 = f32_to_f16_bits(w[rlxq::perm_k(p + 1, nib)] * s);
+      const float w0 = w[rlxq::perm_k(p, nib)] * s, w1 = w[rlxq::perm_k(p + 1, nib)] * s;
+      const uint32_t h0 = a.out_bf16 ? f32_to_bf16_bits(w0) : f32_to_f16_bits(w0);
+      const uint32_t h1 = a.out_bf16 ? f32_to_bf16_bits(w1) : f32_to_f16_bits(w1);
       o[p / 2] = h0 | (h1 << 16);
     }
     if (a.frag_major) {
@@ -961,6 +962,9 @@ RLXQ_SKINNYXR_INST(q4_k, SCH_Q4_K, 4, 2, 2)
 RLXQ_SKINNYXR_INST(mlx4, SCH_MLX4, 1, 2, 4)
 RLXQ_SKINNYXR_INST(mlx4, SCH_MLX4, 2, 2, 3)
 RLXQ_SKINNYXR_INST(mlx4, SCH_MLX4, 4, 2, 2)
+RLXQ_SKINNYXR_INST(mxfp4, SCH_MXFP4, 1, 2, 4)
+RLXQ_SKINNYXR_INST(mxfp4, SCH_MXFP4, 2, 2, 3)
+RLXQ_SKINNYXR_INST(mxfp4, SCH_MXFP4, 4, 2, 2)
 RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 1, 2, 2)
 RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 2, 2, 2)
 RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 4, 2, 1)
@@ -984,6 +988,9 @@ RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 4, 1, 3)
 RLXQ_SKINNYNS_INST(mlx4, SCH_MLX4, 1, 1, 3)
 RLXQ_SKINNYNS_INST(mlx4, SCH_MLX4, 2, 1, 3)
 RLXQ_SKINNYNS_INST(mlx4, SCH_MLX4, 4, 1, 3)
+RLXQ_SKINNYNS_INST(mxfp4, SCH_MXFP4, 1, 1, 3)
+RLXQ_SKINNYNS_INST(mxfp4, SCH_MXFP4, 2, 1, 3)
+RLXQ_SKINNYNS_INST(mxfp4, SCH_MXFP4, 4, 1, 3)
 RLXQ_SKINNYNS_INST(q6_k, SCH_Q6_K, 1, 1, 3)
 RLXQ_SKINNYNS_INST(q6_k, SCH_Q6_K, 2, 1, 3)
 RLXQ_SKINNYNS_INST(q6_k, SCH_Q6_K, 4, 1, 2)

@@ -4,7 +4,7 @@
 #define RLXQ_SKINNY_ARGS_H
 #include <stdint.h>
 
-/* Activation preparation: x [M, K] (f32 or bf16) -> x16 f16 scaled by a
+/* Activation preparation: x [M, K] (f32 or bf16) -> x16 f16 (or bf16) scaled by a
  * power of two per row (inv_s[m] = 1 / scale) and permuted within each
  * 32-element block to the order the packed codes unpack to.  Row-major
  * [M, K], or (frag_major) fragment-major over Mp >= M rows (rows M .. Mp - 1
@@ -22,6 +22,7 @@ typedef struct rlxq_x16_args {
   /* gathered rows (fragment-major only): x16 row r is x row rmap[r] / rdiv,
    * a zero row where rmap[r] < 0; NULL: x16 row r is x row r             */
   const int32_t* rmap;
+  int32_t out_bf16;       /* x16 holds bf16 (MXFP4's bf16 MFMA), not f16  */
 } rlxq_x16_args;
 
 typedef struct rlxq_skinny_args {
@@ -35,7 +36,8 @@ typedef struct rlxq_skinny_args {
   int32_t kslice;         /* K per split, a multiple of 128               */
   int32_t splits, tiles_n, y_bf16;
   /* MLX affine 4-bit: per-group scales and biases [N, K / group] (f32, or
-   * bf16 where sb_bf16); unused by the GGUF formats                     */
+   * bf16 where sb_bf16 == 1); MXFP4: E8M0 scale bytes [N, K / 32]
+   * (sb_bf16 == 2); unused by the GGUF formats                           */
   const void* scales;
   const void* biases;
   int64_t group;

@@ -339,3 +339,79 @@ def test_skinny_mlx4_activation_range_and_no_staged_kernel(ctx, orc, monkeypatch
             assert np.all(got[r] == 0.0)
             continue
         assert rel_err(got[r:r + 1], want[r:r + 1]) <= TOL_F32, r
+
+
+# MXFP4 with E8M0 scale bytes: E2M1 codes times a power of two are exact in
+# bf16, as are the power-of-two-scaled bf16 activations, so the bf16 MFMA
+# products are exact and only the f32 accumulation order differs from the
+# float64 oracle: bar 1e-5
+MXFP4_TOL = 1e-5
+MXFP4_XR = ["1,2,4", "2,2,3", "4,2,2"]
+MXFP4_NS = ["1,1,3", "2,1,3", "4,1,3"]
+
+
+def _mxfp4_case(ctx, orc, rng, m, k, n, ydt="f32", x_scale=None):
+    import torch
+    from test_gemv_gpu import _t, _x_as
+
+    codes, eb = orc.synth_mxfp4(rng, n, k)
+    x32 = rng.standard_normal((m, k)).astype(np.float32)
+    if x_scale is not None:
+        x32 *= x_scale[:, None]
+    xt, xv = _x_as(x32, "bf16")
+    y = ctx.dequant_matmul(xt, _t(codes), 9, n, scales=_t(eb),
+                           y_dtype=torch.bfloat16 if ydt == "bf16" else torch.float32)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy(), orc.mxfp4_matmul_f64(xv, codes, eb, n)
+
+
+@pytest.mark.parametrize("mkn", [(5, 256, 7), (16, 4096, 512), (17, 1024, 300), (33, 768, 129),
+                                 (64, 4096, 256), (100, 768, 200), (256, 384, 40)], ids=str)
+def test_skinny_mxfp4_default(ctx, orc, mkn):
+    m, k, n = mkn
+    announce(f"skinny mxfp4 default {mkn}")
+    got, want = _mxfp4_case(ctx, orc, np.random.default_rng(m * 13 + k + n), m, k, n)
+    prefix = "rlxq_skinnyxr_mxfp4_" if m <= 16 else "rlxq_skinnyns_mxfp4_"
+    assert ctx.last_kernel.startswith(prefix), ctx.last_kernel
+    assert rel_err(got, want) <= MXFP4_TOL
+    got, want = _mxfp4_case(ctx, orc, np.random.default_rng(m * 13 + k + n), m, k, n, ydt="bf16")
+    assert rel_err(got, want) <= TOL_BF16
+
+
+@pytest.mark.parametrize("cfg", [("xr", c) for c in MXFP4_XR] + [("ns", c) for c in MXFP4_NS], ids=str)
+def test_skinny_mxfp4_every_variant(ctx, orc, monkeypatch, cfg):
+    kind, rest = cfg
+    monkeypatch.setenv("RLXQ_SKINNY_XR" if kind == "xr" else "RLXQ_SKINNY_NS", rest)
+    mt, nt, d = (int(v) for v in rest.split(","))
+    for (m, k, n) in [(5, 256, 7), (16 * mt + 3, 2048, 64 * nt * 3 + 5), (9, 12288, 200), (64, 1536, 96),
+                      (3, 768, 64 * nt)]:
+        announce(f"skinny mxfp4 {kind} {rest} {(m, k, n)}")
+        got, want = _mxfp4_case(ctx, orc, np.random.default_rng(m + k + n + mt + 3), m, k, n)
+        assert ctx.last_kernel == f"rlxq_skinny{kind}_mxfp4_mt{mt}_nt{nt}_d{d}", ctx.last_kernel
+        assert rel_err(got, want) <= MXFP4_TOL, (cfg, m, k, n)
+
+
+def test_skinny_mxfp4_activation_range_and_bf16_scales_stay_on_gemv(ctx, orc, monkeypatch):
+    """Rows far apart in magnitude and a zero row; decoded bf16 scales (a
+    general bf16 scale times a code is not exact in bf16) keep the GEMV."""
+    import torch
+    from test_gemv_gpu import _t, _x_as
+
+    m, k, n = 8, 512, 96
+    xs = np.ones(m, dtype=np.float32)
+    xs[0], xs[1], xs[3] = 1e6, 1e-6, 0.0
+    got, want = _mxfp4_case(ctx, orc, np.random.default_rng(37), m, k, n, x_scale=xs)
+    assert ctx.last_kernel.startswith("rlxq_skinnyxr_mxfp4_"), ctx.last_kernel
+    for r in range(m):
+        if r == 3:
+            assert np.all(got[r] == 0.0)
+            continue
+        assert rel_err(got[r:r + 1], want[r:r + 1]) <= MXFP4_TOL, r
+    rng = np.random.default_rng(38)
+    codes, eb = orc.synth_mxfp4(rng, n, k)
+    sb = (eb.astype(np.uint16) << 7).view(np.int16)
+    xt, xv = _x_as(rng.standard_normal((m, k)).astype(np.float32), "bf16")
+    y = ctx.dequant_matmul(xt, _t(codes), 9, n, scales=_t(sb).view(torch.bfloat16))
+    torch.cuda.synchronize()
+    assert not ctx.last_kernel.startswith("rlxq_skinny"), ctx.last_kernel
+    assert rel_err(y.cpu().numpy(), orc.mxfp4_matmul_f64(xv, codes, eb, n)) <= TOL_F32
