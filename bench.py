@@ -333,18 +333,20 @@ def prefill_headline(detail: dict) -> dict:
 
 def batched_section(ctx, gen, sptr, stream) -> dict:
     """Config 3: batched decode, Q4_1 and Q8_0 (and Q4_K, Q6_K, MLX affine
-    4-bit, group 64 with bf16 slabs, and MXFP4 with E8M0 scale bytes beside
-    them), M in {1, 4, 16, 64}, bf16 x, f32 y."""
+    4- and 8-bit, group 64 with bf16 slabs, and MXFP4 with E8M0 scale bytes
+    beside them), M in {1, 4, 16, 64}, bf16 x, f32 y."""
     import torch
     import rlxq
 
     res = {}
     mlx_synth = lambda n, k, g: synth_mlx_gpu(n, k, 4, 64, g)
+    mlx8_synth = lambda n, k, g: synth_mlx_gpu(n, k, 8, 64, g)
     for sname, scheme, bpw, synth in (("q4_1", rlxq.GGUF_Q4_1, Q4_1_BPW, synth_q4_1_gpu),
                                       ("q8_0", rlxq.GGUF_Q8_0, Q8_0_BPW, synth_q8_0_gpu),
                                       ("q4_k", rlxq.GGUF_Q4_K, 144 / 256, synth_q4_k_gpu),
                                       ("q6_k", rlxq.GGUF_Q6_K, 210 / 256, synth_q6_k_gpu),
                                       ("mlx4", rlxq.MLX_AFFINE4, 0.5 + 4 / 64, mlx_synth),
+                                      ("mlx8", rlxq.MLX_AFFINE8, 1 + 4 / 64, mlx8_synth),
                                       ("mxfp4", rlxq.MLX_MXFP4, 0.5 + 1 / 32, synth_mxfp4_gpu)):
         for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):
             wb = n * k * bpw

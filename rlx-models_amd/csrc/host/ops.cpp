@@ -298,7 +298,7 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     if (use_gemm) return gemm_dispatch(ctx, scheme, group, x, w, scales, biases, sb_dtype, rb, m, k, n, y, y_dtype, stream);
   }
   // Batched decode: from 5 rows of bf16 activations (exact in f16 once scaled),
-  // GGUF and MLX affine 4-bit weights stream once for all rows through the
+  // GGUF and MLX affine 4/8-bit weights stream once for all rows through the
   // f16-MFMA kernel (MXFP4 with E8M0 scales through its bf16-MFMA twin); f32
   // activations would lose bits in f16 and stay on the GEMV.
   // RLXQ_DECODE=gemv|skinny forces one where both apply.

@@ -106,7 +106,8 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
                   int64_t n, void* y, int y_dtype, void* stream);
 bool skinny_applies(int scheme, int group, int sb_dtype, int64_t m, int64_t k);
 // Order of the batched-decode activations within a 32-block: 1 the GGUF
-// nibble-unpacking order, 2 MLX's, 0 natural (Q8_0, Q6_K, MXFP4).
+// nibble-unpacking order, 2 MLX's 4-bit order, 0 natural (Q8_0, Q6_K, MLX
+// 8-bit, MXFP4).
 int sk_order(int scheme);
 // MLX per-group scales and biases, or MXFP4's E8M0 scale bytes, for the
 // batched-decode kernels (unused by the GGUF formats).

@@ -177,13 +177,17 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
 
 int sk_order(int scheme) {
   if (scheme == RLXQ_MLX_AFFINE4) return 2;
-  return scheme != RLXQ_GGUF_Q8_0 && scheme != RLXQ_GGUF_Q6_K && scheme != RLXQ_MLX_MXFP4 ? 1 : 0;
+  return scheme != RLXQ_GGUF_Q8_0 && scheme != RLXQ_GGUF_Q6_K && scheme != RLXQ_MLX_MXFP4 &&
+                 scheme != RLXQ_MLX_AFFINE8
+             ? 1
+             : 0;
 }
 
 bool skinny_applies(int scheme, int group, int sb_dtype, int64_t m, int64_t k) {
   return (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q4_1 ||
           ((scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K) && k % 256 == 0) ||
-          (scheme == RLXQ_MLX_AFFINE4 && group >= 32 && group % 32 == 0 && k % group == 0) ||
+          ((scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_AFFINE8) && group >= 32 && group % 32 == 0 &&
+           k % group == 0) ||
           // (E8M0 scales only: a bf16 scale times a code is not exact in bf16)
           (scheme == RLXQ_MLX_MXFP4 && sb_dtype == RLXQ_U8)) &&
          m >= 1 && m <= 256 && k % 128 == 0;
@@ -195,7 +199,7 @@ bool skinny_applies(int scheme, int group, int sb_dtype, int64_t m, int64_t k) {
 // [splits, M, N]) are added in split order.
 int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
                     int64_t k, int64_t n, void* y, int y_dtype, void* stream, const SkinnySb& sb) {
-  const bool mlx = scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_MXFP4;
+  const bool mlx = scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_AFFINE8 || scheme == RLXQ_MLX_MXFP4;
   // The register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR="MT,NT,D"
   // picks a compiled one (every combination for Q4_1, the defaults for Q4_0
   // and Q8_0), "0" the LDS-staged kernels below.
@@ -223,7 +227,7 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
     if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
       int a1, a2, a3;
       if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) xmt = a1, xnt = a2, xd = a3;
-      else if (e[0] == '0')   // (Q4_K, Q6_K, MLX4 and MXFP4 have no LDS-staged kernel)
+      else if (e[0] == '0')   // (Q4_K, Q6_K and the MLX formats have no LDS-staged kernel)
         xr = scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K || mlx;
     }
     if (xr) return skinny_xr_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, xmt, xnt, xd, sb);

@@ -35,14 +35,15 @@ RLXQ_DEV int perm_k(int p, int order) {
 // m = -dmin * mn rounded to f16, and code dword g holding elements 4g..4g+3
 // (low nibbles) and 16 + 4g.. (high nibbles) of the sub-block.
 // An MXFP4 block: its f32 scale (a power of two) and its four code words.
-// An MLX4 block: the group's f32 scale and bias rounded to f16 (the f16
-// range covers the scales of real weight slabs; scales below 2^-14 lose bits
-// as f16 subnormals) and its four code words as they are.
+// An MLX4 (MLX8) block: the group's f32 scale and bias rounded to f16 (the
+// f16 range covers the scales of real weight slabs; scales below 2^-14 lose
+// bits as f16 subnormals) and its four (eight) code words as they are; MLX8's
+// codes, four per word LSB first, unpack in natural order.
 // A Q6_K block normalises to the int8 form of Q8_0 with one f16 scale per
 // 16 weights: scale dword d0 | d1 << 16 (d * sc of the two halves, rounded
 // to f16) and code bytes code + 96, so that code - 32 = byte - 128 as for
 // Q8_0's sign-flipped bytes; its activations stay in natural order.
-template <int SCH> constexpr int sk_bdw() { return (SCH == SCH_Q8_0 || SCH == SCH_Q6_K) ? 9 : 5; }
+template <int SCH> constexpr int sk_bdw() { return (SCH == SCH_Q8_0 || SCH == SCH_Q6_K || SCH == SCH_MLX8) ? 9 : 5; }
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
 // 6:4, lgkmcnt 11:8): wait on one counter, leave the others unconstrained.
@@ -63,7 +64,16 @@ RLXQ_DEV f16x8_t dequant_lane(const uint32_t* bp, int g) {
   const uint32_t dm = bp[0];
   const f16x2_t d2 = as_h2(perm_b32(dm, dm, 0x01000100u));
   f16x2_t w[4];
-  if constexpr (SCH == SCH_Q8_0 || SCH == SCH_Q6_K) {
+  if constexpr (SCH == SCH_MLX8) {
+    // unsigned codes in natural order: d*q + m with one rounding
+    const uint32_t u0 = bp[1 + 2 * g], u1 = bp[2 + 2 * g];
+    const f16x2_t m2 = as_h2(perm_b32(dm, dm, 0x03020302u));
+    const f16x2_t off = {(_Float16)-1024.f, (_Float16)-1024.f};
+    w[0] = __builtin_elementwise_fma(magic_lo(u0) + off, d2, m2);
+    w[1] = __builtin_elementwise_fma(magic_hi(u0) + off, d2, m2);
+    w[2] = __builtin_elementwise_fma(magic_lo(u1) + off, d2, m2);
+    w[3] = __builtin_elementwise_fma(magic_hi(u1) + off, d2, m2);
+  } else if constexpr (SCH == SCH_Q8_0 || SCH == SCH_Q6_K) {
     const uint32_t flip = SCH == SCH_Q8_0 ? 0x80808080u : 0u;
     const uint32_t u0 = bp[1 + 2 * g] ^ flip, u1 = bp[2 + 2 * g] ^ flip;
     // (Q6_K: positions 8g.. lie in half g / 2 of the block)
@@ -156,6 +166,10 @@ RLXQ_DEV void normalise(const RawBlk<SCH>& r, uint32_t* o) {
   } else if constexpr (SCH == SCH_MLX4) {
     o[0] = f32_to_f16_bits(r.s) | (f32_to_f16_bits(r.b) << 16);
     o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;
+  } else if constexpr (SCH == SCH_MLX8) {
+    o[0] = f32_to_f16_bits(r.s) | (f32_to_f16_bits(r.b) << 16);
+    o[1] = r.q0.x; o[2] = r.q0.y; o[3] = r.q0.z; o[4] = r.q0.w;
+    o[5] = r.q1.x; o[6] = r.q1.y; o[7] = r.q1.z; o[8] = r.q1.w;
   } else if constexpr (SCH == SCH_Q4_1) {
     o[0] = r.h;
     o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;

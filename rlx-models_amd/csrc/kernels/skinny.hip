@@ -1,7 +1,7 @@
 // Batched-decode dequant-GEMM for small M (the multi-row decode path):
 // y[m, n] = sum_k x[m, k] * dequant(W)[n, k] for up to 64 activation rows and
-// GGUF Q8_0 / Q4_0 / Q4_1 / Q4_K / Q6_K, MLX affine 4-bit and MXFP4 weights,
-// streaming every weight once for all
+// GGUF Q8_0 / Q4_0 / Q4_1 / Q4_K / Q6_K, MLX affine 4/8-bit and MXFP4
+// weights, streaming every weight once for all
 // rows.
 // Replaces the backend kernel of Op::DequantMatMul at decode batch sizes
 // (crates/rlx-models-core/src/standard_decoder.rs:727-738, M rows per call).
@@ -962,6 +962,9 @@ RLXQ_SKINNYXR_INST(q4_k, SCH_Q4_K, 4, 2, 2)
 RLXQ_SKINNYXR_INST(mlx4, SCH_MLX4, 1, 2, 4)
 RLXQ_SKINNYXR_INST(mlx4, SCH_MLX4, 2, 2, 3)
 RLXQ_SKINNYXR_INST(mlx4, SCH_MLX4, 4, 2, 2)
+RLXQ_SKINNYXR_INST(mlx8, SCH_MLX8, 1, 2, 4)
+RLXQ_SKINNYXR_INST(mlx8, SCH_MLX8, 2, 2, 3)
+RLXQ_SKINNYXR_INST(mlx8, SCH_MLX8, 4, 2, 2)
 RLXQ_SKINNYXR_INST(mxfp4, SCH_MXFP4, 1, 2, 4)
 RLXQ_SKINNYXR_INST(mxfp4, SCH_MXFP4, 2, 2, 3)
 RLXQ_SKINNYXR_INST(mxfp4, SCH_MXFP4, 4, 2, 2)
@@ -988,6 +991,9 @@ RLXQ_SKINNYNS_INST(q4_k, SCH_Q4_K, 4, 1, 3)
 RLXQ_SKINNYNS_INST(mlx4, SCH_MLX4, 1, 1, 3)
 RLXQ_SKINNYNS_INST(mlx4, SCH_MLX4, 2, 1, 3)
 RLXQ_SKINNYNS_INST(mlx4, SCH_MLX4, 4, 1, 3)
+RLXQ_SKINNYNS_INST(mlx8, SCH_MLX8, 1, 1, 3)
+RLXQ_SKINNYNS_INST(mlx8, SCH_MLX8, 2, 1, 3)
+RLXQ_SKINNYNS_INST(mlx8, SCH_MLX8, 4, 1, 3)
 RLXQ_SKINNYNS_INST(mxfp4, SCH_MXFP4, 1, 1, 3)
 RLXQ_SKINNYNS_INST(mxfp4, SCH_MXFP4, 2, 1, 3)
 RLXQ_SKINNYNS_INST(mxfp4, SCH_MXFP4, 4, 1, 3)

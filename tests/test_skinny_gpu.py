@@ -269,12 +269,12 @@ MLX_XR = ["1,2,4", "2,2,3", "4,2,2"]
 MLX_NS = ["1,1,3", "2,1,3", "4,1,3"]
 
 
-def _mlx_case(ctx, orc, rng, m, k, n, group, sb, ydt="f32", x_scale=None):
+def _mlx_case(ctx, orc, rng, m, k, n, group, sb, ydt="f32", x_scale=None, bits=4):
     import torch
     import rlxq
     from test_gemv_gpu import _t, _x_as
 
-    codes = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint32)
+    codes = rng.integers(0, 2 ** 32, (n, k * bits // 32), dtype=np.uint32)
     sc = rng.uniform(0.01, 0.1, (n, k // group)).astype(np.float32)
     bi = rng.uniform(-0.5, 0.1, (n, k // group)).astype(np.float32)
     if sb == "bf16":
@@ -287,10 +287,11 @@ def _mlx_case(ctx, orc, rng, m, k, n, group, sb, ydt="f32", x_scale=None):
     if x_scale is not None:
         x32 *= x_scale[:, None]
     xt, xv = _x_as(x32, "bf16")
-    y = ctx.dequant_matmul(xt, _t(codes.view(np.uint8)), rlxq.MLX_AFFINE4, n, group=group, scales=st, biases=bt,
+    scheme = rlxq.MLX_AFFINE4 if bits == 4 else rlxq.MLX_AFFINE8
+    y = ctx.dequant_matmul(xt, _t(codes.view(np.uint8)), scheme, n, group=group, scales=st, biases=bt,
                            y_dtype=torch.bfloat16 if ydt == "bf16" else torch.float32)
     torch.cuda.synchronize()
-    return y.float().cpu().numpy(), orc.mlx_matmul_f64(xv, codes, sc, bi, n, 4, group)
+    return y.float().cpu().numpy(), orc.mlx_matmul_f64(xv, codes, sc, bi, n, bits, group)
 
 
 @pytest.mark.parametrize("group", [32, 64, 128])
@@ -339,6 +340,41 @@ def test_skinny_mlx4_activation_range_and_no_staged_kernel(ctx, orc, monkeypatch
             assert np.all(got[r] == 0.0)
             continue
         assert rel_err(got[r:r + 1], want[r:r + 1]) <= TOL_F32, r
+
+
+# MLX affine 8-bit: four codes per word, natural order, the group's scale
+# and bias rounded to f16 as for MLX4
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("mkn", [(5, 256, 7), (16, 4096, 512), (33, 768, 129), (64, 4096, 256), (256, 384, 40)],
+                         ids=str)
+def test_skinny_mlx8_default(ctx, orc, mkn, group):
+    m, k, n = mkn
+    if k % group:
+        pytest.skip("K not a multiple of the group")
+    announce(f"skinny mlx8 default {mkn} group={group}")
+    for sb in ("f32", "bf16"):
+        got, want = _mlx_case(ctx, orc, np.random.default_rng(m * 17 + k + n + group), m, k, n, group, sb, bits=8)
+        assert ctx.last_kernel.startswith("rlxq_skinny") and "_mlx8_" in ctx.last_kernel, ctx.last_kernel
+        assert rel_err(got, want) <= TOL_F32, sb
+    got, want = _mlx_case(ctx, orc, np.random.default_rng(m + group), m, k, n, group, "bf16", ydt="bf16", bits=8)
+    assert rel_err(got, want) <= TOL_BF16
+
+
+@pytest.mark.parametrize("cfg", [("xr", c) for c in MLX_XR] + [("ns", c) for c in MLX_NS], ids=str)
+def test_skinny_mlx8_every_variant(ctx, orc, monkeypatch, cfg):
+    kind, rest = cfg
+    monkeypatch.setenv("RLXQ_SKINNY_XR" if kind == "xr" else "RLXQ_SKINNY_NS", rest)
+    mt, nt, d = (int(v) for v in rest.split(","))
+    for (m, k, n, group) in [(5, 256, 7, 32), (16 * mt + 3, 2048, 64 * nt * 3 + 5, 64), (9, 12288, 200, 64),
+                             (64, 1536, 96, 128), (3, 768, 64 * nt, 32)]:
+        announce(f"skinny mlx8 {kind} {rest} {(m, k, n, group)}")
+        rng = np.random.default_rng(m + k + n + mt + 4)
+        xs = np.ones(m, dtype=np.float32)
+        xs[0] = 1e5
+        got, want = _mlx_case(ctx, orc, rng, m, k, n, group, "bf16", x_scale=xs, bits=8)
+        assert ctx.last_kernel == f"rlxq_skinny{kind}_mlx8_mt{mt}_nt{nt}_d{d}", ctx.last_kernel
+        for r in range(m):
+            assert rel_err(got[r:r + 1], want[r:r + 1]) <= TOL_F32, (cfg, m, k, n, r)
 
 
 # MXFP4 with E8M0 scale bytes: E2M1 codes times a power of two are exact in
