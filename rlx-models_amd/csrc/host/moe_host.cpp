@@ -109,9 +109,14 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   // layout, then the prepared rows).  RLXQ_MOE_KERNEL=sk forces them where
   // they apply; xr or lds keeps the GEMV kernels.
   const bool q6k = scheme == RLXQ_GGUF_Q6_K;
+  // (MLX: groups of whole 32-blocks; MXFP4: E8M0 scale bytes only, whose
+  // products with the codes are exact in bf16)
   const bool sk_ok = xbf && k % 128 == 0 &&
                      (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0 ||
-                      ((q4k || q6k) && k % 256 == 0));
+                      ((q4k || q6k) && k % 256 == 0) ||
+                      ((scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_AFFINE8) && group >= 32 &&
+                       group % 32 == 0 && k % group == 0) ||
+                      (scheme == RLXQ_MLX_MXFP4 && sb_dtype == RLXQ_U8));
   // (the gathered f16 rows take about 2 K bytes per entry: calls needing
   // more than 1 GiB of them stay on the GEMV kernels)
   const bool sk_fits = (double)(n_entries + fired_est * 63) * (double)k * 2.0 <= (double)(1u << 30);
@@ -267,6 +272,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     xa.frag_major = 1;
     xa.rdiv = x_div;
     xa.rmap = pa.emap;
+    xa.out_bf16 = scheme == RLXQ_MLX_MXFP4 ? 1 : 0;
     hipFunction_t fx;
     if ((rc = get_fn(ctx, "rlxq_x16_prep", &fx))) return rc;
     void* xargs[] = {&xa};
@@ -297,6 +303,10 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     ka.tiles_n = (int32_t)((width + 16 * nh - 1) / (16 * nh));
     ka.y_bf16 = (!combine && y_dtype == RLXQ_BF16) ? 1 : 0;
     ka.swiglu = swiglu ? 1 : 0;
+    ka.scales = scales;
+    ka.biases = biases;
+    ka.group = is_mlx(scheme) ? group : 32;
+    ka.sb_bf16 = sb_code(sb_dtype);
     std::snprintf(name, sizeof name, "rlxq_moesk_%s_mt%d_nt%d_d%d%s", scheme_name(scheme), sk_mt, NT, D,
                   swiglu ? "_sw" : "");
     hipFunction_t fk;

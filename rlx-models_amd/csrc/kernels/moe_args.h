@@ -76,6 +76,13 @@ typedef struct rlxq_moe_sk_args {
   int32_t swiglu;         /* 1: rows [0, N/2) gate, [N/2, N) up; y [entries, N/2]
                              = silu(x.Wg^T) * (x.Wu^T)                     */
   int32_t pad;
+  /* MLX affine: per-group scales and biases [E, N, K / group] (f32, or bf16
+   * where sb_bf16 == 1); MXFP4: E8M0 bytes [E, N, K / 32] (sb_bf16 == 2);
+   * unused by the GGUF formats (group 32)                                 */
+  const void* scales;
+  const void* biases;
+  int64_t group;
+  int32_t sb_bf16, pad2;
 } rlxq_moe_sk_args;
 
 #endif

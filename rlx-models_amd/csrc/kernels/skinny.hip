@@ -588,8 +588,13 @@ RLXQ_DEV void moe_sk_body(const rlxq_moe_sk_args& a) {
     wrow[t] = (SW && t >= NH) ? width + cc : cc;
   }
   f32x4_t acc[MT][NT];
+  // the expert's scale slabs (MLX, MXFP4): N rows of K / group entries
+  const int64_t slab = (int64_t)e * a.N * (a.K / a.group);
+  const int esz = a.sb_bf16 == 0 ? 4 : (a.sb_bf16 == 1 ? 2 : 1);
+  const void* sc = a.scales ? static_cast<const void*>(static_cast<const uint8_t*>(a.scales) + slab * esz) : nullptr;
+  const void* bi = a.biases ? static_cast<const void*>(static_cast<const uint8_t*>(a.biases) + slab * esz) : nullptr;
   if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.Mp, m0, a.bank + (int64_t)e * a.N * a.rb, a.rb, a.K, 0, a.K, wrow,
-                                      wok, acc))
+                                      wok, acc, sc, bi, a.group, a.sb_bf16))
     return;
   // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
 #pragma unroll
@@ -1082,6 +1087,9 @@ RLXQ_MOESK_SCHEME(q4_1, SCH_Q4_1, 4)
 RLXQ_MOESK_SCHEME(q4_0, SCH_Q4_0, 4)
 RLXQ_MOESK_SCHEME(q8_0, SCH_Q8_0, 4)
 RLXQ_MOESK_SCHEME(q4_k, SCH_Q4_K, 3)
+RLXQ_MOESK_SCHEME(mlx4, SCH_MLX4, 4)
+RLXQ_MOESK_SCHEME(mlx8, SCH_MLX8, 4)
+RLXQ_MOESK_SCHEME(mxfp4, SCH_MXFP4, 4)
 // Q6_K (22-dword raw blocks: shallower rings)
 RLXQ_MOESK_INST(q6_k, SCH_Q6_K, 1, 2, 2)
 RLXQ_MOESK_INST(q6_k, SCH_Q6_K, 1, 4, 1)

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from conftest import announce
-from test_gemv_gpu import _t, rel_err
+from test_gemv_gpu import _t, _x_as, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -161,3 +161,54 @@ def test_every_grouped_mfma_variant(ctx, orc, monkeypatch, cfg, sw):
                                 ids.ravel().astype(np.float32), n, E)
     want = gu[:, :n // 2] / (1.0 + np.exp(-gu[:, :n // 2])) * gu[:, n // 2:] if sw else gu
     assert rel_err(y.cpu().numpy(), want) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["mlx4_f32", "mlx4_bf16", "mlx8_bf16", "mxfp4"])
+@pytest.mark.parametrize("forced", [False, True])
+def test_grouped_mfma_mlx_and_mxfp4(ctx, orc, monkeypatch, fmt, forced):
+    """Op::DequantGroupedMatMulMlx at prefill sizes on the grouped MFMA
+    kernel: MLX affine 4/8-bit banks with [E, N, K / group] scale and bias
+    slabs (group 64) and MXFP4 banks with E8M0 bytes [E, N, K / 32], every
+    row's expert slab picked per chunk; against the oracle row by row."""
+    import torch
+    import rlxq
+
+    if forced:
+        monkeypatch.setenv("RLXQ_MOE_KERNEL", "sk")
+    rows, k, n, E, group = (37, 512, 200, 3, 64) if forced else (160, 1024, 136, 4, 64)
+    announce(f"grouped mfma {fmt} forced={forced} rows={rows}")
+    rng = np.random.default_rng(71 + rows + len(fmt))
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    xt, xv = _x_as(x, "bf16")
+    idx = rng.integers(0, E, rows).astype(np.float32)
+    want = np.zeros((rows, n))
+    if fmt == "mxfp4":
+        codes, eb = orc.synth_mxfp4(rng, E * n, k)
+        y = ctx.grouped_matmul(xt, _t(codes), _t(idx), rlxq.MLX_MXFP4, n, E, scales=_t(eb))
+        for r in range(rows):
+            sl = slice(int(idx[r]) * n, (int(idx[r]) + 1) * n)
+            want[r] = orc.mxfp4_matmul_f64(xv[r:r + 1], codes[sl], eb[sl], n)[0]
+        name, tol = "mxfp4", 1e-5
+    else:
+        bits = 4 if fmt.startswith("mlx4") else 8
+        codes = rng.integers(0, 2 ** 32, (E * n, k * bits // 32), dtype=np.uint32)
+        sc = rng.uniform(0.01, 0.1, (E * n, k // group)).astype(np.float32)
+        bi = rng.uniform(-0.5, 0.1, (E * n, k // group)).astype(np.float32)
+        if fmt.endswith("bf16"):
+            sc = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(sc))
+            bi = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(bi))
+            st, bt = _t(sc).to(torch.bfloat16), _t(bi).to(torch.bfloat16)
+        else:
+            st, bt = _t(sc), _t(bi)
+        scheme = rlxq.MLX_AFFINE4 if bits == 4 else rlxq.MLX_AFFINE8
+        y = ctx.grouped_matmul(xt, _t(codes.view(np.uint8)), _t(idx), scheme, n, E, group=group, scales=st,
+                               biases=bt)
+        for r in range(rows):
+            sl = slice(int(idx[r]) * n, (int(idx[r]) + 1) * n)
+            want[r] = orc.mlx_matmul_f64(xv[r:r + 1], codes[sl], sc[sl], bi[sl], n, bits, group)[0]
+        name, tol = f"mlx{bits}", TOL
+    torch.cuda.synchronize()
+    assert ctx.last_kernel.startswith(f"rlxq_moesk_{name}_"), ctx.last_kernel
+    got = y.cpu().numpy()
+    for r in range(rows):
+        assert rel_err(got[r:r + 1], want[r:r + 1]) <= tol, (fmt, r)
