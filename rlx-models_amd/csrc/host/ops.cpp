@@ -158,10 +158,19 @@ int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const 
   return fail(ctx, RLXQ_E_SCHEME, std::string(what) + ": unsupported scheme " + std::to_string(scheme));
 }
 
-// Prefill dequant-GEMM launch (tilings and split-K below).
-int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const void* w, const void* scales,
-                  const void* biases, int sb_dtype, int64_t rb, int64_t m, int64_t k, int64_t n, void* y,
-                  int y_dtype, void* stream) {
+// Schemes with an f16 variant of the prefill GEMM (f16 weights d*q + m
+// rounded once, MFMA on the prepared f16 activations): the GGUF legacy
+// blocks and the K-quants whose sub-blocks normalise to their forms.
+bool has_f16_gemm(int scheme) {
+  return is_gguf(scheme) || scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K;
+}
+
+// Prefill dequant-GEMM launch (tilings and split-K below).  f32 activations
+// take the f16 variant with each row prepared as a hi and a lo x16 row (the
+// epilogue adds the pair).
+int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dtype, const void* w,
+                  const void* scales, const void* biases, int sb_dtype, int64_t rb, int64_t m, int64_t k, int64_t n,
+                  void* y, int y_dtype, void* stream) {
   // 256 x 256 tiles, 8 waves, global loads two K steps ahead (one for Q6_K
   // and Q3_K, whose larger raw blocks do not fit two stages in 256 VGPRs;
   // Q6_K with its LDS stores after the step's MFMAs, which measured 15%
@@ -180,16 +189,22 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
     tile = std::atoi(te) == 128 ? 128 : 256;
     var = tile == 128 ? "" : (std::strncmp(te, "256w8", 5) == 0 ? te + 3 : "");
   }
-  // GGUF with f32 output: the f16 variant of the 256 tiles, whose f16 weights
-  // keep the output within 1e-3 (bf16 weights do not)
-  const bool has_f16 = is_gguf(scheme);   // Q8_0, Q4_0, Q4_1
-  if (!te && y_dtype == RLXQ_F32 && has_f16) var = bit8 ? "w8f" : "w8p2f";
+  // f32 output (or f32 activations): the f16 variant of the 256 tiles,
+  // whose f16 weights keep the output within 1e-3 (bf16 weights do not)
+  const bool has_f16 = has_f16_gemm(scheme);
+  const bool split = x_dtype == RLXQ_F32;
+  if (!te && (y_dtype == RLXQ_F32 || split) && has_f16)
+    var = bit8 ? "w8f" : (scheme == RLXQ_GGUF_Q6_K ? "w8lf" : "w8p2f");
   const bool w8 = tile == 256 && var[0] == 'w';
-  // "...f": f16 weights and MFMA on the prepared f16 activations (GGUF)
+  // "...f": f16 weights and MFMA on the prepared f16 activations
   const size_t vl = std::strlen(var);
   const bool f16 = vl > 0 && var[vl - 1] == 'f';
-  if (f16 && !has_f16) return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: the f16 GEMM serves Q8_0, Q4_0 and Q4_1");
-  const int64_t tiles_m = (m + tile - 1) / tile, tiles_n = (n + tile - 1) / tile;
+  if (f16 && !has_f16)
+    return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: the f16 GEMM serves Q8_0, Q4_0, Q4_1, Q4_K and Q6_K");
+  if (split && !f16) return fail(ctx, RLXQ_E_DTYPE, "dequant_matmul: f32 activations need an f16 GEMM variant");
+  // x16 rows: two per output row (hi, lo) for f32 activations
+  const int64_t mr = split ? 2 * m : m;
+  const int64_t tiles_m = (mr + tile - 1) / tile, tiles_n = (n + tile - 1) / tile;
   if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
   const int64_t tiles = tiles_m * tiles_n, ksteps = k / 64;
   int64_t splits = 1;
@@ -211,7 +226,8 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
   char* part = nullptr;
   if (f16) {
     rlxq_x16_args xa;
-    if ((rc = prep_x16(ctx, x, RLXQ_BF16, m, k, scheme != RLXQ_GGUF_Q8_0 ? 1 : 0, part_bytes, xa, &part, stream)))
+    if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &part, stream, false, 0, false,
+                       split)))
       return rc;
     a.x = xa.x16;
     a.inv_s = xa.inv_s;
@@ -224,7 +240,8 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, const voi
   a.scales = scales;
   a.biases = biases;
   a.y = y;
-  a.M = m;
+  a.M = mr;
+  a.pairs = split ? 1 : 0;
   a.N = n;
   a.K = k;
   a.rb = rb;
@@ -285,25 +302,30 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // to its f16 variant, which meets the 1e-3 bar.  Everything else stays on the
   // GEMV family, which keeps the products exact.
   // RLXQ_PREFILL=gemv|gemm forces one of them where both apply (tests).
+  // f32 activations (the reference's operand type) take the same MFMA
+  // kernels as hi + lo pairs of f16 (bf16 for MXFP4) rows, on schemes with an
+  // f16 GEMM variant (Q8_0, Q4_0, Q4_1, Q4_K, Q6_K); MLX, MXFP4 and the other
+  // K-quants keep f32 output (and f32 activations) on the GEMV family, whose
+  // weights are not rounded.
   {
-    // (MLX, MXFP4 and the K-quants: bf16 output only; f32 output stays on
-    // the GEMV family, whose weights are not rounded to bf16)
-    const bool gemm_ok = xbf && k % 64 == 0 && m >= 1;
-    const bool f16_gemm = is_gguf(scheme);
+    const bool f16_gemm = has_f16_gemm(scheme);
+    const bool gemm_ok = (xbf || f16_gemm) && k % 64 == 0 && m >= 1;
     bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (f16_gemm && m > 256));
     if (const char* e = std::getenv("RLXQ_PREFILL")) {
       if (!std::strcmp(e, "gemv")) use_gemm = false;
       if (!std::strcmp(e, "gemm")) use_gemm = gemm_ok;
     }
-    if (use_gemm) return gemm_dispatch(ctx, scheme, group, x, w, scales, biases, sb_dtype, rb, m, k, n, y, y_dtype, stream);
+    if (use_gemm)
+      return gemm_dispatch(ctx, scheme, group, x, x_dtype, w, scales, biases, sb_dtype, rb, m, k, n, y, y_dtype,
+                           stream);
   }
-  // Batched decode: from 5 rows of bf16 activations (exact in f16 once scaled),
-  // GGUF and MLX affine 4/8-bit weights stream once for all rows through the
-  // f16-MFMA kernel (MXFP4 with E8M0 scales through its bf16-MFMA twin); f32
-  // activations would lose bits in f16 and stay on the GEMV.
+  // Batched decode: from 5 rows, GGUF and MLX affine 4/8-bit weights stream
+  // once for all rows through the f16-MFMA kernel (MXFP4 with E8M0 scales
+  // through its bf16-MFMA twin).  bf16 activations are exact in f16 once
+  // scaled; f32 activations run as hi + lo row pairs (~22 significant bits).
   // RLXQ_DECODE=gemv|skinny forces one where both apply.
   {
-    const bool sk_ok = skinny_applies(scheme, group, sb_dtype, m, k) && xbf;
+    const bool sk_ok = skinny_applies(scheme, group, sb_dtype, m, k);
     bool use_sk = sk_ok && m >= 5;
     if (const char* e = std::getenv("RLXQ_DECODE")) {
       if (!std::strcmp(e, "gemv")) use_sk = false;
@@ -357,6 +379,29 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
       xr_w = two ? 4 : 8;
   bool use_xr = m == 1 && xbf && xr_scheme && nchunk64 <= xr_max && n < (int64_t(1) << 31);
   int xr_lds = 1;   // 1: the activations pass through LDS once per workgroup
+  // One row of f32 activations: the two-row kernel on its hi and lo bf16
+  // rows (Q4_1, MLX 4-bit, MXFP4 up to four unit chunks, Q4_K up to two),
+  // both rows' sums added into the one output.  RLXQ_GEMV_XR=0 turns it off.
+  {
+    const char* e = std::getenv("RLXQ_GEMV_XR");
+    const bool one_block4 = scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_MXFP4;
+    if (m == 1 && !xbf && (one_block4 || q4k) && nchunk64 <= (q4k ? 2 : 4) && n < (int64_t(1) << 31) &&
+        !(e && e[0] == '0')) {
+      const int nu = (int)nchunk64;
+      int d = nu <= 2 ? 2 : 1, wv = nu == 2 ? 4 : 8;
+      if (q4k) d = nu == 1 ? 2 : 1, wv = 8;
+      if (const char* t = std::getenv("RLXQ_GEMV_XSF")) std::sscanf(t, "%d,%d", &d, &wv);   // "D,W" (tuning)
+      std::snprintf(name, sizeof name, "rlxq_gemvxs_%s_U%d_D%d_W%d_F", scheme_name(scheme), nu, d, wv);
+      if ((rc = get_fn(ctx, name, &fn))) return rc;
+      const size_t lds = 2 * (size_t)(k / 32) * 68;
+      if (lds <= ctx->max_lds) {
+        const int per_cu = blocks_per_cu(ctx, name, fn, 64 * wv, lds);
+        int64_t gx = (int64_t)ctx->cu_count * per_cu;
+        gx = std::min<int64_t>(gx, (n + wv - 1) / wv);
+        return launch(ctx, fn, dim3((unsigned)gx, 1, 1), dim3(64 * wv, 1, 1), lds, stream, args, name);
+      }
+    }
+  }
   if (const char* e = std::getenv("RLXQ_GEMV_XR")) {
     int nu, d, wv, xs = 0;
     if (std::sscanf(e, "%d,%d,%d,%d", &nu, &d, &wv, &xs) >= 3) {

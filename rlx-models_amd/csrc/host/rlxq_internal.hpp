@@ -123,10 +123,11 @@ int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream);
 // x [m, k] -> prepared f16 activations (x16) and row factors (inv_s) at the
 // start of the workspace; `extra` further bytes follow at *rest.  The
 // fragment-major layout holds mp >= m rows (the rows past m zero); out_bf16
-// stores bf16 instead of f16.
+// stores bf16 instead of f16.  split: each row becomes two x16 rows, hi and
+// lo (2m rows; f32 activations keep ~22 significant bits), with a factor each.
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, int order, size_t extra,
              rlxq_x16_args& xa, char** rest, void* stream, bool frag_major = false, int64_t mp = 0,
-             bool out_bf16 = false);
+             bool out_bf16 = false, bool split = false);
 int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
                     int64_t k, int64_t n, void* y, int y_dtype, void* stream, const SkinnySb& sb = SkinnySb());
 int i8b_dispatch(rlxq_ctx* ctx, int group, const void* x, int x_dtype, const void* w, const void* scales,

@@ -30,9 +30,10 @@ int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream) {
 }
 
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, int order, size_t extra,
-             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major, int64_t mp, bool out_bf16) {
-  if (!frag_major || mp < m) mp = m;
-  const size_t x16_bytes = round256((size_t)(mp * k) * 2), s_bytes = round256((size_t)m * 4);
+             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major, int64_t mp, bool out_bf16, bool split) {
+  const int64_t rows = split ? 2 * m : m;   // x16 rows that hold data
+  if (!frag_major || mp < rows) mp = rows;
+  const size_t x16_bytes = round256((size_t)(mp * k) * 2), s_bytes = round256((size_t)rows * 4);
   void* ws = nullptr;
   int rc;
   if ((rc = workspace(ctx, x16_bytes + s_bytes + extra, &ws, stream))) return rc;
@@ -48,6 +49,7 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, in
   xa.nibble_order = order;
   xa.frag_major = frag_major ? 1 : 0;
   xa.out_bf16 = out_bf16 ? 1 : 0;
+  xa.split = split ? 1 : 0;
   *rest = wsb + x16_bytes + s_bytes;
   hipFunction_t fn;
   if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
@@ -63,7 +65,10 @@ namespace {
 int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
                        int64_t k, int64_t n, void* y, int y_dtype, void* stream, int MT, int NT, int D,
                        const SkinnySb& sb) {
-  const int64_t tiles_n = (n + 16 * NT - 1) / (16 * NT), mch = (m + 16 * MT - 1) / (16 * MT);
+  // f32 activations: hi and lo rows (2m x16 rows), added in the epilogue
+  const bool split = x_dtype == RLXQ_F32;
+  const int64_t mr = split ? 2 * m : m;
+  const int64_t tiles_n = (n + 16 * NT - 1) / (16 * NT), mch = (mr + 16 * MT - 1) / (16 * MT);
   const int64_t chunks = k / 128;
   const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   int64_t target = 2 * cus;
@@ -79,7 +84,7 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   int rc;
   const int64_t mp = mch * 16 * MT;
   if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp,
-                     scheme == RLXQ_MLX_MXFP4)))
+                     scheme == RLXQ_MLX_MXFP4, split)))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
@@ -88,7 +93,8 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   a.w = static_cast<const uint8_t*>(w);
   a.part = part_bytes ? reinterpret_cast<float*>(rest) : nullptr;
   a.y = y;
-  a.M = m;
+  a.M = mr;
+  a.pairs = split ? 1 : 0;
   a.N = n;
   a.K = k;
   a.rb = rb;
@@ -110,7 +116,9 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   void* args[] = {&a};
   if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name))) return rc;
   if (splits > 1) {
-    rc = splits_reduce(ctx, a, stream);
+    rlxq_skinny_args r = a;   // the partial sums hold the m output rows
+    r.M = m;
+    rc = splits_reduce(ctx, r, stream);
     if (!rc) ctx->last_kernel = name;
   }
   return rc;
@@ -121,7 +129,10 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
 int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
                        int64_t k, int64_t n, void* y, int y_dtype, void* stream, int MT, int NT, int D,
                        const SkinnySb& sb) {
-  const int64_t tiles_n = (n + 64 * NT - 1) / (64 * NT), mch = (m + 16 * MT - 1) / (16 * MT);
+  // f32 activations: hi and lo rows (2m x16 rows), added in the epilogue
+  const bool split = x_dtype == RLXQ_F32;
+  const int64_t mr = split ? 2 * m : m;
+  const int64_t tiles_n = (n + 64 * NT - 1) / (64 * NT), mch = (mr + 16 * MT - 1) / (16 * MT);
   const int64_t chunks = k / 128;
   const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   int64_t target = 2 * cus;
@@ -137,7 +148,7 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   int rc;
   const int64_t mp = mch * 16 * MT;
   if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp,
-                     scheme == RLXQ_MLX_MXFP4)))
+                     scheme == RLXQ_MLX_MXFP4, split)))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
@@ -146,7 +157,8 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   a.w = static_cast<const uint8_t*>(w);
   a.part = part_bytes ? reinterpret_cast<float*>(rest) : nullptr;
   a.y = y;
-  a.M = m;
+  a.M = mr;
+  a.pairs = split ? 1 : 0;
   a.N = n;
   a.K = k;
   a.rb = rb;
@@ -168,7 +180,9 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   void* args[] = {&a};
   if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name))) return rc;
   if (splits > 1) {
-    rc = splits_reduce(ctx, a, stream);
+    rlxq_skinny_args r = a;   // the partial sums hold the m output rows
+    r.M = m;
+    rc = splits_reduce(ctx, r, stream);
     if (!rc) ctx->last_kernel = name;
   }
   return rc;
@@ -197,9 +211,20 @@ bool skinny_applies(int scheme, int group, int sb_dtype, int64_t m, int64_t k) {
 // the row tiles do not cover the CUs: the smallest power of two that does,
 // at most 32 and at most one split per K step; their partial sums (f32,
 // [splits, M, N]) are added in split order.
-int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
+int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m_out,
                     int64_t k, int64_t n, void* y, int y_dtype, void* stream, const SkinnySb& sb) {
   const bool mlx = scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_AFFINE8 || scheme == RLXQ_MLX_MXFP4;
+  // f32 activations run as hi and lo x16 rows (the register-streamed and
+  // N-split kernels add each pair): the tilings below are chosen on those
+  // rows
+  const bool f32x = x_dtype == RLXQ_F32;
+  const int64_t m = f32x ? 2 * m_out : m_out;
+  auto run_xr = [&](int MT, int NT, int D) {
+    return skinny_xr_dispatch(ctx, scheme, x, x_dtype, w, rb, m_out, k, n, y, y_dtype, stream, MT, NT, D, sb);
+  };
+  auto run_ns = [&](int MT, int NT, int D) {
+    return skinny_ns_dispatch(ctx, scheme, x, x_dtype, w, rb, m_out, k, n, y, y_dtype, stream, MT, NT, D, sb);
+  };
   // The register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR="MT,NT,D"
   // picks a compiled one (every combination for Q4_1, the defaults for Q4_0
   // and Q8_0), "0" the LDS-staged kernels below.
@@ -217,7 +242,7 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
       else if (e[0] == '0') ns = false;
     }
     if (std::getenv("RLXQ_SKINNY_XR") && !std::getenv("RLXQ_SKINNY_NS")) ns = false;
-    if (ns) return skinny_ns_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, nmt, nnt, nd, sb);
+    if (ns) return run_ns(nmt, nnt, nd);
   }
   {
     int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = 2, xd = m <= 16 ? 4 : (m <= 32 ? 3 : 2);
@@ -227,10 +252,10 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
     if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
       int a1, a2, a3;
       if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) xmt = a1, xnt = a2, xd = a3;
-      else if (e[0] == '0')   // (Q4_K, Q6_K and the MLX formats have no LDS-staged kernel)
-        xr = scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K || mlx;
+      else if (e[0] == '0')   // (Q4_K, Q6_K, the MLX formats and f32 activations have no LDS-staged kernel)
+        xr = scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K || mlx || f32x;
     }
-    if (xr) return skinny_xr_dispatch(ctx, scheme, x, x_dtype, w, rb, m, k, n, y, y_dtype, stream, xmt, xnt, xd, sb);
+    if (xr) return run_xr(xmt, xnt, xd);
   }
   const int MT = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
   // blocks per thread per step (K per step = 64 * BPT); 2 measured fastest,

@@ -353,6 +353,43 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
     if (whole) epi(put, std::false_type{});
     else epi(put, std::true_type{});
   };
+  if constexpr (F16) {
+    if (a.pairs) {
+      // hi/lo rows of f32 activations: x16 rows 2r and 2r + 1 sit in a
+      // lane's registers r, r + 1 (r even) and add into output row r
+      // (mb and dm are even)
+      const int64_t mo_rows = a.M >> 1, mbo = mb >> 1;
+      auto epp = [&](auto put, auto checked) {
+        static_for<TM>([&](auto I) {
+          static_for<TN>([&](auto J) {
+            const f32x16_t v = acc[I.value][J.value];
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+              constexpr int dn = J.value * 32;
+              const int dm = I.value * 32 + 8 * (r / 4) + (r % 4);
+              if (!checked.value || (mb + dm < a.M && nb + dn < a.N))
+                put(dm >> 1, dn, (v[r] + v[r + 1]) * a.inv_s[mb + dm]);
+            }
+          });
+        });
+      };
+      auto epp_any = [&](auto put) {
+        if (whole) epp(put, std::false_type{});
+        else epp(put, std::true_type{});
+      };
+      if (a.splits > 1) {
+        float* p = a.part + ((int64_t)sp * mo_rows + mbo) * a.N + nb;
+        epp_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.N + dn] = o; });
+      } else if (a.y_bf16) {
+        uint16_t* p = reinterpret_cast<uint16_t*>(a.y) + mbo * a.y_ld + nb;
+        epp_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.y_ld + dn] = (uint16_t)f32_to_bf16_bits(o); });
+      } else {
+        float* p = reinterpret_cast<float*>(a.y) + mbo * a.y_ld + nb;
+        epp_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.y_ld + dn] = o; });
+      }
+      return;
+    }
+  }
   if (a.splits > 1) {
     float* p = a.part + ((int64_t)sp * a.M + mb) * a.N + nb;
     epi_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.N + dn] = o; });
@@ -398,10 +435,12 @@ RLXQ_GEMM_INST(rlxq_gemm_q2_k_t128, SCH_Q2_K)
     rlxq::gemm256_body<SCH, 2, 4, 1, false, true>(a);                                              \
   }
 // f16 weights converted once per workgroup into LDS, f16 MFMA on the prepared
-// activations (GGUF schemes): rlxq_gemm_<scheme>_t256w8[p2]f
-#define RLXQ_GEMM256F_INST(SNAME, SCH, PF, SUFFIX)                                           \
+// activations (GGUF Q8_0, Q4_0, Q4_1 and the K-quants Q4_K and Q6_K, whose
+// sub-blocks normalise to the Q4_1 and Q8_0 forms):
+// rlxq_gemm_<scheme>_t256w8[p2|l]f
+#define RLXQ_GEMM256F_INST(SNAME, SCH, PF, SUFFIX, LATE)                                     \
   extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8##SUFFIX##f(rlxq_gemm_args a) { \
-    rlxq::gemm256_body<SCH, 2, 4, PF, true>(a);                                                    \
+    rlxq::gemm256_body<SCH, 2, 4, PF, true, LATE>(a);                                              \
   }
 RLXQ_GEMM256_INST(q4_1, SCH_Q4_1)
 RLXQ_GEMM256_INST(q4_0, SCH_Q4_0)
@@ -415,6 +454,8 @@ RLXQ_GEMM256_INST(mxfp4, SCH_MXFP4)
 RLXQ_GEMM256_INST(q5_k, SCH_Q5_K)
 RLXQ_GEMM256_INST(q3_k, SCH_Q3_K)
 RLXQ_GEMM256_INST(q2_k, SCH_Q2_K)
-RLXQ_GEMM256F_INST(q4_1, SCH_Q4_1, 2, p2)
-RLXQ_GEMM256F_INST(q4_0, SCH_Q4_0, 2, p2)
-RLXQ_GEMM256F_INST(q8_0, SCH_Q8_0, 1, )
+RLXQ_GEMM256F_INST(q4_1, SCH_Q4_1, 2, p2, false)
+RLXQ_GEMM256F_INST(q4_0, SCH_Q4_0, 2, p2, false)
+RLXQ_GEMM256F_INST(q8_0, SCH_Q8_0, 1, , false)
+RLXQ_GEMM256F_INST(q4_k, SCH_Q4_K, 2, p2, false)
+RLXQ_GEMM256F_INST(q6_k, SCH_Q6_K, 1, l, true)

@@ -14,7 +14,11 @@ typedef struct rlxq_gemm_args {
   const void* biases;     /* MLX: [N, K/group], else NULL                 */
   void* y;                /* [M, N] output, leading dimension y_ld        */
   int64_t M, N, K, rb, y_ld;
-  int32_t group, sb_bf16, y_bf16, pad;
+  int32_t group, sb_bf16, y_bf16;
+  /* f16 kernels: M counts x16 rows prepared in hi/lo pairs (row 2r + 1 the
+   * remainder of row 2r); the epilogue adds each pair into output row r,
+   * and y and part hold M / 2 rows                                        */
+  int32_t pairs;
   int32_t tiles_m, tiles_n;   /* output tile grid (256 x 256 kernels)     */
   /* split-K (256 x 256 kernels): workgroup = (K slice, tile); slice sp
    * covers K [sp * kslice, (sp + 1) * kslice) and, when splits > 1, writes

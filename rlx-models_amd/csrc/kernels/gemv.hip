@@ -237,8 +237,12 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
 // of D rows of weight loads in flight.
 // ---------------------------------------------------------------------------
 
-template <int SCH, int NU, int D, int WAVES, bool XLDS, int MT = 1>
+// F32X: one row of f32 activations, held as two bf16 rows, the rounded row
+// (hi) and what the rounding left over (lo), so that the pairs keep ~16
+// significant bits of each element; both rows' sums add into the one output.
+template <int SCH, int NU, int D, int WAVES, bool XLDS, int MT = 1, bool F32X = false>
 RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
+  static_assert(!F32X || (MT == 2 && XLDS), "f32 activations: hi and lo rows through LDS");
   constexpr int BLOCKS = Unit<SCH>::BLOCKS;
   constexpr int DW = Unit<SCH>::DW;
   constexpr int BYTES = Unit<SCH>::BYTES;
@@ -309,22 +313,61 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;
     constexpr bool LINEAR = MLX || MX || SCH == SCH_Q4_K;   // half h = elements 16h..16h+15
     uint4 xa[MT][XH], xc[MT][XH];
-#pragma unroll
-    for (int m = 0; m < MT; m++) {
-      const uint16_t* xg = reinterpret_cast<const uint16_t*>(a.x) + (int64_t)(m < a.M ? m : 0) * K;
+    if constexpr (F32X) {
+      // the half-block's 16 f32 elements, split after the first weight
+      // requests: hi = bf16(v), lo = bf16(v - hi)
+      const float* xg = reinterpret_cast<const float*>(a.x);
+      float4 fr[XH][4];
 #pragma unroll
       for (int i = 0; i < XH; i++) {
         const int hb = threadIdx.x + NT * i, b = hb >> 1, h = hb & 1;
-        xa[m][i] = xc[m][i] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int q = 0; q < 4; q++) fr[i][q] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (hb < 2 * bpr) {
-          const uint16_t* p = xg + (int64_t)b * 32;
-          xa[m][i] = *reinterpret_cast<const uint4*>(p + (LINEAR ? 16 * h : 8 * h));
-          xc[m][i] = *reinterpret_cast<const uint4*>(p + (LINEAR ? 16 * h + 8 : 16 + 8 * h));
+          const float* p = xg + (int64_t)b * 32;
+          const int o0 = LINEAR ? 16 * h : 8 * h, o1 = LINEAR ? 16 * h + 8 : 16 + 8 * h;
+          fr[i][0] = *reinterpret_cast<const float4*>(p + o0);
+          fr[i][1] = *reinterpret_cast<const float4*>(p + o0 + 4);
+          fr[i][2] = *reinterpret_cast<const float4*>(p + o1);
+          fr[i][3] = *reinterpret_cast<const float4*>(p + o1 + 4);
         }
       }
-    }
 #pragma unroll
-    for (int i = 0; i < D; i++) load(n0 + (i < cnt ? i : cnt - 1) * G, ring[i]);
+      for (int i = 0; i < D; i++) load(n0 + (i < cnt ? i : cnt - 1) * G, ring[i]);
+      auto split8 = [](float4 u, float4 v, uint4& hi, uint4& lo) {
+        const float e[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+        uint32_t h[8], l[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          h[q] = f32_to_bf16_bits(e[q]);
+          l[q] = f32_to_bf16_bits(e[q] - bf16_bits_to_f32(h[q]));
+        }
+        hi = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+        lo = make_uint4(l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16));
+      };
+#pragma unroll
+      for (int i = 0; i < XH; i++) {
+        split8(fr[i][0], fr[i][1], xa[0][i], xa[1][i]);
+        split8(fr[i][2], fr[i][3], xc[0][i], xc[1][i]);
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        const uint16_t* xg = reinterpret_cast<const uint16_t*>(a.x) + (int64_t)(m < a.M ? m : 0) * K;
+#pragma unroll
+        for (int i = 0; i < XH; i++) {
+          const int hb = threadIdx.x + NT * i, b = hb >> 1, h = hb & 1;
+          xa[m][i] = xc[m][i] = make_uint4(0u, 0u, 0u, 0u);
+          if (hb < 2 * bpr) {
+            const uint16_t* p = xg + (int64_t)b * 32;
+            xa[m][i] = *reinterpret_cast<const uint4*>(p + (LINEAR ? 16 * h : 8 * h));
+            xc[m][i] = *reinterpret_cast<const uint4*>(p + (LINEAR ? 16 * h + 8 : 16 + 8 * h));
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < D; i++) load(n0 + (i < cnt ? i : cnt - 1) * G, ring[i]);
+    }
 #pragma unroll
     for (int m = 0; m < MT; m++) {
       uint32_t* xs = xlds + (size_t)m * bpr * 17;
@@ -475,13 +518,22 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
           if constexpr (HAS_MIN) acc[m] = fmaf(mn, S[m][c][bl], acc[m]);
         }
       }
-#pragma unroll
-    for (int m = 0; m < MT; m++) {
-      const float v = lane_group_sum<64>(acc[m]);
-      if (lane == 0 && yrow >= 0 && m < a.M) {
-        const int64_t off = (yrow + m) * a.y_ld + n;
+    if constexpr (F32X) {
+      const float v = lane_group_sum<64>(acc[0] + acc[1]);
+      if (lane == 0 && yrow >= 0) {
+        const int64_t off = yrow * a.y_ld + n;
         if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v * ysc);
         else reinterpret_cast<float*>(a.y)[off] = v * ysc;
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        const float v = lane_group_sum<64>(acc[m]);
+        if (lane == 0 && yrow >= 0 && m < a.M) {
+          const int64_t off = (yrow + m) * a.y_ld + n;
+          if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v * ysc);
+          else reinterpret_cast<float*>(a.y)[off] = v * ysc;
+        }
       }
     }
   };
@@ -606,7 +658,23 @@ RLXQ_GEMVXS_Q4K
   RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8_M2, SCH, 2, 2, 8, 2)      \
   RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D1_W8_M4, SCH, 2, 1, 8, 4)      \
   RLXQ_GEMVXSM_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8_M4, SCH, 2, 2, 8, 4)
+// one row of f32 activations as hi and lo bf16 rows: rlxq_gemvxs_<scheme>_U<NU>_D<D>_W<W>_F
+#define RLXQ_GEMVXSF_INST(NAME, SCH, NU, D, W)                                        \
+  extern "C" __global__ __launch_bounds__(64 * W) void NAME(rlxq_gemv_args a) {      \
+    rlxq::gemv_xr_body<SCH, NU, D, W, true, 2, true>(a);                              \
+  }
+#define RLXQ_GEMVXSF_SCHEME(SNAME, SCH)                                       \
+  RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U1_D2_W8_F, SCH, 1, 2, 8)          \
+  RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U2_D2_W4_F, SCH, 2, 2, 4)          \
+  RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U2_D1_W4_F, SCH, 2, 1, 4)          \
+  RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U3_D1_W8_F, SCH, 3, 1, 8)          \
+  RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U4_D1_W8_F, SCH, 4, 1, 8)
 #if RLXQ_PART_IS(1)
+RLXQ_GEMVXSF_SCHEME(q4_1, SCH_Q4_1)
+RLXQ_GEMVXSF_SCHEME(mlx4, SCH_MLX4)
+RLXQ_GEMVXSF_SCHEME(mxfp4, SCH_MXFP4)
+RLXQ_GEMVXSF_INST(rlxq_gemvxs_q4_k_U1_D2_W8_F, SCH_Q4_K, 1, 2, 8)
+RLXQ_GEMVXSF_INST(rlxq_gemvxs_q4_k_U2_D1_W8_F, SCH_Q4_K, 2, 1, 8)
 RLXQ_GEMVXSM_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXSM_SCHEME(mlx4, SCH_MLX4)
 RLXQ_GEMVXSM_SCHEME(mxfp4, SCH_MXFP4)

@@ -33,6 +33,36 @@ namespace rlxq {
 
 constexpr int SK_BN = 128;          // weight rows per workgroup
 
+// Stores the sums of 16-row MFMA tiles (row chunk from x16 row m0, column
+// tiles from n0): C[i][j] of a tile sits in lane j + 16 (i / 4), register
+// i % 4, scaled by the row's inv_s, to the split's partial sums or to y.
+// With pairs the x16 rows 2r and 2r + 1 (a lane's registers 0, 1 and 2, 3)
+// are added into output row r.
+template <int MT, int NT>
+RLXQ_DEV void sk_store(const rlxq_skinny_args& a, const f32x4_t (&acc)[MT][NT], int64_t m0, int64_t n0, int sp,
+                       int g, int j) {
+  const int64_t mo_rows = a.pairs ? a.M >> 1 : a.M;
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      if (a.pairs && (r & 1)) continue;
+      const int64_t m = m0 + 16 * mt + 4 * g + r;
+      if (m >= a.M) continue;
+      const int64_t mo = a.pairs ? m >> 1 : m;
+      const float is = a.inv_s[m];
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const int64_t n = n0 + 16 * t + j;
+        if (n >= a.N) continue;
+        const float v = (a.pairs ? acc[mt][t][r] + acc[mt][t][r < 3 ? r + 1 : r] : acc[mt][t][r]) * is;
+        if (a.splits > 1) a.part[((int64_t)sp * mo_rows + mo) * a.N + n] = v;
+        else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[mo * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
+        else reinterpret_cast<float*>(a.y)[mo * a.y_ld + n] = v;
+      }
+    }
+}
+
 
 // BPT blocks per thread per step: 2 threads per weight row, so a step spans
 // NB = 2 * BPT blocks (KS = 32 * NB of K) and wave w contracts blocks
@@ -185,24 +215,13 @@ RLXQ_DEV void skinny_body(const rlxq_skinny_args& a) {
   }
   __syncthreads();
   if (wv != 0) return;
-  // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
 #pragma unroll
   for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int64_t m = m0 + 16 * mt + 4 * g + r;
-      if (m >= a.M) continue;
-      const float is = a.inv_s[m];
+    for (int t = 0; t < NT; t++)
 #pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const int64_t n = n0 + 16 * t + j;
-        if (n >= a.N) continue;
-        const float v = (acc[mt][t][r] + R[((mt * NT + t) * 4 + r) * 64 + lane]) * is;
-        if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
-        else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
-        else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
-      }
-    }
+      for (int r = 0; r < 4; r++) acc[mt][t][r] += R[((mt * NT + t) * 4 + r) * 64 + lane];
+  sk_store<MT, NT>(a, acc, m0, n0, sp, g, j);
 }
 
 // Q4_1 with the weight and activation tiles copied global -> LDS by the
@@ -349,20 +368,10 @@ RLXQ_DEV void skinny_dma_body(const rlxq_skinny_args& a) {
 #pragma unroll
   for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int64_t m = m0 + 16 * mt + 4 * g + r;
-      if (m >= a.M) continue;
-      const float is = a.inv_s[m];
+    for (int t = 0; t < NT; t++)
 #pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const int64_t n = n0 + 16 * t + j;
-        if (n >= a.N) continue;
-        const float v = (acc[mt][t][r] + R[((mt * NT + t) * 4 + r) * 64 + lane]) * is;
-        if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
-        else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
-        else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
-      }
-    }
+      for (int r = 0; r < 4; r++) acc[mt][t][r] += R[((mt * NT + t) * 4 + r) * 64 + lane];
+  sk_store<MT, NT>(a, acc, m0, n0, sp, g, j);
 }
 
 // ---------------------------------------------------------------------------
@@ -537,24 +546,7 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
   if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.Mp, m0, a.w, a.rb, a.K, kb, ke, wrow, wok, acc, a.scales, a.biases,
                                       a.group, a.sb_bf16))
     return;
-  // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int64_t m = m0 + 16 * mt + 4 * g + r;
-      if (m >= a.M) continue;
-      const float is = a.inv_s[m];
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const int64_t n = n0 + 16 * t + j;
-        if (n >= a.N) continue;
-        const float v = acc[mt][t][r] * is;
-        if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
-        else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
-        else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
-      }
-    }
+  sk_store<MT, NT>(a, acc, m0, n0, sp, g, j);
 }
 
 // ---------------------------------------------------------------------------
@@ -740,24 +732,7 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
   for (int d = 0; d < D; d++)
     if (s0 + d < nsteps) step(s0 + d, d);
 
-  // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int64_t m = m0 + 16 * mt + 4 * g + r;
-      if (m >= a.M) continue;
-      const float is = a.inv_s[m];
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const int64_t n = n0 + 16 * t + j;
-        if (n >= a.N) continue;
-        const float v = acc[mt][t][r] * is;
-        if (a.splits > 1) a.part[((int64_t)sp * a.M + m) * a.N + n] = v;
-        else if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
-        else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
-      }
-    }
+  sk_store<MT, NT>(a, acc, m0, n0, sp, g, j);
 }
 
 }  // namespace rlxq
@@ -766,15 +741,20 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
 // fragment-major layout); each thread owns whole 32-element blocks (held in
 // registers, so the permutation is local): blocks t, t + 256, t + 512
 // (K <= 24576 keeps a row in registers; longer rows are read twice).
+// With split, x16 rows 2r and 2r + 1 (two workgroups, which find the same
+// row maximum and scale) hold the f16 (bf16) rounding of row r's scaled
+// elements and the remainder of that rounding.
 extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a) {
   constexpr int RB = 3;   // register-resident blocks per thread
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
+  const int64_t lr = a.split ? r >> 1 : r;   // logical row (entry) of x16 row r
+  const bool lo_part = a.split && (r & 1);
   const int64_t nblk = a.K >> 5;
   const int t = threadIdx.x;
-  const int32_t ent = a.rmap ? (r < a.Mp ? a.rmap[r] : -1) : 0;
-  const int64_t src = a.rmap ? (int64_t)(ent >= 0 ? ent : 0) / a.rdiv : r;   // x row of x16 row r
-  if (a.rmap ? ent < 0 : r >= a.M) {
+  const int32_t ent = a.rmap ? (r < a.Mp ? a.rmap[lr] : -1) : 0;
+  const int64_t src = a.rmap ? (int64_t)(ent >= 0 ? ent : 0) / a.rdiv : lr;   // x row of x16 row r
+  if (a.rmap ? ent < 0 : lr >= a.M) {
     // padding rows of the fragment-major layout: zeros
     if (!a.frag_major || r >= a.Mp) return;
     uint4* dst = reinterpret_cast<uint4*>(a.x16);
@@ -840,9 +820,16 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
     uint32_t o[16];
 #pragma unroll
     for (int p = 0; p < 32; p += 2) {
-      const float w0 = w[rlxq::perm_k(p, nib)] * s, w1 = w[rlxq::perm_k(p + 1, nib)] * s;
-      const uint32_t h0 = a.out_bf16 ? f32_to_bf16_bits(w0) : f32_to_f16_bits(w0);
-      const uint32_t h1 = a.out_bf16 ? f32_to_bf16_bits(w1) : f32_to_f16_bits(w1);
+      float w0 = w[rlxq::perm_k(p, nib)] * s, w1 = w[rlxq::perm_k(p + 1, nib)] * s;
+      uint32_t h0 = a.out_bf16 ? f32_to_bf16_bits(w0) : f32_to_f16_bits(w0);
+      uint32_t h1 = a.out_bf16 ? f32_to_bf16_bits(w1) : f32_to_f16_bits(w1);
+      if (lo_part) {
+        // the remainder w - hi is exact in f32; rounded once more
+        w0 -= a.out_bf16 ? bf16_bits_to_f32(h0) : f16_bits_to_f32(h0);
+        w1 -= a.out_bf16 ? bf16_bits_to_f32(h1) : f16_bits_to_f32(h1);
+        h0 = a.out_bf16 ? f32_to_bf16_bits(w0) : f32_to_f16_bits(w0);
+        h1 = a.out_bf16 ? f32_to_bf16_bits(w1) : f32_to_f16_bits(w1);
+      }
       o[p / 2] = h0 | (h1 << 16);
     }
     if (a.frag_major) {

@@ -23,6 +23,12 @@ typedef struct rlxq_x16_args {
    * a zero row where rmap[r] < 0; NULL: x16 row r is x row r             */
   const int32_t* rmap;
   int32_t out_bf16;       /* x16 holds bf16 (MXFP4's bf16 MFMA), not f16  */
+  /* split: f32 rows in two parts, x16 row 2r the rounded row r (hi) and row
+   * 2r + 1 what that rounding left over (lo, on the same scale), so that
+   * hi + lo carries ~22 (f16) or ~16 (bf16) significant bits of each f32
+   * element; M counts the rows of x (and rmap its entries), Mp the x16
+   * rows (>= 2 M)                                                          */
+  int32_t split;
 } rlxq_x16_args;
 
 typedef struct rlxq_skinny_args {
@@ -42,6 +48,10 @@ typedef struct rlxq_skinny_args {
   const void* biases;
   int64_t group;
   int32_t sb_bf16;
+  /* pairs: M counts x16 rows prepared with split (row 2r hi, 2r + 1 lo of
+   * output row r); the epilogue adds each pair, and y and part hold M / 2
+   * rows                                                                  */
+  int32_t pairs;
 } rlxq_skinny_args;
 
 #endif

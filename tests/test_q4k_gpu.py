@@ -150,13 +150,17 @@ def test_q4k_prefill_gemm(ctx, orc, monkeypatch, mkn, tile):
     assert rel_err(got, want) <= 2e-2
 
 
-def test_q4k_f32_output_prefill_stays_on_gemv(ctx, orc):
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+def test_q4k_f32_output_prefill_on_f16_gemm(ctx, orc, xdt):
+    """f32 output past 256 rows takes the f16 GEMM (sub-blocks normalised to
+    the Q4_1 form, d*sc and -dmin*mn rounded to f16 once), within the 1e-3
+    bar; f32 activations as hi/lo row pairs."""
     m, k, n = 300, 1024, 200
     rng = np.random.default_rng(5)
     packed = orc.synth_q4_k(rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
-    got, want = _run(ctx, orc, x, packed, n)
-    assert ctx.last_kernel.startswith("rlxq_gemv_q4_k_"), ctx.last_kernel
+    got, want = _run(ctx, orc, x, packed, n, xdt=xdt)
+    assert ctx.last_kernel == "rlxq_gemm_q4_k_t256w8p2f", ctx.last_kernel
     assert rel_err(got, want) <= TOL
 
 

@@ -1,7 +1,8 @@
 """Parity of the batched-decode (small M) dequant-GEMM against the CPU oracle,
 through the C ABI: f16 weights (one rounding of d*q + m) and bf16 activations
 (exact in f16 after power-of-two row scaling) on f16 MFMA with fp32
-accumulation.  f32 activations stay on the GEMV (see test_f32_activations_stay_exact).  Bar: max|got - want| / max|want| <= 1e-3 (f32 output), 1e-2
+accumulation.  f32 activations run as hi + lo f16 row pairs (see
+test_f32_activations_take_the_skinny_kernels and tests/test_f32_contract_gpu.py).  Bar: max|got - want| / max|want| <= 1e-3 (f32 output), 1e-2
 (bf16 output), `want` the oracle's dequantized weights contracted in float64."""
 import numpy as np
 import pytest
@@ -112,13 +113,18 @@ def test_skinny_every_register_variant(ctx, orc, monkeypatch, cfg):
         assert rel_err(got, want) <= TOL_F32, (cfg, m, k, n)
 
 
-def test_f32_activations_stay_exact(ctx, orc, monkeypatch):
-    """f32 activations are not routed to the f16 kernel: the dispatcher keeps
-    them on the GEMV, whose products are exact."""
+def test_f32_activations_take_the_skinny_kernels(ctx, orc, monkeypatch):
+    """f32 activations (the reference's operand type) run on the f16 kernels
+    as hi and lo row pairs by default; RLXQ_DECODE=gemv keeps them on the
+    GEMV, whose products are exact."""
     monkeypatch.delenv("RLXQ_DECODE", raising=False)
     rng = np.random.default_rng(3)
     packed = orc.synth_q4_1(rng, 256, 1024)
     x = rng.standard_normal((32, 1024)).astype(np.float32)
+    got, want = run_dense(ctx, orc, 3, x, packed, 256)
+    assert ctx.last_kernel.startswith("rlxq_skinnyns_q4_1_"), ctx.last_kernel
+    assert rel_err(got, want) <= TOL_F32
+    monkeypatch.setenv("RLXQ_DECODE", "gemv")
     got, want = run_dense(ctx, orc, 3, x, packed, 256)
     assert ctx.last_kernel.startswith("rlxq_gemv"), ctx.last_kernel
     assert rel_err(got, want) <= TOL_F32
