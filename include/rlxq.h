@@ -25,9 +25,13 @@
  *     (the library's scratch is kept per stream).
  *   - Scratch: some paths (batched decode, split-K, MoE routing, W8A8) use
  *     device scratch that the context allocates per stream and grows on
- *     demand.  A buffer replaced by growth is kept until
- *     rlxq_release_stream or rlxq_destroy, so a HIP graph captured earlier
- *     stays valid.  A call under stream capture must not need growth (the
+ *     demand, by at least half its size each time (so the buffers growth
+ *     replaces total less than twice the live one).  A replaced buffer that
+ *     was never used under stream capture is freed by a later call on the
+ *     stream once the work queued before its replacement has finished; one
+ *     that was used under capture is kept until rlxq_release_stream or
+ *     rlxq_destroy, so a HIP graph captured earlier stays valid.  A call
+ *     under stream capture must not need growth (the
  *     allocation fails under global capture): size the stream's scratch
  *     first with rlxq_reserve_workspace, or run the call once uncaptured.
  *     The MoE combine fused into the down launch (when selected) also
@@ -147,6 +151,8 @@ const char* rlxq_version(void);
  * streams (per-request streams, torch's stream pool). */
 int rlxq_reserve_workspace(rlxq_ctx* ctx, void* stream, size_t bytes);
 int64_t rlxq_workspace_bytes(const rlxq_ctx* ctx, void* stream);
+/* Bytes of replaced scratch buffers the stream still holds (not yet freed). */
+int64_t rlxq_workspace_retired_bytes(const rlxq_ctx* ctx, void* stream);
 int rlxq_release_stream(rlxq_ctx* ctx, void* stream);
 
 /* Dense DequantMatMul: y[m, n] = sum_k x[m, k] * dequant(W)[n, k].

@@ -441,10 +441,14 @@ int read_config(rlxq_mlx* h, const std::string& dir) {
   JsonParser jp(text.data(), text.size());
   if (!jp.parse(root) || root.kind != Json::OBJ)
     return h->fail(RLXQ_E_FORMAT, "mlx: " + path + " is not a JSON object (" + jp.error() + ")");
+  // Only an mlx-lm `quantization` object holding bits or group_size marks
+  // an MLX-quantized checkpoint (dir_is_mlx_quant,
+  // crates/rlx-models-core/src/weight_registry.rs:27-41); GPTQ / AWQ / fp8
+  // `quantization_config` blocks belong to the plain safetensors path, so
+  // without the marker every tensor is read as stored.
   const Json* q = root.get("quantization");
-  if (!q) q = root.get("quantization_config");
-  if (!q) return RLXQ_OK;
-  if (q->kind != Json::OBJ || !parse_quant(*q, h->quant))
+  if (!q || q->kind != Json::OBJ || (!q->get("bits") && !q->get("group_size"))) return RLXQ_OK;
+  if (!parse_quant(*q, h->quant))
     return h->fail(RLXQ_E_FORMAT, "mlx: " + path + ": quantization needs integer group_size and bits");
   for (const auto& kv : q->obj) {
     if (kv.second.kind == Json::OBJ) {

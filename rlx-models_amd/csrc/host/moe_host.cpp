@@ -220,7 +220,8 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
   const size_t cmap_bytes = sk ? r256((size_t)(1 + sk_mp / rpc) * 4) : 0, emap_bytes = sk ? r256((size_t)sk_mp * 4) : 0;
   const size_t x16_bytes = sk ? r256((size_t)sk_mp * k * 2) : 0, is_bytes = sk ? r256((size_t)sk_mp * 4) : 0;
-  const size_t total_ws = table_bytes + tmp_bytes + cmap_bytes + emap_bytes + x16_bytes + is_bytes;
+  const size_t sum_bytes = sk ? r256((size_t)sk_mp * (k / 32) * 4) : 0;   // block sums of the gathered rows
+  const size_t total_ws = table_bytes + tmp_bytes + cmap_bytes + emap_bytes + x16_bytes + is_bytes + sum_bytes;
   void* ws = nullptr;
   if (total_ws && (rc = workspace(ctx, total_ws, &ws, stream))) return rc;
   int32_t* table = fused ? nullptr : static_cast<int32_t*>(ws);
@@ -264,6 +265,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     xa.x = x;
     xa.x16 = reinterpret_cast<uint16_t*>(skb + cmap_bytes + emap_bytes);
     xa.inv_s = reinterpret_cast<float*>(skb + cmap_bytes + emap_bytes + x16_bytes);
+    xa.ssum = reinterpret_cast<float*>(skb + cmap_bytes + emap_bytes + x16_bytes + is_bytes);
     xa.M = sk_mp;
     xa.K = k;
     xa.Mp = sk_mp;
@@ -273,6 +275,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     xa.rdiv = x_div;
     xa.rmap = pa.emap;
     xa.out_bf16 = scheme == RLXQ_MLX_MXFP4 ? 1 : 0;
+    xa.post_exp = sk_post_exp(scheme);
     hipFunction_t fx;
     if ((rc = get_fn(ctx, "rlxq_x16_prep", &fx))) return rc;
     void* xargs[] = {&xa};
@@ -291,6 +294,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     std::memset(&ka, 0, sizeof ka);
     ka.x16 = xa.x16;
     ka.inv_s = xa.inv_s;
+    ka.ssum = xa.ssum;
     ka.cmap = pa.cmap;
     ka.emap = pa.emap;
     ka.bank = static_cast<const uint8_t*>(bank);

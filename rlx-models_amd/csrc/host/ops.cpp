@@ -158,16 +158,15 @@ int check_weights(rlxq_ctx* ctx, const char* what, int scheme, int group, const 
   return fail(ctx, RLXQ_E_SCHEME, std::string(what) + ": unsupported scheme " + std::to_string(scheme));
 }
 
-// Schemes with an f16 variant of the prefill GEMM (f16 weights d*q + m
-// rounded once, MFMA on the prepared f16 activations): the GGUF legacy
-// blocks and the K-quants whose sub-blocks normalise to their forms.
-bool has_f16_gemm(int scheme) {
-  return is_gguf(scheme) || scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K;
-}
+// Schemes with the exact f32-output variant of the prefill GEMM (each
+// weight's f32 value as f16 hi + lo, f16 MFMA on prepared activations):
+// every format but MXFP4, whose E8M0-scaled codes are exact in bf16 and take
+// the bf16 kernels.
+bool has_exact_gemm(int scheme) { return scheme != RLXQ_MLX_MXFP4; }
 
-// Prefill dequant-GEMM launch (tilings and split-K below).  f32 activations
-// take the f16 variant with each row prepared as a hi and a lo x16 row (the
-// epilogue adds the pair).
+// Prefill dequant-GEMM launch (tilings and split-K below).  f32 output or
+// f32 activations take the exact variant; f32 activations are prepared as a
+// hi and a lo f16 row per row (the epilogue adds the pair).
 int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dtype, const void* w,
                   const void* scales, const void* biases, int sb_dtype, int64_t rb, int64_t m, int64_t k, int64_t n,
                   void* y, int y_dtype, void* stream) {
@@ -176,35 +175,39 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // Q6_K with its LDS stores after the step's MFMAs, which measured 15%
   // faster for it and slower for the others).  When the tiles do not cover the CUs, K is split so that they do
   // (at most 8 slices of at least 8 K steps) and the slices' f32 partial sums
-  // are added in slice order.  RLXQ_GEMM_TILE=128|256|256w8|256w8l|256w8p2|...f
+  // are added in slice order.  RLXQ_GEMM_TILE=128|256|256w8|256w8l|256w8p2|...x
   // forces a tiling (the 128 x 128 one never splits); RLXQ_GEMM_SPLITS=<n>
   // forces the slice count.
   const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   int tile = 256;
   const bool one_stage = scheme == RLXQ_GGUF_Q6_K || scheme == RLXQ_GGUF_Q3_K;
   const char* var = scheme == RLXQ_GGUF_Q6_K ? "w8l" : (one_stage ? "w8" : "w8p2");
-  const bool bit8 = scheme == RLXQ_GGUF_Q8_0;   // (its f16 variant keeps one stage)
   const char* te = std::getenv("RLXQ_GEMM_TILE");
   if (te) {
     tile = std::atoi(te) == 128 ? 128 : 256;
     var = tile == 128 ? "" : (std::strncmp(te, "256w8", 5) == 0 ? te + 3 : "");
   }
-  // f32 output (or f32 activations): the f16 variant of the 256 tiles,
-  // whose f16 weights keep the output within 1e-3 (bf16 weights do not)
-  const bool has_f16 = has_f16_gemm(scheme);
+  // f32 output or f32 activations: the exact variant (bf16 weights, or f16
+  // weights rounded once, do not keep 1e-3 on structured data).  Its
+  // register stages: one for the raw blocks of Q8_0, Q5_K, Q3_K (and Q6_K,
+  // late stores), two for the others.
   const bool split = x_dtype == RLXQ_F32;
-  if (!te && (y_dtype == RLXQ_F32 || split) && has_f16)
-    var = bit8 ? "w8f" : (scheme == RLXQ_GGUF_Q6_K ? "w8lf" : "w8p2f");
+  const bool want_exact = split || y_dtype == RLXQ_F32;
+  if (!te && want_exact && has_exact_gemm(scheme))
+    var = scheme == RLXQ_GGUF_Q6_K ? "w8lx"
+          : (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q5_K || scheme == RLXQ_GGUF_Q3_K) ? "w8x"
+                                                                                               : "w8p2x";
   const bool w8 = tile == 256 && var[0] == 'w';
-  // "...f": f16 weights and MFMA on the prepared f16 activations
   const size_t vl = std::strlen(var);
-  const bool f16 = vl > 0 && var[vl - 1] == 'f';
-  if (f16 && !has_f16)
-    return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: the f16 GEMM serves Q8_0, Q4_0, Q4_1, Q4_K and Q6_K");
-  if (split && !f16) return fail(ctx, RLXQ_E_DTYPE, "dequant_matmul: f32 activations need an f16 GEMM variant");
-  // x16 rows: two per output row (hi, lo) for f32 activations
+  const bool exact = vl > 0 && var[vl - 1] == 'x';
+  if (exact && !has_exact_gemm(scheme))
+    return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: MXFP4 has no exact f16 GEMM variant");
+  if (split && !exact) return fail(ctx, RLXQ_E_DTYPE, "dequant_matmul: f32 activations need the exact GEMM variant");
+  // x16 rows: two per output row (hi, lo) for f32 activations; the exact
+  // variant's tiles cover 128 output columns (hi and lo weight rows)
   const int64_t mr = split ? 2 * m : m;
-  const int64_t tiles_m = (mr + tile - 1) / tile, tiles_n = (n + tile - 1) / tile;
+  const int64_t tn_cols = exact ? tile / 2 : tile;
+  const int64_t tiles_m = (mr + tile - 1) / tile, tiles_n = (n + tn_cols - 1) / tn_cols;
   if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
   const int64_t tiles = tiles_m * tiles_n, ksteps = k / 64;
   int64_t splits = 1;
@@ -224,10 +227,12 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   a.x = x;
   const size_t part_bytes = splits > 1 ? (((size_t)(splits * m * n) * 4 + 255) & ~(size_t)255) : 0;
   char* part = nullptr;
-  if (f16) {
+  if (exact) {
+    // prepared f16 activations in natural order (the exact variant's weights
+    // are in natural order); MLX's 2^8 weight factor undone in the row factors
     rlxq_x16_args xa;
-    if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &part, stream, false, 0, false,
-                       split)))
+    if ((rc = prep_x16(ctx, x, x_dtype, m, k, 0, part_bytes, xa, &part, stream, false, 0, false, split,
+                       sk_post_exp(scheme))))
       return rc;
     a.x = xa.x16;
     a.inv_s = xa.inv_s;
@@ -296,21 +301,22 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
                       scheme == RLXQ_GGUF_Q5_K) ? 2 : 1;
   const int64_t units = (k / 32) / blocks;
 
-  // Prefill: bf16 activations and bf16 output with at least 64 rows go to the
-  // MFMA dequant-GEMM (weights rounded to bf16 in LDS, fp32 accumulation);
-  // GGUF with f32 output past the batched-decode sizes (more than 256 rows)
-  // to its f16 variant, which meets the 1e-3 bar.  Everything else stays on the
-  // GEMV family, which keeps the products exact.
+  // Prefill routing.  bf16 activations and bf16 output from 64 rows: the
+  // bf16 GEMM (weights rounded to bf16, the 2e-2 prefill bar).  f32 output
+  // past 256 rows, or f32 activations (the reference's operand type) from 64
+  // rows with bf16 output: the exact variant (f16 hi + lo weights; f32
+  // activations as hi + lo rows).  MXFP4 with E8M0 scales and bf16
+  // activations is exact on the bf16 GEMM for f32 output too; MXFP4 with f32
+  // activations or bf16 scales stays on the GEMV for f32 output.
   // RLXQ_PREFILL=gemv|gemm forces one of them where both apply (tests).
-  // f32 activations (the reference's operand type) take the same MFMA
-  // kernels as hi + lo pairs of f16 (bf16 for MXFP4) rows, on schemes with an
-  // f16 GEMM variant (Q8_0, Q4_0, Q4_1, Q4_K, Q6_K); MLX, MXFP4 and the other
-  // K-quants keep f32 output (and f32 activations) on the GEMV family, whose
-  // weights are not rounded.
   {
-    const bool f16_gemm = has_f16_gemm(scheme);
-    const bool gemm_ok = (xbf || f16_gemm) && k % 64 == 0 && m >= 1;
-    bool use_gemm = gemm_ok && ((y_dtype == RLXQ_BF16 && m >= 64) || (f16_gemm && m > 256));
+    const bool mx_exact_bf16 = scheme == RLXQ_MLX_MXFP4 && sb_dtype == RLXQ_U8 && xbf;
+    const bool gemm_ok = k % 64 == 0 && (xbf || has_exact_gemm(scheme));
+    bool use_gemm;
+    if (xbf && y_dtype == RLXQ_BF16) use_gemm = m >= 64;
+    else if (y_dtype == RLXQ_BF16) use_gemm = m >= 64;                 // f32 x: exact variant
+    else use_gemm = m > 256 && (has_exact_gemm(scheme) || mx_exact_bf16);
+    use_gemm = use_gemm && gemm_ok;
     if (const char* e = std::getenv("RLXQ_PREFILL")) {
       if (!std::strcmp(e, "gemv")) use_gemm = false;
       if (!std::strcmp(e, "gemm")) use_gemm = gemm_ok;

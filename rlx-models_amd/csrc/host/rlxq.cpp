@@ -156,14 +156,20 @@ int workspace(rlxq_ctx* ctx, size_t bytes, void** out, void* stream) {
     return RLXQ_OK;
   }
   rlxq_ctx::Scratch& w = ctx->ws[stream];
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  bool capturing = true;   // (unknown status: treat as captured, keep buffers)
+  if (hipStreamIsCapturing(hs, &st) == hipSuccess) capturing = st != hipStreamCaptureStatusNone;
+  else (void)hipGetLastError();
+  if (!capturing) reclaim_retired(w);
   if (bytes <= w.bytes) {
+    w.captured = w.captured || capturing;
     *out = w.p;
     return RLXQ_OK;
   }
-  // The buffer being replaced may still be read by queued work or named by a
-  // captured graph: keep it until the stream is released or the context
-  // destroyed.  Nothing waits here.
+  // Geometric growth: an ascending run of sizes replaces O(log) buffers.
   size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  if (want < w.bytes + w.bytes / 2) want = w.bytes + w.bytes / 2;
   want = (want + 4095) & ~size_t(4095);
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, want);
@@ -173,11 +179,49 @@ int workspace(rlxq_ctx* ctx, size_t bytes, void** out, void* stream) {
                 "workspace: hipMalloc(" + std::to_string(want) + "): " + hip_msg(e) +
                     " (under stream capture, size the scratch first with rlxq_reserve_workspace)");
   }
-  if (w.p) w.retired.push_back(w.p);
+  // The buffer being replaced may still be read by queued work: an event
+  // behind that work frees it later.  One that a captured graph may name is
+  // kept until the stream is released.  Nothing waits here.
+  if (w.p) {
+    rlxq_ctx::Retired r{w.p, w.bytes, nullptr};
+    if (!w.captured && !capturing) {
+      hipEvent_t ev = nullptr;
+      if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess) {
+        if (hipEventRecord(ev, hs) == hipSuccess) r.done = ev;
+        else (void)hipEventDestroy(ev);
+      }
+      (void)hipGetLastError();
+    }
+    w.retired.push_back(r);
+  }
   w.p = p;
   w.bytes = want;
+  w.captured = capturing;
   *out = w.p;
   return RLXQ_OK;
+}
+
+void reclaim_retired(rlxq_ctx::Scratch& w) {
+  size_t keep = 0;
+  for (size_t i = 0; i < w.retired.size(); i++) {
+    rlxq_ctx::Retired& r = w.retired[i];
+    if (r.done && hipEventQuery(r.done) == hipSuccess) {
+      (void)hipFree(r.p);
+      (void)hipEventDestroy(r.done);
+      continue;
+    }
+    (void)hipGetLastError();   // (hipErrorNotReady)
+    w.retired[keep++] = r;
+  }
+  w.retired.resize(keep);
+}
+
+void free_retired(rlxq_ctx::Scratch& w) {
+  for (rlxq_ctx::Retired& r : w.retired) {
+    (void)hipFree(r.p);
+    if (r.done) (void)hipEventDestroy(r.done);
+  }
+  w.retired.clear();
 }
 
 int zeroed_counters(rlxq_ctx* ctx, void* stream, int32_t** out) {
@@ -313,7 +357,7 @@ int rlxq_destroy(rlxq_ctx* ctx) {
     for (auto& kv : ctx->ws) {
       if (kv.second.p) (void)hipFree(kv.second.p);
       if (kv.second.counters) (void)hipFree(kv.second.counters);
-      for (void* p : kv.second.retired) (void)hipFree(p);
+      free_retired(kv.second);
     }
     for (hipModule_t m : ctx->modules) (void)hipModuleUnload(m);
   }
@@ -338,6 +382,15 @@ int64_t rlxq_workspace_bytes(const rlxq_ctx* ctx, void* stream) {
   return it == ctx->ws.end() ? 0 : (int64_t)it->second.bytes;
 }
 
+int64_t rlxq_workspace_retired_bytes(const rlxq_ctx* ctx, void* stream) {
+  if (!ctx) return RLXQ_E_NULL;
+  auto it = ctx->ws.find(stream);
+  if (it == ctx->ws.end()) return 0;
+  int64_t t = 0;
+  for (const rlxq_ctx::Retired& r : it->second.retired) t += (int64_t)r.bytes;
+  return t;
+}
+
 int rlxq_release_stream(rlxq_ctx* ctx, void* stream) {
   if (!ctx) return RLXQ_E_NULL;
   ctx->last_error.clear();
@@ -350,7 +403,7 @@ int rlxq_release_stream(rlxq_ctx* ctx, void* stream) {
   if (e != hipSuccess) return fail(ctx, RLXQ_E_HIP, "release_stream: sync: " + hip_msg(e));
   if (it->second.p) (void)hipFree(it->second.p);
   if (it->second.counters) (void)hipFree(it->second.counters);
-  for (void* p : it->second.retired) (void)hipFree(p);
+  free_retired(it->second);
   ctx->ws.erase(it);
   return RLXQ_OK;
 }

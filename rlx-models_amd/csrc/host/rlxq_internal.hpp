@@ -21,14 +21,23 @@ struct rlxq_ctx {
   size_t max_lds = 65536;
   // Library-owned scratch (routing tables, quantised activations, split-K
   // partials), one buffer per stream so that calls on different streams can
-  // overlap.  Grown on demand.  A buffer that growth replaces is never freed
-  // while the context lives (a HIP graph captured earlier may still name it):
-  // it moves to `retired` and is freed by rlxq_release_stream or
-  // rlxq_destroy.
+  // overlap.  Grown on demand, by at least half its size each time, so the
+  // buffers growth replaces add up to less than twice the live one.  A
+  // replaced buffer moves to `retired`: if it was never handed out under
+  // stream capture, with an event recorded behind the stream's queued work,
+  // and it is freed once that event has completed (checked on later calls);
+  // if a captured graph may name it (done == nullptr), it is kept until
+  // rlxq_release_stream or rlxq_destroy.
+  struct Retired {
+    void* p;
+    size_t bytes;
+    hipEvent_t done;
+  };
   struct Scratch {
     void* p = nullptr;
     size_t bytes = 0;
-    std::vector<void*> retired;
+    bool captured = false;   // p was handed out while the stream was capturing
+    std::vector<Retired> retired;
     // kCounterSlots int32 counters, zeroed when allocated; kernels that take
     // them leave them at zero (the fused MoE combine)
     int32_t* counters = nullptr;
@@ -81,6 +90,10 @@ int launch(rlxq_ctx* ctx, hipFunction_t fn, dim3 grid, dim3 block, size_t lds, v
 // Ensures at least `bytes` of context scratch for `stream`; returns its
 // device pointer.
 int workspace(rlxq_ctx* ctx, size_t bytes, void** out, void* stream);
+// Frees the stream's retired buffers whose completion event has passed
+// (reclaim), or all of them (free, after the stream has been synchronised).
+void reclaim_retired(rlxq_ctx::Scratch& w);
+void free_retired(rlxq_ctx::Scratch& w);
 // The stream's zeroed counters (rlxq_ctx::kCounterSlots), allocated and
 // cleared on the stream at first use (not under stream capture).
 int zeroed_counters(rlxq_ctx* ctx, void* stream, int32_t** out);
@@ -127,7 +140,10 @@ int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream);
 // lo (2m rows; f32 activations keep ~22 significant bits), with a factor each.
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, int order, size_t extra,
              rlxq_x16_args& xa, char** rest, void* stream, bool frag_major = false, int64_t mp = 0,
-             bool out_bf16 = false, bool split = false);
+             bool out_bf16 = false, bool split = false, int post_exp = 0);
+// Exponent of the extra row factor the f16-MFMA kernels need for a scheme:
+// -8 for MLX affine (their f16 weights are prescaled by 2^8), else 0.
+int sk_post_exp(int scheme);
 int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
                     int64_t k, int64_t n, void* y, int y_dtype, void* stream, const SkinnySb& sb = SkinnySb());
 int i8b_dispatch(rlxq_ctx* ctx, int group, const void* x, int x_dtype, const void* w, const void* scales,

@@ -30,13 +30,16 @@ int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream) {
 }
 
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, int order, size_t extra,
-             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major, int64_t mp, bool out_bf16, bool split) {
+             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major, int64_t mp, bool out_bf16, bool split,
+             int post_exp) {
   const int64_t rows = split ? 2 * m : m;   // x16 rows that hold data
   if (!frag_major || mp < rows) mp = rows;
+  // fragment-major: the block sums (one f32 per 32 elements) after inv_s
   const size_t x16_bytes = round256((size_t)(mp * k) * 2), s_bytes = round256((size_t)rows * 4);
+  const size_t sum_bytes = frag_major ? round256((size_t)(mp * (k / 32)) * 4) : 0;
   void* ws = nullptr;
   int rc;
-  if ((rc = workspace(ctx, x16_bytes + s_bytes + extra, &ws, stream))) return rc;
+  if ((rc = workspace(ctx, x16_bytes + s_bytes + sum_bytes + extra, &ws, stream))) return rc;
   char* wsb = static_cast<char*>(ws);
   std::memset(&xa, 0, sizeof xa);
   xa.x = x;
@@ -50,7 +53,9 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, in
   xa.frag_major = frag_major ? 1 : 0;
   xa.out_bf16 = out_bf16 ? 1 : 0;
   xa.split = split ? 1 : 0;
-  *rest = wsb + x16_bytes + s_bytes;
+  xa.post_exp = post_exp;
+  xa.ssum = frag_major ? reinterpret_cast<float*>(wsb + x16_bytes + s_bytes) : nullptr;
+  *rest = wsb + x16_bytes + s_bytes + sum_bytes;
   hipFunction_t fn;
   if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
   void* xargs[] = {&xa};
@@ -84,12 +89,13 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   int rc;
   const int64_t mp = mch * 16 * MT;
   if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp,
-                     scheme == RLXQ_MLX_MXFP4, split)))
+                     scheme == RLXQ_MLX_MXFP4, split, sk_post_exp(scheme))))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
   a.x16 = xa.x16;
   a.inv_s = xa.inv_s;
+  a.ssum = xa.ssum;
   a.w = static_cast<const uint8_t*>(w);
   a.part = part_bytes ? reinterpret_cast<float*>(rest) : nullptr;
   a.y = y;
@@ -148,12 +154,13 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   int rc;
   const int64_t mp = mch * 16 * MT;
   if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp,
-                     scheme == RLXQ_MLX_MXFP4, split)))
+                     scheme == RLXQ_MLX_MXFP4, split, sk_post_exp(scheme))))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
   a.x16 = xa.x16;
   a.inv_s = xa.inv_s;
+  a.ssum = xa.ssum;
   a.w = static_cast<const uint8_t*>(w);
   a.part = part_bytes ? reinterpret_cast<float*>(rest) : nullptr;
   a.y = y;
@@ -188,6 +195,8 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   return rc;
 }
 }  // namespace
+
+int sk_post_exp(int scheme) { return (scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_AFFINE8) ? -8 : 0; }
 
 int sk_order(int scheme) {
   if (scheme == RLXQ_MLX_AFFINE4) return 2;
@@ -226,8 +235,8 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
     return skinny_ns_dispatch(ctx, scheme, x, x_dtype, w, rb, m_out, k, n, y, y_dtype, stream, MT, NT, D, sb);
   };
   // The register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR="MT,NT,D"
-  // picks a compiled one (every combination for Q4_1, the defaults for Q4_0
-  // and Q8_0), "0" the LDS-staged kernels below.
+  // picks a compiled one (every combination for Q4_1, the defaults for the
+  // other formats).
   // The N-split kernel (activations shared through LDS): Q4_1 (and Q4_K) past 16 rows,
   // where it measured 5-13% faster than the register-streamed one (at 16 rows
   // and below, and for Q8_0, it was slower).  RLXQ_SKINNY_NS="MT,NT,D" picks
@@ -244,97 +253,14 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
     if (std::getenv("RLXQ_SKINNY_XR") && !std::getenv("RLXQ_SKINNY_NS")) ns = false;
     if (ns) return run_ns(nmt, nnt, nd);
   }
-  {
-    int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = 2, xd = m <= 16 ? 4 : (m <= 32 ? 3 : 2);
-    if (scheme == RLXQ_GGUF_Q4_K) xd = m <= 16 ? 3 : 2;   // its 13-dword raw blocks
-    if (scheme == RLXQ_GGUF_Q6_K) xd = m <= 32 ? 2 : 1;   // its 22-dword raw blocks
-    bool xr = true;
-    if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
-      int a1, a2, a3;
-      if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) xmt = a1, xnt = a2, xd = a3;
-      else if (e[0] == '0')   // (Q4_K, Q6_K, the MLX formats and f32 activations have no LDS-staged kernel)
-        xr = scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K || mlx || f32x;
-    }
-    if (xr) return run_xr(xmt, xnt, xd);
+  int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = 2, xd = m <= 16 ? 4 : (m <= 32 ? 3 : 2);
+  if (scheme == RLXQ_GGUF_Q4_K) xd = m <= 16 ? 3 : 2;   // its 13-dword raw blocks
+  if (scheme == RLXQ_GGUF_Q6_K) xd = m <= 32 ? 2 : 1;   // its 22-dword raw blocks
+  if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
+    int a1, a2, a3;
+    if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) xmt = a1, xnt = a2, xd = a3;
   }
-  const int MT = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
-  // blocks per thread per step (K per step = 64 * BPT); 2 measured fastest,
-  // RLXQ_SKINNY_BPT selects another compiled one (2 or 8 for MT <= 2, 2 or 4
-  // for MT = 4)
-  int BPT = 2;
-  if (const char* e = std::getenv("RLXQ_SKINNY_BPT")) BPT = std::atoi(e);
-  if (k % (64 * BPT)) BPT = 2;
-  // Q4_1, up to 16 rows, K % 256 == 0: the LDS-DMA ring variant (measured
-  // faster there; RLXQ_SKINNY_DMA=0|1 forces it off or on where it applies)
-  bool dma = scheme == RLXQ_GGUF_Q4_1 && k % 256 == 0 && MT == 1;
-  if (const char* e = std::getenv("RLXQ_SKINNY_DMA"))
-    dma = scheme == RLXQ_GGUF_Q4_1 && k % 256 == 0 && std::atoi(e) != 0;
-  const int64_t KS = dma ? 256 : 64 * BPT;
-  const int64_t MC = 16 * MT;
-  const int64_t tiles_n = (n + 127) / 128, mch = (m + MC - 1) / MC;
-  const int64_t ksteps = k / KS;
-  const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-  int64_t target = cus;
-  if (const char* e = std::getenv("RLXQ_SKINNY_WGS")) target = cus * std::atoi(e);
-  int64_t splits = 1;
-  while (tiles_n * mch * splits < target && splits * 2 <= ksteps && splits < 32) splits *= 2;
-  const int64_t kslice = ((ksteps + splits - 1) / splits) * KS;
-  splits = (k + kslice - 1) / kslice;
-  if (tiles_n * mch * splits > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: batched-decode grid");
-
-  const size_t x16_bytes = round256((size_t)(m * k) * 2), s_bytes = round256((size_t)m * 4);
-  const size_t part_bytes = splits > 1 ? round256((size_t)(splits * m * n) * 4) : 0;
-  void* ws = nullptr;
-  int rc;
-  if ((rc = workspace(ctx, x16_bytes + s_bytes + part_bytes, &ws, stream))) return rc;
-  char* wsb = static_cast<char*>(ws);
-
-  rlxq_x16_args xa;
-  std::memset(&xa, 0, sizeof xa);
-  xa.x = x;
-  xa.x16 = reinterpret_cast<uint16_t*>(wsb);
-  xa.inv_s = reinterpret_cast<float*>(wsb + x16_bytes);
-  xa.M = m;
-  xa.K = k;
-  xa.x_bf16 = x_dtype == RLXQ_BF16;
-  xa.nibble_order = sk_order(scheme);
-  hipFunction_t fn;
-  if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
-  void* xargs[] = {&xa};
-  if ((rc = launch(ctx, fn, dim3((unsigned)m), dim3(256), 0, stream, xargs, "rlxq_x16_prep"))) return rc;
-
-  rlxq_skinny_args a;
-  std::memset(&a, 0, sizeof a);
-  a.x16 = xa.x16;
-  a.inv_s = xa.inv_s;
-  a.w = static_cast<const uint8_t*>(w);
-  a.part = part_bytes ? reinterpret_cast<float*>(wsb + x16_bytes + s_bytes) : nullptr;
-  a.y = y;
-  a.M = m;
-  a.N = n;
-  a.K = k;
-  a.rb = rb;
-  a.y_ld = n;
-  a.kslice = (int32_t)kslice;
-  a.splits = (int32_t)splits;
-  a.tiles_n = (int32_t)tiles_n;
-  a.y_bf16 = y_dtype == RLXQ_BF16;
-  char name[48];
-  if (dma) std::snprintf(name, sizeof name, "rlxq_skinny_q4_1_mt%d_dma", MT);
-  else std::snprintf(name, sizeof name, "rlxq_skinny_%s_mt%d_b%d", scheme_name(scheme), MT, BPT);
-  if ((rc = get_fn(ctx, name, &fn))) return rc;
-  const int rdw = 2 * BPT * (scheme == RLXQ_GGUF_Q8_0 ? 9 : 5) + 2;
-  const size_t stage = dma ? 3 * (128 * 160 + (size_t)MC * 512)
-                           : 128 * (size_t)rdw * 4 + (size_t)MC * (KS + 8) * 2;
-  const size_t red = 2 * (size_t)(MT * 8 * 4) * 64 * 4;
-  const size_t lds = stage > red ? stage : red;
-  void* args[] = {&a};
-  if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name))) return rc;
-  if (splits > 1) {
-    rc = splits_reduce(ctx, a, stream);
-    if (!rc) ctx->last_kernel = name;
-  }
-  return rc;
+  return run_xr(xmt, xnt, xd);
 }
 
 }  // namespace rlxq

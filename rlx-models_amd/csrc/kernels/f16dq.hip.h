@@ -30,20 +30,46 @@ RLXQ_DEV int perm_k(int p, int order) {
 }
 
 
-// Normalised block: scale dword (Q4_1, Q4_K, MLX4: d | m << 16, else d) +
-// code dwords.  A Q4_K sub-block normalises to the Q4_1 form: d = d * sc and
-// m = -dmin * mn rounded to f16, and code dword g holding elements 4g..4g+3
-// (low nibbles) and 16 + 4g.. (high nibbles) of the sub-block.
-// An MXFP4 block: its f32 scale (a power of two) and its four code words.
-// An MLX4 (MLX8) block: the group's f32 scale and bias rounded to f16 (the
-// f16 range covers the scales of real weight slabs; scales below 2^-14 lose
-// bits as f16 subnormals) and its four (eight) code words as they are; MLX8's
-// codes, four per word LSB first, unpack in natural order.
-// A Q6_K block normalises to the int8 form of Q8_0 with one f16 scale per
-// 16 weights: scale dword d0 | d1 << 16 (d * sc of the two halves, rounded
-// to f16) and code bytes code + 96, so that code - 32 = byte - 128 as for
-// Q8_0's sign-flipped bytes; its activations stay in natural order.
-template <int SCH> constexpr int sk_bdw() { return (SCH == SCH_Q8_0 || SCH == SCH_Q6_K || SCH == SCH_MLX8) ? 9 : 5; }
+// Normalised block: scale dwords, then the code dwords (sk_cw<SCH>() of them
+// from o[sk_hdr<SCH>()]).  The weights are carried exactly by two f16 MFMA
+// operands per 8 codes (sk_b2): b1 = q * dh rounded to f16 and
+// b2 = fma(q, dh, -b1) [+ q * dl], with q the code (minus its offset) exact in
+// f16.  Since q is an integer of at most 8 bits and dh an f16, q * dh - b1 is
+// a multiple of dh's quantum below b1's rounding step, so b2 holds it exactly
+// (TwoProduct); dl, where present, is the f16 remainder of a scale that f16
+// does not hold (the K-quants' d * sc, MLX's f32 scales), rounded once at
+// ~2^-22 of the weight.  The min / bias term m * sum(x) of a block is carried
+// by one more MFMA per step on the prepared block sums (sk_mb), with m as
+// f16 hi + lo.
+//   Q4_1:  o[0] = d | m << 16 (the stored f16s), codes o[1..4]
+//   Q4_0:  o[0] = d, codes o[1..4] (q - 8 through the -1032 offset)
+//   Q8_0:  o[0] = d, codes o[1..8] (sign-flipped bytes, -1152 offset)
+//   Q4_K:  o[0] = dh | dl << 16 of d * sc, o[1] = mh | ml << 16 of
+//          -dmin * mn, codes o[2..5] in the Q4_1 nibble arrangement
+//   Q6_K:  o[0] = dh0 | dh1 << 16, o[1] = dl0 | dl1 << 16 (d * sc of the two
+//          16-weight halves), codes o[2..9] as code + 96 bytes (so that
+//          code - 32 = byte - 128, the Q8_0 form)
+//   MLX4 / MLX8: o[0] = sh | sl << 16 of 2^8 * scale, o[1] = bh | bl << 16 of
+//          2^8 * bias, codes o[2..5] / o[2..9] as stored (the 2^8 keeps small
+//          group scales normal in f16; the activation preparation folds 2^-8
+//          into the row factors)
+//   MXFP4: o[0] = the f32 scale (a power of two), codes o[1..4]; its E2M1
+//          codes times the scale are exact in bf16 (one bf16 operand)
+constexpr float MLX_PRESCALE = 256.f;   // 2^8; undone through post_exp = -8
+
+template <int SCH> constexpr int sk_hdr() {
+  return (SCH == SCH_Q4_K || SCH == SCH_Q6_K || SCH == SCH_MLX4 || SCH == SCH_MLX8) ? 2 : 1;
+}
+template <int SCH> constexpr int sk_cw() { return (SCH == SCH_Q8_0 || SCH == SCH_Q6_K || SCH == SCH_MLX8) ? 8 : 4; }
+template <int SCH> constexpr int sk_bdw() { return sk_hdr<SCH>() + sk_cw<SCH>(); }
+// formats with a min / bias term (m * block sum)
+template <int SCH> constexpr bool sk_has_m() {
+  return SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SCH == SCH_MLX4 || SCH == SCH_MLX8;
+}
+// formats with a second scale half dl
+template <int SCH> constexpr bool sk_has_dl() {
+  return SCH == SCH_Q4_K || SCH == SCH_Q6_K || SCH == SCH_MLX4 || SCH == SCH_MLX8;
+}
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
 // 6:4, lgkmcnt 11:8): wait on one counter, leave the others unconstrained.
@@ -57,119 +83,149 @@ RLXQ_DEV uint32_t as_u(f16x2_t v) { return __builtin_bit_cast(uint32_t, v); }
 RLXQ_DEV f16x2_t magic_lo(uint32_t u) { return as_h2(perm_b32(0x64646464u, u, 0x04010400u)); }
 RLXQ_DEV f16x2_t magic_hi(uint32_t u) { return as_h2(perm_b32(0x64646464u, u, 0x04030402u)); }
 
-// The lane's B operand: 8 f16 weights of one block of one row, positions
-// 8g .. 8g + 7.  `bp` points at the normalised block.
+// f32 -> f16 hi | f16 lo << 16 with hi + lo ~ v to ~2^-22.
+RLXQ_DEV uint32_t f16_split(float v) {
+  const uint32_t h = f32_to_f16_bits(v);
+  return h | (f32_to_f16_bits(v - f16_bits_to_f32(h)) << 16);
+}
+
+// The lane's B operands for positions 8g .. 8g + 7 of a block: the codes as
+// exact f16 values q (four pairs), then b1 = q * dh, b2 = fma(q, dh, -b1)
+// [+ q * dl].  `bp` points at the normalised block.
 template <int SCH>
-RLXQ_DEV f16x8_t dequant_lane(const uint32_t* bp, int g) {
-  const uint32_t dm = bp[0];
-  const f16x2_t d2 = as_h2(perm_b32(dm, dm, 0x01000100u));
-  f16x2_t w[4];
-  if constexpr (SCH == SCH_MLX8) {
-    // unsigned codes in natural order: d*q + m with one rounding
-    const uint32_t u0 = bp[1 + 2 * g], u1 = bp[2 + 2 * g];
-    const f16x2_t m2 = as_h2(perm_b32(dm, dm, 0x03020302u));
-    const f16x2_t off = {(_Float16)-1024.f, (_Float16)-1024.f};
-    w[0] = __builtin_elementwise_fma(magic_lo(u0) + off, d2, m2);
-    w[1] = __builtin_elementwise_fma(magic_hi(u0) + off, d2, m2);
-    w[2] = __builtin_elementwise_fma(magic_lo(u1) + off, d2, m2);
-    w[3] = __builtin_elementwise_fma(magic_hi(u1) + off, d2, m2);
-  } else if constexpr (SCH == SCH_Q8_0 || SCH == SCH_Q6_K) {
+RLXQ_DEV void sk_b2(const uint32_t* bp, int g, f16x8_t& b1, f16x8_t& b2) {
+  constexpr int H = sk_hdr<SCH>();
+  f16x2_t q[4];
+  if constexpr (SCH == SCH_Q8_0 || SCH == SCH_Q6_K || SCH == SCH_MLX8) {
+    // bytes: Q8_0 sign-flipped (byte ^ 0x80 = code + 128), Q6_K code + 96
+    // (= (code - 32) + 128), MLX8 the unsigned code
     const uint32_t flip = SCH == SCH_Q8_0 ? 0x80808080u : 0u;
-    const uint32_t u0 = bp[1 + 2 * g] ^ flip, u1 = bp[2 + 2 * g] ^ flip;
-    // (Q6_K: positions 8g.. lie in half g / 2 of the block)
-    const f16x2_t dd = SCH == SCH_Q6_K ? as_h2(perm_b32(dm, dm, g < 2 ? 0x01000100u : 0x03020302u)) : d2;
-    const f16x2_t off = {(_Float16)-1152.f, (_Float16)-1152.f};
-    w[0] = (magic_lo(u0) + off) * dd;
-    w[1] = (magic_hi(u0) + off) * dd;
-    w[2] = (magic_lo(u1) + off) * dd;
-    w[3] = (magic_hi(u1) + off) * dd;
+    const uint32_t u0 = bp[H + 2 * g] ^ flip, u1 = bp[H + 1 + 2 * g] ^ flip;
+    const _Float16 off = SCH == SCH_MLX8 ? (_Float16)-1024.f : (_Float16)-1152.f;
+    const f16x2_t o2 = {off, off};
+    q[0] = magic_lo(u0) + o2;
+    q[1] = magic_hi(u0) + o2;
+    q[2] = magic_lo(u1) + o2;
+    q[3] = magic_hi(u1) + o2;
   } else {
-    const uint32_t qs = bp[1 + g];
+    const uint32_t qs = bp[H + g];
     const uint32_t lo = qs & 0x0F0F0F0Fu, hi = (qs >> 4) & 0x0F0F0F0Fu;
-    if constexpr (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SCH == SCH_MLX4) {
-      const f16x2_t m2 = as_h2(perm_b32(dm, dm, 0x03020302u));
-      const f16x2_t off = {(_Float16)-1024.f, (_Float16)-1024.f};
-      w[0] = __builtin_elementwise_fma(magic_lo(lo) + off, d2, m2);
-      w[1] = __builtin_elementwise_fma(magic_hi(lo) + off, d2, m2);
-      w[2] = __builtin_elementwise_fma(magic_lo(hi) + off, d2, m2);
-      w[3] = __builtin_elementwise_fma(magic_hi(hi) + off, d2, m2);
-    } else {
-      const f16x2_t off = {(_Float16)-1032.f, (_Float16)-1032.f};
-      w[0] = (magic_lo(lo) + off) * d2;
-      w[1] = (magic_hi(lo) + off) * d2;
-      w[2] = (magic_lo(hi) + off) * d2;
-      w[3] = (magic_hi(hi) + off) * d2;
-    }
+    const _Float16 off = SCH == SCH_Q4_0 ? (_Float16)-1032.f : (_Float16)-1024.f;
+    const f16x2_t o2 = {off, off};
+    q[0] = magic_lo(lo) + o2;
+    q[1] = magic_hi(lo) + o2;
+    q[2] = magic_lo(hi) + o2;
+    q[3] = magic_hi(hi) + o2;
   }
-  return f16x8_t{w[0].x, w[0].y, w[1].x, w[1].y, w[2].x, w[2].y, w[3].x, w[3].y};
+  // (Q6_K: positions 8g.. lie in half g / 2 of the block)
+  const uint32_t sel = (SCH == SCH_Q6_K && g >= 2) ? 0x03020302u : 0x01000100u;
+  const f16x2_t dh = as_h2(perm_b32(bp[0], bp[0], SCH == SCH_Q6_K ? sel : 0x01000100u));
+  f16x2_t w1[4], w2[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    w1[i] = q[i] * dh;
+    w2[i] = __builtin_elementwise_fma(q[i], dh, -w1[i]);
+  }
+  if constexpr (sk_has_dl<SCH>()) {
+    const uint32_t dlw = SCH == SCH_Q6_K ? bp[1] : bp[0];
+    const uint32_t dsel = SCH == SCH_Q6_K ? sel : 0x03020302u;
+    const f16x2_t dl = as_h2(perm_b32(dlw, dlw, dsel));
+#pragma unroll
+    for (int i = 0; i < 4; i++) w2[i] = __builtin_elementwise_fma(q[i], dl, w2[i]);
+  }
+  b1 = f16x8_t{w1[0].x, w1[0].y, w1[1].x, w1[1].y, w1[2].x, w1[2].y, w1[3].x, w1[3].y};
+  b2 = f16x8_t{w2[0].x, w2[0].y, w2[1].x, w2[1].y, w2[2].x, w2[2].y, w2[3].x, w2[3].y};
 }
 
-// The B operand of one MFMA step and the step itself.  MXFP4 takes bf16
-// MFMA: E2M1 codes times an E8M0 scale (a power of two) are exact in bf16
-// (v_cvt_scalef32_pk_bf16_fp4, one per code pair), as are the bf16
-// activations scaled by a power of two, and its codes unpack in natural
-// order.  The other formats take f16 MFMA with dequant_lane's weights.
-template <int SCH> struct SkOp { typedef f16x8_t type; };
-template <> struct SkOp<SCH_MXFP4> { typedef bf16x8_t type; };
-
+// The B operand of the block's min / bias term: K slots 0, 1, 2 of the lane
+// hold m hi, m hi, m lo (the A operand holds the block sum's hi, lo, hi), so
+// one MFMA adds (S hi + S lo) * m hi + S hi * m lo.
 template <int SCH>
-RLXQ_DEV typename SkOp<SCH>::type sk_b(const uint32_t* bp, int g) {
+RLXQ_DEV f16x8_t sk_mb(const uint32_t* bp) {
+  uint32_t mw;
+  if constexpr (SCH == SCH_Q4_1) mw = bp[0] >> 16;   // the stored f16 m (lo 0)
+  else mw = bp[1];
+  const _Float16 mh = __builtin_bit_cast(_Float16, (uint16_t)(mw & 0xffffu));
+  const _Float16 ml = __builtin_bit_cast(_Float16, (uint16_t)(mw >> 16));
+  const _Float16 z = (_Float16)0.f;
+  return f16x8_t{mh, mh, ml, z, z, z, z, z};
+}
+
+// The A operand of the min / bias term from a block sum (f32).
+RLXQ_DEV f16x8_t sk_ma(float s) {
+  const uint32_t hs = f32_to_f16_bits(s);
+  const _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)hs);
+  const _Float16 l = (_Float16)(s - f16_bits_to_f32(hs));
+  const _Float16 z = (_Float16)0.f;
+  return f16x8_t{h, l, h, z, z, z, z, z};
+}
+
+// MXFP4's single bf16 operand: E2M1 codes times an E8M0 scale (a power of
+// two) are exact in bf16 (v_cvt_scalef32_pk_bf16_fp4, one per code pair), as
+// are the bf16 activations scaled by a power of two; natural code order.
+RLXQ_DEV bf16x8_t sk_b_mxfp4(const uint32_t* bp, int g) {
+  const float sc = __uint_as_float(bp[0]);
+  const uint32_t q = bp[1 + g];
+  const u32x4_t b = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 0)),
+                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 1)),
+                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 2)),
+                     __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 3))};
+  return __builtin_bit_cast(bf16x8_t, b);
+}
+
+// One MFMA step of a normalised block: A (the activation fragment) times the
+// block's weights at positions 8g .. 8g + 7 into acc.
+template <int SCH>
+RLXQ_DEV f32x4_t sk_step(f16x8_t a, const uint32_t* bp, int g, f32x4_t acc) {
   if constexpr (SCH == SCH_MXFP4) {
-    const float sc = __uint_as_float(bp[0]);
-    const uint32_t q = bp[1 + g];
-    const u32x4_t b = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 0)),
-                       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 1)),
-                       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 2)),
-                       __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, sc, 3))};
-    return __builtin_bit_cast(bf16x8_t, b);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), sk_b_mxfp4(bp, g), acc, 0, 0, 0);
   } else {
-    return dequant_lane<SCH>(bp, g);
+    f16x8_t b1, b2;
+    sk_b2<SCH>(bp, g, b1, b2);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b1, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b2, acc, 0, 0, 0);
   }
-}
-
-template <int SCH>
-RLXQ_DEV f32x4_t sk_mfma(f16x8_t a, typename SkOp<SCH>::type b, f32x4_t c) {
-  if constexpr (SCH == SCH_MXFP4)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), b, c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // Raw block -> normalised dwords.
 template <int SCH>
 RLXQ_DEV void normalise(const RawBlk<SCH>& r, uint32_t* o) {
   if constexpr (SCH == SCH_Q6_K) {
+    // d * sc is exact in f32 (11 + 8 bits)
     const float d = f16_bits_to_f32(r.d);
-    const float ds0 = d * (float)(int8_t)(r.sc & 0xffu), ds1 = d * (float)(int8_t)(r.sc >> 8);
-    o[0] = f32_to_f16_bits(ds0) | (f32_to_f16_bits(ds1) << 16);
-    const uint32_t s1 = 4u * (r.q >> 1), s2 = 2u * r.q;
+    const uint32_t s0 = f16_split(d * (float)(int8_t)(r.sc & 0xffu)), s1 = f16_split(d * (float)(int8_t)(r.sc >> 8));
+    o[0] = (s0 & 0xffffu) | (s1 << 16);
+    o[1] = (s0 >> 16) | (s1 & 0xffff0000u);
+    const uint32_t sh1 = 4u * (r.q >> 1), sh2 = 2u * r.q;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const uint32_t l = align_bytes(r.ql[i + 1], r.ql[i], r.off), hq = align_bytes(r.qh[i + 1], r.qh[i], r.off);
       // code (0..63) + 96 per byte: no carry between bytes
-      o[1 + i] = (((l >> s1) & 0x0F0F0F0Fu) | (((hq >> s2) & 0x03030303u) << 4)) + 0x60606060u;
+      o[2 + i] = (((l >> sh1) & 0x0F0F0F0Fu) | (((hq >> sh2) & 0x03030303u) << 4)) + 0x60606060u;
     }
   } else if constexpr (SCH == SCH_Q4_K) {
+    // d * sc and dmin * mn are exact in f32 (11 + 6 bits)
     const uint32_t hd[4] = {r.hd.x, r.hd.y, r.hd.z, r.hd.w};
     float sc, mn;
     q4k_scale_min(hd, (int)r.sub, sc, mn);
-    const uint32_t d1 = f32_to_f16_bits(f16_bits_to_f32(hd[0] & 0xffffu) * sc);
-    const uint32_t m1 = f32_to_f16_bits(-(f16_bits_to_f32(hd[0] >> 16) * mn));
-    o[0] = d1 | (m1 << 16);
+    o[0] = f16_split(f16_bits_to_f32(hd[0] & 0xffffu) * sc);
+    o[1] = f16_split(-(f16_bits_to_f32(hd[0] >> 16) * mn));
     const uint32_t qs[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
     const uint32_t sh = 4 * (r.sub & 1u);
 #pragma unroll
-    for (int g = 0; g < 4; g++) o[1 + g] = ((qs[g] >> sh) & 0x0F0F0F0Fu) | (((qs[4 + g] >> sh) & 0x0F0F0F0Fu) << 4);
+    for (int g = 0; g < 4; g++) o[2 + g] = ((qs[g] >> sh) & 0x0F0F0F0Fu) | (((qs[4 + g] >> sh) & 0x0F0F0F0Fu) << 4);
   } else if constexpr (SCH == SCH_MXFP4) {
     o[0] = __float_as_uint(r.s);
     o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;
   } else if constexpr (SCH == SCH_MLX4) {
-    o[0] = f32_to_f16_bits(r.s) | (f32_to_f16_bits(r.b) << 16);
-    o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;
+    o[0] = f16_split(r.s * MLX_PRESCALE);
+    o[1] = f16_split(r.b * MLX_PRESCALE);
+    o[2] = r.q.x; o[3] = r.q.y; o[4] = r.q.z; o[5] = r.q.w;
   } else if constexpr (SCH == SCH_MLX8) {
-    o[0] = f32_to_f16_bits(r.s) | (f32_to_f16_bits(r.b) << 16);
-    o[1] = r.q0.x; o[2] = r.q0.y; o[3] = r.q0.z; o[4] = r.q0.w;
-    o[5] = r.q1.x; o[6] = r.q1.y; o[7] = r.q1.z; o[8] = r.q1.w;
+    o[0] = f16_split(r.s * MLX_PRESCALE);
+    o[1] = f16_split(r.b * MLX_PRESCALE);
+    o[2] = r.q0.x; o[3] = r.q0.y; o[4] = r.q0.z; o[5] = r.q0.w;
+    o[6] = r.q1.x; o[7] = r.q1.y; o[8] = r.q1.z; o[9] = r.q1.w;
   } else if constexpr (SCH == SCH_Q4_1) {
     o[0] = r.h;
     o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;

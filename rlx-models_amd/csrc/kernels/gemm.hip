@@ -146,9 +146,20 @@ RLXQ_DEV void gemm_body(const rlxq_gemm_args& a) {
 // MFMAs.  The loop body has no branches (row bounds are clamped addresses plus
 // selects), and the next step's LDS stores and conversions sit between the
 // MFMA groups of the current step.
-template <int SCH, int WGM, int WGN, int PF, bool F16, bool LATE = false>
+// EXACT (f16 MFMA, f32 output at the 1e-3 bar on any data): each weight's
+// f32 value, computed with the CPU decoder's arithmetic, is held as an f16
+// hi and lo half in adjacent B rows (B rows 2c, 2c + 1: real column c, so a
+// tile covers 128 real columns); the MFMA then contracts both and the
+// epilogue adds lanes 2c and 2c + 1.  With f16 weights rounded once instead,
+// structured data (the reference's sin / cos parity inputs at K = 1792)
+// already reaches 1.4e-3.  MLX weights are held times 2^8 (undone through
+// the activation row factors) so that small group scales stay normal f16.
+template <int SCH, int WGM, int WGN, int PF, bool F16, bool LATE = false, bool EXACT = false>
 RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
+  static_assert(EXACT == F16, "f16 MFMA runs the exact variant on the prepared f16 activations");
   constexpr int BM = 256, BN = 256;
+  constexpr int NREAL = EXACT ? BN / 2 : BN;   // output columns per tile
+  constexpr float WSCALE = (SCH == SCH_MLX4 || SCH == SCH_MLX8) ? 256.f : 1.f;
   constexpr int NT = 64 * WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -167,7 +178,7 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   if (!tile_of(blockIdx.x % tiles_pad, a.tiles_m, a.tiles_n, 4, tm, tn)) return;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wm = wv % WGM, wn = wv / WGM;
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * NREAL;
   const int64_t kbeg = (int64_t)sp * a.kslice;
   const int64_t kend = kbeg + a.kslice < a.K ? kbeg + a.kslice : a.K;
   const int KT = (int)((kend - kbeg) / GBK);
@@ -185,8 +196,10 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   }
   // weight tile: 256 rows x 2 blocks; thread -> row n0 + (tid & 255), blocks
   // (tid >> 8) + q * (NT / 256)
+  // (EXACT: B row brl holds half brl & 1 of real column n0 + brl / 2)
   const int brl = tid & 255;
-  const int64_t brow = n0 + brl < a.N ? n0 + brl : a.N - 1;
+  const int64_t bcol = n0 + (EXACT ? brl >> 1 : brl);
+  const int64_t brow = bcol < a.N ? bcol : a.N - 1;
 
   // Global loads run PF steps ahead of the MFMAs (PF register stages); the
   // LDS stores and conversions of the next step sit between the MFMA groups
@@ -213,12 +226,15 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   };
   auto store_b = [&](const Stage& P, int buf, int q) {
     uint16_t* dst = Bs + (buf * BN + brl) * GLD + ((tid >> 8) + q) * 32;
-    if constexpr (F16) {
-      // f16 weights d*q + m (one rounding) in the prepared activation order
-      uint32_t o[sk_bdw<SCH>()];
-      normalise<SCH>(P.b[q], o);
+    if constexpr (EXACT) {
+      uint32_t hi[16], lo[16];
+      conv_blk_f16_split<SCH>(P.b[q], WSCALE, hi, lo);
+      const bool low = brl & 1;
 #pragma unroll
-      for (int g = 0; g < 4; g++) *reinterpret_cast<f16x8_t*>(dst + 8 * g) = dequant_lane<SCH>(o, g);
+      for (int i = 0; i < 4; i++)
+        *reinterpret_cast<uint4*>(dst + 8 * i) =
+            low ? make_uint4(lo[4 * i], lo[4 * i + 1], lo[4 * i + 2], lo[4 * i + 3])
+                : make_uint4(hi[4 * i], hi[4 * i + 1], hi[4 * i + 2], hi[4 * i + 3]);
     } else {
       uint32_t o[16];
       conv_blk<SCH>(P.b[q], o);
@@ -333,6 +349,52 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   // no per-element bounds checks, branches or 64-bit multiplies (the
   // per-element form cost 8% of the kernel at M=4096).
   const int64_t mb = m0 + wm * WM + 4 * (lane >> 5);   // the lane's first row
+  if constexpr (EXACT) {
+    // B rows 2c (hi) and 2c + 1 (lo) sit in lanes j, j ^ 1 of a 32x32 tile:
+    // one DPP swap adds them (quad_perm [1, 0, 3, 2]) and the even lane
+    // stores real column c; with pairs, x16 rows 2r, 2r + 1 (a lane's
+    // registers r, r + 1) add into output row r as well.
+    const bool pr = a.pairs != 0;
+    const int64_t mo_rows = pr ? a.M >> 1 : a.M, mbo = pr ? mb >> 1 : mb;
+    const int64_t nbo = n0 + ((wn * WN + (lane & 31)) >> 1);   // real column of tile 0
+    const bool even = (lane & 1) == 0;
+    const bool whole = m0 + BM <= a.M && n0 + NREAL <= a.N;
+    auto epx = [&](auto put, auto checked) {
+      static_for<TM>([&](auto I) {
+        static_for<TN>([&](auto J) {
+          f32x16_t v = acc[I.value][J.value];
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            v[r] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[r]), 0xB1, 0xF, 0xF, true));
+          if (even) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+              if (pr && (r & 1)) continue;
+              constexpr int dn = J.value * 16;
+              const int dm = I.value * 32 + 8 * (r / 4) + (r % 4);
+              const float o = (pr ? v[r] + v[r < 15 ? r + 1 : r] : v[r]) * a.inv_s[mb + dm];
+              if (!checked.value || (mb + dm < a.M && nbo + dn < a.N)) put(pr ? dm >> 1 : dm, dn, o);
+            }
+          }
+        });
+      });
+    };
+    auto epx_any = [&](auto put) {
+      if (whole) epx(put, std::false_type{});
+      else epx(put, std::true_type{});
+    };
+    if (a.splits > 1) {
+      float* p = a.part + ((int64_t)sp * mo_rows + mbo) * a.N + nbo;
+      epx_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.N + dn] = o; });
+    } else if (a.y_bf16) {
+      uint16_t* p = reinterpret_cast<uint16_t*>(a.y) + mbo * a.y_ld + nbo;
+      epx_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.y_ld + dn] = (uint16_t)f32_to_bf16_bits(o); });
+    } else {
+      float* p = reinterpret_cast<float*>(a.y) + mbo * a.y_ld + nbo;
+      epx_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.y_ld + dn] = o; });
+    }
+    return;
+  }
   const int64_t nb = n0 + wn * WN + (lane & 31);       // its column in tile 0
   const bool whole = m0 + BM <= a.M && n0 + BN <= a.N;
   auto epi = [&](auto put, auto checked) {
@@ -344,7 +406,7 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
           constexpr int dn = J.value * 32;
           const int dm = I.value * 32 + 8 * (r / 4) + (r % 4);
           if (!checked.value || (mb + dm < a.M && nb + dn < a.N))
-            put(dm, dn, F16 ? v[r] * a.inv_s[mb + dm] : v[r]);
+            put(dm, dn, v[r]);
         }
       });
     });
@@ -353,43 +415,6 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
     if (whole) epi(put, std::false_type{});
     else epi(put, std::true_type{});
   };
-  if constexpr (F16) {
-    if (a.pairs) {
-      // hi/lo rows of f32 activations: x16 rows 2r and 2r + 1 sit in a
-      // lane's registers r, r + 1 (r even) and add into output row r
-      // (mb and dm are even)
-      const int64_t mo_rows = a.M >> 1, mbo = mb >> 1;
-      auto epp = [&](auto put, auto checked) {
-        static_for<TM>([&](auto I) {
-          static_for<TN>([&](auto J) {
-            const f32x16_t v = acc[I.value][J.value];
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-              constexpr int dn = J.value * 32;
-              const int dm = I.value * 32 + 8 * (r / 4) + (r % 4);
-              if (!checked.value || (mb + dm < a.M && nb + dn < a.N))
-                put(dm >> 1, dn, (v[r] + v[r + 1]) * a.inv_s[mb + dm]);
-            }
-          });
-        });
-      };
-      auto epp_any = [&](auto put) {
-        if (whole) epp(put, std::false_type{});
-        else epp(put, std::true_type{});
-      };
-      if (a.splits > 1) {
-        float* p = a.part + ((int64_t)sp * mo_rows + mbo) * a.N + nb;
-        epp_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.N + dn] = o; });
-      } else if (a.y_bf16) {
-        uint16_t* p = reinterpret_cast<uint16_t*>(a.y) + mbo * a.y_ld + nb;
-        epp_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.y_ld + dn] = (uint16_t)f32_to_bf16_bits(o); });
-      } else {
-        float* p = reinterpret_cast<float*>(a.y) + mbo * a.y_ld + nb;
-        epp_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.y_ld + dn] = o; });
-      }
-      return;
-    }
-  }
   if (a.splits > 1) {
     float* p = a.part + ((int64_t)sp * a.M + mb) * a.N + nb;
     epi_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.N + dn] = o; });
@@ -434,13 +459,11 @@ RLXQ_GEMM_INST(rlxq_gemm_q2_k_t128, SCH_Q2_K)
   extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8l(rlxq_gemm_args a) { \
     rlxq::gemm256_body<SCH, 2, 4, 1, false, true>(a);                                              \
   }
-// f16 weights converted once per workgroup into LDS, f16 MFMA on the prepared
-// activations (GGUF Q8_0, Q4_0, Q4_1 and the K-quants Q4_K and Q6_K, whose
-// sub-blocks normalise to the Q4_1 and Q8_0 forms):
-// rlxq_gemm_<scheme>_t256w8[p2|l]f
-#define RLXQ_GEMM256F_INST(SNAME, SCH, PF, SUFFIX, LATE)                                     \
-  extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8##SUFFIX##f(rlxq_gemm_args a) { \
-    rlxq::gemm256_body<SCH, 2, 4, PF, true, LATE>(a);                                              \
+// Exact f32-output variant (EXACT above): rlxq_gemm_<scheme>_t256w8[p2|l]x,
+// f16 MFMA on the prepared activations (natural order), f16 hi + lo weights
+#define RLXQ_GEMM256X_INST(SNAME, SCH, PF, SUFFIX, LATE)                                     \
+  extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8##SUFFIX##x(rlxq_gemm_args a) { \
+    rlxq::gemm256_body<SCH, 2, 4, PF, true, LATE, true>(a);                                        \
   }
 RLXQ_GEMM256_INST(q4_1, SCH_Q4_1)
 RLXQ_GEMM256_INST(q4_0, SCH_Q4_0)
@@ -454,8 +477,14 @@ RLXQ_GEMM256_INST(mxfp4, SCH_MXFP4)
 RLXQ_GEMM256_INST(q5_k, SCH_Q5_K)
 RLXQ_GEMM256_INST(q3_k, SCH_Q3_K)
 RLXQ_GEMM256_INST(q2_k, SCH_Q2_K)
-RLXQ_GEMM256F_INST(q4_1, SCH_Q4_1, 2, p2, false)
-RLXQ_GEMM256F_INST(q4_0, SCH_Q4_0, 2, p2, false)
-RLXQ_GEMM256F_INST(q8_0, SCH_Q8_0, 1, , false)
-RLXQ_GEMM256F_INST(q4_k, SCH_Q4_K, 2, p2, false)
-RLXQ_GEMM256F_INST(q6_k, SCH_Q6_K, 1, l, true)
+RLXQ_GEMM256X_INST(q4_1, SCH_Q4_1, 2, p2, false)
+RLXQ_GEMM256X_INST(q4_0, SCH_Q4_0, 2, p2, false)
+RLXQ_GEMM256X_INST(q8_0, SCH_Q8_0, 1, , false)
+RLXQ_GEMM256X_INST(q4_k, SCH_Q4_K, 2, p2, false)
+RLXQ_GEMM256X_INST(q6_k, SCH_Q6_K, 1, l, true)
+RLXQ_GEMM256X_INST(q5_k, SCH_Q5_K, 1, , false)
+RLXQ_GEMM256X_INST(q3_k, SCH_Q3_K, 1, , false)
+RLXQ_GEMM256X_INST(q2_k, SCH_Q2_K, 2, p2, false)
+RLXQ_GEMM256X_INST(q8_k, SCH_Q8_K, 2, p2, false)
+RLXQ_GEMM256X_INST(mlx4, SCH_MLX4, 2, p2, false)
+RLXQ_GEMM256X_INST(mlx8, SCH_MLX8, 2, p2, false)

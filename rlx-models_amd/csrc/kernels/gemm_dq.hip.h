@@ -172,6 +172,9 @@ RLXQ_DEV void load_blk(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok
   }
 }
 
+template <int SCH>
+RLXQ_DEV void blk_f32(const RawBlk<SCH>& r, float* v);
+
 // Converts a raw block into 16 dwords of bf16 pairs in natural element order:
 // f32 d*q + m (the CPU decoder's arithmetic), rounded to bf16 (nearest even).
 template <int SCH>
@@ -188,7 +191,17 @@ RLXQ_DEV void conv_blk(const RawBlk<SCH>& r, uint32_t* out) {
       out[4 * i + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q[i], r.s, 3));
     }
   } else {
-  float v[32];
+    float v[32];
+    blk_f32<SCH>(r, v);
+#pragma unroll
+    for (int i = 0; i < 16; i++) out[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+  }
+}
+
+// A raw block's 32 weights in f32, natural element order, with the CPU
+// decoder's arithmetic (d*q + m, one rounding where it has one).
+template <int SCH>
+RLXQ_DEV void blk_f32(const RawBlk<SCH>& r, float* v) {
   if constexpr (SCH == SCH_Q6_K) {
     // code = (ql >> 4 (q >> 1) & 15) | (qh >> 2q & 3) << 4 for each byte;
     // w = (d * sc) * (code - 32), computed as fma(d * sc, code, -32 (d * sc))
@@ -339,8 +352,21 @@ RLXQ_DEV void conv_blk(const RawBlk<SCH>& r, uint32_t* out) {
 #pragma unroll
       for (int e = 0; e < PER; e++) v[PER * i + e] = fmaf(r.s, (float)((wq[i] >> (BITS * e)) & ((1u << BITS) - 1u)), r.b);
   }
+}
+
+// The block's f32 weights times `scale` (a power of two) as f16 hi and lo
+// halves, natural order, two per dword: hi = f16(w), lo = f16(w - hi), so
+// that hi + lo keeps ~22 significant bits of the f32 weight.
+template <int SCH>
+RLXQ_DEV void conv_blk_f16_split(const RawBlk<SCH>& r, float scale, uint32_t* hi, uint32_t* lo) {
+  float v[32];
+  blk_f32<SCH>(r, v);
 #pragma unroll
-  for (int i = 0; i < 16; i++) out[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+  for (int i = 0; i < 16; i++) {
+    const float a = v[2 * i] * scale, b = v[2 * i + 1] * scale;
+    const uint32_t ha = f32_to_f16_bits(a), hb = f32_to_f16_bits(b);
+    hi[i] = ha | (hb << 16);
+    lo[i] = f32_to_f16_bits(a - f16_bits_to_f32(ha)) | (f32_to_f16_bits(b - f16_bits_to_f32(hb)) << 16);
   }
 }
 

@@ -626,12 +626,11 @@ RLXQ_DEV void balanced_dispatch(const rlxq_moe_gemv_args& a, Work work, After af
 // step, steps nw * RP apart).  Each entry counts once for its (token row,
 // tile); the workgroup that brings a count to top_k sums the row's entries
 // over the tile's columns in slot order and resets the count.
-// Visibility across the XCDs' L2 caches without a cache-wide write-back or
-// invalidate per workgroup: the entry rows are stored and read with
-// device-scope (write-through, coherent-level) accesses, every thread waits
-// for its stores to complete before the barrier that precedes the counts,
-// and the sum's loads are issued only after the count that completes the row
-// has returned.
+// Ordering: every thread's entry-row stores complete before the barrier
+// that precedes the counts, and the count is an agent-scope acquire-release
+// read-modify-write, so the workgroup that completes a row has seen (through
+// the release of each earlier count and the barriers) every other
+// workgroup's stores of that row before its sum's agent-scope loads.
 template <int RP>
 RLXQ_DEV void combine_tail(const rlxq_moe_gemv_args& a, const int32_t* ent, int beg, int end, int tn) {
   __shared__ int32_t done[1024];
@@ -643,8 +642,8 @@ RLXQ_DEV void combine_tail(const rlxq_moe_gemv_args& a, const int32_t* ent, int 
     for (int i = beg; i < end; i++) {
       const int r = ent[i] / a.top_k;
       int32_t* c = a.counters + (int64_t)r * a.tiles_n + tn;
-      if (atomicAdd(c, 1) == a.top_k - 1) {
-        atomicExch(c, 0);
+      if (__hip_atomic_fetch_add(c, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == a.top_k - 1) {
+        __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         done[nd++] = r;
       }
     }

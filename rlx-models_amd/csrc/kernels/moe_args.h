@@ -85,6 +85,7 @@ typedef struct rlxq_moe_sk_args {
   const void* biases;
   int64_t group;
   int32_t sb_bf16, pad2;
+  const float* ssum;      /* block sums of x16 (min / bias formats)       */
 } rlxq_moe_sk_args;
 
 #endif

@@ -1,26 +1,25 @@
 // Batched-decode dequant-GEMM for small M (the multi-row decode path):
-// y[m, n] = sum_k x[m, k] * dequant(W)[n, k] for up to 64 activation rows and
-// GGUF Q8_0 / Q4_0 / Q4_1 / Q4_K / Q6_K, MLX affine 4/8-bit and MXFP4
-// weights, streaming every weight once for all
-// rows.
+// y[m, n] = sum_k x[m, k] * dequant(W)[n, k] for up to 256 activation rows
+// (512 prepared rows) and GGUF Q8_0 / Q4_0 / Q4_1 / Q4_K / Q6_K, MLX affine
+// 4/8-bit and MXFP4 weights, streaming every weight once for all rows.
 // Replaces the backend kernel of Op::DequantMatMul at decode batch sizes
 // (crates/rlx-models-core/src/standard_decoder.rs:727-738, M rows per call).
 //
 //  * rlxq_x16_prep: each activation row to f16, scaled by a power of two so
-//    its largest element lies in [2^13, 2^14) (exact; undone in the
+//    its largest element lies in [2^9, 2^10) (exact; undone in the
 //    epilogue), and permuted within each 32-element block to the order in
 //    which a lane unpacks the codes: for the GGUF nibble formats position
 //    8g + e holds element 4g + e (e < 4) or 16 + 4g + e - 4, for MLX's
-//    element 8g + 2e (e < 4) or 8g + 2(e - 4) + 1.
-//  * rlxq_skinny_*: a workgroup takes 128 weight rows, a K split and all M
-//    rows.  Per step the raw blocks are staged in LDS (a run of blocks per
-//    thread, normalised to a dword scale word plus the code dwords) and the
-//    prepared activations next to them; wave w then contracts blocks w,
-//    w + 4, ... of the step: each lane turns its 8 codes into f16 weights with packed f16
-//    arithmetic (exact codes, then d*q + m with one rounding) as the B operand
-//    of v_mfma_f32_16x16x32_f16.  f16 weights keep the products within ~2^-12
-//    of the exact dequantised weights (bf16 weights would not meet a 1e-3
-//    output bound).  The four waves' partial sums are added in a fixed order.
+//    element 8g + 2e (e < 4) or 8g + 2(e - 4) + 1.  f32 rows become a hi and
+//    a lo row (split).  The block sums of the prepared values go beside them
+//    (the min / bias term).
+//  * rlxq_skinnyxr_* (register-streamed) and rlxq_skinnyns_* (N-split):
+//    each lane turns its 8 codes into exact f16 values and the weights into
+//    two f16 operands whose sum is the weight (f16dq.hip.h), both contracted
+//    by v_mfma_f32_16x16x32_f16 into f32; one more MFMA per 128-element
+//    chunk adds the blocks' m * sum(x).  f16 weights rounded once would be
+//    ~2^-12 off each, which structured data accumulates past a 1e-3 output
+//    bar.  MXFP4 codes are exact in bf16 and take one bf16 MFMA.
 //  * rlxq_skinny_reduce: K splits added in split order (also the prefill
 //    GEMM's split-K reduction).
 #include "common.hip.h"
@@ -64,319 +63,50 @@ RLXQ_DEV void sk_store(const rlxq_skinny_args& a, const f32x4_t (&acc)[MT][NT], 
 }
 
 
-// BPT blocks per thread per step: 2 threads per weight row, so a step spans
-// NB = 2 * BPT blocks (KS = 32 * NB of K) and wave w contracts blocks
-// w, w + 4, ...  One LDS buffer: the raw blocks of step s + 1 are in flight
-// in registers while step s is contracted from LDS.
-template <int SCH, int MT, int BPT>
-RLXQ_DEV void skinny_body(const rlxq_skinny_args& a) {
-  constexpr int NT = SK_BN / 16;   // 16-row N tiles per wave
-  constexpr int NB = 2 * BPT, KS = 32 * NB;
-  constexpr int BDW = sk_bdw<SCH>();
-  // row stride: NB blocks + 2 dwords, so that the scale and code reads of 16
-  // rows by 4 lane groups spread over the banks
-  constexpr int RDW = NB * BDW + 2;
-  constexpr int MC = 16 * MT;
-  constexpr int XST = KS + 8;                  // activation LDS row stride (f16)
-  constexpr int XC = MC * (KS / 8) / 256;      // 16-byte activation chunks per thread per step
-  static_assert(XC >= 1 && (MC * (KS / 8)) % 256 == 0, "rows");
-  extern __shared__ __align__(16) uint32_t sm[];
-  uint32_t* Wl = sm;                                              // [SK_BN][RDW]
-  uint16_t* Xl = reinterpret_cast<uint16_t*>(sm + SK_BN * RDW);    // [MC][XST]
-
-  const int tn = blockIdx.x % a.tiles_n;
-  const int sp = (blockIdx.x / a.tiles_n) % a.splits;
-  const int mc = blockIdx.x / (a.tiles_n * a.splits);
-  const int64_t n0 = (int64_t)tn * SK_BN, m0 = (int64_t)mc * MC;
-  const int64_t kb = (int64_t)sp * a.kslice;
-  const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
-  const int steps = (int)((ke - kb) / KS);
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int g = lane >> 4, j = lane & 15;
-
-  rlxq_gemm_args ga;
-  ga.w = a.w;
-  ga.rb = a.rb;
-  ga.K = a.K;
-  ga.group = 32;
-  ga.sb_bf16 = 0;
-  ga.scales = nullptr;
-  ga.biases = nullptr;
-
-  // staging: thread -> weight row tid >> 1, blocks (tid & 1) * BPT + q
-  const int srow = tid >> 1, sblk = (tid & 1) * BPT;
-  const bool sok = n0 + srow < a.N;
-  const int64_t grow = sok ? n0 + srow : a.N - 1;
-  RawBlk<SCH> rb[BPT];
-  uint4 xr[XC];
-  int64_t xoff[XC];
-  bool xok[XC];
+// The MFMAs of one 128-element chunk: normalised blocks o[t] (lane (j, g):
+// block 4c + g of weight row j of tile t), activation fragments xa[mt][i]
+// (positions 8i .. 8i + 7 of the lane group's block, rows 16 mt + j), and,
+// for the formats with a min / bias, the rows' block sums s[mt].  Each step
+// contracts both weight operands (exact f16 hi + lo) into acc; then one MFMA
+// per tile pair adds sum over the four blocks of s * m.
+template <int SCH, int MT, int NT>
+RLXQ_DEV void sk_chunk(const uint32_t (&o)[NT][sk_bdw<SCH>()], const f16x8_t (&xa)[MT][4], const float* s,
+                       f32x4_t (&acc)[MT][NT]) {
 #pragma unroll
-  for (int i = 0; i < XC; i++) {
-    const int c = tid + 256 * i, row = c / (KS / 8);
-    xok[i] = m0 + row < a.M;
-    xoff[i] = (xok[i] ? m0 + row : a.M - 1) * a.K + (c % (KS / 8)) * 8;
-  }
-
-  auto gload = [&](int s) {
-    const int64_t k0 = kb + (int64_t)s * KS;
+  for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int q = 0; q < BPT; q++) load_blk<SCH>(ga, grow, k0 / 32 + sblk + q, sok, rb[q]);
-#pragma unroll
-    for (int i = 0; i < XC; i++) {
-      const uint4 v = *reinterpret_cast<const uint4*>(a.x16 + xoff[i] + k0);
-      xr[i] = xok[i] ? v : make_uint4(0u, 0u, 0u, 0u);
-    }
-  };
-  auto lstore = [&]() {
-#pragma unroll
-    for (int q = 0; q < BPT; q++) {
-      uint32_t o[BDW];
-      normalise<SCH>(rb[q], o);
-      uint32_t* dst = Wl + srow * RDW + (sblk + q) * BDW;
-#pragma unroll
-      for (int i = 0; i < BDW; i++) dst[i] = o[i];
-    }
-#pragma unroll
-    for (int i = 0; i < XC; i++) {
-      const int c = tid + 256 * i;
-      *reinterpret_cast<uint4*>(Xl + (c / (KS / 8)) * XST + (c % (KS / 8)) * 8) = xr[i];
-    }
-  };
-
-  f32x4_t acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-    for (int t = 0; t < NT; t++) acc[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  // wave wv contracts blocks wv + 4i of the step: A = activations, 16 rows x
-  // 8 positions per lane (lane j + 16g: row j, positions 8g..8g+7 of the
-  // block), B = the weights of 16 rows likewise
-  auto compute = [&]() {
-#pragma unroll
-    for (int i = 0; i < NB / 4; i++) {
-      const int blk = wv + 4 * i;
-      f16x8_t af[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; mt++)
-        af[mt] = *reinterpret_cast<const f16x8_t*>(Xl + (16 * mt + j) * XST + 32 * blk + 8 * g);
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const f16x8_t b = dequant_lane<SCH>(Wl + (16 * t + j) * RDW + blk * BDW, g);
+    for (int t = 0; t < NT; t++) {
+      if constexpr (SCH == SCH_MXFP4) {
+        const bf16x8_t b = sk_b_mxfp4(o[t], i);
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
-          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mt], b, acc[mt][t], 0, 0, 0);
+          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[mt][i]), b, acc[mt][t],
+                                                               0, 0, 0);
+      } else {
+        f16x8_t b1, b2;
+        sk_b2<SCH>(o[t], i, b1, b2);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][i], b1, acc[mt][t], 0, 0, 0);
+          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[mt][i], b2, acc[mt][t], 0, 0, 0);
+        }
       }
     }
-  };
-
-  gload(0);
-  lstore();
-  __syncthreads();
-  for (int s = 0; s + 1 < steps; s++) {
-    gload(s + 1);
-    compute();
-    __syncthreads();
-    lstore();
-    __syncthreads();
-  }
-  compute();
-
-  // Add the four waves' sums in the fixed order (w0 + w2) + (w1 + w3).
-  constexpr int E = MT * NT * 4;
-  float* R = reinterpret_cast<float*>(sm);   // [2][E][64], reuses the staging LDS
-  __syncthreads();
-  if (wv >= 2) {
+  if constexpr (sk_has_m<SCH>()) {
+    f16x8_t ma[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
+    for (int mt = 0; mt < MT; mt++) ma[mt] = sk_ma(s[mt]);
 #pragma unroll
-      for (int t = 0; t < NT; t++)
+    for (int t = 0; t < NT; t++) {
+      const f16x8_t mb = sk_mb<SCH>(o[t]);
 #pragma unroll
-        for (int r = 0; r < 4; r++) R[((wv - 2) * E + (mt * NT + t) * 4 + r) * 64 + lane] = acc[mt][t][r];
-  }
-  __syncthreads();
-  if (wv < 2) {
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-      for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) acc[mt][t][r] += R[(wv * E + (mt * NT + t) * 4 + r) * 64 + lane];
-  }
-  __syncthreads();
-  if (wv == 1) {
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-      for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) R[((mt * NT + t) * 4 + r) * 64 + lane] = acc[mt][t][r];
-  }
-  __syncthreads();
-  if (wv != 0) return;
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) acc[mt][t][r] += R[((mt * NT + t) * 4 + r) * 64 + lane];
-  sk_store<MT, NT>(a, acc, m0, n0, sp, g, j);
-}
-
-// Q4_1 with the weight and activation tiles copied global -> LDS by the
-// gfx950 LDS-DMA load (global_load_lds_dwordx4: the 16 bytes of lane l land
-// at the wave's LDS pointer + 16 l), into a ring of D stages of 256 K each, so
-// D - 1 steps of loads are in flight without registers.  A stage holds
-// 128 rows x 8 blocks (160 B per row, the blocks' raw bytes) and MC
-// activation rows x 256 f16 (512 B per row, 16-byte chunks XOR-swizzled by
-// row so the MFMA operand reads of 16 rows spread over the banks).
-template <int MT, int D>
-RLXQ_DEV void skinny_dma_body(const rlxq_skinny_args& a) {
-  constexpr int NT = SK_BN / 16;
-  constexpr int KS = 256, NB = 8;              // K and blocks per step
-  constexpr int WROW = NB * 20;                // raw weight bytes per row per step
-  constexpr int WCH = SK_BN * WROW / 16;       // 16-byte weight chunks per stage
-  constexpr int MC = 16 * MT;
-  constexpr int XCH = MC * KS * 2 / 16;        // 16-byte activation chunks per stage
-  constexpr int NIW = WCH / 256, NIX = XCH / 256;   // DMA instructions per wave per stage
-  static_assert(WCH % 256 == 0 && XCH % 256 == 0, "stage / waves");
-  constexpr int WST = SK_BN * WROW, XSTB = MC * KS * 2, STAGE = WST + XSTB;   // bytes
-  extern __shared__ __align__(16) uint8_t smb[];
-
-  const int tn = blockIdx.x % a.tiles_n;
-  const int sp = (blockIdx.x / a.tiles_n) % a.splits;
-  const int mc = blockIdx.x / (a.tiles_n * a.splits);
-  const int64_t n0 = (int64_t)tn * SK_BN, m0 = (int64_t)mc * MC;
-  const int64_t kb = (int64_t)sp * a.kslice;
-  const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
-  const int steps = (int)((ke - kb) / KS);
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int g = lane >> 4, j = lane & 15;
-
-  // per-lane global sources of this wave's DMA instructions (step offset added later)
-  const uint8_t* wsrc[NIW];
-#pragma unroll
-  for (int i = 0; i < NIW; i++) {
-    const int c = (wv * NIW + i) * 64 + lane;          // chunk of the stage
-    const int r = c / (WROW / 16), piece = c % (WROW / 16);
-    const int64_t row = n0 + r < a.N ? n0 + r : a.N - 1;
-    wsrc[i] = a.w + row * a.rb + 16 * piece;
-  }
-  const uint16_t* xsrc[NIX];
-#pragma unroll
-  for (int i = 0; i < NIX; i++) {
-    const int c = (wv * NIX + i) * 64 + lane;          // LDS chunk position
-    const int r = c / 32, cp = c % 32;                 // 32 chunks per activation row
-    const int lc = cp ^ (r & 15);                      // the logical chunk stored there
-    const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;
-    xsrc[i] = a.x16 + m * a.K + 8 * lc;
-  }
-  auto issue = [&](int s) {
-    uint8_t* st = smb + (s % D) * STAGE;
-    const int64_t k0 = kb + (int64_t)s * KS;
-#pragma unroll
-    for (int i = 0; i < NIW; i++)
-      __builtin_amdgcn_global_load_lds(wsrc[i] + (k0 / 32) * 20, st + (wv * NIW + i) * 1024, 16, 0, 0);
-#pragma unroll
-    for (int i = 0; i < NIX; i++)
-      __builtin_amdgcn_global_load_lds(xsrc[i] + k0, st + WST + (wv * NIX + i) * 1024, 16, 0, 0);
-  };
-  // wait until this wave's loads of step s have landed: at most `later`
-  // steps' loads issued after them may still be outstanding
-  auto wait_for = [&](int later) {
-    constexpr int PER = NIW + NIX;
-    if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER));
-    else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  };
-
-  f32x4_t acc[MT][NT];
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-    for (int t = 0; t < NT; t++) acc[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  auto compute = [&](int s) {
-    const uint8_t* st = smb + (s % D) * STAGE;
-    const uint32_t* Wl = reinterpret_cast<const uint32_t*>(st);
-    const uint16_t* Xl = reinterpret_cast<const uint16_t*>(st + WST);
-#pragma unroll
-    for (int i = 0; i < NB / 4; i++) {
-      const int blk = wv + 4 * i;
-      f16x8_t af[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; mt++) {
-        const int r = 16 * mt + j, lc = 4 * blk + g;
-        af[mt] = *reinterpret_cast<const f16x8_t*>(Xl + r * KS + 8 * (lc ^ (r & 15)));
-      }
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const f16x8_t b = dequant_lane<SCH_Q4_1>(Wl + (16 * t + j) * (WROW / 4) + blk * 5, g);
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mt], b, acc[mt][t], 0, 0, 0);
-      }
+      for (int mt = 0; mt < MT; mt++) acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ma[mt], mb, acc[mt][t], 0, 0, 0);
     }
-  };
-
-  static_assert(D == 3, "the wait counts below assume a ring of 3");
-  for (int s = 0; s < D - 1 && s < steps; s++) issue(s);
-  for (int s = 0; s < steps; s++) {
-    const int later = steps - 1 - s < D - 2 ? steps - 1 - s : D - 2;
-    wait_for(later);
-    // this wave's operand reads of step s - 1 are complete, then the barrier:
-    // step s landed for every wave, and no wave still reads step s - 1's slot
-    __builtin_amdgcn_s_waitcnt(lgkmcnt0_imm());
-    __builtin_amdgcn_s_barrier();
-    if (s + D - 1 < steps) issue(s + D - 1);
-    compute(s);
   }
-
-  // Add the four waves' sums in the fixed order (w0 + w2) + (w1 + w3).
-  constexpr int E = MT * NT * 4;
-  float* R = reinterpret_cast<float*>(smb);
-  __syncthreads();
-  if (wv >= 2) {
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-      for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) R[((wv - 2) * E + (mt * NT + t) * 4 + r) * 64 + lane] = acc[mt][t][r];
-  }
-  __syncthreads();
-  if (wv < 2) {
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-      for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) acc[mt][t][r] += R[(wv * E + (mt * NT + t) * 4 + r) * 64 + lane];
-  }
-  __syncthreads();
-  if (wv == 1) {
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-      for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) R[((mt * NT + t) * 4 + r) * 64 + lane] = acc[mt][t][r];
-  }
-  __syncthreads();
-  if (wv != 0) return;
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) acc[mt][t][r] += R[((mt * NT + t) * 4 + r) * 64 + lane];
-  sk_store<MT, NT>(a, acc, m0, n0, sp, g, j);
 }
 
 // ---------------------------------------------------------------------------
-// Register-streamed variant (GGUF Q4_1, Q4_0, Q8_0): no LDS stage and no
-// barrier per step.
+// Register-streamed variant: no LDS stage and no barrier per step.
 // The four waves of a workgroup take the same NT tiles of 16 weight rows and
 // split their K range in 4-block chunks (chunk c -> wave c % 4).  Lane
 // (j, g) = (lane % 16, lane / 16) loads all the bytes of block 4c + g of row
@@ -392,11 +122,12 @@ RLXQ_DEV void skinny_dma_body(const rlxq_skinny_args& a) {
 // (lane j of tile t reads weight row wrow[t] of the rows at w, stride rb)
 // over K [kb, ke).  Returns true in wave 0, whose acc then holds the sums.
 template <int SCH, int MT, int NT, int D>
-RLXQ_DEV bool skinny_xr_core(const uint16_t* x16, int64_t Mp, int64_t m0, const uint8_t* w, int64_t rb, int64_t K,
-                             int64_t kb, int64_t ke, const int64_t (&wrow)[NT], const bool (&wok)[NT],
-                             f32x4_t (&acc)[MT][NT], const void* scales = nullptr,
+RLXQ_DEV bool skinny_xr_core(const uint16_t* x16, const float* ssum, int64_t Mp, int64_t m0, const uint8_t* w,
+                             int64_t rb, int64_t K, int64_t kb, int64_t ke, const int64_t (&wrow)[NT],
+                             const bool (&wok)[NT], f32x4_t (&acc)[MT][NT], const void* scales = nullptr,
                              const void* biases = nullptr, int64_t group = 32, int32_t sb_bf16 = 0) {
   constexpr int BDW = sk_bdw<SCH>();
+  constexpr bool HM = sk_has_m<SCH>();
   // wave index through readfirstlane: the chunk loop is wave-uniform
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
@@ -416,14 +147,20 @@ RLXQ_DEV bool skinny_xr_core(const uint16_t* x16, int64_t Mp, int64_t m0, const 
   // lane group g at ((4 c + i) Mp + m) 4 + g (16-byte pieces), so the A
   // fragment of 16 rows is one contiguous 1 KB read; the Mp rows cover every
   // 16 MT-row chunk (padding rows zero)
+  // The block sums (min / bias term) in the same order, one f32 per block:
+  // chunk c, row m, lane group g at (c Mp + m) 4 + g.
   const uint4* xrow[MT];
+  const float* srow[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; mt++)
+  for (int mt = 0; mt < MT; mt++) {
     xrow[mt] = reinterpret_cast<const uint4*>(x16) + ((kb / 32) * Mp + m0 + 16 * mt + j) * 4 + g;
+    srow[mt] = HM ? ssum + ((kb / 128) * Mp + m0 + 16 * mt + j) * 4 + g : nullptr;
+  }
 
   struct Stage {
     RawBlk<SCH> w[NT];
     uint4 x[MT][4];
+    float s[HM ? MT : 1];
   };
   auto load = [&](int c, Stage& st) {
 #pragma unroll
@@ -432,6 +169,10 @@ RLXQ_DEV bool skinny_xr_core(const uint16_t* x16, int64_t Mp, int64_t m0, const 
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
       for (int i = 0; i < 4; i++) st.x[mt][i] = xrow[mt][((int64_t)c * 4 + i) * Mp * 4];
+    if constexpr (HM) {
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++) st.s[mt] = srow[mt][(int64_t)c * Mp * 4];
+    }
   };
 
 #pragma unroll
@@ -448,15 +189,12 @@ RLXQ_DEV bool skinny_xr_core(const uint16_t* x16, int64_t Mp, int64_t m0, const 
     uint32_t o[NT][BDW];
 #pragma unroll
     for (int t = 0; t < NT; t++) normalise<SCH>(st.w[t], o[t]);
+    f16x8_t xa[MT][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const auto b = sk_b<SCH>(o[t], i);
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-          acc[mt][t] = sk_mfma<SCH>(__builtin_bit_cast(f16x8_t, st.x[mt][i]), b, acc[mt][t]);
-      }
+      for (int i = 0; i < 4; i++) xa[mt][i] = __builtin_bit_cast(f16x8_t, st.x[mt][i]);
+    sk_chunk<SCH, MT, NT>(o, xa, HM ? st.s : nullptr, acc);
   };
   // (slots past the wave's chunks repeat its last one: a few redundant
   // loads when it has fewer than D chunks, none otherwise; a wave with no
@@ -543,8 +281,8 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
     wrow[t] = wok[t] ? n : a.N - 1;
   }
   f32x4_t acc[MT][NT];
-  if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.Mp, m0, a.w, a.rb, a.K, kb, ke, wrow, wok, acc, a.scales, a.biases,
-                                      a.group, a.sb_bf16))
+  if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.ssum, a.Mp, m0, a.w, a.rb, a.K, kb, ke, wrow, wok, acc, a.scales,
+                                      a.biases, a.group, a.sb_bf16))
     return;
   sk_store<MT, NT>(a, acc, m0, n0, sp, g, j);
 }
@@ -585,8 +323,8 @@ RLXQ_DEV void moe_sk_body(const rlxq_moe_sk_args& a) {
   const int esz = a.sb_bf16 == 0 ? 4 : (a.sb_bf16 == 1 ? 2 : 1);
   const void* sc = a.scales ? static_cast<const void*>(static_cast<const uint8_t*>(a.scales) + slab * esz) : nullptr;
   const void* bi = a.biases ? static_cast<const void*>(static_cast<const uint8_t*>(a.biases) + slab * esz) : nullptr;
-  if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.Mp, m0, a.bank + (int64_t)e * a.N * a.rb, a.rb, a.K, 0, a.K, wrow,
-                                      wok, acc, sc, bi, a.group, a.sb_bf16))
+  if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.ssum, a.Mp, m0, a.bank + (int64_t)e * a.N * a.rb, a.rb, a.K, 0, a.K,
+                                      wrow, wok, acc, sc, bi, a.group, a.sb_bf16))
     return;
   // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
 #pragma unroll
@@ -631,6 +369,7 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
   constexpr int MC = 16 * MT;
   constexpr int AST = 4 * MC * 64;   // bytes of one activation slot
   constexpr int BDW = sk_bdw<SCH>();
+  constexpr bool HM = sk_has_m<SCH>();
   extern __shared__ __align__(16) uint8_t sma[];
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int j = lane & 15, g = lane >> 4;
@@ -662,12 +401,15 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
   // positions 8 wv .. 8 wv + 7 (fragment-major source; the Mp rows cover
   // every m-chunk)
   const u32x4_t* xsrc = reinterpret_cast<const u32x4_t*>(a.x16) + (wv * a.Mp + m0 + j) * 4 + g;
+  // the block sums of rows 16 u + j, block 4c + g (min / bias term)
+  const float* ssrc = HM ? a.ssum + (m0 + j) * 4 + g : nullptr;
 
   // ring slot d: a step's weight blocks wr[d] and activation pieces xr[d]
   // (pieces held as a clang vector type: a ring of HIP's uint4 struct, or
   // one struct of both rings, stayed in scratch memory for some schemes)
   RawBlk<SCH> wr[D][NT];
   u32x4_t xr[D][MT];
+  float sr[D][HM ? MT : 1];
   // steps past the last repeat it (their data is never used), so every step
   // issues the same loads
   auto load = [&](int s, int d) {
@@ -676,6 +418,10 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
     for (int u = 0; u < MT; u++) xr[d][u] = xsrc[(4 * c * a.Mp + 16 * u) * 4];
 #pragma unroll
     for (int t = 0; t < NT; t++) load_blk<SCH>(ga, wrow[t], 4 * c + g, wok[t], wr[d][t]);
+    if constexpr (HM) {
+#pragma unroll
+      for (int u = 0; u < MT; u++) sr[d][u] = ssrc[(c * a.Mp + 16 * u) * 4];
+    }
   };
   auto put = [&](int s, int d) {
     uint8_t* slot = sma + (s & 1) * AST;
@@ -696,18 +442,12 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
     uint32_t o[NT][BDW];
 #pragma unroll
     for (int t = 0; t < NT; t++) normalise<SCH>(wr[d][t], o[t]);
+    f16x8_t xa[MT][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      f16x8_t af[MT];
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int mt = 0; mt < MT; mt++) af[mt] = *reinterpret_cast<const f16x8_t*>(slot + (i * MT + mt) * 1024 + lane * 16);
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const auto b = sk_b<SCH>(o[t], i);
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) acc[mt][t] = sk_mfma<SCH>(af[mt], b, acc[mt][t]);
-      }
-    }
+      for (int mt = 0; mt < MT; mt++) xa[mt][i] = *reinterpret_cast<const f16x8_t*>(slot + (i * MT + mt) * 1024 + lane * 16);
+    sk_chunk<SCH, MT, NT>(o, xa, HM ? sr[d] : nullptr, acc);
   };
   // step s: ring slot s % D holds step s's weights (and step s's
   // activations, already in LDS slot s & 1); slot (s + 1) % D holds step
@@ -758,9 +498,11 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
     // padding rows of the fragment-major layout: zeros
     if (!a.frag_major || r >= a.Mp) return;
     uint4* dst = reinterpret_cast<uint4*>(a.x16);
-    for (int64_t b = t; b < nblk; b += 256)
+    for (int64_t b = t; b < nblk; b += 256) {
 #pragma unroll
       for (int q = 0; q < 4; q++) dst[(((b >> 2) * 4 + q) * a.Mp + r) * 4 + (b & 3)] = make_uint4(0u, 0u, 0u, 0u);
+      if (a.ssum) a.ssum[((b >> 2) * a.Mp + r) * 4 + (b & 3)] = 0.f;
+    }
     return;
   }
   auto load_blk32 = [&](int64_t b, float* v) {
@@ -807,13 +549,14 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
   if ((t & 63) == 0) red[t >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  // a power-of-two scale putting the row maximum in [2^13, 2^14)
-  float s = 1.f, inv = 1.f;
+  // a power-of-two scale putting the row maximum in [2^9, 2^10) (a block
+  // sum then stays below 2^15, inside f16)
+  float s = 1.f, inv = ldexpf(1.f, a.post_exp);
   if (amax > 0.f && amax <= 3.4e38f) {
-    int sh = 13 - ilogbf(amax);
+    int sh = 9 - ilogbf(amax);
     sh = sh < -126 ? -126 : (sh > 126 ? 126 : sh);
     s = ldexpf(1.f, sh);
-    inv = ldexpf(1.f, -sh);
+    inv = ldexpf(ldexpf(1.f, -sh), a.post_exp);
   }
   const int nib = a.nibble_order;
   auto store_blk32 = [&](int64_t b, const float* w) {
@@ -831,6 +574,15 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
         h1 = a.out_bf16 ? f32_to_bf16_bits(w1) : f32_to_f16_bits(w1);
       }
       o[p / 2] = h0 | (h1 << 16);
+    }
+    if (a.frag_major && a.ssum) {
+      float sum = 0.f;
+#pragma unroll
+      for (int q = 0; q < 16; q++) {
+        sum += a.out_bf16 ? bf16_bits_to_f32(o[q] & 0xffffu) : f16_bits_to_f32(o[q] & 0xffffu);
+        sum += a.out_bf16 ? bf16_bits_to_f32(o[q] >> 16) : f16_bits_to_f32(o[q] >> 16);
+      }
+      a.ssum[((b >> 2) * a.Mp + r) * 4 + (b & 3)] = sum;
     }
     if (a.frag_major) {
       uint4* dst = reinterpret_cast<uint4*>(a.x16);
@@ -901,30 +653,6 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_skinny_reduce(rlxq_skinny
   if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[m * a.y_ld + n] = (uint16_t)f32_to_bf16_bits(v);
   else reinterpret_cast<float*>(a.y)[m * a.y_ld + n] = v;
 }
-
-#define RLXQ_SKINNY_INST(SNAME, SCH, MT, BPT)                                                      \
-  extern "C" __global__ __launch_bounds__(256, 2) void rlxq_skinny_##SNAME##_mt##MT##_b##BPT(       \
-      rlxq_skinny_args a) {                                                                        \
-    rlxq::skinny_body<SCH, MT, BPT>(a);                                                            \
-  }
-#define RLXQ_SKINNY_SCHEME(SNAME, SCH) \
-  RLXQ_SKINNY_INST(SNAME, SCH, 1, 2)   \
-  RLXQ_SKINNY_INST(SNAME, SCH, 1, 8)   \
-  RLXQ_SKINNY_INST(SNAME, SCH, 2, 2)   \
-  RLXQ_SKINNY_INST(SNAME, SCH, 2, 8)   \
-  RLXQ_SKINNY_INST(SNAME, SCH, 4, 2)   \
-  RLXQ_SKINNY_INST(SNAME, SCH, 4, 4)
-RLXQ_SKINNY_SCHEME(q4_1, SCH_Q4_1)
-RLXQ_SKINNY_SCHEME(q4_0, SCH_Q4_0)
-RLXQ_SKINNY_SCHEME(q8_0, SCH_Q8_0)
-
-#define RLXQ_SKINNY_DMA_INST(MT)                                                                  \
-  extern "C" __global__ __launch_bounds__(256, 2) void rlxq_skinny_q4_1_mt##MT##_dma(rlxq_skinny_args a) { \
-    rlxq::skinny_dma_body<MT, 3>(a);                                                              \
-  }
-RLXQ_SKINNY_DMA_INST(1)
-RLXQ_SKINNY_DMA_INST(2)
-RLXQ_SKINNY_DMA_INST(4)
 
 // Register-streamed variants: rlxq_skinnyxr_<scheme>_mt<MT>_nt<NT>_d<D>.
 #define RLXQ_SKINNYXR_INST(SNAME, SCH, MT, NT, D)                                                      \

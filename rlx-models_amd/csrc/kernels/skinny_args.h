@@ -29,6 +29,14 @@ typedef struct rlxq_x16_args {
    * element; M counts the rows of x (and rmap its entries), Mp the x16
    * rows (>= 2 M)                                                          */
   int32_t split;
+  /* inv_s[r] carries an extra factor 2^post_exp: the MLX affine kernels'
+   * f16 weights are 2^8 times the true ones (post_exp = -8), so that group
+   * scales down to ~2^-22 stay normal in f16                               */
+  int32_t post_exp;
+  /* fragment-major only, NULL for none: the sum of each prepared 32-element
+   * block (f32, in the order the prepared values sum) at
+   * ((b / 4) Mp + r) 4 + b % 4 for block b of x16 row r (0 for padding rows) */
+  float* ssum;
 } rlxq_x16_args;
 
 typedef struct rlxq_skinny_args {
@@ -52,6 +60,8 @@ typedef struct rlxq_skinny_args {
    * output row r); the epilogue adds each pair, and y and part hold M / 2
    * rows                                                                  */
   int32_t pairs;
+  /* block sums of x16 (rlxq_x16_args.ssum): the formats with a min / bias  */
+  const float* ssum;
 } rlxq_skinny_args;
 
 #endif

@@ -77,6 +77,7 @@ def lib() -> C.CDLL:
         "rlxq_row_bytes": (I64, [I, I64]),
         "rlxq_reserve_workspace": (I, [P, P, S]),
         "rlxq_workspace_bytes": (I64, [P, P]),
+        "rlxq_workspace_retired_bytes": (I64, [P, P]),
         "rlxq_release_stream": (I, [P, P]),
         "rlxq_dequant_matmul": (I, [P, I, I, P, I, P, P, P, I, I64, I64, I64, P, I, P]),
         "rlxq_dequant_matmul_noalloc": (I, [P, I, I, P, I, P, P, P, I, I64, I64, I64, P, I, P]),
@@ -370,6 +371,10 @@ class Context:
 
     def workspace_bytes(self, *, stream=None) -> int:
         return int(lib().rlxq_workspace_bytes(self.h, _stream(stream)))
+
+    def workspace_retired_bytes(self, *, stream=None) -> int:
+        """Bytes of replaced scratch buffers `stream` still holds."""
+        return int(lib().rlxq_workspace_retired_bytes(self.h, _stream(stream)))
 
     def release_stream(self, *, stream=None) -> None:
         """Frees the scratch buffers of `stream` after waiting for it."""

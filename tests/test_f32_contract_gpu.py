@@ -117,15 +117,16 @@ def test_batched_decode_f32_mlx4_and_mxfp4(ctx, orc):
 @pytest.mark.parametrize("scheme", [Q4_1, Q4_K, Q8_0, Q6_K, Q4_0], ids=lambda s: NAMES[s])
 @pytest.mark.parametrize("mkn", [(300, 1280, 272), (512, 4096, 1024), (257, 12288, 300)], ids=str)
 def test_prefill_f32_activations(ctx, orc, scheme, mkn):
-    """More than 256 rows of f32 activations with f32 output: the f16 GEMM
-    on hi/lo row pairs (split-K on the small grids)."""
+    """More than 256 rows of f32 activations with f32 output: the exact GEMM
+    (f16 hi + lo weight rows) on hi/lo activation row pairs (split-K on the
+    small grids)."""
     m, k, n = mkn
     announce(f"f32 contract gemm {NAMES[scheme]} {mkn}")
     rng = np.random.default_rng(m + k + scheme)
     packed = orc.synth(scheme, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, kern = _f32_run(ctx, scheme, x, _t(packed), n)
-    assert kern.startswith(f"rlxq_gemm_{NAMES[scheme]}_t256w8") and kern.endswith("f"), kern
+    assert kern.startswith(f"rlxq_gemm_{NAMES[scheme]}_t256w8") and kern.endswith("x"), kern
     assert rel_err(got, _want(orc, scheme, x, packed, k)) <= TOL, kern
 
 
@@ -138,12 +139,12 @@ def test_prefill_f32_exact_weights_and_bf16_out(ctx, orc):
     packed = _exact_f16_q4_1(orc, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, kern = _f32_run(ctx, Q4_1, x, _t(packed), n)
-    assert kern == "rlxq_gemm_q4_1_t256w8p2f", kern
+    assert kern == "rlxq_gemm_q4_1_t256w8p2x", kern
     want = _want(orc, Q4_1, x, packed, k)
     assert rel_err(got, want) <= TOL_EXACT_W
     # bf16 output from f32 activations: the same kernel, rounded at the store
     y = ctx.dequant_matmul(_t(x), _t(packed), Q4_1, n, y_dtype=torch.bfloat16)
-    assert ctx.last_kernel == "rlxq_gemm_q4_1_t256w8p2f", ctx.last_kernel
+    assert ctx.last_kernel == "rlxq_gemm_q4_1_t256w8p2x", ctx.last_kernel
     torch.cuda.synchronize()
     assert rel_err(y.float().cpu().numpy(), want) <= 8e-3
 
@@ -166,7 +167,7 @@ def test_prefill_f32_config4_full_size_sampled(ctx, orc, scheme, kn):
     y = ctx.dequant_matmul(x, w, scheme, n, y_dtype=torch.float32)
     kern = ctx.last_kernel
     torch.cuda.synchronize()
-    assert kern == f"rlxq_gemm_{NAMES[scheme]}_t256w8p2f", kern
+    assert kern == f"rlxq_gemm_{NAMES[scheme]}_t256w8p2x", kern
     rs = np.random.default_rng(m + n)
     rows = np.sort(rs.choice(m, 48, replace=False))
     cols = np.sort(rs.choice(n, 384, replace=False))
@@ -260,3 +261,32 @@ def test_device_matmul_session_f32_on_mfma(orc):
         assert rel_err(y, _want(orc, Q4_1, x, packed.reshape(n, -1), k)) <= TOL, m
     assert dm.uploads == 1
     dm.close()
+
+
+@pytest.mark.parametrize("scheme", [Q8_0, Q4_0, Q4_1], ids=lambda s: NAMES[s])
+@pytest.mark.parametrize("m", [1, 7, 16, 128, 300])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_reference_structured_inputs_every_path(ctx, orc, scheme, m, xdt):
+    """The reference's own parity data (quant_parity_backends.rs:61-71: x =
+    0.8 sin(0.031 i), W = 0.35 cos(0.017 i + 0.3), quantized) at K = 1792,
+    where rounding each weight once to f16 already costs 1.4e-3 and
+    rounding the activations alone 7e-4: every f32-output path (the register
+    GEMV at M=1, the batched-decode kernels from 5 rows, the exact prefill
+    GEMM past 256) stays within 5e-5, far inside the 1e-3 bar."""
+    import torch
+    from test_gemv_gpu import _ref_input, _ref_weight
+
+    k, n = 1792, 1280
+    announce(f"structured inputs {NAMES[scheme]} m={m} x={xdt}")
+    x = _ref_input(m, k)
+    packed = orc.quantize(scheme, _ref_weight(n, k, 0.3))
+    xt = _t(x) if xdt == "f32" else _t(x).to(torch.bfloat16)
+    xv = xt.float().cpu().numpy()
+    y = ctx.dequant_matmul(xt, _t(packed), scheme, n, y_dtype=torch.float32)
+    kern = ctx.last_kernel
+    torch.cuda.synchronize()
+    if m >= 300:
+        assert kern.startswith(f"rlxq_gemm_{NAMES[scheme]}_t256") and kern.endswith("x"), kern
+    elif m >= 5:
+        assert kern.startswith("rlxq_skinny"), kern
+    assert rel_err(y.cpu().numpy(), _want(orc, scheme, xv, packed, k)) <= 5e-5, kern

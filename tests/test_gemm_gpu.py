@@ -151,29 +151,31 @@ def test_every_gemm_tiling(ctx, orc, scheme, monkeypatch):
 
 
 @pytest.mark.parametrize("scheme", [1, 2, 3])
-def test_f32_output_prefill_takes_the_f16_kernel(ctx, orc, scheme):
+def test_f32_output_prefill_takes_the_exact_kernel(ctx, orc, scheme):
     """GGUF, bf16 activations, f32 output, past the batched-decode sizes: the
-    dispatcher picks the f16 GEMM, and the output meets the 1e-3 bar."""
+    dispatcher picks the exact GEMM (f16 hi + lo weights), and the output
+    meets the 1e-3 bar."""
     m, k, n = 384, 1024, 520
     rng = np.random.default_rng(11 + scheme)
     packed = orc.synth(scheme, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, xv = run_gemm(ctx, orc, scheme, x, packed, n, ydt="f32")
-    assert ctx.last_kernel.endswith("f"), ctx.last_kernel
+    assert ctx.last_kernel.endswith("x"), ctx.last_kernel
     wd = orc.dequantize(scheme, packed, k).astype(np.float64)
     assert rel_err(got, xv.astype(np.float64) @ wd.T) <= 1e-3
 
 
 @pytest.mark.parametrize("scheme", [1, 2, 3])
 @pytest.mark.parametrize("mkn", [(256, 64, 256), (300, 640, 272), (513, 1280, 300), (1000, 4096, 520)], ids=str)
-def test_gemm_f16_shared_conversion(ctx, orc, monkeypatch, scheme, mkn):
-    """256 x 256 tiles with the weights converted once per workgroup to f16
-    and f16 MFMA on the prepared activations: f32 output within 1e-3."""
+def test_gemm_exact_shared_conversion(ctx, orc, monkeypatch, scheme, mkn):
+    """The exact variant: weights converted once per workgroup to f16 hi +
+    lo rows (128 output columns per tile), f16 MFMA on the prepared
+    activations: f32 output within 1e-3."""
     monkeypatch.setenv("RLXQ_PREFILL", "gemm")
-    tile = "256w8f" if scheme == 1 else "256w8p2f"
+    tile = "256w8x" if scheme == 1 else "256w8p2x"
     monkeypatch.setenv("RLXQ_GEMM_TILE", tile)
     m, k, n = mkn
-    announce(f"gemm f16 shared conversion t{tile} scheme={scheme} {mkn}")
+    announce(f"gemm exact shared conversion t{tile} scheme={scheme} {mkn}")
     rng = np.random.default_rng(scheme * 7 + m + k + n)
     packed = orc.synth(scheme, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -185,7 +187,7 @@ def test_gemm_f16_shared_conversion(ctx, orc, monkeypatch, scheme, mkn):
 
 
 @pytest.mark.parametrize("scheme", [1, 2, 3, 4])
-@pytest.mark.parametrize("tile_ydt", [("256w8p2", "bf16"), ("256w8", "f32"), ("256w8p2f", "f32"), ("256w8f", "f32")],
+@pytest.mark.parametrize("tile_ydt", [("256w8p2", "bf16"), ("256w8", "f32"), ("256w8p2x", "f32"), ("256w8x", "f32")],
                          ids=lambda t: f"{t[0]}-{t[1]}")
 @pytest.mark.parametrize("splits", [2, 3, 8])
 def test_gemm_split_k(ctx, orc, monkeypatch, scheme, tile_ydt, splits):
@@ -195,10 +197,8 @@ def test_gemm_split_k(ctx, orc, monkeypatch, scheme, tile_ydt, splits):
     import rlxq
 
     tile, ydt = tile_ydt
-    if tile.endswith("f") and scheme == rlxq.MLX_AFFINE4:
-        pytest.skip("the f16 GEMM serves GGUF codes only")
-    if tile == "256w8f" and scheme != 1 or tile == "256w8p2f" and scheme == 1:
-        pytest.skip("one f16 tiling per scheme")
+    if tile == "256w8x" and scheme != 1 or tile == "256w8p2x" and scheme == 1:
+        pytest.skip("one exact tiling per scheme")
     m, k, n = 300, 64 * 13, 520
     rng = np.random.default_rng(31 * scheme + splits)
     x = rng.standard_normal((m, k)).astype(np.float32)
@@ -222,7 +222,7 @@ def test_gemm_split_k(ctx, orc, monkeypatch, scheme, tile_ydt, splits):
         announce(f"gemm split-k t{tile} scheme={scheme} splits={sp} ydt={ydt}")
         got, xv = run_gemm(ctx, orc, scheme, x, packed, n, ydt=ydt, **kw)
         assert ctx.last_kernel.endswith(f"_t{tile}"), ctx.last_kernel
-        tol = 1e-3 if tile.endswith("f") else TOL_PREFILL
+        tol = 1e-3 if tile.endswith("x") else TOL_PREFILL
         assert rel_err(got, xv.astype(np.float64) @ wd.T) <= tol
         outs[sp] = got
     if ydt == "f32":

@@ -101,16 +101,18 @@ def test_mxfp4_bf16_scales_and_split_k(ctx, orc, monkeypatch):
 
 @pytest.mark.parametrize("scheme", ALL, ids=lambda s: NAMES[s])
 def test_f32_output_prefill_route(ctx, orc, scheme):
-    """f32 output is not routed to the bf16-weight GEMM: Q6_K takes its f16
-    variant (each 16-weight half's d*sc rounded to f16 once, codes exact),
-    the other formats the GEMV family; both keep the 1e-3 bar."""
+    """f32 output is not routed to the bf16-weight GEMM: the K-quants take the
+    exact variant (each weight's f32 value as f16 hi + lo rows), MXFP4 with
+    E8M0 scales the bf16 GEMM (its weights are exact in bf16, as are bf16
+    activations); both keep the 1e-3 bar."""
     m, k, n = 300, 1024, 200
     rng = np.random.default_rng(3 + scheme)
     packed, kw, wd = _weights(orc, scheme, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, xv = _run(ctx, scheme, x, packed, kw, n, "f32")
-    if scheme == Q6_K:
-        assert ctx.last_kernel == "rlxq_gemm_q6_k_t256w8lf", ctx.last_kernel
+    if scheme == MXFP4:
+        assert ctx.last_kernel == "rlxq_gemm_mxfp4_t256w8p2", ctx.last_kernel
     else:
-        assert ctx.last_kernel.startswith("rlxq_gemv"), ctx.last_kernel
+        assert ctx.last_kernel.startswith(f"rlxq_gemm_{NAMES[scheme]}_t256w8") and ctx.last_kernel.endswith("x"), \
+            ctx.last_kernel
     assert rel_err(got, xv @ wd.T) <= 1e-3

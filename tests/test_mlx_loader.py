@@ -182,3 +182,27 @@ def test_single_file_and_errors(tmp_path):
     with pytest.raises(rlxq.RlxqError) as e:
         rlxq.MlxFile(tmp_path / "empty")
     assert e.value.status == rlxq.E_NOTFOUND
+
+
+@pytest.mark.parametrize("cfg", [
+    {"quantization_config": {"quant_method": "gptq", "bits": 4, "group_size": 128, "desc_act": False}},
+    {"quantization_config": {"quant_method": "fp8", "weight_block_size": [128, 128], "fmt": "e4m3"}},
+    {"quantization_config": {"quant_method": "mxfp4", "modules_to_not_convert": ["lm_head"]}},
+    {"quantization": {"mode": "none"}},
+    {"quantization": 4},
+], ids=["gptq", "fp8", "gpt-oss", "no-bits", "not-object"])
+def test_non_mlx_quantization_blocks_read_as_unquantized(tmp_path, cfg):
+    """Only an mlx-lm `quantization` object with bits or group_size marks an
+    MLX checkpoint (dir_is_mlx_quant, crates/rlx-models-core/src/
+    weight_registry.rs:27-41); GPTQ / AWQ / fp8 / gpt-oss `quantization_config`
+    blocks and other `quantization` values leave the tensors unquantized."""
+    rng = np.random.default_rng(1)
+    wq = rng.integers(0, 1 << 32, (32, 16), dtype=np.uint64).astype(np.uint32)
+    (tmp_path / "model.safetensors").write_bytes(
+        safetensors_bytes({"m.weight": wq, "m.scales": _bf16(np.ones((32, 2))), "m.biases": _bf16(np.zeros((32, 2)))}))
+    (tmp_path / "config.json").write_text(json.dumps(dict(cfg, model_type="qwen3")))
+    f = rlxq.MlxFile(tmp_path)
+    assert f.quantization == (0, 0, rlxq.MLX_MODE_NONE)
+    assert f.take_packed("m") is None
+    assert f.tensors["m.weight"]["shape"] == [32, 16]
+    f.close()

@@ -212,3 +212,81 @@ def test_grouped_mfma_mlx_and_mxfp4(ctx, orc, monkeypatch, fmt, forced):
     got = y.cpu().numpy()
     for r in range(rows):
         assert rel_err(got[r:r + 1], want[r:r + 1]) <= tol, (fmt, r)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("slab", ["f32", "bf16"])
+def test_grouped_mfma_mlx_every_group_and_slab(ctx, orc, monkeypatch, bits, group, slab):
+    """The per-expert slab offset e * N * (K / group) and the slab element
+    size on every group size and slab dtype of both bit widths: nine experts,
+    one of them crowded (half the rows), so several chunks of the grouped MFMA
+    kernel read the slabs of different experts."""
+    import torch
+    import rlxq
+
+    monkeypatch.setenv("RLXQ_MOE_KERNEL", "sk")
+    rows, k, n, E = 96, 768, 72, 9
+    announce(f"grouped mfma mlx{bits} group={group} slab={slab}")
+    rng = np.random.default_rng(bits * 1000 + group + len(slab))
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    xt, xv = _x_as(x, "bf16")
+    idx = rng.integers(0, E, rows)
+    idx[::2] = 5
+    idx = idx.astype(np.float32)
+    codes = rng.integers(0, 2 ** 32, (E * n, k * bits // 32), dtype=np.uint32)
+    sc = rng.uniform(0.01, 0.1, (E * n, k // group)).astype(np.float32)
+    bi = rng.uniform(-0.5, 0.1, (E * n, k // group)).astype(np.float32)
+    if slab == "bf16":
+        sc = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(sc))
+        bi = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(bi))
+        st, bt = _t(sc).to(torch.bfloat16), _t(bi).to(torch.bfloat16)
+    else:
+        st, bt = _t(sc), _t(bi)
+    scheme = rlxq.MLX_AFFINE4 if bits == 4 else rlxq.MLX_AFFINE8
+    y = ctx.grouped_matmul(xt, _t(codes.view(np.uint8)), _t(idx), scheme, n, E, group=group, scales=st, biases=bt)
+    torch.cuda.synchronize()
+    assert ctx.last_kernel.startswith(f"rlxq_moesk_mlx{bits}_"), ctx.last_kernel
+    got = y.cpu().numpy()
+    for r in range(rows):
+        sl = slice(int(idx[r]) * n, (int(idx[r]) + 1) * n)
+        want = orc.mlx_matmul_f64(xv[r:r + 1], codes[sl], sc[sl], bi[sl], n, bits, group)
+        assert rel_err(got[r:r + 1], want) <= TOL, (r, int(idx[r]))
+
+
+@pytest.mark.parametrize("path", ["grouped", "dense"])
+def test_mlx8_small_scales_on_f16_kernels(ctx, orc, monkeypatch, path):
+    """MLX 8-bit group scales near 1e-5 (a group of small weights: f16
+    subnormals if rounded unscaled) on the f16 MFMA kernels, which hold the
+    scales and biases times 2^8: within the 1e-3 bar, grouped and dense."""
+    import torch
+    import rlxq
+
+    rows, k, n, E, group = 48, 1024, 96, 3, 64
+    announce(f"mlx8 small scales {path}")
+    rng = np.random.default_rng(404)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    xt, xv = _x_as(x, "bf16")
+    codes = rng.integers(0, 2 ** 32, (E * n, k // 4), dtype=np.uint32)
+    sc = rng.uniform(5e-6, 2e-5, (E * n, k // group)).astype(np.float32)
+    bi = rng.uniform(-2e-3, 0.0, (E * n, k // group)).astype(np.float32)
+    if path == "grouped":
+        monkeypatch.setenv("RLXQ_MOE_KERNEL", "sk")
+        idx = (np.arange(rows) % E).astype(np.float32)
+        y = ctx.grouped_matmul(xt, _t(codes.view(np.uint8)), _t(idx), rlxq.MLX_AFFINE8, n, E, group=group,
+                               scales=_t(sc), biases=_t(bi))
+        torch.cuda.synchronize()
+        assert ctx.last_kernel.startswith("rlxq_moesk_mlx8_"), ctx.last_kernel
+        got = y.cpu().numpy()
+        for r in range(rows):
+            sl = slice(int(idx[r]) * n, (int(idx[r]) + 1) * n)
+            want = orc.mlx_matmul_f64(xv[r:r + 1], codes[sl], sc[sl], bi[sl], n, 8, group)
+            assert rel_err(got[r:r + 1], want) <= TOL, r
+    else:
+        sl = slice(0, n)
+        y = ctx.dequant_matmul(xt, _t(codes[sl].view(np.uint8)), rlxq.MLX_AFFINE8, n, group=group,
+                               scales=_t(sc[sl]), biases=_t(bi[sl]))
+        torch.cuda.synchronize()
+        assert ctx.last_kernel.startswith("rlxq_skinny"), ctx.last_kernel
+        want = orc.mlx_matmul_f64(xv, codes[sl], sc[sl], bi[sl], n, 8, group)
+        assert rel_err(y.cpu().numpy(), want) <= TOL

@@ -152,15 +152,15 @@ def test_q4k_prefill_gemm(ctx, orc, monkeypatch, mkn, tile):
 
 @pytest.mark.parametrize("xdt", ["bf16", "f32"])
 def test_q4k_f32_output_prefill_on_f16_gemm(ctx, orc, xdt):
-    """f32 output past 256 rows takes the f16 GEMM (sub-blocks normalised to
-    the Q4_1 form, d*sc and -dmin*mn rounded to f16 once), within the 1e-3
-    bar; f32 activations as hi/lo row pairs."""
+    """f32 output past 256 rows takes the exact GEMM (each weight's f32 value
+    d*sc*q - dmin*mn as f16 hi + lo), within the 1e-3 bar; f32 activations
+    as hi/lo row pairs."""
     m, k, n = 300, 1024, 200
     rng = np.random.default_rng(5)
     packed = orc.synth_q4_k(rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, want = _run(ctx, orc, x, packed, n, xdt=xdt)
-    assert ctx.last_kernel == "rlxq_gemm_q4_k_t256w8p2f", ctx.last_kernel
+    assert ctx.last_kernel == "rlxq_gemm_q4_k_t256w8p2x", ctx.last_kernel
     assert rel_err(got, want) <= TOL
 
 

@@ -1,7 +1,7 @@
 """Parity of the batched-decode (small M) dequant-GEMM against the CPU oracle,
-through the C ABI: f16 weights (one rounding of d*q + m) and bf16 activations
-(exact in f16 after power-of-two row scaling) on f16 MFMA with fp32
-accumulation.  f32 activations run as hi + lo f16 row pairs (see
+through the C ABI: exact weights (f16 hi + lo operands, the min / bias term
+on block sums) and bf16 activations (exact in f16 after power-of-two row
+scaling) on f16 MFMA with fp32 accumulation.  f32 activations run as hi + lo f16 row pairs (see
 test_f32_activations_take_the_skinny_kernels and tests/test_f32_contract_gpu.py).  Bar: max|got - want| / max|want| <= 1e-3 (f32 output), 1e-2
 (bf16 output), `want` the oracle's dequantized weights contracted in float64."""
 import numpy as np
@@ -68,18 +68,15 @@ def test_skinny_activation_range(ctx, orc, scheme):
         assert rel_err(got[r:r + 1], want[r:r + 1]) <= TOL_F32, r
 
 
-STAGINGS = {"default": {}, "register": {"RLXQ_SKINNY_NS": "0"},
-            "lds": {"RLXQ_SKINNY_XR": "0", "RLXQ_SKINNY_DMA": "0"},
-            "dma": {"RLXQ_SKINNY_XR": "0", "RLXQ_SKINNY_DMA": "1"}}
-KERNEL_PREFIX = {"register": "rlxq_skinnyxr_", "lds": "rlxq_skinny_q4_1_mt", "dma": "rlxq_skinny_q4_1_mt"}
+STAGINGS = {"default": {}, "register": {"RLXQ_SKINNY_NS": "0"}}
+KERNEL_PREFIX = {"register": "rlxq_skinnyxr_"}
 
 
 @pytest.mark.parametrize("staging", list(STAGINGS))
 @pytest.mark.parametrize("mkn", [(5, 256, 136), (16, 4096, 512), (33, 768, 200), (64, 1024, 128)], ids=str)
 def test_skinny_q4_1_every_staging(ctx, orc, monkeypatch, staging, mkn):
     """Q4_1 through the default choice (register-streamed up to 16 rows,
-    N-split above), the register-streamed kernel (no LDS stage), the
-    register-staged LDS kernel and the LDS-DMA-staged kernel."""
+    N-split above) and the register-streamed kernel (no LDS stage)."""
     for key, val in STAGINGS[staging].items():
         monkeypatch.setenv(key, val)
     m, k, n = mkn
@@ -90,7 +87,6 @@ def test_skinny_q4_1_every_staging(ctx, orc, monkeypatch, staging, mkn):
     got, want = run_dense(ctx, orc, 3, x, packed, n, xdt="bf16")
     prefix = KERNEL_PREFIX.get(staging, "rlxq_skinnyxr_" if m <= 16 else "rlxq_skinnyns_q4_1_")
     assert ctx.last_kernel.startswith(prefix), ctx.last_kernel
-    assert ctx.last_kernel.endswith("_dma") == (staging == "dma"), ctx.last_kernel
     assert rel_err(got, want) <= TOL_F32
 
 
@@ -130,20 +126,17 @@ def test_f32_activations_take_the_skinny_kernels(ctx, orc, monkeypatch):
     assert rel_err(got, want) <= TOL_F32
 
 
-@pytest.mark.parametrize("kernel", ["register", "lds"])
 @pytest.mark.parametrize("scheme", [1, 2])
-def test_skinny_q8_0_q4_0_both_kernels(ctx, orc, monkeypatch, scheme, kernel):
+def test_skinny_q8_0_q4_0_register_kernel(ctx, orc, scheme):
     """Q8_0 (34-byte blocks) and Q4_0 (18-byte blocks) through the
-    register-streamed kernel and the LDS-staged one."""
-    if kernel == "lds":
-        monkeypatch.setenv("RLXQ_SKINNY_XR", "0")
+    register-streamed kernel."""
     for (m, k, n) in [(6, 256, 40), (16, 2048, 300), (40, 640, 96), (64, 4096, 130)]:
-        announce(f"skinny scheme={scheme} kernel={kernel} {(m, k, n)}")
+        announce(f"skinny scheme={scheme} {(m, k, n)}")
         rng = np.random.default_rng(scheme * 100 + m + k)
         packed = orc.synth(scheme, rng, n, k)
         x = rng.standard_normal((m, k)).astype(np.float32)
         got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt="bf16")
-        assert ctx.last_kernel.startswith("rlxq_skinnyxr_" if kernel == "register" else "rlxq_skinny_"), ctx.last_kernel
+        assert ctx.last_kernel.startswith("rlxq_skinnyxr_"), ctx.last_kernel
         assert rel_err(got, want) <= TOL_F32, (m, k, n)
 
 

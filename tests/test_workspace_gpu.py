@@ -1,6 +1,8 @@
 """Context scratch across HIP graph capture: a buffer that growth replaces
-stays valid for graphs captured before (it is retired, not freed, until
-rlxq_release_stream / rlxq_destroy), and reserve / release work per stream."""
+stays valid for graphs captured before (one used under capture is retired,
+not freed, until rlxq_release_stream / rlxq_destroy), reserve / release work
+per stream, and an ascending run of sizes grows the scratch geometrically
+and frees the replaced buffers once their work is done."""
 import numpy as np
 import pytest
 
@@ -66,3 +68,45 @@ def test_graph_replay_after_scratch_growth(ctx, orc):
     s.synchronize()
     assert torch.equal(y2, y_eager)
     ctx.release_stream(stream=s.cuda_stream)
+
+
+def test_ascending_sizes_grow_geometrically_and_free_retired(ctx, orc):
+    """A chunked-prefill-like run of ascending M on one stream (batched-decode
+    kernels: prepared activations and split-K partials in the scratch): the
+    scratch grows by at least half each time, so the count of growths stays
+    logarithmic, and the buffers it replaced (never used under capture) are
+    freed by later calls once their work has finished."""
+    import torch
+    import rlxq
+
+    rng = np.random.default_rng(5)
+    k, n = 12288, 256                 # small N, long K: split-K partials
+    packed = orc.synth_q4_1(rng, n, k)
+    w = torch.from_numpy(packed).cuda()
+    s = torch.cuda.Stream()
+    sp = s.cuda_stream
+    sizes, growths = [], 0
+    with torch.cuda.stream(s):
+        for m in range(5, 257, 3):
+            announce(f"workspace ascending m={m}")
+            x = torch.randn((m, k), device="cuda").to(torch.bfloat16)
+            ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_1, n)
+            b = ctx.workspace_bytes(stream=sp)
+            if sizes and b > sizes[-1]:
+                growths += 1
+                assert b >= sizes[-1] * 3 // 2, (m, b, sizes[-1])
+            sizes.append(b)
+            # replaced buffers never exceed twice the live one
+            assert ctx.workspace_retired_bytes(stream=sp) < 2 * b
+    s.synchronize()
+    assert growths <= 12, growths
+    # once the stream's work is done, the next call frees every retired buffer
+    with torch.cuda.stream(s):
+        x = torch.randn((5, k), device="cuda").to(torch.bfloat16)
+        y = ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_1, n)
+    s.synchronize()
+    assert ctx.workspace_retired_bytes(stream=sp) == 0
+    want = orc.matmul_f64(orc.Q4_1, x.float().cpu().numpy(), packed, n)
+    assert float(np.max(np.abs(y.cpu().numpy() - want)) / np.max(np.abs(want))) <= 1e-3
+    ctx.release_stream(stream=sp)
+    assert ctx.workspace_retired_bytes(stream=sp) == 0
