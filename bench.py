@@ -26,6 +26,14 @@ Extra keys of the same JSON line:
   moe_q4_k        the same with Q4_K expert banks (a Q4_K_M MoE checkpoint)
   moe_prefill     the config-5 layer at 256 tokens (grouped MFMA kernels)
   q8_gemv         config 1: Q8_0 2048->2048, f32 activations
+  measured_peaks  this GPU's copy and streaming-read bandwidth and register-
+                  only bf16 MFMA rate (rlxq_peak_probe); roofline and
+                  prefill_roofline also give their fraction of these
+  f32_contract_decode  the decode step with F32 x and y (the reference
+                  operator's operand types); prefill.f32_contract likewise
+Every section's per-call time is the smaller of an eager run and a HIP-graph
+replay of the same launches (both reported), so no figure is the
+interpreter's issue rate.
   gguf_upload     a 537 MB GGUF checkpoint streamed from the page cache to HBM
   cpu_baseline    the C restatement of the reference CPU algorithm timed on
                   this host's cores over bounded samples: config 2 on all
@@ -83,14 +91,13 @@ def synth_q8_0_gpu(n: int, k: int, gen):
 
 def measured_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (scaled by the plain-copy calibration), or None."""
-    path = ROOT / "profiles" / "gemv_q4_1_m1_qwen3_8b_traffic.md"
-    if not path.exists():
-        return None
-    for line in path.read_text().splitlines():
-        f = line.split()
-        if len(f) == 3 and f[0] == "traffic-bytes-per-launch" and f[1] == kernel:
-            return int(f[2])
+    WRITE_SIZE summaries under profiles/ (scaled by the plain-copy
+    calibration; a `traffic-bytes-per-launch <kernel> <bytes>` line), or None."""
+    for path in sorted((ROOT / "profiles").glob("*.md")):
+        for line in path.read_text().splitlines():
+            f = line.split()
+            if len(f) == 3 and f[0] == "traffic-bytes-per-launch" and f[1] == kernel:
+                return int(f[2])
     return None
 
 
@@ -191,16 +198,24 @@ def cpu_baseline(seconds: float = 16.0) -> dict:
 
 
 # ---------------------------------------------------------------- sections
-def _graph_time_us(launch, count: int, stream) -> float:
+def _graph_time_us(ctx, launch, count: int, stream) -> float:
     """Mean microseconds per launch of `count` back-to-back launches recorded
     once into a HIP graph and replayed (HIP events around the replay): the
     GPU-side duration of a launch, free of the interpreter's per-call cost.
-    launch(i, stream_ptr) issues launch i on the given stream."""
+    launch(i, stream_ptr) issues launch i on the given stream.  The capture
+    stream gets the launch stream's scratch size first (nothing allocates
+    under capture) and one eager launch; its scratch is released after."""
     import torch
 
     g = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream()
+    need = ctx.workspace_bytes(stream=stream.cuda_stream)
+    if need:
+        ctx.reserve_workspace(need, stream=cap.cuda_stream)
     cap.wait_stream(stream)
+    with torch.cuda.stream(cap):
+        launch(0, cap.cuda_stream)
+    cap.synchronize()
     with torch.cuda.graph(g, stream=cap):
         sp = torch.cuda.current_stream().cuda_stream
         for i in range(count):
@@ -216,7 +231,66 @@ def _graph_time_us(launch, count: int, stream) -> float:
         ev1.synchronize()
         best = min(best, ev0.elapsed_time(ev1) * 1e3 / count)
     del g
+    torch.cuda.synchronize()
+    ctx.release_stream(stream=cap.cuda_stream)
     return best
+
+
+def _gpu_us(ctx, launch, count: int, stream) -> dict:
+    """GPU microseconds per launch: the smaller of an eager run of `count`
+    launches issued from this interpreter and a HIP-graph replay of the same
+    launches (which carries no host cost per launch), HIP events on the
+    launch stream; both reported.  The eager figure alone is bounded by the
+    interpreter for kernels of a few microseconds."""
+    sptr = stream.cuda_stream
+    us_eager = min(_time_us(lambda i: launch(i, sptr), count, stream) for _ in range(2))
+    us_graph = _graph_time_us(ctx, launch, count, stream)
+    return {"us": min(us_eager, us_graph), "us_eager": round(us_eager, 3), "us_graph": round(us_graph, 3)}
+
+
+def peaks_section(ctx, stream) -> dict:
+    """Measured peaks on this GPU, beside the data-sheet ones: a 1 GiB
+    device-to-device copy (read + write bytes), a 2 GiB streaming read with
+    16-byte loads (rlxq_peak_probe READ: the access pattern of the weight
+    streams), and register-only v_mfma_f32_32x32x16_bf16 (rlxq_peak_probe
+    MFMA).  Best of five timed runs each."""
+    import torch
+    import rlxq
+
+    sptr = stream.cuda_stream
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def best_ms(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        b = float("inf")
+        for _ in range(reps):
+            ev0.record(stream)
+            fn()
+            ev1.record(stream)
+            ev1.synchronize()
+            b = min(b, ev0.elapsed_time(ev1))
+        return b
+
+    n = 1 << 30
+    src = torch.ones(n // 4, device="cuda")
+    dst = torch.empty_like(src)
+    copy_ms = best_ms(lambda: dst.copy_(src))
+    del src, dst
+    rb = 2 << 30
+    buf = torch.ones(rb // 4, device="cuda")
+    sink = torch.empty(1 << 16, dtype=torch.int32, device="cuda")
+    read_ms = best_ms(lambda: ctx.peak_probe(rlxq.PROBE_READ, rb, buf=buf, sink=sink, stream=sptr))
+    del buf
+    iters = 20000
+    flops = ctx.peak_probe(rlxq.PROBE_MFMA, iters, sink=sink, stream=sptr)
+    mfma_ms = best_ms(lambda: ctx.peak_probe(rlxq.PROBE_MFMA, iters, sink=sink, stream=sptr))
+    torch.cuda.empty_cache()
+    return {"hbm_copy_GBps": round(2 * n / copy_ms / 1e6, 1),
+            "hbm_read_GBps": round(rb / read_ms / 1e6, 1),
+            "mfma_bf16_TFLOPs": round(flops / mfma_ms / 1e9, 1),
+            "copy": "1 GiB torch copy_, read + write bytes", "read": "2 GiB, rlxq_probe_read (16-byte loads)",
+            "mfma": "rlxq_probe_mfma: 4 independent v_mfma_f32_32x32x16_bf16 chains per wave, 32 waves per CU"}
 
 
 def decode_roofline(ctx, layers, xs, ys, calls, stream, reps: int) -> tuple[dict, dict]:
@@ -239,7 +313,7 @@ def decode_roofline(ctx, layers, xs, ys, calls, stream, reps: int) -> tuple[dict
             calls[name][i % LAYERS]()
         launch(0, stream.cuda_stream)
         kern = ctx.last_kernel
-        us_graph = _graph_time_us(launch, reps * LAYERS, stream)
+        us_graph = _graph_time_us(ctx, launch, reps * LAYERS, stream)
         us_eager = min(_time_us(run, reps * LAYERS, stream) for _ in range(2))
         us = min(us_graph, us_eager)
         b = gemv_bytes(k, n)
@@ -267,7 +341,7 @@ def prefill_section(ctx, gen, sptr, stream, quick: bool) -> dict:
     import torch
     import rlxq
 
-    res = {"q4_1": {}, "q4_k": {}, "w8a8": {}}
+    res = {"q4_1": {}, "q4_k": {}, "w8a8": {}, "f32_contract": {}}
     ms_list = (4096,) if quick else (512, 2048, 4096)
     for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):
         w = synth_q4_1_gpu(n, k, gen)
@@ -295,6 +369,22 @@ def prefill_section(ctx, gen, sptr, stream, quick: bool) -> dict:
         tf = 2.0 * m * n * k / us / 1e6
         res["q4_k"][f"{name}_m{m}"] = {"m": m, "k": k, "n": n, "kernel": ctx.last_kernel, "us": round(us, 1),
                                        "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+        # the reference operator's own operand types (F32 x in, F32 y out):
+        # the exact variant on hi/lo activation rows, Q4_K and Q4_1
+        for sname, sch, wt in (("q4_k", rlxq.GGUF_Q4_K, w), ("q4_1", rlxq.GGUF_Q4_1, None)):
+            if wt is None:
+                wt = synth_q4_1_gpu(n, k, gen)
+            x32 = torch.randn((m, k), generator=gen, device="cuda")
+            y32 = torch.empty((m, n), device="cuda")
+            run = lambda i: ctx.dequant_matmul(x32, wt, sch, n, y=y32, stream=sptr)
+            run(0)
+            torch.cuda.synchronize()
+            us = _time_us(run, 3, stream)
+            tf = 2.0 * m * n * k / us / 1e6
+            res["f32_contract"][f"{sname}_{name}_m{m}"] = {"m": m, "k": k, "n": n, "kernel": ctx.last_kernel,
+                                                          "us": round(us, 1), "TFLOPs": round(tf, 1),
+                                                          "x": "f32", "y": "f32"}
+            del x32, y32, wt
         del w, x, y
         m = 4096
         wq = torch.randint(-127, 128, (k, n), device="cuda", dtype=torch.int8, generator=gen)
@@ -322,7 +412,17 @@ def prefill_headline(detail: dict) -> dict:
     gu, dn = q["gate_up_m4096"], q["down_m4096"]
     flops = 2.0 * 4096 * (gu["n"] * gu["k"] + dn["n"] * dn["k"])
     tf = flops / (gu["us"] + dn["us"]) / 1e6
+    fc = detail["f32_contract"]
+    f32 = {}
+    for sname in ("q4_1", "q4_k"):
+        a, b = fc.get(f"{sname}_gate_up_m4096"), fc.get(f"{sname}_down_m4096")
+        if a and b:
+            f32[f"{sname}_TFLOPs"] = round(flops / (a["us"] + b["us"]) / 1e6, 1)
+            f32[f"{sname}_kernel"] = a["kernel"]
     return {"TFLOPs": round(tf, 1), "unit": "TFLOP/s", "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+            "f32_contract": dict(f32, workload="the same two shapes with F32 x and F32 y (the reference "
+                                               "operator's operand types): exact f16 hi + lo weights, x as "
+                                               "hi + lo f16 rows"),
             "workload": "Q4_1 group-32 dequant-GEMM, bf16 x and y, f32 accumulate, M=4096: Qwen3-8B gate_up "
                         "4096->24576 + down 12288->4096",
             "kernel": gu["kernel"], "gate_up_m4096_TFLOPs": gu["TFLOPs"], "down_m4096_TFLOPs": dn["TFLOPs"],
@@ -355,22 +455,25 @@ def batched_section(ctx, gen, sptr, stream) -> dict:
                 x = torch.randn((m, k), generator=gen, device="cuda").to(torch.bfloat16)
                 y = torch.empty((m, n), device="cuda")
 
-                def run(i, x=x, y=y, ws=ws, scheme=scheme, n=n):
+                def run(i, sp=sptr, x=x, y=y, ws=ws, scheme=scheme, n=n):
                     w = ws[i % len(ws)]
                     if isinstance(w, tuple) and len(w) == 3:
                         return ctx.dequant_matmul(x, w[0], scheme, n, group=64, scales=w[1], biases=w[2], y=y,
-                                                  stream=sptr)
+                                                  stream=sp)
                     if isinstance(w, tuple):
-                        return ctx.dequant_matmul(x, w[0], scheme, n, scales=w[1], y=y, stream=sptr)
-                    return ctx.dequant_matmul(x, w, scheme, n, y=y, stream=sptr)
+                        return ctx.dequant_matmul(x, w[0], scheme, n, scales=w[1], y=y, stream=sp)
+                    return ctx.dequant_matmul(x, w, scheme, n, y=y, stream=sp)
                 for i in range(len(ws)):
                     run(i)
                 torch.cuda.synchronize()
-                us = _time_us(run, 4 * len(ws), stream)
+                kern = ctx.last_kernel
+                t = _gpu_us(ctx, run, 4 * len(ws), stream)
+                us = t["us"]
                 b = gemv_bytes(k, n, m=m, bpw=bpw)
-                res[f"{sname}_{name}_m{m}"] = {"kernel": ctx.last_kernel, "us": round(us, 2),
+                res[f"{sname}_{name}_m{m}"] = {"kernel": kern, "us": round(us, 2),
                                                "GBps": round(b / us / 1e3, 1),
-                                               "TFLOPs": round(2.0 * m * n * k / us / 1e6, 2)}
+                                               "TFLOPs": round(2.0 * m * n * k / us / 1e6, 2),
+                                               "us_eager": t["us_eager"], "us_graph": t["us_graph"]}
             del ws
             torch.cuda.empty_cache()
     return res
@@ -473,38 +576,41 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
 
     def measure(label, wbytes, make, call):
         ws = [make() for _ in range(_copies(wbytes))]
-        run = lambda i: call(ws[i % len(ws)])
+        run = lambda i, sp=sptr: call(ws[i % len(ws)], sp)
         for i in range(len(ws)):
             run(i)
         torch.cuda.synchronize()
-        us = _time_us(run, 4 * len(ws), stream)
+        kern = ctx.last_kernel
+        t = _gpu_us(ctx, run, 4 * len(ws), stream)
+        us = t["us"]
         b = wbytes + k * 2 + n * 4
-        res[label] = {"kernel": ctx.last_kernel, "us": round(us, 2), "GBps": round(b / us / 1e3, 1),
-                      "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        res[label] = {"kernel": kern, "us": round(us, 2), "GBps": round(b / us / 1e3, 1),
+                      "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "us_eager": t["us_eager"],
+                      "us_graph": t["us_graph"]}
         del ws
         torch.cuda.empty_cache()
 
     measure("q4_0_gemv_m1", n * k * 18 / 32, lambda: synth_q4_0_gpu(n, k, gen),
-            lambda w: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_0, n, y=y, stream=sptr))
+            lambda w, sp: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_0, n, y=y, stream=sp))
     measure("q4_k_gemv_m1", n * k * 144 / 256, lambda: synth_q4_k_gpu(n, k, gen),
-            lambda w: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_K, n, y=y, stream=sptr))
+            lambda w, sp: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_K, n, y=y, stream=sp))
     measure("q6_k_gemv_m1", n * k * 210 / 256, lambda: synth_q6_k_gpu(n, k, gen),
-            lambda w: ctx.dequant_matmul(x, w, rlxq.GGUF_Q6_K, n, y=y, stream=sptr))
+            lambda w, sp: ctx.dequant_matmul(x, w, rlxq.GGUF_Q6_K, n, y=y, stream=sp))
     for name, sch, sb in (("q5_k", rlxq.GGUF_Q5_K, 176), ("q3_k", rlxq.GGUF_Q3_K, 110),
                           ("q2_k", rlxq.GGUF_Q2_K, 84), ("q8_k", rlxq.GGUF_Q8_K, 292)):
         measure(f"{name}_gemv_m1", n * k * sb / 256, lambda name=name: synth_kq_gpu(name, n, k, gen),
-                lambda w, sch=sch: ctx.dequant_matmul(x, w, sch, n, y=y, stream=sptr))
+                lambda w, sp, sch=sch: ctx.dequant_matmul(x, w, sch, n, y=y, stream=sp))
     for bits in (4, 8):
         wb = n * k * bits / 8 + 2 * n * (k // 64) * 2
         measure(f"mlx{bits}_g64_gemv_m1", wb, lambda bits=bits: synth_mlx_gpu(n, k, bits, 64, gen),
-                lambda w, bits=bits: ctx.dequant_matmul(x, w[0], rlxq.MLX_AFFINE4 if bits == 4 else rlxq.MLX_AFFINE8,
-                                                        n, group=64, scales=w[1], biases=w[2], y=y, stream=sptr))
+                lambda w, sp, bits=bits: ctx.dequant_matmul(x, w[0], rlxq.MLX_AFFINE4 if bits == 4 else rlxq.MLX_AFFINE8,
+                                                        n, group=64, scales=w[1], biases=w[2], y=y, stream=sp))
     measure("mxfp4_gemv_m1", n * k / 2 + n * k / 32, lambda: synth_mxfp4_gpu(n, k, gen),
-            lambda w: ctx.dequant_matmul(x, w[0], rlxq.MLX_MXFP4, n, scales=w[1], y=y, stream=sptr))
+            lambda w, sp: ctx.dequant_matmul(x, w[0], rlxq.MLX_MXFP4, n, scales=w[1], y=y, stream=sp))
     measure("int8_block_gemv_m1", n * k + n * 4,
             lambda: (torch.randint(-127, 128, (k, n), device="cuda", dtype=torch.int8, generator=gen),
                      torch.rand((n,), device="cuda", generator=gen) * 0.01 + 1e-4),
-            lambda w: ctx.dequant_matmul(x, w[0], rlxq.INT8_BLOCK, n, group=k, scales=w[1], y=y, stream=sptr))
+            lambda w, sp: ctx.dequant_matmul(x, w[0], rlxq.INT8_BLOCK, n, group=k, scales=w[1], y=y, stream=sp))
 
     # MLX 4-bit grouped op: 128 (token, slot) rows over 128 experts of the
     # MoE gate|up shape 2048->1536 (two banks alternate, 452 MB > MALL)
@@ -513,12 +619,12 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
     xg = torch.randn((R, H), generator=gen, device="cuda").to(torch.bfloat16)
     idx = torch.randint(0, E, (R,), device="cuda", generator=gen).float()
     yg = torch.empty((R, N2), device="cuda")
-    run = lambda i: ctx.grouped_matmul(xg, banks[i % 2][0], idx, rlxq.MLX_AFFINE4, N2, E, group=64,
-                                       scales=banks[i % 2][1], biases=banks[i % 2][2], y=yg, stream=sptr)
+    run = lambda i, sp=sptr: ctx.grouped_matmul(xg, banks[i % 2][0], idx, rlxq.MLX_AFFINE4, N2, E, group=64,
+                                                scales=banks[i % 2][1], biases=banks[i % 2][2], y=yg, stream=sp)
     run(0)
     run(1)
     torch.cuda.synchronize()
-    us = _time_us(run, 20, stream)
+    us = _gpu_us(ctx, run, 20, stream)["us"]
     uniq = int(torch.unique(idx).numel())
     b = uniq * (N2 * H / 2 + 2 * N2 * (H // 64) * 2) + R * H * 2 + R * N2 * 4
     res["mlx4_grouped_gate_up"] = {"kernel": ctx.last_kernel, "us": round(us, 2), "unique_experts": uniq,
@@ -528,12 +634,12 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
     torch.cuda.empty_cache()
     # the same with MXFP4 experts (codes + decoded bf16 scales, no bias slab)
     banks = [synth_mxfp4_gpu(E * N2, H, gen, decoded=True) for _ in range(2)]
-    run = lambda i: ctx.grouped_matmul(xg, banks[i % 2][0], idx, rlxq.MLX_MXFP4, N2, E, scales=banks[i % 2][1],
-                                       y=yg, stream=sptr)
+    run = lambda i, sp=sptr: ctx.grouped_matmul(xg, banks[i % 2][0], idx, rlxq.MLX_MXFP4, N2, E,
+                                                scales=banks[i % 2][1], y=yg, stream=sp)
     run(0)
     run(1)
     torch.cuda.synchronize()
-    us = _time_us(run, 20, stream)
+    us = _gpu_us(ctx, run, 20, stream)["us"]
     b = uniq * (N2 * H / 2 + N2 * (H // 32) * 2) + R * H * 2 + R * N2 * 4
     res["mxfp4_grouped_gate_up"] = {"kernel": ctx.last_kernel, "us": round(us, 2), "unique_experts": uniq,
                                     "GBps": round(b / us / 1e3, 1),
@@ -544,10 +650,10 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
     # dequantisation to f32 (bytes: packed rows read + f32 written)
     wq = [synth_q4_1_gpu(n, k, gen) for _ in range(2)]
     out = torch.empty((n, k), device="cuda")
-    run = lambda i: ctx.dequantize(wq[i % 2], rlxq.GGUF_Q4_1, n, k, out=out, stream=sptr)
+    run = lambda i, sp=sptr: ctx.dequantize(wq[i % 2], rlxq.GGUF_Q4_1, n, k, out=out, stream=sp)
     run(0)
     torch.cuda.synchronize()
-    us = _time_us(run, 10, stream)
+    us = _gpu_us(ctx, run, 10, stream)["us"]
     b = n * k * Q4_1_BPW + n * k * 4
     res["dequantize_q4_1_f32"] = {"kernel": ctx.last_kernel, "us": round(us, 2), "GBps": round(b / us / 1e3, 1),
                                   "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
@@ -576,24 +682,27 @@ def moe_section(ctx, gen, sptr, stream, scheme: str = "q4_1", tokens: int = 16) 
     y = torch.empty((T, H), device="cuda")
     routes = [None, None]
 
-    def layer(i):
+    def layer(i, sp=sptr):
         bgu, bdn = banks[i % 2]
-        ids, probs = ctx.moe_route(logits[i % 2], TOPK, True, stream=sptr)
+        ids, probs = ctx.moe_route(logits[i % 2], TOPK, True, stream=sp)
         routes[i % 2] = ids
-        ctx.moe_grouped(x, bgu, ids, probs, sch, rlxq.MOE_EXPAND_SWIGLU, 2 * I, E, y=act, stream=sptr)
-        ctx.moe_grouped(act, bdn, ids, probs, sch, rlxq.MOE_COMBINE, H, E, y=y, stream=sptr)
+        ctx.moe_grouped(x, bgu, ids, probs, sch, rlxq.MOE_EXPAND_SWIGLU, 2 * I, E, y=act, stream=sp)
+        ctx.moe_grouped(act, bdn, ids, probs, sch, rlxq.MOE_COMBINE, H, E, y=y, stream=sp)
 
     for i in range(4):
         layer(i)
     torch.cuda.synchronize()
-    us = _time_us(layer, 40, stream)
     uniq = [int(torch.unique(r).numel()) for r in routes]
+    kern_down = ctx.last_kernel
+    t = _gpu_us(ctx, layer, 40, stream)
+    us = t["us"]
     u = sum(uniq) / len(uniq)
     per_expert = 2 * I * H * bpw + H * I * bpw
     b = u * per_expert + T * H * 2 + T * TOPK * I * 2 * 2 + T * H * 4
     out = {"tokens": T, "us_per_layer": round(us, 2), "unique_experts": u, "GBps": round(b / us / 1e3, 1),
            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-           "bytes_model": f"unique experts x {int(per_expert):,} B + activations", "kernel_down": ctx.last_kernel}
+           "bytes_model": f"unique experts x {int(per_expert):,} B + activations", "kernel_down": kern_down,
+           "us_eager": t["us_eager"], "us_graph": t["us_graph"]}
     if T <= 64:
         out["launches_per_layer"] = ("route, gate|up + SwiGLU (routing in the workgroups), down and combine in one "
                                      "token-major launch")
@@ -659,12 +768,15 @@ def q8_section(ctx, gen, sptr, stream) -> dict:
     b = gemv_bytes(k, n, bpw=Q8_0_BPW, xsize=4)
     out = {}
     for label, pick in (("warm", lambda i: ws[0]), ("rotated", lambda i: ws[i % len(ws)])):
-        run = lambda i: ctx.dequant_matmul(x, pick(i), rlxq.GGUF_Q8_0, n, y=y, stream=sptr)
+        run = lambda i, sp=sptr: ctx.dequant_matmul(x, pick(i), rlxq.GGUF_Q8_0, n, y=y, stream=sp)
         for i in range(len(ws)):
             run(i)
         torch.cuda.synchronize()
-        us = _time_us(run, 4 * len(ws), stream)
-        out[label] = {"kernel": ctx.last_kernel, "us": round(us, 3), "GBps": round(b / us / 1e3, 1)}
+        kern = ctx.last_kernel
+        t = _gpu_us(ctx, run, 4 * len(ws), stream)
+        us = t["us"]
+        out[label] = {"kernel": kern, "us": round(us, 3), "GBps": round(b / us / 1e3, 1),
+                      "us_eager": t["us_eager"], "us_graph": t["us_graph"]}
     return out
 
 
@@ -678,7 +790,7 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="prefill at M=4096 only")
     ap.add_argument("--cpu-seconds", type=float, default=16.0)
     ap.add_argument("--section", choices=["prefill", "batched", "moe", "moe_q4_k", "moe_prefill", "schemes", "q8",
-                                          "gguf"],
+                                          "gguf", "peaks"],
                     help="profiling mode: run only this section (no decode step, no CPU baseline) and print its "
                          "figures as one JSON object")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -715,7 +827,8 @@ def main() -> int:
                "moe_prefill": lambda: moe_section(ctx, gen, sptr, stream, "q4_1", 256),
                "schemes": lambda: schemes_section(ctx, gen, sptr, stream),
                "q8": lambda: q8_section(ctx, gen, sptr, stream),
-               "gguf": lambda: gguf_section(ctx, gen, sptr, stream)}[a.section]
+               "gguf": lambda: gguf_section(ctx, gen, sptr, stream),
+               "peaks": lambda: peaks_section(ctx, stream)}[a.section]
         print(json.dumps({"section": a.section, "result": run()}), flush=True)
         ctx.close()
         return 0
@@ -750,8 +863,40 @@ def main() -> int:
     value = step_bytes * a.steps / wall / 1e9
 
     roofline, per = decode_roofline(ctx, layers, xs, ys, calls, stream, reps=3)
-    del layers, calls
+
+    # the same step under the reference operator's own operand types: F32
+    # activations in (f32 bytes), F32 output
+    xs32 = {k: torch.randn((1, k), generator=gen, device="cuda") for k in (4096, 12288)}
+    calls32 = {name: [ctx.bind_dequant_matmul(xs32[k], lw[name], rlxq.GGUF_Q4_1, n, y=ys[name], stream=sptr)
+                      for lw in layers] for name, k, n in SHAPES}
+    ctx.dequant_matmul(xs32[4096], layers[0]["o_proj"], rlxq.GGUF_Q4_1, 4096, y=ys["o_proj"], stream=sptr)
+    kern32 = ctx.last_kernel
+    ctx.dequant_matmul(xs32[12288], layers[0]["down"], rlxq.GGUF_Q4_1, 4096, y=ys["down"], stream=sptr)
+    kern32_down = ctx.last_kernel
+
+    def step32():
+        for i in range(LAYERS):
+            for name, _, _ in SHAPES:
+                calls32[name][i]()
+
+    for _ in range(a.warmup):
+        step32()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step32()
+    torch.cuda.synchronize()
+    wall32 = time.perf_counter() - t0
+    step_bytes32 = LAYERS * sum(gemv_bytes(k, n, xsize=4) for _, k, n in SHAPES)
+    f32_step = {"GBps": round(step_bytes32 * a.steps / wall32 / 1e9, 1),
+                "ms_per_step": round(wall32 / a.steps * 1e3, 4),
+                "frac_hbm_peak": round(step_bytes32 * a.steps / wall32 / 1e9 / HBM_PEAK_GBS, 4),
+                "kernel": kern32, "kernel_down": kern32_down,
+                "workload": "the decode step with F32 x [1, K] and F32 y (the reference operator's operand types)"}
+    del layers, calls, calls32, xs32
     torch.cuda.empty_cache()
+    peaks = peaks_section(ctx, stream)
+    roofline["frac_measured_read_peak"] = round(roofline["achieved"] / peaks["hbm_read_GBps"], 4)
 
     out = {
         "metric": "Q4 GEMV HBM GB/s (% peak) at M=1; prefill dequant-GEMM TFLOP/s",
@@ -774,6 +919,8 @@ def main() -> int:
         "us_per_layer": round(sum(p["us"] for p in per.values()), 3),
         "per_shape": per,
         "roofline": roofline,
+        "measured_peaks": peaks,
+        "f32_contract_decode": f32_step,
     }
     if not a.no_extra:
         detail = prefill_section(ctx, gen, sptr, stream, a.quick)
@@ -781,7 +928,11 @@ def main() -> int:
         out["prefill_roofline"] = {"bound": "mfma", "kernel": out["prefill"]["kernel"],
                                    "achieved": out["prefill"]["TFLOPs"], "peak": BF16_PEAK_TFLOPS,
                                    "unit": "TFLOP/s", "frac": out["prefill"]["frac_bf16_peak"],
-                                   "traffic": None}
+                                   "frac_measured_mfma_peak": round(out["prefill"]["TFLOPs"] /
+                                                                    peaks["mfma_bf16_TFLOPs"], 4),
+                                   "traffic": measured_traffic(out["prefill"]["kernel"]),
+                                   "traffic_note": "HBM bytes per launch (mean of the gate_up and down launches) "
+                                                   "from the committed FETCH_SIZE / WRITE_SIZE counters"}
         out["prefill_detail"] = detail
         out["batched_decode"] = batched_section(ctx, gen, sptr, stream)
         out["moe"] = moe_section(ctx, gen, sptr, stream)

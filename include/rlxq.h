@@ -235,6 +235,21 @@ int rlxq_moe_grouped(rlxq_ctx* ctx, int scheme, int mode, const void* x,
                      int64_t k, int64_t n, int64_t num_experts, void* y,
                      int y_dtype, void* stream);
 
+/* Peak probes for the measurement (no counterpart in the reference: they
+ * give the bench its measured denominators besides the data-sheet peaks).
+ *   kind RLXQ_PROBE_MFMA (0): `work` rounds of four independent
+ *     v_mfma_f32_32x32x16_bf16 per wave on register operands, 8 workgroups
+ *     of 4 waves per CU; *count = the flops issued.
+ *   kind RLXQ_PROBE_READ (1): every byte of `buf` [work bytes, 16-byte
+ *     aligned, a multiple of 4096] read once with 16-byte loads; *count =
+ *     work.
+ * sink: device memory of at least 8 x CUs x 4 bytes, written only to keep the
+ * work live.  Time the call with events on `stream`. */
+#define RLXQ_PROBE_MFMA 0
+#define RLXQ_PROBE_READ 1
+int rlxq_peak_probe(rlxq_ctx* ctx, int kind, const void* buf, int64_t work, void* sink, int64_t* count,
+                    void* stream);
+
 /* Router: row softmax of logits [rows, E] (f32), top-k by probability
  * (ties to the lower expert id), optional renormalisation of the kept
  * probabilities (norm_topk_prob, standard_decoder.rs:12634-12661).

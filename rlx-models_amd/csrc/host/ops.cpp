@@ -193,19 +193,23 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // late stores), two for the others.
   const bool split = x_dtype == RLXQ_F32;
   const bool want_exact = split || y_dtype == RLXQ_F32;
+  // (the "...xs" kernels take f32 activations as hi / lo x16 rows)
+  std::string vs = var;
   if (!te && want_exact && has_exact_gemm(scheme))
-    var = scheme == RLXQ_GGUF_Q6_K ? "w8lx"
-          : (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q5_K || scheme == RLXQ_GGUF_Q3_K) ? "w8x"
-                                                                                               : "w8p2x";
-  const bool w8 = tile == 256 && var[0] == 'w';
-  const size_t vl = std::strlen(var);
-  const bool exact = vl > 0 && var[vl - 1] == 'x';
+    vs = scheme == RLXQ_GGUF_Q6_K ? "w8lx"
+         : (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q5_K || scheme == RLXQ_GGUF_Q3_K ||
+            scheme == RLXQ_MLX_AFFINE4) ? "w8x" : "w8p2x";
+  if (split && !vs.empty() && vs.back() == 'x') vs += 's';
+  const bool w8 = tile == 256 && !vs.empty() && vs[0] == 'w';
+  const bool exact = vs.find('x') != std::string::npos;
   if (exact && !has_exact_gemm(scheme))
     return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: MXFP4 has no exact f16 GEMM variant");
-  if (split && !exact) return fail(ctx, RLXQ_E_DTYPE, "dequant_matmul: f32 activations need the exact GEMM variant");
-  // x16 rows: two per output row (hi, lo) for f32 activations; the exact
-  // variant's tiles cover 128 output columns (hi and lo weight rows)
-  const int64_t mr = split ? 2 * m : m;
+  if (split && !(exact && vs.back() == 's'))
+    return fail(ctx, RLXQ_E_DTYPE, "dequant_matmul: f32 activations need the exact GEMM variant");
+  // x16 rows: 64-row blocks of 32 hi and 32 lo rows for f32 activations;
+  // the exact variant's tiles cover 128 output columns (hi and lo weight
+  // rows), and with f32 activations 128 output rows
+  const int64_t mr = split ? (m + 31) / 32 * 64 : m;
   const int64_t tn_cols = exact ? tile / 2 : tile;
   const int64_t tiles_m = (mr + tile - 1) / tile, tiles_n = (n + tn_cols - 1) / tn_cols;
   if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
@@ -218,7 +222,7 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   const int64_t kslice = ((ksteps + splits - 1) / splits) * 64;
   splits = (k + kslice - 1) / kslice;
   char name[64];
-  std::snprintf(name, sizeof name, "rlxq_gemm_%s_t%d%s", scheme_name(scheme), tile, var);
+  std::snprintf(name, sizeof name, "rlxq_gemm_%s_t%d%s", scheme_name(scheme), tile, vs.c_str());
   hipFunction_t fn;
   int rc;
   if ((rc = get_fn(ctx, name, &fn))) return rc;
@@ -231,7 +235,7 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     // prepared f16 activations in natural order (the exact variant's weights
     // are in natural order); MLX's 2^8 weight factor undone in the row factors
     rlxq_x16_args xa;
-    if ((rc = prep_x16(ctx, x, x_dtype, m, k, 0, part_bytes, xa, &part, stream, false, 0, false, split,
+    if ((rc = prep_x16(ctx, x, x_dtype, m, k, 0, part_bytes, xa, &part, stream, false, 0, false, split ? 2 : 0,
                        sk_post_exp(scheme))))
       return rc;
     a.x = xa.x16;
@@ -246,6 +250,7 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   a.biases = biases;
   a.y = y;
   a.M = mr;
+  a.m_out = m;
   a.pairs = split ? 1 : 0;
   a.N = n;
   a.K = k;
@@ -578,6 +583,35 @@ int rlxq_moe_route(rlxq_ctx* ctx, const float* logits, int64_t rows, int64_t num
   int E = (int)num_experts, K = (int)top_k, rn = renorm ? 1 : 0;
   void* args[] = {(void*)&logits, &R, &E, &K, &rn, (void*)&ids, (void*)&probs};
   return launch(ctx, fn, dim3((unsigned)rows), dim3(64), 0, stream, args, name);
+}
+
+int rlxq_peak_probe(rlxq_ctx* ctx, int kind, const void* buf, int64_t work, void* sink, int64_t* count,
+                    void* stream) {
+  if (!ctx) return RLXQ_E_NULL;
+  ctx->last_error.clear();
+  if (!sink || !count) return fail(ctx, RLXQ_E_NULL, "peak_probe: sink and count must be non-null");
+  if (work <= 0) return fail(ctx, RLXQ_E_SHAPE, "peak_probe: work must be positive");
+  DeviceGuard g(ctx->device);
+  const int64_t grid = (int64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256) * 8;
+  hipFunction_t fn;
+  int rc;
+  if (kind == RLXQ_PROBE_MFMA) {
+    if ((rc = get_fn(ctx, "rlxq_probe_mfma", &fn))) return rc;
+    int64_t iters = work;
+    void* args[] = {&iters, &sink};
+    *count = grid * 4 * iters * 4 * 32768;
+    return launch(ctx, fn, dim3((unsigned)grid), dim3(256), 0, stream, args, "rlxq_probe_mfma");
+  }
+  if (kind == RLXQ_PROBE_READ) {
+    if (!buf) return fail(ctx, RLXQ_E_NULL, "peak_probe: buf must be non-null");
+    if (work % 4096 || !aligned(buf, 16)) return fail(ctx, RLXQ_E_ALIGN, "peak_probe: buf 16-byte aligned, 4 KiB multiple");
+    if ((rc = get_fn(ctx, "rlxq_probe_read", &fn))) return rc;
+    int64_t n16 = work / 16;
+    void* args[] = {(void*)&buf, &n16, &sink};
+    *count = work;
+    return launch(ctx, fn, dim3((unsigned)grid), dim3(256), 0, stream, args, "rlxq_probe_read");
+  }
+  return fail(ctx, RLXQ_E_SHAPE, "peak_probe: unknown kind");
 }
 
 }  // extern "C"

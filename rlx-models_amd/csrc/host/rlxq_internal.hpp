@@ -137,10 +137,12 @@ int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream);
 // start of the workspace; `extra` further bytes follow at *rest.  The
 // fragment-major layout holds mp >= m rows (the rows past m zero); out_bf16
 // stores bf16 instead of f16.  split: each row becomes two x16 rows, hi and
-// lo (2m rows; f32 activations keep ~22 significant bits), with a factor each.
+// lo (f32 activations keep ~22 significant bits), with a factor each: rows
+// 2r, 2r + 1 (split 1), or 64-row blocks of 32 hi then 32 lo rows (split 2,
+// row-major; m rounded up to 32, the extra rows zero).
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, int order, size_t extra,
              rlxq_x16_args& xa, char** rest, void* stream, bool frag_major = false, int64_t mp = 0,
-             bool out_bf16 = false, bool split = false, int post_exp = 0);
+             bool out_bf16 = false, int split = 0, int post_exp = 0);
 // Exponent of the extra row factor the f16-MFMA kernels need for a scheme:
 // -8 for MLX affine (their f16 weights are prescaled by 2^8), else 0.
 int sk_post_exp(int scheme);

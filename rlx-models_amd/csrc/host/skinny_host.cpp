@@ -30,9 +30,10 @@ int splits_reduce(rlxq_ctx* ctx, rlxq_skinny_args& a, void* stream) {
 }
 
 int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, int order, size_t extra,
-             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major, int64_t mp, bool out_bf16, bool split,
+             rlxq_x16_args& xa, char** rest, void* stream, bool frag_major, int64_t mp, bool out_bf16, int split,
              int post_exp) {
-  const int64_t rows = split ? 2 * m : m;   // x16 rows that hold data
+  // x16 rows: 2m (split 1), m rounded up to 32 times 2 (split 2), else m
+  const int64_t rows = split == 2 ? (m + 31) / 32 * 64 : (split ? 2 * m : m);
   if (!frag_major || mp < rows) mp = rows;
   // fragment-major: the block sums (one f32 per 32 elements) after inv_s
   const size_t x16_bytes = round256((size_t)(mp * k) * 2), s_bytes = round256((size_t)rows * 4);
@@ -52,7 +53,7 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, in
   xa.nibble_order = order;
   xa.frag_major = frag_major ? 1 : 0;
   xa.out_bf16 = out_bf16 ? 1 : 0;
-  xa.split = split ? 1 : 0;
+  xa.split = split;
   xa.post_exp = post_exp;
   xa.ssum = frag_major ? reinterpret_cast<float*>(wsb + x16_bytes + s_bytes) : nullptr;
   *rest = wsb + x16_bytes + s_bytes + sum_bytes;
@@ -89,7 +90,7 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   int rc;
   const int64_t mp = mch * 16 * MT;
   if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp,
-                     scheme == RLXQ_MLX_MXFP4, split, sk_post_exp(scheme))))
+                     scheme == RLXQ_MLX_MXFP4, split ? 1 : 0, sk_post_exp(scheme))))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);
@@ -154,7 +155,7 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   int rc;
   const int64_t mp = mch * 16 * MT;
   if ((rc = prep_x16(ctx, x, x_dtype, m, k, sk_order(scheme), part_bytes, xa, &rest, stream, true, mp,
-                     scheme == RLXQ_MLX_MXFP4, split, sk_post_exp(scheme))))
+                     scheme == RLXQ_MLX_MXFP4, split ? 1 : 0, sk_post_exp(scheme))))
     return rc;
   rlxq_skinny_args a;
   std::memset(&a, 0, sizeof a);

@@ -148,15 +148,21 @@ RLXQ_DEV void gemm_body(const rlxq_gemm_args& a) {
 // MFMA groups of the current step.
 // EXACT (f16 MFMA, f32 output at the 1e-3 bar on any data): each weight's
 // f32 value, computed with the CPU decoder's arithmetic, is held as an f16
-// hi and lo half in adjacent B rows (B rows 2c, 2c + 1: real column c, so a
-// tile covers 128 real columns); the MFMA then contracts both and the
-// epilogue adds lanes 2c and 2c + 1.  With f16 weights rounded once instead,
-// structured data (the reference's sin / cos parity inputs at K = 1792)
-// already reaches 1.4e-3.  MLX weights are held times 2^8 (undone through
-// the activation row factors) so that small group scales stay normal f16.
-template <int SCH, int WGM, int WGN, int PF, bool F16, bool LATE = false, bool EXACT = false>
+// hi and lo half in B rows 32 apart (B rows 64c' + i and 64c' + 32 + i: real
+// column 32c' + i, so a tile covers 128 real columns and a wave's two 32-row
+// MFMA tiles hold the hi and the lo halves of the same 32 columns); the
+// epilogue adds the two tiles' sums in registers.  SPLITX (f32 activations):
+// the activation rows are prepared the same way, hi and lo rows in 32-row
+// blocks, so a wave's four row tiles are (hi, lo) of two row groups; the
+// lo x lo products (~2^-22 of a term) are skipped, three MFMAs per pair.
+// With f16 weights rounded once instead, structured data (the reference's
+// sin / cos parity inputs at K = 1792) already reaches 1.4e-3.  MLX weights
+// are held times 2^8 (undone through the activation row factors) so that
+// small group scales stay normal f16.
+template <int SCH, int WGM, int WGN, int PF, bool F16, bool LATE = false, bool EXACT = false, bool SPLITX = false>
 RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   static_assert(EXACT == F16, "f16 MFMA runs the exact variant on the prepared f16 activations");
+  static_assert(!SPLITX || EXACT, "hi / lo activation rows on the exact variant");
   constexpr int BM = 256, BN = 256;
   constexpr int NREAL = EXACT ? BN / 2 : BN;   // output columns per tile
   constexpr float WSCALE = (SCH == SCH_MLX4 || SCH == SCH_MLX8) ? 256.f : 1.f;
@@ -196,9 +202,10 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   }
   // weight tile: 256 rows x 2 blocks; thread -> row n0 + (tid & 255), blocks
   // (tid >> 8) + q * (NT / 256)
-  // (EXACT: B row brl holds half brl & 1 of real column n0 + brl / 2)
+  // (EXACT: B row brl holds half (brl >> 5) & 1 of real column
+  // n0 + 32 (brl >> 6) + brl % 32)
   const int brl = tid & 255;
-  const int64_t bcol = n0 + (EXACT ? brl >> 1 : brl);
+  const int64_t bcol = n0 + (EXACT ? ((brl >> 6) << 5) + (brl & 31) : brl);
   const int64_t brow = bcol < a.N ? bcol : a.N - 1;
 
   // Global loads run PF steps ahead of the MFMAs (PF register stages); the
@@ -229,7 +236,7 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
     if constexpr (EXACT) {
       uint32_t hi[16], lo[16];
       conv_blk_f16_split<SCH>(P.b[q], WSCALE, hi, lo);
-      const bool low = brl & 1;
+      const bool low = (brl >> 5) & 1;
 #pragma unroll
       for (int i = 0; i < 4; i++)
         *reinterpret_cast<uint4*>(dst + 8 * i) =
@@ -265,7 +272,9 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; j++)
+          if (!(SPLITX && (i & 1) && (j & 1)))   // (lo activations x lo weights: skipped)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     } else {
       bf16x8_t af[TM], bfr[TN];
 #pragma unroll
@@ -350,33 +359,28 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   // per-element form cost 8% of the kernel at M=4096).
   const int64_t mb = m0 + wm * WM + 4 * (lane >> 5);   // the lane's first row
   if constexpr (EXACT) {
-    // B rows 2c (hi) and 2c + 1 (lo) sit in lanes j, j ^ 1 of a 32x32 tile:
-    // one DPP swap adds them (quad_perm [1, 0, 3, 2]) and the even lane
-    // stores real column c; with pairs, x16 rows 2r, 2r + 1 (a lane's
-    // registers r, r + 1) add into output row r as well.
-    const bool pr = a.pairs != 0;
-    const int64_t mo_rows = pr ? a.M >> 1 : a.M, mbo = pr ? mb >> 1 : mb;
-    const int64_t nbo = n0 + ((wn * WN + (lane & 31)) >> 1);   // real column of tile 0
-    const bool even = (lane & 1) == 0;
-    const bool whole = m0 + BM <= a.M && n0 + NREAL <= a.N;
+    static_assert(TN == 2 && WN == 64, "a wave's two column tiles are the hi and lo halves of 32 columns");
+    // Output: the wave's 32 real columns n0 + 32 wn + (lane & 31); rows of
+    // row tile i (or, with SPLITX, of row group g = tiles 2g (hi), 2g + 1
+    // (lo)).  C[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2), reg
+    // 4*(i/8) + i%4.
+    constexpr int RT = SPLITX ? TM / 2 : TM;          // output row tiles per wave
+    const int64_t m0r = SPLITX ? (int64_t)tm * (BM / 2) : m0;   // first output row of the tile
+    const int64_t mbo = m0r + wm * (WM / (SPLITX ? 2 : 1)) + 4 * (lane >> 5);
+    const int64_t nbo = n0 + wn * (WN / 2) + (lane & 31);
+    const bool whole = m0r + (SPLITX ? BM / 2 : BM) <= a.m_out && n0 + NREAL <= a.N;
     auto epx = [&](auto put, auto checked) {
-      static_for<TM>([&](auto I) {
-        static_for<TN>([&](auto J) {
-          f32x16_t v = acc[I.value][J.value];
+      static_for<RT>([&](auto G) {
+        constexpr int g = G.value;
+        const f32x16_t v = SPLITX ? acc[2 * g][0] + acc[2 * g + 1][0] + acc[2 * g][1] : acc[g][0] + acc[g][1];
+        // the row factor of the tile's (hi) x16 rows
+        const int64_t mp = m0 + wm * WM + (SPLITX ? 64 * g : 32 * g) + 4 * (lane >> 5);
 #pragma unroll
-          for (int r = 0; r < 16; r++)
-            v[r] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[r]), 0xB1, 0xF, 0xF, true));
-          if (even) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-              if (pr && (r & 1)) continue;
-              constexpr int dn = J.value * 16;
-              const int dm = I.value * 32 + 8 * (r / 4) + (r % 4);
-              const float o = (pr ? v[r] + v[r < 15 ? r + 1 : r] : v[r]) * a.inv_s[mb + dm];
-              if (!checked.value || (mb + dm < a.M && nbo + dn < a.N)) put(pr ? dm >> 1 : dm, dn, o);
-            }
-          }
-        });
+        for (int r = 0; r < 16; r++) {
+          const int dm = 32 * g + 8 * (r / 4) + (r % 4);
+          const float o = v[r] * a.inv_s[mp + 8 * (r / 4) + (r % 4)];
+          if (!checked.value || (mbo + dm < a.m_out && nbo < a.N)) put(dm, o);
+        }
       });
     };
     auto epx_any = [&](auto put) {
@@ -384,14 +388,14 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
       else epx(put, std::true_type{});
     };
     if (a.splits > 1) {
-      float* p = a.part + ((int64_t)sp * mo_rows + mbo) * a.N + nbo;
-      epx_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.N + dn] = o; });
+      float* p = a.part + ((int64_t)sp * a.m_out + mbo) * a.N + nbo;
+      epx_any([&](int dm, float o) { p[(int64_t)dm * a.N] = o; });
     } else if (a.y_bf16) {
       uint16_t* p = reinterpret_cast<uint16_t*>(a.y) + mbo * a.y_ld + nbo;
-      epx_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.y_ld + dn] = (uint16_t)f32_to_bf16_bits(o); });
+      epx_any([&](int dm, float o) { p[(int64_t)dm * a.y_ld] = (uint16_t)f32_to_bf16_bits(o); });
     } else {
       float* p = reinterpret_cast<float*>(a.y) + mbo * a.y_ld + nbo;
-      epx_any([&](int dm, int dn, float o) { p[(int64_t)dm * a.y_ld + dn] = o; });
+      epx_any([&](int dm, float o) { p[(int64_t)dm * a.y_ld] = o; });
     }
     return;
   }
@@ -461,9 +465,13 @@ RLXQ_GEMM_INST(rlxq_gemm_q2_k_t128, SCH_Q2_K)
   }
 // Exact f32-output variant (EXACT above): rlxq_gemm_<scheme>_t256w8[p2|l]x,
 // f16 MFMA on the prepared activations (natural order), f16 hi + lo weights
+// and rlxq_gemm_<scheme>_t256w8[p2|l]xs for f32 activations (hi / lo rows)
 #define RLXQ_GEMM256X_INST(SNAME, SCH, PF, SUFFIX, LATE)                                     \
   extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8##SUFFIX##x(rlxq_gemm_args a) { \
-    rlxq::gemm256_body<SCH, 2, 4, PF, true, LATE, true>(a);                                        \
+    rlxq::gemm256_body<SCH, 2, 4, PF, true, LATE, true, false>(a);                                 \
+  }                                                                                                \
+  extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8##SUFFIX##xs(rlxq_gemm_args a) { \
+    rlxq::gemm256_body<SCH, 2, 4, PF, true, LATE, true, true>(a);                                  \
   }
 RLXQ_GEMM256_INST(q4_1, SCH_Q4_1)
 RLXQ_GEMM256_INST(q4_0, SCH_Q4_0)
@@ -486,5 +494,5 @@ RLXQ_GEMM256X_INST(q5_k, SCH_Q5_K, 1, , false)
 RLXQ_GEMM256X_INST(q3_k, SCH_Q3_K, 1, , false)
 RLXQ_GEMM256X_INST(q2_k, SCH_Q2_K, 2, p2, false)
 RLXQ_GEMM256X_INST(q8_k, SCH_Q8_K, 2, p2, false)
-RLXQ_GEMM256X_INST(mlx4, SCH_MLX4, 2, p2, false)
+RLXQ_GEMM256X_INST(mlx4, SCH_MLX4, 1, , false)
 RLXQ_GEMM256X_INST(mlx8, SCH_MLX8, 2, p2, false)

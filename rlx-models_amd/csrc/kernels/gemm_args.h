@@ -15,10 +15,12 @@ typedef struct rlxq_gemm_args {
   void* y;                /* [M, N] output, leading dimension y_ld        */
   int64_t M, N, K, rb, y_ld;
   int32_t group, sb_bf16, y_bf16;
-  /* f16 kernels: M counts x16 rows prepared in hi/lo pairs (row 2r + 1 the
-   * remainder of row 2r); the epilogue adds each pair into output row r,
-   * and y and part hold M / 2 rows                                        */
+  /* exact kernels with f32 activations: M counts x16 rows prepared in
+   * blocks of 64, rows 64b .. 64b + 31 the f16 rounding of rows 32b .. 32b
+   * + 31 (hi) and rows 64b + 32 .. the remainders (lo); y and part hold
+   * m_out rows                                                            */
   int32_t pairs;
+  int64_t m_out;
   int32_t tiles_m, tiles_n;   /* output tile grid (256 x 256 kernels)     */
   /* split-K (256 x 256 kernels): workgroup = (K slice, tile); slice sp
    * covers K [sp * kslice, (sp + 1) * kslice) and, when splits > 1, writes

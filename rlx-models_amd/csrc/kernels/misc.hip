@@ -433,3 +433,66 @@ RLXQ_ROUTE_INST(2)
 RLXQ_ROUTE_INST(4)
 RLXQ_ROUTE_INST(8)
 RLXQ_ROUTE_INST(16)
+
+// ---------------------------------------------------------------------------
+// Peak probes for the measurement (the denominators a roofline fraction can
+// be quoted against besides the data-sheet peaks).
+//
+// MFMA: each wave runs `iters` rounds of four independent
+// v_mfma_f32_32x32x16_bf16 on register operands (no memory traffic, four
+// chains hide the instruction's latency); 32768 flops per instruction.  The
+// accumulators are stored only when a sum nobody can reach is hit, which
+// keeps the chains live.
+typedef __bf16 rlxq_probe_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float rlxq_probe_f32x16 __attribute__((ext_vector_type(16)));
+extern "C" __global__ __launch_bounds__(256) void rlxq_probe_mfma(int64_t iters, float* __restrict__ sink) {
+  const float f = 1.0f + 1e-3f * (float)(threadIdx.x & 7);
+  rlxq_probe_bf16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    a[i] = (__bf16)(f * (float)(i + 1) * 1e-3f);
+    b[i] = (__bf16)(f * (float)(8 - i) * 1e-3f);
+  }
+  rlxq_probe_f32x16 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[c][r] = 0.f;
+  for (int64_t it = 0; it < iters; it++) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[c], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) s += acc[c][r];
+  if (s == -1234.5f) sink[threadIdx.x] = s;
+}
+
+// Streaming read: every byte of `bytes` (a multiple of 16 * 256) read once
+// with 16-byte loads, grid-stride; each workgroup's xor of the data goes to
+// sink[blockIdx.x] (keeps the loads live).  Four loads in flight per thread.
+extern "C" __global__ __launch_bounds__(256) void rlxq_probe_read(const uint4* __restrict__ src, int64_t n16,
+                                                                  uint32_t* __restrict__ sink) {
+  uint32_t acc = 0;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const uint4 v0 = src[i], v1 = src[i + stride], v2 = src[i + 2 * stride], v3 = src[i + 3 * stride];
+    acc ^= v0.x ^ v0.y ^ v0.z ^ v0.w ^ v1.x ^ v1.y ^ v1.z ^ v1.w ^ v2.x ^ v2.y ^ v2.z ^ v2.w ^ v3.x ^ v3.y ^ v3.z ^
+           v3.w;
+  }
+  for (; i < n16; i += stride) {
+    const uint4 v = src[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  __shared__ uint32_t red[256];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+    for (int k = 0; k < 256; k++) t ^= red[k];
+    sink[blockIdx.x] = t;
+  }
+}

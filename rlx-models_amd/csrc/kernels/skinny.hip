@@ -488,15 +488,24 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
   constexpr int RB = 3;   // register-resident blocks per thread
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
-  const int64_t lr = a.split ? r >> 1 : r;   // logical row (entry) of x16 row r
-  const bool lo_part = a.split && (r & 1);
+  // logical row (entry) of x16 row r and its part
+  const int64_t lr = a.split == 2 ? ((r >> 6) << 5) + (r & 31) : (a.split ? r >> 1 : r);
+  const bool lo_part = a.split == 2 ? ((r >> 5) & 1) != 0 : (a.split && (r & 1));
   const int64_t nblk = a.K >> 5;
   const int t = threadIdx.x;
   const int32_t ent = a.rmap ? (r < a.Mp ? a.rmap[lr] : -1) : 0;
   const int64_t src = a.rmap ? (int64_t)(ent >= 0 ? ent : 0) / a.rdiv : lr;   // x row of x16 row r
   if (a.rmap ? ent < 0 : lr >= a.M) {
-    // padding rows of the fragment-major layout: zeros
-    if (!a.frag_major || r >= a.Mp) return;
+    // padding rows: zeros (fragment-major, and the row-major 64-row blocks)
+    if (r >= a.Mp) return;
+    if (!a.frag_major) {
+      if (a.split == 2) {
+        uint4* dst = reinterpret_cast<uint4*>(a.x16 + r * a.K);
+        for (int64_t q = t; q < a.K / 8; q += 256) dst[q] = make_uint4(0u, 0u, 0u, 0u);
+        if (t == 0) a.inv_s[r] = 0.f;
+      }
+      return;
+    }
     uint4* dst = reinterpret_cast<uint4*>(a.x16);
     for (int64_t b = t; b < nblk; b += 256) {
 #pragma unroll

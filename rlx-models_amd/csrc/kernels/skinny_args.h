@@ -23,11 +23,13 @@ typedef struct rlxq_x16_args {
    * a zero row where rmap[r] < 0; NULL: x16 row r is x row r             */
   const int32_t* rmap;
   int32_t out_bf16;       /* x16 holds bf16 (MXFP4's bf16 MFMA), not f16  */
-  /* split: f32 rows in two parts, x16 row 2r the rounded row r (hi) and row
-   * 2r + 1 what that rounding left over (lo, on the same scale), so that
-   * hi + lo carries ~22 (f16) or ~16 (bf16) significant bits of each f32
-   * element; M counts the rows of x (and rmap its entries), Mp the x16
-   * rows (>= 2 M)                                                          */
+  /* split: f32 rows in two parts, the rounded row (hi) and what that
+   * rounding left over (lo, on the same scale), so that hi + lo carries ~22
+   * (f16) or ~16 (bf16) significant bits of each f32 element; M counts the
+   * rows of x (and rmap its entries), Mp the x16 rows.  split 1: x16 rows
+   * 2r (hi) and 2r + 1 (lo) for row r; split 2 (row-major only): blocks of
+   * 64 x16 rows, 64b + i the hi and 64b + 32 + i the lo part of row 32b + i
+   * (rows past M zero)                                                      */
   int32_t split;
   /* inv_s[r] carries an extra factor 2^post_exp: the MLX affine kernels'
    * f16 weights are 2^8 times the true ones (post_exp = -8), so that group

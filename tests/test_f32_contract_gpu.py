@@ -126,7 +126,7 @@ def test_prefill_f32_activations(ctx, orc, scheme, mkn):
     packed = orc.synth(scheme, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, kern = _f32_run(ctx, scheme, x, _t(packed), n)
-    assert kern.startswith(f"rlxq_gemm_{NAMES[scheme]}_t256w8") and kern.endswith("x"), kern
+    assert kern.startswith(f"rlxq_gemm_{NAMES[scheme]}_t256w8") and kern.endswith("xs"), kern
     assert rel_err(got, _want(orc, scheme, x, packed, k)) <= TOL, kern
 
 
@@ -139,12 +139,12 @@ def test_prefill_f32_exact_weights_and_bf16_out(ctx, orc):
     packed = _exact_f16_q4_1(orc, rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, kern = _f32_run(ctx, Q4_1, x, _t(packed), n)
-    assert kern == "rlxq_gemm_q4_1_t256w8p2x", kern
+    assert kern == "rlxq_gemm_q4_1_t256w8p2xs", kern
     want = _want(orc, Q4_1, x, packed, k)
     assert rel_err(got, want) <= TOL_EXACT_W
     # bf16 output from f32 activations: the same kernel, rounded at the store
     y = ctx.dequant_matmul(_t(x), _t(packed), Q4_1, n, y_dtype=torch.bfloat16)
-    assert ctx.last_kernel == "rlxq_gemm_q4_1_t256w8p2x", ctx.last_kernel
+    assert ctx.last_kernel == "rlxq_gemm_q4_1_t256w8p2xs", ctx.last_kernel
     torch.cuda.synchronize()
     assert rel_err(y.float().cpu().numpy(), want) <= 8e-3
 
@@ -167,7 +167,7 @@ def test_prefill_f32_config4_full_size_sampled(ctx, orc, scheme, kn):
     y = ctx.dequant_matmul(x, w, scheme, n, y_dtype=torch.float32)
     kern = ctx.last_kernel
     torch.cuda.synchronize()
-    assert kern == f"rlxq_gemm_{NAMES[scheme]}_t256w8p2x", kern
+    assert kern == f"rlxq_gemm_{NAMES[scheme]}_t256w8p2xs", kern
     rs = np.random.default_rng(m + n)
     rows = np.sort(rs.choice(m, 48, replace=False))
     cols = np.sort(rs.choice(n, 384, replace=False))
@@ -286,7 +286,7 @@ def test_reference_structured_inputs_every_path(ctx, orc, scheme, m, xdt):
     kern = ctx.last_kernel
     torch.cuda.synchronize()
     if m >= 300:
-        assert kern.startswith(f"rlxq_gemm_{NAMES[scheme]}_t256") and kern.endswith("x"), kern
+        assert kern.startswith(f"rlxq_gemm_{NAMES[scheme]}_t256") and kern.endswith("xs" if xdt == "f32" else "x"), kern
     elif m >= 5:
         assert kern.startswith("rlxq_skinny"), kern
     assert rel_err(y.cpu().numpy(), _want(orc, scheme, xv, packed, k)) <= 5e-5, kern

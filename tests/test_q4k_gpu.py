@@ -160,7 +160,7 @@ def test_q4k_f32_output_prefill_on_f16_gemm(ctx, orc, xdt):
     packed = orc.synth_q4_k(rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, want = _run(ctx, orc, x, packed, n, xdt=xdt)
-    assert ctx.last_kernel == "rlxq_gemm_q4_k_t256w8p2x", ctx.last_kernel
+    assert ctx.last_kernel == "rlxq_gemm_q4_k_t256w8p2" + ("xs" if xdt == "f32" else "x"), ctx.last_kernel
     assert rel_err(got, want) <= TOL
 
 
