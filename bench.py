@@ -431,7 +431,7 @@ def prefill_headline(detail: dict) -> dict:
             "w8a8_down_m4096_TOPs": detail["w8a8"]["down_m4096"]["TOPs"]}
 
 
-def batched_section(ctx, gen, sptr, stream) -> dict:
+def batched_section(ctx, gen, sptr, stream, only=None) -> dict:
     """Config 3: batched decode, Q4_1 and Q8_0 (and Q4_K, Q6_K, MLX affine
     4- and 8-bit, group 64 with bf16 slabs, and MXFP4 with E8M0 scale bytes
     beside them), M in {1, 4, 16, 64}, bf16 x, f32 y."""
@@ -448,6 +448,8 @@ def batched_section(ctx, gen, sptr, stream) -> dict:
                                       ("mlx4", rlxq.MLX_AFFINE4, 0.5 + 4 / 64, mlx_synth),
                                       ("mlx8", rlxq.MLX_AFFINE8, 1 + 4 / 64, mlx8_synth),
                                       ("mxfp4", rlxq.MLX_MXFP4, 0.5 + 1 / 32, synth_mxfp4_gpu)):
+        if only and sname not in only:
+            continue
         for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):
             wb = n * k * bpw
             ws = [synth(n, k, gen) for _ in range(_copies(wb))]
@@ -793,6 +795,7 @@ def main() -> int:
                                           "gguf", "peaks"],
                     help="profiling mode: run only this section (no decode step, no CPU baseline) and print its "
                          "figures as one JSON object")
+    ap.add_argument("--schemes", default="", help="batched section: only these formats (comma separated)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy 3 times (the reference for FETCH_SIZE/WRITE_SIZE)")
     a = ap.parse_args()
@@ -821,7 +824,8 @@ def main() -> int:
 
     if a.section:
         run = {"prefill": lambda: prefill_section(ctx, gen, sptr, stream, a.quick),
-               "batched": lambda: batched_section(ctx, gen, sptr, stream),
+               "batched": lambda: batched_section(ctx, gen, sptr, stream,
+                                                  [t for t in a.schemes.split(",") if t] or None),
                "moe": lambda: moe_section(ctx, gen, sptr, stream),
                "moe_q4_k": lambda: moe_section(ctx, gen, sptr, stream, "q4_k"),
                "moe_prefill": lambda: moe_section(ctx, gen, sptr, stream, "q4_1", 256),

@@ -279,7 +279,9 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     hipFunction_t fx;
     if ((rc = get_fn(ctx, "rlxq_x16_prep", &fx))) return rc;
     void* xargs[] = {&xa};
-    if ((rc = launch(ctx, fx, dim3((unsigned)sk_mp), dim3(256), 0, stream, xargs, "rlxq_x16_prep"))) return rc;
+    if ((rc = launch(ctx, fx, dim3((unsigned)sk_mp, (unsigned)((k + 2047) / 2048)), dim3(256), 0, stream, xargs,
+                     "rlxq_x16_prep")))
+      return rc;
     // 2c. the grouped MFMA kernel over (chunk, tile): NT weight tiles of 16
     // rows (SwiGLU: NT / 2 gate tiles and their up tiles)
     const int NT = sk_nt;

@@ -60,7 +60,10 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, in
   hipFunction_t fn;
   if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
   void* xargs[] = {&xa};
-  return launch(ctx, fn, dim3((unsigned)mp), dim3(256), 0, stream, xargs, "rlxq_x16_prep");
+  // workgroup (x16 row, 2048-element chunk of K)
+  if ((k + 2047) / 2048 > 65535 || mp > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "activation preparation grid");
+  return launch(ctx, fn, dim3((unsigned)mp, (unsigned)((k + 2047) / 2048)), dim3(256), 0, stream, xargs,
+                "rlxq_x16_prep");
 }
 
 namespace {

@@ -477,89 +477,122 @@ RLXQ_DEV void skinny_ns_body(const rlxq_skinny_args& a) {
 
 }  // namespace rlxq
 
-// One workgroup of 256 per activation row (per padded row in the
-// fragment-major layout); each thread owns whole 32-element blocks (held in
-// registers, so the permutation is local): blocks t, t + 256, t + 512
-// (K <= 24576 keeps a row in registers; longer rows are read twice).
-// With split, x16 rows 2r and 2r + 1 (two workgroups, which find the same
-// row maximum and scale) hold the f16 (bf16) rounding of row r's scaled
-// elements and the remainder of that rounding.
-extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a) {
-  constexpr int RB = 3;   // register-resident blocks per thread
+// Activation preparation.  Workgroup (r, chunk) handles x16 row r's
+// elements [2048 chunk, 2048 chunk + 2048): thread t one 16-byte piece,
+// positions 8i .. 8i + 7 (i = t % 4) of block 64 chunk + t / 4 in the
+// code-unpacking order.  Every workgroup of a row first reads the whole row
+// for its maximum (L2 hits), so all workgroups find the same power-of-two
+// scale, which puts the row maximum in [2^9, 2^10) (a block sum then stays
+// below 2^15, inside f16).  The four pieces of a block are lanes 4b' .. 4b'
+// + 3 of a wave: their sums add by two lane swaps.  With split, x16 rows
+// 2r, 2r + 1 (split 1) or 64b + i, 64b + 32 + i (split 2) hold the
+// f16 (bf16) rounding of row r's scaled elements (hi) and the remainder of
+// that rounding (lo).
+constexpr int X16_CHUNK = 2048;
+
+// The 8 source elements of piece i of a block (positions 8i .. 8i + 7, code
+// order `ORD`) as offsets into the block.
+template <int ORD>
+RLXQ_DEV int piece_src(int i, int e) {
+  if constexpr (ORD == 0) return 8 * i + e;
+  else if constexpr (ORD == 2) return 8 * i + (e < 4 ? 2 * e : 2 * (e - 4) + 1);
+  else return e < 4 ? 4 * i + e : 16 + 4 * i + (e - 4);
+}
+
+template <int ORD>
+RLXQ_DEV void load_piece(const rlxq_x16_args& a, int64_t src, int64_t b, int i, float* v) {
+  if (a.x_bf16) {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(a.x) + src * a.K + b * 32;
+    if constexpr (ORD == 1) {
+      const uint2 u0 = *reinterpret_cast<const uint2*>(p + 4 * i);
+      const uint2 u1 = *reinterpret_cast<const uint2*>(p + 16 + 4 * i);
+      const uint32_t w[4] = {u0.x, u0.y, u1.x, u1.y};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v[2 * e] = bf16_bits_to_f32(w[e] & 0xffffu);
+        v[2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+      }
+    } else {
+      const uint4 u = *reinterpret_cast<const uint4*>(p + 8 * i);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+      float n[8];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        n[2 * e] = bf16_bits_to_f32(w[e] & 0xffffu);
+        n[2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = n[piece_src<ORD>(i, e) - 8 * i];
+    }
+  } else {
+    const float* p = reinterpret_cast<const float*>(a.x) + src * a.K + b * 32;
+    if constexpr (ORD == 1) {
+      const float4 f0 = *reinterpret_cast<const float4*>(p + 4 * i);
+      const float4 f1 = *reinterpret_cast<const float4*>(p + 16 + 4 * i);
+      v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
+      v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
+    } else {
+      const float4 f0 = *reinterpret_cast<const float4*>(p + 8 * i);
+      const float4 f1 = *reinterpret_cast<const float4*>(p + 8 * i + 4);
+      const float n[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = n[piece_src<ORD>(i, e) - 8 * i];
+    }
+  }
+}
+
+template <int ORD>
+RLXQ_DEV void x16_prep_body(const rlxq_x16_args& a) {
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63;
   // logical row (entry) of x16 row r and its part
   const int64_t lr = a.split == 2 ? ((r >> 6) << 5) + (r & 31) : (a.split ? r >> 1 : r);
   const bool lo_part = a.split == 2 ? ((r >> 5) & 1) != 0 : (a.split && (r & 1));
   const int64_t nblk = a.K >> 5;
-  const int t = threadIdx.x;
+  const int64_t b = (int64_t)blockIdx.y * (X16_CHUNK / 32) + (t >> 2);   // this thread's block
+  const int i = t & 3;                                                   // and piece
+  const bool live = b < nblk;
   const int32_t ent = a.rmap ? (r < a.Mp ? a.rmap[lr] : -1) : 0;
   const int64_t src = a.rmap ? (int64_t)(ent >= 0 ? ent : 0) / a.rdiv : lr;   // x row of x16 row r
+  auto store_piece = [&](uint4 o) {
+    if (a.frag_major)
+      reinterpret_cast<uint4*>(a.x16)[(((b >> 2) * 4 + i) * a.Mp + r) * 4 + (b & 3)] = o;
+    else
+      *reinterpret_cast<uint4*>(a.x16 + r * a.K + b * 32 + 8 * i) = o;
+  };
   if (a.rmap ? ent < 0 : lr >= a.M) {
-    // padding rows: zeros (fragment-major, and the row-major 64-row blocks)
-    if (r >= a.Mp) return;
-    if (!a.frag_major) {
-      if (a.split == 2) {
-        uint4* dst = reinterpret_cast<uint4*>(a.x16 + r * a.K);
-        for (int64_t q = t; q < a.K / 8; q += 256) dst[q] = make_uint4(0u, 0u, 0u, 0u);
-        if (t == 0) a.inv_s[r] = 0.f;
-      }
-      return;
+    // padding rows (fragment-major, and the row-major 64-row blocks): zeros
+    if (live && (a.frag_major || a.split == 2)) {
+      store_piece(make_uint4(0u, 0u, 0u, 0u));
+      if (a.frag_major && a.ssum && i == 0) a.ssum[((b >> 2) * a.Mp + r) * 4 + (b & 3)] = 0.f;
     }
-    uint4* dst = reinterpret_cast<uint4*>(a.x16);
-    for (int64_t b = t; b < nblk; b += 256) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) dst[(((b >> 2) * 4 + q) * a.Mp + r) * 4 + (b & 3)] = make_uint4(0u, 0u, 0u, 0u);
-      if (a.ssum) a.ssum[((b >> 2) * a.Mp + r) * 4 + (b & 3)] = 0.f;
-    }
+    if (!a.frag_major && a.split == 2 && blockIdx.y == 0 && t == 0) a.inv_s[r] = 0.f;
     return;
   }
-  auto load_blk32 = [&](int64_t b, float* v) {
-    if (a.x_bf16) {
-      const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + src * a.K + b * 32);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const uint4 u = p[q];
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          v[8 * q + 2 * e] = bf16_bits_to_f32(w[e] & 0xffffu);
-          v[8 * q + 2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
-        }
-      }
-    } else {
-      const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.x) + src * a.K + b * 32);
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        const float4 u = p[q];
-        v[4 * q] = u.x; v[4 * q + 1] = u.y; v[4 * q + 2] = u.z; v[4 * q + 3] = u.w;
-      }
-    }
-  };
-  float v[RB][32];
+  // the row maximum (every element of the row, 8 per load)
   float amax = 0.f;
+  if (a.x_bf16) {
+    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.x) + src * a.K);
+    for (int64_t q = t; q < a.K / 8; q += 256) {
+      const uint4 u = p[q];
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-  for (int i = 0; i < RB; i++) {
-    const int64_t b = t + 256 * i;
-    if (b < nblk) {
-      load_blk32(b, v[i]);
-#pragma unroll
-      for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(v[i][e]));
+      for (int e = 0; e < 4; e++)
+        amax = fmaxf(amax, fmaxf(fabsf(bf16_bits_to_f32(w[e] & 0xffffu)), fabsf(bf16_bits_to_f32(w[e] >> 16))));
     }
-  }
-  for (int64_t b = t + 256 * RB; b < nblk; b += 256) {
-    float w[32];
-    load_blk32(b, w);
-#pragma unroll
-    for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(w[e]));
+  } else {
+    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.x) + src * a.K);
+    for (int64_t q = t; q < a.K / 4; q += 256) {
+      const float4 f = p[q];
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  if ((t & 63) == 0) red[t >> 6] = amax;
+  if (lane == 0) red[t >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  // a power-of-two scale putting the row maximum in [2^9, 2^10) (a block
-  // sum then stays below 2^15, inside f16)
   float s = 1.f, inv = ldexpf(1.f, a.post_exp);
   if (amax > 0.f && amax <= 3.4e38f) {
     int sh = 9 - ilogbf(amax);
@@ -567,54 +600,40 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a)
     s = ldexpf(1.f, sh);
     inv = ldexpf(ldexpf(1.f, -sh), a.post_exp);
   }
-  const int nib = a.nibble_order;
-  auto store_blk32 = [&](int64_t b, const float* w) {
-    uint32_t o[16];
+  if (blockIdx.y == 0 && t == 0) a.inv_s[r] = inv;
+  float v[8];
+  if (live) load_piece<ORD>(a, src, b, i, v);
+  uint32_t o[4];
+  float sum = 0.f;
 #pragma unroll
-    for (int p = 0; p < 32; p += 2) {
-      float w0 = w[rlxq::perm_k(p, nib)] * s, w1 = w[rlxq::perm_k(p + 1, nib)] * s;
-      uint32_t h0 = a.out_bf16 ? f32_to_bf16_bits(w0) : f32_to_f16_bits(w0);
-      uint32_t h1 = a.out_bf16 ? f32_to_bf16_bits(w1) : f32_to_f16_bits(w1);
-      if (lo_part) {
-        // the remainder w - hi is exact in f32; rounded once more
-        w0 -= a.out_bf16 ? bf16_bits_to_f32(h0) : f16_bits_to_f32(h0);
-        w1 -= a.out_bf16 ? bf16_bits_to_f32(h1) : f16_bits_to_f32(h1);
-        h0 = a.out_bf16 ? f32_to_bf16_bits(w0) : f32_to_f16_bits(w0);
-        h1 = a.out_bf16 ? f32_to_bf16_bits(w1) : f32_to_f16_bits(w1);
-      }
-      o[p / 2] = h0 | (h1 << 16);
+  for (int e = 0; e < 4; e++) {
+    float w0 = live ? v[2 * e] * s : 0.f, w1 = live ? v[2 * e + 1] * s : 0.f;
+    uint32_t h0 = a.out_bf16 ? f32_to_bf16_bits(w0) : f32_to_f16_bits(w0);
+    uint32_t h1 = a.out_bf16 ? f32_to_bf16_bits(w1) : f32_to_f16_bits(w1);
+    if (lo_part) {
+      // the remainder w - hi is exact in f32; rounded once more
+      w0 -= a.out_bf16 ? bf16_bits_to_f32(h0) : f16_bits_to_f32(h0);
+      w1 -= a.out_bf16 ? bf16_bits_to_f32(h1) : f16_bits_to_f32(h1);
+      h0 = a.out_bf16 ? f32_to_bf16_bits(w0) : f32_to_f16_bits(w0);
+      h1 = a.out_bf16 ? f32_to_bf16_bits(w1) : f32_to_f16_bits(w1);
     }
-    if (a.frag_major && a.ssum) {
-      float sum = 0.f;
-#pragma unroll
-      for (int q = 0; q < 16; q++) {
-        sum += a.out_bf16 ? bf16_bits_to_f32(o[q] & 0xffffu) : f16_bits_to_f32(o[q] & 0xffffu);
-        sum += a.out_bf16 ? bf16_bits_to_f32(o[q] >> 16) : f16_bits_to_f32(o[q] >> 16);
-      }
-      a.ssum[((b >> 2) * a.Mp + r) * 4 + (b & 3)] = sum;
-    }
-    if (a.frag_major) {
-      uint4* dst = reinterpret_cast<uint4*>(a.x16);
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-        dst[(((b >> 2) * 4 + q) * a.Mp + r) * 4 + (b & 3)] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
-    } else {
-      uint4* dst = reinterpret_cast<uint4*>(a.x16 + r * a.K + b * 32);
-#pragma unroll
-      for (int q = 0; q < 4; q++) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
-    }
-  };
-#pragma unroll
-  for (int i = 0; i < RB; i++) {
-    const int64_t b = t + 256 * i;
-    if (b < nblk) store_blk32(b, v[i]);
+    o[e] = h0 | (h1 << 16);
+    sum += a.out_bf16 ? bf16_bits_to_f32(h0) : f16_bits_to_f32(h0);
+    sum += a.out_bf16 ? bf16_bits_to_f32(h1) : f16_bits_to_f32(h1);
   }
-  for (int64_t b = t + 256 * RB; b < nblk; b += 256) {
-    float w[32];
-    load_blk32(b, w);
-    store_blk32(b, w);
-  }
-  if (t == 0) a.inv_s[r] = inv;
+  // block sum over the block's four pieces (lanes 4b' .. 4b' + 3), in a
+  // fixed order: (p0 + p1) + (p2 + p3)
+  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 2, 64);
+  if (!live) return;
+  store_piece(make_uint4(o[0], o[1], o[2], o[3]));
+  if (a.frag_major && a.ssum && i == 0) a.ssum[((b >> 2) * a.Mp + r) * 4 + (b & 3)] = sum;
+}
+
+extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a) {
+  if (a.nibble_order == 1) x16_prep_body<1>(a);
+  else if (a.nibble_order == 2) x16_prep_body<2>(a);
+  else x16_prep_body<0>(a);
 }
 
 // Split-K partial sums added in split order.
