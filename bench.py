@@ -433,8 +433,9 @@ def prefill_headline(detail: dict) -> dict:
 
 def batched_section(ctx, gen, sptr, stream, only=None) -> dict:
     """Config 3: batched decode, Q4_1 and Q8_0 (and Q4_K, Q6_K, MLX affine
-    4- and 8-bit, group 64 with bf16 slabs, and MXFP4 with E8M0 scale bytes
-    beside them), M in {1, 4, 16, 64}, bf16 x, f32 y."""
+    4- and 8-bit, group 64 with bf16 slabs, MXFP4 with E8M0 scale bytes,
+    Q5_K, Q3_K, Q2_K and Q8_K beside them), M in {1, 4, 16, 64}, bf16 x,
+    f32 y."""
     import torch
     import rlxq
 
@@ -447,7 +448,11 @@ def batched_section(ctx, gen, sptr, stream, only=None) -> dict:
                                       ("q6_k", rlxq.GGUF_Q6_K, 210 / 256, synth_q6_k_gpu),
                                       ("mlx4", rlxq.MLX_AFFINE4, 0.5 + 4 / 64, mlx_synth),
                                       ("mlx8", rlxq.MLX_AFFINE8, 1 + 4 / 64, mlx8_synth),
-                                      ("mxfp4", rlxq.MLX_MXFP4, 0.5 + 1 / 32, synth_mxfp4_gpu)):
+                                      ("mxfp4", rlxq.MLX_MXFP4, 0.5 + 1 / 32, synth_mxfp4_gpu),
+                                      ("q5_k", rlxq.GGUF_Q5_K, 176 / 256, lambda n, k, g: synth_kq_gpu("q5_k", n, k, g)),
+                                      ("q3_k", rlxq.GGUF_Q3_K, 110 / 256, lambda n, k, g: synth_kq_gpu("q3_k", n, k, g)),
+                                      ("q2_k", rlxq.GGUF_Q2_K, 84 / 256, lambda n, k, g: synth_kq_gpu("q2_k", n, k, g)),
+                                      ("q8_k", rlxq.GGUF_Q8_K, 292 / 256, lambda n, k, g: synth_kq_gpu("q8_k", n, k, g))):
         if only and sname not in only:
             continue
         for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):

@@ -2,6 +2,7 @@
 // preparation, then the skinny kernel, then (small N only) the split-K sum.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -60,10 +61,13 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, in
   hipFunction_t fn;
   if ((rc = get_fn(ctx, "rlxq_x16_prep", &fn))) return rc;
   void* xargs[] = {&xa};
-  // workgroup (x16 row, 2048-element chunk of K)
-  if ((k + 2047) / 2048 > 65535 || mp > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "activation preparation grid");
-  return launch(ctx, fn, dim3((unsigned)mp, (unsigned)((k + 2047) / 2048)), dim3(256), 0, stream, xargs,
-                "rlxq_x16_prep");
+  // workgroup (x16 row, 2048-element chunks of K gy apart): a chunk each
+  // while rows are few, whole rows (one read for the row maximum) once the
+  // rows alone fill the chip
+  const int64_t nchunk = (k + 2047) / 2048, cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+  const int64_t gy = std::max<int64_t>(1, std::min<int64_t>(nchunk, (8 * cus + mp - 1) / mp));
+  if (gy > 65535 || mp > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "activation preparation grid");
+  return launch(ctx, fn, dim3((unsigned)mp, (unsigned)gy), dim3(256), 0, stream, xargs, "rlxq_x16_prep");
 }
 
 namespace {
@@ -200,19 +204,26 @@ int skinny_ns_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
 }
 }  // namespace
 
-int sk_post_exp(int scheme) { return (scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_AFFINE8) ? -8 : 0; }
+// (the formats whose f16 weight operands carry a 2^8 factor, sk_wscale)
+int sk_post_exp(int scheme) {
+  return (scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_AFFINE8 || scheme == RLXQ_GGUF_Q8_K ||
+          scheme == RLXQ_GGUF_Q2_K)
+             ? -8
+             : 0;
+}
 
+// Code order of the prepared activations: the GGUF nibble formats 1, MLX's
+// 4-bit codes 2, the one-code-per-byte forms natural (0).
 int sk_order(int scheme) {
   if (scheme == RLXQ_MLX_AFFINE4) return 2;
-  return scheme != RLXQ_GGUF_Q8_0 && scheme != RLXQ_GGUF_Q6_K && scheme != RLXQ_MLX_MXFP4 &&
-                 scheme != RLXQ_MLX_AFFINE8
-             ? 1
-             : 0;
+  return scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_K ? 1 : 0;
 }
 
 bool skinny_applies(int scheme, int group, int sb_dtype, int64_t m, int64_t k) {
   return (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q4_1 ||
-          ((scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K) && k % 256 == 0) ||
+          ((scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q6_K || scheme == RLXQ_GGUF_Q5_K ||
+            scheme == RLXQ_GGUF_Q3_K || scheme == RLXQ_GGUF_Q2_K || scheme == RLXQ_GGUF_Q8_K) &&
+           k % 256 == 0) ||
           ((scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_AFFINE8) && group >= 32 && group % 32 == 0 &&
            k % group == 0) ||
           // (E8M0 scales only: a bf16 scale times a code is not exact in bf16)
@@ -258,8 +269,10 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
     if (ns) return run_ns(nmt, nnt, nd);
   }
   int xmt = m <= 16 ? 1 : (m <= 32 ? 2 : 4), xnt = 2, xd = m <= 16 ? 4 : (m <= 32 ? 3 : 2);
-  if (scheme == RLXQ_GGUF_Q4_K) xd = m <= 16 ? 3 : 2;   // its 13-dword raw blocks
-  if (scheme == RLXQ_GGUF_Q6_K) xd = m <= 32 ? 2 : 1;   // its 22-dword raw blocks
+  // ring depth by raw block size: Q4_K 13 dwords, Q2_K 11; Q6_K 22, Q5_K 21,
+  // Q3_K 24 (Q8_K's 9 and the legacy blocks take the default)
+  if (scheme == RLXQ_GGUF_Q4_K || scheme == RLXQ_GGUF_Q2_K) xd = m <= 16 ? 3 : 2;
+  if (scheme == RLXQ_GGUF_Q6_K || scheme == RLXQ_GGUF_Q5_K || scheme == RLXQ_GGUF_Q3_K) xd = m <= 32 ? 2 : 1;
   if (const char* e = std::getenv("RLXQ_SKINNY_XR")) {
     int a1, a2, a3;
     if (std::sscanf(e, "%d,%d,%d", &a1, &a2, &a3) == 3) xmt = a1, xnt = a2, xd = a3;

@@ -49,27 +49,45 @@ RLXQ_DEV int perm_k(int p, int order) {
 //   Q6_K:  o[0] = dh0 | dh1 << 16, o[1] = dl0 | dl1 << 16 (d * sc of the two
 //          16-weight halves), codes o[2..9] as code + 96 bytes (so that
 //          code - 32 = byte - 128, the Q8_0 form)
+//   Q5_K:  o[0], o[1] as Q4_K's, codes o[2..9] as the 5-bit code per byte
+//   Q3_K:  o[0], o[1] as Q6_K's (d * (scale - 32) of the two halves), codes
+//          o[2..9] as code + 128 per byte (code in -4 .. 3)
+//   Q8_K:  o[0] = dh | dl << 16 of 2^8 * d, codes o[1..8] (int8, as stored)
+//   Q2_K:  o[0], o[1] = 2^8 * d * sc of the two halves, o[2], o[3] = 2^8 *
+//          dmin * mn (f32), codes o[4..11] one per byte: each weight
+//          fma(d sc, code, -dmin mn) in f32 (the CPU decoder's one rounding)
+//          then splits into f16 hi + lo (two mins per block do not fit the
+//          one block-sum term)
 //   MLX4 / MLX8: o[0] = sh | sl << 16 of 2^8 * scale, o[1] = bh | bl << 16 of
-//          2^8 * bias, codes o[2..5] / o[2..9] as stored (the 2^8 keeps small
-//          group scales normal in f16; the activation preparation folds 2^-8
-//          into the row factors)
+//          2^8 * bias, codes o[2..5] / o[2..9] as stored
 //   MXFP4: o[0] = the f32 scale (a power of two), codes o[1..4]; its E2M1
 //          codes times the scale are exact in bf16 (one bf16 operand)
-constexpr float MLX_PRESCALE = 256.f;   // 2^8; undone through post_exp = -8
+// (2^8: sk_wscale, which keeps small scales normal in f16; the activation
+// preparation folds 2^-8 into the row factors.)
 
 template <int SCH> constexpr int sk_hdr() {
-  return (SCH == SCH_Q4_K || SCH == SCH_Q6_K || SCH == SCH_MLX4 || SCH == SCH_MLX8) ? 2 : 1;
+  return SCH == SCH_Q2_K ? 4
+         : (SCH == SCH_Q4_K || SCH == SCH_Q6_K || SCH == SCH_Q5_K || SCH == SCH_Q3_K || SCH == SCH_MLX4 ||
+            SCH == SCH_MLX8)
+             ? 2
+             : 1;
 }
-template <int SCH> constexpr int sk_cw() { return (SCH == SCH_Q8_0 || SCH == SCH_Q6_K || SCH == SCH_MLX8) ? 8 : 4; }
+// code dwords: one byte per code (8) or one nibble (4)
+template <int SCH> constexpr int sk_cw() {
+  return (SCH == SCH_Q4_0 || SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SCH == SCH_MLX4 || SCH == SCH_MXFP4) ? 4 : 8;
+}
 template <int SCH> constexpr int sk_bdw() { return sk_hdr<SCH>() + sk_cw<SCH>(); }
 // formats with a min / bias term (m * block sum)
 template <int SCH> constexpr bool sk_has_m() {
-  return SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SCH == SCH_MLX4 || SCH == SCH_MLX8;
+  return SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SCH == SCH_Q5_K || SCH == SCH_MLX4 || SCH == SCH_MLX8;
 }
 // formats with a second scale half dl
 template <int SCH> constexpr bool sk_has_dl() {
-  return SCH == SCH_Q4_K || SCH == SCH_Q6_K || SCH == SCH_MLX4 || SCH == SCH_MLX8;
+  return SCH == SCH_Q4_K || SCH == SCH_Q6_K || SCH == SCH_Q5_K || SCH == SCH_Q3_K || SCH == SCH_Q8_K ||
+         SCH == SCH_MLX4 || SCH == SCH_MLX8;
 }
+// formats whose block has two 16-weight halves with scales of their own
+template <int SCH> constexpr bool sk_halves() { return SCH == SCH_Q6_K || SCH == SCH_Q3_K; }
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
 // 6:4, lgkmcnt 11:8): wait on one counter, leave the others unconstrained.
@@ -95,13 +113,31 @@ RLXQ_DEV uint32_t f16_split(float v) {
 template <int SCH>
 RLXQ_DEV void sk_b2(const uint32_t* bp, int g, f16x8_t& b1, f16x8_t& b2) {
   constexpr int H = sk_hdr<SCH>();
+  if constexpr (SCH == SCH_Q2_K) {
+    // f32 weight (half g / 2's scale and min), then hi = f16(w), lo = f16(w - hi)
+    const float dl = __uint_as_float(bp[g >> 1]), ml = __uint_as_float(bp[2 + (g >> 1)]);
+    const uint32_t u[2] = {bp[H + 2 * g], bp[H + 1 + 2 * g]};
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const uint32_t w = u[e >> 1] >> (16 * (e & 1));
+      const float v0 = fmaf(dl, (float)(w & 0xffu), -ml), v1 = fmaf(dl, (float)((w >> 8) & 0xffu), -ml);
+      const uint32_t h0 = f32_to_f16_bits(v0), h1 = f32_to_f16_bits(v1);
+      h[e] = h0 | (h1 << 16);
+      l[e] = f32_to_f16_bits(v0 - f16_bits_to_f32(h0)) | (f32_to_f16_bits(v1 - f16_bits_to_f32(h1)) << 16);
+    }
+    b1 = __builtin_bit_cast(f16x8_t, u32x4_t{h[0], h[1], h[2], h[3]});
+    b2 = __builtin_bit_cast(f16x8_t, u32x4_t{l[0], l[1], l[2], l[3]});
+    return;
+  }
   f16x2_t q[4];
-  if constexpr (SCH == SCH_Q8_0 || SCH == SCH_Q6_K || SCH == SCH_MLX8) {
-    // bytes: Q8_0 sign-flipped (byte ^ 0x80 = code + 128), Q6_K code + 96
-    // (= (code - 32) + 128), MLX8 the unsigned code
-    const uint32_t flip = SCH == SCH_Q8_0 ? 0x80808080u : 0u;
+  if constexpr (sk_cw<SCH>() == 8) {
+    // bytes: Q8_0 / Q8_K sign-flipped (byte ^ 0x80 = code + 128), Q6_K
+    // code + 96 (= (code - 32) + 128), Q3_K code + 128, MLX8 and Q5_K the
+    // unsigned code
+    const uint32_t flip = (SCH == SCH_Q8_0 || SCH == SCH_Q8_K) ? 0x80808080u : 0u;
     const uint32_t u0 = bp[H + 2 * g] ^ flip, u1 = bp[H + 1 + 2 * g] ^ flip;
-    const _Float16 off = SCH == SCH_MLX8 ? (_Float16)-1024.f : (_Float16)-1152.f;
+    const _Float16 off = (SCH == SCH_MLX8 || SCH == SCH_Q5_K) ? (_Float16)-1024.f : (_Float16)-1152.f;
     const f16x2_t o2 = {off, off};
     q[0] = magic_lo(u0) + o2;
     q[1] = magic_hi(u0) + o2;
@@ -117,9 +153,9 @@ RLXQ_DEV void sk_b2(const uint32_t* bp, int g, f16x8_t& b1, f16x8_t& b2) {
     q[2] = magic_lo(hi) + o2;
     q[3] = magic_hi(hi) + o2;
   }
-  // (Q6_K: positions 8g.. lie in half g / 2 of the block)
-  const uint32_t sel = (SCH == SCH_Q6_K && g >= 2) ? 0x03020302u : 0x01000100u;
-  const f16x2_t dh = as_h2(perm_b32(bp[0], bp[0], SCH == SCH_Q6_K ? sel : 0x01000100u));
+  // (two halves: positions 8g.. lie in half g / 2 of the block)
+  const uint32_t sel = (sk_halves<SCH>() && g >= 2) ? 0x03020302u : 0x01000100u;
+  const f16x2_t dh = as_h2(perm_b32(bp[0], bp[0], sk_halves<SCH>() ? sel : 0x01000100u));
   f16x2_t w1[4], w2[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
@@ -127,8 +163,8 @@ RLXQ_DEV void sk_b2(const uint32_t* bp, int g, f16x8_t& b1, f16x8_t& b2) {
     w2[i] = __builtin_elementwise_fma(q[i], dh, -w1[i]);
   }
   if constexpr (sk_has_dl<SCH>()) {
-    const uint32_t dlw = SCH == SCH_Q6_K ? bp[1] : bp[0];
-    const uint32_t dsel = SCH == SCH_Q6_K ? sel : 0x03020302u;
+    const uint32_t dlw = sk_halves<SCH>() ? bp[1] : bp[0];
+    const uint32_t dsel = sk_halves<SCH>() ? sel : 0x03020302u;
     const f16x2_t dl = as_h2(perm_b32(dlw, dlw, dsel));
 #pragma unroll
     for (int i = 0; i < 4; i++) w2[i] = __builtin_elementwise_fma(q[i], dl, w2[i]);
@@ -214,16 +250,59 @@ RLXQ_DEV void normalise(const RawBlk<SCH>& r, uint32_t* o) {
     const uint32_t sh = 4 * (r.sub & 1u);
 #pragma unroll
     for (int g = 0; g < 4; g++) o[2 + g] = ((qs[g] >> sh) & 0x0F0F0F0Fu) | (((qs[4 + g] >> sh) & 0x0F0F0F0Fu) << 4);
+  } else if constexpr (SCH == SCH_Q5_K) {
+    // d * sc and dmin * mn are exact in f32 (11 + 6 bits); code = low or
+    // high nibble | qh bit sub << 4
+    const uint32_t hd[4] = {r.hd.x, r.hd.y, r.hd.z, r.hd.w};
+    float sc, mn;
+    q4k_scale_min(hd, (int)r.sub, sc, mn);
+    o[0] = f16_split(f16_bits_to_f32(hd[0] & 0xffffu) * sc);
+    o[1] = f16_split(-(f16_bits_to_f32(hd[0] >> 16) * mn));
+    const uint32_t qs[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    const uint32_t qh[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+    const uint32_t sh = 4u * (r.sub & 1u);
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[2 + i] = ((qs[i] >> sh) & 0x0F0F0F0Fu) | (((qh[i] >> r.sub) & 0x01010101u) << 4);
+  } else if constexpr (SCH == SCH_Q3_K) {
+    float ds0, ds1;
+    q3k_half_scales(r, ds0, ds1);
+    const uint32_t s0 = f16_split(ds0), s1 = f16_split(ds1);
+    o[0] = (s0 & 0xffffu) | (s1 << 16);
+    o[1] = (s0 >> 16) | (s1 & 0xffff0000u);
+    const uint32_t n = r.sub >> 2, j = r.sub & 3;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t q = align_bytes(r.qs[i + 1], r.qs[i], r.off), hm = align_bytes(r.hm[i + 1], r.hm[i], r.off);
+      // code + 4 = low bits | 4 (mask bit set), per byte; + 124 gives code + 128
+      o[2 + i] = (((q >> (2 * j)) & 0x03030303u) | (((hm >> (4 * n + j)) & 0x01010101u) << 2)) + 0x7C7C7C7Cu;
+    }
+  } else if constexpr (SCH == SCH_Q2_K) {
+    // d * sc and dmin * mn (4-bit sc, mn) are exact in f32
+    const float d = f16_bits_to_f32(r.dd & 0xffffu), dmin = f16_bits_to_f32(r.dd >> 16);
+    const uint32_t c0 = r.sc & 0xffu, c1 = (r.sc >> 8) & 0xffu;
+    constexpr float P = sk_wscale<SCH_Q2_K>();
+    o[0] = __float_as_uint(d * (float)(c0 & 15u) * P);
+    o[1] = __float_as_uint(d * (float)(c1 & 15u) * P);
+    o[2] = __float_as_uint(dmin * (float)(c0 >> 4) * P);
+    o[3] = __float_as_uint(dmin * (float)(c1 >> 4) * P);
+    const uint32_t qs[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    const uint32_t j = r.sub & 3;
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[4 + i] = (qs[i] >> (2 * j)) & 0x03030303u;
+  } else if constexpr (SCH == SCH_Q8_K) {
+    o[0] = f16_split(r.d * sk_wscale<SCH_Q8_K>());
+    o[1] = r.q0.x; o[2] = r.q0.y; o[3] = r.q0.z; o[4] = r.q0.w;
+    o[5] = r.q1.x; o[6] = r.q1.y; o[7] = r.q1.z; o[8] = r.q1.w;
   } else if constexpr (SCH == SCH_MXFP4) {
     o[0] = __float_as_uint(r.s);
     o[1] = r.q.x; o[2] = r.q.y; o[3] = r.q.z; o[4] = r.q.w;
   } else if constexpr (SCH == SCH_MLX4) {
-    o[0] = f16_split(r.s * MLX_PRESCALE);
-    o[1] = f16_split(r.b * MLX_PRESCALE);
+    o[0] = f16_split(r.s * sk_wscale<SCH_MLX4>());
+    o[1] = f16_split(r.b * sk_wscale<SCH_MLX4>());
     o[2] = r.q.x; o[3] = r.q.y; o[4] = r.q.z; o[5] = r.q.w;
   } else if constexpr (SCH == SCH_MLX8) {
-    o[0] = f16_split(r.s * MLX_PRESCALE);
-    o[1] = f16_split(r.b * MLX_PRESCALE);
+    o[0] = f16_split(r.s * sk_wscale<SCH_MLX8>());
+    o[1] = f16_split(r.b * sk_wscale<SCH_MLX8>());
     o[2] = r.q0.x; o[3] = r.q0.y; o[4] = r.q0.z; o[5] = r.q0.w;
     o[6] = r.q1.x; o[7] = r.q1.y; o[8] = r.q1.z; o[9] = r.q1.w;
   } else if constexpr (SCH == SCH_Q4_1) {

@@ -156,16 +156,16 @@ RLXQ_DEV void gemm_body(const rlxq_gemm_args& a) {
 // blocks, so a wave's four row tiles are (hi, lo) of two row groups; the
 // lo x lo products (~2^-22 of a term) are skipped, three MFMAs per pair.
 // With f16 weights rounded once instead, structured data (the reference's
-// sin / cos parity inputs at K = 1792) already reaches 1.4e-3.  MLX weights
-// are held times 2^8 (undone through the activation row factors) so that
-// small group scales stay normal f16.
+// sin / cos parity inputs at K = 1792) already reaches 1.4e-3.  MLX, Q8_K and
+// Q2_K weights are held times 2^8 (sk_wscale; undone through the activation
+// row factors) so that small scales stay normal f16.
 template <int SCH, int WGM, int WGN, int PF, bool F16, bool LATE = false, bool EXACT = false, bool SPLITX = false>
 RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   static_assert(EXACT == F16, "f16 MFMA runs the exact variant on the prepared f16 activations");
   static_assert(!SPLITX || EXACT, "hi / lo activation rows on the exact variant");
   constexpr int BM = 256, BN = 256;
   constexpr int NREAL = EXACT ? BN / 2 : BN;   // output columns per tile
-  constexpr float WSCALE = (SCH == SCH_MLX4 || SCH == SCH_MLX8) ? 256.f : 1.f;
+  constexpr float WSCALE = sk_wscale<SCH>();
   constexpr int NT = 64 * WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;

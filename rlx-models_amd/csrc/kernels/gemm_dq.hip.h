@@ -175,6 +175,33 @@ RLXQ_DEV void load_blk(const rlxq_gemm_args& a, int64_t row, int64_t kb, bool ok
 template <int SCH>
 RLXQ_DEV void blk_f32(const RawBlk<SCH>& r, float* v);
 
+// Power-of-two factor on the f16 weight operands of the exact-weight MFMA
+// paths, undone in the activation row factors (post_exp = -8): 2^8 keeps the
+// small scales of the f32-scaled formats (MLX affine's f32 scales, Q8_K's f32
+// d, Q2_K's per-half d * sc) and their f16 remainders out of the subnormal
+// range.  Weights then have to stay below 2^8 in magnitude.
+template <int SCH> constexpr float sk_wscale() {
+  return (SCH == SCH_MLX4 || SCH == SCH_MLX8 || SCH == SCH_Q8_K || SCH == SCH_Q2_K) ? 256.f : 1.f;
+}
+
+// Q3_K block kb's two 16-weight half scales d * (scale - 32), exact in f32:
+// scale s = 8n + 2j + half (n = (kb / 4) % 2, j = kb % 4), 6 bits held as
+// the low nibble of byte s % 8 (the high nibble past 7) and bits 2 (s / 4)
+// .. + 1 of byte 8 + s % 4 of the 12 scale bytes.
+RLXQ_DEV void q3k_half_scales(const RawBlk<SCH_Q3_K>& r, float& ds0, float& ds1) {
+  const uint32_t w0 = align_bytes(r.sd[1], r.sd[0], r.off), w1 = align_bytes(r.sd[2], r.sd[1], r.off),
+                 w2 = align_bytes(r.sd[3], r.sd[2], r.off);
+  const float d = f16_bits_to_f32((r.sd[3] >> (8 * r.off)) & 0xffffu);
+  // byte i of the 12 scale bytes (selects, not a runtime array index)
+  auto byte = [&](uint32_t i) { return ((i < 4 ? w0 : (i < 8 ? w1 : w2)) >> (8 * (i & 3))) & 0xffu; };
+  auto scale = [&](uint32_t s6) {
+    return (int)(((byte(s6 & 7) >> (4 * (s6 >> 3))) & 15) | (((byte(8 + (s6 & 3)) >> (2 * (s6 >> 2))) & 3) << 4));
+  };
+  const uint32_t s0 = 8 * (r.sub >> 2) + 2 * (r.sub & 3);
+  ds0 = d * (float)(scale(s0) - 32);
+  ds1 = d * (float)(scale(s0 + 1) - 32);
+}
+
 // Converts a raw block into 16 dwords of bf16 pairs in natural element order:
 // f32 d*q + m (the CPU decoder's arithmetic), rounded to bf16 (nearest even).
 template <int SCH>
@@ -236,21 +263,11 @@ RLXQ_DEV void blk_f32(const RawBlk<SCH>& r, float* v) {
       for (int e = 0; e < 4; e++) v[4 * i + e] = fmaf(d1, (float)((c >> (8 * e)) & 0xffu), -m1);
     }
   } else if constexpr (SCH == SCH_Q3_K) {
-    // code = (qs >> 2j & 3) - (hmask bit 4n + j ? 0 : 4), scale s = 8n + 2j + i
-    // (i: the block's two 16-weight halves), w = (d (scale - 32)) code, exact
-    // products rounded once
-    const uint32_t w0 = align_bytes(r.sd[1], r.sd[0], r.off), w1 = align_bytes(r.sd[2], r.sd[1], r.off),
-                   w2 = align_bytes(r.sd[3], r.sd[2], r.off);
-    const float d = f16_bits_to_f32((r.sd[3] >> (8 * r.off)) & 0xffffu);
-    // byte i of the 12 scale bytes (selects, not a runtime array index)
-    auto byte = [&](uint32_t i) { return ((i < 4 ? w0 : (i < 8 ? w1 : w2)) >> (8 * (i & 3))) & 0xffu; };
-    // 6-bit scale s: low nibble of byte s % 8 (high nibble past 7), bits
-    // 2 (s / 4) .. + 1 of byte 8 + s % 4
-    auto scale = [&](uint32_t s6) {
-      return (int)(((byte(s6 & 7) >> (4 * (s6 >> 3))) & 15) | (((byte(8 + (s6 & 3)) >> (2 * (s6 >> 2))) & 3) << 4));
-    };
-    const uint32_t n = r.sub >> 2, j = r.sub & 3, s0 = 8 * n + 2 * j;
-    const float dl0 = d * (float)(scale(s0) - 32), dl1 = d * (float)(scale(s0 + 1) - 32);
+    // code = (qs >> 2j & 3) - (hmask bit 4n + j ? 0 : 4) with the half's
+    // scale d (scale - 32), exact products rounded once
+    const uint32_t n = r.sub >> 2, j = r.sub & 3;
+    float dl0, dl1;
+    q3k_half_scales(r, dl0, dl1);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const uint32_t q = align_bytes(r.qs[i + 1], r.qs[i], r.off), hm = align_bytes(r.hm[i + 1], r.hm[i], r.off);

@@ -1,7 +1,8 @@
 // Batched-decode dequant-GEMM for small M (the multi-row decode path):
 // y[m, n] = sum_k x[m, k] * dequant(W)[n, k] for up to 256 activation rows
-// (512 prepared rows) and GGUF Q8_0 / Q4_0 / Q4_1 / Q4_K / Q6_K, MLX affine
-// 4/8-bit and MXFP4 weights, streaming every weight once for all rows.
+// (512 prepared rows) and GGUF Q8_0 / Q4_0 / Q4_1 / Q4_K / Q5_K / Q6_K /
+// Q3_K / Q2_K / Q8_K, MLX affine 4/8-bit and MXFP4 weights, streaming every
+// weight once for all rows.
 // Replaces the backend kernel of Op::DequantMatMul at decode batch sizes
 // (crates/rlx-models-core/src/standard_decoder.rs:727-738, M rows per call).
 //
@@ -549,13 +550,11 @@ RLXQ_DEV void x16_prep_body(const rlxq_x16_args& a) {
   // logical row (entry) of x16 row r and its part
   const int64_t lr = a.split == 2 ? ((r >> 6) << 5) + (r & 31) : (a.split ? r >> 1 : r);
   const bool lo_part = a.split == 2 ? ((r >> 5) & 1) != 0 : (a.split && (r & 1));
-  const int64_t nblk = a.K >> 5;
-  const int64_t b = (int64_t)blockIdx.y * (X16_CHUNK / 32) + (t >> 2);   // this thread's block
-  const int i = t & 3;                                                   // and piece
-  const bool live = b < nblk;
+  const int64_t nblk = a.K >> 5, nchunk = (a.K + X16_CHUNK - 1) / X16_CHUNK;
+  const int i = t & 3;   // this thread's piece of its block
   const int32_t ent = a.rmap ? (r < a.Mp ? a.rmap[lr] : -1) : 0;
   const int64_t src = a.rmap ? (int64_t)(ent >= 0 ? ent : 0) / a.rdiv : lr;   // x row of x16 row r
-  auto store_piece = [&](uint4 o) {
+  auto store_piece = [&](int64_t b, uint4 o) {
     if (a.frag_major)
       reinterpret_cast<uint4*>(a.x16)[(((b >> 2) * 4 + i) * a.Mp + r) * 4 + (b & 3)] = o;
     else
@@ -563,10 +562,13 @@ RLXQ_DEV void x16_prep_body(const rlxq_x16_args& a) {
   };
   if (a.rmap ? ent < 0 : lr >= a.M) {
     // padding rows (fragment-major, and the row-major 64-row blocks): zeros
-    if (live && (a.frag_major || a.split == 2)) {
-      store_piece(make_uint4(0u, 0u, 0u, 0u));
-      if (a.frag_major && a.ssum && i == 0) a.ssum[((b >> 2) * a.Mp + r) * 4 + (b & 3)] = 0.f;
-    }
+    if (a.frag_major || a.split == 2)
+      for (int64_t cy = blockIdx.y; cy < nchunk; cy += gridDim.y) {
+        const int64_t b = cy * (X16_CHUNK / 32) + (t >> 2);
+        if (b >= nblk) continue;
+        store_piece(b, make_uint4(0u, 0u, 0u, 0u));
+        if (a.frag_major && a.ssum && i == 0) a.ssum[((b >> 2) * a.Mp + r) * 4 + (b & 3)] = 0.f;
+      }
     if (!a.frag_major && a.split == 2 && blockIdx.y == 0 && t == 0) a.inv_s[r] = 0.f;
     return;
   }
@@ -601,6 +603,11 @@ RLXQ_DEV void x16_prep_body(const rlxq_x16_args& a) {
     inv = ldexpf(ldexpf(1.f, -sh), a.post_exp);
   }
   if (blockIdx.y == 0 && t == 0) a.inv_s[r] = inv;
+  // the row's chunks of 2048 elements, gridDim.y apart (one pass over the
+  // row for its maximum, then each chunk, from cache, once)
+  for (int64_t cy = blockIdx.y; cy < nchunk; cy += gridDim.y) {
+  const int64_t b = cy * (X16_CHUNK / 32) + (t >> 2);   // this thread's block
+  const bool live = b < nblk;
   float v[8];
   if (live) load_piece<ORD>(a, src, b, i, v);
   uint32_t o[4];
@@ -625,9 +632,10 @@ RLXQ_DEV void x16_prep_body(const rlxq_x16_args& a) {
   // fixed order: (p0 + p1) + (p2 + p3)
   sum += __shfl_xor(sum, 1, 64);
   sum += __shfl_xor(sum, 2, 64);
-  if (!live) return;
-  store_piece(make_uint4(o[0], o[1], o[2], o[3]));
+  if (!live) continue;
+  store_piece(b, make_uint4(o[0], o[1], o[2], o[3]));
   if (a.frag_major && a.ssum && i == 0) a.ssum[((b >> 2) * a.Mp + r) * 4 + (b & 3)] = sum;
+  }
 }
 
 extern "C" __global__ __launch_bounds__(256) void rlxq_x16_prep(rlxq_x16_args a) {
@@ -719,6 +727,18 @@ RLXQ_SKINNYXR_INST(mxfp4, SCH_MXFP4, 4, 2, 2)
 RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 1, 2, 2)
 RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 2, 2, 2)
 RLXQ_SKINNYXR_INST(q6_k, SCH_Q6_K, 4, 2, 1)
+RLXQ_SKINNYXR_INST(q5_k, SCH_Q5_K, 1, 2, 2)
+RLXQ_SKINNYXR_INST(q5_k, SCH_Q5_K, 2, 2, 2)
+RLXQ_SKINNYXR_INST(q5_k, SCH_Q5_K, 4, 2, 1)
+RLXQ_SKINNYXR_INST(q3_k, SCH_Q3_K, 1, 2, 2)
+RLXQ_SKINNYXR_INST(q3_k, SCH_Q3_K, 2, 2, 2)
+RLXQ_SKINNYXR_INST(q3_k, SCH_Q3_K, 4, 2, 1)
+RLXQ_SKINNYXR_INST(q2_k, SCH_Q2_K, 1, 2, 3)
+RLXQ_SKINNYXR_INST(q2_k, SCH_Q2_K, 2, 2, 2)
+RLXQ_SKINNYXR_INST(q2_k, SCH_Q2_K, 4, 2, 2)
+RLXQ_SKINNYXR_INST(q8_k, SCH_Q8_K, 1, 2, 4)
+RLXQ_SKINNYXR_INST(q8_k, SCH_Q8_K, 2, 2, 3)
+RLXQ_SKINNYXR_INST(q8_k, SCH_Q8_K, 4, 2, 2)
 
 // N-split variants: rlxq_skinnyns_<scheme>_mt<MT>_nt<NT>_d<D>.
 #define RLXQ_SKINNYNS_INST(SNAME, SCH, MT, NT, D)                                                      \
