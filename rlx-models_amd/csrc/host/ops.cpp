@@ -390,6 +390,51 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
       xr_w = two ? 4 : 8;
   bool use_xr = m == 1 && xbf && xr_scheme && nchunk64 <= xr_max && n < (int64_t(1) << 31);
   int xr_lds = 1;   // 1: the activations pass through LDS once per workgroup
+  // The K-split register kernels (KS waves per weight row, their row sums
+  // added in part order in LDS; Q4_1): grid and LDS (activation records,
+  // then [W / KS][rows per wave][KS] partial sums).
+  auto launch_ks = [&](int nu, int d, int wv, int ks, bool f32x) -> int {
+    std::snprintf(name, sizeof name, "rlxq_gemvxs_%s_U%d_D%d_W%d%s_K%d", scheme_name(scheme), nu, d, wv,
+                  f32x ? "_F" : "", ks);
+    int rc2;
+    if ((rc2 = get_fn(ctx, name, &fn))) return rc2;
+    const int rw = wv / ks;
+    const size_t lds0 = (f32x ? 2 : 1) * (size_t)(k / 32) * 68;
+    int per_cu = blocks_per_cu(ctx, name, fn, 64 * wv, lds0 + 1024);
+    int64_t gx = std::min<int64_t>((int64_t)ctx->cu_count * std::max(per_cu, 1), (n + rw - 1) / rw);
+    size_t part = (size_t)rw * ((n + gx * rw - 1) / (gx * rw)) * ks * 4;
+    if (part > 1024) {
+      per_cu = blocks_per_cu(ctx, name, fn, 64 * wv, lds0 + part);
+      gx = std::min<int64_t>((int64_t)ctx->cu_count * std::max(per_cu, 1), (n + rw - 1) / rw);
+      part = (size_t)rw * ((n + gx * rw - 1) / (gx * rw)) * ks * 4;
+    }
+    if (lds0 + part > ctx->max_lds) return 1;   // (not applicable: the caller goes on)
+    return launch(ctx, fn, dim3((unsigned)gx, 1, 1), dim3(64 * wv, 1, 1), lds0 + part, stream, args, name);
+  };
+  // RLXQ_GEMV_XSK="NU,D,W,KS" (bf16) / RLXQ_GEMV_XSFK (f32 activations)
+  // picks a K-split variant for one Q4_1 row whose K fits NU * KS unit
+  // chunks (tuning).
+  if (m == 1 && scheme == RLXQ_GGUF_Q4_1 && n < (int64_t(1) << 31)) {
+    if (const char* e = std::getenv(xbf ? "RLXQ_GEMV_XSK" : "RLXQ_GEMV_XSFK")) {
+      int nu, d, wv, ks;
+      if (std::sscanf(e, "%d,%d,%d,%d", &nu, &d, &wv, &ks) == 4 && nchunk64 <= (int64_t)nu * ks) {
+        const int r = launch_ks(nu, d, wv, ks, !xbf);
+        if (r <= 0) return r;
+      }
+    }
+  }
+  // One row of f32 activations on Q4_1 with many rows at K = 4096 (gate_up:
+  // 14.5 against 15.3 us) or K past four unit chunks (down, K = 12288: 10.3
+  // against 10.6 us on the LDS-record kernel): the two-wave K split.  (bf16
+  // activations measured no gain from it: down 8.0-8.5 us two-way and
+  // 8.3-8.8 four-way against 8.1 on one wave per row.)
+  if (m == 1 && !xbf && scheme == RLXQ_GGUF_Q4_1 && n < (int64_t(1) << 31) &&
+      !(std::getenv("RLXQ_GEMV_XR") && std::getenv("RLXQ_GEMV_XR")[0] == '0')) {
+    int r = 1;
+    if (nchunk64 == 2 && n >= 16384) r = launch_ks(1, 2, 8, 2, true);
+    else if (nchunk64 > 4 && nchunk64 <= 6) r = launch_ks(3, 1, 8, 2, true);
+    if (r <= 0) return r;
+  }
   // One row of f32 activations: the two-row kernel on its hi and lo bf16
   // rows (Q4_1, MLX 4-bit, MXFP4 up to four unit chunks, Q4_K up to two),
   // both rows' sums added into the one output.  RLXQ_GEMV_XR=0 turns it off.

@@ -240,9 +240,16 @@ RLXQ_DEV void gemv_body(const rlxq_gemv_args& a) {
 // F32X: one row of f32 activations, held as two bf16 rows, the rounded row
 // (hi) and what the rounding left over (lo), so that the pairs keep ~16
 // significant bits of each element; both rows' sums add into the one output.
-template <int SCH, int NU, int D, int WAVES, bool XLDS, int MT = 1, bool F32X = false>
+// KS > 1 (K split inside the workgroup, for rows too long for one wave's
+// registers or too few to keep the CUs' loads in flight): waves KS r ..
+// KS r + KS - 1 take the same weight rows, each a contiguous KS-th of the
+// units; their row sums meet in LDS after the last row and are added in
+// part order (fixed, so the result does not depend on timing).
+template <int SCH, int NU, int D, int WAVES, bool XLDS, int MT = 1, bool F32X = false, int KS = 1>
 RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   static_assert(!F32X || (MT == 2 && XLDS), "f32 activations: hi and lo rows through LDS");
+  static_assert(KS == 1 || (XLDS && (MT == 1 || F32X) && WAVES % KS == 0),
+                "K split: one output row, partial sums through LDS");
   constexpr int BLOCKS = Unit<SCH>::BLOCKS;
   constexpr int DW = Unit<SCH>::DW;
   constexpr int BYTES = Unit<SCH>::BYTES;
@@ -258,18 +265,23 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   // to be wave-uniform (scalar branches), so the compiler's wait counts can
   // keep the ring's loads in flight across iterations
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // K part and row slot of this wave; RW row slots per workgroup
+  constexpr int RW = WAVES / KS;
+  const int kh = wv % KS, wr = wv / KS;
   // rows of this wave: n0 + s * G, s < cnt (N < 2^31: 32-bit division)
-  const uint32_t G = gridDim.x * WAVES, n0u = blockIdx.x * WAVES + wv, N32 = (uint32_t)a.N;
+  const uint32_t G = gridDim.x * RW, n0u = blockIdx.x * RW + wr, N32 = (uint32_t)a.N;
   const int64_t n0 = n0u;
   const int64_t cnt = n0u < N32 ? (N32 - n0u + G - 1) / G : 0;
   const int gpr = (MLX || MX) ? K / a.group : 0;
+  // this wave's units [ub, ue)
+  const int UH = (U + KS - 1) / KS, ub = kh * UH, ue = ub + UH < U ? ub + UH : U;
 
   int uc[NU];
   bool uok[NU];
 #pragma unroll
   for (int c = 0; c < NU; c++) {
-    const int u = lane + 64 * c;
-    uok[c] = u < U;
+    const int u = ub + lane + 64 * c;
+    uok[c] = u < ue;
     uc[c] = uok[c] ? u : U - 1;
   }
 
@@ -309,7 +321,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   if constexpr (XLDS) {
     extern __shared__ __align__(16) uint32_t xlds[];
     constexpr int NT = 64 * WAVES;
-    constexpr int XH = (2 * 64 * NU * BLOCKS + NT - 1) / NT;   // half-blocks per thread and row
+    constexpr int XH = (2 * 64 * NU * KS * BLOCKS + NT - 1) / NT;   // half-blocks per thread and row
     constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;
     constexpr bool LINEAR = MLX || MX || SCH == SCH_Q4_K;   // half h = elements 16h..16h+15
     uint4 xa[MT][XH], xc[MT][XH];
@@ -478,6 +490,20 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   if (a.row_map) yrow = a.row_map[0];
   if (a.row_scale) ysc = a.row_scale[0];
 
+  // K split: every part's row sums, [RW][cmax][KS] floats after the
+  // activation records
+  float* kpart = nullptr;
+  int64_t cmax = 0;
+  if constexpr (KS > 1) {
+    extern __shared__ __align__(16) uint32_t xlds[];
+    kpart = reinterpret_cast<float*>(xlds + (size_t)MT * bpr * 17);
+    cmax = (N32 + G - 1) / G;
+  }
+  auto store = [&](int64_t off, float v) {
+    if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v * ysc);
+    else reinterpret_cast<float*>(a.y)[off] = v * ysc;
+  };
+
   const UnpackK kc = unpack_consts();
   // Row s of the wave uses ring slot s % D.  While D more rows follow a full
   // group, each slot is refilled right after use with the row D later (no
@@ -520,20 +546,19 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
       }
     if constexpr (F32X) {
       const float v = lane_group_sum<64>(acc[0] + acc[1]);
-      if (lane == 0 && yrow >= 0) {
-        const int64_t off = yrow * a.y_ld + n;
-        if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v * ysc);
-        else reinterpret_cast<float*>(a.y)[off] = v * ysc;
+      if constexpr (KS > 1) {
+        if (lane == 0) kpart[((int64_t)wr * cmax + st) * KS + kh] = v;
+      } else if (lane == 0 && yrow >= 0) {
+        store(yrow * a.y_ld + n, v);
       }
+    } else if constexpr (KS > 1) {
+      const float v = lane_group_sum<64>(acc[0]);
+      if (lane == 0) kpart[((int64_t)wr * cmax + st) * KS + kh] = v;
     } else {
 #pragma unroll
       for (int m = 0; m < MT; m++) {
         const float v = lane_group_sum<64>(acc[m]);
-        if (lane == 0 && yrow >= 0 && m < a.M) {
-          const int64_t off = (yrow + m) * a.y_ld + n;
-          if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(v * ysc);
-          else reinterpret_cast<float*>(a.y)[off] = v * ysc;
-        }
+        if (lane == 0 && yrow >= 0 && m < a.M) store((yrow + m) * a.y_ld + n, v);
       }
     }
   };
@@ -556,6 +581,19 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
 #pragma unroll
   for (int i = 0; i < D; i++)
     if (s0 + D + i < cnt) row(s0 + D + i, ring[i]);
+  if constexpr (KS > 1) {
+    // every wave has left its row loop: part 0's wave adds the parts of its
+    // rows in part order and stores them
+    __syncthreads();
+    if (kh == 0 && yrow >= 0)
+      for (int64_t st = lane; st < cnt; st += 64) {
+        const float* p = kpart + ((int64_t)wr * cmax + st) * KS;
+        float v = p[0];
+#pragma unroll
+        for (int q = 1; q < KS; q++) v += p[q];
+        store(yrow * a.y_ld + n0 + st * G, v);
+      }
+  }
 }
 
 }  // namespace rlxq
@@ -669,6 +707,30 @@ RLXQ_GEMVXS_Q4K
   RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U2_D1_W4_F, SCH, 2, 1, 4)          \
   RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U3_D1_W8_F, SCH, 3, 1, 8)          \
   RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U4_D1_W8_F, SCH, 4, 1, 8)
+// K split inside the workgroup (KS waves per weight row):
+// rlxq_gemvxs_<scheme>_U<NU>_D<D>_W<W>[_F]_K<KS>, NU unit chunks per part
+#define RLXQ_GEMVXSK_INST(NAME, SCH, NU, D, W, KS)                                    \
+  extern "C" __global__ __launch_bounds__(64 * W) void NAME(rlxq_gemv_args a) {      \
+    rlxq::gemv_xr_body<SCH, NU, D, W, true, 1, false, KS>(a);                         \
+  }
+#define RLXQ_GEMVXSFK_INST(NAME, SCH, NU, D, W, KS)                                   \
+  extern "C" __global__ __launch_bounds__(64 * W) void NAME(rlxq_gemv_args a) {      \
+    rlxq::gemv_xr_body<SCH, NU, D, W, true, 2, true, KS>(a);                          \
+  }
+#if RLXQ_PART_IS(2)
+RLXQ_GEMVXSK_INST(rlxq_gemvxs_q4_1_U1_D2_W8_K2, SCH_Q4_1, 1, 2, 8, 2)
+RLXQ_GEMVXSK_INST(rlxq_gemvxs_q4_1_U1_D3_W8_K2, SCH_Q4_1, 1, 3, 8, 2)
+RLXQ_GEMVXSK_INST(rlxq_gemvxs_q4_1_U1_D2_W16_K2, SCH_Q4_1, 1, 2, 16, 2)
+RLXQ_GEMVXSK_INST(rlxq_gemvxs_q4_1_U3_D1_W8_K2, SCH_Q4_1, 3, 1, 8, 2)
+RLXQ_GEMVXSK_INST(rlxq_gemvxs_q4_1_U3_D2_W8_K2, SCH_Q4_1, 3, 2, 8, 2)
+RLXQ_GEMVXSK_INST(rlxq_gemvxs_q4_1_U3_D1_W16_K2, SCH_Q4_1, 3, 1, 16, 2)
+RLXQ_GEMVXSK_INST(rlxq_gemvxs_q4_1_U2_D1_W8_K4, SCH_Q4_1, 2, 1, 8, 4)
+RLXQ_GEMVXSK_INST(rlxq_gemvxs_q4_1_U2_D2_W8_K4, SCH_Q4_1, 2, 2, 8, 4)
+RLXQ_GEMVXSK_INST(rlxq_gemvxs_q4_1_U2_D1_W16_K4, SCH_Q4_1, 2, 1, 16, 4)
+RLXQ_GEMVXSFK_INST(rlxq_gemvxs_q4_1_U3_D1_W8_F_K2, SCH_Q4_1, 3, 1, 8, 2)
+RLXQ_GEMVXSFK_INST(rlxq_gemvxs_q4_1_U2_D1_W8_F_K2, SCH_Q4_1, 2, 1, 8, 2)
+RLXQ_GEMVXSFK_INST(rlxq_gemvxs_q4_1_U1_D2_W8_F_K2, SCH_Q4_1, 1, 2, 8, 2)
+#endif
 #if RLXQ_PART_IS(1)
 RLXQ_GEMVXSF_SCHEME(q4_1, SCH_Q4_1)
 RLXQ_GEMVXSF_SCHEME(mlx4, SCH_MLX4)

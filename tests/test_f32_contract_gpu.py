@@ -206,6 +206,23 @@ def test_single_row_f32_register_path(ctx, orc, scheme, kn):
     assert rel_err(got, want) <= TOL, kern
 
 
+@pytest.mark.parametrize("kn", [(4096, 16384), (12288, 520), (10240, 33)], ids=str)
+def test_single_row_f32_q4_1_k_split_defaults(ctx, orc, kn):
+    """Q4_1 rows at gate_up's width and K past four unit chunks (down) take
+    the two-wave K-split register kernel by default."""
+    k, n = kn
+    announce(f"f32 contract gemv m=1 k-split k={k} n={n}")
+    rng = np.random.default_rng(k + n)
+    packed = orc.synth(Q4_1, rng, n, k)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    got, kern = _f32_run(ctx, Q4_1, x, _t(packed), n)
+    assert kern.startswith("rlxq_gemvxs_q4_1_") and kern.endswith("_F_K2"), kern
+    assert rel_err(got, _want(orc, Q4_1, x, packed, k)) <= TOL
+    packed = _exact_f16_q4_1(orc, rng, n, k)
+    got, kern = _f32_run(ctx, Q4_1, x, _t(packed), n)
+    assert rel_err(got, _want(orc, Q4_1, x, packed, k)) <= TOL_EXACT_W
+
+
 @pytest.mark.parametrize("kn", [(4096, 4096), (8192, 300)], ids=str)
 def test_single_row_f32_exact_weights(ctx, orc, kn):
     k, n = kn
