@@ -29,6 +29,10 @@ Extra keys of the same JSON line:
   measured_peaks  this GPU's copy and streaming-read bandwidth and register-
                   only bf16 MFMA rate (rlxq_peak_probe); roofline and
                   prefill_roofline also give their fraction of these
+  decode_floor    each decode shape's load-only time (the faster of the
+                  rlxq_peak_probe READ and READ4 probes over its weight
+                  bytes) and a 4 KiB launch: the floor the step's kernels
+                  are measured against (frac_of_floor)
   f32_contract_decode  the decode step with F32 x and y (the reference
                   operator's operand types); prefill.f32_contract likewise
 Every section's per-call time is the smaller of an eager run and a HIP-graph
@@ -291,6 +295,39 @@ def peaks_section(ctx, stream) -> dict:
             "mfma_bf16_TFLOPs": round(flops / mfma_ms / 1e9, 1),
             "copy": "1 GiB torch copy_, read + write bytes", "read": "2 GiB, rlxq_probe_read (16-byte loads)",
             "mfma": "rlxq_probe_mfma: 4 independent v_mfma_f32_32x32x16_bf16 chains per wave, 32 waves per CU"}
+
+
+def decode_floor(ctx, stream) -> dict:
+    """Load-only floor of each decode shape: the smaller time of the two
+    read probes (rlxq_peak_probe READ: a grid-stride loop over 8 workgroups
+    per CU; READ4: a grid sized to the bytes, four independent loads per
+    thread) over each shape's packed weight bytes (rounded up to 4 KiB),
+    rotated over copies that exceed the MALL as the step's weights are, and
+    a launch that reads 4 KiB (the floor of a launch after a launch), timed
+    as the step's own launches (_gpu_us)."""
+    import torch
+    import rlxq
+
+    sink = torch.empty(1 << 16, dtype=torch.int32, device="cuda")
+    out = {}
+    for name, k, n in SHAPES:
+        b = (n * (k // 32) * 20 + 4095) // 4096 * 4096
+        bufs = [torch.zeros(b // 4, device="cuda") for _ in range(_copies(b))]
+        us = {}
+        for kind, key in ((rlxq.PROBE_READ, "us_read"), (rlxq.PROBE_READ4, "us_read4")):
+            def launch(i, sp, bufs=bufs, b=b, kind=kind):
+                ctx.peak_probe(kind, b, buf=bufs[i % len(bufs)], sink=sink, stream=sp)
+            us[key] = round(_gpu_us(ctx, launch, 4 * len(bufs), stream)["us"], 3)
+        best = min(us.values())
+        out[name] = {"bytes": b, "us": best, "GBps": round(b / best / 1e3, 1), **us}
+        del bufs
+    small = torch.zeros(1024, device="cuda")
+    t = _gpu_us(ctx, lambda i, sp: ctx.peak_probe(rlxq.PROBE_READ, 4096, buf=small, sink=sink, stream=sp), 400,
+                stream)
+    out["launch_4KiB_us"] = round(t["us"], 3)
+    out["step_us"] = round(sum(out[nm]["us"] for nm, _, _ in SHAPES), 3)
+    torch.cuda.empty_cache()
+    return out
 
 
 def decode_roofline(ctx, layers, xs, ys, calls, stream, reps: int) -> tuple[dict, dict]:
@@ -797,7 +834,7 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="prefill at M=4096 only")
     ap.add_argument("--cpu-seconds", type=float, default=16.0)
     ap.add_argument("--section", choices=["prefill", "batched", "moe", "moe_q4_k", "moe_prefill", "schemes", "q8",
-                                          "gguf", "peaks"],
+                                          "gguf", "peaks", "floor"],
                     help="profiling mode: run only this section (no decode step, no CPU baseline) and print its "
                          "figures as one JSON object")
     ap.add_argument("--schemes", default="", help="batched section: only these formats (comma separated)")
@@ -837,7 +874,8 @@ def main() -> int:
                "schemes": lambda: schemes_section(ctx, gen, sptr, stream),
                "q8": lambda: q8_section(ctx, gen, sptr, stream),
                "gguf": lambda: gguf_section(ctx, gen, sptr, stream),
-               "peaks": lambda: peaks_section(ctx, stream)}[a.section]
+               "peaks": lambda: peaks_section(ctx, stream),
+               "floor": lambda: decode_floor(ctx, stream)}[a.section]
         print(json.dumps({"section": a.section, "result": run()}), flush=True)
         ctx.close()
         return 0
@@ -906,6 +944,8 @@ def main() -> int:
     torch.cuda.empty_cache()
     peaks = peaks_section(ctx, stream)
     roofline["frac_measured_read_peak"] = round(roofline["achieved"] / peaks["hbm_read_GBps"], 4)
+    floor = decode_floor(ctx, stream)
+    floor["frac_of_floor"] = round(floor["step_us"] / sum(p["us"] for p in per.values()), 4)
 
     out = {
         "metric": "Q4 GEMV HBM GB/s (% peak) at M=1; prefill dequant-GEMM TFLOP/s",
@@ -929,6 +969,7 @@ def main() -> int:
         "per_shape": per,
         "roofline": roofline,
         "measured_peaks": peaks,
+        "decode_floor": floor,
         "f32_contract_decode": f32_step,
     }
     if not a.no_extra:

@@ -241,12 +241,16 @@ int rlxq_moe_grouped(rlxq_ctx* ctx, int scheme, int mode, const void* x,
  *     v_mfma_f32_32x32x16_bf16 per wave on register operands, 8 workgroups
  *     of 4 waves per CU; *count = the flops issued.
  *   kind RLXQ_PROBE_READ (1): every byte of `buf` [work bytes, 16-byte
- *     aligned, a multiple of 4096] read once with 16-byte loads; *count =
- *     work.
- * sink: device memory of at least 8 x CUs x 4 bytes, written only to keep the
- * work live.  Time the call with events on `stream`. */
+ *     aligned, a multiple of 4096] read once with 16-byte loads, a
+ *     grid-stride loop over 8 workgroups per CU; *count = work.
+ *   kind RLXQ_PROBE_READ4 (2): the same bytes with the grid sized to them,
+ *     four independent 16-byte loads per thread (work <= 1 GiB): the
+ *     load-only floor of a small weight stream.
+ * sink: device memory of at least max(8 x CUs, 65536) x 4 bytes, written only
+ * to keep the work live.  Time the call with events on `stream`. */
 #define RLXQ_PROBE_MFMA 0
 #define RLXQ_PROBE_READ 1
+#define RLXQ_PROBE_READ4 2
 int rlxq_peak_probe(rlxq_ctx* ctx, int kind, const void* buf, int64_t work, void* sink, int64_t* count,
                     void* stream);
 

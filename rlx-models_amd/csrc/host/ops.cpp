@@ -656,6 +656,16 @@ int rlxq_peak_probe(rlxq_ctx* ctx, int kind, const void* buf, int64_t work, void
     *count = work;
     return launch(ctx, fn, dim3((unsigned)grid), dim3(256), 0, stream, args, "rlxq_probe_read");
   }
+  if (kind == RLXQ_PROBE_READ4) {
+    if (!buf) return fail(ctx, RLXQ_E_NULL, "peak_probe: buf must be non-null");
+    if (work % 4096 || !aligned(buf, 16)) return fail(ctx, RLXQ_E_ALIGN, "peak_probe: buf 16-byte aligned, 4 KiB multiple");
+    if (work > ((int64_t)1 << 30)) return fail(ctx, RLXQ_E_SHAPE, "peak_probe: READ4 reads at most 1 GiB");
+    if ((rc = get_fn(ctx, "rlxq_probe_read4", &fn))) return rc;
+    int64_t n16 = work / 16;
+    void* args[] = {(void*)&buf, &n16, &sink};
+    *count = work;
+    return launch(ctx, fn, dim3((unsigned)((n16 + 1023) / 1024)), dim3(256), 0, stream, args, "rlxq_probe_read4");
+  }
   return fail(ctx, RLXQ_E_SHAPE, "peak_probe: unknown kind");
 }
 

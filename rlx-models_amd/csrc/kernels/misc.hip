@@ -475,6 +475,31 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_probe_mfma(int64_t iters,
 // measured fastest on MI355X: deeper unrolls of the stride loop, and
 // contiguous spans per workgroup, read 2-15% slower); each workgroup's xor
 // of the data goes to sink[blockIdx.x] (keeps the loads live).
+// The same bytes, four independent 16-byte loads per thread issued before
+// any is used, over a grid sized to them (4 * gridDim.x * 256 >= n16).
+extern "C" __global__ __launch_bounds__(256) void rlxq_probe_read4(const uint4* __restrict__ src, int64_t n16,
+                                                                   uint32_t* __restrict__ sink) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint4 v[4];
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    const int64_t i = i0 + u * stride;
+    v[u] = i < n16 ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  __shared__ uint32_t red[256];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+    for (int k = 0; k < 256; k++) t ^= red[k];
+    sink[blockIdx.x] = t;
+  }
+}
+
 extern "C" __global__ __launch_bounds__(256) void rlxq_probe_read(const uint4* __restrict__ src, int64_t n16,
                                                                   uint32_t* __restrict__ sink) {
   uint32_t acc = 0;
