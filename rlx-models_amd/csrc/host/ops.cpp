@@ -189,8 +189,9 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   }
   // f32 output or f32 activations: the exact variant (bf16 weights, or f16
   // weights rounded once, do not keep 1e-3 on structured data).  Its
-  // register stages: one for the raw blocks of Q8_0, Q5_K, Q3_K (and Q6_K,
-  // late stores), two for the others.
+  // register stages: one for the raw blocks of Q8_0, Q5_K, Q3_K, MLX 4-bit
+  // (and Q6_K, late stores) and for Q4_1 and Q8_K with bf16 activations,
+  // two for the others.
   const bool split = x_dtype == RLXQ_F32;
   const bool want_exact = split || y_dtype == RLXQ_F32;
   // (the "...xs" kernels take f32 activations as hi / lo x16 rows)
@@ -198,7 +199,9 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   if (!te && want_exact && has_exact_gemm(scheme))
     vs = scheme == RLXQ_GGUF_Q6_K ? "w8lx"
          : (scheme == RLXQ_GGUF_Q8_0 || scheme == RLXQ_GGUF_Q5_K || scheme == RLXQ_GGUF_Q3_K ||
-            scheme == RLXQ_MLX_AFFINE4) ? "w8x" : "w8p2x";
+            scheme == RLXQ_MLX_AFFINE4 ||
+            // (Q4_1 and Q8_K: one stage for bf16 activations, two for f32)
+            (!split && (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q8_K))) ? "w8x" : "w8p2x";
   if (split && !vs.empty() && vs.back() == 'x') vs += 's';
   const bool w8 = tile == 256 && !vs.empty() && vs[0] == 'w';
   const bool exact = vs.find('x') != std::string::npos;

@@ -234,14 +234,36 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   auto store_b = [&](const Stage& P, int buf, int q) {
     uint16_t* dst = Bs + (buf * BN + brl) * GLD + ((tid >> 8) + q) * 32;
     if constexpr (EXACT) {
-      uint32_t hi[16], lo[16];
-      conv_blk_f16_split<SCH>(P.b[q], WSCALE, hi, lo);
-      const bool low = (brl >> 5) & 1;
+      // The two threads of a real column (B rows brl and brl ^ 32, the same
+      // raw block) split the block's K range: thread half h converts
+      // elements 16h .. 16h + 15 and writes their hi halves to the column's
+      // hi row and their lo halves to its lo row.
+      const int h = (brl >> 5) & 1;
+      float v[32];
+      blk_f32<SCH>(P.b[q], v);
+      // (the half picked by a bit mask, opaque to the optimiser: a select on
+      // h became an indexed access into v held in scratch memory)
+      uint32_t mh = 0u - (uint32_t)h;
+      asm volatile("" : "+v"(mh));
+      float w[16];
 #pragma unroll
-      for (int i = 0; i < 4; i++)
-        *reinterpret_cast<uint4*>(dst + 8 * i) =
-            low ? make_uint4(lo[4 * i], lo[4 * i + 1], lo[4 * i + 2], lo[4 * i + 3])
-                : make_uint4(hi[4 * i], hi[4 * i + 1], hi[4 * i + 2], hi[4 * i + 3]);
+      for (int e = 0; e < 16; e++)
+        w[e] = __uint_as_float((__float_as_uint(v[16 + e]) & mh) | (__float_as_uint(v[e]) & ~mh)) * WSCALE;
+      uint32_t hi[8], lo[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float a0 = w[2 * i], a1 = w[2 * i + 1];
+        const uint32_t h0 = f32_to_f16_bits(a0), h1 = f32_to_f16_bits(a1);
+        hi[i] = h0 | (h1 << 16);
+        lo[i] = f32_to_f16_bits(a0 - f16_bits_to_f32(h0)) | (f32_to_f16_bits(a1 - f16_bits_to_f32(h1)) << 16);
+      }
+      const int kof = ((tid >> 8) + q) * 32 + 16 * h;
+      uint16_t* dh = Bs + (buf * BN + (brl & ~32)) * GLD + kof;
+      uint16_t* dl = Bs + (buf * BN + (brl | 32)) * GLD + kof;
+      *reinterpret_cast<uint4*>(dh) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+      *reinterpret_cast<uint4*>(dh + 8) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+      *reinterpret_cast<uint4*>(dl) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+      *reinterpret_cast<uint4*>(dl + 8) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
     } else {
       uint32_t o[16];
       conv_blk<SCH>(P.b[q], o);
@@ -466,13 +488,17 @@ RLXQ_GEMM_INST(rlxq_gemm_q2_k_t128, SCH_Q2_K)
 // Exact f32-output variant (EXACT above): rlxq_gemm_<scheme>_t256w8[p2|l]x,
 // f16 MFMA on the prepared activations (natural order), f16 hi + lo weights
 // and rlxq_gemm_<scheme>_t256w8[p2|l]xs for f32 activations (hi / lo rows)
-#define RLXQ_GEMM256X_INST(SNAME, SCH, PF, SUFFIX, LATE)                                     \
+#define RLXQ_GEMM256XN_INST(SNAME, SCH, PF, SUFFIX, LATE)                                    \
   extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8##SUFFIX##x(rlxq_gemm_args a) { \
     rlxq::gemm256_body<SCH, 2, 4, PF, true, LATE, true, false>(a);                                 \
-  }                                                                                                \
+  }
+#define RLXQ_GEMM256XS_INST(SNAME, SCH, PF, SUFFIX, LATE)                                    \
   extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8##SUFFIX##xs(rlxq_gemm_args a) { \
     rlxq::gemm256_body<SCH, 2, 4, PF, true, LATE, true, true>(a);                                  \
   }
+#define RLXQ_GEMM256X_INST(SNAME, SCH, PF, SUFFIX, LATE) \
+  RLXQ_GEMM256XN_INST(SNAME, SCH, PF, SUFFIX, LATE)      \
+  RLXQ_GEMM256XS_INST(SNAME, SCH, PF, SUFFIX, LATE)
 RLXQ_GEMM256_INST(q4_1, SCH_Q4_1)
 RLXQ_GEMM256_INST(q4_0, SCH_Q4_0)
 RLXQ_GEMM256_INST(q8_0, SCH_Q8_0)
@@ -485,7 +511,10 @@ RLXQ_GEMM256_INST(mxfp4, SCH_MXFP4)
 RLXQ_GEMM256_INST(q5_k, SCH_Q5_K)
 RLXQ_GEMM256_INST(q3_k, SCH_Q3_K)
 RLXQ_GEMM256_INST(q2_k, SCH_Q2_K)
-RLXQ_GEMM256X_INST(q4_1, SCH_Q4_1, 2, p2, false)
+// (Q4_1 and Q8_K: the all-real-tiles variant for bf16 activations keeps one
+// register stage; with two it spilled)
+RLXQ_GEMM256XN_INST(q4_1, SCH_Q4_1, 1, , false)
+RLXQ_GEMM256XS_INST(q4_1, SCH_Q4_1, 2, p2, false)
 RLXQ_GEMM256X_INST(q4_0, SCH_Q4_0, 2, p2, false)
 RLXQ_GEMM256X_INST(q8_0, SCH_Q8_0, 1, , false)
 RLXQ_GEMM256X_INST(q4_k, SCH_Q4_K, 2, p2, false)
@@ -493,6 +522,7 @@ RLXQ_GEMM256X_INST(q6_k, SCH_Q6_K, 1, l, true)
 RLXQ_GEMM256X_INST(q5_k, SCH_Q5_K, 1, , false)
 RLXQ_GEMM256X_INST(q3_k, SCH_Q3_K, 1, , false)
 RLXQ_GEMM256X_INST(q2_k, SCH_Q2_K, 2, p2, false)
-RLXQ_GEMM256X_INST(q8_k, SCH_Q8_K, 2, p2, false)
+RLXQ_GEMM256XN_INST(q8_k, SCH_Q8_K, 1, , false)
+RLXQ_GEMM256XS_INST(q8_k, SCH_Q8_K, 2, p2, false)
 RLXQ_GEMM256X_INST(mlx4, SCH_MLX4, 1, , false)
 RLXQ_GEMM256X_INST(mlx8, SCH_MLX8, 2, p2, false)

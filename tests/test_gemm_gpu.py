@@ -172,7 +172,7 @@ def test_gemm_exact_shared_conversion(ctx, orc, monkeypatch, scheme, mkn):
     lo rows (128 output columns per tile), f16 MFMA on the prepared
     activations: f32 output within 1e-3."""
     monkeypatch.setenv("RLXQ_PREFILL", "gemm")
-    tile = "256w8x" if scheme == 1 else "256w8p2x"
+    tile = "256w8x" if scheme in (1, 3) else "256w8p2x"   # Q8_0, Q4_1: one register stage
     monkeypatch.setenv("RLXQ_GEMM_TILE", tile)
     m, k, n = mkn
     announce(f"gemm exact shared conversion t{tile} scheme={scheme} {mkn}")
@@ -197,7 +197,7 @@ def test_gemm_split_k(ctx, orc, monkeypatch, scheme, tile_ydt, splits):
     import rlxq
 
     tile, ydt = tile_ydt
-    one_stage = scheme in (1, 4)   # Q8_0 and MLX 4-bit: the one-stage exact variant
+    one_stage = scheme in (1, 3, 4)   # Q8_0, Q4_1, MLX 4-bit: the one-stage exact variant (bf16 x)
     if tile == "256w8x" and not one_stage or tile == "256w8p2x" and one_stage:
         pytest.skip("one exact tiling per scheme")
     m, k, n = 300, 64 * 13, 520
