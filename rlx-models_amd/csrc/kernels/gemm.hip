@@ -239,16 +239,13 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
       // elements 16h .. 16h + 15 and writes their hi halves to the column's
       // hi row and their lo halves to its lo row.
       const int h = (brl >> 5) & 1;
-      float v[32];
-      blk_f32<SCH>(P.b[q], v);
-      // (the half picked by a bit mask, opaque to the optimiser: a select on
-      // h became an indexed access into v held in scratch memory)
+      // (the half as a bit mask, opaque to the optimiser)
       uint32_t mh = 0u - (uint32_t)h;
       asm volatile("" : "+v"(mh));
       float w[16];
+      blk_f32_half<SCH>(P.b[q], mh, w);
 #pragma unroll
-      for (int e = 0; e < 16; e++)
-        w[e] = __uint_as_float((__float_as_uint(v[16 + e]) & mh) | (__float_as_uint(v[e]) & ~mh)) * WSCALE;
+      for (int e = 0; e < 16; e++) w[e] *= WSCALE;
       uint32_t hi[8], lo[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) {

@@ -371,6 +371,64 @@ RLXQ_DEV void blk_f32(const RawBlk<SCH>& r, float* v) {
   }
 }
 
+// Half h of a raw block's f32 weights (elements 16h .. 16h + 15, natural
+// order), h given as a bit mask (all ones for the second half), the same
+// arithmetic as blk_f32.  The nibble formats pick their code half before
+// converting; the others convert the whole block and pick by the mask
+// (bit operations: a select on h became an indexed access into a scratch
+// copy of the block's values).
+template <int SCH>
+RLXQ_DEV void blk_f32_half(const RawBlk<SCH>& r, uint32_t mh, float* v) {
+  auto pick4 = [&](uint4 a0, uint4 a1) {
+    return make_uint4((a1.x & mh) | (a0.x & ~mh), (a1.y & mh) | (a0.y & ~mh), (a1.z & mh) | (a0.z & ~mh),
+                      (a1.w & mh) | (a0.w & ~mh));
+  };
+  if constexpr (SCH == SCH_Q4_1 || SCH == SCH_Q4_0) {
+    uint32_t qs[4];
+    float d, m;
+    if constexpr (SCH == SCH_Q4_1) {
+      qs[0] = r.q.x; qs[1] = r.q.y; qs[2] = r.q.z; qs[3] = r.q.w;
+      d = f16_bits_to_f32(r.h & 0xffffu);
+      m = f16_bits_to_f32(r.h >> 16);
+    } else {
+      const uint32_t hd = r.off ? (r.w[0] >> 16) : (r.w[0] & 0xffffu);
+#pragma unroll
+      for (int i = 0; i < 4; i++) qs[i] = r.off ? r.w[i + 1] : align_bytes(r.w[i + 1], r.w[i], 2);
+      d = f16_bits_to_f32(hd);
+      m = -8.f * d;
+    }
+    // elements 0..15: low nibbles, 16..31: high nibbles
+    const uint32_t sh = mh & 4u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      uint32_t c = (qs[i] >> sh) & 0x0F0F0F0Fu;
+      asm volatile("" : "+v"(c));
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[4 * i + e] = fmaf(d, (float)((c >> (8 * e)) & 0xffu), m);
+    }
+  } else if constexpr (SCH == SCH_Q4_K) {
+    const uint32_t hd[4] = {r.hd.x, r.hd.y, r.hd.z, r.hd.w};
+    float sc, mn;
+    q4k_scale_min(hd, (int)r.sub, sc, mn);
+    const float d1 = f16_bits_to_f32(hd[0] & 0xffffu) * sc, m1 = -(f16_bits_to_f32(hd[0] >> 16) * mn);
+    const uint4 q = pick4(r.q0, r.q1);
+    const uint32_t qs[4] = {q.x, q.y, q.z, q.w};
+    const int sh = 4 * (int)(r.sub & 1u);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      uint32_t c = (qs[i] >> sh) & 0x0F0F0F0Fu;
+      asm volatile("" : "+v"(c));
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[4 * i + e] = fmaf(d1, (float)((c >> (8 * e)) & 0xffu), m1);
+    }
+  } else {
+    float w[32];
+    blk_f32<SCH>(r, w);
+#pragma unroll
+    for (int e = 0; e < 16; e++) v[e] = __uint_as_float((__float_as_uint(w[16 + e]) & mh) | (__float_as_uint(w[e]) & ~mh));
+  }
+}
+
 // The block's f32 weights times `scale` (a power of two) as f16 hi and lo
 // halves, natural order, two per dword: hi = f16(w), lo = f16(w - hi), so
 // that hi + lo keeps ~22 significant bits of the f32 weight.

@@ -72,7 +72,7 @@ def test_noalloc_rejects_oversized_scratch(ctx, orc):
     import rlxq
 
     rng = np.random.default_rng(79)
-    m, k, n = 1024, 12288, 4096       # f32 output: f16 activations (24 MiB) + split-K partials
+    m, k, n = 3072, 12288, 4096       # f32 output: the exact GEMM's f16 activations alone are 72 MiB
     w = _q4_1(orc, rng, n, k)
     x = _x(rng, m, k)
     y = torch.zeros((m, n), device="cuda")
