@@ -84,7 +84,11 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   const int64_t tiles_n = (n + 16 * NT - 1) / (16 * NT), mch = (mr + 16 * MT - 1) / (16 * MT);
   const int64_t chunks = k / 128;
   const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-  int64_t target = 2 * cus;
+  // 64-row chunks with a two-deep ring (the byte-code formats past 32 rows):
+  // one workgroup per CU, half the K splits (down 12288->4096 at M=64: Q8_0
+  // 51.7 -> 43.0 us, Q8_K 51.2 -> 43.1, Q2_K 61.0 -> 52.9; with a one-deep
+  // ring, or 16-row chunks, fewer splits measured the same or slower)
+  int64_t target = (MT >= 4 && D >= 2) ? cus : 2 * cus;
   if (const char* e = std::getenv("RLXQ_SKINNY_WGS")) target = (int64_t)(cus * std::atof(e));
   int64_t splits = 1;
   while (tiles_n * mch * splits < target && splits * 2 * 4 <= chunks && splits < 32) splits *= 2;
