@@ -705,6 +705,9 @@ RLXQ_GEMVXS_Q4K
   RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U1_D2_W8_F, SCH, 1, 2, 8)          \
   RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U2_D2_W4_F, SCH, 2, 2, 4)          \
   RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U2_D1_W4_F, SCH, 2, 1, 4)          \
+  RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U2_D1_W8_F, SCH, 2, 1, 8)          \
+  RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8_F, SCH, 2, 2, 8)          \
+  RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U2_D1_W16_F, SCH, 2, 1, 16)        \
   RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U3_D1_W8_F, SCH, 3, 1, 8)          \
   RLXQ_GEMVXSF_INST(rlxq_gemvxs_##SNAME##_U4_D1_W8_F, SCH, 4, 1, 8)
 // K split inside the workgroup (KS waves per weight row):

@@ -206,6 +206,27 @@ def test_single_row_f32_register_path(ctx, orc, scheme, kn):
     assert rel_err(got, want) <= TOL, kern
 
 
+# every compiled single-row f32 variant "NU:D,W" (NU unit chunks of 64: K
+# up to 2048 NU)
+F_VARIANTS = ["1:2,8", "2:2,4", "2:1,4", "2:1,8", "2:2,8", "2:1,16", "3:1,8", "4:1,8"]
+
+
+@pytest.mark.parametrize("cfg", F_VARIANTS)
+def test_single_row_f32_every_variant(ctx, orc, monkeypatch, cfg):
+    nu, dw = cfg.split(":")
+    monkeypatch.setenv("RLXQ_GEMV_XSF", dw)
+    d, w = dw.split(",")
+    k = 2048 * int(nu)
+    for n in (4096, 77, 3):
+        announce(f"f32 contract gemv m=1 variant {cfg} k={k} n={n}")
+        rng = np.random.default_rng(k + n + int(w))
+        packed = _exact_f16_q4_1(orc, rng, n, k)
+        x = rng.standard_normal((1, k)).astype(np.float32)
+        got, kern = _f32_run(ctx, Q4_1, x, _t(packed), n)
+        assert kern == f"rlxq_gemvxs_q4_1_U{nu}_D{d}_W{w}_F", kern
+        assert rel_err(got, _want(orc, Q4_1, x, packed, k)) <= TOL_EXACT_W
+
+
 @pytest.mark.parametrize("kn", [(4096, 16384), (12288, 520), (10240, 33)], ids=str)
 def test_single_row_f32_q4_1_k_split_defaults(ctx, orc, kn):
     """Q4_1 rows at gate_up's width and K past four unit chunks (down) take
