@@ -21,7 +21,8 @@ Extra keys of the same JSON line:
   prefill_detail  config 4: Q4_1 dequant-GEMM, M in {512, 2048, 4096}, Q4_K
                   at M=4096, and the W8A8 variant (per-row int8 activations
                   computed on the fly x per-channel int8 weights)
-  batched_decode  config 3: Q4_1 and Q8_0 (and Q4_K, Q6_K), M in {1, 4, 16, 64}
+  batched_decode  config 3: Q4_1 and Q8_0 (and every other format), M in
+                  {1, 4, 16, 64}, bf16 x; and Q4_1 with F32 x and y at 16, 64
   moe             config 5: routed-expert grouped GEMV, 16 tokens, top-8 of 128
   moe_q4_k        the same with Q4_K expert banks (a Q4_K_M MoE checkpoint)
   moe_prefill     the config-5 layer at 256 tokens (grouped MFMA kernels)
@@ -385,13 +386,15 @@ def prefill_section(ctx, gen, sptr, stream, quick: bool) -> dict:
         for m in ms_list:
             x = torch.randn((m, k), generator=gen, device="cuda").to(torch.bfloat16)
             y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
-            run = lambda i: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_1, n, y=y, stream=sptr)
+            run = lambda i, sp=sptr: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_1, n, y=y, stream=sp)
             run(0)
             torch.cuda.synchronize()
-            us = _time_us(run, 5, stream)
+            t = _gpu_us(ctx, run, 20 if m <= 512 else 5, stream)
+            us = t["us"]
             tf = 2.0 * m * n * k / us / 1e6
             res["q4_1"][f"{name}_m{m}"] = {"m": m, "k": k, "n": n, "kernel": ctx.last_kernel, "us": round(us, 1),
-                                           "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+                                           "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+                                           "us_eager": t["us_eager"], "us_graph": t["us_graph"]}
             del x, y
         del w
         # GGUF Q4_K on the same kernels (super-block head + group codes per K step)
@@ -399,10 +402,10 @@ def prefill_section(ctx, gen, sptr, stream, quick: bool) -> dict:
         m = 4096
         x = torch.randn((m, k), generator=gen, device="cuda").to(torch.bfloat16)
         y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
-        run = lambda i: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_K, n, y=y, stream=sptr)
+        run = lambda i, sp=sptr: ctx.dequant_matmul(x, w, rlxq.GGUF_Q4_K, n, y=y, stream=sp)
         run(0)
         torch.cuda.synchronize()
-        us = _time_us(run, 5, stream)
+        us = _gpu_us(ctx, run, 5, stream)["us"]
         tf = 2.0 * m * n * k / us / 1e6
         res["q4_k"][f"{name}_m{m}"] = {"m": m, "k": k, "n": n, "kernel": ctx.last_kernel, "us": round(us, 1),
                                        "TFLOPs": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
@@ -413,10 +416,10 @@ def prefill_section(ctx, gen, sptr, stream, quick: bool) -> dict:
                 wt = synth_q4_1_gpu(n, k, gen)
             x32 = torch.randn((m, k), generator=gen, device="cuda")
             y32 = torch.empty((m, n), device="cuda")
-            run = lambda i: ctx.dequant_matmul(x32, wt, sch, n, y=y32, stream=sptr)
+            run = lambda i, sp=sptr: ctx.dequant_matmul(x32, wt, sch, n, y=y32, stream=sp)
             run(0)
             torch.cuda.synchronize()
-            us = _time_us(run, 3, stream)
+            us = _gpu_us(ctx, run, 3, stream)["us"]
             tf = 2.0 * m * n * k / us / 1e6
             res["f32_contract"][f"{sname}_{name}_m{m}"] = {"m": m, "k": k, "n": n, "kernel": ctx.last_kernel,
                                                           "us": round(us, 1), "TFLOPs": round(tf, 1),
@@ -428,10 +431,10 @@ def prefill_section(ctx, gen, sptr, stream, quick: bool) -> dict:
         sw = torch.rand((n,), device="cuda", generator=gen) * 0.01 + 1e-4
         x = torch.randn((m, k), generator=gen, device="cuda").to(torch.bfloat16)
         y = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
-        run = lambda i: ctx.w8a8_gemm(x, wq, sw, n, y=y, stream=sptr)
+        run = lambda i, sp=sptr: ctx.w8a8_gemm(x, wq, sw, n, y=y, stream=sp)
         run(0)
         torch.cuda.synchronize()
-        us = _time_us(run, 5, stream)
+        us = _gpu_us(ctx, run, 5, stream)["us"]
         tops = 2.0 * m * n * k / us / 1e6
         res["w8a8"][f"{name}_m{m}"] = {"m": m, "k": k, "n": n, "kernel": ctx.last_kernel, "us": round(us, 1),
                                        "TOPs": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
@@ -518,6 +521,28 @@ def batched_section(ctx, gen, sptr, stream, only=None) -> dict:
                                                "GBps": round(b / us / 1e3, 1),
                                                "TFLOPs": round(2.0 * m * n * k / us / 1e6, 2),
                                                "us_eager": t["us_eager"], "us_graph": t["us_graph"]}
+            del ws
+            torch.cuda.empty_cache()
+    # the reference operator's own operand types (F32 x in, F32 y out) on the
+    # same kernels (x as hi + lo f16 rows), Q4_1
+    if not only or "q4_1" in only:
+        for name, k, n in (("gate_up", 4096, 24576), ("down", 12288, 4096)):
+            ws = [synth_q4_1_gpu(n, k, gen) for _ in range(_copies(n * k * Q4_1_BPW))]
+            for m in (16, 64):
+                x = torch.randn((m, k), generator=gen, device="cuda")
+                y = torch.empty((m, n), device="cuda")
+
+                def run(i, sp=sptr, x=x, y=y, ws=ws, n=n):
+                    return ctx.dequant_matmul(x, ws[i % len(ws)], rlxq.GGUF_Q4_1, n, y=y, stream=sp)
+                for i in range(len(ws)):
+                    run(i)
+                torch.cuda.synchronize()
+                kern = ctx.last_kernel
+                t = _gpu_us(ctx, run, 4 * len(ws), stream)
+                b = gemv_bytes(k, n, m=m, bpw=Q4_1_BPW, xsize=4)
+                res[f"f32_q4_1_{name}_m{m}"] = {"kernel": kern, "us": round(t["us"], 2),
+                                                "GBps": round(b / t["us"] / 1e3, 1), "x": "f32", "y": "f32",
+                                                "us_eager": t["us_eager"], "us_graph": t["us_graph"]}
             del ws
             torch.cuda.empty_cache()
     return res
