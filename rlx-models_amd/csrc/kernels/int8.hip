@@ -146,17 +146,23 @@ RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
       P.b[i] = (bnok[i] && k < a.K) ? v : make_uint4(0u, 0u, 0u, 0u);
     }
   };
-  auto store = [&](const Stage& P, int buf) {
+  auto store_a = [&](const Stage& P, int buf) {
 #pragma unroll
     for (int i = 0; i < AP; i++) {
       const int c = tid + NT * i, r = c / ACH, cc = c % ACH;
       *reinterpret_cast<uint4*>(As + (buf * BM + r) * AST + 16 * cc) = P.a[i];
     }
+  };
+  auto store_b = [&](const Stage& P, int buf) {
 #pragma unroll
     for (int i = 0; i < BP; i++) {
       const int c = tid + NT * i, r = c / BCH, cc = c % BCH;
       *reinterpret_cast<uint4*>(Bs + (buf * BK + r) * BST + 16 * cc) = P.b[i];
     }
+  };
+  auto store = [&](const Stage& P, int buf) {
+    store_a(P, buf);
+    store_b(P, buf);
   };
 
   i32x16_t acc[TM][TN];
@@ -168,11 +174,10 @@ RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
   const int g = lane >> 4, s = lane & 15;
-  auto compute = [&](int cur) {
+  auto compute_ks = [&](int cur, int ks) {
     const uint8_t* Ab = As + (cur * BM + wm * WM) * AST;
     const uint8_t* Bb = Bs + cur * BK * BST + wn * WN;
-#pragma unroll
-    for (int ks = 0; ks < BK / 32; ks++) {
+    {
       i32x4_t af[TM], bq[TN];
 #pragma unroll
       for (int i = 0; i < TM; i++)
@@ -191,18 +196,30 @@ RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
         for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bq[j], acc[i][j], 0, 0, 0);
     }
   };
+  auto compute = [&](int cur) {
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ks++) compute_ks(cur, ks);
+  };
   if constexpr (PF == 1) {
+    // the next step's LDS stores sit between the MFMA groups of this one
+    // (activation rows after the first, weight rows after the second), so
+    // they overlap the MFMAs instead of following them
     Stage P;
     load(0, P);
     store(P, 0);
     __syncthreads();
-    for (int kt = 0; kt < KT; kt++) {
-      const bool more = kt + 1 < KT;
-      if (more) load(kt + 1, P);
-      compute(kt & 1);
-      if (more) store(P, (kt & 1) ^ 1);
+    for (int kt = 0; kt + 1 < KT; kt++) {
+      load(kt + 1, P);
+      const int cur = kt & 1;
+#pragma unroll
+      for (int ks = 0; ks < BK / 32; ks++) {
+        compute_ks(cur, ks);
+        if (ks == 0) store_a(P, cur ^ 1);
+        if (ks == 1) store_b(P, cur ^ 1);
+      }
       __syncthreads();
     }
+    compute((KT - 1) & 1);
   } else {
     // global loads two K steps ahead in two register stages, the loop
     // unrolled by two so each stage is a fixed register set
