@@ -3,7 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
 
 One "step" is the decode-token GEMV work of Qwen3-8B with Q4_1 group-32
-weights at M=1: 36 layers x (o 4096->4096, fused qkv
+weights at M=1 (the headline metric's config 2): 36 layers x (o 4096->4096, fused qkv
 4096->6144, fused gate|up 4096->24576, down 12288->4096), each layer with its
 own weights (4.35 GB in HBM, so the 256 MB MALL cannot serve repeats),
 activations bf16 N(0,1), outputs f32.  Inputs are resident in HBM before the
