@@ -111,15 +111,20 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   const bool q6k = scheme == RLXQ_GGUF_Q6_K;
   // (MLX: groups of whole 32-blocks; MXFP4: E8M0 scale bytes only, whose
   // products with the codes are exact in bf16)
-  const bool sk_ok = xbf && k % 128 == 0 &&
+  // (f32 activations run as hi + lo row pairs, added in the epilogue)
+  const bool kq_other = scheme == RLXQ_GGUF_Q5_K || scheme == RLXQ_GGUF_Q3_K || scheme == RLXQ_GGUF_Q2_K ||
+                        scheme == RLXQ_GGUF_Q8_K;
+  const bool sk_ok = k % 128 == 0 &&
                      (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q8_0 ||
-                      ((q4k || q6k) && k % 256 == 0) ||
+                      ((q4k || q6k || kq_other) && k % 256 == 0) ||
                       ((scheme == RLXQ_MLX_AFFINE4 || scheme == RLXQ_MLX_AFFINE8) && group >= 32 &&
                        group % 32 == 0 && k % group == 0) ||
                       (scheme == RLXQ_MLX_MXFP4 && sb_dtype == RLXQ_U8));
-  // (the gathered f16 rows take about 2 K bytes per entry: calls needing
-  // more than 1 GiB of them stay on the GEMV kernels)
-  const bool sk_fits = (double)(n_entries + fired_est * 63) * (double)k * 2.0 <= (double)(1u << 30);
+  // (the gathered f16 rows take about 2 K bytes per entry, twice that for
+  // f32 activations: calls needing more than 1 GiB of them stay on the GEMV
+  // kernels)
+  const bool sk_fits =
+      (double)(n_entries + fired_est * 63) * (double)k * (xbf ? 2.0 : 4.0) <= (double)(1u << 30);
   bool sk = sk_ok && sk_fits && n_entries >= 8 * fired_est;
   if (const char* ev = std::getenv("RLXQ_MOE_KERNEL")) {
     if (!std::strcmp(ev, "sk")) sk = sk_ok && sk_fits;
@@ -211,16 +216,23 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   // (chunks of 16 rows with 4 weight tiles measured best at 16 entries per
   // expert: gate|up 115 us and down 83 us at config 5 with 256 tokens,
   // against 131 and 130 with 2 tiles; 64-row chunks keep 2 tiles)
-  int sk_mt = avg_e <= 24.0 ? 1 : (avg_e <= 48.0 ? 2 : 4), sk_nt = 0, sk_d = 0;
+  // (f32 activations: two x16 rows per entry, so the same x16 rows per
+  // expert at half the entries)
+  const double xr_e = xbf ? avg_e : 2.0 * avg_e;
+  int sk_mt = xr_e <= 24.0 ? 1 : (xr_e <= 48.0 ? 2 : 4), sk_nt = 0, sk_d = 0;
   if (const char* ev = std::getenv("RLXQ_MOE_SK")) std::sscanf(ev, "%d,%d,%d", &sk_mt, &sk_nt, &sk_d);   // tuning
   if (sk_mt != 1 && sk_mt != 2 && sk_mt != 4) sk_mt = 1;
   if (sk_nt != 2 && sk_nt != 4 && sk_nt != 8) sk_nt = sk_mt == 4 ? 2 : 4;
-  const int64_t rpc = 16 * sk_mt;
-  const int64_t sk_mp = sk ? ((n_entries + fired_est * (rpc - 1) + rpc - 1) / rpc) * rpc : 0;
+  // gathered rows per chunk (f32 activations: x16 row pairs, so half the
+  // entries per 16 MT-row chunk)
+  const bool sk_pairs = !xbf;
+  const int64_t rpc = sk_pairs ? 8 * sk_mt : 16 * sk_mt;
+  const int64_t sk_mp = sk ? ((n_entries + fired_est * (rpc - 1) + rpc - 1) / rpc) * rpc : 0;   // gathered rows
+  const int64_t sk_xr = sk_pairs ? 2 * sk_mp : sk_mp;                                            // x16 rows
   auto r256 = [](size_t b) { return (b + 255) & ~size_t(255); };
   const size_t cmap_bytes = sk ? r256((size_t)(1 + sk_mp / rpc) * 4) : 0, emap_bytes = sk ? r256((size_t)sk_mp * 4) : 0;
-  const size_t x16_bytes = sk ? r256((size_t)sk_mp * k * 2) : 0, is_bytes = sk ? r256((size_t)sk_mp * 4) : 0;
-  const size_t sum_bytes = sk ? r256((size_t)sk_mp * (k / 32) * 4) : 0;   // block sums of the gathered rows
+  const size_t x16_bytes = sk ? r256((size_t)sk_xr * k * 2) : 0, is_bytes = sk ? r256((size_t)sk_xr * 4) : 0;
+  const size_t sum_bytes = sk ? r256((size_t)sk_xr * (k / 32) * 4) : 0;   // block sums of the x16 rows
   const size_t total_ws = table_bytes + tmp_bytes + cmap_bytes + emap_bytes + x16_bytes + is_bytes + sum_bytes;
   void* ws = nullptr;
   if (total_ws && (rc = workspace(ctx, total_ws, &ws, stream))) return rc;
@@ -266,10 +278,11 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     xa.x16 = reinterpret_cast<uint16_t*>(skb + cmap_bytes + emap_bytes);
     xa.inv_s = reinterpret_cast<float*>(skb + cmap_bytes + emap_bytes + x16_bytes);
     xa.ssum = reinterpret_cast<float*>(skb + cmap_bytes + emap_bytes + x16_bytes + is_bytes);
-    xa.M = sk_mp;
+    xa.M = sk_xr;
     xa.K = k;
-    xa.Mp = sk_mp;
-    xa.x_bf16 = 1;
+    xa.Mp = sk_xr;
+    xa.x_bf16 = xbf ? 1 : 0;
+    xa.split = sk_pairs ? 1 : 0;   // (rows 2r, 2r + 1: hi and lo of gathered row r)
     xa.nibble_order = sk_order(scheme);
     xa.frag_major = 1;
     xa.rdiv = x_div;
@@ -279,7 +292,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     hipFunction_t fx;
     if ((rc = get_fn(ctx, "rlxq_x16_prep", &fx))) return rc;
     void* xargs[] = {&xa};
-    if ((rc = launch(ctx, fx, dim3((unsigned)sk_mp, (unsigned)((k + 2047) / 2048)), dim3(256), 0, stream, xargs,
+    if ((rc = launch(ctx, fx, dim3((unsigned)sk_xr, (unsigned)((k + 2047) / 2048)), dim3(256), 0, stream, xargs,
                      "rlxq_x16_prep")))
       return rc;
     // 2c. the grouped MFMA kernel over (chunk, tile): NT weight tiles of 16
@@ -291,7 +304,8 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     int D = sk_d;
     if (D <= 0) D = NT >= 4 ? (NT == 8 && sk_mt == 2 ? 1 : (sk_mt == 4 ? 1 : 2))
                             : (sk_mt == 1 ? (q4k ? 3 : 4) : (sk_mt == 2 ? 3 : 2));
-    if (sk_d <= 0 && q6k) D = NT >= 4 || sk_mt == 4 ? 1 : 2;
+    if (sk_d <= 0 && (q6k || scheme == RLXQ_GGUF_Q5_K || scheme == RLXQ_GGUF_Q3_K)) D = NT >= 4 || sk_mt == 4 ? 1 : 2;
+    if (sk_d <= 0 && scheme == RLXQ_GGUF_Q2_K && NT < 4 && sk_mt == 1) D = 3;
     rlxq_moe_sk_args ka;
     std::memset(&ka, 0, sizeof ka);
     ka.x16 = xa.x16;
@@ -305,7 +319,8 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
     ka.K = k;
     ka.rb = rb;
     ka.y_ld = width;
-    ka.Mp = sk_mp;
+    ka.Mp = sk_xr;
+    ka.pairs = sk_pairs ? 1 : 0;
     ka.tiles_n = (int32_t)((width + 16 * nh - 1) / (16 * nh));
     ka.y_bf16 = (!combine && y_dtype == RLXQ_BF16) ? 1 : 0;
     ka.swiglu = swiglu ? 1 : 0;
@@ -317,7 +332,7 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
                   swiglu ? "_sw" : "");
     hipFunction_t fk;
     if ((rc = get_fn(ctx, name, &fk))) return rc;
-    const int64_t grid = (sk_mp / rpc) * ka.tiles_n;
+    const int64_t grid = (sk_mp / rpc) * ka.tiles_n;   // chunks x tiles
     if (grid > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, std::string(what) + ": grid too large");
     const size_t lds = 2 * (size_t)(sk_mt * NT * 4) * 64 * 4;
     void* kargs[] = {&ka};

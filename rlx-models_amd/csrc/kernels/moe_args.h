@@ -75,8 +75,9 @@ typedef struct rlxq_moe_sk_args {
   int32_t tiles_n, y_bf16;
   int32_t swiglu;         /* 1: rows [0, N/2) gate, [N/2, N) up; y [entries, N/2]
                              = silu(x.Wg^T) * (x.Wu^T)                     */
-  /* pairs: the gathered x16 rows are hi/lo pairs (row 2r + 1 the remainder
-   * of row 2r, both on emap[2r]'s entry); the epilogue adds each pair     */
+  /* pairs: the x16 rows are hi/lo pairs (row 2r + 1 the remainder of row
+   * 2r, both of gathered row r, whose entry is emap[r]); the epilogue adds
+   * each pair                                                             */
   int32_t pairs;
   /* MLX affine: per-group scales and biases [E, N, K / group] (f32, or bf16
    * where sb_bf16 == 1); MXFP4: E8M0 bytes [E, N, K / 32] (sb_bf16 == 2);

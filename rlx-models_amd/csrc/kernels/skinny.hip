@@ -327,21 +327,28 @@ RLXQ_DEV void moe_sk_body(const rlxq_moe_sk_args& a) {
   if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.ssum, a.Mp, m0, a.bank + (int64_t)e * a.N * a.rb, a.rb, a.K, 0, a.K,
                                       wrow, wok, acc, sc, bi, a.group, a.sb_bf16))
     return;
-  // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4
+  // C[i][j] of the 16x16 tile sits in lane j + 16*(i/4), register i%4.
+  // With pairs, x16 rows 2r and 2r + 1 (a lane's registers 0, 1 and 2, 3)
+  // are the hi and lo rows of gathered row r: their sums are added.
 #pragma unroll
   for (int mt = 0; mt < MT; mt++)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
+      if (a.pairs && (r & 1)) continue;
       const int64_t m = m0 + 16 * mt + 4 * g + r;
-      const int32_t ent = a.emap[m];
+      const int32_t ent = a.emap[a.pairs ? m >> 1 : m];
       if (ent < 0) continue;
       const float is = a.inv_s[m];
+      const int r2 = a.pairs ? (r < 3 ? r + 1 : r) : r;   // (the pair's lo register)
 #pragma unroll
       for (int t = 0; t < NH; t++) {
         const int64_t c = n0 + 16 * t + j;
         if (c >= width) continue;
-        float o = acc[mt][t][r] * is;
-        if constexpr (SW) o = o / (1.f + expf(-o)) * (acc[mt][t + NH][r] * is);   // silu(g) * u
+        float o = (a.pairs ? acc[mt][t][r] + acc[mt][t][r2] : acc[mt][t][r]) * is;
+        if constexpr (SW) {   // silu(g) * u
+          const float u = (a.pairs ? acc[mt][t + NH][r] + acc[mt][t + NH][r2] : acc[mt][t + NH][r]) * is;
+          o = o / (1.f + expf(-o)) * u;
+        }
         const int64_t off = (int64_t)ent * a.y_ld + c;
         if (a.y_bf16) reinterpret_cast<uint16_t*>(a.y)[off] = (uint16_t)f32_to_bf16_bits(o);
         else reinterpret_cast<float*>(a.y)[off] = o;
@@ -859,3 +866,14 @@ RLXQ_MOESK_INST(q6_k, SCH_Q6_K, 1, 4, 1)
 RLXQ_MOESK_INST(q6_k, SCH_Q6_K, 2, 2, 2)
 RLXQ_MOESK_INST(q6_k, SCH_Q6_K, 2, 4, 1)
 RLXQ_MOESK_INST(q6_k, SCH_Q6_K, 4, 2, 1)
+// Q5_K, Q3_K (21- and 24-dword raw blocks) as Q6_K; Q2_K as Q4_K, Q8_K as Q8_0
+#define RLXQ_MOESK_SHALLOW(SNAME, SCH) \
+  RLXQ_MOESK_INST(SNAME, SCH, 1, 2, 2) \
+  RLXQ_MOESK_INST(SNAME, SCH, 1, 4, 1) \
+  RLXQ_MOESK_INST(SNAME, SCH, 2, 2, 2) \
+  RLXQ_MOESK_INST(SNAME, SCH, 2, 4, 1) \
+  RLXQ_MOESK_INST(SNAME, SCH, 4, 2, 1)
+RLXQ_MOESK_SHALLOW(q5_k, SCH_Q5_K)
+RLXQ_MOESK_SHALLOW(q3_k, SCH_Q3_K)
+RLXQ_MOESK_SCHEME(q2_k, SCH_Q2_K, 3)
+RLXQ_MOESK_SCHEME(q8_k, SCH_Q8_K, 4)
