@@ -26,6 +26,7 @@ Extra keys of the same JSON line:
   moe             config 5: routed-expert grouped GEMV, 16 tokens, top-8 of 128
   moe_q4_k        the same with Q4_K expert banks (a Q4_K_M MoE checkpoint)
   moe_prefill     the config-5 layer at 256 tokens (grouped MFMA kernels)
+  moe_prefill_f32 the same with f32 hidden rows and intermediate
   q8_gemv         config 1: Q8_0 2048->2048, f32 activations
   measured_peaks  this GPU's copy and streaming-read bandwidth and register-
                   only bf16 MFMA rate (rlxq_peak_probe); roofline and
@@ -748,13 +749,15 @@ def schemes_section(ctx, gen, sptr, stream) -> dict:
     return res
 
 
-def moe_section(ctx, gen, sptr, stream, scheme: str = "q4_1", tokens: int = 16) -> dict:
+def moe_section(ctx, gen, sptr, stream, scheme: str = "q4_1", tokens: int = 16, xdt: str = "bf16") -> dict:
     """Config 5: one MoE FFN of a Qwen3-30B-A3B-like layer for 16 tokens, as
     three calls: route (softmax of N(0,1) logits over 128 experts, top-8,
     renormalised), the fused gate|up 2048->1536 + SwiGLU per (token, slot),
     and down 768->2048 with the probability-weighted combine.  Two layers with
     their own expert banks and logits alternate (755 MB of banks).  `tokens`
-    = 256: the same layer at a prefill size (the grouped MFMA kernels)."""
+    = 256: the same layer at a prefill size (the grouped MFMA kernels).
+    `xdt` = "f32": hidden rows and the intermediate in f32 (the reference's
+    operand types; hi/lo row pairs on the grouped MFMA kernels)."""
     import torch
     import rlxq
 
@@ -763,8 +766,9 @@ def moe_section(ctx, gen, sptr, stream, scheme: str = "q4_1", tokens: int = 16) 
                        "q4_k": (synth_q4_k_gpu, rlxq.GGUF_Q4_K, 144 / 256)}[scheme]
     banks = [(synth(E * 2 * I, H, gen), synth(E * H, I, gen)) for _ in range(2)]
     logits = [torch.randn((T, E), generator=gen, device="cuda") for _ in range(2)]
-    x = torch.randn((T, H), generator=gen, device="cuda").to(torch.bfloat16)
-    act = torch.empty((T * TOPK, I), device="cuda", dtype=torch.bfloat16)
+    adt = torch.float32 if xdt == "f32" else torch.bfloat16
+    x = torch.randn((T, H), generator=gen, device="cuda").to(adt)
+    act = torch.empty((T * TOPK, I), device="cuda", dtype=adt)
     y = torch.empty((T, H), device="cuda")
     routes = [None, None]
 
@@ -784,8 +788,9 @@ def moe_section(ctx, gen, sptr, stream, scheme: str = "q4_1", tokens: int = 16) 
     us = t["us"]
     u = sum(uniq) / len(uniq)
     per_expert = 2 * I * H * bpw + H * I * bpw
-    b = u * per_expert + T * H * 2 + T * TOPK * I * 2 * 2 + T * H * 4
-    out = {"tokens": T, "us_per_layer": round(us, 2), "unique_experts": u, "GBps": round(b / us / 1e3, 1),
+    ab = 4 if xdt == "f32" else 2
+    b = u * per_expert + T * H * ab + T * TOPK * I * ab * 2 + T * H * 4
+    out = {"tokens": T, "activations": xdt, "us_per_layer": round(us, 2), "unique_experts": u, "GBps": round(b / us / 1e3, 1),
            "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
            "bytes_model": f"unique experts x {int(per_expert):,} B + activations", "kernel_down": kern_down,
            "us_eager": t["us_eager"], "us_graph": t["us_graph"]}
@@ -875,7 +880,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="only the decode step and its roofline")
     ap.add_argument("--quick", action="store_true", help="prefill at M=4096 only")
     ap.add_argument("--cpu-seconds", type=float, default=16.0)
-    ap.add_argument("--section", choices=["prefill", "batched", "moe", "moe_q4_k", "moe_prefill", "schemes", "q8",
+    ap.add_argument("--section", choices=["prefill", "batched", "moe", "moe_q4_k", "moe_prefill",
+                                          "moe_prefill_f32", "schemes", "q8",
                                           "gguf", "peaks", "floor"],
                     help="profiling mode: run only this section (no decode step, no CPU baseline) and print its "
                          "figures as one JSON object")
@@ -913,6 +919,7 @@ def main() -> int:
                "moe": lambda: moe_section(ctx, gen, sptr, stream),
                "moe_q4_k": lambda: moe_section(ctx, gen, sptr, stream, "q4_k"),
                "moe_prefill": lambda: moe_section(ctx, gen, sptr, stream, "q4_1", 256),
+               "moe_prefill_f32": lambda: moe_section(ctx, gen, sptr, stream, "q4_1", 256, "f32"),
                "schemes": lambda: schemes_section(ctx, gen, sptr, stream),
                "q8": lambda: q8_section(ctx, gen, sptr, stream),
                "gguf": lambda: gguf_section(ctx, gen, sptr, stream),
@@ -1030,6 +1037,7 @@ def main() -> int:
         out["moe"] = moe_section(ctx, gen, sptr, stream)
         out["moe_q4_k"] = moe_section(ctx, gen, sptr, stream, "q4_k")
         out["moe_prefill"] = moe_section(ctx, gen, sptr, stream, "q4_1", 256)
+        out["moe_prefill_f32"] = moe_section(ctx, gen, sptr, stream, "q4_1", 256, "f32")
         out["schemes"] = schemes_section(ctx, gen, sptr, stream)
         out["q8_gemv"] = q8_section(ctx, gen, sptr, stream)
         out["gguf_upload"] = gguf_section(ctx, gen, sptr, stream)

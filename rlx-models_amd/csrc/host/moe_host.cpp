@@ -216,10 +216,10 @@ int grouped_run(rlxq_ctx* ctx, const char* what, int scheme, int group, const vo
   // (chunks of 16 rows with 4 weight tiles measured best at 16 entries per
   // expert: gate|up 115 us and down 83 us at config 5 with 256 tokens,
   // against 131 and 130 with 2 tiles; 64-row chunks keep 2 tiles)
-  // (f32 activations: two x16 rows per entry, so the same x16 rows per
-  // expert at half the entries)
-  const double xr_e = xbf ? avg_e : 2.0 * avg_e;
-  int sk_mt = xr_e <= 24.0 ? 1 : (xr_e <= 48.0 ? 2 : 4), sk_nt = 0, sk_d = 0;
+  // (f32 activations, whose chunks hold half the entries, measured best on
+  // the same chunk sizes: 312 us for the 256-token layer on 16-row chunks,
+  // against 340 on 32-row ones)
+  int sk_mt = avg_e <= 24.0 ? 1 : (avg_e <= 48.0 ? 2 : 4), sk_nt = 0, sk_d = 0;
   if (const char* ev = std::getenv("RLXQ_MOE_SK")) std::sscanf(ev, "%d,%d,%d", &sk_mt, &sk_nt, &sk_d);   // tuning
   if (sk_mt != 1 && sk_mt != 2 && sk_mt != 4) sk_mt = 1;
   if (sk_nt != 2 && sk_nt != 4 && sk_nt != 8) sk_nt = sk_mt == 4 ? 2 : 4;

@@ -72,12 +72,26 @@ int prep_x16(rlxq_ctx* ctx, const void* x, int x_dtype, int64_t m, int64_t k, in
 
 namespace {
 
-// Register-streamed kernel: workgroups (NT x 16 weight rows, K split,
-// 16*MT-row chunk); K splits (powers of two, whole 128-element chunks) until
-// the grid holds about two workgroups per CU (RLXQ_SKINNY_WGS scales that).
+// Bytes of one weight row per 128-element chunk (the LDS-staged kernel's
+// formats; 0 for the others).
+int64_t xl_chunk_bytes(int scheme) {
+  switch (scheme) {
+    case RLXQ_GGUF_Q4_1: return 80;
+    case RLXQ_GGUF_Q4_0: return 72;
+    case RLXQ_GGUF_Q8_0: return 136;
+    case RLXQ_GGUF_Q4_K: return 72;
+    case RLXQ_GGUF_Q5_K: return 88;
+    default: return 0;
+  }
+}
+
+// Register-streamed kernel (SC = 0), or its LDS-staged form (SC chunks a
+// step): workgroups (NT x 16 weight rows, K split, 16*MT-row chunk); K
+// splits (powers of two, whole 128-element chunks, whole steps) until the
+// grid holds about two workgroups per CU (RLXQ_SKINNY_WGS scales that).
 int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const void* w, int64_t rb, int64_t m,
                        int64_t k, int64_t n, void* y, int y_dtype, void* stream, int MT, int NT, int D,
-                       const SkinnySb& sb) {
+                       const SkinnySb& sb, int SC = 0) {
   // f32 activations: hi and lo rows (2m x16 rows), added in the epilogue
   const bool split = x_dtype == RLXQ_F32;
   const int64_t mr = split ? 2 * m : m;
@@ -92,7 +106,10 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   if (const char* e = std::getenv("RLXQ_SKINNY_WGS")) target = (int64_t)(cus * std::atof(e));
   int64_t splits = 1;
   while (tiles_n * mch * splits < target && splits * 2 * 4 <= chunks && splits < 32) splits *= 2;
-  const int64_t kslice = ((chunks + splits - 1) / splits) * 128;
+  // (LDS-staged: each split whole steps of SC chunks; the caller keeps K a
+  // whole number of steps)
+  const int64_t unit = SC > 0 ? SC : 1, steps = chunks / unit;
+  const int64_t kslice = ((steps + splits - 1) / splits) * unit * 128;
   splits = (k + kslice - 1) / kslice;
   if (tiles_n * mch * splits > 0x7fffffff) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: batched-decode grid");
   const size_t part_bytes = splits > 1 ? round256((size_t)(splits * m * n) * 4) : 0;
@@ -127,10 +144,18 @@ int skinny_xr_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, co
   a.group = sb.group;
   a.sb_bf16 = sb.sb_bf16;
   char name[64];
-  std::snprintf(name, sizeof name, "rlxq_skinnyxr_%s_mt%d_nt%d_d%d", scheme_name(scheme), MT, NT, D);
+  size_t lds = 2 * (size_t)(MT * NT * 4) * 64 * 4;   // the waves' sums
+  if (SC > 0) {
+    // four wave regions of 16 NT rows, each LROW bytes (an odd number of
+    // 16-byte units), before the sums
+    const int64_t seg = SC * xl_chunk_bytes(scheme), lrow = (seg / 16) % 2 ? seg : seg + 16;
+    lds += (size_t)(4 * 16 * NT * lrow);
+    std::snprintf(name, sizeof name, "rlxq_skinnyxl_%s_mt%d_nt%d_s%d_d%d", scheme_name(scheme), MT, NT, SC, D);
+  } else {
+    std::snprintf(name, sizeof name, "rlxq_skinnyxr_%s_mt%d_nt%d_d%d", scheme_name(scheme), MT, NT, D);
+  }
   hipFunction_t fn;
   if ((rc = get_fn(ctx, name, &fn))) return rc;
-  const size_t lds = 2 * (size_t)(MT * NT * 4) * 64 * 4;
   void* args[] = {&a};
   if ((rc = launch(ctx, fn, dim3((unsigned)(tiles_n * splits * mch)), dim3(256), lds, stream, args, name))) return rc;
   if (splits > 1) {
@@ -253,6 +278,29 @@ int skinny_dispatch(rlxq_ctx* ctx, int scheme, const void* x, int x_dtype, const
   auto run_ns = [&](int MT, int NT, int D) {
     return skinny_ns_dispatch(ctx, scheme, x, x_dtype, w, rb, m_out, k, n, y, y_dtype, stream, MT, NT, D, sb);
   };
+  // The LDS-staged kernels (Q4_1, Q4_0, Q8_0, Q4_K, Q5_K; K whole 2-chunk
+  // steps), MT 1, NT 2, 2-chunk steps, ring depth 1 (three waves per SIMD):
+  // up to 16 x16 rows, and to 32 for Q4_1, Q4_0 and Q5_K, where they
+  // measured faster than the register-streamed and N-split kernels (config-3
+  // shapes at M = 16, bf16 x: Q4_1 gate_up 28.8 -> 23.0 us, down 22.9 ->
+  // 20.2; Q4_K 36.8 -> 28.0 and 25.8 -> 21.0; Q5_K 45.0 -> 30.1 and 30.4 ->
+  // 22.6; at 64 rows most were slower).  RLXQ_SKINNY_XL="MT,NT,SC,D" picks a
+  // compiled one, "0" turns the default off, and a RLXQ_SKINNY_XR or
+  // RLXQ_SKINNY_NS choice does too.
+  {
+    const bool fmt = xl_chunk_bytes(scheme) > 0;
+    int lmt = 1, lnt = 2, lsc = 2, ld = 1;
+    bool xl = fmt && (m <= 16 || (m <= 32 && (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 ||
+                                              scheme == RLXQ_GGUF_Q5_K)));
+    if (std::getenv("RLXQ_SKINNY_XR") || std::getenv("RLXQ_SKINNY_NS")) xl = false;
+    if (const char* e = std::getenv("RLXQ_SKINNY_XL")) {
+      int a1, a2, a3, a4;
+      if (std::sscanf(e, "%d,%d,%d,%d", &a1, &a2, &a3, &a4) == 4 && fmt && a3 > 0) lmt = a1, lnt = a2, lsc = a3, ld = a4, xl = true;
+      else if (e[0] == '0') xl = false;
+    }
+    if (xl && (k / 128) % lsc == 0)
+      return skinny_xr_dispatch(ctx, scheme, x, x_dtype, w, rb, m_out, k, n, y, y_dtype, stream, lmt, lnt, ld, sb, lsc);
+  }
   // The register-streamed kernels (no LDS stage).  RLXQ_SKINNY_XR="MT,NT,D"
   // picks a compiled one (every combination for Q4_1, the defaults for the
   // other formats).

@@ -106,6 +106,9 @@ RLXQ_DEV void sk_chunk(const uint32_t (&o)[NT][sk_bdw<SCH>()], const f16x8_t (&x
   }
 }
 
+template <int MT, int NT>
+RLXQ_DEV bool sk_wave_sum(f32x4_t (&acc)[MT][NT], float* R, int wv, int lane);
+
 // ---------------------------------------------------------------------------
 // Register-streamed variant: no LDS stage and no barrier per step.
 // The four waves of a workgroup take the same NT tiles of 16 weight rows and
@@ -222,10 +225,16 @@ RLXQ_DEV bool skinny_xr_core(const uint16_t* x16, const float* ssum, int64_t Mp,
   for (int d = 0; d < D; d++)
     if (it0 + D + d < cnt) compute(ring[d]);
 
-  // (w0 + w2) + (w1 + w3)
-  constexpr int E = MT * NT * 4;
   extern __shared__ __align__(16) uint32_t sm[];
-  float* R = reinterpret_cast<float*>(sm);   // [2][E][64]
+  return sk_wave_sum<MT, NT>(acc, reinterpret_cast<float*>(sm), wv, lane);
+}
+
+// The four waves' sums added in the fixed order (w0 + w2) + (w1 + w3)
+// through R ([2][MT NT 4][64] floats of LDS); true in wave 0, whose acc then
+// holds the total.
+template <int MT, int NT>
+RLXQ_DEV bool sk_wave_sum(f32x4_t (&acc)[MT][NT], float* R, int wv, int lane) {
+  constexpr int E = MT * NT * 4;
   if (wv >= 2) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
@@ -285,6 +294,180 @@ RLXQ_DEV void skinny_xr_body(const rlxq_skinny_args& a) {
   if (!skinny_xr_core<SCH, MT, NT, D>(a.x16, a.ssum, a.Mp, m0, a.w, a.rb, a.K, kb, ke, wrow, wok, acc, a.scales,
                                       a.biases, a.group, a.sb_bf16))
     return;
+  sk_store<MT, NT>(a, acc, m0, n0, sp, g, j);
+}
+
+// ---------------------------------------------------------------------------
+// LDS-staged variant (rlxq_skinnyxl_*): the register-streamed kernel's
+// contraction, with the weights reaching the lanes another way.  A wave's
+// unit of K is a step of SC chunks (chunks SC s .. SC s + SC - 1 of its K
+// range; the four waves take steps w, w + 4, ...).  The step's weights for
+// the workgroup's 16 NT rows are one contiguous segment of SC CB bytes per
+// row (CB = bytes of a 128-element chunk of a row); the wave reads them as
+// 16-byte pieces, consecutive lanes on consecutive pieces of a row, and
+// stores them in its own LDS region (rows LROW bytes apart, an odd number of
+// 16-byte units, so the 16 rows a block read touches fall in distinct banks).
+// Lane (j, g) then takes block 4c + g of row j of each tile, chunk c of the
+// step, from there, as the register-streamed kernel takes it from memory.
+// (Reading the weights as 16 row segments of one 20- to 34-byte block per
+// lane moved 63 MB at 3.1 TB/s without any arithmetic; row-contiguous
+// 16-byte pieces of the same rows moved it at 5.1-5.5 TB/s.)
+// The region is the wave's own: its stores and its later loads are ordered
+// by the wave's in-order LDS queue, with no barrier.  The steps' loads (the
+// weight pieces, the activation fragments and the block sums) go D steps
+// ahead into a register ring.
+template <int SCH> constexpr int xl_chunk_bytes() {
+  return SCH == SCH_Q4_1 ? 80 : SCH == SCH_Q4_0 ? 72 : SCH == SCH_Q8_0 ? 136 : SCH == SCH_Q4_K ? 72
+         : SCH == SCH_Q5_K ? 88 : 0;
+}
+template <int SCH, int SC> constexpr int xl_lrow() {
+  constexpr int seg = SC * xl_chunk_bytes<SCH>();
+  return ((seg / 16) & 1) ? seg : seg + 16;
+}
+
+template <int SCH, int MT, int NT, int SC, int D>
+RLXQ_DEV bool skinny_xl_core(const uint16_t* x16, const float* ssum, int64_t Mp, int64_t m0, const uint8_t* w,
+                             int64_t rb, int64_t N, int64_t n0, int64_t kb, int64_t ke, f32x4_t (&acc)[MT][NT],
+                             uint8_t* lds) {
+  constexpr int CB = xl_chunk_bytes<SCH>(), SEG = SC * CB, PPR = SEG / 16, LROW = xl_lrow<SCH, SC>();
+  static_assert(CB > 0 && SEG % 16 == 0, "a step must be whole 16-byte pieces of each row");
+  static_assert(!(SCH == SCH_Q4_K || SCH == SCH_Q5_K) || SC % 2 == 0, "K-quant steps: whole super-blocks");
+  constexpr int R = 16 * NT, NP = R * PPR, NL = (NP + 63) / 64;
+  constexpr int BDW = sk_bdw<SCH>();
+  constexpr bool HM = sk_has_m<SCH>();
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int j = lane & 15, g = lane >> 4;
+  const int nsteps = (int)((ke - kb) / (128 * SC));   // (the host keeps K ranges whole steps)
+  const int cnt = nsteps > wv ? (nsteps - wv + 3) / 4 : 0;
+  uint8_t* reg = lds + wv * (R * LROW);
+
+  // this lane's pieces: piece p = lane + 64 u is unit p % PPR of row p / PPR
+  // (rows past N read row N - 1; their blocks are zeroed when read back)
+  // (byte offsets from the segment of row n0: the rows past N stay within
+  // the workgroup's 16 NT rows, so they fit 32 bits)
+  const uint8_t* wseg = w + n0 * rb + (kb / 128) * CB;
+  uint32_t src[NL];
+  int dst[NL];
+  bool pv[NL];
+#pragma unroll
+  for (int u = 0; u < NL; u++) {
+    const int p = lane + 64 * u;
+    pv[u] = p < NP;
+    const int pp = pv[u] ? p : NP - 1, r = pp / PPR, c = pp % PPR;
+    const int64_t rr = n0 + r < N ? r : N - 1 - n0;
+    src[u] = (uint32_t)(rr * rb + c * 16);
+    dst[u] = r * LROW + c * 16;
+  }
+  bool wok[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) wok[t] = n0 + 16 * t + j < N;
+  rlxq_gemm_args la{};   // block reads from the LDS region
+  la.w = reg;
+  la.rb = LROW;
+
+  const uint4* xrow[MT];
+  const float* srow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++) {
+    xrow[mt] = reinterpret_cast<const uint4*>(x16) + ((kb / 32) * Mp + m0 + 16 * mt + j) * 4 + g;
+    srow[mt] = HM ? ssum + ((kb / 128) * Mp + m0 + 16 * mt + j) * 4 + g : nullptr;
+  }
+  // The ring holds the weight pieces and block sums of D steps; the
+  // activation fragments (L2-resident) are loaded one chunk ahead of use.
+  struct Stage {
+    uint4 w[NL];
+    float s[SC][HM ? MT : 1];
+  };
+  auto load = [&](int it, Stage& st) {
+    const int s = wv + 4 * (it < cnt ? it : cnt - 1);
+#pragma unroll
+    for (int u = 0; u < NL; u++) st.w[u] = ld_u128(wseg + src[u] + (int64_t)s * SEG);
+    if constexpr (HM) {
+#pragma unroll
+      for (int cc = 0; cc < SC; cc++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) st.s[cc][mt] = srow[mt][((int64_t)s * SC + cc) * Mp * 4];
+    }
+  };
+  uint4 xn[MT][4];   // the next chunk's activation fragments
+  auto load_x = [&](int64_t c) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) xn[mt][i] = xrow[mt][(c * 4 + i) * Mp * 4];
+  };
+
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // step it of the wave (ring slot st); the chunk after its last is the
+  // first of step it + 1 (or its own last again, a redundant load)
+  auto compute = [&](const Stage& st, int it) {
+    const int s = wv + 4 * it;
+    const int64_t cnext = it + 1 < cnt ? (int64_t)(s + 4) * SC : (int64_t)s * SC + SC - 1;
+#pragma unroll
+    for (int u = 0; u < NL; u++)
+      if (pv[u]) *reinterpret_cast<uint4*>(reg + dst[u]) = st.w[u];
+#pragma unroll
+    for (int cc = 0; cc < SC; cc++) {
+      f16x8_t xa[MT][4];
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) xa[mt][i] = __builtin_bit_cast(f16x8_t, xn[mt][i]);
+      load_x(cc + 1 < SC ? (int64_t)s * SC + cc + 1 : cnext);
+      uint32_t o[NT][BDW];
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        RawBlk<SCH> b;
+        load_blk<SCH>(la, 16 * t + j, 4 * cc + g, wok[t], b);
+        normalise<SCH>(b, o[t]);
+      }
+      sk_chunk<SCH, MT, NT>(o, xa, HM ? st.s[cc] : nullptr, acc);
+    }
+  };
+  if (cnt > 0) {
+    Stage ring[D];
+#pragma unroll
+    for (int d = 0; d < D; d++) load(d, ring[d]);
+    load_x((int64_t)wv * SC);
+    int it0 = 0;
+    for (; it0 + 2 * D <= cnt; it0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; d++) {
+        compute(ring[d], it0 + d);
+        load(it0 + d + D, ring[d]);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      if (it0 + d < cnt) {
+        compute(ring[d], it0 + d);
+        if (it0 + d + D < cnt) load(it0 + d + D, ring[d]);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; d++)
+      if (it0 + D + d < cnt) compute(ring[d], it0 + D + d);
+  }
+  return sk_wave_sum<MT, NT>(acc, reinterpret_cast<float*>(lds + 4 * R * LROW), wv, lane);
+}
+
+template <int SCH, int MT, int NT, int SC, int D>
+RLXQ_DEV void skinny_xl_body(const rlxq_skinny_args& a) {
+  extern __shared__ __align__(16) uint8_t smx[];
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 15, g = lane >> 4;
+  const int tn = blockIdx.x % a.tiles_n;
+  const int sp = (blockIdx.x / a.tiles_n) % a.splits;
+  const int mc = blockIdx.x / (a.tiles_n * a.splits);
+  const int64_t n0 = (int64_t)tn * 16 * NT, m0 = (int64_t)mc * 16 * MT;
+  const int64_t kb = (int64_t)sp * a.kslice;
+  const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
+  f32x4_t acc[MT][NT];
+  if (!skinny_xl_core<SCH, MT, NT, SC, D>(a.x16, a.ssum, a.Mp, m0, a.w, a.rb, a.N, n0, kb, ke, acc, smx)) return;
   sk_store<MT, NT>(a, acc, m0, n0, sp, g, j);
 }
 
@@ -748,6 +931,23 @@ RLXQ_SKINNYXR_INST(q8_k, SCH_Q8_K, 2, 2, 3)
 RLXQ_SKINNYXR_INST(q8_k, SCH_Q8_K, 4, 2, 2)
 
 // N-split variants: rlxq_skinnyns_<scheme>_mt<MT>_nt<NT>_d<D>.
+// LDS-staged variants: rlxq_skinnyxl_<scheme>_mt<MT>_nt<NT>_s<SC>_d<D>.
+#define RLXQ_SKINNYXL_INST(SNAME, SCH, MT, NT, SC, D)                                                  \
+  extern "C" __global__ __launch_bounds__(256) void rlxq_skinnyxl_##SNAME##_mt##MT##_nt##NT##_s##SC##_d##D( \
+      rlxq_skinny_args a) {                                                                            \
+    rlxq::skinny_xl_body<SCH, MT, NT, SC, D>(a);                                                       \
+  }
+RLXQ_SKINNYXL_INST(q4_1, SCH_Q4_1, 1, 2, 2, 1)
+RLXQ_SKINNYXL_INST(q4_1, SCH_Q4_1, 1, 2, 1, 2)
+RLXQ_SKINNYXL_INST(q4_1, SCH_Q4_1, 1, 2, 1, 3)
+RLXQ_SKINNYXL_INST(q4_1, SCH_Q4_1, 1, 1, 2, 2)
+RLXQ_SKINNYXL_INST(q4_1, SCH_Q4_1, 1, 4, 1, 2)
+RLXQ_SKINNYXL_INST(q4_1, SCH_Q4_1, 2, 1, 2, 1)
+RLXQ_SKINNYXL_INST(q4_0, SCH_Q4_0, 1, 2, 2, 1)
+RLXQ_SKINNYXL_INST(q8_0, SCH_Q8_0, 1, 2, 2, 1)
+RLXQ_SKINNYXL_INST(q4_k, SCH_Q4_K, 1, 2, 2, 1)
+RLXQ_SKINNYXL_INST(q5_k, SCH_Q5_K, 1, 2, 2, 1)
+
 #define RLXQ_SKINNYNS_INST(SNAME, SCH, MT, NT, D)                                                      \
   extern "C" __global__ __launch_bounds__(256) void rlxq_skinnyns_##SNAME##_mt##MT##_nt##NT##_d##D(     \
       rlxq_skinny_args a) {                                                                            \

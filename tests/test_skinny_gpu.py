@@ -7,7 +7,7 @@ test_f32_activations_take_the_skinny_kernels and tests/test_f32_contract_gpu.py)
 import numpy as np
 import pytest
 
-from conftest import announce
+from conftest import announce, skinny_xl_default
 from test_gemv_gpu import TOL_BF16, TOL_F32, rel_err, run_dense
 
 pytestmark = pytest.mark.gpu
@@ -75,8 +75,8 @@ KERNEL_PREFIX = {"register": "rlxq_skinnyxr_"}
 @pytest.mark.parametrize("staging", list(STAGINGS))
 @pytest.mark.parametrize("mkn", [(5, 256, 136), (16, 4096, 512), (33, 768, 200), (64, 1024, 128)], ids=str)
 def test_skinny_q4_1_every_staging(ctx, orc, monkeypatch, staging, mkn):
-    """Q4_1 through the default choice (register-streamed up to 16 rows,
-    N-split above) and the register-streamed kernel (no LDS stage)."""
+    """Q4_1 through the default choice (LDS-staged up to 32 rows, N-split
+    above) and the register-streamed kernel."""
     for key, val in STAGINGS[staging].items():
         monkeypatch.setenv(key, val)
     m, k, n = mkn
@@ -85,7 +85,7 @@ def test_skinny_q4_1_every_staging(ctx, orc, monkeypatch, staging, mkn):
     packed = orc.synth_q4_1(rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, want = run_dense(ctx, orc, 3, x, packed, n, xdt="bf16")
-    prefix = KERNEL_PREFIX.get(staging, "rlxq_skinnyxr_" if m <= 16 else "rlxq_skinnyns_q4_1_")
+    prefix = KERNEL_PREFIX.get(staging, "rlxq_skinnyxl_q4_1_" if m <= 32 else "rlxq_skinnyns_q4_1_")
     assert ctx.last_kernel.startswith(prefix), ctx.last_kernel
     assert rel_err(got, want) <= TOL_F32
 
@@ -128,15 +128,16 @@ def test_f32_activations_take_the_skinny_kernels(ctx, orc, monkeypatch):
 
 @pytest.mark.parametrize("scheme", [1, 2])
 def test_skinny_q8_0_q4_0_register_kernel(ctx, orc, scheme):
-    """Q8_0 (34-byte blocks) and Q4_0 (18-byte blocks) through the
-    register-streamed kernel."""
+    """Q8_0 (34-byte blocks) and Q4_0 (18-byte blocks) through the default
+    kernels: LDS-staged at few rows, register-streamed above."""
     for (m, k, n) in [(6, 256, 40), (16, 2048, 300), (40, 640, 96), (64, 4096, 130)]:
         announce(f"skinny scheme={scheme} {(m, k, n)}")
         rng = np.random.default_rng(scheme * 100 + m + k)
         packed = orc.synth(scheme, rng, n, k)
         x = rng.standard_normal((m, k)).astype(np.float32)
         got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt="bf16")
-        assert ctx.last_kernel.startswith("rlxq_skinnyxr_"), ctx.last_kernel
+        kind = "xl" if skinny_xl_default(scheme, m, k) else "xr"
+        assert ctx.last_kernel.startswith(f"rlxq_skinny{kind}_"), ctx.last_kernel
         assert rel_err(got, want) <= TOL_F32, (m, k, n)
 
 
@@ -181,7 +182,8 @@ def test_skinny_q4_k_default(ctx, orc, mkn):
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[0] *= 300.0
     got, want = run_dense(ctx, orc, 7, x, packed, n, xdt="bf16")
-    prefix = "rlxq_skinnyxr_q4_k_" if m <= 16 else "rlxq_skinnyns_q4_k_"
+    prefix = ("rlxq_skinnyxl_q4_k_" if skinny_xl_default(7, m, k) else "rlxq_skinnyxr_q4_k_") if m <= 16 \
+        else "rlxq_skinnyns_q4_k_"
     assert ctx.last_kernel.startswith(prefix), ctx.last_kernel
     assert rel_err(got, want) <= TOL_F32
     got, want = run_dense(ctx, orc, 7, x, packed, n, xdt="bf16", ydt="bf16")
@@ -205,8 +207,8 @@ def test_skinny_q4_k_every_variant(ctx, orc, monkeypatch, cfg):
 
 
 def test_skinny_q4_k_activation_range_and_no_staged_kernel(ctx, orc, monkeypatch):
-    """Rows far outside the f16 range; RLXQ_SKINNY_XR=0 (the LDS-staged
-    kernels, which Q4_K lacks) keeps Q4_K on the register-streamed kernel."""
+    """Rows far outside the f16 range; RLXQ_SKINNY_XR=0 (no configuration)
+    keeps Q4_K on the register-streamed kernel's default tiling."""
     monkeypatch.setenv("RLXQ_SKINNY_XR", "0")
     m, k, n = 8, 512, 96
     rng = np.random.default_rng(27)

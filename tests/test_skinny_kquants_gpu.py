@@ -16,7 +16,7 @@ it by orders of magnitude."""
 import numpy as np
 import pytest
 
-from conftest import announce
+from conftest import announce, skinny_xl_default
 from test_gemv_gpu import TOL_BF16, rel_err, run_dense
 
 pytestmark = pytest.mark.gpu
@@ -56,7 +56,8 @@ def test_skinny_kquant_default(ctx, orc, name, mkn, xdt):
     announce(f"skinny {name} default {mkn} x={xdt}")
     packed, x = _case(orc, scheme, m, k, n, m * 7 + k + n + scheme)
     got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt=xdt)
-    assert ctx.last_kernel.startswith(f"rlxq_skinnyxr_{name}_"), ctx.last_kernel
+    kind = "xl" if skinny_xl_default(scheme, m, k, xdt) else "xr"
+    assert ctx.last_kernel.startswith(f"rlxq_skinny{kind}_{name}_"), ctx.last_kernel
     assert rel_err(got, want) <= TOL_EXACT, (name, mkn, xdt)
 
 
@@ -84,7 +85,8 @@ def test_skinny_kquant_split_k_bf16_out_and_activation_range(ctx, orc, name):
     announce(f"skinny {name} split-K / bf16 out / range")
     packed, x = _case(orc, scheme, m, k, n, 11 + scheme, x_row0=1.0)
     got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt="bf16", ydt="bf16")
-    assert ctx.last_kernel.startswith(f"rlxq_skinnyxr_{name}_"), ctx.last_kernel
+    kind = "xl" if skinny_xl_default(scheme, m, k) else "xr"
+    assert ctx.last_kernel.startswith(f"rlxq_skinny{kind}_{name}_"), ctx.last_kernel
     assert rel_err(got, want) <= TOL_BF16
     x = x * np.logspace(-30, 30, m, dtype=np.float64)[:, None].astype(np.float32)
     got, want = run_dense(ctx, orc, scheme, x, packed, n, xdt="f32")
@@ -100,5 +102,6 @@ def test_kquants_take_the_skinny_kernels_by_default(ctx, orc, monkeypatch):
         for m, xdt in ((5, "f32"), (63, "bf16")):
             packed, x = _case(orc, scheme, m, 1024, 96, m + scheme)
             got, want = run_dense(ctx, orc, scheme, x, packed, 96, xdt=xdt)
-            assert ctx.last_kernel.startswith(f"rlxq_skinnyxr_{name}_"), (name, m, ctx.last_kernel)
+            kind = "xl" if skinny_xl_default(scheme, m, 1024, xdt) else "xr"
+            assert ctx.last_kernel.startswith(f"rlxq_skinny{kind}_{name}_"), (name, m, ctx.last_kernel)
             assert rel_err(got, want) <= TOL_EXACT
