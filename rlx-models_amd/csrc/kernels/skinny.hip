@@ -460,9 +460,16 @@ RLXQ_DEV void skinny_xl_body(const rlxq_skinny_args& a) {
   extern __shared__ __align__(16) uint8_t smx[];
   const int lane = threadIdx.x & 63;
   const int j = lane & 15, g = lane >> 4;
-  const int tn = blockIdx.x % a.tiles_n;
-  const int sp = (blockIdx.x / a.tiles_n) % a.splits;
-  const int mc = blockIdx.x / (a.tiles_n * a.splits);
+  // Workgroup order: the dispatcher deals workgroups round-robin over the
+  // eight XCDs, so b, b + 8, b + 16, ... share an XCD and its L2.  With a
+  // grid of whole eights, consecutive workgroups of one XCD take the row
+  // chunks of one (tile, split): the weight segments the first reads from
+  // HBM the others find in that L2.  (A permutation of the grid; any order
+  // computes the same sums.)
+  const int G = (int)gridDim.x, mch = G / (a.tiles_n * a.splits);
+  const int L = G % 8 == 0 ? (int)(blockIdx.x % 8) * (G / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+  const int mc = L % mch, rest = L / mch;
+  const int tn = rest % a.tiles_n, sp = rest / a.tiles_n;
   const int64_t n0 = (int64_t)tn * 16 * NT, m0 = (int64_t)mc * 16 * MT;
   const int64_t kb = (int64_t)sp * a.kslice;
   const int64_t ke = kb + a.kslice < a.K ? kb + a.kslice : a.K;
