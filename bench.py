@@ -22,7 +22,10 @@ Extra keys of the same JSON line:
                   at M=4096, and the W8A8 variant (per-row int8 activations
                   computed on the fly x per-channel int8 weights)
   batched_decode  config 3: Q4_1 and Q8_0 (and every other format), M in
-                  {1, 4, 16, 64}, bf16 x; and Q4_1 with F32 x and y at 16, 64
+                  {1, 4, 16, 64}, bf16 x; Q4_1 with F32 x and y at 16, 64;
+                  and load_pattern_probe, the gate_up weight bytes read with
+                  no arithmetic row-contiguously and with the register-
+                  streamed kernel's lane pattern
   moe             config 5: routed-expert grouped GEMV, 16 tokens, top-8 of 128
   moe_q4_k        the same with Q4_K expert banks (a Q4_K_M MoE checkpoint)
   moe_prefill     the config-5 layer at 256 tokens (grouped MFMA kernels)
@@ -541,6 +544,23 @@ def batched_section(ctx, gen, sptr, stream, only=None) -> dict:
                                                "us_eager": t["us_eager"], "us_graph": t["us_graph"]}
             del ws
             torch.cuda.empty_cache()
+    # the weight stream's floor for the gate_up shape's bytes under two lane
+    # patterns, no arithmetic: row-contiguous 16-byte loads (rlxq_peak_probe
+    # READ) and the register-streamed kernel's one 20-byte block per lane,
+    # 16 rows x 80 bytes per wave instruction (TILE20)
+    if not only or "q4_1" in only:
+        b = 24576 * 2560
+        bufs = [torch.zeros(b // 4, device="cuda") for _ in range(_copies(b))]
+        sink = torch.empty(1 << 16, dtype=torch.int32, device="cuda")
+        pat = {"bytes": b, "shape": "Q4_1 gate_up 4096->24576, weights rotated past the MALL"}
+        for kind, key in ((rlxq.PROBE_READ, "row_contiguous"), (rlxq.PROBE_TILE20, "tile20")):
+            def launch(i, sp, kind=kind):
+                ctx.peak_probe(kind, b, buf=bufs[i % len(bufs)], sink=sink, stream=sp)
+            us = _gpu_us(ctx, launch, 4 * len(bufs), stream)["us"]
+            pat[key] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
+        res["load_pattern_probe"] = pat
+        del bufs
+        torch.cuda.empty_cache()
     # the reference operator's own operand types (F32 x in, F32 y out) on the
     # same kernels (x as hi + lo f16 rows), Q4_1
     if not only or "q4_1" in only:

@@ -246,11 +246,18 @@ int rlxq_moe_grouped(rlxq_ctx* ctx, int scheme, int mode, const void* x,
  *   kind RLXQ_PROBE_READ4 (2): the same bytes with the grid sized to them,
  *     four independent 16-byte loads per thread (work <= 1 GiB): the
  *     load-only floor of a small weight stream.
+ *   kind RLXQ_PROBE_TILE20 (3): `buf` [work bytes, a multiple of 81920,
+ *     at most 65536 x 81920]
+ *     as rows of 2560 bytes (4096 Q4_1 codes) read with the register-
+ *     streamed batched-decode kernel's lane pattern and no arithmetic: per
+ *     wave instruction 16 rows x 80 bytes, one 20-byte block per lane;
+ *     *count = work.
  * sink: device memory of at least max(8 x CUs, 65536) x 4 bytes, written only
  * to keep the work live.  Time the call with events on `stream`. */
 #define RLXQ_PROBE_MFMA 0
 #define RLXQ_PROBE_READ 1
 #define RLXQ_PROBE_READ4 2
+#define RLXQ_PROBE_TILE20 3
 int rlxq_peak_probe(rlxq_ctx* ctx, int kind, const void* buf, int64_t work, void* sink, int64_t* count,
                     void* stream);
 

@@ -672,6 +672,15 @@ int rlxq_peak_probe(rlxq_ctx* ctx, int kind, const void* buf, int64_t work, void
     *count = work;
     return launch(ctx, fn, dim3((unsigned)((n16 + 1023) / 1024)), dim3(256), 0, stream, args, "rlxq_probe_read4");
   }
+  if (kind == RLXQ_PROBE_TILE20) {
+    if (!buf) return fail(ctx, RLXQ_E_NULL, "peak_probe: buf must be non-null");
+    if (work % 81920 || !aligned(buf, 16)) return fail(ctx, RLXQ_E_ALIGN, "peak_probe: buf 16-byte aligned, 80 KiB multiple");
+    if (work / 81920 > 65536) return fail(ctx, RLXQ_E_SHAPE, "peak_probe: TILE20 reads at most 65536 x 80 KiB");
+    if ((rc = get_fn(ctx, "rlxq_probe_tile20", &fn))) return rc;
+    void* args[] = {(void*)&buf, &sink};
+    *count = work;
+    return launch(ctx, fn, dim3((unsigned)(work / 81920)), dim3(256), 0, stream, args, "rlxq_probe_tile20");
+  }
   return fail(ctx, RLXQ_E_SHAPE, "peak_probe: unknown kind");
 }
 

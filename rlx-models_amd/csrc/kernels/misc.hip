@@ -500,6 +500,49 @@ extern "C" __global__ __launch_bounds__(256) void rlxq_probe_read4(const uint4* 
   }
 }
 
+// The register-streamed batched-decode kernel's weight reads with no
+// arithmetic: rows of 2560 bytes (4096 Q4_1 codes, 128 blocks of 20 bytes);
+// workgroup b takes rows 32 b .. 32 b + 31 as two 16-row tiles, wave w the
+// 80-byte chunks w, w + 4, ... of them, and lane (j, g) block 4 c + g of
+// row j of each tile as one dword and one 16-byte load, four chunks in
+// flight: 16 rows x 80 bytes per wave instruction.
+extern "C" __global__ __launch_bounds__(256) void rlxq_probe_tile20(const uint8_t* __restrict__ w,
+                                                                    uint32_t* __restrict__ sink) {
+  constexpr int RB = 2560, CH = 8, D = 4;   // CH chunks per wave (32 per row)
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, j = lane & 15, g = lane >> 4;
+  const uint8_t* base = w + (int64_t)blockIdx.x * 32 * RB;
+  uint32_t h[D][2];
+  uint4 q[D][2];
+  auto load = [&](int it, int d) {
+    const int c = wv + 4 * it;
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const uint8_t* p = base + (16 * t + j) * RB + (4 * c + g) * 20;
+      h[d][t] = ld_u32(p);
+      q[d][t] = ld_u128(p + 4);
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < D; d++) load(d, d);
+  uint32_t acc = 0;
+#pragma unroll
+  for (int it0 = 0; it0 < CH; it0 += D)
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+#pragma unroll
+      for (int t = 0; t < 2; t++) acc ^= h[d][t] ^ q[d][t].x ^ q[d][t].y ^ q[d][t].z ^ q[d][t].w;
+      if (it0 + d + D < CH) load(it0 + d + D, d);
+    }
+  __shared__ uint32_t red[256];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+    for (int k = 0; k < 256; k++) t ^= red[k];
+    sink[blockIdx.x] = t;
+  }
+}
+
 extern "C" __global__ __launch_bounds__(256) void rlxq_probe_read(const uint4* __restrict__ src, int64_t n16,
                                                                   uint32_t* __restrict__ sink) {
   uint32_t acc = 0;

@@ -20,7 +20,7 @@ GGUF_Q5_K, GGUF_Q3_K, GGUF_Q2_K, GGUF_Q8_K = 10, 11, 12, 13
 F32, BF16, U8 = 0, 1, 2
 MOE_EXPAND, MOE_COMBINE, MOE_EXPAND_SWIGLU = 0, 1, 2
 OK = 0
-PROBE_MFMA, PROBE_READ, PROBE_READ4 = 0, 1, 2
+PROBE_MFMA, PROBE_READ, PROBE_READ4, PROBE_TILE20 = 0, 1, 2, 3
 E_NULL, E_SHAPE, E_SCHEME, E_ALIGN, E_DTYPE, E_HIP, E_NOMEM, E_INDEX, E_NOKERNEL, E_DEVICE = range(-1, -11, -1)
 E_IO, E_FORMAT, E_NOTFOUND, E_TAKEN, E_SCRATCH = range(-11, -16, -1)
 NOALLOC_SCRATCH_BYTES = 64 << 20   # RLXQ_NOALLOC_SCRATCH_BYTES
@@ -376,7 +376,8 @@ class Context:
 
     def peak_probe(self, kind: int, work: int, *, buf=None, sink, stream=None) -> int:
         """rlxq_peak_probe: launches the probe on `stream`, returns the flops
-        (PROBE_MFMA) or bytes (PROBE_READ, PROBE_READ4) it issues."""
+        (PROBE_MFMA) or bytes (PROBE_READ, PROBE_READ4, PROBE_TILE20) it
+        issues."""
         cnt = C.c_int64(0)
         rc = lib().rlxq_peak_probe(self.h, kind, _ptr(buf), work, _ptr(sink), C.byref(cnt), _stream(stream))
         self._check(rc, "peak_probe")

@@ -27,6 +27,24 @@ def test_read_probes_read_every_byte_once(ctx, kind, nbytes):
     assert got == want
 
 
+@pytest.mark.parametrize("nbytes", [81920, 62914560])
+def test_tile20_probe_reads_every_block_once(ctx, nbytes):
+    """The batched-decode lane-pattern probe (rows of 2560 bytes, one 20-byte
+    block per lane): every dword of every block read exactly once."""
+    import torch
+    import rlxq
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(nbytes + 1)
+    buf = torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), device="cuda", dtype=torch.int32, generator=g)
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    assert ctx.peak_probe(rlxq.PROBE_TILE20, nbytes, buf=buf, sink=sink) == nbytes
+    torch.cuda.synchronize()
+    got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32))
+    want = np.bitwise_xor.reduce(buf.cpu().numpy().view(np.uint32))
+    assert got == want
+
+
 def test_probe_counts_and_refusals(ctx):
     import torch
     import rlxq
@@ -44,6 +62,12 @@ def test_probe_counts_and_refusals(ctx):
         assert e.value.status == rlxq.E_NULL
     with pytest.raises(rlxq.RlxqError) as e:
         ctx.peak_probe(rlxq.PROBE_READ4, (1 << 30) + 4096, buf=buf, sink=sink)
+    assert e.value.status == rlxq.E_SHAPE
+    with pytest.raises(rlxq.RlxqError) as e:
+        ctx.peak_probe(rlxq.PROBE_TILE20, 81920 + 4096, buf=buf, sink=sink)
+    assert e.value.status == rlxq.E_ALIGN
+    with pytest.raises(rlxq.RlxqError) as e:
+        ctx.peak_probe(rlxq.PROBE_TILE20, 65537 * 81920, buf=buf, sink=sink)
     assert e.value.status == rlxq.E_SHAPE
     with pytest.raises(rlxq.RlxqError) as e:
         ctx.peak_probe(7, 4096, buf=buf, sink=sink)
