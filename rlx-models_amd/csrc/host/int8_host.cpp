@@ -36,9 +36,10 @@ const W8a8Cfg kW8a8[] = {
 // Tiling choice; RLXQ_W8A8_CFG=<name> selects one (tuning sweeps and the
 // per-variant parity test).
 // Default: 256 x 256 tiles (8 waves) once they cover the CUs, else 128 x 128;
-// the 256 x 256 tiles take 128-byte K steps from K = 8192 (Qwen3-8B down at
-// M=4096: 244 us against 254 with 64-byte steps; gate_up, K = 4096, the
-// same either way; the two-stage variants of both measured 5-30% slower).
+// the 256 x 256 tiles take 128-byte K steps where K allows (Qwen3-8B at
+// M=4096 after 20 ms of sustained launches: gate_up 451 us against 485 with
+// 64-byte steps, down 227.5 against 232; the two-stage variants of both
+// measured 5-30% slower).
 const W8a8Cfg* pick_w8a8(int64_t m, int64_t n, int64_t k, int cus) {
   if (const char* e = std::getenv("RLXQ_W8A8_CFG")) {
     for (const auto& c : kW8a8)
@@ -47,7 +48,7 @@ const W8a8Cfg* pick_w8a8(int64_t m, int64_t n, int64_t k, int cus) {
   }
   const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256);
   if (t256 < (cus > 0 ? cus : 256)) return &kW8a8[0];
-  return k >= 8192 && k % 128 == 0 ? &kW8a8[6] : &kW8a8[4];
+  return k % 128 == 0 ? &kW8a8[6] : &kW8a8[4];
 }
 
 }  // namespace
