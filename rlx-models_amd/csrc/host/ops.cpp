@@ -382,14 +382,17 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // RLXQ_GEMV_XR="NU,D,W[,XS]" picks the variant (XS=1: through LDS), "0"
   // turns the path off (tuning).
   const bool q4k = scheme == RLXQ_GGUF_Q4_K;
+  // (Q5_K: 64-weight units as Q4_K's, with the qh bytes beside the codes)
+  const bool q5k = scheme == RLXQ_GGUF_Q5_K, u64 = q4k || q5k;
   const bool xr_scheme = scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_MLX_AFFINE4 ||
-                         scheme == RLXQ_MLX_MXFP4 || q4k;
+                         scheme == RLXQ_MLX_MXFP4 || u64;
   const int64_t nchunk64 = (units + 63) / 64;
-  const int64_t xr_max = scheme == RLXQ_GGUF_Q4_0 ? 4 : (q4k ? 3 : 6);
+  const int64_t xr_max = scheme == RLXQ_GGUF_Q4_0 ? 4 : (u64 ? 3 : 6);
   // two chunks (K = 4096 for the one-block units): 4-wave workgroups with one
   // row in flight per wave measured 0.2-0.3 us faster on the small shapes
-  const bool two = nchunk64 == 2 && !q4k;
-  int xr_nu = (int)(nchunk64 == 5 ? 6 : nchunk64), xr_d = (two || nchunk64 > (q4k ? 2 : 3)) ? 1 : 2,
+  const bool two = nchunk64 == 2 && !u64;
+  // (Q5_K's 21-dword units: a one-deep ring from two chunks up)
+  int xr_nu = (int)(nchunk64 == 5 ? 6 : nchunk64), xr_d = (two || nchunk64 > (q5k ? 1 : (u64 ? 2 : 3))) ? 1 : 2,
       xr_w = two ? 4 : 8;
   bool use_xr = m == 1 && xbf && xr_scheme && nchunk64 <= xr_max && n < (int64_t(1) << 31);
   int xr_lds = 1;   // 1: the activations pass through LDS once per workgroup

@@ -255,7 +255,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   constexpr int BYTES = Unit<SCH>::BYTES;
   constexpr bool MLX = SCH == SCH_MLX4;
   constexpr bool MX = SCH == SCH_MXFP4;
-  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || MLX);
+  constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SCH == SCH_Q5_K || MLX);
   static_assert(!Unit<SCH>::BIT8, "register activations serve 4-bit codes");
 
   const int K = a.K;
@@ -323,7 +323,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     constexpr int NT = 64 * WAVES;
     constexpr int XH = (2 * 64 * NU * KS * BLOCKS + NT - 1) / NT;   // half-blocks per thread and row
     constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;
-    constexpr bool LINEAR = MLX || MX || SCH == SCH_Q4_K;   // half h = elements 16h..16h+15
+    constexpr bool LINEAR = MLX || MX || SCH == SCH_Q4_K || SCH == SCH_Q5_K;   // half h = elements 16h..16h+15
     uint4 xa[MT][XH], xc[MT][XH];
     if constexpr (F32X) {
       // the half-block's 16 f32 elements, split after the first weight
@@ -398,7 +398,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
             P[4 * t + 1] = R[1];
             P[4 * t + 2] = R[2];
             P[4 * t + 3] = R[3];
-          } else if constexpr (SCH == SCH_Q4_K) {
+          } else if constexpr (SCH == SCH_Q4_K || SCH == SCH_Q5_K) {
             const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7: pairs (4j+e, 4j+e+2)
             P[4 * t + 0] = perm_b32(R[1], R[0], LO);
             P[4 * t + 1] = perm_b32(R[1], R[0], HI);
@@ -674,8 +674,16 @@ RLXQ_GEMVXR_WIDE(mlx4, SCH_MLX4)
   RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U2_D2_W8, SCH_Q4_K, 2, 2, 8)          \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U2_D1_W8, SCH_Q4_K, 2, 1, 8)          \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_q4_k_U3_D1_W8, SCH_Q4_K, 3, 1, 8)
+// Q5_K (64-weight units of 21 dwords: the head, the qh bytes and the
+// group's qs bytes; Q4_K's pair order): up to three units per lane
+#define RLXQ_GEMVXS_Q5K                                                     \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_q5_k_U1_D2_W8, SCH_Q5_K, 1, 2, 8)          \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_q5_k_U1_D1_W8, SCH_Q5_K, 1, 1, 8)          \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_q5_k_U2_D1_W8, SCH_Q5_K, 2, 1, 8)          \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_q5_k_U3_D1_W8, SCH_Q5_K, 3, 1, 8)
 #if RLXQ_PART_IS(0)
 RLXQ_GEMVXS_Q4K
+RLXQ_GEMVXS_Q5K
 #endif
 // several activation rows (M = 2..4): rlxq_gemvxs_<scheme>_U<NU>_D<D>_W<W>_M<MT>,
 // NU * MT <= 8 units of activations per lane

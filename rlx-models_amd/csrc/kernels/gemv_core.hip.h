@@ -798,7 +798,7 @@ RLXQ_DEV void pairs_from_raw(const uint32_t* R, uint32_t* X) {
   constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;  // low / high halves of (R[a], R[b])
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    if constexpr (SCH == SCH_Q4_K) {
+    if constexpr (SCH == SCH_Q4_K || SCH == SCH_Q5_K) {
       // t = 2j + e holds (4j+e, 4j+e+2): R[2j] and R[2j+1], j = 2i, 2i+1
       X[4 * i + 0] = perm_b32(R[4 * i + 1], R[4 * i], LO);
       X[4 * i + 1] = perm_b32(R[4 * i + 1], R[4 * i], HI);

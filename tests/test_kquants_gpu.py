@@ -60,7 +60,31 @@ def test_kquant_gemv(ctx, orc, name, kn, xdt):
     packed = orc.synth(scheme, rng, n, k)
     x = rng.standard_normal((1, k)).astype(np.float32)
     got, want = _run(ctx, orc, scheme, x, packed, n, xdt=xdt)
-    assert ctx.last_kernel.startswith(f"rlxq_gemv_{name}_"), ctx.last_kernel
+    # (Q5_K with bf16 activations and K up to three 64-unit chunks: the
+    # register kernel)
+    xr = name == "q5_k" and xdt == "bf16" and k // 64 <= 192
+    assert ctx.last_kernel.startswith(f"rlxq_gemvxs_{name}_" if xr else f"rlxq_gemv_{name}_"), ctx.last_kernel
+    assert rel_err(got, want) <= TOL
+
+
+@pytest.mark.parametrize("cfg", ["1,2,8", "1,1,8", "2,1,8", "3,1,8"])
+@pytest.mark.parametrize("kn", [(256, 17), (4096, 1031), (8192, 300), (12288, 520)], ids=str)
+def test_q5_k_register_gemv_every_variant(ctx, orc, monkeypatch, cfg, kn):
+    """Every compiled Q5_K register GEMV (activations of NU 64-weight unit
+    chunks held in registers, the 32 qh bytes and the group's qs bytes in a
+    21-dword unit), K a whole number of units or not of chunks."""
+    k, n = kn
+    nu = int(cfg.split(",")[0])
+    if (k // 64 + 63) // 64 > nu:
+        pytest.skip("K needs more unit chunks than the variant holds")
+    monkeypatch.setenv("RLXQ_GEMV_XR", cfg + ",1")
+    announce(f"q5_k register gemv {cfg} {kn}")
+    rng = np.random.default_rng(k * 3 + n)
+    packed = orc.synth(10, rng, n, k)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    x[0, :7] *= 300.0
+    got, want = _run(ctx, orc, 10, x, packed, n, xdt="bf16")
+    assert ctx.last_kernel == "rlxq_gemvxs_q5_k_U{}_D{}_W{}".format(*cfg.split(",")), ctx.last_kernel
     assert rel_err(got, want) <= TOL
 
 
@@ -95,6 +119,7 @@ VARIANTS = {
 def test_kquant_every_record_variant(ctx, orc, monkeypatch, name, cfg):
     scheme = SCHEMES[name]
     monkeypatch.setenv("RLXQ_GEMV_CFG", cfg)
+    monkeypatch.setenv("RLXQ_GEMV_XR", "0")   # (Q5_K's bf16 rows: not the register kernel)
     k, n = 2816, 300          # 11 super-blocks: Q3_K rows alternate 2- and 4-byte alignment
     announce(f"{name} variant {cfg}")
     rng = np.random.default_rng(11 + scheme)
