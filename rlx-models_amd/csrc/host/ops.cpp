@@ -384,16 +384,23 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   const bool q4k = scheme == RLXQ_GGUF_Q4_K;
   // (Q5_K: 64-weight units as Q4_K's, with the qh bytes beside the codes)
   const bool q5k = scheme == RLXQ_GGUF_Q5_K, u64 = q4k || q5k;
+  // (Q2_K, Q3_K: a scale per 16 weights, two chains per block; their records
+  // carry the first half's activation sum as well)
+  const bool khalf = scheme == RLXQ_GGUF_Q2_K || scheme == RLXQ_GGUF_Q3_K;
   const bool xr_scheme = scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_MLX_AFFINE4 ||
-                         scheme == RLXQ_MLX_MXFP4 || u64;
+                         scheme == RLXQ_MLX_MXFP4 || u64 || khalf;
   const int64_t nchunk64 = (units + 63) / 64;
-  const int64_t xr_max = scheme == RLXQ_GGUF_Q4_0 ? 4 : (u64 ? 3 : 6);
+  const int64_t xr_max = scheme == RLXQ_GGUF_Q4_0 || scheme == RLXQ_GGUF_Q2_K ? 4
+                         : (u64 || scheme == RLXQ_GGUF_Q3_K ? 3 : 6);
   // two chunks (K = 4096 for the one-block units): 4-wave workgroups with one
   // row in flight per wave measured 0.2-0.3 us faster on the small shapes
   const bool two = nchunk64 == 2 && !u64;
   // (Q5_K's 21-dword units: a one-deep ring from two chunks up)
   int xr_nu = (int)(nchunk64 == 5 ? 6 : nchunk64), xr_d = (two || nchunk64 > (q5k ? 1 : (u64 ? 2 : 3))) ? 1 : 2,
       xr_w = two ? 4 : 8;
+  // (gate_up 4096 -> 24576: Q2_K 14.5 us one-deep, 16.0 two-deep, 16.8 on
+  // the LDS-record kernel; Q3_K 25.9, 24.5, 26.8)
+  if (khalf) xr_d = (nchunk64 <= 1 || (scheme == RLXQ_GGUF_Q3_K && nchunk64 == 2)) ? 2 : 1, xr_w = 8;
   bool use_xr = m == 1 && xbf && xr_scheme && nchunk64 <= xr_max && n < (int64_t(1) << 31);
   int xr_lds = 1;   // 1: the activations pass through LDS once per workgroup
   // The K-split register kernels (KS waves per weight row, their row sums
@@ -483,7 +490,8 @@ int gemv_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     std::snprintf(name, sizeof name, "rlxq_gemvx%s_%s_U%d_D%d_W%d", xr_lds ? "s" : "r", scheme_name(scheme), xr_nu,
                   xr_d, xr_w);
     if ((rc = get_fn(ctx, name, &fn))) return rc;
-    const size_t lds = xr_lds ? (size_t)(k / 32) * 68 : 0;   // pair records + block sums
+    // pair records + block sums (+ the first halves' sums)
+    const size_t lds = xr_lds ? (size_t)(k / 32) * (khalf ? 72 : 68) : 0;
     const int per_cu = blocks_per_cu(ctx, name, fn, 64 * xr_w, lds);
     const int64_t wgs_needed = (n + xr_w - 1) / xr_w;
     int64_t gx = (int64_t)ctx->cu_count * per_cu;

@@ -256,6 +256,12 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   constexpr bool MLX = SCH == SCH_MLX4;
   constexpr bool MX = SCH == SCH_MXFP4;
   constexpr bool HAS_MIN = (SCH == SCH_Q4_1 || SCH == SCH_Q4_K || SCH == SCH_Q5_K || MLX);
+  // Q2_K / Q3_K: a scale (Q2_K: and a min) per 16 weights, two dot chains
+  // per block on the halves' activation sums (the records carry the first
+  // half's sum after the block sums)
+  constexpr bool HALF = half_scales<SCH>();
+  static_assert(!HALF || (XLDS && MT == 1 && !F32X && KS == 1), "per-16 scales: one bf16 row through LDS");
+  constexpr int XREC = HALF ? 18 : 17;   // LDS dwords per block: 16 pairs, the sum[, the first half's sum]
   static_assert(!Unit<SCH>::BIT8, "register activations serve 4-bit codes");
 
   const int K = a.K;
@@ -317,13 +323,14 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   // MT activation rows (M <= MT; rows past M read row 0 and are not stored)
   uint32_t X[MT][NU][BLOCKS][16];
   float S[MT][NU][BLOCKS];
+  float SL[MT][NU][BLOCKS];   // (HALF: the first half's sums)
   Buf ring[D];
   if constexpr (XLDS) {
     extern __shared__ __align__(16) uint32_t xlds[];
     constexpr int NT = 64 * WAVES;
     constexpr int XH = (2 * 64 * NU * KS * BLOCKS + NT - 1) / NT;   // half-blocks per thread and row
     constexpr uint32_t LO = 0x05040100u, HI = 0x07060302u;
-    constexpr bool LINEAR = MLX || MX || SCH == SCH_Q4_K || SCH == SCH_Q5_K;   // half h = elements 16h..16h+15
+    constexpr bool LINEAR = MLX || MX || SCH == SCH_Q4_K || SCH == SCH_Q5_K || HALF;   // half h = elements 16h..16h+15
     uint4 xa[MT][XH], xc[MT][XH];
     if constexpr (F32X) {
       // the half-block's 16 f32 elements, split after the first weight
@@ -382,7 +389,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     }
 #pragma unroll
     for (int m = 0; m < MT; m++) {
-      uint32_t* xs = xlds + (size_t)m * bpr * 17;
+      uint32_t* xs = xlds + (size_t)m * bpr * XREC;
       float* xsum = reinterpret_cast<float*>(xs + bpr * 16);
 #pragma unroll
       for (int i = 0; i < XH; i++) {
@@ -398,7 +405,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
             P[4 * t + 1] = R[1];
             P[4 * t + 2] = R[2];
             P[4 * t + 3] = R[3];
-          } else if constexpr (SCH == SCH_Q4_K || SCH == SCH_Q5_K) {
+          } else if constexpr (SCH == SCH_Q4_K || SCH == SCH_Q5_K || HALF) {
             const uint32_t* R = t == 0 ? A : C;   // elements 16h + 8t .. +7: pairs (4j+e, 4j+e+2)
             P[4 * t + 0] = perm_b32(R[1], R[0], LO);
             P[4 * t + 1] = perm_b32(R[1], R[0], HI);
@@ -428,13 +435,14 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
           dst[0] = make_uint4(P[0], P[1], P[2], P[3]);
           dst[1] = make_uint4(P[4], P[5], P[6], P[7]);
           if (h == 0) xsum[b] = sh + so;
+          if (HALF && h == 0) xsum[bpr + b] = sh;   // (half 0: elements 0..15)
         }
       }
     }
     __syncthreads();
 #pragma unroll
     for (int m = 0; m < MT; m++) {
-      const uint32_t* xs = xlds + (size_t)m * bpr * 17;
+      const uint32_t* xs = xlds + (size_t)m * bpr * XREC;
       const float* xsum = reinterpret_cast<const float*>(xs + bpr * 16);
 #pragma unroll
       for (int c = 0; c < NU; c++)
@@ -449,6 +457,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
             X[m][c][bl][4 * q + 2] = v.z; X[m][c][bl][4 * q + 3] = v.w;
           }
           S[m][c][bl] = xsum[blk];
+          if constexpr (HALF) SL[m][c][bl] = xsum[bpr + blk];
         }
     }
   } else {
@@ -496,7 +505,7 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
   int64_t cmax = 0;
   if constexpr (KS > 1) {
     extern __shared__ __align__(16) uint32_t xlds[];
-    kpart = reinterpret_cast<float*>(xlds + (size_t)MT * bpr * 17);
+    kpart = reinterpret_cast<float*>(xlds + (size_t)MT * bpr * XREC);
     cmax = (N32 + G - 1) / G;
   }
   auto store = [&](int64_t off, float v) {
@@ -519,6 +528,26 @@ RLXQ_DEV void gemv_xr_body(const rlxq_gemv_args& a) {
     for (int c = 0; c < NU; c++)
 #pragma unroll
       for (int bl = 0; bl < BLOCKS; bl++) {
+        if constexpr (HALF) {
+          // two 16-weight halves (planes 0..7: elements 0..15), each chain
+          // from -bias times its half's activation sum, its own scale (and
+          // Q2_K's min times that sum)
+          float d0, d1, m0, m1;
+          block_scales_half<SCH>(bf.dw[c], d0, d1, m0, m1);
+          if (!uok[c]) d0 = d1 = m0 = m1 = 0.f;
+          uint32_t pw[16];
+          block_pairs<SCH>(bf.dw[c], bl, pw, kc);
+          const float sl = SL[0][c][bl], sh = S[0][c][bl] - sl;
+          float lo = -chain_bias<SCH>() * sl, hi = -chain_bias<SCH>() * sh;
+#pragma unroll
+          for (int t = 0; t < 8; t++) {
+            lo = dot2_bf16(pw[t], X[0][c][bl][t], lo);
+            hi = dot2_bf16(pw[8 + t], X[0][c][bl][8 + t], hi);
+          }
+          acc[0] = fmaf(d0, lo, fmaf(d1, hi, acc[0]));
+          if constexpr (SCH == SCH_Q2_K) acc[0] = fmaf(m0, sl, fmaf(m1, sh, acc[0]));
+          continue;
+        }
         float d, mn;
         if constexpr (MLX) {
           d = sb_decode(bf.sm[c][bl], a.sb_bf16 != 0);
@@ -681,9 +710,19 @@ RLXQ_GEMVXR_WIDE(mlx4, SCH_MLX4)
   RLXQ_GEMVXS_INST(rlxq_gemvxs_q5_k_U1_D1_W8, SCH_Q5_K, 1, 1, 8)          \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_q5_k_U2_D1_W8, SCH_Q5_K, 2, 1, 8)          \
   RLXQ_GEMVXS_INST(rlxq_gemvxs_q5_k_U3_D1_W8, SCH_Q5_K, 3, 1, 8)
+// Q2_K (11-dword units) and Q3_K (22): one 32-weight block per unit, K up to
+// four (Q2_K) or three (Q3_K) unit chunks
+#define RLXQ_GEMVXS_KHALF(SNAME, SCH)                                       \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U1_D2_W8, SCH, 1, 2, 8)          \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U2_D1_W8, SCH, 2, 1, 8)          \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U2_D2_W8, SCH, 2, 2, 8)          \
+  RLXQ_GEMVXS_INST(rlxq_gemvxs_##SNAME##_U3_D1_W8, SCH, 3, 1, 8)
 #if RLXQ_PART_IS(0)
 RLXQ_GEMVXS_Q4K
 RLXQ_GEMVXS_Q5K
+RLXQ_GEMVXS_KHALF(q2_k, SCH_Q2_K)
+RLXQ_GEMVXS_KHALF(q3_k, SCH_Q3_K)
+RLXQ_GEMVXS_INST(rlxq_gemvxs_q2_k_U4_D1_W8, SCH_Q2_K, 4, 1, 8)
 #endif
 // several activation rows (M = 2..4): rlxq_gemvxs_<scheme>_U<NU>_D<D>_W<W>_M<MT>,
 // NU * MT <= 8 units of activations per lane

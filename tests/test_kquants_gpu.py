@@ -60,31 +60,40 @@ def test_kquant_gemv(ctx, orc, name, kn, xdt):
     packed = orc.synth(scheme, rng, n, k)
     x = rng.standard_normal((1, k)).astype(np.float32)
     got, want = _run(ctx, orc, scheme, x, packed, n, xdt=xdt)
-    # (Q5_K with bf16 activations and K up to three 64-unit chunks: the
-    # register kernel)
-    xr = name == "q5_k" and xdt == "bf16" and k // 64 <= 192
+    # (bf16 activations and K up to the register kernel's unit chunks: Q5_K
+    # three of 64-weight units, Q2_K four and Q3_K three of 32-weight units)
+    xr = xdt == "bf16" and k // XR_UNIT[name] <= 64 * XR_CHUNKS.get(name, 0)
     assert ctx.last_kernel.startswith(f"rlxq_gemvxs_{name}_" if xr else f"rlxq_gemv_{name}_"), ctx.last_kernel
     assert rel_err(got, want) <= TOL
 
 
-@pytest.mark.parametrize("cfg", ["1,2,8", "1,1,8", "2,1,8", "3,1,8"])
-@pytest.mark.parametrize("kn", [(256, 17), (4096, 1031), (8192, 300), (12288, 520)], ids=str)
-def test_q5_k_register_gemv_every_variant(ctx, orc, monkeypatch, cfg, kn):
-    """Every compiled Q5_K register GEMV (activations of NU 64-weight unit
-    chunks held in registers, the 32 qh bytes and the group's qs bytes in a
-    21-dword unit), K a whole number of units or not of chunks."""
+XR_UNIT = {"q5_k": 64, "q3_k": 32, "q2_k": 32, "q8_k": 32}
+XR_CHUNKS = {"q5_k": 3, "q3_k": 3, "q2_k": 4}
+XR_VARIANTS = [("q5_k", c) for c in ("1,2,8", "1,1,8", "2,1,8", "3,1,8")] + \
+              [(nm, c) for nm in ("q2_k", "q3_k") for c in ("1,2,8", "2,1,8", "2,2,8", "3,1,8")] + [("q2_k", "4,1,8")]
+
+
+@pytest.mark.parametrize("name,cfg", XR_VARIANTS, ids=str)
+@pytest.mark.parametrize("kn", [(256, 17), (4096, 1031), (6144, 300), (8192, 520)], ids=str)
+def test_kquant_register_gemv_every_variant(ctx, orc, monkeypatch, name, cfg, kn):
+    """Every compiled register GEMV of Q5_K (64-weight units: the 32 qh
+    bytes and the group's qs bytes in 21 dwords), Q2_K and Q3_K (32-weight
+    units with a scale, Q2_K also a min, per 16 weights: two dot chains per
+    block on the halves' activation sums): activations of NU unit chunks in
+    registers; K a whole number of units or not of chunks."""
+    scheme = SCHEMES[name]
     k, n = kn
     nu = int(cfg.split(",")[0])
-    if (k // 64 + 63) // 64 > nu:
+    if (k // XR_UNIT[name] + 63) // 64 > nu:
         pytest.skip("K needs more unit chunks than the variant holds")
     monkeypatch.setenv("RLXQ_GEMV_XR", cfg + ",1")
-    announce(f"q5_k register gemv {cfg} {kn}")
-    rng = np.random.default_rng(k * 3 + n)
-    packed = orc.synth(10, rng, n, k)
+    announce(f"{name} register gemv {cfg} {kn}")
+    rng = np.random.default_rng(k * 3 + n + scheme)
+    packed = orc.synth(scheme, rng, n, k)
     x = rng.standard_normal((1, k)).astype(np.float32)
     x[0, :7] *= 300.0
-    got, want = _run(ctx, orc, 10, x, packed, n, xdt="bf16")
-    assert ctx.last_kernel == "rlxq_gemvxs_q5_k_U{}_D{}_W{}".format(*cfg.split(",")), ctx.last_kernel
+    got, want = _run(ctx, orc, scheme, x, packed, n, xdt="bf16")
+    assert ctx.last_kernel == f"rlxq_gemvxs_{name}_U{{}}_D{{}}_W{{}}".format(*cfg.split(",")), ctx.last_kernel
     assert rel_err(got, want) <= TOL
 
 
