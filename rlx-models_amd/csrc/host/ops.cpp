@@ -175,9 +175,9 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // Q6_K with its LDS stores after the step's MFMAs, which measured 15%
   // faster for it and slower for the others).  When the tiles do not cover the CUs, K is split so that they do
   // (at most 8 slices of at least 8 K steps) and the slices' f32 partial sums
-  // are added in slice order.  RLXQ_GEMM_TILE=128|256|256w8|256w8l|256w8p2|...x
-  // forces a tiling (the 128 x 128 one never splits); RLXQ_GEMM_SPLITS=<n>
-  // forces the slice count.
+  // are added in slice order.  RLXQ_GEMM_TILE=128|256|256w8|256w8l|256w8p2|...x|
+  // 256n128|256n128w8 forces a tiling (the 128 x 128 one never splits);
+  // RLXQ_GEMM_SPLITS=<n> forces the slice count.
   const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
   int tile = 256;
   const bool one_stage = scheme == RLXQ_GGUF_Q6_K || scheme == RLXQ_GGUF_Q3_K;
@@ -185,7 +185,7 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   const char* te = std::getenv("RLXQ_GEMM_TILE");
   if (te) {
     tile = std::atoi(te) == 128 ? 128 : 256;
-    var = tile == 128 ? "" : (std::strncmp(te, "256w8", 5) == 0 ? te + 3 : "");
+    var = tile == 128 ? "" : ((std::strncmp(te, "256w8", 5) == 0 || std::strncmp(te, "256n128", 7) == 0) ? te + 3 : "");
   }
   // f32 output or f32 activations: the exact variant (bf16 weights, or f16
   // weights rounded once, do not keep 1e-3 on structured data).  Its
@@ -203,8 +203,8 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
             // (Q4_1 and Q8_K: one stage for bf16 activations, two for f32)
             (!split && (scheme == RLXQ_GGUF_Q4_1 || scheme == RLXQ_GGUF_Q8_K))) ? "w8x" : "w8p2x";
   if (split && !vs.empty() && vs.back() == 'x') vs += 's';
-  const bool w8 = tile == 256 && !vs.empty() && vs[0] == 'w';
   const bool exact = vs.find('x') != std::string::npos;
+  bool n128 = tile == 256 && vs.compare(0, 4, "n128") == 0;   // 256 x 128 tiles
   if (exact && !has_exact_gemm(scheme))
     return fail(ctx, RLXQ_E_SCHEME, "dequant_matmul: MXFP4 has no exact f16 GEMM variant");
   if (split && !(exact && vs.back() == 's'))
@@ -213,13 +213,31 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
   // the exact variant's tiles cover 128 output columns (hi and lo weight
   // rows), and with f32 activations 128 output rows
   const int64_t mr = split ? (m + 31) / 32 * 64 : m;
-  const int64_t tn_cols = exact ? tile / 2 : tile;
-  const int64_t tiles_m = (mr + tile - 1) / tile, tiles_n = (n + tn_cols - 1) / tn_cols;
-  if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
-  const int64_t tiles = tiles_m * tiles_n, ksteps = k / 64;
+  const int64_t tiles_m = (mr + tile - 1) / tile, ksteps = k / 64;
+  if (tiles_m * ((n + 63) / 64) > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "dequant_matmul: too many GEMM tiles");
+  auto auto_splits = [&](int64_t t) {
+    int64_t s = 1;
+    while (t * s * 2 <= cus && s < 8 && ksteps / (s * 2) >= 8) s *= 2;
+    return s;
+  };
+  // bf16 variant: 256 x 128 tiles (8 waves) where the 256 x 256 tiles would
+  // split K (half the slices and partial sums; 12288->4096 at M=512 76 -> 67
+  // us, 4096->4096 at M=512 / 2048 43 -> 33 / 88 -> 75) or leave a partly
+  // filled last round of workgroups that the narrower tiles fill (4096->24576
+  // at M=1024: 384 vs 768 tiles on 256 CUs, 235 -> 221 us)
+  if (!te && tile == 256 && !exact) {
+    const int64_t t256 = tiles_m * ((n + 255) / 256), t128 = tiles_m * ((n + 127) / 128);
+    if (auto_splits(t256) > 1 || 2 * ((t256 + cus - 1) / cus) > (t128 + cus - 1) / cus) {
+      n128 = true;
+      vs = "n128w8";
+    }
+  }
+  const bool w8 = tile == 256 && vs.find("w8") != std::string::npos;
+  const int64_t tn_cols = exact ? tile / 2 : (n128 ? 128 : tile);
+  const int64_t tiles_n = (n + tn_cols - 1) / tn_cols, tiles = tiles_m * tiles_n;
   int64_t splits = 1;
   if (tile == 256) {
-    while (tiles * splits * 2 <= cus && splits < 8 && ksteps / (splits * 2) >= 8) splits *= 2;
+    splits = auto_splits(tiles);
     if (const char* e = std::getenv("RLXQ_GEMM_SPLITS")) splits = std::max<int64_t>(1, std::min<int64_t>(std::atoi(e), ksteps));
   }
   const int64_t kslice = ((ksteps + splits - 1) / splits) * 64;
@@ -272,7 +290,7 @@ int gemm_dispatch(rlxq_ctx* ctx, int scheme, int group, const void* x, int x_dty
     const size_t lds = 2 * (128 + 128) * 72 * sizeof(uint16_t);
     return launch(ctx, fn, dim3((unsigned)tiles), dim3(256), lds, stream, args, name);
   }
-  const size_t lds = 2 * (256 + 256) * 72 * sizeof(uint16_t);
+  const size_t lds = 2 * (256 + (n128 ? 128 : 256)) * 72 * sizeof(uint16_t);
   const int64_t grid = 8 * ((tiles + 7) / 8) * splits;
   if ((rc = launch(ctx, fn, dim3((unsigned)grid), dim3(w8 ? 512 : 256), lds, stream, args, name))) return rc;
   if (splits > 1) {

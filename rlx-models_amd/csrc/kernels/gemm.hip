@@ -159,19 +159,28 @@ RLXQ_DEV void gemm_body(const rlxq_gemm_args& a) {
 // sin / cos parity inputs at K = 1792) already reaches 1.4e-3.  MLX, Q8_K and
 // Q2_K weights are held times 2^8 (sk_wscale; undone through the activation
 // row factors) so that small scales stay normal f16.
-template <int SCH, int WGM, int WGN, int PF, bool F16, bool LATE = false, bool EXACT = false, bool SPLITX = false>
+// BNT = 128 (bf16 variant only): 256 x 128 tiles, twice the tiles of a
+// shape, so half the K slices where the tiles do not cover the CUs (half the
+// split-K partial sums written and added).
+template <int SCH, int WGM, int WGN, int PF, bool F16, bool LATE = false, bool EXACT = false, bool SPLITX = false,
+          int BNT = 256>
 RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
   static_assert(EXACT == F16, "f16 MFMA runs the exact variant on the prepared f16 activations");
   static_assert(!SPLITX || EXACT, "hi / lo activation rows on the exact variant");
-  constexpr int BM = 256, BN = 256;
+  static_assert(BNT == 256 || (BNT == 128 && !EXACT), "256 x 128 tiles on the bf16 variant");
+  constexpr int BM = 256, BN = BNT;
   constexpr int NREAL = EXACT ? BN / 2 : BN;   // output columns per tile
   constexpr float WSCALE = sk_wscale<SCH>();
   constexpr int NT = 64 * WGM * WGN;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int AP = 2048 / NT;   // 16-byte activation chunks per thread per step
-  constexpr int BPT = 512 / NT;   // weight blocks per thread per step
-  static_assert(AP % 2 == 0 && BPT >= 1, "threads");
+  // weight blocks per step: 2 BN; per thread BPT, or one in the first 2 BN
+  // threads when there are more threads than blocks (whole waves)
+  constexpr int WB = 2 * BN;
+  constexpr bool WALL = WB >= NT;
+  constexpr int BPT = WALL ? WB / NT : 1;
+  static_assert(AP % 2 == 0 && BPT >= 1 && WB % 64 == 0, "threads");
   extern __shared__ uint16_t smem[];
   uint16_t* As = smem;                // [2][BM][GLD]
   uint16_t* Bs = smem + 2 * BM * GLD;  // [2][BN][GLD]
@@ -200,11 +209,13 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
     const int c = tid + NT * i, r = c >> 3;
     arow[i] = (m0 + r < a.M ? m0 + r : a.M - 1) * a.K + (c & 7) * 8;
   }
-  // weight tile: 256 rows x 2 blocks; thread -> row n0 + (tid & 255), blocks
-  // (tid >> 8) + q * (NT / 256)
+  // weight tile: BN rows x 2 blocks; thread -> row n0 + tid % BN, blocks
+  // tid / BN + q * (NT / BN)
   // (EXACT: B row brl holds half (brl >> 5) & 1 of real column
   // n0 + 32 (brl >> 6) + brl % 32)
-  const int brl = tid & 255;
+  const int brl = tid & (BN - 1);
+  const bool wthread = WALL || tid < WB;
+  auto wblk = [&](int q) { return tid / BN + q * (NT / BN); };
   const int64_t bcol = n0 + (EXACT ? ((brl >> 6) << 5) + (brl & 31) : brl);
   const int64_t brow = bcol < a.N ? bcol : a.N - 1;
 
@@ -221,8 +232,10 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
     kt += kt0;
 #pragma unroll
     for (int i = 0; i < AP; i++) P.a[i] = *reinterpret_cast<const u32x4_t*>(xg + arow[i] + (int64_t)kt * GBK);
+    if (wthread) {
 #pragma unroll
-    for (int q = 0; q < BPT; q++) load_blk<SCH>(a, brow, 2 * (int64_t)kt + (tid >> 8) + q, true, P.b[q]);
+      for (int q = 0; q < BPT; q++) load_blk<SCH>(a, brow, 2 * (int64_t)kt + wblk(q), true, P.b[q]);
+    }
   };
   auto store_a = [&](const Stage& P, int buf, int half) {
 #pragma unroll
@@ -232,7 +245,8 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
     }
   };
   auto store_b = [&](const Stage& P, int buf, int q) {
-    uint16_t* dst = Bs + (buf * BN + brl) * GLD + ((tid >> 8) + q) * 32;
+    if (!wthread) return;
+    uint16_t* dst = Bs + (buf * BN + brl) * GLD + wblk(q) * 32;
     if constexpr (EXACT) {
       // The two threads of a real column (B rows brl and brl ^ 32, the same
       // raw block) split the block's K range: thread half h converts
@@ -254,7 +268,7 @@ RLXQ_DEV void gemm256_body(const rlxq_gemm_args& a) {
         hi[i] = h0 | (h1 << 16);
         lo[i] = f32_to_f16_bits(a0 - f16_bits_to_f32(h0)) | (f32_to_f16_bits(a1 - f16_bits_to_f32(h1)) << 16);
       }
-      const int kof = ((tid >> 8) + q) * 32 + 16 * h;
+      const int kof = wblk(q) * 32 + 16 * h;
       uint16_t* dh = Bs + (buf * BN + (brl & ~32)) * GLD + kof;
       uint16_t* dl = Bs + (buf * BN + (brl | 32)) * GLD + kof;
       *reinterpret_cast<uint4*>(dh) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
@@ -482,6 +496,16 @@ RLXQ_GEMM_INST(rlxq_gemm_q2_k_t128, SCH_Q2_K)
   extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256w8l(rlxq_gemm_args a) { \
     rlxq::gemm256_body<SCH, 2, 4, 1, false, true>(a);                                              \
   }
+// 256 x 128 tiles (bf16 variant): rlxq_gemm_<scheme>_t256n128 (4 waves, 2 x 2,
+// 128 x 64 each) and ..._t256n128w8 (8 waves, 4 x 2, 64 x 64 each; the first
+// four convert the weight blocks)
+#define RLXQ_GEMM256N_INST(SNAME, SCH, PF, LATE)                                              \
+  extern "C" __global__ __launch_bounds__(256, 1) void rlxq_gemm_##SNAME##_t256n128(rlxq_gemm_args a) { \
+    rlxq::gemm256_body<SCH, 2, 2, PF, false, LATE, false, false, 128>(a);                          \
+  }                                                                                                \
+  extern "C" __global__ __launch_bounds__(512, 1) void rlxq_gemm_##SNAME##_t256n128w8(rlxq_gemm_args a) { \
+    rlxq::gemm256_body<SCH, 4, 2, PF, false, LATE, false, false, 128>(a);                          \
+  }
 // Exact f32-output variant (EXACT above): rlxq_gemm_<scheme>_t256w8[p2|l]x,
 // f16 MFMA on the prepared activations (natural order), f16 hi + lo weights
 // and rlxq_gemm_<scheme>_t256w8[p2|l]xs for f32 activations (hi / lo rows)
@@ -508,6 +532,18 @@ RLXQ_GEMM256_INST(mxfp4, SCH_MXFP4)
 RLXQ_GEMM256_INST(q5_k, SCH_Q5_K)
 RLXQ_GEMM256_INST(q3_k, SCH_Q3_K)
 RLXQ_GEMM256_INST(q2_k, SCH_Q2_K)
+RLXQ_GEMM256N_INST(q4_1, SCH_Q4_1, 2, false)
+RLXQ_GEMM256N_INST(q4_0, SCH_Q4_0, 2, false)
+RLXQ_GEMM256N_INST(q8_0, SCH_Q8_0, 2, false)
+RLXQ_GEMM256N_INST(mlx4, SCH_MLX4, 2, false)
+RLXQ_GEMM256N_INST(mlx8, SCH_MLX8, 2, false)
+RLXQ_GEMM256N_INST(q4_k, SCH_Q4_K, 2, false)
+RLXQ_GEMM256N_INST(q6_k, SCH_Q6_K, 1, true)
+RLXQ_GEMM256N_INST(q8_k, SCH_Q8_K, 2, false)
+RLXQ_GEMM256N_INST(mxfp4, SCH_MXFP4, 2, false)
+RLXQ_GEMM256N_INST(q5_k, SCH_Q5_K, 2, false)
+RLXQ_GEMM256N_INST(q3_k, SCH_Q3_K, 1, false)
+RLXQ_GEMM256N_INST(q2_k, SCH_Q2_K, 2, false)
 // (Q4_1 and Q8_K: the all-real-tiles variant for bf16 activations keeps one
 // register stage; with two it spilled)
 RLXQ_GEMM256XN_INST(q4_1, SCH_Q4_1, 1, , false)

@@ -115,7 +115,8 @@ def test_gemm_forced_for_small_m_and_f32_output(ctx, orc, monkeypatch):
 
 @pytest.mark.parametrize("scheme", [1, 2, 3, 4, 5])
 def test_every_gemm_tiling(ctx, orc, scheme, monkeypatch):
-    """Every tiling (128 x 128; 256 x 256 with 4 or 8 waves) on a ragged shape, every scheme:
+    """Every tiling (128 x 128; 256 x 256 with 4 or 8 waves; 256 x 128 with 4
+    or 8 waves) on a ragged shape, every scheme:
     each within the prefill bar, and the two agree to ~1e-6 (f32 output; both
     accumulate K in the same order)."""
     import torch
@@ -139,14 +140,14 @@ def test_every_gemm_tiling(ctx, orc, scheme, monkeypatch):
         wd = orc.dequantize(scheme, packed, k).astype(np.float64)
     outs = {}
     monkeypatch.setenv("RLXQ_PREFILL", "gemm")
-    for tile in ("128", "256", "256w8", "256w8l", "256w8p2"):
+    for tile in ("128", "256", "256w8", "256w8l", "256w8p2", "256n128", "256n128w8"):
         monkeypatch.setenv("RLXQ_GEMM_TILE", tile)
         announce(f"gemm tiling t{tile} scheme={scheme} m={m} k={k} n={n}")
         got, xv = run_gemm(ctx, orc, scheme, x, packed, n, ydt="f32", **kw)
         assert ctx.last_kernel.endswith(f"_t{tile}")
         assert rel_err(got, xv.astype(np.float64) @ wd.T) <= TOL_PREFILL
         outs[tile] = got
-    for t in ("256", "256w8", "256w8l", "256w8p2"):
+    for t in ("256", "256w8", "256w8l", "256w8p2", "256n128", "256n128w8"):
         assert np.allclose(outs["128"], outs[t], rtol=1e-6, atol=1e-6 * np.abs(outs["128"]).max())
 
 
@@ -187,7 +188,8 @@ def test_gemm_exact_shared_conversion(ctx, orc, monkeypatch, scheme, mkn):
 
 
 @pytest.mark.parametrize("scheme", [1, 2, 3, 4])
-@pytest.mark.parametrize("tile_ydt", [("256w8p2", "bf16"), ("256w8", "f32"), ("256w8p2x", "f32"), ("256w8x", "f32")],
+@pytest.mark.parametrize("tile_ydt", [("256w8p2", "bf16"), ("256w8", "f32"), ("256w8p2x", "f32"), ("256w8x", "f32"),
+                                      ("256n128", "bf16"), ("256n128w8", "f32")],
                          ids=lambda t: f"{t[0]}-{t[1]}")
 @pytest.mark.parametrize("splits", [2, 3, 8])
 def test_gemm_split_k(ctx, orc, monkeypatch, scheme, tile_ydt, splits):

@@ -73,7 +73,7 @@ def test_every_tiling_agrees(ctx, orc, monkeypatch, scheme):
     x = rng.standard_normal((m, k)).astype(np.float32)
     monkeypatch.setenv("RLXQ_PREFILL", "gemm")
     outs = {}
-    for tile in ("128", "256", "256w8", "256w8l", "256w8p2"):
+    for tile in ("128", "256", "256w8", "256w8l", "256w8p2", "256n128", "256n128w8"):
         if tile == "256w8p2" and scheme in (Q6_K, Q3_K):
             continue   # (its two register stages do not fit these raw blocks)
         monkeypatch.setenv("RLXQ_GEMM_TILE", tile)
@@ -111,7 +111,8 @@ def test_f32_output_prefill_route(ctx, orc, scheme):
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, xv = _run(ctx, scheme, x, packed, kw, n, "f32")
     if scheme == MXFP4:
-        assert ctx.last_kernel == "rlxq_gemm_mxfp4_t256w8p2", ctx.last_kernel
+        # (the bf16 GEMM; 256 x 128 tiles where 256 x 256 ones would split K)
+        assert ctx.last_kernel in ("rlxq_gemm_mxfp4_t256w8p2", "rlxq_gemm_mxfp4_t256n128w8"), ctx.last_kernel
     else:
         assert ctx.last_kernel.startswith(f"rlxq_gemm_{NAMES[scheme]}_t256w8") and ctx.last_kernel.endswith("x"), \
             ctx.last_kernel
