@@ -232,6 +232,41 @@ def test_gemm_split_k(ctx, orc, monkeypatch, scheme, tile_ydt, splits):
         assert rel_err(outs[splits], outs[1]) <= 1e-5
 
 
+@pytest.mark.parametrize("case", ["f32_x", "n_odd", "bf16_x_f32_y"])
+@pytest.mark.parametrize("splits", [2, 3])
+def test_gemm_split_k_reduction_layouts(ctx, orc, monkeypatch, case, splits):
+    """The split-K partial sums of each layout: F32 activations on the exact
+    variant (hi / lo x16 rows, m_out output rows), an N that is no multiple
+    of 4 (one output per reduction thread), bf16 x with f32 y (the exact
+    variant's 128 output columns), all with row and column tails: within the
+    bar against the oracle and within 1e-5 of the unsplit kernel."""
+    import torch
+
+    m, k, n = 300, 64 * 13, 301 if case == "n_odd" else 392
+    rng = np.random.default_rng(5 * splits + len(case))
+    packed = orc.synth_q4_1(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    wd = orc.dequantize(3, packed, k).astype(np.float64)
+    monkeypatch.setenv("RLXQ_PREFILL", "gemm")
+    outs = {}
+    for sp in (1, splits):
+        monkeypatch.setenv("RLXQ_GEMM_SPLITS", str(sp))
+        announce(f"gemm split-k reduction {case} splits={sp}")
+        if case == "f32_x":
+            xt = _t(x)
+            y = ctx.dequant_matmul(xt, _t(packed), 3, n, y_dtype=torch.float32)
+            assert ctx.last_kernel.endswith("xs"), ctx.last_kernel
+        else:
+            xt = _t(x).to(torch.bfloat16)
+            y = ctx.dequant_matmul(xt, _t(packed), 3, n, y_dtype=torch.float32)
+        torch.cuda.synchronize()
+        got = y.float().cpu().numpy()
+        want = xt.float().cpu().numpy().astype(np.float64) @ wd.T
+        assert rel_err(got, want) <= (1e-3 if case != "n_odd" or ctx.last_kernel.endswith("x") else TOL_PREFILL)
+        outs[sp] = got
+    assert rel_err(outs[splits], outs[1]) <= 1e-5
+
+
 @pytest.mark.parametrize("mkn", [(512, 12288, 4096), (2048, 12288, 4096), (256, 4096, 24576)], ids=str)
 def test_gemm_default_split_on_small_grids(ctx, orc, mkn):
     """Prefill shapes whose 256 x 256 tiles do not cover the CUs: the
