@@ -23,14 +23,16 @@ size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 struct W8a8Cfg {
   const char* name;  // kernel name suffix
   int BM, BN, BK, WGM, WGN;
+  bool kf;           // K must be a multiple of BK (no zeroing along K)
 };
 
 // Compiled W8A8 tilings (kernel rlxq_w8a8_<name>).
 const W8a8Cfg kW8a8[] = {
-    {"m128n128k64w22", 128, 128, 64, 2, 2},  {"m128n128k128w22", 128, 128, 128, 2, 2},
-    {"m256n128k64w22", 256, 128, 64, 2, 2},  {"m128n256k64w22", 128, 256, 64, 2, 2},
-    {"m256n256k64w24", 256, 256, 64, 2, 4},  {"m128n128k128w22_p2", 128, 128, 128, 2, 2},
-    {"m256n256k128w24", 256, 256, 128, 2, 4},
+    {"m128n128k64w22", 128, 128, 64, 2, 2, false},   {"m128n128k128w22", 128, 128, 128, 2, 2, false},
+    {"m256n128k64w22", 256, 128, 64, 2, 2, false},   {"m128n256k64w22", 128, 256, 64, 2, 2, false},
+    {"m256n256k64w24", 256, 256, 64, 2, 4, false},   {"m128n128k128w22_p2", 128, 128, 128, 2, 2, false},
+    {"m256n256k128w24", 256, 256, 128, 2, 4, false}, {"m256n256k64w24_kf", 256, 256, 64, 2, 4, true},
+    {"m256n256k128w24_kf", 256, 256, 128, 2, 4, true},
 };
 
 // Tiling choice; RLXQ_W8A8_CFG=<name> selects one (tuning sweeps and the
@@ -48,7 +50,8 @@ const W8a8Cfg* pick_w8a8(int64_t m, int64_t n, int64_t k, int cus) {
   }
   const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256);
   if (t256 < (cus > 0 ? cus : 256)) return &kW8a8[0];
-  return k % 128 == 0 ? &kW8a8[6] : &kW8a8[4];
+  // (the _kf forms where K is a whole number of steps)
+  return k % 128 == 0 ? &kW8a8[8] : (k % 64 == 0 ? &kW8a8[7] : &kW8a8[4]);
 }
 
 }  // namespace
@@ -180,6 +183,7 @@ int rlxq_w8a8_gemm(rlxq_ctx* ctx, const void* x, int x_dtype, const int8_t* wq, 
 
   const W8a8Cfg* c = pick_w8a8(m, n, k, ctx->cu_count);
   if (!c) return fail(ctx, RLXQ_E_NOKERNEL, "w8a8_gemm: RLXQ_W8A8_CFG names no compiled tiling");
+  if (c->kf && k % c->BK) return fail(ctx, RLXQ_E_SHAPE, "w8a8_gemm: this tiling needs K to be a multiple of its K step");
   const int64_t tiles_m = (m + c->BM - 1) / c->BM, tiles_n = (n + c->BN - 1) / c->BN;
   if (tiles_m * tiles_n > 0x7ffffff0) return fail(ctx, RLXQ_E_SHAPE, "w8a8_gemm: too many tiles");
 

@@ -77,7 +77,10 @@ RLXQ_DEV void w8a8_epilogue(const rlxq_w8a8_args& a, const i32x16_t (&acc)[TM][T
 // of BK bytes; each wave computes a (BM/WGM) x (BN/WGN) sub-tile from 32x32
 // MFMA tiles.  Global loads of step k+1 are in flight during the MFMAs of step
 // k; LDS tiles are double-buffered with one barrier per step.
-template <int BM, int BN, int BK, int WGM, int WGN, int GM, int PF>
+// KF: K is a whole number of BK steps, so every load is in range along K and
+// none is zeroed; rows past M and columns past N read the clamped row or
+// column and only feed outputs that are not stored.
+template <int BM, int BN, int BK, int WGM, int WGN, int GM, int PF, bool KF = false>
 RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
   constexpr int NT = WGM * WGN * 64;
   constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -136,14 +139,22 @@ RLXQ_DEV void w8a8_body(const rlxq_w8a8_args& a) {
 #pragma unroll
     for (int i = 0; i < AP; i++) {
       const int64_t k = k0 + akof[i];
-      const uint4 v = *reinterpret_cast<const uint4*>(abase[i] + (k < a.K ? k : a.K - 16));
-      P.a[i] = (amok[i] && k < a.K) ? v : make_uint4(0u, 0u, 0u, 0u);
+      if constexpr (KF) {
+        P.a[i] = *reinterpret_cast<const uint4*>(abase[i] + k);
+      } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(abase[i] + (k < a.K ? k : a.K - 16));
+        P.a[i] = (amok[i] && k < a.K) ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
     }
 #pragma unroll
     for (int i = 0; i < BP; i++) {
       const int64_t k = k0 + bkr[i];
-      const uint4 v = *reinterpret_cast<const uint4*>(bbase[i] + (k < a.K ? k : a.K - 1) * a.N);
-      P.b[i] = (bnok[i] && k < a.K) ? v : make_uint4(0u, 0u, 0u, 0u);
+      if constexpr (KF) {
+        P.b[i] = *reinterpret_cast<const uint4*>(bbase[i] + k * a.N);
+      } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(bbase[i] + (k < a.K ? k : a.K - 1) * a.N);
+        P.b[i] = (bnok[i] && k < a.K) ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
     }
   };
   auto store_a = [&](const Stage& P, int buf) {
@@ -526,6 +537,14 @@ RLXQ_W8A8_INST(128, 256, 64, 2, 2)
 RLXQ_W8A8_INST(256, 256, 64, 2, 4)
 RLXQ_W8A8_INST_P2(128, 128, 128, 2, 2)
 RLXQ_W8A8_INST(256, 256, 128, 2, 4)
+// K a whole number of steps: ..._kf (no zeroing selects in the loads)
+#define RLXQ_W8A8_INST_KF(BM, BN, BK, WGM, WGN)                                                     \
+  extern "C" __global__ __launch_bounds__(WGM * WGN * 64) void rlxq_w8a8_m##BM##n##BN##k##BK##w##WGM##WGN##_kf( \
+      rlxq_w8a8_args a) {                                                                          \
+    rlxq::w8a8_body<BM, BN, BK, WGM, WGN, 8, 1, true>(a);                                          \
+  }
+RLXQ_W8A8_INST_KF(256, 256, 64, 2, 4)
+RLXQ_W8A8_INST_KF(256, 256, 128, 2, 4)
 
 #define RLXQ_I8B_INST(MT, XN, XBF)                                                        \
   extern "C" __global__ __launch_bounds__(256) void rlxq_i8b_##XN##_mt##MT(rlxq_i8b_args a) { \

@@ -120,17 +120,34 @@ def test_w8a8_bf16_output_bit_exact(ctx, orc, rng):
 
 
 W8A8_CFGS = ["m128n128k64w22", "m128n128k128w22", "m256n128k64w22", "m128n256k64w22", "m256n256k64w24",
-             "m128n128k128w22_p2", "m256n256k128w24"]
+             "m128n128k128w22_p2", "m256n256k128w24", "m256n256k64w24_kf", "m256n256k128w24_kf"]
 
 
 @pytest.mark.parametrize("cfg", W8A8_CFGS)
 def test_every_w8a8_tiling(ctx, orc, rng, cfg, monkeypatch):
-    """Every compiled tiling, on a ragged shape (M, N, K not multiples of the tile)."""
+    """Every compiled tiling, on a ragged shape (M, N, K not multiples of the
+    tile; the _kf tilings, which need K to be a multiple of their K step, on
+    K = 640 or 768 with M and N ragged)."""
     monkeypatch.setenv("RLXQ_W8A8_CFG", cfg)
-    announce(f"w8a8 tiling {cfg} m=333 k=592 n=400")
-    got, want = _w8a8_case(ctx, orc, rng, 333, 592, 400)
+    k = (768 if "k128" in cfg else 640) if cfg.endswith("_kf") else 592
+    announce(f"w8a8 tiling {cfg} m=333 k={k} n=400")
+    got, want = _w8a8_case(ctx, orc, rng, 333, k, 400)
     assert ctx.last_kernel == f"rlxq_w8a8_{cfg}"
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_w8a8_whole_step_tiling_refuses_other_k(ctx, monkeypatch):
+    """A _kf tiling forced on a K that is not a multiple of its K step is
+    refused before any launch."""
+    import torch
+    import rlxq
+
+    monkeypatch.setenv("RLXQ_W8A8_CFG", "m256n256k128w24_kf")
+    x = torch.zeros((4, 576), device="cuda")
+    wq = torch.zeros((576, 32), dtype=torch.int8, device="cuda")
+    with pytest.raises(rlxq.RlxqError) as e:
+        ctx.w8a8_gemm(x, wq, torch.ones((32,), device="cuda"), 32)
+    assert e.value.status == rlxq.E_SHAPE
 
 
 @pytest.mark.parametrize("k,n", [(4096, 24576), (12288, 4096)], ids=lambda s: str(s))
