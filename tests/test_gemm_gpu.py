@@ -270,17 +270,50 @@ def test_gemm_split_k_reduction_layouts(ctx, orc, monkeypatch, case, splits):
 @pytest.mark.parametrize("mkn", [(512, 12288, 4096), (2048, 12288, 4096), (256, 4096, 24576)], ids=str)
 def test_gemm_default_split_on_small_grids(ctx, orc, mkn):
     """Prefill shapes whose 256 x 256 tiles do not cover the CUs: the
-    dispatcher splits K by itself; the output stays within the bar."""
+    dispatcher takes the 256 x 128 tiles and splits K by itself where those
+    do not cover them either; the output stays within the bar."""
     m, k, n = mkn
     announce(f"gemm default split {mkn}")
     rng = np.random.default_rng(m + n)
     packed = orc.synth_q4_1(rng, n, k)
     x = rng.standard_normal((m, k)).astype(np.float32)
     got, xv = run_gemm(ctx, orc, 3, x, packed, n)
-    assert ctx.last_kernel.startswith("rlxq_gemm_q4_1_t256"), ctx.last_kernel
+    # (256 x 256 tiles would split K on all three: the 256 x 128 tiles serve)
+    assert ctx.last_kernel == "rlxq_gemm_q4_1_t256n128w8", ctx.last_kernel
     w = orc.dequantize(3, packed, k).astype(np.float32)
     want = (xv @ w.T).astype(np.float64)
     assert rel_err(got, want) <= TOL_PREFILL
+
+
+@pytest.mark.parametrize("mkn,want", [((4096, 4096, 24576), "t256w8p2"), ((2048, 4096, 24576), "t256w8p2"),
+                                      ((512, 4096, 24576), "t256w8p2"), ((1024, 4096, 24576), "t256n128w8"),
+                                      ((4096, 12288, 4096), "t256w8p2"), ((1024, 4096, 4096), "t256n128w8")], ids=str)
+def test_gemm_default_tiling_rule(ctx, orc, mkn, want):
+    """The dispatcher's tiling for bf16 in and out on 256 CUs: 256 x 256
+    tiles where they fill whole rounds of workgroups without a K split,
+    256 x 128 tiles where the 256 x 256 ones would split K or leave a partly
+    filled last round (4096->24576 at M=1024: 384 tiles, 768 of 256 x 128).
+    A sampled block of the output is checked against the oracle."""
+    import torch
+
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the rule's cases assume 256 CUs")
+    m, k, n = mkn
+    announce(f"gemm default tiling {mkn}")
+    g = torch.Generator(device="cuda").manual_seed(m + n)
+    x = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
+    rng = np.random.default_rng(m + k)
+    cols = 256
+    packed = orc.synth_q4_1(rng, cols, k)
+    wfull = torch.zeros((n * k * 5 // 8,), dtype=torch.uint8, device="cuda")
+    wfull[: cols * k * 5 // 8] = _t(packed.ravel())
+    y = ctx.dequant_matmul(x, wfull, 3, n, y_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert ctx.last_kernel == f"rlxq_gemm_q4_1_{want}", ctx.last_kernel
+    rows = np.arange(0, m, max(1, m // 64))
+    xv = x.float().cpu().numpy()[rows].astype(np.float64)
+    want_y = xv @ orc.dequantize(3, packed, k).astype(np.float64).T
+    assert rel_err(y.float().cpu().numpy()[rows, :cols], want_y) <= TOL_PREFILL
 
 
 @pytest.mark.parametrize("m,k,n", [(2048, 4096, 24576), (4096, 4096, 24576), (2048, 12288, 4096),
